@@ -1,0 +1,247 @@
+/*
+ * numrs_hip.h -- C ABI of the MI355X (gfx950) backend for numrs's reverse-mode
+ * autograd hot path.
+ *
+ * The reference (rjaguiluz/numrs, Rust) runs every backward node on the host:
+ * each BackwardFn (numrs-core/src/autograd/mod.rs:136) borrows host Arrays and
+ * returns freshly allocated ones, and Tensor::backward
+ * (autograd/tensor.rs:173-215) adds them into the inputs' grad cells with
+ * accumulate_gradient (tensor.rs:120-132).  This library replaces those bodies
+ * with HIP kernels on device-resident buffers, so a Rust `hip` backend under
+ * numrs-core/src/backend/hip would bind exactly these symbols.
+ *
+ * Conventions
+ *   - Every pointer argument that names tensor data is a DEVICE pointer owned
+ *     by the caller (allocate with numrs_hip_malloc or any hipMalloc).  fp32,
+ *     row-major, contiguous.
+ *   - Every call is asynchronous on the context's stream and returns an int
+ *     status: NUMRS_HIP_OK (0) or a negative code; the message is available
+ *     from numrs_hip_last_error(ctx).  No call aborts the process.
+ *   - `accumulate` = 1 means out += result (the reference's
+ *     accumulate_gradient); 0 means out = result.
+ *   - Entry points that need scratch memory take it from the context's
+ *     workspace, which grows on first use of a larger size (numrs_hip_reserve
+ *     pre-sizes it).
+ *   - One context per host thread; the reference autograd is single-threaded
+ *     (Rc/RefCell, thread-local grad mode: autograd/mod.rs:194-206).
+ */
+#ifndef NUMRS_HIP_H
+#define NUMRS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct numrs_hip_ctx numrs_hip_ctx;
+
+enum {
+  NUMRS_HIP_OK = 0,
+  NUMRS_HIP_E_INVALID = -1, /* null pointer, negative size, bad enum value   */
+  NUMRS_HIP_E_SHAPE = -2,   /* shapes that do not fit together              */
+  NUMRS_HIP_E_HIP = -3,     /* a HIP runtime call failed                    */
+  NUMRS_HIP_E_NOMEM = -4,   /* device allocation failed                     */
+  NUMRS_HIP_E_NODEV = -5    /* no usable gfx950 device                      */
+};
+
+/* Unbroadcast modes for bias / broadcast-reduce gradients. */
+enum {
+  /* Column/axis reduction to the target shape (what the mathematics asks). */
+  NUMRS_HIP_UNBROADCAST_CORRECT = 0,
+  /* The reference's behaviour: any shape mismatch becomes a full sum
+   * (backward.rs:12-39) that accumulate_gradient's zip() adds into element 0
+   * only (tensor.rs:120-132). */
+  NUMRS_HIP_UNBROADCAST_REFERENCE = 1
+};
+
+/* Unary backward kinds: dx = g * f'(.) with the saved forward value `v`. */
+enum {
+  NUMRS_HIP_RELU = 0,    /* v = x (input):  x > 0 ? g : 0      backward.rs:152-163 */
+  NUMRS_HIP_SIGMOID = 1, /* v = s (output): (g*s)*(1-s)         backward.rs:166-177 */
+  NUMRS_HIP_TANH = 2,    /* v = y (output): g*(1-y*y)           backward.rs:503-517 */
+  NUMRS_HIP_EXP = 3,     /* v = e (output): g*e                 backward.rs:180-191 */
+  NUMRS_HIP_LOG = 4,     /* v = x (input):  g/x                 backward.rs:194-205 */
+  NUMRS_HIP_GELU = 5,    /* v = x (input):  g*(Phi(x)+x*phi(x)) exact-erf GELU (no reference op) */
+  NUMRS_HIP_SQRT = 6,    /* v = x (input):  g*(x^-0.5*0.5)      backward.rs:441-463 */
+  NUMRS_HIP_SIN = 7,     /* v = x (input):  g*cos(x)            backward.rs:466-472 */
+  NUMRS_HIP_COS = 8,     /* v = x (input):  g*(sin(x)*-1)       backward.rs:475-483 */
+  NUMRS_HIP_TAN = 9,     /* v = t (output): g*(1+t*t)           backward.rs:486-500 */
+  NUMRS_HIP_POW = 10     /* v = x (input):  g*(x^(p-1)*p)       backward.rs:407-438 */
+};
+
+/* Binary backward kinds (same-shape operands; broadcasting is a separate
+ * numrs_hip_sum_to_shape on the result). */
+enum {
+  NUMRS_HIP_ADD = 0, /* dx = g,   dy = g                 backward.rs:43-54   */
+  NUMRS_HIP_SUB = 1, /* dx = g,   dy = g*-1              backward.rs:57-70   */
+  NUMRS_HIP_MUL = 2, /* dx = g*y, dy = g*x               backward.rs:74-87   */
+  NUMRS_HIP_DIV = 3  /* dx = g/y, dy = (g*(x/(y*y)))*-1  backward.rs:90-109  */
+};
+
+/* ---------------------------------------------------------------------- */
+/* Context, memory, streams, timing                                        */
+/* ---------------------------------------------------------------------- */
+
+/* Creates a context on HIP device `device` with its own stream (default
+ * priority).  Fails with NUMRS_HIP_E_NODEV when the device is absent or not
+ * gfx950.  Replaces nothing in the reference (its ops run on the caller's
+ * thread); it is the state a backend/hip module would hold, like
+ * DispatchTable's OnceCell (backend/dispatch.rs:713-721). */
+int numrs_hip_create(int device, numrs_hip_ctx **out);
+int numrs_hip_destroy(numrs_hip_ctx *ctx);
+/* Message of the last failed call on this context ("" if none). */
+const char *numrs_hip_last_error(numrs_hip_ctx *ctx);
+/* Message of the last failed numrs_hip_create on this thread. */
+const char *numrs_hip_create_error(void);
+/* Number of compute units and the gcn arch name ("gfx950..."). */
+int numrs_hip_device_info(numrs_hip_ctx *ctx, int *num_cus, char *arch, size_t arch_len);
+
+/* Device memory.  Replaces the host Vec<f32> behind Array::data
+ * (array/array.rs:14-22) and the zero-filled grad cell of Tensor::new
+ * (autograd/tensor.rs:41-59). */
+int numrs_hip_malloc(numrs_hip_ctx *ctx, size_t bytes, void **dptr);
+int numrs_hip_free(numrs_hip_ctx *ctx, void *dptr);
+int numrs_hip_upload(numrs_hip_ctx *ctx, void *dst, const void *host_src, size_t bytes);
+int numrs_hip_download(numrs_hip_ctx *ctx, void *host_dst, const void *src, size_t bytes);
+int numrs_hip_copy(numrs_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Fills `n` floats with `value` by a kernel (safe inside HIP graph capture).
+ * value = 0 is Tensor::zero_grad (autograd/tensor.rs:135-142). */
+int numrs_hip_fill(numrs_hip_ctx *ctx, float *dst, int64_t n, float value);
+/* Waits for all work queued on the context's stream. */
+int numrs_hip_sync(numrs_hip_ctx *ctx);
+/* Grows the workspace to at least `bytes` (otherwise it grows on demand). */
+int numrs_hip_reserve(numrs_hip_ctx *ctx, size_t bytes);
+/* The context's hipStream_t, for callers that enqueue their own work. */
+void *numrs_hip_stream(numrs_hip_ctx *ctx);
+
+/* HIP events recorded on the context's stream; slot in [0, 256). */
+int numrs_hip_timer_record(numrs_hip_ctx *ctx, int slot);
+int numrs_hip_timer_elapsed_ms(numrs_hip_ctx *ctx, int slot_start, int slot_end, float *ms);
+
+/* ---------------------------------------------------------------------- */
+/* Dense contractions (fp32 MFMA)                                          */
+/* ---------------------------------------------------------------------- */
+
+/* matmul_backward (autograd/backward.rs:113-149) for C[M,N] = A[M,K] @ B[K,N]:
+ *   dA[M,K] = dC @ B^T,  dB[K,N] = A^T @ dC.
+ * dA == NULL or dB == NULL skips that gradient (the reference always computes
+ * both; skipping is what its caller discards at tensor.rs:205-209).  Both
+ * products run in ONE launch of an LDS-tiled v_mfma_f32_32x32x2f32 kernel. */
+int numrs_hip_matmul_backward(numrs_hip_ctx *ctx, const float *dC, const float *A,
+                              const float *B, float *dA, float *dB, int64_t M, int64_t K,
+                              int64_t N, int accumulate);
+
+/* The same for `batch` independent products laid out with element strides
+ * stride_a, stride_b, stride_c between consecutive matrices (dA/dB use the
+ * A/B strides).  Attention's batched grads use this; the reference has only
+ * 2-D matmul (backward.rs:118-120). */
+int numrs_hip_matmul_backward_batched(numrs_hip_ctx *ctx, const float *dC, const float *A,
+                                      const float *B, float *dA, float *dB, int64_t batch,
+                                      int64_t M, int64_t K, int64_t N, int64_t stride_a,
+                                      int64_t stride_b, int64_t stride_c, int accumulate);
+
+/* General product C[M,N] (+)= op(A) @ op(B), op = transpose when trans_* = 1
+ * (A stored [K,M] / B stored [N,K]).  The forward of Tensor::matmul
+ * (autograd/ops.rs:101-119 -> ops::matmul -> DispatchTable.matmul,
+ * backend/dispatch.rs:69-93) and the Linear forward x @ W^T
+ * (autograd/nn.rs:217-235) without materialising W^T. */
+int numrs_hip_matmul(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, int64_t M,
+                     int64_t K, int64_t N, int trans_a, int trans_b, int accumulate);
+
+/* Batched form of numrs_hip_matmul with element strides between matrices. */
+int numrs_hip_matmul_batched(numrs_hip_ctx *ctx, const float *A, const float *B, float *C,
+                             int64_t batch, int64_t M, int64_t K, int64_t N, int64_t stride_a,
+                             int64_t stride_b, int64_t stride_c, int trans_a, int trans_b,
+                             int accumulate);
+
+/* ---------------------------------------------------------------------- */
+/* Broadcast-reduce gradients                                              */
+/* ---------------------------------------------------------------------- */
+
+/* unbroadcast (backward.rs:12-39) + accumulate_gradient (tensor.rs:120-132):
+ * reduces g (shape gshape[0..gnd)) onto out (shape oshape[0..ond)), shapes
+ * right-aligned numpy style.  CORRECT sums every axis where out has size 1
+ * or is missing; REFERENCE sums everything into out[0] (accumulate = 0 then
+ * writes [sum, 0, ..., 0], the reference's fresh zero grad plus the zip). */
+int numrs_hip_sum_to_shape(numrs_hip_ctx *ctx, const float *g, const int64_t *gshape, int gnd,
+                           float *out, const int64_t *oshape, int ond, int mode, int accumulate);
+
+/* relu_backward (backward.rs:152-163) fused with the bias branch of
+ * add_backward (backward.rs:43-54) for y = ReLU(x + b), x[rows,cols],
+ * b[cols]:  dx = (z > 0) ? g : 0 with z = x + b the saved pre-activation,
+ * db = column sum of dx (mode CORRECT) or its full sum in db[0] (REFERENCE).
+ * dx or db may be NULL.  Reads g and z once: 12 B/element. */
+int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx,
+                                 float *db, int64_t rows, int64_t cols, int mode, int accumulate);
+
+/* ---------------------------------------------------------------------- */
+/* Elementwise backward                                                    */
+/* ---------------------------------------------------------------------- */
+
+/* dx (+)= g * f'(v) for the unary kinds above; `param` is the exponent for
+ * NUMRS_HIP_POW and ignored otherwise. */
+int numrs_hip_unary_backward(numrs_hip_ctx *ctx, int kind, const float *g, const float *v,
+                             float *dx, int64_t n, float param, int accumulate);
+
+/* Binary backward for same-shape operands; dx or dy may be NULL. */
+int numrs_hip_binary_backward(numrs_hip_ctx *ctx, int kind, const float *g, const float *x,
+                              const float *y, float *dx, float *dy, int64_t n, int accumulate);
+
+/* sum_backward / mean_backward (backward.rs:208-236): dx (+)= g[0] * scale
+ * with scale = 1 (sum) or the f32 division g[0]/n performed as in the
+ * reference when divide_by_n = 1 (mean). g_scalar is a device pointer. */
+int numrs_hip_fill_grad(numrs_hip_ctx *ctx, const float *g_scalar, float *dx, int64_t n,
+                        int divide_by_n, int accumulate);
+
+/* mse_backward (backward.rs:239-261): dp = ((g*2)*(p-t))/n, dt = -dp.
+ * g_scalar is a device pointer; dp or dt may be NULL. */
+int numrs_hip_mse_backward(numrs_hip_ctx *ctx, const float *g_scalar, const float *p,
+                           const float *t, float *dp, float *dt, int64_t n, int accumulate);
+
+/* ---------------------------------------------------------------------- */
+/* Row-wise kernels                                                        */
+/* ---------------------------------------------------------------------- */
+
+/* cross_entropy_backward (backward.rs:265-301): per row softmax of the
+ * logits[B,C] minus the target, times g[0]/B.  The target is either a
+ * one-hot float matrix (onehot != NULL, as the reference takes it) or int32
+ * class labels (labels != NULL; a label outside [0,C) yields an all-zero
+ * target row, as a zero one-hot row would). */
+int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, const float *logits,
+                                  const float *onehot, const int32_t *labels, float *dlogits,
+                                  int64_t B, int64_t C, int accumulate);
+
+/* softmax_backward (backward.rs:521-541), rows of length cols:
+ * dx (+)= y * (g - sum_row(g*y)). */
+int numrs_hip_softmax_backward(numrs_hip_ctx *ctx, const float *y, const float *g, float *dx,
+                               int64_t rows, int64_t cols, int accumulate);
+
+/* Row argmax as int32.  tie_last = 0: first maximum (ops::argmax,
+ * backend/cpu/scalar.rs:517-528); tie_last = 1: last maximum with NaN
+ * compared as Equal (Trainer::evaluate's max_by, autograd/train.rs:213-228). */
+int numrs_hip_argmax_rows(numrs_hip_ctx *ctx, const float *x, int32_t *idx, int64_t rows,
+                          int64_t cols, int tie_last);
+
+/* ---------------------------------------------------------------------- */
+/* Optimizer steps                                                         */
+/* ---------------------------------------------------------------------- */
+
+/* SGD::step for one parameter (optim/sgd.rs:130-167, weight decay
+ * optim/base.rs:26-36): g' = g + wd*p; mu != 0: v = mu*v + g', p -= lr*v;
+ * else p -= lr*g'.  v may be NULL when mu == 0. */
+int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, int64_t n,
+                       float lr, float mu, float wd);
+
+/* Adam::step for one parameter (optim/adam.rs:310-353) at step t (the
+ * already-incremented counter): bias corrections 1 - b^t are computed on the
+ * host with f32::powi's semantics, then one fused pass updates p, m, v
+ * (28 B/element). */
+int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, float *v,
+                        int64_t n, float lr, float b1, float b2, float eps, float wd, int t);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NUMRS_HIP_H */

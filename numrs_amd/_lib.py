@@ -1,0 +1,91 @@
+"""ctypes binding of libnumrs_hip.so (declarations mirror include/numrs_hip.h).
+
+The library is loaded from numrs_amd/lib/ only.  There is no fallback: if it
+is missing or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "libnumrs_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG), "include", "numrs_hip.h")
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "numrs_hip_create": (_i, [_i, ctypes.POINTER(_vp)]),
+    "numrs_hip_destroy": (_i, [_vp]),
+    "numrs_hip_last_error": (ctypes.c_char_p, [_vp]),
+    "numrs_hip_create_error": (ctypes.c_char_p, []),
+    "numrs_hip_device_info": (_i, [_vp, ctypes.POINTER(_i), ctypes.c_char_p, _sz]),
+    "numrs_hip_malloc": (_i, [_vp, _sz, ctypes.POINTER(_vp)]),
+    "numrs_hip_free": (_i, [_vp, _vp]),
+    "numrs_hip_upload": (_i, [_vp, _vp, _vp, _sz]),
+    "numrs_hip_download": (_i, [_vp, _vp, _vp, _sz]),
+    "numrs_hip_copy": (_i, [_vp, _vp, _vp, _sz]),
+    "numrs_hip_fill": (_i, [_vp, _vp, _i64, _f]),
+    "numrs_hip_sync": (_i, [_vp]),
+    "numrs_hip_reserve": (_i, [_vp, _sz]),
+    "numrs_hip_stream": (_vp, [_vp]),
+    "numrs_hip_timer_record": (_i, [_vp, _i]),
+    "numrs_hip_timer_elapsed_ms": (_i, [_vp, _i, _i, ctypes.POINTER(_f)]),
+    "numrs_hip_matmul_backward": (_i, [_vp] * 6 + [_i64] * 3 + [_i]),
+    "numrs_hip_matmul_backward_batched": (_i, [_vp] * 6 + [_i64] * 7 + [_i]),
+    "numrs_hip_matmul": (_i, [_vp] * 4 + [_i64] * 3 + [_i] * 3),
+    "numrs_hip_matmul_batched": (_i, [_vp] * 4 + [_i64] * 7 + [_i] * 3),
+    "numrs_hip_sum_to_shape": (_i, [_vp, _vp, _i64p, _i, _vp, _i64p, _i, _i, _i]),
+    "numrs_hip_relu_bias_backward": (_i, [_vp] * 5 + [_i64, _i64, _i, _i]),
+    "numrs_hip_unary_backward": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _f, _i]),
+    "numrs_hip_binary_backward": (_i, [_vp, _i] + [_vp] * 5 + [_i64, _i]),
+    "numrs_hip_fill_grad": (_i, [_vp, _vp, _vp, _i64, _i, _i]),
+    "numrs_hip_mse_backward": (_i, [_vp] * 6 + [_i64, _i]),
+    "numrs_hip_softmax_ce_backward": (_i, [_vp] * 6 + [_i64, _i64, _i]),
+    "numrs_hip_softmax_backward": (_i, [_vp] * 4 + [_i64, _i64, _i]),
+    "numrs_hip_argmax_rows": (_i, [_vp] * 3 + [_i64, _i64, _i]),
+    "numrs_hip_sgd_step": (_i, [_vp] * 4 + [_i64, _f, _f, _f]),
+    "numrs_hip_adam_step": (_i, [_vp] * 5 + [_i64, _f, _f, _f, _f, _f, _i]),
+}
+
+# Enum values of include/numrs_hip.h.
+OK, E_INVALID, E_SHAPE, E_HIP, E_NOMEM, E_NODEV = 0, -1, -2, -3, -4, -5
+UNBROADCAST_CORRECT, UNBROADCAST_REFERENCE = 0, 1
+RELU, SIGMOID, TANH, EXP, LOG, GELU, SQRT, SIN, COS, TAN, POW = range(11)
+ADD, SUB, MUL, DIV = range(4)
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def header_functions(path: str = HEADER_PATH) -> list[str]:
+    """Names of every function the C header declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(numrs_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryMissing(
+            f"{LIB_PATH} is not built; run `python -m numrs_amd.build` (there is no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

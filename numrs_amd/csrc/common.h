@@ -1,0 +1,72 @@
+// Internal declarations shared by the HIP translation units of libnumrs_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "numrs_hip.h"
+
+constexpr int kMaxTimers = 256;
+
+struct numrs_hip_ctx {
+  int device = 0;
+  int num_cus = 0;
+  char arch[64] = {0};
+  hipStream_t stream = nullptr;
+  hipEvent_t events[kMaxTimers] = {};
+  void *workspace = nullptr;
+  size_t workspace_bytes = 0;
+  char last_error[512] = {0};
+};
+
+namespace numrs_hip {
+
+// Records a formatted message on the context and returns `code`.
+int fail(numrs_hip_ctx *ctx, int code, const char *fmt, ...);
+
+// Returns the context's workspace with at least `bytes` bytes (grows it).
+int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out);
+
+// Checks the launch that was just enqueued.
+int check_launch(numrs_hip_ctx *ctx, const char *what);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace numrs_hip
+
+#define NRS_CHECK_CTX(ctx)                       \
+  do {                                           \
+    if ((ctx) == nullptr) return NUMRS_HIP_E_INVALID; \
+  } while (0)
+
+#define NRS_HIP(ctx, call)                                                              \
+  do {                                                                                  \
+    hipError_t e_ = (call);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return numrs_hip::fail((ctx), NUMRS_HIP_E_HIP, "%s failed: %s", #call,            \
+                             hipGetErrorString(e_));                                    \
+  } while (0)
+
+// Grid sizing for element-streaming kernels.
+inline unsigned grid_for(int64_t work_items, int per_block) {
+  int64_t g = (work_items + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > 0x7fffffff) g = 0x7fffffff;
+  return static_cast<unsigned>(g);
+}
+
+// Wavefront (64 lanes) reductions via DPP-free cross-lane shuffles.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}

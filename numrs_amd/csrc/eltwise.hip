@@ -1,0 +1,431 @@
+// Element-streaming kernels: unary/binary backward, sum/mean fill, MSE
+// backward, SGD and Adam steps.
+//
+// All are HBM-bound.  Each thread moves two float4 per operand, placed
+// blockDim*4 floats apart so every wave load is a contiguous 1 KiB; scalar
+// tails and misaligned operands take the per-element path.  This translation
+// unit is built with -ffp-contract=off: the reference (Rust) never fuses
+// a*b+c, and the operation order below is the reference's, so results for
+// the select/multiply/divide/sqrt kernels are bit-identical to it.
+#include <cmath>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kVecPerThread = 2;
+constexpr int kElemsPerBlock = kBlock * 4 * kVecPerThread;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Unary backward: dx = g * f'(v)
+// ---------------------------------------------------------------------------
+
+template <int KIND>
+__device__ __forceinline__ float unary_grad(float g, float v, float p) {
+  if constexpr (KIND == NUMRS_HIP_RELU) {
+    return v > 0.0f ? g : 0.0f;  // backward.rs:158 (strict)
+  } else if constexpr (KIND == NUMRS_HIP_SIGMOID) {
+    return (g * v) * (1.0f - v);  // backward.rs:172
+  } else if constexpr (KIND == NUMRS_HIP_TANH) {
+    return g * (1.0f - v * v);  // backward.rs:508-515
+  } else if constexpr (KIND == NUMRS_HIP_EXP) {
+    return g * v;  // backward.rs:186
+  } else if constexpr (KIND == NUMRS_HIP_LOG) {
+    return g / v;  // backward.rs:200
+  } else if constexpr (KIND == NUMRS_HIP_GELU) {
+    const float cdf = 0.5f * (1.0f + erff(v * 0.70710678118654752f));
+    const float pdf = 0.39894228040143268f * expf(-0.5f * v * v);
+    return g * (cdf + v * pdf);
+  } else if constexpr (KIND == NUMRS_HIP_SQRT) {
+    return g * (powf(v, -0.5f) * 0.5f);  // backward.rs:452-460
+  } else if constexpr (KIND == NUMRS_HIP_SIN) {
+    return g * cosf(v);  // backward.rs:469-470
+  } else if constexpr (KIND == NUMRS_HIP_COS) {
+    return g * (sinf(v) * -1.0f);  // backward.rs:478-481
+  } else if constexpr (KIND == NUMRS_HIP_TAN) {
+    return g * (1.0f + v * v);  // backward.rs:491-498
+  } else {  // NUMRS_HIP_POW
+    return g * (powf(v, p - 1.0f) * p);  // backward.rs:427-435
+  }
+}
+
+template <int KIND, bool VEC>
+__global__ void __launch_bounds__(kBlock)
+    unary_bwd_kernel(const float *__restrict__ g, const float *__restrict__ v,
+                     float *__restrict__ dx, int64_t n, float p, int acc) {
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+    if (VEC && i + 3 < n) {
+      const f4 gv = *reinterpret_cast<const f4 *>(g + i);
+      const f4 vv = *reinterpret_cast<const f4 *>(v + i);
+      f4 r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = unary_grad<KIND>(gv[e], vv[e], p);
+      if (acc) r += *reinterpret_cast<const f4 *>(dx + i);
+      *reinterpret_cast<f4 *>(dx + i) = r;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (i + e < n) {
+          float r = unary_grad<KIND>(g[i + e], v[i + e], p);
+          dx[i + e] = acc ? dx[i + e] + r : r;
+        }
+      }
+    }
+  }
+}
+
+template <int KIND>
+int launch_unary(numrs_hip_ctx *ctx, const float *g, const float *v, float *dx, int64_t n,
+                 float p, int acc) {
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  const bool vec = numrs_hip::aligned16(g) && numrs_hip::aligned16(v) && numrs_hip::aligned16(dx);
+  if (vec)
+    unary_bwd_kernel<KIND, true><<<grid, kBlock, 0, ctx->stream>>>(g, v, dx, n, p, acc);
+  else
+    unary_bwd_kernel<KIND, false><<<grid, kBlock, 0, ctx->stream>>>(g, v, dx, n, p, acc);
+  return numrs_hip::check_launch(ctx, "unary_bwd_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Binary backward (same shapes)
+// ---------------------------------------------------------------------------
+
+template <int KIND>
+__device__ __forceinline__ void binary_grad(float g, float x, float y, float &dx, float &dy) {
+  if constexpr (KIND == NUMRS_HIP_ADD) {
+    dx = g;
+    dy = g;
+  } else if constexpr (KIND == NUMRS_HIP_SUB) {
+    dx = g;
+    dy = g * -1.0f;  // backward.rs:65-66
+  } else if constexpr (KIND == NUMRS_HIP_MUL) {
+    dx = g * y;  // backward.rs:79
+    dy = g * x;  // backward.rs:83
+  } else {       // DIV, backward.rs:95-104
+    dx = g / y;
+    const float ysq = y * y;
+    const float term = x / ysq;
+    dy = (g * term) * -1.0f;
+  }
+}
+
+template <int KIND>
+__global__ void __launch_bounds__(kBlock)
+    binary_bwd_kernel(const float *__restrict__ g, const float *__restrict__ x,
+                      const float *__restrict__ y, float *__restrict__ dx, float *__restrict__ dy,
+                      int64_t n, int acc) {
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 4 * kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock;
+    if (i < n) {
+      const float xv = (KIND == NUMRS_HIP_MUL || KIND == NUMRS_HIP_DIV) ? x[i] : 0.0f;
+      const float yv = (KIND == NUMRS_HIP_MUL || KIND == NUMRS_HIP_DIV) ? y[i] : 0.0f;
+      float a, b;
+      binary_grad<KIND>(g[i], xv, yv, a, b);
+      if (dx) dx[i] = acc ? dx[i] + a : a;
+      if (dy) dy[i] = acc ? dy[i] + b : b;
+    }
+  }
+}
+
+template <int KIND>
+int launch_binary(numrs_hip_ctx *ctx, const float *g, const float *x, const float *y, float *dx,
+                  float *dy, int64_t n, int acc) {
+  binary_bwd_kernel<KIND><<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(g, x, y, dx, dy,
+                                                                                   n, acc);
+  return numrs_hip::check_launch(ctx, "binary_bwd_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// sum/mean backward fill, MSE backward
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kBlock)
+    fill_grad_kernel(const float *__restrict__ g0, float *__restrict__ dx, int64_t n, float nf,
+                     int divide, int acc) {
+  const float v = divide ? g0[0] / nf : g0[0];  // backward.rs:213 / :228
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 4 * kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock;
+    if (i < n) dx[i] = acc ? dx[i] + v : v;
+  }
+}
+
+__global__ void __launch_bounds__(kBlock)
+    mse_bwd_kernel(const float *__restrict__ g0, const float *__restrict__ p,
+                   const float *__restrict__ t, float *__restrict__ dp, float *__restrict__ dt,
+                   int64_t n, float nf, int acc) {
+  const float gs = g0[0];
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 4 * kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock;
+    if (i < n) {
+      const float v = ((gs * 2.0f) * (p[i] - t[i])) / nf;  // backward.rs:250
+      if (dp) dp[i] = acc ? dp[i] + v : v;
+      if (dt) dt[i] = acc ? dt[i] + (-v) : -v;  // backward.rs:257
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Optimizers
+// ---------------------------------------------------------------------------
+
+// SGD::step, optim/sgd.rs:130-167 (+ apply_weight_decay, optim/base.rs:26-36).
+template <bool MOMENTUM, bool DECAY, bool VEC>
+__global__ void __launch_bounds__(kBlock)
+    sgd_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ v,
+               int64_t n, float lr, float mu, float wd) {
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+    if (VEC && i + 3 < n) {
+      f4 pv = *reinterpret_cast<const f4 *>(p + i);
+      f4 gv = *reinterpret_cast<const f4 *>(g + i);
+      f4 vv;
+      if (MOMENTUM) vv = *reinterpret_cast<const f4 *>(v + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float gg = gv[e];
+        if (DECAY) gg = gg + wd * pv[e];
+        if (MOMENTUM) {
+          vv[e] = mu * vv[e] + gg;
+          pv[e] = pv[e] - lr * vv[e];
+        } else {
+          pv[e] = pv[e] - lr * gg;
+        }
+      }
+      *reinterpret_cast<f4 *>(p + i) = pv;
+      if (MOMENTUM) *reinterpret_cast<f4 *>(v + i) = vv;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t k = i + e;
+        if (k < n) {
+          float gg = g[k];
+          if (DECAY) gg = gg + wd * p[k];
+          if (MOMENTUM) {
+            v[k] = mu * v[k] + gg;
+            p[k] = p[k] - lr * v[k];
+          } else {
+            p[k] = p[k] - lr * gg;
+          }
+        }
+      }
+    }
+  }
+}
+
+struct AdamArgs {
+  float lr, b1, b2, eps, wd, omb1, omb2, bc1, bc2;
+};
+
+__device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v, const AdamArgs &a,
+                                          bool decay) {
+  if (decay) g = g + a.wd * p;                   // optim/base.rs:31-33
+  m = a.b1 * m + a.omb1 * g;                     // adam.rs:330-332
+  v = a.b2 * v + a.omb2 * g * g;                 // adam.rs:335-337
+  const float mh = m / a.bc1;                    // adam.rs:346
+  const float vh = v / a.bc2;                    // adam.rs:347
+  p = p - a.lr * mh / (sqrtf(vh) + a.eps);       // adam.rs:348
+}
+
+// Adam::step, optim/adam.rs:310-353, fused into one pass over p, g, m, v.
+template <bool DECAY, bool VEC>
+__global__ void __launch_bounds__(kBlock)
+    adam_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m,
+                float *__restrict__ v, int64_t n, AdamArgs a) {
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+    if (VEC && i + 3 < n) {
+      f4 pv = *reinterpret_cast<const f4 *>(p + i);
+      const f4 gv = *reinterpret_cast<const f4 *>(g + i);
+      f4 mv = *reinterpret_cast<const f4 *>(m + i);
+      f4 vv = *reinterpret_cast<const f4 *>(v + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float pe = pv[e], me = mv[e], ve = vv[e];
+        adam_elem(pe, gv[e], me, ve, a, DECAY);
+        pv[e] = pe;
+        mv[e] = me;
+        vv[e] = ve;
+      }
+      *reinterpret_cast<f4 *>(p + i) = pv;
+      *reinterpret_cast<f4 *>(m + i) = mv;
+      *reinterpret_cast<f4 *>(v + i) = vv;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t k = i + e;
+        if (k < n) {
+          float pe = p[k], me = m[k], ve = v[k];
+          adam_elem(pe, g[k], me, ve, a, DECAY);
+          p[k] = pe;
+          m[k] = me;
+          v[k] = ve;
+        }
+      }
+    }
+  }
+}
+
+// f32::powi as lowered by Rust/LLVM on x86-64 (compiler-rt __powisf2):
+// square-and-multiply over the exponent's bits, low bit first.
+float powi_f32(float a, int b) {
+  const bool recip = b < 0;
+  if (recip) b = -b;
+  float r = 1.0f;
+  for (;;) {
+    if (b & 1) r = r * a;
+    b /= 2;
+    if (b == 0) break;
+    a = a * a;
+  }
+  return recip ? 1.0f / r : r;
+}
+
+int check_n(numrs_hip_ctx *ctx, const char *who, int64_t n) {
+  if (n < 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative length", who);
+  return NUMRS_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int numrs_hip_unary_backward(numrs_hip_ctx *ctx, int kind, const float *g, const float *v,
+                             float *dx, int64_t n, float param, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_unary_backward", n)) return rc;
+  if (n == 0) return NUMRS_HIP_OK;
+  if (g == nullptr || v == nullptr || dx == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_unary_backward: null pointer");
+  switch (kind) {
+    case NUMRS_HIP_RELU: return launch_unary<NUMRS_HIP_RELU>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_SIGMOID:
+      return launch_unary<NUMRS_HIP_SIGMOID>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_TANH: return launch_unary<NUMRS_HIP_TANH>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_EXP: return launch_unary<NUMRS_HIP_EXP>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_LOG: return launch_unary<NUMRS_HIP_LOG>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_GELU: return launch_unary<NUMRS_HIP_GELU>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_SQRT: return launch_unary<NUMRS_HIP_SQRT>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_SIN: return launch_unary<NUMRS_HIP_SIN>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_COS: return launch_unary<NUMRS_HIP_COS>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_TAN: return launch_unary<NUMRS_HIP_TAN>(ctx, g, v, dx, n, param, accumulate);
+    case NUMRS_HIP_POW: return launch_unary<NUMRS_HIP_POW>(ctx, g, v, dx, n, param, accumulate);
+    default:
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_unary_backward: kind %d", kind);
+  }
+}
+
+int numrs_hip_binary_backward(numrs_hip_ctx *ctx, int kind, const float *g, const float *x,
+                              const float *y, float *dx, float *dy, int64_t n, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_binary_backward", n)) return rc;
+  if (n == 0 || (dx == nullptr && dy == nullptr)) return NUMRS_HIP_OK;
+  const bool needs_xy = kind == NUMRS_HIP_MUL || kind == NUMRS_HIP_DIV;
+  if (g == nullptr || (needs_xy && (x == nullptr || y == nullptr)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_binary_backward: null pointer");
+  switch (kind) {
+    case NUMRS_HIP_ADD: return launch_binary<NUMRS_HIP_ADD>(ctx, g, x, y, dx, dy, n, accumulate);
+    case NUMRS_HIP_SUB: return launch_binary<NUMRS_HIP_SUB>(ctx, g, x, y, dx, dy, n, accumulate);
+    case NUMRS_HIP_MUL: return launch_binary<NUMRS_HIP_MUL>(ctx, g, x, y, dx, dy, n, accumulate);
+    case NUMRS_HIP_DIV: return launch_binary<NUMRS_HIP_DIV>(ctx, g, x, y, dx, dy, n, accumulate);
+    default:
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_binary_backward: kind %d",
+                             kind);
+  }
+}
+
+int numrs_hip_fill_grad(numrs_hip_ctx *ctx, const float *g_scalar, float *dx, int64_t n,
+                        int divide_by_n, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_fill_grad", n)) return rc;
+  if (n == 0) return NUMRS_HIP_OK;
+  if (g_scalar == nullptr || dx == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_fill_grad: null pointer");
+  fill_grad_kernel<<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(
+      g_scalar, dx, n, (float)n, divide_by_n, accumulate);
+  return numrs_hip::check_launch(ctx, "fill_grad_kernel");
+}
+
+int numrs_hip_mse_backward(numrs_hip_ctx *ctx, const float *g_scalar, const float *p,
+                           const float *t, float *dp, float *dt, int64_t n, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_mse_backward", n)) return rc;
+  if (n == 0 || (dp == nullptr && dt == nullptr)) return NUMRS_HIP_OK;
+  if (g_scalar == nullptr || p == nullptr || t == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_backward: null pointer");
+  mse_bwd_kernel<<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt,
+                                                                          n, (float)n, accumulate);
+  return numrs_hip::check_launch(ctx, "mse_bwd_kernel");
+}
+
+int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, int64_t n,
+                       float lr, float mu, float wd) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_sgd_step", n)) return rc;
+  if (n == 0) return NUMRS_HIP_OK;
+  if (p == nullptr || g == nullptr || (mu != 0.0f && v == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_sgd_step: null pointer");
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(g) &&
+                   (mu == 0.0f || numrs_hip::aligned16(v));
+  const bool mom = mu != 0.0f, dec = wd != 0.0f;
+#define NRS_SGD(M, D)                                                                   \
+  do {                                                                                  \
+    if (vec)                                                                            \
+      sgd_kernel<M, D, true><<<grid, kBlock, 0, ctx->stream>>>(p, g, v, n, lr, mu, wd);  \
+    else                                                                                \
+      sgd_kernel<M, D, false><<<grid, kBlock, 0, ctx->stream>>>(p, g, v, n, lr, mu, wd); \
+  } while (0)
+  if (mom && dec) NRS_SGD(true, true);
+  else if (mom) NRS_SGD(true, false);
+  else if (dec) NRS_SGD(false, true);
+  else NRS_SGD(false, false);
+#undef NRS_SGD
+  return numrs_hip::check_launch(ctx, "sgd_kernel");
+}
+
+int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, float *v,
+                        int64_t n, float lr, float b1, float b2, float eps, float wd, int t) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_adam_step", n)) return rc;
+  if (t < 1) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_adam_step: t < 1");
+  if (n == 0) return NUMRS_HIP_OK;
+  if (p == nullptr || g == nullptr || m == nullptr || v == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_adam_step: null pointer");
+  AdamArgs a;
+  a.lr = lr;
+  a.b1 = b1;
+  a.b2 = b2;
+  a.eps = eps;
+  a.wd = wd;
+  a.omb1 = 1.0f - b1;
+  a.omb2 = 1.0f - b2;
+  a.bc1 = 1.0f - powi_f32(b1, t);  // adam.rs:314
+  a.bc2 = 1.0f - powi_f32(b2, t);  // adam.rs:315
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(g) &&
+                   numrs_hip::aligned16(m) && numrs_hip::aligned16(v);
+  const bool dec = wd != 0.0f;
+  if (dec && vec) adam_kernel<true, true><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+  else if (dec) adam_kernel<true, false><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+  else if (vec) adam_kernel<false, true><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+  else adam_kernel<false, false><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+  return numrs_hip::check_launch(ctx, "adam_kernel");
+}
+
+}  // extern "C"

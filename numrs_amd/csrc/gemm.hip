@@ -1,0 +1,398 @@
+// fp32 MFMA GEMMs for matmul_backward (dA = dC @ B^T, dB = A^T @ dC) and the
+// forward products, on gfx950 (CDNA4).
+//
+// One generic tile routine computes C[P,Q] (+)= X[P,R] @ Y[R,Q] where each
+// operand is either "R-contiguous" (the reduction index is the fast one in
+// memory: X[p*ld + r], Y[q*ld + r]) or "P/Q-contiguous" (X[r*ld + p],
+// Y[r*ld + q]).  The four layouts cover every product on the path:
+//   dA = dC @ B^T   X = dC (R-contig), Y = B   (R-contig)   [NT]
+//   dB = A^T @ dC   X = A  (P-contig), Y = dC  (Q-contig)   [TN]
+//   C  = A @ B      X = A  (R-contig), Y = B   (Q-contig)   [NN]
+//   y  = x @ W^T    X = x  (R-contig), Y = W   (R-contig)   [NT]
+//
+// Work decomposition
+//   * Workgroup tile 128(P) x 128(Q), 256 threads = 4 wave64s in a 2x2 grid,
+//     each wave owns a 64x64 sub-tile = 2x2 blocks of v_mfma_f32_32x32x2f32
+//     (16 accumulator VGPRs per block per lane).
+//   * Reduction tile BR = 32, double-buffered in LDS, one barrier per tile; the
+//     next tile's global loads are in flight while the MFMAs of the current
+//     one run.
+//   * An MFMA 32x32x2 consumes, per lane l = 32*h + c, X[p=c][r=h] and
+//     Y[r=h][q=c].  Eight consecutive reduction indices are fed to four
+//     MFMAs as r = 4h + j (j = 0..3): an R-contiguous operand then gives each
+//     lane four consecutive floats (one ds_read_b128 from a [p][r] LDS tile of
+//     row stride 36 floats, conflict-free), and a P-contiguous operand gives
+//     four ds_read_b32 from a [r][p] tile whose lanes read consecutive words.
+//     Neither layout is transposed on its way into LDS.
+//   * XCD-aware ordering: gfx950 dispatches workgroup b to XCD b % 8; the
+//     logical tile index is permuted so each XCD owns a contiguous 4 x 8 patch
+//     of tiles and its private L2 sees the operand rows/columns it reuses.
+//   * matmul_backward launches dA and dB tiles in ONE grid (2 x 256 tiles at
+//     2048^2 = 2 workgroups per CU on 256 CUs).
+#include "common.h"
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int kBP = 128;                 // tile extent along P and along Q
+constexpr int kBR = 32;                  // reduction tile
+constexpr int kThreads = 256;
+constexpr int kRcStride = kBR + 4;       // [p][r] tile row stride (floats)
+constexpr int kPcStride = kBP + 8;       // [r][p] tile row stride (floats)
+constexpr int kTileFloats = kBP * kRcStride;  // 4608 >= kBR * kPcStride = 4352
+constexpr int kGroupRows = 4;            // tile rows per raster group
+
+struct Gemm {
+  const float *X;
+  const float *Y;
+  float *C;
+  int64_t ldx, ldy, ldc;
+  int64_t bsx, bsy, bsc;  // batch strides (elements)
+  int P, Q, R;
+  int tiles_p, tiles_q;
+  int accumulate;
+};
+
+// Loads one 128 x 32 operand tile from global memory into registers
+// (4 x float4 per thread) with zero fill outside [0,P) x [0,R).
+template <bool RC, bool VEC>
+struct TileLoad {
+  f4 v[4];
+
+  __device__ __forceinline__ void load(const float *__restrict__ base, int64_t ld, int p0, int r0,
+                                       int P, int R, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + kThreads * i;
+      int p, r;
+      if (RC) {
+        p = idx >> 3;
+        r = (idx & 7) * 4;
+      } else {
+        r = idx >> 5;
+        p = (idx & 31) * 4;
+      }
+      const int gp = p0 + p, gr = r0 + r;
+      if (VEC) {
+        // Extents are multiples of 4, so a float4 is wholly in or out.
+        const bool in = RC ? (gp < P && gr < R) : (gr < R && gp < P);
+        const float *src = RC ? base + (int64_t)gp * ld + gr : base + (int64_t)gr * ld + gp;
+        v[i] = in ? *reinterpret_cast<const f4 *>(src) : f4{0.f, 0.f, 0.f, 0.f};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool in = RC ? (gp < P && gr + e < R) : (gr < R && gp + e < P);
+          const float *src =
+              RC ? base + (int64_t)gp * ld + gr + e : base + (int64_t)gr * ld + gp + e;
+          v[i][e] = in ? *src : 0.f;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float *__restrict__ lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + kThreads * i;
+      if (RC) {
+        *reinterpret_cast<f4 *>(lds + (idx >> 3) * kRcStride + (idx & 7) * 4) = v[i];
+      } else {
+        *reinterpret_cast<f4 *>(lds + (idx >> 5) * kPcStride + (idx & 31) * 4) = v[i];
+      }
+    }
+  }
+};
+
+// Four reduction-consecutive operand values for MFMA group g at lane (h, c).
+template <bool RC>
+__device__ __forceinline__ f4 frag(const float *__restrict__ lds, int pbase, int c, int h, int g) {
+  if (RC) {
+    return *reinterpret_cast<const f4 *>(lds + (pbase + c) * kRcStride + 8 * g + 4 * h);
+  } else {
+    f4 f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = lds[(8 * g + 4 * h + j) * kPcStride + pbase + c];
+    return f;
+  }
+}
+
+template <bool XRC, bool YRC, bool VEC>
+__device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, float *smem) {
+  // Raster order: groups of kGroupRows tile-rows, column-major inside a group.
+  const int per_group = kGroupRows * d.tiles_q;
+  const int gidx = tile / per_group;
+  const int first_p = gidx * kGroupRows;
+  const int rows_in_group = min(d.tiles_p - first_p, kGroupRows);
+  const int in_group = tile - gidx * per_group;
+  const int tp = first_p + in_group % rows_in_group;
+  const int tq = in_group / rows_in_group;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wp = wave >> 1, wq = wave & 1;
+  const int c = lane & 31, h = lane >> 5;
+  const int p0 = tp * kBP, q0 = tq * kBP;
+
+  const float *__restrict__ X = d.X + (int64_t)batch * d.bsx;
+  const float *__restrict__ Y = d.Y + (int64_t)batch * d.bsy;
+  float *__restrict__ C = d.C + (int64_t)batch * d.bsc;
+
+  float *xs0 = smem, *xs1 = smem + kTileFloats;
+  float *ys0 = smem + 2 * kTileFloats, *ys1 = smem + 3 * kTileFloats;
+
+  f16v acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+
+  TileLoad<XRC, VEC> lx;
+  TileLoad<YRC, VEC> ly;
+  const int nk = (d.R + kBR - 1) / kBR;
+
+  lx.load(X, d.ldx, p0, 0, d.P, d.R, tid);
+  ly.load(Y, d.ldy, q0, 0, d.Q, d.R, tid);
+  lx.store(xs0, tid);
+  ly.store(ys0, tid);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) {
+      lx.load(X, d.ldx, p0, (kt + 1) * kBR, d.P, d.R, tid);
+      ly.load(Y, d.ldy, q0, (kt + 1) * kBR, d.Q, d.R, tid);
+    }
+    const float *xl = (kt & 1) ? xs1 : xs0;
+    const float *yl = (kt & 1) ? ys1 : ys0;
+#pragma unroll
+    for (int g = 0; g < kBR / 8; ++g) {
+      const f4 a0 = frag<XRC>(xl, wp * 64, c, h, g);
+      const f4 a1 = frag<XRC>(xl, wp * 64 + 32, c, h, g);
+      const f4 b0 = frag<YRC>(yl, wq * 64, c, h, g);
+      const f4 b1 = frag<YRC>(yl, wq * 64 + 32, c, h, g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc00, 0, 0, 0);
+        acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b1[j], acc01, 0, 0, 0);
+        acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b0[j], acc10, 0, 0, 0);
+        acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc11, 0, 0, 0);
+      }
+    }
+    if (more) {
+      lx.store((kt & 1) ? xs0 : xs1, tid);
+      ly.store((kt & 1) ? ys0 : ys1, tid);
+    }
+    __syncthreads();
+  }
+
+  // 32x32 accumulator layout: lane (h, c), register i holds
+  // row 8*(i/4) + 4*h + (i%4), column c.
+  const f16v *accs[4] = {&acc00, &acc01, &acc10, &acc11};
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int bi = blk >> 1, bj = blk & 1;
+    const int q = q0 + wq * 64 + bj * 32 + c;
+    const f16v &a = *accs[blk];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int p = p0 + wp * 64 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+      if (p < d.P && q < d.Q) {
+        float *dst = C + (int64_t)p * d.ldc + q;
+        *dst = d.accumulate ? *dst + a[i] : a[i];
+      }
+    }
+  }
+}
+
+// Maps the hardware workgroup id to a logical tile so that XCD k (which
+// receives ids k, k+8, k+16, ...) owns logical tiles [k*n/8, (k+1)*n/8).
+__device__ __forceinline__ int xcd_tile(int b, int n) {
+  if ((n & 7) != 0) return b;
+  return (b & 7) * (n >> 3) + (b >> 3);
+}
+
+template <bool XRC, bool YRC, bool VEC>
+__global__ void __launch_bounds__(kThreads) gemm_kernel(Gemm d) {
+  __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  gemm_tile<XRC, YRC, VEC>(d, tile, blockIdx.y, smem);
+}
+
+// dA (NT) and dB (TN) of matmul_backward in one grid: logical tiles
+// [0, tiles_a) are dA tiles, the rest dB tiles.
+template <bool VEC>
+__global__ void __launch_bounds__(kThreads) matmul_backward_kernel(Gemm da, Gemm db, int tiles_a) {
+  __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    gemm_tile<true, true, VEC>(da, tile, blockIdx.y, smem);
+  else
+    gemm_tile<false, false, VEC>(db, tile - tiles_a, blockIdx.y, smem);
+}
+
+int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
+
+// Vector (float4) loads need 16-byte aligned bases, leading dimensions and
+// contiguous extents that are multiples of 4.
+bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
+  auto ok = [](const void *p, int64_t ld, int64_t bs, int64_t contig) {
+    return numrs_hip::aligned16(p) && (ld & 3) == 0 && (bs & 3) == 0 && (contig & 3) == 0;
+  };
+  return ok(d.X, d.ldx, d.bsx, xrc ? d.R : d.P) && ok(d.Y, d.ldy, d.bsy, yrc ? d.R : d.Q);
+}
+
+int check_dims(numrs_hip_ctx *ctx, const char *who, int64_t batch, int64_t M, int64_t K,
+               int64_t N) {
+  if (batch < 0 || M < 0 || K < 0 || N < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative dimension", who);
+  const int64_t lim = (int64_t)1 << 30;
+  if (M >= lim || K >= lim || N >= lim || batch >= 65536)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: dimension too large", who);
+  return NUMRS_HIP_OK;
+}
+
+Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, int64_t ldc,
+          int64_t bsx, int64_t bsy, int64_t bsc, int64_t P, int64_t Q, int64_t R, int acc) {
+  Gemm g;
+  g.X = X;
+  g.Y = Y;
+  g.C = C;
+  g.ldx = ldx;
+  g.ldy = ldy;
+  g.ldc = ldc;
+  g.bsx = bsx;
+  g.bsy = bsy;
+  g.bsc = bsc;
+  g.P = (int)P;
+  g.Q = (int)Q;
+  g.R = (int)R;
+  g.tiles_p = tiles(P);
+  g.tiles_q = tiles(Q);
+  g.accumulate = acc;
+  return g;
+}
+
+// Zero-length reduction: C = 0 (or unchanged when accumulating).
+int zero_output(numrs_hip_ctx *ctx, float *C, int64_t count, int acc) {
+  if (acc || count == 0) return NUMRS_HIP_OK;
+  return numrs_hip_fill(ctx, C, count, 0.0f);
+}
+
+template <bool XRC, bool YRC>
+int launch_one(numrs_hip_ctx *ctx, const Gemm &g, int64_t batch) {
+  const int64_t n_tiles = (int64_t)g.tiles_p * g.tiles_q;
+  if (n_tiles == 0 || batch == 0) return NUMRS_HIP_OK;
+  if (n_tiles > 0x7fffffff)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "gemm: too many tiles");
+  dim3 grid((unsigned)n_tiles, (unsigned)batch);
+  if (vec_ok(g, XRC, YRC))
+    gemm_kernel<XRC, YRC, true><<<grid, kThreads, 0, ctx->stream>>>(g);
+  else
+    gemm_kernel<XRC, YRC, false><<<grid, kThreads, 0, ctx->stream>>>(g);
+  return numrs_hip::check_launch(ctx, "gemm_kernel");
+}
+
+int gemm_dispatch(numrs_hip_ctx *ctx, const Gemm &g, int64_t batch, bool xrc, bool yrc) {
+  if (xrc && yrc) return launch_one<true, true>(ctx, g, batch);
+  if (xrc && !yrc) return launch_one<true, false>(ctx, g, batch);
+  if (!xrc && yrc) return launch_one<false, true>(ctx, g, batch);
+  return launch_one<false, false>(ctx, g, batch);
+}
+
+int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, const float *B,
+                         float *dA, float *dB, int64_t batch, int64_t M, int64_t K, int64_t N,
+                         int64_t sa, int64_t sb, int64_t sc, int acc) {
+  const char *who = "numrs_hip_matmul_backward";
+  int rc = check_dims(ctx, who, batch, M, K, N);
+  if (rc) return rc;
+  if (dA == nullptr && dB == nullptr) return NUMRS_HIP_OK;
+  if (dC == nullptr || (dA != nullptr && B == nullptr) || (dB != nullptr && A == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input pointer", who);
+  if (batch == 0 || M == 0 || K == 0 || N == 0) {
+    // Empty reduction dimension gives zero gradients.
+    for (int64_t b = 0; b < batch; ++b) {
+      if (dA) rc = zero_output(ctx, dA + b * sa, M * K, acc);
+      if (!rc && dB) rc = zero_output(ctx, dB + b * sb, K * N, acc);
+      if (rc) return rc;
+    }
+    return NUMRS_HIP_OK;
+  }
+  // dA[M,K] = dC[M,N] @ B[K,N]^T : P=M, Q=K, R=N, X=dC (ld N), Y=B (ld N)
+  Gemm ga = make(dC, B, dA, N, N, K, sc, sb, sa, M, K, N, acc);
+  // dB[K,N] = A[M,K]^T @ dC[M,N] : P=K, Q=N, R=M, X=A (ld K), Y=dC (ld N)
+  Gemm gb = make(A, dC, dB, K, N, N, sa, sc, sb, K, N, M, acc);
+  if (dA == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
+  if (dB == nullptr) return gemm_dispatch(ctx, ga, batch, true, true);
+  const int64_t ta = (int64_t)ga.tiles_p * ga.tiles_q;
+  const int64_t tb = (int64_t)gb.tiles_p * gb.tiles_q;
+  if (ta + tb > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);
+  dim3 grid((unsigned)(ta + tb), (unsigned)batch);
+  if (vec_ok(ga, true, true) && vec_ok(gb, false, false))
+    matmul_backward_kernel<true><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
+  else
+    matmul_backward_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
+  return numrs_hip::check_launch(ctx, "matmul_backward_kernel");
+}
+
+int matmul_impl(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, int64_t batch,
+                int64_t M, int64_t K, int64_t N, int64_t sa, int64_t sb, int64_t sc, int ta,
+                int tb, int acc) {
+  const char *who = "numrs_hip_matmul";
+  int rc = check_dims(ctx, who, batch, M, K, N);
+  if (rc) return rc;
+  if (batch == 0 || M == 0 || N == 0) return NUMRS_HIP_OK;
+  if (C == nullptr || ((A == nullptr || B == nullptr) && K > 0))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (K == 0) {
+    for (int64_t b = 0; b < batch; ++b)
+      if ((rc = zero_output(ctx, C + b * sc, M * N, acc))) return rc;
+    return NUMRS_HIP_OK;
+  }
+  // op(A)[M,K]: R-contiguous unless transposed (stored [K,M]).
+  const bool xrc = !ta;
+  const int64_t ldx = ta ? M : K;
+  // op(B)[K,N]: Q-contiguous unless transposed (stored [N,K], R-contiguous).
+  const bool yrc = tb != 0;
+  const int64_t ldy = tb ? K : N;
+  Gemm g = make(A, B, C, ldx, ldy, N, sa, sb, sc, M, N, K, acc);
+  return gemm_dispatch(ctx, g, batch, xrc, yrc);
+}
+
+}  // namespace
+
+extern "C" {
+
+int numrs_hip_matmul_backward(numrs_hip_ctx *ctx, const float *dC, const float *A,
+                              const float *B, float *dA, float *dB, int64_t M, int64_t K,
+                              int64_t N, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  return matmul_backward_impl(ctx, dC, A, B, dA, dB, 1, M, K, N, 0, 0, 0, accumulate);
+}
+
+int numrs_hip_matmul_backward_batched(numrs_hip_ctx *ctx, const float *dC, const float *A,
+                                      const float *B, float *dA, float *dB, int64_t batch,
+                                      int64_t M, int64_t K, int64_t N, int64_t stride_a,
+                                      int64_t stride_b, int64_t stride_c, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (stride_a < 0 || stride_b < 0 || stride_c < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "negative batch stride");
+  return matmul_backward_impl(ctx, dC, A, B, dA, dB, batch, M, K, N, stride_a, stride_b,
+                              stride_c, accumulate);
+}
+
+int numrs_hip_matmul(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, int64_t M,
+                     int64_t K, int64_t N, int trans_a, int trans_b, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  return matmul_impl(ctx, A, B, C, 1, M, K, N, 0, 0, 0, trans_a, trans_b, accumulate);
+}
+
+int numrs_hip_matmul_batched(numrs_hip_ctx *ctx, const float *A, const float *B, float *C,
+                             int64_t batch, int64_t M, int64_t K, int64_t N, int64_t stride_a,
+                             int64_t stride_b, int64_t stride_c, int trans_a, int trans_b,
+                             int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (stride_a < 0 || stride_b < 0 || stride_c < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "negative batch stride");
+  return matmul_impl(ctx, A, B, C, batch, M, K, N, stride_a, stride_b, stride_c, trans_a,
+                     trans_b, accumulate);
+}
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+// Context, device memory, workspace, timing and error reporting.
+#include <cstring>
+#include <string>
+
+#include "common.h"
+
+namespace numrs_hip {
+
+int fail(numrs_hip_ctx *ctx, int code, const char *fmt, ...) {
+  if (ctx != nullptr) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(ctx->last_error, sizeof(ctx->last_error), fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out) {
+  if (bytes <= ctx->workspace_bytes && ctx->workspace != nullptr) {
+    *out = ctx->workspace;
+    return NUMRS_HIP_OK;
+  }
+  // Growing: earlier kernels may still read the old buffer, so drain first.
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (ctx->workspace != nullptr) NRS_HIP(ctx, hipFree(ctx->workspace));
+  ctx->workspace = nullptr;
+  ctx->workspace_bytes = 0;
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  if (hipMalloc(&ctx->workspace, want) != hipSuccess) {
+    ctx->workspace = nullptr;
+    return fail(ctx, NUMRS_HIP_E_NOMEM, "workspace allocation of %zu bytes failed", want);
+  }
+  ctx->workspace_bytes = want;
+  *out = ctx->workspace;
+  return NUMRS_HIP_OK;
+}
+
+int check_launch(numrs_hip_ctx *ctx, const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(ctx, NUMRS_HIP_E_HIP, "launch of %s failed: %s", what, hipGetErrorString(e));
+  return NUMRS_HIP_OK;
+}
+
+}  // namespace numrs_hip
+
+using numrs_hip::fail;
+
+static thread_local char g_create_error[512] = {0};
+
+namespace {
+
+__global__ void fill_kernel(float *__restrict__ dst, int64_t n, float value) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = value;
+}
+
+}  // namespace
+
+extern "C" {
+
+int numrs_hip_create(int device, numrs_hip_ctx **out) {
+  g_create_error[0] = 0;
+  if (out == nullptr) return NUMRS_HIP_E_INVALID;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= device || device < 0) {
+    snprintf(g_create_error, sizeof(g_create_error), "no HIP device %d (count %d)", device, count);
+    return NUMRS_HIP_E_NODEV;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+    snprintf(g_create_error, sizeof(g_create_error), "hipGetDeviceProperties(%d) failed", device);
+    return NUMRS_HIP_E_NODEV;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    snprintf(g_create_error, sizeof(g_create_error),
+             "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    return NUMRS_HIP_E_NODEV;
+  }
+  auto *ctx = new numrs_hip_ctx();
+  ctx->device = device;
+  ctx->num_cus = prop.multiProcessorCount;
+  std::strncpy(ctx->arch, prop.gcnArchName, sizeof(ctx->arch) - 1);
+  if (hipSetDevice(device) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+    snprintf(g_create_error, sizeof(g_create_error), "stream creation on device %d failed",
+             device);
+    delete ctx;
+    return NUMRS_HIP_E_HIP;
+  }
+  for (int i = 0; i < kMaxTimers; ++i) {
+    if (hipEventCreate(&ctx->events[i]) != hipSuccess) {
+      snprintf(g_create_error, sizeof(g_create_error), "hipEventCreate failed");
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ctx->events[j]);
+      (void)hipStreamDestroy(ctx->stream);
+      delete ctx;
+      return NUMRS_HIP_E_HIP;
+    }
+  }
+  *out = ctx;
+  return NUMRS_HIP_OK;
+}
+
+const char *numrs_hip_create_error(void) { return g_create_error; }
+
+int numrs_hip_destroy(numrs_hip_ctx *ctx) {
+  NRS_CHECK_CTX(ctx);
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (int i = 0; i < kMaxTimers; ++i) (void)hipEventDestroy(ctx->events[i]);
+  if (ctx->workspace != nullptr) (void)hipFree(ctx->workspace);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return NUMRS_HIP_OK;
+}
+
+const char *numrs_hip_last_error(numrs_hip_ctx *ctx) {
+  return ctx == nullptr ? "null context" : ctx->last_error;
+}
+
+int numrs_hip_device_info(numrs_hip_ctx *ctx, int *num_cus, char *arch, size_t arch_len) {
+  NRS_CHECK_CTX(ctx);
+  if (num_cus != nullptr) *num_cus = ctx->num_cus;
+  if (arch != nullptr && arch_len > 0) {
+    std::strncpy(arch, ctx->arch, arch_len - 1);
+    arch[arch_len - 1] = 0;
+  }
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_malloc(numrs_hip_ctx *ctx, size_t bytes, void **dptr) {
+  NRS_CHECK_CTX(ctx);
+  if (dptr == nullptr) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_malloc: null out pointer");
+  *dptr = nullptr;
+  NRS_HIP(ctx, hipSetDevice(ctx->device));
+  if (bytes == 0) return NUMRS_HIP_OK;
+  if (hipMalloc(dptr, bytes) != hipSuccess) {
+    *dptr = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, NUMRS_HIP_E_NOMEM, "hipMalloc of %zu bytes failed", bytes);
+  }
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_free(numrs_hip_ctx *ctx, void *dptr) {
+  NRS_CHECK_CTX(ctx);
+  if (dptr == nullptr) return NUMRS_HIP_OK;
+  NRS_HIP(ctx, hipFree(dptr));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_upload(numrs_hip_ctx *ctx, void *dst, const void *host_src, size_t bytes) {
+  NRS_CHECK_CTX(ctx);
+  if (bytes == 0) return NUMRS_HIP_OK;
+  if (dst == nullptr || host_src == nullptr)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_upload: null pointer");
+  NRS_HIP(ctx, hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_download(numrs_hip_ctx *ctx, void *host_dst, const void *src, size_t bytes) {
+  NRS_CHECK_CTX(ctx);
+  if (bytes == 0) return NUMRS_HIP_OK;
+  if (host_dst == nullptr || src == nullptr)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_download: null pointer");
+  NRS_HIP(ctx, hipMemcpyAsync(host_dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_copy(numrs_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  NRS_CHECK_CTX(ctx);
+  if (bytes == 0) return NUMRS_HIP_OK;
+  if (dst == nullptr || src == nullptr)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_copy: null pointer");
+  NRS_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_fill(numrs_hip_ctx *ctx, float *dst, int64_t n, float value) {
+  NRS_CHECK_CTX(ctx);
+  if (n < 0) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_fill: negative size");
+  if (n == 0) return NUMRS_HIP_OK;
+  if (dst == nullptr) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_fill: null pointer");
+  unsigned grid = grid_for(n, 256);
+  if (grid > 65536) grid = 65536;
+  fill_kernel<<<grid, 256, 0, ctx->stream>>>(dst, n, value);
+  return numrs_hip::check_launch(ctx, "fill_kernel");
+}
+
+int numrs_hip_sync(numrs_hip_ctx *ctx) {
+  NRS_CHECK_CTX(ctx);
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_reserve(numrs_hip_ctx *ctx, size_t bytes) {
+  NRS_CHECK_CTX(ctx);
+  void *p = nullptr;
+  return numrs_hip::workspace(ctx, bytes, &p);
+}
+
+void *numrs_hip_stream(numrs_hip_ctx *ctx) {
+  return ctx == nullptr ? nullptr : static_cast<void *>(ctx->stream);
+}
+
+int numrs_hip_timer_record(numrs_hip_ctx *ctx, int slot) {
+  NRS_CHECK_CTX(ctx);
+  if (slot < 0 || slot >= kMaxTimers)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "timer slot %d outside [0,%d)", slot, kMaxTimers);
+  NRS_HIP(ctx, hipEventRecord(ctx->events[slot], ctx->stream));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_timer_elapsed_ms(numrs_hip_ctx *ctx, int slot_start, int slot_end, float *ms) {
+  NRS_CHECK_CTX(ctx);
+  if (ms == nullptr || slot_start < 0 || slot_start >= kMaxTimers || slot_end < 0 ||
+      slot_end >= kMaxTimers)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "bad timer slots %d,%d", slot_start, slot_end);
+  NRS_HIP(ctx, hipEventSynchronize(ctx->events[slot_end]));
+  NRS_HIP(ctx, hipEventElapsedTime(ms, ctx->events[slot_start], ctx->events[slot_end]));
+  return NUMRS_HIP_OK;
+}
+
+}  // extern "C"

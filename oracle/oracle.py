@@ -1,0 +1,397 @@
+"""numpy-facing wrapper of the C oracle (oracle/numrs_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker.  The product library never
+imports this module.  Every function forwards to the C restatement, which cites
+the numrs reference file:line it follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "build", "liboracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_SO):
+            build()
+        _lib = ctypes.CDLL(_SO)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L) -> None:
+    sig = {
+        "orc_sum_avx2_order": (_f32, [_f32p, _i64]),
+        "orc_sum_seq": (_f32, [_f32p, _i64]),
+        "orc_sum_rows_avx2_order": (None, [_f32p, _i64, _i64, _f32p]),
+        "orc_transpose": (None, [_f32p, _i64, _i64, _f32p]),
+        "orc_accumulate": (None, [_f32p, _i64, _f32p, _i64]),
+        "orc_matmul_backward_rows": (None, [_f32p] * 5 + [_i64] * 7),
+        "orc_matmul_backward": (None, [_f32p] * 5 + [_i64] * 3),
+        "orc_matmul_backward_f64_rows": (None, [_f32p] * 5 + [_i64] * 7 + [_f64p]),
+        "orc_matmul_backward_f64": (None, [_f32p] * 5 + [_i64] * 3 + [_f64p]),
+        "orc_matmul_f64": (None, [_f32p] * 3 + [_i64] * 3 + [_f64p]),
+        "orc_relu_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_sigmoid_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_exp_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_log_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_tanh_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_tan_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_pow_backward": (None, [_f32p, _f32p, _f32, _f32p, _i64]),
+        "orc_sqrt_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_sin_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_cos_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_sub_backward": (None, [_f32p] * 3 + [_i64]),
+        "orc_mul_backward": (None, [_f32p] * 5 + [_i64]),
+        "orc_div_backward": (None, [_f32p] * 5 + [_i64]),
+        "orc_sum_backward": (None, [_f32, _f32p, _i64]),
+        "orc_mean_backward": (None, [_f32, _f32p, _i64]),
+        "orc_mse_backward": (None, [_f32, _f32p, _f32p, _f32p, _f32p, _i64]),
+        "orc_mse_loss": (_f32, [_f32p, _f32p, _i64]),
+        "orc_mean_fwd": (_f32, [_f32p, _i64]),
+        "orc_cross_entropy_backward": (None, [_f32, _f32p, _f32p, _f32p, _i64, _i64]),
+        "orc_cross_entropy_loss": (_f32, [_f32p, _f32p, _i64, _i64]),
+        "orc_softmax_backward": (None, [_f32p, _f32p, _f32p, _i64, _i64, _f32p]),
+        "orc_unbroadcast_reference_accumulate": (None, [_f32p, _i64, _f32p]),
+        "orc_sum_to_shape_f64": (ctypes.c_int, [_f32p, _i64p, ctypes.c_int, _f32p, _i64p,
+                                                ctypes.c_int, _f64p]),
+        "orc_powi": (_f32, [_f32, ctypes.c_int]),
+        "orc_sgd_step": (None, [_f32p, _f32p, _f32p, _i64, _f32, _f32, _f32]),
+        "orc_adam_step": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _f32, _f32, _f32, _f32,
+                                 _f32, ctypes.c_int]),
+        "orc_argmax_rows": (None, [_f32p, _i64, _i64, _i32p, ctypes.c_int]),
+        "orc_relu": (None, [_f32p, _f32p, _i64]),
+        "orc_sigmoid": (None, [_f32p, _f32p, _i64]),
+        "orc_gelu_backward_f64": (None, [_f32p] * 3 + [_i64]),
+        "orc_gelu_f64": (None, [_f32p, _f32p, _i64]),
+        "orc_layernorm_fwd_f64": (None, [_f32p] * 6 + [_i64, _i64, _f32]),
+        "orc_layernorm_backward_f64": (None, [_f32p] * 6 + [_i64, _i64, _f32, _f64p]),
+        "orc_softmax_rows_f64": (None, [_f32p, _f32p, _i64, _i64]),
+        "orc_softmax_backward_f64": (None, [_f32p] * 3 + [_i64, _i64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a, ctype=_f32p):
+    return None if a is None else a.ctypes.data_as(ctype)
+
+
+def _f(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# --- reductions -------------------------------------------------------------
+
+def sum_avx2_order(x) -> np.float32:
+    x = _f(x)
+    return np.float32(lib().orc_sum_avx2_order(_p(x), x.size))
+
+
+def sum_seq(x) -> np.float32:
+    x = _f(x)
+    return np.float32(lib().orc_sum_seq(_p(x), x.size))
+
+
+def transpose(x) -> np.ndarray:
+    x = _f(x)
+    r, c = x.shape
+    y = np.empty((c, r), np.float32)
+    lib().orc_transpose(_p(x), r, c, _p(y))
+    return y
+
+
+def accumulate(dst: np.ndarray, src) -> None:
+    src = _f(src)
+    lib().orc_accumulate(_p(dst), dst.size, _p(src), src.size)
+
+
+# --- matmul -----------------------------------------------------------------
+
+def matmul_backward(dC, A, B, need_a=True, need_b=True, f64=False, rows_a=None, rows_b=None):
+    """(dA, dB) = (dC @ B^T, A^T @ dC).  f64=False is the fp32 loop of
+    backward.rs:123-146; f64=True accumulates in float64.  rows_a/rows_b
+    restrict the computed rows (others stay NaN)."""
+    dC, A, B = _f(dC), _f(A), _f(B)
+    M, K = A.shape
+    N = B.shape[1]
+    assert B.shape[0] == K and dC.shape == (M, N)
+    dA = np.full((M, K), np.nan, np.float32) if need_a else None
+    dB = np.full((K, N), np.nan, np.float32) if need_b else None
+    a0, a1 = rows_a if rows_a is not None else (0, M)
+    b0, b1 = rows_b if rows_b is not None else (0, K)
+    if f64:
+        work = np.empty(max(K, N), np.float64)
+        lib().orc_matmul_backward_f64_rows(_p(dC), _p(A), _p(B), _p(dA), _p(dB), M, K, N,
+                                           a0, a1, b0, b1, _p(work, _f64p))
+    else:
+        lib().orc_matmul_backward_rows(_p(dC), _p(A), _p(B), _p(dA), _p(dB), M, K, N,
+                                       a0, a1, b0, b1)
+    return dA, dB
+
+
+def matmul_f64(A, B) -> np.ndarray:
+    A, B = _f(A), _f(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    work = np.empty(N, np.float64)
+    lib().orc_matmul_f64(_p(A), _p(B), _p(C), M, K, N, _p(work, _f64p))
+    return C
+
+
+# --- elementwise backward ---------------------------------------------------
+
+def _unary(name, g, x):
+    g, x = _f(g), _f(x)
+    dx = np.empty_like(g)
+    getattr(lib(), name)(_p(g), _p(x), _p(dx), g.size)
+    return dx
+
+
+def relu_backward(g, x):
+    return _unary("orc_relu_backward", g, x)
+
+
+def sigmoid_backward(g, s):
+    return _unary("orc_sigmoid_backward", g, s)
+
+
+def exp_backward(g, e):
+    return _unary("orc_exp_backward", g, e)
+
+
+def log_backward(g, x):
+    return _unary("orc_log_backward", g, x)
+
+
+def tanh_backward(g, y):
+    return _unary("orc_tanh_backward", g, y)
+
+
+def tan_backward(g, t):
+    return _unary("orc_tan_backward", g, t)
+
+
+def sqrt_backward(g, x):
+    return _unary("orc_sqrt_backward", g, x)
+
+
+def sin_backward(g, x):
+    return _unary("orc_sin_backward", g, x)
+
+
+def cos_backward(g, x):
+    return _unary("orc_cos_backward", g, x)
+
+
+def gelu_backward(g, x):
+    return _unary("orc_gelu_backward_f64", g, x)
+
+
+def pow_backward(g, x, expo):
+    g, x = _f(g), _f(x)
+    dx = np.empty_like(g)
+    lib().orc_pow_backward(_p(g), _p(x), float(expo), _p(dx), g.size)
+    return dx
+
+
+def sub_backward(g):
+    g = _f(g)
+    dx, dy = np.empty_like(g), np.empty_like(g)
+    lib().orc_sub_backward(_p(g), _p(dx), _p(dy), g.size)
+    return dx, dy
+
+
+def mul_backward(g, x, y):
+    g, x, y = _f(g), _f(x), _f(y)
+    dx, dy = np.empty_like(g), np.empty_like(g)
+    lib().orc_mul_backward(_p(g), _p(x), _p(y), _p(dx), _p(dy), g.size)
+    return dx, dy
+
+
+def div_backward(g, x, y):
+    g, x, y = _f(g), _f(x), _f(y)
+    dx, dy = np.empty_like(g), np.empty_like(g)
+    lib().orc_div_backward(_p(g), _p(x), _p(y), _p(dx), _p(dy), g.size)
+    return dx, dy
+
+
+def sum_backward(g0, shape):
+    dx = np.empty(shape, np.float32)
+    lib().orc_sum_backward(float(g0), _p(dx), dx.size)
+    return dx
+
+
+def mean_backward(g0, shape):
+    dx = np.empty(shape, np.float32)
+    lib().orc_mean_backward(float(g0), _p(dx), dx.size)
+    return dx
+
+
+def mse_backward(g0, p, t):
+    p, t = _f(p), _f(t)
+    dp, dt = np.empty_like(p), np.empty_like(p)
+    lib().orc_mse_backward(float(g0), _p(p), _p(t), _p(dp), _p(dt), p.size)
+    return dp, dt
+
+
+def mse_loss(p, t) -> np.float32:
+    p, t = _f(p), _f(t)
+    return np.float32(lib().orc_mse_loss(_p(p), _p(t), p.size))
+
+
+def mean_fwd(x) -> np.float32:
+    x = _f(x)
+    return np.float32(lib().orc_mean_fwd(_p(x), x.size))
+
+
+def cross_entropy_backward(g0, logits, onehot):
+    x, t = _f(logits), _f(onehot)
+    B, C = x.shape
+    dx = np.empty_like(x)
+    lib().orc_cross_entropy_backward(float(g0), _p(x), _p(t), _p(dx), B, C)
+    return dx
+
+
+def cross_entropy_loss(logits, onehot) -> np.float32:
+    x, t = _f(logits), _f(onehot)
+    B, C = x.shape
+    return np.float32(lib().orc_cross_entropy_loss(_p(x), _p(t), B, C))
+
+
+def softmax_backward(y, g, f64=False):
+    y, g = _f(y), _f(g)
+    rows, cols = y.shape
+    dx = np.empty_like(y)
+    if f64:
+        lib().orc_softmax_backward_f64(_p(y), _p(g), _p(dx), rows, cols)
+    else:
+        work = np.empty(cols, np.float32)
+        lib().orc_softmax_backward(_p(y), _p(g), _p(dx), rows, cols, _p(work))
+    return dx
+
+
+def softmax_rows(x):
+    x = _f(x)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    lib().orc_softmax_rows_f64(_p(x), _p(y), rows, cols)
+    return y
+
+
+# --- unbroadcast --------------------------------------------------------------
+
+def unbroadcast_reference_accumulate(g, out_grad: np.ndarray) -> None:
+    """REFERENCE mode (backward.rs:12-39 + tensor.rs:120-132): sum into element 0."""
+    g = _f(g)
+    lib().orc_unbroadcast_reference_accumulate(_p(g), g.size, _p(out_grad))
+
+
+def sum_to_shape(g, shape):
+    g = _f(g)
+    gshape = np.array(g.shape, np.int64)
+    oshape = np.array(shape, np.int64)
+    out = np.empty(shape, np.float32)
+    work = np.empty(max(out.size, 1), np.float64)
+    rc = lib().orc_sum_to_shape_f64(_p(g), _p(gshape, _i64p), g.ndim, _p(out),
+                                    _p(oshape, _i64p), len(shape), _p(work, _f64p))
+    if rc != 0:
+        raise ValueError(f"cannot sum {g.shape} to {tuple(shape)}")
+    return out
+
+
+# --- optimizers -----------------------------------------------------------------
+
+def powi(a: float, t: int) -> np.float32:
+    return np.float32(lib().orc_powi(float(a), int(t)))
+
+
+def sgd_step(p: np.ndarray, g, v: np.ndarray | None, lr, mu=0.0, wd=0.0) -> None:
+    g = _f(g)
+    lib().orc_sgd_step(_p(p), _p(g), _p(v), p.size, lr, mu, wd)
+
+
+def adam_step(p: np.ndarray, g, m: np.ndarray, v: np.ndarray, t: int, lr=1e-3, b1=0.9,
+              b2=0.999, eps=1e-8, wd=0.0) -> None:
+    g = _f(g)
+    lib().orc_adam_step(_p(p), _p(g), _p(m), _p(v), p.size, lr, b1, b2, eps, wd, int(t))
+
+
+# --- integer paths ----------------------------------------------------------------
+
+def argmax_rows(x, tie_last=False) -> np.ndarray:
+    x = _f(x)
+    rows, cols = x.shape
+    idx = np.empty(rows, np.int32)
+    lib().orc_argmax_rows(_p(x), rows, cols, _p(idx, _i32p), int(tie_last))
+    return idx
+
+
+# --- forward helpers -----------------------------------------------------------------
+
+def relu(x):
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().orc_relu(_p(x), _p(y), x.size)
+    return y
+
+
+def sigmoid(x):
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().orc_sigmoid(_p(x), _p(y), x.size)
+    return y
+
+
+def gelu(x):
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().orc_gelu_f64(_p(x), _p(y), x.size)
+    return y
+
+
+def layernorm_fwd(x, gamma, beta, eps=1e-5):
+    x, gamma, beta = _f(x), _f(gamma), _f(beta)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    mean = np.empty(rows, np.float32)
+    rstd = np.empty(rows, np.float32)
+    lib().orc_layernorm_fwd_f64(_p(x), _p(gamma), _p(beta), _p(y), _p(mean), _p(rstd),
+                                rows, cols, eps)
+    return y, mean, rstd
+
+
+def layernorm_backward(g, x, gamma, eps=1e-5):
+    g, x, gamma = _f(g), _f(x), _f(gamma)
+    rows, cols = x.shape
+    dx = np.empty_like(x)
+    dgamma = np.empty(cols, np.float32)
+    dbeta = np.empty(cols, np.float32)
+    work = np.empty(2 * cols, np.float64)
+    lib().orc_layernorm_backward_f64(_p(g), _p(x), _p(gamma), _p(dx), _p(dgamma), _p(dbeta),
+                                     rows, cols, eps, _p(work, _f64p))
+    return dx, dgamma, dbeta

@@ -1,0 +1,447 @@
+"""GPU parity: every HIP kernel against the CPU oracle on identical seeded inputs.
+
+Bars (north star): bit-exact for select/multiply/divide/sqrt kernels, the
+optimizers and every integer path; |g - r| <= 1e-5 + 1e-4|r| against the
+float64-accumulated oracle for reductions and contractions, whose summation
+order differs from the reference's.  Full BASELINE sizes are checked through
+sampled rows plus size-independent identities (checksums of checksums,
+exact power-of-two linearity).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from numrs_amd import HipError
+from numrs_amd import _lib as L
+from oracle import oracle as O
+from tests.conftest import assert_bits, assert_close, rand
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def rng():
+    return np.random.default_rng(20261201)
+
+
+# ---------------------------------------------------------------------------
+# matmul_backward (backward.rs:113-149)
+# ---------------------------------------------------------------------------
+
+SMALL_GEMMS = [(1, 1, 1), (2, 2, 2), (5, 3, 7), (64, 784, 128), (64, 128, 10), (130, 70, 257),
+               (128, 128, 128), (256, 96, 192), (33, 1, 65), (1, 300, 1), (300, 4, 260)]
+
+
+@pytest.mark.parametrize("M,K,N", SMALL_GEMMS)
+def test_matmul_backward_small(hip_ctx, rng, M, K, N):
+    say(f"matmul_backward M={M} K={K} N={N}")
+    A, B, dC = rand(rng, (M, K)), rand(rng, (K, N)), rand(rng, (M, N))
+    dA_ref, dB_ref = O.matmul_backward(dC, A, B, f64=True)
+    c = hip_ctx
+    dA, dB = c.empty((M, K)), c.empty((K, N))
+    c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), dA, dB)
+    assert_close(dA.numpy(), dA_ref, what="dA")
+    assert_close(dB.numpy(), dB_ref, what="dB")
+
+
+def test_matmul_backward_kat(hip_ctx):
+    # numrs-core/tests/autograd_matmul.rs:6-47
+    c = hip_ctx
+    A = c.to_device(np.array([[1, 2], [3, 4]], np.float32))
+    B = c.to_device(np.eye(2, dtype=np.float32))
+    dC = c.to_device(np.ones((2, 2), np.float32))
+    dA, dB = c.empty((2, 2)), c.empty((2, 2))
+    c.matmul_backward(dC, A, B, dA, dB)
+    assert dA.numpy().ravel().tolist() == [1, 1, 1, 1]
+    assert dB.numpy().ravel().tolist() == [4, 4, 6, 6]
+
+
+def test_matmul_backward_accumulate_and_skip(hip_ctx, rng):
+    M, K, N = 96, 160, 72
+    say("matmul_backward accumulate/skip")
+    A, B, dC = rand(rng, (M, K)), rand(rng, (K, N)), rand(rng, (M, N))
+    ga, gb = rand(rng, (M, K)), rand(rng, (K, N))
+    dA_ref, dB_ref = O.matmul_backward(dC, A, B, f64=True)
+    c = hip_ctx
+    dA, dB = c.to_device(ga), c.to_device(gb)
+    dCd, Ad, Bd = c.to_device(dC), c.to_device(A), c.to_device(B)
+    c.matmul_backward(dCd, Ad, Bd, dA, dB, accumulate=True)
+    assert_close(dA.numpy(), ga.astype(np.float64) + dA_ref, what="dA acc")
+    assert_close(dB.numpy(), gb.astype(np.float64) + dB_ref, what="dB acc")
+    only_b = c.to_device(np.full((K, N), 7.0, np.float32))
+    c.matmul_backward(dCd, Ad, None, None, only_b)
+    assert_close(only_b.numpy(), dB_ref, what="dB only")
+    only_a = c.empty((M, K))
+    c.matmul_backward(dCd, None, Bd, only_a, None)
+    assert_close(only_a.numpy(), dA_ref, what="dA only")
+
+
+def _checksums(dC, A, B):
+    """sum(dA) and sum(dB) from O(n^2) float64 identities:
+    sum_ij (dC B^T)_ij = sum_l (sum_i dC_il)(sum_j B_jl);
+    sum_ij (A^T dC)_ij = sum_l (sum_i A_li)(sum_j dC_lj)."""
+    d = dC.astype(np.float64)
+    sa = float(d.sum(0) @ B.astype(np.float64).sum(0))
+    sb = float(A.astype(np.float64).sum(1) @ d.sum(1))
+    return sa, sb
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 2048), (4096, 1024, 4096)])
+def test_matmul_backward_baseline_sizes(hip_ctx, rng, M, K, N):
+    say(f"matmul_backward baseline M={M} K={K} N={N}")
+    A, B, dC = rand(rng, (M, K)), rand(rng, (K, N)), rand(rng, (M, N))
+    c = hip_ctx
+    dCd, Ad, Bd = c.to_device(dC), c.to_device(A), c.to_device(B)
+    dA, dB = c.empty((M, K)), c.empty((K, N))
+    c.matmul_backward(dCd, Ad, Bd, dA, dB)
+    ga, gb = dA.numpy(), dB.numpy()
+    # Sampled rows against the float64 oracle: first/last rows of tiles and XCD groups.
+    for r0 in (0, 127, 128, 1023, M - 2):
+        ra, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=(r0, r0 + 2))
+        assert_close(ga[r0:r0 + 2], ra[r0:r0 + 2], what=f"dA rows {r0}")
+    for r0 in (0, 129, K // 2, K - 2):
+        _, rb = O.matmul_backward(dC, A, B, need_a=False, f64=True, rows_b=(r0, r0 + 2))
+        assert_close(gb[r0:r0 + 2], rb[r0:r0 + 2], what=f"dB rows {r0}")
+    # Whole-output identities.
+    sa, sb = _checksums(dC, A, B)
+    assert abs(ga.astype(np.float64).sum() - sa) <= 1e-4 * np.abs(ga).sum()
+    assert abs(gb.astype(np.float64).sum() - sb) <= 1e-4 * np.abs(gb).sum()
+    # Exact power-of-two linearity: dC*2 doubles every bit pattern's value.
+    dC2 = c.to_device(dC * 2)
+    dA2, dB2 = c.empty((M, K)), c.empty((K, N))
+    c.matmul_backward(dC2, Ad, Bd, dA2, dB2)
+    assert_bits(dA2.numpy(), ga * 2, "dA linearity")
+    assert_bits(dB2.numpy(), gb * 2, "dB linearity")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,K,N", [(64, 784, 128), (37, 19, 53), (256, 256, 256)])
+def test_matmul_forward(hip_ctx, rng, ta, tb, M, K, N):
+    say(f"matmul ta={ta} tb={tb} {M}x{K}x{N}")
+    A = rand(rng, (K, M) if ta else (M, K))
+    B = rand(rng, (N, K) if tb else (K, N))
+    ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    c = hip_ctx
+    C = c.empty((M, N))
+    c.matmul(c.to_device(A), c.to_device(B), C, trans_a=bool(ta), trans_b=bool(tb))
+    assert_close(C.numpy(), ref)
+
+
+def test_matmul_backward_batched(hip_ctx, rng):
+    bt, M, K, N = 6, 40, 64, 72
+    say("matmul_backward_batched")
+    A, B, dC = rand(rng, (bt, M, K)), rand(rng, (bt, K, N)), rand(rng, (bt, M, N))
+    c = hip_ctx
+    dA, dB = c.empty((bt, M, K)), c.empty((bt, K, N))
+    c.matmul_backward_batched(c.to_device(dC), c.to_device(A), c.to_device(B), dA, dB)
+    ga, gb = dA.numpy(), dB.numpy()
+    for i in range(bt):
+        ra, rb = O.matmul_backward(dC[i], A[i], B[i], f64=True)
+        assert_close(ga[i], ra, what=f"dA[{i}]")
+        assert_close(gb[i], rb, what=f"dB[{i}]")
+
+
+def test_matmul_empty_reduction(hip_ctx):
+    c = hip_ctx
+    dC = c.zeros((3, 0))
+    A = c.to_device(np.ones((3, 4), np.float32))
+    B = c.zeros((4, 0))
+    dA = c.to_device(np.full((3, 4), 5.0, np.float32))
+    c.matmul_backward(dC, A, B, dA, None)
+    assert (dA.numpy() == 0).all()
+
+
+# ---------------------------------------------------------------------------
+# Broadcast-reduce: relu + bias (C3), sum_to_shape
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (64, 128), (65, 257), (200, 1000),
+                                       (4096, 4096)])
+def test_relu_bias_backward(hip_ctx, rng, rows, cols):
+    say(f"relu_bias_backward {rows}x{cols}")
+    g, z = rand(rng, (rows, cols)), rand(rng, (rows, cols))
+    z[0, 0] = 0.0  # strict '>' at zero
+    c = hip_ctx
+    gd, zd = c.to_device(g), c.to_device(z)
+    dx, db = c.empty((rows, cols)), c.empty((cols,))
+    c.relu_bias_backward(gd, zd, dx, db)
+    ref_dx = O.relu_backward(g, z)
+    got_dx = dx.numpy()
+    assert_bits(got_dx, ref_dx, "dx")
+    assert_close(db.numpy(), ref_dx.astype(np.float64).sum(0), what="db")
+    # REFERENCE mode: the reference's full-sum-into-element-0 bias grad.
+    dbr = c.empty((cols,))
+    c.relu_bias_backward(gd, zd, None, dbr, mode=L.UNBROADCAST_REFERENCE)
+    want = np.zeros(cols)
+    want[0] = ref_dx.astype(np.float64).sum()
+    got = dbr.numpy()
+    assert_close(got[1:], want[1:], what="db ref rest")
+    assert abs(got[0] - want[0]) <= 1e-5 + 1e-4 * np.abs(ref_dx).sum() ** 0.5 * 10, "db ref [0]"
+
+
+def test_relu_bias_backward_accumulate_and_maskonly(hip_ctx, rng):
+    rows, cols = 130, 300
+    g, z = rand(rng, (rows, cols)), rand(rng, (rows, cols))
+    g0x, g0b = rand(rng, (rows, cols)), rand(rng, cols)
+    c = hip_ctx
+    dx, db = c.to_device(g0x), c.to_device(g0b)
+    c.relu_bias_backward(c.to_device(g), c.to_device(z), dx, db, accumulate=True)
+    m = O.relu_backward(g, z)
+    assert_bits(dx.numpy(), g0x + m, "dx acc")
+    assert_close(db.numpy(), g0b.astype(np.float64) + m.astype(np.float64).sum(0), what="db acc")
+    only = c.empty((rows, cols))
+    c.relu_bias_backward(c.to_device(g), c.to_device(z), only, None)
+    assert_bits(only.numpy(), m, "mask only")
+
+
+SUM_CASES = [((4, 5), (5,)), ((4, 5), (1, 5)), ((4, 5), (4, 1)), ((3, 4, 5), (4, 1)),
+             ((3, 4, 5), (3, 1, 5)), ((2, 3), (1,)), ((7,), (1,)), ((2, 3, 4), (2, 3, 4)),
+             ((1000, 333), (333,)), ((17, 4096), (17, 1)), ((5, 1, 6), (1, 1, 6)),
+             ((300000,), (1,))]
+
+
+@pytest.mark.parametrize("gs,os_", SUM_CASES)
+def test_sum_to_shape(hip_ctx, rng, gs, os_):
+    say(f"sum_to_shape {gs}->{os_}")
+    g = rand(rng, gs)
+    c = hip_ctx
+    out = c.empty(os_)
+    c.sum_to_shape(c.to_device(g), out)
+    assert_close(out.numpy(), O.sum_to_shape(g, os_), what=f"{gs}->{os_}")
+    prev = rand(rng, os_)
+    out2 = c.to_device(prev)
+    c.sum_to_shape(c.to_device(g), out2, accumulate=True)
+    assert_close(out2.numpy(), prev.astype(np.float64) + O.sum_to_shape(g, os_), what="acc")
+
+
+def test_sum_to_shape_reference_mode(hip_ctx, rng):
+    g = rand(rng, (64, 10))
+    c = hip_ctx
+    out = c.to_device(np.full(10, 3.0, np.float32))
+    c.sum_to_shape(c.to_device(g), out, mode=L.UNBROADCAST_REFERENCE, accumulate=True)
+    want = np.full(10, 3.0, np.float32)
+    O.unbroadcast_reference_accumulate(g, want)
+    assert_close(out.numpy(), want, what="reference acc")
+    out = c.to_device(np.full(10, 3.0, np.float32))
+    c.sum_to_shape(c.to_device(g), out, mode=L.UNBROADCAST_REFERENCE)
+    want = np.zeros(10, np.float32)
+    O.unbroadcast_reference_accumulate(g, want)
+    assert_close(out.numpy(), want, what="reference fresh")
+
+
+def test_sum_to_shape_rejects_bad_shape(hip_ctx):
+    c = hip_ctx
+    with pytest.raises(HipError) as e:
+        c.sum_to_shape(c.zeros((4, 5)), c.zeros((3,)))
+    assert e.value.code == L.E_SHAPE
+
+
+# ---------------------------------------------------------------------------
+# Elementwise backward
+# ---------------------------------------------------------------------------
+
+UNARY = [  # kind, oracle, input range, saved value from x, bit-exact?
+    (L.RELU, O.relu_backward, (-2, 2), lambda x: x, True),
+    (L.SIGMOID, O.sigmoid_backward, (-6, 6), lambda x: O.sigmoid(x), True),
+    (L.TANH, O.tanh_backward, (-3, 3), lambda x: np.tanh(x).astype(np.float32), True),
+    (L.EXP, O.exp_backward, (-3, 3), lambda x: np.exp(x).astype(np.float32), True),
+    (L.LOG, O.log_backward, (0.1, 4), lambda x: x, True),
+    (L.TAN, O.tan_backward, (-1.3, 1.3), lambda x: np.tan(x).astype(np.float32), True),
+    (L.GELU, O.gelu_backward, (-5, 5), lambda x: x, False),
+    (L.SQRT, O.sqrt_backward, (0.05, 9), lambda x: x, False),
+    (L.SIN, O.sin_backward, (-6, 6), lambda x: x, False),
+    (L.COS, O.cos_backward, (-6, 6), lambda x: x, False),
+]
+
+
+@pytest.mark.parametrize("n", [1, 5, 1000, 1 << 20])
+@pytest.mark.parametrize("kind,orc,rng_,saved,exact", UNARY, ids=[str(u[0]) for u in UNARY])
+def test_unary_backward(hip_ctx, rng, n, kind, orc, rng_, saved, exact):
+    say(f"unary_backward kind={kind} n={n}")
+    x = rng.uniform(*rng_, n).astype(np.float32)
+    if kind == L.RELU:
+        x[: min(3, n)] = 0.0
+    v = saved(x)
+    g = rand(rng, n)
+    c = hip_ctx
+    dx = c.empty(n)
+    c.unary_backward(kind, c.to_device(g), c.to_device(v), dx)
+    ref = orc(g, v)
+    if exact:
+        assert_bits(dx.numpy(), ref, f"kind {kind}")
+    else:
+        assert_close(dx.numpy(), ref, what=f"kind {kind}")
+
+
+def test_pow_backward(hip_ctx, rng):
+    x = rng.uniform(0.1, 3, 5000).astype(np.float32)
+    g = rand(rng, 5000)
+    c = hip_ctx
+    dx = c.empty(5000)
+    c.unary_backward(L.POW, c.to_device(g), c.to_device(x), dx, param=2.5)
+    assert_close(dx.numpy(), O.pow_backward(g, x, 2.5))
+
+
+def test_unary_accumulate_and_misaligned(hip_ctx, rng):
+    n = 4099
+    x, g, prev = rand(rng, n), rand(rng, n), rand(rng, n)
+    c = hip_ctx
+    xd, gd = c.to_device(x), c.to_device(g)
+    base = c.to_device(np.concatenate([[0.0], prev]).astype(np.float32))
+    dx = base.view(1, (n,))  # 4-byte offset: scalar path
+    c.unary_backward(L.RELU, gd, xd, dx, accumulate=True)
+    assert_bits(dx.numpy(), prev + O.relu_backward(g, x), "relu acc misaligned")
+
+
+@pytest.mark.parametrize("kind", [L.ADD, L.SUB, L.MUL, L.DIV])
+def test_binary_backward(hip_ctx, rng, kind):
+    n = 100003
+    g, x = rand(rng, n), rand(rng, n)
+    y = rng.uniform(0.5, 2, n).astype(np.float32) * rng.choice([-1, 1], n).astype(np.float32)
+    c = hip_ctx
+    dx, dy = c.empty(n), c.empty(n)
+    c.binary_backward(kind, c.to_device(g), c.to_device(x), c.to_device(y), dx, dy)
+    if kind == L.ADD:
+        rx, ry = g, g
+    elif kind == L.SUB:
+        rx, ry = O.sub_backward(g)
+    elif kind == L.MUL:
+        rx, ry = O.mul_backward(g, x, y)
+    else:
+        rx, ry = O.div_backward(g, x, y)
+    assert_bits(dx.numpy(), rx, "dx")
+    assert_bits(dy.numpy(), ry, "dy")
+
+
+def test_fill_grad_and_mse(hip_ctx, rng):
+    c = hip_ctx
+    g0 = c.to_device(np.array([0.7], np.float32))
+    n = 12345
+    dx = c.empty(n)
+    c.fill_grad(g0, dx)
+    assert_bits(dx.numpy(), O.sum_backward(np.float32(0.7), (n,)), "sum bwd")
+    c.fill_grad(g0, dx, divide_by_n=True)
+    assert_bits(dx.numpy(), O.mean_backward(np.float32(0.7), (n,)), "mean bwd")
+    p, t = rand(rng, n), rand(rng, n)
+    dp, dt = c.empty(n), c.empty(n)
+    c.mse_backward(g0, c.to_device(p), c.to_device(t), dp, dt)
+    rp, rt = O.mse_backward(np.float32(0.7), p, t)
+    assert_bits(dp.numpy(), rp, "mse dp")
+    assert_bits(dt.numpy(), rt, "mse dt")
+    # reference KAT tests/autograd_loss.rs:5-37
+    one = c.to_device(np.array([1.0], np.float32))
+    dp3 = c.empty(3)
+    c.mse_backward(one, c.to_device(np.array([1, 2, 3.0])), c.to_device(np.array([1, 2, 5.0])), dp3)
+    got = dp3.numpy()
+    assert got[0] == 0.0 and abs(got[2] + 1.333333) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Row-wise: softmax-CE, softmax backward, argmax
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,C", [(1, 2), (64, 10), (7, 1000), (256, 129)])
+def test_softmax_ce_backward(hip_ctx, rng, B, C):
+    say(f"softmax_ce_backward {B}x{C}")
+    x = rand(rng, (B, C), 3.0)
+    labels = rng.integers(0, C, B).astype(np.int32)
+    onehot = np.eye(C, dtype=np.float32)[labels]
+    c = hip_ctx
+    g0 = c.to_device(np.array([1.0], np.float32))
+    xd = c.to_device(x)
+    d1, d2 = c.empty((B, C)), c.empty((B, C))
+    c.softmax_ce_backward(g0, xd, d1, onehot=c.to_device(onehot))
+    c.softmax_ce_backward(g0, xd, d2, labels=c.to_device(labels))
+    ref = O.cross_entropy_backward(1.0, x, onehot)
+    assert_close(d1.numpy(), ref, what="onehot")
+    assert_bits(d2.numpy(), d1.numpy(), "labels == onehot")
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (5, 7), (2048, 256), (3, 5000)])
+def test_softmax_backward(hip_ctx, rng, rows, cols):
+    y = O.softmax_rows(rand(rng, (rows, cols), 2.0))
+    g = rand(rng, (rows, cols))
+    c = hip_ctx
+    dx = c.empty((rows, cols))
+    c.softmax_backward(c.to_device(y), c.to_device(g), dx)
+    assert_close(dx.numpy(), O.softmax_backward(y, g, f64=True))
+
+
+def test_argmax_rows(hip_ctx, rng):
+    say("argmax")
+    c = hip_ctx
+    cases = [rand(rng, (64, 10)), rand(rng, (5, 1000)),
+             np.array([[1, 3, 2, 3, 1], [3, 1, 4, 1, 5], [-5, -2, -3, -4, -2]], np.float32),
+             np.array([[np.nan, 1, 2], [1, np.nan, 0], [0, 2, np.nan], [0.0, -0.0, 0.0],
+                       [2, 2, 2], [np.nan, np.nan, np.nan]], np.float32),
+             rng.integers(0, 3, (300, 130)).astype(np.float32)]
+    for x in cases:
+        for tie_last in (False, True):
+            idx = c.empty((x.shape[0],), np.int32)
+            c.argmax_rows(c.to_device(x), idx, tie_last=tie_last)
+            assert idx.numpy().tolist() == O.argmax_rows(x, tie_last).tolist(), (x, tie_last)
+
+
+# ---------------------------------------------------------------------------
+# Optimizers
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("mu,wd", [(0.0, 0.0), (0.9, 0.0), (0.0, 0.1), (0.9, 1e-4)])
+def test_sgd_step(hip_ctx, rng, mu, wd):
+    n = 101770  # the C1 MLP parameter count
+    p, g = rand(rng, n), rand(rng, n)
+    v = np.zeros(n, np.float32)
+    c = hip_ctx
+    pd, gd, vd = c.to_device(p), c.to_device(g), c.to_device(v)
+    for _ in range(3):
+        c.sgd_step(pd, gd, vd if mu else None, lr=0.01, mu=mu, wd=wd)
+        O.sgd_step(p, g, v if mu else None, 0.01, mu, wd)
+    assert_bits(pd.numpy(), p, "p")
+    if mu:
+        assert_bits(vd.numpy(), v, "v")
+
+
+@pytest.mark.parametrize("n,wd", [(1, 0.0), (1003, 0.0), (1 << 24, 0.0), (4097, 0.01)])
+def test_adam_step(hip_ctx, rng, n, wd):
+    say(f"adam n={n} wd={wd}")
+    p, g = rand(rng, n), rand(rng, n)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    c = hip_ctx
+    pd, gd, md, vd = c.to_device(p), c.to_device(g), c.to_device(m), c.to_device(v)
+    steps = 2 if n > 100000 else 11
+    for t in range(1, steps + 1):
+        c.adam_step(pd, gd, md, vd, t, lr=1e-3, wd=wd)
+        O.adam_step(p, g, m, v, t, lr=1e-3, wd=wd)
+    assert_bits(pd.numpy(), p, "p")
+    assert_bits(md.numpy(), m, "m")
+    assert_bits(vd.numpy(), v, "v")
+
+
+def test_adam_kat(hip_ctx):
+    # tests/autograd/optim/adam.rs:8-62
+    c = hip_ctx
+    p, g = c.to_device(np.array([1.0], np.float32)), c.to_device(np.array([1.0], np.float32))
+    m, v = c.zeros(1), c.zeros(1)
+    c.adam_step(p, g, m, v, 1, lr=0.1)
+    assert abs(p.numpy()[0] - 0.9) < 1e-5
+    c.adam_step(p, g, m, v, 2, lr=0.1)
+    assert abs(p.numpy()[0] - 0.8) < 1e-4
+
+
+def test_error_paths(hip_ctx):
+    c = hip_ctx
+    x = c.zeros(4)
+    with pytest.raises(HipError) as e:
+        c.unary_backward(99, x, x, x)
+    assert e.value.code == L.E_INVALID
+    with pytest.raises(HipError):
+        c.adam_step(x, x, x, x, 0)
+    with pytest.raises(HipError):
+        c.softmax_ce_backward(x.view(0, (1,)), x.view(0, (2, 2)), x.view(0, (2, 2)))
