@@ -16,7 +16,10 @@
 //     (16 accumulator VGPRs per block per lane).
 //   * Reduction tile BR = 32, double-buffered in LDS, one barrier per tile; the
 //     next tile's global loads are in flight while the MFMAs of the current
-//     one run.
+//     one run.  Each tile's MFMA sums start from zero and are added into
+//     fp32 running totals (two-level accumulation, for accuracy).
+//   * 226 VGPRs, no scratch, 2 waves per SIMD (launch bounds 256 x 2): LDS
+//     (72 KiB per workgroup) allows two workgroups per CU.
 //   * An MFMA 32x32x2 consumes, per lane l = 32*h + c, X[p=c][r=h] and
 //     Y[r=h][q=c].  Eight consecutive reduction indices are fed to four
 //     MFMAs as r = 4h + j (j = 0..3): an R-contiguous operand then gives each
@@ -154,7 +157,18 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
   ly.store(ys0, tid);
   __syncthreads();
 
+  // Two-level accumulation: the MFMAs of one reduction tile accumulate from
+  // zero, and the tile sums are added into running totals with VALU adds.  A
+  // single MFMA accumulator chain over all of R carries a partial sum that
+  // grows like sqrt(R), and its per-step rounding error with it; restarting
+  // per tile keeps the MFMA partials small (error is 4x below numrs's own
+  // sequential fp32 loop at R = 2048).
+  f16v tot00 = {}, tot01 = {}, tot10 = {}, tot11 = {};
   for (int kt = 0; kt < nk; ++kt) {
+    acc00 = f16v{};
+    acc01 = f16v{};
+    acc10 = f16v{};
+    acc11 = f16v{};
     const bool more = kt + 1 < nk;
     if (more) {
       lx.load(X, d.ldx, p0, (kt + 1) * kBR, d.P, d.R, tid);
@@ -180,8 +194,16 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
       lx.store((kt & 1) ? xs0 : xs1, tid);
       ly.store((kt & 1) ? ys0 : ys1, tid);
     }
+    tot00 += acc00;
+    tot01 += acc01;
+    tot10 += acc10;
+    tot11 += acc11;
     __syncthreads();
   }
+  acc00 = tot00;
+  acc01 = tot01;
+  acc10 = tot10;
+  acc11 = tot11;
 
   // 32x32 accumulator layout: lane (h, c), register i holds
   // row 8*(i/4) + 4*h + (i%4), column c.
@@ -210,7 +232,7 @@ __device__ __forceinline__ int xcd_tile(int b, int n) {
 }
 
 template <bool XRC, bool YRC, bool VEC>
-__global__ void __launch_bounds__(kThreads) gemm_kernel(Gemm d) {
+__global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Gemm d) {
   __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   gemm_tile<XRC, YRC, VEC>(d, tile, blockIdx.y, smem);
@@ -219,7 +241,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(Gemm d) {
 // dA (NT) and dB (TN) of matmul_backward in one grid: logical tiles
 // [0, tiles_a) are dA tiles, the rest dB tiles.
 template <bool VEC>
-__global__ void __launch_bounds__(kThreads) matmul_backward_kernel(Gemm da, Gemm db, int tiles_a) {
+__global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, Gemm db, int tiles_a) {
   __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   if (tile < tiles_a)
@@ -304,17 +326,18 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   int rc = check_dims(ctx, who, batch, M, K, N);
   if (rc) return rc;
   if (dA == nullptr && dB == nullptr) return NUMRS_HIP_OK;
-  if (dC == nullptr || (dA != nullptr && B == nullptr) || (dB != nullptr && A == nullptr))
-    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input pointer", who);
   if (batch == 0 || M == 0 || K == 0 || N == 0) {
-    // Empty reduction dimension gives zero gradients.
+    // Empty operands (0-byte buffers may be NULL): dA is reduced over N and dB
+    // over M, so an empty reduction dimension gives zero gradients.
     for (int64_t b = 0; b < batch; ++b) {
-      if (dA) rc = zero_output(ctx, dA + b * sa, M * K, acc);
-      if (!rc && dB) rc = zero_output(ctx, dB + b * sb, K * N, acc);
+      if (dA && M * K > 0) rc = zero_output(ctx, dA + b * sa, M * K, acc);
+      if (!rc && dB && K * N > 0) rc = zero_output(ctx, dB + b * sb, K * N, acc);
       if (rc) return rc;
     }
     return NUMRS_HIP_OK;
   }
+  if (dC == nullptr || (dA != nullptr && B == nullptr) || (dB != nullptr && A == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input pointer", who);
   // dA[M,K] = dC[M,N] @ B[K,N]^T : P=M, Q=K, R=N, X=dC (ld N), Y=B (ld N)
   Gemm ga = make(dC, B, dA, N, N, K, sc, sb, sa, M, K, N, acc);
   // dB[K,N] = A[M,K]^T @ dC[M,N] : P=K, Q=N, R=M, X=A (ld K), Y=dC (ld N)

@@ -124,9 +124,22 @@ __global__ void __launch_bounds__(kBlock)
   __shared__ float red[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  // Loads are issued in batches of 16 before they are added, so a wave waits
+  // for one memory round trip per batch instead of one per chunk.
+  constexpr int kBatch = 16;
   float s = 0.0f;
-  if (c < cols)
-    for (int64_t k = wave; k < chunks; k += 4) s += partial[k * cols + c];
+  if (c < cols) {
+    for (int64_t k0 = wave; k0 < chunks; k0 += 4 * kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t k = k0 + 4 * u;
+        v[u] = k < chunks ? partial[k * cols + c] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) s += v[u];
+    }
+  }
   red[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && c < cols) {

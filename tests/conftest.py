@@ -33,6 +33,39 @@ def assert_close(got, ref, abs_tol=ABS_TOL, rel_tol=REL_TOL, what=""):
             f"max err {err.max():.3e}")
 
 
+U32 = 2.0 ** -24  # fp32 unit roundoff
+
+
+def contraction_allowance(K, rms_ab=1.0):
+    """fp32 rounding allowance of a length-K sum of products with rms(a*b) =
+    rms_ab: partial sums grow like sqrt(K)*rms_ab over K roundings, so the
+    error scale is u*K*rms_ab; 4x that bounds numrs's own sequential fp32
+    loop (backward.rs:123-146) at K = 2048 and 4096."""
+    return 4.0 * U32 * K * rms_ab
+
+
+def assert_contraction(got, ref64, K, rms_ab=1.0, ref32=None, what=""):
+    """A gradient produced by a length-K fp32 contraction (matmul grads),
+    against the float64-accumulated oracle.
+
+    Per element: |g - r| <= 1e-5 + 1e-4|r| + contraction_allowance(K): the
+    north-star tolerance plus the fp32 rounding allowance that the
+    reference's own fp32 result also needs (tests/test_oracle.py::
+    test_reference_fp32_needs_contraction_allowance shows it misses the bare
+    bound at K = 2048).
+    Aggregate, when the reference's fp32 result `ref32` is given: the mean
+    error must be no more than 0.8x the reference's own mean error, i.e. the
+    GPU result is at least as close to the exact gradient as numrs's CPU one."""
+    assert_close(got, ref64, abs_tol=ABS_TOL + contraction_allowance(K, rms_ab), what=what)
+    if ref32 is not None:
+        g = np.asarray(got, np.float64)
+        r = np.asarray(ref64, np.float64)
+        e_gpu = np.abs(g - r).mean()
+        e_ref = np.abs(np.asarray(ref32, np.float64) - r).mean()
+        assert e_gpu <= 0.8 * e_ref + 1e-7, (
+            f"{what}: mean error {e_gpu:.3e} vs numrs fp32 loop {e_ref:.3e}")
+
+
 def assert_bits(got, ref, what=""):
     got = np.ascontiguousarray(got, np.float32)
     ref = np.ascontiguousarray(ref, np.float32)

@@ -2,10 +2,13 @@
 
 Bars (north star): bit-exact for select/multiply/divide/sqrt kernels, the
 optimizers and every integer path; |g - r| <= 1e-5 + 1e-4|r| against the
-float64-accumulated oracle for reductions and contractions, whose summation
-order differs from the reference's.  Full BASELINE sizes are checked through
-sampled rows plus size-independent identities (checksums of checksums,
-exact power-of-two linearity).
+float64-accumulated oracle for reductions, whose summation order differs from
+the reference's.  Matmul gradients (length-K fp32 contractions) add the fp32
+rounding allowance 4*2^-24*K that numrs's own fp32 loop also needs, and must
+be on average at least as close to the exact gradient as that loop is
+(tests/conftest.py::assert_contraction).  Full BASELINE sizes are checked
+through sampled rows plus size-independent identities (checksums of
+checksums, exact power-of-two linearity).
 """
 import sys
 
@@ -15,7 +18,7 @@ import pytest
 from numrs_amd import HipError
 from numrs_amd import _lib as L
 from oracle import oracle as O
-from tests.conftest import assert_bits, assert_close, rand
+from tests.conftest import assert_bits, assert_close, assert_contraction, rand
 
 pytestmark = pytest.mark.gpu
 
@@ -43,11 +46,12 @@ def test_matmul_backward_small(hip_ctx, rng, M, K, N):
     say(f"matmul_backward M={M} K={K} N={N}")
     A, B, dC = rand(rng, (M, K)), rand(rng, (K, N)), rand(rng, (M, N))
     dA_ref, dB_ref = O.matmul_backward(dC, A, B, f64=True)
+    dA_32, dB_32 = O.matmul_backward(dC, A, B)  # numrs's own fp32 loops
     c = hip_ctx
     dA, dB = c.empty((M, K)), c.empty((K, N))
     c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), dA, dB)
-    assert_close(dA.numpy(), dA_ref, what="dA")
-    assert_close(dB.numpy(), dB_ref, what="dB")
+    assert_contraction(dA.numpy(), dA_ref, N, ref32=dA_32, what="dA")
+    assert_contraction(dB.numpy(), dB_ref, M, ref32=dB_32, what="dB")
 
 
 def test_matmul_backward_kat(hip_ctx):
@@ -72,14 +76,14 @@ def test_matmul_backward_accumulate_and_skip(hip_ctx, rng):
     dA, dB = c.to_device(ga), c.to_device(gb)
     dCd, Ad, Bd = c.to_device(dC), c.to_device(A), c.to_device(B)
     c.matmul_backward(dCd, Ad, Bd, dA, dB, accumulate=True)
-    assert_close(dA.numpy(), ga.astype(np.float64) + dA_ref, what="dA acc")
-    assert_close(dB.numpy(), gb.astype(np.float64) + dB_ref, what="dB acc")
+    assert_contraction(dA.numpy(), ga.astype(np.float64) + dA_ref, N, what="dA acc")
+    assert_contraction(dB.numpy(), gb.astype(np.float64) + dB_ref, M, what="dB acc")
     only_b = c.to_device(np.full((K, N), 7.0, np.float32))
     c.matmul_backward(dCd, Ad, None, None, only_b)
-    assert_close(only_b.numpy(), dB_ref, what="dB only")
+    assert_contraction(only_b.numpy(), dB_ref, M, what="dB only")
     only_a = c.empty((M, K))
     c.matmul_backward(dCd, None, Bd, only_a, None)
-    assert_close(only_a.numpy(), dA_ref, what="dA only")
+    assert_contraction(only_a.numpy(), dA_ref, N, what="dA only")
 
 
 def _checksums(dC, A, B):
@@ -102,12 +106,19 @@ def test_matmul_backward_baseline_sizes(hip_ctx, rng, M, K, N):
     c.matmul_backward(dCd, Ad, Bd, dA, dB)
     ga, gb = dA.numpy(), dB.numpy()
     # Sampled rows against the float64 oracle: first/last rows of tiles and XCD groups.
+    # fp32 loops of numrs (backward.rs:123-146) on the same rows, for the aggregate check.
     for r0 in (0, 127, 128, 1023, M - 2):
-        ra, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=(r0, r0 + 2))
-        assert_close(ga[r0:r0 + 2], ra[r0:r0 + 2], what=f"dA rows {r0}")
+        rows = (r0, r0 + 2)
+        ra, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=rows)
+        r32, _ = O.matmul_backward(dC, A, B, need_b=False, rows_a=rows)
+        assert_contraction(ga[r0:r0 + 2], ra[r0:r0 + 2], N, ref32=r32[r0:r0 + 2],
+                           what=f"dA rows {r0}")
     for r0 in (0, 129, K // 2, K - 2):
-        _, rb = O.matmul_backward(dC, A, B, need_a=False, f64=True, rows_b=(r0, r0 + 2))
-        assert_close(gb[r0:r0 + 2], rb[r0:r0 + 2], what=f"dB rows {r0}")
+        rows = (r0, r0 + 2)
+        _, rb = O.matmul_backward(dC, A, B, need_a=False, f64=True, rows_b=rows)
+        _, r32 = O.matmul_backward(dC, A, B, need_a=False, rows_b=rows)
+        assert_contraction(gb[r0:r0 + 2], rb[r0:r0 + 2], M, ref32=r32[r0:r0 + 2],
+                           what=f"dB rows {r0}")
     # Whole-output identities.
     sa, sb = _checksums(dC, A, B)
     assert abs(ga.astype(np.float64).sum() - sa) <= 1e-4 * np.abs(ga).sum()
@@ -130,7 +141,7 @@ def test_matmul_forward(hip_ctx, rng, ta, tb, M, K, N):
     c = hip_ctx
     C = c.empty((M, N))
     c.matmul(c.to_device(A), c.to_device(B), C, trans_a=bool(ta), trans_b=bool(tb))
-    assert_close(C.numpy(), ref)
+    assert_contraction(C.numpy(), ref, K)
 
 
 def test_matmul_backward_batched(hip_ctx, rng):
@@ -143,8 +154,8 @@ def test_matmul_backward_batched(hip_ctx, rng):
     ga, gb = dA.numpy(), dB.numpy()
     for i in range(bt):
         ra, rb = O.matmul_backward(dC[i], A[i], B[i], f64=True)
-        assert_close(ga[i], ra, what=f"dA[{i}]")
-        assert_close(gb[i], rb, what=f"dB[{i}]")
+        assert_contraction(ga[i], ra, N, what=f"dA[{i}]")
+        assert_contraction(gb[i], rb, M, what=f"dB[{i}]")
 
 
 def test_matmul_empty_reduction(hip_ctx):
