@@ -119,6 +119,41 @@ def bench_adam(ctx, rng, n, steps, warmup):
     return {"ms_per_step": total / steps, "kernel_ms": per, "bytes": 28.0 * n}
 
 
+def bench_c1(ctx, steps, warmup):
+    """2-layer MLP (64x784 -> 128 -> ReLU -> 10, softmax CE,
+    SGD lr 0.01) -- forward, backward and SGD step through the device
+    autograd engine, timed per step with a device sync at the end of each
+    step (a loss read-back is what a training loop does)."""
+    import numrs_amd as nr
+    from numrs_amd import Tensor, nn, optim
+    from tests.mlp_oracle import make_c1
+
+    nr.set_default_context(ctx)
+    p = make_c1(seed=1)
+    l1 = nn.Linear.with_weights(784, 128, p["W1"], p["b1"])
+    l2 = nn.Linear.with_weights(128, 10, p["W2"], p["b2"])
+    model = nn.Sequential([l1, nn.ReLU(), l2])
+    opt = optim.SGD.simple(model.parameters(), 0.01)
+    x = Tensor.new(p["x"], False)
+    onehot = Tensor.new(np.eye(10, dtype=np.float32)[p["labels"]], False)
+
+    def step():
+        loss = model.forward(x).cross_entropy_loss(onehot)
+        loss.backward()
+        opt.step()
+        opt.zero_grad()
+        return loss
+
+    for _ in range(warmup):
+        step().item()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    loss.item()
+    per = (time.perf_counter() - t0) / steps
+    return {"us_per_step": per * 1e6, "loss": loss.item()}
+
+
 def cpu_baseline(A, B, dC, rows_a: int, rows_b: int):
     """numrs's matmul_backward restated in C (single thread, fp32 triple
     loops of backward.rs:123-146), timed on this host over a bounded sample
@@ -207,6 +242,12 @@ def main() -> int:
                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
                           "algorithmic_bytes": ad["bytes"]})
         log(f"  C3 adam {ad['kernel_ms']:.4f} ms {gbs:.1f} GB/s")
+        c1 = bench_c1(ctx, args.steps, args.warmup)
+        secondary.append({"workload": "C1 MLP train step 64x784->128->10, CE, SGD 0.01 "
+                                      "(forward+backward+step via the device autograd engine)",
+                          "value": round(c1["us_per_step"], 1), "unit": "us/step",
+                          "bound": "latency", "final_loss": round(c1["loss"], 6)})
+        log(f"  C1 MLP step {c1['us_per_step']:.1f} us")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -241,6 +241,127 @@ int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, i
 int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, float *v,
                         int64_t n, float lr, float b1, float b2, float eps, float wd, int t);
 
+/* ---------------------------------------------------------------------- */
+/* Forward kernels the engine records (DispatchTable / ops.rs analogues)   */
+/* ---------------------------------------------------------------------- */
+
+/* out = a (op) b with numpy broadcasting, kind in NUMRS_HIP_ADD..DIV
+ * (ops::add/sub/mul/div via promotion_wrappers.rs:25-168). */
+int numrs_hip_binary_forward(numrs_hip_ctx *ctx, int kind, const float *a, const int64_t *ashape,
+                             int and_, const float *b, const int64_t *bshape, int bnd, float *out);
+/* y = f(x) for the unary kinds (ops.rs:122-211, 453-554; GELU exact-erf). */
+int numrs_hip_unary_forward(numrs_hip_ctx *ctx, int kind, const float *x, float *y, int64_t n,
+                            float param);
+/* y[cols,rows] = x[rows,cols]^T (ops/shape/transpose.rs:9-88). */
+int numrs_hip_transpose(numrs_hip_ctx *ctx, const float *x, float *y, int64_t rows, int64_t cols);
+/* out[0] = sum(x) or mean(x) (ops.rs:214-252). */
+int numrs_hip_sum(numrs_hip_ctx *ctx, const float *x, int64_t n, int mean, float *out);
+/* out[0] = mean((p-t)^2) (ops.rs:255-278). */
+int numrs_hip_mse_loss(numrs_hip_ctx *ctx, const float *p, const float *t, int64_t n, float *out);
+/* out[0] = mean over rows of softmax cross-entropy (ops.rs:281-334); one-hot
+ * target or int32 labels. */
+int numrs_hip_cross_entropy_loss(numrs_hip_ctx *ctx, const float *logits, const float *onehot,
+                                 const int32_t *labels, int64_t B, int64_t C, float *out);
+/* Row softmax of x*scale over the last axis (the reference's Softmax module
+ * cannot run on an axis: ops/stats/softmax.rs:13-16). */
+int numrs_hip_softmax_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t rows,
+                              int64_t cols, float scale);
+/* LayerNorm over the last axis (no reference op): y = (x-mean)*rstd*gamma +
+ * beta, rstd = 1/sqrt(biased var + eps); mean/rstd per row (may be NULL). */
+int numrs_hip_layernorm_forward(numrs_hip_ctx *ctx, const float *x, const float *gamma,
+                                const float *beta, float *y, float *mean, float *rstd,
+                                int64_t rows, int64_t cols, float eps);
+/* LayerNorm backward from the saved mean/rstd: dx, dgamma = sum_rows g*xhat,
+ * dbeta = sum_rows g (any may be NULL); rows of at most 2048. */
+int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float *x,
+                                 const float *gamma, const float *mean, const float *rstd,
+                                 float *dx, float *dgamma, float *dbeta, int64_t rows,
+                                 int64_t cols, int accumulate);
+
+/* ---------------------------------------------------------------------- */
+/* Tensor engine: numrs's Tensor / backward / optimizers, device-resident   */
+/* ---------------------------------------------------------------------- */
+
+/* A tensor handle (autograd/tensor.rs:18-33): device data, a grad cell
+ * shared by every reference to the tensor, and the node that produced it.
+ * Handles must be freed before their context is destroyed.  Errors are
+ * reported through numrs_hip_last_error of the tensor's context. */
+typedef struct numrs_hip_tensor numrs_hip_tensor;
+typedef struct numrs_hip_optim numrs_hip_optim;
+
+/* Grad mode, thread-local (is_grad_enabled / set_grad_enabled, mod.rs:194-206). */
+void numrs_hip_set_grad_enabled(int enabled);
+int numrs_hip_is_grad_enabled(void);
+/* Broadcast-gradient mode of the engine's add/sub/mul/div nodes. */
+int numrs_hip_set_unbroadcast_mode(numrs_hip_ctx *ctx, int mode);
+
+/* Tensor::new (tensor.rs:41-59): uploads `host`. */
+int numrs_hip_tensor_new(numrs_hip_ctx *ctx, const float *host, const int64_t *shape, int ndim,
+                         int requires_grad, numrs_hip_tensor **out);
+int numrs_hip_tensor_free(numrs_hip_tensor *t);
+/* Writes up to cap dims into shape; returns ndim (Tensor::shape, :86-88). */
+int numrs_hip_tensor_shape(const numrs_hip_tensor *t, int64_t *shape, int cap);
+int64_t numrs_hip_tensor_numel(const numrs_hip_tensor *t);
+int numrs_hip_tensor_requires_grad(const numrs_hip_tensor *t);
+int numrs_hip_tensor_is_leaf(const numrs_hip_tensor *t);
+/* Tensor::values (:91-93): downloads n = numel floats. */
+int numrs_hip_tensor_values(numrs_hip_tensor *t, float *host, int64_t n);
+/* Tensor::gradient (:96-98): 1 and the grad copied into host, or 0 when the
+ * tensor has no grad (None). */
+int numrs_hip_tensor_gradient(numrs_hip_tensor *t, float *host, int64_t n);
+/* Tensor::set_gradient (:110-117) and zero_grad (:135-142). */
+int numrs_hip_tensor_set_gradient(numrs_hip_tensor *t, const float *host, int64_t n);
+int numrs_hip_tensor_zero_grad(numrs_hip_tensor *t);
+/* Device pointers of the values and grad (grad NULL when none; materialised). */
+int numrs_hip_tensor_device_ptrs(numrs_hip_tensor *t, float **data, float **grad);
+/* Tensor::backward (:173-215). */
+int numrs_hip_tensor_backward(numrs_hip_tensor *t);
+/* Tensor::detach (:146-154). */
+int numrs_hip_tensor_detach(numrs_hip_tensor *t, numrs_hip_tensor **out);
+/* Tensor::add/sub/mul/div (ops.rs:16-98), kind NUMRS_HIP_ADD..DIV. */
+int numrs_hip_tensor_binary(int kind, numrs_hip_tensor *a, numrs_hip_tensor *b,
+                            numrs_hip_tensor **out);
+/* Tensor::relu/sigmoid/tanh/exp/log/sqrt/sin/cos/tan/pow (ops.rs:121-554)
+ * and gelu; param = exponent for NUMRS_HIP_POW. */
+int numrs_hip_tensor_unary(int kind, numrs_hip_tensor *a, float param, numrs_hip_tensor **out);
+/* Tensor::matmul (ops.rs:101-119), 2-D. */
+int numrs_hip_tensor_matmul(numrs_hip_tensor *a, numrs_hip_tensor *b, numrs_hip_tensor **out);
+/* Tensor::transpose (tensor.rs:242-259), 2-D. */
+int numrs_hip_tensor_transpose(numrs_hip_tensor *a, numrs_hip_tensor **out);
+/* Tensor::reshape (ops.rs:353-369). */
+int numrs_hip_tensor_reshape(numrs_hip_tensor *a, const int64_t *shape, int ndim,
+                             numrs_hip_tensor **out);
+/* Tensor::sum / Tensor::mean (ops.rs:214-252) -> [1]. */
+int numrs_hip_tensor_sum(numrs_hip_tensor *a, int mean, numrs_hip_tensor **out);
+/* Tensor::mse_loss (ops.rs:255-278) -> [1]. */
+int numrs_hip_tensor_mse_loss(numrs_hip_tensor *pred, numrs_hip_tensor *target,
+                              numrs_hip_tensor **out);
+/* Tensor::cross_entropy_loss (ops.rs:281-334), one-hot target -> [1]. */
+int numrs_hip_tensor_cross_entropy_loss(numrs_hip_tensor *logits, numrs_hip_tensor *target,
+                                        numrs_hip_tensor **out);
+/* The same with int32 class labels (host array of logits rows) instead of a
+ * one-hot tensor: the reference builds the one-hot on the host first. */
+int numrs_hip_tensor_cross_entropy_labels(numrs_hip_tensor *logits, const int32_t *host_labels,
+                                          numrs_hip_tensor **out);
+/* Row softmax over the last axis (Softmax module, nn.rs:345-375, on an axis). */
+int numrs_hip_tensor_softmax(numrs_hip_tensor *a, numrs_hip_tensor **out);
+/* LayerNorm over the last axis (no reference op). */
+int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
+                                numrs_hip_tensor *beta, float eps, numrs_hip_tensor **out);
+
+/* SGD::new (optim/sgd.rs:90-112) / Adam::new (optim/adam.rs:250-285) over
+ * parameter tensors; step / zero_grad / learning_rate / set_learning_rate
+ * are the Optimizer trait (optim/base.rs:8-23). */
+int numrs_hip_optim_sgd(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
+                        float momentum, float wd, numrs_hip_optim **out);
+int numrs_hip_optim_adam(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
+                         float b1, float b2, float eps, float wd, numrs_hip_optim **out);
+int numrs_hip_optim_step(numrs_hip_optim *opt);
+int numrs_hip_optim_zero_grad(numrs_hip_optim *opt);
+int numrs_hip_optim_set_lr(numrs_hip_optim *opt, float lr);
+float numrs_hip_optim_lr(const numrs_hip_optim *opt);
+int numrs_hip_optim_free(numrs_hip_optim *opt);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,52 @@ SIGNATURES = {
     "numrs_hip_argmax_rows": (_i, [_vp] * 3 + [_i64, _i64, _i]),
     "numrs_hip_sgd_step": (_i, [_vp] * 4 + [_i64, _f, _f, _f]),
     "numrs_hip_adam_step": (_i, [_vp] * 5 + [_i64, _f, _f, _f, _f, _f, _i]),
+    # forward kernels
+    "numrs_hip_binary_forward": (_i, [_vp, _i, _vp, _i64p, _i, _vp, _i64p, _i, _vp]),
+    "numrs_hip_unary_forward": (_i, [_vp, _i, _vp, _vp, _i64, _f]),
+    "numrs_hip_transpose": (_i, [_vp, _vp, _vp, _i64, _i64]),
+    "numrs_hip_sum": (_i, [_vp, _vp, _i64, _i, _vp]),
+    "numrs_hip_mse_loss": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "numrs_hip_cross_entropy_loss": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "numrs_hip_softmax_forward": (_i, [_vp, _vp, _vp, _i64, _i64, _f]),
+    "numrs_hip_layernorm_forward": (_i, [_vp] * 7 + [_i64, _i64, _f]),
+    "numrs_hip_layernorm_backward": (_i, [_vp] * 9 + [_i64, _i64, _i]),
+    # tensor engine
+    "numrs_hip_set_grad_enabled": (None, [_i]),
+    "numrs_hip_is_grad_enabled": (_i, []),
+    "numrs_hip_set_unbroadcast_mode": (_i, [_vp, _i]),
+    "numrs_hip_tensor_new": (_i, [_vp, _vp, _i64p, _i, _i, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_free": (_i, [_vp]),
+    "numrs_hip_tensor_shape": (_i, [_vp, _i64p, _i]),
+    "numrs_hip_tensor_numel": (_i64, [_vp]),
+    "numrs_hip_tensor_requires_grad": (_i, [_vp]),
+    "numrs_hip_tensor_is_leaf": (_i, [_vp]),
+    "numrs_hip_tensor_values": (_i, [_vp, _vp, _i64]),
+    "numrs_hip_tensor_gradient": (_i, [_vp, _vp, _i64]),
+    "numrs_hip_tensor_set_gradient": (_i, [_vp, _vp, _i64]),
+    "numrs_hip_tensor_zero_grad": (_i, [_vp]),
+    "numrs_hip_tensor_device_ptrs": (_i, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_backward": (_i, [_vp]),
+    "numrs_hip_tensor_detach": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_binary": (_i, [_i, _vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_unary": (_i, [_i, _vp, _f, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_matmul": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_transpose": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_reshape": (_i, [_vp, _i64p, _i, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_sum": (_i, [_vp, _i, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_mse_loss": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_cross_entropy_loss": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_cross_entropy_labels": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_softmax": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_layer_norm": (_i, [_vp, _vp, _vp, _f, ctypes.POINTER(_vp)]),
+    "numrs_hip_optim_sgd": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, ctypes.POINTER(_vp)]),
+    "numrs_hip_optim_adam": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, _f, _f,
+                                 ctypes.POINTER(_vp)]),
+    "numrs_hip_optim_step": (_i, [_vp]),
+    "numrs_hip_optim_zero_grad": (_i, [_vp]),
+    "numrs_hip_optim_set_lr": (_i, [_vp, _f]),
+    "numrs_hip_optim_lr": (_f, [_vp]),
+    "numrs_hip_optim_free": (_i, [_vp]),
 }
 
 # Enum values of include/numrs_hip.h.

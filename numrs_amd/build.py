@@ -24,7 +24,8 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJ = os.path.join(PKG, "lib", "obj")
 LIB = os.path.join(PKG, "lib", "libnumrs_hip.so")
 
-SOURCES = ["runtime.hip", "gemm.hip", "eltwise.hip", "reduce.hip", "rowwise.hip"]
+SOURCES = ["runtime.hip", "gemm.hip", "eltwise.hip", "reduce.hip", "rowwise.hip", "fwd.hip",
+           "autograd.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = [

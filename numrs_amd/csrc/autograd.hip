@@ -1,0 +1,1024 @@
+// Device-resident autograd engine: numrs's Tensor / ComputeNode / backward
+// (autograd/tensor.rs, autograd/mod.rs, autograd/ops.rs) with every buffer on
+// the GPU and every BackwardFn body a kernel of this library.
+//
+// Semantics kept from the reference:
+//   * A tensor that requires grad owns a grad cell shared by all handles and
+//     graph references to it (Rc<RefCell<Array>>, tensor.rs:18-33).  The cell
+//     is logically zero at creation (tensor.rs:41-83); it is materialised
+//     lazily: the first backward producer writes it (accumulate = 0), later
+//     producers add (accumulate = 1) -- accumulate_gradient, tensor.rs:120-132.
+//   * backward() seeds ones of the output's shape (set_gradient, :178-183),
+//     builds the DFS post-order of build_topo (:218-239; non-leaf nodes are
+//     visited once, inputs in order), and walks it in reverse (:191-212),
+//     handing each node's grad to its backward body, which writes directly
+//     into the grads of the inputs that require grad (:205-209).
+//   * A node is recorded only when grad mode is on and an input requires
+//     grad (ops.rs:21 and every op); grad mode is thread-local (mod.rs:194-206).
+//   * Broadcast gradients go through unbroadcast (backward.rs:12-39) in the
+//     context's mode: CORRECT (axis sums) or REFERENCE (the reference's
+//     full sum into element 0).
+// Every BackwardFn is linear in its incoming grad, so a node whose grad was
+// never written (still logically zero) contributes nothing and is skipped.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <unordered_set>
+#include <utility>
+#include <vector>
+
+#include "common.h"
+
+namespace {
+
+using numrs_hip::fail;
+
+thread_local bool g_grad_enabled = true;  // mod.rs:194-206
+
+enum class Op {
+  Leaf, Add, Sub, Mul, Div, MatMul, Transpose, Unary, Sum, Mean, MSE, CrossEntropy,
+  CrossEntropyLabels, Reshape, Softmax, LayerNorm
+};
+
+struct Storage {
+  numrs_hip_ctx *ctx = nullptr;
+  float *ptr = nullptr;
+  size_t bytes = 0;
+  ~Storage() { numrs_hip::block_free(ctx, ptr, bytes); }
+};
+using Buf = std::shared_ptr<Storage>;
+
+struct GradCell {
+  Buf buf;
+  bool valid = false;  // false: logically zero
+};
+
+struct Node;
+struct Impl {
+  numrs_hip_ctx *ctx = nullptr;
+  std::vector<int64_t> shape;
+  Buf data;
+  std::shared_ptr<GradCell> grad;  // null when the tensor does not require grad
+  bool requires_grad = false;
+  bool is_leaf = true;
+  std::shared_ptr<Node> node;
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    return n;
+  }
+};
+using T = std::shared_ptr<Impl>;
+
+struct Node {
+  uint64_t id;
+  Op op;
+  int kind = 0;       // unary kind / mean flag
+  float param = 0.f;  // pow exponent, LayerNorm eps
+  std::vector<T> inputs;
+  std::vector<Buf> saved;  // LayerNorm mean/rstd, int32 labels
+};
+
+uint64_t next_node_id() {  // NodeId::new, mod.rs:46-51
+  static uint64_t counter = 0;
+  return counter++;
+}
+
+int alloc_buf(numrs_hip_ctx *ctx, int64_t count, size_t elem, Buf *out) {
+  auto s = std::make_shared<Storage>();
+  s->ctx = ctx;
+  s->bytes = (size_t)count * elem;
+  void *p = nullptr;
+  if (int rc = numrs_hip::block_alloc(ctx, s->bytes, &p)) return rc;
+  s->ptr = static_cast<float *>(p);
+  *out = std::move(s);
+  return NUMRS_HIP_OK;
+}
+
+int make_tensor(numrs_hip_ctx *ctx, std::vector<int64_t> shape, bool requires_grad, T *out) {
+  auto t = std::make_shared<Impl>();
+  t->ctx = ctx;
+  t->shape = std::move(shape);
+  if (int rc = alloc_buf(ctx, t->numel(), sizeof(float), &t->data)) return rc;
+  t->requires_grad = requires_grad;
+  if (requires_grad) t->grad = std::make_shared<GradCell>();
+  *out = std::move(t);
+  return NUMRS_HIP_OK;
+}
+
+// Tensor::from_operation (tensor.rs:62-83): attaches the node when recording.
+void attach(T &out, Op op, std::vector<T> inputs, int kind = 0, float param = 0.f,
+            std::vector<Buf> saved = {}) {
+  auto n = std::make_shared<Node>();
+  n->id = next_node_id();
+  n->op = op;
+  n->kind = kind;
+  n->param = param;
+  n->inputs = std::move(inputs);
+  n->saved = std::move(saved);
+  out->node = std::move(n);
+  out->is_leaf = false;
+}
+
+bool recording(std::initializer_list<const T *> ins) {
+  if (!g_grad_enabled) return false;
+  for (const T *t : ins)
+    if ((*t)->requires_grad) return true;
+  return false;
+}
+
+// Grad buffer of `t` for a producer; *acc tells whether to add (1) or write (0).
+int grad_target(const T &t, float **ptr, int *acc) {
+  GradCell &c = *t->grad;
+  if (!c.buf)
+    if (int rc = alloc_buf(t->ctx, t->numel(), sizeof(float), &c.buf)) return rc;
+  *acc = c.valid ? 1 : 0;
+  c.valid = true;
+  *ptr = c.buf->ptr;
+  return NUMRS_HIP_OK;
+}
+
+// Grad of `t` as a materialised buffer (zero-filled if never written).
+int grad_materialise(const T &t) {
+  GradCell &c = *t->grad;
+  if (!c.buf)
+    if (int rc = alloc_buf(t->ctx, t->numel(), sizeof(float), &c.buf)) return rc;
+  if (!c.valid) {
+    if (int rc = numrs_hip_fill(t->ctx, c.buf->ptr, t->numel(), 0.0f)) return rc;
+    c.valid = true;
+  }
+  return NUMRS_HIP_OK;
+}
+
+bool same_shape(const std::vector<int64_t> &a, const std::vector<int64_t> &b) { return a == b; }
+
+// ---------------------------------------------------------------------------
+// Backward bodies (backward.rs), writing into input grads
+// ---------------------------------------------------------------------------
+
+// dst_grad(in) (+)= unbroadcast(src) where src has shape `gshape`.
+int add_into(const T &in, const float *src, const std::vector<int64_t> &gshape) {
+  numrs_hip_ctx *ctx = in->ctx;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(in, &dst, &acc)) return rc;
+  return numrs_hip_sum_to_shape(ctx, src, gshape.data(), (int)gshape.size(), dst,
+                                in->shape.data(), (int)in->shape.size(), ctx->unbroadcast_mode,
+                                acc);
+}
+
+int temp(numrs_hip_ctx *ctx, int64_t n, Buf *out) { return alloc_buf(ctx, n, sizeof(float), out); }
+
+int bw_add_sub(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0], &y = n.inputs[1];
+  numrs_hip_ctx *ctx = out->ctx;
+  const int64_t N = out->numel();
+  if (x->requires_grad)
+    if (int rc = add_into(x, g, out->shape)) return rc;  // backward.rs:50 / :62
+  if (!y->requires_grad) return NUMRS_HIP_OK;
+  if (n.op == Op::Add) return add_into(y, g, out->shape);  // backward.rs:51
+  // sub: dy = unbroadcast(g * -1), backward.rs:65-67
+  if (same_shape(y->shape, out->shape)) {
+    float *dst;
+    int acc;
+    if (int rc = grad_target(y, &dst, &acc)) return rc;
+    return numrs_hip_binary_backward(ctx, NUMRS_HIP_SUB, g, nullptr, nullptr, nullptr, dst, N, acc);
+  }
+  Buf t;
+  if (int rc = temp(ctx, N, &t)) return rc;
+  if (int rc = numrs_hip_binary_backward(ctx, NUMRS_HIP_SUB, g, nullptr, nullptr, nullptr, t->ptr,
+                                         N, 0))
+    return rc;
+  return add_into(y, t->ptr, out->shape);
+}
+
+int bw_mul_div(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0], &y = n.inputs[1];
+  numrs_hip_ctx *ctx = out->ctx;
+  const int64_t N = out->numel();
+  const int kind = n.op == Op::Mul ? NUMRS_HIP_MUL : NUMRS_HIP_DIV;
+  const bool flat = same_shape(x->shape, out->shape) && same_shape(y->shape, out->shape);
+  if (flat) {
+    // backward.rs:74-109 on equal shapes: one fused pass per grad (separate
+    // calls when both inputs share one grad cell, e.g. x * x).
+    float *dx = nullptr, *dy = nullptr;
+    int ax = 0, ay = 0;
+    if (x->requires_grad && y->requires_grad && x->grad == y->grad) {
+      if (int rc = grad_target(x, &dx, &ax)) return rc;
+      if (int rc = numrs_hip_binary_backward(ctx, kind, g, x->data->ptr, y->data->ptr, dx, nullptr,
+                                             N, ax))
+        return rc;
+      return numrs_hip_binary_backward(ctx, kind, g, x->data->ptr, y->data->ptr, nullptr, dx, N, 1);
+    }
+    if (x->requires_grad)
+      if (int rc = grad_target(x, &dx, &ax)) return rc;
+    if (y->requires_grad)
+      if (int rc = grad_target(y, &dy, &ay)) return rc;
+    if (dx && dy && ax != ay) {
+      if (int rc = numrs_hip_binary_backward(ctx, kind, g, x->data->ptr, y->data->ptr, dx, nullptr,
+                                             N, ax))
+        return rc;
+      return numrs_hip_binary_backward(ctx, kind, g, x->data->ptr, y->data->ptr, nullptr, dy, N, ay);
+    }
+    return numrs_hip_binary_backward(ctx, kind, g, x->data->ptr, y->data->ptr, dx, dy, N,
+                                     dx ? ax : ay);
+  }
+  // Broadcasting operands: form the full-shape products with the forward
+  // kernels, then unbroadcast (backward.rs:79-84, 95-106).
+  const auto &os = out->shape;
+  Buf t;
+  if (int rc = temp(ctx, N, &t)) return rc;
+  if (x->requires_grad) {
+    // mul: g * y   div: g / y
+    if (int rc = numrs_hip_binary_forward(ctx, kind, g, os.data(), (int)os.size(), y->data->ptr,
+                                          y->shape.data(), (int)y->shape.size(), t->ptr))
+      return rc;
+    if (int rc = add_into(x, t->ptr, os)) return rc;
+  }
+  if (!y->requires_grad) return NUMRS_HIP_OK;
+  if (kind == NUMRS_HIP_MUL) {  // g * x
+    if (int rc = numrs_hip_binary_forward(ctx, NUMRS_HIP_MUL, g, os.data(), (int)os.size(),
+                                          x->data->ptr, x->shape.data(), (int)x->shape.size(),
+                                          t->ptr))
+      return rc;
+    return add_into(y, t->ptr, os);
+  }
+  // div: ((g * (x / (y*y))) * -1), backward.rs:99-104
+  Buf ysq, term;
+  const int64_t ny = y->numel();
+  if (int rc = temp(ctx, ny, &ysq)) return rc;
+  if (int rc = numrs_hip_binary_forward(ctx, NUMRS_HIP_MUL, y->data->ptr, y->shape.data(),
+                                        (int)y->shape.size(), y->data->ptr, y->shape.data(),
+                                        (int)y->shape.size(), ysq->ptr))
+    return rc;
+  if (int rc = temp(ctx, N, &term)) return rc;
+  if (int rc = numrs_hip_binary_forward(ctx, NUMRS_HIP_DIV, x->data->ptr, x->shape.data(),
+                                        (int)x->shape.size(), ysq->ptr, y->shape.data(),
+                                        (int)y->shape.size(), term->ptr))
+    return rc;
+  if (int rc = numrs_hip_binary_forward(ctx, NUMRS_HIP_MUL, g, os.data(), (int)os.size(),
+                                        term->ptr, os.data(), (int)os.size(), t->ptr))
+    return rc;
+  const int64_t one = 1;
+  const float neg = -1.0f;
+  Buf negb;
+  if (int rc = temp(ctx, 1, &negb)) return rc;
+  if (int rc = numrs_hip_fill(ctx, negb->ptr, 1, neg)) return rc;
+  if (int rc = numrs_hip_binary_forward(ctx, NUMRS_HIP_MUL, t->ptr, os.data(), (int)os.size(),
+                                        negb->ptr, &one, 1, term->ptr))
+    return rc;
+  return add_into(y, term->ptr, os);
+}
+
+int bw_matmul(const T &out, const float *g, Node &n) {
+  const T &a = n.inputs[0], &b = n.inputs[1];
+  numrs_hip_ctx *ctx = out->ctx;
+  const int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+  float *da = nullptr, *db = nullptr;
+  int aa = 0, ab = 0;
+  if (a->requires_grad && b->requires_grad && a->grad == b->grad) {  // x @ x
+    if (int rc = grad_target(a, &da, &aa)) return rc;
+    if (int rc = numrs_hip_matmul_backward(ctx, g, a->data->ptr, b->data->ptr, da, nullptr, M, K,
+                                           N, aa))
+      return rc;
+    return numrs_hip_matmul_backward(ctx, g, a->data->ptr, b->data->ptr, nullptr, da, M, K, N, 1);
+  }
+  // dA only when A requires grad (the reference computes and drops it, tensor.rs:206).
+  if (a->requires_grad)
+    if (int rc = grad_target(a, &da, &aa)) return rc;
+  if (b->requires_grad)
+    if (int rc = grad_target(b, &db, &ab)) return rc;
+  if (da && db && aa != ab) {
+    if (int rc = numrs_hip_matmul_backward(ctx, g, a->data->ptr, b->data->ptr, da, nullptr, M, K,
+                                           N, aa))
+      return rc;
+    return numrs_hip_matmul_backward(ctx, g, a->data->ptr, b->data->ptr, nullptr, db, M, K, N, ab);
+  }
+  return numrs_hip_matmul_backward(ctx, g, a->data->ptr, b->data->ptr, da, db, M, K, N,
+                                   da ? aa : ab);
+}
+
+int bw_transpose(const T &out, const float *g, Node &n) {  // backward.rs:305-312
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  numrs_hip_ctx *ctx = out->ctx;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  // out is [c, r]; its transpose is x's [r, c]
+  const int64_t r = out->shape[0], c = out->shape[1];
+  if (!acc) return numrs_hip_transpose(ctx, g, dst, r, c);
+  Buf t;
+  if (int rc = temp(ctx, x->numel(), &t)) return rc;
+  if (int rc = numrs_hip_transpose(ctx, g, t->ptr, r, c)) return rc;
+  return numrs_hip_binary_backward(ctx, NUMRS_HIP_ADD, t->ptr, nullptr, nullptr, dst, nullptr,
+                                   x->numel(), 1);
+}
+
+int bw_unary(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  // sigmoid/tanh/exp/tan read the forward output (backward.rs:166-191,
+  // 486-517); the others read the input.
+  const bool uses_output = n.kind == NUMRS_HIP_SIGMOID || n.kind == NUMRS_HIP_TANH ||
+                           n.kind == NUMRS_HIP_EXP || n.kind == NUMRS_HIP_TAN;
+  const float *v = uses_output ? out->data->ptr : x->data->ptr;
+  return numrs_hip_unary_backward(out->ctx, n.kind, g, v, dst, x->numel(), n.param, acc);
+}
+
+int bw_sum(const T &out, const float *g, Node &n) {  // backward.rs:208-236
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  return numrs_hip_fill_grad(out->ctx, g, dst, x->numel(), n.op == Op::Mean, acc);
+}
+
+int bw_mse(const T &out, const float *g, Node &n) {  // backward.rs:239-261
+  const T &p = n.inputs[0], &t = n.inputs[1];
+  float *dp = nullptr, *dt = nullptr;
+  int ap = 0, at = 0;
+  if (p->requires_grad)
+    if (int rc = grad_target(p, &dp, &ap)) return rc;
+  if (t->requires_grad && !(p->requires_grad && p->grad == t->grad))
+    if (int rc = grad_target(t, &dt, &at)) return rc;
+  if (dp && dt && ap != at) {
+    if (int rc = numrs_hip_mse_backward(out->ctx, g, p->data->ptr, t->data->ptr, dp, nullptr,
+                                        p->numel(), ap))
+      return rc;
+    return numrs_hip_mse_backward(out->ctx, g, p->data->ptr, t->data->ptr, nullptr, dt,
+                                  p->numel(), at);
+  }
+  return numrs_hip_mse_backward(out->ctx, g, p->data->ptr, t->data->ptr, dp, dt, p->numel(),
+                                dp ? ap : at);
+}
+
+int bw_ce(const T &out, const float *g, Node &n) {  // backward.rs:265-301
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;  // the target's grad is [0]: nothing to add
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  const int64_t B = x->shape[0], C = x->shape[1];
+  if (n.op == Op::CrossEntropyLabels)
+    return numrs_hip_softmax_ce_backward(out->ctx, g, x->data->ptr, nullptr,
+                                         reinterpret_cast<const int32_t *>(n.saved[0]->ptr), dst,
+                                         B, C, acc);
+  return numrs_hip_softmax_ce_backward(out->ctx, g, x->data->ptr, n.inputs[1]->data->ptr, nullptr,
+                                       dst, B, C, acc);
+}
+
+int bw_reshape(const T &out, const float *g, Node &n) {  // backward.rs:315-330
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  if (!acc) return numrs_hip_copy(out->ctx, dst, g, (size_t)x->numel() * sizeof(float));
+  return numrs_hip_binary_backward(out->ctx, NUMRS_HIP_ADD, g, nullptr, nullptr, dst, nullptr,
+                                   x->numel(), 1);
+}
+
+int bw_softmax(const T &out, const float *g, Node &n) {  // backward.rs:521-541
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  const int64_t cols = out->shape.back();
+  return numrs_hip_softmax_backward(out->ctx, out->data->ptr, g, dst, out->numel() / cols, cols,
+                                    acc);
+}
+
+int bw_layernorm(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0], &gm = n.inputs[1], &bt = n.inputs[2];
+  const int64_t cols = x->shape.back(), rows = x->numel() / cols;
+  numrs_hip_ctx *ctx = out->ctx;
+  float *dx = nullptr, *dg = nullptr, *db = nullptr;
+  int ax = 0, ag = 0, ab = 0;
+  if (x->requires_grad)
+    if (int rc = grad_target(x, &dx, &ax)) return rc;
+  if (gm->requires_grad)
+    if (int rc = grad_target(gm, &dg, &ag)) return rc;
+  if (bt->requires_grad)
+    if (int rc = grad_target(bt, &db, &ab)) return rc;
+  const float *mean = n.saved[0]->ptr, *rstd = n.saved[1]->ptr;
+  if ((dx && dg && ax != ag) || (dx && db && ax != ab) || (dg && db && ag != ab)) {
+    if (dx)
+      if (int rc = numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd, dx,
+                                                nullptr, nullptr, rows, cols, ax))
+        return rc;
+    if (dg)
+      if (int rc = numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd,
+                                                nullptr, dg, nullptr, rows, cols, ag))
+        return rc;
+    if (db)
+      return numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd, nullptr,
+                                          nullptr, db, rows, cols, ab);
+    return NUMRS_HIP_OK;
+  }
+  return numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd, dx, dg, db,
+                                      rows, cols, dx ? ax : (dg ? ag : ab));
+}
+
+int run_backward_fn(const T &out) {
+  Node &n = *out->node;
+  const float *g = out->grad->buf->ptr;
+  switch (n.op) {
+    case Op::Add:
+    case Op::Sub: return bw_add_sub(out, g, n);
+    case Op::Mul:
+    case Op::Div: return bw_mul_div(out, g, n);
+    case Op::MatMul: return bw_matmul(out, g, n);
+    case Op::Transpose: return bw_transpose(out, g, n);
+    case Op::Unary: return bw_unary(out, g, n);
+    case Op::Sum:
+    case Op::Mean: return bw_sum(out, g, n);
+    case Op::MSE: return bw_mse(out, g, n);
+    case Op::CrossEntropy:
+    case Op::CrossEntropyLabels: return bw_ce(out, g, n);
+    case Op::Reshape: return bw_reshape(out, g, n);
+    case Op::Softmax: return bw_softmax(out, g, n);
+    case Op::LayerNorm: return bw_layernorm(out, g, n);
+    case Op::Leaf: return NUMRS_HIP_OK;
+  }
+  return NUMRS_HIP_OK;
+}
+
+// build_topo (tensor.rs:218-239) without recursion: post-order DFS over
+// inputs in order, each non-leaf node visited once.  Leaves carry no
+// backward body, so they are not listed.
+std::vector<Impl *> build_topo(const T &root) {
+  std::vector<Impl *> order;
+  std::unordered_set<uint64_t> visited;
+  std::vector<std::pair<Impl *, size_t>> stack;
+  if (!root->node) return order;
+  visited.insert(root->node->id);
+  stack.emplace_back(root.get(), 0);
+  while (!stack.empty()) {
+    auto &[t, i] = stack.back();
+    if (i < t->node->inputs.size()) {
+      Impl *in = t->node->inputs[i].get();
+      ++i;
+      if (in->node && visited.insert(in->node->id).second) stack.emplace_back(in, 0);
+      continue;
+    }
+    order.push_back(t);
+    stack.pop_back();
+  }
+  return order;
+}
+
+int backward(const T &root) {  // tensor.rs:173-215
+  numrs_hip_ctx *ctx = root->ctx;
+  if (!root->requires_grad) return fail(ctx, NUMRS_HIP_E_INVALID, "Tensor does not require gradients");
+  GradCell &rg = *root->grad;
+  if (!rg.buf)
+    if (int rc = alloc_buf(ctx, root->numel(), sizeof(float), &rg.buf)) return rc;
+  if (int rc = numrs_hip_fill(ctx, rg.buf->ptr, root->numel(), 1.0f)) return rc;
+  rg.valid = true;
+  std::vector<Impl *> topo = build_topo(root);
+  for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
+    Impl *t = *it;
+    if (!t->grad || !t->grad->valid) continue;  // grad still zero: contributes nothing
+    // Non-owning handle: the root keeps the whole graph alive during the sweep.
+    T self(std::shared_ptr<Impl>{}, t);
+    if (int rc = run_backward_fn(self)) return rc;
+  }
+  return NUMRS_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Forward ops (autograd/ops.rs)
+// ---------------------------------------------------------------------------
+
+int op_binary(int kind, const T &a, const T &b, T *out) {
+  numrs_hip_ctx *ctx = a->ctx;
+  const size_t nd = std::max(a->shape.size(), b->shape.size());
+  std::vector<int64_t> os(nd);
+  for (size_t d = 0; d < nd; ++d) {
+    const int da = (int)d - (int)(nd - a->shape.size()), db = (int)d - (int)(nd - b->shape.size());
+    const int64_t ea = da >= 0 ? a->shape[da] : 1, eb = db >= 0 ? b->shape[db] : 1;
+    if (ea != eb && ea != 1 && eb != 1)
+      return fail(ctx, NUMRS_HIP_E_SHAPE, "shapes do not broadcast");
+    os[d] = std::max(ea, eb);
+  }
+  const bool rec = recording({&a, &b});
+  T r;
+  if (int rc = make_tensor(ctx, os, rec, &r)) return rc;
+  if (int rc = numrs_hip_binary_forward(ctx, kind, a->data->ptr, a->shape.data(),
+                                        (int)a->shape.size(), b->data->ptr, b->shape.data(),
+                                        (int)b->shape.size(), r->data->ptr))
+    return rc;
+  if (rec) {
+    static const Op ops[4] = {Op::Add, Op::Sub, Op::Mul, Op::Div};
+    attach(r, ops[kind], {a, b});
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_matmul(const T &a, const T &b, T *out) {  // ops.rs:101-119
+  numrs_hip_ctx *ctx = a->ctx;
+  if (a->shape.size() != 2 || b->shape.size() != 2 || a->shape[1] != b->shape[0])
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "matmul expects [M,K] @ [K,N]");
+  const int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+  const bool rec = recording({&a, &b});
+  T r;
+  if (int rc = make_tensor(ctx, {M, N}, rec, &r)) return rc;
+  if (int rc = numrs_hip_matmul(ctx, a->data->ptr, b->data->ptr, r->data->ptr, M, K, N, 0, 0, 0))
+    return rc;
+  if (rec) attach(r, Op::MatMul, {a, b});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_transpose(const T &a, T *out) {  // tensor.rs:242-259
+  numrs_hip_ctx *ctx = a->ctx;
+  if (a->shape.size() != 2) return fail(ctx, NUMRS_HIP_E_SHAPE, "transpose expects 2-D");
+  const bool rec = recording({&a});
+  T r;
+  if (int rc = make_tensor(ctx, {a->shape[1], a->shape[0]}, rec, &r)) return rc;
+  if (int rc = numrs_hip_transpose(ctx, a->data->ptr, r->data->ptr, a->shape[0], a->shape[1]))
+    return rc;
+  if (rec) attach(r, Op::Transpose, {a});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_unary(int kind, const T &a, float param, T *out) {
+  numrs_hip_ctx *ctx = a->ctx;
+  const bool rec = recording({&a});
+  T r;
+  if (int rc = make_tensor(ctx, a->shape, rec, &r)) return rc;
+  if (int rc = numrs_hip_unary_forward(ctx, kind, a->data->ptr, r->data->ptr, a->numel(), param))
+    return rc;
+  if (rec) attach(r, Op::Unary, {a}, kind, param);
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_sum(const T &a, bool mean, T *out) {  // ops.rs:214-252
+  numrs_hip_ctx *ctx = a->ctx;
+  const bool rec = recording({&a});
+  T r;
+  if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
+  if (int rc = numrs_hip_sum(ctx, a->data->ptr, a->numel(), mean ? 1 : 0, r->data->ptr)) return rc;
+  if (rec) attach(r, mean ? Op::Mean : Op::Sum, {a});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_mse(const T &p, const T &t, T *out) {  // ops.rs:255-278
+  numrs_hip_ctx *ctx = p->ctx;
+  if (p->numel() != t->numel()) return fail(ctx, NUMRS_HIP_E_SHAPE, "mse_loss: size mismatch");
+  const bool rec = recording({&p, &t});
+  T r;
+  if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
+  if (int rc = numrs_hip_mse_loss(ctx, p->data->ptr, t->data->ptr, p->numel(), r->data->ptr))
+    return rc;
+  if (rec) attach(r, Op::MSE, {p, t});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_ce(const T &x, const T &t, T *out) {  // ops.rs:281-334
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.size() != 2 || t->shape.size() != 2)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "CrossEntropy expect 2D tensors [batch, classes]");
+  if (x->shape != t->shape) return fail(ctx, NUMRS_HIP_E_SHAPE, "CrossEntropy: shape mismatch");
+  const bool rec = recording({&x, &t});
+  T r;
+  if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
+  if (int rc = numrs_hip_cross_entropy_loss(ctx, x->data->ptr, t->data->ptr, nullptr, x->shape[0],
+                                            x->shape[1], r->data->ptr))
+    return rc;
+  if (rec) attach(r, Op::CrossEntropy, {x, t});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_ce_labels(const T &x, const int32_t *host_labels, T *out) {
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.size() != 2) return fail(ctx, NUMRS_HIP_E_SHAPE, "CrossEntropy expects [batch, classes]");
+  const int64_t B = x->shape[0], C = x->shape[1];
+  for (int64_t i = 0; i < B; ++i)
+    if (host_labels[i] < 0 || host_labels[i] >= C)
+      return fail(ctx, NUMRS_HIP_E_INVALID, "label %d of row %lld outside [0,%lld)",
+                  host_labels[i], (long long)i, (long long)C);
+  Buf lab;
+  if (int rc = alloc_buf(ctx, B, sizeof(int32_t), &lab)) return rc;
+  if (int rc = numrs_hip_upload(ctx, lab->ptr, host_labels, (size_t)B * sizeof(int32_t))) return rc;
+  const bool rec = recording({&x});
+  T r;
+  if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
+  if (int rc = numrs_hip_cross_entropy_loss(ctx, x->data->ptr, nullptr,
+                                            reinterpret_cast<const int32_t *>(lab->ptr), B, C,
+                                            r->data->ptr))
+    return rc;
+  if (rec) attach(r, Op::CrossEntropyLabels, {x}, 0, 0.f, {lab});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_reshape(const T &a, std::vector<int64_t> shape, T *out) {  // ops.rs:353-369
+  numrs_hip_ctx *ctx = a->ctx;
+  int64_t n = 1;
+  for (int64_t d : shape) {
+    if (d < 0) return fail(ctx, NUMRS_HIP_E_SHAPE, "reshape: negative dimension");
+    n *= d;
+  }
+  if (n != a->numel()) return fail(ctx, NUMRS_HIP_E_SHAPE, "reshape: element count differs");
+  const bool rec = recording({&a});
+  auto r = std::make_shared<Impl>();
+  r->ctx = ctx;
+  r->shape = std::move(shape);
+  r->data = a->data;  // values are never written in place by the graph: share them
+  r->requires_grad = rec;
+  if (rec) {
+    r->grad = std::make_shared<GradCell>();
+    attach(r, Op::Reshape, {a});
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_softmax(const T &a, T *out) {
+  numrs_hip_ctx *ctx = a->ctx;
+  if (a->shape.empty()) return fail(ctx, NUMRS_HIP_E_SHAPE, "softmax of a scalar");
+  const bool rec = recording({&a});
+  T r;
+  if (int rc = make_tensor(ctx, a->shape, rec, &r)) return rc;
+  const int64_t cols = a->shape.back();
+  if (int rc = numrs_hip_softmax_forward(ctx, a->data->ptr, r->data->ptr, a->numel() / cols, cols,
+                                         1.0f))
+    return rc;
+  if (rec) attach(r, Op::Softmax, {a});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_layernorm(const T &x, const T &gamma, const T &beta, float eps, T *out) {
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.empty()) return fail(ctx, NUMRS_HIP_E_SHAPE, "layer_norm of a scalar");
+  const int64_t cols = x->shape.back(), rows = x->numel() / cols;
+  if (gamma->numel() != cols || beta->numel() != cols)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "layer_norm: gamma/beta must have the last-axis length");
+  const bool rec = recording({&x, &gamma, &beta});
+  T r;
+  if (int rc = make_tensor(ctx, x->shape, rec, &r)) return rc;
+  Buf mean, rstd;
+  if (int rc = alloc_buf(ctx, rows, sizeof(float), &mean)) return rc;
+  if (int rc = alloc_buf(ctx, rows, sizeof(float), &rstd)) return rc;
+  if (int rc = numrs_hip_layernorm_forward(ctx, x->data->ptr, gamma->data->ptr, beta->data->ptr,
+                                           r->data->ptr, mean->ptr, rstd->ptr, rows, cols, eps))
+    return rc;
+  if (rec) attach(r, Op::LayerNorm, {x, gamma, beta}, 0, eps, {mean, rstd});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Optimizers (optim/base.rs, sgd.rs, adam.rs)
+// ---------------------------------------------------------------------------
+
+struct Optim {
+  numrs_hip_ctx *ctx;
+  bool adam;
+  std::vector<T> params;
+  std::vector<Buf> s1, s2;  // SGD velocity | Adam m, v
+  float lr, mu = 0.f, wd = 0.f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+  int t = 0;
+};
+
+}  // namespace
+
+struct numrs_hip_tensor {
+  T t;
+};
+struct numrs_hip_optim {
+  Optim o;
+};
+
+namespace {
+
+int wrap(T t, numrs_hip_tensor **out) {
+  *out = new numrs_hip_tensor{std::move(t)};
+  return NUMRS_HIP_OK;
+}
+
+int check2(const numrs_hip_tensor *a, const numrs_hip_tensor *b, numrs_hip_tensor **out) {
+  if (a == nullptr || b == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  if (a->t->ctx != b->t->ctx)
+    return fail(a->t->ctx, NUMRS_HIP_E_INVALID, "tensors belong to different contexts");
+  *out = nullptr;
+  return NUMRS_HIP_OK;
+}
+
+int new_optim(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, bool adam, Optim *o) {
+  o->ctx = ctx;
+  o->adam = adam;
+  for (int i = 0; i < n; ++i) {
+    if (params[i] == nullptr) return fail(ctx, NUMRS_HIP_E_INVALID, "null parameter %d", i);
+    const T &p = params[i]->t;
+    o->params.push_back(p);
+    Buf a, b;
+    // Velocities / moments start at zero (sgd.rs:96-103, adam.rs:258-272).
+    if (int rc = alloc_buf(ctx, p->numel(), sizeof(float), &a)) return rc;
+    if (int rc = numrs_hip_fill(ctx, a->ptr, p->numel(), 0.0f)) return rc;
+    if (adam) {
+      if (int rc = alloc_buf(ctx, p->numel(), sizeof(float), &b)) return rc;
+      if (int rc = numrs_hip_fill(ctx, b->ptr, p->numel(), 0.0f)) return rc;
+    }
+    o->s1.push_back(a);
+    o->s2.push_back(b);
+  }
+  return NUMRS_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void numrs_hip_set_grad_enabled(int enabled) { g_grad_enabled = enabled != 0; }
+int numrs_hip_is_grad_enabled(void) { return g_grad_enabled ? 1 : 0; }
+
+int numrs_hip_set_unbroadcast_mode(numrs_hip_ctx *ctx, int mode) {
+  NRS_CHECK_CTX(ctx);
+  if (mode != NUMRS_HIP_UNBROADCAST_CORRECT && mode != NUMRS_HIP_UNBROADCAST_REFERENCE)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "unbroadcast mode %d", mode);
+  ctx->unbroadcast_mode = mode;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_tensor_new(numrs_hip_ctx *ctx, const float *host, const int64_t *shape, int ndim,
+                         int requires_grad, numrs_hip_tensor **out) {
+  NRS_CHECK_CTX(ctx);
+  if (out == nullptr || ndim < 0 || ndim > 8 || (ndim > 0 && shape == nullptr))
+    return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_tensor_new: bad arguments");
+  std::vector<int64_t> s(shape, shape + ndim);
+  for (int64_t d : s)
+    if (d < 0) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_tensor_new: negative dimension");
+  T t;
+  if (int rc = make_tensor(ctx, s, requires_grad != 0, &t)) return rc;
+  if (t->numel() > 0) {
+    if (host == nullptr) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_tensor_new: null data");
+    if (int rc = numrs_hip_upload(ctx, t->data->ptr, host, (size_t)t->numel() * sizeof(float)))
+      return rc;
+  }
+  return wrap(std::move(t), out);
+}
+
+int numrs_hip_tensor_free(numrs_hip_tensor *t) {
+  delete t;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_tensor_shape(const numrs_hip_tensor *t, int64_t *shape, int cap) {
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  const int nd = (int)t->t->shape.size();
+  for (int i = 0; i < nd && i < cap && shape; ++i) shape[i] = t->t->shape[i];
+  return nd;
+}
+
+int64_t numrs_hip_tensor_numel(const numrs_hip_tensor *t) {
+  return t == nullptr ? NUMRS_HIP_E_INVALID : t->t->numel();
+}
+
+int numrs_hip_tensor_requires_grad(const numrs_hip_tensor *t) {
+  return t == nullptr ? NUMRS_HIP_E_INVALID : (t->t->requires_grad ? 1 : 0);
+}
+
+int numrs_hip_tensor_is_leaf(const numrs_hip_tensor *t) {
+  return t == nullptr ? NUMRS_HIP_E_INVALID : (t->t->is_leaf ? 1 : 0);
+}
+
+int numrs_hip_tensor_values(numrs_hip_tensor *t, float *host, int64_t n) {
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  if (n != t->t->numel()) return fail(t->t->ctx, NUMRS_HIP_E_SHAPE, "values: buffer of %lld for %lld elements", (long long)n, (long long)t->t->numel());
+  return numrs_hip_download(t->t->ctx, host, t->t->data->ptr, (size_t)n * sizeof(float));
+}
+
+int numrs_hip_tensor_gradient(numrs_hip_tensor *t, float *host, int64_t n) {
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  const T &x = t->t;
+  if (!x->grad) return 0;  // Option::None (tensor.rs:96-98)
+  if (n != x->numel()) return fail(x->ctx, NUMRS_HIP_E_SHAPE, "gradient: buffer size mismatch");
+  if (int rc = grad_materialise(x)) return rc;
+  if (int rc = numrs_hip_download(x->ctx, host, x->grad->buf->ptr, (size_t)n * sizeof(float)))
+    return rc;
+  return 1;
+}
+
+int numrs_hip_tensor_set_gradient(numrs_hip_tensor *t, const float *host, int64_t n) {
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  const T &x = t->t;
+  if (!x->grad) return fail(x->ctx, NUMRS_HIP_E_INVALID, "Tensor does not require gradients");
+  if (n != x->numel()) return fail(x->ctx, NUMRS_HIP_E_SHAPE, "set_gradient: size mismatch");
+  if (!x->grad->buf)
+    if (int rc = alloc_buf(x->ctx, n, sizeof(float), &x->grad->buf)) return rc;
+  if (int rc = numrs_hip_upload(x->ctx, x->grad->buf->ptr, host, (size_t)n * sizeof(float))) return rc;
+  x->grad->valid = true;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_tensor_zero_grad(numrs_hip_tensor *t) {  // tensor.rs:135-142
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  if (t->t->grad) t->t->grad->valid = false;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_tensor_device_ptrs(numrs_hip_tensor *t, float **data, float **grad) {
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  if (data) *data = t->t->data->ptr;
+  if (grad) {
+    *grad = nullptr;
+    if (t->t->grad) {
+      if (int rc = grad_materialise(t->t)) return rc;
+      *grad = t->t->grad->buf->ptr;
+    }
+  }
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_tensor_backward(numrs_hip_tensor *t) {
+  if (t == nullptr) return NUMRS_HIP_E_INVALID;
+  return backward(t->t);
+}
+
+int numrs_hip_tensor_detach(numrs_hip_tensor *t, numrs_hip_tensor **out) {  // tensor.rs:146-154
+  if (t == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  auto r = std::make_shared<Impl>();
+  r->ctx = t->t->ctx;
+  r->shape = t->t->shape;
+  r->data = t->t->data;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_binary(int kind, numrs_hip_tensor *a, numrs_hip_tensor *b,
+                            numrs_hip_tensor **out) {
+  if (int rc = check2(a, b, out)) return rc;
+  if (kind < NUMRS_HIP_ADD || kind > NUMRS_HIP_DIV)
+    return fail(a->t->ctx, NUMRS_HIP_E_INVALID, "binary kind %d", kind);
+  T r;
+  if (int rc = op_binary(kind, a->t, b->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_unary(int kind, numrs_hip_tensor *a, float param, numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  if (kind < NUMRS_HIP_RELU || kind > NUMRS_HIP_POW)
+    return fail(a->t->ctx, NUMRS_HIP_E_INVALID, "unary kind %d", kind);
+  T r;
+  if (int rc = op_unary(kind, a->t, param, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_matmul(numrs_hip_tensor *a, numrs_hip_tensor *b, numrs_hip_tensor **out) {
+  if (int rc = check2(a, b, out)) return rc;
+  T r;
+  if (int rc = op_matmul(a->t, b->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_transpose(numrs_hip_tensor *a, numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_transpose(a->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_reshape(numrs_hip_tensor *a, const int64_t *shape, int ndim,
+                             numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr || ndim < 0 || ndim > 8 || (ndim && !shape))
+    return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_reshape(a->t, std::vector<int64_t>(shape, shape + ndim), &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_sum(numrs_hip_tensor *a, int mean, numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_sum(a->t, mean != 0, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_mse_loss(numrs_hip_tensor *pred, numrs_hip_tensor *target,
+                              numrs_hip_tensor **out) {
+  if (int rc = check2(pred, target, out)) return rc;
+  T r;
+  if (int rc = op_mse(pred->t, target->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_cross_entropy_loss(numrs_hip_tensor *logits, numrs_hip_tensor *target,
+                                        numrs_hip_tensor **out) {
+  if (int rc = check2(logits, target, out)) return rc;
+  T r;
+  if (int rc = op_ce(logits->t, target->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_cross_entropy_labels(numrs_hip_tensor *logits, const int32_t *host_labels,
+                                          numrs_hip_tensor **out) {
+  if (logits == nullptr || host_labels == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_ce_labels(logits->t, host_labels, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_softmax(numrs_hip_tensor *a, numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_softmax(a->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
+                                numrs_hip_tensor *beta, float eps, numrs_hip_tensor **out) {
+  if (x == nullptr || gamma == nullptr || beta == nullptr || out == nullptr)
+    return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_layernorm(x->t, gamma->t, beta->t, eps, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_optim_sgd(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
+                        float momentum, float wd, numrs_hip_optim **out) {
+  NRS_CHECK_CTX(ctx);
+  if (out == nullptr || n < 0 || (n > 0 && params == nullptr)) return NUMRS_HIP_E_INVALID;
+  auto *o = new numrs_hip_optim();
+  o->o.lr = lr;
+  o->o.mu = momentum;
+  o->o.wd = wd;
+  if (int rc = new_optim(ctx, params, n, false, &o->o)) {
+    delete o;
+    return rc;
+  }
+  *out = o;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_adam(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
+                         float b1, float b2, float eps, float wd, numrs_hip_optim **out) {
+  NRS_CHECK_CTX(ctx);
+  if (out == nullptr || n < 0 || (n > 0 && params == nullptr)) return NUMRS_HIP_E_INVALID;
+  auto *o = new numrs_hip_optim();
+  o->o.lr = lr;
+  o->o.b1 = b1;
+  o->o.b2 = b2;
+  o->o.eps = eps;
+  o->o.wd = wd;
+  if (int rc = new_optim(ctx, params, n, true, &o->o)) {
+    delete o;
+    return rc;
+  }
+  *out = o;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_step(numrs_hip_optim *opt) {
+  if (opt == nullptr) return NUMRS_HIP_E_INVALID;
+  Optim &o = opt->o;
+  if (o.adam) ++o.t;  // adam.rs:311
+  for (size_t i = 0; i < o.params.size(); ++i) {
+    const T &p = o.params[i];
+    if (!p->requires_grad) continue;  // sgd.rs:134-136, adam.rs:320-322
+    if (int rc = grad_materialise(p)) return rc;
+    const float *g = p->grad->buf->ptr;
+    int rc = o.adam ? numrs_hip_adam_step(o.ctx, p->data->ptr, g, o.s1[i]->ptr, o.s2[i]->ptr,
+                                          p->numel(), o.lr, o.b1, o.b2, o.eps, o.wd, o.t)
+                    : numrs_hip_sgd_step(o.ctx, p->data->ptr, g, o.s1[i]->ptr, p->numel(), o.lr,
+                                         o.mu, o.wd);
+    if (rc) return rc;
+  }
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_zero_grad(numrs_hip_optim *opt) {  // sgd.rs:169-173
+  if (opt == nullptr) return NUMRS_HIP_E_INVALID;
+  for (const T &p : opt->o.params)
+    if (p->grad) p->grad->valid = false;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_set_lr(numrs_hip_optim *opt, float lr) {
+  if (opt == nullptr) return NUMRS_HIP_E_INVALID;
+  opt->o.lr = lr;
+  return NUMRS_HIP_OK;
+}
+
+float numrs_hip_optim_lr(const numrs_hip_optim *opt) { return opt == nullptr ? NAN : opt->o.lr; }
+
+int numrs_hip_optim_free(numrs_hip_optim *opt) {
+  delete opt;
+  return NUMRS_HIP_OK;
+}
+
+}  // extern "C"

@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <unordered_map>
+#include <vector>
 
 #include "numrs_hip.h"
 
@@ -17,8 +19,21 @@ struct numrs_hip_ctx {
   char arch[64] = {0};
   hipStream_t stream = nullptr;
   hipEvent_t events[kMaxTimers] = {};
-  void *workspace = nullptr;
+  void *workspace = nullptr;  // reduction partials (reused by every call)
   size_t workspace_bytes = 0;
+  void *scratch = nullptr;    // a second region for values that must outlive a
+  size_t scratch_bytes = 0;   // workspace user inside the same call
+  // Stream-ordered block cache of the tensor engine: every kernel runs on
+  // `stream`, so a block released by one tensor can be handed to the next
+  // allocation without a device synchronisation.
+  std::unordered_map<size_t, std::vector<void *>> free_blocks;
+  size_t cached_bytes = 0;
+  // Engine blocks still owned by tensors.  numrs_hip_destroy with live blocks
+  // only marks the context destroyed; the last block_free then deletes it, so
+  // tensors may safely outlive their context's destroy call.
+  int64_t live_blocks = 0;
+  bool destroyed = false;
+  int unbroadcast_mode = NUMRS_HIP_UNBROADCAST_CORRECT;
   char last_error[512] = {0};
 };
 
@@ -29,6 +44,16 @@ int fail(numrs_hip_ctx *ctx, int code, const char *fmt, ...);
 
 // Returns the context's workspace with at least `bytes` bytes (grows it).
 int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out);
+
+// Second scratch region (see numrs_hip_ctx::scratch).
+int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out);
+
+// Cached device allocation for engine tensors; sizes are rounded up so that
+// released blocks are reusable.  block_free returns the block to the cache.
+int block_alloc(numrs_hip_ctx *ctx, size_t bytes, void **out);
+void block_free(numrs_hip_ctx *ctx, void *p, size_t bytes);
+size_t block_round(size_t bytes);
+void cache_release(numrs_hip_ctx *ctx);
 
 // Checks the launch that was just enqueued.
 int check_launch(numrs_hip_ctx *ctx, const char *what);

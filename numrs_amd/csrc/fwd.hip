@@ -1,0 +1,409 @@
+// Forward kernels the autograd engine records nodes for: broadcasting binary
+// ops, activations, 2-D transpose, full reductions and losses, row softmax and
+// LayerNorm.  They stand where the reference's DispatchTable kernels and the
+// inline loops of autograd/ops.rs stand (backend/dispatch.rs:69-93,
+// autograd/ops.rs:14-555), so that a whole training step stays on the device.
+#include <cmath>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Elementwise binary with numpy broadcasting (promotion_wrappers.rs:25-168)
+// ---------------------------------------------------------------------------
+
+template <int OP>
+__device__ __forceinline__ float bin(float a, float b) {
+  if constexpr (OP == NUMRS_HIP_ADD) return a + b;
+  else if constexpr (OP == NUMRS_HIP_SUB) return a - b;
+  else if constexpr (OP == NUMRS_HIP_MUL) return a * b;
+  else return a / b;
+}
+
+struct Bcast {
+  int nd;
+  int64_t shape[8];
+  int64_t sa[8], sb[8];  // element strides of a and b (0 on broadcast axes)
+};
+
+template <int OP>
+__global__ void __launch_bounds__(kBlock)
+    binary_flat_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                       float *__restrict__ out, int64_t n, int a_scalar, int b_scalar) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  out[i] = bin<OP>(a[a_scalar ? 0 : i], b[b_scalar ? 0 : i]);
+}
+
+// [rows, cols] op [cols] (the Linear bias add and its relatives).
+template <int OP>
+__global__ void __launch_bounds__(kBlock)
+    binary_rowbcast_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                           float *__restrict__ out, int64_t rows, int64_t cols, int b_is_row) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= rows * cols) return;
+  const int64_t c = i % cols;
+  out[i] = b_is_row ? bin<OP>(a[i], b[c]) : bin<OP>(b[c], a[i]);
+}
+
+template <int OP>
+__global__ void __launch_bounds__(kBlock)
+    binary_bcast_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                        float *__restrict__ out, int64_t n, Bcast bc) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  int64_t rem = i, ia = 0, ib = 0;
+  for (int d = bc.nd - 1; d >= 0; --d) {
+    const int64_t c = rem % bc.shape[d];
+    rem /= bc.shape[d];
+    ia += c * bc.sa[d];
+    ib += c * bc.sb[d];
+  }
+  out[i] = bin<OP>(a[ia], b[ib]);
+}
+
+// ---------------------------------------------------------------------------
+// Unary forward (autograd/ops.rs:122-211, 488-554; GELU is new)
+// ---------------------------------------------------------------------------
+
+template <int KIND>
+__device__ __forceinline__ float un(float x, float p) {
+  if constexpr (KIND == NUMRS_HIP_RELU) return fmaxf(x, 0.0f);  // x.max(0.0), NaN -> 0
+  else if constexpr (KIND == NUMRS_HIP_SIGMOID) return 1.0f / (1.0f + expf(-x));
+  else if constexpr (KIND == NUMRS_HIP_TANH) return tanhf(x);
+  else if constexpr (KIND == NUMRS_HIP_EXP) return expf(x);
+  else if constexpr (KIND == NUMRS_HIP_LOG) return logf(x);
+  else if constexpr (KIND == NUMRS_HIP_GELU) return x * 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+  else if constexpr (KIND == NUMRS_HIP_SQRT) return sqrtf(x);
+  else if constexpr (KIND == NUMRS_HIP_SIN) return sinf(x);
+  else if constexpr (KIND == NUMRS_HIP_COS) return cosf(x);
+  else if constexpr (KIND == NUMRS_HIP_TAN) return tanf(x);
+  else return powf(x, p);
+}
+
+template <int KIND>
+__global__ void __launch_bounds__(kBlock)
+    unary_fwd_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t n, float p) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) y[i] = un<KIND>(x[i], p);
+}
+
+// ---------------------------------------------------------------------------
+// Transpose (ops/shape/transpose.rs:9-88): 32x32 LDS tiles, padded rows.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kBlock)
+    transpose_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
+                     int64_t cols) {
+  __shared__ float tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) tile[k][tx] = x[r * cols + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;  // output row c, column r
+    if (c < cols && r < rows) y[c * rows + r] = tile[tx][k];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Full reductions: sum / mean / MSE loss (ops.rs:214-278)
+// ---------------------------------------------------------------------------
+
+// kind 0: sum x; 1: sum (x - t)^2
+template <int KIND>
+__global__ void __launch_bounds__(kBlock)
+    reduce_pass1(const float *__restrict__ x, const float *__restrict__ t, int64_t n,
+                 float *__restrict__ partial) {
+  __shared__ float red[kBlock / 64];
+  float s = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kBlock) {
+    if (KIND == 0) {
+      s += x[i];
+    } else {
+      const float d = x[i] - t[i];
+      s += d * d;
+    }
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// out[0] = (sum of partials) / div   (div = 1 for a plain sum)
+__global__ void __launch_bounds__(kBlock)
+    reduce_final(const float *__restrict__ partial, int64_t count, float div,
+                 float *__restrict__ out) {
+  __shared__ float red[kBlock / 64];
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < count; i += kBlock) s += partial[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = (((red[0] + red[1]) + red[2]) + red[3]) / div;
+}
+
+// Cross-entropy rows (ops.rs:281-318): per row -sum_j t_j * ((x_j - m) - log(sum e)).
+template <bool LABELS>
+__global__ void __launch_bounds__(kBlock)
+    ce_rows_kernel(const float *__restrict__ x, const float *__restrict__ onehot,
+                   const int32_t *__restrict__ labels, float *__restrict__ row_loss, int64_t B,
+                   int64_t C) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= B) return;
+  const float *xr = x + row * C;
+  float m = -INFINITY;
+  for (int64_t j = lane; j < C; j += 64) m = fmaxf(m, xr[j]);
+  m = wave_max(m);
+  float s = 0.0f;
+  for (int64_t j = lane; j < C; j += 64) s += expf(xr[j] - m);
+  s = wave_sum(s);
+  const float ls = logf(s);
+  float l = 0.0f;
+  for (int64_t j = lane; j < C; j += 64) {
+    const float t = LABELS ? (j == (int64_t)labels[row] ? 1.0f : 0.0f) : onehot[row * C + j];
+    l += -t * ((xr[j] - m) - ls);
+  }
+  l = wave_sum(l);
+  if (lane == 0) row_loss[row] = l;
+}
+
+// ---------------------------------------------------------------------------
+// Row softmax and LayerNorm forward (new ops for the transformer config)
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kBlock)
+    softmax_rows_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
+                        int64_t cols, float scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = x + row * cols;
+  float m = -INFINITY;
+  for (int64_t j = lane; j < cols; j += 64) m = fmaxf(m, xr[j] * scale);
+  m = wave_max(m);
+  float s = 0.0f;
+  for (int64_t j = lane; j < cols; j += 64) s += expf(xr[j] * scale - m);
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  for (int64_t j = lane; j < cols; j += 64) y[row * cols + j] = expf(xr[j] * scale - m) * inv;
+}
+
+// y = (x - mean) * rstd * gamma + beta; rstd = 1/sqrt(var + eps), biased var.
+__global__ void __launch_bounds__(kBlock)
+    layernorm_fwd_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
+                         const float *__restrict__ beta, float *__restrict__ y,
+                         float *__restrict__ mean, float *__restrict__ rstd, int64_t rows,
+                         int64_t cols, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = x + row * cols;
+  float s = 0.0f;
+  for (int64_t j = lane; j < cols; j += 64) s += xr[j];
+  const float mu = wave_sum(s) / (float)cols;
+  float v = 0.0f;
+  for (int64_t j = lane; j < cols; j += 64) {
+    const float d = xr[j] - mu;
+    v += d * d;
+  }
+  const float rs = 1.0f / sqrtf(wave_sum(v) / (float)cols + eps);
+  for (int64_t j = lane; j < cols; j += 64)
+    y[row * cols + j] = (xr[j] - mu) * rs * gamma[j] + beta[j];
+  if (lane == 0) {
+    if (mean) mean[row] = mu;
+    if (rstd) rstd[row] = rs;
+  }
+}
+
+template <int OP>
+int launch_binary_fwd(numrs_hip_ctx *ctx, const float *a, const int64_t *as, int and_,
+                      const float *b, const int64_t *bs, int bnd, float *out) {
+  int64_t an = 1, bn = 1;
+  for (int d = 0; d < and_; ++d) an *= as[d];
+  for (int d = 0; d < bnd; ++d) bn *= bs[d];
+  const int nd = and_ > bnd ? and_ : bnd;
+  Bcast bc;
+  bc.nd = nd;
+  int64_t n = 1;
+  for (int d = 0; d < nd; ++d) {
+    const int da = d - (nd - and_), db = d - (nd - bnd);
+    const int64_t ea = da >= 0 ? as[da] : 1, eb = db >= 0 ? bs[db] : 1;
+    if (ea != eb && ea != 1 && eb != 1)
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_SHAPE, "binary op: shapes do not broadcast");
+    bc.shape[d] = ea > eb ? ea : eb;
+    n *= bc.shape[d];
+  }
+  if (n == 0) return NUMRS_HIP_OK;
+  const unsigned grid = grid_for(n, kBlock);
+  if (an == n && bn == n) {
+    binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, 0, 0);
+  } else if (bn == 1 && an == n) {
+    binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, 0, 1);
+  } else if (an == 1 && bn == n) {
+    binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, 1, 0);
+  } else if (an == n && bnd >= 1 && bn == bs[bnd - 1] && bn == bc.shape[nd - 1]) {
+    binary_rowbcast_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n / bn, bn, 1);
+  } else if (bn == n && and_ >= 1 && an == as[and_ - 1] && an == bc.shape[nd - 1]) {
+    binary_rowbcast_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(b, a, out, n / an, an, 0);
+  } else {
+    int64_t sa = 1, sb = 1;
+    for (int d = nd - 1; d >= 0; --d) {
+      const int da = d - (nd - and_), db = d - (nd - bnd);
+      const int64_t ea = da >= 0 ? as[da] : 1, eb = db >= 0 ? bs[db] : 1;
+      bc.sa[d] = ea == 1 ? 0 : sa;
+      bc.sb[d] = eb == 1 ? 0 : sb;
+      sa *= ea;
+      sb *= eb;
+    }
+    binary_bcast_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, bc);
+  }
+  return numrs_hip::check_launch(ctx, "binary forward");
+}
+
+int full_reduce(numrs_hip_ctx *ctx, int kind, const float *x, const float *t, int64_t n,
+                float div, float *out) {
+  int64_t blocks = (n + kBlock * 16 - 1) / (kBlock * 16);
+  if (blocks < 1) blocks = 1;
+  if (blocks > 1024) blocks = 1024;
+  void *ws = nullptr;
+  if (int rc = numrs_hip::workspace(ctx, (size_t)blocks * sizeof(float), &ws)) return rc;
+  float *partial = static_cast<float *>(ws);
+  if (kind == 0)
+    reduce_pass1<0><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  else
+    reduce_pass1<1><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  if (int rc = numrs_hip::check_launch(ctx, "reduce_pass1")) return rc;
+  reduce_final<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, div, out);
+  return numrs_hip::check_launch(ctx, "reduce_final");
+}
+
+}  // namespace
+
+extern "C" {
+
+int numrs_hip_binary_forward(numrs_hip_ctx *ctx, int kind, const float *a, const int64_t *ashape,
+                             int and_, const float *b, const int64_t *bshape, int bnd, float *out) {
+  NRS_CHECK_CTX(ctx);
+  if (and_ < 0 || bnd < 0 || and_ > 8 || bnd > 8 || (and_ && !ashape) || (bnd && !bshape))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_binary_forward: bad shapes");
+  if (a == nullptr || b == nullptr || out == nullptr) {
+    int64_t an = 1, bn = 1;
+    for (int d = 0; d < and_; ++d) an *= ashape[d];
+    for (int d = 0; d < bnd; ++d) bn *= bshape[d];
+    if (an != 0 && bn != 0)
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_binary_forward: null pointer");
+  }
+  switch (kind) {
+    case NUMRS_HIP_ADD: return launch_binary_fwd<NUMRS_HIP_ADD>(ctx, a, ashape, and_, b, bshape, bnd, out);
+    case NUMRS_HIP_SUB: return launch_binary_fwd<NUMRS_HIP_SUB>(ctx, a, ashape, and_, b, bshape, bnd, out);
+    case NUMRS_HIP_MUL: return launch_binary_fwd<NUMRS_HIP_MUL>(ctx, a, ashape, and_, b, bshape, bnd, out);
+    case NUMRS_HIP_DIV: return launch_binary_fwd<NUMRS_HIP_DIV>(ctx, a, ashape, and_, b, bshape, bnd, out);
+    default: return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_binary_forward: kind %d", kind);
+  }
+}
+
+int numrs_hip_unary_forward(numrs_hip_ctx *ctx, int kind, const float *x, float *y, int64_t n,
+                            float param) {
+  NRS_CHECK_CTX(ctx);
+  if (n < 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_unary_forward: n < 0");
+  if (n == 0) return NUMRS_HIP_OK;
+  if (x == nullptr || y == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_unary_forward: null pointer");
+  const unsigned grid = grid_for(n, kBlock);
+#define NRS_UN(K) unary_fwd_kernel<K><<<grid, kBlock, 0, ctx->stream>>>(x, y, n, param); break
+  switch (kind) {
+    case NUMRS_HIP_RELU: NRS_UN(NUMRS_HIP_RELU);
+    case NUMRS_HIP_SIGMOID: NRS_UN(NUMRS_HIP_SIGMOID);
+    case NUMRS_HIP_TANH: NRS_UN(NUMRS_HIP_TANH);
+    case NUMRS_HIP_EXP: NRS_UN(NUMRS_HIP_EXP);
+    case NUMRS_HIP_LOG: NRS_UN(NUMRS_HIP_LOG);
+    case NUMRS_HIP_GELU: NRS_UN(NUMRS_HIP_GELU);
+    case NUMRS_HIP_SQRT: NRS_UN(NUMRS_HIP_SQRT);
+    case NUMRS_HIP_SIN: NRS_UN(NUMRS_HIP_SIN);
+    case NUMRS_HIP_COS: NRS_UN(NUMRS_HIP_COS);
+    case NUMRS_HIP_TAN: NRS_UN(NUMRS_HIP_TAN);
+    case NUMRS_HIP_POW: NRS_UN(NUMRS_HIP_POW);
+    default: return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_unary_forward: kind %d", kind);
+  }
+#undef NRS_UN
+  return numrs_hip::check_launch(ctx, "unary_fwd_kernel");
+}
+
+int numrs_hip_transpose(numrs_hip_ctx *ctx, const float *x, float *y, int64_t rows, int64_t cols) {
+  NRS_CHECK_CTX(ctx);
+  if (rows < 0 || cols < 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: negative size");
+  if (rows == 0 || cols == 0) return NUMRS_HIP_OK;
+  if (x == nullptr || y == nullptr) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: null pointer");
+  if ((rows + 31) / 32 > 65535) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: too many rows");
+  dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
+  transpose_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
+  return numrs_hip::check_launch(ctx, "transpose_kernel");
+}
+
+int numrs_hip_sum(numrs_hip_ctx *ctx, const float *x, int64_t n, int mean, float *out) {
+  NRS_CHECK_CTX(ctx);
+  if (n < 0 || out == nullptr || (n > 0 && x == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_sum: bad arguments");
+  if (n == 0) return numrs_hip_fill(ctx, out, 1, mean ? NAN : 0.0f);
+  return full_reduce(ctx, 0, x, nullptr, n, mean ? (float)n : 1.0f, out);
+}
+
+int numrs_hip_mse_loss(numrs_hip_ctx *ctx, const float *p, const float *t, int64_t n, float *out) {
+  NRS_CHECK_CTX(ctx);
+  if (n <= 0 || p == nullptr || t == nullptr || out == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_loss: bad arguments");
+  return full_reduce(ctx, 1, p, t, n, (float)n, out);
+}
+
+int numrs_hip_cross_entropy_loss(numrs_hip_ctx *ctx, const float *logits, const float *onehot,
+                                 const int32_t *labels, int64_t B, int64_t C, float *out) {
+  NRS_CHECK_CTX(ctx);
+  if (B <= 0 || C <= 0 || logits == nullptr || out == nullptr ||
+      (onehot == nullptr) == (labels == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_cross_entropy_loss: bad arguments");
+  // Row losses live in the scratch region; the reduction below uses the workspace.
+  float *rows = nullptr;
+  if (int rc = numrs_hip::scratch(ctx, (size_t)B * sizeof(float), &rows)) return rc;
+  if (labels)
+    ce_rows_kernel<true><<<grid_for(B, 4), kBlock, 0, ctx->stream>>>(logits, onehot, labels, rows, B, C);
+  else
+    ce_rows_kernel<false><<<grid_for(B, 4), kBlock, 0, ctx->stream>>>(logits, onehot, labels, rows, B, C);
+  if (int rc = numrs_hip::check_launch(ctx, "ce_rows_kernel")) return rc;
+  return full_reduce(ctx, 0, rows, nullptr, B, (float)B, out);
+}
+
+int numrs_hip_softmax_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t rows,
+                              int64_t cols, float scale) {
+  NRS_CHECK_CTX(ctx);
+  if (rows < 0 || cols < 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "softmax: negative size");
+  if (rows == 0 || cols == 0) return NUMRS_HIP_OK;
+  if (x == nullptr || y == nullptr) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "softmax: null pointer");
+  softmax_rows_kernel<<<grid_for(rows, 4), kBlock, 0, ctx->stream>>>(x, y, rows, cols, scale);
+  return numrs_hip::check_launch(ctx, "softmax_rows_kernel");
+}
+
+int numrs_hip_layernorm_forward(numrs_hip_ctx *ctx, const float *x, const float *gamma,
+                                const float *beta, float *y, float *mean, float *rstd,
+                                int64_t rows, int64_t cols, float eps) {
+  NRS_CHECK_CTX(ctx);
+  if (rows < 0 || cols <= 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "layernorm: bad size");
+  if (rows == 0) return NUMRS_HIP_OK;
+  if (x == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "layernorm: null pointer");
+  layernorm_fwd_kernel<<<grid_for(rows, 4), kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean,
+                                                                      rstd, rows, cols, eps);
+  return numrs_hip::check_launch(ctx, "layernorm_fwd_kernel");
+}
+
+}  // extern "C"

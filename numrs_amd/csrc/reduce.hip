@@ -229,6 +229,70 @@ __global__ void __launch_bounds__(kBlock)
   out[o] = acc ? out[o] + s : s;
 }
 
+// LayerNorm backward (new op; closed form, fp32):
+//   xh = (x - mean) * rstd,  gg = g * gamma
+//   dx = rstd * (gg - mean_row(gg) - xh * mean_row(gg * xh))
+//   dgamma = sum_rows g * xh,  dbeta = sum_rows g
+// Pass 1: a block owns kLnRows rows; each wave takes every 4th row and
+// keeps per-column partials of g*xh and g in its own LDS rows (lane j owns
+// columns j, j+64, ...: no sharing, no atomics).  The four wave partials are
+// added in wave order into the [chunk, cols] workspace; the dgamma/dbeta
+// finalize is colreduce_finalize.
+constexpr int kLnMaxCols = 2048;
+constexpr int kLnRows = 16;  // rows per block: [4096, 512] gives 256 blocks
+
+__global__ void __launch_bounds__(kBlock)
+    layernorm_bwd_pass1(const float *__restrict__ g, const float *__restrict__ x,
+                        const float *__restrict__ gamma, const float *__restrict__ mean,
+                        const float *__restrict__ rstd, float *__restrict__ dx,
+                        float *__restrict__ part_g, float *__restrict__ part_b, int64_t rows,
+                        int64_t cols, int acc_dx, int want_params) {
+  extern __shared__ float lds[];  // [2][4][cols]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float *pg = lds + wave * cols;
+  float *pb = lds + (4 + wave) * cols;
+  for (int64_t j = lane; j < cols; j += 64) {
+    pg[j] = 0.0f;
+    pb[j] = 0.0f;
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * kLnRows;
+  const int64_t r1 = min(r0 + (int64_t)kLnRows, rows);
+  const float inv_n = 1.0f / (float)cols;
+  for (int64_t r = r0 + wave; r < r1; r += 4) {
+    const float *xr = x + r * cols, *gr = g + r * cols;
+    const float mu = mean[r], rs = rstd[r];
+    float m1 = 0.0f, m2 = 0.0f;
+    for (int64_t j = lane; j < cols; j += 64) {
+      const float xh = (xr[j] - mu) * rs;
+      const float gg = gr[j] * gamma[j];
+      m1 += gg;
+      m2 += gg * xh;
+      pg[j] += gr[j] * xh;
+      pb[j] += gr[j];
+    }
+    m1 = wave_sum(m1) * inv_n;
+    m2 = wave_sum(m2) * inv_n;
+    if (dx != nullptr) {
+      float *dr = dx + r * cols;
+      for (int64_t j = lane; j < cols; j += 64) {
+        const float xh = (xr[j] - mu) * rs;
+        const float gg = gr[j] * gamma[j];
+        const float v = rs * ((gg - m1) - xh * m2);
+        dr[j] = acc_dx ? dr[j] + v : v;
+      }
+    }
+  }
+  if (!want_params) return;
+  __syncthreads();
+  for (int64_t j = threadIdx.x; j < cols; j += kBlock) {
+    const float sg = ((lds[j] + lds[cols + j]) + lds[2 * cols + j]) + lds[3 * cols + j];
+    const float sb = ((lds[4 * cols + j] + lds[5 * cols + j]) + lds[6 * cols + j]) +
+                     lds[7 * cols + j];
+    part_g[(int64_t)blockIdx.x * cols + j] = sg;
+    part_b[(int64_t)blockIdx.x * cols + j] = sb;
+  }
+}
+
 int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, float *out,
               int64_t rows, int64_t cols, int mode, int acc_dx, int acc_out, int64_t out_n) {
   const int64_t strips = (cols + kColsPerBlock - 1) / kColsPerBlock;
@@ -314,6 +378,53 @@ int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float
     return numrs_hip::check_launch(ctx, "relu_mask_kernel");
   }
   return colreduce(ctx, g, z, dx, db, rows, cols, mode, accumulate, accumulate, cols);
+}
+
+int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float *x,
+                                 const float *gamma, const float *mean, const float *rstd,
+                                 float *dx, float *dgamma, float *dbeta, int64_t rows,
+                                 int64_t cols, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_layernorm_backward";
+  if (rows < 0 || cols <= 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: bad size", who);
+  if (cols > kLnMaxCols)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: rows longer than %d", who, kLnMaxCols);
+  if (rows == 0) {
+    if (accumulate) return NUMRS_HIP_OK;
+    int rc = dgamma ? numrs_hip_fill(ctx, dgamma, cols, 0.0f) : NUMRS_HIP_OK;
+    if (!rc && dbeta) rc = numrs_hip_fill(ctx, dbeta, cols, 0.0f);
+    return rc;
+  }
+  if (g == nullptr || x == nullptr || gamma == nullptr || mean == nullptr || rstd == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
+  const int want = dgamma != nullptr || dbeta != nullptr;
+  if (dx == nullptr && !want) return NUMRS_HIP_OK;
+  const int64_t chunks = (rows + kLnRows - 1) / kLnRows;
+  if (chunks > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too many rows", who);
+  float *part = nullptr;
+  if (want) {
+    void *ws = nullptr;
+    if (int rc = numrs_hip::workspace(ctx, (size_t)(2 * chunks * cols) * sizeof(float), &ws))
+      return rc;
+    part = static_cast<float *>(ws);
+  }
+  const size_t lds = (size_t)8 * cols * sizeof(float);
+  layernorm_bwd_pass1<<<(unsigned)chunks, kBlock, lds, ctx->stream>>>(
+      g, x, gamma, mean, rstd, dx, part, part ? part + chunks * cols : nullptr, rows, cols,
+      accumulate, want);
+  if (int rc = numrs_hip::check_launch(ctx, "layernorm_bwd_pass1")) return rc;
+  if (dgamma) {
+    colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(part, dgamma, chunks, cols,
+                                                                       accumulate);
+    if (int rc = numrs_hip::check_launch(ctx, "colreduce_finalize")) return rc;
+  }
+  if (dbeta) {
+    colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(part + chunks * cols, dbeta,
+                                                                       chunks, cols, accumulate);
+    if (int rc = numrs_hip::check_launch(ctx, "colreduce_finalize")) return rc;
+  }
+  return NUMRS_HIP_OK;
 }
 
 int numrs_hip_sum_to_shape(numrs_hip_ctx *ctx, const float *g, const int64_t *gshape, int gnd,

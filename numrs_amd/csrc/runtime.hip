@@ -36,6 +36,82 @@ int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out) {
   return NUMRS_HIP_OK;
 }
 
+int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out) {
+  if (bytes <= ctx->scratch_bytes && ctx->scratch != nullptr) {
+    *out = static_cast<float *>(ctx->scratch);
+    return NUMRS_HIP_OK;
+  }
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (ctx->scratch != nullptr) NRS_HIP(ctx, hipFree(ctx->scratch));
+  ctx->scratch = nullptr;
+  ctx->scratch_bytes = 0;
+  size_t want = bytes < (1u << 16) ? (1u << 16) : bytes;
+  if (hipMalloc(&ctx->scratch, want) != hipSuccess) {
+    ctx->scratch = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, NUMRS_HIP_E_NOMEM, "scratch allocation of %zu bytes failed", want);
+  }
+  ctx->scratch_bytes = want;
+  *out = static_cast<float *>(ctx->scratch);
+  return NUMRS_HIP_OK;
+}
+
+size_t block_round(size_t bytes) {
+  if (bytes <= 4096) return (bytes + 255) & ~size_t(255);
+  // Round up to 1/8 steps of the enclosing power of two.
+  size_t p = 1;
+  while (p < bytes) p <<= 1;
+  const size_t step = p / 8;
+  return (bytes + step - 1) / step * step;
+}
+
+int block_alloc(numrs_hip_ctx *ctx, size_t bytes, void **out) {
+  *out = nullptr;
+  if (bytes == 0) return NUMRS_HIP_OK;
+  if (ctx->destroyed) return fail(ctx, NUMRS_HIP_E_INVALID, "context already destroyed");
+  const size_t size = block_round(bytes);
+  auto it = ctx->free_blocks.find(size);
+  if (it != ctx->free_blocks.end() && !it->second.empty()) {
+    *out = it->second.back();
+    it->second.pop_back();
+    ctx->cached_bytes -= size;
+    ++ctx->live_blocks;
+    return NUMRS_HIP_OK;
+  }
+  if (hipMalloc(out, size) != hipSuccess) {
+    (void)hipGetLastError();
+    cache_release(ctx);
+    if (hipMalloc(out, size) != hipSuccess) {
+      *out = nullptr;
+      (void)hipGetLastError();
+      return fail(ctx, NUMRS_HIP_E_NOMEM, "device allocation of %zu bytes failed", size);
+    }
+  }
+  ++ctx->live_blocks;
+  return NUMRS_HIP_OK;
+}
+
+void block_free(numrs_hip_ctx *ctx, void *p, size_t bytes) {
+  if (p == nullptr) return;
+  --ctx->live_blocks;
+  if (ctx->destroyed) {
+    (void)hipFree(p);
+    if (ctx->live_blocks == 0) delete ctx;
+    return;
+  }
+  const size_t size = block_round(bytes);
+  ctx->free_blocks[size].push_back(p);
+  ctx->cached_bytes += size;
+}
+
+void cache_release(numrs_hip_ctx *ctx) {
+  (void)hipStreamSynchronize(ctx->stream);
+  for (auto &kv : ctx->free_blocks)
+    for (void *p : kv.second) (void)hipFree(p);
+  ctx->free_blocks.clear();
+  ctx->cached_bytes = 0;
+}
+
 int check_launch(numrs_hip_ctx *ctx, const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -111,9 +187,14 @@ int numrs_hip_destroy(numrs_hip_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   for (int i = 0; i < kMaxTimers; ++i) (void)hipEventDestroy(ctx->events[i]);
+  numrs_hip::cache_release(ctx);
   if (ctx->workspace != nullptr) (void)hipFree(ctx->workspace);
+  if (ctx->scratch != nullptr) (void)hipFree(ctx->scratch);
+  ctx->workspace = ctx->scratch = nullptr;
   (void)hipStreamDestroy(ctx->stream);
-  delete ctx;
+  ctx->stream = nullptr;
+  ctx->destroyed = true;
+  if (ctx->live_blocks == 0) delete ctx;  // else the last engine block frees it
   return NUMRS_HIP_OK;
 }
 

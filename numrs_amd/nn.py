@@ -1,0 +1,131 @@
+"""NN modules over the device Tensor (mirrors numrs-core/src/autograd/nn.rs).
+
+`Linear.forward` records the reference's node sequence exactly --
+Transpose(W), MatMul(x, W^T), Add(., b) (nn.rs:217-235) -- so its backward
+runs transpose_backward, matmul_backward and add_backward/unbroadcast.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .autograd import Tensor, default_context
+
+
+class Module:
+    """trait Module (nn.rs:23-42)."""
+
+    training = True
+
+    def forward(self, x: Tensor) -> Tensor:
+        raise NotImplementedError
+
+    def __call__(self, x: Tensor) -> Tensor:
+        return self.forward(x)
+
+    def parameters(self) -> list[Tensor]:
+        return []
+
+    def train(self) -> None:
+        self.training = True
+
+    def eval(self) -> None:
+        self.training = False
+
+
+class Linear(Module):
+    """y = x @ W^T + b with W [out, in], b [out] (nn.rs:57-235)."""
+
+    def __init__(self, in_features: int, out_features: int, ctx=None):
+        # Linear::new's deterministic fill: sin(0.123 i) * sqrt(1/in) (nn.rs:67-96).
+        k = np.float32(np.sqrt(np.float32(1.0) / np.float32(in_features)))
+        i = np.arange(in_features * out_features, dtype=np.float32)
+        w = (np.sin(i * np.float32(0.123)) * k).astype(np.float32)
+        self._init(in_features, out_features, w, np.zeros(out_features, np.float32), ctx)
+
+    @classmethod
+    def with_weights(cls, in_features: int, out_features: int, weight, bias, ctx=None) -> "Linear":
+        """Linear::with_weights (nn.rs:107-129)."""
+        obj = cls.__new__(cls)
+        obj._init(in_features, out_features, weight, bias, ctx)
+        return obj
+
+    def _init(self, fin, fout, w, b, ctx):
+        ctx = ctx or default_context()
+        self.in_features, self.out_features = fin, fout
+        self.weight = Tensor.new(np.asarray(w, np.float32).reshape(fout, fin), True, ctx=ctx)
+        self.bias = Tensor.new(np.asarray(b, np.float32).reshape(fout), True, ctx=ctx)
+
+    def forward(self, x: Tensor) -> Tensor:
+        w_t = self.weight.transpose()
+        return x.matmul(w_t).add(self.bias)
+
+    def parameters(self) -> list[Tensor]:
+        return [self.weight, self.bias]
+
+
+class ReLU(Module):
+    def forward(self, x: Tensor) -> Tensor:  # nn.rs:306-320
+        return x.relu()
+
+
+class Sigmoid(Module):
+    def forward(self, x: Tensor) -> Tensor:  # nn.rs:324-338
+        return x.sigmoid()
+
+
+class Tanh(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return x.tanh()
+
+
+class GELU(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return x.gelu()
+
+
+class Softmax(Module):
+    """Row softmax over the last axis (nn.rs:345-375 asks for it; the
+    reference's ops::softmax cannot take an axis)."""
+
+    def forward(self, x: Tensor) -> Tensor:
+        return x.softmax()
+
+
+class LayerNorm(Module):
+    def __init__(self, features: int, eps: float = 1e-5, ctx=None):
+        ctx = ctx or default_context()
+        self.eps = eps
+        self.gamma = Tensor.new(np.ones(features, np.float32), True, ctx=ctx)
+        self.beta = Tensor.new(np.zeros(features, np.float32), True, ctx=ctx)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return x.layer_norm(self.gamma, self.beta, self.eps)
+
+    def parameters(self) -> list[Tensor]:
+        return [self.gamma, self.beta]
+
+
+class Sequential(Module):
+    """nn.rs:257-302."""
+
+    def __init__(self, layers):
+        self.layers = list(layers)
+
+    def add(self, layer: Module) -> None:
+        self.layers.append(layer)
+
+    def forward(self, x: Tensor) -> Tensor:
+        for layer in self.layers:
+            x = layer.forward(x)
+        return x
+
+    def parameters(self) -> list[Tensor]:
+        return [p for layer in self.layers for p in layer.parameters()]
+
+    def train(self) -> None:
+        for layer in self.layers:
+            layer.train()
+
+    def eval(self) -> None:
+        for layer in self.layers:
+            layer.eval()

@@ -57,3 +57,23 @@ def test_header_enums_match_bindings():
                                                  L.UNBROADCAST_REFERENCE),
                       ("NUMRS_HIP_E_NODEV", L.E_NODEV)]:
         assert f"{name} = {val}" in text, name
+
+
+def test_grad_mode_is_thread_local_host_state():
+    # autograd/mod.rs:194-206: is_grad_enabled / set_grad_enabled, no GPU involved
+    import threading
+
+    from numrs_amd import is_grad_enabled, no_grad, set_grad_enabled
+
+    assert is_grad_enabled()
+    with no_grad():
+        assert not is_grad_enabled()
+        seen = []
+        t = threading.Thread(target=lambda: seen.append(is_grad_enabled()))
+        t.start()
+        t.join()
+        assert seen == [True]
+    assert is_grad_enabled()
+    set_grad_enabled(False)
+    set_grad_enabled(True)
+    assert is_grad_enabled()
