@@ -154,6 +154,47 @@ def bench_c1(ctx, steps, warmup):
     return {"us_per_step": per * 1e6, "loss": loss.item()}
 
 
+def c4_flops(B=16, S=256, D=512, H=8, F=2048):
+    """Forward GEMM flops of the pre-LN block (QKV/O projections, FFN,
+    QK^T and PV); backward is twice that (dX and dW per product)."""
+    T = B * S
+    fwd = 2 * T * D * D * 4 + 2 * T * D * F * 2 + 2 * 2 * B * H * S * S * (D // H)
+    return fwd, 2 * fwd
+
+
+def bench_c4(ctx, steps, warmup):
+    """pre-LN transformer encoder block train step
+    (B 16, S 256, d 512, 8 heads, FFN 2048 GELU, MSE): forward + backward +
+    SGD step through the device autograd engine."""
+    import numrs_amd as nr
+    from numrs_amd import Tensor, nn, optim
+    from tests.transformer_oracle import make_c4
+
+    nr.set_default_context(ctx)
+    w, x, t, (B, S, H) = make_c4(seed=4)
+    blk = nn.TransformerEncoderBlock(w, H)
+    opt = optim.SGD.simple(blk.parameters(), 1e-3)
+    xt, tt = Tensor.new(x, False), Tensor.new(t, False)
+
+    def step():
+        loss = blk.forward_seq(xt, B, S).mse_loss(tt)
+        loss.backward()
+        opt.step()
+        opt.zero_grad()
+        return loss
+
+    for _ in range(warmup):
+        step().item()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    loss.item()
+    per = (time.perf_counter() - t0) / steps
+    fwd, bwd = c4_flops()
+    return {"ms_per_step": per * 1e3, "tflops": (fwd + bwd) / per / 1e12, "loss": loss.item()}
+
+
 def cpu_baseline(A, B, dC, rows_a: int, rows_b: int):
     """numrs's matmul_backward restated in C (single thread, fp32 triple
     loops of backward.rs:123-146), timed on this host over a bounded sample
@@ -248,6 +289,15 @@ def main() -> int:
                           "value": round(c1["us_per_step"], 1), "unit": "us/step",
                           "bound": "latency", "final_loss": round(c1["loss"], 6)})
         log(f"  C1 MLP step {c1['us_per_step']:.1f} us")
+        c4 = bench_c4(ctx, max(3, args.steps // 5), 2)
+        secondary.append({"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
+                                      "heads, FFN 2048 GELU, MSE, SGD) via the device engine",
+                          "value": round(c4["ms_per_step"], 3), "unit": "ms/step",
+                          "tflops_over_step": round(c4["tflops"], 2),
+                          "frac_of_fp32_mfma": round(c4["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4),
+                          "bound": "mfma (GEMMs) + hbm (LN/GELU/softmax)",
+                          "final_loss": round(c4["loss"], 6)})
+        log(f"  C4 block step {c4['ms_per_step']:.3f} ms {c4['tflops']:.1f} TFLOP/s")
 
     cpu = None
     if not args.no_cpu_baseline:

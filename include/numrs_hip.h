@@ -156,6 +156,33 @@ int numrs_hip_matmul_batched(numrs_hip_ctx *ctx, const float *A, const float *B,
                              int64_t stride_b, int64_t stride_c, int trans_a, int trans_b,
                              int accumulate);
 
+/* General strided product, the building block of attention's batched
+ * gradients: for z in [0, batch), with zo = z / batch_inner and
+ * zi = z % batch_inner, operand A_z starts at A + zo*sa_outer + zi*sa_inner
+ * with leading dimension lda (likewise B_z, C_z), and
+ *   C_z[M,N] (+)= alpha * op(A_z) @ op(B_z),  op = transpose when trans_* = 1.
+ * Two batch levels address head-interleaved layouts ([batch, seq, heads,
+ * dim]) in place.  No reference counterpart (its matmul is 2-D only,
+ * backward.rs:118-120). */
+int numrs_hip_gemm(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B, int64_t ldb,
+                   float *C, int64_t ldc, int64_t M, int64_t K, int64_t N, int trans_a,
+                   int trans_b, float alpha, int accumulate, int64_t batch, int64_t batch_inner,
+                   int64_t sa_outer, int64_t sa_inner, int64_t sb_outer, int64_t sb_inner,
+                   int64_t sc_outer, int64_t sc_inner);
+
+/* Multi-head attention (no reference op).  q, k, v, out are
+ * [B*S, D] row-major with head h of token (b, s) in columns [h*D/H, (h+1)*D/H).
+ * Forward: P = softmax(Q K^T / sqrt(D/H)) per (b, h) into P [B*H, S, S],
+ * out = P V.  Backward from the saved P: dV = P^T dO, dS = softmax_backward(P,
+ * dO V^T), dQ = dS K / sqrt(dh), dK = dS^T Q / sqrt(dh); dq/dk/dv may be NULL;
+ * uses B*H*S*S floats of workspace. */
+int numrs_hip_attention_forward(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,
+                                float *P, float *out, int64_t B, int64_t S, int64_t H, int64_t D);
+int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                 const float *v, const float *P, const float *dout, float *dq,
+                                 float *dk, float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
+                                 int accumulate);
+
 /* ---------------------------------------------------------------------- */
 /* Broadcast-reduce gradients                                              */
 /* ---------------------------------------------------------------------- */
@@ -348,6 +375,10 @@ int numrs_hip_tensor_softmax(numrs_hip_tensor *a, numrs_hip_tensor **out);
 /* LayerNorm over the last axis (no reference op). */
 int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
                                 numrs_hip_tensor *beta, float eps, numrs_hip_tensor **out);
+
+/* Multi-head attention node over q, k, v [B*S, D] (numrs_hip_attention_forward). */
+int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
+                               int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out);
 
 /* SGD::new (optim/sgd.rs:90-112) / Adam::new (optim/adam.rs:250-285) over
  * parameter tensors; step / zero_grad / learning_rate / set_learning_rate

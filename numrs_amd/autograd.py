@@ -272,6 +272,12 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_layer_norm(self._h, gamma._h, beta._h, eps,
                                                               ctypes.byref(h)), h)
 
+    def attention(self, k: "Tensor", v: "Tensor", batch: int, seq: int, heads: int) -> "Tensor":
+        """Multi-head attention with self as q; q, k, v are [batch*seq, dim]."""
+        h = ctypes.c_void_p()
+        return self._out(L.load().numrs_hip_tensor_attention(self._h, k._h, v._h, batch, seq, heads,
+                                                             ctypes.byref(h)), h)
+
     def __repr__(self) -> str:
         return f"Tensor(shape={list(self.shape())}, requires_grad={self.requires_grad})"
 

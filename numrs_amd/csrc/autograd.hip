@@ -38,7 +38,7 @@ thread_local bool g_grad_enabled = true;  // mod.rs:194-206
 
 enum class Op {
   Leaf, Add, Sub, Mul, Div, MatMul, Transpose, Unary, Sum, Mean, MSE, CrossEntropy,
-  CrossEntropyLabels, Reshape, Softmax, LayerNorm
+  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention
 };
 
 struct Storage {
@@ -76,6 +76,7 @@ struct Node {
   Op op;
   int kind = 0;       // unary kind / mean flag
   float param = 0.f;  // pow exponent, LayerNorm eps
+  int64_t dims[3] = {0, 0, 0};  // attention batch, seq, heads
   std::vector<T> inputs;
   std::vector<Buf> saved;  // LayerNorm mean/rstd, int32 labels
 };
@@ -426,6 +427,50 @@ int bw_layernorm(const T &out, const float *g, Node &n) {
                                       rows, cols, dx ? ax : (dg ? ag : ab));
 }
 
+int bw_attention(const T &out, const float *g, Node &n) {
+  const T &q = n.inputs[0], &k = n.inputs[1], &v = n.inputs[2];
+  float *dq = nullptr, *dk = nullptr, *dv = nullptr;
+  int aq = 1, ak = 1, av = 1;
+  if (q->requires_grad)
+    if (int rc = grad_target(q, &dq, &aq)) return rc;
+  if (k->requires_grad && k->grad != q->grad)
+    if (int rc = grad_target(k, &dk, &ak)) return rc;
+  if (v->requires_grad && v->grad != q->grad && v->grad != k->grad)
+    if (int rc = grad_target(v, &dv, &av)) return rc;
+  // One accumulate flag for the three grads: zero-fill any first-written one.
+  const int acc = (dq && aq) || (dk && ak) || (dv && av);
+  numrs_hip_ctx *ctx = out->ctx;
+  if (acc) {
+    if (dq && !aq) if (int rc = numrs_hip_fill(ctx, dq, q->numel(), 0.0f)) return rc;
+    if (dk && !ak) if (int rc = numrs_hip_fill(ctx, dk, k->numel(), 0.0f)) return rc;
+    if (dv && !av) if (int rc = numrs_hip_fill(ctx, dv, v->numel(), 0.0f)) return rc;
+  }
+  const int64_t D = q->shape[1];
+  if (int rc = numrs_hip_attention_backward(ctx, q->data->ptr, k->data->ptr, v->data->ptr,
+                                            n.saved[0]->ptr, g, dq, dk, dv, n.dims[0], n.dims[1],
+                                            n.dims[2], D, acc))
+    return rc;
+  // Shared grad cells (self-attention on one tensor): the remaining grads add.
+  if (k->requires_grad && !dk) {
+    float *t;
+    int a;
+    if (int rc = grad_target(k, &t, &a)) return rc;
+    if (int rc = numrs_hip_attention_backward(ctx, q->data->ptr, k->data->ptr, v->data->ptr,
+                                              n.saved[0]->ptr, g, nullptr, t, nullptr, n.dims[0],
+                                              n.dims[1], n.dims[2], D, 1))
+      return rc;
+  }
+  if (v->requires_grad && !dv) {
+    float *t;
+    int a;
+    if (int rc = grad_target(v, &t, &a)) return rc;
+    return numrs_hip_attention_backward(ctx, q->data->ptr, k->data->ptr, v->data->ptr,
+                                        n.saved[0]->ptr, g, nullptr, nullptr, t, n.dims[0],
+                                        n.dims[1], n.dims[2], D, 1);
+  }
+  return NUMRS_HIP_OK;
+}
+
 int run_backward_fn(const T &out) {
   Node &n = *out->node;
   const float *g = out->grad->buf->ptr;
@@ -445,6 +490,7 @@ int run_backward_fn(const T &out) {
     case Op::Reshape: return bw_reshape(out, g, n);
     case Op::Softmax: return bw_softmax(out, g, n);
     case Op::LayerNorm: return bw_layernorm(out, g, n);
+    case Op::Attention: return bw_attention(out, g, n);
     case Op::Leaf: return NUMRS_HIP_OK;
   }
   return NUMRS_HIP_OK;
@@ -679,6 +725,30 @@ int op_layernorm(const T &x, const T &gamma, const T &beta, float eps, T *out) {
                                            r->data->ptr, mean->ptr, rstd->ptr, rows, cols, eps))
     return rc;
   if (rec) attach(r, Op::LayerNorm, {x, gamma, beta}, 0, eps, {mean, rstd});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_attention(const T &q, const T &k, const T &v, int64_t B, int64_t S, int64_t H, T *out) {
+  numrs_hip_ctx *ctx = q->ctx;
+  if (q->shape.size() != 2 || q->shape != k->shape || q->shape != v->shape)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "attention: q, k, v must be equal [batch*seq, dim]");
+  if (B <= 0 || S <= 0 || H <= 0 || q->shape[0] != B * S || q->shape[1] % H != 0)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "attention: rows != batch*seq or dim %% heads != 0");
+  const bool rec = recording({&q, &k, &v});
+  T r;
+  if (int rc = make_tensor(ctx, q->shape, rec, &r)) return rc;
+  Buf P;
+  if (int rc = alloc_buf(ctx, B * H * S * S, sizeof(float), &P)) return rc;
+  if (int rc = numrs_hip_attention_forward(ctx, q->data->ptr, k->data->ptr, v->data->ptr, P->ptr,
+                                           r->data->ptr, B, S, H, q->shape[1]))
+    return rc;
+  if (rec) {
+    attach(r, Op::Attention, {q, k, v}, 0, 0.f, {P});
+    r->node->dims[0] = B;
+    r->node->dims[1] = S;
+    r->node->dims[2] = H;
+  }
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -946,6 +1016,14 @@ int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
     return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_layernorm(x->t, gamma->t, beta->t, eps, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
+                               int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out) {
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_attention(q->t, k->t, v->t, batch, seq, heads, &r)) return rc;
   return wrap(std::move(r), out);
 }
 

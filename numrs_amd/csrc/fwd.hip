@@ -182,9 +182,10 @@ __global__ void __launch_bounds__(kBlock)
 // Row softmax and LayerNorm forward (new ops for the transformer config)
 // ---------------------------------------------------------------------------
 
+// x and y may alias (in-place use by attention): a row is read completely
+// (max, sum) before it is written, and each lane reads x[j] before y[j].
 __global__ void __launch_bounds__(kBlock)
-    softmax_rows_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
-                        int64_t cols, float scale) {
+    softmax_rows_kernel(const float *x, float *y, int64_t rows, int64_t cols, float scale) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;

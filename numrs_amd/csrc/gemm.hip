@@ -52,10 +52,16 @@ struct Gemm {
   const float *Y;
   float *C;
   int64_t ldx, ldy, ldc;
-  int64_t bsx, bsy, bsc;  // batch strides (elements)
+  // Batch z = zo * binner + zi addresses X + zo*bsx + zi*bsx2 (same for Y, C):
+  // one level covers plain batches, two levels cover head-interleaved
+  // layouts such as [batch, seq, heads, dim].
+  int64_t bsx, bsy, bsc;
+  int64_t bsx2, bsy2, bsc2;
+  int binner;
   int P, Q, R;
   int tiles_p, tiles_q;
   int accumulate;
+  float alpha;  // C = alpha * X@Y (+ C)
 };
 
 // Loads one 128 x 32 operand tile from global memory into registers
@@ -138,9 +144,10 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
   const int c = lane & 31, h = lane >> 5;
   const int p0 = tp * kBP, q0 = tq * kBP;
 
-  const float *__restrict__ X = d.X + (int64_t)batch * d.bsx;
-  const float *__restrict__ Y = d.Y + (int64_t)batch * d.bsy;
-  float *__restrict__ C = d.C + (int64_t)batch * d.bsc;
+  const int64_t zo = batch / d.binner, zi = batch - zo * d.binner;
+  const float *__restrict__ X = d.X + zo * d.bsx + zi * d.bsx2;
+  const float *__restrict__ Y = d.Y + zo * d.bsy + zi * d.bsy2;
+  float *__restrict__ C = d.C + zo * d.bsc + zi * d.bsc2;
 
   float *xs0 = smem, *xs1 = smem + kTileFloats;
   float *ys0 = smem + 2 * kTileFloats, *ys1 = smem + 3 * kTileFloats;
@@ -218,7 +225,8 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
       const int p = p0 + wp * 64 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (p < d.P && q < d.Q) {
         float *dst = C + (int64_t)p * d.ldc + q;
-        *dst = d.accumulate ? *dst + a[i] : a[i];
+        const float v = d.alpha * a[i];
+        *dst = d.accumulate ? *dst + v : v;
       }
     }
   }
@@ -255,10 +263,12 @@ int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
 // Vector (float4) loads need 16-byte aligned bases, leading dimensions and
 // contiguous extents that are multiples of 4.
 bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
-  auto ok = [](const void *p, int64_t ld, int64_t bs, int64_t contig) {
-    return numrs_hip::aligned16(p) && (ld & 3) == 0 && (bs & 3) == 0 && (contig & 3) == 0;
+  auto ok = [](const void *p, int64_t ld, int64_t bs, int64_t bs2, int64_t contig) {
+    return numrs_hip::aligned16(p) && (ld & 3) == 0 && (bs & 3) == 0 && (bs2 & 3) == 0 &&
+           (contig & 3) == 0;
   };
-  return ok(d.X, d.ldx, d.bsx, xrc ? d.R : d.P) && ok(d.Y, d.ldy, d.bsy, yrc ? d.R : d.Q);
+  return ok(d.X, d.ldx, d.bsx, d.bsx2, xrc ? d.R : d.P) &&
+         ok(d.Y, d.ldy, d.bsy, d.bsy2, yrc ? d.R : d.Q);
 }
 
 int check_dims(numrs_hip_ctx *ctx, const char *who, int64_t batch, int64_t M, int64_t K,
@@ -283,6 +293,9 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.bsx = bsx;
   g.bsy = bsy;
   g.bsc = bsc;
+  g.bsx2 = g.bsy2 = g.bsc2 = 0;
+  g.binner = 1;
+  g.alpha = 1.0f;
   g.P = (int)P;
   g.Q = (int)Q;
   g.R = (int)R;
@@ -379,9 +392,52 @@ int matmul_impl(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, in
   return gemm_dispatch(ctx, g, batch, xrc, yrc);
 }
 
+int gemm_general(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B, int64_t ldb,
+                 float *C, int64_t ldc, int64_t M, int64_t K, int64_t N, int ta, int tb,
+                 float alpha, int acc, int64_t batch, int64_t binner, int64_t sao, int64_t sai,
+                 int64_t sbo, int64_t sbi, int64_t sco, int64_t sci) {
+  const char *who = "numrs_hip_gemm";
+  int rc = check_dims(ctx, who, batch, M, K, N);
+  if (rc) return rc;
+  if (binner < 1 || binner > batch + (batch == 0))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: batch_inner %lld", who, (long long)binner);
+  if (lda < 0 || ldb < 0 || ldc < N || sao < 0 || sai < 0 || sbo < 0 || sbi < 0 || sco < 0 ||
+      sci < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: bad leading dimension or stride", who);
+  if (lda < (ta ? M : K) || ldb < (tb ? K : N))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: leading dimension too small", who);
+  if (batch == 0 || M == 0 || N == 0) return NUMRS_HIP_OK;
+  if (C == nullptr || ((A == nullptr || B == nullptr) && K > 0))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  Gemm g = make(A, B, C, lda, ldb, ldc, sao, sbo, sco, M, N, K, acc);
+  g.bsx2 = sai;
+  g.bsy2 = sbi;
+  g.bsc2 = sci;
+  g.binner = (int)binner;
+  g.alpha = alpha;
+  if (K == 0) {
+    if (acc) return NUMRS_HIP_OK;
+    if (ldc != N || binner != 1 || sco != M * N)
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: empty reduction into a strided C", who);
+    return numrs_hip_fill(ctx, C, batch * M * N, 0.0f);
+  }
+  return gemm_dispatch(ctx, g, batch, !ta, tb != 0);
+}
+
 }  // namespace
 
 extern "C" {
+
+int numrs_hip_gemm(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B, int64_t ldb,
+                   float *C, int64_t ldc, int64_t M, int64_t K, int64_t N, int trans_a,
+                   int trans_b, float alpha, int accumulate, int64_t batch, int64_t batch_inner,
+                   int64_t sa_outer, int64_t sa_inner, int64_t sb_outer, int64_t sb_inner,
+                   int64_t sc_outer, int64_t sc_inner) {
+  NRS_CHECK_CTX(ctx);
+  return gemm_general(ctx, A, lda, B, ldb, C, ldc, M, K, N, trans_a, trans_b, alpha, accumulate,
+                      batch, batch_inner, sa_outer, sa_inner, sb_outer, sb_inner, sc_outer,
+                      sc_inner);
+}
 
 int numrs_hip_matmul_backward(numrs_hip_ctx *ctx, const float *dC, const float *A,
                               const float *B, float *dA, float *dB, int64_t M, int64_t K,

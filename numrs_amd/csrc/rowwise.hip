@@ -41,9 +41,11 @@ __global__ void __launch_bounds__(kBlock)
 }
 
 // softmax_backward, backward.rs:521-541: dx = y * (g - sum_row(g * y)).
+// g and dx may alias (in-place use by attention): each lane reads g[j] before
+// it writes dx[j], and the row dot product is complete before any write.
 __global__ void __launch_bounds__(kBlock)
-    softmax_bwd_kernel(const float *__restrict__ y, const float *__restrict__ g,
-                       float *__restrict__ dx, int64_t rows, int64_t cols, int acc) {
+    softmax_bwd_kernel(const float *__restrict__ y, const float *g, float *dx, int64_t rows,
+                       int64_t cols, int acc) {
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;

@@ -129,3 +129,46 @@ class Sequential(Module):
     def eval(self) -> None:
         for layer in self.layers:
             layer.eval()
+
+
+class MultiHeadAttention(Module):
+    """Self-attention projections + fused attention node (no reference op)."""
+
+    def __init__(self, wq, wk, wv, wo, heads: int, ctx=None):
+        d = np.asarray(wq).shape[0]
+        z = np.zeros(d, np.float32)
+        self.heads = heads
+        self.q = Linear.with_weights(d, d, wq, z, ctx)
+        self.k = Linear.with_weights(d, d, wk, z, ctx)
+        self.v = Linear.with_weights(d, d, wv, z, ctx)
+        self.o = Linear.with_weights(d, d, wo, z, ctx)
+
+    def forward_seq(self, x: Tensor, batch: int, seq: int) -> Tensor:
+        a = self.q(x).attention(self.k(x), self.v(x), batch, seq, self.heads)
+        return self.o(a)
+
+    def parameters(self) -> list[Tensor]:
+        return [p for m in (self.q, self.k, self.v, self.o) for p in m.parameters()]
+
+
+class TransformerEncoderBlock(Module):
+    """Pre-LN encoder block on x [batch*seq, d_model]:
+    r = x + Attn(LN1(x));  y = r + W2 GELU(W1 LN2(r))."""
+
+    def __init__(self, weights: dict, heads: int, ctx=None):
+        d = np.asarray(weights["wq"]).shape[0]
+        f = np.asarray(weights["w1"]).shape[0]
+        self.ln1 = LayerNorm(d, ctx=ctx)
+        self.ln2 = LayerNorm(d, ctx=ctx)
+        self.attn = MultiHeadAttention(weights["wq"], weights["wk"], weights["wv"], weights["wo"],
+                                       heads, ctx)
+        self.ff1 = Linear.with_weights(d, f, weights["w1"], np.zeros(f, np.float32), ctx)
+        self.ff2 = Linear.with_weights(f, d, weights["w2"], np.zeros(d, np.float32), ctx)
+
+    def forward_seq(self, x: Tensor, batch: int, seq: int) -> Tensor:
+        r = x.add(self.attn.forward_seq(self.ln1(x), batch, seq))
+        return r.add(self.ff2(self.ff1(self.ln2(r)).gelu()))
+
+    def parameters(self) -> list[Tensor]:
+        return (self.ln1.parameters() + self.attn.parameters() + self.ln2.parameters() +
+                self.ff1.parameters() + self.ff2.parameters())

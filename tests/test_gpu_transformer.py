@@ -1,0 +1,117 @@
+"""Attention (N3) kernels and the C4 transformer block on the GPU against the
+float64 oracle (tests/transformer_oracle.py, pinned to torch autograd)."""
+import math
+
+import numpy as np
+import pytest
+
+import numrs_amd as nr
+from numrs_amd import Tensor, nn
+from tests import transformer_oracle as TO
+from tests.conftest import assert_contraction, rand
+
+pytestmark = pytest.mark.gpu
+
+
+def _mha_ref(q, k, v, B, S, H):
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    dh = q.shape[1] // H
+    Q, K, V = (TO._heads(a, B, S, H) for a in (q, k, v))
+    s = Q @ K.transpose(0, 1, 3, 2) / math.sqrt(dh)
+    P = np.exp(s - s.max(-1, keepdims=True))
+    P /= P.sum(-1, keepdims=True)
+    return P, Q, K, V
+
+
+@pytest.mark.parametrize("B,S,H,D", [(2, 40, 4, 64), (1, 7, 1, 5), (3, 256, 8, 512)])
+def test_attention_forward_backward(hip_ctx, B, S, H, D):
+    print(f"[gpu] attention B={B} S={S} H={H} D={D}", flush=True)
+    rng = np.random.default_rng(B * 1000 + S)
+    q, k, v, dO = (rand(rng, (B * S, D)) for _ in range(4))
+    c = hip_ctx
+    qd, kd, vd, gd = (c.to_device(a) for a in (q, k, v, dO))
+    P, out = c.empty((B * H, S, S)), c.empty((B * S, D))
+    assert L_attention_fwd(c, qd, kd, vd, P, out, B, S, H, D) == 0
+    Pr, Q, K, V = _mha_ref(q, k, v, B, S, H)
+    dh = D // H
+    assert_contraction(P.numpy().reshape(B, H, S, S), Pr, dh, what="P")
+    assert_contraction(out.numpy(), TO._merge(Pr @ V, B, S), S, what="out")
+    dq, dk, dv = (c.empty((B * S, D)) for _ in range(3))
+    assert L_attention_bwd(c, qd, kd, vd, P, gd, dq, dk, dv, B, S, H, D) == 0
+    dA = TO._heads(dO.astype(np.float64), B, S, H)
+    dV = Pr.transpose(0, 1, 3, 2) @ dA
+    dP = dA @ V.transpose(0, 1, 3, 2)
+    dS = Pr * (dP - (dP * Pr).sum(-1, keepdims=True)) / math.sqrt(dh)
+    assert_contraction(dv.numpy(), TO._merge(dV, B, S), S, what="dv")
+    assert_contraction(dq.numpy(), TO._merge(dS @ K, B, S), S + dh, what="dq")
+    assert_contraction(dk.numpy(), TO._merge(dS.transpose(0, 1, 3, 2) @ Q, B, S), S + dh,
+                       what="dk")
+
+
+def L_attention_fwd(c, q, k, v, P, out, B, S, H, D):
+    from numrs_amd import _lib as L
+    return L.load().numrs_hip_attention_forward(c.handle, q.ptr, k.ptr, v.ptr, P.ptr, out.ptr,
+                                                B, S, H, D)
+
+
+def L_attention_bwd(c, q, k, v, P, g, dq, dk, dv, B, S, H, D):
+    from numrs_amd import _lib as L
+    return L.load().numrs_hip_attention_backward(c.handle, q.ptr, k.ptr, v.ptr, P.ptr, g.ptr,
+                                                 dq.ptr, dk.ptr, dv.ptr, B, S, H, D, 0)
+
+
+def test_gemm_two_level_batch(hip_ctx):
+    # C_z = alpha * A_z @ B_z^T over head slices of [B*S, H*dh] (the QK^T product)
+    from numrs_amd import _lib as L
+    B, S, H, dh = 2, 33, 3, 20
+    D = H * dh
+    rng = np.random.default_rng(2)
+    q, k = rand(rng, (B * S, D)), rand(rng, (B * S, D))
+    c = hip_ctx
+    out = c.empty((B * H, S, S))
+    qd, kd = c.to_device(q), c.to_device(k)
+    rc = L.load().numrs_hip_gemm(c.handle, qd.ptr, D, kd.ptr, D, out.ptr, S, S, dh, S, 0, 1, 0.5, 0,
+                                 B * H, H, S * D, dh, S * D, dh, H * S * S, S * S)
+    assert rc == 0
+    Q, K = TO._heads(q.astype(np.float64), B, S, H), TO._heads(k.astype(np.float64), B, S, H)
+    ref = 0.5 * (Q @ K.transpose(0, 1, 3, 2))
+    assert_contraction(out.numpy().reshape(B, H, S, S), ref, dh)
+
+
+def _norm_rel(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+
+
+def _run_block(dims_full, seed):
+    w, x, t, dims = TO.make_c4(seed=seed, **dims_full)
+    B, S, H = dims
+    blk = nn.TransformerEncoderBlock(w, H)
+    xt = Tensor.new(x, True)
+    y = blk.forward_seq(xt, B, S)
+    loss = y.mse_loss(Tensor.new(t, False))
+    loss.backward()
+    return w, x, t, dims, blk, xt, loss, y
+
+
+@pytest.mark.parametrize("dims_full", [dict(B=2, S=64, D=128, H=4, F=256),
+                                       dict(B=16, S=256, D=512, H=8, F=2048)],
+                         ids=["small", "baseline"])
+def test_c4_block_matches_oracle(hip_ctx, dims_full):
+    print(f"[gpu] C4 block {dims_full}", flush=True)
+    nr.set_default_context(hip_ctx)
+    w, x, t, dims, blk, xt, loss, y = _run_block(dims_full, seed=4)
+    ref_loss, g, ref_y = TO.block(w, x, t, dims)
+    assert abs(loss.item() - ref_loss) <= 1e-5 * abs(ref_loss)
+    assert _norm_rel(y.values(), ref_y) < 1e-5
+    got = {"wq": blk.attn.q.weight, "wk": blk.attn.k.weight, "wv": blk.attn.v.weight,
+           "wo": blk.attn.o.weight, "w1": blk.ff1.weight, "w2": blk.ff2.weight,
+           "ln1_gamma": blk.ln1.gamma, "ln1_beta": blk.ln1.beta, "ln2_gamma": blk.ln2.gamma,
+           "ln2_beta": blk.ln2.beta, "bq": blk.attn.q.bias, "bo": blk.attn.o.bias,
+           "c1": blk.ff1.bias, "c2": blk.ff2.bias, "x": xt}
+    for name, tensor in got.items():
+        gg, rr = tensor.gradient(), g[name]
+        # fp32 through ~10 dependent contractions (K up to 2048) against float64:
+        # norm-wise relative error, and every element within 1e-3 of the max.
+        assert _norm_rel(gg, rr) < 2e-4, (name, _norm_rel(gg, rr))
+        assert np.abs(gg - rr).max() <= 1e-3 * np.abs(rr).max(), name

@@ -1,0 +1,115 @@
+"""C4 (pre-LN transformer encoder block) forward and backward in float64
+numpy -- test infrastructure.  The block has no numrs counterpart (no
+attention, LayerNorm or GELU in the reference), so this is the mathematics:
+closed-form backward of every node, pinned against torch float64 autograd in
+tests/test_oracle_new_ops.py.  LayerNorm / GELU / softmax backward reuse the
+C oracle's float64 routines where they exist.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def make_c4(seed=4, B=16, S=256, D=512, H=8, F=2048):
+    """BASELINE config 4 inputs: x, target ~ N(0,1), Xavier-uniform weights,
+    LN gamma = 1, beta = 0, zero biases."""
+    rng = np.random.default_rng(seed)
+
+    def xav(o, i):
+        a = math.sqrt(6.0 / (i + o))
+        return rng.uniform(-a, a, (o, i)).astype(np.float32)
+
+    w = {"wq": xav(D, D), "wk": xav(D, D), "wv": xav(D, D), "wo": xav(D, D),
+         "w1": xav(F, D), "w2": xav(D, F)}
+    x = rng.standard_normal((B * S, D), dtype=np.float32)
+    t = rng.standard_normal((B * S, D), dtype=np.float32)
+    return w, x, t, (B, S, H)
+
+
+def _ln(x, eps=1e-5):
+    mu = x.mean(1, keepdims=True)
+    var = ((x - mu) ** 2).mean(1, keepdims=True)
+    rs = 1.0 / np.sqrt(var + eps)
+    return (x - mu) * rs, rs
+
+
+def _ln_bwd(g, xh, rs, gamma):
+    gg = g * gamma
+    return rs * (gg - gg.mean(1, keepdims=True) - xh * (gg * xh).mean(1, keepdims=True))
+
+
+try:
+    from scipy.special import erf as _erf
+except ImportError:  # pragma: no cover
+    _erf = np.vectorize(math.erf)
+
+
+def _gelu(x):
+    return x * 0.5 * (1.0 + _erf(x / math.sqrt(2.0)))
+
+
+def _gelu_grad(x):
+    return 0.5 * (1.0 + _erf(x / math.sqrt(2.0))) + x * np.exp(-0.5 * x * x) / math.sqrt(2 * math.pi)
+
+
+def _heads(a, B, S, H):
+    return a.reshape(B, S, H, -1).transpose(0, 2, 1, 3)  # [B, H, S, dh]
+
+
+def _merge(a, B, S):
+    return a.transpose(0, 2, 1, 3).reshape(B * S, -1)
+
+
+def block(w, x, t, dims):
+    """Returns (loss, grads dict, output y) in float64."""
+    B, S, H = dims
+    f = {k: v.astype(np.float64) for k, v in w.items()}
+    x = x.astype(np.float64)
+    t = t.astype(np.float64)
+    D = x.shape[1]
+    dh = D // H
+    xh1, rs1 = _ln(x)
+    ln1 = xh1  # gamma 1, beta 0
+    q, k, v = ln1 @ f["wq"].T, ln1 @ f["wk"].T, ln1 @ f["wv"].T
+    Q, K, V = _heads(q, B, S, H), _heads(k, B, S, H), _heads(v, B, S, H)
+    s = Q @ K.transpose(0, 1, 3, 2) / math.sqrt(dh)
+    s = s - s.max(-1, keepdims=True)
+    P = np.exp(s)
+    P /= P.sum(-1, keepdims=True)
+    A = _merge(P @ V, B, S)
+    o = A @ f["wo"].T
+    r = x + o
+    xh2, rs2 = _ln(r)
+    h1 = xh2 @ f["w1"].T
+    a1 = _gelu(h1)
+    y = r + a1 @ f["w2"].T
+    n = y.size
+    loss = ((y - t) ** 2).sum() / n
+
+    dy = 2.0 * (y - t) / n
+    g = {}
+    g["w2"] = dy.T @ a1
+    da1 = dy @ f["w2"]
+    dh1 = da1 * _gelu_grad(h1)
+    g["w1"] = dh1.T @ xh2
+    dln2 = dh1 @ f["w1"]
+    g["ln2_gamma"] = (dln2 * xh2).sum(0)
+    g["ln2_beta"] = dln2.sum(0)
+    dr = dy + _ln_bwd(dln2, xh2, rs2, 1.0)
+    g["wo"] = dr.T @ A
+    dA = _heads(dr @ f["wo"], B, S, H)
+    dV = P.transpose(0, 1, 3, 2) @ dA
+    dP = dA @ V.transpose(0, 1, 3, 2)
+    dS = P * (dP - (dP * P).sum(-1, keepdims=True)) / math.sqrt(dh)
+    dQ, dK = dS @ K, dS.transpose(0, 1, 3, 2) @ Q
+    dq, dk, dv = _merge(dQ, B, S), _merge(dK, B, S), _merge(dV, B, S)
+    g["wq"], g["wk"], g["wv"] = dq.T @ ln1, dk.T @ ln1, dv.T @ ln1
+    dln1 = dq @ f["wq"] + dk @ f["wk"] + dv @ f["wv"]
+    g["ln1_gamma"] = (dln1 * xh1).sum(0)
+    g["ln1_beta"] = dln1.sum(0)
+    g["x"] = dr + _ln_bwd(dln1, xh1, rs1, 1.0)
+    g["bq"], g["bk"], g["bv"] = dq.sum(0), dk.sum(0), dv.sum(0)
+    g["bo"], g["c1"], g["c2"] = dr.sum(0), dh1.sum(0), dy.sum(0)
+    return loss, g, y
