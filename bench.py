@@ -232,6 +232,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-rows-a", type=int, default=512)
     ap.add_argument("--cpu-rows-b", type=int, default=192)
+    ap.add_argument("--only", choices=["c1", "c4"], default=None,
+                    help="run only this secondary workload (for profiling); prints its entry")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -248,6 +250,14 @@ def main() -> int:
     n_cus, arch = ctx.info()
     log(f"device {arch}, {n_cus} CUs")
     rng = np.random.default_rng(SEED)
+
+    if args.only is not None:
+        fn = {"c1": lambda: bench_c1(ctx, args.steps, args.warmup),
+              "c4": lambda: bench_c4(ctx, args.steps, args.warmup)}[args.only]
+        res = fn()
+        print(json.dumps({"workload": args.only, **res}), flush=True)
+        ctx.close()
+        return 0
 
     M = K = N = 2048
     log(f"matmul_backward {M}x{K}x{N}: {args.warmup} warmup + {args.steps} timed steps")

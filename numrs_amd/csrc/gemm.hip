@@ -32,6 +32,11 @@
 //     of tiles and its private L2 sees the operand rows/columns it reuses.
 //   * matmul_backward launches dA and dB tiles in ONE grid (2 x 256 tiles at
 //     2048^2 = 2 workgroups per CU on 256 CUs).
+//   * Split-K for products with few output tiles and long reductions (the
+//     weight gradients X^T dY of Linear layers): each split writes a plain
+//     partial, splitk_reduce adds them in split order -- deterministic.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -62,6 +67,12 @@ struct Gemm {
   int tiles_p, tiles_q;
   int accumulate;
   float alpha;  // C = alpha * X@Y (+ C)
+  // Split-K: with splits > 1 the reduction is cut into `splits` ranges of
+  // whole k-tiles; range s writes its plain partial product to
+  // partial + s*P*Q (row stride Q) and splitk_reduce forms alpha*sum (+C).
+  int splits;
+  int ktiles_per_split;
+  float *partial;
 };
 
 // Loads one 128 x 32 operand tile from global memory into registers
@@ -129,6 +140,9 @@ __device__ __forceinline__ f4 frag(const float *__restrict__ lds, int pbase, int
 
 template <bool XRC, bool YRC, bool VEC>
 __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, float *smem) {
+  // Split-K: consecutive logical tiles are the k-ranges of one output tile.
+  const int split = tile % d.splits;
+  tile /= d.splits;
   // Raster order: groups of kGroupRows tile-rows, column-major inside a group.
   const int per_group = kGroupRows * d.tiles_q;
   const int gidx = tile / per_group;
@@ -156,10 +170,13 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
 
   TileLoad<XRC, VEC> lx;
   TileLoad<YRC, VEC> ly;
-  const int nk = (d.R + kBR - 1) / kBR;
+  const int nk_all = (d.R + kBR - 1) / kBR;
+  const int kt_begin = split * d.ktiles_per_split;
+  const int nk = max(0, min(nk_all - kt_begin, d.ktiles_per_split));
+  const int r_begin = kt_begin * kBR;
 
-  lx.load(X, d.ldx, p0, 0, d.P, d.R, tid);
-  ly.load(Y, d.ldy, q0, 0, d.Q, d.R, tid);
+  lx.load(X, d.ldx, p0, r_begin, d.P, d.R, tid);
+  ly.load(Y, d.ldy, q0, r_begin, d.Q, d.R, tid);
   lx.store(xs0, tid);
   ly.store(ys0, tid);
   __syncthreads();
@@ -178,8 +195,8 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
     acc11 = f16v{};
     const bool more = kt + 1 < nk;
     if (more) {
-      lx.load(X, d.ldx, p0, (kt + 1) * kBR, d.P, d.R, tid);
-      ly.load(Y, d.ldy, q0, (kt + 1) * kBR, d.Q, d.R, tid);
+      lx.load(X, d.ldx, p0, r_begin + (kt + 1) * kBR, d.P, d.R, tid);
+      ly.load(Y, d.ldy, q0, r_begin + (kt + 1) * kBR, d.Q, d.R, tid);
     }
     const float *xl = (kt & 1) ? xs1 : xs0;
     const float *yl = (kt & 1) ? ys1 : ys0;
@@ -224,12 +241,31 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
     for (int i = 0; i < 16; ++i) {
       const int p = p0 + wp * 64 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (p < d.P && q < d.Q) {
-        float *dst = C + (int64_t)p * d.ldc + q;
-        const float v = d.alpha * a[i];
-        *dst = d.accumulate ? *dst + v : v;
+        if (d.splits > 1) {
+          d.partial[((int64_t)split * d.P + p) * d.Q + q] = a[i];
+        } else {
+          float *dst = C + (int64_t)p * d.ldc + q;
+          const float v = d.alpha * a[i];
+          *dst = d.accumulate ? *dst + v : v;
+        }
       }
     }
   }
+}
+
+// C = alpha * sum_s partial[s] (+ C), splits added in order s = 0, 1, ...
+__global__ void __launch_bounds__(256)
+    splitk_reduce(const float *__restrict__ partial, float *__restrict__ C, int64_t ldc, int P,
+                  int Q, int splits, float alpha, int acc) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = (int64_t)P * Q;
+  if (i >= n) return;
+  float s = 0.0f;
+  for (int k = 0; k < splits; ++k) s += partial[k * n + i];
+  const int64_t p = i / Q, q = i - p * Q;
+  float *dst = C + p * ldc + q;
+  const float v = alpha * s;
+  *dst = acc ? *dst + v : v;
 }
 
 // Maps the hardware workgroup id to a logical tile so that XCD k (which
@@ -259,6 +295,35 @@ __global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, G
 }
 
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
+
+// Split-K plan for one product: a grid under 256 workgroups leaves most of
+// the 256 CUs idle (a [512,512] weight gradient over 4096 tokens is 16
+// tiles), so the reduction is split until the product has ~256 workgroups,
+// keeping at least 8 k-tiles (256 reduction steps) per split.  Batched
+// products already fill the grid through their batch dimension.
+int plan_splits(const Gemm &g, int64_t batch) {
+  const int64_t t = (int64_t)g.tiles_p * g.tiles_q;
+  const int nk = (g.R + kBR - 1) / kBR;
+  if (batch != 1 || t >= 256 || nk < 16) return 1;
+  int64_t s = (256 + t - 1) / t;
+  s = std::min<int64_t>(s, nk / 8);
+  s = std::min<int64_t>(s, 32);
+  return (int)std::max<int64_t>(s, 1);
+}
+
+void apply_splits(Gemm &g, int splits, float *partial) {
+  const int nk = (g.R + kBR - 1) / kBR;
+  g.splits = splits;
+  g.ktiles_per_split = (nk + splits - 1) / splits;
+  g.partial = partial;
+}
+
+int reduce_splits(numrs_hip_ctx *ctx, const Gemm &g) {
+  const int64_t n = (int64_t)g.P * g.Q;
+  splitk_reduce<<<grid_for(n, 256), 256, 0, ctx->stream>>>(g.partial, g.C, g.ldc, g.P, g.Q,
+                                                          g.splits, g.alpha, g.accumulate);
+  return numrs_hip::check_launch(ctx, "splitk_reduce");
+}
 
 // Vector (float4) loads need 16-byte aligned bases, leading dimensions and
 // contiguous extents that are multiples of 4.
@@ -296,6 +361,9 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.bsx2 = g.bsy2 = g.bsc2 = 0;
   g.binner = 1;
   g.alpha = 1.0f;
+  g.splits = 1;
+  g.ktiles_per_split = (int)((R + kBR - 1) / kBR);
+  g.partial = nullptr;
   g.P = (int)P;
   g.Q = (int)Q;
   g.R = (int)R;
@@ -312,17 +380,25 @@ int zero_output(numrs_hip_ctx *ctx, float *C, int64_t count, int acc) {
 }
 
 template <bool XRC, bool YRC>
-int launch_one(numrs_hip_ctx *ctx, const Gemm &g, int64_t batch) {
+int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   const int64_t n_tiles = (int64_t)g.tiles_p * g.tiles_q;
   if (n_tiles == 0 || batch == 0) return NUMRS_HIP_OK;
-  if (n_tiles > 0x7fffffff)
+  const int splits = plan_splits(g, batch);
+  if (splits > 1) {
+    void *ws = nullptr;
+    const size_t bytes = (size_t)splits * g.P * g.Q * sizeof(float);
+    if (int rc = numrs_hip::workspace(ctx, bytes, &ws)) return rc;
+    apply_splits(g, splits, static_cast<float *>(ws));
+  }
+  if (n_tiles * splits > 0x7fffffff)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "gemm: too many tiles");
-  dim3 grid((unsigned)n_tiles, (unsigned)batch);
+  dim3 grid((unsigned)(n_tiles * splits), (unsigned)batch);
   if (vec_ok(g, XRC, YRC))
     gemm_kernel<XRC, YRC, true><<<grid, kThreads, 0, ctx->stream>>>(g);
   else
     gemm_kernel<XRC, YRC, false><<<grid, kThreads, 0, ctx->stream>>>(g);
-  return numrs_hip::check_launch(ctx, "gemm_kernel");
+  if (int rc = numrs_hip::check_launch(ctx, "gemm_kernel")) return rc;
+  return splits > 1 ? reduce_splits(ctx, g) : NUMRS_HIP_OK;
 }
 
 int gemm_dispatch(numrs_hip_ctx *ctx, const Gemm &g, int64_t batch, bool xrc, bool yrc) {
@@ -357,15 +433,29 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   Gemm gb = make(A, dC, dB, K, N, N, sa, sc, sb, K, N, M, acc);
   if (dA == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
   if (dB == nullptr) return gemm_dispatch(ctx, ga, batch, true, true);
-  const int64_t ta = (int64_t)ga.tiles_p * ga.tiles_q;
-  const int64_t tb = (int64_t)gb.tiles_p * gb.tiles_q;
+  const int sa_ = plan_splits(ga, batch), sb_ = plan_splits(gb, batch);
+  if (sa_ > 1 || sb_ > 1) {
+    const size_t na = sa_ > 1 ? (size_t)sa_ * ga.P * ga.Q : 0;
+    const size_t nb = sb_ > 1 ? (size_t)sb_ * gb.P * gb.Q : 0;
+    void *ws = nullptr;
+    if (int rc2 = numrs_hip::workspace(ctx, (na + nb) * sizeof(float), &ws)) return rc2;
+    float *base = static_cast<float *>(ws);
+    if (sa_ > 1) apply_splits(ga, sa_, base);
+    if (sb_ > 1) apply_splits(gb, sb_, base + na);
+  }
+  const int64_t ta = (int64_t)ga.tiles_p * ga.tiles_q * sa_;
+  const int64_t tb = (int64_t)gb.tiles_p * gb.tiles_q * sb_;
   if (ta + tb > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);
   dim3 grid((unsigned)(ta + tb), (unsigned)batch);
   if (vec_ok(ga, true, true) && vec_ok(gb, false, false))
     matmul_backward_kernel<true><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
   else
     matmul_backward_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
-  return numrs_hip::check_launch(ctx, "matmul_backward_kernel");
+  if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_kernel")) return rc2;
+  if (sa_ > 1)
+    if (int rc2 = reduce_splits(ctx, ga)) return rc2;
+  if (sb_ > 1) return reduce_splits(ctx, gb);
+  return NUMRS_HIP_OK;
 }
 
 int matmul_impl(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, int64_t batch,

@@ -456,3 +456,37 @@ def test_error_paths(hip_ctx):
         c.adam_step(x, x, x, x, 0)
     with pytest.raises(HipError):
         c.softmax_ce_backward(x.view(0, (1,)), x.view(0, (2, 2)), x.view(0, (2, 2)))
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 512, 512), (4096, 256, 384), (8192, 128, 64),
+                                   (3000, 130, 70)])
+@pytest.mark.parametrize("acc", [False, True])
+def test_matmul_backward_split_k(hip_ctx, rng, M, K, N, acc):
+    # Weight-gradient shapes: dB = A^T dC has few output tiles and a long
+    # reduction over M, so it runs split-K (deterministic partials + reduce).
+    say(f"split-k matmul_backward M={M} K={K} N={N} acc={acc}")
+    A, B, dC = rand(rng, (M, K)), rand(rng, (K, N)), rand(rng, (M, N))
+    ga, gb = rand(rng, (M, K)), rand(rng, (K, N))
+    c = hip_ctx
+    dA = c.to_device(ga) if acc else c.empty((M, K))
+    dB = c.to_device(gb) if acc else c.empty((K, N))
+    c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), dA, dB, accumulate=acc)
+    _, rb = O.matmul_backward(dC, A, B, need_a=False, f64=True)
+    _, rb32 = O.matmul_backward(dC, A, B, need_a=False)
+    base_b = gb.astype(np.float64) if acc else 0.0
+    assert_contraction(dB.numpy(), base_b + rb, M, ref32=None if acc else rb32, what="dB")
+    ra, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=(0, 64))
+    base_a = ga[:64].astype(np.float64) if acc else 0.0
+    assert_contraction(dA.numpy()[:64], base_a + ra[:64], N, what="dA rows")
+    # determinism: a second run gives identical bits
+    dB2 = c.to_device(gb) if acc else c.empty((K, N))
+    c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), None, dB2, accumulate=acc)
+    assert_bits(dB2.numpy(), dB.numpy(), "split-k determinism")
+
+
+def test_matmul_forward_split_k_long_reduction(hip_ctx, rng):
+    A, B = rand(rng, (64, 8192)), rand(rng, (8192, 64))
+    c = hip_ctx
+    C = c.empty((64, 64))
+    c.matmul(c.to_device(A), c.to_device(B), C)
+    assert_contraction(C.numpy(), A.astype(np.float64) @ B.astype(np.float64), 8192)
