@@ -156,6 +156,21 @@ int numrs_hip_matmul_batched(numrs_hip_ctx *ctx, const float *A, const float *B,
                              int64_t stride_b, int64_t stride_c, int trans_a, int trans_b,
                              int accumulate);
 
+/* Linear layer y[T,out] = x[T,in] @ W[out,in]^T + b (b may be NULL) as one
+ * MFMA product with the bias added in its epilogue.  Same values as the
+ * reference's Transpose -> MatMul -> Add node sequence (autograd/nn.rs:217-235)
+ * without materialising W^T. */
+int numrs_hip_linear_forward(numrs_hip_ctx *ctx, const float *x, const float *W, const float *b,
+                             float *y, int64_t T, int64_t in, int64_t out);
+/* Its backward from g = dL/dy: dx = g @ W and dW = g^T @ x in one launch
+ * (what matmul_backward + transpose_backward compute for those nodes,
+ * backward.rs:113-149, 305-312), db = unbroadcast(g) in `mode`
+ * (backward.rs:43-54).  Any of dx/dW/db may be NULL; one accumulate flag per
+ * output. */
+int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x, const float *W,
+                              float *dx, float *dW, float *db, int64_t T, int64_t in, int64_t out,
+                              int acc_dx, int acc_dw, int acc_db, int mode);
+
 /* General strided product, the building block of attention's batched
  * gradients: for z in [0, batch), with zo = z / batch_inner and
  * zi = z % batch_inner, operand A_z starts at A + zo*sa_outer + zi*sa_inner
@@ -261,12 +276,23 @@ int numrs_hip_argmax_rows(numrs_hip_ctx *ctx, const float *x, int32_t *idx, int6
 int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, int64_t n,
                        float lr, float mu, float wd);
 
+/* SGD over `count` parameter tensors in one launch (the per-parameter loop
+ * of sgd.rs:131-164 fused): p[i], g[i], v[i] (v may be NULL when mu == 0)
+ * of n[i] elements each.  The pointer arrays are host arrays. */
+int numrs_hip_sgd_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *const *g,
+                             float *const *v, const int64_t *n, int count, float lr, float mu,
+                             float wd);
+
 /* Adam::step for one parameter (optim/adam.rs:310-353) at step t (the
  * already-incremented counter): bias corrections 1 - b^t are computed on the
  * host with f32::powi's semantics, then one fused pass updates p, m, v
  * (28 B/element). */
 int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, float *v,
                         int64_t n, float lr, float b1, float b2, float eps, float wd, int t);
+/* Adam over `count` parameter tensors in one launch (adam.rs:317-350 fused). */
+int numrs_hip_adam_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *const *g,
+                              float *const *m, float *const *v, const int64_t *n, int count,
+                              float lr, float b1, float b2, float eps, float wd, int t);
 
 /* ---------------------------------------------------------------------- */
 /* Forward kernels the engine records (DispatchTable / ops.rs analogues)   */
@@ -299,11 +325,12 @@ int numrs_hip_layernorm_forward(numrs_hip_ctx *ctx, const float *x, const float 
                                 const float *beta, float *y, float *mean, float *rstd,
                                 int64_t rows, int64_t cols, float eps);
 /* LayerNorm backward from the saved mean/rstd: dx, dgamma = sum_rows g*xhat,
- * dbeta = sum_rows g (any may be NULL); rows of at most 2048. */
+ * dbeta = sum_rows g (any may be NULL; one accumulate flag each); rows of at
+ * most 2048.  One pass over g and x plus two column finalizes. */
 int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float *x,
                                  const float *gamma, const float *mean, const float *rstd,
                                  float *dx, float *dgamma, float *dbeta, int64_t rows,
-                                 int64_t cols, int accumulate);
+                                 int64_t cols, int acc_dx, int acc_dgamma, int acc_dbeta);
 
 /* ---------------------------------------------------------------------- */
 /* Tensor engine: numrs's Tensor / backward / optimizers, device-resident   */
@@ -376,6 +403,10 @@ int numrs_hip_tensor_softmax(numrs_hip_tensor *a, numrs_hip_tensor **out);
 int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
                                 numrs_hip_tensor *beta, float eps, numrs_hip_tensor **out);
 
+/* Linear node y = x @ W^T + b over x [T, in], W [out, in], b [out] or NULL:
+ * one node with Linear::forward's values and gradients (nn.rs:217-235). */
+int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
+                            numrs_hip_tensor **out);
 /* Multi-head attention node over q, k, v [B*S, D] (numrs_hip_attention_forward). */
 int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
                                int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out);

@@ -42,6 +42,8 @@ SIGNATURES = {
     "numrs_hip_matmul_backward_batched": (_i, [_vp] * 6 + [_i64] * 7 + [_i]),
     "numrs_hip_matmul": (_i, [_vp] * 4 + [_i64] * 3 + [_i] * 3),
     "numrs_hip_matmul_batched": (_i, [_vp] * 4 + [_i64] * 7 + [_i] * 3),
+    "numrs_hip_linear_forward": (_i, [_vp] * 5 + [_i64] * 3),
+    "numrs_hip_linear_backward": (_i, [_vp] * 7 + [_i64] * 3 + [_i] * 4),
     "numrs_hip_gemm": (_i, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i, _i, _f, _i,
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "numrs_hip_sum_to_shape": (_i, [_vp, _vp, _i64p, _i, _vp, _i64p, _i, _i, _i]),
@@ -55,6 +57,8 @@ SIGNATURES = {
     "numrs_hip_argmax_rows": (_i, [_vp] * 3 + [_i64, _i64, _i]),
     "numrs_hip_sgd_step": (_i, [_vp] * 4 + [_i64, _f, _f, _f]),
     "numrs_hip_adam_step": (_i, [_vp] * 5 + [_i64, _f, _f, _f, _f, _f, _i]),
+    "numrs_hip_sgd_step_multi": (_i, [_vp] * 4 + [_i64p, _i, _f, _f, _f]),
+    "numrs_hip_adam_step_multi": (_i, [_vp] * 5 + [_i64p, _i, _f, _f, _f, _f, _f, _i]),
     # forward kernels
     "numrs_hip_binary_forward": (_i, [_vp, _i, _vp, _i64p, _i, _vp, _i64p, _i, _vp]),
     "numrs_hip_unary_forward": (_i, [_vp, _i, _vp, _vp, _i64, _f]),
@@ -64,7 +68,7 @@ SIGNATURES = {
     "numrs_hip_cross_entropy_loss": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "numrs_hip_softmax_forward": (_i, [_vp, _vp, _vp, _i64, _i64, _f]),
     "numrs_hip_layernorm_forward": (_i, [_vp] * 7 + [_i64, _i64, _f]),
-    "numrs_hip_layernorm_backward": (_i, [_vp] * 9 + [_i64, _i64, _i]),
+    "numrs_hip_layernorm_backward": (_i, [_vp] * 9 + [_i64, _i64, _i, _i, _i]),
     "numrs_hip_attention_forward": (_i, [_vp] * 6 + [_i64] * 4),
     "numrs_hip_attention_backward": (_i, [_vp] * 9 + [_i64] * 4 + [_i]),
     # tensor engine
@@ -95,6 +99,7 @@ SIGNATURES = {
     "numrs_hip_tensor_cross_entropy_labels": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_softmax": (_i, [_vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_layer_norm": (_i, [_vp, _vp, _vp, _f, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_linear": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_attention": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_optim_sgd": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, ctypes.POINTER(_vp)]),
     "numrs_hip_optim_adam": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, _f, _f,

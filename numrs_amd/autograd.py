@@ -272,6 +272,13 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_layer_norm(self._h, gamma._h, beta._h, eps,
                                                               ctypes.byref(h)), h)
 
+    def linear(self, weight: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
+        """self @ weight^T + bias as one node (Linear::forward's values and grads)."""
+        h = ctypes.c_void_p()
+        return self._out(L.load().numrs_hip_tensor_linear(self._h, weight._h,
+                                                          bias._h if bias is not None else None,
+                                                          ctypes.byref(h)), h)
+
     def attention(self, k: "Tensor", v: "Tensor", batch: int, seq: int, heads: int) -> "Tensor":
         """Multi-head attention with self as q; q, k, v are [batch*seq, dim]."""
         h = ctypes.c_void_p()

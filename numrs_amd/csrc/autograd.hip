@@ -38,7 +38,7 @@ thread_local bool g_grad_enabled = true;  // mod.rs:194-206
 
 enum class Op {
   Leaf, Add, Sub, Mul, Div, MatMul, Transpose, Unary, Sum, Mean, MSE, CrossEntropy,
-  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention
+  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention, Linear
 };
 
 struct Storage {
@@ -399,7 +399,6 @@ int bw_softmax(const T &out, const float *g, Node &n) {  // backward.rs:521-541
 int bw_layernorm(const T &out, const float *g, Node &n) {
   const T &x = n.inputs[0], &gm = n.inputs[1], &bt = n.inputs[2];
   const int64_t cols = x->shape.back(), rows = x->numel() / cols;
-  numrs_hip_ctx *ctx = out->ctx;
   float *dx = nullptr, *dg = nullptr, *db = nullptr;
   int ax = 0, ag = 0, ab = 0;
   if (x->requires_grad)
@@ -408,23 +407,8 @@ int bw_layernorm(const T &out, const float *g, Node &n) {
     if (int rc = grad_target(gm, &dg, &ag)) return rc;
   if (bt->requires_grad)
     if (int rc = grad_target(bt, &db, &ab)) return rc;
-  const float *mean = n.saved[0]->ptr, *rstd = n.saved[1]->ptr;
-  if ((dx && dg && ax != ag) || (dx && db && ax != ab) || (dg && db && ag != ab)) {
-    if (dx)
-      if (int rc = numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd, dx,
-                                                nullptr, nullptr, rows, cols, ax))
-        return rc;
-    if (dg)
-      if (int rc = numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd,
-                                                nullptr, dg, nullptr, rows, cols, ag))
-        return rc;
-    if (db)
-      return numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd, nullptr,
-                                          nullptr, db, rows, cols, ab);
-    return NUMRS_HIP_OK;
-  }
-  return numrs_hip_layernorm_backward(ctx, g, x->data->ptr, gm->data->ptr, mean, rstd, dx, dg, db,
-                                      rows, cols, dx ? ax : (dg ? ag : ab));
+  return numrs_hip_layernorm_backward(out->ctx, g, x->data->ptr, gm->data->ptr, n.saved[0]->ptr,
+                                      n.saved[1]->ptr, dx, dg, db, rows, cols, ax, ag, ab);
 }
 
 int bw_attention(const T &out, const float *g, Node &n) {
@@ -471,6 +455,33 @@ int bw_attention(const T &out, const float *g, Node &n) {
   return NUMRS_HIP_OK;
 }
 
+int bw_linear(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0], &W = n.inputs[1];
+  const T *b = n.inputs.size() > 2 ? &n.inputs[2] : nullptr;
+  const int64_t Tn = x->shape[0], in = x->shape[1], outf = W->shape[0];
+  numrs_hip_ctx *ctx = out->ctx;
+  float *dx = nullptr, *dW = nullptr, *db = nullptr;
+  int ax = 0, aw = 0, ab = 0;
+  const bool shared = x->requires_grad && W->requires_grad && x->grad == W->grad;
+  if (x->requires_grad)
+    if (int rc = grad_target(x, &dx, &ax)) return rc;
+  if (W->requires_grad && !shared)
+    if (int rc = grad_target(W, &dW, &aw)) return rc;
+  if (b && (*b)->requires_grad)
+    if (int rc = grad_target(*b, &db, &ab)) return rc;
+  if (int rc = numrs_hip_linear_backward(ctx, g, x->data->ptr, W->data->ptr, dx, dW, db, Tn, in,
+                                         outf, ax, aw, ab, ctx->unbroadcast_mode))
+    return rc;
+  if (shared) {  // x is W: its second gradient adds
+    float *t;
+    int a;
+    if (int rc = grad_target(W, &t, &a)) return rc;
+    return numrs_hip_linear_backward(ctx, g, x->data->ptr, W->data->ptr, nullptr, t, nullptr, Tn,
+                                     in, outf, 0, 1, 0, ctx->unbroadcast_mode);
+  }
+  return NUMRS_HIP_OK;
+}
+
 int run_backward_fn(const T &out) {
   Node &n = *out->node;
   const float *g = out->grad->buf->ptr;
@@ -491,6 +502,7 @@ int run_backward_fn(const T &out) {
     case Op::Softmax: return bw_softmax(out, g, n);
     case Op::LayerNorm: return bw_layernorm(out, g, n);
     case Op::Attention: return bw_attention(out, g, n);
+    case Op::Linear: return bw_linear(out, g, n);
     case Op::Leaf: return NUMRS_HIP_OK;
   }
   return NUMRS_HIP_OK;
@@ -725,6 +737,28 @@ int op_layernorm(const T &x, const T &gamma, const T &beta, float eps, T *out) {
                                            r->data->ptr, mean->ptr, rstd->ptr, rows, cols, eps))
     return rc;
   if (rec) attach(r, Op::LayerNorm, {x, gamma, beta}, 0, eps, {mean, rstd});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_linear(const T &x, const T &W, const T *b, T *out) {
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.size() != 2 || W->shape.size() != 2 || x->shape[1] != W->shape[1])
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "linear expects x [T,in], W [out,in]");
+  if (b && ((*b)->numel() != W->shape[0]))
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "linear: bias must have out elements");
+  const bool rec = b ? recording({&x, &W, b}) : recording({&x, &W});
+  T r;
+  if (int rc = make_tensor(ctx, {x->shape[0], W->shape[0]}, rec, &r)) return rc;
+  if (int rc = numrs_hip_linear_forward(ctx, x->data->ptr, W->data->ptr,
+                                        b ? (*b)->data->ptr : nullptr, r->data->ptr, x->shape[0],
+                                        x->shape[1], W->shape[0]))
+    return rc;
+  if (rec) {
+    std::vector<T> ins{x, W};
+    if (b) ins.push_back(*b);
+    attach(r, Op::Linear, std::move(ins));
+  }
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -1019,6 +1053,14 @@ int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
   return wrap(std::move(r), out);
 }
 
+int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
+                            numrs_hip_tensor **out) {
+  if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
 int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
                                int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out) {
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
@@ -1065,18 +1107,26 @@ int numrs_hip_optim_step(numrs_hip_optim *opt) {
   if (opt == nullptr) return NUMRS_HIP_E_INVALID;
   Optim &o = opt->o;
   if (o.adam) ++o.t;  // adam.rs:311
+  std::vector<float *> ps, ms, vs;
+  std::vector<const float *> gs;
+  std::vector<int64_t> ns;
   for (size_t i = 0; i < o.params.size(); ++i) {
     const T &p = o.params[i];
     if (!p->requires_grad) continue;  // sgd.rs:134-136, adam.rs:320-322
     if (int rc = grad_materialise(p)) return rc;
-    const float *g = p->grad->buf->ptr;
-    int rc = o.adam ? numrs_hip_adam_step(o.ctx, p->data->ptr, g, o.s1[i]->ptr, o.s2[i]->ptr,
-                                          p->numel(), o.lr, o.b1, o.b2, o.eps, o.wd, o.t)
-                    : numrs_hip_sgd_step(o.ctx, p->data->ptr, g, o.s1[i]->ptr, p->numel(), o.lr,
-                                         o.mu, o.wd);
-    if (rc) return rc;
+    ps.push_back(p->data->ptr);
+    gs.push_back(p->grad->buf->ptr);
+    ms.push_back(o.s1[i]->ptr);
+    vs.push_back(o.adam ? o.s2[i]->ptr : nullptr);
+    ns.push_back(p->numel());
   }
-  return NUMRS_HIP_OK;
+  if (ps.empty()) return NUMRS_HIP_OK;
+  const int count = (int)ps.size();
+  if (o.adam)
+    return numrs_hip_adam_step_multi(o.ctx, ps.data(), gs.data(), ms.data(), vs.data(), ns.data(),
+                                     count, o.lr, o.b1, o.b2, o.eps, o.wd, o.t);
+  return numrs_hip_sgd_step_multi(o.ctx, ps.data(), gs.data(), o.mu != 0.0f ? ms.data() : nullptr,
+                                  ns.data(), count, o.lr, o.mu, o.wd);
 }
 
 int numrs_hip_optim_zero_grad(numrs_hip_optim *opt) {  // sgd.rs:169-173

@@ -281,6 +281,88 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+// Multi-tensor optimizer launch: up to kMaxMulti parameter tensors share one
+// grid; block b belongs to the tensor t with start[t] <= b < start[t+1] and
+// covers that tensor's elements from (b - start[t]) * kElemsPerBlock.
+constexpr int kMaxMulti = 32;
+
+struct MultiArgs {
+  float *p[kMaxMulti];
+  const float *g[kMaxMulti];
+  float *s1[kMaxMulti];  // SGD velocity / Adam m
+  float *s2[kMaxMulti];  // Adam v
+  int64_t n[kMaxMulti];
+  int64_t start[kMaxMulti + 1];
+  int count;
+};
+
+__device__ __forceinline__ int multi_find(const MultiArgs &a, int64_t b) {
+  int t = 0;
+  while (t + 1 < a.count && a.start[t + 1] <= b) ++t;
+  return t;
+}
+
+template <bool MOMENTUM, bool DECAY>
+__global__ void __launch_bounds__(kBlock)
+    sgd_multi_kernel(MultiArgs a, float lr, float mu, float wd) {
+  const int t = multi_find(a, blockIdx.x);
+  float *__restrict__ p = a.p[t];
+  const float *__restrict__ g = a.g[t];
+  float *__restrict__ v = a.s1[t];
+  const int64_t n = a.n[t];
+  const int64_t base = (int64_t)(blockIdx.x - a.start[t]) * kElemsPerBlock + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 4 * kVecPerThread; ++u) {
+    const int64_t k = base + (int64_t)u * kBlock;
+    if (k < n) {
+      float gg = g[k];
+      if (DECAY) gg = gg + wd * p[k];
+      if (MOMENTUM) {
+        v[k] = mu * v[k] + gg;
+        p[k] = p[k] - lr * v[k];
+      } else {
+        p[k] = p[k] - lr * gg;
+      }
+    }
+  }
+}
+
+template <bool DECAY>
+__global__ void __launch_bounds__(kBlock) adam_multi_kernel(MultiArgs a, AdamArgs args) {
+  const int t = multi_find(a, blockIdx.x);
+  const int64_t n = a.n[t];
+  const int64_t base = (int64_t)(blockIdx.x - a.start[t]) * kElemsPerBlock + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 4 * kVecPerThread; ++u) {
+    const int64_t k = base + (int64_t)u * kBlock;
+    if (k < n) {
+      float pe = a.p[t][k], me = a.s1[t][k], ve = a.s2[t][k];
+      adam_elem(pe, a.g[t][k], me, ve, args, DECAY);
+      a.p[t][k] = pe;
+      a.s1[t][k] = me;
+      a.s2[t][k] = ve;
+    }
+  }
+}
+
+// Fills `a` for tensors [first, first+cnt); returns the number of blocks.
+int64_t multi_pack(MultiArgs &a, float *const *p, const float *const *g, float *const *s1,
+                   float *const *s2, const int64_t *n, int first, int cnt) {
+  a.count = cnt;
+  int64_t blocks = 0;
+  for (int i = 0; i < cnt; ++i) {
+    a.p[i] = p[first + i];
+    a.g[i] = g[first + i];
+    a.s1[i] = s1 ? s1[first + i] : nullptr;
+    a.s2[i] = s2 ? s2[first + i] : nullptr;
+    a.n[i] = n[first + i];
+    a.start[i] = blocks;
+    blocks += (n[first + i] + kElemsPerBlock - 1) / kElemsPerBlock;
+  }
+  a.start[cnt] = blocks;
+  return blocks;
+}
+
 // f32::powi as lowered by Rust/LLVM on x86-64 (compiler-rt __powisf2):
 // square-and-multiply over the exponent's bits, low bit first.
 float powi_f32(float a, int b) {
@@ -397,6 +479,67 @@ int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, i
   else NRS_SGD(false, false);
 #undef NRS_SGD
   return numrs_hip::check_launch(ctx, "sgd_kernel");
+}
+
+int numrs_hip_sgd_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *const *g,
+                             float *const *v, const int64_t *n, int count, float lr, float mu,
+                             float wd) {
+  NRS_CHECK_CTX(ctx);
+  if (count < 0 || (count > 0 && (p == nullptr || g == nullptr || n == nullptr)) ||
+      (mu != 0.0f && count > 0 && v == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_sgd_step_multi: bad arguments");
+  for (int i = 0; i < count; ++i)
+    if (n[i] < 0 || (n[i] > 0 && (p[i] == nullptr || g[i] == nullptr ||
+                                  (mu != 0.0f && v[i] == nullptr))))
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_sgd_step_multi: tensor %d", i);
+  for (int first = 0; first < count; first += kMaxMulti) {
+    MultiArgs a;
+    const int cnt = count - first < kMaxMulti ? count - first : kMaxMulti;
+    const int64_t blocks = multi_pack(a, p, g, mu != 0.0f ? v : nullptr, nullptr, n, first, cnt);
+    if (blocks == 0) continue;
+    if (blocks > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "too many elements");
+    const bool mom = mu != 0.0f, dec = wd != 0.0f;
+    const unsigned grid = (unsigned)blocks;
+    if (mom && dec) sgd_multi_kernel<true, true><<<grid, kBlock, 0, ctx->stream>>>(a, lr, mu, wd);
+    else if (mom) sgd_multi_kernel<true, false><<<grid, kBlock, 0, ctx->stream>>>(a, lr, mu, wd);
+    else if (dec) sgd_multi_kernel<false, true><<<grid, kBlock, 0, ctx->stream>>>(a, lr, mu, wd);
+    else sgd_multi_kernel<false, false><<<grid, kBlock, 0, ctx->stream>>>(a, lr, mu, wd);
+    if (int rc = numrs_hip::check_launch(ctx, "sgd_multi_kernel")) return rc;
+  }
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_adam_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *const *g,
+                              float *const *m, float *const *v, const int64_t *n, int count,
+                              float lr, float b1, float b2, float eps, float wd, int t) {
+  NRS_CHECK_CTX(ctx);
+  if (t < 1) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_adam_step_multi: t < 1");
+  if (count < 0 || (count > 0 && (!p || !g || !m || !v || !n)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_adam_step_multi: bad arguments");
+  for (int i = 0; i < count; ++i)
+    if (n[i] < 0 || (n[i] > 0 && (!p[i] || !g[i] || !m[i] || !v[i])))
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_adam_step_multi: tensor %d", i);
+  AdamArgs args;
+  args.lr = lr;
+  args.b1 = b1;
+  args.b2 = b2;
+  args.eps = eps;
+  args.wd = wd;
+  args.omb1 = 1.0f - b1;
+  args.omb2 = 1.0f - b2;
+  args.bc1 = 1.0f - powi_f32(b1, t);
+  args.bc2 = 1.0f - powi_f32(b2, t);
+  for (int first = 0; first < count; first += kMaxMulti) {
+    MultiArgs a;
+    const int cnt = count - first < kMaxMulti ? count - first : kMaxMulti;
+    const int64_t blocks = multi_pack(a, p, g, m, v, n, first, cnt);
+    if (blocks == 0) continue;
+    if (blocks > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "too many elements");
+    if (wd != 0.0f) adam_multi_kernel<true><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(a, args);
+    else adam_multi_kernel<false><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(a, args);
+    if (int rc = numrs_hip::check_launch(ctx, "adam_multi_kernel")) return rc;
+  }
+  return NUMRS_HIP_OK;
 }
 
 int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, float *v,

@@ -73,6 +73,9 @@ struct Gemm {
   int splits;
   int ktiles_per_split;
   float *partial;
+  // Optional bias added per output column after alpha: C = alpha*X@Y + bias[q]
+  // (+ C); the Linear forward's "+ b" folded into the product's epilogue.
+  const float *bias;
 };
 
 // Loads one 128 x 32 operand tile from global memory into registers
@@ -245,7 +248,8 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
           d.partial[((int64_t)split * d.P + p) * d.Q + q] = a[i];
         } else {
           float *dst = C + (int64_t)p * d.ldc + q;
-          const float v = d.alpha * a[i];
+          float v = d.alpha * a[i];
+          if (d.bias != nullptr) v = v + d.bias[q];
           *dst = d.accumulate ? *dst + v : v;
         }
       }
@@ -256,15 +260,24 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
 // C = alpha * sum_s partial[s] (+ C), splits added in order s = 0, 1, ...
 __global__ void __launch_bounds__(256)
     splitk_reduce(const float *__restrict__ partial, float *__restrict__ C, int64_t ldc, int P,
-                  int Q, int splits, float alpha, int acc) {
+                  int Q, int splits, float alpha, int acc, const float *__restrict__ bias) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t n = (int64_t)P * Q;
   if (i >= n) return;
+  // Loads of all splits are issued before the ordered adds.
+  constexpr int kBatch = 8;
   float s = 0.0f;
-  for (int k = 0; k < splits; ++k) s += partial[k * n + i];
+  for (int k0 = 0; k0 < splits; k0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = k0 + u < splits ? partial[(k0 + u) * n + i] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) s += v[u];
+  }
   const int64_t p = i / Q, q = i - p * Q;
   float *dst = C + p * ldc + q;
-  const float v = alpha * s;
+  float v = alpha * s;
+  if (bias != nullptr) v = v + bias[q];
   *dst = acc ? *dst + v : v;
 }
 
@@ -282,8 +295,19 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Gemm d) {
   gemm_tile<XRC, YRC, VEC>(d, tile, blockIdx.y, smem);
 }
 
-// dA (NT) and dB (TN) of matmul_backward in one grid: logical tiles
-// [0, tiles_a) are dA tiles, the rest dB tiles.
+// Two products in one grid: logical tiles [0, tiles_a) belong to `a`, the
+// rest to `b`.  matmul_backward: dA = dC B^T (NT) with dB = A^T dC (TN);
+// the Linear backward: dx = g W (NN) with dW = g^T x (TN).
+template <bool XRC_A, bool YRC_A, bool VEC>
+__global__ void __launch_bounds__(kThreads, 2) gemm_pair_kernel(Gemm a, Gemm b, int tiles_a) {
+  __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    gemm_tile<XRC_A, YRC_A, VEC>(a, tile, blockIdx.y, smem);
+  else
+    gemm_tile<false, false, VEC>(b, tile - tiles_a, blockIdx.y, smem);
+}
+
 template <bool VEC>
 __global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, Gemm db, int tiles_a) {
   __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
@@ -321,7 +345,7 @@ void apply_splits(Gemm &g, int splits, float *partial) {
 int reduce_splits(numrs_hip_ctx *ctx, const Gemm &g) {
   const int64_t n = (int64_t)g.P * g.Q;
   splitk_reduce<<<grid_for(n, 256), 256, 0, ctx->stream>>>(g.partial, g.C, g.ldc, g.P, g.Q,
-                                                          g.splits, g.alpha, g.accumulate);
+                                                          g.splits, g.alpha, g.accumulate, g.bias);
   return numrs_hip::check_launch(ctx, "splitk_reduce");
 }
 
@@ -364,6 +388,7 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.splits = 1;
   g.ktiles_per_split = (int)((R + kBR - 1) / kBR);
   g.partial = nullptr;
+  g.bias = nullptr;
   g.P = (int)P;
   g.Q = (int)Q;
   g.R = (int)R;
@@ -514,9 +539,93 @@ int gemm_general(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B
   return gemm_dispatch(ctx, g, batch, !ta, tb != 0);
 }
 
+// Launches a (first, TN-second) product pair in one grid with per-product
+// split-K; `first_nt` selects the NT (matmul_backward dA) or NN (Linear dx)
+// layout of the first product.  Either product may be absent (C == null).
+int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char *who) {
+  const bool has_a = ga.C != nullptr, has_b = gb.C != nullptr;
+  if (!has_a && !has_b) return NUMRS_HIP_OK;
+  if (!has_a) return gemm_dispatch(ctx, gb, 1, false, false);
+  if (!has_b) return gemm_dispatch(ctx, ga, 1, true, first_nt);
+  const int sa_ = plan_splits(ga, 1), sb_ = plan_splits(gb, 1);
+  if (sa_ > 1 || sb_ > 1) {
+    const size_t na = sa_ > 1 ? (size_t)sa_ * ga.P * ga.Q : 0;
+    const size_t nb = sb_ > 1 ? (size_t)sb_ * gb.P * gb.Q : 0;
+    void *ws = nullptr;
+    if (int rc = numrs_hip::workspace(ctx, (na + nb) * sizeof(float), &ws)) return rc;
+    float *base = static_cast<float *>(ws);
+    if (sa_ > 1) apply_splits(ga, sa_, base);
+    if (sb_ > 1) apply_splits(gb, sb_, base + na);
+  }
+  const int64_t ta = (int64_t)ga.tiles_p * ga.tiles_q * sa_;
+  const int64_t tb = (int64_t)gb.tiles_p * gb.tiles_q * sb_;
+  if (ta + tb > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);
+  dim3 grid((unsigned)(ta + tb), 1);
+  const bool vec = vec_ok(ga, true, first_nt) && vec_ok(gb, false, false);
+  if (first_nt) {
+    if (vec) gemm_pair_kernel<true, true, true><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
+    else gemm_pair_kernel<true, true, false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
+  } else {
+    if (vec) gemm_pair_kernel<true, false, true><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
+    else gemm_pair_kernel<true, false, false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
+  }
+  if (int rc = numrs_hip::check_launch(ctx, "gemm_pair_kernel")) return rc;
+  if (sa_ > 1)
+    if (int rc = reduce_splits(ctx, ga)) return rc;
+  if (sb_ > 1) return reduce_splits(ctx, gb);
+  return NUMRS_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int numrs_hip_linear_forward(numrs_hip_ctx *ctx, const float *x, const float *W, const float *b,
+                             float *y, int64_t T, int64_t in, int64_t out) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_forward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (T == 0 || out == 0) return NUMRS_HIP_OK;
+  if (y == nullptr || (in > 0 && (x == nullptr || W == nullptr)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (in == 0) {  // empty product: y = b broadcast over rows (or 0)
+    if (int rc = numrs_hip_fill(ctx, y, T * out, 0.0f)) return rc;
+    if (b == nullptr) return NUMRS_HIP_OK;
+    const int64_t bs = out;
+    const int64_t ys[2] = {T, out};
+    return numrs_hip_binary_forward(ctx, NUMRS_HIP_ADD, y, ys, 2, b, &bs, 1, y);
+  }
+  // y[T,out] = x[T,in] @ W[out,in]^T + b : X = x (R-contig), Y = W^T (R-contig)
+  Gemm g = make(x, W, y, in, in, out, 0, 0, 0, T, out, in, 0);
+  g.bias = b;
+  return gemm_dispatch(ctx, g, 1, true, true);
+}
+
+int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x, const float *W,
+                              float *dx, float *dW, float *db, int64_t T, int64_t in, int64_t out,
+                              int acc_dx, int acc_dw, int acc_db, int mode) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_backward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (g == nullptr || (dx && W == nullptr) || (dW && x == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
+  if (T == 0 || out == 0) {  // empty reductions: zero gradients
+    if (dx && !acc_dx && T * in > 0)
+      if (int rc = numrs_hip_fill(ctx, dx, T * in, 0.0f)) return rc;
+    if (dW && !acc_dw && out * in > 0)
+      if (int rc = numrs_hip_fill(ctx, dW, out * in, 0.0f)) return rc;
+  } else if (in > 0) {
+    // dx[T,in] = g[T,out] @ W[out,in] : X = g (R-contig), Y = W (Q-contig)  [NN]
+    Gemm gx = make(g, W, dx, out, in, in, 0, 0, 0, T, in, out, acc_dx);
+    // dW[out,in] = g^T @ x : X = g^T (P-contig), Y = x (Q-contig)          [TN]
+    Gemm gw = make(g, x, dW, out, in, in, 0, 0, 0, out, in, T, acc_dw);
+    if (int rc = launch_pair(ctx, gx, gw, false, who)) return rc;
+  }
+  if (db == nullptr || out == 0) return NUMRS_HIP_OK;
+  const int64_t gs[2] = {T, out};
+  const int64_t bs = out;
+  return numrs_hip_sum_to_shape(ctx, g, gs, 2, db, &bs, 1, mode, acc_db);
+}
 
 int numrs_hip_gemm(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B, int64_t ldb,
                    float *C, int64_t ldc, int64_t M, int64_t K, int64_t N, int trans_a,

@@ -383,7 +383,7 @@ int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float
 int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float *x,
                                  const float *gamma, const float *mean, const float *rstd,
                                  float *dx, float *dgamma, float *dbeta, int64_t rows,
-                                 int64_t cols, int accumulate) {
+                                 int64_t cols, int acc_dx, int acc_dgamma, int acc_dbeta) {
   NRS_CHECK_CTX(ctx);
   const char *who = "numrs_hip_layernorm_backward";
   if (rows < 0 || cols <= 0)
@@ -391,9 +391,8 @@ int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float
   if (cols > kLnMaxCols)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: rows longer than %d", who, kLnMaxCols);
   if (rows == 0) {
-    if (accumulate) return NUMRS_HIP_OK;
-    int rc = dgamma ? numrs_hip_fill(ctx, dgamma, cols, 0.0f) : NUMRS_HIP_OK;
-    if (!rc && dbeta) rc = numrs_hip_fill(ctx, dbeta, cols, 0.0f);
+    int rc = (dgamma && !acc_dgamma) ? numrs_hip_fill(ctx, dgamma, cols, 0.0f) : NUMRS_HIP_OK;
+    if (!rc && dbeta && !acc_dbeta) rc = numrs_hip_fill(ctx, dbeta, cols, 0.0f);
     return rc;
   }
   if (g == nullptr || x == nullptr || gamma == nullptr || mean == nullptr || rstd == nullptr)
@@ -412,16 +411,16 @@ int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float
   const size_t lds = (size_t)8 * cols * sizeof(float);
   layernorm_bwd_pass1<<<(unsigned)chunks, kBlock, lds, ctx->stream>>>(
       g, x, gamma, mean, rstd, dx, part, part ? part + chunks * cols : nullptr, rows, cols,
-      accumulate, want);
+      acc_dx, want);
   if (int rc = numrs_hip::check_launch(ctx, "layernorm_bwd_pass1")) return rc;
   if (dgamma) {
     colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(part, dgamma, chunks, cols,
-                                                                       accumulate);
+                                                                       acc_dgamma);
     if (int rc = numrs_hip::check_launch(ctx, "colreduce_finalize")) return rc;
   }
   if (dbeta) {
     colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(part + chunks * cols, dbeta,
-                                                                       chunks, cols, accumulate);
+                                                                       chunks, cols, acc_dbeta);
     if (int rc = numrs_hip::check_launch(ctx, "colreduce_finalize")) return rc;
   }
   return NUMRS_HIP_OK;

@@ -33,7 +33,14 @@ class Module:
 
 
 class Linear(Module):
-    """y = x @ W^T + b with W [out, in], b [out] (nn.rs:57-235)."""
+    """y = x @ W^T + b with W [out, in], b [out] (nn.rs:57-235).
+
+    By default the layer is one fused node (an NT product with the bias in its
+    epilogue; backward dx = g W and dW = g^T x in one launch).  `fused=False`
+    records the reference's own three nodes instead; both give the same
+    gradients."""
+
+    fused = True
 
     def __init__(self, in_features: int, out_features: int, ctx=None):
         # Linear::new's deterministic fill: sin(0.123 i) * sqrt(1/in) (nn.rs:67-96).
@@ -56,6 +63,8 @@ class Linear(Module):
         self.bias = Tensor.new(np.asarray(b, np.float32).reshape(fout), True, ctx=ctx)
 
     def forward(self, x: Tensor) -> Tensor:
+        if self.fused:
+            return x.linear(self.weight, self.bias)
         w_t = self.weight.transpose()
         return x.matmul(w_t).add(self.bias)
 

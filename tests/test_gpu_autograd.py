@@ -349,3 +349,20 @@ def test_argmax_evaluate_rule():
     idx = c.empty((2,), np.int32)
     c.argmax_rows(c.to_device(logits), idx, tie_last=True)
     assert idx.numpy().tolist() == [2, 1]
+
+
+def test_fused_linear_equals_reference_node_sequence():
+    # nn.Linear's fused node vs the reference's Transpose -> MatMul -> Add nodes.
+    p = make_c1(seed=3)
+    onehot = np.eye(10, dtype=np.float32)[p["labels"]]
+    grads = []
+    for fused in (True, False):
+        model, l1, l2 = _c1_model(p)
+        l1.fused = l2.fused = fused
+        loss = model.forward(Tensor.new(p["x"], False)).cross_entropy_loss(
+            Tensor.new(onehot, False))
+        loss.backward()
+        grads.append([t.gradient() for t in (l1.weight, l1.bias, l2.weight, l2.bias)]
+                     + [loss.item()])
+    for a, b in zip(*grads):
+        assert_close(a, b, abs_tol=1e-7, rel_tol=1e-6)

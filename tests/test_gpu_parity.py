@@ -490,3 +490,73 @@ def test_matmul_forward_split_k_long_reduction(hip_ctx, rng):
     C = c.empty((64, 64))
     c.matmul(c.to_device(A), c.to_device(B), C)
     assert_contraction(C.numpy(), A.astype(np.float64) @ B.astype(np.float64), 8192)
+
+
+@pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (64, 128, 10), (4096, 512, 2048),
+                                        (33, 17, 5)])
+def test_linear_forward_backward(hip_ctx, rng, T, fin, fout):
+    # Linear::forward (nn.rs:217-235) and the grads its Transpose/MatMul/Add
+    # nodes produce (backward.rs:43-54, 113-149, 305-312).
+    say(f"linear T={T} in={fin} out={fout}")
+    x, W, b, g = rand(rng, (T, fin)), rand(rng, (fout, fin)), rand(rng, fout), rand(rng, (T, fout))
+    c = hip_ctx
+    xd, Wd, bd, gd = (c.to_device(a) for a in (x, W, b, g))
+    y = c.empty((T, fout))
+    rc = L.load().numrs_hip_linear_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, y.ptr, T, fin, fout)
+    assert rc == 0
+    ref_y = O.matmul_f64(x, O.transpose(W)).astype(np.float64) + b
+    assert_contraction(y.numpy(), ref_y, fin, what="y")
+    prev = {k: rand(rng, s) for k, s in (("dx", (T, fin)), ("dW", (fout, fin)), ("db", fout))}
+    for acc in ((0, 0, 0), (1, 0, 1), (0, 1, 0)):
+        dx, dW, db = (c.to_device(prev[k]) for k in ("dx", "dW", "db"))
+        rc = L.load().numrs_hip_linear_backward(c.handle, gd.ptr, xd.ptr, Wd.ptr, dx.ptr, dW.ptr,
+                                                db.ptr, T, fin, fout, *acc, L.UNBROADCAST_CORRECT)
+        assert rc == 0
+        rdx, rdwt = O.matmul_backward(g, x, O.transpose(W), f64=True)
+        base = [prev[k].astype(np.float64) if a else 0.0 for k, a in zip(("dx", "dW", "db"), acc)]
+        assert_contraction(dx.numpy(), base[0] + rdx, fout, what=f"dx {acc}")
+        assert_contraction(dW.numpy(), base[1] + O.transpose(rdwt), T, what=f"dW {acc}")
+        assert_close(db.numpy(), base[2] + g.astype(np.float64).sum(0), what=f"db {acc}")
+    # REFERENCE-mode bias gradient: full sum into db[0]
+    db = c.to_device(prev["db"])
+    rc = L.load().numrs_hip_linear_backward(c.handle, gd.ptr, xd.ptr, Wd.ptr, None, None, db.ptr,
+                                            T, fin, fout, 0, 0, 0, L.UNBROADCAST_REFERENCE)
+    assert rc == 0
+    want = np.zeros(fout, np.float32)
+    O.unbroadcast_reference_accumulate(g, want)
+    assert_close(db.numpy(), want, abs_tol=1e-4, what="db reference")
+
+
+def test_optimizer_multi_tensor_bit_exact(hip_ctx, rng):
+    import ctypes
+
+    sizes = [100352, 128, 1280, 10, 1, 4097, 33]
+    c = hip_ctx
+    for kind in ("sgd", "sgd_mom", "adam"):
+        ps = [rand(rng, n) for n in sizes]
+        gs = [rand(rng, n) for n in sizes]
+        ms = [np.zeros(n, np.float32) for n in sizes]
+        vs = [np.zeros(n, np.float32) for n in sizes]
+        pd = [c.to_device(a) for a in ps]
+        gd = [c.to_device(a) for a in gs]
+        md = [c.to_device(a) for a in ms]
+        vd = [c.to_device(a) for a in vs]
+        arr = lambda ds: (ctypes.c_void_p * len(ds))(*[d.ptr for d in ds])
+        ns = (ctypes.c_int64 * len(sizes))(*sizes)
+        for t in (1, 2, 3):
+            if kind == "adam":
+                rc = L.load().numrs_hip_adam_step_multi(c.handle, arr(pd), arr(gd), arr(md),
+                                                        arr(vd), ns, len(sizes), 1e-3, 0.9, 0.999,
+                                                        1e-8, 0.01, t)
+                for i in range(len(sizes)):
+                    O.adam_step(ps[i], gs[i], ms[i], vs[i], t, wd=0.01)
+            else:
+                mu = 0.9 if kind == "sgd_mom" else 0.0
+                rc = L.load().numrs_hip_sgd_step_multi(c.handle, arr(pd), arr(gd),
+                                                       arr(md) if mu else None, ns, len(sizes),
+                                                       0.01, mu, 1e-4)
+                for i in range(len(sizes)):
+                    O.sgd_step(ps[i], gs[i], ms[i] if mu else None, 0.01, mu, 1e-4)
+            assert rc == 0
+        for i in range(len(sizes)):
+            assert_bits(pd[i].numpy(), ps[i], f"{kind} p[{i}]")
