@@ -195,6 +195,46 @@ def bench_c4(ctx, steps, warmup):
     return {"ms_per_step": per * 1e3, "tflops": (fwd + bwd) / per / 1e12, "loss": loss.item()}
 
 
+def c5_flops(B=64, T=128, I=64, H=256):
+    """Forward GEMM flops of the 2-layer LSTM (input and recurrent products;
+    the 256->1 head is negligible); BPTT is twice that."""
+    fwd = 2 * B * T * 4 * H * (I + H) + 2 * B * T * 4 * H * (H + H)
+    return fwd, 2 * fwd
+
+
+def bench_c5(ctx, steps, warmup):
+    """2-layer LSTM forecaster (in 64, hidden 256, seq 128,
+    batch 64, Linear 256->1 head on the last step, MSE) -- forward, BPTT and
+    SGD step through the device autograd engine."""
+    import numrs_amd as nr
+    from numrs_amd import Tensor, nn, optim
+    from tests.lstm_oracle import make_c5
+
+    nr.set_default_context(ctx)
+    layers, hw, hb, x, target = make_c5(seed=5)
+    model = nn.LSTMForecaster(layers, hw, hb)
+    opt = optim.SGD.simple(model.parameters(), 1e-3)
+    xt, tt = Tensor.new(x, False), Tensor.new(target, False)
+
+    def step():
+        loss = model.forward(xt).mse_loss(tt)
+        loss.backward()
+        opt.step()
+        opt.zero_grad()
+        return loss
+
+    for _ in range(warmup):
+        step().item()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    loss.item()
+    per = (time.perf_counter() - t0) / steps
+    fwd, bwd = c5_flops()
+    return {"ms_per_step": per * 1e3, "tflops": (fwd + bwd) / per / 1e12, "loss": loss.item()}
+
+
 def cpu_baseline(A, B, dC, rows_a: int, rows_b: int):
     """numrs's matmul_backward restated in C (single thread, fp32 triple
     loops of backward.rs:123-146), timed on this host over a bounded sample
@@ -232,7 +272,7 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-rows-a", type=int, default=512)
     ap.add_argument("--cpu-rows-b", type=int, default=192)
-    ap.add_argument("--only", choices=["c1", "c4"], default=None,
+    ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
     args = ap.parse_args()
 
@@ -253,7 +293,8 @@ def main() -> int:
 
     if args.only is not None:
         fn = {"c1": lambda: bench_c1(ctx, args.steps, args.warmup),
-              "c4": lambda: bench_c4(ctx, args.steps, args.warmup)}[args.only]
+              "c4": lambda: bench_c4(ctx, args.steps, args.warmup),
+              "c5": lambda: bench_c5(ctx, args.steps, args.warmup)}[args.only]
         res = fn()
         print(json.dumps({"workload": args.only, **res}), flush=True)
         ctx.close()
@@ -308,6 +349,15 @@ def main() -> int:
                           "bound": "mfma (GEMMs) + hbm (LN/GELU/softmax)",
                           "final_loss": round(c4["loss"], 6)})
         log(f"  C4 block step {c4['ms_per_step']:.3f} ms {c4['tflops']:.1f} TFLOP/s")
+        c5 = bench_c5(ctx, max(3, args.steps // 10), 1)
+        secondary.append({"workload": "C5 2-layer LSTM forecaster train step (in 64, hidden 256, "
+                                      "seq 128, batch 64, head 256->1, MSE, SGD) via the device "
+                                      "engine",
+                          "value": round(c5["ms_per_step"], 3), "unit": "ms/step",
+                          "tflops_over_step": round(c5["tflops"], 2),
+                          "bound": "latency (256 sequential step kernels per direction)",
+                          "final_loss": round(c5["loss"], 6)})
+        log(f"  C5 LSTM step {c5['ms_per_step']:.3f} ms {c5['tflops']:.2f} TFLOP/s")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -198,6 +198,29 @@ int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float
                                  float *dk, float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
                                  int accumulate);
 
+/* LSTM layer (no reference op), gate order i, f, g, o:
+ * x [B, T, I], W_ih [4H, I], W_hh [4H, H], b [4H] (NULL = 0), h0/c0 [B, H]
+ * (NULL = 0).  Forward writes h_seq, c_seq [B, T, H] and the gate
+ * activations acts [B, T, 4H] the backward needs.  Backward (BPTT) from
+ * dh_seq [B, T, H] (NULL = 0): dx [B, T, I], dW_ih, dW_hh, db (any may be
+ * NULL; one accumulate flag each); the weight gradients are single products
+ * over all steps. */
+int numrs_hip_lstm_forward(numrs_hip_ctx *ctx, const float *x, const float *w_ih,
+                           const float *w_hh, const float *b, const float *h0, const float *c0,
+                           float *h_seq, float *c_seq, float *acts, int64_t B, int64_t T,
+                           int64_t I, int64_t H);
+int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_ih,
+                            const float *w_hh, const float *h0, const float *c0,
+                            const float *h_seq, const float *c_seq, const float *acts,
+                            const float *dh_seq, float *dx, float *dw_ih, float *dw_hh, float *db,
+                            int64_t B, int64_t T, int64_t I, int64_t H, int acc_dx, int acc_dw_ih,
+                            int acc_dw_hh, int acc_db);
+/* y[b, :] = x[b, t, :] for x [B, T, D] (backward = 0), or its backward
+ * y[b, t, :] (+)= x[b, :] over a [B, T, D] gradient, zero elsewhere when not
+ * accumulating (backward = 1). */
+int numrs_hip_time_slice(numrs_hip_ctx *ctx, const float *x, float *y, int64_t B, int64_t T,
+                         int64_t D, int64_t t, int backward, int accumulate);
+
 /* ---------------------------------------------------------------------- */
 /* Broadcast-reduce gradients                                              */
 /* ---------------------------------------------------------------------- */
@@ -407,6 +430,11 @@ int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
  * one node with Linear::forward's values and gradients (nn.rs:217-235). */
 int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
                             numrs_hip_tensor **out);
+/* LSTM layer node: x [B, T, I] -> h_seq [B, T, H] (numrs_hip_lstm_forward). */
+int numrs_hip_tensor_lstm(numrs_hip_tensor *x, numrs_hip_tensor *w_ih, numrs_hip_tensor *w_hh,
+                          numrs_hip_tensor *b, numrs_hip_tensor **out);
+/* Time-step slice node: x [B, T, D] -> x[:, t, :] [B, D]. */
+int numrs_hip_tensor_time_slice(numrs_hip_tensor *x, int64_t t, numrs_hip_tensor **out);
 /* Multi-head attention node over q, k, v [B*S, D] (numrs_hip_attention_forward). */
 int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
                                int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out);

@@ -69,6 +69,9 @@ SIGNATURES = {
     "numrs_hip_softmax_forward": (_i, [_vp, _vp, _vp, _i64, _i64, _f]),
     "numrs_hip_layernorm_forward": (_i, [_vp] * 7 + [_i64, _i64, _f]),
     "numrs_hip_layernorm_backward": (_i, [_vp] * 9 + [_i64, _i64, _i, _i, _i]),
+    "numrs_hip_lstm_forward": (_i, [_vp] * 10 + [_i64] * 4),
+    "numrs_hip_lstm_backward": (_i, [_vp] * 14 + [_i64] * 4 + [_i] * 4),
+    "numrs_hip_time_slice": (_i, [_vp] * 3 + [_i64] * 4 + [_i, _i]),
     "numrs_hip_attention_forward": (_i, [_vp] * 6 + [_i64] * 4),
     "numrs_hip_attention_backward": (_i, [_vp] * 9 + [_i64] * 4 + [_i]),
     # tensor engine
@@ -100,6 +103,8 @@ SIGNATURES = {
     "numrs_hip_tensor_softmax": (_i, [_vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_layer_norm": (_i, [_vp, _vp, _vp, _f, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_linear": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_lstm": (_i, [_vp] * 4 + [ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_time_slice": (_i, [_vp, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_attention": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_optim_sgd": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, ctypes.POINTER(_vp)]),
     "numrs_hip_optim_adam": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, _f, _f,

@@ -279,6 +279,18 @@ class Tensor:
                                                           bias._h if bias is not None else None,
                                                           ctypes.byref(h)), h)
 
+    def lstm(self, w_ih: "Tensor", w_hh: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
+        """LSTM layer over self [B, T, I] -> hidden states [B, T, H]."""
+        h = ctypes.c_void_p()
+        return self._out(L.load().numrs_hip_tensor_lstm(self._h, w_ih._h, w_hh._h,
+                                                        bias._h if bias is not None else None,
+                                                        ctypes.byref(h)), h)
+
+    def time_slice(self, t: int) -> "Tensor":
+        """self[:, t, :] of a [B, T, D] tensor."""
+        h = ctypes.c_void_p()
+        return self._out(L.load().numrs_hip_tensor_time_slice(self._h, int(t), ctypes.byref(h)), h)
+
     def attention(self, k: "Tensor", v: "Tensor", batch: int, seq: int, heads: int) -> "Tensor":
         """Multi-head attention with self as q; q, k, v are [batch*seq, dim]."""
         h = ctypes.c_void_p()

@@ -38,7 +38,7 @@ thread_local bool g_grad_enabled = true;  // mod.rs:194-206
 
 enum class Op {
   Leaf, Add, Sub, Mul, Div, MatMul, Transpose, Unary, Sum, Mean, MSE, CrossEntropy,
-  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention, Linear
+  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention, Linear, LSTM, TimeSlice
 };
 
 struct Storage {
@@ -482,6 +482,35 @@ int bw_linear(const T &out, const float *g, Node &n) {
   return NUMRS_HIP_OK;
 }
 
+int bw_lstm(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0], &wih = n.inputs[1], &whh = n.inputs[2];
+  const T *b = n.inputs.size() > 3 ? &n.inputs[3] : nullptr;
+  const int64_t B = x->shape[0], Tn = x->shape[1], I = x->shape[2], H = whh->shape[1];
+  float *dx = nullptr, *dwi = nullptr, *dwh = nullptr, *db = nullptr;
+  int ax = 0, awi = 0, awh = 0, ab = 0;
+  if (x->requires_grad)
+    if (int rc = grad_target(x, &dx, &ax)) return rc;
+  if (wih->requires_grad)
+    if (int rc = grad_target(wih, &dwi, &awi)) return rc;
+  if (whh->requires_grad && whh->grad != wih->grad)
+    if (int rc = grad_target(whh, &dwh, &awh)) return rc;
+  if (b && (*b)->requires_grad)
+    if (int rc = grad_target(*b, &db, &ab)) return rc;
+  return numrs_hip_lstm_backward(out->ctx, x->data->ptr, wih->data->ptr, whh->data->ptr, nullptr,
+                                 nullptr, out->data->ptr, n.saved[1]->ptr, n.saved[0]->ptr, g, dx,
+                                 dwi, dwh, db, B, Tn, I, H, ax, awi, awh, ab);
+}
+
+int bw_time_slice(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  return numrs_hip_time_slice(out->ctx, g, dst, x->shape[0], x->shape[1], x->shape[2], n.dims[0],
+                              1, acc);
+}
+
 int run_backward_fn(const T &out) {
   Node &n = *out->node;
   const float *g = out->grad->buf->ptr;
@@ -503,6 +532,8 @@ int run_backward_fn(const T &out) {
     case Op::LayerNorm: return bw_layernorm(out, g, n);
     case Op::Attention: return bw_attention(out, g, n);
     case Op::Linear: return bw_linear(out, g, n);
+    case Op::LSTM: return bw_lstm(out, g, n);
+    case Op::TimeSlice: return bw_time_slice(out, g, n);
     case Op::Leaf: return NUMRS_HIP_OK;
   }
   return NUMRS_HIP_OK;
@@ -758,6 +789,51 @@ int op_linear(const T &x, const T &W, const T *b, T *out) {
     std::vector<T> ins{x, W};
     if (b) ins.push_back(*b);
     attach(r, Op::Linear, std::move(ins));
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_lstm(const T &x, const T &wih, const T &whh, const T *b, T *out) {
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.size() != 3 || wih->shape.size() != 2 || whh->shape.size() != 2)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "lstm expects x [B,T,I], W_ih [4H,I], W_hh [4H,H]");
+  const int64_t B = x->shape[0], Tn = x->shape[1], I = x->shape[2], H = whh->shape[1];
+  if (wih->shape[0] != 4 * H || wih->shape[1] != I || whh->shape[0] != 4 * H ||
+      (b && (*b)->numel() != 4 * H))
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "lstm: weight shapes do not match H = %lld", (long long)H);
+  const bool rec = b ? recording({&x, &wih, &whh, b}) : recording({&x, &wih, &whh});
+  T r;
+  if (int rc = make_tensor(ctx, {B, Tn, H}, rec, &r)) return rc;
+  Buf acts, cseq;
+  if (int rc = alloc_buf(ctx, B * Tn * 4 * H, sizeof(float), &acts)) return rc;
+  if (int rc = alloc_buf(ctx, B * Tn * H, sizeof(float), &cseq)) return rc;
+  if (int rc = numrs_hip_lstm_forward(ctx, x->data->ptr, wih->data->ptr, whh->data->ptr,
+                                      b ? (*b)->data->ptr : nullptr, nullptr, nullptr,
+                                      r->data->ptr, cseq->ptr, acts->ptr, B, Tn, I, H))
+    return rc;
+  if (rec) {
+    std::vector<T> ins{x, wih, whh};
+    if (b) ins.push_back(*b);
+    attach(r, Op::LSTM, std::move(ins), 0, 0.f, {acts, cseq});
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_time_slice(const T &x, int64_t t, T *out) {
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.size() != 3 || t < 0 || t >= x->shape[1])
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "time_slice expects [B,T,D] and 0 <= t < T");
+  const bool rec = recording({&x});
+  T r;
+  if (int rc = make_tensor(ctx, {x->shape[0], x->shape[2]}, rec, &r)) return rc;
+  if (int rc = numrs_hip_time_slice(ctx, x->data->ptr, r->data->ptr, x->shape[0], x->shape[1],
+                                    x->shape[2], t, 0, 0))
+    return rc;
+  if (rec) {
+    attach(r, Op::TimeSlice, {x});
+    r->node->dims[0] = t;
   }
   *out = std::move(r);
   return NUMRS_HIP_OK;
@@ -1058,6 +1134,22 @@ int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_
   if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_lstm(numrs_hip_tensor *x, numrs_hip_tensor *w_ih, numrs_hip_tensor *w_hh,
+                          numrs_hip_tensor *b, numrs_hip_tensor **out) {
+  if (x == nullptr || w_ih == nullptr || w_hh == nullptr || out == nullptr)
+    return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_lstm(x->t, w_ih->t, w_hh->t, b ? &b->t : nullptr, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_time_slice(numrs_hip_tensor *x, int64_t t, numrs_hip_tensor **out) {
+  if (x == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_time_slice(x->t, t, &r)) return rc;
   return wrap(std::move(r), out);
 }
 

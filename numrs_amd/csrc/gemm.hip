@@ -547,7 +547,22 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
   if (!has_a && !has_b) return NUMRS_HIP_OK;
   if (!has_a) return gemm_dispatch(ctx, gb, 1, false, false);
   if (!has_b) return gemm_dispatch(ctx, ga, 1, true, first_nt);
-  const int sa_ = plan_splits(ga, 1), sb_ = plan_splits(gb, 1);
+  // Joint split plan: the pair shares one grid, so only the product with
+  // fewer tiles (the weight gradient) is split, until the pair has ~256
+  // workgroups.
+  int sa_ = 1, sb_ = 1;
+  {
+    const int64_t ta0 = (int64_t)ga.tiles_p * ga.tiles_q, tb0 = (int64_t)gb.tiles_p * gb.tiles_q;
+    if (ta0 + tb0 < 256) {
+      const bool b_small = tb0 <= ta0;
+      const Gemm &sm = b_small ? gb : ga;
+      const int64_t t_small = b_small ? tb0 : ta0, t_other = b_small ? ta0 : tb0;
+      const int nk = (sm.R + kBR - 1) / kBR;
+      int64_t sp = (256 - t_other + t_small - 1) / t_small;
+      sp = std::max<int64_t>(1, std::min<int64_t>({sp, (int64_t)nk / 8, 32}));
+      (b_small ? sb_ : sa_) = (int)sp;
+    }
+  }
   if (sa_ > 1 || sb_ > 1) {
     const size_t na = sa_ > 1 ? (size_t)sa_ * ga.P * ga.Q : 0;
     const size_t nb = sb_ > 1 ? (size_t)sb_ * gb.P * gb.Q : 0;

@@ -181,3 +181,39 @@ class TransformerEncoderBlock(Module):
     def parameters(self) -> list[Tensor]:
         return (self.ln1.parameters() + self.attn.parameters() + self.ln2.parameters() +
                 self.ff1.parameters() + self.ff2.parameters())
+
+
+class LSTM(Module):
+    """One LSTM layer (gate order i, f, g, o) over x [B, T, I] -> [B, T, H]."""
+
+    def __init__(self, w_ih, w_hh, bias=None, ctx=None):
+        w_ih = np.asarray(w_ih, np.float32)
+        w_hh = np.asarray(w_hh, np.float32)
+        self.hidden = w_hh.shape[1]
+        self.w_ih = Tensor.new(w_ih, True, ctx=ctx)
+        self.w_hh = Tensor.new(w_hh, True, ctx=ctx)
+        b = np.zeros(4 * self.hidden, np.float32) if bias is None else bias
+        self.bias = Tensor.new(np.asarray(b, np.float32), True, ctx=ctx)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return x.lstm(self.w_ih, self.w_hh, self.bias)
+
+    def parameters(self) -> list[Tensor]:
+        return [self.w_ih, self.w_hh, self.bias]
+
+
+class LSTMForecaster(Module):
+    """Stacked LSTM layers and a Linear head on the last step's hidden state."""
+
+    def __init__(self, layers: list[dict], head_w, head_b, ctx=None):
+        self.layers = [LSTM(l["w_ih"], l["w_hh"], l.get("b"), ctx) for l in layers]
+        hw = np.asarray(head_w, np.float32)
+        self.head = Linear.with_weights(hw.shape[1], hw.shape[0], hw, head_b, ctx)
+
+    def forward(self, x: Tensor) -> Tensor:
+        for layer in self.layers:
+            x = layer.forward(x)
+        return self.head(x.time_slice(x.shape()[1] - 1))
+
+    def parameters(self) -> list[Tensor]:
+        return [p for l in self.layers for p in l.parameters()] + self.head.parameters()

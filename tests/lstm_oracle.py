@@ -1,0 +1,112 @@
+"""C5 (2-layer LSTM forecaster) forward and BPTT in float64 numpy -- test
+infrastructure.  numrs has no recurrent layer, so this is the mathematics
+(gate order i, f, g, o, one bias per layer), pinned against torch float64
+autograd in tests/test_oracle_new_ops.py."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def _xavier(rng, fan_out, fan_in):
+    a = math.sqrt(6.0 / (fan_in + fan_out))
+    return rng.uniform(-a, a, (fan_out, fan_in)).astype(np.float32)
+
+
+def make_c5(seed=5, B=64, T=128, I=64, H=256, n_layers=2):
+    """BASELINE config 5 inputs: each feature is a sum of 3 sinusoids with
+    random phases plus N(0, 0.1) noise; Xavier-uniform weights, zero biases;
+    target ~ N(0, 1) per series (the head predicts one value per series)."""
+    rng = np.random.default_rng(seed)
+    t = np.arange(T, dtype=np.float64)
+    omega = rng.uniform(0.05, 0.5, 3)
+    phase = rng.uniform(0.0, 2 * math.pi, (B, I, 3))
+    x = np.sin(omega[None, None, None, :] * t[None, :, None, None] + phase[:, None, :, :]).sum(-1)
+    x = (x + rng.normal(0.0, 0.1, x.shape)).astype(np.float32)  # [B, T, I]
+    layers = []
+    fin = I
+    for _ in range(n_layers):
+        layers.append({"w_ih": _xavier(rng, 4 * H, fin), "w_hh": _xavier(rng, 4 * H, H),
+                       "b": np.zeros(4 * H, np.float32)})
+        fin = H
+    head_w = _xavier(rng, 1, H)
+    head_b = np.zeros(1, np.float32)
+    target = rng.standard_normal((B, 1)).astype(np.float32)
+    return layers, head_w, head_b, x, target
+
+
+def _sig(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def lstm_layer(x, w_ih, w_hh, b):
+    """x [B, T, I] float64 -> (h_seq, cache)."""
+    B, T, _ = x.shape
+    H = w_hh.shape[1]
+    h = np.zeros((B, H))
+    c = np.zeros((B, H))
+    hs, cs, acts = [], [], []
+    for t in range(T):
+        z = x[:, t] @ w_ih.T + h @ w_hh.T + b
+        i, f, g, o = _sig(z[:, :H]), _sig(z[:, H:2 * H]), np.tanh(z[:, 2 * H:3 * H]), _sig(z[:, 3 * H:])
+        c = f * c + i * g
+        h = o * np.tanh(c)
+        hs.append(h)
+        cs.append(c)
+        acts.append((i, f, g, o))
+    return np.stack(hs, 1), (np.stack(cs, 1), acts)
+
+
+def lstm_layer_backward(x, w_ih, w_hh, h_seq, cache, dh_seq):
+    B, T, _ = x.shape
+    H = w_hh.shape[1]
+    c_seq, acts = cache
+    dx = np.zeros_like(x)
+    dwi, dwh, db = np.zeros_like(w_ih), np.zeros_like(w_hh), np.zeros(4 * H)
+    dh_next = np.zeros((B, H))
+    dc_next = np.zeros((B, H))
+    for t in range(T - 1, -1, -1):
+        i, f, g, o = acts[t]
+        c = c_seq[:, t]
+        cp = c_seq[:, t - 1] if t > 0 else np.zeros((B, H))
+        hp = h_seq[:, t - 1] if t > 0 else np.zeros((B, H))
+        dh = dh_seq[:, t] + dh_next
+        tc = np.tanh(c)
+        dc = dh * o * (1 - tc ** 2) + dc_next
+        dz = np.concatenate([dc * g * i * (1 - i), dc * cp * f * (1 - f), dc * i * (1 - g ** 2),
+                             dh * tc * o * (1 - o)], 1)
+        dwi += dz.T @ x[:, t]
+        dwh += dz.T @ hp
+        db += dz.sum(0)
+        dx[:, t] = dz @ w_ih
+        dh_next = dz @ w_hh
+        dc_next = dc * f
+    return dx, dwi, dwh, db
+
+
+def forecaster(layers, head_w, head_b, x, target):
+    """Loss and float64 gradients of every parameter (and of x)."""
+    h = x.astype(np.float64)
+    ins, outs, caches = [], [], []
+    for l in layers:
+        w = {k: v.astype(np.float64) for k, v in l.items()}
+        ins.append(h)
+        h, cache = lstm_layer(h, w["w_ih"], w["w_hh"], w["b"])
+        outs.append(h)
+        caches.append((w, cache))
+    last = h[:, -1]
+    y = last @ head_w.astype(np.float64).T + head_b
+    n = y.size
+    loss = ((y - target) ** 2).sum() / n
+    dy = 2 * (y - target) / n
+    grads = {"head_w": dy.T @ last, "head_b": dy.sum(0)}
+    dh = np.zeros_like(h)
+    dh[:, -1] = dy @ head_w.astype(np.float64)
+    for li in range(len(layers) - 1, -1, -1):
+        w, cache = caches[li]
+        dxl, dwi, dwh, db = lstm_layer_backward(ins[li], w["w_ih"], w["w_hh"], outs[li], cache, dh)
+        grads[f"w_ih{li}"], grads[f"w_hh{li}"], grads[f"b{li}"] = dwi, dwh, db
+        dh = dxl
+    grads["x"] = dh
+    return loss, grads, y

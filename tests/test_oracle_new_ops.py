@@ -50,3 +50,35 @@ def test_transformer_block_oracle_matches_torch_autograd():
                          ("c2", extra["c2"])):
         np.testing.assert_allclose(g[ours], theirs.grad.numpy(), rtol=1e-9, atol=1e-12,
                                    err_msg=ours)
+
+
+def test_lstm_forecaster_oracle_matches_torch_autograd():
+    from tests import lstm_oracle as LO
+
+    layers, hw, hb, x, target = LO.make_c5(seed=3, B=3, T=6, I=4, H=5, n_layers=2)
+    loss, g, _ = LO.forecaster(layers, hw, hb, x, target)
+
+    lstm = torch.nn.LSTM(4, 5, num_layers=2, batch_first=True).double()
+    with torch.no_grad():
+        for li, l in enumerate(layers):
+            getattr(lstm, f"weight_ih_l{li}").copy_(torch.tensor(l["w_ih"], dtype=torch.float64))
+            getattr(lstm, f"weight_hh_l{li}").copy_(torch.tensor(l["w_hh"], dtype=torch.float64))
+            getattr(lstm, f"bias_ih_l{li}").copy_(torch.tensor(l["b"], dtype=torch.float64))
+            getattr(lstm, f"bias_hh_l{li}").zero_()
+    tx = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    thw = torch.tensor(hw, dtype=torch.float64, requires_grad=True)
+    thb = torch.tensor(hb, dtype=torch.float64, requires_grad=True)
+    out, _ = lstm(tx)
+    y = out[:, -1] @ thw.T + thb
+    tl = ((y - torch.tensor(target, dtype=torch.float64)) ** 2).mean()
+    tl.backward()
+    assert abs(loss - tl.item()) < 1e-12
+    for li in range(2):
+        np.testing.assert_allclose(g[f"w_ih{li}"], getattr(lstm, f"weight_ih_l{li}").grad.numpy(),
+                                   rtol=1e-9, atol=1e-13)
+        np.testing.assert_allclose(g[f"w_hh{li}"], getattr(lstm, f"weight_hh_l{li}").grad.numpy(),
+                                   rtol=1e-9, atol=1e-13)
+        np.testing.assert_allclose(g[f"b{li}"], getattr(lstm, f"bias_ih_l{li}").grad.numpy(),
+                                   rtol=1e-9, atol=1e-13)
+    np.testing.assert_allclose(g["head_w"], thw.grad.numpy(), rtol=1e-9, atol=1e-13)
+    np.testing.assert_allclose(g["x"], tx.grad.numpy(), rtol=1e-9, atol=1e-13)
