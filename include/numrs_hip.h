@@ -185,7 +185,7 @@ int numrs_hip_gemm(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float 
                    int64_t sa_outer, int64_t sa_inner, int64_t sb_outer, int64_t sb_inner,
                    int64_t sc_outer, int64_t sc_inner);
 
-/* Multi-head attention (no reference op; SURVEY N3).  q, k, v, out are
+/* Multi-head attention (no reference op).  q, k, v, out are
  * [B*S, D] row-major with head h of token (b, s) in columns [h*D/H, (h+1)*D/H).
  * Forward: P = softmax(Q K^T / sqrt(D/H)) per (b, h) into P [B*H, S, S],
  * out = P V.  Backward from the saved P: dV = P^T dO, dS = softmax_backward(P,
@@ -198,7 +198,7 @@ int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float
                                  float *dk, float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
                                  int accumulate);
 
-/* LSTM layer (no reference op; SURVEY N4), gate order i, f, g, o:
+/* LSTM layer (no reference op), gate order i, f, g, o:
  * x [B, T, I], W_ih [4H, I], W_hh [4H, H], b [4H] (NULL = 0), h0/c0 [B, H]
  * (NULL = 0).  Forward writes h_seq, c_seq [B, T, H] and the gate
  * activations acts [B, T, 4H] the backward needs.  Backward (BPTT) from

@@ -16,132 +16,282 @@
 //   all steps as single products: dW_ih = dG^T x, dW_hh = dG^T H_prev
 //   (H_prev = h shifted one step), db = column sum of dG, dx = dG W_ih.
 //
-// Step kernels: one wave per (64 hidden units, kBatchPerLane batch rows).
-// Lane j owns hidden unit j of those rows for every step, so the cell state
-// it carries (c, dc) is only ever touched by that lane.  The recurrent
-// product reads the weight row segment with coalesced vector loads and the
-// h / dG value of the row, identical across the wave, once per k.
+// Step kernels: one 1024-thread block per (64 hidden units, kRows batch
+// rows).  The step is latency-bound (a few MiB of L2-resident reads), so the
+// recurrent reduction is cut into 16 slices, one per wave; the block's h (or
+// dG) rows are staged in LDS once, W_hh is packed so a lane's four gate
+// weights for one reduction index are one 16-byte load, and each lane issues
+// the weight loads of kChunk indices before their FMAs, carrying all kRows
+// rows of its hidden unit.  The slices meet in LDS in a fixed order, and wave
+// u < kRows finishes row b0 + u, so the cell state of (b, j) (c, dc) is always
+// touched by the same thread.
 #include <cmath>
 
 #include "common.h"
 
 namespace {
 
-constexpr int kBatchPerLane = 2;
+constexpr int kRows = 4;    // batch rows carried by each lane
+constexpr int kWaves = 16;  // the recurrent reduction is split across the block's waves
+constexpr int kThreads = 64 * kWaves;
+// reduction indices whose weight loads are issued together (sized to stay
+// within the 128 VGPRs a 1024-thread block allows)
+template <bool STAGE, bool FWD>
+constexpr int chunk() { return STAGE ? (FWD ? 16 : 12) : (FWD ? 6 : 3); }
+constexpr int kFwdStageH = 2048;  // largest H whose h rows the forward stages in LDS
+constexpr int kBwdStageH = 1024;  // largest H whose dG rows the backward stages in LDS
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Forward step t.  whhT is W_hh^T [H, 4H]; G holds x W_ih^T + b on entry and
-// the activations on exit (in place: each lane reads its four values first).
-__global__ void __launch_bounds__(64)
-    lstm_fwd_step(float *G, const float *__restrict__ whhT, const float *__restrict__ h0,
-                  const float *__restrict__ c0, float *__restrict__ h_seq,
-                  float *__restrict__ c_seq, int B, int T, int H, int t) {
-  const int jblocks = (H + 63) / 64;
-  const int jb = blockIdx.x % jblocks, bp = blockIdx.x / jblocks;
-  const int j = jb * 64 + threadIdx.x;
-  const int b0 = bp * kBatchPerLane;
-  const int H4 = 4 * H;
-  float acc[kBatchPerLane][4];
-#pragma unroll
-  for (int u = 0; u < kBatchPerLane; ++u)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) acc[u][g] = 0.0f;
-  const bool have_prev = t > 0 || h0 != nullptr;
-  if (have_prev && j < H) {
-    const float *hp[kBatchPerLane];
-#pragma unroll
-    for (int u = 0; u < kBatchPerLane; ++u) {
-      const int b = min(b0 + u, B - 1);
-      hp[u] = t > 0 ? h_seq + ((int64_t)b * T + t - 1) * H : h0 + (int64_t)b * H;
-    }
-    for (int k = 0; k < H; ++k) {
-      const float *wrow = whhT + (int64_t)k * H4 + j;
-      const float w0 = wrow[0], w1 = wrow[H], w2 = wrow[2 * H], w3 = wrow[3 * H];
-#pragma unroll
-      for (int u = 0; u < kBatchPerLane; ++u) {
-        const float hv = hp[u][k];
-        acc[u][0] += hv * w0;
-        acc[u][1] += hv * w1;
-        acc[u][2] += hv * w2;
-        acc[u][3] += hv * w3;
-      }
-    }
-  }
-  if (j >= H) return;
-#pragma unroll
-  for (int u = 0; u < kBatchPerLane; ++u) {
-    const int b = b0 + u;
-    if (b >= B) break;
-    const int64_t gb = ((int64_t)b * T + t) * H4;
-    const float i = sigm(G[gb + j] + acc[u][0]);
-    const float f = sigm(G[gb + H + j] + acc[u][1]);
-    const float g = tanhf(G[gb + 2 * H + j] + acc[u][2]);
-    const float o = sigm(G[gb + 3 * H + j] + acc[u][3]);
-    const float cp = t > 0 ? c_seq[((int64_t)b * T + t - 1) * H + j]
-                           : (c0 != nullptr ? c0[(int64_t)b * H + j] : 0.0f);
-    const float c = f * cp + i * g;
-    const float h = o * tanhf(c);
-    G[gb + j] = i;
-    G[gb + H + j] = f;
-    G[gb + 2 * H + j] = g;
-    G[gb + 3 * H + j] = o;
-    c_seq[((int64_t)b * T + t) * H + j] = c;
-    h_seq[((int64_t)b * T + t) * H + j] = h;
-  }
+// Packed recurrent weights: P[(k * H + j) * 4 + g] = in[g * sg + k * sk + j],
+// so the four gate weights a lane needs for reduction index k are one 16-byte
+// load.  Forward: in = W_hh^T [H, 4H] (sg = H, sk = 4H), P[k, j, g] =
+// W_hh[gH + j, k].  Backward: in = W_hh [4H, H] (sg = H*H, sk = H), P[k, j, g]
+// = W_hh[gH + k, j].
+__global__ void __launch_bounds__(256)
+    pack_gates(const float *__restrict__ in, float *__restrict__ out, int H, int64_t sg,
+               int64_t sk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (g, k, j), j fastest
+  const int64_t n = (int64_t)4 * H * H;
+  if (i >= n) return;
+  const int64_t j = i % H, k = (i / H) % H, g = i / ((int64_t)H * H);
+  out[(k * H + j) * 4 + g] = in[g * sg + k * sk + j];
 }
 
-// Backward step t.  whh is W_hh [4H, H]; dG rows t+1 are complete (previous
-// launch); dc holds dc_{t+1} * f_{t+1} on entry and dc_t * f_t on exit.
-__global__ void __launch_bounds__(64)
-    lstm_bwd_step(float *__restrict__ dG, const float *__restrict__ whh,
+// Forward step t.  wp is the forward packing of W_hh; G holds x W_ih^T + b on
+// entry and the activations on exit (in place: each thread reads its four
+// values first).  Block = 16 waves for 64 hidden units x kRows batch rows:
+// wave w forms the partial products over k in its sixteenth of [0, H), LDS
+// holds the partials, which are added in wave order, and the first kRows
+// waves finish the cells.  The epilogue's inputs, the first weight chunk and
+// the staging of the block's h_{t-1} rows in LDS (STAGE) are all issued
+// before the first wait, so their memory latencies overlap.
+template <bool STAGE>
+__global__ void __launch_bounds__(kThreads)
+    lstm_fwd_step(float *G, const float4 *__restrict__ wp, const float *__restrict__ h0,
+                  const float *__restrict__ c0, float *__restrict__ h_seq,
+                  float *__restrict__ c_seq, int B, int T, int H, int t) {
+  __shared__ float part[kWaves][kRows * 4][64];
+  __shared__ float hs[STAGE ? kRows * kFwdStageH : 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int jblocks = (H + 63) / 64;
+  const int jb = blockIdx.x % jblocks, bp = blockIdx.x / jblocks;
+  const int j = jb * 64 + lane;
+  const int b0 = bp * kRows;
+  const int H4 = 4 * H;
+  const bool has_h = t > 0 || h0 != nullptr;
+
+  // epilogue inputs of cell (b0 + wave, j)
+  const int be = b0 + wave;
+  const bool epi = wave < kRows && be < B && j < H;
+  const int64_t gb = ((int64_t)be * T + t) * H4;
+  float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f}, cp = 0.0f;
+  if (epi) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) gin[g] = G[gb + g * H + j];
+    cp = t > 0 ? c_seq[((int64_t)be * T + t - 1) * H + j]
+               : (c0 != nullptr ? c0[(int64_t)be * H + j] : 0.0f);
+  }
+
+  const float *hp[kRows];
+#pragma unroll
+  for (int u = 0; u < kRows; ++u) {
+    const int b = min(b0 + u, B - 1);
+    hp[u] = t > 0 ? h_seq + ((int64_t)b * T + t - 1) * H : h0 + (int64_t)b * H;
+  }
+  const bool work = has_h && j < H;
+  const int kc = (H + kWaves - 1) / kWaves;
+  const int k0 = wave * kc, k1 = min(H, k0 + kc);
+  constexpr int kChunk = chunk<STAGE, true>();
+  float4 w[kChunk];
+  int k = k0;
+  bool full = work && k + kChunk <= k1;
+  if (full) {
+#pragma unroll
+    for (int s = 0; s < kChunk; ++s) w[s] = wp[(int64_t)(k + s) * H + j];
+  }
+  if (STAGE && has_h) {
+    for (int i = threadIdx.x; i < kRows * H; i += kThreads) {
+      const int u = i / H;
+      hs[i] = hp[u][i - u * H];
+    }
+    __syncthreads();
+  }
+  float acc[kRows][4];
+#pragma unroll
+  for (int u = 0; u < kRows; ++u)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) acc[u][g] = 0.0f;
+  if (work) {
+    auto step = [&](int kk, const float4 &wv) {
+#pragma unroll
+      for (int u = 0; u < kRows; ++u) {
+        const float hv = STAGE ? hs[u * H + kk] : hp[u][kk];
+        acc[u][0] += hv * wv.x;
+        acc[u][1] += hv * wv.y;
+        acc[u][2] += hv * wv.z;
+        acc[u][3] += hv * wv.w;
+      }
+    };
+    if (full) {  // the prefetched chunk
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) step(k + s, w[s]);
+      k += kChunk;
+    }
+    for (; k + kChunk <= k1; k += kChunk) {
+      float4 wn[kChunk];
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) wn[s] = wp[(int64_t)(k + s) * H + j];
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) step(k + s, wn[s]);
+    }
+    for (; k < k1; ++k) step(k, wp[(int64_t)k * H + j]);
+  }
+#pragma unroll
+  for (int u = 0; u < kRows; ++u)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) part[wave][u * 4 + g][lane] = acc[u][g];
+  __syncthreads();
+  // thread (wave, lane) adds the kWaves partials of column `wave` (row u =
+  // wave / 4, gate wave % 4) in wave order; it alone reads and rewrites it
+  {
+    float sum = part[0][wave][lane];
+#pragma unroll
+    for (int v = 1; v < kWaves; ++v) sum += part[v][wave][lane];
+    part[0][wave][lane] = sum;
+  }
+  __syncthreads();
+  if (!epi) return;
+  const int u = wave;
+  const float i = sigm(gin[0] + part[0][u * 4 + 0][lane]);
+  const float f = sigm(gin[1] + part[0][u * 4 + 1][lane]);
+  const float g = tanhf(gin[2] + part[0][u * 4 + 2][lane]);
+  const float o = sigm(gin[3] + part[0][u * 4 + 3][lane]);
+  const float c = f * cp + i * g;
+  const float h = o * tanhf(c);
+  G[gb + j] = i;
+  G[gb + H + j] = f;
+  G[gb + 2 * H + j] = g;
+  G[gb + 3 * H + j] = o;
+  c_seq[((int64_t)be * T + t) * H + j] = c;
+  h_seq[((int64_t)be * T + t) * H + j] = h;
+}
+
+// Backward step t.  wp is the backward packing of W_hh; dG rows t+1 are
+// complete (previous launch); dc holds dc_{t+1} * f_{t+1} on entry and
+// dc_t * f_t on exit, and each (b, j) is always handled by the same thread.
+// The block stages its dG_{t+1} rows in LDS as [u][k][g] (STAGE), and wave w
+// reduces over k in its sixteenth of [0, H), all four gates per k:
+// dh[b, j] += sum_g dG[b, gH + k] W_hh[gH + k, j].  As in the forward, the
+// epilogue's inputs, the first weight chunk and the staging are issued
+// before the first wait.
+template <bool STAGE>
+__global__ void __launch_bounds__(kThreads)
+    lstm_bwd_step(float *__restrict__ dG, const float4 *__restrict__ wp,
                   const float *__restrict__ acts, const float *__restrict__ c_seq,
                   const float *__restrict__ c0, const float *__restrict__ dh_out,
                   float *__restrict__ dc, int B, int T, int H, int t) {
+  __shared__ float part[kWaves][kRows][64];
+  __shared__ float4 ds[STAGE ? kRows * kBwdStageH : 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int jblocks = (H + 63) / 64;
   const int jb = blockIdx.x % jblocks, bp = blockIdx.x / jblocks;
-  const int j = jb * 64 + threadIdx.x;
-  const int b0 = bp * kBatchPerLane;
+  const int j = jb * 64 + lane;
+  const int b0 = bp * kRows;
   const int H4 = 4 * H;
-  float rec[kBatchPerLane];
+  const bool has_next = t + 1 < T;
+
+  // epilogue inputs of cell (b0 + wave, j)
+  const int be = b0 + wave;
+  const bool epi = wave < kRows && be < B && j < H;
+  const int64_t row = (int64_t)be * T + t;
+  const int64_t gb = row * H4;
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, c = 0.0f, cp = 0.0f, dho = 0.0f, dcn = 0.0f;
+  if (epi) {
 #pragma unroll
-  for (int u = 0; u < kBatchPerLane; ++u) rec[u] = 0.0f;
-  if (t + 1 < T && j < H) {
-    const float *dn[kBatchPerLane];
-#pragma unroll
-    for (int u = 0; u < kBatchPerLane; ++u) {
-      const int b = min(b0 + u, B - 1);
-      dn[u] = dG + ((int64_t)b * T + t + 1) * H4;
-    }
-    for (int n = 0; n < H4; ++n) {
-      const float w = whh[(int64_t)n * H + j];
-#pragma unroll
-      for (int u = 0; u < kBatchPerLane; ++u) rec[u] += dn[u][n] * w;
-    }
+    for (int g = 0; g < 4; ++g) a[g] = acts[gb + g * H + j];
+    c = c_seq[row * H + j];
+    cp = t > 0 ? c_seq[(row - 1) * H + j] : (c0 != nullptr ? c0[(int64_t)be * H + j] : 0.0f);
+    if (dh_out != nullptr) dho = dh_out[row * H + j];
+    if (has_next) dcn = dc[(int64_t)be * H + j];
   }
-  if (j >= H) return;
+
+  const float *dn[kRows];
 #pragma unroll
-  for (int u = 0; u < kBatchPerLane; ++u) {
-    const int b = b0 + u;
-    if (b >= B) break;
-    const int64_t row = (int64_t)b * T + t;
-    const int64_t gb = row * H4;
-    const float dh = (dh_out != nullptr ? dh_out[row * H + j] : 0.0f) + rec[u];
-    const float i = acts[gb + j], f = acts[gb + H + j], g = acts[gb + 2 * H + j],
-                o = acts[gb + 3 * H + j];
-    const float c = c_seq[row * H + j];
-    const float tc = tanhf(c);
-    const float cp = t > 0 ? c_seq[(row - 1) * H + j]
-                           : (c0 != nullptr ? c0[(int64_t)b * H + j] : 0.0f);
-    const float dcn = t + 1 < T ? dc[(int64_t)b * H + j] : 0.0f;
-    const float dct = dh * o * (1.0f - tc * tc) + dcn;
-    dG[gb + j] = (dct * g) * i * (1.0f - i);
-    dG[gb + H + j] = (dct * cp) * f * (1.0f - f);
-    dG[gb + 2 * H + j] = (dct * i) * (1.0f - g * g);
-    dG[gb + 3 * H + j] = (dh * tc) * o * (1.0f - o);
-    dc[(int64_t)b * H + j] = dct * f;
+  for (int u = 0; u < kRows; ++u) {
+    const int b = min(b0 + u, B - 1);
+    dn[u] = dG + ((int64_t)b * T + t + 1) * H4;
   }
+  const bool work = has_next && j < H;
+  const int kc = (H + kWaves - 1) / kWaves;
+  const int k0 = wave * kc, k1 = min(H, k0 + kc);
+  constexpr int kChunk = chunk<STAGE, false>();
+  float4 w[kChunk];
+  int k = k0;
+  bool full = work && k + kChunk <= k1;
+  if (full) {
+#pragma unroll
+    for (int s = 0; s < kChunk; ++s) w[s] = wp[(int64_t)(k + s) * H + j];
+  }
+  if (STAGE && has_next) {
+    float *dsf = reinterpret_cast<float *>(ds);
+    for (int i = threadIdx.x; i < kRows * H4; i += kThreads) {
+      const int u = i / H4, n = i - u * H4;
+      const int g = n / H, kk = n - g * H;
+      dsf[(u * H + kk) * 4 + g] = dn[u][n];
+    }
+    __syncthreads();
+  }
+  float rec[kRows];
+#pragma unroll
+  for (int u = 0; u < kRows; ++u) rec[u] = 0.0f;
+  if (work) {
+    auto step = [&](int kk, const float4 &wv) {
+#pragma unroll
+      for (int u = 0; u < kRows; ++u) {
+        const float4 d = STAGE ? ds[u * H + kk]
+                               : make_float4(dn[u][kk], dn[u][H + kk], dn[u][2 * H + kk],
+                                             dn[u][3 * H + kk]);
+        rec[u] += d.x * wv.x;
+        rec[u] += d.y * wv.y;
+        rec[u] += d.z * wv.z;
+        rec[u] += d.w * wv.w;
+      }
+    };
+    if (full) {  // the prefetched chunk
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) step(k + s, w[s]);
+      k += kChunk;
+    }
+    for (; k + kChunk <= k1; k += kChunk) {
+      float4 wn[kChunk];
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) wn[s] = wp[(int64_t)(k + s) * H + j];
+#pragma unroll
+      for (int s = 0; s < kChunk; ++s) step(k + s, wn[s]);
+    }
+    for (; k < k1; ++k) step(k, wp[(int64_t)k * H + j]);
+  }
+#pragma unroll
+  for (int u = 0; u < kRows; ++u) part[wave][u][lane] = rec[u];
+  __syncthreads();
+  if (!epi) return;
+  const int u = wave;
+  float r = part[0][u][lane];
+#pragma unroll
+  for (int v = 1; v < kWaves; ++v) r += part[v][u][lane];
+  const float i = a[0], f = a[1], g = a[2], o = a[3];
+  const float dh = dho + r;
+  const float tc = tanhf(c);
+  const float dct = dh * o * (1.0f - tc * tc) + dcn;
+  dG[gb + j] = (dct * g) * i * (1.0f - i);
+  dG[gb + H + j] = (dct * cp) * f * (1.0f - f);
+  dG[gb + 2 * H + j] = (dct * i) * (1.0f - g * g);
+  dG[gb + 3 * H + j] = (dh * tc) * o * (1.0f - o);
+  dc[(int64_t)be * H + j] = dct * f;
 }
+
+static_assert(kRows * 4 == kWaves, "one LDS column of partials per wave");
 
 // H_prev[b, t] = h_seq[b, t-1] (t > 0), h0[b] or 0 (t = 0).
 __global__ void __launch_bounds__(256)
@@ -155,7 +305,7 @@ __global__ void __launch_bounds__(256)
 }
 
 unsigned step_grid(int B, int H) {
-  return (unsigned)(((H + 63) / 64) * ((B + kBatchPerLane - 1) / kBatchPerLane));
+  return (unsigned)(((H + 63) / 64) * ((B + kRows - 1) / kRows));
 }
 
 int check(numrs_hip_ctx *ctx, int64_t B, int64_t T, int64_t I, int64_t H) {
@@ -217,13 +367,22 @@ int numrs_hip_lstm_forward(numrs_hip_ctx *ctx, const float *x, const float *w_ih
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "lstm_forward: null pointer");
   // acts <- x W_ih^T + b for every (b, t) row
   if (int rc = numrs_hip_linear_forward(ctx, x, w_ih, b, acts, B * T, I, 4 * H)) return rc;
-  TempBlock whhT(ctx);
+  TempBlock whhT(ctx), wp(ctx);
   if (int rc = whhT.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
+  if (int rc = wp.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
   if (int rc = numrs_hip_transpose(ctx, w_hh, whhT.f(), 4 * H, H)) return rc;
+  pack_gates<<<grid_for(4 * H * H, 256), 256, 0, ctx->stream>>>(whhT.f(), wp.f(), (int)H, H,
+                                                                4 * H);
+  if (int rc = numrs_hip::check_launch(ctx, "pack_gates")) return rc;
   const unsigned grid = step_grid((int)B, (int)H);
+  const float4 *wp4 = reinterpret_cast<const float4 *>(wp.p);
   for (int64_t t = 0; t < T; ++t) {
-    lstm_fwd_step<<<grid, 64, 0, ctx->stream>>>(acts, whhT.f(), h0, c0, h_seq, c_seq, (int)B,
-                                                (int)T, (int)H, (int)t);
+    if (H <= kFwdStageH)
+      lstm_fwd_step<true><<<grid, kThreads, 0, ctx->stream>>>(acts, wp4, h0, c0, h_seq, c_seq,
+                                                              (int)B, (int)T, (int)H, (int)t);
+    else
+      lstm_fwd_step<false><<<grid, kThreads, 0, ctx->stream>>>(acts, wp4, h0, c0, h_seq, c_seq,
+                                                               (int)B, (int)T, (int)H, (int)t);
     if (int rc = numrs_hip::check_launch(ctx, "lstm_fwd_step")) return rc;
   }
   return NUMRS_HIP_OK;
@@ -243,13 +402,22 @@ int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_i
   TempBlock dG(ctx), dc(ctx);
   if (int rc = dG.alloc((size_t)(rows * H4) * sizeof(float))) return rc;
   if (int rc = dc.alloc((size_t)(B * H) * sizeof(float))) return rc;
+  TempBlock wp(ctx);
+  if (int rc = wp.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
+  pack_gates<<<grid_for(4 * H * H, 256), 256, 0, ctx->stream>>>(w_hh, wp.f(), (int)H, H * H, H);
+  if (int rc = numrs_hip::check_launch(ctx, "pack_gates")) return rc;
+  const float4 *wp4 = reinterpret_cast<const float4 *>(wp.p);
   const unsigned grid = step_grid((int)B, (int)H);
   for (int64_t t = T - 1; t >= 0; --t) {
-    lstm_bwd_step<<<grid, 64, 0, ctx->stream>>>(dG.f(), w_hh, acts, c_seq, c0, dh_seq, dc.f(),
-                                                (int)B, (int)T, (int)H, (int)t);
+    if (H <= kBwdStageH)
+      lstm_bwd_step<true><<<grid, kThreads, 0, ctx->stream>>>(
+          dG.f(), wp4, acts, c_seq, c0, dh_seq, dc.f(), (int)B, (int)T, (int)H, (int)t);
+    else
+      lstm_bwd_step<false><<<grid, kThreads, 0, ctx->stream>>>(
+          dG.f(), wp4, acts, c_seq, c0, dh_seq, dc.f(), (int)B, (int)T, (int)H, (int)t);
     if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step")) return rc;
   }
-  // Weight gradients over all steps at once (SURVEY N4: batched over time).
+  // Weight gradients over all steps at once (batched over time).
   if (dw_ih)  // dW_ih[4H, I] = dG^T x
     if (int rc = numrs_hip_gemm(ctx, dG.f(), H4, x, I, dw_ih, I, H4, rows, I, 1, 0, 1.0f,
                                 acc_dw_ih, 1, 1, 0, 0, 0, 0, 0, 0))

@@ -17,8 +17,10 @@ def _norm_rel(got, ref):
 
 @pytest.mark.parametrize("dims", [dict(B=3, T=6, I=4, H=5), dict(B=8, T=20, I=16, H=64),
                                   dict(B=5, T=9, I=70, H=130),
-                                  dict(B=64, T=128, I=64, H=256)],
-                         ids=["tiny", "medium", "ragged", "baseline"])
+                                  dict(B=64, T=128, I=64, H=256),
+                                  dict(B=3, T=4, I=8, H=1040), dict(B=2, T=3, I=8, H=2056)],
+                         ids=["tiny", "medium", "ragged", "baseline",
+                              "wide_unstaged_bwd", "wide_unstaged"])
 def test_lstm_forecaster_matches_oracle(hip_ctx, dims):
     print(f"[gpu] lstm forecaster {dims}", flush=True)
     nr.set_default_context(hip_ctx)
