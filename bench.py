@@ -78,6 +78,77 @@ def traffic_from_profile(name: str):
         return None
 
 
+COPY_PROBE_BYTES = 256 << 20  # calibration copy: reads and writes this many bytes
+
+
+def traffic_probe(ctx, rng, reps: int = 3) -> None:
+    """The launches the two counter runs (FETCH_SIZE, then WRITE_SIZE) measure:
+    `reps` device copies of COPY_PROBE_BYTES -- the calibration kernel, whose
+    true HBM traffic is known -- then `reps` 2048^3 matmul_backward launches."""
+    n = COPY_PROBE_BYTES // 4
+    src, dst = ctx.to_device(randn(rng, n)), ctx.empty(n)
+    for _ in range(reps):
+        ctx.copy(dst, src)
+    ctx.sync()
+    M = K = N = 2048
+    A_, B_, dC_ = (ctx.to_device(randn(rng, s)) for s in ((M, K), (K, N), (M, N)))
+    dA_, dB_ = ctx.empty((M, K)), ctx.empty((K, N))
+    for _ in range(reps):
+        ctx.matmul_backward(dC_, A_, B_, dA_, dB_)
+    ctx.sync()
+    log(f"traffic probe: {reps} copies of {COPY_PROBE_BYTES} B, {reps} matmul_backward 2048^3")
+
+
+def _pmc_per_dispatch(directory: str, counter: str) -> dict:
+    """Mean value of `counter` per dispatch, by kernel name, from a rocprofv3
+    --pmc -f csv output directory."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {directory}")
+    per = {}
+    for path in files:
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = (row["Kernel_Name"], row["Dispatch_Id"])
+                per[key] = per.get(key, 0.0) + float(row["Counter_Value"])
+    out = {}
+    for (name, _), v in per.items():
+        out.setdefault(name, []).append(v)
+    return {k: float(np.mean(v)) for k, v in out.items()}
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> dict:
+    """HBM bytes per matmul_backward launch: FETCH_SIZE and WRITE_SIZE (KiB
+    per dispatch), each scaled by the factor that maps the copy kernel's
+    reading of the same counter onto its known COPY_PROBE_BYTES."""
+    fetch = _pmc_per_dispatch(fetch_dir, "FETCH_SIZE")
+    write = _pmc_per_dispatch(write_dir, "WRITE_SIZE")
+
+    def pick(d, part):
+        keys = [k for k in d if part in k]
+        if len(keys) != 1:
+            raise KeyError(f"{part}: {keys}")
+        return d[keys[0]]
+
+    known_kib = COPY_PROBE_BYTES / 1024.0
+    f_copy, w_copy = pick(fetch, "copy_kernel"), pick(write, "copy_kernel")
+    f_mm, w_mm = pick(fetch, "matmul_backward_kernel"), pick(write, "matmul_backward_kernel")
+    ff, fw = known_kib / f_copy, known_kib / w_copy
+    traffic = (f_mm * ff + w_mm * fw) * 1024.0
+    algorithmic = 5 * 2048 * 2048 * 4  # read A, B, dC; write dA, dB
+    res = {"kernel": "matmul_backward_kernel", "workload": "C2 2048^3",
+           "fetch_kib_raw": f_mm, "write_kib_raw": w_mm,
+           "copy_fetch_kib_raw": f_copy, "copy_write_kib_raw": w_copy,
+           "copy_bytes": COPY_PROBE_BYTES, "fetch_factor": ff, "write_factor": fw,
+           "bytes_per_launch": traffic, "algorithmic_bytes": algorithmic,
+           "traffic_over_algorithmic": traffic / algorithmic}
+    return res
+
+
 def bench_matmul_backward(ctx, rng, M, K, N, steps, warmup):
     A, B, dC = randn(rng, (M, K)), randn(rng, (K, N)), randn(rng, (M, N))
     dA_, B_, dC_ = ctx.empty((M, K)), ctx.to_device(B), ctx.to_device(dC)
@@ -274,7 +345,21 @@ def main() -> int:
     ap.add_argument("--cpu-rows-b", type=int, default=192)
     ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the calibration copy and the 2048^3 matmul_backward "
+                         "(run under rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn the two --pmc outputs of --traffic-probe into "
+                         "profiles/matmul_backward_2048_traffic.json (no GPU needed)")
     args = ap.parse_args()
+
+    if args.traffic_summary:
+        res = traffic_summary(*args.traffic_summary)
+        with open(os.path.join(ROOT, "profiles", "matmul_backward_2048_traffic.json"), "w") as f:
+            json.dump(res, f, indent=1)
+            f.write("\n")
+        print(json.dumps(res), flush=True)
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has "
@@ -290,6 +375,11 @@ def main() -> int:
     n_cus, arch = ctx.info()
     log(f"device {arch}, {n_cus} CUs")
     rng = np.random.default_rng(SEED)
+
+    if args.traffic_probe:
+        traffic_probe(ctx, rng)
+        ctx.close()
+        return 0
 
     if args.only is not None:
         fn = {"c1": lambda: bench_c1(ctx, args.steps, args.warmup),

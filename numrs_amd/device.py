@@ -140,6 +140,13 @@ class Context:
         host = np.ascontiguousarray(host, dtype=dtype)
         return self.empty(host.shape, dtype).upload(host)
 
+    def copy(self, dst: DeviceArray, src: DeviceArray, nbytes: int | None = None) -> None:
+        """Device-to-device copy of nbytes (default: all of src) on the stream."""
+        n = src.nbytes if nbytes is None else int(nbytes)
+        if n > min(src.nbytes, dst.nbytes):
+            raise ValueError("copy larger than an operand")
+        self._check(L.load().numrs_hip_copy(self.handle, dst.ptr, src.ptr, n))
+
     def sync(self) -> None:
         self._check(L.load().numrs_hip_sync(self.handle))
 

@@ -353,6 +353,17 @@ def test_fill_grad_and_mse(hip_ctx, rng):
     assert got[0] == 0.0 and abs(got[2] + 1.333333) < 1e-5
 
 
+@pytest.mark.parametrize("n,off", [(1 << 20, 0), (12345, 0), (4099, 1), (3, 0)])
+def test_copy(hip_ctx, rng, n, off):
+    """numrs_hip_copy: the float4 kernel (aligned) and the fallback (offset views)."""
+    c = hip_ctx
+    x = rand(rng, n + off)
+    src, dst = c.to_device(x), c.zeros(n + off)
+    c.copy(dst.view(off, (n,)), src.view(off, (n,)))
+    got = dst.numpy()
+    assert_bits(got[off:], x[off:], "copy")
+    assert np.all(got[:off] == 0)
+
 # ---------------------------------------------------------------------------
 # Row-wise: softmax-CE, softmax backward, argmax
 # ---------------------------------------------------------------------------
