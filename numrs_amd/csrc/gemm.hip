@@ -36,6 +36,7 @@
 //     weight gradients X^T dY of Linear layers): each split writes a plain
 //     partial, splitk_reduce adds them in split order -- deterministic.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -318,6 +319,263 @@ __global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, G
     gemm_tile<false, false, VEC>(db, tile - tiles_a, blockIdx.y, smem);
 }
 
+// ---------------------------------------------------------------------------
+// Streamed large-tile path, for aligned products with at least one output
+// tile per CU (matmul_backward at 2048^2 and up).
+//   * Workgroup tile 256(P) x 128(Q), one workgroup per CU (one wave per
+//     SIMD); each wave owns 128 x 64 = 4 x 2 MFMA blocks, so every operand
+//     fragment read from LDS feeds more MFMAs than in the 128 x 128 path.
+//   * Operands go global -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging, no ds_write) into a three-stage ring of 48 KiB stages: the
+//     tile used at step kt was issued right after the barrier that ended
+//     step kt-3's reads, two tiles ahead.  One barrier per reduction tile.
+//   * A DMA instruction writes 1 KiB contiguously, so the LDS layouts are
+//     XOR-swizzled instead of padded: an R-contiguous tile is [p][32] with
+//     16-byte chunk c stored at c ^ ((p & 7) ^ ((p >> 3) & 1)); a
+//     P-contiguous tile is [32][EXT] with column bit 5 flipped on rows whose
+//     bit 2 is set.  Both keep the fragment reads free of bank conflicts.
+//   * Two-level accumulation with the MFMA partials added into the running
+//     totals every three reduction tiles (96 reduction steps).
+// Requires P % 256 == 0, Q % 128 == 0, R % 32 == 0 and vec_ok operands.
+// ---------------------------------------------------------------------------
+constexpr int kSP = 256, kSQ = 128;         // workgroup tile
+constexpr int kSStageX = kSP * kBR;         // floats per X stage (32 KiB)
+constexpr int kSStageY = kSQ * kBR;         // floats per Y stage (16 KiB)
+constexpr int kSDma = kSP / 32 + kSQ / 32;  // DMA instructions per wave per tile
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__shared__ __attribute__((aligned(1024))) float g_sx0[kSStageX];
+__shared__ __attribute__((aligned(1024))) float g_sy0[kSStageY];
+__shared__ __attribute__((aligned(1024))) float g_sx1[kSStageX];
+__shared__ __attribute__((aligned(1024))) float g_sy1[kSStageY];
+__shared__ __attribute__((aligned(1024))) float g_sx2[kSStageX];
+__shared__ __attribute__((aligned(1024))) float g_sy2[kSStageY];
+
+__device__ __forceinline__ int rc_swizzle(int p) { return (p & 7) ^ ((p >> 3) & 1); }
+
+// This wave's EXT/32 DMA instructions for one EXT x 32 operand tile (each
+// instruction: 64 lanes x 16 bytes = 1 KiB of LDS starting at lds + m*256).
+template <bool RC, int EXT>
+__device__ __forceinline__ void stream_issue(const float *__restrict__ base, int64_t ld, int p0,
+                                             int r0, float *lds, int wave, int lane) {
+  constexpr int kPerWave = EXT / 32;
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int m = wave * kPerWave + i;
+    const float *src;
+    if (RC) {  // 8 rows of 32 floats per instruction
+      const int p = 8 * m + (lane >> 3);
+      const int k = (lane & 7) ^ rc_swizzle(p);
+      src = base + (int64_t)(p0 + p) * ld + r0 + 4 * k;
+    } else {  // 1024 / (4 EXT) rows of EXT floats per instruction
+      constexpr int kChunks = EXT / 4;
+      const int r = m * (64 / kChunks) + lane / kChunks;
+      const int lc = (lane % kChunks) ^ (((r >> 2) & 1) << 3);
+      src = base + (int64_t)(r0 + r) * ld + p0 + 4 * lc;
+    }
+    __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)(lds + m * 256), 16, 0, 0);
+  }
+}
+
+// Fragment of MFMA group g (reduction indices 8g + 4h + j) for rows
+// pb + c of a swizzled tile; same lane contract as frag().
+template <bool RC, int EXT>
+__device__ __forceinline__ f4 stream_frag(const float *lds, int pb, int c, int h, int g) {
+  if (RC) {
+    const int p = pb + c;
+    const int cp = (2 * g + h) ^ rc_swizzle(p);
+    return *reinterpret_cast<const f4 *>(lds + p * 32 + cp * 4);
+  } else {
+    f4 f;
+    const int col = (pb + c) ^ (h << 5);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = lds[(8 * g + 4 * h + j) * EXT + col];
+    return f;
+  }
+}
+
+struct StreamFrags {
+  f4 a[4], b[2];
+};
+
+template <bool XRC, bool YRC>
+__device__ __forceinline__ void stream_read(StreamFrags &f, const float *xl, const float *yl,
+                                            int wp, int wq, int c, int h, int g) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f.a[i] = stream_frag<XRC, kSP>(xl, wp * 128 + 32 * i, c, h, g);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) f.b[j] = stream_frag<YRC, kSQ>(yl, wq * 64 + 32 * j, c, h, g);
+}
+
+template <bool XRC, bool YRC>
+__device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) {
+  const int per_group = kGroupRows * d.tiles_q;
+  const int gidx = tile / per_group;
+  const int first_p = gidx * kGroupRows;
+  const int rows_in_group = min(d.tiles_p - first_p, kGroupRows);
+  const int in_group = tile - gidx * per_group;
+  const int tp = first_p + in_group % rows_in_group;
+  const int tq = in_group / rows_in_group;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wp = wave >> 1, wq = wave & 1;
+  const int c = lane & 31, h = lane >> 5;
+  const int p0 = tp * kSP, q0 = tq * kSQ;
+
+  const int64_t zo = batch / d.binner, zi = batch - zo * d.binner;
+  const float *__restrict__ X = d.X + zo * d.bsx + zi * d.bsx2;
+  const float *__restrict__ Y = d.Y + zo * d.bsy + zi * d.bsy2;
+  float *__restrict__ C = d.C + zo * d.bsc + zi * d.bsc2;
+  const int nk = d.R / kBR;
+
+  // Prologue: tiles 0, 1, 2 into stages 0, 1, 2; wait for tile 0.
+  stream_issue<XRC, kSP>(X, d.ldx, p0, 0, g_sx0, wave, lane);
+  stream_issue<YRC, kSQ>(Y, d.ldy, q0, 0, g_sy0, wave, lane);
+  if (nk > 1) {
+    stream_issue<XRC, kSP>(X, d.ldx, p0, kBR, g_sx1, wave, lane);
+    stream_issue<YRC, kSQ>(Y, d.ldy, q0, kBR, g_sy1, wave, lane);
+  }
+  if (nk > 2) {
+    stream_issue<XRC, kSP>(X, d.ldx, p0, 2 * kBR, g_sx2, wave, lane);
+    stream_issue<YRC, kSQ>(Y, d.ldy, q0, 2 * kBR, g_sy2, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0x3f70 | (2 * kSDma));  // vmcnt(24)
+  } else if (nk > 1) {
+    __builtin_amdgcn_s_waitcnt(0x3f70 | kSDma);  // vmcnt(12)
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+  }
+  __syncthreads();
+
+  f16v acc[4][2], tot[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      acc[i][j] = f16v{};
+      tot[i][j] = f16v{};
+    }
+  StreamFrags cur, nxt;
+  stream_read<XRC, YRC>(cur, g_sx0, g_sy0, wp, wq, c, h, 0);
+
+  // One reduction tile kt held in (xl, yl); (xn, yn) holds tile kt+1.  Group
+  // g's MFMAs run while group g+1's fragments load; before the last group
+  // the barrier ends this tile's reads, tile kt+3 is issued into (xl, yl)
+  // and tile kt+1's first fragments are read.  The flags (compile-time, so
+  // the stages stay distinct objects for the waitcnt model) say whether
+  // tile kt+1 exists, whether tile kt+2 is still in flight, and whether
+  // tile kt+3 exists.
+  auto step = [&](auto next_t, auto two_t, auto issue_t, int kt, float *xl, float *yl, float *xn,
+                  float *yn) {
+    constexpr bool kNext = decltype(next_t)::value;
+    constexpr bool kTwo = decltype(two_t)::value;
+    constexpr bool kIssue = decltype(issue_t)::value;
+#pragma unroll
+    for (int g = 0; g < kBR / 8; ++g) {
+      if (g < kBR / 8 - 1) {
+        stream_read<XRC, YRC>(nxt, xl, yl, wp, wq, c, h, g + 1);
+      } else if (kNext) {
+        if (kTwo)
+          __builtin_amdgcn_s_waitcnt(0x3f70 | kSDma);  // tile kt+1 landed, kt+2 may fly
+        else
+          __builtin_amdgcn_s_waitcnt(0x3f70);
+        __syncthreads();
+        if (kIssue) {
+          stream_issue<XRC, kSP>(X, d.ldx, p0, (kt + 3) * kBR, xl, wave, lane);
+          stream_issue<YRC, kSQ>(Y, d.ldy, q0, (kt + 3) * kBR, yl, wave, lane);
+        }
+        stream_read<XRC, YRC>(nxt, xn, yn, wp, wq, c, h, 0);
+      }
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[i][sl], cur.b[j][sl], acc[i][j],
+                                                            0, 0, 0);
+      cur = nxt;
+    }
+  };
+  auto flush = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        tot[i][j] += acc[i][j];
+        acc[i][j] = f16v{};
+      }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  float *x0 = g_sx0, *x1 = g_sx1, *x2 = g_sx2;
+  float *y0 = g_sy0, *y1 = g_sy1, *y2 = g_sy2;
+  int kt = 0;
+  for (; kt + 5 < nk; kt += 3) {
+    step(T_{}, T_{}, T_{}, kt, x0, y0, x1, y1);
+    step(T_{}, T_{}, T_{}, kt + 1, x1, y1, x2, y2);
+    step(T_{}, T_{}, T_{}, kt + 2, x2, y2, x0, y0);
+    flush();
+  }
+  // The last 1..5 tiles (kt is a multiple of 3, so tile kt sits in stage 0).
+  switch (nk - kt) {
+    case 5:
+      step(T_{}, T_{}, T_{}, kt, x0, y0, x1, y1);
+      step(T_{}, T_{}, T_{}, kt + 1, x1, y1, x2, y2);
+      step(T_{}, T_{}, F_{}, kt + 2, x2, y2, x0, y0);
+      step(T_{}, F_{}, F_{}, kt + 3, x0, y0, x1, y1);
+      step(F_{}, F_{}, F_{}, kt + 4, x1, y1, x2, y2);
+      break;
+    case 4:
+      step(T_{}, T_{}, T_{}, kt, x0, y0, x1, y1);
+      step(T_{}, T_{}, F_{}, kt + 1, x1, y1, x2, y2);
+      step(T_{}, F_{}, F_{}, kt + 2, x2, y2, x0, y0);
+      step(F_{}, F_{}, F_{}, kt + 3, x0, y0, x1, y1);
+      break;
+    case 3:
+      step(T_{}, T_{}, F_{}, kt, x0, y0, x1, y1);
+      step(T_{}, F_{}, F_{}, kt + 1, x1, y1, x2, y2);
+      step(F_{}, F_{}, F_{}, kt + 2, x2, y2, x0, y0);
+      break;
+    case 2:
+      step(T_{}, F_{}, F_{}, kt, x0, y0, x1, y1);
+      step(F_{}, F_{}, F_{}, kt + 1, x1, y1, x2, y2);
+      break;
+    default:
+      step(F_{}, F_{}, F_{}, kt, x0, y0, x1, y1);
+      break;
+  }
+  flush();
+
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const int q = q0 + wq * 64 + bj * 32 + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int p = p0 + wp * 128 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        float *dst = C + (int64_t)p * d.ldc + q;
+        float v = d.alpha * tot[bi][bj][i];
+        if (d.bias != nullptr) v = v + d.bias[q];
+        *dst = d.accumulate ? *dst + v : v;
+      }
+    }
+}
+
+template <bool XRC, bool YRC>
+__global__ void __launch_bounds__(kThreads, 1) gemm_stream_kernel(Gemm d) {
+  stream_tile<XRC, YRC>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
+}
+
+__global__ void __launch_bounds__(kThreads, 1) matmul_backward_stream(Gemm da, Gemm db, int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<true, true>(da, tile, blockIdx.y);
+  else
+    stream_tile<false, false>(db, tile - tiles_a, blockIdx.y);
+}
+
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
 
 // Split-K plan for one product: a grid under 256 workgroups leaves most of
@@ -358,6 +616,24 @@ bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
   };
   return ok(d.X, d.ldx, d.bsx, d.bsx2, xrc ? d.R : d.P) &&
          ok(d.Y, d.ldy, d.bsy, d.bsy2, yrc ? d.R : d.Q);
+}
+
+// The streamed path takes whole 256 x 128 output tiles and whole reduction
+// tiles of 16-byte aligned operands, and is used when the product has at
+// least one such tile per CU (with fewer, the 128 x 128 path with split-K
+// keeps more CUs busy).
+bool stream_fits(const Gemm &g, bool xrc, bool yrc) {
+  return g.P % kSP == 0 && g.Q % kSQ == 0 && g.R % kBR == 0 && g.R > 0 &&
+         vec_ok(g, xrc, yrc);
+}
+
+Gemm as_stream(Gemm g) {
+  g.tiles_p = g.P / kSP;
+  g.tiles_q = g.Q / kSQ;
+  g.splits = 1;
+  g.ktiles_per_split = g.R / kBR;
+  g.partial = nullptr;
+  return g;
 }
 
 int check_dims(numrs_hip_ctx *ctx, const char *who, int64_t batch, int64_t M, int64_t K,
@@ -408,6 +684,15 @@ template <bool XRC, bool YRC>
 int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   const int64_t n_tiles = (int64_t)g.tiles_p * g.tiles_q;
   if (n_tiles == 0 || batch == 0) return NUMRS_HIP_OK;
+  if (stream_fits(g, XRC, YRC)) {
+    const Gemm sg = as_stream(g);
+    const int64_t st = (int64_t)sg.tiles_p * sg.tiles_q;
+    if (st * batch >= ctx->num_cus) {
+      dim3 grid((unsigned)st, (unsigned)batch);
+      gemm_stream_kernel<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
+      return numrs_hip::check_launch(ctx, "gemm_stream_kernel");
+    }
+  }
   const int splits = plan_splits(g, batch);
   if (splits > 1) {
     void *ws = nullptr;
@@ -458,6 +743,15 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   Gemm gb = make(A, dC, dB, K, N, N, sa, sc, sb, K, N, M, acc);
   if (dA == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
   if (dB == nullptr) return gemm_dispatch(ctx, ga, batch, true, true);
+  if (stream_fits(ga, true, true) && stream_fits(gb, false, false)) {
+    const Gemm sa = as_stream(ga), sb = as_stream(gb);
+    const int64_t ta = (int64_t)sa.tiles_p * sa.tiles_q, tb = (int64_t)sb.tiles_p * sb.tiles_q;
+    if ((ta + tb) * batch >= ctx->num_cus) {
+      dim3 grid((unsigned)(ta + tb), (unsigned)batch);
+      matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      return numrs_hip::check_launch(ctx, "matmul_backward_stream");
+    }
+  }
   const int sa_ = plan_splits(ga, batch), sb_ = plan_splits(gb, batch);
   if (sa_ > 1 || sb_ > 1) {
     const size_t na = sa_ > 1 ? (size_t)sa_ * ga.P * ga.Q : 0;

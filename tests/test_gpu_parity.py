@@ -131,6 +131,48 @@ def test_matmul_backward_baseline_sizes(hip_ctx, rng, M, K, N):
     assert_bits(dB2.numpy(), gb * 2, "dB linearity")
 
 
+# Streamed large-tile path (256 x 128 workgroup tiles, DMA ring): taken for
+# aligned products with at least one such tile per CU.  Batches of 256 x 128
+# products reach the 256-tile threshold at small sizes; reductions of 1..7
+# and 32 tiles cover every prologue/tail case of the three-stage ring.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("K", [32, 64, 96, 128, 160, 192, 224, 1024])
+def test_matmul_streamed_batched(hip_ctx, rng, ta, tb, K):
+    batch, M, N = 128, 256, 256
+    say(f"streamed matmul batch={batch} M={M} K={K} N={N} ta={ta} tb={tb}")
+    A = rand(rng, (batch, K, M) if ta else (batch, M, K))
+    B = rand(rng, (batch, N, K) if tb else (batch, K, N))
+    C0 = rand(rng, (batch, M, N))
+    c = hip_ctx
+    Ad, Bd = c.to_device(A), c.to_device(B)
+    C = c.to_device(C0)
+    c.matmul_batched(Ad, Bd, C, trans_a=bool(ta), trans_b=bool(tb), accumulate=True)
+    a64 = A.astype(np.float64).transpose(0, 2, 1) if ta else A.astype(np.float64)
+    b64 = B.astype(np.float64).transpose(0, 2, 1) if tb else B.astype(np.float64)
+    ref = C0.astype(np.float64) + a64 @ b64
+    assert_contraction(C.numpy(), ref, K, what="streamed C += A B")
+
+
+@pytest.mark.parametrize("acc", [False, True])
+def test_matmul_backward_streamed(hip_ctx, rng, acc):
+    """matmul_backward through the streamed pair kernel (dA NT + dB TN tiles
+    in one grid) at a batched shape whose tile count reaches the threshold."""
+    batch, M, K, N = 4, 2048, 1024, 256
+    say(f"streamed matmul_backward batch={batch} M={M} K={K} N={N} acc={acc}")
+    A, B, dC = rand(rng, (batch, M, K)), rand(rng, (batch, K, N)), rand(rng, (batch, M, N))
+    ga0 = rand(rng, (batch, M, K)) if acc else np.zeros((batch, M, K), np.float32)
+    gb0 = rand(rng, (batch, K, N)) if acc else np.zeros((batch, K, N), np.float32)
+    c = hip_ctx
+    dA, dB = c.to_device(ga0), c.to_device(gb0)
+    c.matmul_backward_batched(c.to_device(dC), c.to_device(A), c.to_device(B), dA, dB,
+                              accumulate=acc)
+    d64 = dC.astype(np.float64)
+    ra = ga0 + d64 @ B.astype(np.float64).transpose(0, 2, 1)
+    rb = gb0 + A.astype(np.float64).transpose(0, 2, 1) @ d64
+    assert_contraction(dA.numpy(), ra, N, what="dA")
+    assert_contraction(dB.numpy(), rb, M, what="dB")
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,K,N", [(64, 784, 128), (37, 19, 53), (256, 256, 256)])
 def test_matmul_forward(hip_ctx, rng, ta, tb, M, K, N):
