@@ -78,6 +78,9 @@ def traffic_from_profile(name: str):
         return None
 
 
+# The kernel matmul_backward launches for aligned shapes with a 256 x 128 tile
+# per CU (2048^3 and the non-square C2 case): dA and dB tiles in one grid.
+HEAD_KERNEL = "matmul_backward_stream"
 COPY_PROBE_BYTES = 256 << 20  # calibration copy: reads and writes this many bytes
 
 
@@ -136,11 +139,11 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> dict:
 
     known_kib = COPY_PROBE_BYTES / 1024.0
     f_copy, w_copy = pick(fetch, "copy_kernel"), pick(write, "copy_kernel")
-    f_mm, w_mm = pick(fetch, "matmul_backward_kernel"), pick(write, "matmul_backward_kernel")
+    f_mm, w_mm = pick(fetch, HEAD_KERNEL), pick(write, HEAD_KERNEL)
     ff, fw = known_kib / f_copy, known_kib / w_copy
     traffic = (f_mm * ff + w_mm * fw) * 1024.0
     algorithmic = 5 * 2048 * 2048 * 4  # read A, B, dC; write dA, dB
-    res = {"kernel": "matmul_backward_kernel", "workload": "C2 2048^3",
+    res = {"kernel": HEAD_KERNEL, "workload": "C2 2048^3",
            "fetch_kib_raw": f_mm, "write_kib_raw": w_mm,
            "copy_fetch_kib_raw": f_copy, "copy_write_kib_raw": w_copy,
            "copy_bytes": COPY_PROBE_BYTES, "fetch_factor": ff, "write_factor": fw,
@@ -404,7 +407,7 @@ def main() -> int:
                                    args.warmup)
         tf = sq["flops"] / (sq["kernel_ms"] * 1e-3) / 1e12
         secondary.append({"workload": "C2' matmul_backward A[4096,1024] B[1024,4096]",
-                          "kernel": "matmul_backward_kernel", "kernel_ms": round(sq["kernel_ms"], 5),
+                          "kernel": HEAD_KERNEL, "kernel_ms": round(sq["kernel_ms"], 5),
                           "value": round(tf * 1e3, 1), "unit": "GFLOP/s",
                           "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "bound": "mfma",
                           "sample_ok": sq["sample_ok"]})
@@ -472,7 +475,7 @@ def main() -> int:
         "config": {"workload": "C2 matmul_backward: dA = dC @ B^T, dB = A^T @ dC, fp32",
                    "M": M, "K": K, "N": N, "flops_per_step": head["flops"],
                    "sample_ok": head["sample_ok"], "device": arch, "cus": n_cus},
-        "roofline": {"bound": "mfma", "kernel": "matmul_backward_kernel",
+        "roofline": {"bound": "mfma", "kernel": HEAD_KERNEL,
                      "achieved": round(achieved_tf, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved_tf / PEAK_FP32_MFMA_TFLOPS, 4),
                      "kernel_ms": round(head["kernel_ms"], 5),
