@@ -30,8 +30,9 @@
 //   * XCD-aware ordering: gfx950 dispatches workgroup b to XCD b % 8; the
 //     logical tile index is permuted so each XCD owns a contiguous 4 x 8 patch
 //     of tiles and its private L2 sees the operand rows/columns it reuses.
-//   * matmul_backward launches dA and dB tiles in ONE grid (2 x 256 tiles at
-//     2048^2 = 2 workgroups per CU on 256 CUs).
+//   * matmul_backward launches dA and dB tiles in ONE grid.
+//   * Aligned products with at least one 256 x 128 tile per CU take the
+//     streamed large-tile path further down (DMA ring, one workgroup per CU).
 //   * Split-K for products with few output tiles and long reductions (the
 //     weight gradients X^T dY of Linear layers): each split writes a plain
 //     partial, splitk_reduce adds them in split order -- deterministic.
