@@ -80,6 +80,33 @@ enum {
   NUMRS_HIP_DIV = 3  /* dx = g/y, dy = (g*(x/(y*y)))*-1  backward.rs:90-109  */
 };
 
+/* Optimizers beyond SGD and Adam (autograd/optim/mod.rs:1-41).  Their
+ * hyperparameters are passed as a float array in the reference constructor's
+ * order; the state slots s1/s2 per kind are listed. */
+enum {
+  NUMRS_HIP_OPT_ADAMW = 0,    /* lr, b1, b2, eps, wd;            s1 m, s2 v      adamw.rs:50-83 */
+  NUMRS_HIP_OPT_RMSPROP = 1,  /* lr, alpha, eps, wd, momentum;   s1 v, s2 buf*   rmsprop.rs:47-81 */
+  NUMRS_HIP_OPT_ADAGRAD = 2,  /* lr, eps, wd;                    s1 sum g^2      adagrad.rs:43-63 */
+  NUMRS_HIP_OPT_NADAM = 3,    /* lr, b1, b2, eps, wd;            s1 m, s2 v      nadam.rs:57-90 */
+  NUMRS_HIP_OPT_RADAM = 4,    /* lr, b1, b2, eps, wd;            s1 m, s2 v      radam.rs:53-86 */
+  NUMRS_HIP_OPT_ADADELTA = 5, /* rho, eps, wd;                   s1 E[g^2], s2 E[dx^2]  adadelta.rs:53-81 */
+  NUMRS_HIP_OPT_ADABOUND = 6, /* lr, final_lr, b1, b2, eps, wd, gamma; s1 m, s2 v  adabound.rs:70-107 */
+  NUMRS_HIP_OPT_RPROP = 7,    /* lr_init, eta+, eta-, lr_min, lr_max; s1 step sizes (start
+                                 at lr_init), s2 previous gradient (start at 0)  rprop.rs:63-94 */
+  NUMRS_HIP_OPT_LAMB = 8      /* lr, b1, b2, eps, wd;            s1 m, s2 v      lamb.rs:63-96 */
+};
+/* (* RMSprop's s2 is used only when momentum > 0.) */
+
+/* LR schedulers (autograd/optim/schedulers.rs); hyperparameters in the
+ * constructor's order, counts passed as floats. */
+enum {
+  NUMRS_HIP_SCHED_STEP = 0,        /* step_size, gamma          schedulers.rs:20-61 */
+  NUMRS_HIP_SCHED_EXPONENTIAL = 1, /* gamma                     schedulers.rs:68-102 */
+  NUMRS_HIP_SCHED_COSINE = 2,      /* t_max, eta_min            schedulers.rs:113-153 */
+  NUMRS_HIP_SCHED_PLATEAU = 3,     /* factor, patience, min_lr  schedulers.rs:172-238 */
+  NUMRS_HIP_SCHED_WARMUP = 4       /* warmup_steps, start_lr    schedulers.rs:249-295 */
+};
+
 /* ---------------------------------------------------------------------- */
 /* Context, memory, streams, timing                                        */
 /* ---------------------------------------------------------------------- */
@@ -317,6 +344,24 @@ int numrs_hip_adam_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *
                               float *const *m, float *const *v, const int64_t *n, int count,
                               float lr, float b1, float b2, float eps, float wd, int t);
 
+/* One step of optimizer `kind` over `count` parameter tensors in one launch
+ * (each Optimizer::step loop over params fused): p[i], g[i] and the kind's
+ * state slots s1[i]/s2[i] (see the enum) of n[i] elements; `hyper` holds the
+ * kind's nhyper hyperparameters; t is the already-incremented step counter
+ * for the Adam-family kinds.  Element arithmetic follows each reference
+ * step in order (bit-identical for all kinds but LAMB, whose layer norms are
+ * blocked sums).  Pointer arrays are host arrays. */
+int numrs_hip_optimizer_step(numrs_hip_ctx *ctx, int kind, float *const *p,
+                             const float *const *g, float *const *s1, float *const *s2,
+                             const int64_t *n, int count, const float *hyper, int nhyper, int t);
+/* Lookahead's slow-weight sync (optim/lookahead.rs:88-120):
+ * slow = slow + alpha*(fast - slow); fast = slow. */
+int numrs_hip_lookahead_update(numrs_hip_ctx *ctx, float *const *fast, float *const *slow,
+                               const int64_t *n, int count, float alpha);
+/* out[0] = sum_i x[i]*y[i] (device scalar), two deterministic passes: the
+ * dot product of L-BFGS's two-loop recursion (optim/lbfgs.rs:109-111). */
+int numrs_hip_dot(numrs_hip_ctx *ctx, const float *x, const float *y, int64_t n, float *out);
+
 /* ---------------------------------------------------------------------- */
 /* Forward kernels the engine records (DispatchTable / ops.rs analogues)   */
 /* ---------------------------------------------------------------------- */
@@ -451,6 +496,35 @@ int numrs_hip_optim_zero_grad(numrs_hip_optim *opt);
 int numrs_hip_optim_set_lr(numrs_hip_optim *opt, float lr);
 float numrs_hip_optim_lr(const numrs_hip_optim *opt);
 int numrs_hip_optim_free(numrs_hip_optim *opt);
+
+/* AdamW::new, RMSprop::new, AdaGrad::new, NAdam::new, RAdam::new,
+ * AdaDelta::new, AdaBound::new, Rprop::new, LAMB::new over parameter tensors
+ * (kind and hyperparameters as for numrs_hip_optimizer_step).  AdaDelta's
+ * learning rate reads 1 and ignores sets (adadelta.rs:139-146); Rprop's is
+ * the mean step size and a set resets every step size (rprop.rs:163-181). */
+int numrs_hip_optim_create(numrs_hip_ctx *ctx, int kind, numrs_hip_tensor **params, int n,
+                           const float *hyper, int nhyper, numrs_hip_optim **out);
+/* Lookahead::new (optim/lookahead.rs:59-84) wrapping `inner`, which it takes
+ * over (freeing the Lookahead frees it); slow weights start at the current
+ * parameter values.  Its lr is the inner optimizer's. */
+int numrs_hip_optim_lookahead(numrs_hip_optim *inner, numrs_hip_tensor **params, int n, int k,
+                              float alpha, numrs_hip_optim **out);
+/* LBFGS::new (optim/lbfgs.rs:60-76): two-loop recursion over the flattened
+ * parameters with `history_size` (s, y) pairs; max_iter is kept but unused,
+ * as in the reference. */
+int numrs_hip_optim_lbfgs(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
+                          int history_size, int max_iter, numrs_hip_optim **out);
+
+/* LR schedulers over an engine optimizer (optim/schedulers.rs).  step()
+ * follows Scheduler::step; ReduceLROnPlateau takes step_metric() instead
+ * (its step() is refused, as the reference panics there). */
+typedef struct numrs_hip_scheduler numrs_hip_scheduler;
+int numrs_hip_scheduler_create(int kind, const float *hyper, int nhyper,
+                               numrs_hip_scheduler **out);
+int numrs_hip_scheduler_step(numrs_hip_scheduler *s, numrs_hip_optim *opt);
+int numrs_hip_scheduler_step_metric(numrs_hip_scheduler *s, float metric, numrs_hip_optim *opt);
+float numrs_hip_scheduler_get_lr(const numrs_hip_scheduler *s);
+int numrs_hip_scheduler_free(numrs_hip_scheduler *s);
 
 #ifdef __cplusplus
 }

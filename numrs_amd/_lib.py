@@ -114,6 +114,20 @@ SIGNATURES = {
     "numrs_hip_optim_set_lr": (_i, [_vp, _f]),
     "numrs_hip_optim_lr": (_f, [_vp]),
     "numrs_hip_optim_free": (_i, [_vp]),
+    "numrs_hip_optimizer_step": (_i, [_vp, _i] + [_vp] * 4 + [_i64p, _i, _vp, _i, _i]),
+    "numrs_hip_lookahead_update": (_i, [_vp, _vp, _vp, _i64p, _i, _f]),
+    "numrs_hip_dot": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "numrs_hip_optim_create": (_i, [_vp, _i, ctypes.POINTER(_vp), _i, _vp, _i,
+                                    ctypes.POINTER(_vp)]),
+    "numrs_hip_optim_lookahead": (_i, [_vp, ctypes.POINTER(_vp), _i, _i, _f,
+                                       ctypes.POINTER(_vp)]),
+    "numrs_hip_optim_lbfgs": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _i, _i,
+                                   ctypes.POINTER(_vp)]),
+    "numrs_hip_scheduler_create": (_i, [_i, _vp, _i, ctypes.POINTER(_vp)]),
+    "numrs_hip_scheduler_step": (_i, [_vp, _vp]),
+    "numrs_hip_scheduler_step_metric": (_i, [_vp, _f, _vp]),
+    "numrs_hip_scheduler_get_lr": (_f, [_vp]),
+    "numrs_hip_scheduler_free": (_i, [_vp]),
 }
 
 # Enum values of include/numrs_hip.h.
@@ -121,6 +135,9 @@ OK, E_INVALID, E_SHAPE, E_HIP, E_NOMEM, E_NODEV = 0, -1, -2, -3, -4, -5
 UNBROADCAST_CORRECT, UNBROADCAST_REFERENCE = 0, 1
 RELU, SIGMOID, TANH, EXP, LOG, GELU, SQRT, SIN, COS, TAN, POW = range(11)
 ADD, SUB, MUL, DIV = range(4)
+(OPT_ADAMW, OPT_RMSPROP, OPT_ADAGRAD, OPT_NADAM, OPT_RADAM, OPT_ADADELTA, OPT_ADABOUND, OPT_RPROP,
+ OPT_LAMB) = range(9)
+SCHED_STEP, SCHED_EXPONENTIAL, SCHED_COSINE, SCHED_PLATEAU, SCHED_WARMUP = range(5)
 
 _lib = None
 

@@ -867,13 +867,35 @@ int op_attention(const T &q, const T &k, const T &v, int64_t B, int64_t S, int64
 // Optimizers (optim/base.rs, sgd.rs, adam.rs)
 // ---------------------------------------------------------------------------
 
+// An engine optimizer: SGD / Adam (their own kernels), one of the
+// NUMRS_HIP_OPT_* kinds (numrs_hip_optimizer_step), a Lookahead around an
+// inner optimizer, or L-BFGS over the flattened parameters.
+enum class Family { SGD, Adam, Kind, Lookahead, LBFGS };
+
 struct Optim {
-  numrs_hip_ctx *ctx;
-  bool adam;
+  numrs_hip_ctx *ctx = nullptr;
+  Family fam = Family::SGD;
+  bool adam = false;
   std::vector<T> params;
-  std::vector<Buf> s1, s2;  // SGD velocity | Adam m, v
-  float lr, mu = 0.f, wd = 0.f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+  std::vector<Buf> s1, s2;  // SGD velocity | Adam m, v | the kind's state slots
+  float lr = 0.f, mu = 0.f, wd = 0.f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
   int t = 0;
+  // NUMRS_HIP_OPT_* kinds
+  int kind = -1;
+  float hyper[8] = {};
+  int nhyper = 0;
+  // Lookahead (lookahead.rs:28-47)
+  numrs_hip_optim *inner = nullptr;
+  std::vector<Buf> slow;
+  int la_k = 0, la_counter = 0;
+  float la_alpha = 0.f;
+  // L-BFGS (lbfgs.rs:20-36): history of (s, y) over the flattened parameters
+  int history = 0, max_iter = 0;
+  int64_t total = 0;
+  std::vector<Buf> s_hist, y_hist;
+  Buf cur_p, cur_g, prev_p, prev_g, work_q, work_r, scalar;
+  bool has_prev = false;
+  ~Optim();
 };
 
 }  // namespace
@@ -884,6 +906,12 @@ struct numrs_hip_tensor {
 struct numrs_hip_optim {
   Optim o;
 };
+
+namespace {
+Optim::~Optim() {
+  if (inner != nullptr) delete inner;
+}
+}  // namespace
 
 namespace {
 
@@ -918,6 +946,180 @@ int new_optim(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, bool adam, O
     o->s1.push_back(a);
     o->s2.push_back(b);
   }
+  return NUMRS_HIP_OK;
+}
+
+}  // namespace
+
+namespace {
+
+int kind_hyper_count(int kind) {
+  switch (kind) {
+    case NUMRS_HIP_OPT_ADAMW:
+    case NUMRS_HIP_OPT_RMSPROP:
+    case NUMRS_HIP_OPT_NADAM:
+    case NUMRS_HIP_OPT_RADAM:
+    case NUMRS_HIP_OPT_RPROP:
+    case NUMRS_HIP_OPT_LAMB:
+      return 5;
+    case NUMRS_HIP_OPT_ADAGRAD:
+    case NUMRS_HIP_OPT_ADADELTA:
+      return 3;
+    case NUMRS_HIP_OPT_ADABOUND:
+      return 7;
+    default:
+      return -1;
+  }
+}
+
+// The Adam-family kinds advance a step counter at the top of step().
+bool kind_uses_t(int kind) {
+  return kind == NUMRS_HIP_OPT_ADAMW || kind == NUMRS_HIP_OPT_NADAM ||
+         kind == NUMRS_HIP_OPT_RADAM || kind == NUMRS_HIP_OPT_ADABOUND ||
+         kind == NUMRS_HIP_OPT_LAMB;
+}
+
+// Downloads a device scalar (synchronises the stream).
+int read_scalar(numrs_hip_ctx *ctx, const float *dev, float *host) {
+  return numrs_hip_download(ctx, host, dev, sizeof(float));
+}
+
+// Rprop::learning_rate: the mean step size over every parameter.
+float rprop_mean_step(const Optim &o) {
+  float total = 0.0f;
+  int64_t count = 0;
+  for (size_t i = 0; i < o.s1.size(); ++i) {
+    if (!o.s1[i]) continue;
+    const int64_t n = o.params[i]->numel();
+    if (n == 0) continue;
+    float *dev = nullptr;
+    if (numrs_hip::scratch(o.ctx, sizeof(float), &dev)) return NAN;
+    if (numrs_hip_sum(o.ctx, o.s1[i]->ptr, n, 0, dev)) return NAN;
+    float part = 0.0f;
+    if (read_scalar(o.ctx, dev, &part)) return NAN;
+    total = total + part;
+    count += n;
+  }
+  return total / (float)count;
+}
+
+// Lookahead::step, lookahead.rs:88-120.
+int lookahead_step(Optim &o) {
+  if (int rc = numrs_hip_optim_step(o.inner)) return rc;
+  o.la_counter += 1;
+  if (o.la_counter < o.la_k) return NUMRS_HIP_OK;
+  o.la_counter = 0;
+  std::vector<float *> fast, slow;
+  std::vector<int64_t> ns;
+  for (size_t i = 0; i < o.params.size(); ++i) {
+    fast.push_back(o.params[i]->data->ptr);
+    slow.push_back(o.slow[i]->ptr);
+    ns.push_back(o.params[i]->numel());
+  }
+  return numrs_hip_lookahead_update(o.ctx, fast.data(), slow.data(), ns.data(), (int)ns.size(),
+                                    o.la_alpha);
+}
+
+// Flattens the parameters (and their gradients, zeros when absent) into
+// dst, lbfgs.rs:80-106.
+int flatten(Optim &o, float *dst, bool grads) {
+  int64_t off = 0;
+  for (const T &p : o.params) {
+    const int64_t n = p->numel();
+    if (n > 0) {
+      if (!grads) {
+        if (int rc = numrs_hip_copy(o.ctx, dst + off, p->data->ptr, (size_t)n * sizeof(float)))
+          return rc;
+      } else if (p->grad && p->grad->valid) {
+        if (int rc = numrs_hip_copy(o.ctx, dst + off, p->grad->buf->ptr, (size_t)n * sizeof(float)))
+          return rc;
+      } else {
+        if (int rc = numrs_hip_fill(o.ctx, dst + off, n, 0.0f)) return rc;
+      }
+    }
+    off += n;
+  }
+  return NUMRS_HIP_OK;
+}
+
+int dot_host(Optim &o, const float *x, const float *y, float *out) {
+  if (int rc = numrs_hip_dot(o.ctx, x, y, o.total, o.scalar->ptr)) return rc;
+  return read_scalar(o.ctx, o.scalar->ptr, out);
+}
+
+// LBFGS::step, lbfgs.rs:157-212, with the two-loop recursion of :114-154;
+// vectors stay on the device, the recursion's scalars are f32 host values.
+int lbfgs_step(Optim &o) {
+  using namespace numrs_hip;
+  const int64_t n = o.total;
+  if (int rc = flatten(o, o.cur_p->ptr, false)) return rc;
+  if (int rc = flatten(o, o.cur_g->ptr, true)) return rc;
+  if (o.has_prev) {
+    Buf sb, yb;
+    if (int rc = alloc_buf(o.ctx, n, sizeof(float), &sb)) return rc;
+    if (int rc = alloc_buf(o.ctx, n, sizeof(float), &yb)) return rc;
+    if (int rc = vec_op(o.ctx, sb->ptr, o.cur_p->ptr, o.prev_p->ptr, 0.f, n, kVecSub)) return rc;
+    if (int rc = vec_op(o.ctx, yb->ptr, o.cur_g->ptr, o.prev_g->ptr, 0.f, n, kVecSub)) return rc;
+    float sy = 0.f;
+    if (int rc = dot_host(o, sb->ptr, yb->ptr, &sy)) return rc;
+    if (sy > 1e-10f) {
+      o.s_hist.push_back(sb);
+      o.y_hist.push_back(yb);
+      if ((int)o.s_hist.size() > o.history) {
+        o.s_hist.erase(o.s_hist.begin());
+        o.y_hist.erase(o.y_hist.begin());
+      }
+    }
+  }
+  // direction d = -H g, written into work_r
+  float *q = o.work_q->ptr, *r = o.work_r->ptr;
+  const int m = (int)o.s_hist.size();
+  if (m == 0) {
+    if (int rc = vec_op(o.ctx, r, o.cur_g->ptr, nullptr, 0.f, n, kVecNeg)) return rc;
+  } else {
+    if (int rc = numrs_hip_copy(o.ctx, q, o.cur_g->ptr, (size_t)n * sizeof(float))) return rc;
+    std::vector<float> alpha(m), rho(m);
+    for (int i = m - 1; i >= 0; --i) {
+      float ys = 0.f, sq = 0.f;
+      if (int rc = dot_host(o, o.y_hist[i]->ptr, o.s_hist[i]->ptr, &ys)) return rc;
+      rho[i] = 1.0f / fmaxf(ys, 1e-10f);
+      if (int rc = dot_host(o, o.s_hist[i]->ptr, q, &sq)) return rc;
+      alpha[i] = rho[i] * sq;
+      if (int rc = vec_op(o.ctx, q, q, o.y_hist[i]->ptr, alpha[i], n, kVecAxmy)) return rc;
+    }
+    float sy = 0.f, yy = 0.f;
+    if (int rc = dot_host(o, o.s_hist[m - 1]->ptr, o.y_hist[m - 1]->ptr, &sy)) return rc;
+    if (int rc = dot_host(o, o.y_hist[m - 1]->ptr, o.y_hist[m - 1]->ptr, &yy)) return rc;
+    const float gamma = sy / fmaxf(yy, 1e-10f);
+    if (int rc = vec_op(o.ctx, r, q, nullptr, gamma, n, kVecScale)) return rc;
+    for (int i = 0; i < m; ++i) {
+      float yr = 0.f;
+      if (int rc = dot_host(o, o.y_hist[i]->ptr, r, &yr)) return rc;
+      const float beta = rho[i] * yr;
+      if (int rc = vec_op(o.ctx, r, r, o.s_hist[i]->ptr, alpha[i] - beta, n, kVecAypx))
+        return rc;
+    }
+    if (int rc = vec_op(o.ctx, r, r, nullptr, 0.f, n, kVecNeg)) return rc;
+  }
+  // p += lr * d, per parameter (lbfgs.rs:187-197)
+  int64_t off = 0;
+  for (const T &p : o.params) {
+    const int64_t k = p->numel();
+    if (int rc = vec_op(o.ctx, p->data->ptr, p->data->ptr, r + off, o.lr, k, kVecAxpy)) return rc;
+    off += k;
+  }
+  // keep this step's flattened state (lbfgs.rs:199-201)
+  if (!o.has_prev) {
+    if (int rc = alloc_buf(o.ctx, n > 0 ? n : 1, sizeof(float), &o.prev_p)) return rc;
+    if (int rc = alloc_buf(o.ctx, n > 0 ? n : 1, sizeof(float), &o.prev_g)) return rc;
+  }
+  std::swap(o.prev_p, o.cur_p);
+  std::swap(o.prev_g, o.cur_g);
+  if (!o.cur_p) {
+    if (int rc = alloc_buf(o.ctx, n > 0 ? n : 1, sizeof(float), &o.cur_p)) return rc;
+    if (int rc = alloc_buf(o.ctx, n > 0 ? n : 1, sizeof(float), &o.cur_g)) return rc;
+  }
+  o.has_prev = true;
   return NUMRS_HIP_OK;
 }
 
@@ -1198,7 +1400,13 @@ int numrs_hip_optim_adam(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, f
 int numrs_hip_optim_step(numrs_hip_optim *opt) {
   if (opt == nullptr) return NUMRS_HIP_E_INVALID;
   Optim &o = opt->o;
+  switch (o.fam) {
+    case Family::Lookahead: return lookahead_step(o);
+    case Family::LBFGS: return lbfgs_step(o);
+    default: break;
+  }
   if (o.adam) ++o.t;  // adam.rs:311
+  if (o.fam == Family::Kind && kind_uses_t(o.kind)) ++o.t;  // e.g. adamw.rs:93
   std::vector<float *> ps, ms, vs;
   std::vector<const float *> gs;
   std::vector<int64_t> ns;
@@ -1208,12 +1416,15 @@ int numrs_hip_optim_step(numrs_hip_optim *opt) {
     if (int rc = grad_materialise(p)) return rc;
     ps.push_back(p->data->ptr);
     gs.push_back(p->grad->buf->ptr);
-    ms.push_back(o.s1[i]->ptr);
-    vs.push_back(o.adam ? o.s2[i]->ptr : nullptr);
+    ms.push_back(o.s1[i] ? o.s1[i]->ptr : nullptr);
+    vs.push_back(o.s2[i] ? o.s2[i]->ptr : nullptr);
     ns.push_back(p->numel());
   }
   if (ps.empty()) return NUMRS_HIP_OK;
   const int count = (int)ps.size();
+  if (o.fam == Family::Kind)
+    return numrs_hip_optimizer_step(o.ctx, o.kind, ps.data(), gs.data(), ms.data(), vs.data(),
+                                    ns.data(), count, o.hyper, o.nhyper, o.t);
   if (o.adam)
     return numrs_hip_adam_step_multi(o.ctx, ps.data(), gs.data(), ms.data(), vs.data(), ns.data(),
                                      count, o.lr, o.b1, o.b2, o.eps, o.wd, o.t);
@@ -1223,6 +1434,7 @@ int numrs_hip_optim_step(numrs_hip_optim *opt) {
 
 int numrs_hip_optim_zero_grad(numrs_hip_optim *opt) {  // sgd.rs:169-173
   if (opt == nullptr) return NUMRS_HIP_E_INVALID;
+  if (opt->o.fam == Family::Lookahead) return numrs_hip_optim_zero_grad(opt->o.inner);
   for (const T &p : opt->o.params)
     if (p->grad) p->grad->valid = false;
   return NUMRS_HIP_OK;
@@ -1230,14 +1442,150 @@ int numrs_hip_optim_zero_grad(numrs_hip_optim *opt) {  // sgd.rs:169-173
 
 int numrs_hip_optim_set_lr(numrs_hip_optim *opt, float lr) {
   if (opt == nullptr) return NUMRS_HIP_E_INVALID;
-  opt->o.lr = lr;
+  Optim &o = opt->o;
+  if (o.fam == Family::Lookahead) return numrs_hip_optim_set_lr(o.inner, lr);  // lookahead.rs:130
+  if (o.fam == Family::Kind) {
+    if (o.kind == NUMRS_HIP_OPT_ADADELTA) return NUMRS_HIP_OK;  // adadelta.rs:144-146
+    if (o.kind == NUMRS_HIP_OPT_RPROP) {  // rprop.rs:174-181: every step size = lr
+      for (size_t i = 0; i < o.s1.size(); ++i)
+        if (o.s1[i])
+          if (int rc = numrs_hip_fill(o.ctx, o.s1[i]->ptr, o.params[i]->numel(), lr)) return rc;
+      o.hyper[0] = lr;
+      return NUMRS_HIP_OK;
+    }
+    o.hyper[0] = lr;
+  }
+  o.lr = lr;
   return NUMRS_HIP_OK;
 }
 
-float numrs_hip_optim_lr(const numrs_hip_optim *opt) { return opt == nullptr ? NAN : opt->o.lr; }
+float numrs_hip_optim_lr(const numrs_hip_optim *opt) {
+  if (opt == nullptr) return NAN;
+  const Optim &o = opt->o;
+  if (o.fam == Family::Lookahead) return numrs_hip_optim_lr(o.inner);  // lookahead.rs:126
+  if (o.fam == Family::Kind) {
+    if (o.kind == NUMRS_HIP_OPT_ADADELTA) return 1.0f;  // adadelta.rs:139-142
+    if (o.kind == NUMRS_HIP_OPT_RPROP) return rprop_mean_step(o);  // rprop.rs:163-172
+    return o.hyper[0];
+  }
+  return o.lr;
+}
 
 int numrs_hip_optim_free(numrs_hip_optim *opt) {
   delete opt;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_create(numrs_hip_ctx *ctx, int kind, numrs_hip_tensor **params, int n,
+                           const float *hyper, int nhyper, numrs_hip_optim **out) {
+  NRS_CHECK_CTX(ctx);
+  if (out == nullptr || n < 0 || (n > 0 && params == nullptr) || hyper == nullptr ||
+      nhyper < 1 || nhyper > 8)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_optim_create: bad arguments");
+  *out = nullptr;
+  if (kind_hyper_count(kind) != nhyper)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "optimizer kind %d takes %d hyperparameters, got %d",
+                kind, kind_hyper_count(kind), nhyper);
+  auto *o = new numrs_hip_optim();
+  Optim &op = o->o;
+  op.ctx = ctx;
+  op.fam = Family::Kind;
+  op.kind = kind;
+  op.nhyper = nhyper;
+  for (int i = 0; i < nhyper; ++i) op.hyper[i] = hyper[i];
+  op.lr = hyper[0];
+  // State slots start at zero, Rprop's step sizes at lr_init (rprop.rs:71-76).
+  const bool two = !(kind == NUMRS_HIP_OPT_ADAGRAD ||
+                     (kind == NUMRS_HIP_OPT_RMSPROP && !(hyper[4] > 0.0f)));
+  for (int i = 0; i < n; ++i) {
+    if (params[i] == nullptr) {
+      delete o;
+      return fail(ctx, NUMRS_HIP_E_INVALID, "null parameter %d", i);
+    }
+    const T &p = params[i]->t;
+    op.params.push_back(p);
+    Buf a, b;
+    const float first = kind == NUMRS_HIP_OPT_RPROP ? hyper[0] : 0.0f;
+    int rc = alloc_buf(ctx, p->numel(), sizeof(float), &a);
+    if (!rc) rc = numrs_hip_fill(ctx, a->ptr, p->numel(), first);
+    if (!rc && two) rc = alloc_buf(ctx, p->numel(), sizeof(float), &b);
+    if (!rc && two) rc = numrs_hip_fill(ctx, b->ptr, p->numel(), 0.0f);
+    if (rc) {
+      delete o;
+      return rc;
+    }
+    op.s1.push_back(a);
+    op.s2.push_back(b);
+  }
+  *out = o;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_lookahead(numrs_hip_optim *inner, numrs_hip_tensor **params, int n, int k,
+                              float alpha, numrs_hip_optim **out) {
+  if (inner == nullptr || out == nullptr || n < 0 || (n > 0 && params == nullptr) || k < 1)
+    return NUMRS_HIP_E_INVALID;
+  numrs_hip_ctx *ctx = inner->o.ctx;
+  *out = nullptr;
+  auto *o = new numrs_hip_optim();
+  Optim &op = o->o;
+  op.ctx = ctx;
+  op.fam = Family::Lookahead;
+  op.la_k = k;
+  op.la_alpha = alpha;
+  for (int i = 0; i < n; ++i) {
+    if (params[i] == nullptr) {
+      delete o;
+      return fail(ctx, NUMRS_HIP_E_INVALID, "null parameter %d", i);
+    }
+    const T &p = params[i]->t;
+    op.params.push_back(p);
+    Buf b;  // slow weights start as the current values (lookahead.rs:66-75)
+    int rc = alloc_buf(ctx, p->numel(), sizeof(float), &b);
+    if (!rc) rc = numrs_hip_copy(ctx, b->ptr, p->data->ptr, (size_t)p->numel() * sizeof(float));
+    if (rc) {
+      delete o;
+      return rc;
+    }
+    op.slow.push_back(b);
+  }
+  op.inner = inner;  // taken over only on success
+  *out = o;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_optim_lbfgs(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
+                          int history_size, int max_iter, numrs_hip_optim **out) {
+  NRS_CHECK_CTX(ctx);
+  if (out == nullptr || n < 0 || (n > 0 && params == nullptr) || history_size < 0)
+    return NUMRS_HIP_E_INVALID;
+  *out = nullptr;
+  auto *o = new numrs_hip_optim();
+  Optim &op = o->o;
+  op.ctx = ctx;
+  op.fam = Family::LBFGS;
+  op.lr = lr;
+  op.history = history_size;
+  op.max_iter = max_iter;
+  for (int i = 0; i < n; ++i) {
+    if (params[i] == nullptr) {
+      delete o;
+      return fail(ctx, NUMRS_HIP_E_INVALID, "null parameter %d", i);
+    }
+    op.params.push_back(params[i]->t);
+    op.total += params[i]->t->numel();
+  }
+  const int64_t m = op.total > 0 ? op.total : 1;
+  int rc = alloc_buf(ctx, m, sizeof(float), &op.cur_p);
+  if (!rc) rc = alloc_buf(ctx, m, sizeof(float), &op.cur_g);
+  if (!rc) rc = alloc_buf(ctx, m, sizeof(float), &op.work_q);
+  if (!rc) rc = alloc_buf(ctx, m, sizeof(float), &op.work_r);
+  if (!rc) rc = alloc_buf(ctx, 1, sizeof(float), &op.scalar);
+  if (rc) {
+    delete o;
+    return rc;
+  }
+  *out = o;
   return NUMRS_HIP_OK;
 }
 

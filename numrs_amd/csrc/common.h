@@ -58,6 +58,19 @@ void cache_release(numrs_hip_ctx *ctx);
 // Checks the launch that was just enqueued.
 int check_launch(numrs_hip_ctx *ctx, const char *what);
 
+// Vector operations of the L-BFGS two-loop recursion (optim/lbfgs.rs),
+// out[i] = f(a[i], b[i], s) in the reference's operation order.
+enum VecOp {
+  kVecSub = 0,    // a - b
+  kVecAxmy = 1,   // a - s*b
+  kVecScale = 2,  // s*a
+  kVecAypx = 3,   // a + b*s
+  kVecNeg = 4,    // -a
+  kVecAxpy = 5    // a + s*b
+};
+int vec_op(numrs_hip_ctx *ctx, float *out, const float *a, const float *b, float s, int64_t n,
+           int op);
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace numrs_hip

@@ -252,6 +252,30 @@ class Context:
         self._check(L.load().numrs_hip_adam_step(self.handle, _p(p), _p(g), _p(m), _p(v), p.size,
                                                  lr, b1, b2, eps, wd, int(t)))
 
+    def optimizer_step(self, kind: int, ps, gs, s1s, s2s, hyper, t: int = 0) -> None:
+        """numrs_hip_optimizer_step over lists of device arrays (None = no slot)."""
+        k = len(ps)
+
+        def arr(xs):
+            if xs is None:
+                return None
+            return (ctypes.c_void_p * max(k, 1))(*[_p(x) for x in xs])
+
+        n = (ctypes.c_int64 * max(k, 1))(*[x.size for x in ps])
+        h = (ctypes.c_float * len(hyper))(*[float(x) for x in hyper])
+        self._check(L.load().numrs_hip_optimizer_step(
+            self.handle, kind, arr(ps), arr(gs), arr(s1s), arr(s2s), n, k, h, len(hyper), int(t)))
+
+    def lookahead_update(self, fast, slow, alpha: float) -> None:
+        k = len(fast)
+        fa = (ctypes.c_void_p * max(k, 1))(*[_p(x) for x in fast])
+        sa = (ctypes.c_void_p * max(k, 1))(*[_p(x) for x in slow])
+        n = (ctypes.c_int64 * max(k, 1))(*[x.size for x in fast])
+        self._check(L.load().numrs_hip_lookahead_update(self.handle, fa, sa, n, k, alpha))
+
+    def dot(self, x, y, out) -> None:
+        self._check(L.load().numrs_hip_dot(self.handle, _p(x), _p(y), x.size, _p(out)))
+
 
 def shape_of(x: Sequence[int] | DeviceArray) -> tuple[int, ...]:
     return x.shape if isinstance(x, DeviceArray) else tuple(x)

@@ -38,6 +38,14 @@
  *   orc_sum_avx2_order           equals sequential/fp64 sum on exactly representable inputs
  *   orc_gelu_backward_f64        NEW op (no reference): finite differences + torch fp64 vectors
  *   orc_layernorm_backward_f64   NEW op (no reference): finite differences + torch fp64 vectors
+ *   orc_adamw/rmsprop/adagrad/nadam/radam/adadelta/adabound/rprop/lamb_step
+ *                                KATs tests/autograd/optim/standard_opts.rs, advanced_opts.rs;
+ *                                float64 closed forms of each update rule over several steps;
+ *                                special cases (AdamW wd=0 vs Adam, RAdam's SGD branch, Rprop
+ *                                sign flips and signum(+-0))
+ *   orc_lookahead_sync           closed form slow + a(fast - slow)
+ *   orc_dot_seq                  exact on integer-valued inputs; float64 dot
+ *   orc_sched_*                  closed forms (gamma^k, cosine, linear ramp) and plateau traces
  */
 #include <math.h>
 #include <stdint.h>
@@ -621,4 +629,249 @@ EXPORT void orc_softmax_backward_f64(const float *y, const float *g, float *dx, 
     for (int64_t j = 0; j < cols; ++j) rs += (double)go[j] * (double)s[j];
     for (int64_t j = 0; j < cols; ++j) dx[r * cols + j] = (float)((double)s[j] * ((double)go[j] - rs));
   }
+}
+
+/* ------------------------------------------------------------------------- */
+/* The other optimizers (autograd/optim/) and the LR schedulers              */
+/* ------------------------------------------------------------------------- */
+/* Each step is one parameter tensor, in the reference's operation order
+ * (Rust evaluates a*b*c as (a*b)*c and never contracts).  Scalars the
+ * reference derives once per step are derived here the same way: powi is
+ * orc_powi, powf/cosf/sqrtf are the C library's, as Rust's f32 methods call
+ * them on Linux. */
+
+/* f32::signum: 1.0 for +0.0 and positives, -1.0 for -0.0 and negatives. */
+static float orc_signum(float x) { return isnan(x) ? x : copysignf(1.0f, x); }
+
+/* AdamW::step, optim/adamw.rs:92-129 (decay applied to the parameter). */
+EXPORT void orc_adamw_step(float *p, const float *g, float *m, float *v, int64_t n, float lr,
+                           float b1, float b2, float eps, float wd, int t) {
+  const float bc1 = 1.0f - orc_powi(b1, t), bc2 = 1.0f - orc_powi(b2, t);
+  for (int64_t i = 0; i < n; ++i) m[i] = b1 * m[i] + (1.0f - b1) * g[i];
+  for (int64_t i = 0; i < n; ++i) v[i] = b2 * v[i] + (1.0f - b2) * g[i] * g[i];
+  for (int64_t i = 0; i < n; ++i) {
+    const float mh = m[i] / bc1, vh = v[i] / bc2;
+    p[i] = p[i] - lr * (mh / (sqrtf(vh) + eps) + wd * p[i]);
+  }
+}
+
+/* RMSprop::step, optim/rmsprop.rs:90-135 (apply_weight_decay first). */
+EXPORT void orc_rmsprop_step(float *p, const float *g0, float *v, float *buf, int64_t n,
+                             float lr, float alpha, float eps, float wd, float mom) {
+  for (int64_t i = 0; i < n; ++i) {
+    float g = g0[i];
+    if (wd != 0.0f) g = g + wd * p[i];
+    v[i] = alpha * v[i] + (1.0f - alpha) * g * g;
+    if (mom > 0.0f) {
+      buf[i] = mom * buf[i] + g / (sqrtf(v[i]) + eps);
+      p[i] = p[i] - lr * buf[i];
+    } else {
+      p[i] = p[i] - lr * g / (sqrtf(v[i]) + eps);
+    }
+  }
+}
+
+/* AdaGrad::step, optim/adagrad.rs:72-99. */
+EXPORT void orc_adagrad_step(float *p, const float *g0, float *acc, int64_t n, float lr,
+                             float eps, float wd) {
+  for (int64_t i = 0; i < n; ++i) {
+    float g = g0[i];
+    if (wd != 0.0f) g = g + wd * p[i];
+    acc[i] = acc[i] + g * g;
+    p[i] = p[i] - lr * g / (sqrtf(acc[i]) + eps);
+  }
+}
+
+/* NAdam::step, optim/nadam.rs:99-145 (bias corrections with powf). */
+EXPORT void orc_nadam_step(float *p, const float *g0, float *m, float *v, int64_t n, float lr,
+                           float b1, float b2, float eps, float wd, int t) {
+  const float tf = (float)t;
+  const float bc1 = 1.0f - powf(b1, tf), bc2 = 1.0f - powf(b2, tf);
+  for (int64_t i = 0; i < n; ++i) {
+    float g = g0[i];
+    if (wd != 0.0f) g = g + wd * p[i];
+    m[i] = b1 * m[i] + (1.0f - b1) * g;
+    v[i] = b2 * v[i] + (1.0f - b2) * g * g;
+    const float mh = m[i] / bc1, vh = v[i] / bc2;
+    const float mbar = b1 * mh + (1.0f - b1) * g / bc1;
+    p[i] = p[i] - lr * mbar / (sqrtf(vh) + eps);
+  }
+}
+
+/* RAdam::step, optim/radam.rs:95-161: the rectification term is derived once
+ * per step; returns 1 when the adaptive (rectified) update was used. */
+EXPORT int orc_radam_step(float *p, const float *g0, float *m, float *v, int64_t n, float lr,
+                          float b1, float b2, float eps, float wd, int t) {
+  const float tf = (float)t;
+  const float bc1 = 1.0f - powf(b1, tf), bc2 = 1.0f - powf(b2, tf);
+  const float rho_inf = 2.0f / (1.0f - b2) - 1.0f;
+  const float rho_t = rho_inf - 2.0f * tf * powf(b2, tf) / bc2;
+  const int adaptive = rho_t > 5.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float g = g0[i];
+    if (wd != 0.0f) g = g + wd * p[i];
+    m[i] = b1 * m[i] + (1.0f - b1) * g;
+    v[i] = b2 * v[i] + (1.0f - b2) * g * g;
+  }
+  if (adaptive) {
+    const float r = sqrtf((rho_t - 4.0f) * (rho_t - 2.0f) * rho_inf /
+                          ((rho_inf - 4.0f) * (rho_inf - 2.0f) * rho_t));
+    for (int64_t i = 0; i < n; ++i) {
+      const float mh = m[i] / bc1, vh = v[i] / bc2;
+      p[i] = p[i] - lr * r * mh / (sqrtf(vh) + eps);
+    }
+  } else {
+    for (int64_t i = 0; i < n; ++i) p[i] = p[i] - lr * (m[i] / bc1);
+  }
+  return adaptive;
+}
+
+/* AdaDelta::step, optim/adadelta.rs:90-131 (deltas use the old E[dx^2]). */
+EXPORT void orc_adadelta_step(float *p, const float *g0, float *eg, float *ed, int64_t n,
+                              float rho, float eps, float wd) {
+  for (int64_t i = 0; i < n; ++i) {
+    float g = g0[i];
+    if (wd != 0.0f) g = g + wd * p[i];
+    eg[i] = rho * eg[i] + (1.0f - rho) * g * g;
+    const float delta = (sqrtf(ed[i] + eps) / sqrtf(eg[i] + eps)) * g;
+    ed[i] = rho * ed[i] + (1.0f - rho) * delta * delta;
+    p[i] = p[i] - delta;
+  }
+}
+
+/* AdaBound::step, optim/adabound.rs:116-179 (decay only when wd > 0). */
+EXPORT void orc_adabound_step(float *p, const float *g0, float *m, float *v, int64_t n, float lr,
+                              float final_lr, float b1, float b2, float eps, float wd, float gamma,
+                              int t) {
+  const float gamma_t = gamma * (float)t;
+  const float lower = final_lr * (1.0f - 1.0f / (gamma_t + 1.0f));
+  const float upper = final_lr * (1.0f + 1.0f / fmaxf(gamma_t, 1e-8f));
+  const float bc1 = 1.0f - orc_powi(b1, t), bc2 = 1.0f - orc_powi(b2, t);
+  const float step_size = lr * (sqrtf(bc2) / bc1);
+  for (int64_t i = 0; i < n; ++i) {
+    float g = g0[i];
+    if (wd > 0.0f) g = g + wd * p[i];
+    m[i] = b1 * m[i] + (1.0f - b1) * g;
+    v[i] = b2 * v[i] + (1.0f - b2) * g * g;
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    const float mh = m[i] / bc1, vh = v[i] / bc2;
+    const float denom = sqrtf(vh) + eps;
+    const float lr_t = step_size / denom;
+    const float lr_c = fminf(fmaxf(lr_t, lower), upper);
+    p[i] = p[i] - lr_c * mh;
+  }
+}
+
+/* Rprop::step, optim/rprop.rs:103-155 (init :63-93) (step sizes start at lr_init). */
+EXPORT void orc_rprop_step(float *p, const float *g, float *step, float *prev, int64_t n,
+                           float eta_plus, float eta_minus, float lr_min, float lr_max) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float sp = g[i] * prev[i];
+    if (sp > 0.0f) {
+      step[i] = fminf(step[i] * eta_plus, lr_max);
+      p[i] = p[i] - step[i] * orc_signum(g[i]);
+      prev[i] = g[i];
+    } else if (sp < 0.0f) {
+      step[i] = fmaxf(step[i] * eta_minus, lr_min);
+      prev[i] = 0.0f;
+    } else {
+      p[i] = p[i] - step[i] * orc_signum(g[i]);
+      prev[i] = g[i];
+    }
+  }
+}
+
+/* LAMB::step, optim/lamb.rs:105-176: Adam direction (+ wd*p when wd > 0),
+ * layer norms as sequential f32 sums of squares, trust ratio ||w||/||r||
+ * (1 when either is 0).  `u` is scratch of n floats.  Returns the ratio. */
+EXPORT float orc_lamb_step(float *p, const float *g, float *m, float *v, float *u, int64_t n,
+                           float lr, float b1, float b2, float eps, float wd, int t) {
+  for (int64_t i = 0; i < n; ++i) {
+    m[i] = b1 * m[i] + (1.0f - b1) * g[i];
+    v[i] = b2 * v[i] + (1.0f - b2) * g[i] * g[i];
+  }
+  const float bc1 = 1.0f - orc_powi(b1, t), bc2 = 1.0f - orc_powi(b2, t);
+  for (int64_t i = 0; i < n; ++i) {
+    const float mh = m[i] / bc1, vh = v[i] / bc2;
+    u[i] = mh / (sqrtf(vh) + eps);
+  }
+  if (wd > 0.0f)
+    for (int64_t i = 0; i < n; ++i) u[i] = u[i] + wd * p[i];
+  float w2 = 0.0f, u2 = 0.0f;
+  for (int64_t i = 0; i < n; ++i) w2 = w2 + p[i] * p[i];
+  for (int64_t i = 0; i < n; ++i) u2 = u2 + u[i] * u[i];
+  const float wn = sqrtf(w2), un = sqrtf(u2);
+  const float trust = (wn > 0.0f && un > 0.0f) ? wn / un : 1.0f;
+  for (int64_t i = 0; i < n; ++i) p[i] = p[i] - lr * trust * u[i];
+  return trust;
+}
+
+/* Lookahead slow-weight update, optim/lookahead.rs:88-120:
+ * slow = slow + alpha*(fast - slow); fast = slow. */
+EXPORT void orc_lookahead_sync(float *fast, float *slow, int64_t n, float alpha) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float s = slow[i] + alpha * (fast[i] - slow[i]);
+    slow[i] = s;
+    fast[i] = s;
+  }
+}
+
+/* L-BFGS dot product, optim/lbfgs.rs:109-111: sequential f32 sum of products. */
+EXPORT float orc_dot_seq(const float *a, const float *b, int64_t n) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) s = s + a[i] * b[i];
+  return s;
+}
+
+/* LR schedulers, optim/schedulers.rs.  State is a float[6] owned by the
+ * caller: [0] kind-specific counter, [1] initial/target lr, [2] best metric,
+ * [3] epochs since improvement.  Each call returns the learning rate the
+ * optimizer holds afterwards (given its current `lr`). */
+EXPORT float orc_sched_step_lr(float *st, float lr, int step_size, float gamma) {  /* schedulers.rs:43-61 */
+  if (st[0] == 0.0f) st[1] = lr;
+  st[0] = st[0] + 1.0f;
+  if (((int64_t)st[0]) % step_size == 0) lr = lr * gamma;
+  return lr;
+}
+EXPORT float orc_sched_exponential(float *st, float lr, float gamma) {  /* schedulers.rs:88-102 */
+  if (st[0] == 0.0f) st[1] = lr;
+  st[0] = st[0] + 1.0f;
+  return lr * gamma;
+}
+EXPORT float orc_sched_cosine(float *st, float lr, int t_max, float eta_min) {  /* schedulers.rs:136-153 */
+  if (st[0] == 0.0f) st[1] = lr;
+  st[0] = st[0] + 1.0f;
+  const float pi = 3.14159265358979323846f;
+  const float t = (float)(int64_t)st[0], tm = (float)t_max;
+  return eta_min + (st[1] - eta_min) * (1.0f + cosf(pi * t / tm)) / 2.0f;
+}
+EXPORT float orc_sched_plateau(float *st, float lr, float metric, float factor, int patience,
+                               float min_lr) {  /* schedulers.rs:205-227 */
+  if (st[1] == 0.0f) st[1] = lr;
+  if (st[0] == 0.0f) { st[0] = 1.0f; st[2] = INFINITY; st[3] = 0.0f; }
+  if (metric < st[2]) {
+    st[2] = metric;
+    st[3] = 0.0f;
+  } else {
+    st[3] = st[3] + 1.0f;
+    if ((int)st[3] >= patience) {
+      const float nl = fmaxf(lr * factor, min_lr);
+      if (nl < lr) {
+        lr = nl;
+        st[3] = 0.0f;
+      }
+    }
+  }
+  return lr;
+}
+EXPORT float orc_sched_warmup(float *st, float lr, int warmup, float start_lr) {  /* schedulers.rs:272-295 */
+  if (st[0] == 0.0f) {
+    st[1] = lr;
+    lr = start_lr;
+  }
+  st[0] = st[0] + 1.0f;
+  const int cur = (int)st[0];
+  if (cur <= warmup) lr = start_lr + (st[1] - start_lr) * ((float)cur / (float)warmup);
+  return lr;
 }

@@ -89,6 +89,22 @@ def _declare(L) -> None:
         "orc_layernorm_backward_f64": (None, [_f32p] * 6 + [_i64, _i64, _f32, _f64p]),
         "orc_softmax_rows_f64": (None, [_f32p, _f32p, _i64, _i64]),
         "orc_softmax_backward_f64": (None, [_f32p] * 3 + [_i64, _i64]),
+        "orc_adamw_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 5 + [ctypes.c_int]),
+        "orc_rmsprop_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 5),
+        "orc_adagrad_step": (None, [_f32p] * 3 + [_i64] + [_f32] * 3),
+        "orc_nadam_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 5 + [ctypes.c_int]),
+        "orc_radam_step": (ctypes.c_int, [_f32p] * 4 + [_i64] + [_f32] * 5 + [ctypes.c_int]),
+        "orc_adadelta_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 3),
+        "orc_adabound_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 7 + [ctypes.c_int]),
+        "orc_rprop_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 4),
+        "orc_lamb_step": (_f32, [_f32p] * 5 + [_i64] + [_f32] * 5 + [ctypes.c_int]),
+        "orc_lookahead_sync": (None, [_f32p, _f32p, _i64, _f32]),
+        "orc_dot_seq": (_f32, [_f32p, _f32p, _i64]),
+        "orc_sched_step_lr": (_f32, [_f32p, _f32, ctypes.c_int, _f32]),
+        "orc_sched_exponential": (_f32, [_f32p, _f32, _f32]),
+        "orc_sched_cosine": (_f32, [_f32p, _f32, ctypes.c_int, _f32]),
+        "orc_sched_plateau": (_f32, [_f32p, _f32, _f32, _f32, ctypes.c_int, _f32]),
+        "orc_sched_warmup": (_f32, [_f32p, _f32, ctypes.c_int, _f32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -339,6 +355,131 @@ def adam_step(p: np.ndarray, g, m: np.ndarray, v: np.ndarray, t: int, lr=1e-3, b
               b2=0.999, eps=1e-8, wd=0.0) -> None:
     g = _f(g)
     lib().orc_adam_step(_p(p), _p(g), _p(m), _p(v), p.size, lr, b1, b2, eps, wd, int(t))
+
+
+def _st(x):
+    return None if x is None else _p(x)
+
+
+def adamw_step(p, g, m, v, t, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.01):
+    lib().orc_adamw_step(_p(p), _p(_f(g)), _p(m), _p(v), p.size, lr, b1, b2, eps, wd, int(t))
+
+
+def rmsprop_step(p, g, v, buf, lr, alpha=0.99, eps=1e-8, wd=0.0, momentum=0.0):
+    lib().orc_rmsprop_step(_p(p), _p(_f(g)), _p(v), _p(buf), p.size, lr, alpha, eps, wd, momentum)
+
+
+def adagrad_step(p, g, acc, lr, eps=1e-10, wd=0.0):
+    lib().orc_adagrad_step(_p(p), _p(_f(g)), _p(acc), p.size, lr, eps, wd)
+
+
+def nadam_step(p, g, m, v, t, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.0):
+    lib().orc_nadam_step(_p(p), _p(_f(g)), _p(m), _p(v), p.size, lr, b1, b2, eps, wd, int(t))
+
+
+def radam_step(p, g, m, v, t, lr, b1=0.9, b2=0.999, eps=1e-8, wd=0.0) -> bool:
+    return bool(lib().orc_radam_step(_p(p), _p(_f(g)), _p(m), _p(v), p.size, lr, b1, b2, eps, wd,
+                                     int(t)))
+
+
+def adadelta_step(p, g, eg, ed, rho=0.95, eps=1e-6, wd=0.0):
+    lib().orc_adadelta_step(_p(p), _p(_f(g)), _p(eg), _p(ed), p.size, rho, eps, wd)
+
+
+def adabound_step(p, g, m, v, t, lr, final_lr=0.1, b1=0.9, b2=0.999, eps=1e-8, wd=0.0,
+                  gamma=0.001):
+    lib().orc_adabound_step(_p(p), _p(_f(g)), _p(m), _p(v), p.size, lr, final_lr, b1, b2, eps,
+                            wd, gamma, int(t))
+
+
+def rprop_step(p, g, step, prev, eta_plus=1.2, eta_minus=0.5, lr_min=1e-6, lr_max=50.0):
+    lib().orc_rprop_step(_p(p), _p(_f(g)), _p(step), _p(prev), p.size, eta_plus, eta_minus,
+                         lr_min, lr_max)
+
+
+def lamb_step(p, g, m, v, t, lr, b1=0.9, b2=0.999, eps=1e-6, wd=0.01) -> np.float32:
+    u = np.empty_like(p)
+    return np.float32(lib().orc_lamb_step(_p(p), _p(_f(g)), _p(m), _p(v), _p(u), p.size, lr, b1,
+                                          b2, eps, wd, int(t)))
+
+
+def lookahead_sync(fast, slow, alpha):
+    lib().orc_lookahead_sync(_p(fast), _p(slow), fast.size, alpha)
+
+
+def dot_seq(a, b) -> np.float32:
+    a, b = _f(a), _f(b)
+    return np.float32(lib().orc_dot_seq(_p(a), _p(b), a.size))
+
+
+class Scheduler:
+    """optim/schedulers.rs restated over a plain learning-rate value."""
+
+    def __init__(self, kind: str, *args):
+        self.kind, self.args = kind, args
+        self.st = np.zeros(6, np.float32)
+
+    def step(self, lr, metric=None) -> np.float32:
+        L, st, a = lib(), _p(self.st), self.args
+        if self.kind == "step":
+            return np.float32(L.orc_sched_step_lr(st, lr, int(a[0]), a[1]))
+        if self.kind == "exponential":
+            return np.float32(L.orc_sched_exponential(st, lr, a[0]))
+        if self.kind == "cosine":
+            return np.float32(L.orc_sched_cosine(st, lr, int(a[0]), a[1]))
+        if self.kind == "plateau":
+            return np.float32(L.orc_sched_plateau(st, lr, metric, a[0], int(a[1]), a[2]))
+        if self.kind == "warmup":
+            return np.float32(L.orc_sched_warmup(st, lr, int(a[0]), a[1]))
+        raise ValueError(self.kind)
+
+
+class LBFGS:
+    """L-BFGS over flattened parameters, optim/lbfgs.rs:38-212: two-loop
+    recursion with f32 scalars and sequential f32 dot products (orc_dot_seq)."""
+
+    def __init__(self, lr=1.0, history_size=10):
+        self.lr, self.h = np.float32(lr), history_size
+        self.s, self.y = [], []
+        self.prev_p = self.prev_g = None
+
+    def _dir(self, g):
+        f = np.float32
+        if not self.s:
+            return -g
+        m = len(self.s)
+        q = g.copy()
+        alpha, rho = [f(0)] * m, [f(0)] * m
+        for i in reversed(range(m)):
+            rho[i] = f(1.0) / max(dot_seq(self.y[i], self.s[i]), f(1e-10))
+            alpha[i] = rho[i] * dot_seq(self.s[i], q)
+            q = (q - alpha[i] * self.y[i]).astype(np.float32)
+        gamma = dot_seq(self.s[-1], self.y[-1]) / max(dot_seq(self.y[-1], self.y[-1]), f(1e-10))
+        r = (gamma * q).astype(np.float32)
+        for i in range(m):
+            beta = rho[i] * dot_seq(self.y[i], r)
+            r = (r + self.s[i] * f(alpha[i] - beta)).astype(np.float32)
+        return -r
+
+    def step(self, params: list, grads: list) -> None:
+        cur_p = np.concatenate([x.ravel() for x in params]).astype(np.float32)
+        cur_g = np.concatenate([x.ravel() for x in grads]).astype(np.float32)
+        if self.prev_p is not None:
+            s = (cur_p - self.prev_p).astype(np.float32)
+            y = (cur_g - self.prev_g).astype(np.float32)
+            if dot_seq(s, y) > np.float32(1e-10):
+                self.s.append(s)
+                self.y.append(y)
+                if len(self.s) > self.h:
+                    self.s.pop(0)
+                    self.y.pop(0)
+        d = self._dir(cur_g)
+        off = 0
+        for x in params:
+            n = x.size
+            x.ravel()[:] = (x.ravel() + self.lr * d[off:off + n]).astype(np.float32)
+            off += n
+        self.prev_p, self.prev_g = cur_p, cur_g
 
 
 # --- integer paths ----------------------------------------------------------------
