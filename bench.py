@@ -40,28 +40,44 @@ def randn(rng, shape):
     return rng.standard_normal(shape, dtype=np.float32)
 
 
+class QueueAhead:
+    """GPU work queued in front of a timed region: four 2048^3 matmul_backward
+    launches (about 1.2 ms) keep the GPU busy while the host enqueues the
+    region's launches, so the region measures back-to-back kernels and never
+    the host's launch rate."""
+
+    def __init__(self, ctx, rng):
+        n = 2048
+        self.ctx = ctx
+        self.bufs = [ctx.to_device(randn(rng, (n, n))) for _ in range(3)]
+        self.outs = [ctx.empty((n, n)) for _ in range(2)]
+
+    def __call__(self) -> None:
+        dC, A, B = self.bufs
+        for _ in range(4):
+            self.ctx.matmul_backward(dC, A, B, self.outs[0], self.outs[1])
+
+
+_AHEAD = None
+
+
 def time_launches(ctx, launch, steps: int, warmup: int):
-    """Runs `launch` warmup times, then `steps` times inside one timed region
-    (event slots 0/1) on the context's stream -- the stream the kernels run
-    on.  The first min(steps, 127) launches also get their own event pair
-    (slots 2.., read only after the region, so the host never stalls the
-    stream).  Returns (total ms of the region, mean per-launch ms)."""
+    """Runs `launch` warmup times, then `steps` times back to back inside one
+    timed region (HIP events in slots 0/1 on the context's stream, the stream
+    the kernels run on), queued behind QueueAhead's work.  Returns (total ms
+    of the region, mean ms per launch)."""
     for _ in range(warmup):
         launch()
     ctx.sync()
-    paired = min(steps, 127)
+    if _AHEAD is not None:
+        _AHEAD()
     ctx.timer_record(0)
-    for i in range(steps):
-        if i < paired:
-            ctx.timer_record(2 + 2 * i)
+    for _ in range(steps):
         launch()
-        if i < paired:
-            ctx.timer_record(3 + 2 * i)
     ctx.timer_record(1)
     ctx.sync()
     total = ctx.timer_elapsed_ms(0, 1)
-    per = [ctx.timer_elapsed_ms(2 + 2 * i, 3 + 2 * i) for i in range(paired)]
-    return total, float(np.mean(per))
+    return total, total / steps
 
 
 def traffic_from_profile(name: str):
@@ -337,6 +353,292 @@ def cpu_baseline(A, B, dC, rows_a: int, rows_b: int):
     }
 
 
+ROW_ELEMS = (4096, 4096)  # BASELINE configs[2] (C3), the elementwise/broadcast config
+
+
+def _cpu_time(fn, reps: int = 1) -> float:
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
+    """One measurement per hot-path row: the kernel behind each backward
+    function at a BASELINE-config shape, timed as back-to-back launches between
+    HIP events on the library's stream, against the roofline that bounds it;
+    beside it the
+    numrs CPU algorithm (the oracle's C restatement, one thread) on a bounded
+    sample of the same input, scaled to the full size, and a check of the GPU
+    output against that same oracle output on the sample."""
+    from numrs_amd import _lib as L
+    from oracle import oracle as O
+
+    out = []
+
+    def f32(shape, scale=1.0):
+        return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+    def record(row, fn_name, kernel, shape, bytes_=None, flops=None, launch=None,
+               cpu_fn=None, cpu_scale=1.0, cpu_sample="", check=None, note=""):
+        total, per = time_launches(ctx, launch, steps, warmup)
+        ent = {"row": row, "function": fn_name, "kernel": kernel, "shape": shape,
+               "kernel_us": round(per * 1e3, 2)}
+        if bytes_ is not None:
+            gbs = bytes_ / (per * 1e-3) / 1e9
+            ent.update({"bound": "hbm", "algorithmic_bytes": int(bytes_),
+                        "achieved": round(gbs, 1), "unit": "GB/s",
+                        "frac": round(gbs / PEAK_HBM_GBS, 4)})
+        else:
+            tf = flops / (per * 1e-3) / 1e12
+            ent.update({"bound": "mfma", "algorithmic_flops": int(flops),
+                        "achieved": round(tf, 2), "unit": "TFLOP/s",
+                        "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)})
+        if cpu and cpu_fn is not None:
+            t = _cpu_time(cpu_fn) * cpu_scale
+            ent["cpu_baseline"] = {"us": round(t * 1e6, 1), "kind": "port", "cores": 1,
+                                   "sample": cpu_sample}
+            ent["gpu_vs_cpu"] = round(t / (per * 1e-3), 1)
+        elif cpu:
+            ent["cpu_baseline"] = None
+        if check is not None:
+            ent["sample_ok"] = bool(check())
+        if note:
+            ent["note"] = note
+        out.append(ent)
+        log(f"  {row:4s} {fn_name:28s} {ent['kernel_us']:9.2f} us  {ent['achieved']:9.1f} "
+            f"{ent['unit']}  frac {ent['frac']:.3f}")
+
+    def same_bits(a, b):
+        return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+    def close(a, b, rtol=1e-5, atol=1e-6):
+        return np.allclose(np.asarray(a, np.float64), np.asarray(b, np.float64), rtol=rtol,
+                           atol=atol)
+
+    R, C = ROW_ELEMS
+    n = R * C
+    ns = 1 << 20  # CPU sample: the first 1,048,576 elements
+    scale = n / ns
+    samp = f"first {ns:,} of {n:,} elements, scaled x{scale:g}"
+    g, x, y = f32((R, C)), f32((R, C)), f32((R, C))
+    g_, x_, y_ = ctx.to_device(g), ctx.to_device(x), ctx.to_device(y)
+    dx_, dy_ = ctx.empty((R, C)), ctx.empty((R, C))
+    shape = f"[{R},{C}] (C3)"
+
+    # a3 accumulate_gradient: g += incoming (tensor.rs:120-132)
+    acc_ = ctx.to_device(y)
+    record("a3", "accumulate_gradient", "binary_backward(ADD, acc)", shape, bytes_=12.0 * n,
+           launch=lambda: ctx.binary_backward(L.ADD, g_, None, None, acc_, None, accumulate=True),
+           cpu_fn=lambda: O.accumulate(y.ravel()[:ns].copy(), g.ravel()[:ns]), cpu_scale=scale,
+           cpu_sample=samp)
+    # a7 sub_backward: dx = g, dy = -g
+    record("a7", "sub_backward", "binary_backward(SUB)", shape, bytes_=12.0 * n,
+           launch=lambda: ctx.binary_backward(L.SUB, g_, None, None, dx_, dy_),
+           cpu_fn=lambda: O.sub_backward(g.ravel()[:ns]), cpu_scale=scale, cpu_sample=samp,
+           check=lambda: same_bits(dy_.numpy().ravel()[:ns], O.sub_backward(g.ravel()[:ns])[1]))
+    # a8 mul_backward: dx = g*y, dy = g*x
+    record("a8", "mul_backward", "binary_backward(MUL)", shape, bytes_=20.0 * n,
+           launch=lambda: ctx.binary_backward(L.MUL, g_, x_, y_, dx_, dy_),
+           cpu_fn=lambda: O.mul_backward(g.ravel()[:ns], x.ravel()[:ns], y.ravel()[:ns]),
+           cpu_scale=scale, cpu_sample=samp,
+           check=lambda: same_bits(dx_.numpy().ravel()[:ns],
+                                   O.mul_backward(g.ravel()[:ns], x.ravel()[:ns],
+                                                  y.ravel()[:ns])[0]))
+    # a9 div_backward: dx = g/y, dy = -g*x/y^2
+    record("a9", "div_backward", "binary_backward(DIV)", shape, bytes_=20.0 * n,
+           launch=lambda: ctx.binary_backward(L.DIV, g_, x_, y_, dx_, dy_),
+           cpu_fn=lambda: O.div_backward(g.ravel()[:ns], x.ravel()[:ns], y.ravel()[:ns]),
+           cpu_scale=scale, cpu_sample=samp,
+           check=lambda: same_bits(dy_.numpy().ravel()[:ns],
+                                   O.div_backward(g.ravel()[:ns], x.ravel()[:ns],
+                                                  y.ravel()[:ns])[1]))
+    # a13-a15, a21, N1 unary grads: read g and the saved value, write dx
+    pos = np.abs(x) + np.float32(0.5)
+    pos_ = ctx.to_device(pos)
+    sig = (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+    sig_ = ctx.to_device(sig)
+    th = np.tanh(x).astype(np.float32)
+    th_ = ctx.to_device(th)
+    for row, name, kind, v, v_, ofn, exact in [
+            ("a13", "sigmoid_backward", L.SIGMOID, sig, sig_, O.sigmoid_backward, True),
+            ("a14", "tanh_backward", L.TANH, th, th_, O.tanh_backward, True),
+            ("a15", "exp_backward", L.EXP, pos, pos_, O.exp_backward, True),
+            ("a15", "log_backward", L.LOG, pos, pos_, O.log_backward, True),
+            ("a21", "sqrt_backward", L.SQRT, pos, pos_, O.sqrt_backward, False),
+            ("N1", "gelu_backward (new op)", L.GELU, x, x_, None, False)]:
+        vs = v.ravel()[:ns]
+        if ofn is not None:
+            cfn = (lambda ofn=ofn, vs=vs: ofn(g.ravel()[:ns], vs))
+            chk = (lambda ofn=ofn, vs=vs, exact=exact:
+                   (same_bits if exact else close)(dx_.numpy().ravel()[:ns],
+                                                   ofn(g.ravel()[:ns], vs)))
+        else:
+            cfn = None
+            chk = (lambda vs=vs: close(dx_.numpy().ravel()[:ns],
+                                       O.gelu_backward(g.ravel()[:ns], vs), 1e-5, 1e-6))
+        record(row, name, f"unary_backward({name.split('_')[0].upper()})", shape,
+               bytes_=12.0 * n,
+               launch=(lambda kind=kind, v_=v_: ctx.unary_backward(kind, g_, v_, dx_)),
+               cpu_fn=cfn, cpu_scale=scale, cpu_sample=samp, check=chk,
+               note="" if ofn is not None else "no numrs CPU path: the reference has no GELU")
+    record("a21", "pow_backward (n=3)", "unary_backward(POW)", shape, bytes_=12.0 * n,
+           launch=lambda: ctx.unary_backward(L.POW, g_, x_, dx_, 3.0),
+           cpu_fn=lambda: O.pow_backward(g.ravel()[:ns], x.ravel()[:ns], 3.0), cpu_scale=scale,
+           cpu_sample=samp,
+           check=lambda: close(dx_.numpy().ravel()[:ns],
+                               O.pow_backward(g.ravel()[:ns], x.ravel()[:ns], 3.0), 1e-5, 1e-5))
+    # a11 transpose_backward: dX = dY^T (8 B/elem)
+    tr_ = ctx.empty((C, R))
+    rs = ns // C
+    record("a11", "transpose_backward", "transpose_kernel", shape, bytes_=8.0 * n,
+           launch=lambda: ctx._check(L.load().numrs_hip_transpose(ctx.handle, g_.ptr, tr_.ptr,
+                                                                    R, C)),
+           cpu_fn=lambda: O.transpose(g[:rs]), cpu_scale=R / rs,
+           cpu_sample=f"first {rs} of {R} rows, scaled x{R / rs:g}",
+           check=lambda: same_bits(tr_.numpy()[:, :rs], O.transpose(g[:rs])))
+    del tr_
+    # a16/a17 sum/mean backward: fill with g[0] (or g[0]/n), 4 B/elem
+    g1_ = ctx.to_device(np.array([0.75], np.float32))
+    record("a17", "mean_backward", "fill_grad", shape, bytes_=4.0 * n,
+           launch=lambda: ctx.fill_grad(g1_, dx_, divide_by_n=True),
+           cpu_fn=lambda: O.mean_backward(0.75, (ns,)), cpu_scale=scale, cpu_sample=samp,
+           check=lambda: same_bits(dx_.numpy().ravel()[:16], O.mean_backward(0.75, (n,))[:16]))
+    # a25 ops::sum over all elements (4 B/elem)
+    s_ = ctx.empty((1,))
+    record("a25", "ops::sum (full)", "reduce_pass1+final", shape, bytes_=4.0 * n,
+           launch=lambda: ctx._check(L.load().numrs_hip_sum(ctx.handle, g_.ptr, n, 0, s_.ptr)),
+           cpu_fn=lambda: O.sum_avx2_order(g.ravel()[:ns]), cpu_scale=scale,
+           cpu_sample=samp + " (8-lane order of simd.rs:247-283, one thread)",
+           check=lambda: abs(float(s_.numpy()[0]) - float(g.astype(np.float64).sum()))
+           <= 1e-3 * np.sqrt(n))
+    # a5 unbroadcast to a bias: [R, C] -> [C] column reduce (4 B/elem)
+    b_ = ctx.empty((C,))
+    record("a5", "unbroadcast (bias, CORRECT)", "colreduce_pass1+finalize", shape,
+           bytes_=4.0 * n + 4.0 * C,
+           launch=lambda: ctx.sum_to_shape(g_, b_),
+           cpu_fn=lambda: O.sum_avx2_order(g.ravel()[:ns]), cpu_scale=scale,
+           cpu_sample=samp + " (numrs reduces with ops::sum, backward.rs:12-39)",
+           check=lambda: close(b_.numpy(), g.astype(np.float64).sum(0), 1e-4, 1e-3))
+    del acc_, pos_, sig_, th_
+    # a18 mse_backward at C4's output [4096, 512] (dp only: 12 B/elem)
+    p, t = f32((4096, 512)), f32((4096, 512))
+    p_, t_, dp_ = ctx.to_device(p), ctx.to_device(t), ctx.empty((4096, 512))
+    record("a18", "mse_backward", "mse_backward_kernel", "[4096,512] (C4 output)",
+           bytes_=12.0 * p.size,
+           launch=lambda: ctx.mse_backward(g1_, p_, t_, dp_),
+           cpu_fn=lambda: O.mse_backward(0.75, p, t), cpu_sample="whole input",
+           check=lambda: same_bits(dp_.numpy(), O.mse_backward(0.75, p, t)[0]))
+    del p_, t_, dp_
+    # a19 cross_entropy_backward, one-hot target (12 B/elem)
+    B_, C_ = 16384, 1024
+    logits = f32((B_, C_), 2.0)
+    lab = rng.integers(0, C_, B_)
+    onehot = np.zeros((B_, C_), np.float32)
+    onehot[np.arange(B_), lab] = 1.0
+    lg_, oh_, dl_ = ctx.to_device(logits), ctx.to_device(onehot), ctx.empty((B_, C_))
+    record("a19", "cross_entropy_backward", "softmax_ce_backward", f"[{B_},{C_}] one-hot",
+           bytes_=12.0 * B_ * C_,
+           launch=lambda: ctx.softmax_ce_backward(g1_, lg_, dl_, onehot=oh_),
+           cpu_fn=lambda: O.cross_entropy_backward(0.75, logits[:512], onehot[:512]),
+           cpu_scale=B_ / 512, cpu_sample=f"first 512 of {B_} rows, scaled x{B_ / 512:g}",
+           check=lambda: close(dl_.numpy()[:512],
+                               O.cross_entropy_backward(0.75, logits[:512], onehot[:512]) *
+                               np.float32(512 / B_), 1e-5, 1e-7),
+           note="C1's [64,10] is latency-bound; C3's element count shows the roofline")
+    del lg_, oh_, dl_
+    # a20 softmax_backward over C4's attention probabilities [128*256, 256]
+    rows_s = 16 * 8 * 256
+    sm = O.softmax_rows(f32((rows_s, 256)))
+    gs = f32((rows_s, 256))
+    sm_, gs_, ds_ = ctx.to_device(sm), ctx.to_device(gs), ctx.empty((rows_s, 256))
+    record("a20", "softmax_backward", "softmax_backward_kernel", "[32768,256] (C4 attention)",
+           bytes_=12.0 * sm.size,
+           launch=lambda: ctx.softmax_backward(sm_, gs_, ds_),
+           cpu_fn=lambda: O.softmax_backward(sm[:4096], gs[:4096]), cpu_scale=rows_s / 4096,
+           cpu_sample=f"first 4096 of {rows_s} rows, scaled x{rows_s / 4096:g}",
+           check=lambda: close(ds_.numpy()[:4096], O.softmax_backward(sm[:4096], gs[:4096]),
+                               1e-5, 1e-6))
+    del sm_, gs_, ds_
+    # N2 layernorm backward: C4's row width 512, C3's element count
+    RL = 32768
+    xl, gl = f32((RL, 512)), f32((RL, 512))
+    gam = (1.0 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    _, mean, rstd = O.layernorm_fwd(xl, gam, np.zeros(512, np.float32))
+    xl_, gl_, gam_ = ctx.to_device(xl), ctx.to_device(gl), ctx.to_device(gam)
+    mean_, rstd_ = ctx.to_device(mean), ctx.to_device(rstd)
+    dxl_, dgm_, dbt_ = ctx.empty((RL, 512)), ctx.empty((512,)), ctx.empty((512,))
+    record("N2", "layernorm_backward (new op)", "layernorm_bwd_vec+finalize",
+           f"[{RL},512] (C4 rows of 512; C3 element count)", bytes_=12.0 * xl.size + 8.0 * RL,
+           launch=lambda: ctx._check(L.load().numrs_hip_layernorm_backward(
+               ctx.handle, gl_.ptr, xl_.ptr, gam_.ptr, mean_.ptr, rstd_.ptr, dxl_.ptr, dgm_.ptr,
+               dbt_.ptr, RL, 512, 0, 0, 0)),
+           check=lambda: close(dxl_.numpy()[:4096],
+                               O.layernorm_backward(gl[:4096], xl[:4096], gam)[0], 1e-4, 1e-5),
+           note="no numrs CPU path: the reference has no LayerNorm; C4's own [4096,512] "
+                "is 8 MB per operand and latency-bound")
+    del xl_, gl_, gam_, mean_, rstd_, dxl_, dgm_, dbt_
+    # N5 argmax over rows (int result; 4 B/elem + 4 B/row)
+    am = f32((16384, 1024))
+    am_, idx_ = ctx.to_device(am), ctx.empty((16384,), np.int32)
+    record("N5", "argmax (rows, first max)", "argmax_vec", "[16384,1024]",
+           bytes_=4.0 * am.size + 4.0 * 16384,
+           launch=lambda: ctx.argmax_rows(am_, idx_),
+           cpu_fn=lambda: O.argmax_rows(am[:512]), cpu_scale=32.0,
+           cpu_sample="first 512 of 16384 rows, scaled x32",
+           check=lambda: np.array_equal(idx_.numpy(), O.argmax_rows(am)),
+           note="C1's [64,10] is latency-bound; C3's element count shows the roofline")
+    del am_, idx_
+    # a23 SGD step (mu = 0): read p, g, write p (12 B/elem)
+    nsgd = 1 << 24
+    ps, gsg = f32(nsgd), f32(nsgd)
+    ps_, gsg_ = ctx.to_device(ps), ctx.to_device(gsg)
+    record("a23", "SGD::step (mu=0)", "sgd_kernel", "16,777,216 params", bytes_=12.0 * nsgd,
+           launch=lambda: ctx.sgd_step(ps_, gsg_, lr=0.01),
+           cpu_fn=lambda: O.sgd_step(ps[:ns].copy(), gsg[:ns], None, 0.01), cpu_scale=nsgd / ns,
+           cpu_sample=f"first {ns:,} of {nsgd:,} params, scaled x{nsgd / ns:g}")
+    del ps_, gsg_
+    # a26 Linear::forward at C4's FFN up-projection: y[4096,2048] = x[4096,512] W^T + b
+    T_, In, Out = 4096, 512, 2048
+    xw, W, bb = f32((T_, In)), f32((Out, In), 0.05), f32(Out)
+    xw_, W_, bb_, yw_ = ctx.to_device(xw), ctx.to_device(W), ctx.to_device(bb), ctx.empty((T_, Out))
+    record("a26", "Linear::forward (fused)", "gemm (bias epilogue)", "[4096,512]x[512,2048]",
+           flops=2.0 * T_ * In * Out,
+           launch=lambda: ctx._check(L.load().numrs_hip_linear_forward(
+               ctx.handle, xw_.ptr, W_.ptr, bb_.ptr, yw_.ptr, T_, In, Out)),
+           check=lambda: close(yw_.numpy()[:64], xw[:64].astype(np.float64) @
+                               W.T.astype(np.float64) + bb, 1e-4, 1e-4),
+           note="numrs runs this forward through MKL sgemm; no CPU port here")
+    # a26 backward of the same layer: dx = g W, dW = g^T x, db = colsum(g)
+    gw = f32((T_, Out))
+    gw_, dxw_, dW_, db_ = ctx.to_device(gw), ctx.empty((T_, In)), ctx.empty((Out, In)), ctx.empty((Out,))
+    record("a10+a11+a5", "Linear backward (fused)", "gemm_pair + colreduce",
+           "[4096,512]x[512,2048]", flops=4.0 * T_ * In * Out,
+           launch=lambda: ctx._check(L.load().numrs_hip_linear_backward(
+               ctx.handle, gw_.ptr, xw_.ptr, W_.ptr, dxw_.ptr, dW_.ptr, db_.ptr, T_, In, Out,
+               0, 0, 0, L.UNBROADCAST_CORRECT)),
+           check=lambda: close(dxw_.numpy()[:64], gw[:64].astype(np.float64) @ W, 1e-4, 1e-4))
+    del xw_, W_, bb_, yw_, gw_, dxw_, dW_, db_
+    # N3 attention backward at C4: 128 heads of 256x256x64
+    Bq, Sq, Hq, Dq = 16, 256, 8, 512
+    q, k, v, do = (f32((Bq * Sq, Dq), 0.5) for _ in range(4))
+    q_, k_, v_, do_ = (ctx.to_device(a) for a in (q, k, v, do))
+    P_ = ctx.empty((Bq * Hq, Sq, Sq))
+    o_ = ctx.empty((Bq * Sq, Dq))
+    ctx._check(L.load().numrs_hip_attention_forward(ctx.handle, q_.ptr, k_.ptr, v_.ptr, P_.ptr,
+                                                    o_.ptr, Bq, Sq, Hq, Dq))
+    dq_, dk_, dv_ = (ctx.empty((Bq * Sq, Dq)) for _ in range(3))
+    dh = Dq // Hq
+    record("N3", "attention backward (new op)", "gemm (batched) + softmax_backward",
+           "16x256, 8 heads of 64", flops=4 * 2.0 * Bq * Hq * Sq * Sq * dh,
+           launch=lambda: ctx._check(L.load().numrs_hip_attention_backward(
+               ctx.handle, q_.ptr, k_.ptr, v_.ptr, P_.ptr, do_.ptr, dq_.ptr, dk_.ptr, dv_.ptr,
+               Bq, Sq, Hq, Dq, 0)),
+           note="four batched products + row softmax backward; no numrs CPU path")
+    del q_, k_, v_, do_, P_, o_, dq_, dk_, dv_
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -346,6 +648,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-rows-a", type=int, default=512)
     ap.add_argument("--cpu-rows-b", type=int, default=192)
+    ap.add_argument("--rows", action="store_true",
+                    help="measure every hot-path row's kernel instead (one JSON line per row)")
     ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -378,9 +682,18 @@ def main() -> int:
     n_cus, arch = ctx.info()
     log(f"device {arch}, {n_cus} CUs")
     rng = np.random.default_rng(SEED)
+    global _AHEAD
+    if not args.traffic_probe:
+        _AHEAD = QueueAhead(ctx, np.random.default_rng(SEED + 1))
 
     if args.traffic_probe:
         traffic_probe(ctx, rng)
+        ctx.close()
+        return 0
+
+    if args.rows:
+        for ent in bench_rows(ctx, rng, args.steps, args.warmup, cpu=not args.no_cpu_baseline):
+            print(json.dumps(ent), flush=True)
         ctx.close()
         return 0
 

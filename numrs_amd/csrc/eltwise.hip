@@ -23,6 +23,32 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // Unary backward: dx = g * f'(v)
 // ---------------------------------------------------------------------------
 
+// powf(v, -0.5) as 1/sqrt(v): both operations are correctly rounded, so the
+// result is within an ulp of powf's, at a fraction of the cost of the general
+// powf.  powf's special cases are kept: +-0 -> +inf (sqrtf(-0) is -0),
+// -inf -> +0 (sqrtf(-inf) is NaN), +inf -> +0, other negatives and NaN -> NaN.
+__device__ __forceinline__ float pow_neg_half(float v) {
+  if (v == 0.0f) return INFINITY;
+  if (v == -INFINITY) return 0.0f;
+  return 1.0f / sqrtf(v);
+}
+
+// powf(v, e) with the exponents that pow_backward meets most (x^2 and x^3
+// layers, reciprocals) evaluated without the general powf.  Each shortcut
+// returns exactly what a correctly rounded powf returns, special values
+// included: e = 0 -> 1 (also for NaN), e = 1 -> v, e = 2 -> v*v (one rounding
+// of the exact square), e = -1 -> 1/v (+-0 -> +-inf), e = -0.5 as above.
+// Other exponents use powf.  e is the same for every thread, so the branch is
+// uniform.
+__device__ __forceinline__ float pow_grad_base(float v, float e) {
+  if (e == 2.0f) return v * v;
+  if (e == 1.0f) return v;
+  if (e == 0.0f) return 1.0f;
+  if (e == -1.0f) return 1.0f / v;
+  if (e == -0.5f) return pow_neg_half(v);
+  return powf(v, e);
+}
+
 template <int KIND>
 __device__ __forceinline__ float unary_grad(float g, float v, float p) {
   if constexpr (KIND == NUMRS_HIP_RELU) {
@@ -40,7 +66,7 @@ __device__ __forceinline__ float unary_grad(float g, float v, float p) {
     const float pdf = 0.39894228040143268f * expf(-0.5f * v * v);
     return g * (cdf + v * pdf);
   } else if constexpr (KIND == NUMRS_HIP_SQRT) {
-    return g * (powf(v, -0.5f) * 0.5f);  // backward.rs:452-460
+    return g * (pow_neg_half(v) * 0.5f);  // backward.rs:452-460
   } else if constexpr (KIND == NUMRS_HIP_SIN) {
     return g * cosf(v);  // backward.rs:469-470
   } else if constexpr (KIND == NUMRS_HIP_COS) {
@@ -48,7 +74,47 @@ __device__ __forceinline__ float unary_grad(float g, float v, float p) {
   } else if constexpr (KIND == NUMRS_HIP_TAN) {
     return g * (1.0f + v * v);  // backward.rs:491-498
   } else {  // NUMRS_HIP_POW
-    return g * (powf(v, p - 1.0f) * p);  // backward.rs:427-435
+    return g * (pow_grad_base(v, p - 1.0f) * p);  // backward.rs:427-435
+  }
+}
+
+// One thread's 8 elements (two float4 groups kBlock*4 apart); threads whose
+// groups both lie inside the array issue every load before any store.
+template <int KIND, bool VEC, bool ACC>
+__device__ __forceinline__ void unary_bwd_body(const float *__restrict__ g,
+                                               const float *__restrict__ v,
+                                               float *__restrict__ dx, int64_t n, float p) {
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+  const int64_t last = base + (int64_t)(kVecPerThread - 1) * kBlock * 4;
+  if (VEC && last + 3 < n) {
+    f4 gv[kVecPerThread], vv[kVecPerThread], ov[kVecPerThread];
+#pragma unroll
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int64_t i = base + (int64_t)u * kBlock * 4;
+      gv[u] = *reinterpret_cast<const f4 *>(g + i);
+      vv[u] = *reinterpret_cast<const f4 *>(v + i);
+      if (ACC) ov[u] = *reinterpret_cast<const f4 *>(dx + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int64_t i = base + (int64_t)u * kBlock * 4;
+      f4 r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = unary_grad<KIND>(gv[u][e], vv[u][e], p);
+      *reinterpret_cast<f4 *>(dx + i) = ACC ? ov[u] + r : r;
+    }
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (i + e < n) {
+        const float r = unary_grad<KIND>(g[i + e], v[i + e], p);
+        dx[i + e] = ACC ? dx[i + e] + r : r;
+      }
+    }
   }
 }
 
@@ -56,28 +122,8 @@ template <int KIND, bool VEC>
 __global__ void __launch_bounds__(kBlock)
     unary_bwd_kernel(const float *__restrict__ g, const float *__restrict__ v,
                      float *__restrict__ dx, int64_t n, float p, int acc) {
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
-#pragma unroll
-  for (int u = 0; u < kVecPerThread; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock * 4;
-    if (VEC && i + 3 < n) {
-      const f4 gv = *reinterpret_cast<const f4 *>(g + i);
-      const f4 vv = *reinterpret_cast<const f4 *>(v + i);
-      f4 r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = unary_grad<KIND>(gv[e], vv[e], p);
-      if (acc) r += *reinterpret_cast<const f4 *>(dx + i);
-      *reinterpret_cast<f4 *>(dx + i) = r;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (i + e < n) {
-          float r = unary_grad<KIND>(g[i + e], v[i + e], p);
-          dx[i + e] = acc ? dx[i + e] + r : r;
-        }
-      }
-    }
-  }
+  if (acc) unary_bwd_body<KIND, VEC, true>(g, v, dx, n, p);
+  else unary_bwd_body<KIND, VEC, false>(g, v, dx, n, p);
 }
 
 template <int KIND>
@@ -115,31 +161,102 @@ __device__ __forceinline__ void binary_grad(float g, float x, float y, float &dx
   }
 }
 
-template <int KIND>
+// One thread's 8 elements with the outputs present (DX, DY) and the
+// accumulate flag (ACC) fixed at compile time: every load is then issued
+// before the first store, instead of being sunk into the branches that use it.
+// One thread's 8 elements (two float4 groups kBlock*4 apart) with the
+// outputs present (DX, DY) and the accumulate flag (ACC) fixed at compile
+// time.  Threads whose groups both lie inside the array issue every load
+// before any store; the last block's ragged end goes element by element.
+template <int KIND, bool VEC, bool DX, bool DY, bool ACC>
+__device__ __forceinline__ void binary_bwd_body(const float *__restrict__ g,
+                                                const float *__restrict__ x,
+                                                const float *__restrict__ y,
+                                                float *__restrict__ dx, float *__restrict__ dy,
+                                                int64_t n) {
+  constexpr bool kReadsXY = KIND == NUMRS_HIP_MUL || KIND == NUMRS_HIP_DIV;
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+  const int64_t last = base + (int64_t)(kVecPerThread - 1) * kBlock * 4;
+  if (VEC && last + 3 < n) {
+    f4 gv[kVecPerThread], xv[kVecPerThread], yv[kVecPerThread], ov[kVecPerThread],
+        pv[kVecPerThread];
+#pragma unroll
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int64_t i = base + (int64_t)u * kBlock * 4;
+      gv[u] = *reinterpret_cast<const f4 *>(g + i);
+      if (kReadsXY) {
+        xv[u] = *reinterpret_cast<const f4 *>(x + i);
+        yv[u] = *reinterpret_cast<const f4 *>(y + i);
+      } else {
+        xv[u] = yv[u] = f4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (ACC && DX) ov[u] = *reinterpret_cast<const f4 *>(dx + i);
+      if (ACC && DY) pv[u] = *reinterpret_cast<const f4 *>(dy + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int64_t i = base + (int64_t)u * kBlock * 4;
+      f4 a, b;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float ae, be;
+        binary_grad<KIND>(gv[u][e], xv[u][e], yv[u][e], ae, be);
+        a[e] = ae;
+        b[e] = be;
+      }
+      if (DX) *reinterpret_cast<f4 *>(dx + i) = ACC ? ov[u] + a : a;
+      if (DY) *reinterpret_cast<f4 *>(dy + i) = ACC ? pv[u] + b : b;
+    }
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t k = i + e;
+      if (k < n) {
+        const float xe = kReadsXY ? x[k] : 0.0f;
+        const float ye = kReadsXY ? y[k] : 0.0f;
+        float a, b;
+        binary_grad<KIND>(g[k], xe, ye, a, b);
+        if (DX) dx[k] = ACC ? dx[k] + a : a;
+        if (DY) dy[k] = ACC ? dy[k] + b : b;
+      }
+    }
+  }
+}
+
+template <int KIND, bool VEC>
 __global__ void __launch_bounds__(kBlock)
     binary_bwd_kernel(const float *__restrict__ g, const float *__restrict__ x,
                       const float *__restrict__ y, float *__restrict__ dx, float *__restrict__ dy,
                       int64_t n, int acc) {
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x;
-#pragma unroll
-  for (int u = 0; u < 4 * kVecPerThread; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
-    if (i < n) {
-      const float xv = (KIND == NUMRS_HIP_MUL || KIND == NUMRS_HIP_DIV) ? x[i] : 0.0f;
-      const float yv = (KIND == NUMRS_HIP_MUL || KIND == NUMRS_HIP_DIV) ? y[i] : 0.0f;
-      float a, b;
-      binary_grad<KIND>(g[i], xv, yv, a, b);
-      if (dx) dx[i] = acc ? dx[i] + a : a;
-      if (dy) dy[i] = acc ? dy[i] + b : b;
-    }
+  // The flags are uniform: one branch per thread picks the specialised body.
+  if (dx != nullptr && dy != nullptr) {
+    if (acc) binary_bwd_body<KIND, VEC, true, true, true>(g, x, y, dx, dy, n);
+    else binary_bwd_body<KIND, VEC, true, true, false>(g, x, y, dx, dy, n);
+  } else if (dx != nullptr) {
+    if (acc) binary_bwd_body<KIND, VEC, true, false, true>(g, x, y, dx, dy, n);
+    else binary_bwd_body<KIND, VEC, true, false, false>(g, x, y, dx, dy, n);
+  } else if (dy != nullptr) {
+    if (acc) binary_bwd_body<KIND, VEC, false, true, true>(g, x, y, dx, dy, n);
+    else binary_bwd_body<KIND, VEC, false, true, false>(g, x, y, dx, dy, n);
   }
 }
 
 template <int KIND>
 int launch_binary(numrs_hip_ctx *ctx, const float *g, const float *x, const float *y, float *dx,
                   float *dy, int64_t n, int acc) {
-  binary_bwd_kernel<KIND><<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(g, x, y, dx, dy,
-                                                                                   n, acc);
+  const bool reads_xy = KIND == NUMRS_HIP_MUL || KIND == NUMRS_HIP_DIV;
+  const bool vec = numrs_hip::aligned16(g) && numrs_hip::aligned16(dx) &&
+                   numrs_hip::aligned16(dy) &&
+                   (!reads_xy || (numrs_hip::aligned16(x) && numrs_hip::aligned16(y)));
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  if (vec)
+    binary_bwd_kernel<KIND, true><<<grid, kBlock, 0, ctx->stream>>>(g, x, y, dx, dy, n, acc);
+  else
+    binary_bwd_kernel<KIND, false><<<grid, kBlock, 0, ctx->stream>>>(g, x, y, dx, dy, n, acc);
   return numrs_hip::check_launch(ctx, "binary_bwd_kernel");
 }
 
@@ -147,31 +264,63 @@ int launch_binary(numrs_hip_ctx *ctx, const float *g, const float *x, const floa
 // sum/mean backward fill, MSE backward
 // ---------------------------------------------------------------------------
 
+template <bool VEC>
 __global__ void __launch_bounds__(kBlock)
     fill_grad_kernel(const float *__restrict__ g0, float *__restrict__ dx, int64_t n, float nf,
                      int divide, int acc) {
   const float v = divide ? g0[0] / nf : g0[0];  // backward.rs:213 / :228
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
 #pragma unroll
-  for (int u = 0; u < 4 * kVecPerThread; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
-    if (i < n) dx[i] = acc ? dx[i] + v : v;
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+    if (VEC && i + 3 < n) {
+      f4 r = {v, v, v, v};
+      if (acc) r += *reinterpret_cast<const f4 *>(dx + i);
+      *reinterpret_cast<f4 *>(dx + i) = r;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + e < n) dx[i + e] = acc ? dx[i + e] + v : v;
+    }
   }
 }
 
+template <bool VEC>
 __global__ void __launch_bounds__(kBlock)
     mse_bwd_kernel(const float *__restrict__ g0, const float *__restrict__ p,
                    const float *__restrict__ t, float *__restrict__ dp, float *__restrict__ dt,
                    int64_t n, float nf, int acc) {
   const float gs = g0[0];
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
 #pragma unroll
-  for (int u = 0; u < 4 * kVecPerThread; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
-    if (i < n) {
-      const float v = ((gs * 2.0f) * (p[i] - t[i])) / nf;  // backward.rs:250
-      if (dp) dp[i] = acc ? dp[i] + v : v;
-      if (dt) dt[i] = acc ? dt[i] + (-v) : -v;  // backward.rs:257
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = base + (int64_t)u * kBlock * 4;
+    if (VEC && i + 3 < n) {
+      const f4 pv = *reinterpret_cast<const f4 *>(p + i);
+      const f4 tv = *reinterpret_cast<const f4 *>(t + i);
+      f4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = ((gs * 2.0f) * (pv[e] - tv[e])) / nf;  // backward.rs:250
+      if (dp) {
+        f4 o = v;
+        if (acc) o += *reinterpret_cast<const f4 *>(dp + i);
+        *reinterpret_cast<f4 *>(dp + i) = o;
+      }
+      if (dt) {
+        f4 o = -v;  // backward.rs:257
+        if (acc) o = *reinterpret_cast<const f4 *>(dt + i) + (-v);
+        *reinterpret_cast<f4 *>(dt + i) = o;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t k = i + e;
+        if (k < n) {
+          const float v = ((gs * 2.0f) * (p[k] - t[k])) / nf;  // backward.rs:250
+          if (dp) dp[k] = acc ? dp[k] + v : v;
+          if (dt) dt[k] = acc ? dt[k] + (-v) : -v;  // backward.rs:257
+        }
+      }
     }
   }
 }
@@ -438,8 +587,12 @@ int numrs_hip_fill_grad(numrs_hip_ctx *ctx, const float *g_scalar, float *dx, in
   if (n == 0) return NUMRS_HIP_OK;
   if (g_scalar == nullptr || dx == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_fill_grad: null pointer");
-  fill_grad_kernel<<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(
-      g_scalar, dx, n, (float)n, divide_by_n, accumulate);
+  if (numrs_hip::aligned16(dx))
+    fill_grad_kernel<true><<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(
+        g_scalar, dx, n, (float)n, divide_by_n, accumulate);
+  else
+    fill_grad_kernel<false><<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(
+        g_scalar, dx, n, (float)n, divide_by_n, accumulate);
   return numrs_hip::check_launch(ctx, "fill_grad_kernel");
 }
 
@@ -450,8 +603,15 @@ int numrs_hip_mse_backward(numrs_hip_ctx *ctx, const float *g_scalar, const floa
   if (n == 0 || (dp == nullptr && dt == nullptr)) return NUMRS_HIP_OK;
   if (g_scalar == nullptr || p == nullptr || t == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_backward: null pointer");
-  mse_bwd_kernel<<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt,
-                                                                          n, (float)n, accumulate);
+  const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(t) &&
+                   numrs_hip::aligned16(dp) && numrs_hip::aligned16(dt);
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  if (vec)
+    mse_bwd_kernel<true><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt, n, (float)n,
+                                                           accumulate);
+  else
+    mse_bwd_kernel<false><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt, n, (float)n,
+                                                            accumulate);
   return numrs_hip::check_launch(ctx, "mse_bwd_kernel");
 }
 

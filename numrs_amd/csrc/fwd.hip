@@ -113,25 +113,97 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+// 64 x 64 tiles with float4 global loads and stores, for 16-byte aligned
+// matrices whose dimensions are multiples of 4 (each float4 is then wholly
+// inside or outside the matrix).  Thread t loads rows t/16 + 16i, columns
+// 4(t%16)..+3, and stores output row t/16 + 16i (a column of x), output
+// columns 4(t%16)..+3, read down the LDS tile.  Row stride 65 keeps the
+// column reads spread over the banks.
+__global__ void __launch_bounds__(kBlock)
+    transpose64_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
+                       int64_t cols) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x, q = t & 15, k0 = t >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = k0 + 16 * i;
+    const int64_t r = r0 + k, c = c0 + 4 * q;
+    if (r < rows && c < cols) {
+      const f4v v = *reinterpret_cast<const f4v *>(x + r * cols + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tile[k][4 * q + e] = v[e];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = k0 + 16 * i;  // output row c0 + k, output columns r0 + 4q..
+    const int64_t c = c0 + k, r = r0 + 4 * q;
+    if (c < cols && r < rows) {
+      f4v v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = tile[4 * q + e][k];
+      *reinterpret_cast<f4v *>(y + c * rows + r) = v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Full reductions: sum / mean / MSE loss (ops.rs:214-278)
 // ---------------------------------------------------------------------------
 
-// kind 0: sum x; 1: sum (x - t)^2
-template <int KIND>
+// kind 0: sum x; 1: sum (x - t)^2.  Each thread keeps four independent
+// partial sums over a grid-stride walk of float4 groups (VEC: 16-byte
+// aligned operands), so four loads per operand are in flight at once; the
+// partials are added in a fixed order, then across the wave and the block.
+template <int KIND, bool VEC>
 __global__ void __launch_bounds__(kBlock)
     reduce_pass1(const float *__restrict__ x, const float *__restrict__ t, int64_t n,
                  float *__restrict__ partial) {
   __shared__ float red[kBlock / 64];
+  auto term = [&](float xv, float tv) {
+    if (KIND == 0) return xv;
+    const float d = xv - tv;
+    return d * d;
+  };
   float s = 0.0f;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kBlock) {
-    if (KIND == 0) {
-      s += x[i];
-    } else {
-      const float d = x[i] - t[i];
-      s += d * d;
+  if (VEC) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const int64_t n4 = n / 4;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+      f4v xv[4], tv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        xv[u] = reinterpret_cast<const f4v *>(x)[i + u * stride];
+        if (KIND == 1) tv[u] = reinterpret_cast<const f4v *>(t)[i + u * stride];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[u] += term(xv[u][e], KIND == 1 ? tv[u][e] : 0.0f);
     }
+    for (; i < n4; i += stride) {
+      const f4v xv = reinterpret_cast<const f4v *>(x)[i];
+      f4v tv = {0.f, 0.f, 0.f, 0.f};
+      if (KIND == 1) tv = reinterpret_cast<const f4v *>(t)[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[0] += term(xv[e], tv[e]);
+    }
+    // The n % 4 tail, taken by the first threads of block 0.
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+      const int64_t k = n4 * 4 + threadIdx.x;
+      acc[0] += term(x[k], KIND == 1 ? t[k] : 0.0f);
+    }
+    s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kBlock)
+      s += term(x[i], KIND == 1 ? t[i] : 0.0f);
   }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -144,8 +216,20 @@ __global__ void __launch_bounds__(kBlock)
     reduce_final(const float *__restrict__ partial, int64_t count, float div,
                  float *__restrict__ out) {
   __shared__ float red[kBlock / 64];
+  // Loads go out in batches of 8 before they are added (in index order), so
+  // a thread waits for one memory round trip per batch.
   float s = 0.0f;
-  for (int64_t i = threadIdx.x; i < count; i += kBlock) s += partial[i];
+  for (int64_t i0 = threadIdx.x; i0 < count; i0 += 8 * kBlock) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t k = i0 + (int64_t)u * kBlock;
+      v[u] = k < count ? partial[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + (int64_t)u * kBlock < count) s += v[u];
+  }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
@@ -280,10 +364,16 @@ int full_reduce(numrs_hip_ctx *ctx, int kind, const float *x, const float *t, in
   void *ws = nullptr;
   if (int rc = numrs_hip::workspace(ctx, (size_t)blocks * sizeof(float), &ws)) return rc;
   float *partial = static_cast<float *>(ws);
-  if (kind == 0)
-    reduce_pass1<0><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  const bool vec = numrs_hip::aligned16(x) && (kind == 0 || numrs_hip::aligned16(t));
+  const unsigned grid = (unsigned)blocks;
+  if (kind == 0 && vec)
+    reduce_pass1<0, true><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  else if (kind == 0)
+    reduce_pass1<0, false><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  else if (vec)
+    reduce_pass1<1, true><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
   else
-    reduce_pass1<1><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+    reduce_pass1<1, false><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
   if (int rc = numrs_hip::check_launch(ctx, "reduce_pass1")) return rc;
   reduce_final<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, div, out);
   return numrs_hip::check_launch(ctx, "reduce_final");
@@ -347,6 +437,11 @@ int numrs_hip_transpose(numrs_hip_ctx *ctx, const float *x, float *y, int64_t ro
   if (rows == 0 || cols == 0) return NUMRS_HIP_OK;
   if (x == nullptr || y == nullptr) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: null pointer");
   if ((rows + 31) / 32 > 65535) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: too many rows");
+  if ((rows & 3) == 0 && (cols & 3) == 0 && numrs_hip::aligned16(x) && numrs_hip::aligned16(y)) {
+    dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+    transpose64_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
+    return numrs_hip::check_launch(ctx, "transpose64_kernel");
+  }
   dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
   transpose_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
   return numrs_hip::check_launch(ctx, "transpose_kernel");

@@ -3,15 +3,22 @@
 //
 // Column reductions (the bias case, [rows, cols] -> [cols]) run in two
 // deterministic passes:
-//   pass 1: a 256-thread block owns 256 columns x kRowsPerBlock rows.  Each
-//           wave walks every 4th row of the chunk, so a wave's load is 1 KiB
-//           of one row; per-thread float4 column partials are combined across
-//           the 4 waves through LDS and written to a [chunks, cols] workspace.
-//   pass 2: a block of 64 columns; wave w adds chunks w, w+4, ... and the four
-//           wave sums are combined in a fixed order.
+//   pass 1: the grid is strips x classes.  A 256-thread block owns a strip of
+//           512 columns (each lane two float4 column groups, 256 columns
+//           apart) and walks the row bands y, y + Q, y + 2Q, ... of its class
+//           y (a band is 4 rows, one per wave; Q = gridDim.y).  At any moment
+//           the whole grid therefore reads one contiguous stretch of rows,
+//           which keeps HBM pages open; on MI355X this sweep order runs the
+//           fused ReLU backward at 4096^2 about 10% faster than blocks that
+//           each own a private run of rows.  Per-lane column partials are
+//           combined across the 4 waves through LDS and written to a
+//           [Q, cols] workspace.
+//   pass 2: a block of 64 columns; wave w adds classes w, w+4, ... and the
+//           four wave sums are combined in a fixed order.
 // The fused ReLU kernel writes dx in pass 1 while it accumulates, so g and z
 // are read exactly once (12 B/element).  No atomics: results do not depend
 // on scheduling.
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -19,15 +26,16 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kColsPerBlock = 256;
-constexpr int kRowsPerBlock = 64;
+constexpr int kColsPerBlock = 512;
+constexpr int kBandRows = 4;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-// Column index of element e (0..3) of thread lane `l` in a 256-column strip.
+// Column of element e (0..7) of lane l in a 512-column strip.  VEC: two float4
+// groups, 4l..4l+3 and 256+4l..256+4l+3; otherwise l + 64e (coalesced scalars).
 template <bool VEC>
 __device__ __forceinline__ int strip_col(int l, int e) {
-  return VEC ? 4 * l + e : l + 64 * e;
+  return VEC ? (e >> 2) * 256 + 4 * l + (e & 3) : l + 64 * e;
 }
 
 // Pass 1.  RELU: dx = z > 0 ? g : 0 (also written out when dx != nullptr);
@@ -37,32 +45,68 @@ __global__ void __launch_bounds__(kBlock)
     colreduce_pass1(const float *__restrict__ g, const float *__restrict__ z,
                     float *__restrict__ dx, float *__restrict__ partial, int64_t rows,
                     int64_t cols, int acc_dx) {
-  __shared__ f4 red[4][64];
+  __shared__ f4 red[4][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c0 = (int64_t)blockIdx.x * kColsPerBlock;
-  const int64_t r0 = (int64_t)blockIdx.y * kRowsPerBlock;
-  const int64_t r1 = min(r0 + (int64_t)kRowsPerBlock, rows);
-  f4 sum = {0.f, 0.f, 0.f, 0.f};
-  const bool full = VEC && c0 + strip_col<VEC>(lane, 3) < cols;
-  for (int64_t r = r0 + wave; r < r1; r += 4) {
+  const int64_t classes = gridDim.y;
+  f4 sum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  // With VEC, cols % 4 == 0, so a float4 group is either wholly inside or
+  // wholly outside the matrix.
+  const bool full0 = VEC && c0 + strip_col<VEC>(lane, 3) < cols;
+  const bool full1 = VEC && c0 + strip_col<VEC>(lane, 7) < cols;
+  // Strips wholly inside the matrix (all but a ragged last one) issue both
+  // float4 loads of g and of z before any use, so each wave keeps four loads
+  // in flight; a per-lane guard would split them into separate waits.
+  const bool whole = VEC && c0 + kColsPerBlock <= cols;
+  for (int64_t band = blockIdx.y; band * kBandRows < rows; band += classes) {
+    const int64_t r = band * kBandRows + wave;
+    if (r >= rows) break;  // wave-uniform; later bands of this class are further down
     const int64_t off = r * cols + c0;
-    if (full) {
-      const int64_t i = off + 4 * lane;
-      f4 gv = *reinterpret_cast<const f4 *>(g + i);
+    if (whole) {
+      const int64_t i0 = off + 4 * lane, i1 = i0 + 256;
+      f4 g0 = *reinterpret_cast<const f4 *>(g + i0);
+      f4 g1 = *reinterpret_cast<const f4 *>(g + i1);
       if (RELU) {
-        const f4 zv = *reinterpret_cast<const f4 *>(z + i);
+        const f4 z0 = *reinterpret_cast<const f4 *>(z + i0);
+        const f4 z1 = *reinterpret_cast<const f4 *>(z + i1);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) gv[e] = zv[e] > 0.0f ? gv[e] : 0.0f;  // backward.rs:158
+        for (int e = 0; e < 4; ++e) {
+          g0[e] = z0[e] > 0.0f ? g0[e] : 0.0f;  // backward.rs:158
+          g1[e] = z1[e] > 0.0f ? g1[e] : 0.0f;
+        }
         if (dx != nullptr) {
-          f4 out = gv;
-          if (acc_dx) out += *reinterpret_cast<const f4 *>(dx + i);
-          *reinterpret_cast<f4 *>(dx + i) = out;
+          f4 o0 = g0, o1 = g1;
+          if (acc_dx) {
+            o0 += *reinterpret_cast<const f4 *>(dx + i0);
+            o1 += *reinterpret_cast<const f4 *>(dx + i1);
+          }
+          *reinterpret_cast<f4 *>(dx + i0) = o0;
+          *reinterpret_cast<f4 *>(dx + i1) = o1;
         }
       }
-      sum += gv;
+      sum[0] += g0;
+      sum[1] += g1;
+    } else if (VEC) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (!(h == 0 ? full0 : full1)) continue;
+        const int64_t i = off + 256 * h + 4 * lane;
+        f4 gv = *reinterpret_cast<const f4 *>(g + i);
+        if (RELU) {
+          const f4 zv = *reinterpret_cast<const f4 *>(z + i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gv[e] = zv[e] > 0.0f ? gv[e] : 0.0f;  // backward.rs:158
+          if (dx != nullptr) {
+            f4 out = gv;
+            if (acc_dx) out += *reinterpret_cast<const f4 *>(dx + i);
+            *reinterpret_cast<f4 *>(dx + i) = out;
+          }
+        }
+        sum[h] += gv;
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 8; ++e) {
         const int64_t c = c0 + strip_col<VEC>(lane, e);
         if (c < cols) {
           const int64_t i = r * cols + c;
@@ -71,19 +115,21 @@ __global__ void __launch_bounds__(kBlock)
             gv = z[i] > 0.0f ? gv : 0.0f;
             if (dx != nullptr) dx[i] = acc_dx ? dx[i] + gv : gv;
           }
-          sum[e] += gv;
+          sum[e >> 2][e & 3] += gv;
         }
       }
     }
   }
-  red[wave][lane] = sum;
+  red[wave][0][lane] = sum[0];
+  red[wave][1][lane] = sum[1];
   __syncthreads();
-  if (wave == 0) {
-    const f4 s = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  if (wave < 2) {
+    const int h = wave;
+    const f4 s = ((red[0][h][lane] + red[1][h][lane]) + red[2][h][lane]) + red[3][h][lane];
     float *dst = partial + (int64_t)blockIdx.y * cols + c0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int64_t c = strip_col<VEC>(lane, e);
+      const int64_t c = strip_col<VEC>(lane, 4 * h + e);
       if (c0 + c < cols) dst[c] = s[e];
     }
   }
@@ -116,24 +162,33 @@ __global__ void __launch_bounds__(kBlock)
 }
 
 // Pass 2 (CORRECT): out[c] (+)= sum over chunks of partial[k][c].  A block
-// covers 64 columns; wave w adds chunks w, w+4, ..., and the four wave sums
-// are combined in wave order.
-__global__ void __launch_bounds__(kBlock)
-    colreduce_finalize(const float *__restrict__ partial, float *__restrict__ out, int64_t chunks,
-                       int64_t cols, int acc) {
-  __shared__ float red[4][64];
+// of kFinWaves waves covers 64 columns; wave w adds chunks w, w + kFinWaves,
+// ... (loads issued in batches, so a wave waits for one memory round trip per
+// batch), and wave 0 adds the wave sums in wave order.  blockIdx.y selects
+// one of two independent (partial, out, acc) sets, so LayerNorm's dgamma and
+// dbeta finish in one launch.
+constexpr int kFinWaves = 16;
+
+struct FinalizeSet {
+  const float *partial[2];
+  float *out[2];
+  int acc[2];
+};
+
+__global__ void __launch_bounds__(64 * kFinWaves)
+    colreduce_finalize(FinalizeSet set, int64_t chunks, int64_t cols) {
+  __shared__ float red[kFinWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float *__restrict__ partial = set.partial[blockIdx.y];
   const int64_t c = (int64_t)blockIdx.x * 64 + lane;
-  // Loads are issued in batches of 16 before they are added, so a wave waits
-  // for one memory round trip per batch instead of one per chunk.
-  constexpr int kBatch = 16;
+  constexpr int kBatch = 8;
   float s = 0.0f;
   if (c < cols) {
-    for (int64_t k0 = wave; k0 < chunks; k0 += 4 * kBatch) {
+    for (int64_t k0 = wave; k0 < chunks; k0 += kFinWaves * kBatch) {
       float v[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const int64_t k = k0 + 4 * u;
+        const int64_t k = k0 + kFinWaves * u;
         v[u] = k < chunks ? partial[k * cols + c] : 0.0f;
       }
 #pragma unroll
@@ -143,9 +198,28 @@ __global__ void __launch_bounds__(kBlock)
   red[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && c < cols) {
-    const float t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-    out[c] = acc ? out[c] + t : t;
+    float t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kFinWaves; ++w) t += red[w][lane];
+    float *out = set.out[blockIdx.y];
+    out[c] = set.acc[blockIdx.y] ? out[c] + t : t;
   }
+}
+
+// Launches the finalize for one or two (partial, out) sets (out1 may be null).
+int launch_finalize(numrs_hip_ctx *ctx, const float *part0, float *out0, int acc0,
+                    const float *part1, float *out1, int acc1, int64_t chunks, int64_t cols) {
+  FinalizeSet set{{part0, part1}, {out0, out1}, {acc0, acc1}};
+  if (out0 == nullptr) {
+    set.partial[0] = part1;
+    set.out[0] = out1;
+    set.acc[0] = acc1;
+    out1 = nullptr;
+  }
+  if (set.out[0] == nullptr) return NUMRS_HIP_OK;
+  dim3 grid(grid_for(cols, 64), out1 != nullptr ? 2 : 1);
+  colreduce_finalize<<<grid, 64 * kFinWaves, 0, ctx->stream>>>(set, chunks, cols);
+  return numrs_hip::check_launch(ctx, "colreduce_finalize");
 }
 
 // Pass 2 (REFERENCE): the full sum lands in out[0]; with acc = 0 the rest
@@ -154,8 +228,19 @@ __global__ void __launch_bounds__(kBlock)
     full_reduce_finalize(const float *__restrict__ partial, int64_t count, float *__restrict__ out,
                          int64_t out_n, int acc, int zero_rest) {
   __shared__ float red[kBlock / 64];
+  // Loads go out in batches of 8 before they are added (in index order).
   float s = 0.0f;
-  for (int64_t i = threadIdx.x; i < count; i += kBlock) s += partial[i];
+  for (int64_t i0 = threadIdx.x; i0 < count; i0 += 8 * kBlock) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t k = i0 + (int64_t)u * kBlock;
+      v[u] = k < count ? partial[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + (int64_t)u * kBlock < count) s += v[u];
+  }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
@@ -293,12 +378,117 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+// Vectorised pass 1 for rows of at most kLnMaxCols columns with cols % 4 == 0
+// and 16-byte aligned operands.  Lane l owns the float4 column groups
+// l, l + 64, ... (NV of them), so its partials of g*xh and g stay in
+// registers across all rows it visits, and each row is read once with float4
+// loads.  The grid sweeps rows in interleaved bands of 4 (one row per wave):
+// block b takes bands b, b + gridDim.x, ...  Wave partials are combined in
+// wave order through LDS and written to the [gridDim.x, cols] workspaces.
+template <int NV>
+__global__ void __launch_bounds__(kBlock)
+    layernorm_bwd_vec(const float *__restrict__ g, const float *__restrict__ x,
+                      const float *__restrict__ gamma, const float *__restrict__ mean,
+                      const float *__restrict__ rstd, float *__restrict__ dx,
+                      float *__restrict__ part_g, float *__restrict__ part_b, int64_t rows,
+                      int64_t cols, int acc_dx, int want_params) {
+  __shared__ f4 red[4][64 * NV];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  bool in[NV];
+  f4 gm[NV], pg[NV], pb[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = 4 * (int64_t)(lane + 64 * i);
+    in[i] = c < cols;
+    gm[i] = in[i] ? *reinterpret_cast<const f4 *>(gamma + c) : f4{0.f, 0.f, 0.f, 0.f};
+    pg[i] = f4{0.f, 0.f, 0.f, 0.f};
+    pb[i] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float inv_n = 1.0f / (float)cols;
+  // One row of the wave's walk: statistics, dx, and the column partials.
+  auto row = [&](int64_t r, const f4 *xv, const f4 *gv) {
+    const float mu = mean[r], rs = rstd[r];
+    float m1 = 0.0f, m2 = 0.0f;
+    f4 xh[NV], gg[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xh[i][e] = (xv[i][e] - mu) * rs;
+        gg[i][e] = gv[i][e] * gm[i][e];
+        m1 += gg[i][e];
+        m2 += gg[i][e] * xh[i][e];
+        pg[i][e] += gv[i][e] * xh[i][e];
+        pb[i][e] += gv[i][e];
+      }
+    }
+    m1 = wave_sum(m1) * inv_n;
+    m2 = wave_sum(m2) * inv_n;
+    if (dx != nullptr) {
+      float *dr = dx + r * cols;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (!in[i]) continue;
+        const int64_t c = 4 * (int64_t)(lane + 64 * i);
+        f4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = rs * ((gg[i][e] - m1) - xh[i][e] * m2);
+        if (acc_dx) v += *reinterpret_cast<const f4 *>(dr + c);
+        *reinterpret_cast<f4 *>(dr + c) = v;
+      }
+    }
+  };
+  // The wave walks rows band*4 + wave for bands b, b + Q, b + 2Q, ...
+  // (Q = gridDim.x), two bands per iteration so that two rows' loads are in
+  // flight together; the rows are still taken in walk order.
+  const int64_t q = gridDim.x;
+  for (int64_t band = blockIdx.x; band * 4 < rows; band += 2 * q) {
+    const int64_t r0 = band * 4 + wave, r1 = (band + q) * 4 + wave;
+    if (r0 >= rows) break;  // wave-uniform; later bands of this block lie further down
+    const bool two = r1 < rows;
+    f4 xv0[NV], gv0[NV], xv1[NV], gv1[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = 4 * (int64_t)(lane + 64 * i);
+      const f4 z = {0.f, 0.f, 0.f, 0.f};
+      xv0[i] = in[i] ? *reinterpret_cast<const f4 *>(x + r0 * cols + c) : z;
+      gv0[i] = in[i] ? *reinterpret_cast<const f4 *>(g + r0 * cols + c) : z;
+      xv1[i] = (two && in[i]) ? *reinterpret_cast<const f4 *>(x + r1 * cols + c) : z;
+      gv1[i] = (two && in[i]) ? *reinterpret_cast<const f4 *>(g + r1 * cols + c) : z;
+    }
+    row(r0, xv0, gv0);
+    if (two) row(r1, xv1, gv1);
+  }
+  if (!want_params) return;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass) __syncthreads();  // the previous pass's reads are done
+#pragma unroll
+    for (int i = 0; i < NV; ++i) red[wave][64 * i + lane] = pass ? pb[i] : pg[i];
+    __syncthreads();
+    float *dst = (pass ? part_b : part_g) + (int64_t)blockIdx.x * cols;
+    for (int q = threadIdx.x; q < 64 * NV; q += kBlock) {
+      const int64_t c = 4 * (int64_t)q;
+      if (c >= cols) continue;
+      const f4 t = ((red[0][q] + red[1][q]) + red[2][q]) + red[3][q];
+      *reinterpret_cast<f4 *>(dst + c) = t;
+    }
+  }
+}
+
 int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, float *out,
               int64_t rows, int64_t cols, int mode, int acc_dx, int acc_out, int64_t out_n) {
   const int64_t strips = (cols + kColsPerBlock - 1) / kColsPerBlock;
-  const int64_t chunks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  if (strips > 0x7fffffff || chunks > 65535)
+  const int64_t bands = (rows + kBandRows - 1) / kBandRows;
+  if (strips > 0x7fffffff)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "column reduction too large");
+  // About one block per CU in all for the fused ReLU kernel (three streams):
+  // more blocks in flight scatter the reads over more HBM pages and measured
+  // slower.  A plain column sum reads one stream and needs two blocks per CU
+  // to keep enough loads in flight.
+  const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const int64_t per_cu = z == nullptr ? 2 : 1;
+  int64_t chunks = (per_cu * cus + strips - 1) / strips;
+  chunks = std::max<int64_t>(1, std::min<int64_t>({chunks, bands, 65535}));
   void *ws = nullptr;
   if (int rc = numrs_hip::workspace(ctx, (size_t)(chunks * cols) * sizeof(float), &ws)) return rc;
   float *partial = static_cast<float *>(ws);
@@ -321,14 +511,11 @@ int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, flo
                                                                       cols, 0);
   }
   if (int rc = numrs_hip::check_launch(ctx, "colreduce_pass1")) return rc;
-  if (mode == NUMRS_HIP_UNBROADCAST_CORRECT) {
-    colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(partial, out, chunks,
-                                                                            cols, acc_out);
-  } else {
-    full_reduce_finalize<<<1, kBlock, 0, ctx->stream>>>(partial, chunks * cols, out, out_n,
-                                                        acc_out, !acc_out);
-  }
-  return numrs_hip::check_launch(ctx, "colreduce_finalize");
+  if (mode == NUMRS_HIP_UNBROADCAST_CORRECT)
+    return launch_finalize(ctx, partial, out, acc_out, nullptr, nullptr, 0, chunks, cols);
+  full_reduce_finalize<<<1, kBlock, 0, ctx->stream>>>(partial, chunks * cols, out, out_n,
+                                                      acc_out, !acc_out);
+  return numrs_hip::check_launch(ctx, "full_reduce_finalize");
 }
 
 int full_sum(numrs_hip_ctx *ctx, const float *g, int64_t n, float *out, int64_t out_n, int acc,
@@ -399,7 +586,11 @@ int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
   const int want = dgamma != nullptr || dbeta != nullptr;
   if (dx == nullptr && !want) return NUMRS_HIP_OK;
-  const int64_t chunks = (rows + kLnRows - 1) / kLnRows;
+  const bool vec = (cols & 3) == 0 && numrs_hip::aligned16(g) && numrs_hip::aligned16(x) &&
+                   numrs_hip::aligned16(gamma) && (dx == nullptr || numrs_hip::aligned16(dx));
+  const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const int64_t chunks = vec ? std::min<int64_t>(cus, (rows + 3) / 4)
+                             : (rows + kLnRows - 1) / kLnRows;
   if (chunks > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too many rows", who);
   float *part = nullptr;
   if (want) {
@@ -408,22 +599,30 @@ int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float
       return rc;
     part = static_cast<float *>(ws);
   }
-  const size_t lds = (size_t)8 * cols * sizeof(float);
-  layernorm_bwd_pass1<<<(unsigned)chunks, kBlock, lds, ctx->stream>>>(
-      g, x, gamma, mean, rstd, dx, part, part ? part + chunks * cols : nullptr, rows, cols,
-      acc_dx, want);
-  if (int rc = numrs_hip::check_launch(ctx, "layernorm_bwd_pass1")) return rc;
-  if (dgamma) {
-    colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(part, dgamma, chunks, cols,
-                                                                       acc_dgamma);
-    if (int rc = numrs_hip::check_launch(ctx, "colreduce_finalize")) return rc;
+  float *part_b = part ? part + chunks * cols : nullptr;
+  if (vec) {
+    const unsigned grid = (unsigned)chunks;
+    if (cols <= 256)
+      layernorm_bwd_vec<1><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
+                                                             part_b, rows, cols, acc_dx, want);
+    else if (cols <= 512)
+      layernorm_bwd_vec<2><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
+                                                             part_b, rows, cols, acc_dx, want);
+    else if (cols <= 1024)
+      layernorm_bwd_vec<4><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
+                                                             part_b, rows, cols, acc_dx, want);
+    else
+      layernorm_bwd_vec<8><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
+                                                             part_b, rows, cols, acc_dx, want);
+    if (int rc = numrs_hip::check_launch(ctx, "layernorm_bwd_vec")) return rc;
+  } else {
+    const size_t lds = (size_t)8 * cols * sizeof(float);
+    layernorm_bwd_pass1<<<(unsigned)chunks, kBlock, lds, ctx->stream>>>(
+        g, x, gamma, mean, rstd, dx, part, part_b, rows, cols, acc_dx, want);
+    if (int rc = numrs_hip::check_launch(ctx, "layernorm_bwd_pass1")) return rc;
   }
-  if (dbeta) {
-    colreduce_finalize<<<grid_for(cols, 64), kBlock, 0, ctx->stream>>>(part + chunks * cols, dbeta,
-                                                                       chunks, cols, acc_dbeta);
-    if (int rc = numrs_hip::check_launch(ctx, "colreduce_finalize")) return rc;
-  }
-  return NUMRS_HIP_OK;
+  if (!want) return NUMRS_HIP_OK;
+  return launch_finalize(ctx, part, dgamma, acc_dgamma, part_b, dbeta, acc_dbeta, chunks, cols);
 }
 
 int numrs_hip_sum_to_shape(numrs_hip_ctx *ctx, const float *g, const int64_t *gshape, int gnd,

@@ -10,6 +10,18 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kRowsPerBlock = kBlock / 64;
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Register-resident variants (rows of at most 256*NV columns, cols % 4 == 0,
+// 16-byte aligned operands): lane l holds the float4 column groups l,
+// l + 64, ... (NV of them), so a row is read from memory once, with float4
+// loads, and every row statistic is computed from registers.  Longer or
+// unaligned rows use the looped kernels.
+template <int NV>
+__device__ __forceinline__ int64_t vcol(int lane, int i) {
+  return 4 * (int64_t)(lane + 64 * i);
+}
+
 // cross_entropy_backward, backward.rs:265-301:
 //   m = max_j x_j (f32::max fold, NaN ignored)      backward.rs:285
 //   s = sum_j exp(x_j - m)                           backward.rs:286
@@ -40,6 +52,59 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+template <bool LABELS, int NV>
+__global__ void __launch_bounds__(kBlock)
+    softmax_ce_bwd_vec(const float *__restrict__ g0, const float *__restrict__ x,
+                       const float *__restrict__ onehot, const int32_t *__restrict__ labels,
+                       float *__restrict__ dx, int64_t B, int64_t C, int acc) {
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= B) return;
+  const float *xr = x + row * C;
+  f4 xv[NV], tv[NV];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = vcol<NV>(lane, i);
+    if (c < C) {
+      xv[i] = *reinterpret_cast<const f4 *>(xr + c);
+      if (!LABELS) tv[i] = *reinterpret_cast<const f4 *>(onehot + row * C + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) m = fmaxf(m, xv[i][e]);  // backward.rs:285
+    }
+  }
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (vcol<NV>(lane, i) < C) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[i][e] = expf(xv[i][e] - m);  // backward.rs:286
+        s += xv[i][e];
+      }
+    }
+  }
+  s = wave_sum(s);
+  const float scale = g0[0] / (float)B;
+  const int32_t label = LABELS ? labels[row] : -1;
+  float *out = dx + row * C;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = vcol<NV>(lane, i);
+    if (c < C) {
+      f4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float t = LABELS ? (c + e == (int64_t)label ? 1.0f : 0.0f) : tv[i][e];
+        v[e] = (xv[i][e] / s - t) * scale;  // backward.rs:289-291
+      }
+      if (acc) v += *reinterpret_cast<const f4 *>(out + c);
+      *reinterpret_cast<f4 *>(out + c) = v;
+    }
+  }
+}
+
 // softmax_backward, backward.rs:521-541: dx = y * (g - sum_row(g * y)).
 // g and dx may alias (in-place use by attention): each lane reads g[j] before
 // it writes dx[j], and the row dot product is complete before any write.
@@ -60,6 +125,41 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+template <int NV>
+__global__ void __launch_bounds__(kBlock)
+    softmax_bwd_vec(const float *__restrict__ y, const float *g, float *dx, int64_t rows,
+                    int64_t cols, int acc) {
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *yr = y + row * cols, *gr = g + row * cols;
+  f4 yv[NV], gv[NV];
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = vcol<NV>(lane, i);
+    if (c < cols) {
+      yv[i] = *reinterpret_cast<const f4 *>(yr + c);
+      gv[i] = *reinterpret_cast<const f4 *>(gr + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d += gv[i][e] * yv[i][e];
+    }
+  }
+  d = wave_sum(d);  // every lane's reads of g are done before any write below
+  float *out = dx + row * cols;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = vcol<NV>(lane, i);
+    if (c < cols) {
+      f4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = yv[i][e] * (gv[i][e] - d);
+      if (acc) v += *reinterpret_cast<const f4 *>(out + c);
+      *reinterpret_cast<f4 *>(out + c) = v;
+    }
+  }
+}
+
 // Row argmax with an explicit tie rule.
 //   tie_last = 0 (ops::argmax, backend/cpu/scalar.rs:517-528): a sequential
 //     scan that replaces only on strict '>'.  NaN never replaces; a NaN in
@@ -72,14 +172,16 @@ __global__ void __launch_bounds__(kBlock)
 //     NaN's index when it is the final element.
 // Both are evaluated as a lane-parallel scan over contiguous segments and a
 // wave combine that applies the same rule to (value, index) pairs.
-__device__ __forceinline__ bool better_first(float v, int64_t i, float bv, int64_t bi) {
+template <typename I>
+__device__ __forceinline__ bool better_first(float v, I i, float bv, I bi) {
   // Candidate (v, i) beats (bv, bi) under "first strict maximum".
   if (v != v) return false;
   if (bv != bv) return true;
   return v > bv || (v == bv && i < bi);
 }
 
-__device__ __forceinline__ bool better_last(float v, int64_t i, float bv, int64_t bi) {
+template <typename I>
+__device__ __forceinline__ bool better_last(float v, I i, float bv, I bi) {
   if (v != v) return false;
   if (bv != bv) return true;
   return v > bv || (v == bv && i > bi);
@@ -136,6 +238,96 @@ __global__ void __launch_bounds__(kBlock)
   if (lane == 0) idx[row] = (int32_t)(bi < 0 ? start : bi);
 }
 
+// A lane visits its elements in increasing column order, so within a lane
+// the tie rule reduces to one comparison: first max keeps the earlier
+// element (replace on strict '>'), last max takes the later one ('>=').
+// Columns fit in int32 (the host checks), so indices are 32-bit.
+template <int NV, bool TIE_LAST>
+__global__ void __launch_bounds__(kBlock)
+    argmax_vec(const float *__restrict__ x, int32_t *__restrict__ idx, int64_t rows,
+               int64_t cols) {
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = x + row * cols;
+  const int ncols = (int)cols;
+  f4 xv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (int)vcol<NV>(lane, i);
+    if (c < ncols) xv[i] = *reinterpret_cast<const f4 *>(xr + c);
+  }
+  int start = 0;
+  if (TIE_LAST) {
+    // Last NaN position: the scan restarts after it.
+    int last_nan = -1;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (int)vcol<NV>(lane, i);
+      if (c < ncols) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (xv[i][e] != xv[i][e]) last_nan = c + e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) last_nan = max(last_nan, __shfl_xor(last_nan, off, 64));
+    if (last_nan == ncols - 1) {
+      if (lane == 0) idx[row] = last_nan;
+      return;
+    }
+    start = last_nan + 1;
+  } else if (xr[0] != xr[0]) {
+    if (lane == 0) idx[row] = 0;
+    return;
+  }
+  // Lane scan.  No NaN lies at or after `start` with TIE_LAST; without it a
+  // NaN never replaces.
+  float bv = 0.0f;
+  int bi = -1;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (int)vcol<NV>(lane, i);
+    if (c < ncols) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = xv[i][e];
+        const int j = c + e;
+        const bool take = TIE_LAST ? (j >= start && (bi < 0 || v >= bv))
+                                   : (v == v && (bi < 0 || v > bv));
+        if (take) {
+          bv = v;
+          bi = j;
+        }
+      }
+    }
+  }
+  // Wave combine of (value, index) pairs with the full rule.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    const bool take = (oi >= 0) && (bi < 0 || (TIE_LAST ? better_last(ov, oi, bv, bi)
+                                                        : better_first(ov, oi, bv, bi)));
+    if (take) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) idx[row] = bi < 0 ? start : bi;
+}
+
+// Number of float4 groups per lane for a register-resident row, or 0 when the
+// looped kernel must be used.
+inline int row_nv(int64_t cols, bool aligned) {
+  if (!aligned || (cols & 3) != 0) return 0;
+  if (cols <= 256) return 1;
+  if (cols <= 512) return 2;
+  if (cols <= 1024) return 4;
+  if (cols <= 2048) return 8;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -152,6 +344,26 @@ int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, con
   if ((onehot == nullptr) == (labels == nullptr))
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: pass exactly one of onehot/labels", who);
   const unsigned grid = grid_for(B, kRowsPerBlock);
+  const int nv = row_nv(C, numrs_hip::aligned16(logits) && numrs_hip::aligned16(dlogits) &&
+                               (onehot == nullptr || numrs_hip::aligned16(onehot)));
+#define NRS_CE_VEC(NV)                                                                           \
+  if (labels != nullptr)                                                                         \
+    softmax_ce_bwd_vec<true, NV><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot,      \
+                                                                   labels, dlogits, B, C,        \
+                                                                   accumulate);                  \
+  else                                                                                           \
+    softmax_ce_bwd_vec<false, NV><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot,     \
+                                                                    labels, dlogits, B, C,       \
+                                                                    accumulate);                 \
+  return numrs_hip::check_launch(ctx, "softmax_ce_bwd_vec");
+  switch (nv) {
+    case 1: { NRS_CE_VEC(1) }
+    case 2: { NRS_CE_VEC(2) }
+    case 4: { NRS_CE_VEC(4) }
+    case 8: { NRS_CE_VEC(8) }
+    default: break;
+  }
+#undef NRS_CE_VEC
   if (labels != nullptr)
     softmax_ce_bwd_kernel<true><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot, labels,
                                                                   dlogits, B, C, accumulate);
@@ -170,8 +382,16 @@ int numrs_hip_softmax_backward(numrs_hip_ctx *ctx, const float *y, const float *
   if (rows == 0 || cols == 0) return NUMRS_HIP_OK;
   if (y == nullptr || g == nullptr || dx == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
-  softmax_bwd_kernel<<<grid_for(rows, kRowsPerBlock), kBlock, 0, ctx->stream>>>(y, g, dx, rows,
-                                                                                cols, accumulate);
+  const unsigned grid = grid_for(rows, kRowsPerBlock);
+  switch (row_nv(cols, numrs_hip::aligned16(y) && numrs_hip::aligned16(g) &&
+                           numrs_hip::aligned16(dx))) {
+    case 1: softmax_bwd_vec<1><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+    case 2: softmax_bwd_vec<2><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+    case 4: softmax_bwd_vec<4><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+    case 8: softmax_bwd_vec<8><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+    default:
+      softmax_bwd_kernel<<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate);
+  }
   return numrs_hip::check_launch(ctx, "softmax_bwd_kernel");
 }
 
@@ -185,8 +405,22 @@ int numrs_hip_argmax_rows(numrs_hip_ctx *ctx, const float *x, int32_t *idx, int6
   if (cols > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: row too long", who);
   if (x == nullptr || idx == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
-  argmax_kernel<<<grid_for(rows, kRowsPerBlock), kBlock, 0, ctx->stream>>>(x, idx, rows, cols,
-                                                                           tie_last ? 1 : 0);
+  const unsigned grid = grid_for(rows, kRowsPerBlock);
+  const int tl = tie_last ? 1 : 0;
+#define NRS_ARGMAX_VEC(NV)                                                              \
+  if (tl)                                                                               \
+    argmax_vec<NV, true><<<grid, kBlock, 0, ctx->stream>>>(x, idx, rows, cols);          \
+  else                                                                                  \
+    argmax_vec<NV, false><<<grid, kBlock, 0, ctx->stream>>>(x, idx, rows, cols);         \
+  break;
+  switch (row_nv(cols, numrs_hip::aligned16(x))) {
+    case 1: NRS_ARGMAX_VEC(1)
+    case 2: NRS_ARGMAX_VEC(2)
+    case 4: NRS_ARGMAX_VEC(4)
+    case 8: NRS_ARGMAX_VEC(8)
+    default: argmax_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, idx, rows, cols, tl);
+  }
+#undef NRS_ARGMAX_VEC
   return numrs_hip::check_launch(ctx, "argmax_kernel");
 }
 
