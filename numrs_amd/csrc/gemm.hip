@@ -842,21 +842,27 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
   if (!has_a && !has_b) return NUMRS_HIP_OK;
   if (!has_a) return gemm_dispatch(ctx, gb, 1, false, false);
   if (!has_b) return gemm_dispatch(ctx, ga, 1, true, first_nt);
-  // Joint split plan: the pair shares one grid, so only the product with
-  // fewer tiles (the weight gradient) is split, until the pair has ~256
-  // workgroups.
+  // Joint split plan, balanced by work: the pair shares one grid, and a
+  // workgroup's time is its number of reduction tiles.  The weight gradient
+  // (long reduction over tokens) next to dx (short reduction over features)
+  // would otherwise leave a few long workgroups running alone -- Linear
+  // 2048 -> 512 over 4096 tokens: 512 dx tiles of 16 k-tiles and 64 dW tiles
+  // of 128.  Each product is cut so that no workgroup holds more than the
+  // larger of (a) the shorter product's reduction and (b) the average work
+  // per workgroup slot (two per CU), keeping at least 8 k-tiles per split.
   int sa_ = 1, sb_ = 1;
   {
     const int64_t ta0 = (int64_t)ga.tiles_p * ga.tiles_q, tb0 = (int64_t)gb.tiles_p * gb.tiles_q;
-    if (ta0 + tb0 < 256) {
-      const bool b_small = tb0 <= ta0;
-      const Gemm &sm = b_small ? gb : ga;
-      const int64_t t_small = b_small ? tb0 : ta0, t_other = b_small ? ta0 : tb0;
-      const int nk = (sm.R + kBR - 1) / kBR;
-      int64_t sp = (256 - t_other + t_small - 1) / t_small;
-      sp = std::max<int64_t>(1, std::min<int64_t>({sp, (int64_t)nk / 8, 32}));
-      (b_small ? sb_ : sa_) = (int)sp;
-    }
+    const int64_t ka = (ga.R + kBR - 1) / kBR, kb = (gb.R + kBR - 1) / kBR;
+    const int64_t slots = 2 * (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
+    const int64_t avg = (ta0 * ka + tb0 * kb + slots - 1) / slots;
+    const int64_t target = std::max<int64_t>({std::min(ka, kb), avg, 8});
+    auto splits_for = [&](int64_t nk) {
+      int64_t sp = (nk + target - 1) / target;
+      return (int)std::max<int64_t>(1, std::min<int64_t>({sp, nk / 8, 32}));
+    };
+    sa_ = splits_for(ka);
+    sb_ = splits_for(kb);
   }
   if (sa_ > 1 || sb_ > 1) {
     const size_t na = sa_ > 1 ? (size_t)sa_ * ga.P * ga.Q : 0;

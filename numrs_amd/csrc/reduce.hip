@@ -58,67 +58,103 @@ __global__ void __launch_bounds__(kBlock)
   // float4 loads of g and of z before any use, so each wave keeps four loads
   // in flight; a per-lane guard would split them into separate waits.
   const bool whole = VEC && c0 + kColsPerBlock <= cols;
-  for (int64_t band = blockIdx.y; band * kBandRows < rows; band += classes) {
-    const int64_t r = band * kBandRows + wave;
-    if (r >= rows) break;  // wave-uniform; later bands of this class are further down
-    const int64_t off = r * cols + c0;
-    if (whole) {
-      const int64_t i0 = off + 4 * lane, i1 = i0 + 256;
-      f4 g0 = *reinterpret_cast<const f4 *>(g + i0);
-      f4 g1 = *reinterpret_cast<const f4 *>(g + i1);
-      if (RELU) {
-        const f4 z0 = *reinterpret_cast<const f4 *>(z + i0);
-        const f4 z1 = *reinterpret_cast<const f4 *>(z + i1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          g0[e] = z0[e] > 0.0f ? g0[e] : 0.0f;  // backward.rs:158
-          g1[e] = z1[e] > 0.0f ? g1[e] : 0.0f;
-        }
-        if (dx != nullptr) {
-          f4 o0 = g0, o1 = g1;
-          if (acc_dx) {
-            o0 += *reinterpret_cast<const f4 *>(dx + i0);
-            o1 += *reinterpret_cast<const f4 *>(dx + i1);
-          }
-          *reinterpret_cast<f4 *>(dx + i0) = o0;
-          *reinterpret_cast<f4 *>(dx + i1) = o1;
-        }
-      }
-      sum[0] += g0;
-      sum[1] += g1;
-    } else if (VEC) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (!(h == 0 ? full0 : full1)) continue;
-        const int64_t i = off + 256 * h + 4 * lane;
-        f4 gv = *reinterpret_cast<const f4 *>(g + i);
+  if (whole) {
+    // Whole strip: the next band's loads are issued before the current band
+    // is processed (register double buffering), so each wave keeps two
+    // bands' loads in flight; bands are still summed in walk order.
+    int64_t r = (int64_t)blockIdx.y * kBandRows + wave;
+    if (r < rows) {
+      const int64_t step = classes * kBandRows;
+      f4 ga[2], za[2], gb[2], zb[2];
+      auto load = [&](int64_t row, f4 *gv, f4 *zv) {
+        const int64_t i0 = row * cols + c0 + 4 * lane;
+        gv[0] = *reinterpret_cast<const f4 *>(g + i0);
+        gv[1] = *reinterpret_cast<const f4 *>(g + i0 + 256);
         if (RELU) {
-          const f4 zv = *reinterpret_cast<const f4 *>(z + i);
+          zv[0] = *reinterpret_cast<const f4 *>(z + i0);
+          zv[1] = *reinterpret_cast<const f4 *>(z + i0 + 256);
+        }
+      };
+      auto band = [&](int64_t row, const f4 *gv, const f4 *zv) {
+        const int64_t i0 = row * cols + c0 + 4 * lane, i1 = i0 + 256;
+        f4 g0 = gv[0], g1 = gv[1];
+        if (RELU) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) gv[e] = zv[e] > 0.0f ? gv[e] : 0.0f;  // backward.rs:158
+          for (int e = 0; e < 4; ++e) {
+            g0[e] = zv[0][e] > 0.0f ? g0[e] : 0.0f;  // backward.rs:158
+            g1[e] = zv[1][e] > 0.0f ? g1[e] : 0.0f;
+          }
           if (dx != nullptr) {
-            f4 out = gv;
-            if (acc_dx) out += *reinterpret_cast<const f4 *>(dx + i);
-            *reinterpret_cast<f4 *>(dx + i) = out;
+            f4 o0 = g0, o1 = g1;
+            if (acc_dx) {
+              o0 += *reinterpret_cast<const f4 *>(dx + i0);
+              o1 += *reinterpret_cast<const f4 *>(dx + i1);
+            }
+            *reinterpret_cast<f4 *>(dx + i0) = o0;
+            *reinterpret_cast<f4 *>(dx + i1) = o1;
           }
         }
-        sum[h] += gv;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t c = c0 + strip_col<VEC>(lane, e);
-        if (c < cols) {
-          const int64_t i = r * cols + c;
-          float gv = g[i];
-          if (RELU) {
-            gv = z[i] > 0.0f ? gv : 0.0f;
-            if (dx != nullptr) dx[i] = acc_dx ? dx[i] + gv : gv;
-          }
-          sum[e >> 2][e & 3] += gv;
-        }
+        sum[0] += g0;
+        sum[1] += g1;
+      };
+      // Two register sets alternate (a copy out of a set with loads in
+      // flight would wait for them).  The prefetch is unconditional -- past
+      // the end it re-reads the current row -- so the wait before a band
+      // only covers that band's own loads.
+      load(r, ga, za);
+      while (true) {
+        const int64_t r1 = r + step;
+        load(r1 < rows ? r1 : r, gb, zb);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the band's work
+        band(r, ga, za);
+        if (r1 >= rows) break;
+        const int64_t r2 = r1 + step;
+        load(r2 < rows ? r2 : r1, ga, za);
+        __builtin_amdgcn_sched_barrier(0);
+        band(r1, gb, zb);
+        if (r2 >= rows) break;
+        r = r2;
       }
     }
+  } else {
+    for (int64_t band = blockIdx.y; band * kBandRows < rows; band += classes) {
+      const int64_t r = band * kBandRows + wave;
+      if (r >= rows) break;  // wave-uniform; later bands of this class are further down
+      const int64_t off = r * cols + c0;
+      if (VEC) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (!(h == 0 ? full0 : full1)) continue;
+          const int64_t i = off + 256 * h + 4 * lane;
+          f4 gv = *reinterpret_cast<const f4 *>(g + i);
+          if (RELU) {
+            const f4 zv = *reinterpret_cast<const f4 *>(z + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gv[e] = zv[e] > 0.0f ? gv[e] : 0.0f;  // backward.rs:158
+            if (dx != nullptr) {
+              f4 out = gv;
+              if (acc_dx) out += *reinterpret_cast<const f4 *>(dx + i);
+              *reinterpret_cast<f4 *>(dx + i) = out;
+            }
+          }
+          sum[h] += gv;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t c = c0 + strip_col<VEC>(lane, e);
+          if (c < cols) {
+            const int64_t i = r * cols + c;
+            float gv = g[i];
+            if (RELU) {
+              gv = z[i] > 0.0f ? gv : 0.0f;
+              if (dx != nullptr) dx[i] = acc_dx ? dx[i] + gv : gv;
+            }
+            sum[e >> 2][e & 3] += gv;
+          }
+        }
+      }
+  }
   }
   red[wave][0][lane] = sum[0];
   red[wave][1][lane] = sum[1];
@@ -252,14 +288,39 @@ __global__ void __launch_bounds__(kBlock)
     for (int64_t i = 1 + threadIdx.x; i < out_n; i += kBlock) out[i] = 0.0f;
 }
 
-// Full sum pass 1: grid-stride partial per block.
+// Full sum pass 1: grid-stride partial per block.  With 16-byte aligned g
+// (VEC), a thread walks float4 groups, eight loads in flight, into four
+// partial sums added in a fixed order.
+template <bool VEC>
 __global__ void __launch_bounds__(kBlock)
     full_reduce_pass1(const float *__restrict__ g, int64_t n, float *__restrict__ partial) {
   __shared__ float red[kBlock / 64];
   float s = 0.0f;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kBlock)
-    s += g[i];
+  if (VEC) {
+    const int64_t n4 = n / 4, stride = (int64_t)gridDim.x * kBlock;
+    int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (; i + 7 * stride < n4; i += 8 * stride) {
+      f4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = reinterpret_cast<const f4 *>(g)[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[u & 3] += v[u][e];
+    }
+    for (; i < n4; i += stride) {
+      const f4 v = reinterpret_cast<const f4 *>(g)[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[0] += v[e];
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) acc[0] += g[n4 * 4 + threadIdx.x];
+    s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kBlock)
+      s += g[i];
+  }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
@@ -406,8 +467,7 @@ __global__ void __launch_bounds__(kBlock)
   }
   const float inv_n = 1.0f / (float)cols;
   // One row of the wave's walk: statistics, dx, and the column partials.
-  auto row = [&](int64_t r, const f4 *xv, const f4 *gv) {
-    const float mu = mean[r], rs = rstd[r];
+  auto row = [&](int64_t r, const f4 *xv, const f4 *gv, float mu, float rs) {
     float m1 = 0.0f, m2 = 0.0f;
     f4 xh[NV], gg[NV];
 #pragma unroll
@@ -439,25 +499,49 @@ __global__ void __launch_bounds__(kBlock)
     }
   };
   // The wave walks rows band*4 + wave for bands b, b + Q, b + 2Q, ...
-  // (Q = gridDim.x), two bands per iteration so that two rows' loads are in
-  // flight together; the rows are still taken in walk order.
+  // (Q = gridDim.x).  The next row's loads, its statistics included, are
+  // issued before the current row is processed (register double buffering):
+  // the memory counter retires loads in issue order, so a statistic loaded
+  // after the prefetch would make the wave wait for the prefetch as well.
   const int64_t q = gridDim.x;
-  for (int64_t band = blockIdx.x; band * 4 < rows; band += 2 * q) {
-    const int64_t r0 = band * 4 + wave, r1 = (band + q) * 4 + wave;
-    if (r0 >= rows) break;  // wave-uniform; later bands of this block lie further down
-    const bool two = r1 < rows;
-    f4 xv0[NV], gv0[NV], xv1[NV], gv1[NV];
+  auto load = [&](int64_t r, f4 *xv, f4 *gv, float &mu, float &rs) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int64_t c = 4 * (int64_t)(lane + 64 * i);
+      // Lanes past the row end load column 0 and discard it: an
+      // unconditional load keeps the wait counts exact.
+      const int64_t c = in[i] ? 4 * (int64_t)(lane + 64 * i) : 0;
       const f4 z = {0.f, 0.f, 0.f, 0.f};
-      xv0[i] = in[i] ? *reinterpret_cast<const f4 *>(x + r0 * cols + c) : z;
-      gv0[i] = in[i] ? *reinterpret_cast<const f4 *>(g + r0 * cols + c) : z;
-      xv1[i] = (two && in[i]) ? *reinterpret_cast<const f4 *>(x + r1 * cols + c) : z;
-      gv1[i] = (two && in[i]) ? *reinterpret_cast<const f4 *>(g + r1 * cols + c) : z;
+      const f4 xl = *reinterpret_cast<const f4 *>(x + r * cols + c);
+      const f4 gl = *reinterpret_cast<const f4 *>(g + r * cols + c);
+      xv[i] = in[i] ? xl : z;
+      gv[i] = in[i] ? gl : z;
     }
-    row(r0, xv0, gv0);
-    if (two) row(r1, xv1, gv1);
+    mu = mean[r];
+    rs = rstd[r];
+  };
+  // Two register sets alternate (no copies: a copy out of a set with loads
+  // in flight would wait for them).  The prefetch is unconditional -- past
+  // the end it re-reads the current row -- so the wait before a row only
+  // covers that row's own loads.
+  int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t step = 4 * q;
+  if (r < rows) {
+    f4 xa[NV], ga[NV], xb[NV], gb[NV];
+    float mua, rsa, mub, rsb;
+    load(r, xa, ga, mua, rsa);
+    while (true) {
+      const int64_t r1 = r + step;
+      load(r1 < rows ? r1 : r, xb, gb, mub, rsb);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the row's work
+      row(r, xa, ga, mua, rsa);
+      if (r1 >= rows) break;
+      const int64_t r2 = r1 + step;
+      load(r2 < rows ? r2 : r1, xa, ga, mua, rsa);
+      __builtin_amdgcn_sched_barrier(0);
+      row(r1, xb, gb, mub, rsb);
+      if (r2 >= rows) break;
+      r = r2;
+    }
   }
   if (!want_params) return;
   for (int pass = 0; pass < 2; ++pass) {
@@ -520,13 +604,18 @@ int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, flo
 
 int full_sum(numrs_hip_ctx *ctx, const float *g, int64_t n, float *out, int64_t out_n, int acc,
              int zero_rest) {
+  // At most one block per CU (more blocks measured slower for a read-only sweep).
+  const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
   int64_t blocks = (n + kBlock * 16 - 1) / (kBlock * 16);
   if (blocks < 1) blocks = 1;
-  if (blocks > 2048) blocks = 2048;
+  if (blocks > cus) blocks = cus;
   void *ws = nullptr;
   if (int rc = numrs_hip::workspace(ctx, (size_t)blocks * sizeof(float), &ws)) return rc;
   float *partial = static_cast<float *>(ws);
-  full_reduce_pass1<<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(g, n, partial);
+  if (numrs_hip::aligned16(g))
+    full_reduce_pass1<true><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(g, n, partial);
+  else
+    full_reduce_pass1<false><<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(g, n, partial);
   if (int rc = numrs_hip::check_launch(ctx, "full_reduce_pass1")) return rc;
   full_reduce_finalize<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, out, out_n, acc, zero_rest);
   return numrs_hip::check_launch(ctx, "full_reduce_finalize");
