@@ -260,6 +260,18 @@ int numrs_hip_time_slice(numrs_hip_ctx *ctx, const float *x, float *y, int64_t B
 int numrs_hip_sum_to_shape(numrs_hip_ctx *ctx, const float *g, const int64_t *gshape, int gnd,
                            float *out, const int64_t *oshape, int ond, int mode, int accumulate);
 
+/* ops::sum / ops::mean over one axis (ops/reduction/sum.rs:7-10 ->
+ * backend/cpu/scalar.rs:584-700): x viewed as [outer, n, inner] with the
+ * reduced axis in the middle; out[outer, inner] (the axis removed).  The
+ * mean divides the sum by n.  Empty axis: 0 (sum) or NaN (mean). */
+int numrs_hip_reduce_axis(numrs_hip_ctx *ctx, const float *x, int64_t outer, int64_t n,
+                          int64_t inner, int mean, float *out);
+/* Backward of the axis reduction: dx[outer, n, inner] (+)= g[outer, inner],
+ * divided by n for the mean (sum_backward / mean_backward, backward.rs:208-236,
+ * along the axis the forward reduced). */
+int numrs_hip_broadcast_axis(numrs_hip_ctx *ctx, const float *g, int64_t outer, int64_t n,
+                             int64_t inner, int mean, float *dx, int accumulate);
+
 /* relu_backward (backward.rs:152-163) fused with the bias branch of
  * add_backward (backward.rs:43-54) for y = ReLU(x + b), x[rows,cols],
  * b[cols]:  dx = (z > 0) ? g : 0 with z = x + b the saved pre-activation,
@@ -387,6 +399,14 @@ int numrs_hip_cross_entropy_loss(numrs_hip_ctx *ctx, const float *logits, const 
  * cannot run on an axis: ops/stats/softmax.rs:13-16). */
 int numrs_hip_softmax_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t rows,
                               int64_t cols, float scale);
+/* Softmax along one axis of x viewed as [outer, n, inner] (the reference's
+ * ops::softmax rejects an axis, ops/stats/softmax.rs:13-16); the last axis
+ * (inner = 1) uses the row kernels.  Backward: softmax_backward
+ * (backward.rs:521-541) along the same axis, dx (+)= y * (g - sum(g*y)). */
+int numrs_hip_softmax_axis_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t outer,
+                                   int64_t n, int64_t inner);
+int numrs_hip_softmax_axis_backward(numrs_hip_ctx *ctx, const float *y, const float *g, float *dx,
+                                    int64_t outer, int64_t n, int64_t inner, int accumulate);
 /* LayerNorm over the last axis (no reference op): y = (x-mean)*rstd*gamma +
  * beta, rstd = 1/sqrt(biased var + eps); mean/rstd per row (may be NULL). */
 int numrs_hip_layernorm_forward(numrs_hip_ctx *ctx, const float *x, const float *gamma,
@@ -467,6 +487,23 @@ int numrs_hip_tensor_cross_entropy_labels(numrs_hip_tensor *logits, const int32_
                                           numrs_hip_tensor **out);
 /* Row softmax over the last axis (Softmax module, nn.rs:345-375, on an axis). */
 int numrs_hip_tensor_softmax(numrs_hip_tensor *a, numrs_hip_tensor **out);
+/* Tensor sum / mean over one axis (0 <= axis < ndim): the axis is removed
+ * from the shape, a 1-D input gives [1] (ops::sum / ops::mean with
+ * Some(axis), backend/cpu/scalar.rs:584-700; the reference's autograd
+ * records OpKind::Sum { axis } but only ever reduces fully, ops.rs:214-252,
+ * and its sum_backward ignores the axis, backward.rs:208-221). */
+int numrs_hip_tensor_sum_axis(numrs_hip_tensor *a, int64_t axis, int mean, numrs_hip_tensor **out);
+/* Tensor softmax along one axis (0 <= axis < ndim); the reference rejects an
+ * axis (ops/stats/softmax.rs:13-16). */
+int numrs_hip_tensor_softmax_axis(numrs_hip_tensor *a, int64_t axis, numrs_hip_tensor **out);
+/* Softmax along one axis of x viewed as [outer, n, inner] (the reference's
+ * ops::softmax rejects an axis, ops/stats/softmax.rs:13-16); the last axis
+ * (inner = 1) uses the row kernels.  Backward: softmax_backward
+ * (backward.rs:521-541) along the same axis, dx (+)= y * (g - sum(g*y)). */
+int numrs_hip_softmax_axis_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t outer,
+                                   int64_t n, int64_t inner);
+int numrs_hip_softmax_axis_backward(numrs_hip_ctx *ctx, const float *y, const float *g, float *dx,
+                                    int64_t outer, int64_t n, int64_t inner, int accumulate);
 /* LayerNorm over the last axis (no reference op). */
 int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
                                 numrs_hip_tensor *beta, float eps, numrs_hip_tensor **out);

@@ -54,6 +54,10 @@ SIGNATURES = {
     "numrs_hip_mse_backward": (_i, [_vp] * 6 + [_i64, _i]),
     "numrs_hip_softmax_ce_backward": (_i, [_vp] * 6 + [_i64, _i64, _i]),
     "numrs_hip_softmax_backward": (_i, [_vp] * 4 + [_i64, _i64, _i]),
+    "numrs_hip_reduce_axis": (_i, [_vp, _vp, _i64, _i64, _i64, _i, _vp]),
+    "numrs_hip_broadcast_axis": (_i, [_vp, _vp, _i64, _i64, _i64, _i, _vp, _i]),
+    "numrs_hip_softmax_axis_forward": (_i, [_vp, _vp, _vp, _i64, _i64, _i64]),
+    "numrs_hip_softmax_axis_backward": (_i, [_vp] * 4 + [_i64, _i64, _i64, _i]),
     "numrs_hip_argmax_rows": (_i, [_vp] * 3 + [_i64, _i64, _i]),
     "numrs_hip_sgd_step": (_i, [_vp] * 4 + [_i64, _f, _f, _f]),
     "numrs_hip_adam_step": (_i, [_vp] * 5 + [_i64, _f, _f, _f, _f, _f, _i]),
@@ -101,6 +105,8 @@ SIGNATURES = {
     "numrs_hip_tensor_cross_entropy_loss": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_cross_entropy_labels": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_softmax": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_sum_axis": (_i, [_vp, _i64, _i, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_softmax_axis": (_i, [_vp, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_layer_norm": (_i, [_vp, _vp, _vp, _f, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_linear": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_lstm": (_i, [_vp] * 4 + [ctypes.POINTER(_vp)]),

@@ -238,13 +238,29 @@ class Tensor:
     def flatten(self) -> "Tensor":
         return self.reshape((self.numel(),))
 
-    def sum(self) -> "Tensor":
-        h = ctypes.c_void_p()
-        return self._out(L.load().numrs_hip_tensor_sum(self._h, 0, ctypes.byref(h)), h)
+    def _axis(self, axis: int) -> int:
+        nd = len(self.shape())
+        a = axis + nd if axis < 0 else axis
+        if not 0 <= a < nd:
+            raise ValueError(f"axis {axis} out of range for {nd} dimensions")
+        return a
 
-    def mean(self) -> "Tensor":
+    def sum(self, axis: int | None = None) -> "Tensor":
+        """Tensor::sum (ops.rs:214-231): all elements into shape [1]; with an
+        axis, that axis is removed (ops::sum(a, Some(axis)))."""
         h = ctypes.c_void_p()
-        return self._out(L.load().numrs_hip_tensor_sum(self._h, 1, ctypes.byref(h)), h)
+        if axis is None:
+            return self._out(L.load().numrs_hip_tensor_sum(self._h, 0, ctypes.byref(h)), h)
+        return self._out(L.load().numrs_hip_tensor_sum_axis(self._h, self._axis(axis), 0,
+                                                             ctypes.byref(h)), h)
+
+    def mean(self, axis: int | None = None) -> "Tensor":
+        """Tensor::mean (ops.rs:234-252); with an axis, ops::mean(a, Some(axis))."""
+        h = ctypes.c_void_p()
+        if axis is None:
+            return self._out(L.load().numrs_hip_tensor_sum(self._h, 1, ctypes.byref(h)), h)
+        return self._out(L.load().numrs_hip_tensor_sum_axis(self._h, self._axis(axis), 1,
+                                                             ctypes.byref(h)), h)
 
     def mse_loss(self, target: "Tensor") -> "Tensor":
         h = ctypes.c_void_p()
@@ -263,9 +279,14 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_cross_entropy_labels(self._h, lab.ctypes.data,
                                                                         ctypes.byref(h)), h)
 
-    def softmax(self) -> "Tensor":
+    def softmax(self, axis: int = -1) -> "Tensor":
+        """Softmax along `axis` (default the last, row kernels); the reference
+        rejects an axis (ops/stats/softmax.rs:13-16)."""
         h = ctypes.c_void_p()
-        return self._out(L.load().numrs_hip_tensor_softmax(self._h, ctypes.byref(h)), h)
+        a = self._axis(axis)
+        if a == len(self.shape()) - 1:
+            return self._out(L.load().numrs_hip_tensor_softmax(self._h, ctypes.byref(h)), h)
+        return self._out(L.load().numrs_hip_tensor_softmax_axis(self._h, a, ctypes.byref(h)), h)
 
     def layer_norm(self, gamma: "Tensor", beta: "Tensor", eps: float = 1e-5) -> "Tensor":
         h = ctypes.c_void_p()

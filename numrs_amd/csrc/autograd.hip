@@ -38,7 +38,8 @@ thread_local bool g_grad_enabled = true;  // mod.rs:194-206
 
 enum class Op {
   Leaf, Add, Sub, Mul, Div, MatMul, Transpose, Unary, Sum, Mean, MSE, CrossEntropy,
-  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention, Linear, LSTM, TimeSlice
+  CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention, Linear, LSTM, TimeSlice, SumAxis,
+  SoftmaxAxis
 };
 
 struct Storage {
@@ -76,7 +77,7 @@ struct Node {
   Op op;
   int kind = 0;       // unary kind / mean flag
   float param = 0.f;  // pow exponent, LayerNorm eps
-  int64_t dims[3] = {0, 0, 0};  // attention batch, seq, heads
+  int64_t dims[3] = {0, 0, 0};  // attention batch, seq, heads; axis ops' [outer, n, inner]
   std::vector<T> inputs;
   std::vector<Buf> saved;  // LayerNorm mean/rstd, int32 labels
 };
@@ -396,6 +397,28 @@ int bw_softmax(const T &out, const float *g, Node &n) {  // backward.rs:521-541
                                     acc);
 }
 
+// sum/mean over one axis: the incoming grad [outer, inner] broadcast back
+// along the reduced axis (divided by n for the mean), backward.rs:208-236
+// applied per reduced slice.
+int bw_sum_axis(const T &out, const float *g, Node &n) {
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  return numrs_hip_broadcast_axis(out->ctx, g, n.dims[0], n.dims[1], n.dims[2], n.kind, dst, acc);
+}
+
+int bw_softmax_axis(const T &out, const float *g, Node &n) {  // backward.rs:521-541
+  const T &x = n.inputs[0];
+  if (!x->requires_grad) return NUMRS_HIP_OK;
+  float *dst;
+  int acc;
+  if (int rc = grad_target(x, &dst, &acc)) return rc;
+  return numrs_hip_softmax_axis_backward(out->ctx, out->data->ptr, g, dst, n.dims[0], n.dims[1],
+                                         n.dims[2], acc);
+}
+
 int bw_layernorm(const T &out, const float *g, Node &n) {
   const T &x = n.inputs[0], &gm = n.inputs[1], &bt = n.inputs[2];
   const int64_t cols = x->shape.back(), rows = x->numel() / cols;
@@ -534,6 +557,8 @@ int run_backward_fn(const T &out) {
     case Op::Linear: return bw_linear(out, g, n);
     case Op::LSTM: return bw_lstm(out, g, n);
     case Op::TimeSlice: return bw_time_slice(out, g, n);
+    case Op::SumAxis: return bw_sum_axis(out, g, n);
+    case Op::SoftmaxAxis: return bw_softmax_axis(out, g, n);
     case Op::Leaf: return NUMRS_HIP_OK;
   }
   return NUMRS_HIP_OK;
@@ -748,6 +773,60 @@ int op_softmax(const T &a, T *out) {
                                          1.0f))
     return rc;
   if (rec) attach(r, Op::Softmax, {a});
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+// x viewed as [outer, n, inner] around `axis`.
+int axis_view(const T &a, int64_t axis, int64_t v[3]) {
+  const int64_t nd = (int64_t)a->shape.size();
+  if (axis < 0 || axis >= nd)
+    return fail(a->ctx, NUMRS_HIP_E_SHAPE, "axis %lld out of range for %lld dimensions",
+                (long long)axis, (long long)nd);
+  v[0] = v[2] = 1;
+  for (int64_t d = 0; d < axis; ++d) v[0] *= a->shape[d];
+  v[1] = a->shape[axis];
+  for (int64_t d = axis + 1; d < nd; ++d) v[2] *= a->shape[d];
+  return NUMRS_HIP_OK;
+}
+
+// ops::sum / ops::mean with Some(axis): the axis is removed from the shape,
+// a 1-D input gives shape [1] (backend/cpu/scalar.rs:584-597).
+int op_sum_axis(const T &a, int64_t axis, bool mean, T *out) {
+  numrs_hip_ctx *ctx = a->ctx;
+  int64_t v[3];
+  if (int rc = axis_view(a, axis, v)) return rc;
+  std::vector<int64_t> shape;
+  for (size_t d = 0; d < a->shape.size(); ++d)
+    if ((int64_t)d != axis) shape.push_back(a->shape[d]);
+  if (shape.empty()) shape.push_back(1);
+  const bool rec = recording({&a});
+  T r;
+  if (int rc = make_tensor(ctx, shape, rec, &r)) return rc;
+  if (int rc = numrs_hip_reduce_axis(ctx, a->data->ptr, v[0], v[1], v[2], mean ? 1 : 0,
+                                     r->data->ptr))
+    return rc;
+  if (rec) {
+    attach(r, Op::SumAxis, {a}, mean ? 1 : 0);
+    std::copy(v, v + 3, r->node->dims);
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_softmax_axis(const T &a, int64_t axis, T *out) {
+  numrs_hip_ctx *ctx = a->ctx;
+  int64_t v[3];
+  if (int rc = axis_view(a, axis, v)) return rc;
+  const bool rec = recording({&a});
+  T r;
+  if (int rc = make_tensor(ctx, a->shape, rec, &r)) return rc;
+  if (int rc = numrs_hip_softmax_axis_forward(ctx, a->data->ptr, r->data->ptr, v[0], v[1], v[2]))
+    return rc;
+  if (rec) {
+    attach(r, Op::SoftmaxAxis, {a});
+    std::copy(v, v + 3, r->node->dims);
+  }
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -1319,6 +1398,21 @@ int numrs_hip_tensor_softmax(numrs_hip_tensor *a, numrs_hip_tensor **out) {
   if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_softmax(a->t, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_sum_axis(numrs_hip_tensor *a, int64_t axis, int mean,
+                              numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_sum_axis(a->t, axis, mean != 0, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_softmax_axis(numrs_hip_tensor *a, int64_t axis, numrs_hip_tensor **out) {
+  if (a == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_softmax_axis(a->t, axis, &r)) return rc;
   return wrap(std::move(r), out);
 }
 

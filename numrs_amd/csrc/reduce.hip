@@ -340,6 +340,44 @@ __global__ void __launch_bounds__(kBlock)
   if (lane == 0) out[r] = acc ? out[r] + s : s;
 }
 
+// Axis reduction x[outer, n, inner] -> out[outer, inner] (ops::sum / ops::mean
+// with Some(axis), backend/cpu/scalar.rs:584-700): one thread per output,
+// summing its n values in axis order (the reference's order for an inner
+// axis); threads of a wave hold consecutive inner indices, so every load
+// of the walk is coalesced.  MEAN divides the sum by n afterwards, as the
+// reference does (`*x /= axis_size as f32`, scalar.rs:314-316).
+__global__ void __launch_bounds__(kBlock)
+    axis_reduce_kernel(const float *__restrict__ x, float *__restrict__ out, int64_t outer,
+                       int64_t n, int64_t inner, int mean) {
+  const int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (o >= outer * inner) return;
+  const int64_t b = o / inner, i = o - b * inner;
+  const float *src = x + b * n * inner + i;
+  float s = 0.0f;
+  for (int64_t k = 0; k < n; ++k) s += src[k * inner];
+  out[o] = mean ? s / (float)n : s;
+}
+
+// out[i] = out[i] / d (the mean's division after a column reduction).
+__global__ void __launch_bounds__(kBlock)
+    div_scalar_kernel(float *__restrict__ out, int64_t count, float d) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < count) out[i] = out[i] / d;
+}
+
+// Backward of the axis reduction: dx[o, k, i] (+)= g[o, i] (or g[o, i] / n
+// for the mean, the division of mean_backward, backward.rs:224-236).
+__global__ void __launch_bounds__(kBlock)
+    broadcast_axis_kernel(const float *__restrict__ g, float *__restrict__ dx, int64_t outer,
+                          int64_t n, int64_t inner, int mean, int acc) {
+  const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (idx >= outer * n * inner) return;
+  const int64_t b = idx / (n * inner), i = idx % inner;
+  const float gv = g[b * inner + i];
+  const float v = mean ? gv / (float)n : gv;
+  dx[idx] = acc ? dx[idx] + v : v;
+}
+
 // General fallback: output element per thread; up to 8 merged axes.
 struct AxisPlan {
   int n;                 // merged axes
@@ -802,6 +840,50 @@ int numrs_hip_sum_to_shape(numrs_hip_ctx *ctx, const float *g, const int64_t *gs
   generic_reduce_kernel<<<grid_for(on, kBlock), kBlock, 0, ctx->stream>>>(g, out, on, plan, red_n,
                                                                           accumulate);
   return numrs_hip::check_launch(ctx, "generic_reduce_kernel");
+}
+
+int numrs_hip_reduce_axis(numrs_hip_ctx *ctx, const float *x, int64_t outer, int64_t n,
+                          int64_t inner, int mean, float *out) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_reduce_axis";
+  if (outer < 0 || n < 0 || inner < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative size", who);
+  const int64_t on = outer * inner;
+  if (on == 0) return NUMRS_HIP_OK;
+  if (out == nullptr || (n > 0 && x == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (n == 0) return numrs_hip_fill(ctx, out, on, mean ? NAN : 0.0f);
+  if (inner == 1) {  // last axis: one wave per row
+    rowreduce_kernel<<<grid_for(outer, 4), kBlock, 0, ctx->stream>>>(x, out, outer, n, 0);
+    if (int rc = numrs_hip::check_launch(ctx, "rowreduce_kernel")) return rc;
+  } else if (outer == 1) {  // leading axis: the column reduction
+    if (int rc = colreduce(ctx, x, nullptr, nullptr, out, n, inner, NUMRS_HIP_UNBROADCAST_CORRECT,
+                           0, 0, inner))
+      return rc;
+  } else {
+    axis_reduce_kernel<<<grid_for(on, kBlock), kBlock, 0, ctx->stream>>>(x, out, outer, n, inner,
+                                                                         mean);
+    return numrs_hip::check_launch(ctx, "axis_reduce_kernel");
+  }
+  if (!mean) return NUMRS_HIP_OK;
+  div_scalar_kernel<<<grid_for(on, kBlock), kBlock, 0, ctx->stream>>>(out, on, (float)n);
+  return numrs_hip::check_launch(ctx, "div_scalar_kernel");
+}
+
+int numrs_hip_broadcast_axis(numrs_hip_ctx *ctx, const float *g, int64_t outer, int64_t n,
+                             int64_t inner, int mean, float *dx, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_broadcast_axis";
+  if (outer < 0 || n < 0 || inner < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative size", who);
+  const int64_t total = outer * n * inner;
+  if (total == 0) return NUMRS_HIP_OK;
+  if (g == nullptr || dx == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  broadcast_axis_kernel<<<grid_for(total, kBlock), kBlock, 0, ctx->stream>>>(g, dx, outer, n,
+                                                                             inner, mean,
+                                                                             accumulate);
+  return numrs_hip::check_launch(ctx, "broadcast_axis_kernel");
 }
 
 }  // extern "C"

@@ -317,6 +317,42 @@ __global__ void __launch_bounds__(kBlock)
   if (lane == 0) idx[row] = bi < 0 ? start : bi;
 }
 
+// Softmax along an inner axis of x[outer, n, inner] (no reference kernel:
+// ops/stats/softmax.rs:13-16 rejects an axis).  One thread per (o, i)
+// walks the axis with stride `inner`; a wave's threads hold consecutive
+// inner indices, so the loads are coalesced.  y = exp(x - max) / sum.
+__global__ void __launch_bounds__(kBlock)
+    softmax_axis_fwd_kernel(const float *x, float *y, int64_t outer, int64_t n, int64_t inner) {
+  const int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (o >= outer * inner) return;
+  const int64_t b = o / inner, i = o - b * inner;
+  const float *src = x + b * n * inner + i;
+  float *dst = y + b * n * inner + i;
+  float m = -INFINITY;
+  for (int64_t k = 0; k < n; ++k) m = fmaxf(m, src[k * inner]);
+  float s = 0.0f;
+  for (int64_t k = 0; k < n; ++k) s += expf(src[k * inner] - m);
+  for (int64_t k = 0; k < n; ++k) dst[k * inner] = expf(src[k * inner] - m) / s;
+}
+
+// softmax_backward (backward.rs:521-541) along an inner axis:
+// dx = y * (g - sum_axis(g * y)).
+__global__ void __launch_bounds__(kBlock)
+    softmax_axis_bwd_kernel(const float *__restrict__ y, const float *g, float *dx, int64_t outer,
+                            int64_t n, int64_t inner, int acc) {
+  const int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (o >= outer * inner) return;
+  const int64_t b = o / inner, i = o - b * inner;
+  const int64_t base = b * n * inner + i;
+  float d = 0.0f;
+  for (int64_t k = 0; k < n; ++k) d += g[base + k * inner] * y[base + k * inner];
+  for (int64_t k = 0; k < n; ++k) {
+    const int64_t j = base + k * inner;
+    const float v = y[j] * (g[j] - d);
+    dx[j] = acc ? dx[j] + v : v;
+  }
+}
+
 // Number of float4 groups per lane for a register-resident row, or 0 when the
 // looped kernel must be used.
 inline int row_nv(int64_t cols, bool aligned) {
@@ -422,6 +458,36 @@ int numrs_hip_argmax_rows(numrs_hip_ctx *ctx, const float *x, int32_t *idx, int6
   }
 #undef NRS_ARGMAX_VEC
   return numrs_hip::check_launch(ctx, "argmax_kernel");
+}
+
+int numrs_hip_softmax_axis_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t outer,
+                                   int64_t n, int64_t inner) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_softmax_axis_forward";
+  if (outer < 0 || n < 0 || inner < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative size", who);
+  if (outer * n * inner == 0) return NUMRS_HIP_OK;
+  if (x == nullptr || y == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (inner == 1) return numrs_hip_softmax_forward(ctx, x, y, outer, n, 1.0f);
+  softmax_axis_fwd_kernel<<<grid_for(outer * inner, kBlock), kBlock, 0, ctx->stream>>>(
+      x, y, outer, n, inner);
+  return numrs_hip::check_launch(ctx, "softmax_axis_fwd_kernel");
+}
+
+int numrs_hip_softmax_axis_backward(numrs_hip_ctx *ctx, const float *y, const float *g, float *dx,
+                                    int64_t outer, int64_t n, int64_t inner, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_softmax_axis_backward";
+  if (outer < 0 || n < 0 || inner < 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative size", who);
+  if (outer * n * inner == 0) return NUMRS_HIP_OK;
+  if (y == nullptr || g == nullptr || dx == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (inner == 1) return numrs_hip_softmax_backward(ctx, y, g, dx, outer, n, accumulate);
+  softmax_axis_bwd_kernel<<<grid_for(outer * inner, kBlock), kBlock, 0, ctx->stream>>>(
+      y, g, dx, outer, n, inner, accumulate);
+  return numrs_hip::check_launch(ctx, "softmax_axis_bwd_kernel");
 }
 
 }  // extern "C"

@@ -38,6 +38,14 @@
  *   orc_sum_avx2_order           equals sequential/fp64 sum on exactly representable inputs
  *   orc_gelu_backward_f64        NEW op (no reference): finite differences + torch fp64 vectors
  *   orc_layernorm_backward_f64   NEW op (no reference): finite differences + torch fp64 vectors
+ *   orc_reduce_axis              exact on integer-valued inputs vs numpy; sum over the axis then the
+ *                                rest equals the full sum; axis = last/first/middle agree with
+ *                                transposed row sums
+ *   orc_broadcast_axis           finite differences of sum/mean(x, axis) . g
+ *   orc_softmax_axis_f64         NEW (no reference axis softmax): equals orc_softmax_rows_f64 of the
+ *                                axis moved last; sums to 1 along the axis
+ *   orc_softmax_axis_backward_f64  finite differences of sum(g * softmax(x, axis)); equals
+ *                                orc_softmax_backward_f64 of the axis moved last
  *   orc_adamw/rmsprop/adagrad/nadam/radam/adadelta/adabound/rprop/lamb_step
  *                                KATs tests/autograd/optim/standard_opts.rs, advanced_opts.rs;
  *                                float64 closed forms of each update rule over several steps;
@@ -629,6 +637,68 @@ EXPORT void orc_softmax_backward_f64(const float *y, const float *g, float *dx, 
     for (int64_t j = 0; j < cols; ++j) rs += (double)go[j] * (double)s[j];
     for (int64_t j = 0; j < cols; ++j) dx[r * cols + j] = (float)((double)s[j] * ((double)go[j] - rs));
   }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Axis reductions and axis softmax                                          */
+/* ------------------------------------------------------------------------- */
+/* x viewed as [outer, n, inner] with the reduced axis in the middle. */
+
+/* ops::sum / ops::mean with Some(axis): every output starts at 0.0 and adds
+ * its n values in axis order (backend/cpu/scalar.rs:722-770, the generic
+ * axis loop visits elements in linear order; :305-312 for the last axis),
+ * then the mean divides by n (:314-316, :785-788). */
+EXPORT void orc_reduce_axis(const float *x, int64_t outer, int64_t n, int64_t inner, int mean,
+                            float *out) {
+  for (int64_t b = 0; b < outer; ++b)
+    for (int64_t i = 0; i < inner; ++i) {
+      float s = 0.0f;
+      for (int64_t k = 0; k < n; ++k) s += x[(b * n + k) * inner + i];
+      out[b * inner + i] = mean ? s / (float)n : s;
+    }
+}
+
+/* Backward of the axis reduction: sum_backward / mean_backward
+ * (backward.rs:208-236) applied per reduced slice, dx = g (or g / n). */
+EXPORT void orc_broadcast_axis(const float *g, int64_t outer, int64_t n, int64_t inner, int mean,
+                               float *dx) {
+  for (int64_t b = 0; b < outer; ++b)
+    for (int64_t k = 0; k < n; ++k)
+      for (int64_t i = 0; i < inner; ++i) {
+        const float gv = g[b * inner + i];
+        dx[(b * n + k) * inner + i] = mean ? gv / (float)n : gv;
+      }
+}
+
+/* Softmax along an axis (NEW: the reference rejects an axis,
+ * ops/stats/softmax.rs:13-16), float64 throughout. */
+EXPORT void orc_softmax_axis_f64(const float *x, int64_t outer, int64_t n, int64_t inner,
+                                 float *y) {
+  for (int64_t b = 0; b < outer; ++b)
+    for (int64_t i = 0; i < inner; ++i) {
+      const float *xs = x + b * n * inner + i;
+      double mx = -INFINITY, s = 0.0;
+      for (int64_t k = 0; k < n; ++k) mx = xs[k * inner] > mx ? xs[k * inner] : mx;
+      for (int64_t k = 0; k < n; ++k) s += exp((double)xs[k * inner] - mx);
+      for (int64_t k = 0; k < n; ++k)
+        y[b * n * inner + i + k * inner] = (float)(exp((double)xs[k * inner] - mx) / s);
+    }
+}
+
+/* softmax_backward (backward.rs:521-541) along an axis, float64 sums:
+ * dx = y * (g - sum_axis(g * y)). */
+EXPORT void orc_softmax_axis_backward_f64(const float *y, const float *g, int64_t outer, int64_t n,
+                                          int64_t inner, float *dx) {
+  for (int64_t b = 0; b < outer; ++b)
+    for (int64_t i = 0; i < inner; ++i) {
+      const int64_t base = b * n * inner + i;
+      double d = 0.0;
+      for (int64_t k = 0; k < n; ++k) d += (double)g[base + k * inner] * (double)y[base + k * inner];
+      for (int64_t k = 0; k < n; ++k) {
+        const int64_t j = base + k * inner;
+        dx[j] = (float)((double)y[j] * ((double)g[j] - d));
+      }
+    }
 }
 
 /* ------------------------------------------------------------------------- */

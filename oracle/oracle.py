@@ -23,6 +23,7 @@ _i32p = ctypes.POINTER(ctypes.c_int32)
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
+_i = ctypes.c_int
 
 
 def build() -> None:
@@ -88,6 +89,10 @@ def _declare(L) -> None:
         "orc_layernorm_fwd_f64": (None, [_f32p] * 6 + [_i64, _i64, _f32]),
         "orc_layernorm_backward_f64": (None, [_f32p] * 6 + [_i64, _i64, _f32, _f64p]),
         "orc_softmax_rows_f64": (None, [_f32p, _f32p, _i64, _i64]),
+        "orc_reduce_axis": (None, [_f32p, _i64, _i64, _i64, _i, _f32p]),
+        "orc_broadcast_axis": (None, [_f32p, _i64, _i64, _i64, _i, _f32p]),
+        "orc_softmax_axis_f64": (None, [_f32p, _i64, _i64, _i64, _f32p]),
+        "orc_softmax_axis_backward_f64": (None, [_f32p, _f32p, _i64, _i64, _i64, _f32p]),
         "orc_softmax_backward_f64": (None, [_f32p] * 3 + [_i64, _i64]),
         "orc_adamw_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 5 + [ctypes.c_int]),
         "orc_rmsprop_step": (None, [_f32p] * 4 + [_i64] + [_f32] * 5),
@@ -317,6 +322,54 @@ def softmax_rows(x):
     y = np.empty_like(x)
     lib().orc_softmax_rows_f64(_p(x), _p(y), rows, cols)
     return y
+
+
+# --- axis reductions and axis softmax -------------------------------------------
+
+def axis_view(shape, axis):
+    """(outer, n, inner) of `shape` around `axis`."""
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    return outer, int(shape[axis]), inner
+
+
+def _axis_out_shape(shape, axis):
+    s = tuple(d for k, d in enumerate(shape) if k != axis)
+    return s if s else (1,)
+
+
+def reduce_axis(x, axis, mean=False):
+    """ops::sum / ops::mean with Some(axis) (scalar.rs:584-788): the axis removed."""
+    x = _f(x)
+    o, n, i = axis_view(x.shape, axis)
+    out = np.empty(_axis_out_shape(x.shape, axis), np.float32)
+    lib().orc_reduce_axis(_p(x), o, n, i, int(mean), _p(out))
+    return out
+
+
+def broadcast_axis(g, shape, axis, mean=False):
+    """Backward of reduce_axis: g broadcast back along the axis (divided by n for the mean)."""
+    g = _f(g)
+    o, n, i = axis_view(shape, axis)
+    dx = np.empty(shape, np.float32)
+    lib().orc_broadcast_axis(_p(g), o, n, i, int(mean), _p(dx))
+    return dx
+
+
+def softmax_axis(x, axis):
+    x = _f(x)
+    o, n, i = axis_view(x.shape, axis)
+    y = np.empty_like(x)
+    lib().orc_softmax_axis_f64(_p(x), o, n, i, _p(y))
+    return y
+
+
+def softmax_axis_backward(y, g, axis):
+    y, g = _f(y), _f(g)
+    o, n, i = axis_view(y.shape, axis)
+    dx = np.empty_like(y)
+    lib().orc_softmax_axis_backward_f64(_p(y), _p(g), o, n, i, _p(dx))
+    return dx
 
 
 # --- unbroadcast --------------------------------------------------------------
