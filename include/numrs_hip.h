@@ -533,6 +533,19 @@ int numrs_hip_optim_zero_grad(numrs_hip_optim *opt);
 int numrs_hip_optim_set_lr(numrs_hip_optim *opt, float lr);
 float numrs_hip_optim_lr(const numrs_hip_optim *opt);
 int numrs_hip_optim_free(numrs_hip_optim *opt);
+/* Optimizer state for checkpoints (TrainingState.optimizer_state of the
+ * reference's JSON checkpoint, llo/model.rs:207-220, ops/model.rs:550-590,
+ * where the reference leaves it empty).  Up to two state slots per parameter
+ * -- SGD: velocity; Adam: m, v; the NUMRS_HIP_OPT_* kinds: their two state
+ * arrays -- plus the step counter t.  Lookahead and L-BFGS are not exported.
+ * get/set copy one slot of one parameter (n = the parameter's element count)
+ * between host memory and the device, synchronously. */
+int numrs_hip_optim_state_info(const numrs_hip_optim *o, int *n_params, int *n_slots,
+                               int64_t *step);
+int numrs_hip_optim_state_get(numrs_hip_optim *o, int param, int slot, float *host, int64_t n);
+int numrs_hip_optim_state_set(numrs_hip_optim *o, int param, int slot, const float *host,
+                              int64_t n);
+int numrs_hip_optim_set_step(numrs_hip_optim *o, int64_t step);
 
 /* AdamW::new, RMSprop::new, AdaGrad::new, NAdam::new, RAdam::new,
  * AdaDelta::new, AdaBound::new, Rprop::new, LAMB::new over parameter tensors

@@ -11,7 +11,7 @@ from ._lib import LIB_PATH, LibraryMissing, header_functions, load  # noqa: F401
 from .autograd import (Tensor, default_context, is_grad_enabled, no_grad,  # noqa: F401
                        set_default_context, set_grad_enabled, set_unbroadcast_mode)
 from .device import Context, DeviceArray, HipError  # noqa: F401
-from . import nn, optim  # noqa: F401,E402
+from . import checkpoint, nn, optim  # noqa: F401,E402
 
 __all__ = ["Context", "DeviceArray", "HipError", "LibraryMissing", "load", "header_functions",
            "LIB_PATH", "Tensor", "no_grad", "is_grad_enabled", "set_grad_enabled",

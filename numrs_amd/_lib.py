@@ -120,6 +120,11 @@ SIGNATURES = {
     "numrs_hip_optim_set_lr": (_i, [_vp, _f]),
     "numrs_hip_optim_lr": (_f, [_vp]),
     "numrs_hip_optim_free": (_i, [_vp]),
+    "numrs_hip_optim_state_info": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                                        ctypes.POINTER(_i64)]),
+    "numrs_hip_optim_state_get": (_i, [_vp, _i, _i, _vp, _i64]),
+    "numrs_hip_optim_state_set": (_i, [_vp, _i, _i, _vp, _i64]),
+    "numrs_hip_optim_set_step": (_i, [_vp, _i64]),
     "numrs_hip_optimizer_step": (_i, [_vp, _i] + [_vp] * 4 + [_i64p, _i, _vp, _i, _i]),
     "numrs_hip_lookahead_update": (_i, [_vp, _vp, _vp, _i64p, _i, _f]),
     "numrs_hip_dot": (_i, [_vp, _vp, _vp, _i64, _vp]),

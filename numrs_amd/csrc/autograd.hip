@@ -1570,6 +1570,65 @@ int numrs_hip_optim_free(numrs_hip_optim *opt) {
   return NUMRS_HIP_OK;
 }
 
+// Optimizer state for checkpoints: the per-parameter state slots (SGD
+// velocity; Adam m, v; the other kinds' s1/s2) and the step counter.
+// Lookahead and L-BFGS keep state of another shape and are not exported.
+int numrs_hip_optim_state_info(const numrs_hip_optim *opt, int *n_params, int *n_slots,
+                               int64_t *step) {
+  if (opt == nullptr) return NUMRS_HIP_E_INVALID;
+  const Optim &o = opt->o;
+  if (o.fam == Family::Lookahead || o.fam == Family::LBFGS)
+    return fail(o.ctx, NUMRS_HIP_E_INVALID, "optimizer state export covers SGD, Adam and the "
+                "element-wise kinds, not Lookahead or L-BFGS");
+  int slots = 0;
+  for (size_t i = 0; i < o.params.size(); ++i) {
+    if (o.s1[i]) slots = std::max(slots, 1);
+    if (o.s2[i]) slots = 2;
+  }
+  if (n_params != nullptr) *n_params = (int)o.params.size();
+  if (n_slots != nullptr) *n_slots = slots;
+  if (step != nullptr) *step = o.t;
+  return NUMRS_HIP_OK;
+}
+
+namespace {
+int state_buf(const Optim &o, int param, int slot, int64_t n, float **ptr) {
+  if (o.fam == Family::Lookahead || o.fam == Family::LBFGS)
+    return fail(o.ctx, NUMRS_HIP_E_INVALID, "no exportable state for Lookahead or L-BFGS");
+  if (param < 0 || param >= (int)o.params.size() || slot < 0 || slot > 1)
+    return fail(o.ctx, NUMRS_HIP_E_INVALID, "state slot %d of parameter %d does not exist", slot,
+                param);
+  const Buf &b = slot == 0 ? o.s1[param] : o.s2[param];
+  if (!b) return fail(o.ctx, NUMRS_HIP_E_INVALID, "parameter %d has no state slot %d", param, slot);
+  if (n != o.params[param]->numel())
+    return fail(o.ctx, NUMRS_HIP_E_SHAPE, "state of parameter %d holds %lld values, not %lld",
+                param, (long long)o.params[param]->numel(), (long long)n);
+  *ptr = b->ptr;
+  return NUMRS_HIP_OK;
+}
+}  // namespace
+
+int numrs_hip_optim_state_get(numrs_hip_optim *opt, int param, int slot, float *host, int64_t n) {
+  if (opt == nullptr || (host == nullptr && n > 0)) return NUMRS_HIP_E_INVALID;
+  float *p = nullptr;
+  if (int rc = state_buf(opt->o, param, slot, n, &p)) return rc;
+  return numrs_hip_download(opt->o.ctx, host, p, (size_t)n * sizeof(float));
+}
+
+int numrs_hip_optim_state_set(numrs_hip_optim *opt, int param, int slot, const float *host,
+                              int64_t n) {
+  if (opt == nullptr || (host == nullptr && n > 0)) return NUMRS_HIP_E_INVALID;
+  float *p = nullptr;
+  if (int rc = state_buf(opt->o, param, slot, n, &p)) return rc;
+  return numrs_hip_upload(opt->o.ctx, p, host, (size_t)n * sizeof(float));
+}
+
+int numrs_hip_optim_set_step(numrs_hip_optim *opt, int64_t step) {
+  if (opt == nullptr || step < 0 || step > 0x7fffffff) return NUMRS_HIP_E_INVALID;
+  opt->o.t = (int)step;
+  return NUMRS_HIP_OK;
+}
+
 int numrs_hip_optim_create(numrs_hip_ctx *ctx, int kind, numrs_hip_tensor **params, int n,
                            const float *hyper, int nhyper, numrs_hip_optim **out) {
   NRS_CHECK_CTX(ctx);

@@ -37,6 +37,33 @@ class Optimizer:
     def num_params(self) -> int:
         return len(self._params)
 
+    def state_info(self) -> tuple[int, int, int]:
+        """(parameters, state slots per parameter, step counter) for checkpoints."""
+        n, k, t = ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+        self.ctx._check(L.load().numrs_hip_optim_state_info(self._h, ctypes.byref(n),
+                                                            ctypes.byref(k), ctypes.byref(t)))
+        return n.value, k.value, t.value
+
+    def get_state(self, param: int, slot: int):
+        """One state slot of one parameter as a float32 array of the parameter's shape."""
+        import numpy as np
+
+        shape = self._params[param].shape()
+        out = np.empty(shape, np.float32)
+        self.ctx._check(L.load().numrs_hip_optim_state_get(self._h, param, slot,
+                                                           out.ctypes.data, out.size))
+        return out
+
+    def set_state(self, param: int, slot: int, values) -> None:
+        import numpy as np
+
+        arr = np.ascontiguousarray(values, np.float32).ravel()
+        self.ctx._check(L.load().numrs_hip_optim_state_set(self._h, param, slot,
+                                                           arr.ctypes.data, arr.size))
+
+    def set_step(self, step: int) -> None:
+        self.ctx._check(L.load().numrs_hip_optim_set_step(self._h, int(step)))
+
     def __del__(self):
         try:
             if self._h:
@@ -62,6 +89,8 @@ class SGD(Optimizer):
         ctx._check(L.load().numrs_hip_optim_sgd(ctx.handle, arr, n, lr, momentum, weight_decay,
                                                 ctypes.byref(h)))
         super().__init__(h.value, ctx, params)
+        # OptimizerKind::SGD (llo/model.rs:31) and the names of the state slots
+        self._ckpt = ("SGD", {"momentum": momentum}, ("velocity",))
 
     @classmethod
     def simple(cls, params, lr: float) -> "SGD":
@@ -81,6 +110,7 @@ class Adam(Optimizer):
         ctx._check(L.load().numrs_hip_optim_adam(ctx.handle, arr, n, lr, beta1, beta2, eps,
                                                  weight_decay, ctypes.byref(h)))
         super().__init__(h.value, ctx, params)
+        self._ckpt = ("Adam", {"beta1": beta1, "beta2": beta2, "epsilon": eps}, ("m", "v"))
 
     @classmethod
     def default(cls, params, lr: float) -> "Adam":
@@ -116,6 +146,8 @@ class RMSprop(Optimizer):
     def __init__(self, params, lr: float, alpha=0.99, eps=1e-8, weight_decay=0.0, momentum=0.0):
         super().__init__(*_kind_optim(L.OPT_RMSPROP, params,
                                       (lr, alpha, eps, weight_decay, momentum)))
+        self._ckpt = ("RMSprop", {"decay": alpha, "epsilon": eps},
+                      ("square_avg", "momentum_buffer"))
 
     @classmethod
     def default(cls, params, lr: float) -> "RMSprop":  # rmsprop.rs:84-86
@@ -127,6 +159,7 @@ class AdaGrad(Optimizer):
 
     def __init__(self, params, lr: float, eps=1e-10, weight_decay=0.0):
         super().__init__(*_kind_optim(L.OPT_ADAGRAD, params, (lr, eps, weight_decay)))
+        self._ckpt = ("AdaGrad", {"epsilon": eps}, ("sum_sq",))
 
     @classmethod
     def default(cls, params, lr: float) -> "AdaGrad":  # adagrad.rs:66-68
