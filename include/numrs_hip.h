@@ -382,6 +382,32 @@ int numrs_hip_dot(numrs_hip_ctx *ctx, const float *x, const float *y, int64_t n,
  * (ops::add/sub/mul/div via promotion_wrappers.rs:25-168). */
 int numrs_hip_binary_forward(numrs_hip_ctx *ctx, int kind, const float *a, const int64_t *ashape,
                              int and_, const float *b, const int64_t *bshape, int bnd, float *out);
+/* DispatchTable (backend/dispatch.rs:51-93) kinds, in the reference's order:
+ * ElementwiseKind (llo/elementwise.rs:38-68) and ReductionKind
+ * (llo/reduction.rs:12-19). */
+enum {
+  NUMRS_HIP_EW_ADD = 0, NUMRS_HIP_EW_MUL, NUMRS_HIP_EW_SUB, NUMRS_HIP_EW_DIV, NUMRS_HIP_EW_POW,
+  NUMRS_HIP_EW_SQRT, NUMRS_HIP_EW_SIN, NUMRS_HIP_EW_COS, NUMRS_HIP_EW_TAN, NUMRS_HIP_EW_ASIN,
+  NUMRS_HIP_EW_ACOS, NUMRS_HIP_EW_ATAN, NUMRS_HIP_EW_ABS, NUMRS_HIP_EW_NEG, NUMRS_HIP_EW_EXP,
+  NUMRS_HIP_EW_LOG, NUMRS_HIP_EW_RELU, NUMRS_HIP_EW_LEAKY_RELU, NUMRS_HIP_EW_SIGMOID,
+  NUMRS_HIP_EW_TANH, NUMRS_HIP_EW_SOFTPLUS
+};
+enum {
+  NUMRS_HIP_RED_SUM = 0, NUMRS_HIP_RED_MAX, NUMRS_HIP_RED_MIN, NUMRS_HIP_RED_MEAN,
+  NUMRS_HIP_RED_ARGMAX, NUMRS_HIP_RED_VARIANCE
+};
+/* DispatchTable.elementwise: out[i] = kind(a[i], b[i]) for same-shape
+ * operands (backend/cpu/scalar.rs:11-150); the unary kinds (SQRT..SOFTPLUS)
+ * read a only and b may be NULL. */
+int numrs_hip_elementwise(numrs_hip_ctx *ctx, int kind, const float *a, const float *b,
+                          float *out, int64_t n);
+/* DispatchTable.reduction: x[shape] reduced over all elements (axis < 0:
+ * out has 1 value) or over `axis` (out holds the shape without that axis),
+ * kind NUMRS_HIP_RED_* with the reference's semantics
+ * (backend/cpu/scalar.rs:495-788): ArgMax returns the index as a float,
+ * Variance is the population variance. */
+int numrs_hip_reduction(numrs_hip_ctx *ctx, int kind, const float *x, const int64_t *shape,
+                        int nd, int axis, float *out);
 /* y = f(x) for the unary kinds (ops.rs:122-211, 453-554; GELU exact-erf). */
 int numrs_hip_unary_forward(numrs_hip_ctx *ctx, int kind, const float *x, float *y, int64_t n,
                             float param);

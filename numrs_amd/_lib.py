@@ -55,6 +55,8 @@ SIGNATURES = {
     "numrs_hip_softmax_ce_backward": (_i, [_vp] * 6 + [_i64, _i64, _i]),
     "numrs_hip_softmax_backward": (_i, [_vp] * 4 + [_i64, _i64, _i]),
     "numrs_hip_reduce_axis": (_i, [_vp, _vp, _i64, _i64, _i64, _i, _vp]),
+    "numrs_hip_elementwise": (_i, [_vp, _i, _vp, _vp, _vp, _i64]),
+    "numrs_hip_reduction": (_i, [_vp, _i, _vp, _i64p, _i, _i, _vp]),
     "numrs_hip_broadcast_axis": (_i, [_vp, _vp, _i64, _i64, _i64, _i, _vp, _i]),
     "numrs_hip_softmax_axis_forward": (_i, [_vp, _vp, _vp, _i64, _i64, _i64]),
     "numrs_hip_softmax_axis_backward": (_i, [_vp] * 4 + [_i64, _i64, _i64, _i]),
@@ -146,6 +148,11 @@ OK, E_INVALID, E_SHAPE, E_HIP, E_NOMEM, E_NODEV = 0, -1, -2, -3, -4, -5
 UNBROADCAST_CORRECT, UNBROADCAST_REFERENCE = 0, 1
 RELU, SIGMOID, TANH, EXP, LOG, GELU, SQRT, SIN, COS, TAN, POW = range(11)
 ADD, SUB, MUL, DIV = range(4)
+# DispatchTable kinds (llo/elementwise.rs:38-68, llo/reduction.rs:12-19)
+(EW_ADD, EW_MUL, EW_SUB, EW_DIV, EW_POW, EW_SQRT, EW_SIN, EW_COS, EW_TAN, EW_ASIN, EW_ACOS,
+ EW_ATAN, EW_ABS, EW_NEG, EW_EXP, EW_LOG, EW_RELU, EW_LEAKY_RELU, EW_SIGMOID, EW_TANH,
+ EW_SOFTPLUS) = range(21)
+RED_SUM, RED_MAX, RED_MIN, RED_MEAN, RED_ARGMAX, RED_VARIANCE = range(6)
 (OPT_ADAMW, OPT_RMSPROP, OPT_ADAGRAD, OPT_NADAM, OPT_RADAM, OPT_ADADELTA, OPT_ADABOUND, OPT_RPROP,
  OPT_LAMB) = range(9)
 SCHED_STEP, SCHED_EXPONENTIAL, SCHED_COSINE, SCHED_PLATEAU, SCHED_WARMUP = range(5)

@@ -25,7 +25,7 @@ OBJ = os.path.join(PKG, "lib", "obj")
 LIB = os.path.join(PKG, "lib", "libnumrs_hip.so")
 
 SOURCES = ["runtime.hip", "gemm.hip", "eltwise.hip", "reduce.hip", "rowwise.hip", "fwd.hip",
-           "attention.hip", "lstm.hip", "optim.hip", "autograd.hip"]
+           "attention.hip", "lstm.hip", "optim.hip", "dispatch.hip", "autograd.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = [

@@ -194,6 +194,18 @@ class Context:
             self.handle, _p(A), _p(B), _p(C), batch, M, K, N, M * K, K * N, M * N,
             int(trans_a), int(trans_b), int(accumulate)))
 
+    # -- DispatchTable forward kernels (backend/dispatch.rs:51-93) -----------------------
+    def elementwise(self, kind: int, a, b, out) -> None:
+        """DispatchTable.elementwise: out = kind(a, b), same shapes; b unused by unary kinds."""
+        self._check(L.load().numrs_hip_elementwise(self.handle, kind, _p(a), _p(b), _p(out),
+                                                   a.size))
+
+    def reduction(self, kind: int, x, axis: int | None, out) -> None:
+        """DispatchTable.reduction over all elements (axis None) or one axis."""
+        shp = (ctypes.c_int64 * max(len(x.shape), 1))(*x.shape)
+        self._check(L.load().numrs_hip_reduction(self.handle, kind, _p(x), shp, len(x.shape),
+                                                 -1 if axis is None else int(axis), _p(out)))
+
     # -- reductions ---------------------------------------------------------------------
     def sum_to_shape(self, g, out, mode=L.UNBROADCAST_CORRECT, accumulate=False) -> None:
         gs = (ctypes.c_int64 * max(len(g.shape), 1))(*g.shape)

@@ -38,6 +38,12 @@
  *   orc_sum_avx2_order           equals sequential/fp64 sum on exactly representable inputs
  *   orc_gelu_backward_f64        NEW op (no reference): finite differences + torch fp64 vectors
  *   orc_layernorm_backward_f64   NEW op (no reference): finite differences + torch fp64 vectors
+ *   orc_elementwise              exact kinds bit-exact vs numpy float32 (fmax for relu); the libm kinds
+ *                                within 2 ulp of float64 numpy; KATs tests/ops_elementwise.rs,
+ *                                ops_math.rs
+ *   orc_reduction                numpy nanmax/nanmin/sum/mean/var on finite data; the NaN and tie
+ *                                rules of ArgMax spelled out case by case; KATs
+ *                                tests/ops_reduction_complex.rs
  *   orc_reduce_axis              exact on integer-valued inputs vs numpy; sum over the axis then the
  *                                rest equals the full sum; axis = last/first/middle agree with
  *                                transposed row sums
@@ -699,6 +705,121 @@ EXPORT void orc_softmax_axis_backward_f64(const float *y, const float *g, int64_
         dx[j] = (float)((double)y[j] * ((double)g[j] - d));
       }
     }
+}
+
+/* ------------------------------------------------------------------------- */
+/* DispatchTable forward kernels (backend/cpu/scalar.rs)                     */
+/* ------------------------------------------------------------------------- */
+
+/* elementwise_scalar (scalar.rs:11-150): kinds in ElementwiseKind order
+ * (llo/elementwise.rs:38-68).  Rust's f32 methods call the C library. */
+EXPORT void orc_elementwise(int kind, const float *a, const float *b, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float x = a[i], y = b ? b[i] : 0.0f;
+    float r;
+    switch (kind) {
+      case 0: r = x + y; break;
+      case 1: r = x * y; break;
+      case 2: r = x - y; break;
+      case 3: r = x / y; break;
+      case 4: r = powf(x, y); break;
+      case 5: r = sqrtf(x); break;
+      case 6: r = sinf(x); break;
+      case 7: r = cosf(x); break;
+      case 8: r = tanf(x); break;
+      case 9: r = asinf(x); break;
+      case 10: r = acosf(x); break;
+      case 11: r = atanf(x); break;
+      case 12: r = fabsf(x); break;
+      case 13: r = -x; break;
+      case 14: r = expf(x); break;
+      case 15: r = logf(x); break;
+      case 16: r = fmaxf(x, 0.0f); break;                     /* x.max(0.0) */
+      case 17: r = x > 0.0f ? x : 0.01f * x; break;          /* :120-125 */
+      case 18: r = 1.0f / (1.0f + expf(-x)); break;          /* :127-131 */
+      case 19: r = tanhf(x); break;
+      default: r = logf(1.0f + expf(x)); break;              /* softplus, :139-143 */
+    }
+    out[i] = r;
+  }
+}
+
+/* reduce_scalar (scalar.rs:495-788), ReductionKind order Sum, Max, Min, Mean,
+ * ArgMax, Variance (llo/reduction.rs:12-19).  axis < 0: all elements (the
+ * Rayon sum of :500 is restated as a sequential sum; its split order is not
+ * fixed).  axis >= 0: x viewed as [outer, n, inner]. */
+EXPORT int orc_reduction(int kind, const float *x, const int64_t *shape, int nd, int axis,
+                         float *out) {
+  int64_t total = 1;
+  for (int d = 0; d < nd; ++d) total *= shape[d];
+  if (axis < 0) {
+    if (total == 0) return -1;
+    float r = 0.0f;
+    switch (kind) {
+      case 0: for (int64_t i = 0; i < total; ++i) r += x[i]; break;
+      case 1: r = -INFINITY; for (int64_t i = 0; i < total; ++i) r = fmaxf(r, x[i]); break;
+      case 2: r = INFINITY; for (int64_t i = 0; i < total; ++i) r = fminf(r, x[i]); break;
+      case 3: for (int64_t i = 0; i < total; ++i) r += x[i]; r = r / (float)total; break;
+      case 4: { /* :517-528 */
+        int64_t mi = 0;
+        float mv = x[0];
+        for (int64_t i = 1; i < total; ++i)
+          if (x[i] > mv) { mv = x[i]; mi = i; }
+        r = (float)mi;
+        break;
+      }
+      default: { /* Welford, :529-541 */
+        const float nn = (float)total;
+        float mean = 0.0f, m2 = 0.0f;
+        for (int64_t i = 0; i < total; ++i) {
+          const float delta = x[i] - mean;
+          mean += delta / (float)(i + 1);
+          const float delta2 = x[i] - mean;
+          m2 += delta * delta2;
+        }
+        r = m2 / nn;
+      }
+    }
+    out[0] = r;
+    return 0;
+  }
+  if (axis >= nd) return -1;
+  int64_t outer = 1, inner = 1;
+  for (int d = 0; d < axis; ++d) outer *= shape[d];
+  for (int d = axis + 1; d < nd; ++d) inner *= shape[d];
+  const int64_t n = shape[axis];
+  for (int64_t b = 0; b < outer; ++b)
+    for (int64_t i = 0; i < inner; ++i) {
+      const float *s = x + b * n * inner + i;
+      float r = 0.0f;
+      switch (kind) {
+        case 0: for (int64_t k = 0; k < n; ++k) r += s[k * inner]; break;
+        case 1: r = -INFINITY; for (int64_t k = 0; k < n; ++k) r = fmaxf(r, s[k * inner]); break;
+        case 2: r = INFINITY; for (int64_t k = 0; k < n; ++k) r = fminf(r, s[k * inner]); break;
+        case 3: for (int64_t k = 0; k < n; ++k) r += s[k * inner]; r = r / (float)n; break;
+        case 4: { /* :345-362, 623-668: fold from (0, -inf), strict '>' */
+          float mv = -INFINITY;
+          int64_t mi = 0;
+          for (int64_t k = 0; k < n; ++k)
+            if (s[k * inner] > mv) { mv = s[k * inner]; mi = k; }
+          r = (float)mi;
+          break;
+        }
+        default: { /* :364-393, 671-717: mean, then mean of squared deviations */
+          float sum = 0.0f;
+          for (int64_t k = 0; k < n; ++k) sum += s[k * inner];
+          const float mean = sum / (float)n;
+          float v = 0.0f;
+          for (int64_t k = 0; k < n; ++k) {
+            const float d = s[k * inner] - mean;
+            v += d * d;
+          }
+          r = v / (float)n;
+        }
+      }
+      out[b * inner + i] = r;
+    }
+  return 0;
 }
 
 /* ------------------------------------------------------------------------- */

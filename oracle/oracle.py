@@ -90,6 +90,8 @@ def _declare(L) -> None:
         "orc_layernorm_backward_f64": (None, [_f32p] * 6 + [_i64, _i64, _f32, _f64p]),
         "orc_softmax_rows_f64": (None, [_f32p, _f32p, _i64, _i64]),
         "orc_reduce_axis": (None, [_f32p, _i64, _i64, _i64, _i, _f32p]),
+        "orc_elementwise": (None, [_i, _f32p, _f32p, _f32p, _i64]),
+        "orc_reduction": (_i, [_i, _f32p, _i64p, _i, _i, _f32p]),
         "orc_broadcast_axis": (None, [_f32p, _i64, _i64, _i64, _i, _f32p]),
         "orc_softmax_axis_f64": (None, [_f32p, _i64, _i64, _i64, _f32p]),
         "orc_softmax_axis_backward_f64": (None, [_f32p, _f32p, _i64, _i64, _i64, _f32p]),
@@ -322,6 +324,32 @@ def softmax_rows(x):
     y = np.empty_like(x)
     lib().orc_softmax_rows_f64(_p(x), _p(y), rows, cols)
     return y
+
+
+# --- DispatchTable forward kernels ----------------------------------------------
+
+def elementwise(kind: int, a, b=None):
+    """elementwise_scalar(a, b, kind) (backend/cpu/scalar.rs:11-150)."""
+    a = _f(a)
+    bb = None if b is None else _f(b)
+    out = np.empty_like(a)
+    lib().orc_elementwise(kind, _p(a), _p(bb), _p(out), a.size)
+    return out
+
+
+def reduction(kind: int, x, axis=None):
+    """reduce_scalar(a, axis, kind) (backend/cpu/scalar.rs:495-788)."""
+    x = _f(x)
+    shape = np.array(x.shape, np.int64)
+    if axis is None:
+        out = np.empty(1, np.float32)
+    else:
+        out = np.empty(_axis_out_shape(x.shape, axis), np.float32)
+    rc = lib().orc_reduction(kind, _p(x), _p(shape, _i64p), x.ndim,
+                             -1 if axis is None else int(axis), _p(out))
+    if rc != 0:
+        raise ValueError("bad reduction arguments")
+    return out
 
 
 # --- axis reductions and axis softmax -------------------------------------------
