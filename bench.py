@@ -650,7 +650,6 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-rows-a", type=int, default=512)
     ap.add_argument("--cpu-rows-b", type=int, default=192)

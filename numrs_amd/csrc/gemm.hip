@@ -410,6 +410,10 @@ __device__ __forceinline__ void stream_read(StreamFrags &f, const float *xl, con
 
 template <bool XRC, bool YRC>
 __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) {
+  // Split-K: consecutive logical tiles are the k-ranges of one output tile
+  // (the planner leaves no range empty).
+  const int split = tile % d.splits;
+  tile /= d.splits;
   const int per_group = kGroupRows * d.tiles_q;
   const int gidx = tile / per_group;
   const int first_p = gidx * kGroupRows;
@@ -428,7 +432,16 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   const float *__restrict__ X = d.X + zo * d.bsx + zi * d.bsx2;
   const float *__restrict__ Y = d.Y + zo * d.bsy + zi * d.bsy2;
   float *__restrict__ C = d.C + zo * d.bsc + zi * d.bsc2;
-  const int nk = d.R / kBR;
+  int64_t ldc = d.ldc;
+  const int kt0 = split * d.ktiles_per_split;
+  const int nk = min(d.R / kBR - kt0, d.ktiles_per_split);
+  X += XRC ? (int64_t)kt0 * kBR : (int64_t)kt0 * kBR * d.ldx;
+  Y += YRC ? (int64_t)kt0 * kBR : (int64_t)kt0 * kBR * d.ldy;
+  const bool part = d.splits > 1;
+  if (part) {  // plain partial product, row stride Q; splitk_reduce finishes
+    C = d.partial + (int64_t)split * d.P * d.Q;
+    ldc = d.Q;
+  }
 
   // Prologue: tiles 0, 1, 2 into stages 0, 1, 2; wait for tile 0.
   stream_issue<XRC, kSP>(X, d.ldx, p0, 0, g_sx0, wave, lane);
@@ -556,10 +569,14 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int p = p0 + wp * 128 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-        float *dst = C + (int64_t)p * d.ldc + q;
-        float v = d.alpha * tot[bi][bj][i];
-        if (d.bias != nullptr) v = v + d.bias[q];
-        *dst = d.accumulate ? *dst + v : v;
+        float *dst = C + (int64_t)p * ldc + q;
+        if (part) {
+          *dst = tot[bi][bj][i];
+        } else {
+          float v = d.alpha * tot[bi][bj][i];
+          if (d.bias != nullptr) v = v + d.bias[q];
+          *dst = d.accumulate ? *dst + v : v;
+        }
       }
     }
 }
@@ -575,6 +592,16 @@ __global__ void __launch_bounds__(kThreads, 1) matmul_backward_stream(Gemm da, G
     stream_tile<true, true>(da, tile, blockIdx.y);
   else
     stream_tile<false, false>(db, tile - tiles_a, blockIdx.y);
+}
+
+// The Linear backward pair on the streamed path: dx = g W (NN) with
+// dW = g^T x (TN), logical tiles [0, tiles_a) for dx.
+__global__ void __launch_bounds__(kThreads, 1) linear_backward_stream(Gemm dx, Gemm dw, int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<true, false>(dx, tile, blockIdx.y);
+  else
+    stream_tile<false, false>(dw, tile - tiles_a, blockIdx.y);
 }
 
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
@@ -637,6 +664,74 @@ Gemm as_stream(Gemm g) {
   return g;
 }
 
+// Split plan for the streamed path (batch 1), which runs one workgroup per
+// CU.  A workgroup's time is its number of reduction tiles plus about one
+// tile of fixed cost (prologue, epilogue), and a grid of W workgroups runs in
+// ceil(W / CUs) waves; a split product also writes and re-reads its fp32
+// partials (8 bytes per element per split).  Candidate per-workgroup
+// reduction lengths T are ceil(k / s) for s = 1..32 of either product; each
+// product is cut into ceil(k / T) ranges of equal length (at most 32 ranges,
+// none empty) and the plan with the smallest estimate wins, ties going to
+// fewer workgroups.  Product b is absent when tb == 0.
+struct StreamPlan {
+  int sa, sb;
+};
+
+int stream_cut(int64_t k, int64_t T) {
+  const int64_t s = std::min<int64_t>((k + T - 1) / T, 32);
+  const int64_t per = (k + s - 1) / s;
+  return (int)((k + per - 1) / per);
+}
+
+StreamPlan plan_stream(int64_t cus, int64_t ta, int64_t ka, int64_t pqa, int64_t tb, int64_t kb,
+                       int64_t pqb) {
+  constexpr double kTileUs = 4.3;        // one 256 x 128 x 32 step at ~80% of peak
+  cus = std::max<int64_t>(cus, 1);
+  constexpr double kBytesPerUs = 6.0e6;  // streaming rate of the partial traffic
+  StreamPlan best{1, 1};
+  double best_t = 0.0;
+  int64_t best_w = 0;
+  bool first = true;
+  for (int cand = 0; cand < 64; ++cand) {
+    const int64_t k = cand < 32 ? ka : kb;
+    if (cand >= 32 && tb == 0) break;
+    const int64_t T = (k + (cand & 31)) / ((cand & 31) + 1);
+    if (T < 1) continue;
+    const int sa = stream_cut(ka, T), sb = tb ? stream_cut(kb, T) : 1;
+    const int64_t la = (ka + sa - 1) / sa, lb = tb ? (kb + sb - 1) / sb : 0;
+    const int64_t w = ta * sa + tb * sb;
+    double t = (double)((w + cus - 1) / cus) * (double)(std::max(la, lb) + 1) * kTileUs;
+    if (sa > 1) t += 8.0 * sa * pqa / kBytesPerUs + 2.0;
+    if (sb > 1) t += 8.0 * sb * pqb / kBytesPerUs + 2.0;
+    if (first || t < best_t || (t == best_t && w < best_w)) {
+      first = false;
+      best = {sa, sb};
+      best_t = t;
+      best_w = w;
+    }
+  }
+  return best;
+}
+
+// Whether a batch-1 product (or pair) goes to the streamed path: enough work
+// for four 256 x 128 x 32 steps per CU.
+bool stream_worth(numrs_hip_ctx *ctx, int64_t work_tiles) {
+  return work_tiles >= 4 * (int64_t)ctx->num_cus;
+}
+
+// Points the split products of a streamed plan at the context's workspace.
+int stream_splits(numrs_hip_ctx *ctx, Gemm &ga, int sa, Gemm *gb, int sb) {
+  const size_t na = sa > 1 ? (size_t)sa * ga.P * ga.Q : 0;
+  const size_t nb = gb != nullptr && sb > 1 ? (size_t)sb * gb->P * gb->Q : 0;
+  if (na + nb == 0) return NUMRS_HIP_OK;
+  void *ws = nullptr;
+  if (int rc = numrs_hip::workspace(ctx, (na + nb) * sizeof(float), &ws)) return rc;
+  float *base = static_cast<float *>(ws);
+  if (sa > 1) apply_splits(ga, sa, base);
+  if (nb) apply_splits(*gb, sb, base + na);
+  return NUMRS_HIP_OK;
+}
+
 int check_dims(numrs_hip_ctx *ctx, const char *who, int64_t batch, int64_t M, int64_t K,
                int64_t N) {
   if (batch < 0 || M < 0 || K < 0 || N < 0)
@@ -686,9 +781,16 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   const int64_t n_tiles = (int64_t)g.tiles_p * g.tiles_q;
   if (n_tiles == 0 || batch == 0) return NUMRS_HIP_OK;
   if (stream_fits(g, XRC, YRC)) {
-    const Gemm sg = as_stream(g);
-    const int64_t st = (int64_t)sg.tiles_p * sg.tiles_q;
-    if (st * batch >= ctx->num_cus) {
+    Gemm sg = as_stream(g);
+    const int64_t st = (int64_t)sg.tiles_p * sg.tiles_q, nk = sg.R / kBR;
+    if (batch == 1 && stream_worth(ctx, st * nk)) {
+      const StreamPlan pl = plan_stream(ctx->num_cus, st, nk, (int64_t)sg.P * sg.Q, 0, 0, 0);
+      if (int rc = stream_splits(ctx, sg, pl.sa, nullptr, 1)) return rc;
+      gemm_stream_kernel<XRC, YRC><<<dim3((unsigned)(st * pl.sa), 1), kThreads, 0, ctx->stream>>>(sg);
+      if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
+      return pl.sa > 1 ? reduce_splits(ctx, sg) : NUMRS_HIP_OK;
+    }
+    if (batch > 1 && st * batch >= ctx->num_cus) {
       dim3 grid((unsigned)st, (unsigned)batch);
       gemm_stream_kernel<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
       return numrs_hip::check_launch(ctx, "gemm_stream_kernel");
@@ -745,9 +847,21 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   if (dA == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
   if (dB == nullptr) return gemm_dispatch(ctx, ga, batch, true, true);
   if (stream_fits(ga, true, true) && stream_fits(gb, false, false)) {
-    const Gemm sa = as_stream(ga), sb = as_stream(gb);
+    Gemm sa = as_stream(ga), sb = as_stream(gb);
     const int64_t ta = (int64_t)sa.tiles_p * sa.tiles_q, tb = (int64_t)sb.tiles_p * sb.tiles_q;
-    if ((ta + tb) * batch >= ctx->num_cus) {
+    const int64_t ka = sa.R / kBR, kb = sb.R / kBR;
+    if (batch == 1 && stream_worth(ctx, ta * ka + tb * kb)) {
+      const StreamPlan pl = plan_stream(ctx->num_cus, ta, ka, (int64_t)sa.P * sa.Q, tb, kb,
+                                        (int64_t)sb.P * sb.Q);
+      if (int rc2 = stream_splits(ctx, sa, pl.sa, &sb, pl.sb)) return rc2;
+      dim3 grid((unsigned)(ta * pl.sa + tb * pl.sb), 1);
+      matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
+      if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
+      if (pl.sa > 1)
+        if (int rc2 = reduce_splits(ctx, sa)) return rc2;
+      return pl.sb > 1 ? reduce_splits(ctx, sb) : NUMRS_HIP_OK;
+    }
+    if (batch > 1 && (ta + tb) * batch >= ctx->num_cus) {
       dim3 grid((unsigned)(ta + tb), (unsigned)batch);
       matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
       return numrs_hip::check_launch(ctx, "matmul_backward_stream");
@@ -842,6 +956,25 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
   if (!has_a && !has_b) return NUMRS_HIP_OK;
   if (!has_a) return gemm_dispatch(ctx, gb, 1, false, false);
   if (!has_b) return gemm_dispatch(ctx, ga, 1, true, first_nt);
+  if (stream_fits(ga, true, first_nt) && stream_fits(gb, false, false)) {
+    Gemm sa = as_stream(ga), sb = as_stream(gb);
+    const int64_t ta = (int64_t)sa.tiles_p * sa.tiles_q, tb = (int64_t)sb.tiles_p * sb.tiles_q;
+    const int64_t ka = sa.R / kBR, kb = sb.R / kBR;
+    if (stream_worth(ctx, ta * ka + tb * kb)) {
+      const StreamPlan pl = plan_stream(ctx->num_cus, ta, ka, (int64_t)sa.P * sa.Q, tb, kb,
+                                        (int64_t)sb.P * sb.Q);
+      if (int rc = stream_splits(ctx, sa, pl.sa, &sb, pl.sb)) return rc;
+      dim3 grid((unsigned)(ta * pl.sa + tb * pl.sb), 1);
+      if (first_nt)
+        matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
+      else
+        linear_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
+      if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
+      if (pl.sa > 1)
+        if (int rc = reduce_splits(ctx, sa)) return rc;
+      return pl.sb > 1 ? reduce_splits(ctx, sb) : NUMRS_HIP_OK;
+    }
+  }
   // Joint split plan, balanced by work: the pair shares one grid, and a
   // workgroup's time is its number of reduction tiles.  The weight gradient
   // (long reduction over tokens) next to dx (short reduction over features)

@@ -664,7 +664,7 @@ def test_error_paths(hip_ctx):
 
 
 @pytest.mark.parametrize("M,K,N", [(4096, 512, 512), (4096, 256, 384), (8192, 128, 64),
-                                   (3000, 130, 70)])
+                                   (3000, 130, 70), (1024, 1024, 1024), (2048, 1024, 512)])
 @pytest.mark.parametrize("acc", [False, True])
 def test_matmul_backward_split_k(hip_ctx, rng, M, K, N, acc):
     # Weight-gradient shapes: dB = A^T dC has few output tiles and a long
@@ -683,10 +683,17 @@ def test_matmul_backward_split_k(hip_ctx, rng, M, K, N, acc):
     ra, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=(0, 64))
     base_a = ga[:64].astype(np.float64) if acc else 0.0
     assert_contraction(dA.numpy()[:64], base_a + ra[:64], N, what="dA rows")
-    # determinism: a second run gives identical bits
+    # determinism: the same call again gives identical bits
+    dA2 = c.to_device(ga) if acc else c.empty((M, K))
     dB2 = c.to_device(gb) if acc else c.empty((K, N))
-    c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), None, dB2, accumulate=acc)
+    c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), dA2, dB2, accumulate=acc)
     assert_bits(dB2.numpy(), dB.numpy(), "split-k determinism")
+    assert_bits(dA2.numpy(), dA.numpy(), "split-k determinism (dA)")
+    # dB alone: its own split plan (the pair's plan balances both products,
+    # so the rounding may differ from the pair's dB), same tolerance.
+    dB3 = c.to_device(gb) if acc else c.empty((K, N))
+    c.matmul_backward(c.to_device(dC), c.to_device(A), c.to_device(B), None, dB3, accumulate=acc)
+    assert_contraction(dB3.numpy(), base_b + rb, M, ref32=None if acc else rb32, what="dB alone")
 
 
 def test_matmul_forward_split_k_long_reduction(hip_ctx, rng):
@@ -697,8 +704,11 @@ def test_matmul_forward_split_k_long_reduction(hip_ctx, rng):
     assert_contraction(C.numpy(), A.astype(np.float64) @ B.astype(np.float64), 8192)
 
 
+# (4096, 512, 2048), (4096, 2048, 512) and (4096, 512, 512) are the C4 block's
+# Linear shapes: the streamed 256 x 128 path with split-K ranges planned per
+# product (dx and dW in one grid, each reduced in split order).
 @pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (64, 128, 10), (4096, 512, 2048),
-                                        (33, 17, 5)])
+                                        (4096, 2048, 512), (4096, 512, 512), (33, 17, 5)])
 def test_linear_forward_backward(hip_ctx, rng, T, fin, fout):
     # Linear::forward (nn.rs:217-235) and the grads its Transpose/MatMul/Add
     # nodes produce (backward.rs:43-54, 113-149, 305-312).
