@@ -259,28 +259,44 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
   }
 }
 
-// C = alpha * sum_s partial[s] (+ C), splits added in order s = 0, 1, ...
-__global__ void __launch_bounds__(256)
-    splitk_reduce(const float *__restrict__ partial, float *__restrict__ C, int64_t ldc, int P,
-                  int Q, int splits, float alpha, int acc, const float *__restrict__ bias) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t n = (int64_t)P * Q;
-  if (i >= n) return;
-  // Loads of all splits are issued before the ordered adds.
-  constexpr int kBatch = 8;
-  float s = 0.0f;
-  for (int k0 = 0; k0 < splits; k0 += kBatch) {
-    float v[kBatch];
+// One split product's reduction: C = alpha * sum_s partial[s] (+ bias[q])
+// (+ C), partial s at partial + s*n with row stride Q.
+struct SplitSet {
+  const float *partial;
+  float *C;
+  const float *bias;
+  int64_t ldc, n;
+  int Q, splits, acc;
+  float alpha;
+};
+
+// Splits are added in order s = 0, 1, ... (deterministic); the loads of a
+// batch of splits are issued before its ordered adds.  blockIdx.y selects one
+// of two products reduced by the same launch.  VEC: four consecutive
+// elements of one row per thread (Q, ldc and the pointers 16-byte aligned).
+template <bool VEC>
+__global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1) {
+  const SplitSet &d = blockIdx.y ? s1 : s0;
+  typedef typename std::conditional<VEC, f4, float>::type V;
+  constexpr int kW = VEC ? 4 : 1;
+  constexpr int kBatch = VEC ? 4 : 8;
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kW;
+  if (e >= d.n) return;
+  V s = V{};
+  for (int k0 = 0; k0 < d.splits; k0 += kBatch) {
+    V v[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) v[u] = k0 + u < splits ? partial[(k0 + u) * n + i] : 0.0f;
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < d.splits) v[u] = *reinterpret_cast<const V *>(d.partial + (k0 + u) * d.n + e);
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) s += v[u];
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < d.splits) s += v[u];
   }
-  const int64_t p = i / Q, q = i - p * Q;
-  float *dst = C + p * ldc + q;
-  float v = alpha * s;
-  if (bias != nullptr) v = v + bias[q];
-  *dst = acc ? *dst + v : v;
+  const int64_t p = e / d.Q, q = e - p * d.Q;
+  V *dst = reinterpret_cast<V *>(d.C + p * d.ldc + q);
+  V v = d.alpha * s;
+  if (d.bias != nullptr) v = v + *reinterpret_cast<const V *>(d.bias + q);
+  *dst = d.acc ? *dst + v : v;
 }
 
 // Maps the hardware workgroup id to a logical tile so that XCD k (which
@@ -344,6 +360,15 @@ constexpr int kSStageX = kSP * kBR;         // floats per X stage (32 KiB)
 constexpr int kSStageY = kSQ * kBR;         // floats per Y stage (16 KiB)
 constexpr int kSDma = kSP / 32 + kSQ / 32;  // DMA instructions per wave per tile
 typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (expcnt and lgkmcnt left at their no-wait maxima).  The
+// 6-bit vmcnt is split: bits 3:0 of the immediate hold vmcnt[3:0] and bits
+// 15:14 hold vmcnt[5:4].
+constexpr int wait_vm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
+static_assert(wait_vm(0) == 0x3f70 && wait_vm(12) == 0x3f7c && wait_vm(24) == 0x7f78,
+              "vmcnt immediate encoding");
+static_assert(2 * (kSP / 32 + kSQ / 32) < 64, "vmcnt is 6 bits");
 
 __shared__ __attribute__((aligned(1024))) float g_sx0[kSStageX];
 __shared__ __attribute__((aligned(1024))) float g_sy0[kSStageY];
@@ -453,11 +478,11 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   if (nk > 2) {
     stream_issue<XRC, kSP>(X, d.ldx, p0, 2 * kBR, g_sx2, wave, lane);
     stream_issue<YRC, kSQ>(Y, d.ldy, q0, 2 * kBR, g_sy2, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0x3f70 | (2 * kSDma));  // vmcnt(24)
+    __builtin_amdgcn_s_waitcnt(wait_vm(2 * kSDma));  // tile 0 landed, 1 and 2 may fly
   } else if (nk > 1) {
-    __builtin_amdgcn_s_waitcnt(0x3f70 | kSDma);  // vmcnt(12)
+    __builtin_amdgcn_s_waitcnt(wait_vm(kSDma));
   } else {
-    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(wait_vm(0));
   }
   __syncthreads();
 
@@ -490,9 +515,9 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
         stream_read<XRC, YRC>(nxt, xl, yl, wp, wq, c, h, g + 1);
       } else if (kNext) {
         if (kTwo)
-          __builtin_amdgcn_s_waitcnt(0x3f70 | kSDma);  // tile kt+1 landed, kt+2 may fly
+          __builtin_amdgcn_s_waitcnt(wait_vm(kSDma));  // tile kt+1 landed, kt+2 may fly
         else
-          __builtin_amdgcn_s_waitcnt(0x3f70);
+          __builtin_amdgcn_s_waitcnt(wait_vm(0));
         __syncthreads();
         if (kIssue) {
           stream_issue<XRC, kSP>(X, d.ldx, p0, (kt + 3) * kBR, xl, wave, lane);
@@ -628,10 +653,34 @@ void apply_splits(Gemm &g, int splits, float *partial) {
   g.partial = partial;
 }
 
-int reduce_splits(numrs_hip_ctx *ctx, const Gemm &g) {
-  const int64_t n = (int64_t)g.P * g.Q;
-  splitk_reduce<<<grid_for(n, 256), 256, 0, ctx->stream>>>(g.partial, g.C, g.ldc, g.P, g.Q,
-                                                          g.splits, g.alpha, g.accumulate, g.bias);
+// Reduces the split products among a and b (either may be null or unsplit)
+// with one launch.
+int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b) {
+  const Gemm *g[2];
+  int m = 0;
+  if (a != nullptr && a->splits > 1) g[m++] = a;
+  if (b != nullptr && b->splits > 1) g[m++] = b;
+  if (m == 0) return NUMRS_HIP_OK;
+  SplitSet set[2];
+  bool vec = true;
+  int64_t most = 0;
+  for (int i = 0; i < m; ++i) {
+    const Gemm &d = *g[i];
+    set[i] = SplitSet{d.partial, d.C, d.bias, d.ldc, (int64_t)d.P * d.Q, d.Q, d.splits,
+                      d.accumulate, d.alpha};
+    vec = vec && d.Q % 4 == 0 && d.ldc % 4 == 0 && numrs_hip::aligned16(d.C) &&
+          numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias));
+    most = std::max(most, set[i].n);
+  }
+  if (m == 1) set[1] = set[0];
+  const int64_t blocks = (most / (vec ? 4 : 1) + 255) / 256;
+  if (blocks > 0x7fffffff)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "splitk_reduce: too large");
+  dim3 grid((unsigned)blocks, (unsigned)m);
+  if (vec)
+    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1]);
+  else
+    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1]);
   return numrs_hip::check_launch(ctx, "splitk_reduce");
 }
 
@@ -788,7 +837,7 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
       if (int rc = stream_splits(ctx, sg, pl.sa, nullptr, 1)) return rc;
       gemm_stream_kernel<XRC, YRC><<<dim3((unsigned)(st * pl.sa), 1), kThreads, 0, ctx->stream>>>(sg);
       if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
-      return pl.sa > 1 ? reduce_splits(ctx, sg) : NUMRS_HIP_OK;
+      return reduce_splits(ctx, &sg, nullptr);
     }
     if (batch > 1 && st * batch >= ctx->num_cus) {
       dim3 grid((unsigned)st, (unsigned)batch);
@@ -811,7 +860,7 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   else
     gemm_kernel<XRC, YRC, false><<<grid, kThreads, 0, ctx->stream>>>(g);
   if (int rc = numrs_hip::check_launch(ctx, "gemm_kernel")) return rc;
-  return splits > 1 ? reduce_splits(ctx, g) : NUMRS_HIP_OK;
+  return reduce_splits(ctx, &g, nullptr);
 }
 
 int gemm_dispatch(numrs_hip_ctx *ctx, const Gemm &g, int64_t batch, bool xrc, bool yrc) {
@@ -857,9 +906,7 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
       dim3 grid((unsigned)(ta * pl.sa + tb * pl.sb), 1);
       matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
       if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
-      if (pl.sa > 1)
-        if (int rc2 = reduce_splits(ctx, sa)) return rc2;
-      return pl.sb > 1 ? reduce_splits(ctx, sb) : NUMRS_HIP_OK;
+      return reduce_splits(ctx, &sa, &sb);
     }
     if (batch > 1 && (ta + tb) * batch >= ctx->num_cus) {
       dim3 grid((unsigned)(ta + tb), (unsigned)batch);
@@ -886,10 +933,7 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   else
     matmul_backward_kernel<false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
   if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_kernel")) return rc2;
-  if (sa_ > 1)
-    if (int rc2 = reduce_splits(ctx, ga)) return rc2;
-  if (sb_ > 1) return reduce_splits(ctx, gb);
-  return NUMRS_HIP_OK;
+  return reduce_splits(ctx, &ga, &gb);
 }
 
 int matmul_impl(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, int64_t batch,
@@ -970,9 +1014,7 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
       else
         linear_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
       if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
-      if (pl.sa > 1)
-        if (int rc = reduce_splits(ctx, sa)) return rc;
-      return pl.sb > 1 ? reduce_splits(ctx, sb) : NUMRS_HIP_OK;
+      return reduce_splits(ctx, &sa, &sb);
     }
   }
   // Joint split plan, balanced by work: the pair shares one grid, and a
@@ -1019,10 +1061,7 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
     else gemm_pair_kernel<true, false, false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
   }
   if (int rc = numrs_hip::check_launch(ctx, "gemm_pair_kernel")) return rc;
-  if (sa_ > 1)
-    if (int rc = reduce_splits(ctx, ga)) return rc;
-  if (sb_ > 1) return reduce_splits(ctx, gb);
-  return NUMRS_HIP_OK;
+  return reduce_splits(ctx, &ga, &gb);
 }
 
 }  // namespace
