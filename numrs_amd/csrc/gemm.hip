@@ -353,12 +353,21 @@ __global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, G
 //     bit 2 is set.  Both keep the fragment reads free of bank conflicts.
 //   * Two-level accumulation with the MFMA partials added into the running
 //     totals every three reduction tiles (96 reduction steps).
-// Requires P % 256 == 0, Q % 128 == 0, R % 32 == 0 and vec_ok operands.
+//   * A small-tile variant (128 x 64, 24 KiB stages, two workgroups per CU,
+//     each wave 64 x 32 = 2 x 1 MFMA blocks) serves products whose output is
+//     too small to give every CU a large tile's worth of work; the split
+//     planner picks the tile and the split-K ranges per product.
+// Requires P % TP == 0, Q % TQ == 0, R % 32 == 0 and vec_ok operands.
 // ---------------------------------------------------------------------------
-constexpr int kSP = 256, kSQ = 128;         // workgroup tile
-constexpr int kSStageX = kSP * kBR;         // floats per X stage (32 KiB)
-constexpr int kSStageY = kSQ * kBR;         // floats per Y stage (16 KiB)
-constexpr int kSDma = kSP / 32 + kSQ / 32;  // DMA instructions per wave per tile
+constexpr int kSP = 256, kSQ = 128;  // large workgroup tile
+constexpr int kHP = 128, kHQ = 64;   // small workgroup tile
+template <int TP, int TQ>
+struct StreamCfg {
+  static constexpr int kStageX = TP * kBR;         // floats per X stage
+  static constexpr int kStageY = TQ * kBR;         // floats per Y stage
+  static constexpr int kDma = TP / 32 + TQ / 32;   // DMA instructions per wave per tile
+  static constexpr int kBI = TP / 64, kBJ = TQ / 64;  // 32 x 32 blocks per wave (2 x 2 waves)
+};
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
@@ -368,14 +377,22 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int wait_vm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
 static_assert(wait_vm(0) == 0x3f70 && wait_vm(12) == 0x3f7c && wait_vm(24) == 0x7f78,
               "vmcnt immediate encoding");
-static_assert(2 * (kSP / 32 + kSQ / 32) < 64, "vmcnt is 6 bits");
+static_assert(2 * StreamCfg<kSP, kSQ>::kDma < 64, "vmcnt is 6 bits");
 
-__shared__ __attribute__((aligned(1024))) float g_sx0[kSStageX];
-__shared__ __attribute__((aligned(1024))) float g_sy0[kSStageY];
-__shared__ __attribute__((aligned(1024))) float g_sx1[kSStageX];
-__shared__ __attribute__((aligned(1024))) float g_sy1[kSStageY];
-__shared__ __attribute__((aligned(1024))) float g_sx2[kSStageX];
-__shared__ __attribute__((aligned(1024))) float g_sy2[kSStageY];
+// Three LDS stages per tile size: distinct objects, so the compiler's waitcnt
+// model sees that fragment reads never alias the in-flight DMA.
+__shared__ __attribute__((aligned(1024))) float g_sx0[StreamCfg<kSP, kSQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_sy0[StreamCfg<kSP, kSQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_sx1[StreamCfg<kSP, kSQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_sy1[StreamCfg<kSP, kSQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_sx2[StreamCfg<kSP, kSQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_sy2[StreamCfg<kSP, kSQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_hx0[StreamCfg<kHP, kHQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_hy0[StreamCfg<kHP, kHQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_hx1[StreamCfg<kHP, kHQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_hy1[StreamCfg<kHP, kHQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_hx2[StreamCfg<kHP, kHQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_hy2[StreamCfg<kHP, kHQ>::kStageY];
 
 __device__ __forceinline__ int rc_swizzle(int p) { return (p & 7) ^ ((p >> 3) & 1); }
 
@@ -420,21 +437,26 @@ __device__ __forceinline__ f4 stream_frag(const float *lds, int pb, int c, int h
   }
 }
 
+template <int BI, int BJ>
 struct StreamFrags {
-  f4 a[4], b[2];
+  f4 a[BI], b[BJ];
 };
 
-template <bool XRC, bool YRC>
-__device__ __forceinline__ void stream_read(StreamFrags &f, const float *xl, const float *yl,
-                                            int wp, int wq, int c, int h, int g) {
+template <bool XRC, bool YRC, int TP, int TQ>
+__device__ __forceinline__ void stream_read(StreamFrags<TP / 64, TQ / 64> &f, const float *xl,
+                                            const float *yl, int wp, int wq, int c, int h, int g) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) f.a[i] = stream_frag<XRC, kSP>(xl, wp * 128 + 32 * i, c, h, g);
+  for (int i = 0; i < TP / 64; ++i)
+    f.a[i] = stream_frag<XRC, TP>(xl, wp * (TP / 2) + 32 * i, c, h, g);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) f.b[j] = stream_frag<YRC, kSQ>(yl, wq * 64 + 32 * j, c, h, g);
+  for (int j = 0; j < TQ / 64; ++j)
+    f.b[j] = stream_frag<YRC, TQ>(yl, wq * (TQ / 2) + 32 * j, c, h, g);
 }
 
-template <bool XRC, bool YRC>
+template <bool XRC, bool YRC, int TP, int TQ>
 __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) {
+  using Cfg = StreamCfg<TP, TQ>;
+  constexpr int kBI = Cfg::kBI, kBJ = Cfg::kBJ, kDma = Cfg::kDma;
   // Split-K: consecutive logical tiles are the k-ranges of one output tile
   // (the planner leaves no range empty).
   const int split = tile % d.splits;
@@ -451,7 +473,7 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   const int lane = tid & 63, wave = tid >> 6;
   const int wp = wave >> 1, wq = wave & 1;
   const int c = lane & 31, h = lane >> 5;
-  const int p0 = tp * kSP, q0 = tq * kSQ;
+  const int p0 = tp * TP, q0 = tq * TQ;
 
   const int64_t zo = batch / d.binner, zi = batch - zo * d.binner;
   const float *__restrict__ X = d.X + zo * d.bsx + zi * d.bsx2;
@@ -468,34 +490,43 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
     ldc = d.Q;
   }
 
+  float *x0, *x1, *x2, *y0, *y1, *y2;
+  if constexpr (TP == kSP) {
+    x0 = g_sx0, x1 = g_sx1, x2 = g_sx2;
+    y0 = g_sy0, y1 = g_sy1, y2 = g_sy2;
+  } else {
+    x0 = g_hx0, x1 = g_hx1, x2 = g_hx2;
+    y0 = g_hy0, y1 = g_hy1, y2 = g_hy2;
+  }
+
   // Prologue: tiles 0, 1, 2 into stages 0, 1, 2; wait for tile 0.
-  stream_issue<XRC, kSP>(X, d.ldx, p0, 0, g_sx0, wave, lane);
-  stream_issue<YRC, kSQ>(Y, d.ldy, q0, 0, g_sy0, wave, lane);
+  stream_issue<XRC, TP>(X, d.ldx, p0, 0, x0, wave, lane);
+  stream_issue<YRC, TQ>(Y, d.ldy, q0, 0, y0, wave, lane);
   if (nk > 1) {
-    stream_issue<XRC, kSP>(X, d.ldx, p0, kBR, g_sx1, wave, lane);
-    stream_issue<YRC, kSQ>(Y, d.ldy, q0, kBR, g_sy1, wave, lane);
+    stream_issue<XRC, TP>(X, d.ldx, p0, kBR, x1, wave, lane);
+    stream_issue<YRC, TQ>(Y, d.ldy, q0, kBR, y1, wave, lane);
   }
   if (nk > 2) {
-    stream_issue<XRC, kSP>(X, d.ldx, p0, 2 * kBR, g_sx2, wave, lane);
-    stream_issue<YRC, kSQ>(Y, d.ldy, q0, 2 * kBR, g_sy2, wave, lane);
-    __builtin_amdgcn_s_waitcnt(wait_vm(2 * kSDma));  // tile 0 landed, 1 and 2 may fly
+    stream_issue<XRC, TP>(X, d.ldx, p0, 2 * kBR, x2, wave, lane);
+    stream_issue<YRC, TQ>(Y, d.ldy, q0, 2 * kBR, y2, wave, lane);
+    __builtin_amdgcn_s_waitcnt(wait_vm(2 * kDma));  // tile 0 landed, 1 and 2 may fly
   } else if (nk > 1) {
-    __builtin_amdgcn_s_waitcnt(wait_vm(kSDma));
+    __builtin_amdgcn_s_waitcnt(wait_vm(kDma));
   } else {
     __builtin_amdgcn_s_waitcnt(wait_vm(0));
   }
   __syncthreads();
 
-  f16v acc[4][2], tot[4][2];
+  f16v acc[kBI][kBJ], tot[kBI][kBJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kBI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kBJ; ++j) {
       acc[i][j] = f16v{};
       tot[i][j] = f16v{};
     }
-  StreamFrags cur, nxt;
-  stream_read<XRC, YRC>(cur, g_sx0, g_sy0, wp, wq, c, h, 0);
+  StreamFrags<kBI, kBJ> cur, nxt;
+  stream_read<XRC, YRC, TP, TQ>(cur, x0, y0, wp, wq, c, h, 0);
 
   // One reduction tile kt held in (xl, yl); (xn, yn) holds tile kt+1.  Group
   // g's MFMAs run while group g+1's fragments load; before the last group
@@ -512,25 +543,25 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
 #pragma unroll
     for (int g = 0; g < kBR / 8; ++g) {
       if (g < kBR / 8 - 1) {
-        stream_read<XRC, YRC>(nxt, xl, yl, wp, wq, c, h, g + 1);
+        stream_read<XRC, YRC, TP, TQ>(nxt, xl, yl, wp, wq, c, h, g + 1);
       } else if (kNext) {
         if (kTwo)
-          __builtin_amdgcn_s_waitcnt(wait_vm(kSDma));  // tile kt+1 landed, kt+2 may fly
+          __builtin_amdgcn_s_waitcnt(wait_vm(kDma));  // tile kt+1 landed, kt+2 may fly
         else
           __builtin_amdgcn_s_waitcnt(wait_vm(0));
         __syncthreads();
         if (kIssue) {
-          stream_issue<XRC, kSP>(X, d.ldx, p0, (kt + 3) * kBR, xl, wave, lane);
-          stream_issue<YRC, kSQ>(Y, d.ldy, q0, (kt + 3) * kBR, yl, wave, lane);
+          stream_issue<XRC, TP>(X, d.ldx, p0, (kt + 3) * kBR, xl, wave, lane);
+          stream_issue<YRC, TQ>(Y, d.ldy, q0, (kt + 3) * kBR, yl, wave, lane);
         }
-        stream_read<XRC, YRC>(nxt, xn, yn, wp, wq, c, h, 0);
+        stream_read<XRC, YRC, TP, TQ>(nxt, xn, yn, wp, wq, c, h, 0);
       }
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kBI; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < kBJ; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[i][sl], cur.b[j][sl], acc[i][j],
                                                             0, 0, 0);
       cur = nxt;
@@ -538,17 +569,15 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   };
   auto flush = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kBI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kBJ; ++j) {
         tot[i][j] += acc[i][j];
         acc[i][j] = f16v{};
       }
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
-  float *x0 = g_sx0, *x1 = g_sx1, *x2 = g_sx2;
-  float *y0 = g_sy0, *y1 = g_sy1, *y2 = g_sy2;
   int kt = 0;
   for (; kt + 5 < nk; kt += 3) {
     step(T_{}, T_{}, T_{}, kt, x0, y0, x1, y1);
@@ -587,13 +616,13 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   flush();
 
 #pragma unroll
-  for (int bi = 0; bi < 4; ++bi)
+  for (int bi = 0; bi < kBI; ++bi)
 #pragma unroll
-    for (int bj = 0; bj < 2; ++bj) {
-      const int q = q0 + wq * 64 + bj * 32 + c;
+    for (int bj = 0; bj < kBJ; ++bj) {
+      const int q = q0 + wq * (TQ / 2) + bj * 32 + c;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int p = p0 + wp * 128 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const int p = p0 + wp * (TP / 2) + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         float *dst = C + (int64_t)p * ldc + q;
         if (part) {
           *dst = tot[bi][bj][i];
@@ -608,25 +637,49 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
 
 template <bool XRC, bool YRC>
 __global__ void __launch_bounds__(kThreads, 1) gemm_stream_kernel(Gemm d) {
-  stream_tile<XRC, YRC>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
+  stream_tile<XRC, YRC, kSP, kSQ>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
 }
 
+template <bool XRC, bool YRC>
+__global__ void __launch_bounds__(kThreads, 2) gemm_stream_small(Gemm d) {
+  stream_tile<XRC, YRC, kHP, kHQ>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
+}
+
+// Pairs on the streamed path, logical tiles [0, tiles_a) for the first
+// product.  matmul_backward: dA = dC B^T (NT) with dB = A^T dC (TN); the
+// Linear backward: dx = g W (NN) with dW = g^T x (TN).
 __global__ void __launch_bounds__(kThreads, 1) matmul_backward_stream(Gemm da, Gemm db, int tiles_a) {
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   if (tile < tiles_a)
-    stream_tile<true, true>(da, tile, blockIdx.y);
+    stream_tile<true, true, kSP, kSQ>(da, tile, blockIdx.y);
   else
-    stream_tile<false, false>(db, tile - tiles_a, blockIdx.y);
+    stream_tile<false, false, kSP, kSQ>(db, tile - tiles_a, blockIdx.y);
 }
 
-// The Linear backward pair on the streamed path: dx = g W (NN) with
-// dW = g^T x (TN), logical tiles [0, tiles_a) for dx.
+__global__ void __launch_bounds__(kThreads, 2) matmul_backward_stream_small(Gemm da, Gemm db,
+                                                                            int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<true, true, kHP, kHQ>(da, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kHP, kHQ>(db, tile - tiles_a, blockIdx.y);
+}
+
 __global__ void __launch_bounds__(kThreads, 1) linear_backward_stream(Gemm dx, Gemm dw, int tiles_a) {
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   if (tile < tiles_a)
-    stream_tile<true, false>(dx, tile, blockIdx.y);
+    stream_tile<true, false, kSP, kSQ>(dx, tile, blockIdx.y);
   else
-    stream_tile<false, false>(dw, tile - tiles_a, blockIdx.y);
+    stream_tile<false, false, kSP, kSQ>(dw, tile - tiles_a, blockIdx.y);
+}
+
+__global__ void __launch_bounds__(kThreads, 2) linear_backward_stream_small(Gemm dx, Gemm dw,
+                                                                            int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<true, false, kHP, kHQ>(dx, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kHP, kHQ>(dw, tile - tiles_a, blockIdx.y);
 }
 
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
@@ -695,35 +748,46 @@ bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
          ok(d.Y, d.ldy, d.bsy, d.bsy2, yrc ? d.R : d.Q);
 }
 
-// The streamed path takes whole 256 x 128 output tiles and whole reduction
-// tiles of 16-byte aligned operands, and is used when the product has at
-// least one such tile per CU (with fewer, the 128 x 128 path with split-K
-// keeps more CUs busy).
-bool stream_fits(const Gemm &g, bool xrc, bool yrc) {
-  return g.P % kSP == 0 && g.Q % kSQ == 0 && g.R % kBR == 0 && g.R > 0 &&
-         vec_ok(g, xrc, yrc);
+// The streamed path takes whole TP x TQ output tiles and whole reduction
+// tiles of 16-byte aligned operands.
+bool stream_fits(const Gemm &g, bool xrc, bool yrc, int tp, int tq) {
+  return g.P % tp == 0 && g.Q % tq == 0 && g.R % kBR == 0 && g.R > 0 && vec_ok(g, xrc, yrc);
 }
 
-Gemm as_stream(Gemm g) {
-  g.tiles_p = g.P / kSP;
-  g.tiles_q = g.Q / kSQ;
+Gemm as_stream(Gemm g, bool small) {
+  g.tiles_p = g.P / (small ? kHP : kSP);
+  g.tiles_q = g.Q / (small ? kHQ : kSQ);
   g.splits = 1;
   g.ktiles_per_split = g.R / kBR;
   g.partial = nullptr;
   return g;
 }
 
-// Split plan for the streamed path (batch 1), which runs one workgroup per
-// CU.  A workgroup's time is its number of reduction tiles plus about one
-// tile of fixed cost (prologue, epilogue), and a grid of W workgroups runs in
-// ceil(W / CUs) waves; a split product also writes and re-reads its fp32
-// partials (8 bytes per element per split).  Candidate per-workgroup
-// reduction lengths T are ceil(k / s) for s = 1..32 of either product; each
-// product is cut into ceil(k / T) ranges of equal length (at most 32 ranges,
-// none empty) and the plan with the smallest estimate wins, ties going to
-// fewer workgroups.  Product b is absent when tb == 0.
+// Split plan for the streamed path (batch 1).  Model, fitted to MI355X
+// timings of both tile shapes over reduction lengths 1..128 tiles: a grid of
+// W workgroups puts n = ceil(W / CUs) on the busiest CU.  Large tiles run one
+// at a time, each costing T tile steps (T = its reduction tiles) plus a fixed
+// cost (pipeline fill, epilogue, launch); small tiles run two at a time per
+// CU, slower per step than a small tile alone.  A split product also writes
+// and re-reads its fp32 partials (8 bytes per element per split) and launches
+// a reduce.  Candidate per-workgroup reduction lengths T are ceil(k / s) for
+// s = 1..32 of either product; each product is cut into ceil(k / T) ranges of
+// equal length (at most 32 ranges, none empty) and the smallest estimate
+// wins, ties going to fewer workgroups.  Product b is absent when tb == 0.
+constexpr double kLargeTileUs = 4.22, kLargeFixedUs = 18.0;
+constexpr double kSmallPairUs = 2.3, kSmallAloneUs = 1.4, kSmallFixedUs = 7.0;
+constexpr double kPartialBytesPerUs = 6.0e6;
+
+double stream_wave_us(bool small, int64_t n, int64_t T) {
+  if (!small) return (double)n * ((double)T * kLargeTileUs + kLargeFixedUs);
+  return (double)(n / 2) * ((double)T * kSmallPairUs + kSmallFixedUs) +
+         (double)(n % 2) * ((double)T * kSmallAloneUs + kSmallFixedUs);
+}
+
 struct StreamPlan {
+  bool small;
   int sa, sb;
+  double t;
 };
 
 int stream_cut(int64_t k, int64_t T) {
@@ -732,13 +796,10 @@ int stream_cut(int64_t k, int64_t T) {
   return (int)((k + per - 1) / per);
 }
 
-StreamPlan plan_stream(int64_t cus, int64_t ta, int64_t ka, int64_t pqa, int64_t tb, int64_t kb,
-                       int64_t pqb) {
-  constexpr double kTileUs = 4.3;        // one 256 x 128 x 32 step at ~80% of peak
+StreamPlan plan_shape(int64_t cus, int64_t ta, int64_t ka, int64_t pqa, int64_t tb, int64_t kb,
+                      int64_t pqb, bool small) {
   cus = std::max<int64_t>(cus, 1);
-  constexpr double kBytesPerUs = 6.0e6;  // streaming rate of the partial traffic
-  StreamPlan best{1, 1};
-  double best_t = 0.0;
+  StreamPlan best{false, 1, 1, 0.0};
   int64_t best_w = 0;
   bool first = true;
   for (int cand = 0; cand < 64; ++cand) {
@@ -749,37 +810,58 @@ StreamPlan plan_stream(int64_t cus, int64_t ta, int64_t ka, int64_t pqa, int64_t
     const int sa = stream_cut(ka, T), sb = tb ? stream_cut(kb, T) : 1;
     const int64_t la = (ka + sa - 1) / sa, lb = tb ? (kb + sb - 1) / sb : 0;
     const int64_t w = ta * sa + tb * sb;
-    double t = (double)((w + cus - 1) / cus) * (double)(std::max(la, lb) + 1) * kTileUs;
-    if (sa > 1) t += 8.0 * sa * pqa / kBytesPerUs + 2.0;
-    if (sb > 1) t += 8.0 * sb * pqb / kBytesPerUs + 2.0;
-    if (first || t < best_t || (t == best_t && w < best_w)) {
+    double t = stream_wave_us(small, (w + cus - 1) / cus, std::max(la, lb));
+    if (sa > 1) t += 8.0 * sa * pqa / kPartialBytesPerUs + 2.0;
+    if (sb > 1) t += 8.0 * sb * pqb / kPartialBytesPerUs + 2.0;
+    if (first || t < best.t || (t == best.t && w < best_w)) {
       first = false;
-      best = {sa, sb};
-      best_t = t;
+      best = {small, sa, sb, t};
       best_w = w;
     }
   }
   return best;
 }
 
-// Whether a batch-1 product (or pair) goes to the streamed path: enough work
-// for four 256 x 128 x 32 steps per CU.
-bool stream_worth(numrs_hip_ctx *ctx, int64_t work_tiles) {
-  return work_tiles >= 4 * (int64_t)ctx->num_cus;
+// Streamed-path plan for a batch-1 product a, or a pair with the TN product b
+// in the same grid: picks the tile shape and the split-K ranges.  False when
+// neither shape fits both products, or when the work is under four large
+// tile steps per CU (the 128 x 128 path is then as good).
+bool plan_streamed(numrs_hip_ctx *ctx, const Gemm &a, bool xa, bool ya, const Gemm *b,
+                   StreamPlan *pl) {
+  const double flops = 2.0 * a.P * a.Q * a.R + (b ? 2.0 * b->P * b->Q * b->R : 0.0);
+  if (flops < 4.0 * ctx->num_cus * (2.0 * kSP * kSQ * kBR)) return false;
+  bool any = false;
+  for (int small = 0; small < 2; ++small) {
+    const int tp = small ? kHP : kSP, tq = small ? kHQ : kSQ;
+    if (!stream_fits(a, xa, ya, tp, tq) || (b && !stream_fits(*b, false, false, tp, tq))) continue;
+    const int64_t ta = (int64_t)(a.P / tp) * (a.Q / tq), ka = a.R / kBR;
+    const int64_t tb = b ? (int64_t)(b->P / tp) * (b->Q / tq) : 0, kb = b ? b->R / kBR : 0;
+    if ((ta + tb) * 32 > 0x7fffffff) continue;  // grid of at most 32 splits per tile
+    const StreamPlan c = plan_shape(ctx->num_cus, ta, ka, (int64_t)a.P * a.Q, tb, kb,
+                                    b ? (int64_t)b->P * b->Q : 0, small != 0);
+    if (!any || c.t < pl->t) *pl = c;
+    any = true;
+  }
+  return any;
 }
 
-// Points the split products of a streamed plan at the context's workspace.
-int stream_splits(numrs_hip_ctx *ctx, Gemm &ga, int sa, Gemm *gb, int sb) {
-  const size_t na = sa > 1 ? (size_t)sa * ga.P * ga.Q : 0;
-  const size_t nb = gb != nullptr && sb > 1 ? (size_t)sb * gb->P * gb->Q : 0;
+// Stream descriptors for a plan, with split products pointed at the
+// context's workspace.
+int stream_prepare(numrs_hip_ctx *ctx, const StreamPlan &pl, Gemm &ga, Gemm *gb) {
+  ga = as_stream(ga, pl.small);
+  if (gb != nullptr) *gb = as_stream(*gb, pl.small);
+  const size_t na = pl.sa > 1 ? (size_t)pl.sa * ga.P * ga.Q : 0;
+  const size_t nb = gb != nullptr && pl.sb > 1 ? (size_t)pl.sb * gb->P * gb->Q : 0;
   if (na + nb == 0) return NUMRS_HIP_OK;
   void *ws = nullptr;
   if (int rc = numrs_hip::workspace(ctx, (na + nb) * sizeof(float), &ws)) return rc;
   float *base = static_cast<float *>(ws);
-  if (sa > 1) apply_splits(ga, sa, base);
-  if (nb) apply_splits(*gb, sb, base + na);
+  if (na) apply_splits(ga, pl.sa, base);
+  if (nb) apply_splits(*gb, pl.sb, base + na);
   return NUMRS_HIP_OK;
 }
+
+int64_t stream_grid(const Gemm &g) { return (int64_t)g.tiles_p * g.tiles_q * g.splits; }
 
 int check_dims(numrs_hip_ctx *ctx, const char *who, int64_t batch, int64_t M, int64_t K,
                int64_t N) {
@@ -829,17 +911,22 @@ template <bool XRC, bool YRC>
 int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   const int64_t n_tiles = (int64_t)g.tiles_p * g.tiles_q;
   if (n_tiles == 0 || batch == 0) return NUMRS_HIP_OK;
-  if (stream_fits(g, XRC, YRC)) {
-    Gemm sg = as_stream(g);
-    const int64_t st = (int64_t)sg.tiles_p * sg.tiles_q, nk = sg.R / kBR;
-    if (batch == 1 && stream_worth(ctx, st * nk)) {
-      const StreamPlan pl = plan_stream(ctx->num_cus, st, nk, (int64_t)sg.P * sg.Q, 0, 0, 0);
-      if (int rc = stream_splits(ctx, sg, pl.sa, nullptr, 1)) return rc;
-      gemm_stream_kernel<XRC, YRC><<<dim3((unsigned)(st * pl.sa), 1), kThreads, 0, ctx->stream>>>(sg);
-      if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
-      return reduce_splits(ctx, &sg, nullptr);
-    }
-    if (batch > 1 && st * batch >= ctx->num_cus) {
+  StreamPlan pl;
+  if (batch == 1 && plan_streamed(ctx, g, XRC, YRC, nullptr, &pl)) {
+    Gemm sg = g;
+    if (int rc = stream_prepare(ctx, pl, sg, nullptr)) return rc;
+    const dim3 grid((unsigned)stream_grid(sg), 1);
+    if (pl.small)
+      gemm_stream_small<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
+    else
+      gemm_stream_kernel<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
+    if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
+    return reduce_splits(ctx, &sg, nullptr);
+  }
+  if (batch > 1 && stream_fits(g, XRC, YRC, kSP, kSQ)) {
+    const Gemm sg = as_stream(g, false);
+    const int64_t st = (int64_t)sg.tiles_p * sg.tiles_q;
+    if (st * batch >= ctx->num_cus) {
       dim3 grid((unsigned)st, (unsigned)batch);
       gemm_stream_kernel<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
       return numrs_hip::check_launch(ctx, "gemm_stream_kernel");
@@ -895,20 +982,23 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   Gemm gb = make(A, dC, dB, K, N, N, sa, sc, sb, K, N, M, acc);
   if (dA == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
   if (dB == nullptr) return gemm_dispatch(ctx, ga, batch, true, true);
-  if (stream_fits(ga, true, true) && stream_fits(gb, false, false)) {
-    Gemm sa = as_stream(ga), sb = as_stream(gb);
+  StreamPlan pl;
+  if (batch == 1 && plan_streamed(ctx, ga, true, true, &gb, &pl)) {
+    Gemm sa = ga, sb = gb;
+    if (int rc2 = stream_prepare(ctx, pl, sa, &sb)) return rc2;
+    const int64_t na = stream_grid(sa);
+    const dim3 grid((unsigned)(na + stream_grid(sb)), 1);
+    if (pl.small)
+      matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
+    else
+      matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
+    if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
+    return reduce_splits(ctx, &sa, &sb);
+  }
+  if (batch > 1 && stream_fits(ga, true, true, kSP, kSQ) && stream_fits(gb, false, false, kSP, kSQ)) {
+    const Gemm sa = as_stream(ga, false), sb = as_stream(gb, false);
     const int64_t ta = (int64_t)sa.tiles_p * sa.tiles_q, tb = (int64_t)sb.tiles_p * sb.tiles_q;
-    const int64_t ka = sa.R / kBR, kb = sb.R / kBR;
-    if (batch == 1 && stream_worth(ctx, ta * ka + tb * kb)) {
-      const StreamPlan pl = plan_stream(ctx->num_cus, ta, ka, (int64_t)sa.P * sa.Q, tb, kb,
-                                        (int64_t)sb.P * sb.Q);
-      if (int rc2 = stream_splits(ctx, sa, pl.sa, &sb, pl.sb)) return rc2;
-      dim3 grid((unsigned)(ta * pl.sa + tb * pl.sb), 1);
-      matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
-      if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
-      return reduce_splits(ctx, &sa, &sb);
-    }
-    if (batch > 1 && (ta + tb) * batch >= ctx->num_cus) {
+    if ((ta + tb) * batch >= ctx->num_cus) {
       dim3 grid((unsigned)(ta + tb), (unsigned)batch);
       matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
       return numrs_hip::check_launch(ctx, "matmul_backward_stream");
@@ -1000,22 +1090,22 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
   if (!has_a && !has_b) return NUMRS_HIP_OK;
   if (!has_a) return gemm_dispatch(ctx, gb, 1, false, false);
   if (!has_b) return gemm_dispatch(ctx, ga, 1, true, first_nt);
-  if (stream_fits(ga, true, first_nt) && stream_fits(gb, false, false)) {
-    Gemm sa = as_stream(ga), sb = as_stream(gb);
-    const int64_t ta = (int64_t)sa.tiles_p * sa.tiles_q, tb = (int64_t)sb.tiles_p * sb.tiles_q;
-    const int64_t ka = sa.R / kBR, kb = sb.R / kBR;
-    if (stream_worth(ctx, ta * ka + tb * kb)) {
-      const StreamPlan pl = plan_stream(ctx->num_cus, ta, ka, (int64_t)sa.P * sa.Q, tb, kb,
-                                        (int64_t)sb.P * sb.Q);
-      if (int rc = stream_splits(ctx, sa, pl.sa, &sb, pl.sb)) return rc;
-      dim3 grid((unsigned)(ta * pl.sa + tb * pl.sb), 1);
-      if (first_nt)
-        matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
-      else
-        linear_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)(ta * pl.sa));
-      if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
-      return reduce_splits(ctx, &sa, &sb);
-    }
+  StreamPlan pl;
+  if (plan_streamed(ctx, ga, true, first_nt, &gb, &pl)) {
+    Gemm sa = ga, sb = gb;
+    if (int rc = stream_prepare(ctx, pl, sa, &sb)) return rc;
+    const int64_t na = stream_grid(sa);
+    const dim3 grid((unsigned)(na + stream_grid(sb)), 1);
+    if (first_nt && pl.small)
+      matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
+    else if (first_nt)
+      matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
+    else if (pl.small)
+      linear_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
+    else
+      linear_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
+    if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
+    return reduce_splits(ctx, &sa, &sb);
   }
   // Joint split plan, balanced by work: the pair shares one grid, and a
   // workgroup's time is its number of reduction tiles.  The weight gradient
