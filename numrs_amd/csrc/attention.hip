@@ -73,16 +73,11 @@ int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float
     return rc;
   // dS = P * (dP - rowsum(dP * P)), in place over dP
   if (int rc = numrs_hip_softmax_backward(ctx, P, dP, dP, Z * S, S, 0)) return rc;
-  // dQ_z = alpha * dS_z K_z ;  dK_z = alpha * dS_z^T Q_z
-  if (dq)
-    if (int rc = numrs_hip_gemm(ctx, dP, S, k, D, dq, D, S, S, dh, 0, 0, alpha, accumulate, Z, H,
-                                H * S * S, S * S, S * D, dh, S * D, dh))
-      return rc;
-  if (dk)
-    if (int rc = numrs_hip_gemm(ctx, dP, S, q, D, dk, D, S, S, dh, 1, 0, alpha, accumulate, Z, H,
-                                H * S * S, S * S, S * D, dh, S * D, dh))
-      return rc;
-  return NUMRS_HIP_OK;
+  // dQ_z = alpha * dS_z K_z ;  dK_z = alpha * dS_z^T Q_z  (one launch for both)
+  const numrs_hip::BatchedMat dS{dP, S, H * S * S, S * S};
+  const numrs_hip::BatchedMat Km{k, D, S * D, dh}, Qm{q, D, S * D, dh};
+  const numrs_hip::BatchedOut dQ{dq, D, S * D, dh}, dK{dk, D, S * D, dh};
+  return numrs_hip::gemm_nn_tn_pair(ctx, dS, Km, dQ, Qm, dK, S, S, dh, alpha, accumulate, Z, H);
 }
 
 }  // extern "C"

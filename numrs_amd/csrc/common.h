@@ -73,6 +73,25 @@ int vec_op(numrs_hip_ctx *ctx, float *out, const float *a, const float *b, float
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A batched row-major fp32 matrix: element (i, j) of batch z = zo*inner + zi
+// sits at p + zo*so + zi*si + i*ld + j.
+struct BatchedMat {
+  const float *p;
+  int64_t ld, so, si;
+};
+struct BatchedOut {
+  float *p;
+  int64_t ld, so, si;
+};
+
+// C1_z = alpha X_z Y1_z ([M,K] x [K,N]) and C2_z = alpha X_z^T Y2_z
+// ([K,M] x [M,N]) for z < batch, in one launch where the streamed path fits
+// (the shape of the Linear backward and of attention's dQ/dK).  Either
+// output may be null; accumulate adds into the outputs.
+int gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, BatchedOut C1, BatchedMat Y2,
+                    BatchedOut C2, int64_t M, int64_t K, int64_t N, float alpha, int accumulate,
+                    int64_t batch, int64_t binner);
+
 }  // namespace numrs_hip
 
 #define NRS_CHECK_CTX(ctx)                       \

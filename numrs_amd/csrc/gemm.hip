@@ -863,6 +863,30 @@ int stream_prepare(numrs_hip_ctx *ctx, const StreamPlan &pl, Gemm &ga, Gemm *gb)
 
 int64_t stream_grid(const Gemm &g) { return (int64_t)g.tiles_p * g.tiles_q * g.splits; }
 
+// Tile shape for a batched product (or a pair sharing the grid): no split-K,
+// so the shape whose tiles fill the CUs with the smaller modelled time;
+// false when neither shape fits or gives at least one tile per CU.
+bool pick_batched_stream(numrs_hip_ctx *ctx, const Gemm &a, bool xa, bool ya, const Gemm *b,
+                         int64_t batch, bool *small_out) {
+  bool any = false;
+  double best = 0.0;
+  const int64_t cus = std::max(ctx->num_cus, 1);
+  for (int small = 0; small < 2; ++small) {
+    const int tp = small ? kHP : kSP, tq = small ? kHQ : kSQ;
+    if (!stream_fits(a, xa, ya, tp, tq) || (b && !stream_fits(*b, false, false, tp, tq))) continue;
+    const int64_t t = (int64_t)(a.P / tp) * (a.Q / tq) + (b ? (int64_t)(b->P / tp) * (b->Q / tq) : 0);
+    if (t * batch < cus || t > 0x7fffffff) continue;
+    const int64_t T = std::max<int64_t>(a.R, b ? b->R : 0) / kBR;
+    const double est = stream_wave_us(small != 0, (t * batch + cus - 1) / cus, T);
+    if (!any || est < best) {
+      best = est;
+      *small_out = small != 0;
+    }
+    any = true;
+  }
+  return any;
+}
+
 int check_dims(numrs_hip_ctx *ctx, const char *who, int64_t batch, int64_t M, int64_t K,
                int64_t N) {
   if (batch < 0 || M < 0 || K < 0 || N < 0)
@@ -923,14 +947,15 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
     if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
     return reduce_splits(ctx, &sg, nullptr);
   }
-  if (batch > 1 && stream_fits(g, XRC, YRC, kSP, kSQ)) {
-    const Gemm sg = as_stream(g, false);
-    const int64_t st = (int64_t)sg.tiles_p * sg.tiles_q;
-    if (st * batch >= ctx->num_cus) {
-      dim3 grid((unsigned)st, (unsigned)batch);
+  bool small = false;
+  if (batch > 1 && pick_batched_stream(ctx, g, XRC, YRC, nullptr, batch, &small)) {
+    const Gemm sg = as_stream(g, small);
+    dim3 grid((unsigned)stream_grid(sg), (unsigned)batch);
+    if (small)
+      gemm_stream_small<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
+    else
       gemm_stream_kernel<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
-      return numrs_hip::check_launch(ctx, "gemm_stream_kernel");
-    }
+    return numrs_hip::check_launch(ctx, "gemm_stream_kernel");
   }
   const int splits = plan_splits(g, batch);
   if (splits > 1) {
@@ -995,14 +1020,16 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
     if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
     return reduce_splits(ctx, &sa, &sb);
   }
-  if (batch > 1 && stream_fits(ga, true, true, kSP, kSQ) && stream_fits(gb, false, false, kSP, kSQ)) {
-    const Gemm sa = as_stream(ga, false), sb = as_stream(gb, false);
-    const int64_t ta = (int64_t)sa.tiles_p * sa.tiles_q, tb = (int64_t)sb.tiles_p * sb.tiles_q;
-    if ((ta + tb) * batch >= ctx->num_cus) {
-      dim3 grid((unsigned)(ta + tb), (unsigned)batch);
+  bool small = false;
+  if (batch > 1 && pick_batched_stream(ctx, ga, true, true, &gb, batch, &small)) {
+    const Gemm sa = as_stream(ga, small), sb = as_stream(gb, small);
+    const int64_t ta = stream_grid(sa), tb = stream_grid(sb);
+    dim3 grid((unsigned)(ta + tb), (unsigned)batch);
+    if (small)
+      matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    else
       matmul_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
-      return numrs_hip::check_launch(ctx, "matmul_backward_stream");
-    }
+    return numrs_hip::check_launch(ctx, "matmul_backward_stream");
   }
   const int sa_ = plan_splits(ga, batch), sb_ = plan_splits(gb, batch);
   if (sa_ > 1 || sb_ > 1) {
@@ -1155,6 +1182,57 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
 }
 
 }  // namespace
+
+int numrs_hip::gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, BatchedOut C1,
+                               BatchedMat Y2, BatchedOut C2, int64_t M, int64_t K, int64_t N,
+                               float alpha, int accumulate, int64_t batch, int64_t binner) {
+  const char *who = "gemm_nn_tn_pair";
+  if (int rc = check_dims(ctx, who, batch, M, K, N)) return rc;
+  if (binner < 1 || binner > std::max<int64_t>(batch, 1))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: batch_inner %lld", who, (long long)binner);
+  if (batch == 0 || N == 0 || (C1.p == nullptr && C2.p == nullptr)) return NUMRS_HIP_OK;
+  // C1[M,N] = X[M,K] Y1[K,N]: P=M, Q=N, R=K, X reduction-contiguous.
+  Gemm ga = make(X.p, Y1.p, C1.p, X.ld, Y1.ld, C1.ld, X.so, Y1.so, C1.so, M, N, K, accumulate);
+  // C2[K,N] = X^T Y2[M,N]: P=K, Q=N, R=M, X output-contiguous.
+  Gemm gb = make(X.p, Y2.p, C2.p, X.ld, Y2.ld, C2.ld, X.so, Y2.so, C2.so, K, N, M, accumulate);
+  ga.bsx2 = X.si, ga.bsy2 = Y1.si, ga.bsc2 = C1.si;
+  gb.bsx2 = X.si, gb.bsy2 = Y2.si, gb.bsc2 = C2.si;
+  ga.binner = gb.binner = (int)binner;
+  ga.alpha = gb.alpha = alpha;
+  if (M == 0 || K == 0) {
+    // an empty reduction leaves zeros (or the accumulated values)
+    for (int64_t z = 0; z < batch && !accumulate; ++z) {
+      const int64_t zo = z / binner, zi = z - zo * binner;
+      if (C1.p && M > 0)
+        for (int64_t r = 0; r < M; ++r)
+          if (int rc = numrs_hip_fill(ctx, C1.p + zo * C1.so + zi * C1.si + r * C1.ld, N, 0.0f))
+            return rc;
+      if (C2.p && K > 0)
+        for (int64_t r = 0; r < K; ++r)
+          if (int rc = numrs_hip_fill(ctx, C2.p + zo * C2.so + zi * C2.si + r * C2.ld, N, 0.0f))
+            return rc;
+    }
+    return NUMRS_HIP_OK;
+  }
+  if (X.p == nullptr || (C1.p && Y1.p == nullptr) || (C2.p && Y2.p == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
+  if (C1.p == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
+  if (C2.p == nullptr) return gemm_dispatch(ctx, ga, batch, true, false);
+  if (batch == 1) return launch_pair(ctx, ga, gb, false, who);
+  bool small = false;
+  if (pick_batched_stream(ctx, ga, true, false, &gb, batch, &small)) {
+    const Gemm sa = as_stream(ga, small), sb = as_stream(gb, small);
+    const int64_t ta = stream_grid(sa), tb = stream_grid(sb);
+    dim3 grid((unsigned)(ta + tb), (unsigned)batch);
+    if (small)
+      linear_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    else
+      linear_backward_stream<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    return numrs_hip::check_launch(ctx, who);
+  }
+  if (int rc = gemm_dispatch(ctx, ga, batch, true, false)) return rc;
+  return gemm_dispatch(ctx, gb, batch, false, false);
+}
 
 extern "C" {
 

@@ -186,9 +186,11 @@ def test_matmul_forward(hip_ctx, rng, ta, tb, M, K, N):
     assert_contraction(C.numpy(), ref, K)
 
 
-def test_matmul_backward_batched(hip_ctx, rng):
-    bt, M, K, N = 6, 40, 64, 72
-    say("matmul_backward_batched")
+# (32, 256, 128, 256): 256 tiles of 128 x 64 over the batch -- the batched
+# small-tile streamed pair.
+@pytest.mark.parametrize("bt,M,K,N", [(6, 40, 64, 72), (32, 256, 128, 256)])
+def test_matmul_backward_batched(hip_ctx, rng, bt, M, K, N):
+    say(f"matmul_backward_batched bt={bt} M={M} K={K} N={N}")
     A, B, dC = rand(rng, (bt, M, K)), rand(rng, (bt, K, N)), rand(rng, (bt, M, N))
     c = hip_ctx
     dA, dB = c.empty((bt, M, K)), c.empty((bt, K, N))

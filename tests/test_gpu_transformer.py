@@ -23,7 +23,10 @@ def _mha_ref(q, k, v, B, S, H):
     return P, Q, K, V
 
 
-@pytest.mark.parametrize("B,S,H,D", [(2, 40, 4, 64), (1, 7, 1, 5), (3, 256, 8, 512)])
+# (16, 256, 8, 512) is the C4 shape: 128 heads, enough 128 x 64 tiles for the
+# batched streamed products (dQ and dK as one pair launch).
+@pytest.mark.parametrize("B,S,H,D", [(2, 40, 4, 64), (1, 7, 1, 5), (3, 256, 8, 512),
+                                     (16, 256, 8, 512)])
 def test_attention_forward_backward(hip_ctx, B, S, H, D):
     print(f"[gpu] attention B={B} S={S} H={H} D={D}", flush=True)
     rng = np.random.default_rng(B * 1000 + S)
