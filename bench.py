@@ -634,7 +634,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
                                                     o_.ptr, Bq, Sq, Hq, Dq))
     dq_, dk_, dv_ = (ctx.empty((Bq * Sq, Dq)) for _ in range(3))
     dh = Dq // Hq
-    record("N3", "attention backward (new op)", "gemm (batched) + softmax_backward",
+    record("N3", "attention backward (new op)", "attn_rows (dO V^T + softmax bwd) + batched dV, dQ+dK GEMMs",
            "16x256, 8 heads of 64", flops=4 * 2.0 * Bq * Hq * Sq * Sq * dh,
            launch=lambda: ctx._check(L.load().numrs_hip_attention_backward(
                ctx.handle, q_.ptr, k_.ptr, v_.ptr, P_.ptr, do_.ptr, dq_.ptr, dk_.ptr, dv_.ptr,

@@ -24,9 +24,13 @@ def _mha_ref(q, k, v, B, S, H):
 
 
 # (16, 256, 8, 512) is the C4 shape: 128 heads, enough 128 x 64 tiles for the
-# batched streamed products (dQ and dK as one pair launch).
+# batched streamed products (dQ and dK as one pair launch).  Head size 64 with
+# S a multiple of 128 (up to 512) takes the fused row-block kernels (Q K^T +
+# softmax, dO V^T + softmax backward); S = 128, 384, 512 cover their other
+# column-block counts.
 @pytest.mark.parametrize("B,S,H,D", [(2, 40, 4, 64), (1, 7, 1, 5), (3, 256, 8, 512),
-                                     (16, 256, 8, 512)])
+                                     (16, 256, 8, 512), (2, 128, 2, 128), (1, 384, 1, 64),
+                                     (1, 512, 2, 128)])
 def test_attention_forward_backward(hip_ctx, B, S, H, D):
     print(f"[gpu] attention B={B} S={S} H={H} D={D}", flush=True)
     rng = np.random.default_rng(B * 1000 + S)
