@@ -370,7 +370,28 @@ struct StreamCfg {
   static constexpr int kWP = TP / (NW / 2);
   static constexpr int kBI = kWP / 32, kBJ = TQ / 64;  // 32 x 32 MFMA blocks per wave
 };
-typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) float lds_float_t;
+
+// One LDS DMA instruction: each lane copies 16 bytes from src into LDS at
+// lds_bytes + 16 * lane.  Written as inline asm so that the compiler neither
+// sinks the issue towards the next barrier nor adds its own vmcnt waits for
+// it (it cannot tell which LDS stage an LDS DMA writes, so it would wait for
+// every outstanding one before any fragment read).  The caller places the
+// vmcnt waits: vector-memory operations complete in issue order.  The
+// s_nop covers the M0 write -> LDS DMA hazard.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const float *src, uint32_t lds_bytes) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_bytes)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_bytes(const float *p) {
+  return (uint32_t)(uintptr_t)(const lds_float_t *)p;
+}
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
 // are outstanding (expcnt and lgkmcnt left at their no-wait maxima).  The
@@ -381,8 +402,8 @@ static_assert(wait_vm(0) == 0x3f70 && wait_vm(12) == 0x3f7c && wait_vm(24) == 0x
               "vmcnt immediate encoding");
 static_assert(2 * StreamCfg<kSP, kSQ>::kDma < 64, "vmcnt is 6 bits");
 
-// Three LDS stages per tile size: distinct objects, so the compiler's waitcnt
-// model sees that fragment reads never alias the in-flight DMA.
+// Three LDS stages per tile size, as distinct objects so that every stage
+// address folds to a constant (the DMA's M0 value is then a scalar move).
 __shared__ __attribute__((aligned(1024))) float g_sx0[StreamCfg<kSP, kSQ>::kStageX];
 __shared__ __attribute__((aligned(1024))) float g_sy0[StreamCfg<kSP, kSQ>::kStageY];
 __shared__ __attribute__((aligned(1024))) float g_sx1[StreamCfg<kSP, kSQ>::kStageX];
@@ -420,7 +441,7 @@ __device__ __forceinline__ void stream_issue(const float *__restrict__ base, int
       const int lc = (lane % kChunks) ^ (((r >> 2) & 1) << 3);
       src = base + (int64_t)(r0 + r) * ld + p0 + 4 * lc;
     }
-    __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)(lds + m * 256), 16, 0, 0);
+    lds_dma16(src, __builtin_amdgcn_readfirstlane(lds_bytes(lds + m * 256)));
   }
 }
 

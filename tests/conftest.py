@@ -66,6 +66,35 @@ def assert_contraction(got, ref64, K, rms_ab=1.0, ref32=None, what=""):
             f"{what}: mean error {e_gpu:.3e} vs numrs fp32 loop {e_ref:.3e}")
 
 
+def assert_sum(got, ref64, n, ref32=None, what=""):
+    """A result produced by length-n fp32 sums (column sums, bias grads),
+    against the float64 sum.
+
+    Per element: |g - r| <= 1e-5 + 1e-4|r| + 2e-7 n.  A column whose terms
+    cancel to near zero keeps the rounding of its partial sums, which no fp32
+    order avoids (on a 4096 x 2048 N(0,1) matrix numrs's own sequential loop
+    misses the bare bound on 4 columns, by up to 1.4x); 2e-7 n is the
+    allowance the axis-reduction tests use.
+    Aggregate, when numrs's sequential fp32 result `ref32` is given: the mean
+    error must be at most 0.8x that loop's mean error."""
+    assert_close(got, ref64, abs_tol=ABS_TOL + 2e-7 * n, what=what)
+    if ref32 is not None:
+        r = np.asarray(ref64, np.float64)
+        e_gpu = np.abs(np.asarray(got, np.float64) - r).mean()
+        e_ref = np.abs(np.asarray(ref32, np.float64) - r).mean()
+        assert e_gpu <= 0.8 * e_ref + 1e-7, (
+            f"{what}: mean error {e_gpu:.3e} vs numrs sequential fp32 sum {e_ref:.3e}")
+
+
+def seq_colsum32(x):
+    """Column sums of a 2-D fp32 array in numrs's order: one sequential fp32
+    accumulation down each column (add.accumulate is sequential)."""
+    x = np.asarray(x, np.float32)
+    if x.shape[0] == 0:
+        return np.zeros(x.shape[1], np.float32)
+    return np.add.accumulate(x, axis=0, dtype=np.float32)[-1]
+
+
 def assert_bits(got, ref, what=""):
     got = np.ascontiguousarray(got, np.float32)
     ref = np.ascontiguousarray(ref, np.float32)
