@@ -370,28 +370,25 @@ struct StreamCfg {
   static constexpr int kWP = TP / (NW / 2);
   static constexpr int kBI = kWP / 32, kBJ = TQ / 64;  // 32 x 32 MFMA blocks per wave
 };
-typedef __attribute__((address_space(3))) float lds_float_t;
 
-// One LDS DMA instruction: each lane copies 16 bytes from src into LDS at
-// lds_bytes + 16 * lane.  Written as inline asm so that the compiler neither
-// sinks the issue towards the next barrier nor adds its own vmcnt waits for
-// it (it cannot tell which LDS stage an LDS DMA writes, so it would wait for
-// every outstanding one before any fragment read).  The caller places the
-// vmcnt waits: vector-memory operations complete in issue order.  The
-// s_nop covers the M0 write -> LDS DMA hazard.
+// One LDS DMA instruction: each lane copies 16 bytes from base + off (off in
+// bytes, per lane; base uniform) into LDS at lds + 16 * lane.  Written as
+// inline asm so that the compiler neither sinks the issue towards the next
+// barrier nor adds its own vmcnt waits for it (it cannot tell which LDS stage
+// an LDS DMA writes, so it would wait for every outstanding one before any
+// fragment read).  The caller places the vmcnt waits: vector-memory
+// operations complete in issue order.  The s_nop covers the M0 write -> LDS
+// DMA hazard.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const float *src, uint32_t lds_bytes) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ __forceinline__ void lds_dma16(const float *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(src), "s"(lds_bytes)
+               : "v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
-__device__ __forceinline__ uint32_t lds_bytes(const float *p) {
-  return (uint32_t)(uintptr_t)(const lds_float_t *)p;
-}
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
 // are outstanding (expcnt and lgkmcnt left at their no-wait maxima).  The
@@ -420,29 +417,47 @@ __shared__ __attribute__((aligned(1024))) float g_hy2[StreamCfg<kHP, kHQ>::kStag
 __device__ __forceinline__ int rc_swizzle(int p) { return (p & 7) ^ ((p >> 3) & 1); }
 
 // This wave's share of the EXT/8 DMA instructions for one EXT x 32 operand
-// tile (each instruction: 64 lanes x 16 bytes = 1 KiB of LDS starting at
-// lds + m*256), NW waves per workgroup.
-template <bool RC, int EXT, int NW = 4>
-__device__ __forceinline__ void stream_issue(const float *__restrict__ base, int64_t ld, int p0,
-                                             int r0, float *lds, int wave, int lane) {
-  constexpr int kPerWave = EXT / (8 * NW);
+// tile (each instruction: 64 lanes x 16 bytes = 1 KiB of LDS at stage byte
+// address lds + 1024 m), NW waves per workgroup.  The per-lane source
+// offsets do not change along the reduction: stream_offsets computes them
+// once, in bytes from the tile's uniform base (row p0 for an R-contiguous
+// operand, column p0 otherwise, at reduction tile 0), and stream_issue adds
+// the reduction tile to the base.
+template <int EXT, int NW>
+struct StreamSlots {
+  static constexpr int kPerWave = EXT / (8 * NW);
   static_assert(kPerWave >= 1 && kPerWave * 8 * NW == EXT, "DMA split across waves");
+  uint32_t off[kPerWave];
+};
+
+template <bool RC, int EXT, int NW>
+__device__ __forceinline__ void stream_offsets(StreamSlots<EXT, NW> &sl, int64_t ld, int wave,
+                                               int lane) {
 #pragma unroll
-  for (int i = 0; i < kPerWave; ++i) {
-    const int m = wave * kPerWave + i;
-    const float *src;
+  for (int i = 0; i < StreamSlots<EXT, NW>::kPerWave; ++i) {
+    const int m = wave * StreamSlots<EXT, NW>::kPerWave + i;
     if (RC) {  // 8 rows of 32 floats per instruction
       const int p = 8 * m + (lane >> 3);
       const int k = (lane & 7) ^ rc_swizzle(p);
-      src = base + (int64_t)(p0 + p) * ld + r0 + 4 * k;
+      sl.off[i] = (uint32_t)(4 * ((int64_t)p * ld + 4 * k));
     } else {  // 1024 / (4 EXT) rows of EXT floats per instruction
       constexpr int kChunks = EXT / 4;
       const int r = m * (64 / kChunks) + lane / kChunks;
       const int lc = (lane % kChunks) ^ (((r >> 2) & 1) << 3);
-      src = base + (int64_t)(r0 + r) * ld + p0 + 4 * lc;
+      sl.off[i] = (uint32_t)(4 * ((int64_t)r * ld + 4 * lc));
     }
-    lds_dma16(src, __builtin_amdgcn_readfirstlane(lds_bytes(lds + m * 256)));
   }
+}
+
+// base: the operand's uniform tile base advanced to the reduction tile;
+// lds: the stage's byte address; wave_u: the wave index as a uniform value.
+template <int EXT, int NW>
+__device__ __forceinline__ void stream_issue(const StreamSlots<EXT, NW> &sl, const float *base,
+                                             uint32_t lds, uint32_t wave_u) {
+  constexpr int kPerWave = StreamSlots<EXT, NW>::kPerWave;
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i)
+    lds_dma16(base, sl.off[i], lds + 1024u * (wave_u * kPerWave + i));
 }
 
 // Fragment of MFMA group g (reduction indices 8g + 4h + j) for rows
@@ -526,16 +541,30 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
     y0 = g_hy0, y1 = g_hy1, y2 = g_hy2;
   }
 
+  // DMA sources: uniform tile bases (advanced by xstep / ystep floats per
+  // reduction tile) plus per-lane byte offsets fixed for the whole reduction.
+  const float *Xb = X + (XRC ? (int64_t)p0 * d.ldx : (int64_t)p0);
+  const float *Yb = Y + (YRC ? (int64_t)q0 * d.ldy : (int64_t)q0);
+  const int64_t xstep = XRC ? kBR : (int64_t)kBR * d.ldx;
+  const int64_t ystep = YRC ? kBR : (int64_t)kBR * d.ldy;
+  StreamSlots<TP, NW> xs;
+  StreamSlots<TQ, NW> ys;
+  stream_offsets<XRC>(xs, d.ldx, wave, lane);
+  stream_offsets<YRC>(ys, d.ldy, wave, lane);
+  const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // Stage byte addresses in LDS: the low 32 bits of a generic pointer into
+  // the shared aperture are its LDS offset.
+  auto lds_addr = [](const float *p) { return (uint32_t)(uintptr_t)p; };
+  auto issue = [&](int t, const float *xl, const float *yl) {
+    stream_issue<TP, NW>(xs, Xb + t * xstep, lds_addr(xl), wave_u);
+    stream_issue<TQ, NW>(ys, Yb + t * ystep, lds_addr(yl), wave_u);
+  };
+
   // Prologue: tiles 0, 1, 2 into stages 0, 1, 2; wait for tile 0.
-  stream_issue<XRC, TP, NW>(X, d.ldx, p0, 0, x0, wave, lane);
-  stream_issue<YRC, TQ, NW>(Y, d.ldy, q0, 0, y0, wave, lane);
-  if (nk > 1) {
-    stream_issue<XRC, TP, NW>(X, d.ldx, p0, kBR, x1, wave, lane);
-    stream_issue<YRC, TQ, NW>(Y, d.ldy, q0, kBR, y1, wave, lane);
-  }
+  issue(0, x0, y0);
+  if (nk > 1) issue(1, x1, y1);
   if (nk > 2) {
-    stream_issue<XRC, TP, NW>(X, d.ldx, p0, 2 * kBR, x2, wave, lane);
-    stream_issue<YRC, TQ, NW>(Y, d.ldy, q0, 2 * kBR, y2, wave, lane);
+    issue(2, x2, y2);
     __builtin_amdgcn_s_waitcnt(wait_vm(2 * kDma));  // tile 0 landed, 1 and 2 may fly
   } else if (nk > 1) {
     __builtin_amdgcn_s_waitcnt(wait_vm(kDma));
@@ -571,6 +600,7 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
     for (int g = 0; g < kBR / 8; ++g) {
       if (g < kBR / 8 - 1) {
         stream_read<XRC, YRC, TP, TQ, NW>(nxt, xl, yl, wp, wq, c, h, g + 1);
+        __builtin_amdgcn_sched_barrier(0);
       } else if (kNext) {
         if (kTwo)
           __builtin_amdgcn_s_waitcnt(wait_vm(kDma));  // tile kt+1 landed, kt+2 may fly
@@ -578,8 +608,7 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
           __builtin_amdgcn_s_waitcnt(wait_vm(0));
         __syncthreads();
         if (kIssue) {
-          stream_issue<XRC, TP, NW>(X, d.ldx, p0, (kt + 3) * kBR, xl, wave, lane);
-          stream_issue<YRC, TQ, NW>(Y, d.ldy, q0, (kt + 3) * kBR, yl, wave, lane);
+          issue(kt + 3, xl, yl);
         }
         stream_read<XRC, YRC, TP, TQ, NW>(nxt, xn, yn, wp, wq, c, h, 0);
       }
@@ -783,8 +812,12 @@ bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
 
 // The streamed path takes whole TP x TQ output tiles and whole reduction
 // tiles of 16-byte aligned operands.
+// The DMA's per-lane source offsets are 32-bit byte offsets of at most
+// 256 rows from the tile base, so leading dimensions stay below 2^22 floats.
 bool stream_fits(const Gemm &g, bool xrc, bool yrc, int tp, int tq) {
-  return g.P % tp == 0 && g.Q % tq == 0 && g.R % kBR == 0 && g.R > 0 && vec_ok(g, xrc, yrc);
+  constexpr int64_t kMaxLd = int64_t(1) << 22;
+  return g.P % tp == 0 && g.Q % tq == 0 && g.R % kBR == 0 && g.R > 0 && vec_ok(g, xrc, yrc) &&
+         g.ldx < kMaxLd && g.ldy < kMaxLd;
 }
 
 Gemm as_stream(Gemm g, bool small) {
