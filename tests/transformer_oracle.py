@@ -62,23 +62,39 @@ def _merge(a, B, S):
     return a.transpose(0, 2, 1, 3).reshape(B * S, -1)
 
 
+def attention_forward(q, k, v, B, S, H):
+    """softmax(Q K^T / sqrt(dh)) V per head; q, k, v [B*S, H*dh] float64.
+    Returns the merged output [B*S, H*dh] and what the backward needs."""
+    dh = q.shape[1] // H
+    Q, K, V = _heads(q, B, S, H), _heads(k, B, S, H), _heads(v, B, S, H)
+    s = Q @ K.transpose(0, 1, 3, 2) / math.sqrt(dh)
+    s = s - s.max(-1, keepdims=True)
+    P = np.exp(s)
+    P /= P.sum(-1, keepdims=True)
+    return _merge(P @ V, B, S), (Q, K, V, P, dh)
+
+
+def attention_backward(dA, cache, B, S, H):
+    """Grads of q, k, v [B*S, H*dh] from the merged output grad dA."""
+    Q, K, V, P, dh = cache
+    dA = _heads(dA, B, S, H)
+    dV = P.transpose(0, 1, 3, 2) @ dA
+    dP = dA @ V.transpose(0, 1, 3, 2)
+    dS = P * (dP - (dP * P).sum(-1, keepdims=True)) / math.sqrt(dh)
+    dQ, dK = dS @ K, dS.transpose(0, 1, 3, 2) @ Q
+    return _merge(dQ, B, S), _merge(dK, B, S), _merge(dV, B, S)
+
+
 def block(w, x, t, dims):
     """Returns (loss, grads dict, output y) in float64."""
     B, S, H = dims
     f = {k: v.astype(np.float64) for k, v in w.items()}
     x = x.astype(np.float64)
     t = t.astype(np.float64)
-    D = x.shape[1]
-    dh = D // H
     xh1, rs1 = _ln(x)
     ln1 = xh1  # gamma 1, beta 0
     q, k, v = ln1 @ f["wq"].T, ln1 @ f["wk"].T, ln1 @ f["wv"].T
-    Q, K, V = _heads(q, B, S, H), _heads(k, B, S, H), _heads(v, B, S, H)
-    s = Q @ K.transpose(0, 1, 3, 2) / math.sqrt(dh)
-    s = s - s.max(-1, keepdims=True)
-    P = np.exp(s)
-    P /= P.sum(-1, keepdims=True)
-    A = _merge(P @ V, B, S)
+    A, att = attention_forward(q, k, v, B, S, H)
     o = A @ f["wo"].T
     r = x + o
     xh2, rs2 = _ln(r)
@@ -99,12 +115,7 @@ def block(w, x, t, dims):
     g["ln2_beta"] = dln2.sum(0)
     dr = dy + _ln_bwd(dln2, xh2, rs2, 1.0)
     g["wo"] = dr.T @ A
-    dA = _heads(dr @ f["wo"], B, S, H)
-    dV = P.transpose(0, 1, 3, 2) @ dA
-    dP = dA @ V.transpose(0, 1, 3, 2)
-    dS = P * (dP - (dP * P).sum(-1, keepdims=True)) / math.sqrt(dh)
-    dQ, dK = dS @ K, dS.transpose(0, 1, 3, 2) @ Q
-    dq, dk, dv = _merge(dQ, B, S), _merge(dK, B, S), _merge(dV, B, S)
+    dq, dk, dv = attention_backward(dr @ f["wo"], att, B, S, H)
     g["wq"], g["wk"], g["wv"] = dq.T @ ln1, dk.T @ ln1, dv.T @ ln1
     dln1 = dq @ f["wq"] + dk @ f["wk"] + dv @ f["wv"]
     g["ln1_gamma"] = (dln1 * xh1).sum(0)
