@@ -22,6 +22,15 @@ __device__ __forceinline__ int64_t vcol(int lane, int i) {
   return 4 * (int64_t)(lane + 64 * i);
 }
 
+// The float4 at column c of row r, for every lane: a column past the row end
+// reloads the row's last float4 instead (cols % 4 == 0 and cols >= 4 on the
+// register-resident path), so the load needs no branch.  Callers ignore the
+// values of such columns.  A load under `if (c < cols)` would make each
+// column group its own memory round trip.
+__device__ __forceinline__ f4 load_cols(const float *r, int64_t c, int64_t cols) {
+  return *reinterpret_cast<const f4 *>(r + (c < cols ? c : cols - 4));
+}
+
 // cross_entropy_backward, backward.rs:265-301:
 //   m = max_j x_j (f32::max fold, NaN ignored)      backward.rs:285
 //   s = sum_j exp(x_j - m)                           backward.rs:286
@@ -62,13 +71,16 @@ __global__ void __launch_bounds__(kBlock)
   if (row >= B) return;
   const float *xr = x + row * C;
   f4 xv[NV], tv[NV];
-  float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t c = vcol<NV>(lane, i);
-    if (c < C) {
-      xv[i] = *reinterpret_cast<const f4 *>(xr + c);
-      if (!LABELS) tv[i] = *reinterpret_cast<const f4 *>(onehot + row * C + c);
+    xv[i] = load_cols(xr, c, C);
+    if (!LABELS) tv[i] = load_cols(onehot + row * C, c, C);
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (vcol<NV>(lane, i) < C) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) m = fmaxf(m, xv[i][e]);  // backward.rs:285
     }
@@ -134,13 +146,16 @@ __global__ void __launch_bounds__(kBlock)
   if (row >= rows) return;
   const float *yr = y + row * cols, *gr = g + row * cols;
   f4 yv[NV], gv[NV];
-  float d = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t c = vcol<NV>(lane, i);
-    if (c < cols) {
-      yv[i] = *reinterpret_cast<const f4 *>(yr + c);
-      gv[i] = *reinterpret_cast<const f4 *>(gr + c);
+    yv[i] = load_cols(yr, c, cols);
+    gv[i] = load_cols(gr, c, cols);
+  }
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (vcol<NV>(lane, i) < cols) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) d += gv[i][e] * yv[i][e];
     }
@@ -238,25 +253,13 @@ __global__ void __launch_bounds__(kBlock)
   if (lane == 0) idx[row] = (int32_t)(bi < 0 ? start : bi);
 }
 
-// A lane visits its elements in increasing column order, so within a lane
-// the tie rule reduces to one comparison: first max keeps the earlier
-// element (replace on strict '>'), last max takes the later one ('>=').
-// Columns fit in int32 (the host checks), so indices are 32-bit.
+// Argmax of a register-resident row (lane l holds the float4 groups
+// vcol<NV>(l, i)).  A lane visits its elements in increasing column order,
+// so within a lane the tie rule reduces to one comparison: first max keeps
+// the earlier element (replace on strict '>'), last max takes the later one
+// ('>=').  Columns fit in int32 (the host checks), so indices are 32-bit.
 template <int NV, bool TIE_LAST>
-__global__ void __launch_bounds__(kBlock)
-    argmax_vec(const float *__restrict__ x, int32_t *__restrict__ idx, int64_t rows,
-               int64_t cols) {
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const float *xr = x + row * cols;
-  const int ncols = (int)cols;
-  f4 xv[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (int)vcol<NV>(lane, i);
-    if (c < ncols) xv[i] = *reinterpret_cast<const f4 *>(xr + c);
-  }
+__device__ __forceinline__ int argmax_regs(const f4 (&xv)[NV], int ncols, int lane) {
   int start = 0;
   if (TIE_LAST) {
     // Last NaN position: the scan restarts after it.
@@ -272,14 +275,12 @@ __global__ void __launch_bounds__(kBlock)
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) last_nan = max(last_nan, __shfl_xor(last_nan, off, 64));
-    if (last_nan == ncols - 1) {
-      if (lane == 0) idx[row] = last_nan;
-      return;
-    }
+    if (last_nan == ncols - 1) return last_nan;
     start = last_nan + 1;
-  } else if (xr[0] != xr[0]) {
-    if (lane == 0) idx[row] = 0;
-    return;
+  } else {
+    // x[0] is lane 0's first element; a NaN there stays the maximum.
+    const float x0 = __shfl(xv[0][0], 0, 64);
+    if (x0 != x0) return 0;
   }
   // Lane scan.  No NaN lies at or after `start` with TIE_LAST; without it a
   // NaN never replaces.
@@ -314,7 +315,30 @@ __global__ void __launch_bounds__(kBlock)
       bi = oi;
     }
   }
-  if (lane == 0) idx[row] = bi < 0 ? start : bi;
+  return bi < 0 ? start : bi;
+}
+
+template <int NV>
+__device__ __forceinline__ void load_row_regs(f4 (&xv)[NV], const float *xr, int ncols, int lane) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) xv[i] = load_cols(xr, vcol<NV>(lane, i), ncols);
+}
+
+// One wave per row.  (Measured on MI355X at [16384, 1024]: persistent
+// waves that load the next row before reducing the current one ran 10-20%
+// slower than this one-shot form.)
+template <int NV, bool TIE_LAST>
+__global__ void __launch_bounds__(kBlock)
+    argmax_vec(const float *__restrict__ x, int32_t *__restrict__ idx, int64_t rows,
+               int64_t cols) {
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // row is uniform over the wave
+  const int ncols = (int)cols;
+  f4 xv[NV];
+  load_row_regs<NV>(xv, x + row * cols, ncols, lane);
+  const int r = argmax_regs<NV, TIE_LAST>(xv, ncols, lane);
+  if (lane == 0) idx[row] = r;
 }
 
 // Softmax along an inner axis of x[outer, n, inner] (no reference kernel:
