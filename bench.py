@@ -221,7 +221,7 @@ def bench_c1(ctx, steps, warmup):
     step (a loss read-back is what a training loop does)."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
-    from tests.mlp_oracle import make_c1
+    from tests.workloads import make_c1
 
     nr.set_default_context(ctx)
     p = make_c1(seed=1)
@@ -263,7 +263,7 @@ def bench_c4(ctx, steps, warmup):
     SGD step through the device autograd engine."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
-    from tests.transformer_oracle import make_c4
+    from tests.workloads import make_c4
 
     nr.set_default_context(ctx)
     w, x, t, (B, S, H) = make_c4(seed=4)
@@ -303,7 +303,7 @@ def bench_c5(ctx, steps, warmup):
     SGD step through the device autograd engine."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
-    from tests.lstm_oracle import make_c5
+    from tests.workloads import make_c5
 
     nr.set_default_context(ctx)
     layers, hw, hb, x, target = make_c5(seed=5)

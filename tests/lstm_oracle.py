@@ -8,32 +8,7 @@ import math
 
 import numpy as np
 
-
-def _xavier(rng, fan_out, fan_in):
-    a = math.sqrt(6.0 / (fan_in + fan_out))
-    return rng.uniform(-a, a, (fan_out, fan_in)).astype(np.float32)
-
-
-def make_c5(seed=5, B=64, T=128, I=64, H=256, n_layers=2):
-    """BASELINE config 5 inputs: each feature is a sum of 3 sinusoids with
-    random phases plus N(0, 0.1) noise; Xavier-uniform weights, zero biases;
-    target ~ N(0, 1) per series (the head predicts one value per series)."""
-    rng = np.random.default_rng(seed)
-    t = np.arange(T, dtype=np.float64)
-    omega = rng.uniform(0.05, 0.5, 3)
-    phase = rng.uniform(0.0, 2 * math.pi, (B, I, 3))
-    x = np.sin(omega[None, None, None, :] * t[None, :, None, None] + phase[:, None, :, :]).sum(-1)
-    x = (x + rng.normal(0.0, 0.1, x.shape)).astype(np.float32)  # [B, T, I]
-    layers = []
-    fin = I
-    for _ in range(n_layers):
-        layers.append({"w_ih": _xavier(rng, 4 * H, fin), "w_hh": _xavier(rng, 4 * H, H),
-                       "b": np.zeros(4 * H, np.float32)})
-        fin = H
-    head_w = _xavier(rng, 1, H)
-    head_b = np.zeros(1, np.float32)
-    target = rng.standard_normal((B, 1)).astype(np.float32)
-    return layers, head_w, head_b, x, target
+from tests.workloads import make_c5  # noqa: F401  (re-exported for the tests)
 
 
 def _sig(z):

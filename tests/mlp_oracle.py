@@ -17,23 +17,7 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import oracle as O
-
-
-def xavier(rng, fan_out, fan_in):
-    a = np.sqrt(6.0 / (fan_in + fan_out))
-    return rng.uniform(-a, a, (fan_out, fan_in)).astype(np.float32)
-
-
-def make_c1(seed: int = 1, batch: int = 64, fin: int = 784, hidden: int = 128, classes: int = 10):
-    """BASELINE config 1 inputs: x ~ N(0,1), Xavier-uniform weights, zero
-    biases, uniform int labels in [0, classes)."""
-    rng = np.random.default_rng(seed)
-    return {
-        "x": rng.standard_normal((batch, fin), dtype=np.float32),
-        "W1": xavier(rng, hidden, fin), "b1": np.zeros(hidden, np.float32),
-        "W2": xavier(rng, classes, hidden), "b2": np.zeros(classes, np.float32),
-        "labels": rng.integers(0, classes, batch).astype(np.int32),
-    }
+from tests.workloads import make_c1, xavier  # noqa: F401  (re-exported for the tests)
 
 
 def _bias_grad(g, n, mode):

@@ -11,21 +11,7 @@ import math
 
 import numpy as np
 
-
-def make_c4(seed=4, B=16, S=256, D=512, H=8, F=2048):
-    """BASELINE config 4 inputs: x, target ~ N(0,1), Xavier-uniform weights,
-    LN gamma = 1, beta = 0, zero biases."""
-    rng = np.random.default_rng(seed)
-
-    def xav(o, i):
-        a = math.sqrt(6.0 / (i + o))
-        return rng.uniform(-a, a, (o, i)).astype(np.float32)
-
-    w = {"wq": xav(D, D), "wk": xav(D, D), "wv": xav(D, D), "wo": xav(D, D),
-         "w1": xav(F, D), "w2": xav(D, F)}
-    x = rng.standard_normal((B * S, D), dtype=np.float32)
-    t = rng.standard_normal((B * S, D), dtype=np.float32)
-    return w, x, t, (B, S, H)
+from tests.workloads import make_c4  # noqa: F401  (re-exported for the tests)
 
 
 def _ln(x, eps=1e-5):
