@@ -749,16 +749,28 @@ int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
 // Split-K plan for one product: a grid under 256 workgroups leaves most of
 // the 256 CUs idle (a [512,512] weight gradient over 4096 tokens is 16
 // tiles), so the reduction is split until the product has ~256 workgroups,
-// keeping at least 8 k-tiles (256 reduction steps) per split.  Batched
-// products already fill the grid through their batch dimension.
+// keeping at least 8 k-tiles (256 reduction steps) per split.  Products of
+// at most four output tiles (C1's layers: [64,784] x [784,128] is one tile
+// over 25 k-tiles) split down to single k-tiles: their partials are small,
+// and a lone workgroup walks its k-tiles one after another at about 3 us
+// each on MI355X, against one splitk_reduce launch of about 4 us.  Batched
+// products already fill the grid through their batch dimension.  The split
+// count is recomputed from the k-tiles per split, so no range is empty.
 int plan_splits(const Gemm &g, int64_t batch) {
   const int64_t t = (int64_t)g.tiles_p * g.tiles_q;
   const int nk = (g.R + kBR - 1) / kBR;
-  if (batch != 1 || t >= 256 || nk < 16) return 1;
+  if (batch != 1 || t >= 256) return 1;
   int64_t s = (256 + t - 1) / t;
-  s = std::min<int64_t>(s, nk / 8);
+  if (t <= 4 && nk >= 3) {
+    s = std::min<int64_t>(s, nk);
+  } else {
+    if (nk < 16) return 1;
+    s = std::min<int64_t>(s, nk / 8);
+  }
   s = std::min<int64_t>(s, 32);
-  return (int)std::max<int64_t>(s, 1);
+  if (s <= 1) return 1;
+  const int64_t per = (nk + s - 1) / s;
+  return (int)((nk + per - 1) / per);
 }
 
 void apply_splits(Gemm &g, int splits, float *partial) {
