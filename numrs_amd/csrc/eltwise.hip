@@ -18,6 +18,8 @@ constexpr int kVecPerThread = 2;
 constexpr int kElemsPerBlock = kBlock * 4 * kVecPerThread;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+using numrs_hip::ldv;
+using numrs_hip::stv;
 
 // ---------------------------------------------------------------------------
 // Unary backward: dx = g * f'(v)
@@ -80,7 +82,7 @@ __device__ __forceinline__ float unary_grad(float g, float v, float p) {
 
 // One thread's 8 elements (two float4 groups kBlock*4 apart); threads whose
 // groups both lie inside the array issue every load before any store.
-template <int KIND, bool VEC, bool ACC>
+template <int KIND, int VEC, bool ACC>
 __device__ __forceinline__ void unary_bwd_body(const float *__restrict__ g,
                                                const float *__restrict__ v,
                                                float *__restrict__ dx, int64_t n, float p) {
@@ -91,9 +93,9 @@ __device__ __forceinline__ void unary_bwd_body(const float *__restrict__ g,
 #pragma unroll
     for (int u = 0; u < kVecPerThread; ++u) {
       const int64_t i = base + (int64_t)u * kBlock * 4;
-      gv[u] = *reinterpret_cast<const f4 *>(g + i);
-      vv[u] = *reinterpret_cast<const f4 *>(v + i);
-      if (ACC) ov[u] = *reinterpret_cast<const f4 *>(dx + i);
+      gv[u] = ldv<VEC>(g + i);
+      vv[u] = ldv<VEC>(v + i);
+      if (ACC) ov[u] = ldv<VEC>(dx + i);
     }
 #pragma unroll
     for (int u = 0; u < kVecPerThread; ++u) {
@@ -101,7 +103,7 @@ __device__ __forceinline__ void unary_bwd_body(const float *__restrict__ g,
       f4 r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) r[e] = unary_grad<KIND>(gv[u][e], vv[u][e], p);
-      *reinterpret_cast<f4 *>(dx + i) = ACC ? ov[u] + r : r;
+      stv<VEC>(dx + i, ACC ? ov[u] + r : r);
     }
     return;
   }
@@ -118,7 +120,7 @@ __device__ __forceinline__ void unary_bwd_body(const float *__restrict__ g,
   }
 }
 
-template <int KIND, bool VEC>
+template <int KIND, int VEC>
 __global__ void __launch_bounds__(kBlock)
     unary_bwd_kernel(const float *__restrict__ g, const float *__restrict__ v,
                      float *__restrict__ dx, int64_t n, float p, int acc) {
@@ -131,10 +133,10 @@ int launch_unary(numrs_hip_ctx *ctx, const float *g, const float *v, float *dx, 
                  float p, int acc) {
   const unsigned grid = grid_for(n, kElemsPerBlock);
   const bool vec = numrs_hip::aligned16(g) && numrs_hip::aligned16(v) && numrs_hip::aligned16(dx);
-  if (vec)
-    unary_bwd_kernel<KIND, true><<<grid, kBlock, 0, ctx->stream>>>(g, v, dx, n, p, acc);
-  else
-    unary_bwd_kernel<KIND, false><<<grid, kBlock, 0, ctx->stream>>>(g, v, dx, n, p, acc);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
+    unary_bwd_kernel<KIND, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(g, v, dx, n, p,
+                                                                                acc);
+  });
   return numrs_hip::check_launch(ctx, "unary_bwd_kernel");
 }
 
@@ -168,7 +170,7 @@ __device__ __forceinline__ void binary_grad(float g, float x, float y, float &dx
 // outputs present (DX, DY) and the accumulate flag (ACC) fixed at compile
 // time.  Threads whose groups both lie inside the array issue every load
 // before any store; the last block's ragged end goes element by element.
-template <int KIND, bool VEC, bool DX, bool DY, bool ACC>
+template <int KIND, int VEC, bool DX, bool DY, bool ACC>
 __device__ __forceinline__ void binary_bwd_body(const float *__restrict__ g,
                                                 const float *__restrict__ x,
                                                 const float *__restrict__ y,
@@ -183,15 +185,15 @@ __device__ __forceinline__ void binary_bwd_body(const float *__restrict__ g,
 #pragma unroll
     for (int u = 0; u < kVecPerThread; ++u) {
       const int64_t i = base + (int64_t)u * kBlock * 4;
-      gv[u] = *reinterpret_cast<const f4 *>(g + i);
+      gv[u] = ldv<VEC>(g + i);
       if (kReadsXY) {
-        xv[u] = *reinterpret_cast<const f4 *>(x + i);
-        yv[u] = *reinterpret_cast<const f4 *>(y + i);
+        xv[u] = ldv<VEC>(x + i);
+        yv[u] = ldv<VEC>(y + i);
       } else {
         xv[u] = yv[u] = f4{0.f, 0.f, 0.f, 0.f};
       }
-      if (ACC && DX) ov[u] = *reinterpret_cast<const f4 *>(dx + i);
-      if (ACC && DY) pv[u] = *reinterpret_cast<const f4 *>(dy + i);
+      if (ACC && DX) ov[u] = ldv<VEC>(dx + i);
+      if (ACC && DY) pv[u] = ldv<VEC>(dy + i);
     }
 #pragma unroll
     for (int u = 0; u < kVecPerThread; ++u) {
@@ -204,8 +206,8 @@ __device__ __forceinline__ void binary_bwd_body(const float *__restrict__ g,
         a[e] = ae;
         b[e] = be;
       }
-      if (DX) *reinterpret_cast<f4 *>(dx + i) = ACC ? ov[u] + a : a;
-      if (DY) *reinterpret_cast<f4 *>(dy + i) = ACC ? pv[u] + b : b;
+      if (DX) stv<VEC>(dx + i, ACC ? ov[u] + a : a);
+      if (DY) stv<VEC>(dy + i, ACC ? pv[u] + b : b);
     }
     return;
   }
@@ -227,7 +229,7 @@ __device__ __forceinline__ void binary_bwd_body(const float *__restrict__ g,
   }
 }
 
-template <int KIND, bool VEC>
+template <int KIND, int VEC>
 __global__ void __launch_bounds__(kBlock)
     binary_bwd_kernel(const float *__restrict__ g, const float *__restrict__ x,
                       const float *__restrict__ y, float *__restrict__ dx, float *__restrict__ dy,
@@ -253,10 +255,10 @@ int launch_binary(numrs_hip_ctx *ctx, const float *g, const float *x, const floa
                    numrs_hip::aligned16(dy) &&
                    (!reads_xy || (numrs_hip::aligned16(x) && numrs_hip::aligned16(y)));
   const unsigned grid = grid_for(n, kElemsPerBlock);
-  if (vec)
-    binary_bwd_kernel<KIND, true><<<grid, kBlock, 0, ctx->stream>>>(g, x, y, dx, dy, n, acc);
-  else
-    binary_bwd_kernel<KIND, false><<<grid, kBlock, 0, ctx->stream>>>(g, x, y, dx, dy, n, acc);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
+    binary_bwd_kernel<KIND, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(g, x, y, dx, dy,
+                                                                                 n, acc);
+  });
   return numrs_hip::check_launch(ctx, "binary_bwd_kernel");
 }
 
@@ -264,7 +266,7 @@ int launch_binary(numrs_hip_ctx *ctx, const float *g, const float *x, const floa
 // sum/mean backward fill, MSE backward
 // ---------------------------------------------------------------------------
 
-template <bool VEC>
+template <int VEC>
 __global__ void __launch_bounds__(kBlock)
     fill_grad_kernel(const float *__restrict__ g0, float *__restrict__ dx, int64_t n, float nf,
                      int divide, int acc) {
@@ -275,8 +277,8 @@ __global__ void __launch_bounds__(kBlock)
     const int64_t i = base + (int64_t)u * kBlock * 4;
     if (VEC && i + 3 < n) {
       f4 r = {v, v, v, v};
-      if (acc) r += *reinterpret_cast<const f4 *>(dx + i);
-      *reinterpret_cast<f4 *>(dx + i) = r;
+      if (acc) r += ldv<VEC>(dx + i);
+      stv<VEC>(dx + i, r);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -285,7 +287,7 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
-template <bool VEC>
+template <int VEC>
 __global__ void __launch_bounds__(kBlock)
     mse_bwd_kernel(const float *__restrict__ g0, const float *__restrict__ p,
                    const float *__restrict__ t, float *__restrict__ dp, float *__restrict__ dt,
@@ -296,20 +298,20 @@ __global__ void __launch_bounds__(kBlock)
   for (int u = 0; u < kVecPerThread; ++u) {
     const int64_t i = base + (int64_t)u * kBlock * 4;
     if (VEC && i + 3 < n) {
-      const f4 pv = *reinterpret_cast<const f4 *>(p + i);
-      const f4 tv = *reinterpret_cast<const f4 *>(t + i);
+      const f4 pv = ldv<VEC>(p + i);
+      const f4 tv = ldv<VEC>(t + i);
       f4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = ((gs * 2.0f) * (pv[e] - tv[e])) / nf;  // backward.rs:250
       if (dp) {
         f4 o = v;
-        if (acc) o += *reinterpret_cast<const f4 *>(dp + i);
-        *reinterpret_cast<f4 *>(dp + i) = o;
+        if (acc) o += ldv<VEC>(dp + i);
+        stv<VEC>(dp + i, o);
       }
       if (dt) {
         f4 o = -v;  // backward.rs:257
-        if (acc) o = *reinterpret_cast<const f4 *>(dt + i) + (-v);
-        *reinterpret_cast<f4 *>(dt + i) = o;
+        if (acc) o = ldv<VEC>(dt + i) + (-v);
+        stv<VEC>(dt + i, o);
       }
     } else {
 #pragma unroll
@@ -330,7 +332,7 @@ __global__ void __launch_bounds__(kBlock)
 // ---------------------------------------------------------------------------
 
 // SGD::step, optim/sgd.rs:130-167 (+ apply_weight_decay, optim/base.rs:26-36).
-template <bool MOMENTUM, bool DECAY, bool VEC>
+template <bool MOMENTUM, bool DECAY, int VEC>
 __global__ void __launch_bounds__(kBlock)
     sgd_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ v,
                int64_t n, float lr, float mu, float wd) {
@@ -339,10 +341,10 @@ __global__ void __launch_bounds__(kBlock)
   for (int u = 0; u < kVecPerThread; ++u) {
     const int64_t i = base + (int64_t)u * kBlock * 4;
     if (VEC && i + 3 < n) {
-      f4 pv = *reinterpret_cast<const f4 *>(p + i);
-      f4 gv = *reinterpret_cast<const f4 *>(g + i);
+      f4 pv = ldv<VEC>(p + i);
+      f4 gv = ldv<VEC>(g + i);
       f4 vv;
-      if (MOMENTUM) vv = *reinterpret_cast<const f4 *>(v + i);
+      if (MOMENTUM) vv = ldv<VEC>(v + i);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float gg = gv[e];
@@ -354,8 +356,8 @@ __global__ void __launch_bounds__(kBlock)
           pv[e] = pv[e] - lr * gg;
         }
       }
-      *reinterpret_cast<f4 *>(p + i) = pv;
-      if (MOMENTUM) *reinterpret_cast<f4 *>(v + i) = vv;
+      stv<VEC>(p + i, pv);
+      if (MOMENTUM) stv<VEC>(v + i, vv);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -390,7 +392,7 @@ __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
 }
 
 // Adam::step, optim/adam.rs:310-353, fused into one pass over p, g, m, v.
-template <bool DECAY, bool VEC>
+template <bool DECAY, int VEC>
 __global__ void __launch_bounds__(kBlock)
     adam_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m,
                 float *__restrict__ v, int64_t n, AdamArgs a) {
@@ -399,10 +401,10 @@ __global__ void __launch_bounds__(kBlock)
   for (int u = 0; u < kVecPerThread; ++u) {
     const int64_t i = base + (int64_t)u * kBlock * 4;
     if (VEC && i + 3 < n) {
-      f4 pv = *reinterpret_cast<const f4 *>(p + i);
-      const f4 gv = *reinterpret_cast<const f4 *>(g + i);
-      f4 mv = *reinterpret_cast<const f4 *>(m + i);
-      f4 vv = *reinterpret_cast<const f4 *>(v + i);
+      f4 pv = ldv<VEC>(p + i);
+      const f4 gv = ldv<VEC>(g + i);
+      f4 mv = ldv<VEC>(m + i);
+      f4 vv = ldv<VEC>(v + i);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float pe = pv[e], me = mv[e], ve = vv[e];
@@ -411,9 +413,9 @@ __global__ void __launch_bounds__(kBlock)
         mv[e] = me;
         vv[e] = ve;
       }
-      *reinterpret_cast<f4 *>(p + i) = pv;
-      *reinterpret_cast<f4 *>(m + i) = mv;
-      *reinterpret_cast<f4 *>(v + i) = vv;
+      stv<VEC>(p + i, pv);
+      stv<VEC>(m + i, mv);
+      stv<VEC>(v + i, vv);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -587,12 +589,11 @@ int numrs_hip_fill_grad(numrs_hip_ctx *ctx, const float *g_scalar, float *dx, in
   if (n == 0) return NUMRS_HIP_OK;
   if (g_scalar == nullptr || dx == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_fill_grad: null pointer");
-  if (numrs_hip::aligned16(dx))
-    fill_grad_kernel<true><<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(
-        g_scalar, dx, n, (float)n, divide_by_n, accumulate);
-  else
-    fill_grad_kernel<false><<<grid_for(n, kElemsPerBlock), kBlock, 0, ctx->stream>>>(
-        g_scalar, dx, n, (float)n, divide_by_n, accumulate);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(numrs_hip::aligned16(dx), n), [&](auto V) {
+    fill_grad_kernel<decltype(V)::value><<<grid_for(n, kElemsPerBlock), kBlock, 0,
+                                           ctx->stream>>>(g_scalar, dx, n, (float)n, divide_by_n,
+                                                          accumulate);
+  });
   return numrs_hip::check_launch(ctx, "fill_grad_kernel");
 }
 
@@ -606,12 +607,10 @@ int numrs_hip_mse_backward(numrs_hip_ctx *ctx, const float *g_scalar, const floa
   const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(t) &&
                    numrs_hip::aligned16(dp) && numrs_hip::aligned16(dt);
   const unsigned grid = grid_for(n, kElemsPerBlock);
-  if (vec)
-    mse_bwd_kernel<true><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt, n, (float)n,
-                                                           accumulate);
-  else
-    mse_bwd_kernel<false><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt, n, (float)n,
-                                                            accumulate);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
+    mse_bwd_kernel<decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt,
+                                                                         n, (float)n, accumulate);
+  });
   return numrs_hip::check_launch(ctx, "mse_bwd_kernel");
 }
 
@@ -626,13 +625,11 @@ int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, i
   const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(g) &&
                    (mu == 0.0f || numrs_hip::aligned16(v));
   const bool mom = mu != 0.0f, dec = wd != 0.0f;
-#define NRS_SGD(M, D)                                                                   \
-  do {                                                                                  \
-    if (vec)                                                                            \
-      sgd_kernel<M, D, true><<<grid, kBlock, 0, ctx->stream>>>(p, g, v, n, lr, mu, wd);  \
-    else                                                                                \
-      sgd_kernel<M, D, false><<<grid, kBlock, 0, ctx->stream>>>(p, g, v, n, lr, mu, wd); \
-  } while (0)
+#define NRS_SGD(M, D)                                                                      \
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {                       \
+    sgd_kernel<M, D, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(p, g, v, n, lr, mu, \
+                                                                          wd);             \
+  })
   if (mom && dec) NRS_SGD(true, true);
   else if (mom) NRS_SGD(true, false);
   else if (dec) NRS_SGD(false, true);
@@ -724,10 +721,12 @@ int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, 
   const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(g) &&
                    numrs_hip::aligned16(m) && numrs_hip::aligned16(v);
   const bool dec = wd != 0.0f;
-  if (dec && vec) adam_kernel<true, true><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
-  else if (dec) adam_kernel<true, false><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
-  else if (vec) adam_kernel<false, true><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
-  else adam_kernel<false, false><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
+    if (dec)
+      adam_kernel<true, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+    else
+      adam_kernel<false, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(p, g, m, v, n, a);
+  });
   return numrs_hip::check_launch(ctx, "adam_kernel");
 }
 

@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(kBlock)
 // grid stride (VEC: 16-byte aligned operands), eight loads per operand in
 // flight at once, into four independent partial sums that are added in a
 // fixed order, then across the wave and the block.
-template <int KIND, bool VEC>
+template <int KIND, int VEC>
 __global__ void __launch_bounds__(kBlock)
     reduce_pass1(const float *__restrict__ x, const float *__restrict__ t, int64_t n,
                  float *__restrict__ partial) {
@@ -179,8 +179,8 @@ __global__ void __launch_bounds__(kBlock)
       f4v xv[8], tv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        xv[u] = reinterpret_cast<const f4v *>(x)[i + u * stride];
-        if (KIND == 1) tv[u] = reinterpret_cast<const f4v *>(t)[i + u * stride];
+        xv[u] = numrs_hip::ldv<VEC>(x + 4 * (i + u * stride));
+        if (KIND == 1) tv[u] = numrs_hip::ldv<VEC>(t + 4 * (i + u * stride));
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -189,9 +189,9 @@ __global__ void __launch_bounds__(kBlock)
           acc[u & 3] += term(xv[u][e], KIND == 1 ? tv[u][e] : 0.0f);
     }
     for (; i < n4; i += stride) {
-      const f4v xv = reinterpret_cast<const f4v *>(x)[i];
+      const f4v xv = numrs_hip::ldv<VEC>(x + 4 * i);
       f4v tv = {0.f, 0.f, 0.f, 0.f};
-      if (KIND == 1) tv = reinterpret_cast<const f4v *>(t)[i];
+      if (KIND == 1) tv = numrs_hip::ldv<VEC>(t + 4 * i);
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[0] += term(xv[e], tv[e]);
     }
@@ -370,14 +370,12 @@ int full_reduce(numrs_hip_ctx *ctx, int kind, const float *x, const float *t, in
   float *partial = static_cast<float *>(ws);
   const bool vec = numrs_hip::aligned16(x) && (kind == 0 || numrs_hip::aligned16(t));
   const unsigned grid = (unsigned)blocks;
-  if (kind == 0 && vec)
-    reduce_pass1<0, true><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
-  else if (kind == 0)
-    reduce_pass1<0, false><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
-  else if (vec)
-    reduce_pass1<1, true><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
-  else
-    reduce_pass1<1, false><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
+    if (kind == 0)
+      reduce_pass1<0, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+    else
+      reduce_pass1<1, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+  });
   if (int rc = numrs_hip::check_launch(ctx, "reduce_pass1")) return rc;
   reduce_final<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, div, out);
   return numrs_hip::check_launch(ctx, "reduce_final");

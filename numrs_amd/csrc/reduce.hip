@@ -30,6 +30,8 @@ constexpr int kColsPerBlock = 512;
 constexpr int kBandRows = 4;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+using numrs_hip::ldv;
+using numrs_hip::stv;
 
 // Column of element e (0..7) of lane l in a 512-column strip.  VEC: two float4
 // groups, 4l..4l+3 and 256+4l..256+4l+3; otherwise l + 64e (coalesced scalars).
@@ -40,7 +42,7 @@ __device__ __forceinline__ int strip_col(int l, int e) {
 
 // Pass 1.  RELU: dx = z > 0 ? g : 0 (also written out when dx != nullptr);
 // otherwise the reduced value is g itself.
-template <bool RELU, bool VEC>
+template <bool RELU, int VEC>
 __global__ void __launch_bounds__(kBlock)
     colreduce_pass1(const float *__restrict__ g, const float *__restrict__ z,
                     float *__restrict__ dx, float *__restrict__ partial, int64_t rows,
@@ -52,8 +54,8 @@ __global__ void __launch_bounds__(kBlock)
   f4 sum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   // With VEC, cols % 4 == 0, so a float4 group is either wholly inside or
   // wholly outside the matrix.
-  const bool full0 = VEC && c0 + strip_col<VEC>(lane, 3) < cols;
-  const bool full1 = VEC && c0 + strip_col<VEC>(lane, 7) < cols;
+  const bool full0 = VEC && c0 + strip_col<(VEC != 0)>(lane, 3) < cols;
+  const bool full1 = VEC && c0 + strip_col<(VEC != 0)>(lane, 7) < cols;
   // Strips wholly inside the matrix (all but a ragged last one) issue both
   // float4 loads of g and of z before any use, so each wave keeps four loads
   // in flight; a per-lane guard would split them into separate waits.
@@ -68,11 +70,11 @@ __global__ void __launch_bounds__(kBlock)
       f4 ga[2], za[2], gb[2], zb[2];
       auto load = [&](int64_t row, f4 *gv, f4 *zv) {
         const int64_t i0 = row * cols + c0 + 4 * lane;
-        gv[0] = *reinterpret_cast<const f4 *>(g + i0);
-        gv[1] = *reinterpret_cast<const f4 *>(g + i0 + 256);
+        gv[0] = ldv<VEC>(g + i0);
+        gv[1] = ldv<VEC>(g + i0 + 256);
         if (RELU) {
-          zv[0] = *reinterpret_cast<const f4 *>(z + i0);
-          zv[1] = *reinterpret_cast<const f4 *>(z + i0 + 256);
+          zv[0] = ldv<VEC>(z + i0);
+          zv[1] = ldv<VEC>(z + i0 + 256);
         }
       };
       auto band = [&](int64_t row, const f4 *gv, const f4 *zv) {
@@ -87,11 +89,11 @@ __global__ void __launch_bounds__(kBlock)
           if (dx != nullptr) {
             f4 o0 = g0, o1 = g1;
             if (acc_dx) {
-              o0 += *reinterpret_cast<const f4 *>(dx + i0);
-              o1 += *reinterpret_cast<const f4 *>(dx + i1);
+              o0 += ldv<VEC>(dx + i0);
+              o1 += ldv<VEC>(dx + i1);
             }
-            *reinterpret_cast<f4 *>(dx + i0) = o0;
-            *reinterpret_cast<f4 *>(dx + i1) = o1;
+            stv<VEC>(dx + i0, o0);
+            stv<VEC>(dx + i1, o1);
           }
         }
         sum[0] += g0;
@@ -126,15 +128,15 @@ __global__ void __launch_bounds__(kBlock)
         for (int h = 0; h < 2; ++h) {
           if (!(h == 0 ? full0 : full1)) continue;
           const int64_t i = off + 256 * h + 4 * lane;
-          f4 gv = *reinterpret_cast<const f4 *>(g + i);
+          f4 gv = ldv<VEC>(g + i);
           if (RELU) {
-            const f4 zv = *reinterpret_cast<const f4 *>(z + i);
+            const f4 zv = ldv<VEC>(z + i);
 #pragma unroll
             for (int e = 0; e < 4; ++e) gv[e] = zv[e] > 0.0f ? gv[e] : 0.0f;  // backward.rs:158
             if (dx != nullptr) {
               f4 out = gv;
-              if (acc_dx) out += *reinterpret_cast<const f4 *>(dx + i);
-              *reinterpret_cast<f4 *>(dx + i) = out;
+              if (acc_dx) out += ldv<VEC>(dx + i);
+              stv<VEC>(dx + i, out);
             }
           }
           sum[h] += gv;
@@ -142,7 +144,7 @@ __global__ void __launch_bounds__(kBlock)
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int64_t c = c0 + strip_col<VEC>(lane, e);
+          const int64_t c = c0 + strip_col<(VEC != 0)>(lane, e);
           if (c < cols) {
             const int64_t i = r * cols + c;
             float gv = g[i];
@@ -165,7 +167,7 @@ __global__ void __launch_bounds__(kBlock)
     float *dst = partial + (int64_t)blockIdx.y * cols + c0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int64_t c = strip_col<VEC>(lane, 4 * h + e);
+      const int64_t c = strip_col<(VEC != 0)>(lane, 4 * h + e);
       if (c0 + c < cols) dst[c] = s[e];
     }
   }
@@ -484,7 +486,7 @@ __global__ void __launch_bounds__(kBlock)
 // loads.  The grid sweeps rows in interleaved bands of 4 (one row per wave):
 // block b takes bands b, b + gridDim.x, ...  Wave partials are combined in
 // wave order through LDS and written to the [gridDim.x, cols] workspaces.
-template <int NV>
+template <int NV, int VM>
 __global__ void __launch_bounds__(kBlock)
     layernorm_bwd_vec(const float *__restrict__ g, const float *__restrict__ x,
                       const float *__restrict__ gamma, const float *__restrict__ mean,
@@ -531,8 +533,8 @@ __global__ void __launch_bounds__(kBlock)
         f4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = rs * ((gg[i][e] - m1) - xh[i][e] * m2);
-        if (acc_dx) v += *reinterpret_cast<const f4 *>(dr + c);
-        *reinterpret_cast<f4 *>(dr + c) = v;
+        if (acc_dx) v += ldv<VM>(dr + c);
+        stv<VM>(dr + c, v);
       }
     }
   };
@@ -549,8 +551,8 @@ __global__ void __launch_bounds__(kBlock)
       // unconditional load keeps the wait counts exact.
       const int64_t c = in[i] ? 4 * (int64_t)(lane + 64 * i) : 0;
       const f4 z = {0.f, 0.f, 0.f, 0.f};
-      const f4 xl = *reinterpret_cast<const f4 *>(x + r * cols + c);
-      const f4 gl = *reinterpret_cast<const f4 *>(g + r * cols + c);
+      const f4 xl = ldv<VM>(x + r * cols + c);
+      const f4 gl = ldv<VM>(g + r * cols + c);
       xv[i] = in[i] ? xl : z;
       gv[i] = in[i] ? gl : z;
     }
@@ -617,21 +619,14 @@ int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, flo
   const bool vec = numrs_hip::aligned16(g) && (z == nullptr || numrs_hip::aligned16(z)) &&
                    (dx == nullptr || numrs_hip::aligned16(dx)) && (cols & 3) == 0;
   dim3 grid((unsigned)strips, (unsigned)chunks);
-  if (z != nullptr) {
-    if (vec)
-      colreduce_pass1<true, true><<<grid, kBlock, 0, ctx->stream>>>(g, z, dx, partial, rows, cols,
-                                                                    acc_dx);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, rows * cols), [&](auto V) {
+    if (z != nullptr)
+      colreduce_pass1<true, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(
+          g, z, dx, partial, rows, cols, acc_dx);
     else
-      colreduce_pass1<true, false><<<grid, kBlock, 0, ctx->stream>>>(g, z, dx, partial, rows,
-                                                                     cols, acc_dx);
-  } else {
-    if (vec)
-      colreduce_pass1<false, true><<<grid, kBlock, 0, ctx->stream>>>(g, z, dx, partial, rows,
-                                                                     cols, 0);
-    else
-      colreduce_pass1<false, false><<<grid, kBlock, 0, ctx->stream>>>(g, z, dx, partial, rows,
-                                                                      cols, 0);
-  }
+      colreduce_pass1<false, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(
+          g, z, dx, partial, rows, cols, 0);
+  });
   if (int rc = numrs_hip::check_launch(ctx, "colreduce_pass1")) return rc;
   if (mode == NUMRS_HIP_UNBROADCAST_CORRECT)
     return launch_finalize(ctx, partial, out, acc_out, nullptr, nullptr, 0, chunks, cols);
@@ -729,18 +724,25 @@ int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float
   float *part_b = part ? part + chunks * cols : nullptr;
   if (vec) {
     const unsigned grid = (unsigned)chunks;
-    if (cols <= 256)
-      layernorm_bwd_vec<1><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
-                                                             part_b, rows, cols, acc_dx, want);
-    else if (cols <= 512)
-      layernorm_bwd_vec<2><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
-                                                             part_b, rows, cols, acc_dx, want);
-    else if (cols <= 1024)
-      layernorm_bwd_vec<4><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
-                                                             part_b, rows, cols, acc_dx, want);
-    else
-      layernorm_bwd_vec<8><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx, part,
-                                                             part_b, rows, cols, acc_dx, want);
+    numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, rows * cols), [&](auto V) {
+      constexpr int VM = decltype(V)::value;
+      if (cols <= 256)
+        layernorm_bwd_vec<1, VM><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx,
+                                                                   part, part_b, rows, cols,
+                                                                   acc_dx, want);
+      else if (cols <= 512)
+        layernorm_bwd_vec<2, VM><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx,
+                                                                   part, part_b, rows, cols,
+                                                                   acc_dx, want);
+      else if (cols <= 1024)
+        layernorm_bwd_vec<4, VM><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx,
+                                                                   part, part_b, rows, cols,
+                                                                   acc_dx, want);
+      else
+        layernorm_bwd_vec<8, VM><<<grid, kBlock, 0, ctx->stream>>>(g, x, gamma, mean, rstd, dx,
+                                                                   part, part_b, rows, cols,
+                                                                   acc_dx, want);
+    });
     if (int rc = numrs_hip::check_launch(ctx, "layernorm_bwd_vec")) return rc;
   } else {
     const size_t lds = (size_t)8 * cols * sizeof(float);

@@ -27,8 +27,9 @@ __device__ __forceinline__ int64_t vcol(int lane, int i) {
 // register-resident path), so the load needs no branch.  Callers ignore the
 // values of such columns.  A load under `if (c < cols)` would make each
 // column group its own memory round trip.
+template <int VM = 1>
 __device__ __forceinline__ f4 load_cols(const float *r, int64_t c, int64_t cols) {
-  return *reinterpret_cast<const f4 *>(r + (c < cols ? c : cols - 4));
+  return numrs_hip::ldv<VM>(r + (c < cols ? c : cols - 4));
 }
 
 // cross_entropy_backward, backward.rs:265-301:
@@ -61,7 +62,7 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
-template <bool LABELS, int NV>
+template <bool LABELS, int NV, int VM>
 __global__ void __launch_bounds__(kBlock)
     softmax_ce_bwd_vec(const float *__restrict__ g0, const float *__restrict__ x,
                        const float *__restrict__ onehot, const int32_t *__restrict__ labels,
@@ -74,8 +75,8 @@ __global__ void __launch_bounds__(kBlock)
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t c = vcol<NV>(lane, i);
-    xv[i] = load_cols(xr, c, C);
-    if (!LABELS) tv[i] = load_cols(onehot + row * C, c, C);
+    xv[i] = load_cols<VM>(xr, c, C);
+    if (!LABELS) tv[i] = load_cols<VM>(onehot + row * C, c, C);
   }
   float m = -INFINITY;
 #pragma unroll
@@ -111,8 +112,8 @@ __global__ void __launch_bounds__(kBlock)
         const float t = LABELS ? (c + e == (int64_t)label ? 1.0f : 0.0f) : tv[i][e];
         v[e] = (xv[i][e] / s - t) * scale;  // backward.rs:289-291
       }
-      if (acc) v += *reinterpret_cast<const f4 *>(out + c);
-      *reinterpret_cast<f4 *>(out + c) = v;
+      if (acc) v += numrs_hip::ldv<VM>(out + c);
+      numrs_hip::stv<VM>(out + c, v);
     }
   }
 }
@@ -137,7 +138,7 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
-template <int NV>
+template <int NV, int VM>
 __global__ void __launch_bounds__(kBlock)
     softmax_bwd_vec(const float *__restrict__ y, const float *g, float *dx, int64_t rows,
                     int64_t cols, int acc) {
@@ -149,8 +150,8 @@ __global__ void __launch_bounds__(kBlock)
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t c = vcol<NV>(lane, i);
-    yv[i] = load_cols(yr, c, cols);
-    gv[i] = load_cols(gr, c, cols);
+    yv[i] = load_cols<VM>(yr, c, cols);
+    gv[i] = load_cols<VM>(gr, c, cols);
   }
   float d = 0.0f;
 #pragma unroll
@@ -169,8 +170,8 @@ __global__ void __launch_bounds__(kBlock)
       f4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = yv[i][e] * (gv[i][e] - d);
-      if (acc) v += *reinterpret_cast<const f4 *>(out + c);
-      *reinterpret_cast<f4 *>(out + c) = v;
+      if (acc) v += numrs_hip::ldv<VM>(out + c);
+      numrs_hip::stv<VM>(out + c, v);
     }
   }
 }
@@ -318,16 +319,16 @@ __device__ __forceinline__ int argmax_regs(const f4 (&xv)[NV], int ncols, int la
   return bi < 0 ? start : bi;
 }
 
-template <int NV>
+template <int NV, int VM>
 __device__ __forceinline__ void load_row_regs(f4 (&xv)[NV], const float *xr, int ncols, int lane) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) xv[i] = load_cols(xr, vcol<NV>(lane, i), ncols);
+  for (int i = 0; i < NV; ++i) xv[i] = load_cols<VM>(xr, vcol<NV>(lane, i), ncols);
 }
 
 // One wave per row.  (Measured on MI355X at [16384, 1024]: persistent
 // waves that load the next row before reducing the current one ran 10-20%
 // slower than this one-shot form.)
-template <int NV, bool TIE_LAST>
+template <int NV, bool TIE_LAST, int VM>
 __global__ void __launch_bounds__(kBlock)
     argmax_vec(const float *__restrict__ x, int32_t *__restrict__ idx, int64_t rows,
                int64_t cols) {
@@ -336,7 +337,7 @@ __global__ void __launch_bounds__(kBlock)
   if (row >= rows) return;  // row is uniform over the wave
   const int ncols = (int)cols;
   f4 xv[NV];
-  load_row_regs<NV>(xv, x + row * cols, ncols, lane);
+  load_row_regs<NV, VM>(xv, x + row * cols, ncols, lane);
   const int r = argmax_regs<NV, TIE_LAST>(xv, ncols, lane);
   if (lane == 0) idx[row] = r;
 }
@@ -406,15 +407,15 @@ int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, con
   const unsigned grid = grid_for(B, kRowsPerBlock);
   const int nv = row_nv(C, numrs_hip::aligned16(logits) && numrs_hip::aligned16(dlogits) &&
                                (onehot == nullptr || numrs_hip::aligned16(onehot)));
-#define NRS_CE_VEC(NV)                                                                           \
-  if (labels != nullptr)                                                                         \
-    softmax_ce_bwd_vec<true, NV><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot,      \
-                                                                   labels, dlogits, B, C,        \
-                                                                   accumulate);                  \
-  else                                                                                           \
-    softmax_ce_bwd_vec<false, NV><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot,     \
-                                                                    labels, dlogits, B, C,       \
-                                                                    accumulate);                 \
+#define NRS_CE_VEC(NV)                                                                        \
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, B * C), [&](auto V) {                     \
+    if (labels != nullptr)                                                                    \
+      softmax_ce_bwd_vec<true, NV, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(      \
+          g_scalar, logits, onehot, labels, dlogits, B, C, accumulate);                       \
+    else                                                                                      \
+      softmax_ce_bwd_vec<false, NV, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(     \
+          g_scalar, logits, onehot, labels, dlogits, B, C, accumulate);                       \
+  });                                                                                         \
   return numrs_hip::check_launch(ctx, "softmax_ce_bwd_vec");
   switch (nv) {
     case 1: { NRS_CE_VEC(1) }
@@ -443,15 +444,21 @@ int numrs_hip_softmax_backward(numrs_hip_ctx *ctx, const float *y, const float *
   if (y == nullptr || g == nullptr || dx == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
   const unsigned grid = grid_for(rows, kRowsPerBlock);
-  switch (row_nv(cols, numrs_hip::aligned16(y) && numrs_hip::aligned16(g) &&
-                           numrs_hip::aligned16(dx))) {
-    case 1: softmax_bwd_vec<1><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
-    case 2: softmax_bwd_vec<2><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
-    case 4: softmax_bwd_vec<4><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
-    case 8: softmax_bwd_vec<8><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
-    default:
-      softmax_bwd_kernel<<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate);
+  const int nv = row_nv(cols, numrs_hip::aligned16(y) && numrs_hip::aligned16(g) &&
+                                  numrs_hip::aligned16(dx));
+  if (nv == 0) {
+    softmax_bwd_kernel<<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate);
+    return numrs_hip::check_launch(ctx, "softmax_bwd_kernel");
   }
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, rows * cols), [&](auto V) {
+    constexpr int VM = decltype(V)::value;
+    switch (nv) {
+      case 1: softmax_bwd_vec<1, VM><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+      case 2: softmax_bwd_vec<2, VM><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+      case 4: softmax_bwd_vec<4, VM><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+      default: softmax_bwd_vec<8, VM><<<grid, kBlock, 0, ctx->stream>>>(y, g, dx, rows, cols, accumulate); break;
+    }
+  });
   return numrs_hip::check_launch(ctx, "softmax_bwd_kernel");
 }
 
@@ -467,11 +474,15 @@ int numrs_hip_argmax_rows(numrs_hip_ctx *ctx, const float *x, int32_t *idx, int6
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
   const unsigned grid = grid_for(rows, kRowsPerBlock);
   const int tl = tie_last ? 1 : 0;
-#define NRS_ARGMAX_VEC(NV)                                                              \
-  if (tl)                                                                               \
-    argmax_vec<NV, true><<<grid, kBlock, 0, ctx->stream>>>(x, idx, rows, cols);          \
-  else                                                                                  \
-    argmax_vec<NV, false><<<grid, kBlock, 0, ctx->stream>>>(x, idx, rows, cols);         \
+#define NRS_ARGMAX_VEC(NV)                                                                \
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, rows * cols), [&](auto V) {           \
+    if (tl)                                                                               \
+      argmax_vec<NV, true, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, idx, rows, \
+                                                                                  cols);     \
+    else                                                                                  \
+      argmax_vec<NV, false, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, idx,   \
+                                                                                   rows, cols); \
+  });                                                                                     \
   break;
   switch (row_nv(cols, numrs_hip::aligned16(x))) {
     case 1: NRS_ARGMAX_VEC(1)
