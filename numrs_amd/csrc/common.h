@@ -76,13 +76,15 @@ int vec_op(numrs_hip_ctx *ctx, float *out, const float *a, const float *b, float
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Access modes of the streaming kernels: 0 per element, 1 float4, 2 float4
-// with the non-temporal hint.  Arrays of at least kStreamElems floats (64 MB)
-// do not stay in the 256 MB Infinity Cache from one kernel of a training
-// step to the next, and streaming them past the caches measured 13-14%
-// faster on MI355X from HBM (read-2-write-1: 0.70 -> 0.80 of 8 TB/s;
+// with the non-temporal hint.  Arrays of at least kStreamElems floats (32 MB)
+// are unlikely to stay in the 256 MB Infinity Cache from one kernel of a
+// training step to the next, and streaming them past the caches measured
+// 13-14% faster on MI355X from HBM (read-2-write-1: 0.70 -> 0.80 of 8 TB/s;
 // read-3-write-2: 0.70 -> 0.79).  Smaller arrays keep cached accesses, so a
-// consumer kernel can find them in the cache.
-constexpr int64_t kStreamElems = int64_t(1) << 24;
+// consumer kernel can find them in the cache.  (2^23 rather than 2^24: the
+// C4 attention softmax backward at 2^23 elements went 0.64 -> 0.71 of HBM,
+// and the C4 step time did not change.)
+constexpr int64_t kStreamElems = int64_t(1) << 23;
 inline int vec_mode(bool vec, int64_t n) { return !vec ? 0 : (n >= kStreamElems ? 2 : 1); }
 
 // Calls f(std::integral_constant<int, mode>{}) for a runtime access mode,

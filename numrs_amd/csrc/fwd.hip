@@ -119,6 +119,11 @@ __global__ void __launch_bounds__(kBlock)
 // 4(t%16)..+3, and stores output row t/16 + 16i (a column of x), output
 // columns 4(t%16)..+3, read down the LDS tile.  Row stride 65 keeps the
 // column reads spread over the banks.
+// All four loads are issued before the tile is written: a tile row past the
+// matrix edge reloads the last row or column group (rows and cols are
+// nonzero multiples of 4 here) and is not stored, so no load sits in a branch
+// with its use.  VM is the access mode (non-temporal for large matrices).
+template <int VM>
 __global__ void __launch_bounds__(kBlock)
     transpose64_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
                        int64_t cols) {
@@ -126,14 +131,18 @@ __global__ void __launch_bounds__(kBlock)
   __shared__ float tile[64][65];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int t = threadIdx.x, q = t & 15, k0 = t >> 4;
+  f4v v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = r0 + k0 + 16 * i, c = c0 + 4 * q;
+    v[i] = numrs_hip::ldv<VM>(x + (r < rows ? r : rows - 1) * cols + (c < cols ? c : cols - 4));
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int k = k0 + 16 * i;
-    const int64_t r = r0 + k, c = c0 + 4 * q;
-    if (r < rows && c < cols) {
-      const f4v v = *reinterpret_cast<const f4v *>(x + r * cols + c);
+    if (r0 + k < rows && c0 + 4 * q < cols) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tile[k][4 * q + e] = v[e];
+      for (int e = 0; e < 4; ++e) tile[k][4 * q + e] = v[i][e];
     }
   }
   __syncthreads();
@@ -145,7 +154,7 @@ __global__ void __launch_bounds__(kBlock)
       f4v v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = tile[4 * q + e][k];
-      *reinterpret_cast<f4v *>(y + c * rows + r) = v;
+      numrs_hip::stv<VM>(y + c * rows + r, v);
     }
   }
 }
@@ -441,7 +450,9 @@ int numrs_hip_transpose(numrs_hip_ctx *ctx, const float *x, float *y, int64_t ro
   if ((rows + 31) / 32 > 65535) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: too many rows");
   if ((rows & 3) == 0 && (cols & 3) == 0 && numrs_hip::aligned16(x) && numrs_hip::aligned16(y)) {
     dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
-    transpose64_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
+    numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, rows * cols), [&](auto V) {
+      transpose64_kernel<decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
+    });
     return numrs_hip::check_launch(ctx, "transpose64_kernel");
   }
   dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
