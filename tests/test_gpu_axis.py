@@ -49,9 +49,8 @@ def test_reduce_and_broadcast_axis(hip_ctx, shape, axis, mean):
                  abs_tol=tol, what="vs float64")
     assert_close(out.numpy(), want, abs_tol=2 * tol, what="vs numrs loop")
     g = rand(rng, (o * i,))
-    dx = c.empty(shape)
-    c._check(L.load().numrs_hip_broadcast_axis(c.handle, c.to_device(g).ptr, o, n, i, mean,
-                                                dx.ptr, 0))
+    dx, gd = c.empty(shape), c.to_device(g)  # held for the call: a temporary is freed at once
+    c._check(L.load().numrs_hip_broadcast_axis(c.handle, gd.ptr, o, n, i, mean, dx.ptr, 0))
     assert_bits(dx.numpy(), O.broadcast_axis(g, shape, axis, mean=bool(mean)), "broadcast")
 
 
@@ -73,14 +72,15 @@ def test_softmax_axis_forward_backward(hip_ctx, shape, axis):
     g = rand(rng, shape)
     o, n, i = O.axis_view(shape, axis)
     c = hip_ctx
-    y = c.empty(shape)
-    c._check(L.load().numrs_hip_softmax_axis_forward(c.handle, c.to_device(x).ptr, y.ptr, o, n, i))
+    y, xd = c.empty(shape), c.to_device(x)  # held for the call: a temporary is freed at once
+    c._check(L.load().numrs_hip_softmax_axis_forward(c.handle, xd.ptr, y.ptr, o, n, i))
     want_y = O.softmax_axis(x, axis)
     assert_close(y.numpy(), want_y, what="softmax")
     yd = c.to_device(want_y)
     dx = c.to_device(np.ones(shape, np.float32))
-    c._check(L.load().numrs_hip_softmax_axis_backward(c.handle, yd.ptr, c.to_device(g).ptr, dx.ptr,
-                                                       o, n, i, 1))
+    gd = c.to_device(g)
+    c._check(L.load().numrs_hip_softmax_axis_backward(c.handle, yd.ptr, gd.ptr, dx.ptr, o, n, i,
+                                                       1))
     assert_close(dx.numpy(), 1.0 + O.softmax_axis_backward(want_y, g, axis).astype(np.float64),
                  what="softmax backward (accumulate)")
 

@@ -473,8 +473,8 @@ def test_transpose(hip_ctx, rng, rows, cols):
     dimensions are multiples of 4, 32x32 tiles otherwise; a copy, so bit-exact."""
     x = rand(rng, (rows, cols))
     c = hip_ctx
-    y = c.empty((cols, rows))
-    c._check(L.load().numrs_hip_transpose(c.handle, c.to_device(x).ptr, y.ptr, rows, cols))
+    y, xd = c.empty((cols, rows)), c.to_device(x)  # held for the call: a temporary is freed at once
+    c._check(L.load().numrs_hip_transpose(c.handle, xd.ptr, y.ptr, rows, cols))
     assert_bits(y.numpy(), np.ascontiguousarray(x.T), f"transpose {rows}x{cols}")
 
 
