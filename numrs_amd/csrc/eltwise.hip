@@ -332,11 +332,13 @@ __global__ void __launch_bounds__(kBlock)
 // ---------------------------------------------------------------------------
 
 // SGD::step, optim/sgd.rs:130-167 (+ apply_weight_decay, optim/base.rs:26-36).
+// One block's kElemsPerBlock elements starting at blk * kElemsPerBlock (shared
+// by sgd_kernel and, for tensors in streaming mode, sgd_multi_kernel).
 template <bool MOMENTUM, bool DECAY, int VEC>
-__global__ void __launch_bounds__(kBlock)
-    sgd_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ v,
-               int64_t n, float lr, float mu, float wd) {
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+__device__ __forceinline__ void sgd_block(float *__restrict__ p, const float *__restrict__ g,
+                                          float *__restrict__ v, int64_t n, float lr, float mu,
+                                          float wd, int64_t blk) {
+  const int64_t base = blk * kElemsPerBlock + threadIdx.x * 4;
   const int64_t last = base + (int64_t)(kVecPerThread - 1) * kBlock * 4;
   if (VEC && last + 3 < n) {  // both groups' loads before any store (as in adam_kernel)
     f4 pv[kVecPerThread], gv[kVecPerThread], vv[kVecPerThread];
@@ -406,6 +408,13 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+template <bool MOMENTUM, bool DECAY, int VEC>
+__global__ void __launch_bounds__(kBlock)
+    sgd_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ v,
+               int64_t n, float lr, float mu, float wd) {
+  sgd_block<MOMENTUM, DECAY, VEC>(p, g, v, n, lr, mu, wd, blockIdx.x);
+}
+
 struct AdamArgs {
   float lr, b1, b2, eps, wd, omb1, omb2, bc1, bc2;
 };
@@ -421,11 +430,13 @@ __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
 }
 
 // Adam::step, optim/adam.rs:310-353, fused into one pass over p, g, m, v.
+// One block's kElemsPerBlock elements starting at blk * kElemsPerBlock (shared
+// by adam_kernel and, for tensors in streaming mode, adam_multi_kernel).
 template <bool DECAY, int VEC>
-__global__ void __launch_bounds__(kBlock)
-    adam_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m,
-                float *__restrict__ v, int64_t n, AdamArgs a) {
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
+__device__ __forceinline__ void adam_block(float *__restrict__ p, const float *__restrict__ g,
+                                           float *__restrict__ m, float *__restrict__ v,
+                                           int64_t n, const AdamArgs &a, int64_t blk) {
+  const int64_t base = blk * kElemsPerBlock + threadIdx.x * 4;
   const int64_t last = base + (int64_t)(kVecPerThread - 1) * kBlock * 4;
   if (VEC && last + 3 < n) {
     // Both groups' loads before any store: 0.71 -> 0.76 of HBM on MI355X for
@@ -492,6 +503,13 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+template <bool DECAY, int VEC>
+__global__ void __launch_bounds__(kBlock)
+    adam_kernel(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m,
+                float *__restrict__ v, int64_t n, AdamArgs a) {
+  adam_block<DECAY, VEC>(p, g, m, v, n, a, blockIdx.x);
+}
+
 // Multi-tensor optimizer launch: up to kMaxMulti parameter tensors share one
 // grid; block b belongs to the tensor t with start[t] <= b < start[t+1] and
 // covers that tensor's elements from (b - start[t]) * kElemsPerBlock.
@@ -504,6 +522,7 @@ struct MultiArgs {
   float *s2[kMaxMulti];  // Adam v
   int64_t n[kMaxMulti];
   int64_t start[kMaxMulti + 1];
+  int mode[kMaxMulti];  // access mode of each tensor (2: the float4 streaming body)
   int count;
 };
 
@@ -521,6 +540,10 @@ __global__ void __launch_bounds__(kBlock)
   const float *__restrict__ g = a.g[t];
   float *__restrict__ v = a.s1[t];
   const int64_t n = a.n[t];
+  if (a.mode[t] == 2) {  // a large tensor: the single-tensor kernel's float4 streaming body
+    sgd_block<MOMENTUM, DECAY, 2>(p, g, v, n, lr, mu, wd, blockIdx.x - a.start[t]);
+    return;
+  }
   const int64_t base = (int64_t)(blockIdx.x - a.start[t]) * kElemsPerBlock + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < 4 * kVecPerThread; ++u) {
@@ -542,6 +565,10 @@ template <bool DECAY>
 __global__ void __launch_bounds__(kBlock) adam_multi_kernel(MultiArgs a, AdamArgs args) {
   const int t = multi_find(a, blockIdx.x);
   const int64_t n = a.n[t];
+  if (a.mode[t] == 2) {  // a large tensor: the single-tensor kernel's float4 streaming body
+    adam_block<DECAY, 2>(a.p[t], a.g[t], a.s1[t], a.s2[t], n, args, blockIdx.x - a.start[t]);
+    return;
+  }
   const int64_t base = (int64_t)(blockIdx.x - a.start[t]) * kElemsPerBlock + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < 4 * kVecPerThread; ++u) {
@@ -567,6 +594,9 @@ int64_t multi_pack(MultiArgs &a, float *const *p, const float *const *g, float *
     a.s1[i] = s1 ? s1[first + i] : nullptr;
     a.s2[i] = s2 ? s2[first + i] : nullptr;
     a.n[i] = n[first + i];
+    const bool vec = numrs_hip::aligned16(a.p[i]) && numrs_hip::aligned16(a.g[i]) &&
+                     numrs_hip::aligned16(a.s1[i]) && numrs_hip::aligned16(a.s2[i]);
+    a.mode[i] = numrs_hip::vec_mode(vec, a.n[i]);
     a.start[i] = blocks;
     blocks += (n[first + i] + kElemsPerBlock - 1) / kElemsPerBlock;
   }

@@ -758,7 +758,8 @@ def test_linear_forward_backward(hip_ctx, rng, T, fin, fout):
 def test_optimizer_multi_tensor_bit_exact(hip_ctx, rng):
     import ctypes
 
-    sizes = [100352, 128, 1280, 10, 1, 4097, 33]
+    # (1 << 23) + 5 takes the float4 streaming body inside the multi-tensor launch
+    sizes = [100352, 128, 1280, 10, 1, 4097, 33, (1 << 23) + 5]
     c = hip_ctx
     for kind in ("sgd", "sgd_mom", "adam"):
         ps = [rand(rng, n) for n in sizes]
