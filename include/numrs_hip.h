@@ -332,26 +332,26 @@ int numrs_hip_argmax_rows(numrs_hip_ctx *ctx, const float *x, int32_t *idx, int6
 /* Optimizer steps                                                         */
 /* ---------------------------------------------------------------------- */
 
-/* SGD::step for one parameter (optim/sgd.rs:130-167, weight decay
+/* SGD::step for one parameter (optim/sgd.rs:87-124, weight decay
  * optim/base.rs:26-36): g' = g + wd*p; mu != 0: v = mu*v + g', p -= lr*v;
  * else p -= lr*g'.  v may be NULL when mu == 0. */
 int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, int64_t n,
                        float lr, float mu, float wd);
 
 /* SGD over `count` parameter tensors in one launch (the per-parameter loop
- * of sgd.rs:131-164 fused): p[i], g[i], v[i] (v may be NULL when mu == 0)
+ * of sgd.rs:88-121 fused): p[i], g[i], v[i] (v may be NULL when mu == 0)
  * of n[i] elements each.  The pointer arrays are host arrays. */
 int numrs_hip_sgd_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *const *g,
                              float *const *v, const int64_t *n, int count, float lr, float mu,
                              float wd);
 
-/* Adam::step for one parameter (optim/adam.rs:310-353) at step t (the
+/* Adam::step for one parameter (optim/adam.rs:124-167) at step t (the
  * already-incremented counter): bias corrections 1 - b^t are computed on the
  * host with f32::powi's semantics, then one fused pass updates p, m, v
  * (28 B/element). */
 int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, float *v,
                         int64_t n, float lr, float b1, float b2, float eps, float wd, int t);
-/* Adam over `count` parameter tensors in one launch (adam.rs:317-350 fused). */
+/* Adam over `count` parameter tensors in one launch (adam.rs:131-164 fused). */
 int numrs_hip_adam_step_multi(numrs_hip_ctx *ctx, float *const *p, const float *const *g,
                               float *const *m, float *const *v, const int64_t *n, int count,
                               float lr, float b1, float b2, float eps, float wd, int t);
@@ -547,7 +547,7 @@ int numrs_hip_tensor_time_slice(numrs_hip_tensor *x, int64_t t, numrs_hip_tensor
 int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
                                int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out);
 
-/* SGD::new (optim/sgd.rs:90-112) / Adam::new (optim/adam.rs:250-285) over
+/* SGD::new (optim/sgd.rs:47-69) / Adam::new (optim/adam.rs:64-99) over
  * parameter tensors; step / zero_grad / learning_rate / set_learning_rate
  * are the Optimizer trait (optim/base.rs:8-23). */
 int numrs_hip_optim_sgd(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, float lr,
@@ -560,7 +560,7 @@ int numrs_hip_optim_set_lr(numrs_hip_optim *opt, float lr);
 float numrs_hip_optim_lr(const numrs_hip_optim *opt);
 int numrs_hip_optim_free(numrs_hip_optim *opt);
 /* Optimizer state for checkpoints (TrainingState.optimizer_state of the
- * reference's JSON checkpoint, llo/model.rs:207-220, ops/model.rs:550-590,
+ * reference's JSON checkpoint, llo/model.rs:207-220, ops/model.rs:550-588,
  * where the reference leaves it empty).  Up to two state slots per parameter
  * -- SGD: velocity; Adam: m, v; the NUMRS_HIP_OPT_* kinds: their two state
  * arrays -- plus the step counter t.  Lookahead and L-BFGS are not exported.

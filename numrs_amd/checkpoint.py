@@ -1,7 +1,7 @@
 """numrs's JSON training checkpoint for device-resident parameters and
 optimizer state.
 
-The file is what numrs's `save_checkpoint` writes (ops/model.rs:544-590):
+The file is what numrs's `save_checkpoint` writes (ops/model.rs:544-588):
 serde_json of `{ "model": OnnxModel, "training_state": TrainingState }`
 (llo/model.rs).  Parameters are the model graph's initializers
 (`OnnxTensor { name, dtype: 1 (FLOAT), shape, data: little-endian f32 bytes }`,
@@ -109,7 +109,7 @@ def save_checkpoint(path: str, params: dict, optimizer=None, *, epoch: int = 0,
 
 @dataclass
 class Checkpoint:
-    """load_checkpoint(path) -> (OnnxModel, TrainingState) (ops/model.rs:577-590)."""
+    """load_checkpoint(path) -> (OnnxModel, TrainingState) (ops/model.rs:577-588)."""
     name: str
     initializers: dict
     epoch: int

@@ -1015,7 +1015,7 @@ int new_optim(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, bool adam, O
     const T &p = params[i]->t;
     o->params.push_back(p);
     Buf a, b;
-    // Velocities / moments start at zero (sgd.rs:96-103, adam.rs:258-272).
+    // Velocities / moments start at zero (sgd.rs:53-60, adam.rs:72-86).
     if (int rc = alloc_buf(ctx, p->numel(), sizeof(float), &a)) return rc;
     if (int rc = numrs_hip_fill(ctx, a->ptr, p->numel(), 0.0f)) return rc;
     if (adam) {
@@ -1499,14 +1499,14 @@ int numrs_hip_optim_step(numrs_hip_optim *opt) {
     case Family::LBFGS: return lbfgs_step(o);
     default: break;
   }
-  if (o.adam) ++o.t;  // adam.rs:311
+  if (o.adam) ++o.t;  // adam.rs:125
   if (o.fam == Family::Kind && kind_uses_t(o.kind)) ++o.t;  // e.g. adamw.rs:93
   std::vector<float *> ps, ms, vs;
   std::vector<const float *> gs;
   std::vector<int64_t> ns;
   for (size_t i = 0; i < o.params.size(); ++i) {
     const T &p = o.params[i];
-    if (!p->requires_grad) continue;  // sgd.rs:134-136, adam.rs:320-322
+    if (!p->requires_grad) continue;  // sgd.rs:91-93, adam.rs:134-136
     if (int rc = grad_materialise(p)) return rc;
     ps.push_back(p->data->ptr);
     gs.push_back(p->grad->buf->ptr);
@@ -1526,7 +1526,7 @@ int numrs_hip_optim_step(numrs_hip_optim *opt) {
                                   ns.data(), count, o.lr, o.mu, o.wd);
 }
 
-int numrs_hip_optim_zero_grad(numrs_hip_optim *opt) {  // sgd.rs:169-173
+int numrs_hip_optim_zero_grad(numrs_hip_optim *opt) {  // sgd.rs:126-130
   if (opt == nullptr) return NUMRS_HIP_E_INVALID;
   if (opt->o.fam == Family::Lookahead) return numrs_hip_optim_zero_grad(opt->o.inner);
   for (const T &p : opt->o.params)

@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(kBlock)
 // Optimizers
 // ---------------------------------------------------------------------------
 
-// SGD::step, optim/sgd.rs:130-167 (+ apply_weight_decay, optim/base.rs:26-36).
+// SGD::step, optim/sgd.rs:87-124 (+ apply_weight_decay, optim/base.rs:26-36).
 // One block's kElemsPerBlock elements starting at blk * kElemsPerBlock (shared
 // by sgd_kernel and, for tensors in streaming mode, sgd_multi_kernel).
 template <bool MOMENTUM, bool DECAY, int VEC>
@@ -422,14 +422,14 @@ struct AdamArgs {
 __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v, const AdamArgs &a,
                                           bool decay) {
   if (decay) g = g + a.wd * p;                   // optim/base.rs:31-33
-  m = a.b1 * m + a.omb1 * g;                     // adam.rs:330-332
-  v = a.b2 * v + a.omb2 * g * g;                 // adam.rs:335-337
-  const float mh = m / a.bc1;                    // adam.rs:346
-  const float vh = v / a.bc2;                    // adam.rs:347
-  p = p - a.lr * mh / (sqrtf(vh) + a.eps);       // adam.rs:348
+  m = a.b1 * m + a.omb1 * g;                     // adam.rs:144-146
+  v = a.b2 * v + a.omb2 * g * g;                 // adam.rs:149-151
+  const float mh = m / a.bc1;                    // adam.rs:160
+  const float vh = v / a.bc2;                    // adam.rs:161
+  p = p - a.lr * mh / (sqrtf(vh) + a.eps);       // adam.rs:162
 }
 
-// Adam::step, optim/adam.rs:310-353, fused into one pass over p, g, m, v.
+// Adam::step, optim/adam.rs:124-167, fused into one pass over p, g, m, v.
 // One block's kElemsPerBlock elements starting at blk * kElemsPerBlock (shared
 // by adam_kernel and, for tensors in streaming mode, adam_multi_kernel).
 template <bool DECAY, int VEC>
@@ -805,8 +805,8 @@ int numrs_hip_adam_step(numrs_hip_ctx *ctx, float *p, const float *g, float *m, 
   a.wd = wd;
   a.omb1 = 1.0f - b1;
   a.omb2 = 1.0f - b2;
-  a.bc1 = 1.0f - powi_f32(b1, t);  // adam.rs:314
-  a.bc2 = 1.0f - powi_f32(b2, t);  // adam.rs:315
+  a.bc1 = 1.0f - powi_f32(b1, t);  // adam.rs:128
+  a.bc2 = 1.0f - powi_f32(b2, t);  // adam.rs:129
   const unsigned grid = grid_for(n, kElemsPerBlock);
   const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(g) &&
                    numrs_hip::aligned16(m) && numrs_hip::aligned16(v);

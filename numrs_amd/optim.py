@@ -79,7 +79,7 @@ def _handles(params: list[Tensor]):
 
 
 class SGD(Optimizer):
-    """SGD::new(params, lr, momentum, weight_decay) (optim/sgd.rs:90-112)."""
+    """SGD::new(params, lr, momentum, weight_decay) (optim/sgd.rs:47-69)."""
 
     def __init__(self, params, lr: float, momentum: float = 0.0, weight_decay: float = 0.0):
         params = list(params)
@@ -94,12 +94,12 @@ class SGD(Optimizer):
 
     @classmethod
     def simple(cls, params, lr: float) -> "SGD":
-        """SGD::simple (sgd.rs:114-116)."""
+        """SGD::simple (sgd.rs:71-73)."""
         return cls(params, lr, 0.0, 0.0)
 
 
 class Adam(Optimizer):
-    """Adam::new(params, lr, beta1, beta2, eps, weight_decay) (optim/adam.rs:250-285)."""
+    """Adam::new(params, lr, beta1, beta2, eps, weight_decay) (optim/adam.rs:64-99)."""
 
     def __init__(self, params, lr: float, beta1: float = 0.9, beta2: float = 0.999,
                  eps: float = 1e-8, weight_decay: float = 0.0):
@@ -114,7 +114,7 @@ class Adam(Optimizer):
 
     @classmethod
     def default(cls, params, lr: float) -> "Adam":
-        """Adam::default (adam.rs:288-290)."""
+        """Adam::default (adam.rs:102-104)."""
         return cls(params, lr)
 
 

@@ -458,7 +458,7 @@ EXPORT float orc_powi(float a, int b) {
   return recip ? 1.0f / r : r;
 }
 
-/* SGD::step for one parameter, optim/sgd.rs:130-167 with
+/* SGD::step for one parameter, optim/sgd.rs:87-124 with
  * apply_weight_decay (optim/base.rs:26-36):
  *   g' = g + wd*p  (only when wd != 0)
  *   mu != 0: v = mu*v + g'; p -= lr*v      else p -= lr*g'            */
@@ -477,7 +477,7 @@ EXPORT void orc_sgd_step(float *p, const float *g, float *v, int64_t n, float lr
 }
 
 /* Adam::step for one parameter at step t (already incremented),
- * optim/adam.rs:310-353:
+ * optim/adam.rs:124-167:
  *   bc1 = 1 - b1^t, bc2 = 1 - b2^t (powi);  g' = g + wd*p (wd != 0)
  *   m = b1*m + (1-b1)*g';  v = b2*v + ((1-b2)*g')*g'
  *   p -= (lr * (m/bc1)) / (sqrt(v/bc2) + eps)                          */

@@ -6,7 +6,7 @@ MatMul(x, W^T) -> Add(., b); ReLU between; cross_entropy_loss at the end.
 Backward walks those nodes in reverse (tensor.rs:173-215):
 cross_entropy_backward -> add_backward (+ unbroadcast of the bias) ->
 matmul_backward -> transpose_backward -> relu_backward -> ... .  SGD then
-updates every parameter (optim/sgd.rs:130-167).
+updates every parameter (optim/sgd.rs:87-124).
 
 The forward products use the float64 oracle (the reference's forward sgemm is
 MKL, not vendored: its bits are not reproducible); everything in-tree Rust is

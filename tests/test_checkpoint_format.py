@@ -1,7 +1,7 @@
 """numrs's JSON checkpoint format, on the CPU.
 
 The document is serde_json of {model: OnnxModel, training_state: TrainingState}
-(ops/model.rs:544-590, llo/model.rs): the reader is checked on a document laid
+(ops/model.rs:544-588, llo/model.rs): the reader is checked on a document laid
 out field by field as those serde derives write it (the reference ships no
 checkpoint file), and the writer's output is checked for the same fields,
 enum tagging and byte encoding."""

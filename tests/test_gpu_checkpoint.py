@@ -1,6 +1,6 @@
 """Checkpoint and resume of device-resident training state, on the GPU.
 
-A run saved with numrs's checkpoint format (ops/model.rs:544-590) after three
+A run saved with numrs's checkpoint format (ops/model.rs:544-588) after three
 steps and restored into fresh tensors and a fresh optimizer must continue
 bit for bit like the uninterrupted run: parameters, optimizer state slots and
 the step counter all travel through the file."""

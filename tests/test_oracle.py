@@ -72,7 +72,7 @@ def test_kat_sum_mean():
 
 
 def test_kat_add_mul_graph():
-    # tests/autograd_basic.rs:91-146: z = x*y (+x): dx = y (+1), dy = x.
+    # tests/autograd_basic.rs:45-100: z = x*y (+x): dx = y (+1), dy = x.
     dx, dy = O.mul_backward(np.ones(2), np.array([2, 3.0]), np.array([4, 5.0]))
     assert dx.tolist() == [4, 5] and dy.tolist() == [2, 3]
     # complex graph x=2, y=3: add node gives dx 1, mul node gives y=3; accumulated -> 4.
