@@ -231,12 +231,24 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_transpose(self._h, ctypes.byref(h)), h)
 
     def reshape(self, shape) -> "Tensor":
+        """Tensor::reshape (ops.rs:353-369): a new tensor holding a copy of the
+        values in `shape`; its backward reshapes the grad back
+        (reshape_backward, backward.rs:324-330)."""
         sa, nd = _shape_arr(shape)
         h = ctypes.c_void_p()
         return self._out(L.load().numrs_hip_tensor_reshape(self._h, sa, nd, ctypes.byref(h)), h)
 
-    def flatten(self) -> "Tensor":
-        return self.reshape((self.numel(),))
+    def flatten(self, start_dim: int = 0, end_dim: int | None = None) -> "Tensor":
+        """Tensor::flatten(start_dim, end_dim) (ops.rs:336-351, ops/shape/flatten.rs:13-43):
+        dims start_dim..=end_dim merge into one; end_dim is clamped to the last
+        dim.  The backward is flatten_backward (backward.rs:315-321)."""
+        shape = self.shape()
+        nd = len(shape)
+        end = nd - 1 if end_dim is None or end_dim >= nd else int(end_dim)
+        if start_dim > end:
+            raise ValueError(f"flatten: start_dim ({start_dim}) cannot come after end_dim ({end})")
+        flat = int(np.prod(shape[start_dim:end + 1], dtype=np.int64))
+        return self.reshape(tuple(shape[:start_dim]) + (flat,) + tuple(shape[end + 1:]))
 
     def _axis(self, axis: int) -> int:
         nd = len(self.shape())

@@ -252,9 +252,11 @@ int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float
                                 H * S * S, S * S, S * D, dh, S * D, dh))
       return rc;
   if (!dq && !dk) return NUMRS_HIP_OK;
-  void *ws = nullptr;
-  if (int rc = numrs_hip::workspace(ctx, (size_t)(Z * S * S) * sizeof(float), &ws)) return rc;
-  float *dP = static_cast<float *>(ws);
+  // dS lives in a block of its own: the dQ/dK products below may split their
+  // reduction and write partials to the context workspace while reading dS.
+  numrs_hip::TempBlock dSb(ctx);
+  if (int rc = dSb.alloc((size_t)(Z * S * S) * sizeof(float))) return rc;
+  float *dP = dSb.f();
   if (rows_fit(S, dh, D, dout, v, P) && rows_fit(S, dh, D, dout, v, dP) && B * H < 65536) {
     // dS = P * (dP - rowsum(dP * P)) with dP = dO V^T, in one kernel
     if (int rc = launch_rows<1>(ctx, dout, v, P, dP, B, S, H, D, 1.0f)) return rc;

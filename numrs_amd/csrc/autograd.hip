@@ -424,14 +424,22 @@ int bw_layernorm(const T &out, const float *g, Node &n) {
   const int64_t cols = x->shape.back(), rows = x->numel() / cols;
   float *dx = nullptr, *dg = nullptr, *db = nullptr;
   int ax = 0, ag = 0, ab = 0;
+  // One tensor as both gamma and beta: its two gradients add, in a second call.
+  const bool shared_gb = gm->requires_grad && bt->requires_grad && gm->grad == bt->grad;
   if (x->requires_grad)
     if (int rc = grad_target(x, &dx, &ax)) return rc;
   if (gm->requires_grad)
     if (int rc = grad_target(gm, &dg, &ag)) return rc;
-  if (bt->requires_grad)
+  if (bt->requires_grad && !shared_gb)
     if (int rc = grad_target(bt, &db, &ab)) return rc;
+  if (int rc = numrs_hip_layernorm_backward(out->ctx, g, x->data->ptr, gm->data->ptr,
+                                            n.saved[0]->ptr, n.saved[1]->ptr, dx, dg, db, rows,
+                                            cols, ax, ag, ab))
+    return rc;
+  if (!shared_gb) return NUMRS_HIP_OK;
+  if (int rc = grad_target(bt, &db, &ab)) return rc;
   return numrs_hip_layernorm_backward(out->ctx, g, x->data->ptr, gm->data->ptr, n.saved[0]->ptr,
-                                      n.saved[1]->ptr, dx, dg, db, rows, cols, ax, ag, ab);
+                                      n.saved[1]->ptr, nullptr, nullptr, db, rows, cols, 0, 0, 1);
 }
 
 int bw_attention(const T &out, const float *g, Node &n) {
@@ -513,15 +521,25 @@ int bw_lstm(const T &out, const float *g, Node &n) {
   int ax = 0, awi = 0, awh = 0, ab = 0;
   if (x->requires_grad)
     if (int rc = grad_target(x, &dx, &ax)) return rc;
+  // One tensor as both W_ih and W_hh (I == H): its second gradient adds, in a
+  // second call.
+  const bool shared_w = wih->requires_grad && whh->requires_grad && whh->grad == wih->grad;
   if (wih->requires_grad)
     if (int rc = grad_target(wih, &dwi, &awi)) return rc;
-  if (whh->requires_grad && whh->grad != wih->grad)
+  if (whh->requires_grad && !shared_w)
     if (int rc = grad_target(whh, &dwh, &awh)) return rc;
   if (b && (*b)->requires_grad)
     if (int rc = grad_target(*b, &db, &ab)) return rc;
+  if (int rc = numrs_hip_lstm_backward(out->ctx, x->data->ptr, wih->data->ptr, whh->data->ptr,
+                                       nullptr, nullptr, out->data->ptr, n.saved[1]->ptr,
+                                       n.saved[0]->ptr, g, dx, dwi, dwh, db, B, Tn, I, H, ax, awi,
+                                       awh, ab))
+    return rc;
+  if (!shared_w) return NUMRS_HIP_OK;
+  if (int rc = grad_target(whh, &dwh, &awh)) return rc;
   return numrs_hip_lstm_backward(out->ctx, x->data->ptr, wih->data->ptr, whh->data->ptr, nullptr,
-                                 nullptr, out->data->ptr, n.saved[1]->ptr, n.saved[0]->ptr, g, dx,
-                                 dwi, dwh, db, B, Tn, I, H, ax, awi, awh, ab);
+                                 nullptr, out->data->ptr, n.saved[1]->ptr, n.saved[0]->ptr, g,
+                                 nullptr, nullptr, dwh, nullptr, B, Tn, I, H, 0, 0, 1, 0);
 }
 
 int bw_time_slice(const T &out, const float *g, Node &n) {
@@ -740,24 +758,44 @@ int op_ce_labels(const T &x, const int32_t *host_labels, T *out) {
   return NUMRS_HIP_OK;
 }
 
-int op_reshape(const T &a, std::vector<int64_t> shape, T *out) {  // ops.rs:353-369
+// Tensor::reshape (ops.rs:353-369) over ops::reshape's shape rules
+// (ops/shape/reshape.rs:43-100): at most one -1, inferred from the element
+// count; any other negative size, or a count that does not match, is an error.
+int op_reshape(const T &a, std::vector<int64_t> shape, T *out) {
   numrs_hip_ctx *ctx = a->ctx;
-  int64_t n = 1;
-  for (int64_t d : shape) {
-    if (d < 0) return fail(ctx, NUMRS_HIP_E_SHAPE, "reshape: negative dimension");
-    n *= d;
+  const int64_t total = a->numel();
+  int64_t known = 1;
+  int infer = -1;
+  for (size_t i = 0; i < shape.size(); ++i) {
+    const int64_t d = shape[i];
+    if (d == -1) {
+      if (infer >= 0)
+        return fail(ctx, NUMRS_HIP_E_SHAPE, "Can only specify one unknown dimension with -1");
+      infer = (int)i;
+    } else if (d < 0) {
+      return fail(ctx, NUMRS_HIP_E_SHAPE, "Invalid dimension size: %lld", (long long)d);
+    } else {
+      known *= d;
+    }
   }
-  if (n != a->numel()) return fail(ctx, NUMRS_HIP_E_SHAPE, "reshape: element count differs");
+  if (infer >= 0) {
+    if (known == 0)
+      return fail(ctx, NUMRS_HIP_E_SHAPE, "Cannot infer dimension when other dimensions are zero");
+    if (total % known != 0)
+      return fail(ctx, NUMRS_HIP_E_SHAPE, "Cannot reshape array of size %lld", (long long)total);
+    shape[infer] = total / known;
+  } else if (known != total) {
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "Cannot reshape array of size %lld", (long long)total);
+  }
+  const int64_t n = total;
   const bool rec = recording({&a});
-  auto r = std::make_shared<Impl>();
-  r->ctx = ctx;
-  r->shape = std::move(shape);
-  r->data = a->data;  // values are never written in place by the graph: share them
-  r->requires_grad = rec;
-  if (rec) {
-    r->grad = std::make_shared<GradCell>();
-    attach(r, Op::Reshape, {a});
-  }
+  // ops::reshape returns a new Array (ops.rs:356): the result owns a copy, so
+  // an in-place optimizer update of the source leaves it unchanged.
+  T r;
+  if (int rc = make_tensor(ctx, std::move(shape), rec, &r)) return rc;
+  if (int rc = numrs_hip_copy(ctx, r->data->ptr, a->data->ptr, (size_t)n * sizeof(float)))
+    return rc;
+  if (rec) attach(r, Op::Reshape, {a});
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -1312,12 +1350,16 @@ int numrs_hip_tensor_backward(numrs_hip_tensor *t) {
   return backward(t->t);
 }
 
-int numrs_hip_tensor_detach(numrs_hip_tensor *t, numrs_hip_tensor **out) {  // tensor.rs:146-154
+// detach clones the values (tensor.rs:146-154, data.clone()): an optimizer
+// step on the source later does not change the detached tensor.
+int numrs_hip_tensor_detach(numrs_hip_tensor *t, numrs_hip_tensor **out) {
   if (t == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
-  auto r = std::make_shared<Impl>();
-  r->ctx = t->t->ctx;
-  r->shape = t->t->shape;
-  r->data = t->t->data;
+  const T &src = t->t;
+  T r;
+  if (int rc = make_tensor(src->ctx, src->shape, false, &r)) return rc;
+  if (int rc = numrs_hip_copy(src->ctx, r->data->ptr, src->data->ptr,
+                              (size_t)src->numel() * sizeof(float)))
+    return rc;
   return wrap(std::move(r), out);
 }
 

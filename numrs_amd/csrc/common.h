@@ -57,6 +57,25 @@ void block_free(numrs_hip_ctx *ctx, void *p, size_t bytes);
 size_t block_round(size_t bytes);
 void cache_release(numrs_hip_ctx *ctx);
 
+// Temporary device block from the context's block cache, released at scope
+// exit (stream-ordered: a released block is only reused by later work on the
+// same stream).  Unlike the workspace, a block stays valid while the calls
+// made inside its scope use the workspace themselves.
+struct TempBlock {
+  numrs_hip_ctx *ctx;
+  void *p = nullptr;
+  size_t bytes = 0;
+  explicit TempBlock(numrs_hip_ctx *c) : ctx(c) {}
+  TempBlock(const TempBlock &) = delete;
+  TempBlock &operator=(const TempBlock &) = delete;
+  int alloc(size_t b) {
+    bytes = b;
+    return block_alloc(ctx, b, &p);
+  }
+  float *f() const { return static_cast<float *>(p); }
+  ~TempBlock() { block_free(ctx, p, bytes); }
+};
+
 // Checks the launch that was just enqueued.
 int check_launch(numrs_hip_ctx *ctx, const char *what);
 

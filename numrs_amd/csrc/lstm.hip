@@ -315,20 +315,7 @@ int check(numrs_hip_ctx *ctx, int64_t B, int64_t T, int64_t I, int64_t H) {
   return NUMRS_HIP_OK;
 }
 
-// Temporary device block from the context's block cache (stream-ordered:
-// released blocks are only reused by later work on the same stream).
-struct TempBlock {
-  numrs_hip_ctx *ctx;
-  void *p = nullptr;
-  size_t bytes = 0;
-  explicit TempBlock(numrs_hip_ctx *c) : ctx(c) {}
-  int alloc(size_t b) {
-    bytes = b;
-    return numrs_hip::block_alloc(ctx, b, &p);
-  }
-  float *f() const { return static_cast<float *>(p); }
-  ~TempBlock() { numrs_hip::block_free(ctx, p, bytes); }
-};
+using numrs_hip::TempBlock;
 
 // y[b, :] = x[b, t, :] for x [B, T, D] (the last-step head input), and its
 // backward dx[b, t, :] (+)= g[b, :] with zeros elsewhere when not accumulating.

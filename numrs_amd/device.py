@@ -24,14 +24,15 @@ class HipError(RuntimeError):
 class DeviceArray:
     """A device allocation holding a contiguous fp32/int32 array."""
 
-    __slots__ = ("ctx", "ptr", "shape", "dtype", "_owned")
+    __slots__ = ("ctx", "ptr", "shape", "dtype", "_owned", "_base")
 
-    def __init__(self, ctx: "Context", ptr: int, shape, dtype=np.float32, owned=True):
+    def __init__(self, ctx: "Context", ptr: int, shape, dtype=np.float32, owned=True, base=None):
         self.ctx = ctx
         self.ptr = ptr
         self.shape = tuple(int(s) for s in shape)
         self.dtype = np.dtype(dtype)
         self._owned = owned
+        self._base = base  # the allocation a view keeps alive
 
     @property
     def size(self) -> int:
@@ -62,9 +63,14 @@ class DeviceArray:
         return self
 
     def view(self, offset_elems: int, shape) -> "DeviceArray":
-        """A non-owning view starting `offset_elems` elements in."""
+        """A view starting `offset_elems` elements in; it holds a reference to
+        the owning array, so the allocation lives as long as any view of it."""
+        n = int(np.prod(tuple(int(s) for s in shape), dtype=np.int64))
+        if offset_elems < 0 or offset_elems + n > self.size:
+            raise ValueError(f"view of {n} elements at {offset_elems} outside {self.size}")
+        base = self if self._owned else self._base
         return DeviceArray(self.ctx, self.ptr + offset_elems * self.dtype.itemsize, shape,
-                           self.dtype, owned=False)
+                           self.dtype, owned=False, base=base)
 
     def free(self) -> None:
         if self._owned and self.ptr and self.ctx.handle:

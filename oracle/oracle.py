@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py, always as the checker.  The product library never
-imports this module.  Every function forwards to the C restatement, which cites
-the numrs reference file:line it follows.
+imports this module.  Every arithmetic function forwards to the C restatement,
+which cites the numrs reference file:line it follows; the shape-only functions
+(reshape / flatten) are restated here in Python with their citations.
 """
 from __future__ import annotations
 
@@ -150,6 +151,55 @@ def transpose(x) -> np.ndarray:
 def accumulate(dst: np.ndarray, src) -> None:
     src = _f(src)
     lib().orc_accumulate(_p(dst), dst.size, _p(src), src.size)
+
+
+# --- shape ops (no arithmetic: restated here in Python) ------------------------
+
+def reshape_shape(total: int, new_shape) -> tuple:
+    """ops::reshape's shape rules (ops/shape/reshape.rs:43-100): at most one
+    -1, inferred as total / (product of the others); any other negative size,
+    or a product that differs from `total`, raises ValueError."""
+    infer, known = None, 1
+    for i, d in enumerate(new_shape):
+        d = int(d)
+        if d == -1:
+            if infer is not None:
+                raise ValueError("Can only specify one unknown dimension with -1")
+            infer = i
+        elif d < 0:
+            raise ValueError(f"Invalid dimension size: {d}")
+        else:
+            known *= d
+    out = [int(d) for d in new_shape]
+    if infer is not None:
+        if known == 0:
+            raise ValueError("Cannot infer dimension when other dimensions are zero")
+        if total % known:
+            raise ValueError(f"Cannot reshape array of size {total}")
+        out[infer] = total // known
+    elif known != total:
+        raise ValueError(f"Cannot reshape array of size {total}")
+    return tuple(out)
+
+
+def flatten_shape(shape, start_dim: int, end_dim: int) -> tuple:
+    """ops::flatten's output shape (ops/shape/flatten.rs:13-43): end_dim is
+    clamped to the last dim, dims start_dim..=end_dim merge into one."""
+    nd = len(shape)
+    end = nd - 1 if end_dim >= nd else end_dim
+    if start_dim > end:
+        raise ValueError(f"flatten: start_dim ({start_dim}) cannot come after end_dim ({end})")
+    flat = 1
+    for i in range(start_dim, end + 1):
+        flat *= int(shape[i])
+    return tuple(int(s) for s in shape[:start_dim]) + (flat,) + tuple(int(s) for s in shape[end + 1:])
+
+
+def reshape_backward(g, input_shape) -> np.ndarray:
+    """reshape_backward / flatten_backward (backward.rs:315-330): the incoming
+    grad, in row-major order, reshaped to the input's shape (a copy)."""
+    g = _f(g)
+    return g.reshape(reshape_shape(g.size, input_shape)).copy()
 
 
 # --- matmul -----------------------------------------------------------------

@@ -19,8 +19,8 @@ def lstm_layer(x, w_ih, w_hh, b):
     """x [B, T, I] float64 -> (h_seq, cache)."""
     B, T, _ = x.shape
     H = w_hh.shape[1]
-    h = np.zeros((B, H))
-    c = np.zeros((B, H))
+    h = np.zeros((B, H), x.dtype)
+    c = np.zeros((B, H), x.dtype)
     hs, cs, acts = [], [], []
     for t in range(T):
         z = x[:, t] @ w_ih.T + h @ w_hh.T + b
@@ -38,14 +38,15 @@ def lstm_layer_backward(x, w_ih, w_hh, h_seq, cache, dh_seq):
     H = w_hh.shape[1]
     c_seq, acts = cache
     dx = np.zeros_like(x)
-    dwi, dwh, db = np.zeros_like(w_ih), np.zeros_like(w_hh), np.zeros(4 * H)
-    dh_next = np.zeros((B, H))
-    dc_next = np.zeros((B, H))
+    dt = x.dtype
+    dwi, dwh, db = np.zeros_like(w_ih), np.zeros_like(w_hh), np.zeros(4 * H, dt)
+    dh_next = np.zeros((B, H), dt)
+    dc_next = np.zeros((B, H), dt)
     for t in range(T - 1, -1, -1):
         i, f, g, o = acts[t]
         c = c_seq[:, t]
-        cp = c_seq[:, t - 1] if t > 0 else np.zeros((B, H))
-        hp = h_seq[:, t - 1] if t > 0 else np.zeros((B, H))
+        cp = c_seq[:, t - 1] if t > 0 else np.zeros((B, H), dt)
+        hp = h_seq[:, t - 1] if t > 0 else np.zeros((B, H), dt)
         dh = dh_seq[:, t] + dh_next
         tc = np.tanh(c)
         dc = dh * o * (1 - tc ** 2) + dc_next
@@ -60,24 +61,28 @@ def lstm_layer_backward(x, w_ih, w_hh, h_seq, cache, dh_seq):
     return dx, dwi, dwh, db
 
 
-def forecaster(layers, head_w, head_b, x, target):
-    """Loss and float64 gradients of every parameter (and of x)."""
-    h = x.astype(np.float64)
+def forecaster(layers, head_w, head_b, x, target, dtype=np.float64):
+    """Loss and gradients of every parameter (and of x), computed in `dtype`:
+    float64 is the oracle; float32 runs the same BPTT in fp32 on the CPU, the
+    error scale an fp32 CPU implementation reaches."""
+    h = x.astype(dtype)
     ins, outs, caches = [], [], []
     for l in layers:
-        w = {k: v.astype(np.float64) for k, v in l.items()}
+        w = {k: v.astype(dtype) for k, v in l.items()}
         ins.append(h)
         h, cache = lstm_layer(h, w["w_ih"], w["w_hh"], w["b"])
         outs.append(h)
         caches.append((w, cache))
     last = h[:, -1]
-    y = last @ head_w.astype(np.float64).T + head_b
+    hw = head_w.astype(dtype)
+    y = last @ hw.T + head_b.astype(dtype)
     n = y.size
+    target = target.astype(dtype)
     loss = ((y - target) ** 2).sum() / n
     dy = 2 * (y - target) / n
     grads = {"head_w": dy.T @ last, "head_b": dy.sum(0)}
     dh = np.zeros_like(h)
-    dh[:, -1] = dy @ head_w.astype(np.float64)
+    dh[:, -1] = dy @ hw
     for li in range(len(layers) - 1, -1, -1):
         w, cache = caches[li]
         dxl, dwi, dwh, db = lstm_layer_backward(ins[li], w["w_ih"], w["w_hh"], outs[li], cache, dh)

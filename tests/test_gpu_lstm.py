@@ -6,13 +6,9 @@ import pytest
 import numrs_amd as nr
 from numrs_amd import Tensor, nn
 from tests import lstm_oracle as LO
+from tests.conftest import assert_chain
 
 pytestmark = pytest.mark.gpu
-
-
-def _norm_rel(got, ref):
-    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    return np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
 
 
 @pytest.mark.parametrize("dims", [dict(B=3, T=6, I=4, H=5), dict(B=8, T=20, I=16, H=64),
@@ -31,17 +27,22 @@ def test_lstm_forecaster_matches_oracle(hip_ctx, dims):
     loss = y.mse_loss(Tensor.new(target, False))
     loss.backward()
     ref_loss, g, ref_y = LO.forecaster(layers, hw, hb, x, target)
-    assert _norm_rel(y.values(), ref_y) < 1e-5
+    # The same BPTT in fp32 on the CPU: the error scale an fp32 CPU
+    # implementation reaches, which the GPU must not exceed.
+    _, g32, y32 = LO.forecaster(layers, hw, hb, x, target, dtype=np.float32)
     assert abs(loss.item() - ref_loss) <= 1e-5 * abs(ref_loss) + 1e-7
+    # At the BASELINE size the GPU must be at least as close to float64 as the
+    # fp32 CPU chain.  The other shapes have tensors of 5..100 elements (y is
+    # [B, 1]), where the mean of two independent fp32 rounding patterns is
+    # noise: there the GPU may be up to 2x the CPU chain's error.
+    base = dims["B"] == 64 and dims["T"] == 128
+    fac = dict(mean_factor=1.0, max_factor=1.5) if base else dict(mean_factor=2.0, max_factor=3.0)
+    assert_chain(y.values(), ref_y, y32, what="y", **fac)
     got = {"head_w": model.head.weight, "head_b": model.head.bias, "x": xt}
     for li, layer in enumerate(model.layers):
         got[f"w_ih{li}"], got[f"w_hh{li}"], got[f"b{li}"] = layer.w_ih, layer.w_hh, layer.bias
     for name, tensor in got.items():
-        gg, rr = tensor.gradient(), g[name]
-        # fp32 BPTT through 2 x T steps against float64: norm-wise relative error
-        # and every element within 1e-3 of the tensor's largest gradient.
-        assert _norm_rel(gg, rr) < 5e-4, (name, _norm_rel(gg, rr))
-        assert np.abs(gg - rr).max() <= 1e-3 * np.abs(rr).max(), name
+        assert_chain(tensor.gradient(), g[name], g32[name], what=name, **fac)
 
 
 def test_time_slice_grad(hip_ctx):

@@ -6,9 +6,10 @@ float64-accumulated oracle for reductions, whose summation order differs from
 the reference's.  Matmul gradients (length-K fp32 contractions) add the fp32
 rounding allowance 4*2^-24*K that numrs's own fp32 loop also needs, and must
 be on average at least as close to the exact gradient as that loop is
-(tests/conftest.py::assert_contraction).  Full BASELINE sizes are checked
-through sampled rows plus size-independent identities (checksums of
-checksums, exact power-of-two linearity).
+(tests/conftest.py::assert_contraction).  At the full BASELINE matmul sizes
+every output element is compared with a float64 host product, the fp32 loop
+runs on sampled rows for the aggregate bar, and size-independent identities
+(checksums of checksums, exact power-of-two linearity) are checked besides.
 """
 import sys
 
@@ -106,20 +107,35 @@ def test_matmul_backward_baseline_sizes(hip_ctx, rng, M, K, N):
     dA, dB = c.empty((M, K)), c.empty((K, N))
     c.matmul_backward(dCd, Ad, Bd, dA, dB)
     ga, gb = dA.numpy(), dB.numpy()
-    # Sampled rows against the float64 oracle: first/last rows of tiles and XCD groups.
-    # fp32 loops of numrs (backward.rs:123-146) on the same rows, for the aggregate check.
+    # Every element of dA and dB against float64 host products (BLAS in
+    # float64: exact to ~1e-13 here), under the per-element contraction bar.
+    d64 = dC.astype(np.float64)
+    ra = d64 @ B.astype(np.float64).T
+    assert_contraction(ga, ra, N, what="dA (every element)")
+    rb = A.astype(np.float64).T @ d64
+    assert_contraction(gb, rb, M, what="dB (every element)")
+    # The oracle's float64-accumulated rows (rounded once to fp32) agree with
+    # the host product on sampled rows, and numrs's own fp32 loops
+    # (backward.rs:123-146) on those rows give the aggregate bar: the GPU
+    # result is on average closer to the exact gradient.
+    def rounded_once(o, r):
+        return (np.abs(o - r) <= 2.0 ** -23 * np.abs(r) + 1e-30).all()
+
     for r0 in (0, 127, 128, 1023, M - 2):
         rows = (r0, r0 + 2)
-        ra, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=rows)
+        o64, _ = O.matmul_backward(dC, A, B, need_b=False, f64=True, rows_a=rows)
+        assert rounded_once(o64[r0:r0 + 2], ra[r0:r0 + 2]), f"oracle dA rows {r0}"
         r32, _ = O.matmul_backward(dC, A, B, need_b=False, rows_a=rows)
         assert_contraction(ga[r0:r0 + 2], ra[r0:r0 + 2], N, ref32=r32[r0:r0 + 2],
                            what=f"dA rows {r0}")
     for r0 in (0, 129, K // 2, K - 2):
         rows = (r0, r0 + 2)
-        _, rb = O.matmul_backward(dC, A, B, need_a=False, f64=True, rows_b=rows)
+        _, o64 = O.matmul_backward(dC, A, B, need_a=False, f64=True, rows_b=rows)
+        assert rounded_once(o64[r0:r0 + 2], rb[r0:r0 + 2]), f"oracle dB rows {r0}"
         _, r32 = O.matmul_backward(dC, A, B, need_a=False, rows_b=rows)
         assert_contraction(gb[r0:r0 + 2], rb[r0:r0 + 2], M, ref32=r32[r0:r0 + 2],
                            what=f"dB rows {r0}")
+    del ra, rb, d64
     # Whole-output identities.
     sa, sb = _checksums(dC, A, B)
     assert abs(ga.astype(np.float64).sum() - sa) <= 1e-4 * np.abs(ga).sum()

@@ -8,7 +8,7 @@ import pytest
 import numrs_amd as nr
 from numrs_amd import Tensor, nn
 from tests import transformer_oracle as TO
-from tests.conftest import assert_contraction, rand
+from tests.conftest import assert_chain, assert_contraction, rand
 
 pytestmark = pytest.mark.gpu
 
@@ -85,11 +85,6 @@ def test_gemm_two_level_batch(hip_ctx):
     assert_contraction(out.numpy().reshape(B, H, S, S), ref, dh)
 
 
-def _norm_rel(got, ref):
-    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    return np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
-
-
 def _run_block(dims_full, seed):
     w, x, t, dims = TO.make_c4(seed=seed, **dims_full)
     B, S, H = dims
@@ -109,16 +104,15 @@ def test_c4_block_matches_oracle(hip_ctx, dims_full):
     nr.set_default_context(hip_ctx)
     w, x, t, dims, blk, xt, loss, y = _run_block(dims_full, seed=4)
     ref_loss, g, ref_y = TO.block(w, x, t, dims)
+    # The same chain in fp32 on the CPU: the error scale an fp32 CPU
+    # implementation reaches, which the GPU must not exceed.
+    _, g32, y32 = TO.block(w, x, t, dims, dtype=np.float32)
     assert abs(loss.item() - ref_loss) <= 1e-5 * abs(ref_loss)
-    assert _norm_rel(y.values(), ref_y) < 1e-5
+    assert_chain(y.values(), ref_y, y32, what="y")
     got = {"wq": blk.attn.q.weight, "wk": blk.attn.k.weight, "wv": blk.attn.v.weight,
            "wo": blk.attn.o.weight, "w1": blk.ff1.weight, "w2": blk.ff2.weight,
            "ln1_gamma": blk.ln1.gamma, "ln1_beta": blk.ln1.beta, "ln2_gamma": blk.ln2.gamma,
            "ln2_beta": blk.ln2.beta, "bq": blk.attn.q.bias, "bo": blk.attn.o.bias,
            "c1": blk.ff1.bias, "c2": blk.ff2.bias, "x": xt}
     for name, tensor in got.items():
-        gg, rr = tensor.gradient(), g[name]
-        # fp32 through ~10 dependent contractions (K up to 2048) against float64:
-        # norm-wise relative error, and every element within 1e-3 of the max.
-        assert _norm_rel(gg, rr) < 2e-4, (name, _norm_rel(gg, rr))
-        assert np.abs(gg - rr).max() <= 1e-3 * np.abs(rr).max(), name
+        assert_chain(tensor.gradient(), g[name], g32[name], what=name)

@@ -340,3 +340,48 @@ def test_layernorm_backward_finite_difference(rng):
                  abs_tol=2e-4, rel_tol=2e-3, what="dbeta")
     y, mean, rstd = O.layernorm_fwd(x, gamma, beta, eps)
     assert_close(y, fwd(x64, gm64, bt64), what="ln fwd")
+
+
+# --- reshape / flatten (a22) ---------------------------------------------------
+
+def test_kat_reshape_shapes():
+    # ops/shape/reshape.rs:115-195
+    assert O.reshape_shape(6, [3, 2]) == (3, 2)                     # test_reshape_basic
+    assert O.reshape_shape(8, [2, 2, 2]) == (2, 2, 2)               # test_reshape_3d
+    assert O.reshape_shape(6, [-1, 3]) == (2, 3)                    # test_reshape_infer_dimension
+    assert O.reshape_shape(4, [-1, 2]) == (2, 2)                    # ..._infer_first_dimension
+    assert O.reshape_shape(4, [-1]) == (4,)                         # test_reshape_flatten
+    with pytest.raises(ValueError):
+        O.reshape_shape(4, [2, 3])                                  # test_reshape_invalid_size
+    with pytest.raises(ValueError):
+        O.reshape_shape(4, [-1, -1])                                # test_reshape_multiple_infer
+    assert O.reshape_shape(1, [1, 1, 1]) == (1, 1, 1)               # test_reshape_to_scalar_like
+    assert O.reshape_shape(4, [2, 2]) == (2, 2)                     # test_reshape_identity
+    with pytest.raises(ValueError):
+        O.reshape_shape(0, [0, -1])     # "Cannot infer dimension when other dimensions are zero"
+    with pytest.raises(ValueError):
+        O.reshape_shape(6, [-2, 3])     # "Invalid dimension size"
+
+
+def test_flatten_shapes():
+    # ops/shape/flatten.rs:13-43: merge start..=end, end clamped to the last dim
+    assert O.flatten_shape((2, 3, 4), 1, 2) == (2, 12)
+    assert O.flatten_shape((2, 3, 4), 0, 1) == (6, 4)
+    assert O.flatten_shape((2, 3, 4), 0, 99) == (24,)
+    assert O.flatten_shape((2, 3, 4), 1, 1) == (2, 3, 4)
+    with pytest.raises(ValueError):
+        O.flatten_shape((2, 3, 4), 2, 1)
+
+
+def test_reshape_backward_is_the_row_major_inverse(rng):
+    # backward.rs:315-330: the grad keeps row-major order.  Reshaping forward
+    # and then backward is the identity, and an index permutation of the
+    # grad (a transposed operand) is caught on non-square shapes.
+    g = rand(rng, (3, 8))
+    dx = O.reshape_backward(g, (4, 6))
+    assert dx.shape == (4, 6)
+    assert np.array_equal(dx.ravel(), g.ravel())
+    assert np.array_equal(O.reshape_backward(dx, (3, 8)), g)
+    assert not np.array_equal(dx, g.T.reshape(4, 6))
+    dx[0, 0] += 1.0                                 # a copy, not a view
+    assert dx.ravel()[0] != g.ravel()[0]

@@ -71,12 +71,14 @@ def attention_backward(dA, cache, B, S, H):
     return _merge(dQ, B, S), _merge(dK, B, S), _merge(dV, B, S)
 
 
-def block(w, x, t, dims):
-    """Returns (loss, grads dict, output y) in float64."""
+def block(w, x, t, dims, dtype=np.float64):
+    """Returns (loss, grads dict, output y), computed in `dtype`: float64 is
+    the oracle; float32 runs the same chain in fp32 on the CPU (BLAS sgemm
+    products), the error scale an fp32 CPU implementation reaches."""
     B, S, H = dims
-    f = {k: v.astype(np.float64) for k, v in w.items()}
-    x = x.astype(np.float64)
-    t = t.astype(np.float64)
+    f = {k: v.astype(dtype) for k, v in w.items()}
+    x = x.astype(dtype)
+    t = t.astype(dtype)
     xh1, rs1 = _ln(x)
     ln1 = xh1  # gamma 1, beta 0
     q, k, v = ln1 @ f["wq"].T, ln1 @ f["wk"].T, ln1 @ f["wv"].T
