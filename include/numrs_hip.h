@@ -280,6 +280,19 @@ int numrs_hip_broadcast_axis(numrs_hip_ctx *ctx, const float *g, int64_t outer, 
 int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx,
                                  float *db, int64_t rows, int64_t cols, int mode, int accumulate);
 
+/* No counterpart in the reference.  numrs_hip_relu_bias_backward for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): same arguments and
+ * results, but the column-sum partials live in a static per-GPU array of
+ * 2^20 floats (4 MiB) instead of the context workspace, and the call makes no
+ * hipMalloc / hipFree or other allocating call.  A shape whose partials
+ * exceed the array returns NUMRS_HIP_E_INVALID (on a 256-CU MI355X: more
+ * than 2^20 columns with db requested).  Calls that overlap on one GPU (two
+ * contexts) race on the array. */
+int numrs_hip_relu_bias_backward_noalloc(numrs_hip_ctx *ctx, const float *g, const float *z,
+                                         float *dx, float *db, int64_t rows, int64_t cols,
+                                         int mode, int accumulate);
+
 /* ---------------------------------------------------------------------- */
 /* Elementwise backward                                                    */
 /* ---------------------------------------------------------------------- */

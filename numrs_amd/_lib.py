@@ -48,6 +48,7 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "numrs_hip_sum_to_shape": (_i, [_vp, _vp, _i64p, _i, _vp, _i64p, _i, _i, _i]),
     "numrs_hip_relu_bias_backward": (_i, [_vp] * 5 + [_i64, _i64, _i, _i]),
+    "numrs_hip_relu_bias_backward_noalloc": (_i, [_vp] * 5 + [_i64, _i64, _i, _i]),
     "numrs_hip_unary_backward": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _f, _i]),
     "numrs_hip_binary_backward": (_i, [_vp, _i] + [_vp] * 5 + [_i64, _i]),
     "numrs_hip_fill_grad": (_i, [_vp, _vp, _vp, _i64, _i, _i]),

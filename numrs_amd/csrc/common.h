@@ -36,6 +36,10 @@ struct numrs_hip_ctx {
   int64_t live_blocks = 0;
   bool destroyed = false;
   int unbroadcast_mode = NUMRS_HIP_UNBROADCAST_CORRECT;
+  // Device address of reduce.hip's static partials array on this context's
+  // device, resolved at creation (the allocation-free entry point uses it).
+  float *noalloc_partials = nullptr;
+  int noalloc_status = 0;
   char last_error[512] = {0};
 };
 
@@ -78,6 +82,11 @@ struct TempBlock {
 
 // Checks the launch that was just enqueued.
 int check_launch(numrs_hip_ctx *ctx, const char *what);
+
+// Resolves, with the context's device current, the device address of the
+// static partials array of the allocation-free column reduction (reduce.hip)
+// into ctx->noalloc_partials; once per device, later contexts reuse it.
+int noalloc_init(numrs_hip_ctx *ctx);
 
 // Vector operations of the L-BFGS two-loop recursion (optim/lbfgs.rs),
 // out[i] = f(a[i], b[i], s) in the reference's operation order.

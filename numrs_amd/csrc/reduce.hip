@@ -20,6 +20,8 @@
 // on scheduling.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -599,23 +601,37 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
-int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, float *out,
-              int64_t rows, int64_t cols, int mode, int acc_dx, int acc_out, int64_t out_n) {
+// Row classes (pass-1 blocks per strip) of a column reduction; its partials
+// take chunks * cols floats.
+int64_t colreduce_chunks(const numrs_hip_ctx *ctx, int64_t rows, int64_t cols, bool relu) {
   const int64_t strips = (cols + kColsPerBlock - 1) / kColsPerBlock;
   const int64_t bands = (rows + kBandRows - 1) / kBandRows;
-  if (strips > 0x7fffffff)
-    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "column reduction too large");
   // About one block per CU in all for the fused ReLU kernel (three streams):
   // more blocks in flight scatter the reads over more HBM pages and measured
   // slower.  A plain column sum reads one stream and needs two blocks per CU
   // to keep enough loads in flight.
   const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-  const int64_t per_cu = z == nullptr ? 2 : 1;
-  int64_t chunks = (per_cu * cus + strips - 1) / strips;
-  chunks = std::max<int64_t>(1, std::min<int64_t>({chunks, bands, 65535}));
-  void *ws = nullptr;
-  if (int rc = numrs_hip::workspace(ctx, (size_t)(chunks * cols) * sizeof(float), &ws)) return rc;
-  float *partial = static_cast<float *>(ws);
+  const int64_t per_cu = relu ? 1 : 2;
+  const int64_t chunks = (per_cu * cus + strips - 1) / strips;
+  return std::max<int64_t>(1, std::min<int64_t>({chunks, bands, 65535}));
+}
+
+// `partials`: a buffer of at least colreduce_chunks(...) * cols floats, or
+// nullptr for the context's workspace.
+int colreduce(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx, float *out,
+              int64_t rows, int64_t cols, int mode, int acc_dx, int acc_out, int64_t out_n,
+              float *partials = nullptr) {
+  const int64_t strips = (cols + kColsPerBlock - 1) / kColsPerBlock;
+  if (strips > 0x7fffffff)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "column reduction too large");
+  const int64_t chunks = colreduce_chunks(ctx, rows, cols, z != nullptr);
+  float *partial = partials;
+  if (partial == nullptr) {
+    void *ws = nullptr;
+    if (int rc = numrs_hip::workspace(ctx, (size_t)(chunks * cols) * sizeof(float), &ws))
+      return rc;
+    partial = static_cast<float *>(ws);
+  }
   const bool vec = numrs_hip::aligned16(g) && (z == nullptr || numrs_hip::aligned16(z)) &&
                    (dx == nullptr || numrs_hip::aligned16(dx)) && (cols & 3) == 0;
   dim3 grid((unsigned)strips, (unsigned)chunks);
@@ -654,15 +670,52 @@ int full_sum(numrs_hip_ctx *ctx, const float *g, int64_t n, float *out, int64_t 
   return numrs_hip::check_launch(ctx, "full_reduce_finalize");
 }
 
+// Shared body of numrs_hip_relu_bias_backward (partials == nullptr: the
+// context's workspace) and of its allocation-free variant.
+int relu_bias_backward(numrs_hip_ctx *ctx, const char *who, const float *g, const float *z,
+                       float *dx, float *db, int64_t rows, int64_t cols, int mode, int accumulate,
+                       float *partials);
+
 }  // namespace
 
-extern "C" {
+// Pass-1 partials of the allocation-free fused ReLU + bias backward: a
+// file-scope device array, one copy per GPU, held until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host the name is
+// a stand-in, not a device address); it uses the address that noalloc_init
+// resolved for the context's device.
+constexpr int64_t kNoAllocPartials = int64_t(1) << 20;  // floats: 4 MiB per GPU
+static __device__ __align__(256) float scratch[kNoAllocPartials];
 
-int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx,
-                                 float *db, int64_t rows, int64_t cols, int mode,
-                                 int accumulate) {
-  NRS_CHECK_CTX(ctx);
-  const char *who = "numrs_hip_relu_bias_backward";
+namespace numrs_hip {
+
+int noalloc_init(numrs_hip_ctx *ctx) {
+  static std::mutex mu;
+  static std::unordered_map<int, float *> by_device;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = by_device.find(ctx->device);
+  if (it == by_device.end()) {
+    // numrs_hip_create has made ctx->device current.  `::scratch` is the
+    // array; inside this namespace a bare `scratch` is the workspace function.
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return fail(ctx, NUMRS_HIP_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s",
+                  ctx->device, hipGetErrorString(e));
+    }
+    it = by_device.emplace(ctx->device, static_cast<float *>(p)).first;
+  }
+  ctx->noalloc_partials = it->second;
+  return NUMRS_HIP_OK;
+}
+
+}  // namespace numrs_hip
+
+namespace {
+
+int relu_bias_backward(numrs_hip_ctx *ctx, const char *who, const float *g, const float *z,
+                       float *dx, float *db, int64_t rows, int64_t cols, int mode, int accumulate,
+                       float *partials) {
   if (rows < 0 || cols < 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative size", who);
   if (mode != NUMRS_HIP_UNBROADCAST_CORRECT && mode != NUMRS_HIP_UNBROADCAST_REFERENCE)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: mode %d", who, mode);
@@ -686,7 +739,45 @@ int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float
                                                                                    accumulate);
     return numrs_hip::check_launch(ctx, "relu_mask_kernel");
   }
-  return colreduce(ctx, g, z, dx, db, rows, cols, mode, accumulate, accumulate, cols);
+  return colreduce(ctx, g, z, dx, db, rows, cols, mode, accumulate, accumulate, cols, partials);
+}
+
+}  // namespace
+
+extern "C" {
+
+int numrs_hip_relu_bias_backward(numrs_hip_ctx *ctx, const float *g, const float *z, float *dx,
+                                 float *db, int64_t rows, int64_t cols, int mode,
+                                 int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  return relu_bias_backward(ctx, "numrs_hip_relu_bias_backward", g, z, dx, db, rows, cols, mode,
+                            accumulate, nullptr);
+}
+
+// The same computation with the pass-1 partials in the static `scratch`
+// array: no hipMalloc, hipFree or other allocating call.  Calls that overlap
+// on one GPU (two contexts' streams) race on the array; every call writes
+// all the partials it reads, so nothing needs clearing between calls.
+int numrs_hip_relu_bias_backward_noalloc(numrs_hip_ctx *ctx, const float *g, const float *z,
+                                         float *dx, float *db, int64_t rows, int64_t cols,
+                                         int mode, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_relu_bias_backward_noalloc";
+  if (ctx->noalloc_partials == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_HIP,
+                           "%s: the partials array has no device address (status %d at create)",
+                           who, ctx->noalloc_status);
+  if (db != nullptr && rows > 0 && cols > 0) {
+    const int64_t need = colreduce_chunks(ctx, rows, cols, true) * cols;
+    if (need > kNoAllocPartials)
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID,
+                             "%s: %lld x %lld needs %lld partial floats, above the %lld of the "
+                             "allocation-free path",
+                             who, (long long)rows, (long long)cols, (long long)need,
+                             (long long)kNoAllocPartials);
+  }
+  return relu_bias_backward(ctx, who, g, z, dx, db, rows, cols, mode, accumulate,
+                            ctx->noalloc_partials);
 }
 
 int numrs_hip_layernorm_backward(numrs_hip_ctx *ctx, const float *g, const float *x,

@@ -184,6 +184,9 @@ int numrs_hip_create(int device, numrs_hip_ctx **out) {
       return NUMRS_HIP_E_HIP;
     }
   }
+  // A failure here only disables the allocation-free entry point, which then
+  // reports it; every other entry point works without the array.
+  ctx->noalloc_status = numrs_hip::noalloc_init(ctx);
   *out = ctx;
   return NUMRS_HIP_OK;
 }
