@@ -17,8 +17,11 @@ several copies of the workload's buffers, enough that each launch's operands
 were pushed out of the 256 MB Infinity Cache since that copy's last use: the
 figures are HBM-resident rates.  Each entry also reports the same launch
 repeated on one set of buffers (`resident_*`), which a cache-sized working
-set serves partly from that cache.  The default 100 untimed warmup launches
-let the device settle first (the early launches of a run are slower).
+set serves partly from that cache.  Before any measurement an untimed,
+time-based device warm-up (--device-warm-ms, default 300 ms of 2048^3
+launches) lets the device settle, since the early launches of a run are
+slower; its length is reported as `warm_ms` in the JSON line.  The --warmup
+launches of each workload follow it, untimed as well.
 """
 from __future__ import annotations
 
@@ -68,6 +71,41 @@ class QueueAhead:
 
 _AHEAD = None
 
+# Untimed, time-based warm-up of every timed region (--warm-ms).  The first
+# launches after the GPU has idled are slower: a trace of the default run
+# shows the 2048^3 launch at 291 us (1st), 308 (10th), 280 (30th), 258 (60th),
+# 246 (90th) and 240-243 us after 150 launches, and the ramp starts over after
+# the second or so of host work (buffer uploads) between two regions.  So
+# each region first runs its own launch for WARM_MS of wall time, after its
+# --warmup launches; the counts are reported in the JSON line.
+WARM_MS = 50.0
+_WARM_LAUNCHES: dict = {}
+
+
+def host_cpu() -> dict:
+    """The host CPU the CPU baselines run on: model name, logical CPUs, and
+    the CPUs this process may use."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"model": model, "logical_cpus": os.cpu_count(), "usable_cpus": usable}
+
+
+def cpu_threads() -> int:
+    """Threads for an all-cores CPU baseline: the usable CPUs, at most 16
+    (one GPU's share of the box)."""
+    return max(1, min(16, host_cpu()["usable_cpus"]))
+
 # MI355X's Infinity Cache (MALL) holds 256 MB in front of HBM.  A kernel
 # relaunched on the same buffers whose bytes fit in it reads them back from
 # that cache, not from HBM (a 201 MB read-2-write-1 stream measured 0.98 of
@@ -97,19 +135,38 @@ class Rot:
         return self.copies[i % len(self.copies)]
 
 
-def time_launches(ctx, launch, steps: int, warmup: int):
-    """Calls launch(i) for i = 0, 1, ... : warmup times, then `steps` times
-    back to back inside one timed region (HIP events in slots 0/1 on the
-    context's stream, the stream the kernels run on), queued behind
+def warm_for(ctx, launch, first: int, ms: float) -> int:
+    """Untimed launches launch(first), launch(first + 1), ... in batches of 32,
+    each batch waited for, until `ms` of wall time have passed; returns how
+    many were made."""
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(32):
+            launch(first + n)
+            n += 1
+        ctx.sync()
+    return n
+
+
+def time_launches(ctx, launch, steps: int, warmup: int, tag: str = ""):
+    """Calls launch(i) for i = 0, 1, ... : warmup times, then for WARM_MS of
+    wall time (untimed; the count is kept under `tag` for the JSON line), then
+    `steps` times back to back inside one timed region (HIP events in slots
+    0/1 on the context's stream, the stream the kernels run on), queued behind
     QueueAhead's work.  Returns (total ms of the region, mean ms per
     launch)."""
     for i in range(warmup):
         launch(i)
+    nw = warm_for(ctx, launch, warmup, WARM_MS)
+    if tag:
+        _WARM_LAUNCHES.setdefault(tag, []).append(warmup + nw)
+    first = warmup + nw
     ctx.sync()
     if _AHEAD is not None:
         _AHEAD()
     ctx.timer_record(0)
-    for i in range(warmup, warmup + steps):
+    for i in range(first, first + steps):
         launch(i)
     ctx.timer_record(1)
     ctx.sync()
@@ -140,19 +197,56 @@ COPY_PROBE_BYTES = 256 << 20  # calibration copy: reads and writes this many byt
 def traffic_probe(ctx, rng, reps: int = 3) -> None:
     """The launches the two counter runs (FETCH_SIZE, then WRITE_SIZE) measure:
     `reps` device copies of COPY_PROBE_BYTES -- the calibration kernel, whose
-    true HBM traffic is known -- then `reps` 2048^3 matmul_backward launches."""
+    true HBM traffic is known -- then `reps` launches each of the 2048^3
+    matmul_backward, the C3 fused ReLU + bias backward (4096^2) and the C3
+    Adam step (2^24 params), each launch on its own copy of the operands."""
     n = COPY_PROBE_BYTES // 4
     src, dst = ctx.to_device(randn(rng, n)), ctx.empty(n)
     for _ in range(reps):
         ctx.copy(dst, src)
     ctx.sync()
+    # The non-temporal calibration pair (arrays of 2^23 floats and more are
+    # streamed with non-temporal accesses): a fill that writes exactly n
+    # floats (fill_grad_kernel) and a full sum that reads exactly n floats
+    # (reduce_pass1; its partials are a few KiB).
+    from numrs_amd import _lib as L
+    g0, s = ctx.to_device(np.ones(1, np.float32)), ctx.empty((1,))
+    for _ in range(reps):
+        ctx.fill_grad(g0, dst)
+        ctx._check(L.load().numrs_hip_sum(ctx.handle, src.ptr, n, 0, s.ptr))
+    ctx.sync()
+    # The same pair below the streaming threshold (2^22 floats, cached float4
+    # accesses): a second cached calibration beside copy_kernel.
+    nc = 1 << 22
+    sc, dc = src.view(0, (nc,)), dst.view(0, (nc,))
+    for _ in range(reps):
+        ctx.fill_grad(g0, dc)
+        ctx._check(L.load().numrs_hip_sum(ctx.handle, sc.ptr, nc, 0, s.ptr))
+    ctx.sync()
+    del src, dst, sc, dc
     M = K = N = 2048
     A_, B_, dC_ = (ctx.to_device(randn(rng, s)) for s in ((M, K), (K, N), (M, N)))
     dA_, dB_ = ctx.empty((M, K)), ctx.empty((K, N))
     for _ in range(reps):
         ctx.matmul_backward(dC_, A_, B_, dA_, dB_)
     ctx.sync()
-    log(f"traffic probe: {reps} copies of {COPY_PROBE_BYTES} B, {reps} matmul_backward 2048^3")
+    del A_, B_, dC_, dA_, dB_
+    R = C = 4096
+    for _ in range(reps):
+        g, z = ctx.to_device(randn(rng, (R, C))), ctx.to_device(randn(rng, (R, C)))
+        dx, db = ctx.empty((R, C)), ctx.empty((C,))
+        ctx.relu_bias_backward(g, z, dx, db)
+        ctx.sync()
+        del g, z, dx, db
+    na = 1 << 24
+    for t in range(reps):
+        p, g = ctx.to_device(randn(rng, na)), ctx.to_device(randn(rng, na))
+        m, v = ctx.zeros(na), ctx.zeros(na)
+        ctx.adam_step(p, g, m, v, t + 1, lr=1e-3)
+        ctx.sync()
+        del p, g, m, v
+    log(f"traffic probe: {reps} copies of {COPY_PROBE_BYTES} B, {reps} matmul_backward 2048^3, "
+        f"{reps} relu+bias 4096^2, {reps} Adam 2^24")
 
 
 def _pmc_per_dispatch(directory: str, counter: str) -> dict:
@@ -170,42 +264,160 @@ def _pmc_per_dispatch(directory: str, counter: str) -> dict:
                 if row.get("Counter_Name") != counter:
                     continue
                 key = (row["Kernel_Name"], row["Dispatch_Id"])
-                per[key] = per.get(key, 0.0) + float(row["Counter_Value"])
+                if key in per:
+                    raise ValueError(f"{counter}: two records for dispatch {key}")
+                per[key] = float(row["Counter_Value"])
     out = {}
     for (name, _), v in per.items():
         out.setdefault(name, []).append(v)
-    return {k: float(np.mean(v)) for k, v in out.items()}
+    return {k: (float(np.mean(v)), len(v)) for k, v in out.items()}
 
 
-def traffic_summary(fetch_dir: str, write_dir: str) -> dict:
-    """HBM bytes per matmul_backward launch: FETCH_SIZE and WRITE_SIZE (KiB
-    per dispatch), each scaled by the factor that maps the copy kernel's
-    reading of the same counter onto its known COPY_PROBE_BYTES."""
+# Kernels of the traffic probe: (profile name, workload, [(kernel-name part,
+# access mode)] whose dispatches make up one launch of the workload,
+# algorithmic bytes).  Mode "nt": the kernel streams with non-temporal
+# accesses, and its counters are scaled by the non-temporal calibration pair.
+TRAFFIC_KERNELS = [
+    ("matmul_backward_2048", "C2 2048^3", [(HEAD_KERNEL, "cached")],
+     5 * 2048 * 2048 * 4),                          # read A, B, dC; write dA, dB
+    ("relu_bias_4096", "C3 relu(X+b) backward 4096^2",
+     [("colreduce_pass1<true", "nt"), ("colreduce_finalize", "cached")],
+     12 * 4096 * 4096 + 4 * 4096),                  # read g, z; write dx; write db
+    ("adam_16m", "C3 Adam step 2^24 params", [("adam_kernel", "nt")],
+     28 * (1 << 24)),                               # read p, g, m, v; write p, m, v
+]
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> list:
+    """HBM bytes per launch of each probed workload: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by the factor that maps a
+    calibration kernel's reading of the same counter onto its known bytes --
+    copy_kernel (COPY_PROBE_BYTES read and written, cached accesses) for
+    cached kernels, reduce_pass1 (reads) and fill_grad_kernel (writes) over
+    the same bytes for non-temporal ones -- summed over the workload's
+    kernels."""
     fetch = _pmc_per_dispatch(fetch_dir, "FETCH_SIZE")
     write = _pmc_per_dispatch(write_dir, "WRITE_SIZE")
 
-    def pick(d, part):
+    def pick(d, part, reps=3):
+        # The probe makes `reps` dispatches of each kernel; a short or padded
+        # record set is refused.
         keys = [k for k in d if part in k]
         if len(keys) != 1:
             raise KeyError(f"{part}: {keys}")
-        return d[keys[0]]
+        mean, count = d[keys[0]]
+        if count != reps:
+            raise ValueError(f"{part}: {count} dispatch records, expected {reps}: the counter "
+                             f"output is incomplete")
+        return mean
 
     known_kib = COPY_PROBE_BYTES / 1024.0
-    f_copy, w_copy = pick(fetch, "copy_kernel"), pick(write, "copy_kernel")
-    f_mm, w_mm = pick(fetch, HEAD_KERNEL), pick(write, HEAD_KERNEL)
-    ff, fw = known_kib / f_copy, known_kib / w_copy
-    traffic = (f_mm * ff + w_mm * fw) * 1024.0
-    algorithmic = 5 * 2048 * 2048 * 4  # read A, B, dC; write dA, dB
-    res = {"kernel": HEAD_KERNEL, "workload": "C2 2048^3",
-           "fetch_kib_raw": f_mm, "write_kib_raw": w_mm,
-           "copy_fetch_kib_raw": f_copy, "copy_write_kib_raw": w_copy,
-           "copy_bytes": COPY_PROBE_BYTES, "fetch_factor": ff, "write_factor": fw,
-           "bytes_per_launch": traffic, "algorithmic_bytes": algorithmic,
-           "traffic_over_algorithmic": traffic / algorithmic}
-    return res
+    small_kib = 4.0 * (1 << 22) / 1024.0
+    # Access mode 2 (non-temporal) and 1 (cached float4) of the calibration
+    # pair; copy_kernel is a second cached calibration.
+    cal = {"cached": (pick(fetch, "copy_kernel"), pick(write, "copy_kernel")),
+           "nt": (pick(fetch, "::reduce_pass1<0, 2>"), pick(write, "fill_grad_kernel<2>"))}
+    fac = {m: (known_kib / f, known_kib / w) for m, (f, w) in cal.items()}
+    cached2 = (small_kib / pick(fetch, "::reduce_pass1<0, 1>"),
+               small_kib / pick(write, "fill_grad_kernel<1>"))
+    out = []
+    for name, workload, parts, algorithmic in TRAFFIC_KERNELS:
+        f_raw = w_raw = traffic = 0.0
+        for part, mode in parts:
+            f, w = pick(fetch, part), pick(write, part)
+            f_raw, w_raw = f_raw + f, w_raw + w
+            traffic += (f * fac[mode][0] + w * fac[mode][1]) * 1024.0
+        out.append({"name": name, "kernel": "+".join(p for p, _ in parts), "workload": workload,
+                    "modes": [m for _, m in parts], "fetch_kib_raw": f_raw, "write_kib_raw": w_raw,
+                    "calibration_kib_raw": {m: list(v) for m, v in cal.items()},
+                    "calibration_bytes": COPY_PROBE_BYTES,
+                    "factors": {m: list(v) for m, v in fac.items()},
+                    "cached_factors_second_pair": list(cached2),
+                    "bytes_per_launch": traffic, "algorithmic_bytes": algorithmic,
+                    "traffic_over_algorithmic": traffic / algorithmic})
+    return out
 
 
-def bench_matmul_backward(ctx, rng, M, K, N, steps, warmup):
+def trace_summary(trace_csv: str, bench_out: str) -> str:
+    """Markdown summary of a rocprofv3 --kernel-trace of the default bench
+    run: the timed dispatches of each workload, picked out of the trace by
+    the launch order bench.py follows (counts from the run's JSON line), so
+    the kernel's own durations can be set beside the line's figures."""
+    import csv
+
+    with open(bench_out) as f:
+        line = [json.loads(s) for s in f if s.startswith("{")][-1]
+    K = line["steps"]
+    K2 = max(5, K // 2)
+    warm = line["warm_launches"]  # per tag: untimed launches before [timed, resident]
+    with open(trace_csv) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+
+    def seq(part, grid=None):
+        return [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
+                if part in r["Kernel_Name"] and (grid is None or int(r["Grid_Size_X"]) == grid)]
+
+    c2, c2p = seq(HEAD_KERNEL, 256 * 512), seq(HEAD_KERNEL, 512 * 512)
+    relu, fin, adam = seq("colreduce_pass1<true"), seq("colreduce_finalize"), seq("adam_kernel")
+    # 2048^3 dispatches in launch order: per region its untimed launches, 4
+    # queue-ahead, K timed; the same for the resident region; one check
+    # launch; then 4 queue-ahead before each later timed region.  The other
+    # kernels: untimed launches, K timed, untimed, K resident.
+    a, b = warm["C2"]
+    t0 = a + 4
+    r0 = t0 + K + b + 4
+    c, _ = warm["C2'"]
+    e, _ = warm["C3 relu"]
+    g, _ = warm["C3 Adam"]
+    both = [x + y for x, y in zip(relu[e:e + K], fin[e:e + K])]
+    sec = {s["workload"][:7]: s for s in line.get("secondary", [])}
+    spec = [
+        ("C2 2048^3, timed", HEAD_KERNEL, c2[t0:t0 + K], 4.0 * 2048 ** 3, "flop",
+         line["roofline"]["kernel_ms"]),
+        ("C2 2048^3, resident", HEAD_KERNEL, c2[r0:r0 + K], 4.0 * 2048 ** 3, "flop",
+         line["roofline"]["resident_kernel_ms"]),
+        ("C2' 4096x1024x4096, timed", HEAD_KERNEL, c2p[c:c + K2], 4.0 * 4096 * 1024 * 4096,
+         "flop", sec.get("C2' mat", {}).get("kernel_ms")),
+        ("C3 relu+bias, pass 1, timed", "colreduce_pass1<true, 2>", relu[e:e + K], None, None,
+         None),
+        ("C3 relu+bias, finalize, timed", "colreduce_finalize", fin[e:e + K], None, None, None),
+        ("C3 relu+bias, both kernels", "pass 1 + finalize", both, 12.0 * 4096 * 4096 + 4 * 4096,
+         "byte", sec.get("C3 relu", {}).get("kernel_ms")),
+        ("C3 Adam 2^24, timed", "adam_kernel<false, 2>", adam[g:g + K], 28.0 * (1 << 24), "byte",
+         sec.get("C3 Adam", {}).get("kernel_ms")),
+    ]
+    out = ["| Workload | Kernel | Dispatches | Mean (us) | Min (us) | Max (us) | Work per launch "
+           "| Achieved (trace mean) | Fraction | bench.py line (ms) |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
+    for label, kern, d, work, kind, bench_ms in spec:
+        if not d:
+            continue
+        mean = float(np.mean(d))
+        ach = frac = ""
+        if kind == "flop":
+            tf = work / (mean * 1e-6) / 1e12
+            ach, frac = f"{tf:.1f} TFLOP/s", f"{tf / PEAK_FP32_MFMA_TFLOPS:.3f}"
+            wk = f"{work / 1e9:.2f} GFLOP"
+        elif kind == "byte":
+            gb = work / (mean * 1e-6) / 1e9
+            ach, frac = f"{gb:.0f} GB/s", f"{gb / PEAK_HBM_GBS:.3f}"
+            wk = f"{work / 1e6:.1f} MB"
+        else:
+            wk = ""
+        out.append(f"| {label} | {kern} | {len(d)} | {mean:.1f} | {min(d):.1f} | {max(d):.1f} | "
+                   f"{wk} | {ach} | {frac} | {bench_ms if bench_ms is not None else ''} |")
+    ramp = c2[:a]
+    if ramp:
+        pts = [i for i in (0, 9, 29, 59, 89, 149) if i < len(ramp)]
+        out.append("")
+        out.append(f"C2's untimed launches before its timed region ({a}: {line['warmup']} "
+                   f"--warmup + {line['warm_ms']} ms time-based): launch " +
+                   ", ".join(f"{i + 1}: {ramp[i]:.1f} us" for i in pts) +
+                   f"; mean of the last 8: {np.mean(ramp[-8:]):.1f} us.")
+    return "\n".join(out)
+
+
+def bench_matmul_backward(ctx, rng, M, K, N, steps, warmup, tag="C2"):
     """Timed over launches that cycle through n_sets copies of A, B, dC, dA,
     dB (operands streamed from HBM); `resident_ms` repeats the launch on one
     set, whose 80 MB stay in the Infinity Cache."""
@@ -217,8 +429,8 @@ def bench_matmul_backward(ctx, rng, M, K, N, steps, warmup):
     def launch(i):
         ctx.matmul_backward(dC_[i], A_[i], B_[i], dA_[i], dB_[i])
 
-    total, per = time_launches(ctx, launch, steps, warmup)
-    _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup)
+    total, per = time_launches(ctx, launch, steps, warmup, tag)
+    _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup, tag)
     launch(0)
     flops = 4.0 * M * K * N
     # Sanity: one sampled row of each gradient against float64 numpy.
@@ -243,8 +455,8 @@ def bench_relu_bias(ctx, rng, rows, cols, steps, warmup):
     def launch(i):
         ctx.relu_bias_backward(g_[i], z_[i], dx_[i], db_[i])
 
-    total, per = time_launches(ctx, launch, steps, warmup)
-    _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup)
+    total, per = time_launches(ctx, launch, steps, warmup, "C3 relu")
+    _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup, "C3 relu")
     return {"ms_per_step": total / steps, "kernel_ms": per, "resident_ms": resident,
             "sets": k, "bytes": nbytes}
 
@@ -259,8 +471,8 @@ def bench_adam(ctx, rng, n, steps, warmup):
         state["t"] += 1
         ctx.adam_step(p_[i], g_[i], m_[i], v_[i], state["t"], lr=1e-3)
 
-    total, per = time_launches(ctx, launch, steps, warmup)
-    _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup)
+    total, per = time_launches(ctx, launch, steps, warmup, "C3 Adam")
+    _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup, "C3 Adam")
     return {"ms_per_step": total / steps, "kernel_ms": per, "resident_ms": resident,
             "sets": k, "bytes": 28.0 * n}
 
@@ -292,6 +504,7 @@ def bench_c1(ctx, steps, warmup):
 
     for _ in range(warmup):
         step().item()
+    _WARM_LAUNCHES["C1"] = [warmup + warm_for(ctx, lambda i: step(), 0, WARM_MS)]
     t0 = time.perf_counter()
     for _ in range(steps):
         loss = step()
@@ -331,6 +544,7 @@ def bench_c4(ctx, steps, warmup):
 
     for _ in range(warmup):
         step().item()
+    _WARM_LAUNCHES["C4"] = [warmup + warm_for(ctx, lambda i: step(), 0, WARM_MS)]
     ctx.sync()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -371,6 +585,7 @@ def bench_c5(ctx, steps, warmup):
 
     for _ in range(warmup):
         step().item()
+    _WARM_LAUNCHES["C5"] = [warmup + warm_for(ctx, lambda i: step(), 0, WARM_MS)]
     ctx.sync()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -396,17 +611,81 @@ def cpu_baseline(A, B, dC, rows_a: int, rows_b: int):
     O.matmul_backward(dC, A, B, need_a=False, rows_b=(0, rows_b))
     tb = time.perf_counter() - t0
     full_s = ta / rows_a * M + tb / rows_b * K
+    cpu = host_cpu()
     return {
         "value": round(4.0 * M * K * N / full_s / 1e9, 4),
         "unit": "GFLOP/s",
         "cores": 1,
         "kind": "port",
+        "cpu_model": cpu["model"],
         "sample": (f"C restatement of numrs matmul_backward (oracle/numrs_oracle.c, fp32 triple "
-                   f"loops of backward.rs:123-146), {rows_a} of {M} dA rows ({ta:.2f} s) + "
-                   f"{rows_b} of {K} dB rows ({tb:.2f} s), scaled to the full 2048^3 step "
-                   f"({full_s:.1f} s); host {platform.processor() or platform.machine()}, "
-                   f"{os.cpu_count()} logical CPUs visible, 1 thread used"),
+                   f"loops of backward.rs:123-146, single-threaded as there), {rows_a} of {M} dA "
+                   f"rows ({ta:.2f} s) + {rows_b} of {K} dB rows ({tb:.2f} s), scaled to the "
+                   f"full 2048^3 step ({full_s:.1f} s); {cpu['logical_cpus']} logical CPUs, "
+                   f"{cpu['usable_cpus']} usable, 1 thread used"),
     }
+
+
+def cpu_baseline_c1(reps: int = 5) -> dict:
+    """numrs's C1 train step on the host, in the reference's node order
+    (autograd/train.rs:159-183 over backward.rs): the forward products in host
+    BLAS sgemm (numrs runs them through MKL, blas/mod.rs), everything after
+    the forward in the oracle's C restatement on one thread -- CE backward,
+    the bias unbroadcast, matmul_backward's fp32 triple loops for dA and dB
+    (backward.rs:123-146; the reference computes dA of the input too,
+    tensor.rs:206), transposes, ReLU backward and SGD (sgd.rs:87-124).
+    Median of `reps` whole steps."""
+    from oracle import oracle as O
+    from tests.workloads import make_c1
+
+    p = make_c1(seed=1)
+    x, onehot = p["x"], np.eye(10, dtype=np.float32)[p["labels"]]
+    W1, b1, W2, b2 = (p[k].copy() for k in ("W1", "b1", "W2", "b2"))
+
+    def step():
+        W1t, W2t = O.transpose(W1), O.transpose(W2)
+        z1 = x @ W1t + b1
+        h = O.relu(z1)
+        z2 = h @ W2t + b2
+        O.cross_entropy_loss(z2, onehot)
+        dz2 = O.cross_entropy_backward(1.0, z2, onehot)
+        db2 = O.sum_to_shape(dz2, (10,))
+        dh, dW2t = O.matmul_backward(dz2, h, W2t)
+        dz1 = O.relu_backward(dh, z1)
+        db1 = O.sum_to_shape(dz1, (128,))
+        _, dW1t = O.matmul_backward(dz1, x, W1t)
+        for prm, g in ((W1, O.transpose(dW1t)), (b1, db1), (W2, O.transpose(dW2t)), (b2, db2)):
+            O.sgd_step(prm, g, None, 0.01)
+
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    us = float(np.median(times)) * 1e6
+    cpu = host_cpu()
+    return {"value": round(us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+            "cpu_model": cpu["model"],
+            "sample": f"whole step, median of {reps}; forward products in host BLAS sgemm "
+                      f"(numrs: MKL), backward and SGD in the oracle's C loops on 1 thread"}
+
+
+def cpu_baseline_adam(n: int, sample: int = 1 << 22) -> dict:
+    """numrs's Adam::step loop (optim/adam.rs:124-167, one thread, scalar)
+    restated in C, on the first `sample` of n parameters, scaled to n."""
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(SEED + 7)
+    p, g = randn(rng, sample), randn(rng, sample)
+    m, v = np.zeros(sample, np.float32), np.zeros(sample, np.float32)
+    O.adam_step(p, g, m, v, 1)  # page in
+    t0 = time.perf_counter()
+    O.adam_step(p, g, m, v, 2)
+    dt = (time.perf_counter() - t0) * n / sample
+    return {"value": round(28.0 * n / dt / 1e9, 3), "unit": "GB/s", "ms": round(dt * 1e3, 2),
+            "cores": 1, "kind": "port", "cpu_model": host_cpu()["model"],
+            "sample": f"first {sample:,} of {n:,} params ({dt * sample / n * 1e3:.1f} ms), "
+                      f"scaled x{n / sample:g}"}
 
 
 ROW_ELEMS = (4096, 4096)  # BASELINE configs[2] (C3), the elementwise/broadcast config
@@ -435,8 +714,10 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     def f32(shape, scale=1.0):
         return (rng.standard_normal(shape) * scale).astype(np.float32)
 
+    cpu_model = host_cpu()["model"]
+
     def record(row, fn_name, kernel, shape, bytes_=None, flops=None, launch=None,
-               cpu_fn=None, cpu_scale=1.0, cpu_sample="", check=None, note=""):
+               cpu_fn=None, cpu_scale=1.0, cpu_sample="", check=None, note="", cpu_cores=1):
         total, per = time_launches(ctx, launch, steps, warmup)
         _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup)
         launch(0)  # the checks read copy 0
@@ -455,9 +736,10 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
                         "achieved": round(tf, 2), "unit": "TFLOP/s",
                         "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)})
         if cpu and cpu_fn is not None:
+            cpu_fn()  # page the sample in
             t = _cpu_time(cpu_fn) * cpu_scale
-            ent["cpu_baseline"] = {"us": round(t * 1e6, 1), "kind": "port", "cores": 1,
-                                   "sample": cpu_sample}
+            ent["cpu_baseline"] = {"us": round(t * 1e6, 1), "kind": "port", "cores": cpu_cores,
+                                   "cpu_model": cpu_model, "sample": cpu_sample}
             ent["gpu_vs_cpu"] = round(t / (per * 1e-3), 1)
         elif cpu:
             ent["cpu_baseline"] = None
@@ -568,22 +850,29 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
            cpu_fn=lambda: O.mean_backward(0.75, (ns,)), cpu_scale=scale, cpu_sample=samp,
            check=lambda: same_bits(dx_[0].numpy().ravel()[:16],
                                    O.mean_backward(0.75, (n,))[:16]))
-    # a25 ops::sum over all elements (4 B/elem)
+    # a25 ops::sum over all elements (4 B/elem).  CPU: the whole array on all
+    # usable cores (at most 16), each thread's chunk in the AVX2 8-lane order
+    # of simd.rs:247-283 -- Rayon's par_iter split (scalar.rs:500) over the
+    # reference's SIMD loop.
     s_ = ctx.empty((1,))
+    nt = cpu_threads()
+    gflat = g.ravel()
+    mt_samp = f"whole {n:,}-element array, {nt} threads x 8-lane AVX2 order"
     record("a25", "ops::sum (full)", "reduce_pass1+final", shape, bytes_=4.0 * n,
            launch=lambda i: ctx._check(L.load().numrs_hip_sum(ctx.handle, g_[i].ptr, n, 0,
                                                                 s_.ptr)),
-           cpu_fn=lambda: O.sum_avx2_order(g.ravel()[:ns]), cpu_scale=scale,
-           cpu_sample=samp + " (8-lane order of simd.rs:247-283, one thread)",
+           cpu_fn=lambda: O.sum_avx2_order_mt(gflat, nt), cpu_cores=nt, cpu_sample=mt_samp,
            check=lambda: abs(float(s_.numpy()[0]) - float(g.astype(np.float64).sum()))
            <= 1e-3 * np.sqrt(n))
-    # a5 unbroadcast to a bias: [R, C] -> [C] column reduce (4 B/elem)
+    # a5 unbroadcast to a bias: [R, C] -> [C] column reduce (4 B/elem).  numrs
+    # reduces a broadcast grad with ops::sum over everything (backward.rs:12-39),
+    # so its CPU cost is the full sum above.
     b_ = ctx.empty((C,))
     record("a5", "unbroadcast (bias, CORRECT)", "colreduce_pass1+finalize", shape,
            bytes_=4.0 * n + 4.0 * C,
            launch=lambda i: ctx.sum_to_shape(g_[i], b_),
-           cpu_fn=lambda: O.sum_avx2_order(g.ravel()[:ns]), cpu_scale=scale,
-           cpu_sample=samp + " (numrs reduces with ops::sum, backward.rs:12-39)",
+           cpu_fn=lambda: O.sum_avx2_order_mt(gflat, nt), cpu_cores=nt,
+           cpu_sample=mt_samp + " (numrs reduces with ops::sum, backward.rs:12-39)",
            check=lambda: close(b_.numpy(), g.astype(np.float64).sum(0), 1e-4, 1e-3))
     del acc_, pos_, sig_, th_, g_, x_, y_, dx_, dy_
     # a18 mse_backward at C4's output [4096, 512] (dp only: 12 B/elem)
@@ -717,10 +1006,14 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
 
 
 def main() -> int:
+    global WARM_MS, _AHEAD
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--warm-ms", type=float, default=WARM_MS,
+                    help="untimed, time-based warm-up of each timed region on its own launches, "
+                         "after its --warmup launches (reported in the JSON line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-rows-a", type=int, default=512)
@@ -730,19 +1023,26 @@ def main() -> int:
     ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="only launch the calibration copy and the 2048^3 matmul_backward "
-                         "(run under rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)")
+                    help="only launch the calibration copy, the 2048^3 matmul_backward, the C3 "
+                         "relu+bias backward and the C3 Adam step (run under rocprofv3 --pmc "
+                         "FETCH_SIZE, then WRITE_SIZE)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two --pmc outputs of --traffic-probe into "
-                         "profiles/matmul_backward_2048_traffic.json (no GPU needed)")
+                         "profiles/<kernel>_traffic.json files (no GPU needed)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_OUT"),
+                    help="markdown table of the timed dispatches in a rocprofv3 kernel trace of "
+                         "the default run, beside that run's JSON line (no GPU needed)")
     args = ap.parse_args()
 
     if args.traffic_summary:
-        res = traffic_summary(*args.traffic_summary)
-        with open(os.path.join(ROOT, "profiles", "matmul_backward_2048_traffic.json"), "w") as f:
-            json.dump(res, f, indent=1)
-            f.write("\n")
-        print(json.dumps(res), flush=True)
+        for res in traffic_summary(*args.traffic_summary):
+            with open(os.path.join(ROOT, "profiles", f"{res['name']}_traffic.json"), "w") as f:
+                json.dump(res, f, indent=1)
+                f.write("\n")
+            print(json.dumps(res), flush=True)
+        return 0
+    if args.trace_summary:
+        print(trace_summary(*args.trace_summary), flush=True)
         return 0
 
     if args.gpus != 1:
@@ -759,7 +1059,6 @@ def main() -> int:
     n_cus, arch = ctx.info()
     log(f"device {arch}, {n_cus} CUs")
     rng = np.random.default_rng(SEED)
-    global _AHEAD
     if not args.traffic_probe:
         _AHEAD = QueueAhead(ctx, np.random.default_rng(SEED + 1))
 
@@ -767,6 +1066,8 @@ def main() -> int:
         traffic_probe(ctx, rng)
         ctx.close()
         return 0
+
+    WARM_MS = max(0.0, args.warm_ms)
 
     if args.rows:
         for ent in bench_rows(ctx, rng, args.steps, args.warmup, cpu=not args.no_cpu_baseline):
@@ -797,7 +1098,7 @@ def main() -> int:
     secondary = []
     if not args.no_secondary:
         sq = bench_matmul_backward(ctx, rng, 4096, 1024, 4096, max(5, args.steps // 2),
-                                   args.warmup)
+                                   args.warmup, "C2'")
         tf = sq["flops"] / (sq["kernel_ms"] * 1e-3) / 1e12
         secondary.append({"workload": "C2' matmul_backward A[4096,1024] B[1024,4096]",
                           "kernel": HEAD_KERNEL, "kernel_ms": round(sq["kernel_ms"], 5),
@@ -813,23 +1114,31 @@ def main() -> int:
                           "kernel_ms": round(rb["kernel_ms"], 5), "value": round(gbs, 1),
                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
                           "algorithmic_bytes": rb["bytes"], "operand_sets": rb["sets"],
+                          "traffic": traffic_from_profile("relu_bias_4096"),
                           "resident_kernel_ms": round(rb["resident_ms"], 5)})
         log(f"  C3 relu+bias {rb['kernel_ms']:.4f} ms {gbs:.1f} GB/s "
             f"(resident {rb['resident_ms']:.4f} ms)")
         ad = bench_adam(ctx, rng, 1 << 24, args.steps, args.warmup)
         gbs = ad["bytes"] / (ad["kernel_ms"] * 1e-3) / 1e9
-        secondary.append({"workload": "C3 Adam step, 16,777,216 params", "kernel": "adam_kernel",
-                          "kernel_ms": round(ad["kernel_ms"], 5), "value": round(gbs, 1),
-                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
-                          "algorithmic_bytes": ad["bytes"], "operand_sets": ad["sets"],
-                          "resident_kernel_ms": round(ad["resident_ms"], 5)})
+        ent = {"workload": "C3 Adam step, 16,777,216 params", "kernel": "adam_kernel",
+               "kernel_ms": round(ad["kernel_ms"], 5), "value": round(gbs, 1),
+               "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
+               "algorithmic_bytes": ad["bytes"], "operand_sets": ad["sets"],
+               "traffic": traffic_from_profile("adam_16m"),
+               "resident_kernel_ms": round(ad["resident_ms"], 5)}
+        if not args.no_cpu_baseline:
+            ent["cpu_baseline"] = cpu_baseline_adam(1 << 24)
+        secondary.append(ent)
         log(f"  C3 adam {ad['kernel_ms']:.4f} ms {gbs:.1f} GB/s "
             f"(resident {ad['resident_ms']:.4f} ms)")
         c1 = bench_c1(ctx, args.steps, args.warmup)
-        secondary.append({"workload": "C1 MLP train step 64x784->128->10, CE, SGD 0.01 "
-                                      "(forward+backward+step via the device autograd engine)",
-                          "value": round(c1["us_per_step"], 1), "unit": "us/step",
-                          "bound": "latency", "final_loss": round(c1["loss"], 6)})
+        ent = {"workload": "C1 MLP train step 64x784->128->10, CE, SGD 0.01 "
+                           "(forward+backward+step via the device autograd engine)",
+               "value": round(c1["us_per_step"], 1), "unit": "us/step",
+               "bound": "latency", "final_loss": round(c1["loss"], 6)}
+        if not args.no_cpu_baseline:
+            ent["cpu_baseline"] = cpu_baseline_c1()
+        secondary.append(ent)
         log(f"  C1 MLP step {c1['us_per_step']:.1f} us")
         c4 = bench_c4(ctx, max(3, args.steps // 5), 2)
         secondary.append({"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
@@ -864,6 +1173,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warm_ms": WARM_MS,
+        "warm_launches": _WARM_LAUNCHES,
         "ms_per_step": round(head["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",

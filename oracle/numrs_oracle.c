@@ -60,8 +60,11 @@
  *   orc_lookahead_sync           closed form slow + a(fast - slow)
  *   orc_dot_seq                  exact on integer-valued inputs; float64 dot
  *   orc_sched_*                  closed forms (gamma^k, cosine, linear ramp) and plateau traces
+ *   orc_sum_avx2_order_mt        exact on integer-valued inputs for every thread count; equals
+ *                                orc_sum_avx2_order with one thread
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -97,6 +100,66 @@ EXPORT float orc_sum_seq(const float *x, int64_t n) {
  * row reduced with the same 8-lane order as the full sum. */
 EXPORT void orc_sum_rows_avx2_order(const float *x, int64_t rows, int64_t cols, float *out) {
   for (int64_t r = 0; r < rows; ++r) out[r] = orc_sum_avx2_order(x + r * cols, cols);
+}
+
+/* The 8-lane sum compiled for AVX2 (the instructions simd.rs:247-283 uses),
+ * vectorised at O3: the same additions in the same order, so the same bits. */
+__attribute__((target("avx2"), optimize("O3"))) static float sum8_avx2(const float *x,
+                                                                        int64_t n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int l = 0; l < 8; ++l) acc[l] = acc[l] + x[i + l];
+  float s = 0.0f;
+  for (int l = 0; l < 8; ++l) s = s + acc[l];
+  for (; i < n; ++i) s = s + x[i];
+  return s;
+}
+
+struct sum_job {
+  const float *x;
+  int64_t n;
+  int avx2;
+  float out;
+};
+
+static void *sum_worker(void *arg) {
+  struct sum_job *j = (struct sum_job *)arg;
+  j->out = j->avx2 ? sum8_avx2(j->x, j->n) : orc_sum_avx2_order(j->x, j->n);
+  return NULL;
+}
+
+/* A full sum on `threads` host threads, the shape of Rayon's par_iter().sum()
+ * (backend/cpu/scalar.rs:500) with each thread's contiguous chunk reduced in
+ * the 8-lane order of simd.rs:247-283: chunks of a multiple of 8 elements,
+ * partial sums added in chunk order.  Used as the all-cores CPU baseline of
+ * the reduction rows; its bits depend on the thread count (as Rayon's do). */
+EXPORT float orc_sum_avx2_order_mt(const float *x, int64_t n, int threads) {
+  if (threads < 1) threads = 1;
+  if (threads > 256) threads = 256;
+  const int avx2 = __builtin_cpu_supports("avx2");
+  int64_t chunk = (n + threads - 1) / threads;
+  chunk = (chunk + 7) / 8 * 8;
+  struct sum_job jobs[256];
+  pthread_t tid[256];
+  int created[256];
+  for (int t = 0; t < threads; ++t) {
+    const int64_t lo = (int64_t)t * chunk;
+    const int64_t hi = lo + chunk < n ? lo + chunk : n;
+    jobs[t].x = x + (lo < n ? lo : n);
+    jobs[t].n = hi > lo ? hi - lo : 0;
+    jobs[t].avx2 = avx2;
+    jobs[t].out = 0.0f;
+    created[t] = t > 0 && jobs[t].n > 0 && pthread_create(&tid[t], NULL, sum_worker, &jobs[t]) == 0;
+    if (t > 0 && !created[t]) sum_worker(&jobs[t]);  /* no thread: sum it here */
+  }
+  sum_worker(&jobs[0]);
+  float s = jobs[0].out;
+  for (int t = 1; t < threads; ++t) {
+    if (created[t]) pthread_join(tid[t], NULL);
+    s = s + jobs[t].out;
+  }
+  return s;
 }
 
 /* 2-D transpose, ops/shape/transpose.rs:9-33 (blocking does not change values). */

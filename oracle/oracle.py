@@ -47,6 +47,7 @@ def _declare(L) -> None:
         "orc_sum_avx2_order": (_f32, [_f32p, _i64]),
         "orc_sum_seq": (_f32, [_f32p, _i64]),
         "orc_sum_rows_avx2_order": (None, [_f32p, _i64, _i64, _f32p]),
+        "orc_sum_avx2_order_mt": (_f32, [_f32p, _i64, _i]),
         "orc_transpose": (None, [_f32p, _i64, _i64, _f32p]),
         "orc_accumulate": (None, [_f32p, _i64, _f32p, _i64]),
         "orc_matmul_backward_rows": (None, [_f32p] * 5 + [_i64] * 7),
@@ -138,6 +139,13 @@ def sum_avx2_order(x) -> np.float32:
 def sum_seq(x) -> np.float32:
     x = _f(x)
     return np.float32(lib().orc_sum_seq(_p(x), x.size))
+
+
+def sum_avx2_order_mt(x, threads: int) -> np.float32:
+    """The full sum on `threads` host threads, each chunk in the 8-lane order
+    (the all-cores CPU baseline of the reduction rows)."""
+    x = _f(x)
+    return np.float32(lib().orc_sum_avx2_order_mt(_p(x), x.size, int(threads)))
 
 
 def transpose(x) -> np.ndarray:

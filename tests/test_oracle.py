@@ -190,6 +190,21 @@ def test_sum_orders_exact(rng):
         assert O.sum_seq(x) == exact
 
 
+def test_threaded_sum_exact_and_single_thread_order(rng):
+    # Integer-valued inputs sum exactly in any order: every chunking must give
+    # the exact sum; one thread is the 8-lane order itself, bit for bit.
+    for n in (0, 1, 7, 8, 13, 37, 1000, 100003):
+        x = rng.integers(-50, 50, n).astype(np.float32)
+        exact = float(x.astype(np.int64).sum())
+        for t in (1, 2, 3, 8, 16):
+            assert O.sum_avx2_order_mt(x, t) == exact, (n, t)
+    y = rng.standard_normal(1 << 16).astype(np.float32)
+    assert O.sum_avx2_order_mt(y, 1) == O.sum_avx2_order(y)
+    # A dropped chunk fails: the sum of the halves.
+    h = y.size // 2
+    assert O.sum_avx2_order_mt(y, 2) == np.float32(O.sum_avx2_order(y[:h]) + O.sum_avx2_order(y[h:]))
+
+
 def test_sum_to_shape_matches_numpy(rng):
     cases = [((4, 5), (5,)), ((4, 5), (1, 5)), ((4, 5), (4, 1)), ((3, 4, 5), (4, 1)),
              ((3, 4, 5), (3, 1, 5)), ((2, 3), (1,)), ((7,), (1,)), ((2, 3, 4), (2, 3, 4))]
