@@ -293,6 +293,220 @@ __global__ void __launch_bounds__(kThreads)
 
 static_assert(kRows * 4 == kWaves, "one LDS column of partials per wave");
 
+// ---------------------------------------------------------------------------
+// Tiled step kernels for H % 64 == 0 (the C5 shape): 256-thread workgroups,
+// 256 of them at B = 64, H = 256, so one step spans every CU; both read W_hh
+// in its stored [4H, H] layout (no repacking launch).
+// ---------------------------------------------------------------------------
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFRows = 16;   // forward: batch rows per workgroup (the MFMA's M)
+constexpr int kFUnits = 4;   // forward: hidden units per workgroup (x 4 gates = the MFMA's N)
+constexpr int kBRows = 8;    // backward: batch rows per workgroup
+constexpr int kBUnits = 8;   // backward: hidden units per workgroup
+
+// Forward step t on fp32 MFMA.  Workgroup (unit group, row group) owns rows
+// b0..b0+15 and units j0..j0+3; its 16 gate columns are c = 4g + u, gate g of
+// unit j0 + u, i.e. W_hh row n(c) = g*H + j0 + u.  The product
+// pre[m][c] = sum_k h_{t-1}[b0+m][k] W_hh[n(c)][k] runs as
+// v_mfma_f32_16x16x4f32 with the reduction split over the 4 waves (wave w
+// takes k in [w H/4, (w+1) H/4)).  In each 64-long block of a wave's range,
+// MFMA s = 4i + e gives lane (r, q) = (l % 16, l / 16) the index
+// k = kb + 16i + 4q + e on both operands, so a lane's 16 h values and 16
+// weights of the block are four float4 loads each, and the four lanes of a
+// row read 64 contiguous bytes per load.  Lane l ends with column l % 16 of rows
+// 4(l / 16) .. +3; the four wave partials meet in LDS and are added in wave
+// order, and wave 0 finishes the 64 cells (lane = 4m + u).  The epilogue's
+// inputs are loaded before the product, so their latencies overlap.
+__global__ void __launch_bounds__(256)
+    lstm_fwd_step_tiled(float *G, const float *__restrict__ whh, const float *__restrict__ h0,
+                        const float *__restrict__ c0, float *__restrict__ h_seq,
+                        float *__restrict__ c_seq, int B, int T, int H, int t) {
+  __shared__ float part[4][kFRows][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ugroups = H / kFUnits;
+  const int ug = blockIdx.x % ugroups, rg = blockIdx.x / ugroups;
+  const int j0 = ug * kFUnits, b0 = rg * kFRows;
+  const int H4 = 4 * H;
+
+  // epilogue inputs of cell (m, u) = (lane / 4, lane % 4), wave 0
+  const int em = lane >> 2, eu = lane & 3;
+  const int be = b0 + em, je = j0 + eu;
+  const bool epi = wave == 0 && be < B;
+  const int64_t gb = ((int64_t)be * T + t) * H4;
+  float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f}, cp = 0.0f;
+  if (epi) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) gin[g] = G[gb + g * H + je];
+    cp = t > 0 ? c_seq[((int64_t)be * T + t - 1) * H + je]
+               : (c0 != nullptr ? c0[(int64_t)be * H + je] : 0.0f);
+  }
+
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (t > 0 || h0 != nullptr) {
+    const int r = lane & 15, q = lane >> 4;
+    const int b = min(b0 + r, B - 1);
+    const float *hrow = t > 0 ? h_seq + ((int64_t)b * T + t - 1) * H : h0 + (int64_t)b * H;
+    const float *wrow = whh + (int64_t)((r >> 2) * H + j0 + (r & 3)) * H;
+    const int kw = H >> 2;
+    for (int kb = wave * kw; kb < (wave + 1) * kw; kb += 64) {
+      f4 a[4], w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = *reinterpret_cast<const f4 *>(hrow + kb + 16 * i + 4 * q);
+        w[i] = *reinterpret_cast<const f4 *>(wrow + kb + 16 * i + 4 * q);
+      }
+#pragma unroll
+      for (int s = 0; s < 16; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s >> 2][s & 3], w[s >> 2][s & 3], acc, 0, 0,
+                                                   0);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) part[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
+  __syncthreads();
+  if (!epi) return;
+  float pre[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int c = 4 * g + eu;
+    pre[g] = gin[g] + (((part[0][em][c] + part[1][em][c]) + part[2][em][c]) + part[3][em][c]);
+  }
+  const float i = sigm(pre[0]);
+  const float f = sigm(pre[1]);
+  const float g = tanhf(pre[2]);
+  const float o = sigm(pre[3]);
+  const float c = f * cp + i * g;
+  const float h = o * tanhf(c);
+  G[gb + je] = i;
+  G[gb + H + je] = f;
+  G[gb + 2 * H + je] = g;
+  G[gb + 3 * H + je] = o;
+  c_seq[((int64_t)be * T + t) * H + je] = c;
+  h_seq[((int64_t)be * T + t) * H + je] = h;
+}
+
+// Backward step t on the VALU.  The product dh[b][j] = sum_n dG_{t+1}[b][n]
+// W_hh[n][j] has only H output columns over a 4H-long reduction, so it is
+// register-blocked rather than MFMA-shaped: workgroup (unit group, row group)
+// owns rows b0..b0+7 and units j0..j0+7, wave w the 4 x 4 cell block of rows
+// b0 + 4(w / 2) and units j0 + 4(w % 2), and lane l of the wave the
+// reduction slice n in [l H/16, (l+1) H/16).  wt is W_hh^T [H, 4H], so a
+// lane's slice is contiguous both in the block's four dG rows and in the
+// four units' rows of wt: it loads both as float4s (consecutive lanes read
+// consecutive slices) and carries the 16 cells.  The 64 lanes' partials are
+// then summed through LDS (a chain of cross-lane shuffles measured 3 us
+// slower per step), and lane 4c finishes cell c.  dc holds
+// dc_{t+1} f_{t+1} on entry and dc_t f_t on exit, each (b, j) touched by one
+// lane only.
+__global__ void __launch_bounds__(256)
+    lstm_bwd_step_tiled(float *__restrict__ dG, const float *__restrict__ wt,
+                        const float *__restrict__ acts, const float *__restrict__ c_seq,
+                        const float *__restrict__ c0, const float *__restrict__ dh_out,
+                        float *__restrict__ dc, int B, int T, int H, int t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ugroups = H / kBUnits;
+  const int ug = blockIdx.x % ugroups, rg = blockIdx.x / ugroups;
+  const int rb = rg * kBRows + 4 * (wave >> 1), ub = ug * kBUnits + 4 * (wave & 1);
+  const int H4 = 4 * H;
+  const bool has_next = t + 1 < T;
+
+  // epilogue inputs of cell ec = lane / 4: row rb + ec / 4, unit ub + ec % 4
+  const int ec = lane >> 2;
+  const int be = rb + (ec >> 2), je = ub + (ec & 3);
+  const bool epi = (lane & 3) == 0 && be < B;
+  const int64_t row = (int64_t)be * T + t;
+  const int64_t gb = row * H4;
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, c = 0.0f, cp = 0.0f, dho = 0.0f, dcn = 0.0f;
+  if (epi) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) a[g] = acts[gb + g * H + je];
+    c = c_seq[row * H + je];
+    cp = t > 0 ? c_seq[(row - 1) * H + je] : (c0 != nullptr ? c0[(int64_t)be * H + je] : 0.0f);
+    if (dh_out != nullptr) dho = dh_out[row * H + je];
+    if (has_next) dcn = dc[(int64_t)be * H + je];
+  }
+
+  float v[16];  // cell (i, u) of the wave's block at 4i + u
+#pragma unroll
+  for (int k = 0; k < 16; ++k) v[k] = 0.0f;
+  if (has_next) {
+    const float *drow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      drow[i] = dG + ((int64_t)min(rb + i, B - 1) * T + t + 1) * H4;
+    const int ns = H >> 4;  // slice length, a multiple of 4
+    const int n0 = lane * ns;
+    const float *wrow[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) wrow[u] = wt + (int64_t)(ub + u) * H4;
+    for (int nb = n0; nb < n0 + ns; nb += 16) {
+      f4 d[4][4], w[4][4];  // [n group][row], [n group][unit]
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (nb + 4 * e < n0 + ns) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) d[e][i] = *reinterpret_cast<const f4 *>(drow[i] + nb + 4 * e);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) w[e][u] = *reinterpret_cast<const f4 *>(wrow[u] + nb + 4 * e);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (nb + 4 * e < n0 + ns) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int u = 0; u < 4; ++u) v[4 * i + u] += d[e][i][s] * w[e][u][s];
+        }
+      }
+    }
+  }
+  // The 64 lanes' partials of the wave's 16 cells, summed through LDS in two
+  // levels: lane l adds cell l / 4 over the 16 lanes 16 (l % 4) .. +15, then
+  // lane 4c adds its cell's four quarter sums, in quarter order.
+  __shared__ float part[4][64][17];  // [wave][lane][cell], padded row
+  __shared__ float quarter[4][16][4];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) part[wave][lane][k] = v[k];
+  __syncthreads();
+  {
+    const int q0 = (lane & 3) * 16;
+    float s = part[wave][q0][ec];
+#pragma unroll
+    for (int m = 1; m < 16; ++m) s += part[wave][q0 + m][ec];
+    quarter[wave][ec][lane & 3] = s;
+  }
+  __syncthreads();
+  if (!epi) return;
+  const float r = ((quarter[wave][ec][0] + quarter[wave][ec][1]) + quarter[wave][ec][2]) +
+                  quarter[wave][ec][3];
+  const float i = a[0], f = a[1], g = a[2], o = a[3];
+  const float dh = dho + r;
+  const float tc = tanhf(c);
+  const float dct = dh * o * (1.0f - tc * tc) + dcn;
+  dG[gb + je] = (dct * g) * i * (1.0f - i);
+  dG[gb + H + je] = (dct * cp) * f * (1.0f - f);
+  dG[gb + 2 * H + je] = (dct * i) * (1.0f - g * g);
+  dG[gb + 3 * H + je] = (dh * tc) * o * (1.0f - o);
+  dc[(int64_t)be * H + je] = dct * f;
+}
+
+// Whether the tiled step kernels take this shape.  The forward walks each
+// wave's quarter of the reduction in whole 64-long blocks (H % 256 == 0); the
+// backward's lane slices are H/16 long in float4 steps (H % 64 == 0).  Both
+// read rows of W_hh and of h or dG as float4s.
+bool tiled_fwd_fits(int64_t H, const void *whh, const void *h_seq, const void *h0) {
+  return H % 256 == 0 && numrs_hip::aligned16(whh) && numrs_hip::aligned16(h_seq) &&
+         (h0 == nullptr || numrs_hip::aligned16(h0));
+}
+bool tiled_bwd_fits(int64_t H, const void *whh, const void *dG) {
+  return H % 64 == 0 && numrs_hip::aligned16(whh) && numrs_hip::aligned16(dG);
+}
+
 // H_prev[b, t] = h_seq[b, t-1] (t > 0), h0[b] or 0 (t = 0).
 __global__ void __launch_bounds__(256)
     shift_hidden(const float *__restrict__ h_seq, const float *__restrict__ h0,
@@ -354,6 +568,15 @@ int numrs_hip_lstm_forward(numrs_hip_ctx *ctx, const float *x, const float *w_ih
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "lstm_forward: null pointer");
   // acts <- x W_ih^T + b for every (b, t) row
   if (int rc = numrs_hip_linear_forward(ctx, x, w_ih, b, acts, B * T, I, 4 * H)) return rc;
+  if (tiled_fwd_fits(H, w_hh, h_seq, h0)) {
+    const unsigned grid = (unsigned)((H / kFUnits) * ((B + kFRows - 1) / kFRows));
+    for (int64_t t = 0; t < T; ++t) {
+      lstm_fwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(acts, w_hh, h0, c0, h_seq, c_seq,
+                                                          (int)B, (int)T, (int)H, (int)t);
+      if (int rc = numrs_hip::check_launch(ctx, "lstm_fwd_step_tiled")) return rc;
+    }
+    return NUMRS_HIP_OK;
+  }
   TempBlock whhT(ctx), wp(ctx);
   if (int rc = whhT.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
   if (int rc = wp.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
@@ -389,20 +612,33 @@ int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_i
   TempBlock dG(ctx), dc(ctx);
   if (int rc = dG.alloc((size_t)(rows * H4) * sizeof(float))) return rc;
   if (int rc = dc.alloc((size_t)(B * H) * sizeof(float))) return rc;
-  TempBlock wp(ctx);
-  if (int rc = wp.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
-  pack_gates<<<grid_for(4 * H * H, 256), 256, 0, ctx->stream>>>(w_hh, wp.f(), (int)H, H * H, H);
-  if (int rc = numrs_hip::check_launch(ctx, "pack_gates")) return rc;
-  const float4 *wp4 = reinterpret_cast<const float4 *>(wp.p);
-  const unsigned grid = step_grid((int)B, (int)H);
-  for (int64_t t = T - 1; t >= 0; --t) {
-    if (H <= kBwdStageH)
-      lstm_bwd_step<true><<<grid, kThreads, 0, ctx->stream>>>(
-          dG.f(), wp4, acts, c_seq, c0, dh_seq, dc.f(), (int)B, (int)T, (int)H, (int)t);
-    else
-      lstm_bwd_step<false><<<grid, kThreads, 0, ctx->stream>>>(
-          dG.f(), wp4, acts, c_seq, c0, dh_seq, dc.f(), (int)B, (int)T, (int)H, (int)t);
-    if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step")) return rc;
+  if (tiled_bwd_fits(H, w_hh, dG.p)) {
+    TempBlock wt(ctx);  // W_hh^T [H, 4H]
+    if (int rc = wt.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
+    if (int rc = numrs_hip_transpose(ctx, w_hh, wt.f(), 4 * H, H)) return rc;
+    const unsigned grid = (unsigned)((H / kBUnits) * ((B + kBRows - 1) / kBRows));
+    for (int64_t t = T - 1; t >= 0; --t) {
+      lstm_bwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(dG.f(), wt.f(), acts, c_seq, c0, dh_seq,
+                                                          dc.f(), (int)B, (int)T, (int)H, (int)t);
+      if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step_tiled")) return rc;
+    }
+  } else {
+    TempBlock wp(ctx);
+    if (int rc = wp.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
+    pack_gates<<<grid_for(4 * H * H, 256), 256, 0, ctx->stream>>>(w_hh, wp.f(), (int)H, H * H,
+                                                                  H);
+    if (int rc = numrs_hip::check_launch(ctx, "pack_gates")) return rc;
+    const float4 *wp4 = reinterpret_cast<const float4 *>(wp.p);
+    const unsigned grid = step_grid((int)B, (int)H);
+    for (int64_t t = T - 1; t >= 0; --t) {
+      if (H <= kBwdStageH)
+        lstm_bwd_step<true><<<grid, kThreads, 0, ctx->stream>>>(
+            dG.f(), wp4, acts, c_seq, c0, dh_seq, dc.f(), (int)B, (int)T, (int)H, (int)t);
+      else
+        lstm_bwd_step<false><<<grid, kThreads, 0, ctx->stream>>>(
+            dG.f(), wp4, acts, c_seq, c0, dh_seq, dc.f(), (int)B, (int)T, (int)H, (int)t);
+      if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step")) return rc;
+    }
   }
   // Weight gradients over all steps at once (batched over time).
   if (dw_ih)  // dW_ih[4H, I] = dG^T x

@@ -11,12 +11,17 @@ from tests.conftest import assert_chain
 pytestmark = pytest.mark.gpu
 
 
+# H % 256 == 0 takes the tiled MFMA forward step and H % 64 == 0 the tiled
+# backward step: "baseline" (the C5 shape), "tiled_rows" (512 units, batch 20:
+# partial row groups in both), "medium" and "bwd_tiled_h192" (tiled backward
+# only); the others keep the per-unit kernels.
 @pytest.mark.parametrize("dims", [dict(B=3, T=6, I=4, H=5), dict(B=8, T=20, I=16, H=64),
                                   dict(B=5, T=9, I=70, H=130),
                                   dict(B=64, T=128, I=64, H=256),
+                                  dict(B=20, T=7, I=24, H=512), dict(B=9, T=6, I=16, H=192),
                                   dict(B=3, T=4, I=8, H=1040), dict(B=2, T=3, I=8, H=2056)],
-                         ids=["tiny", "medium", "ragged", "baseline",
-                              "wide_unstaged_bwd", "wide_unstaged"])
+                         ids=["tiny", "medium", "ragged", "baseline", "tiled_rows",
+                              "bwd_tiled_h192", "wide_unstaged_bwd", "wide_unstaged"])
 def test_lstm_forecaster_matches_oracle(hip_ctx, dims):
     print(f"[gpu] lstm forecaster {dims}", flush=True)
     nr.set_default_context(hip_ctx)
@@ -32,11 +37,14 @@ def test_lstm_forecaster_matches_oracle(hip_ctx, dims):
     _, g32, y32 = LO.forecaster(layers, hw, hb, x, target, dtype=np.float32)
     assert abs(loss.item() - ref_loss) <= 1e-5 * abs(ref_loss) + 1e-7
     # At the BASELINE size the GPU must be at least as close to float64 as the
-    # fp32 CPU chain.  The other shapes have tensors of 5..100 elements (y is
-    # [B, 1]), where the mean of two independent fp32 rounding patterns is
-    # noise: there the GPU may be up to 2x the CPU chain's error.
+    # fp32 CPU chain, on every tensor.  The other shapes have tensors of
+    # 1..100 elements (head_b is one number, y is [B, 1]), where the mean of
+    # two independent fp32 rounding patterns is noise: there the GPU may be up
+    # to 2x the CPU chain's error, and tensors under 64 elements are held to
+    # the per-element and norm-wise bars only.
     base = dims["B"] == 64 and dims["T"] == 128
-    fac = dict(mean_factor=1.0, max_factor=1.5) if base else dict(mean_factor=2.0, max_factor=3.0)
+    fac = (dict(mean_factor=1.0, max_factor=1.5) if base else
+           dict(mean_factor=2.0, max_factor=3.0, factor_min_size=64))
     assert_chain(y.values(), ref_y, y32, what="y", **fac)
     got = {"head_w": model.head.weight, "head_b": model.head.bias, "x": xt}
     for li, layer in enumerate(model.layers):
