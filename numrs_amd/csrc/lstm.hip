@@ -465,25 +465,26 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
-  // The 64 lanes' partials of the wave's 16 cells, summed through LDS in two
-  // levels: lane l adds cell l / 4 over the 16 lanes 16 (l % 4) .. +15, then
-  // lane 4c adds its cell's four quarter sums, in quarter order.
-  __shared__ float part[4][64][17];  // [wave][lane][cell], padded row
-  __shared__ float quarter[4][16][4];
+  // The 64 lanes' partials of the wave's 16 cells, summed through LDS: the
+  // partials are stored cell-major, lane l reads the 16 partials of cell
+  // l / 4 from lanes 16 (l % 4) .. +15 as four float4s and adds them in a
+  // fixed pairwise order, and the four quarter sums of a cell (lanes
+  // 4c .. 4c+3) are added by two exchanges.
+  __shared__ f4 part[4][16][16];  // [wave][cell][lane / 4]: lane l at part[..][l / 4][l % 4]
+  float *pw = reinterpret_cast<float *>(&part[wave][0][0]);
 #pragma unroll
-  for (int k = 0; k < 16; ++k) part[wave][lane][k] = v[k];
+  for (int k = 0; k < 16; ++k) pw[k * 64 + lane] = v[k];
   __syncthreads();
+  float r;
   {
-    const int q0 = (lane & 3) * 16;
-    float s = part[wave][q0][ec];
-#pragma unroll
-    for (int m = 1; m < 16; ++m) s += part[wave][q0 + m][ec];
-    quarter[wave][ec][lane & 3] = s;
+    const f4 *src = &part[wave][ec][4 * (lane & 3)];
+    const f4 p0 = src[0], p1 = src[1], p2 = src[2], p3 = src[3];
+    r = (((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]))) +
+        (((p2[0] + p2[1]) + (p2[2] + p2[3])) + ((p3[0] + p3[1]) + (p3[2] + p3[3])));
   }
-  __syncthreads();
+  r += __shfl_xor(r, 1, 64);
+  r += __shfl_xor(r, 2, 64);
   if (!epi) return;
-  const float r = ((quarter[wave][ec][0] + quarter[wave][ec][1]) + quarter[wave][ec][2]) +
-                  quarter[wave][ec][3];
   const float i = a[0], f = a[1], g = a[2], o = a[3];
   const float dh = dho + r;
   const float tc = tanhf(c);
