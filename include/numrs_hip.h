@@ -224,6 +224,18 @@ int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float
                                  const float *v, const float *P, const float *dout, float *dq,
                                  float *dk, float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
                                  int accumulate);
+/* The same with explicit row strides: q, k, v (and dq, dk, dv) rows at
+ * ld_qkv, out / dout rows at ld_out, both >= D.  With ld_qkv = 3D, q, k, v
+ * can be the three column blocks of one packed [B*S, 3D] projection. */
+int numrs_hip_attention_forward_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                        const float *v, int64_t ld_qkv, float *P, float *out,
+                                        int64_t ld_out, int64_t B, int64_t S, int64_t H,
+                                        int64_t D);
+int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                         const float *v, int64_t ld_qkv, const float *P,
+                                         const float *dout, int64_t ld_out, float *dq, float *dk,
+                                         float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
+                                         int accumulate);
 
 /* LSTM layer (no reference op), gate order i, f, g, o:
  * x [B, T, I], W_ih [4H, I], W_hh [4H, H], b [4H] (NULL = 0), h0/c0 [B, H]
@@ -559,6 +571,11 @@ int numrs_hip_tensor_time_slice(numrs_hip_tensor *x, int64_t t, numrs_hip_tensor
 /* Multi-head attention node over q, k, v [B*S, D] (numrs_hip_attention_forward). */
 int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_hip_tensor *v,
                                int64_t batch, int64_t seq, int64_t heads, numrs_hip_tensor **out);
+/* The same node over one packed projection qkv [B*S, 3D] (q, k, v its column
+ * blocks, as a Linear to 3D features produces them): out [B*S, D]; the
+ * backward writes the packed grad [B*S, 3D]. */
+int numrs_hip_tensor_attention_qkv(numrs_hip_tensor *qkv, int64_t batch, int64_t seq,
+                                   int64_t heads, numrs_hip_tensor **out);
 
 /* SGD::new (optim/sgd.rs:47-69) / Adam::new (optim/adam.rs:64-99) over
  * parameter tensors; step / zero_grad / learning_rate / set_learning_rate

@@ -81,6 +81,9 @@ SIGNATURES = {
     "numrs_hip_time_slice": (_i, [_vp] * 3 + [_i64] * 4 + [_i, _i]),
     "numrs_hip_attention_forward": (_i, [_vp] * 6 + [_i64] * 4),
     "numrs_hip_attention_backward": (_i, [_vp] * 9 + [_i64] * 4 + [_i]),
+    "numrs_hip_attention_forward_strided": (_i, [_vp] * 4 + [_i64, _vp, _vp] + [_i64] * 5),
+    "numrs_hip_attention_backward_strided": (_i, [_vp] * 4 + [_i64, _vp, _vp, _i64] + [_vp] * 3 +
+                                             [_i64] * 4 + [_i]),
     # tensor engine
     "numrs_hip_set_grad_enabled": (None, [_i]),
     "numrs_hip_is_grad_enabled": (_i, []),
@@ -115,6 +118,7 @@ SIGNATURES = {
     "numrs_hip_tensor_lstm": (_i, [_vp] * 4 + [ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_time_slice": (_i, [_vp, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_attention": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_attention_qkv": (_i, [_vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_optim_sgd": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, ctypes.POINTER(_vp)]),
     "numrs_hip_optim_adam": (_i, [_vp, ctypes.POINTER(_vp), _i, _f, _f, _f, _f, _f,
                                  ctypes.POINTER(_vp)]),

@@ -330,6 +330,13 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_attention(self._h, k._h, v._h, batch, seq, heads,
                                                              ctypes.byref(h)), h)
 
+    def attention_qkv(self, batch: int, seq: int, heads: int) -> "Tensor":
+        """Multi-head attention over self = a packed projection [batch*seq, 3*dim]
+        whose column blocks are q, k and v; returns [batch*seq, dim]."""
+        h = ctypes.c_void_p()
+        return self._out(L.load().numrs_hip_tensor_attention_qkv(self._h, batch, seq, heads,
+                                                                 ctypes.byref(h)), h)
+
     def __repr__(self) -> str:
         return f"Tensor(shape={list(self.shape())}, requires_grad={self.requires_grad})"
 

@@ -43,14 +43,14 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
                                                         const float *__restrict__ W,
                                                         const float *__restrict__ P,
                                                         float *__restrict__ out, int S, int H,
-                                                        int64_t ld, float alpha) {
+                                                        int64_t ldx, int64_t ldw, float alpha) {
   __shared__ float red[4][kRowsPerBlock];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, hh = lane >> 5;
   const int z = blockIdx.y, b = z / H, head = z - b * H;
   const int row0 = blockIdx.x * kRowsPerBlock, col0 = wave * 32 * BJ;
-  const float *Xz = X + (int64_t)b * S * ld + (int64_t)head * kHeadDim;
-  const float *Wz = W + (int64_t)b * S * ld + (int64_t)head * kHeadDim;
+  const float *Xz = X + (int64_t)b * S * ldx + (int64_t)head * kHeadDim;
+  const float *Wz = W + (int64_t)b * S * ldw + (int64_t)head * kHeadDim;
   const int64_t zoff = (int64_t)z * S * S;
 
   f16v acc[2][BJ];
@@ -63,10 +63,10 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
     f4 a[2], w[BJ];
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi)
-      a[bi] = *reinterpret_cast<const f4 *>(Xz + (int64_t)(row0 + 32 * bi + c) * ld + 8 * g + 4 * hh);
+      a[bi] = *reinterpret_cast<const f4 *>(Xz + (int64_t)(row0 + 32 * bi + c) * ldx + 8 * g + 4 * hh);
 #pragma unroll
     for (int bj = 0; bj < BJ; ++bj)
-      w[bj] = *reinterpret_cast<const f4 *>(Wz + (int64_t)(col0 + 32 * bj + c) * ld + 8 * g + 4 * hh);
+      w[bj] = *reinterpret_cast<const f4 *>(Wz + (int64_t)(col0 + 32 * bj + c) * ldw + 8 * g + 4 * hh);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -180,29 +180,35 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
 }
 
 // Whether the fused row-block kernel takes this shape: dh = 64, S a multiple
-// of 128 up to 512, 16-byte aligned rows and probability matrices.
-bool rows_fit(int64_t S, int64_t dh, int64_t D, const void *x, const void *w, const void *p) {
-  return dh == kHeadDim && S % 128 == 0 && S <= 512 && D % 4 == 0 && numrs_hip::aligned16(x) &&
-         numrs_hip::aligned16(w) && numrs_hip::aligned16(p);
+// of 128 up to 512, rows of both operands at 16-byte strides and 16-byte
+// aligned, 16-byte aligned probability matrices.
+bool rows_fit(int64_t S, int64_t dh, int64_t ldx, int64_t ldw, const void *x, const void *w,
+              const void *p) {
+  return dh == kHeadDim && S % 128 == 0 && S <= 512 && ldx % 4 == 0 && ldw % 4 == 0 &&
+         numrs_hip::aligned16(x) && numrs_hip::aligned16(w) && numrs_hip::aligned16(p);
 }
 
 template <int MODE>
-int launch_rows(numrs_hip_ctx *ctx, const float *X, const float *W, const float *P, float *out,
-                int64_t B, int64_t S, int64_t H, int64_t D, float alpha) {
+int launch_rows(numrs_hip_ctx *ctx, const float *X, int64_t ldx, const float *W, int64_t ldw,
+                const float *P, float *out, int64_t B, int64_t S, int64_t H, float alpha) {
   const dim3 grid((unsigned)(S / kRowsPerBlock), (unsigned)(B * H));
+  const int s = (int)S, h = (int)H;
   switch (S / 128) {
-    case 1: attn_rows_kernel<MODE, 1><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, (int)S, (int)H, D, alpha); break;
-    case 2: attn_rows_kernel<MODE, 2><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, (int)S, (int)H, D, alpha); break;
-    case 3: attn_rows_kernel<MODE, 3><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, (int)S, (int)H, D, alpha); break;
-    default: attn_rows_kernel<MODE, 4><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, (int)S, (int)H, D, alpha); break;
+    case 1: attn_rows_kernel<MODE, 1><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
+    case 2: attn_rows_kernel<MODE, 2><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
+    case 3: attn_rows_kernel<MODE, 3><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
+    default: attn_rows_kernel<MODE, 4><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
   }
   return numrs_hip::check_launch(ctx, "attn_rows_kernel");
 }
 
-int check(numrs_hip_ctx *ctx, int64_t B, int64_t S, int64_t H, int64_t D) {
+int check(numrs_hip_ctx *ctx, int64_t B, int64_t S, int64_t H, int64_t D, int64_t ld_qkv,
+          int64_t ld_out) {
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0 || D % H != 0)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_SHAPE,
                            "attention: batch, seq, heads > 0 and dim divisible by heads");
+  if (ld_qkv < D || ld_out < D)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_SHAPE, "attention: row strides below the dim");
   return NUMRS_HIP_OK;
 }
 
@@ -210,46 +216,51 @@ int check(numrs_hip_ctx *ctx, int64_t B, int64_t S, int64_t H, int64_t D) {
 
 extern "C" {
 
-int numrs_hip_attention_forward(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,
-                                float *P, float *out, int64_t B, int64_t S, int64_t H,
-                                int64_t D) {
+// q, k, v rows (and dq, dk, dv in the backward) at stride ld_qkv, out / dout
+// rows at stride ld_out: q, k, v may be column slices of one packed
+// [B*S, 3D] projection (ld_qkv = 3D).
+int numrs_hip_attention_forward_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                        const float *v, int64_t ld_qkv, float *P, float *out,
+                                        int64_t ld_out, int64_t B, int64_t S, int64_t H,
+                                        int64_t D) {
   NRS_CHECK_CTX(ctx);
-  if (int rc = check(ctx, B, S, H, D)) return rc;
+  if (int rc = check(ctx, B, S, H, D, ld_qkv, ld_out)) return rc;
   if (!q || !k || !v || !P || !out)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "attention_forward: null pointer");
-  const int64_t dh = D / H, Z = B * H;
+  const int64_t dh = D / H, Z = B * H, li = ld_qkv, lo = ld_out;
   const float alpha = 1.0f / sqrtf((float)dh);
-  if (rows_fit(S, dh, D, q, k, P) && B * H < 65536) {
+  if (rows_fit(S, dh, li, li, q, k, P) && B * H < 65536) {
     // P = softmax_rows(alpha * Q K^T) in one kernel
-    if (int rc = launch_rows<0>(ctx, q, k, nullptr, P, B, S, H, D, alpha)) return rc;
-    return numrs_hip_gemm(ctx, P, S, v, D, out, D, S, S, dh, 0, 0, 1.0f, 0, Z, H, H * S * S,
-                          S * S, S * D, dh, S * D, dh);
+    if (int rc = launch_rows<0>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha)) return rc;
+    return numrs_hip_gemm(ctx, P, S, v, li, out, lo, S, S, dh, 0, 0, 1.0f, 0, Z, H, H * S * S,
+                          S * S, S * li, dh, S * lo, dh);
   }
   // S_z = alpha * Q_z K_z^T  -> P (row-major [S, S] per z)
-  if (int rc = numrs_hip_gemm(ctx, q, D, k, D, P, S, S, dh, S, 0, 1, alpha, 0, Z, H, S * D, dh,
-                              S * D, dh, H * S * S, S * S))
+  if (int rc = numrs_hip_gemm(ctx, q, li, k, li, P, S, S, dh, S, 0, 1, alpha, 0, Z, H, S * li, dh,
+                              S * li, dh, H * S * S, S * S))
     return rc;
   // in-place row softmax (each row is read completely before it is written)
   if (int rc = numrs_hip_softmax_forward(ctx, P, P, Z * S, S, 1.0f)) return rc;
   // O_z = P_z V_z
-  return numrs_hip_gemm(ctx, P, S, v, D, out, D, S, S, dh, 0, 0, 1.0f, 0, Z, H, H * S * S, S * S,
-                        S * D, dh, S * D, dh);
+  return numrs_hip_gemm(ctx, P, S, v, li, out, lo, S, S, dh, 0, 0, 1.0f, 0, Z, H, H * S * S,
+                        S * S, S * li, dh, S * lo, dh);
 }
 
-int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float *k,
-                                 const float *v, const float *P, const float *dout, float *dq,
-                                 float *dk, float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
-                                 int accumulate) {
+int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                         const float *v, int64_t ld_qkv, const float *P,
+                                         const float *dout, int64_t ld_out, float *dq, float *dk,
+                                         float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
+                                         int accumulate) {
   NRS_CHECK_CTX(ctx);
-  if (int rc = check(ctx, B, S, H, D)) return rc;
+  if (int rc = check(ctx, B, S, H, D, ld_qkv, ld_out)) return rc;
   if (!q || !k || !v || !P || !dout)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "attention_backward: null input");
-  const int64_t dh = D / H, Z = B * H;
+  const int64_t dh = D / H, Z = B * H, li = ld_qkv, lo = ld_out;
   const float alpha = 1.0f / sqrtf((float)dh);
   // dV_z = P_z^T dO_z
   if (dv)
-    if (int rc = numrs_hip_gemm(ctx, P, S, dout, D, dv, D, S, S, dh, 1, 0, 1.0f, accumulate, Z, H,
-                                H * S * S, S * S, S * D, dh, S * D, dh))
+    if (int rc = numrs_hip_gemm(ctx, P, S, dout, lo, dv, li, S, S, dh, 1, 0, 1.0f, accumulate, Z,
+                                H, H * S * S, S * S, S * lo, dh, S * li, dh))
       return rc;
   if (!dq && !dk) return NUMRS_HIP_OK;
   // dS lives in a block of its own: the dQ/dK products below may split their
@@ -257,22 +268,36 @@ int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float
   numrs_hip::TempBlock dSb(ctx);
   if (int rc = dSb.alloc((size_t)(Z * S * S) * sizeof(float))) return rc;
   float *dP = dSb.f();
-  if (rows_fit(S, dh, D, dout, v, P) && rows_fit(S, dh, D, dout, v, dP) && B * H < 65536) {
+  if (rows_fit(S, dh, lo, li, dout, v, P) && numrs_hip::aligned16(dP) && B * H < 65536) {
     // dS = P * (dP - rowsum(dP * P)) with dP = dO V^T, in one kernel
-    if (int rc = launch_rows<1>(ctx, dout, v, P, dP, B, S, H, D, 1.0f)) return rc;
+    if (int rc = launch_rows<1>(ctx, dout, lo, v, li, P, dP, B, S, H, 1.0f)) return rc;
   } else {
     // dP_z = dO_z V_z^T
-    if (int rc = numrs_hip_gemm(ctx, dout, D, v, D, dP, S, S, dh, S, 0, 1, 1.0f, 0, Z, H, S * D,
-                                dh, S * D, dh, H * S * S, S * S))
+    if (int rc = numrs_hip_gemm(ctx, dout, lo, v, li, dP, S, S, dh, S, 0, 1, 1.0f, 0, Z, H,
+                                S * lo, dh, S * li, dh, H * S * S, S * S))
       return rc;
     // dS = P * (dP - rowsum(dP * P)), in place over dP
     if (int rc = numrs_hip_softmax_backward(ctx, P, dP, dP, Z * S, S, 0)) return rc;
   }
   // dQ_z = alpha * dS_z K_z ;  dK_z = alpha * dS_z^T Q_z  (one launch for both)
   const numrs_hip::BatchedMat dS{dP, S, H * S * S, S * S};
-  const numrs_hip::BatchedMat Km{k, D, S * D, dh}, Qm{q, D, S * D, dh};
-  const numrs_hip::BatchedOut dQ{dq, D, S * D, dh}, dK{dk, D, S * D, dh};
+  const numrs_hip::BatchedMat Km{k, li, S * li, dh}, Qm{q, li, S * li, dh};
+  const numrs_hip::BatchedOut dQ{dq, li, S * li, dh}, dK{dk, li, S * li, dh};
   return numrs_hip::gemm_nn_tn_pair(ctx, dS, Km, dQ, Qm, dK, S, S, dh, alpha, accumulate, Z, H);
+}
+
+int numrs_hip_attention_forward(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,
+                                float *P, float *out, int64_t B, int64_t S, int64_t H,
+                                int64_t D) {
+  return numrs_hip_attention_forward_strided(ctx, q, k, v, D, P, out, D, B, S, H, D);
+}
+
+int numrs_hip_attention_backward(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                 const float *v, const float *P, const float *dout, float *dq,
+                                 float *dk, float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
+                                 int accumulate) {
+  return numrs_hip_attention_backward_strided(ctx, q, k, v, D, P, dout, D, dq, dk, dv, B, S, H, D,
+                                              accumulate);
 }
 
 }  // extern "C"

@@ -442,7 +442,23 @@ int bw_layernorm(const T &out, const float *g, Node &n) {
                                       n.saved[1]->ptr, nullptr, nullptr, db, rows, cols, 0, 0, 1);
 }
 
+// Attention over one packed projection qkv [B*S, 3D]: its grad is written (or
+// added) as the packed [B*S, 3D] block dq | dk | dv.
+int bw_attention_packed(const T &out, const float *g, Node &n) {
+  const T &qkv = n.inputs[0];
+  if (!qkv->requires_grad) return NUMRS_HIP_OK;
+  const int64_t D = out->shape[1];
+  const float *p = qkv->data->ptr;
+  float *d;
+  int acc;
+  if (int rc = grad_target(qkv, &d, &acc)) return rc;
+  return numrs_hip_attention_backward_strided(out->ctx, p, p + D, p + 2 * D, 3 * D,
+                                              n.saved[0]->ptr, g, D, d, d + D, d + 2 * D,
+                                              n.dims[0], n.dims[1], n.dims[2], D, acc);
+}
+
 int bw_attention(const T &out, const float *g, Node &n) {
+  if (n.inputs.size() == 1) return bw_attention_packed(out, g, n);
   const T &q = n.inputs[0], &k = n.inputs[1], &v = n.inputs[2];
   float *dq = nullptr, *dk = nullptr, *dv = nullptr;
   int aq = 1, ak = 1, av = 1;
@@ -980,6 +996,34 @@ int op_attention(const T &q, const T &k, const T &v, int64_t B, int64_t S, int64
   return NUMRS_HIP_OK;
 }
 
+// Attention over a packed projection qkv [B*S, 3D]: q, k, v are its column
+// blocks (row stride 3D), the output is [B*S, D].
+int op_attention_qkv(const T &qkv, int64_t B, int64_t S, int64_t H, T *out) {
+  numrs_hip_ctx *ctx = qkv->ctx;
+  if (qkv->shape.size() != 2 || qkv->shape[1] % 3 != 0)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "attention_qkv: qkv must be [batch*seq, 3*dim]");
+  const int64_t D = qkv->shape[1] / 3;
+  if (B <= 0 || S <= 0 || H <= 0 || qkv->shape[0] != B * S || D % H != 0)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "attention_qkv: rows != batch*seq or dim %% heads != 0");
+  const bool rec = recording({&qkv});
+  T r;
+  if (int rc = make_tensor(ctx, {B * S, D}, rec, &r)) return rc;
+  Buf P;
+  if (int rc = alloc_buf(ctx, B * H * S * S, sizeof(float), &P)) return rc;
+  const float *p = qkv->data->ptr;
+  if (int rc = numrs_hip_attention_forward_strided(ctx, p, p + D, p + 2 * D, 3 * D, P->ptr,
+                                                   r->data->ptr, D, B, S, H, D))
+    return rc;
+  if (rec) {
+    attach(r, Op::Attention, {qkv}, 0, 0.f, {P});
+    r->node->dims[0] = B;
+    r->node->dims[1] = S;
+    r->node->dims[2] = H;
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Optimizers (optim/base.rs, sgd.rs, adam.rs)
 // ---------------------------------------------------------------------------
@@ -1496,6 +1540,14 @@ int numrs_hip_tensor_attention(numrs_hip_tensor *q, numrs_hip_tensor *k, numrs_h
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_attention(q->t, k->t, v->t, batch, seq, heads, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_attention_qkv(numrs_hip_tensor *qkv, int64_t batch, int64_t seq,
+                                   int64_t heads, numrs_hip_tensor **out) {
+  if (qkv == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_attention_qkv(qkv->t, batch, seq, heads, &r)) return rc;
   return wrap(std::move(r), out);
 }
 

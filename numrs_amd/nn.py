@@ -141,23 +141,55 @@ class Sequential(Module):
 
 
 class MultiHeadAttention(Module):
-    """Self-attention projections + fused attention node (no reference op)."""
+    """Self-attention projections + fused attention node (no reference op).
+
+    By default (`fused_qkv`) the q, k and v projections are one Linear to 3d
+    features, W_qkv = [W_q; W_k; W_v] and b_qkv = [b_q; b_k; b_v], whose packed
+    [batch*seq, 3d] output the attention node reads in place: one product
+    forward and one product pair backward instead of three.  `fused_qkv =
+    False` keeps three Linear layers; both give the same values and grads."""
+
+    fused_qkv = True
 
     def __init__(self, wq, wk, wv, wo, heads: int, ctx=None):
         d = np.asarray(wq).shape[0]
         z = np.zeros(d, np.float32)
-        self.heads = heads
-        self.q = Linear.with_weights(d, d, wq, z, ctx)
-        self.k = Linear.with_weights(d, d, wk, z, ctx)
-        self.v = Linear.with_weights(d, d, wv, z, ctx)
+        self.heads, self.dim = heads, d
+        if self.fused_qkv:
+            w = np.concatenate([np.asarray(a, np.float32).reshape(d, d) for a in (wq, wk, wv)])
+            self.qkv = Linear.with_weights(d, 3 * d, w, np.zeros(3 * d, np.float32), ctx)
+            self.projections = [self.qkv]
+        else:
+            self.q = Linear.with_weights(d, d, wq, z, ctx)
+            self.k = Linear.with_weights(d, d, wk, z, ctx)
+            self.v = Linear.with_weights(d, d, wv, z, ctx)
+            self.projections = [self.q, self.k, self.v]
         self.o = Linear.with_weights(d, d, wo, z, ctx)
 
     def forward_seq(self, x: Tensor, batch: int, seq: int) -> Tensor:
-        a = self.q(x).attention(self.k(x), self.v(x), batch, seq, self.heads)
+        if self.fused_qkv:
+            a = self.qkv(x).attention_qkv(batch, seq, self.heads)
+        else:
+            a = self.q(x).attention(self.k(x), self.v(x), batch, seq, self.heads)
         return self.o(a)
 
+    def projection_grads(self) -> dict:
+        """Gradients of the q, k, v projections as wq, wk, wv [d, d] and bq,
+        bk, bv [d], from either form."""
+        d = self.dim
+        if not self.fused_qkv:
+            out = {f"w{n}": getattr(self, n).weight.gradient() for n in ("q", "k", "v")}
+            out.update({f"b{n}": getattr(self, n).bias.gradient() for n in ("q", "k", "v")})
+            return out
+        gw, gb = self.qkv.weight.gradient(), self.qkv.bias.gradient()
+        out = {}
+        for i, n in enumerate(("q", "k", "v")):
+            out[f"w{n}"] = gw[i * d:(i + 1) * d]
+            out[f"b{n}"] = gb[i * d:(i + 1) * d]
+        return out
+
     def parameters(self) -> list[Tensor]:
-        return [p for m in (self.q, self.k, self.v, self.o) for p in m.parameters()]
+        return [p for m in self.projections + [self.o] for p in m.parameters()]
 
 
 class TransformerEncoderBlock(Module):

@@ -55,6 +55,42 @@ def test_attention_forward_backward(hip_ctx, B, S, H, D):
                        what="dk")
 
 
+@pytest.mark.parametrize("B,S,H,D", [(16, 256, 8, 512), (2, 128, 2, 128), (2, 40, 4, 64)])
+@pytest.mark.parametrize("acc", [0, 1])
+def test_attention_strided_packed_qkv(hip_ctx, B, S, H, D, acc):
+    """q, k, v (and dq, dk, dv) as the column blocks of one packed [B*S, 3D]
+    buffer (row stride 3D): the fused row-block path (dh = 64, S % 128 == 0)
+    and the GEMM fallback, written and accumulated."""
+    from numrs_amd import _lib as L
+    print(f"[gpu] attention strided B={B} S={S} H={H} D={D} acc={acc}", flush=True)
+    rng = np.random.default_rng(3 * B + S)
+    qkv, dO, prev = rand(rng, (B * S, 3 * D)), rand(rng, (B * S, D)), rand(rng, (B * S, 3 * D))
+    c = hip_ctx
+    qd, gd = c.to_device(qkv), c.to_device(dO)
+    P, out = c.empty((B * H, S, S)), c.empty((B * S, D))
+    f4 = 4  # bytes per float
+    lib = L.load()
+    assert lib.numrs_hip_attention_forward_strided(
+        c.handle, qd.ptr, qd.ptr + D * f4, qd.ptr + 2 * D * f4, 3 * D, P.ptr, out.ptr, D,
+        B, S, H, D) == 0
+    q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    Pr, Q, K, V = _mha_ref(q, k, v, B, S, H)
+    dh = D // H
+    assert_contraction(out.numpy(), TO._merge(Pr @ V, B, S), S, what="out")
+    dqkv = c.to_device(prev) if acc else c.zeros((B * S, 3 * D))
+    assert lib.numrs_hip_attention_backward_strided(
+        c.handle, qd.ptr, qd.ptr + D * f4, qd.ptr + 2 * D * f4, 3 * D, P.ptr, gd.ptr, D,
+        dqkv.ptr, dqkv.ptr + D * f4, dqkv.ptr + 2 * D * f4, B, S, H, D, acc) == 0
+    dA = TO._heads(dO.astype(np.float64), B, S, H)
+    dP = dA @ V.transpose(0, 1, 3, 2)
+    dS = Pr * (dP - (dP * Pr).sum(-1, keepdims=True)) / math.sqrt(dh)
+    ref = np.concatenate([TO._merge(dS @ K, B, S), TO._merge(dS.transpose(0, 1, 3, 2) @ Q, B, S),
+                          TO._merge(Pr.transpose(0, 1, 3, 2) @ dA, B, S)], axis=1)
+    if acc:
+        ref = ref + prev.astype(np.float64)
+    assert_contraction(dqkv.numpy(), ref, S + dh, what="dqkv (packed)")
+
+
 def L_attention_fwd(c, q, k, v, P, out, B, S, H, D):
     from numrs_amd import _lib as L
     return L.load().numrs_hip_attention_forward(c.handle, q.ptr, k.ptr, v.ptr, P.ptr, out.ptr,
@@ -96,12 +132,14 @@ def _run_block(dims_full, seed):
     return w, x, t, dims, blk, xt, loss, y
 
 
+@pytest.mark.parametrize("fused_qkv", [True, False], ids=["qkv_fused", "qkv_separate"])
 @pytest.mark.parametrize("dims_full", [dict(B=2, S=64, D=128, H=4, F=256),
                                        dict(B=16, S=256, D=512, H=8, F=2048)],
                          ids=["small", "baseline"])
-def test_c4_block_matches_oracle(hip_ctx, dims_full):
-    print(f"[gpu] C4 block {dims_full}", flush=True)
+def test_c4_block_matches_oracle(hip_ctx, dims_full, fused_qkv, monkeypatch):
+    print(f"[gpu] C4 block {dims_full} fused_qkv={fused_qkv}", flush=True)
     nr.set_default_context(hip_ctx)
+    monkeypatch.setattr(nn.MultiHeadAttention, "fused_qkv", fused_qkv)
     w, x, t, dims, blk, xt, loss, y = _run_block(dims_full, seed=4)
     ref_loss, g, ref_y = TO.block(w, x, t, dims)
     # The same chain in fp32 on the CPU: the error scale an fp32 CPU
@@ -109,10 +147,15 @@ def test_c4_block_matches_oracle(hip_ctx, dims_full):
     _, g32, y32 = TO.block(w, x, t, dims, dtype=np.float32)
     assert abs(loss.item() - ref_loss) <= 1e-5 * abs(ref_loss)
     assert_chain(y.values(), ref_y, y32, what="y")
-    got = {"wq": blk.attn.q.weight, "wk": blk.attn.k.weight, "wv": blk.attn.v.weight,
-           "wo": blk.attn.o.weight, "w1": blk.ff1.weight, "w2": blk.ff2.weight,
+    got = {"wo": blk.attn.o.weight, "w1": blk.ff1.weight, "w2": blk.ff2.weight,
            "ln1_gamma": blk.ln1.gamma, "ln1_beta": blk.ln1.beta, "ln2_gamma": blk.ln2.gamma,
-           "ln2_beta": blk.ln2.beta, "bq": blk.attn.q.bias, "bo": blk.attn.o.bias,
-           "c1": blk.ff1.bias, "c2": blk.ff2.bias, "x": xt}
-    for name, tensor in got.items():
-        assert_chain(tensor.gradient(), g[name], g32[name], what=name)
+           "ln2_beta": blk.ln2.beta, "bo": blk.attn.o.bias, "c1": blk.ff1.bias,
+           "c2": blk.ff2.bias, "x": xt}
+    grads = {name: tensor.gradient() for name, tensor in got.items()}
+    proj = blk.attn.projection_grads()
+    grads.update({n: proj[n] for n in ("wq", "wk", "wv", "bq", "bv")})
+    for name, gg in grads.items():
+        assert_chain(gg, g[name], g32[name], what=name)
+    # The key bias gets no gradient (softmax is shift-invariant along a row):
+    # exactly zero in the float64 oracle, rounding noise here.
+    assert np.abs(proj["bk"]).max() <= 1e-5 * np.abs(g["bq"]).max() + 1e-12
