@@ -270,12 +270,61 @@ struct SplitSet {
   float alpha;
 };
 
+// Column sums out[c] (+)= sum_r g[r ldg + c] of a [rows, cols] block in one
+// pass (the Linear backward's bias gradient, carried by the launch that
+// reduces the weight gradient's splits).  A workgroup owns 16 columns (four
+// float4 groups, cols % 4 == 0) and 64 row classes: thread (class k, group
+// j) adds rows k, k + 64, ... in order, 16 loads in flight, and the 64 class
+// sums of a column are added in class order through LDS -- deterministic.
+struct ColSum {
+  const float *g;
+  float *out;
+  int64_t rows, cols, ldg;
+  int acc;
+};
+constexpr int kColSumCols = 16;
+
+__device__ __forceinline__ void colsum_block(const ColSum &c, int64_t blk) {
+  __shared__ f4 red[64 * 4];
+  const int j = threadIdx.x & 3, k = threadIdx.x >> 2;
+  const int64_t col = blk * kColSumCols + 4 * j;
+  f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (col < c.cols) {
+    const float *p = c.g + col;
+    for (int64_t r0 = k; r0 < c.rows; r0 += 64 * 16) {
+      f4 v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int64_t r = r0 + 64 * u;
+        v[u] = r < c.rows ? *reinterpret_cast<const f4 *>(p + r * c.ldg) : f4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += v[u];
+    }
+  }
+  red[k * 4 + j] = s;
+  __syncthreads();
+  if (threadIdx.x < kColSumCols) {
+    const int cc = threadIdx.x, jj = cc >> 2, e = cc & 3;
+    float t = 0.0f;
+    for (int kk = 0; kk < 64; ++kk) t += red[kk * 4 + jj][e];
+    const int64_t gc = blk * kColSumCols + cc;
+    if (gc < c.cols) c.out[gc] = c.acc ? c.out[gc] + t : t;
+  }
+}
+
 // Splits are added in order s = 0, 1, ... (deterministic); the loads of a
 // batch of splits are issued before its ordered adds.  blockIdx.y selects one
-// of two products reduced by the same launch.  VEC: four consecutive
-// elements of one row per thread (Q, ldc and the pointers 16-byte aligned).
+// of two products reduced by the same launch, or (y == cs_slot) the column
+// sums `cs`.  VEC: four consecutive elements of one row per thread (Q, ldc
+// and the pointers 16-byte aligned).
 template <bool VEC>
-__global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1) {
+__global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, ColSum cs,
+                                                     int cs_slot) {
+  if ((int)blockIdx.y == cs_slot) {
+    if ((int64_t)blockIdx.x * kColSumCols < cs.cols) colsum_block(cs, blockIdx.x);
+    return;
+  }
   const SplitSet &d = blockIdx.y ? s1 : s0;
   typedef typename std::conditional<VEC, f4, float>::type V;
   constexpr int kW = VEC ? 4 : 1;
@@ -780,15 +829,24 @@ void apply_splits(Gemm &g, int splits, float *partial) {
   g.partial = partial;
 }
 
+// Whether the column sums of g [rows, cols] (row stride ldg) can ride in the
+// split-reduce launch: float4 column groups and at most 8192 rows (a
+// workgroup walks every row of its 16 columns).
+bool colsum_fits(const float *g, int64_t rows, int64_t cols, int64_t ldg) {
+  return cols % 4 == 0 && ldg % 4 == 0 && numrs_hip::aligned16(g) && rows <= 8192 &&
+         (cols + kColSumCols - 1) / kColSumCols <= 0x7fffffff;
+}
+
 // Reduces the split products among a and b (either may be null or unsplit)
-// with one launch.
-int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b) {
+// with one launch, which also forms the column sums `cs` when given (then the
+// launch is made even when nothing was split).
+int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum *cs = nullptr) {
   const Gemm *g[2];
   int m = 0;
   if (a != nullptr && a->splits > 1) g[m++] = a;
   if (b != nullptr && b->splits > 1) g[m++] = b;
-  if (m == 0) return NUMRS_HIP_OK;
-  SplitSet set[2];
+  if (m == 0 && cs == nullptr) return NUMRS_HIP_OK;
+  SplitSet set[2] = {};
   bool vec = true;
   int64_t most = 0;
   for (int i = 0; i < m; ++i) {
@@ -800,14 +858,21 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b) {
     most = std::max(most, set[i].n);
   }
   if (m == 1) set[1] = set[0];
-  const int64_t blocks = (most / (vec ? 4 : 1) + 255) / 256;
+  int64_t blocks = (most / (vec ? 4 : 1) + 255) / 256;
+  ColSum c{};
+  int slot = -1;
+  if (cs != nullptr) {
+    c = *cs;
+    slot = m;
+    blocks = std::max<int64_t>(blocks, (c.cols + kColSumCols - 1) / kColSumCols);
+  }
   if (blocks > 0x7fffffff)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "splitk_reduce: too large");
-  dim3 grid((unsigned)blocks, (unsigned)m);
+  dim3 grid((unsigned)std::max<int64_t>(blocks, 1), (unsigned)(m + (cs != nullptr)));
   if (vec)
-    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1]);
+    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, slot);
   else
-    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1]);
+    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, slot);
   return numrs_hip::check_launch(ctx, "splitk_reduce");
 }
 
@@ -1190,11 +1255,18 @@ int gemm_general(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B
 // Launches a (first, TN-second) product pair in one grid with per-product
 // split-K; `first_nt` selects the NT (matmul_backward dA) or NN (Linear dx)
 // layout of the first product.  Either product may be absent (C == null).
-int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char *who) {
+// `cs` (optional): column sums that the pair's split-reduce launch forms too
+// (or a launch of their own when neither product is split).
+int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char *who,
+                const ColSum *cs = nullptr) {
   const bool has_a = ga.C != nullptr, has_b = gb.C != nullptr;
-  if (!has_a && !has_b) return NUMRS_HIP_OK;
-  if (!has_a) return gemm_dispatch(ctx, gb, 1, false, false);
-  if (!has_b) return gemm_dispatch(ctx, ga, 1, true, first_nt);
+  if (!has_a && !has_b) return cs ? reduce_splits(ctx, nullptr, nullptr, cs) : NUMRS_HIP_OK;
+  if (!has_a || !has_b) {
+    if (int rc = has_a ? gemm_dispatch(ctx, ga, 1, true, first_nt)
+                       : gemm_dispatch(ctx, gb, 1, false, false))
+      return rc;
+    return cs ? reduce_splits(ctx, nullptr, nullptr, cs) : NUMRS_HIP_OK;
+  }
   StreamPlan pl;
   if (plan_streamed(ctx, ga, true, first_nt, &gb, &pl)) {
     Gemm sa = ga, sb = gb;
@@ -1210,7 +1282,7 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
     else
       linear_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)na);
     if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
-    return reduce_splits(ctx, &sa, &sb);
+    return reduce_splits(ctx, &sa, &sb, cs);
   }
   // Joint split plan, balanced by work: the pair shares one grid, and a
   // workgroup's time is its number of reduction tiles.  The weight gradient
@@ -1256,7 +1328,7 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
     else gemm_pair_kernel<true, false, false><<<grid, kThreads, 0, ctx->stream>>>(ga, gb, (int)ta);
   }
   if (int rc = numrs_hip::check_launch(ctx, "gemm_pair_kernel")) return rc;
-  return reduce_splits(ctx, &ga, &gb);
+  return reduce_splits(ctx, &ga, &gb, cs);
 }
 
 }  // namespace
@@ -1348,12 +1420,22 @@ int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x
       if (int rc = numrs_hip_fill(ctx, dx, T * in, 0.0f)) return rc;
     if (dW && !acc_dw && out * in > 0)
       if (int rc = numrs_hip_fill(ctx, dW, out * in, 0.0f)) return rc;
-  } else if (in > 0) {
-    // dx[T,in] = g[T,out] @ W[out,in] : X = g (R-contig), Y = W (Q-contig)  [NN]
-    Gemm gx = make(g, W, dx, out, in, in, 0, 0, 0, T, in, out, acc_dx);
-    // dW[out,in] = g^T @ x : X = g^T (P-contig), Y = x (Q-contig)          [TN]
-    Gemm gw = make(g, x, dW, out, in, in, 0, 0, 0, out, in, T, acc_dw);
-    if (int rc = launch_pair(ctx, gx, gw, false, who)) return rc;
+  } else {
+    // db = column sums of g (CORRECT mode), formed by the launch that reduces
+    // the pair's splits rather than by two launches of its own
+    ColSum cs{g, db, T, out, out, acc_db};
+    const bool fuse_db = db != nullptr && mode == NUMRS_HIP_UNBROADCAST_CORRECT &&
+                         colsum_fits(g, T, out, out);
+    if (in > 0) {
+      // dx[T,in] = g[T,out] @ W[out,in] : X = g (R-contig), Y = W (Q-contig)  [NN]
+      Gemm gx = make(g, W, dx, out, in, in, 0, 0, 0, T, in, out, acc_dx);
+      // dW[out,in] = g^T @ x : X = g^T (P-contig), Y = x (Q-contig)          [TN]
+      Gemm gw = make(g, x, dW, out, in, in, 0, 0, 0, out, in, T, acc_dw);
+      if (int rc = launch_pair(ctx, gx, gw, false, who, fuse_db ? &cs : nullptr)) return rc;
+    } else if (fuse_db) {
+      if (int rc = reduce_splits(ctx, nullptr, nullptr, &cs)) return rc;
+    }
+    if (fuse_db) return NUMRS_HIP_OK;
   }
   if (db == nullptr || out == 0) return NUMRS_HIP_OK;
   const int64_t gs[2] = {T, out};

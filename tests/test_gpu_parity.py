@@ -724,11 +724,17 @@ def test_matmul_forward_split_k_long_reduction(hip_ctx, rng):
     assert_contraction(C.numpy(), A.astype(np.float64) @ B.astype(np.float64), 8192)
 
 
-# (4096, 512, 2048), (4096, 2048, 512) and (4096, 512, 512) are the C4 block's
-# Linear shapes: the streamed 256 x 128 path with split-K ranges planned per
-# product (dx and dW in one grid, each reduced in split order).
+# (4096, 512, 2048), (4096, 2048, 512), (4096, 512, 512) and (4096, 512, 1536)
+# (the packed q/k/v projection) are the C4 block's Linear shapes: the streamed
+# 256 x 128 path with split-K ranges planned per product (dx and dW in one
+# grid, each reduced in split order).  The bias gradient (CORRECT mode) is
+# formed by the split-reduce launch for float4 columns and up to 8192 rows:
+# (8192, 64, 100) ends on a partial 16-column group; (9000, 32, 64) and
+# (130, 96, 18) take the two-pass column reduce.
 @pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (64, 128, 10), (4096, 512, 2048),
-                                        (4096, 2048, 512), (4096, 512, 512), (33, 17, 5)])
+                                        (4096, 2048, 512), (4096, 512, 512), (4096, 512, 1536),
+                                        (8192, 64, 100), (9000, 32, 64), (130, 96, 18),
+                                        (33, 17, 5)])
 def test_linear_forward_backward(hip_ctx, rng, T, fin, fout):
     # Linear::forward (nn.rs:217-235) and the grads its Transpose/MatMul/Add
     # nodes produce (backward.rs:43-54, 113-149, 305-312).
