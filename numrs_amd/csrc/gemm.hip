@@ -272,45 +272,58 @@ struct SplitSet {
 
 // Column sums out[c] (+)= sum_r g[r ldg + c] of a [rows, cols] block in one
 // pass (the Linear backward's bias gradient, carried by the launch that
-// reduces the weight gradient's splits).  A workgroup owns 16 columns (four
-// float4 groups, cols % 4 == 0) and 64 row classes: thread (class k, group
-// j) adds rows k, k + 64, ... in order, 16 loads in flight, and the 64 class
-// sums of a column are added in class order through LDS -- deterministic.
+// reduces the weight gradient's splits).  A workgroup owns four columns (one
+// float4 group, cols % 4 == 0) and 256 row classes: thread k adds rows k,
+// k + 256, ... in order, 16 loads in flight (all of a 4096-row block at
+// once); the 256 class sums of a column are then added through LDS in a
+// fixed order (64 sums of four consecutive classes, then those 64 in order)
+// -- deterministic.  Consecutive column groups run on one XCD, so the
+// workgroups that share a cache line read it through the same L2.
 struct ColSum {
   const float *g;
   float *out;
   int64_t rows, cols, ldg;
   int acc;
 };
-constexpr int kColSumCols = 16;
+constexpr int kColSumCols = 4;
 
 __device__ __forceinline__ void colsum_block(const ColSum &c, int64_t blk) {
-  __shared__ f4 red[64 * 4];
-  const int j = threadIdx.x & 3, k = threadIdx.x >> 2;
-  const int64_t col = blk * kColSumCols + 4 * j;
+  __shared__ f4 red[256];
+  const int k = threadIdx.x;
+  const float *p = c.g + blk * kColSumCols;
   f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (col < c.cols) {
-    const float *p = c.g + col;
-    for (int64_t r0 = k; r0 < c.rows; r0 += 64 * 16) {
-      f4 v[16];
+  for (int64_t r0 = k; r0 < c.rows; r0 += 256 * 16) {
+    f4 v[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int64_t r = r0 + 64 * u;
-        v[u] = r < c.rows ? *reinterpret_cast<const f4 *>(p + r * c.ldg) : f4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int u = 0; u < 16; ++u) s += v[u];
+    for (int u = 0; u < 16; ++u) {
+      const int64_t r = r0 + 256 * u;
+      v[u] = r < c.rows ? *reinterpret_cast<const f4 *>(p + r * c.ldg) : f4{0.f, 0.f, 0.f, 0.f};
     }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) s += v[u];
   }
-  red[k * 4 + j] = s;
+  red[k] = s;
   __syncthreads();
-  if (threadIdx.x < kColSumCols) {
-    const int cc = threadIdx.x, jj = cc >> 2, e = cc & 3;
-    float t = 0.0f;
-    for (int kk = 0; kk < 64; ++kk) t += red[kk * 4 + jj][e];
-    const int64_t gc = blk * kColSumCols + cc;
-    if (gc < c.cols) c.out[gc] = c.acc ? c.out[gc] + t : t;
+  f4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (k < 64) t = ((red[4 * k] + red[4 * k + 1]) + red[4 * k + 2]) + red[4 * k + 3];
+  __syncthreads();
+  if (k < 64) red[k] = t;
+  __syncthreads();
+  if (k < kColSumCols) {
+    float u = 0.0f;
+    for (int kk = 0; kk < 64; ++kk) u += red[kk][k];
+    const int64_t gc = blk * kColSumCols + k;
+    c.out[gc] = c.acc ? c.out[gc] + u : u;
   }
+}
+
+// Workgroup b of a launch row of n workgroups (hardware ids go to the eight
+// XCDs in turn, n % 8 == 0) -> column group, so that XCD x owns groups
+// [x m/8, (x+1) m/8) of the m groups; -1 for a workgroup with no group.
+__device__ __forceinline__ int64_t colsum_group(int b, int n, int64_t m) {
+  if ((n & 7) != 0 || (m & 7) != 0) return b < m ? b : -1;
+  const int64_t idx = b >> 3;
+  return idx < (m >> 3) ? (b & 7) * (m >> 3) + idx : -1;
 }
 
 // Splits are added in order s = 0, 1, ... (deterministic); the loads of a
@@ -322,7 +335,8 @@ template <bool VEC>
 __global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, ColSum cs,
                                                      int cs_slot) {
   if ((int)blockIdx.y == cs_slot) {
-    if ((int64_t)blockIdx.x * kColSumCols < cs.cols) colsum_block(cs, blockIdx.x);
+    const int64_t grp = colsum_group(blockIdx.x, gridDim.x, cs.cols / kColSumCols);
+    if (grp >= 0) colsum_block(cs, grp);
     return;
   }
   const SplitSet &d = blockIdx.y ? s1 : s0;
@@ -834,7 +848,7 @@ void apply_splits(Gemm &g, int splits, float *partial) {
 // workgroup walks every row of its 16 columns).
 bool colsum_fits(const float *g, int64_t rows, int64_t cols, int64_t ldg) {
   return cols % 4 == 0 && ldg % 4 == 0 && numrs_hip::aligned16(g) && rows <= 8192 &&
-         (cols + kColSumCols - 1) / kColSumCols <= 0x7fffffff;
+         cols / kColSumCols <= 0x7ffffff0;
 }
 
 // Reduces the split products among a and b (either may be null or unsplit)
@@ -864,7 +878,8 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum
   if (cs != nullptr) {
     c = *cs;
     slot = m;
-    blocks = std::max<int64_t>(blocks, (c.cols + kColSumCols - 1) / kColSumCols);
+    blocks = std::max<int64_t>(blocks, c.cols / kColSumCols);
+    blocks = (blocks + 7) & ~int64_t{7};  // whole rounds of the eight XCDs
   }
   if (blocks > 0x7fffffff)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "splitk_reduce: too large");
@@ -885,6 +900,149 @@ bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
   };
   return ok(d.X, d.ldx, d.bsx, d.bsx2, xrc ? d.R : d.P) &&
          ok(d.Y, d.ldy, d.bsy, d.bsy2, yrc ? d.R : d.Q);
+}
+
+// ---------------------------------------------------------------------------
+// Tiny products (a small batch's MLP layers: [64,784] x [784,128],
+// [64,128] x [128,10] and their gradients).  128 x 128 tiles would leave all
+// but a few CUs idle and walk the reduction serially, so a workgroup owns one
+// 16 x 16 output block and its eight waves split the reduction: wave w takes
+// the 16-wide reduction steps w, w + 8, ..., four v_mfma_f32_16x16x4f32 per
+// step, with operands loaded straight from global memory (L2 serves the reuse
+// across blocks); the eight partial blocks are then added in wave order
+// through LDS -- deterministic.  One launch carries up to two products (a
+// gradient pair) and the column sums of a bias gradient.
+//   MFMA 16x16x4 lane contract (lane l = 16 g + i): A row i at reduction slot
+//   g; B reduction slot g at column i; D column i, rows 4g + v (v = 0..3).
+//   Reduction index k = 16 s + 4 g + j feeds MFMA j of step s at slot g, for
+//   A and B alike.
+constexpr int kTinyWaves = 8;
+constexpr int kTinyThreads = 64 * kTinyWaves;
+constexpr int kTinyU = 8;  // reduction steps per load batch and wave
+constexpr int kTinyColsumCols = 64;
+constexpr int kTinyColsumRows = 8192;
+constexpr int64_t kTinyMacs = int64_t{1} << 24;
+constexpr int kTinyMaxR = 4096;  // at most four load batches per wave
+
+template <bool XRC, bool YRC>
+__device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
+  const int tq_n = (d.Q + 15) >> 4;
+  const int tp = tile / tq_n, tq = tile - tp * tq_n;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int p = tp * 16 + i, q = tq * 16 + i;
+  const int64_t zo = batch / d.binner, zi = batch - zo * d.binner;
+  const float *__restrict__ X = d.X + zo * d.bsx + zi * d.bsx2;
+  const float *__restrict__ Y = d.Y + zo * d.bsy + zi * d.bsy2;
+  float *__restrict__ C = d.C + zo * d.bsc + zi * d.bsc2;
+  const bool pin = p < d.P, qin = q < d.Q;
+  const int steps = (d.R + 15) >> 4;
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = w; s0 < steps; s0 += kTinyWaves * kTinyU) {
+    f4 a[kTinyU], b[kTinyU];
+#pragma unroll
+    for (int u = 0; u < kTinyU; ++u) {
+      const int s = s0 + kTinyWaves * u;  // wave-uniform
+      if (s < steps) {
+        const int k = 16 * s + 4 * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool kin = k + j < d.R;
+          a[u][j] = pin && kin ? X[XRC ? (int64_t)p * d.ldx + k + j : (int64_t)(k + j) * d.ldx + p]
+                               : 0.0f;
+          b[u][j] = qin && kin ? Y[YRC ? (int64_t)q * d.ldy + k + j : (int64_t)(k + j) * d.ldy + q]
+                               : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kTinyU; ++u)
+      if (s0 + kTinyWaves * u < steps)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][j], b[u][j], acc, 0, 0, 0);
+  }
+  __shared__ float part[kTinyWaves][256];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) part[w][(4 * g + v) * 16 + i] = acc[v];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int t = threadIdx.x;
+    float s = part[0][t];
+#pragma unroll
+    for (int ww = 1; ww < kTinyWaves; ++ww) s += part[ww][t];
+    const int pp = tp * 16 + (t >> 4), qq = tq * 16 + (t & 15);
+    if (pp < d.P && qq < d.Q) {
+      float *dst = C + (int64_t)pp * d.ldc + qq;
+      float v = d.alpha * s;
+      if (d.bias != nullptr) v = v + d.bias[qq];
+      *dst = d.accumulate ? *dst + v : v;
+    }
+  }
+}
+
+// Column sums of a small bias gradient: 64 columns per workgroup, thread
+// (class k, column c) adds rows k, k + 8, ... in order, and the eight class
+// sums are added in class order.
+__device__ __forceinline__ void tiny_colsum(const ColSum &c, int blk) {
+  __shared__ float red[kTinyWaves][kTinyColsumCols];
+  const int cl = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blk * kTinyColsumCols + cl;
+  float s = 0.0f;
+  if (col < c.cols) {
+#pragma unroll 8
+    for (int64_t r = k; r < c.rows; r += kTinyWaves) s += c.g[r * c.ldg + col];
+  }
+  red[k][cl] = s;
+  __syncthreads();
+  if (threadIdx.x < kTinyColsumCols && col < c.cols) {
+    float t = red[0][cl];
+#pragma unroll
+    for (int kk = 1; kk < kTinyWaves; ++kk) t += red[kk][cl];
+    c.out[col] = c.acc ? c.out[col] + t : t;
+  }
+}
+
+// Workgroups [0, tiles_a) form product a (layout XA, YA), the next tiles_b
+// product b (TN), the rest (batch 0 only) the column sums cs.
+template <bool XA, bool YA>
+__global__ void __launch_bounds__(kTinyThreads) tiny_gemm_kernel(Gemm a, Gemm b, int tiles_a,
+                                                                 int tiles_b, ColSum cs) {
+  const int t = blockIdx.x;
+  if (t < tiles_a)
+    tiny_tile<XA, YA>(a, t, blockIdx.y);
+  else if (t < tiles_a + tiles_b)
+    tiny_tile<false, false>(b, t - tiles_a, blockIdx.y);
+  else if (blockIdx.y == 0)
+    tiny_colsum(cs, t - tiles_a - tiles_b);
+}
+
+int64_t tiny_tiles(const Gemm &g) { return (int64_t)((g.P + 15) / 16) * ((g.Q + 15) / 16); }
+
+bool tiny_fits(const Gemm &g, int64_t batch) {
+  return g.splits == 1 && g.R <= kTinyMaxR && (int64_t)g.P * g.Q * g.R * batch <= kTinyMacs;
+}
+
+// One launch of the tiny kernel: product a (layout xa, ya), optionally a TN
+// product b, and (batch 1) the column sums cs.
+int launch_tiny(numrs_hip_ctx *ctx, const Gemm &a, bool xa, bool ya, const Gemm *b,
+                int64_t batch, const ColSum *cs) {
+  const int64_t ta = tiny_tiles(a), tb = b != nullptr ? tiny_tiles(*b) : 0;
+  const int64_t tc = cs != nullptr ? (cs->cols + kTinyColsumCols - 1) / kTinyColsumCols : 0;
+  if (ta + tb + tc > 0x7fffffff || batch < 1 || batch > 65535 || (cs != nullptr && batch != 1))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "tiny_gemm: bad launch shape");
+  const dim3 grid((unsigned)(ta + tb + tc), (unsigned)batch);
+  const Gemm &bb = b != nullptr ? *b : a;
+  const ColSum c = cs != nullptr ? *cs : ColSum{};
+  if (xa && ya)
+    tiny_gemm_kernel<true, true><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
+  else if (xa)
+    tiny_gemm_kernel<true, false><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
+  else if (ya)
+    tiny_gemm_kernel<false, true><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
+  else
+    tiny_gemm_kernel<false, false><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
+  return numrs_hip::check_launch(ctx, "tiny_gemm_kernel");
 }
 
 // The streamed path takes whole TP x TQ output tiles and whole reduction
@@ -1078,6 +1236,7 @@ template <bool XRC, bool YRC>
 int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   const int64_t n_tiles = (int64_t)g.tiles_p * g.tiles_q;
   if (n_tiles == 0 || batch == 0) return NUMRS_HIP_OK;
+  if (tiny_fits(g, batch)) return launch_tiny(ctx, g, XRC, YRC, nullptr, batch, nullptr);
   StreamPlan pl;
   if (batch == 1 && plan_streamed(ctx, g, XRC, YRC, nullptr, &pl)) {
     Gemm sg = g;
@@ -1150,6 +1309,8 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   Gemm gb = make(A, dC, dB, K, N, N, sa, sc, sb, K, N, M, acc);
   if (dA == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
   if (dB == nullptr) return gemm_dispatch(ctx, ga, batch, true, true);
+  if (tiny_fits(ga, batch) && tiny_fits(gb, batch))
+    return launch_tiny(ctx, ga, true, true, &gb, batch, nullptr);
   StreamPlan pl;
   if (batch == 1 && plan_streamed(ctx, ga, true, true, &gb, &pl)) {
     Gemm sa = ga, sb = gb;
@@ -1255,11 +1416,24 @@ int gemm_general(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B
 // Launches a (first, TN-second) product pair in one grid with per-product
 // split-K; `first_nt` selects the NT (matmul_backward dA) or NN (Linear dx)
 // layout of the first product.  Either product may be absent (C == null).
-// `cs` (optional): column sums that the pair's split-reduce launch forms too
-// (or a launch of their own when neither product is split).
+// `cs` (optional): column sums that the pair's launch forms too -- the tiny
+// kernel's own workgroups, or the split-reduce launch (a launch of its own
+// when neither product is split) where colsum_fits; *cs_done says whether
+// they were formed.
 int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char *who,
-                const ColSum *cs = nullptr) {
+                const ColSum *cs_in = nullptr, bool *cs_done = nullptr) {
   const bool has_a = ga.C != nullptr, has_b = gb.C != nullptr;
+  if (cs_done != nullptr) *cs_done = false;
+  if ((has_a || has_b) && (!has_a || tiny_fits(ga, 1)) && (!has_b || tiny_fits(gb, 1)) &&
+      (cs_in == nullptr || cs_in->rows <= kTinyColsumRows)) {
+    if (cs_done != nullptr) *cs_done = cs_in != nullptr;
+    if (has_a) return launch_tiny(ctx, ga, true, first_nt, has_b ? &gb : nullptr, 1, cs_in);
+    return launch_tiny(ctx, gb, false, false, nullptr, 1, cs_in);
+  }
+  const ColSum *cs =
+      cs_in != nullptr && colsum_fits(cs_in->g, cs_in->rows, cs_in->cols, cs_in->ldg) ? cs_in
+                                                                                    : nullptr;
+  if (cs_done != nullptr) *cs_done = cs != nullptr;
   if (!has_a && !has_b) return cs ? reduce_splits(ctx, nullptr, nullptr, cs) : NUMRS_HIP_OK;
   if (!has_a || !has_b) {
     if (int rc = has_a ? gemm_dispatch(ctx, ga, 1, true, first_nt)
@@ -1369,6 +1543,8 @@ int numrs_hip::gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, 
   if (C1.p == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
   if (C2.p == nullptr) return gemm_dispatch(ctx, ga, batch, true, false);
   if (batch == 1) return launch_pair(ctx, ga, gb, false, who);
+  if (tiny_fits(ga, batch) && tiny_fits(gb, batch))
+    return launch_tiny(ctx, ga, true, false, &gb, batch, nullptr);
   bool small = false;
   if (pick_batched_stream(ctx, ga, true, false, &gb, batch, &small)) {
     const Gemm sa = as_stream(ga, small), sb = as_stream(gb, small);
@@ -1421,21 +1597,24 @@ int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x
     if (dW && !acc_dw && out * in > 0)
       if (int rc = numrs_hip_fill(ctx, dW, out * in, 0.0f)) return rc;
   } else {
-    // db = column sums of g (CORRECT mode), formed by the launch that reduces
-    // the pair's splits rather than by two launches of its own
+    // db = column sums of g (CORRECT mode), formed by the pair's own launch
+    // (tiny products) or by the launch that reduces its splits, rather than
+    // by two launches of their own
     ColSum cs{g, db, T, out, out, acc_db};
-    const bool fuse_db = db != nullptr && mode == NUMRS_HIP_UNBROADCAST_CORRECT &&
-                         colsum_fits(g, T, out, out);
+    const bool want_db = db != nullptr && mode == NUMRS_HIP_UNBROADCAST_CORRECT;
+    bool db_done = false;
     if (in > 0) {
       // dx[T,in] = g[T,out] @ W[out,in] : X = g (R-contig), Y = W (Q-contig)  [NN]
       Gemm gx = make(g, W, dx, out, in, in, 0, 0, 0, T, in, out, acc_dx);
       // dW[out,in] = g^T @ x : X = g^T (P-contig), Y = x (Q-contig)          [TN]
       Gemm gw = make(g, x, dW, out, in, in, 0, 0, 0, out, in, T, acc_dw);
-      if (int rc = launch_pair(ctx, gx, gw, false, who, fuse_db ? &cs : nullptr)) return rc;
-    } else if (fuse_db) {
+      if (int rc = launch_pair(ctx, gx, gw, false, who, want_db ? &cs : nullptr, &db_done))
+        return rc;
+    } else if (want_db && colsum_fits(g, T, out, out)) {
       if (int rc = reduce_splits(ctx, nullptr, nullptr, &cs)) return rc;
+      db_done = true;
     }
-    if (fuse_db) return NUMRS_HIP_OK;
+    if (db_done) return NUMRS_HIP_OK;
   }
   if (db == nullptr || out == 0) return NUMRS_HIP_OK;
   const int64_t gs[2] = {T, out};
