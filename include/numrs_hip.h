@@ -197,6 +197,23 @@ int numrs_hip_linear_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
 int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x, const float *W,
                               float *dx, float *dW, float *db, int64_t T, int64_t in, int64_t out,
                               int acc_dx, int acc_dw, int acc_db, int mode);
+/* No counterpart in the reference: the Linear layer followed by ReLU
+ * (nn.rs:217-235, then ReLU::forward, nn.rs:306-320), y = max(x @ W^T + b, 0)
+ * with the ReLU forward kernel's x.max(0).  Small products (at most 2^24
+ * multiply-adds, reduction <= 4096) clamp in the product's epilogue; larger
+ * ones run numrs_hip_linear_forward and the ReLU in place. */
+int numrs_hip_linear_relu_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
+                                  const float *b, float *y, int64_t T, int64_t in, int64_t out);
+/* Its backward from g = dL/dy, y the forward's output: the pre-activation
+ * gradient (y > 0) ? g : 0 -- relu_backward's strict mask (backward.rs:152-163);
+ * y > 0 exactly where the pre-activation is > 0 -- then the Linear backward
+ * as numrs_hip_linear_backward.  Small products apply the mask as the GEMM
+ * loads g (dx, dW and db in one launch); larger ones form the masked
+ * gradient first. */
+int numrs_hip_linear_relu_backward(numrs_hip_ctx *ctx, const float *g, const float *y,
+                                   const float *x, const float *W, float *dx, float *dW,
+                                   float *db, int64_t T, int64_t in, int64_t out, int acc_dx,
+                                   int acc_dw, int acc_db, int mode);
 
 /* General strided product, the building block of attention's batched
  * gradients: for z in [0, batch), with zo = z / batch_inner and
@@ -563,6 +580,13 @@ int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
  * one node with Linear::forward's values and gradients (nn.rs:217-235). */
 int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
                             numrs_hip_tensor **out);
+/* No counterpart in the reference: a Linear node followed by ReLU
+ * (nn.rs:217-235, then ReLU::forward, nn.rs:306-320) as one node, y =
+ * max(x @ W^T + b, 0), with numrs_hip_linear_relu_forward/_backward.  Same
+ * values and parameter gradients as the two nodes; the pre-activation is not
+ * a tensor of its own. */
+int numrs_hip_tensor_linear_relu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
+                                 numrs_hip_tensor **out);
 /* LSTM layer node: x [B, T, I] -> h_seq [B, T, H] (numrs_hip_lstm_forward). */
 int numrs_hip_tensor_lstm(numrs_hip_tensor *x, numrs_hip_tensor *w_ih, numrs_hip_tensor *w_hh,
                           numrs_hip_tensor *b, numrs_hip_tensor **out);

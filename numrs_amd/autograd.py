@@ -305,12 +305,15 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_layer_norm(self._h, gamma._h, beta._h, eps,
                                                               ctypes.byref(h)), h)
 
-    def linear(self, weight: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
-        """self @ weight^T + bias as one node (Linear::forward's values and grads)."""
+    def linear(self, weight: "Tensor", bias: "Tensor | None" = None,
+               relu: bool = False) -> "Tensor":
+        """self @ weight^T + bias as one node (Linear::forward's values and
+        grads); relu=True also applies ReLU in the same node (the Linear ->
+        ReLU pair, same values and parameter gradients)."""
         h = ctypes.c_void_p()
-        return self._out(L.load().numrs_hip_tensor_linear(self._h, weight._h,
-                                                          bias._h if bias is not None else None,
-                                                          ctypes.byref(h)), h)
+        fn = L.load().numrs_hip_tensor_linear_relu if relu else L.load().numrs_hip_tensor_linear
+        return self._out(fn(self._h, weight._h, bias._h if bias is not None else None,
+                            ctypes.byref(h)), h)
 
     def lstm(self, w_ih: "Tensor", w_hh: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
         """LSTM layer over self [B, T, I] -> hidden states [B, T, H]."""

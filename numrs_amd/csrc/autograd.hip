@@ -516,15 +516,21 @@ int bw_linear(const T &out, const float *g, Node &n) {
     if (int rc = grad_target(W, &dW, &aw)) return rc;
   if (b && (*b)->requires_grad)
     if (int rc = grad_target(*b, &db, &ab)) return rc;
-  if (int rc = numrs_hip_linear_backward(ctx, g, x->data->ptr, W->data->ptr, dx, dW, db, Tn, in,
-                                         outf, ax, aw, ab, ctx->unbroadcast_mode))
-    return rc;
+  // n.kind = 1: the output went through ReLU; its saved value masks g.
+  const float *y = out->data->ptr;
+  auto run = [&](float *dx_, float *dW_, float *db_, int ax_, int aw_, int ab_) {
+    if (n.kind == 1)
+      return numrs_hip_linear_relu_backward(ctx, g, y, x->data->ptr, W->data->ptr, dx_, dW_, db_,
+                                            Tn, in, outf, ax_, aw_, ab_, ctx->unbroadcast_mode);
+    return numrs_hip_linear_backward(ctx, g, x->data->ptr, W->data->ptr, dx_, dW_, db_, Tn, in,
+                                     outf, ax_, aw_, ab_, ctx->unbroadcast_mode);
+  };
+  if (int rc = run(dx, dW, db, ax, aw, ab)) return rc;
   if (shared) {  // x is W: its second gradient adds
     float *t;
     int a;
     if (int rc = grad_target(W, &t, &a)) return rc;
-    return numrs_hip_linear_backward(ctx, g, x->data->ptr, W->data->ptr, nullptr, t, nullptr, Tn,
-                                     in, outf, 0, 1, 0, ctx->unbroadcast_mode);
+    return run(nullptr, t, nullptr, 0, 1, 0);
   }
   return NUMRS_HIP_OK;
 }
@@ -905,7 +911,9 @@ int op_layernorm(const T &x, const T &gamma, const T &beta, float eps, T *out) {
   return NUMRS_HIP_OK;
 }
 
-int op_linear(const T &x, const T &W, const T *b, T *out) {
+// relu = 1: y = ReLU(x W^T + b) as one node (the Linear -> ReLU pair of a
+// Sequential), whose backward masks g by y > 0 before the Linear backward.
+int op_linear(const T &x, const T &W, const T *b, T *out, int relu = 0) {
   numrs_hip_ctx *ctx = x->ctx;
   if (x->shape.size() != 2 || W->shape.size() != 2 || x->shape[1] != W->shape[1])
     return fail(ctx, NUMRS_HIP_E_SHAPE, "linear expects x [T,in], W [out,in]");
@@ -914,14 +922,14 @@ int op_linear(const T &x, const T &W, const T *b, T *out) {
   const bool rec = b ? recording({&x, &W, b}) : recording({&x, &W});
   T r;
   if (int rc = make_tensor(ctx, {x->shape[0], W->shape[0]}, rec, &r)) return rc;
-  if (int rc = numrs_hip_linear_forward(ctx, x->data->ptr, W->data->ptr,
-                                        b ? (*b)->data->ptr : nullptr, r->data->ptr, x->shape[0],
-                                        x->shape[1], W->shape[0]))
+  auto fwd = relu ? numrs_hip_linear_relu_forward : numrs_hip_linear_forward;
+  if (int rc = fwd(ctx, x->data->ptr, W->data->ptr, b ? (*b)->data->ptr : nullptr, r->data->ptr,
+                   x->shape[0], x->shape[1], W->shape[0]))
     return rc;
   if (rec) {
     std::vector<T> ins{x, W};
     if (b) ins.push_back(*b);
-    attach(r, Op::Linear, std::move(ins));
+    attach(r, Op::Linear, std::move(ins), relu);
   }
   *out = std::move(r);
   return NUMRS_HIP_OK;
@@ -1516,6 +1524,14 @@ int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_
   if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_linear_relu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
+                                 numrs_hip_tensor **out) {
+  if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r, 1)) return rc;
   return wrap(std::move(r), out);
 }
 

@@ -170,7 +170,7 @@ __global__ void __launch_bounds__(kBlock)
 template <int KIND, int VEC>
 __global__ void __launch_bounds__(kBlock)
     reduce_pass1(const float *__restrict__ x, const float *__restrict__ t, int64_t n,
-                 float *__restrict__ partial) {
+                 float *__restrict__ partial, float div) {
   __shared__ float red[kBlock / 64];
   auto term = [&](float xv, float tv) {
     if (KIND == 0) return xv;
@@ -218,7 +218,10 @@ __global__ void __launch_bounds__(kBlock)
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
-  if (threadIdx.x == 0) partial[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+  if (threadIdx.x == 0) {
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    partial[blockIdx.x] = gridDim.x == 1 ? tot / div : tot;  // a lone block writes the result
+  }
 }
 
 // out[0] = (sum of partials) / div   (div = 1 for a plain sum)
@@ -374,18 +377,23 @@ int full_reduce(numrs_hip_ctx *ctx, int kind, const float *x, const float *t, in
   int64_t blocks = (n + kBlock * 16 - 1) / (kBlock * 16);
   if (blocks < 1) blocks = 1;
   if (blocks > cus) blocks = cus;
-  void *ws = nullptr;
-  if (int rc = numrs_hip::workspace(ctx, (size_t)blocks * sizeof(float), &ws)) return rc;
-  float *partial = static_cast<float *>(ws);
+  // A single block (n <= 4096) divides and writes `out` itself.
+  float *partial = out;
+  if (blocks > 1) {
+    void *ws = nullptr;
+    if (int rc = numrs_hip::workspace(ctx, (size_t)blocks * sizeof(float), &ws)) return rc;
+    partial = static_cast<float *>(ws);
+  }
   const bool vec = numrs_hip::aligned16(x) && (kind == 0 || numrs_hip::aligned16(t));
   const unsigned grid = (unsigned)blocks;
   numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
     if (kind == 0)
-      reduce_pass1<0, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+      reduce_pass1<0, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial, div);
     else
-      reduce_pass1<1, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial);
+      reduce_pass1<1, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial, div);
   });
   if (int rc = numrs_hip::check_launch(ctx, "reduce_pass1")) return rc;
+  if (blocks == 1) return NUMRS_HIP_OK;
   reduce_final<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, div, out);
   return numrs_hip::check_launch(ctx, "reduce_final");
 }

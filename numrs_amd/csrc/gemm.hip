@@ -78,6 +78,12 @@ struct Gemm {
   // Optional bias added per output column after alpha: C = alpha*X@Y + bias[q]
   // (+ C); the Linear forward's "+ b" folded into the product's epilogue.
   const float *bias;
+  // Tiny kernel only: X entries whose `xmask` entry (same layout and
+  // offsets as X) is not > 0 read as zero (ReLU backward applied on load),
+  // and `relu` clamps the stored result at zero (ReLU forward in the
+  // epilogue).
+  const float *xmask;
+  int relu;
 };
 
 // Loads one 128 x 32 operand tile from global memory into registers
@@ -268,6 +274,7 @@ struct SplitSet {
   int64_t ldc, n;
   int Q, splits, acc;
   float alpha;
+  int relu;  // clamp the result at zero (the Linear+ReLU forward)
 };
 
 // Column sums out[c] (+)= sum_r g[r ldg + c] of a [rows, cols] block in one
@@ -284,6 +291,7 @@ struct ColSum {
   float *out;
   int64_t rows, cols, ldg;
   int acc;
+  const float *mask;  // tiny kernel only (see tiny_colsum)
 };
 constexpr int kColSumCols = 4;
 
@@ -359,7 +367,16 @@ __global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, C
   V *dst = reinterpret_cast<V *>(d.C + p * d.ldc + q);
   V v = d.alpha * s;
   if (d.bias != nullptr) v = v + *reinterpret_cast<const V *>(d.bias + q);
-  *dst = d.acc ? *dst + v : v;
+  v = d.acc ? *dst + v : v;
+  if (d.relu) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
+    } else {
+      v = fmaxf(v, 0.0f);
+    }
+  }
+  *dst = v;
 }
 
 // Maps the hardware workgroup id to a logical tile so that XCD k (which
@@ -866,7 +883,7 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum
   for (int i = 0; i < m; ++i) {
     const Gemm &d = *g[i];
     set[i] = SplitSet{d.partial, d.C, d.bias, d.ldc, (int64_t)d.P * d.Q, d.Q, d.splits,
-                      d.accumulate, d.alpha};
+                      d.accumulate, d.alpha, d.relu};
     vec = vec && d.Q % 4 == 0 && d.ldc % 4 == 0 && numrs_hip::aligned16(d.C) &&
           numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias));
     most = std::max(most, set[i].n);
@@ -918,14 +935,19 @@ bool vec_ok(const Gemm &d, bool xrc, bool yrc) {
 //   A and B alike.
 constexpr int kTinyWaves = 8;
 constexpr int kTinyThreads = 64 * kTinyWaves;
-constexpr int kTinyU = 8;  // reduction steps per load batch and wave
+// Reduction steps per load batch and wave: 8 (143 VGPRs, one workgroup per
+// CU) for reductions over 512, else 4 (79 VGPRs, three per CU).
+constexpr int kTinyUBig = 8, kTinyUSmall = 4;
 constexpr int kTinyColsumCols = 64;
 constexpr int kTinyColsumRows = 8192;
 constexpr int64_t kTinyMacs = int64_t{1} << 24;
 constexpr int kTinyMaxR = 4096;  // at most four load batches per wave
 
-template <bool XRC, bool YRC>
+template <bool XRC, bool YRC, int U>
 __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
+  // Split-K: consecutive logical blocks are the k-ranges of one output block.
+  const int split = tile % d.splits;
+  tile /= d.splits;
   const int tq_n = (d.Q + 15) >> 4;
   const int tp = tile / tq_n, tq = tile - tp * tq_n;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -935,28 +957,42 @@ __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
   const float *__restrict__ X = d.X + zo * d.bsx + zi * d.bsx2;
   const float *__restrict__ Y = d.Y + zo * d.bsy + zi * d.bsy2;
   float *__restrict__ C = d.C + zo * d.bsc + zi * d.bsc2;
+  const float *__restrict__ M = d.xmask != nullptr ? d.xmask + zo * d.bsx + zi * d.bsx2 : nullptr;
   const bool pin = p < d.P, qin = q < d.Q;
-  const int steps = (d.R + 15) >> 4;
+  // This split's 16-wide reduction steps [s_lo, steps); k-tiles are 32 wide.
+  const int s_lo = split * d.ktiles_per_split * 2;
+  const int steps = min((d.R + 15) >> 4, s_lo + d.ktiles_per_split * 2);
+  // Byte offsets from the (wave-uniform) operand bases fit in 32 bits
+  // (tiny_fits), so each load needs one VGPR of address.
+  const char *Xc = reinterpret_cast<const char *>(X), *Yc = reinterpret_cast<const char *>(Y);
+  const char *Mc = reinterpret_cast<const char *>(M);
+  const uint32_t ldx4 = 4u * (uint32_t)d.ldx, ldy4 = 4u * (uint32_t)d.ldy;
+  const uint32_t xo = XRC ? (uint32_t)p * ldx4 : 4u * (uint32_t)p;  // reduction index 0
+  const uint32_t yo = YRC ? (uint32_t)q * ldy4 : 4u * (uint32_t)q;
+  const uint32_t xk = XRC ? 4u : ldx4, yk = YRC ? 4u : ldy4;  // bytes per reduction index
+  auto ld = [](const char *base, uint32_t off) {
+    return *reinterpret_cast<const float *>(base + off);
+  };
   f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = w; s0 < steps; s0 += kTinyWaves * kTinyU) {
-    f4 a[kTinyU], b[kTinyU];
+  for (int s0 = s_lo + w; s0 < steps; s0 += kTinyWaves * U) {
+    f4 a[U], b[U];
 #pragma unroll
-    for (int u = 0; u < kTinyU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int s = s0 + kTinyWaves * u;  // wave-uniform
       if (s < steps) {
         const int k = 16 * s + 4 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const bool kin = k + j < d.R;
-          a[u][j] = pin && kin ? X[XRC ? (int64_t)p * d.ldx + k + j : (int64_t)(k + j) * d.ldx + p]
-                               : 0.0f;
-          b[u][j] = qin && kin ? Y[YRC ? (int64_t)q * d.ldy + k + j : (int64_t)(k + j) * d.ldy + q]
-                               : 0.0f;
+          const uint32_t xoff = xo + (uint32_t)(k + j) * xk;
+          a[u][j] = pin && kin ? ld(Xc, xoff) : 0.0f;
+          if (Mc != nullptr) a[u][j] = pin && kin && ld(Mc, xoff) > 0.0f ? a[u][j] : 0.0f;
+          b[u][j] = qin && kin ? ld(Yc, yo + (uint32_t)(k + j) * yk) : 0.0f;
         }
       }
     }
 #pragma unroll
-    for (int u = 0; u < kTinyU; ++u)
+    for (int u = 0; u < U; ++u)
       if (s0 + kTinyWaves * u < steps)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -972,26 +1008,39 @@ __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
 #pragma unroll
     for (int ww = 1; ww < kTinyWaves; ++ww) s += part[ww][t];
     const int pp = tp * 16 + (t >> 4), qq = tq * 16 + (t & 15);
-    if (pp < d.P && qq < d.Q) {
+    if (pp < d.P && qq < d.Q && d.splits > 1) {
+      d.partial[((int64_t)split * d.P + pp) * d.Q + qq] = s;  // splitk_reduce finishes
+    } else if (pp < d.P && qq < d.Q) {
       float *dst = C + (int64_t)pp * d.ldc + qq;
       float v = d.alpha * s;
       if (d.bias != nullptr) v = v + d.bias[qq];
-      *dst = d.accumulate ? *dst + v : v;
+      v = d.accumulate ? *dst + v : v;
+      if (d.relu) v = fmaxf(v, 0.0f);  // the ReLU forward kernel's x.max(0)
+      *dst = v;
     }
   }
 }
 
 // Column sums of a small bias gradient: 64 columns per workgroup, thread
 // (class k, column c) adds rows k, k + 8, ... in order, and the eight class
-// sums are added in class order.
+// sums are added in class order.  With `mask` (same layout as g), entries
+// whose mask is not > 0 count as zero.
 __device__ __forceinline__ void tiny_colsum(const ColSum &c, int blk) {
   __shared__ float red[kTinyWaves][kTinyColsumCols];
   const int cl = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int64_t col = (int64_t)blk * kTinyColsumCols + cl;
   float s = 0.0f;
   if (col < c.cols) {
+    if (c.mask != nullptr) {
 #pragma unroll 8
-    for (int64_t r = k; r < c.rows; r += kTinyWaves) s += c.g[r * c.ldg + col];
+      for (int64_t r = k; r < c.rows; r += kTinyWaves) {
+        const int64_t idx = r * c.ldg + col;
+        s += c.mask[idx] > 0.0f ? c.g[idx] : 0.0f;
+      }
+    } else {
+#pragma unroll 8
+      for (int64_t r = k; r < c.rows; r += kTinyWaves) s += c.g[r * c.ldg + col];
+    }
   }
   red[k][cl] = s;
   __syncthreads();
@@ -1005,14 +1054,14 @@ __device__ __forceinline__ void tiny_colsum(const ColSum &c, int blk) {
 
 // Workgroups [0, tiles_a) form product a (layout XA, YA), the next tiles_b
 // product b (TN), the rest (batch 0 only) the column sums cs.
-template <bool XA, bool YA>
+template <bool XA, bool YA, int U>
 __global__ void __launch_bounds__(kTinyThreads) tiny_gemm_kernel(Gemm a, Gemm b, int tiles_a,
                                                                  int tiles_b, ColSum cs) {
   const int t = blockIdx.x;
   if (t < tiles_a)
-    tiny_tile<XA, YA>(a, t, blockIdx.y);
+    tiny_tile<XA, YA, U>(a, t, blockIdx.y);
   else if (t < tiles_a + tiles_b)
-    tiny_tile<false, false>(b, t - tiles_a, blockIdx.y);
+    tiny_tile<false, false, U>(b, t - tiles_a, blockIdx.y);
   else if (blockIdx.y == 0)
     tiny_colsum(cs, t - tiles_a - tiles_b);
 }
@@ -1020,29 +1069,80 @@ __global__ void __launch_bounds__(kTinyThreads) tiny_gemm_kernel(Gemm a, Gemm b,
 int64_t tiny_tiles(const Gemm &g) { return (int64_t)((g.P + 15) / 16) * ((g.Q + 15) / 16); }
 
 bool tiny_fits(const Gemm &g, int64_t batch) {
-  return g.splits == 1 && g.R <= kTinyMaxR && (int64_t)g.P * g.Q * g.R * batch <= kTinyMacs;
+  // Each operand's byte extent under either layout stays below 2^31 (the
+  // kernel's 32-bit load offsets).
+  auto span = [](int64_t ext, int64_t other, int64_t ld) {
+    return 4 * std::max((ext - 1) * ld + other, (other - 1) * ld + ext) < (int64_t{1} << 31);
+  };
+  return g.splits == 1 && g.R <= kTinyMaxR && (int64_t)g.P * g.Q * g.R * batch <= kTinyMacs &&
+         span(g.P, g.R, g.ldx) && span(g.Q, g.R, g.ldy);
+}
+
+// Split-K for tiny products with few output blocks and a long reduction
+// (the first MLP layer: 32 blocks over 784): blocks x splits fill the CUs,
+// each split keeping at least four 32-wide k-tiles (a 16-wide step per
+// wave); splitk_reduce then adds the splits in order.  A lone workgroup
+// per CU streaming a long reduction is bound by its outstanding loads.
+int tiny_split(int64_t cus, int64_t blocks, int R) {
+  const int64_t kt = (R + kBR - 1) / kBR;
+  int64_t sp = std::min<int64_t>({(cus + blocks - 1) / blocks, kt / 4, 32});
+  if (sp <= 1) return 1;
+  const int64_t per = (kt + sp - 1) / sp;
+  return (int)((kt + per - 1) / per);
 }
 
 // One launch of the tiny kernel: product a (layout xa, ya), optionally a TN
-// product b, and (batch 1) the column sums cs.
-int launch_tiny(numrs_hip_ctx *ctx, const Gemm &a, bool xa, bool ya, const Gemm *b,
+// product b, and (batch 1) the column sums cs; then the split reduction
+// when a batch-1 product was split.
+int launch_tiny(numrs_hip_ctx *ctx, const Gemm &a_in, bool xa, bool ya, const Gemm *b_in,
                 int64_t batch, const ColSum *cs) {
-  const int64_t ta = tiny_tiles(a), tb = b != nullptr ? tiny_tiles(*b) : 0;
+  Gemm a = a_in, bb = b_in != nullptr ? *b_in : a_in;
+  const Gemm *b = b_in != nullptr ? &bb : nullptr;
+  int64_t ta = tiny_tiles(a), tb = b != nullptr ? tiny_tiles(*b) : 0;
   const int64_t tc = cs != nullptr ? (cs->cols + kTinyColsumCols - 1) / kTinyColsumCols : 0;
   if (ta + tb + tc > 0x7fffffff || batch < 1 || batch > 65535 || (cs != nullptr && batch != 1))
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "tiny_gemm: bad launch shape");
+  int sa = 1, sb = 1;
+  if (batch == 1) {
+    const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    sa = tiny_split(cus, ta + tb, a.R);
+    if (b != nullptr) sb = tiny_split(cus, ta + tb, b->R);
+  }
+  if (sa > 1 || sb > 1) {
+    const size_t na = sa > 1 ? (size_t)sa * a.P * a.Q : 0;
+    const size_t nb = sb > 1 ? (size_t)sb * bb.P * bb.Q : 0;
+    void *ws = nullptr;
+    if (int rc = numrs_hip::workspace(ctx, (na + nb) * sizeof(float), &ws)) return rc;
+    float *base = static_cast<float *>(ws);
+    if (sa > 1) apply_splits(a, sa, base);
+    if (sb > 1) apply_splits(bb, sb, base + na);
+    ta *= sa;
+    tb *= sb;
+  }
   const dim3 grid((unsigned)(ta + tb + tc), (unsigned)batch);
-  const Gemm &bb = b != nullptr ? *b : a;
   const ColSum c = cs != nullptr ? *cs : ColSum{};
-  if (xa && ya)
-    tiny_gemm_kernel<true, true><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
-  else if (xa)
-    tiny_gemm_kernel<true, false><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
-  else if (ya)
-    tiny_gemm_kernel<false, true><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
+  const int most_r = std::max(a.R, b != nullptr ? b->R : 0);
+  auto go = [&](auto U) {
+    constexpr int kU = decltype(U)::value;
+    if (xa && ya)
+      tiny_gemm_kernel<true, true, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                (int)tb, c);
+    else if (xa)
+      tiny_gemm_kernel<true, false, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                 (int)tb, c);
+    else if (ya)
+      tiny_gemm_kernel<false, true, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                 (int)tb, c);
+    else
+      tiny_gemm_kernel<false, false, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                  (int)tb, c);
+  };
+  if (most_r > 16 * kTinyWaves * kTinyUSmall && sa == 1 && sb == 1)
+    go(std::integral_constant<int, kTinyUBig>{});
   else
-    tiny_gemm_kernel<false, false><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta, (int)tb, c);
-  return numrs_hip::check_launch(ctx, "tiny_gemm_kernel");
+    go(std::integral_constant<int, kTinyUSmall>{});
+  if (int rc = numrs_hip::check_launch(ctx, "tiny_gemm_kernel")) return rc;
+  return reduce_splits(ctx, sa > 1 ? &a : nullptr, sb > 1 ? &bb : nullptr);
 }
 
 // The streamed path takes whole TP x TQ output tiles and whole reduction
@@ -1217,6 +1317,8 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.ktiles_per_split = (int)((R + kBR - 1) / kBR);
   g.partial = nullptr;
   g.bias = nullptr;
+  g.xmask = nullptr;
+  g.relu = 0;
   g.P = (int)P;
   g.Q = (int)Q;
   g.R = (int)R;
@@ -1430,9 +1532,10 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
     if (has_a) return launch_tiny(ctx, ga, true, first_nt, has_b ? &gb : nullptr, 1, cs_in);
     return launch_tiny(ctx, gb, false, false, nullptr, 1, cs_in);
   }
-  const ColSum *cs =
-      cs_in != nullptr && colsum_fits(cs_in->g, cs_in->rows, cs_in->cols, cs_in->ldg) ? cs_in
-                                                                                    : nullptr;
+  const ColSum *cs = cs_in != nullptr && cs_in->mask == nullptr &&
+                             colsum_fits(cs_in->g, cs_in->rows, cs_in->cols, cs_in->ldg)
+                         ? cs_in
+                         : nullptr;
   if (cs_done != nullptr) *cs_done = cs != nullptr;
   if (!has_a && !has_b) return cs ? reduce_splits(ctx, nullptr, nullptr, cs) : NUMRS_HIP_OK;
   if (!has_a || !has_b) {
@@ -1620,6 +1723,67 @@ int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x
   const int64_t gs[2] = {T, out};
   const int64_t bs = out;
   return numrs_hip_sum_to_shape(ctx, g, gs, 2, db, &bs, 1, mode, acc_db);
+}
+
+int numrs_hip_linear_relu_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
+                                  const float *b, float *y, int64_t T, int64_t in, int64_t out) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_relu_forward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (T == 0 || out == 0) return NUMRS_HIP_OK;
+  if (y == nullptr || (in > 0 && (x == nullptr || W == nullptr)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (in > 0) {
+    Gemm g = make(x, W, y, in, in, out, 0, 0, 0, T, out, in, 0);
+    g.bias = b;
+    g.relu = 1;
+    if (tiny_fits(g, 1)) return launch_tiny(ctx, g, true, true, nullptr, 1, nullptr);
+  }
+  // Larger products: the Linear forward, then the ReLU in place.
+  if (int rc = numrs_hip_linear_forward(ctx, x, W, b, y, T, in, out)) return rc;
+  return numrs_hip_unary_forward(ctx, NUMRS_HIP_RELU, y, y, T * out, 0.0f);
+}
+
+int numrs_hip_linear_relu_backward(numrs_hip_ctx *ctx, const float *g, const float *y,
+                                   const float *x, const float *W, float *dx, float *dW,
+                                   float *db, int64_t T, int64_t in, int64_t out, int acc_dx,
+                                   int acc_dw, int acc_db, int mode) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_relu_backward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (T == 0 || out == 0)  // empty reductions: the Linear backward's zero gradients
+    return numrs_hip_linear_backward(ctx, g, x, W, dx, dW, db, T, in, out, acc_dx, acc_dw, acc_db,
+                                     mode);
+  if (g == nullptr || y == nullptr || (dx && W == nullptr) || (dW && x == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
+  if ((dx != nullptr || dW != nullptr) && in > 0 &&
+      (db == nullptr || (mode == NUMRS_HIP_UNBROADCAST_CORRECT && T <= kTinyColsumRows))) {
+    // The pre-activation gradient (y > 0 ? g : 0) applied as the tiny
+    // kernel loads g: one launch for dx, dW and db.
+    Gemm gx = make(g, W, dx, out, in, in, 0, 0, 0, T, in, out, acc_dx);
+    Gemm gw = make(g, x, dW, out, in, in, 0, 0, 0, out, in, T, acc_dw);
+    gx.xmask = gw.xmask = y;
+    if ((dx == nullptr || tiny_fits(gx, 1)) && (dW == nullptr || tiny_fits(gw, 1))) {
+      const ColSum cs{g, db, T, out, out, acc_db, y};
+      const ColSum *csp = db != nullptr ? &cs : nullptr;
+      if (dx != nullptr) return launch_tiny(ctx, gx, true, false, dW ? &gw : nullptr, 1, csp);
+      return launch_tiny(ctx, gw, false, false, nullptr, 1, csp);
+    }
+  }
+  // Otherwise the masked gradient first, then the Linear backward on it.
+  if ((dx == nullptr && dW == nullptr) || in == 0) {
+    if (int rc = numrs_hip_linear_backward(ctx, g, x, W, dx, dW, nullptr, T, in, out, acc_dx,
+                                           acc_dw, 0, mode))
+      return rc;
+    return db ? numrs_hip_relu_bias_backward(ctx, g, y, nullptr, db, T, out, mode, acc_db)
+              : NUMRS_HIP_OK;
+  }
+  numrs_hip::TempBlock gm(ctx);
+  if (int rc = gm.alloc((size_t)T * out * sizeof(float))) return rc;
+  if (int rc = numrs_hip_relu_bias_backward(ctx, g, y, gm.f(), nullptr, T, out, mode, 0))
+    return rc;
+  return numrs_hip_linear_backward(ctx, gm.f(), x, W, dx, dW, db, T, in, out, acc_dx, acc_dw,
+                                   acc_db, mode);
 }
 
 int numrs_hip_gemm(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B, int64_t ldb,

@@ -115,7 +115,13 @@ class LayerNorm(Module):
 
 
 class Sequential(Module):
-    """nn.rs:257-302."""
+    """nn.rs:257-302.
+
+    A fused Linear directly followed by ReLU runs as one Linear+ReLU node
+    (`fuse_relu`, default on): the same output and parameter gradients, one
+    node fewer (the pre-activation is not a tensor of its own)."""
+
+    fuse_relu = True
 
     def __init__(self, layers):
         self.layers = list(layers)
@@ -124,8 +130,16 @@ class Sequential(Module):
         self.layers.append(layer)
 
     def forward(self, x: Tensor) -> Tensor:
-        for layer in self.layers:
+        i, layers = 0, self.layers
+        while i < len(layers):
+            layer = layers[i]
+            if (self.fuse_relu and type(layer) is Linear and layer.fused and i + 1 < len(layers)
+                    and type(layers[i + 1]) is ReLU):
+                x = x.linear(layer.weight, layer.bias, relu=True)
+                i += 2
+                continue
             x = layer.forward(x)
+            i += 1
         return x
 
     def parameters(self) -> list[Tensor]:

@@ -366,3 +366,24 @@ def test_fused_linear_equals_reference_node_sequence():
                      + [loss.item()])
     for a, b in zip(*grads):
         assert_close(a, b, abs_tol=1e-7, rel_tol=1e-6)
+
+
+@pytest.mark.parametrize("T", [64, 2048])
+def test_sequential_linear_relu_node_equals_two_nodes(monkeypatch, T):
+    # Sequential's Linear+ReLU node vs the Linear node and the ReLU node: the
+    # same loss and parameter gradients, bit for bit (T = 64 takes the tiny
+    # kernel's fused epilogue and masked loads, T = 2048 the separate passes).
+    rng = np.random.default_rng(T)
+    p = make_c1(seed=5)
+    x = rng.standard_normal((T, 784)).astype(np.float32)
+    onehot = np.eye(10, dtype=np.float32)[rng.integers(0, 10, T)]
+    out = []
+    for fuse in (True, False):
+        monkeypatch.setattr(nn.Sequential, "fuse_relu", fuse)
+        model, l1, l2 = _c1_model(p)
+        loss = model.forward(Tensor.new(x, False)).cross_entropy_loss(Tensor.new(onehot, False))
+        loss.backward()
+        out.append([loss.values()] + [t.gradient() for t in (l1.weight, l1.bias, l2.weight,
+                                                              l2.bias)])
+    for a, b in zip(*out):
+        assert np.array_equal(a, b)

@@ -777,6 +777,66 @@ def test_linear_forward_backward(hip_ctx, rng, T, fin, fout):
         f"db reference: |gpu - exact| {e_gpu:.3e} vs numrs fp32 sum {e_ref:.3e}")
 
 
+# Linear followed by ReLU as one op.  (64, 784, 128), (64, 128, 10), (130,
+# 96, 18) and (33, 17, 5) take the tiny kernel (ReLU in the forward epilogue,
+# the backward mask applied as g is loaded, dx/dW/db in one launch);
+# (4096, 512, 512) the Linear path with the ReLU and the mask as passes of
+# their own.  Each result must equal the two-op composition bit for bit.
+@pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (64, 128, 10), (130, 96, 18),
+                                        (33, 17, 5), (4096, 512, 512)])
+def test_linear_relu_forward_backward(hip_ctx, rng, T, fin, fout):
+    say(f"linear+relu T={T} in={fin} out={fout}")
+    lib = L.load()
+    x, W, b, g = rand(rng, (T, fin)), rand(rng, (fout, fin)), rand(rng, fout), rand(rng, (T, fout))
+    c = hip_ctx
+    xd, Wd, bd, gd = (c.to_device(a) for a in (x, W, b, g))
+    y, y2 = c.empty((T, fout)), c.empty((T, fout))
+    assert lib.numrs_hip_linear_relu_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, y.ptr, T, fin,
+                                             fout) == 0
+    assert lib.numrs_hip_linear_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, y2.ptr, T, fin, fout) == 0
+    assert lib.numrs_hip_unary_forward(c.handle, L.RELU, y2.ptr, y2.ptr, T * fout, 0.0) == 0
+    yv = y.numpy()
+    assert np.array_equal(yv, y2.numpy()), "fused forward != linear + relu"
+    ref_y = O.matmul_f64(x, O.transpose(W)).astype(np.float64) + b
+    assert_contraction(yv, np.maximum(ref_y, 0.0), fin, what="y")
+    assert (yv >= 0).all()
+    # the mask is the GPU's own y > 0, so sign flips at |pre| ~ rounding do not matter
+    gm = np.where(yv > 0, g, 0.0).astype(np.float32)
+    gmd = c.to_device(gm)
+    prev = {k: rand(rng, s) for k, s in (("dx", (T, fin)), ("dW", (fout, fin)), ("db", fout))}
+    for acc in ((0, 0, 0), (1, 0, 1), (0, 1, 0)):
+        dx, dW, db = (c.to_device(prev[k]) for k in ("dx", "dW", "db"))
+        assert lib.numrs_hip_linear_relu_backward(c.handle, gd.ptr, y.ptr, xd.ptr, Wd.ptr, dx.ptr,
+                                                  dW.ptr, db.ptr, T, fin, fout, *acc,
+                                                  L.UNBROADCAST_CORRECT) == 0
+        dx2, dW2, db2 = (c.to_device(prev[k]) for k in ("dx", "dW", "db"))
+        assert lib.numrs_hip_linear_backward(c.handle, gmd.ptr, xd.ptr, Wd.ptr, dx2.ptr, dW2.ptr,
+                                             db2.ptr, T, fin, fout, *acc,
+                                             L.UNBROADCAST_CORRECT) == 0
+        for name, a, b2 in (("dx", dx, dx2), ("dW", dW, dW2), ("db", db, db2)):
+            assert np.array_equal(a.numpy(), b2.numpy()), f"{name} {acc}: fused != composition"
+        rdx, rdwt = O.matmul_backward(gm, x, O.transpose(W), f64=True)
+        base = [prev[k].astype(np.float64) if a else 0.0 for k, a in zip(("dx", "dW", "db"), acc)]
+        assert_contraction(dx.numpy(), base[0] + rdx, fout, what=f"dx {acc}")
+        assert_contraction(dW.numpy(), base[1] + O.transpose(rdwt), T, what=f"dW {acc}")
+        assert_sum(db.numpy(), base[2] + gm.astype(np.float64).sum(0), T, what=f"db {acc}")
+    # only some of the gradients, and the REFERENCE-mode bias (full sum in db[0])
+    dW = c.to_device(prev["dW"])
+    assert lib.numrs_hip_linear_relu_backward(c.handle, gd.ptr, y.ptr, xd.ptr, Wd.ptr, None,
+                                              dW.ptr, None, T, fin, fout, 0, 0, 0,
+                                              L.UNBROADCAST_CORRECT) == 0
+    rdx, rdwt = O.matmul_backward(gm, x, O.transpose(W), f64=True)
+    assert_contraction(dW.numpy(), O.transpose(rdwt), T, what="dW alone")
+    db, db2 = c.to_device(prev["db"]), c.to_device(prev["db"])
+    assert lib.numrs_hip_linear_relu_backward(c.handle, gd.ptr, y.ptr, xd.ptr, Wd.ptr, None, None,
+                                              db.ptr, T, fin, fout, 0, 0, 0,
+                                              L.UNBROADCAST_REFERENCE) == 0
+    assert lib.numrs_hip_relu_bias_backward(c.handle, gd.ptr, y.ptr, None, db2.ptr, T, fout,
+                                            L.UNBROADCAST_REFERENCE, 0) == 0
+    assert np.array_equal(db.numpy(), db2.numpy()), "db reference mode"
+    assert np.all(db.numpy()[1:] == 0)
+
+
 def test_optimizer_multi_tensor_bit_exact(hip_ctx, rng):
     import ctypes
 
