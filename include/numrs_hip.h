@@ -214,6 +214,14 @@ int numrs_hip_linear_relu_backward(numrs_hip_ctx *ctx, const float *g, const flo
                                    const float *x, const float *W, float *dx, float *dW,
                                    float *db, int64_t T, int64_t in, int64_t out, int acc_dx,
                                    int acc_dw, int acc_db, int mode);
+/* No counterpart in the reference: y = res + (x @ W^T + b), res [T, out] (may
+ * alias y), the residual added in the product's epilogue after the bias --
+ * the values of numrs_hip_linear_forward followed by an elementwise add
+ * (Linear::forward, nn.rs:217-235, then ops::add), bit for bit.  Its backward
+ * is numrs_hip_linear_backward from g plus dres = g. */
+int numrs_hip_linear_residual_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
+                                      const float *b, const float *res, float *y, int64_t T,
+                                      int64_t in, int64_t out);
 
 /* General strided product, the building block of attention's batched
  * gradients: for z in [0, batch), with zo = z / batch_inner and
@@ -587,6 +595,14 @@ int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_
  * a tensor of its own. */
 int numrs_hip_tensor_linear_relu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
                                  numrs_hip_tensor **out);
+/* No counterpart in the reference: the residual step y = res + (x @ W^T + b)
+ * of a residual block -- Linear::forward (nn.rs:217-235) then the Add node
+ * (add_backward, backward.rs:43-54) -- as one node, res [T, out] added in the
+ * product's epilogue (numrs_hip_linear_residual_forward).  res's gradient is
+ * g; x, W and b get the Linear node's gradients. */
+int numrs_hip_tensor_linear_residual(numrs_hip_tensor *x, numrs_hip_tensor *W,
+                                     numrs_hip_tensor *b, numrs_hip_tensor *res,
+                                     numrs_hip_tensor **out);
 /* LSTM layer node: x [B, T, I] -> h_seq [B, T, H] (numrs_hip_lstm_forward). */
 int numrs_hip_tensor_lstm(numrs_hip_tensor *x, numrs_hip_tensor *w_ih, numrs_hip_tensor *w_hh,
                           numrs_hip_tensor *b, numrs_hip_tensor **out);

@@ -305,15 +305,23 @@ class Tensor:
         return self._out(L.load().numrs_hip_tensor_layer_norm(self._h, gamma._h, beta._h, eps,
                                                               ctypes.byref(h)), h)
 
-    def linear(self, weight: "Tensor", bias: "Tensor | None" = None,
-               relu: bool = False) -> "Tensor":
+    def linear(self, weight: "Tensor", bias: "Tensor | None" = None, relu: bool = False,
+               residual: "Tensor | None" = None) -> "Tensor":
         """self @ weight^T + bias as one node (Linear::forward's values and
-        grads); relu=True also applies ReLU in the same node (the Linear ->
-        ReLU pair, same values and parameter gradients)."""
+        grads).  relu=True also applies ReLU in the same node (the Linear ->
+        ReLU pair); residual=r returns r + (self @ weight^T + bias) as one
+        node (the Linear then Add of a residual block).  Both give the same
+        values and gradients as the separate nodes."""
         h = ctypes.c_void_p()
-        fn = L.load().numrs_hip_tensor_linear_relu if relu else L.load().numrs_hip_tensor_linear
-        return self._out(fn(self._h, weight._h, bias._h if bias is not None else None,
-                            ctypes.byref(h)), h)
+        lib = L.load()
+        b = bias._h if bias is not None else None
+        if residual is not None:
+            if relu:
+                raise ValueError("linear: relu and residual together are not supported")
+            return self._out(lib.numrs_hip_tensor_linear_residual(self._h, weight._h, b,
+                                                                  residual._h, ctypes.byref(h)), h)
+        fn = lib.numrs_hip_tensor_linear_relu if relu else lib.numrs_hip_tensor_linear
+        return self._out(fn(self._h, weight._h, b, ctypes.byref(h)), h)
 
     def lstm(self, w_ih: "Tensor", w_hh: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
         """LSTM layer over self [B, T, I] -> hidden states [B, T, H]."""

@@ -504,7 +504,12 @@ int bw_attention(const T &out, const float *g, Node &n) {
 
 int bw_linear(const T &out, const float *g, Node &n) {
   const T &x = n.inputs[0], &W = n.inputs[1];
-  const T *b = n.inputs.size() > 2 ? &n.inputs[2] : nullptr;
+  const bool relu = (n.kind & 1) != 0, has_res = (n.kind & 2) != 0;
+  const size_t nb = n.inputs.size() - (has_res ? 1 : 0);
+  const T *b = nb > 2 ? &n.inputs[2] : nullptr;
+  // the residual's gradient is g (add_backward, backward.rs:43-54)
+  if (has_res && n.inputs.back()->requires_grad)
+    if (int rc = add_into(n.inputs.back(), g, out->shape)) return rc;
   const int64_t Tn = x->shape[0], in = x->shape[1], outf = W->shape[0];
   numrs_hip_ctx *ctx = out->ctx;
   float *dx = nullptr, *dW = nullptr, *db = nullptr;
@@ -516,10 +521,10 @@ int bw_linear(const T &out, const float *g, Node &n) {
     if (int rc = grad_target(W, &dW, &aw)) return rc;
   if (b && (*b)->requires_grad)
     if (int rc = grad_target(*b, &db, &ab)) return rc;
-  // n.kind = 1: the output went through ReLU; its saved value masks g.
+  // The output went through ReLU: its saved value masks g.
   const float *y = out->data->ptr;
   auto run = [&](float *dx_, float *dW_, float *db_, int ax_, int aw_, int ab_) {
-    if (n.kind == 1)
+    if (relu)
       return numrs_hip_linear_relu_backward(ctx, g, y, x->data->ptr, W->data->ptr, dx_, dW_, db_,
                                             Tn, in, outf, ax_, aw_, ab_, ctx->unbroadcast_mode);
     return numrs_hip_linear_backward(ctx, g, x->data->ptr, W->data->ptr, dx_, dW_, db_, Tn, in,
@@ -913,23 +918,38 @@ int op_layernorm(const T &x, const T &gamma, const T &beta, float eps, T *out) {
 
 // relu = 1: y = ReLU(x W^T + b) as one node (the Linear -> ReLU pair of a
 // Sequential), whose backward masks g by y > 0 before the Linear backward.
-int op_linear(const T &x, const T &W, const T *b, T *out, int relu = 0) {
+// res: y = res + (x W^T + b) as one node (a residual block's "x + Linear(a)"),
+// the residual added in the product's epilogue; its gradient is g itself.
+// Node kind: bit 0 ReLU, bit 1 residual (the last input).
+int op_linear(const T &x, const T &W, const T *b, T *out, int relu = 0, const T *res = nullptr) {
   numrs_hip_ctx *ctx = x->ctx;
   if (x->shape.size() != 2 || W->shape.size() != 2 || x->shape[1] != W->shape[1])
     return fail(ctx, NUMRS_HIP_E_SHAPE, "linear expects x [T,in], W [out,in]");
   if (b && ((*b)->numel() != W->shape[0]))
     return fail(ctx, NUMRS_HIP_E_SHAPE, "linear: bias must have out elements");
-  const bool rec = b ? recording({&x, &W, b}) : recording({&x, &W});
+  if (res && ((*res)->shape != std::vector<int64_t>{x->shape[0], W->shape[0]} || relu))
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "linear: residual must be [T, out] (and no ReLU)");
+  std::vector<const T *> all{&x, &W};
+  if (b) all.push_back(b);
+  if (res) all.push_back(res);
+  bool rec = false;
+  for (const T *t : all) rec = rec || ((*t)->requires_grad && g_grad_enabled);
   T r;
   if (int rc = make_tensor(ctx, {x->shape[0], W->shape[0]}, rec, &r)) return rc;
-  auto fwd = relu ? numrs_hip_linear_relu_forward : numrs_hip_linear_forward;
-  if (int rc = fwd(ctx, x->data->ptr, W->data->ptr, b ? (*b)->data->ptr : nullptr, r->data->ptr,
-                   x->shape[0], x->shape[1], W->shape[0]))
-    return rc;
+  const float *bp = b ? (*b)->data->ptr : nullptr;
+  int rc = 0;
+  if (res)
+    rc = numrs_hip_linear_residual_forward(ctx, x->data->ptr, W->data->ptr, bp, (*res)->data->ptr,
+                                           r->data->ptr, x->shape[0], x->shape[1], W->shape[0]);
+  else
+    rc = (relu ? numrs_hip_linear_relu_forward : numrs_hip_linear_forward)(
+        ctx, x->data->ptr, W->data->ptr, bp, r->data->ptr, x->shape[0], x->shape[1], W->shape[0]);
+  if (rc) return rc;
   if (rec) {
     std::vector<T> ins{x, W};
     if (b) ins.push_back(*b);
-    attach(r, Op::Linear, std::move(ins), relu);
+    if (res) ins.push_back(*res);
+    attach(r, Op::Linear, std::move(ins), (relu ? 1 : 0) | (res ? 2 : 0));
   }
   *out = std::move(r);
   return NUMRS_HIP_OK;
@@ -1532,6 +1552,15 @@ int numrs_hip_tensor_linear_relu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs
   if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r, 1)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_linear_residual(numrs_hip_tensor *x, numrs_hip_tensor *W,
+                                     numrs_hip_tensor *b, numrs_hip_tensor *res,
+                                     numrs_hip_tensor **out) {
+  if (x == nullptr || W == nullptr || res == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r, 0, &res->t)) return rc;
   return wrap(std::move(r), out);
 }
 

@@ -84,6 +84,11 @@ struct Gemm {
   // epilogue).
   const float *xmask;
   int relu;
+  // Optional residual added after the bias: C = alpha*X@Y + bias[q] +
+  // res[p*ldr + q] (+ C) -- the "x + Linear(a)" of a residual block folded
+  // into the product's epilogue (batch-1 products).
+  const float *res;
+  int64_t ldr;
 };
 
 // Loads one 128 x 32 operand tile from global memory into registers
@@ -243,6 +248,28 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
   // 32x32 accumulator layout: lane (h, c), register i holds
   // row 8*(i/4) + 4*h + (i%4), column c.
   const f16v *accs[4] = {&acc00, &acc01, &acc10, &acc11};
+  // Residual and bias values are all loaded before the first store (res or
+  // bias may alias C as far as the compiler knows, which would otherwise
+  // order each load after the previous store).
+  float bq[2];
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int q = q0 + wq * 64 + bj * 32 + c;
+    bq[bj] = d.splits == 1 && d.bias != nullptr && q < d.Q ? d.bias[q] : 0.0f;
+  }
+  f16v rv[4];
+  if (d.splits == 1 && d.res != nullptr) {
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int bi = blk >> 1, bj = blk & 1;
+      const int q = q0 + wq * 64 + bj * 32 + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int p = p0 + wp * 64 + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        rv[blk][i] = p < d.P && q < d.Q ? d.res[(int64_t)p * d.ldr + q] : 0.0f;
+      }
+    }
+  }
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
     const int bi = blk >> 1, bj = blk & 1;
@@ -257,7 +284,8 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
         } else {
           float *dst = C + (int64_t)p * d.ldc + q;
           float v = d.alpha * a[i];
-          if (d.bias != nullptr) v = v + d.bias[q];
+          if (d.bias != nullptr) v = v + bq[bj];
+          if (d.res != nullptr) v = v + rv[blk][i];
           *dst = d.accumulate ? *dst + v : v;
         }
       }
@@ -275,6 +303,8 @@ struct SplitSet {
   int Q, splits, acc;
   float alpha;
   int relu;  // clamp the result at zero (the Linear+ReLU forward)
+  const float *res;  // residual added after the bias (row stride ldr)
+  int64_t ldr;
 };
 
 // Column sums out[c] (+)= sum_r g[r ldg + c] of a [rows, cols] block in one
@@ -367,6 +397,7 @@ __global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, C
   V *dst = reinterpret_cast<V *>(d.C + p * d.ldc + q);
   V v = d.alpha * s;
   if (d.bias != nullptr) v = v + *reinterpret_cast<const V *>(d.bias + q);
+  if (d.res != nullptr) v = v + *reinterpret_cast<const V *>(d.res + p * d.ldr + q);
   v = d.acc ? *dst + v : v;
   if (d.relu) {
     if constexpr (VEC) {
@@ -751,6 +782,27 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   }
   flush();
 
+  // Residual values are all loaded (into the dead MFMA partials) before the
+  // first store: res may alias C, which would otherwise order each load
+  // after the previous store.
+  const bool with_res = !part && d.res != nullptr;
+  if (with_res) {
+#pragma unroll
+    for (int bi = 0; bi < kBI; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < kBJ; ++bj) {
+        const int q = q0 + wq * (TQ / 2) + bj * 32 + c;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int p = p0 + wp * Cfg::kWP + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          acc[bi][bj][i] = d.res[(int64_t)p * d.ldr + q];
+        }
+      }
+  }
+  float bq[kBJ];  // this lane's bias columns, also read before any store
+#pragma unroll
+  for (int bj = 0; bj < kBJ; ++bj)
+    bq[bj] = !part && d.bias != nullptr ? d.bias[q0 + wq * (TQ / 2) + bj * 32 + c] : 0.0f;
 #pragma unroll
   for (int bi = 0; bi < kBI; ++bi)
 #pragma unroll
@@ -764,7 +816,8 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
           *dst = tot[bi][bj][i];
         } else {
           float v = d.alpha * tot[bi][bj][i];
-          if (d.bias != nullptr) v = v + d.bias[q];
+          if (d.bias != nullptr) v = v + bq[bj];
+          if (with_res) v = v + acc[bi][bj][i];
           *dst = d.accumulate ? *dst + v : v;
         }
       }
@@ -883,9 +936,10 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum
   for (int i = 0; i < m; ++i) {
     const Gemm &d = *g[i];
     set[i] = SplitSet{d.partial, d.C, d.bias, d.ldc, (int64_t)d.P * d.Q, d.Q, d.splits,
-                      d.accumulate, d.alpha, d.relu};
+                      d.accumulate, d.alpha, d.relu, d.res, d.ldr};
     vec = vec && d.Q % 4 == 0 && d.ldc % 4 == 0 && numrs_hip::aligned16(d.C) &&
-          numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias));
+          numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias)) &&
+          (d.res == nullptr || (numrs_hip::aligned16(d.res) && d.ldr % 4 == 0));
     most = std::max(most, set[i].n);
   }
   if (m == 1) set[1] = set[0];
@@ -1014,6 +1068,7 @@ __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
       float *dst = C + (int64_t)pp * d.ldc + qq;
       float v = d.alpha * s;
       if (d.bias != nullptr) v = v + d.bias[qq];
+      if (d.res != nullptr) v = v + d.res[(int64_t)pp * d.ldr + qq];
       v = d.accumulate ? *dst + v : v;
       if (d.relu) v = fmaxf(v, 0.0f);  // the ReLU forward kernel's x.max(0)
       *dst = v;
@@ -1319,6 +1374,8 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.bias = nullptr;
   g.xmask = nullptr;
   g.relu = 0;
+  g.res = nullptr;
+  g.ldr = 0;
   g.P = (int)P;
   g.Q = (int)Q;
   g.R = (int)R;
@@ -1784,6 +1841,27 @@ int numrs_hip_linear_relu_backward(numrs_hip_ctx *ctx, const float *g, const flo
     return rc;
   return numrs_hip_linear_backward(ctx, gm.f(), x, W, dx, dW, db, T, in, out, acc_dx, acc_dw,
                                    acc_db, mode);
+}
+
+int numrs_hip_linear_residual_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
+                                      const float *b, const float *res, float *y, int64_t T,
+                                      int64_t in, int64_t out) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_residual_forward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (T == 0 || out == 0) return NUMRS_HIP_OK;
+  if (y == nullptr || res == nullptr || (in > 0 && (x == nullptr || W == nullptr)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
+  if (in == 0) {  // empty product: y = b broadcast over rows (or 0), then + res
+    if (int rc = numrs_hip_linear_forward(ctx, x, W, b, y, T, in, out)) return rc;
+    const int64_t ys[2] = {T, out};
+    return numrs_hip_binary_forward(ctx, NUMRS_HIP_ADD, res, ys, 2, y, ys, 2, y);
+  }
+  Gemm g = make(x, W, y, in, in, out, 0, 0, 0, T, out, in, 0);
+  g.bias = b;
+  g.res = res;
+  g.ldr = out;
+  return gemm_dispatch(ctx, g, 1, true, true);
 }
 
 int numrs_hip_gemm(numrs_hip_ctx *ctx, const float *A, int64_t lda, const float *B, int64_t ldb,

@@ -180,12 +180,20 @@ class MultiHeadAttention(Module):
             self.projections = [self.q, self.k, self.v]
         self.o = Linear.with_weights(d, d, wo, z, ctx)
 
-    def forward_seq(self, x: Tensor, batch: int, seq: int) -> Tensor:
+    def forward_seq(self, x: Tensor, batch: int, seq: int, residual: Tensor | None = None
+                    ) -> Tensor:
+        """Attention output projection of x [batch*seq, d]; with `residual`,
+        residual + that projection (one node when the projection is a fused
+        Linear)."""
         if self.fused_qkv:
             a = self.qkv(x).attention_qkv(batch, seq, self.heads)
         else:
             a = self.q(x).attention(self.k(x), self.v(x), batch, seq, self.heads)
-        return self.o(a)
+        if residual is None:
+            return self.o(a)
+        if self.o.fused:
+            return a.linear(self.o.weight, self.o.bias, residual=residual)
+        return residual.add(self.o(a))
 
     def projection_grads(self) -> dict:
         """Gradients of the q, k, v projections as wq, wk, wv [d, d] and bq,
@@ -208,7 +216,12 @@ class MultiHeadAttention(Module):
 
 class TransformerEncoderBlock(Module):
     """Pre-LN encoder block on x [batch*seq, d_model]:
-    r = x + Attn(LN1(x));  y = r + W2 GELU(W1 LN2(r))."""
+    r = x + Attn(LN1(x));  y = r + W2 GELU(W1 LN2(r)).
+
+    With `fuse_residual` (default) each residual add rides in the epilogue of
+    the projection before it (one node each, same values and gradients)."""
+
+    fuse_residual = True
 
     def __init__(self, weights: dict, heads: int, ctx=None):
         d = np.asarray(weights["wq"]).shape[0]
@@ -221,8 +234,12 @@ class TransformerEncoderBlock(Module):
         self.ff2 = Linear.with_weights(f, d, weights["w2"], np.zeros(d, np.float32), ctx)
 
     def forward_seq(self, x: Tensor, batch: int, seq: int) -> Tensor:
-        r = x.add(self.attn.forward_seq(self.ln1(x), batch, seq))
-        return r.add(self.ff2(self.ff1(self.ln2(r)).gelu()))
+        if not (self.fuse_residual and self.ff2.fused):
+            r = x.add(self.attn.forward_seq(self.ln1(x), batch, seq))
+            return r.add(self.ff2(self.ff1(self.ln2(r)).gelu()))
+        r = self.attn.forward_seq(self.ln1(x), batch, seq, residual=x)
+        h = self.ff1(self.ln2(r)).gelu()
+        return h.linear(self.ff2.weight, self.ff2.bias, residual=r)
 
     def parameters(self) -> list[Tensor]:
         return (self.ln1.parameters() + self.attn.parameters() + self.ln2.parameters() +

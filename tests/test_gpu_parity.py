@@ -837,6 +837,33 @@ def test_linear_relu_forward_backward(hip_ctx, rng, T, fin, fout):
     assert np.all(db.numpy()[1:] == 0)
 
 
+# y = res + (x W^T + b) with the residual in the epilogue of each GEMM path:
+# tiny (64, 784, 128) and (130, 96, 18), streamed (4096, 512, 512), streamed
+# with split-K (4096, 2048, 512: the epilogue runs in the split reduction),
+# the 128 x 128 path (1000, 300, 136).  Bit for bit the Linear forward
+# followed by an add; also with res aliasing y.
+@pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (130, 96, 18), (4096, 512, 512),
+                                        (4096, 2048, 512), (1000, 300, 136)])
+def test_linear_residual_forward(hip_ctx, rng, T, fin, fout):
+    say(f"linear+residual T={T} in={fin} out={fout}")
+    lib = L.load()
+    x, W, b, r = rand(rng, (T, fin)), rand(rng, (fout, fin)), rand(rng, fout), rand(rng, (T, fout))
+    c = hip_ctx
+    xd, Wd, bd, rd = (c.to_device(a) for a in (x, W, b, r))
+    y, f = c.empty((T, fout)), c.empty((T, fout))
+    assert lib.numrs_hip_linear_residual_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, rd.ptr, y.ptr,
+                                                 T, fin, fout) == 0
+    assert lib.numrs_hip_linear_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, f.ptr, T, fin, fout) == 0
+    want = r + f.numpy()  # fp32 add, as the add kernel rounds it
+    assert np.array_equal(y.numpy(), want), "fused residual != linear + add"
+    ref = O.matmul_f64(x, O.transpose(W)).astype(np.float64) + b + r
+    assert_contraction(y.numpy(), ref, fin, what="y")
+    # in place: res is y
+    assert lib.numrs_hip_linear_residual_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, rd.ptr, rd.ptr,
+                                                 T, fin, fout) == 0
+    assert np.array_equal(rd.numpy(), want), "residual aliasing y"
+
+
 def test_optimizer_multi_tensor_bit_exact(hip_ctx, rng):
     import ctypes
 

@@ -132,6 +132,24 @@ def _run_block(dims_full, seed):
     return w, x, t, dims, blk, xt, loss, y
 
 
+@pytest.mark.parametrize("dims_full", [dict(B=2, S=64, D=128, H=4, F=256),
+                                       dict(B=16, S=256, D=512, H=8, F=2048)],
+                         ids=["small", "baseline"])
+def test_c4_residual_nodes_equal_add_nodes(hip_ctx, dims_full, monkeypatch):
+    """The block with each residual add folded into its projection node
+    equals the block with separate Add nodes, bit for bit."""
+    print(f"[gpu] C4 residual fusion {dims_full}", flush=True)
+    nr.set_default_context(hip_ctx)
+    out = []
+    for fuse in (True, False):
+        monkeypatch.setattr(nn.TransformerEncoderBlock, "fuse_residual", fuse)
+        w, x, t, dims, blk, xt, loss, y = _run_block(dims_full, seed=6)
+        out.append([y.values(), loss.values(), xt.gradient()] +
+                    [p.gradient() for p in blk.parameters()])
+    for i, (a, b) in enumerate(zip(*out)):
+        assert np.array_equal(a, b), i
+
+
 @pytest.mark.parametrize("fused_qkv", [True, False], ids=["qkv_fused", "qkv_separate"])
 @pytest.mark.parametrize("dims_full", [dict(B=2, S=64, D=128, H=4, F=256),
                                        dict(B=16, S=256, D=512, H=8, F=2048)],
