@@ -199,9 +199,8 @@ int numrs_hip_linear_backward(numrs_hip_ctx *ctx, const float *g, const float *x
                               int acc_dx, int acc_dw, int acc_db, int mode);
 /* No counterpart in the reference: the Linear layer followed by ReLU
  * (nn.rs:217-235, then ReLU::forward, nn.rs:306-320), y = max(x @ W^T + b, 0)
- * with the ReLU forward kernel's x.max(0).  Small products (at most 2^24
- * multiply-adds, reduction <= 4096) clamp in the product's epilogue; larger
- * ones run numrs_hip_linear_forward and the ReLU in place. */
+ * with the ReLU forward kernel's x.max(0), applied in the product's
+ * epilogue. */
 int numrs_hip_linear_relu_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
                                   const float *b, float *y, int64_t T, int64_t in, int64_t out);
 /* Its backward from g = dL/dy, y the forward's output: the pre-activation
@@ -211,6 +210,20 @@ int numrs_hip_linear_relu_forward(numrs_hip_ctx *ctx, const float *x, const floa
  * loads g (dx, dW and db in one launch); larger ones form the masked
  * gradient first. */
 int numrs_hip_linear_relu_backward(numrs_hip_ctx *ctx, const float *g, const float *y,
+                                   const float *x, const float *W, float *dx, float *dW,
+                                   float *db, int64_t T, int64_t in, int64_t out, int acc_dx,
+                                   int acc_dw, int acc_db, int mode);
+/* No counterpart in the reference: the Linear layer followed by GELU (the
+ * exact-erf GELU of the unary kernels), y = GELU(x @ W^T + b), with the
+ * pre-activation x @ W^T + b also stored in `pre` [T, out] (not aliasing y)
+ * by the product's epilogue -- the values of numrs_hip_linear_forward then
+ * numrs_hip_unary_forward(GELU), bit for bit. */
+int numrs_hip_linear_gelu_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
+                                  const float *b, float *y, float *pre, int64_t T, int64_t in,
+                                  int64_t out);
+/* Its backward from g = dL/dy: g * GELU'(pre) (numrs_hip_unary_backward),
+ * then numrs_hip_linear_backward on it. */
+int numrs_hip_linear_gelu_backward(numrs_hip_ctx *ctx, const float *g, const float *pre,
                                    const float *x, const float *W, float *dx, float *dW,
                                    float *db, int64_t T, int64_t in, int64_t out, int acc_dx,
                                    int acc_dw, int acc_db, int mode);
@@ -594,6 +607,12 @@ int numrs_hip_tensor_linear(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_
  * values and parameter gradients as the two nodes; the pre-activation is not
  * a tensor of its own. */
 int numrs_hip_tensor_linear_relu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
+                                 numrs_hip_tensor **out);
+/* No counterpart in the reference: a Linear node followed by GELU as one
+ * node, y = GELU(x @ W^T + b) (numrs_hip_linear_gelu_forward/_backward; the
+ * pre-activation is saved inside the node).  Same values and gradients as
+ * the two nodes. */
+int numrs_hip_tensor_linear_gelu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
                                  numrs_hip_tensor **out);
 /* No counterpart in the reference: the residual step y = res + (x @ W^T + b)
  * of a residual block -- Linear::forward (nn.rs:217-235) then the Add node

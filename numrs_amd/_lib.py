@@ -47,6 +47,8 @@ SIGNATURES = {
     "numrs_hip_linear_relu_forward": (_i, [_vp] * 5 + [_i64] * 3),
     "numrs_hip_linear_relu_backward": (_i, [_vp] * 8 + [_i64] * 3 + [_i] * 4),
     "numrs_hip_linear_residual_forward": (_i, [_vp] * 6 + [_i64] * 3),
+    "numrs_hip_linear_gelu_forward": (_i, [_vp] * 6 + [_i64] * 3),
+    "numrs_hip_linear_gelu_backward": (_i, [_vp] * 8 + [_i64] * 3 + [_i] * 4),
     "numrs_hip_gemm": (_i, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i, _i, _f, _i,
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "numrs_hip_sum_to_shape": (_i, [_vp, _vp, _i64p, _i, _vp, _i64p, _i, _i, _i]),
@@ -120,6 +122,7 @@ SIGNATURES = {
     "numrs_hip_tensor_linear": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_linear_relu": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_linear_residual": (_i, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_linear_gelu": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_lstm": (_i, [_vp] * 4 + [ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_time_slice": (_i, [_vp, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_attention": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),

@@ -306,21 +306,23 @@ class Tensor:
                                                               ctypes.byref(h)), h)
 
     def linear(self, weight: "Tensor", bias: "Tensor | None" = None, relu: bool = False,
-               residual: "Tensor | None" = None) -> "Tensor":
+               residual: "Tensor | None" = None, gelu: bool = False) -> "Tensor":
         """self @ weight^T + bias as one node (Linear::forward's values and
-        grads).  relu=True also applies ReLU in the same node (the Linear ->
-        ReLU pair); residual=r returns r + (self @ weight^T + bias) as one
-        node (the Linear then Add of a residual block).  Both give the same
-        values and gradients as the separate nodes."""
+        grads).  relu=True / gelu=True also apply that activation in the same
+        node (the Linear -> ReLU / GELU pair); residual=r returns r + (self @
+        weight^T + bias) as one node (the Linear then Add of a residual
+        block).  Each gives the same values and gradients as the separate
+        nodes."""
         h = ctypes.c_void_p()
         lib = L.load()
         b = bias._h if bias is not None else None
+        if relu + gelu + (residual is not None) > 1:
+            raise ValueError("linear: at most one of relu, gelu and residual")
         if residual is not None:
-            if relu:
-                raise ValueError("linear: relu and residual together are not supported")
             return self._out(lib.numrs_hip_tensor_linear_residual(self._h, weight._h, b,
                                                                   residual._h, ctypes.byref(h)), h)
-        fn = lib.numrs_hip_tensor_linear_relu if relu else lib.numrs_hip_tensor_linear
+        fn = (lib.numrs_hip_tensor_linear_relu if relu else
+              lib.numrs_hip_tensor_linear_gelu if gelu else lib.numrs_hip_tensor_linear)
         return self._out(fn(self._h, weight._h, b, ctypes.byref(h)), h)
 
     def lstm(self, w_ih: "Tensor", w_hh: "Tensor", bias: "Tensor | None" = None) -> "Tensor":

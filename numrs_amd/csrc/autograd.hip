@@ -504,7 +504,7 @@ int bw_attention(const T &out, const float *g, Node &n) {
 
 int bw_linear(const T &out, const float *g, Node &n) {
   const T &x = n.inputs[0], &W = n.inputs[1];
-  const bool relu = (n.kind & 1) != 0, has_res = (n.kind & 2) != 0;
+  const bool relu = (n.kind & 1) != 0, has_res = (n.kind & 2) != 0, gelu = (n.kind & 4) != 0;
   const size_t nb = n.inputs.size() - (has_res ? 1 : 0);
   const T *b = nb > 2 ? &n.inputs[2] : nullptr;
   // the residual's gradient is g (add_backward, backward.rs:43-54)
@@ -524,6 +524,10 @@ int bw_linear(const T &out, const float *g, Node &n) {
   // The output went through ReLU: its saved value masks g.
   const float *y = out->data->ptr;
   auto run = [&](float *dx_, float *dW_, float *db_, int ax_, int aw_, int ab_) {
+    if (gelu)
+      return numrs_hip_linear_gelu_backward(ctx, g, n.saved[0]->ptr, x->data->ptr, W->data->ptr,
+                                            dx_, dW_, db_, Tn, in, outf, ax_, aw_, ab_,
+                                            ctx->unbroadcast_mode);
     if (relu)
       return numrs_hip_linear_relu_backward(ctx, g, y, x->data->ptr, W->data->ptr, dx_, dW_, db_,
                                             Tn, in, outf, ax_, aw_, ab_, ctx->unbroadcast_mode);
@@ -916,19 +920,22 @@ int op_layernorm(const T &x, const T &gamma, const T &beta, float eps, T *out) {
   return NUMRS_HIP_OK;
 }
 
-// relu = 1: y = ReLU(x W^T + b) as one node (the Linear -> ReLU pair of a
+// act 1: y = ReLU(x W^T + b) as one node (the Linear -> ReLU pair of a
 // Sequential), whose backward masks g by y > 0 before the Linear backward.
+// act 2: y = GELU(x W^T + b) as one node, the pre-activation saved by the
+// product's epilogue for GELU's backward.
 // res: y = res + (x W^T + b) as one node (a residual block's "x + Linear(a)"),
 // the residual added in the product's epilogue; its gradient is g itself.
-// Node kind: bit 0 ReLU, bit 1 residual (the last input).
-int op_linear(const T &x, const T &W, const T *b, T *out, int relu = 0, const T *res = nullptr) {
+// Node kind: bit 0 ReLU, bit 1 residual (the last input), bit 2 GELU.
+int op_linear(const T &x, const T &W, const T *b, T *out, int act = 0, const T *res = nullptr) {
+  const int relu = act == 1;
   numrs_hip_ctx *ctx = x->ctx;
   if (x->shape.size() != 2 || W->shape.size() != 2 || x->shape[1] != W->shape[1])
     return fail(ctx, NUMRS_HIP_E_SHAPE, "linear expects x [T,in], W [out,in]");
   if (b && ((*b)->numel() != W->shape[0]))
     return fail(ctx, NUMRS_HIP_E_SHAPE, "linear: bias must have out elements");
-  if (res && ((*res)->shape != std::vector<int64_t>{x->shape[0], W->shape[0]} || relu))
-    return fail(ctx, NUMRS_HIP_E_SHAPE, "linear: residual must be [T, out] (and no ReLU)");
+  if (res && ((*res)->shape != std::vector<int64_t>{x->shape[0], W->shape[0]} || act))
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "linear: residual must be [T, out] (and no activation)");
   std::vector<const T *> all{&x, &W};
   if (b) all.push_back(b);
   if (res) all.push_back(res);
@@ -938,7 +945,12 @@ int op_linear(const T &x, const T &W, const T *b, T *out, int relu = 0, const T 
   if (int rc = make_tensor(ctx, {x->shape[0], W->shape[0]}, rec, &r)) return rc;
   const float *bp = b ? (*b)->data->ptr : nullptr;
   int rc = 0;
-  if (res)
+  Buf pre;
+  if (act == 2) {
+    if ((rc = alloc_buf(ctx, x->shape[0] * W->shape[0], sizeof(float), &pre))) return rc;
+    rc = numrs_hip_linear_gelu_forward(ctx, x->data->ptr, W->data->ptr, bp, r->data->ptr,
+                                       pre->ptr, x->shape[0], x->shape[1], W->shape[0]);
+  } else if (res)
     rc = numrs_hip_linear_residual_forward(ctx, x->data->ptr, W->data->ptr, bp, (*res)->data->ptr,
                                            r->data->ptr, x->shape[0], x->shape[1], W->shape[0]);
   else
@@ -949,7 +961,10 @@ int op_linear(const T &x, const T &W, const T *b, T *out, int relu = 0, const T 
     std::vector<T> ins{x, W};
     if (b) ins.push_back(*b);
     if (res) ins.push_back(*res);
-    attach(r, Op::Linear, std::move(ins), (relu ? 1 : 0) | (res ? 2 : 0));
+    if (act == 2)
+      attach(r, Op::Linear, std::move(ins), 4, 0.f, {pre});
+    else
+      attach(r, Op::Linear, std::move(ins), (relu ? 1 : 0) | (res ? 2 : 0));
   }
   *out = std::move(r);
   return NUMRS_HIP_OK;
@@ -1552,6 +1567,14 @@ int numrs_hip_tensor_linear_relu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs
   if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r, 1)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_linear_gelu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs_hip_tensor *b,
+                                 numrs_hip_tensor **out) {
+  if (x == nullptr || W == nullptr || out == nullptr) return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_linear(x->t, W->t, b ? &b->t : nullptr, &r, 2)) return rc;
   return wrap(std::move(r), out);
 }
 

@@ -145,6 +145,12 @@ __device__ __forceinline__ void stv(float *p, nrs_f4 v) {
     *reinterpret_cast<nrs_f4 *>(p) = v;
 }
 
+// GELU, exact-erf form: x * 0.5 * (1 + erf(x / sqrt 2)); shared by the unary
+// forward kernel and the GEMM epilogue, so both round alike.
+__device__ __forceinline__ float gelu_erf(float x) {
+  return x * 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+}
+
 // A batched row-major fp32 matrix: element (i, j) of batch z = zo*inner + zi
 // sits at p + zo*so + zi*si + i*ld + j.
 struct BatchedMat {

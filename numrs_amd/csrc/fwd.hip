@@ -77,7 +77,7 @@ __device__ __forceinline__ float un(float x, float p) {
   else if constexpr (KIND == NUMRS_HIP_TANH) return tanhf(x);
   else if constexpr (KIND == NUMRS_HIP_EXP) return expf(x);
   else if constexpr (KIND == NUMRS_HIP_LOG) return logf(x);
-  else if constexpr (KIND == NUMRS_HIP_GELU) return x * 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+  else if constexpr (KIND == NUMRS_HIP_GELU) return numrs_hip::gelu_erf(x);
   else if constexpr (KIND == NUMRS_HIP_SQRT) return sqrtf(x);
   else if constexpr (KIND == NUMRS_HIP_SIN) return sinf(x);
   else if constexpr (KIND == NUMRS_HIP_COS) return cosf(x);

@@ -79,17 +79,26 @@ struct Gemm {
   // (+ C); the Linear forward's "+ b" folded into the product's epilogue.
   const float *bias;
   // Tiny kernel only: X entries whose `xmask` entry (same layout and
-  // offsets as X) is not > 0 read as zero (ReLU backward applied on load),
-  // and `relu` clamps the stored result at zero (ReLU forward in the
-  // epilogue).
+  // offsets as X) is not > 0 read as zero (ReLU backward applied on load).
   const float *xmask;
-  int relu;
+  // Activation applied last in the epilogue (batch-1 products): kActRelu
+  // (x.max(0)) or kActGelu (exact erf); with `pre` the value before it is
+  // stored there too (row stride ldc), for the activation's backward.
+  int act;
+  float *pre;
   // Optional residual added after the bias: C = alpha*X@Y + bias[q] +
   // res[p*ldr + q] (+ C) -- the "x + Linear(a)" of a residual block folded
   // into the product's epilogue (batch-1 products).
   const float *res;
   int64_t ldr;
 };
+
+// Epilogue activations: the ReLU forward kernel's x.max(0) and the unary
+// kernel's exact-erf GELU, value for value.
+constexpr int kActRelu = 1, kActGelu = 2;
+__device__ __forceinline__ float act_value(int act, float v) {
+  return act == kActRelu ? fmaxf(v, 0.0f) : numrs_hip::gelu_erf(v);
+}
 
 // Loads one 128 x 32 operand tile from global memory into registers
 // (4 x float4 per thread) with zero fill outside [0,P) x [0,R).
@@ -154,7 +163,9 @@ __device__ __forceinline__ f4 frag(const float *__restrict__ lds, int pbase, int
   }
 }
 
-template <bool XRC, bool YRC, bool VEC>
+// ACT: the epilogue applies d.act (separate instantiation, as for the
+// streamed tiles).
+template <bool XRC, bool YRC, bool VEC, bool ACT = false>
 __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, float *smem) {
   // Split-K: consecutive logical tiles are the k-ranges of one output tile.
   const int split = tile % d.splits;
@@ -286,7 +297,12 @@ __device__ __forceinline__ void gemm_tile(const Gemm &d, int tile, int batch, fl
           float v = d.alpha * a[i];
           if (d.bias != nullptr) v = v + bq[bj];
           if (d.res != nullptr) v = v + rv[blk][i];
-          *dst = d.accumulate ? *dst + v : v;
+          v = d.accumulate ? *dst + v : v;
+          if constexpr (ACT) {
+            if (d.pre != nullptr) d.pre[(int64_t)p * d.ldc + q] = v;
+            v = act_value(d.act, v);
+          }
+          *dst = v;
         }
       }
     }
@@ -302,7 +318,8 @@ struct SplitSet {
   int64_t ldc, n;
   int Q, splits, acc;
   float alpha;
-  int relu;  // clamp the result at zero (the Linear+ReLU forward)
+  int act;     // activation applied last (Gemm::act)
+  float *pre;  // optional pre-activation output (row stride ldc)
   const float *res;  // residual added after the bias (row stride ldr)
   int64_t ldr;
 };
@@ -399,12 +416,13 @@ __global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, C
   if (d.bias != nullptr) v = v + *reinterpret_cast<const V *>(d.bias + q);
   if (d.res != nullptr) v = v + *reinterpret_cast<const V *>(d.res + p * d.ldr + q);
   v = d.acc ? *dst + v : v;
-  if (d.relu) {
+  if (d.act) {
+    if (d.pre != nullptr) *reinterpret_cast<V *>(d.pre + p * d.ldc + q) = v;
     if constexpr (VEC) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
+      for (int e = 0; e < 4; ++e) v[e] = act_value(d.act, v[e]);
     } else {
-      v = fmaxf(v, 0.0f);
+      v = act_value(d.act, v);
     }
   }
   *dst = v;
@@ -417,11 +435,11 @@ __device__ __forceinline__ int xcd_tile(int b, int n) {
   return (b & 7) * (n >> 3) + (b >> 3);
 }
 
-template <bool XRC, bool YRC, bool VEC>
+template <bool XRC, bool YRC, bool VEC, bool ACT = false>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Gemm d) {
   __shared__ __attribute__((aligned(16))) float smem[4 * kTileFloats];
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  gemm_tile<XRC, YRC, VEC>(d, tile, blockIdx.y, smem);
+  gemm_tile<XRC, YRC, VEC, ACT>(d, tile, blockIdx.y, smem);
 }
 
 // Two products in one grid: logical tiles [0, tiles_a) belong to `a`, the
@@ -606,7 +624,9 @@ __device__ __forceinline__ void stream_read(
     f.b[j] = stream_frag<YRC, TQ>(yl, wq * (TQ / 2) + 32 * j, c, h, g);
 }
 
-template <bool XRC, bool YRC, int TP, int TQ, int NW = 4>
+// ACT: the epilogue applies d.act (and stores d.pre); a separate
+// instantiation, so products without an activation keep the plain epilogue.
+template <bool XRC, bool YRC, int TP, int TQ, int NW = 4, bool ACT = false>
 __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) {
   using Cfg = StreamCfg<TP, TQ, NW>;
   constexpr int kBI = Cfg::kBI, kBJ = Cfg::kBJ, kDma = Cfg::kDma;
@@ -818,7 +838,12 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
           float v = d.alpha * tot[bi][bj][i];
           if (d.bias != nullptr) v = v + bq[bj];
           if (with_res) v = v + acc[bi][bj][i];
-          *dst = d.accumulate ? *dst + v : v;
+          v = d.accumulate ? *dst + v : v;
+          if constexpr (ACT) {
+            if (d.pre != nullptr) d.pre[(int64_t)p * ldc + q] = v;
+            v = act_value(d.act, v);
+          }
+          *dst = v;
         }
       }
     }
@@ -830,14 +855,15 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
 constexpr int kBigWaves = 8;
 constexpr int kBigThreads = 64 * kBigWaves;
 
-template <bool XRC, bool YRC>
+template <bool XRC, bool YRC, bool ACT = false>
 __global__ void __launch_bounds__(kBigThreads, 1) gemm_stream_kernel(Gemm d) {
-  stream_tile<XRC, YRC, kSP, kSQ, kBigWaves>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
+  stream_tile<XRC, YRC, kSP, kSQ, kBigWaves, ACT>(d, xcd_tile(blockIdx.x, gridDim.x),
+                                                  blockIdx.y);
 }
 
-template <bool XRC, bool YRC>
+template <bool XRC, bool YRC, bool ACT = false>
 __global__ void __launch_bounds__(kThreads, 2) gemm_stream_small(Gemm d) {
-  stream_tile<XRC, YRC, kHP, kHQ>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
+  stream_tile<XRC, YRC, kHP, kHQ, 4, ACT>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
 }
 
 // Pairs on the streamed path, logical tiles [0, tiles_a) for the first
@@ -936,10 +962,11 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum
   for (int i = 0; i < m; ++i) {
     const Gemm &d = *g[i];
     set[i] = SplitSet{d.partial, d.C, d.bias, d.ldc, (int64_t)d.P * d.Q, d.Q, d.splits,
-                      d.accumulate, d.alpha, d.relu, d.res, d.ldr};
+                      d.accumulate, d.alpha, d.act, d.pre, d.res, d.ldr};
     vec = vec && d.Q % 4 == 0 && d.ldc % 4 == 0 && numrs_hip::aligned16(d.C) &&
           numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias)) &&
-          (d.res == nullptr || (numrs_hip::aligned16(d.res) && d.ldr % 4 == 0));
+          (d.res == nullptr || (numrs_hip::aligned16(d.res) && d.ldr % 4 == 0)) &&
+          (d.pre == nullptr || numrs_hip::aligned16(d.pre));
     most = std::max(most, set[i].n);
   }
   if (m == 1) set[1] = set[0];
@@ -1070,7 +1097,10 @@ __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
       if (d.bias != nullptr) v = v + d.bias[qq];
       if (d.res != nullptr) v = v + d.res[(int64_t)pp * d.ldr + qq];
       v = d.accumulate ? *dst + v : v;
-      if (d.relu) v = fmaxf(v, 0.0f);  // the ReLU forward kernel's x.max(0)
+      if (d.act) {
+        if (d.pre != nullptr) d.pre[(int64_t)pp * d.ldc + qq] = v;
+        v = act_value(d.act, v);
+      }
       *dst = v;
     }
   }
@@ -1373,7 +1403,8 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.partial = nullptr;
   g.bias = nullptr;
   g.xmask = nullptr;
-  g.relu = 0;
+  g.act = 0;
+  g.pre = nullptr;
   g.res = nullptr;
   g.ldr = 0;
   g.P = (int)P;
@@ -1401,10 +1432,20 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
     Gemm sg = g;
     if (int rc = stream_prepare(ctx, pl, sg, nullptr)) return rc;
     const dim3 grid((unsigned)stream_grid(sg), 1);
-    if (pl.small)
+    if (sg.act && sg.splits == 1) {  // activation in the tile epilogue (the Linear forward)
+      if constexpr (XRC && YRC) {
+        if (pl.small)
+          gemm_stream_small<true, true, true><<<grid, kThreads, 0, ctx->stream>>>(sg);
+        else
+          gemm_stream_kernel<true, true, true><<<grid, kBigThreads, 0, ctx->stream>>>(sg);
+      } else {
+        return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "gemm: activation on a non-NT product");
+      }
+    } else if (pl.small) {
       gemm_stream_small<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
-    else
+    } else {
       gemm_stream_kernel<XRC, YRC><<<grid, kBigThreads, 0, ctx->stream>>>(sg);
+    }
     if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
     return reduce_splits(ctx, &sg, nullptr);
   }
@@ -1428,10 +1469,20 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   if (n_tiles * splits > 0x7fffffff)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "gemm: too many tiles");
   dim3 grid((unsigned)(n_tiles * splits), (unsigned)batch);
-  if (vec_ok(g, XRC, YRC))
+  if (g.act && g.splits == 1) {  // activation in the tile epilogue (the Linear forward)
+    if constexpr (XRC && YRC) {
+      if (vec_ok(g, XRC, YRC))
+        gemm_kernel<true, true, true, true><<<grid, kThreads, 0, ctx->stream>>>(g);
+      else
+        gemm_kernel<true, true, false, true><<<grid, kThreads, 0, ctx->stream>>>(g);
+    } else {
+      return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "gemm: activation on a non-NT product");
+    }
+  } else if (vec_ok(g, XRC, YRC)) {
     gemm_kernel<XRC, YRC, true><<<grid, kThreads, 0, ctx->stream>>>(g);
-  else
+  } else {
     gemm_kernel<XRC, YRC, false><<<grid, kThreads, 0, ctx->stream>>>(g);
+  }
   if (int rc = numrs_hip::check_launch(ctx, "gemm_kernel")) return rc;
   return reduce_splits(ctx, &g, nullptr);
 }
@@ -1790,15 +1841,55 @@ int numrs_hip_linear_relu_forward(numrs_hip_ctx *ctx, const float *x, const floa
   if (T == 0 || out == 0) return NUMRS_HIP_OK;
   if (y == nullptr || (in > 0 && (x == nullptr || W == nullptr)))
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
-  if (in > 0) {
-    Gemm g = make(x, W, y, in, in, out, 0, 0, 0, T, out, in, 0);
-    g.bias = b;
-    g.relu = 1;
-    if (tiny_fits(g, 1)) return launch_tiny(ctx, g, true, true, nullptr, 1, nullptr);
+  if (in == 0) {  // empty product: ReLU of the broadcast bias
+    if (int rc = numrs_hip_linear_forward(ctx, x, W, b, y, T, in, out)) return rc;
+    return numrs_hip_unary_forward(ctx, NUMRS_HIP_RELU, y, y, T * out, 0.0f);
   }
-  // Larger products: the Linear forward, then the ReLU in place.
-  if (int rc = numrs_hip_linear_forward(ctx, x, W, b, y, T, in, out)) return rc;
-  return numrs_hip_unary_forward(ctx, NUMRS_HIP_RELU, y, y, T * out, 0.0f);
+  Gemm g = make(x, W, y, in, in, out, 0, 0, 0, T, out, in, 0);
+  g.bias = b;
+  g.act = kActRelu;
+  return gemm_dispatch(ctx, g, 1, true, true);
+}
+
+int numrs_hip_linear_gelu_forward(numrs_hip_ctx *ctx, const float *x, const float *W,
+                                  const float *b, float *y, float *pre, int64_t T, int64_t in,
+                                  int64_t out) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_gelu_forward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (T == 0 || out == 0) return NUMRS_HIP_OK;
+  if (y == nullptr || pre == nullptr || pre == y || (in > 0 && (x == nullptr || W == nullptr)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null or aliased pointer", who);
+  if (in == 0) {  // empty product: GELU of the broadcast bias
+    if (int rc = numrs_hip_linear_forward(ctx, x, W, b, pre, T, in, out)) return rc;
+    return numrs_hip_unary_forward(ctx, NUMRS_HIP_GELU, pre, y, T * out, 0.0f);
+  }
+  Gemm g = make(x, W, y, in, in, out, 0, 0, 0, T, out, in, 0);
+  g.bias = b;
+  g.act = kActGelu;
+  g.pre = pre;
+  return gemm_dispatch(ctx, g, 1, true, true);
+}
+
+int numrs_hip_linear_gelu_backward(numrs_hip_ctx *ctx, const float *g, const float *pre,
+                                   const float *x, const float *W, float *dx, float *dW,
+                                   float *db, int64_t T, int64_t in, int64_t out, int acc_dx,
+                                   int acc_dw, int acc_db, int mode) {
+  NRS_CHECK_CTX(ctx);
+  const char *who = "numrs_hip_linear_gelu_backward";
+  if (int rc = check_dims(ctx, who, 1, T, in, out)) return rc;
+  if (T == 0 || out == 0)
+    return numrs_hip_linear_backward(ctx, g, x, W, dx, dW, db, T, in, out, acc_dx, acc_dw, acc_db,
+                                     mode);
+  if (g == nullptr || pre == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
+  // The pre-activation gradient g * GELU'(pre), then the Linear backward.
+  numrs_hip::TempBlock gp(ctx);
+  if (int rc = gp.alloc((size_t)T * out * sizeof(float))) return rc;
+  if (int rc = numrs_hip_unary_backward(ctx, NUMRS_HIP_GELU, g, pre, gp.f(), T * out, 0.0f, 0))
+    return rc;
+  return numrs_hip_linear_backward(ctx, gp.f(), x, W, dx, dW, db, T, in, out, acc_dx, acc_dw,
+                                   acc_db, mode);
 }
 
 int numrs_hip_linear_relu_backward(numrs_hip_ctx *ctx, const float *g, const float *y,

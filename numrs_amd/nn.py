@@ -234,10 +234,14 @@ class TransformerEncoderBlock(Module):
         self.ff2 = Linear.with_weights(f, d, weights["w2"], np.zeros(d, np.float32), ctx)
 
     def forward_seq(self, x: Tensor, batch: int, seq: int) -> Tensor:
-        if not (self.fuse_residual and self.ff2.fused):
+        if not (self.fuse_residual and self.ff1.fused and self.ff2.fused):
             r = x.add(self.attn.forward_seq(self.ln1(x), batch, seq))
             return r.add(self.ff2(self.ff1(self.ln2(r)).gelu()))
         r = self.attn.forward_seq(self.ln1(x), batch, seq, residual=x)
+        # GELU stays a node of its own: in the FFN's first projection the
+        # epilogue would also store the pre-activation, and that 256 x 128
+        # tile epilogue (every CU writing at once) costs more than the
+        # separate pass (measured on MI355X at [4096, 2048]).
         h = self.ff1(self.ln2(r)).gelu()
         return h.linear(self.ff2.weight, self.ff2.bias, residual=r)
 

@@ -864,6 +864,47 @@ def test_linear_residual_forward(hip_ctx, rng, T, fin, fout):
     assert np.array_equal(rd.numpy(), want), "residual aliasing y"
 
 
+# Linear followed by GELU as one op, the pre-activation stored by the
+# epilogue: tiny (64, 784, 128) and (33, 17, 5), streamed (4096, 512, 2048:
+# the C4 FFN's first projection), streamed with split-K (4096, 2048, 512),
+# the 128 x 128 path (1000, 300, 136).  Bit for bit the two-op composition.
+@pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (33, 17, 5), (4096, 512, 2048),
+                                        (4096, 2048, 512), (1000, 300, 136)])
+def test_linear_gelu_forward_backward(hip_ctx, rng, T, fin, fout):
+    say(f"linear+gelu T={T} in={fin} out={fout}")
+    lib = L.load()
+    x, W, b, g = rand(rng, (T, fin)), rand(rng, (fout, fin)), rand(rng, fout), rand(rng, (T, fout))
+    c = hip_ctx
+    xd, Wd, bd, gd = (c.to_device(a) for a in (x, W, b, g))
+    y, pre, y2, pre2 = (c.empty((T, fout)) for _ in range(4))
+    assert lib.numrs_hip_linear_gelu_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, y.ptr, pre.ptr, T,
+                                             fin, fout) == 0
+    assert lib.numrs_hip_linear_forward(c.handle, xd.ptr, Wd.ptr, bd.ptr, pre2.ptr, T, fin,
+                                        fout) == 0
+    assert lib.numrs_hip_unary_forward(c.handle, L.GELU, pre2.ptr, y2.ptr, T * fout, 0.0) == 0
+    assert np.array_equal(pre.numpy(), pre2.numpy()), "pre-activation"
+    assert np.array_equal(y.numpy(), y2.numpy()), "fused forward != linear + gelu"
+    ref_pre = O.matmul_f64(x, O.transpose(W)).astype(np.float64) + b
+    assert_contraction(pre.numpy(), ref_pre, fin, what="pre")
+    assert_close(y.numpy(), O.gelu(pre.numpy().astype(np.float64)), abs_tol=1e-6, rel_tol=1e-5,
+                 what="y = gelu(pre)")
+    prev = {k: rand(rng, s) for k, s in (("dx", (T, fin)), ("dW", (fout, fin)), ("db", fout))}
+    gp = c.empty((T, fout))
+    assert lib.numrs_hip_unary_backward(c.handle, L.GELU, gd.ptr, pre.ptr, gp.ptr, T * fout, 0.0,
+                                        0) == 0
+    for acc in ((0, 0, 0), (1, 0, 1)):
+        dx, dW, db = (c.to_device(prev[k]) for k in ("dx", "dW", "db"))
+        assert lib.numrs_hip_linear_gelu_backward(c.handle, gd.ptr, pre.ptr, xd.ptr, Wd.ptr, dx.ptr,
+                                                  dW.ptr, db.ptr, T, fin, fout, *acc,
+                                                  L.UNBROADCAST_CORRECT) == 0
+        dx2, dW2, db2 = (c.to_device(prev[k]) for k in ("dx", "dW", "db"))
+        assert lib.numrs_hip_linear_backward(c.handle, gp.ptr, xd.ptr, Wd.ptr, dx2.ptr, dW2.ptr,
+                                             db2.ptr, T, fin, fout, *acc,
+                                             L.UNBROADCAST_CORRECT) == 0
+        for name, a, b2 in (("dx", dx, dx2), ("dW", dW, dW2), ("db", db, db2)):
+            assert np.array_equal(a.numpy(), b2.numpy()), f"{name} {acc}: fused != composition"
+
+
 def test_optimizer_multi_tensor_bit_exact(hip_ctx, rng):
     import ctypes
 
