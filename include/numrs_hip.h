@@ -292,6 +292,34 @@ int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_i
                             const float *dh_seq, float *dx, float *dw_ih, float *dw_hh, float *db,
                             int64_t B, int64_t T, int64_t I, int64_t H, int acc_dx, int acc_dw_ih,
                             int acc_dw_hh, int acc_db);
+/* No counterpart in the reference (numrs has no recurrent layer): two
+ * stacked LSTM layers, x [B, T, I] -> layer 1 (W_ih1 [4H1, I], W_hh1
+ * [4H1, H1], b1) -> h1_seq [B, T, H1] -> layer 2 (W_ih2 [4H2, H1], W_hh2
+ * [4H2, H2], b2) -> h2_seq [B, T, H2], zero initial states; the saved
+ * c/acts sequences as in numrs_hip_lstm_forward.  Same values as two
+ * numrs_hip_lstm_forward calls up to fp32 rounding order.  When both layers
+ * take the tiled steps (H1, H2 multiples of 256) the layers interleave: one
+ * launch runs layer 1's step t and layer 2's step t - 1, which reduces h1
+ * against W_ih2 inside the step (T + 1 dependent launches instead of 2T). */
+int numrs_hip_lstm2_forward(numrs_hip_ctx *ctx, const float *x, const float *w_ih1,
+                            const float *w_hh1, const float *b1, const float *w_ih2,
+                            const float *w_hh2, const float *b2, float *h1_seq, float *c1_seq,
+                            float *acts1, float *h2_seq, float *c2_seq, float *acts2, int64_t B,
+                            int64_t T, int64_t I, int64_t H1, int64_t H2);
+/* Its BPTT from dh2_seq [B, T, H2] (may be NULL): the gradients of x and of
+ * both layers' parameters (each may be NULL, one accumulate flag each).
+ * With H1, H2 multiples of 64 one launch runs layer 2's step t and layer
+ * 1's step t + 1, whose dh takes dG2 W_ih2 of its step directly (T + 1
+ * dependent launches instead of 2T). */
+int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_ih1,
+                             const float *w_hh1, const float *w_ih2, const float *w_hh2,
+                             const float *h1_seq, const float *c1_seq, const float *acts1,
+                             const float *h2_seq, const float *c2_seq, const float *acts2,
+                             const float *dh2_seq, float *dx, float *dw_ih1, float *dw_hh1,
+                             float *db1, float *dw_ih2, float *dw_hh2, float *db2, int64_t B,
+                             int64_t T, int64_t I, int64_t H1, int64_t H2, int acc_dx,
+                             int acc_dw_ih1, int acc_dw_hh1, int acc_db1, int acc_dw_ih2,
+                             int acc_dw_hh2, int acc_db2);
 /* y[b, :] = x[b, t, :] for x [B, T, D] (backward = 0), or its backward
  * y[b, t, :] (+)= x[b, :] over a [B, T, D] gradient, zero elsewhere when not
  * accumulating (backward = 1). */
@@ -622,6 +650,14 @@ int numrs_hip_tensor_linear_gelu(numrs_hip_tensor *x, numrs_hip_tensor *W, numrs
 int numrs_hip_tensor_linear_residual(numrs_hip_tensor *x, numrs_hip_tensor *W,
                                      numrs_hip_tensor *b, numrs_hip_tensor *res,
                                      numrs_hip_tensor **out);
+/* No counterpart in the reference: two stacked LSTM layers as one node,
+ * x [B, T, I] -> h2_seq [B, T, H2] (numrs_hip_lstm2_forward/_backward); b1
+ * and b2 may be NULL.  Same values and gradients as two LSTM nodes up to
+ * fp32 rounding order. */
+int numrs_hip_tensor_lstm2(numrs_hip_tensor *x, numrs_hip_tensor *w_ih1, numrs_hip_tensor *w_hh1,
+                           numrs_hip_tensor *b1, numrs_hip_tensor *w_ih2,
+                           numrs_hip_tensor *w_hh2, numrs_hip_tensor *b2,
+                           numrs_hip_tensor **out);
 /* LSTM layer node: x [B, T, I] -> h_seq [B, T, H] (numrs_hip_lstm_forward). */
 int numrs_hip_tensor_lstm(numrs_hip_tensor *x, numrs_hip_tensor *w_ih, numrs_hip_tensor *w_hh,
                           numrs_hip_tensor *b, numrs_hip_tensor **out);

@@ -83,6 +83,8 @@ SIGNATURES = {
     "numrs_hip_layernorm_backward": (_i, [_vp] * 9 + [_i64, _i64, _i, _i, _i]),
     "numrs_hip_lstm_forward": (_i, [_vp] * 10 + [_i64] * 4),
     "numrs_hip_lstm_backward": (_i, [_vp] * 14 + [_i64] * 4 + [_i] * 4),
+    "numrs_hip_lstm2_forward": (_i, [_vp] * 14 + [_i64] * 5),
+    "numrs_hip_lstm2_backward": (_i, [_vp] * 20 + [_i64] * 5 + [_i] * 7),
     "numrs_hip_time_slice": (_i, [_vp] * 3 + [_i64] * 4 + [_i, _i]),
     "numrs_hip_attention_forward": (_i, [_vp] * 6 + [_i64] * 4),
     "numrs_hip_attention_backward": (_i, [_vp] * 9 + [_i64] * 4 + [_i]),
@@ -124,6 +126,7 @@ SIGNATURES = {
     "numrs_hip_tensor_linear_residual": (_i, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_linear_gelu": (_i, [_vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_lstm": (_i, [_vp] * 4 + [ctypes.POINTER(_vp)]),
+    "numrs_hip_tensor_lstm2": (_i, [_vp] * 7 + [ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_time_slice": (_i, [_vp, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_attention": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
     "numrs_hip_tensor_attention_qkv": (_i, [_vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),

@@ -332,6 +332,16 @@ class Tensor:
                                                         bias._h if bias is not None else None,
                                                         ctypes.byref(h)), h)
 
+    def lstm2(self, w_ih1: "Tensor", w_hh1: "Tensor", b1: "Tensor | None", w_ih2: "Tensor",
+              w_hh2: "Tensor", b2: "Tensor | None") -> "Tensor":
+        """Two stacked LSTM layers over self [B, T, I] as one node -> the
+        upper layer's hidden states [B, T, H2] (zero initial states)."""
+        h = ctypes.c_void_p()
+        opt = lambda t: t._h if t is not None else None
+        return self._out(L.load().numrs_hip_tensor_lstm2(self._h, w_ih1._h, w_hh1._h, opt(b1),
+                                                         w_ih2._h, w_hh2._h, opt(b2),
+                                                         ctypes.byref(h)), h)
+
     def time_slice(self, t: int) -> "Tensor":
         """self[:, t, :] of a [B, T, D] tensor."""
         h = ctypes.c_void_p()

@@ -39,7 +39,7 @@ thread_local bool g_grad_enabled = true;  // mod.rs:194-206
 enum class Op {
   Leaf, Add, Sub, Mul, Div, MatMul, Transpose, Unary, Sum, Mean, MSE, CrossEntropy,
   CrossEntropyLabels, Reshape, Softmax, LayerNorm, Attention, Linear, LSTM, TimeSlice, SumAxis,
-  SoftmaxAxis
+  SoftmaxAxis, LSTM2
 };
 
 struct Storage {
@@ -573,6 +573,54 @@ int bw_lstm(const T &out, const float *g, Node &n) {
                                  nullptr, nullptr, dwh, nullptr, B, Tn, I, H, 0, 0, 1, 0);
 }
 
+// Two stacked LSTM layers (inputs x, W_ih1, W_hh1, [b1], W_ih2, W_hh2, [b2];
+// kind bit 0 / 1: b1 / b2 present; saved acts1, c1, h1, acts2, c2).  A
+// parameter whose grad cell is shared with another input (one tensor used
+// twice) gets its gradient in a temporary first, added in afterwards.
+int bw_lstm2(const T &out, const float *g, Node &n) {
+  const bool hb1 = (n.kind & 1) != 0, hb2 = (n.kind & 2) != 0;
+  size_t k = 0;
+  const T &x = n.inputs[k++];
+  const T *ps[6] = {};  // W_ih1, W_hh1, b1, W_ih2, W_hh2, b2
+  ps[0] = &n.inputs[k++];
+  ps[1] = &n.inputs[k++];
+  if (hb1) ps[2] = &n.inputs[k++];
+  ps[3] = &n.inputs[k++];
+  ps[4] = &n.inputs[k++];
+  if (hb2) ps[5] = &n.inputs[k++];
+  numrs_hip_ctx *ctx = out->ctx;
+  const int64_t B = x->shape[0], Tn = x->shape[1], I = x->shape[2];
+  const int64_t H1 = (*ps[1])->shape[1], H2 = (*ps[4])->shape[1];
+  const T *all[7] = {&x, ps[0], ps[1], ps[2], ps[3], ps[4], ps[5]};
+  float *dst[7] = {};
+  int acc[7] = {};
+  Buf tmp[7];
+  for (int i = 0; i < 7; ++i) {
+    if (all[i] == nullptr || !(*all[i])->requires_grad) continue;
+    bool shared = false;
+    for (int j = 0; j < 7; ++j)
+      if (j != i && all[j] != nullptr && (*all[j])->requires_grad &&
+          (*all[j])->grad == (*all[i])->grad)
+        shared = true;
+    if (shared) {
+      if (int rc = temp(ctx, (*all[i])->numel(), &tmp[i])) return rc;
+      dst[i] = tmp[i]->ptr;
+    } else if (int rc = grad_target(*all[i], &dst[i], &acc[i])) {
+      return rc;
+    }
+  }
+  if (int rc = numrs_hip_lstm2_backward(
+          ctx, x->data->ptr, (*ps[0])->data->ptr, (*ps[1])->data->ptr, (*ps[3])->data->ptr,
+          (*ps[4])->data->ptr, n.saved[2]->ptr, n.saved[1]->ptr, n.saved[0]->ptr, out->data->ptr,
+          n.saved[4]->ptr, n.saved[3]->ptr, g, dst[0], dst[1], dst[2], dst[3], dst[4], dst[5],
+          dst[6], B, Tn, I, H1, H2, acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6]))
+    return rc;
+  for (int i = 0; i < 7; ++i)
+    if (tmp[i])
+      if (int rc = add_into(*all[i], tmp[i]->ptr, (*all[i])->shape)) return rc;
+  return NUMRS_HIP_OK;
+}
+
 int bw_time_slice(const T &out, const float *g, Node &n) {
   const T &x = n.inputs[0];
   if (!x->requires_grad) return NUMRS_HIP_OK;
@@ -605,6 +653,7 @@ int run_backward_fn(const T &out) {
     case Op::Attention: return bw_attention(out, g, n);
     case Op::Linear: return bw_linear(out, g, n);
     case Op::LSTM: return bw_lstm(out, g, n);
+    case Op::LSTM2: return bw_lstm2(out, g, n);
     case Op::TimeSlice: return bw_time_slice(out, g, n);
     case Op::SumAxis: return bw_sum_axis(out, g, n);
     case Op::SoftmaxAxis: return bw_softmax_axis(out, g, n);
@@ -992,6 +1041,50 @@ int op_lstm(const T &x, const T &wih, const T &whh, const T *b, T *out) {
     std::vector<T> ins{x, wih, whh};
     if (b) ins.push_back(*b);
     attach(r, Op::LSTM, std::move(ins), 0, 0.f, {acts, cseq});
+  }
+  *out = std::move(r);
+  return NUMRS_HIP_OK;
+}
+
+int op_lstm2(const T &x, const T &wih1, const T &whh1, const T *b1, const T &wih2,
+             const T &whh2, const T *b2, T *out) {
+  numrs_hip_ctx *ctx = x->ctx;
+  if (x->shape.size() != 3 || wih1->shape.size() != 2 || whh1->shape.size() != 2 ||
+      wih2->shape.size() != 2 || whh2->shape.size() != 2)
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "lstm2 expects x [B,T,I] and 2-D weights");
+  const int64_t B = x->shape[0], Tn = x->shape[1], I = x->shape[2];
+  const int64_t H1 = whh1->shape[1], H2 = whh2->shape[1];
+  if (wih1->shape != std::vector<int64_t>{4 * H1, I} ||
+      whh1->shape != std::vector<int64_t>{4 * H1, H1} ||
+      wih2->shape != std::vector<int64_t>{4 * H2, H1} ||
+      whh2->shape != std::vector<int64_t>{4 * H2, H2} || (b1 && (*b1)->numel() != 4 * H1) ||
+      (b2 && (*b2)->numel() != 4 * H2))
+    return fail(ctx, NUMRS_HIP_E_SHAPE, "lstm2: weight shapes do not match H1 = %lld, H2 = %lld",
+                (long long)H1, (long long)H2);
+  const T *all[7] = {&x, &wih1, &whh1, b1, &wih2, &whh2, b2};
+  bool rec = false;
+  for (const T *t : all) rec = rec || (t != nullptr && (*t)->requires_grad && g_grad_enabled);
+  T r;
+  if (int rc = make_tensor(ctx, {B, Tn, H2}, rec, &r)) return rc;
+  Buf acts1, c1, h1, acts2, c2;
+  if (int rc = alloc_buf(ctx, B * Tn * 4 * H1, sizeof(float), &acts1)) return rc;
+  if (int rc = alloc_buf(ctx, B * Tn * H1, sizeof(float), &c1)) return rc;
+  if (int rc = alloc_buf(ctx, B * Tn * H1, sizeof(float), &h1)) return rc;
+  if (int rc = alloc_buf(ctx, B * Tn * 4 * H2, sizeof(float), &acts2)) return rc;
+  if (int rc = alloc_buf(ctx, B * Tn * H2, sizeof(float), &c2)) return rc;
+  if (int rc = numrs_hip_lstm2_forward(
+          ctx, x->data->ptr, wih1->data->ptr, whh1->data->ptr, b1 ? (*b1)->data->ptr : nullptr,
+          wih2->data->ptr, whh2->data->ptr, b2 ? (*b2)->data->ptr : nullptr, h1->ptr, c1->ptr,
+          acts1->ptr, r->data->ptr, c2->ptr, acts2->ptr, B, Tn, I, H1, H2))
+    return rc;
+  if (rec) {
+    std::vector<T> ins{x, wih1, whh1};
+    if (b1) ins.push_back(*b1);
+    ins.push_back(wih2);
+    ins.push_back(whh2);
+    if (b2) ins.push_back(*b2);
+    attach(r, Op::LSTM2, std::move(ins), (b1 ? 1 : 0) | (b2 ? 2 : 0), 0.f,
+           {acts1, c1, h1, acts2, c2});
   }
   *out = std::move(r);
   return NUMRS_HIP_OK;
@@ -1593,6 +1686,20 @@ int numrs_hip_tensor_lstm(numrs_hip_tensor *x, numrs_hip_tensor *w_ih, numrs_hip
     return NUMRS_HIP_E_INVALID;
   T r;
   if (int rc = op_lstm(x->t, w_ih->t, w_hh->t, b ? &b->t : nullptr, &r)) return rc;
+  return wrap(std::move(r), out);
+}
+
+int numrs_hip_tensor_lstm2(numrs_hip_tensor *x, numrs_hip_tensor *w_ih1, numrs_hip_tensor *w_hh1,
+                           numrs_hip_tensor *b1, numrs_hip_tensor *w_ih2,
+                           numrs_hip_tensor *w_hh2, numrs_hip_tensor *b2,
+                           numrs_hip_tensor **out) {
+  if (x == nullptr || w_ih1 == nullptr || w_hh1 == nullptr || w_ih2 == nullptr ||
+      w_hh2 == nullptr || out == nullptr)
+    return NUMRS_HIP_E_INVALID;
+  T r;
+  if (int rc = op_lstm2(x->t, w_ih1->t, w_hh1->t, b1 ? &b1->t : nullptr, w_ih2->t, w_hh2->t,
+                        b2 ? &b2->t : nullptr, &r))
+    return rc;
   return wrap(std::move(r), out);
 }
 

@@ -319,14 +319,26 @@ constexpr int kBUnits = 8;   // backward: hidden units per workgroup
 // 4(l / 16) .. +3; the four wave partials meet in LDS and are added in wave
 // order, and wave 0 finishes the 64 cells (lane = 4m + u).  The epilogue's
 // inputs are loaded before the product, so their latencies overlap.
-__global__ void __launch_bounds__(256)
-    lstm_fwd_step_tiled(float *G, const float *__restrict__ whh, const float *__restrict__ h0,
-                        const float *__restrict__ c0, float *__restrict__ h_seq,
-                        float *__restrict__ c_seq, int B, int T, int H, int t) {
+// One layer's forward step for the tiled kernels.  G [B, T, 4H] holds the
+// input projection x W_ih^T + b on entry (xin == nullptr) and the
+// activations on exit.  With xin (a stacked layer fed by the layer below in
+// the same launch), the step reduces its input rows xin[b, t, :] [B, T, I]
+// against W_ih [4H, I] as well, and the bias (may be null) stands in for G.
+struct FwdStep {
+  float *G;
+  const float *whh;
+  const float *xin, *wih, *bias;
+  const float *h0, *c0;
+  float *h_seq, *c_seq;
+  int H, I, t;
+};
+
+__device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, int T) {
   __shared__ float part[4][kFRows][16];
+  const int H = s.H, t = s.t;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ugroups = H / kFUnits;
-  const int ug = blockIdx.x % ugroups, rg = blockIdx.x / ugroups;
+  const int ug = blk % ugroups, rg = blk / ugroups;
   const int j0 = ug * kFUnits, b0 = rg * kFRows;
   const int H4 = 4 * H;
 
@@ -338,31 +350,38 @@ __global__ void __launch_bounds__(256)
   float gin[4] = {0.0f, 0.0f, 0.0f, 0.0f}, cp = 0.0f;
   if (epi) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) gin[g] = G[gb + g * H + je];
-    cp = t > 0 ? c_seq[((int64_t)be * T + t - 1) * H + je]
-               : (c0 != nullptr ? c0[(int64_t)be * H + je] : 0.0f);
+    for (int g = 0; g < 4; ++g)
+      gin[g] = s.xin == nullptr ? s.G[gb + g * H + je]
+                                : (s.bias != nullptr ? s.bias[g * H + je] : 0.0f);
+    cp = t > 0 ? s.c_seq[((int64_t)be * T + t - 1) * H + je]
+               : (s.c0 != nullptr ? s.c0[(int64_t)be * H + je] : 0.0f);
   }
 
+  // pre[m][c] = sum_k a[m][k] w[n(c)][k] over one operand pair, the
+  // reduction split over the four waves in 64-long blocks.
+  const int r = lane & 15, q = lane >> 4;
+  const int b = min(b0 + r, B - 1);
   f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (t > 0 || h0 != nullptr) {
-    const int r = lane & 15, q = lane >> 4;
-    const int b = min(b0 + r, B - 1);
-    const float *hrow = t > 0 ? h_seq + ((int64_t)b * T + t - 1) * H : h0 + (int64_t)b * H;
-    const float *wrow = whh + (int64_t)((r >> 2) * H + j0 + (r & 3)) * H;
-    const int kw = H >> 2;
+  auto reduce = [&](const float *arow, const float *wrow, int K) {
+    const int kw = K >> 2;
     for (int kb = wave * kw; kb < (wave + 1) * kw; kb += 64) {
       f4 a[4], w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        a[i] = *reinterpret_cast<const f4 *>(hrow + kb + 16 * i + 4 * q);
+        a[i] = *reinterpret_cast<const f4 *>(arow + kb + 16 * i + 4 * q);
         w[i] = *reinterpret_cast<const f4 *>(wrow + kb + 16 * i + 4 * q);
       }
 #pragma unroll
-      for (int s = 0; s < 16; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s >> 2][s & 3], w[s >> 2][s & 3], acc, 0, 0,
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e >> 2][e & 3], w[e >> 2][e & 3], acc, 0, 0,
                                                    0);
     }
-  }
+  };
+  const int64_t wr = (int64_t)((r >> 2) * H + j0 + (r & 3));  // W row n(c) of column r
+  if (t > 0 || s.h0 != nullptr)
+    reduce(t > 0 ? s.h_seq + ((int64_t)b * T + t - 1) * H : s.h0 + (int64_t)b * H,
+           s.whh + wr * H, H);
+  if (s.xin != nullptr) reduce(s.xin + ((int64_t)b * T + t) * s.I, s.wih + wr * s.I, s.I);
 #pragma unroll
   for (int v = 0; v < 4; ++v) part[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
   __syncthreads();
@@ -379,12 +398,30 @@ __global__ void __launch_bounds__(256)
   const float o = sigm(pre[3]);
   const float c = f * cp + i * g;
   const float h = o * tanhf(c);
-  G[gb + je] = i;
-  G[gb + H + je] = f;
-  G[gb + 2 * H + je] = g;
-  G[gb + 3 * H + je] = o;
-  c_seq[((int64_t)be * T + t) * H + je] = c;
-  h_seq[((int64_t)be * T + t) * H + je] = h;
+  s.G[gb + je] = i;
+  s.G[gb + H + je] = f;
+  s.G[gb + 2 * H + je] = g;
+  s.G[gb + 3 * H + je] = o;
+  s.c_seq[((int64_t)be * T + t) * H + je] = c;
+  s.h_seq[((int64_t)be * T + t) * H + je] = h;
+}
+
+__global__ void __launch_bounds__(256) lstm_fwd_step_tiled(FwdStep s, int B, int T) {
+  fwd_step_tile(s, blockIdx.x, B, T);
+}
+
+// Two stacked layers in one launch (the diagonal schedule): workgroups
+// [0, blocks_a) run step a.t of the lower layer, the rest step b.t of the
+// upper one, which reads the lower layer's h at b.t -- finished by the
+// previous launch.  (Splitting the upper step's input projection into a job
+// of its own, one step ahead, measured slower on MI355X: a launch's time
+// follows its workgroup count more than its reduction depth.)
+__global__ void __launch_bounds__(256)
+    lstm_fwd_diag(FwdStep a, FwdStep b, int blocks_a, int B, int T) {
+  if ((int)blockIdx.x < blocks_a)
+    fwd_step_tile(a, blockIdx.x, B, T);
+  else
+    fwd_step_tile(b, blockIdx.x - blocks_a, B, T);
 }
 
 // Backward step t on the VALU.  The product dh[b][j] = sum_n dG_{t+1}[b][n]
@@ -400,14 +437,28 @@ __global__ void __launch_bounds__(256)
 // slower per step), and lane 4c finishes cell c.  dc holds
 // dc_{t+1} f_{t+1} on entry and dc_t f_t on exit, each (b, j) touched by one
 // lane only.
-__global__ void __launch_bounds__(256)
-    lstm_bwd_step_tiled(float *__restrict__ dG, const float *__restrict__ wt,
-                        const float *__restrict__ acts, const float *__restrict__ c_seq,
-                        const float *__restrict__ c0, const float *__restrict__ dh_out,
-                        float *__restrict__ dc, int B, int T, int H, int t) {
+// One layer's backward step for the tiled kernels.  dG [B, T, 4H] receives
+// the step's gate gradients; wt is W_hh^T [H, 4H]; dh_out [B, T, H] (may be
+// null) is the gradient arriving at h_t from outside the recurrence.  With
+// dG_up (a stacked layer whose output feeds the layer above, run in the same
+// launch one step behind), dh also takes dG_up[b, t, :] W_ih_up from the
+// upper layer's gate gradients of step t (finished by the previous launch),
+// wt_up = W_ih_up^T [H, 4Hu].
+struct BwdStep {
+  float *dG;
+  const float *wt;
+  const float *acts, *c_seq, *c0;
+  const float *dh_out;
+  const float *dG_up, *wt_up;
+  float *dc;
+  int H, Hu, t;
+};
+
+__device__ __forceinline__ void bwd_step_tile(const BwdStep &s, int blk, int B, int T) {
+  const int H = s.H, t = s.t;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ugroups = H / kBUnits;
-  const int ug = blockIdx.x % ugroups, rg = blockIdx.x / ugroups;
+  const int ug = blk % ugroups, rg = blk / ugroups;
   const int rb = rg * kBRows + 4 * (wave >> 1), ub = ug * kBUnits + 4 * (wave & 1);
   const int H4 = 4 * H;
   const bool has_next = t + 1 < T;
@@ -421,26 +472,29 @@ __global__ void __launch_bounds__(256)
   float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, c = 0.0f, cp = 0.0f, dho = 0.0f, dcn = 0.0f;
   if (epi) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) a[g] = acts[gb + g * H + je];
-    c = c_seq[row * H + je];
-    cp = t > 0 ? c_seq[(row - 1) * H + je] : (c0 != nullptr ? c0[(int64_t)be * H + je] : 0.0f);
-    if (dh_out != nullptr) dho = dh_out[row * H + je];
-    if (has_next) dcn = dc[(int64_t)be * H + je];
+    for (int g = 0; g < 4; ++g) a[g] = s.acts[gb + g * H + je];
+    c = s.c_seq[row * H + je];
+    cp = t > 0 ? s.c_seq[(row - 1) * H + je]
+               : (s.c0 != nullptr ? s.c0[(int64_t)be * H + je] : 0.0f);
+    if (s.dh_out != nullptr) dho = s.dh_out[row * H + je];
+    if (has_next) dcn = s.dc[(int64_t)be * H + je];
   }
 
   float v[16];  // cell (i, u) of the wave's block at 4i + u
 #pragma unroll
   for (int k = 0; k < 16; ++k) v[k] = 0.0f;
-  if (has_next) {
+  // v += sum_n d[row i][n] w[unit u][n] over this lane's slice of a 4Hx-long
+  // reduction (d row stride and w row stride 4Hx).
+  auto reduce = [&](const float *dbase, int64_t tt, const float *wbase, int Hx) {
+    const int Hx4 = 4 * Hx;
     const float *drow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      drow[i] = dG + ((int64_t)min(rb + i, B - 1) * T + t + 1) * H4;
-    const int ns = H >> 4;  // slice length, a multiple of 4
+    for (int i = 0; i < 4; ++i) drow[i] = dbase + ((int64_t)min(rb + i, B - 1) * T + tt) * Hx4;
+    const int ns = Hx >> 4;  // slice length, a multiple of 4
     const int n0 = lane * ns;
     const float *wrow[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) wrow[u] = wt + (int64_t)(ub + u) * H4;
+    for (int u = 0; u < 4; ++u) wrow[u] = wbase + (int64_t)(ub + u) * Hx4;
     for (int nb = n0; nb < n0 + ns; nb += 16) {
       f4 d[4][4], w[4][4];  // [n group][row], [n group][unit]
 #pragma unroll
@@ -456,15 +510,17 @@ __global__ void __launch_bounds__(256)
       for (int e = 0; e < 4; ++e) {
         if (nb + 4 * e < n0 + ns) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
+          for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-              for (int u = 0; u < 4; ++u) v[4 * i + u] += d[e][i][s] * w[e][u][s];
+              for (int u = 0; u < 4; ++u) v[4 * i + u] += d[e][i][q] * w[e][u][q];
         }
       }
     }
-  }
+  };
+  if (has_next) reduce(s.dG, t + 1, s.wt, H);
+  if (s.dG_up != nullptr) reduce(s.dG_up, t, s.wt_up, s.Hu);
   // The 64 lanes' partials of the wave's 16 cells, summed through LDS: the
   // partials are stored cell-major, lane l reads the 16 partials of cell
   // l / 4 from lanes 16 (l % 4) .. +15 as four float4s and adds them in a
@@ -489,11 +545,26 @@ __global__ void __launch_bounds__(256)
   const float dh = dho + r;
   const float tc = tanhf(c);
   const float dct = dh * o * (1.0f - tc * tc) + dcn;
-  dG[gb + je] = (dct * g) * i * (1.0f - i);
-  dG[gb + H + je] = (dct * cp) * f * (1.0f - f);
-  dG[gb + 2 * H + je] = (dct * i) * (1.0f - g * g);
-  dG[gb + 3 * H + je] = (dh * tc) * o * (1.0f - o);
-  dc[(int64_t)be * H + je] = dct * f;
+  s.dG[gb + je] = (dct * g) * i * (1.0f - i);
+  s.dG[gb + H + je] = (dct * cp) * f * (1.0f - f);
+  s.dG[gb + 2 * H + je] = (dct * i) * (1.0f - g * g);
+  s.dG[gb + 3 * H + je] = (dh * tc) * o * (1.0f - o);
+  s.dc[(int64_t)be * H + je] = dct * f;
+}
+
+__global__ void __launch_bounds__(256) lstm_bwd_step_tiled(BwdStep s, int B, int T) {
+  bwd_step_tile(s, blockIdx.x, B, T);
+}
+
+// Two stacked layers' backward in one launch: workgroups [0, blocks_a) run
+// step a.t of the upper layer, the rest step b.t = a.t + 1 of the lower
+// layer, whose dh takes the upper layer's dG at b.t from the previous launch.
+__global__ void __launch_bounds__(256)
+    lstm_bwd_diag(BwdStep a, BwdStep b, int blocks_a, int B, int T) {
+  if ((int)blockIdx.x < blocks_a)
+    bwd_step_tile(a, blockIdx.x, B, T);
+  else
+    bwd_step_tile(b, blockIdx.x - blocks_a, B, T);
 }
 
 // Whether the tiled step kernels take this shape.  The forward walks each
@@ -555,6 +626,43 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// One layer's parameter and input gradients from its gate gradients dG
+// [B*T, 4H] of every step, batched over time as single products:
+// dW_ih = dG^T x, dW_hh = dG^T H_prev, db = column sum of dG, dx = dG W_ih
+// (each output may be null).
+int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const float *w_ih,
+                     const float *h_seq, const float *h0, float *dx, float *dw_ih, float *dw_hh,
+                     float *db, int64_t B, int64_t T, int64_t I, int64_t H, int acc_dx,
+                     int acc_dw_ih, int acc_dw_hh, int acc_db) {
+  const int64_t rows = B * T, H4 = 4 * H;
+  if (dw_ih)  // dW_ih[4H, I] = dG^T x
+    if (int rc = numrs_hip_gemm(ctx, dG, H4, x, I, dw_ih, I, H4, rows, I, 1, 0, 1.0f, acc_dw_ih,
+                                1, 1, 0, 0, 0, 0, 0, 0))
+      return rc;
+  if (dw_hh) {  // dW_hh[4H, H] = dG^T H_prev
+    TempBlock hp(ctx);
+    if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
+    shift_hidden<<<grid_for(rows * H, 256), 256, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)B,
+                                                                   (int)T, (int)H);
+    if (int rc = numrs_hip::check_launch(ctx, "shift_hidden")) return rc;
+    if (int rc = numrs_hip_gemm(ctx, dG, H4, hp.f(), H, dw_hh, H, H4, rows, H, 1, 0, 1.0f,
+                                acc_dw_hh, 1, 1, 0, 0, 0, 0, 0, 0))
+      return rc;
+  }
+  if (db) {  // db[4H] = column sum of dG
+    const int64_t gs[2] = {rows, H4};
+    const int64_t bs = H4;
+    if (int rc = numrs_hip_sum_to_shape(ctx, dG, gs, 2, db, &bs, 1,
+                                        NUMRS_HIP_UNBROADCAST_CORRECT, acc_db))
+      return rc;
+  }
+  if (dx)  // dx[B*T, I] = dG W_ih
+    if (int rc = numrs_hip_gemm(ctx, dG, H4, w_ih, I, dx, I, rows, H4, I, 0, 0, 1.0f, acc_dx, 1,
+                                1, 0, 0, 0, 0, 0, 0))
+      return rc;
+  return NUMRS_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -571,9 +679,10 @@ int numrs_hip_lstm_forward(numrs_hip_ctx *ctx, const float *x, const float *w_ih
   if (int rc = numrs_hip_linear_forward(ctx, x, w_ih, b, acts, B * T, I, 4 * H)) return rc;
   if (tiled_fwd_fits(H, w_hh, h_seq, h0)) {
     const unsigned grid = (unsigned)((H / kFUnits) * ((B + kFRows - 1) / kFRows));
+    FwdStep st{acts, w_hh, nullptr, nullptr, nullptr, h0, c0, h_seq, c_seq, (int)H, 0, 0};
     for (int64_t t = 0; t < T; ++t) {
-      lstm_fwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(acts, w_hh, h0, c0, h_seq, c_seq,
-                                                          (int)B, (int)T, (int)H, (int)t);
+      st.t = (int)t;
+      lstm_fwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(st, (int)B, (int)T);
       if (int rc = numrs_hip::check_launch(ctx, "lstm_fwd_step_tiled")) return rc;
     }
     return NUMRS_HIP_OK;
@@ -618,9 +727,10 @@ int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_i
     if (int rc = wt.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
     if (int rc = numrs_hip_transpose(ctx, w_hh, wt.f(), 4 * H, H)) return rc;
     const unsigned grid = (unsigned)((H / kBUnits) * ((B + kBRows - 1) / kBRows));
+    BwdStep st{dG.f(), wt.f(), acts, c_seq, c0, dh_seq, nullptr, nullptr, dc.f(), (int)H, 0, 0};
     for (int64_t t = T - 1; t >= 0; --t) {
-      lstm_bwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(dG.f(), wt.f(), acts, c_seq, c0, dh_seq,
-                                                          dc.f(), (int)B, (int)T, (int)H, (int)t);
+      st.t = (int)t;
+      lstm_bwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(st, (int)B, (int)T);
       if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step_tiled")) return rc;
     }
   } else {
@@ -641,33 +751,110 @@ int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_i
       if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step")) return rc;
     }
   }
-  // Weight gradients over all steps at once (batched over time).
-  if (dw_ih)  // dW_ih[4H, I] = dG^T x
-    if (int rc = numrs_hip_gemm(ctx, dG.f(), H4, x, I, dw_ih, I, H4, rows, I, 1, 0, 1.0f,
-                                acc_dw_ih, 1, 1, 0, 0, 0, 0, 0, 0))
+  return lstm_param_grads(ctx, dG.f(), x, w_ih, h_seq, h0, dx, dw_ih, dw_hh, db, B, T, I, H,
+                          acc_dx, acc_dw_ih, acc_dw_hh, acc_db);
+}
+
+int numrs_hip_lstm2_forward(numrs_hip_ctx *ctx, const float *x, const float *w_ih1,
+                            const float *w_hh1, const float *b1, const float *w_ih2,
+                            const float *w_hh2, const float *b2, float *h1_seq, float *c1_seq,
+                            float *acts1, float *h2_seq, float *c2_seq, float *acts2, int64_t B,
+                            int64_t T, int64_t I, int64_t H1, int64_t H2) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check(ctx, B, T, I, H1)) return rc;
+  if (int rc = check(ctx, B, T, H1, H2)) return rc;
+  if (!x || !w_ih1 || !w_hh1 || !w_ih2 || !w_hh2 || !h1_seq || !c1_seq || !acts1 || !h2_seq ||
+      !c2_seq || !acts2)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "lstm2_forward: null pointer");
+  const bool diag = tiled_fwd_fits(H1, w_hh1, h1_seq, nullptr) &&
+                    tiled_fwd_fits(H2, w_hh2, h2_seq, nullptr) && numrs_hip::aligned16(w_ih2);
+  if (!diag) {  // one layer after the other
+    if (int rc = numrs_hip_lstm_forward(ctx, x, w_ih1, w_hh1, b1, nullptr, nullptr, h1_seq, c1_seq,
+                                        acts1, B, T, I, H1))
       return rc;
-  if (dw_hh) {  // dW_hh[4H, H] = dG^T H_prev
-    TempBlock hp(ctx);
-    if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
-    shift_hidden<<<grid_for(rows * H, 256), 256, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)B,
-                                                                   (int)T, (int)H);
-    if (int rc = numrs_hip::check_launch(ctx, "shift_hidden")) return rc;
-    if (int rc = numrs_hip_gemm(ctx, dG.f(), H4, hp.f(), H, dw_hh, H, H4, rows, H, 1, 0, 1.0f,
-                                acc_dw_hh, 1, 1, 0, 0, 0, 0, 0, 0))
-      return rc;
+    return numrs_hip_lstm_forward(ctx, h1_seq, w_ih2, w_hh2, b2, nullptr, nullptr, h2_seq, c2_seq,
+                                  acts2, B, T, H1, H2);
   }
-  if (db) {  // db[4H] = column sum of dG
-    const int64_t gs[2] = {rows, H4};
-    const int64_t bs = H4;
-    if (int rc = numrs_hip_sum_to_shape(ctx, dG.f(), gs, 2, db, &bs, 1,
-                                        NUMRS_HIP_UNBROADCAST_CORRECT, acc_db))
-      return rc;
+  // acts1 <- x W_ih1^T + b1 for every (b, t) row; the upper layer reduces
+  // h1 against W_ih2 inside its steps.
+  if (int rc = numrs_hip_linear_forward(ctx, x, w_ih1, b1, acts1, B * T, I, 4 * H1)) return rc;
+  FwdStep lo{acts1, w_hh1, nullptr, nullptr, nullptr, nullptr, nullptr, h1_seq, c1_seq,
+             (int)H1, 0, 0};
+  FwdStep up{acts2, w_hh2, h1_seq, w_ih2, b2, nullptr, nullptr, h2_seq, c2_seq, (int)H2, (int)H1,
+             0};
+  const int rgroups = (int)((B + kFRows - 1) / kFRows);
+  const int g_lo = (int)(H1 / kFUnits) * rgroups, g_up = (int)(H2 / kFUnits) * rgroups;
+  // Launch d: lower step d and upper step d - 1.
+  for (int64_t d = 0; d <= T; ++d) {
+    const int ga = d < T ? g_lo : 0, gb = d >= 1 ? g_up : 0;
+    lo.t = (int)d;
+    up.t = (int)d - 1;
+    lstm_fwd_diag<<<(unsigned)(ga + gb), 256, 0, ctx->stream>>>(lo, up, ga, (int)B, (int)T);
+    if (int rc = numrs_hip::check_launch(ctx, "lstm_fwd_diag")) return rc;
   }
-  if (dx)  // dx[B*T, I] = dG W_ih
-    if (int rc = numrs_hip_gemm(ctx, dG.f(), H4, w_ih, I, dx, I, rows, H4, I, 0, 0, 1.0f, acc_dx,
-                                1, 1, 0, 0, 0, 0, 0, 0))
-      return rc;
   return NUMRS_HIP_OK;
+}
+
+int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_ih1,
+                             const float *w_hh1, const float *w_ih2, const float *w_hh2,
+                             const float *h1_seq, const float *c1_seq, const float *acts1,
+                             const float *h2_seq, const float *c2_seq, const float *acts2,
+                             const float *dh2_seq, float *dx, float *dw_ih1, float *dw_hh1,
+                             float *db1, float *dw_ih2, float *dw_hh2, float *db2, int64_t B,
+                             int64_t T, int64_t I, int64_t H1, int64_t H2, int acc_dx,
+                             int acc_dw_ih1, int acc_dw_hh1, int acc_db1, int acc_dw_ih2,
+                             int acc_dw_hh2, int acc_db2) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check(ctx, B, T, I, H1)) return rc;
+  if (int rc = check(ctx, B, T, H1, H2)) return rc;
+  if (!x || !w_ih1 || !w_hh1 || !w_ih2 || !w_hh2 || !h1_seq || !c1_seq || !acts1 || !h2_seq ||
+      !c2_seq || !acts2)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "lstm2_backward: null input");
+  TempBlock dG1(ctx), dG2(ctx);
+  if (int rc = dG1.alloc((size_t)(B * T * 4 * H1) * sizeof(float))) return rc;
+  if (int rc = dG2.alloc((size_t)(B * T * 4 * H2) * sizeof(float))) return rc;
+  const bool diag = tiled_bwd_fits(H1, w_hh1, dG1.p) && tiled_bwd_fits(H2, w_hh2, dG2.p) &&
+                    numrs_hip::aligned16(w_ih2);
+  if (!diag) {  // the upper layer's backward, then the lower one's from its dx
+    TempBlock dh1(ctx);
+    if (int rc = dh1.alloc((size_t)(B * T * H1) * sizeof(float))) return rc;
+    if (int rc = numrs_hip_lstm_backward(ctx, h1_seq, w_ih2, w_hh2, nullptr, nullptr, h2_seq,
+                                         c2_seq, acts2, dh2_seq, dh1.f(), dw_ih2, dw_hh2, db2, B,
+                                         T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2))
+      return rc;
+    return numrs_hip_lstm_backward(ctx, x, w_ih1, w_hh1, nullptr, nullptr, h1_seq, c1_seq, acts1,
+                                   dh1.f(), dx, dw_ih1, dw_hh1, db1, B, T, I, H1, acc_dx,
+                                   acc_dw_ih1, acc_dw_hh1, acc_db1);
+  }
+  TempBlock dc1(ctx), dc2(ctx), wt1(ctx), wt2(ctx), wtu(ctx);
+  if (int rc = dc1.alloc((size_t)(B * H1) * sizeof(float))) return rc;
+  if (int rc = dc2.alloc((size_t)(B * H2) * sizeof(float))) return rc;
+  if (int rc = wt1.alloc((size_t)(4 * H1 * H1) * sizeof(float))) return rc;
+  if (int rc = wt2.alloc((size_t)(4 * H2 * H2) * sizeof(float))) return rc;
+  if (int rc = wtu.alloc((size_t)(4 * H2 * H1) * sizeof(float))) return rc;
+  if (int rc = numrs_hip_transpose(ctx, w_hh1, wt1.f(), 4 * H1, H1)) return rc;  // [H1, 4H1]
+  if (int rc = numrs_hip_transpose(ctx, w_hh2, wt2.f(), 4 * H2, H2)) return rc;  // [H2, 4H2]
+  if (int rc = numrs_hip_transpose(ctx, w_ih2, wtu.f(), 4 * H2, H1)) return rc;  // [H1, 4H2]
+  BwdStep up{dG2.f(), wt2.f(), acts2, c2_seq, nullptr, dh2_seq, nullptr, nullptr, dc2.f(),
+             (int)H2, 0, 0};
+  BwdStep lo{dG1.f(), wt1.f(), acts1, c1_seq, nullptr, nullptr, dG2.f(), wtu.f(), dc1.f(),
+             (int)H1, (int)H2, 0};
+  const int rgroups = (int)((B + kBRows - 1) / kBRows);
+  const int g_up = (int)(H2 / kBUnits) * rgroups, g_lo = (int)(H1 / kBUnits) * rgroups;
+  // Launch d: upper step T-1-d and lower step T-d (the lower layer's dh at
+  // step T-d takes the upper layer's dG of that step from launch d-1).
+  for (int64_t d = 0; d <= T; ++d) {
+    const int ga = d < T ? g_up : 0, gb = d >= 1 ? g_lo : 0;
+    up.t = (int)(T - 1 - d);
+    lo.t = (int)(T - d);
+    lstm_bwd_diag<<<(unsigned)(ga + gb), 256, 0, ctx->stream>>>(up, lo, ga, (int)B, (int)T);
+    if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_diag")) return rc;
+  }
+  if (int rc = lstm_param_grads(ctx, dG2.f(), h1_seq, w_ih2, h2_seq, nullptr, nullptr, dw_ih2,
+                                dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2))
+    return rc;
+  return lstm_param_grads(ctx, dG1.f(), x, w_ih1, h1_seq, nullptr, dx, dw_ih1, dw_hh1, db1, B, T,
+                          I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1);
 }
 
 int numrs_hip_time_slice(numrs_hip_ctx *ctx, const float *x, float *y, int64_t B, int64_t T,

@@ -22,9 +22,14 @@ pytestmark = pytest.mark.gpu
                                   dict(B=3, T=4, I=8, H=1040), dict(B=2, T=3, I=8, H=2056)],
                          ids=["tiny", "medium", "ragged", "baseline", "tiled_rows",
                               "bwd_tiled_h192", "wide_unstaged_bwd", "wide_unstaged"])
-def test_lstm_forecaster_matches_oracle(hip_ctx, dims):
-    print(f"[gpu] lstm forecaster {dims}", flush=True)
+@pytest.mark.parametrize("stack", [True, False], ids=["stacked", "per_layer"])
+def test_lstm_forecaster_matches_oracle(hip_ctx, dims, stack, monkeypatch):
+    # stacked: both layers as one node (numrs_hip_lstm2_*: the diagonal
+    # schedule where both layers take the tiled steps, the per-layer
+    # sequence otherwise); per_layer: one node per layer.
+    print(f"[gpu] lstm forecaster {dims} stack={stack}", flush=True)
     nr.set_default_context(hip_ctx)
+    monkeypatch.setattr(nn.LSTMForecaster, "fuse_stack", stack)
     layers, hw, hb, x, target = LO.make_c5(seed=7, n_layers=2, **dims)
     model = nn.LSTMForecaster(layers, hw, hb)
     xt = Tensor.new(x, True)
@@ -61,3 +66,35 @@ def test_time_slice_grad(hip_ctx):
     y.sum().backward()
     g = x.gradient()
     assert (g[:, 1] == 1).all() and (g[:, 0] == 0).all() and (g[:, 2] == 0).all()
+
+
+@pytest.mark.parametrize("H", [64, 256])
+def test_lstm_stack_shared_weight_matches_two_layers(hip_ctx, H, monkeypatch):
+    """One tensor as W_hh of both layers (and I = H): the stacked node's
+    gradient for it is the sum of both layers' parts, as with two nodes.
+    H = 64 runs the diagonal backward after a per-layer forward; H = 256 the
+    diagonal schedule both ways."""
+    print(f"[gpu] lstm stack shared weight H={H}", flush=True)
+    nr.set_default_context(hip_ctx)
+    rng = np.random.default_rng(H)
+    B, T = 8, 5
+    x = (rng.standard_normal((B, T, H)) * 0.5).astype(np.float32)
+    w = lambda *s: (rng.standard_normal(s) * 0.1).astype(np.float32)
+    wih1, whh, b1, wih2, b2 = w(4 * H, H), w(4 * H, H), w(4 * H), w(4 * H, H), w(4 * H)
+    up = rng.standard_normal((B, T, H)).astype(np.float32)
+    out = []
+    for stack in (True, False):
+        monkeypatch.setattr(nn.LSTMForecaster, "fuse_stack", stack)
+        xt = Tensor.new(x, True)
+        t_whh = Tensor.new(whh, True)
+        t = [Tensor.new(a, True) for a in (wih1, b1, wih2, b2)]
+        if stack:
+            y = xt.lstm2(t[0], t_whh, t[1], t[2], t_whh, t[3])
+        else:
+            y = xt.lstm(t[0], t_whh, t[1]).lstm(t[2], t_whh, t[3])
+        y.mul(Tensor.new(up, False)).sum().backward()
+        out.append([y.values(), xt.gradient(), t_whh.gradient()] + [a.gradient() for a in t])
+    names = ["y", "x", "w_hh (shared)", "w_ih1", "b1", "w_ih2", "b2"]
+    for name, a, b in zip(names, *out):
+        scale = max(np.abs(b).max(), 1e-6)
+        assert np.abs(a - b).max() <= 1e-5 * scale + 1e-6, name
