@@ -567,6 +567,99 @@ __global__ void __launch_bounds__(256)
     bwd_step_tile(b, blockIdx.x - blocks_a, B, T);
 }
 
+// Backward step on fp32 MFMA (H % 256 == 0; for a stacked lower layer also
+// Hu % 256 == 0).  Workgroup (unit group, row group) owns rows b0..b0+15 and
+// units j0..j0+15 and computes dh[m][u] = sum_n dG_{t+1}[b0+m][n]
+// W_hh[n][j0+u] (+ sum_n dG_up[b0+m][n] W_ih_up[n][j0+u]) as
+// v_mfma_f32_16x16x4f32: A = dG row b0 + (l % 16), B = W^T row j0 + (l % 16),
+// both at n = nb + 16i + 4(l / 16) + e, so each lane's operands are float4
+// loads; the 4H-long reduction is split over 16 waves, 64 per wave, and the
+// 16 wave partials meet in LDS and are added in wave order.  Threads 0..255
+// then finish one cell each.  A 16 x 16 tile reads each operand row once per
+// 16 outputs, a quarter of the VALU step's 4 x 4 blocks.
+constexpr int kMRows = 16, kMUnits = 16, kMWaves = 16;
+
+__device__ __forceinline__ void bwd_step_mfma(const BwdStep &s, int blk, int B, int T) {
+  __shared__ float part[kMWaves][16][16];
+  const int H = s.H, t = s.t;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ugroups = H / kMUnits;
+  const int ug = blk % ugroups, rg = blk / ugroups;
+  const int j0 = ug * kMUnits, b0 = rg * kMRows;
+  const int H4 = 4 * H;
+  const bool has_next = t + 1 < T;
+
+  // epilogue inputs of cell (em, eu) = (tid / 16, tid % 16), threads 0..255
+  const int tid = threadIdx.x;
+  const int em = tid >> 4, eu = tid & 15;
+  const int be = b0 + em, je = j0 + eu;
+  const bool epi = tid < 256 && be < B;
+  const int64_t row = (int64_t)be * T + t;
+  const int64_t gb = row * H4;
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, c = 0.0f, cp = 0.0f, dho = 0.0f, dcn = 0.0f;
+  if (epi) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) a[g] = s.acts[gb + g * H + je];
+    c = s.c_seq[row * H + je];
+    cp = t > 0 ? s.c_seq[(row - 1) * H + je]
+               : (s.c0 != nullptr ? s.c0[(int64_t)be * H + je] : 0.0f);
+    if (s.dh_out != nullptr) dho = s.dh_out[row * H + je];
+    if (has_next) dcn = s.dc[(int64_t)be * H + je];
+  }
+
+  const int r = lane & 15, q = lane >> 4;
+  const int b = min(b0 + r, B - 1);
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto reduce = [&](const float *dbase, int64_t tt, const float *wbase, int Hx) {
+    const int Hx4 = 4 * Hx;
+    const float *drow = dbase + ((int64_t)b * T + tt) * Hx4;
+    const float *wrow = wbase + (int64_t)(j0 + r) * Hx4;
+    const int kw = Hx4 / kMWaves;  // a multiple of 64
+    for (int nb = wave * kw; nb < (wave + 1) * kw; nb += 64) {
+      f4 d[4], w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        d[i] = *reinterpret_cast<const f4 *>(drow + nb + 16 * i + 4 * q);
+        w[i] = *reinterpret_cast<const f4 *>(wrow + nb + 16 * i + 4 * q);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(d[e >> 2][e & 3], w[e >> 2][e & 3], acc, 0, 0,
+                                                   0);
+    }
+  };
+  if (has_next) reduce(s.dG, t + 1, s.wt, H);
+  if (s.dG_up != nullptr) reduce(s.dG_up, t, s.wt_up, s.Hu);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) part[wave][4 * q + v][r] = acc[v];
+  __syncthreads();
+  if (!epi) return;
+  float sum = part[0][em][eu];
+#pragma unroll
+  for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
+  const float i = a[0], f = a[1], g = a[2], o = a[3];
+  const float dh = dho + sum;
+  const float tc = tanhf(c);
+  const float dct = dh * o * (1.0f - tc * tc) + dcn;
+  s.dG[gb + je] = (dct * g) * i * (1.0f - i);
+  s.dG[gb + H + je] = (dct * cp) * f * (1.0f - f);
+  s.dG[gb + 2 * H + je] = (dct * i) * (1.0f - g * g);
+  s.dG[gb + 3 * H + je] = (dh * tc) * o * (1.0f - o);
+  s.dc[(int64_t)be * H + je] = dct * f;
+}
+
+__global__ void __launch_bounds__(64 * kMWaves) lstm_bwd_step_mfma(BwdStep s, int B, int T) {
+  bwd_step_mfma(s, blockIdx.x, B, T);
+}
+
+__global__ void __launch_bounds__(64 * kMWaves)
+    lstm_bwd_diag_mfma(BwdStep a, BwdStep b, int blocks_a, int B, int T) {
+  if ((int)blockIdx.x < blocks_a)
+    bwd_step_mfma(a, blockIdx.x, B, T);
+  else
+    bwd_step_mfma(b, blockIdx.x - blocks_a, B, T);
+}
+
 // Whether the tiled step kernels take this shape.  The forward walks each
 // wave's quarter of the reduction in whole 64-long blocks (H % 256 == 0); the
 // backward's lane slices are H/16 long in float4 steps (H % 64 == 0).  Both
@@ -726,12 +819,21 @@ int numrs_hip_lstm_backward(numrs_hip_ctx *ctx, const float *x, const float *w_i
     TempBlock wt(ctx);  // W_hh^T [H, 4H]
     if (int rc = wt.alloc((size_t)(4 * H * H) * sizeof(float))) return rc;
     if (int rc = numrs_hip_transpose(ctx, w_hh, wt.f(), 4 * H, H)) return rc;
-    const unsigned grid = (unsigned)((H / kBUnits) * ((B + kBRows - 1) / kBRows));
     BwdStep st{dG.f(), wt.f(), acts, c_seq, c0, dh_seq, nullptr, nullptr, dc.f(), (int)H, 0, 0};
-    for (int64_t t = T - 1; t >= 0; --t) {
-      st.t = (int)t;
-      lstm_bwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(st, (int)B, (int)T);
-      if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step_tiled")) return rc;
+    if (H % 256 == 0) {
+      const unsigned grid = (unsigned)((H / kMUnits) * ((B + kMRows - 1) / kMRows));
+      for (int64_t t = T - 1; t >= 0; --t) {
+        st.t = (int)t;
+        lstm_bwd_step_mfma<<<grid, 64 * kMWaves, 0, ctx->stream>>>(st, (int)B, (int)T);
+        if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step_mfma")) return rc;
+      }
+    } else {
+      const unsigned grid = (unsigned)((H / kBUnits) * ((B + kBRows - 1) / kBRows));
+      for (int64_t t = T - 1; t >= 0; --t) {
+        st.t = (int)t;
+        lstm_bwd_step_tiled<<<grid, 256, 0, ctx->stream>>>(st, (int)B, (int)T);
+        if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_step_tiled")) return rc;
+      }
     }
   } else {
     TempBlock wp(ctx);
@@ -839,15 +941,22 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
              (int)H2, 0, 0};
   BwdStep lo{dG1.f(), wt1.f(), acts1, c1_seq, nullptr, nullptr, dG2.f(), wtu.f(), dc1.f(),
              (int)H1, (int)H2, 0};
-  const int rgroups = (int)((B + kBRows - 1) / kBRows);
-  const int g_up = (int)(H2 / kBUnits) * rgroups, g_lo = (int)(H1 / kBUnits) * rgroups;
+  // MFMA steps when both layers' reductions split into 64-long wave blocks.
+  const bool mfma = H1 % 256 == 0 && H2 % 256 == 0;
+  const int rows_per = mfma ? kMRows : kBRows, units_per = mfma ? kMUnits : kBUnits;
+  const int rgroups = (int)((B + rows_per - 1) / rows_per);
+  const int g_up = (int)(H2 / units_per) * rgroups, g_lo = (int)(H1 / units_per) * rgroups;
   // Launch d: upper step T-1-d and lower step T-d (the lower layer's dh at
   // step T-d takes the upper layer's dG of that step from launch d-1).
   for (int64_t d = 0; d <= T; ++d) {
     const int ga = d < T ? g_up : 0, gb = d >= 1 ? g_lo : 0;
     up.t = (int)(T - 1 - d);
     lo.t = (int)(T - d);
-    lstm_bwd_diag<<<(unsigned)(ga + gb), 256, 0, ctx->stream>>>(up, lo, ga, (int)B, (int)T);
+    if (mfma)
+      lstm_bwd_diag_mfma<<<(unsigned)(ga + gb), 64 * kMWaves, 0, ctx->stream>>>(up, lo, ga, (int)B,
+                                                                                (int)T);
+    else
+      lstm_bwd_diag<<<(unsigned)(ga + gb), 256, 0, ctx->stream>>>(up, lo, ga, (int)B, (int)T);
     if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_diag")) return rc;
   }
   if (int rc = lstm_param_grads(ctx, dG2.f(), h1_seq, w_ih2, h2_seq, nullptr, nullptr, dw_ih2,
