@@ -341,6 +341,18 @@ int bw_sum(const T &out, const float *g, Node &n) {  // backward.rs:208-236
   return numrs_hip_fill_grad(out->ctx, g, dst, x->numel(), n.op == Op::Mean, acc);
 }
 
+// The sweep's root, when it is a scalar loss whose backward kernel writes
+// the seed itself (see backward()); taken by that node's backward.
+thread_local const Impl *g_seed_root = nullptr;
+
+// The root's gradient cell when `out` is the root whose seed is still to be
+// written (then the loss kernel writes it), else null.
+float *take_seed(const T &out) {
+  if (g_seed_root == nullptr || out.get() != g_seed_root) return nullptr;
+  g_seed_root = nullptr;
+  return out->grad->buf->ptr;
+}
+
 int bw_mse(const T &out, const float *g, Node &n) {  // backward.rs:239-261
   const T &p = n.inputs[0], &t = n.inputs[1];
   float *dp = nullptr, *dt = nullptr;
@@ -349,15 +361,17 @@ int bw_mse(const T &out, const float *g, Node &n) {  // backward.rs:239-261
     if (int rc = grad_target(p, &dp, &ap)) return rc;
   if (t->requires_grad && !(p->requires_grad && p->grad == t->grad))
     if (int rc = grad_target(t, &dt, &at)) return rc;
+  numrs_hip_ctx *ctx = out->ctx;
+  float *seed = (dp || dt) ? take_seed(out) : nullptr;
   if (dp && dt && ap != at) {
-    if (int rc = numrs_hip_mse_backward(out->ctx, g, p->data->ptr, t->data->ptr, dp, nullptr,
-                                        p->numel(), ap))
+    if (int rc = numrs_hip::mse_backward_impl(ctx, g, seed, p->data->ptr, t->data->ptr, dp,
+                                              nullptr, p->numel(), ap))
       return rc;
-    return numrs_hip_mse_backward(out->ctx, g, p->data->ptr, t->data->ptr, nullptr, dt,
-                                  p->numel(), at);
+    return numrs_hip_mse_backward(ctx, g, p->data->ptr, t->data->ptr, nullptr, dt, p->numel(),
+                                  at);
   }
-  return numrs_hip_mse_backward(out->ctx, g, p->data->ptr, t->data->ptr, dp, dt, p->numel(),
-                                dp ? ap : at);
+  return numrs_hip::mse_backward_impl(ctx, g, seed, p->data->ptr, t->data->ptr, dp, dt,
+                                      p->numel(), dp ? ap : at);
 }
 
 int bw_ce(const T &out, const float *g, Node &n) {  // backward.rs:265-301
@@ -367,12 +381,13 @@ int bw_ce(const T &out, const float *g, Node &n) {  // backward.rs:265-301
   int acc;
   if (int rc = grad_target(x, &dst, &acc)) return rc;
   const int64_t B = x->shape[0], C = x->shape[1];
+  float *seed = take_seed(out);
   if (n.op == Op::CrossEntropyLabels)
-    return numrs_hip_softmax_ce_backward(out->ctx, g, x->data->ptr, nullptr,
-                                         reinterpret_cast<const int32_t *>(n.saved[0]->ptr), dst,
-                                         B, C, acc);
-  return numrs_hip_softmax_ce_backward(out->ctx, g, x->data->ptr, n.inputs[1]->data->ptr, nullptr,
-                                       dst, B, C, acc);
+    return numrs_hip::softmax_ce_backward_impl(
+        out->ctx, g, seed, x->data->ptr, nullptr,
+        reinterpret_cast<const int32_t *>(n.saved[0]->ptr), dst, B, C, acc);
+  return numrs_hip::softmax_ce_backward_impl(out->ctx, g, seed, x->data->ptr,
+                                             n.inputs[1]->data->ptr, nullptr, dst, B, C, acc);
 }
 
 int bw_reshape(const T &out, const float *g, Node &n) {  // backward.rs:315-330
@@ -692,17 +707,31 @@ int backward(const T &root) {  // tensor.rs:173-215
   GradCell &rg = *root->grad;
   if (!rg.buf)
     if (int rc = alloc_buf(ctx, root->numel(), sizeof(float), &rg.buf)) return rc;
-  if (int rc = numrs_hip_fill(ctx, rg.buf->ptr, root->numel(), 1.0f)) return rc;
+  // Seed ones (:178-183).  A scalar MSE or cross-entropy root has its seed
+  // written by its own backward kernel, which takes g = 1 directly: one
+  // launch fewer per step.  If that kernel does not run, the fill follows.
+  const Op rop = root->node ? root->node->op : Op::Leaf;
+  const bool seed_in_kernel = root->numel() == 1 && (rop == Op::MSE || rop == Op::CrossEntropy ||
+                                                     rop == Op::CrossEntropyLabels);
+  if (seed_in_kernel)
+    g_seed_root = root.get();
+  else if (int rc = numrs_hip_fill(ctx, rg.buf->ptr, root->numel(), 1.0f))
+    return rc;
   rg.valid = true;
   std::vector<Impl *> topo = build_topo(root);
-  for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
+  int rc = NUMRS_HIP_OK;
+  for (auto it = topo.rbegin(); it != topo.rend() && rc == NUMRS_HIP_OK; ++it) {
     Impl *t = *it;
     if (!t->grad || !t->grad->valid) continue;  // grad still zero: contributes nothing
     // Non-owning handle: the root keeps the whole graph alive during the sweep.
     T self(std::shared_ptr<Impl>{}, t);
-    if (int rc = run_backward_fn(self)) return rc;
+    rc = run_backward_fn(self);
   }
-  return NUMRS_HIP_OK;
+  if (g_seed_root != nullptr) {  // the root's kernel did not take the seed
+    g_seed_root = nullptr;
+    if (rc == NUMRS_HIP_OK) rc = numrs_hip_fill(ctx, rg.buf->ptr, root->numel(), 1.0f);
+  }
+  return rc;
 }
 
 // ---------------------------------------------------------------------------

@@ -83,6 +83,17 @@ struct TempBlock {
 // Checks the launch that was just enqueued.
 int check_launch(numrs_hip_ctx *ctx, const char *what);
 
+// Loss backward kernels for the engine's root node: with `seed` non-null the
+// incoming gradient is the sweep's seed 1 (not read from g_scalar) and the
+// kernel writes that 1 into seed[0], the root's gradient cell, so the seed
+// needs no launch of its own.  seed == nullptr is numrs_hip_mse_backward /
+// numrs_hip_softmax_ce_backward.
+int mse_backward_impl(numrs_hip_ctx *ctx, const float *g_scalar, float *seed, const float *p,
+                      const float *t, float *dp, float *dt, int64_t n, int accumulate);
+int softmax_ce_backward_impl(numrs_hip_ctx *ctx, const float *g_scalar, float *seed,
+                             const float *logits, const float *onehot, const int32_t *labels,
+                             float *dlogits, int64_t B, int64_t C, int accumulate);
+
 // Resolves, with the context's device current, the device address of the
 // static partials array of the allocation-free column reduction (reduce.hip)
 // into ctx->noalloc_partials; once per device, later contexts reuse it.

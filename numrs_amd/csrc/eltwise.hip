@@ -291,8 +291,11 @@ template <int VEC>
 __global__ void __launch_bounds__(kBlock)
     mse_bwd_kernel(const float *__restrict__ g0, const float *__restrict__ p,
                    const float *__restrict__ t, float *__restrict__ dp, float *__restrict__ dt,
-                   int64_t n, float nf, int acc) {
-  const float gs = g0[0];
+                   int64_t n, float nf, int acc, float *__restrict__ seed) {
+  // seed: the loss is the backward's root -- g is its seed 1 (written here
+  // for the root's gradient cell) rather than a value read back from g0.
+  if (seed != nullptr && blockIdx.x == 0 && threadIdx.x == 0) seed[0] = 1.0f;
+  const float gs = seed != nullptr ? 1.0f : g0[0];
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock + threadIdx.x * 4;
 #pragma unroll
   for (int u = 0; u < kVecPerThread; ++u) {
@@ -626,6 +629,30 @@ int check_n(numrs_hip_ctx *ctx, const char *who, int64_t n) {
 
 }  // namespace
 
+namespace numrs_hip {
+
+// mse_backward; with `seed` (the loss is the sweep's root) g is its seed 1,
+// which the kernel also writes to seed[0].
+int mse_backward_impl(numrs_hip_ctx *ctx, const float *g_scalar, float *seed, const float *p,
+                      const float *t, float *dp, float *dt, int64_t n, int accumulate) {
+  if (int rc = check_n(ctx, "numrs_hip_mse_backward", n)) return rc;
+  if (n == 0 || (dp == nullptr && dt == nullptr)) {
+    return seed != nullptr ? numrs_hip_fill(ctx, seed, 1, 1.0f) : NUMRS_HIP_OK;
+  }
+  if ((g_scalar == nullptr && seed == nullptr) || p == nullptr || t == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_backward: null pointer");
+  const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(t) &&
+                   numrs_hip::aligned16(dp) && numrs_hip::aligned16(dt);
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
+    mse_bwd_kernel<decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(
+        g_scalar, p, t, dp, dt, n, (float)n, accumulate, seed);
+  });
+  return numrs_hip::check_launch(ctx, "mse_bwd_kernel");
+}
+
+}  // namespace numrs_hip
+
 extern "C" {
 
 int numrs_hip_unary_backward(numrs_hip_ctx *ctx, int kind, const float *g, const float *v,
@@ -690,18 +717,7 @@ int numrs_hip_fill_grad(numrs_hip_ctx *ctx, const float *g_scalar, float *dx, in
 int numrs_hip_mse_backward(numrs_hip_ctx *ctx, const float *g_scalar, const float *p,
                            const float *t, float *dp, float *dt, int64_t n, int accumulate) {
   NRS_CHECK_CTX(ctx);
-  if (int rc = check_n(ctx, "numrs_hip_mse_backward", n)) return rc;
-  if (n == 0 || (dp == nullptr && dt == nullptr)) return NUMRS_HIP_OK;
-  if (g_scalar == nullptr || p == nullptr || t == nullptr)
-    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_backward: null pointer");
-  const bool vec = numrs_hip::aligned16(p) && numrs_hip::aligned16(t) &&
-                   numrs_hip::aligned16(dp) && numrs_hip::aligned16(dt);
-  const unsigned grid = grid_for(n, kElemsPerBlock);
-  numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
-    mse_bwd_kernel<decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, p, t, dp, dt,
-                                                                         n, (float)n, accumulate);
-  });
-  return numrs_hip::check_launch(ctx, "mse_bwd_kernel");
+  return numrs_hip::mse_backward_impl(ctx, g_scalar, nullptr, p, t, dp, dt, n, accumulate);
 }
 
 int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, int64_t n,

@@ -275,6 +275,48 @@ __global__ void __launch_bounds__(kBlock)
   if (lane == 0) row_loss[row] = l;
 }
 
+// The whole cross-entropy loss of a small batch (B <= kCeSmallRows) in one
+// workgroup: wave w forms the row losses of rows w, w + 16, ... as
+// ce_rows_kernel does and adds them in row order; the 16 wave sums are then
+// added in wave order and divided by B.  One launch instead of the row
+// kernel and a reduction.
+constexpr int kCeSmallWaves = 16;
+constexpr int64_t kCeSmallRows = 512;
+
+template <bool LABELS>
+__global__ void __launch_bounds__(64 * kCeSmallWaves)
+    ce_loss_small_kernel(const float *__restrict__ x, const float *__restrict__ onehot,
+                         const int32_t *__restrict__ labels, int64_t B, int64_t C,
+                         float *__restrict__ out) {
+  __shared__ float red[kCeSmallWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float acc = 0.0f;
+  for (int64_t row = wave; row < B; row += kCeSmallWaves) {
+    const float *xr = x + row * C;
+    float m = -INFINITY;
+    for (int64_t j = lane; j < C; j += 64) m = fmaxf(m, xr[j]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int64_t j = lane; j < C; j += 64) s += expf(xr[j] - m);
+    s = wave_sum(s);
+    const float ls = logf(s);
+    float l = 0.0f;
+    for (int64_t j = lane; j < C; j += 64) {
+      const float t = LABELS ? (j == (int64_t)labels[row] ? 1.0f : 0.0f) : onehot[row * C + j];
+      l += -t * ((xr[j] - m) - ls);
+    }
+    acc += wave_sum(l);
+  }
+  if (lane == 0) red[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = red[0];
+#pragma unroll
+    for (int w = 1; w < kCeSmallWaves; ++w) t += red[w];
+    out[0] = t / (float)B;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Row softmax and LayerNorm forward (new ops for the transformer config)
 // ---------------------------------------------------------------------------
@@ -489,6 +531,15 @@ int numrs_hip_cross_entropy_loss(numrs_hip_ctx *ctx, const float *logits, const 
   if (B <= 0 || C <= 0 || logits == nullptr || out == nullptr ||
       (onehot == nullptr) == (labels == nullptr))
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_cross_entropy_loss: bad arguments");
+  if (B <= kCeSmallRows) {
+    if (labels)
+      ce_loss_small_kernel<true><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(logits, onehot,
+                                                                           labels, B, C, out);
+    else
+      ce_loss_small_kernel<false><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(logits, onehot,
+                                                                            labels, B, C, out);
+    return numrs_hip::check_launch(ctx, "ce_loss_small_kernel");
+  }
   // Row losses live in the scratch region; the reduction below uses the workspace.
   float *rows = nullptr;
   if (int rc = numrs_hip::scratch(ctx, (size_t)B * sizeof(float), &rows)) return rc;

@@ -40,7 +40,8 @@ template <bool LABELS>
 __global__ void __launch_bounds__(kBlock)
     softmax_ce_bwd_kernel(const float *__restrict__ g0, const float *__restrict__ x,
                           const float *__restrict__ onehot, const int32_t *__restrict__ labels,
-                          float *__restrict__ dx, int64_t B, int64_t C, int acc) {
+                          float *__restrict__ dx, int64_t B, int64_t C, int acc,
+                          float *__restrict__ seed) {
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= B) return;
@@ -51,7 +52,9 @@ __global__ void __launch_bounds__(kBlock)
   float s = 0.0f;
   for (int64_t j = lane; j < C; j += 64) s += expf(xr[j] - m);
   s = wave_sum(s);
-  const float scale = g0[0] / (float)B;
+  // seed: the loss is the sweep's root; g is its seed 1, written to seed[0]
+  if (seed != nullptr && blockIdx.x == 0 && threadIdx.x == 0) seed[0] = 1.0f;
+  const float scale = (seed != nullptr ? 1.0f : g0[0]) / (float)B;
   const int32_t label = LABELS ? labels[row] : -1;
   float *out = dx + row * C;
   for (int64_t j = lane; j < C; j += 64) {
@@ -66,7 +69,8 @@ template <bool LABELS, int NV, int VM>
 __global__ void __launch_bounds__(kBlock)
     softmax_ce_bwd_vec(const float *__restrict__ g0, const float *__restrict__ x,
                        const float *__restrict__ onehot, const int32_t *__restrict__ labels,
-                       float *__restrict__ dx, int64_t B, int64_t C, int acc) {
+                       float *__restrict__ dx, int64_t B, int64_t C, int acc,
+                          float *__restrict__ seed) {
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= B) return;
@@ -99,7 +103,9 @@ __global__ void __launch_bounds__(kBlock)
     }
   }
   s = wave_sum(s);
-  const float scale = g0[0] / (float)B;
+  // seed: the loss is the sweep's root; g is its seed 1, written to seed[0]
+  if (seed != nullptr && blockIdx.x == 0 && threadIdx.x == 0) seed[0] = 1.0f;
+  const float scale = (seed != nullptr ? 1.0f : g0[0]) / (float)B;
   const int32_t label = LABELS ? labels[row] : -1;
   float *out = dx + row * C;
 #pragma unroll
@@ -391,16 +397,17 @@ inline int row_nv(int64_t cols, bool aligned) {
 
 }  // namespace
 
-extern "C" {
+namespace numrs_hip {
 
-int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, const float *logits,
-                                  const float *onehot, const int32_t *labels, float *dlogits,
-                                  int64_t B, int64_t C, int accumulate) {
-  NRS_CHECK_CTX(ctx);
+// softmax_ce_backward; with `seed` (the loss is the sweep's root) g is its
+// seed 1, which the kernel also writes to seed[0].
+int softmax_ce_backward_impl(numrs_hip_ctx *ctx, const float *g_scalar, float *seed,
+                             const float *logits, const float *onehot, const int32_t *labels,
+                             float *dlogits, int64_t B, int64_t C, int accumulate) {
   const char *who = "numrs_hip_softmax_ce_backward";
   if (B < 0 || C < 0) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: negative size", who);
-  if (B == 0 || C == 0) return NUMRS_HIP_OK;
-  if (g_scalar == nullptr || logits == nullptr || dlogits == nullptr)
+  if (B == 0 || C == 0) return seed != nullptr ? numrs_hip_fill(ctx, seed, 1, 1.0f) : NUMRS_HIP_OK;
+  if ((g_scalar == nullptr && seed == nullptr) || logits == nullptr || dlogits == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null pointer", who);
   if ((onehot == nullptr) == (labels == nullptr))
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: pass exactly one of onehot/labels", who);
@@ -411,10 +418,10 @@ int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, con
   numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, B * C), [&](auto V) {                     \
     if (labels != nullptr)                                                                    \
       softmax_ce_bwd_vec<true, NV, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(      \
-          g_scalar, logits, onehot, labels, dlogits, B, C, accumulate);                       \
+          g_scalar, logits, onehot, labels, dlogits, B, C, accumulate, seed);                       \
     else                                                                                      \
       softmax_ce_bwd_vec<false, NV, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(     \
-          g_scalar, logits, onehot, labels, dlogits, B, C, accumulate);                       \
+          g_scalar, logits, onehot, labels, dlogits, B, C, accumulate, seed);                       \
   });                                                                                         \
   return numrs_hip::check_launch(ctx, "softmax_ce_bwd_vec");
   switch (nv) {
@@ -427,12 +434,24 @@ int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, con
 #undef NRS_CE_VEC
   if (labels != nullptr)
     softmax_ce_bwd_kernel<true><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot, labels,
-                                                                  dlogits, B, C, accumulate);
+                                                                  dlogits, B, C, accumulate, seed);
   else
     softmax_ce_bwd_kernel<false><<<grid, kBlock, 0, ctx->stream>>>(g_scalar, logits, onehot,
                                                                    labels, dlogits, B, C,
-                                                                   accumulate);
+                                                                   accumulate, seed);
   return numrs_hip::check_launch(ctx, "softmax_ce_bwd_kernel");
+}
+
+}  // namespace numrs_hip
+
+extern "C" {
+
+int numrs_hip_softmax_ce_backward(numrs_hip_ctx *ctx, const float *g_scalar, const float *logits,
+                                  const float *onehot, const int32_t *labels, float *dlogits,
+                                  int64_t B, int64_t C, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  return numrs_hip::softmax_ce_backward_impl(ctx, g_scalar, nullptr, logits, onehot, labels,
+                                             dlogits, B, C, accumulate);
 }
 
 int numrs_hip_softmax_backward(numrs_hip_ctx *ctx, const float *y, const float *g, float *dx,

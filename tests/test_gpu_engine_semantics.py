@@ -187,3 +187,44 @@ def test_attention_single_head(S, mode):
     for name, t in (("dq", q), ("dk", k), ("dv", v)):
         if name != mode:
             assert t.gradient() is None, name
+
+
+@pytest.mark.parametrize("loss_kind", ["mse", "ce", "ce_labels"])
+@pytest.mark.parametrize("input_grad", [True, False])
+def test_loss_root_seed(hip_ctx, loss_kind, input_grad):
+    """backward() seeds the root's gradient with ones (tensor.rs:178-183).  A
+    scalar MSE / cross-entropy root has the seed written by its own backward
+    kernel; when that kernel does not run (the input needs no gradient) the
+    seed is still written."""
+    print(f"[gpu] loss seed {loss_kind} input_grad={input_grad}", flush=True)
+    if loss_kind == "ce_labels" and not input_grad:
+        pytest.skip("labels carry no gradient: the loss would not require one")
+    nr.set_default_context(hip_ctx)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((6, 5)).astype(np.float32)
+    xt = Tensor.new(x, input_grad)
+    if loss_kind == "mse":
+        t = rng.standard_normal((6, 5)).astype(np.float32)
+        loss = xt.mse_loss(Tensor.new(t, True))
+        want_x = (2.0 * (x.astype(np.float64) - t)) / x.size
+    else:
+        lab = rng.integers(0, 5, 6)
+        if loss_kind == "ce":
+            # a one-hot target that requires grad keeps the loss recorded when
+            # the logits do not (its gradient is the reference's [0])
+            loss = xt.cross_entropy_loss(Tensor.new(np.eye(5, dtype=np.float32)[lab],
+                                                    not input_grad))
+        else:
+            loss = xt.cross_entropy_labels(lab)
+        e = np.exp(x - x.max(1, keepdims=True))
+        want_x = (e / e.sum(1, keepdims=True) - np.eye(5)[lab]) / 6
+    loss.backward()
+    assert loss.gradient().tolist() == [1.0]
+    if input_grad:
+        assert_close(xt.gradient(), want_x, abs_tol=1e-7, rel_tol=1e-5, what="input grad")
+    # a second backward accumulates (the seed is 1 again, the input grad doubles)
+    if input_grad:
+        first = xt.gradient().copy()
+        loss.backward()
+        assert loss.gradient().tolist() == [1.0]
+        assert_close(xt.gradient(), 2 * first, abs_tol=1e-7, rel_tol=1e-6, what="accumulated")

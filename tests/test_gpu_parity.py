@@ -905,6 +905,32 @@ def test_linear_gelu_forward_backward(hip_ctx, rng, T, fin, fout):
             assert np.array_equal(a.numpy(), b2.numpy()), f"{name} {acc}: fused != composition"
 
 
+# Cross-entropy loss forward: one workgroup for B <= 512 rows, the row kernel
+# and a two-pass mean above.
+@pytest.mark.parametrize("B,C", [(64, 10), (512, 33), (513, 10), (4096, 100)])
+@pytest.mark.parametrize("labels_api", [False, True])
+def test_cross_entropy_loss_forward(hip_ctx, rng, B, C, labels_api):
+    say(f"ce loss B={B} C={C} labels={labels_api}")
+    x = rand(rng, (B, C)) * 3
+    lab = rng.integers(0, C, B).astype(np.int32)
+    onehot = np.eye(C, dtype=np.float32)[lab]
+    c = hip_ctx
+    xd, out = c.to_device(x), c.empty((1,))
+    if labels_api:
+        ld = c.to_device(lab)
+        rc = L.load().numrs_hip_cross_entropy_loss(c.handle, xd.ptr, None, ld.ptr, B, C, out.ptr)
+    else:
+        od = c.to_device(onehot)
+        rc = L.load().numrs_hip_cross_entropy_loss(c.handle, xd.ptr, od.ptr, None, B, C, out.ptr)
+    assert rc == 0
+    x64 = x.astype(np.float64)
+    m = x64.max(1, keepdims=True)
+    lse = np.log(np.exp(x64 - m).sum(1)) + m[:, 0]
+    ref = float((lse - x64[np.arange(B), lab]).mean())
+    assert abs(float(out.numpy()[0]) - ref) <= 1e-5 + 1e-5 * abs(ref)
+    assert abs(float(O.cross_entropy_loss(x, onehot)) - ref) <= 1e-5 + 1e-5 * abs(ref)
+
+
 def test_optimizer_multi_tensor_bit_exact(hip_ctx, rng):
     import ctypes
 
