@@ -489,6 +489,9 @@ __global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, G
 // ---------------------------------------------------------------------------
 constexpr int kSP = 256, kSQ = 128;  // large workgroup tile
 constexpr int kHP = 128, kHQ = 64;   // small workgroup tile
+constexpr int kMP = 64, kMQ = 64;    // mini workgroup tile (batched products, up to 3 per CU)
+// Streamed tile shapes, as the planners name them.
+constexpr int kShapeLarge = 0, kShapeSmall = 1, kShapeMini = 2;
 template <int TP, int TQ, int NW = 4>
 struct StreamCfg {
   static constexpr int kStageX = TP * kBR;  // floats per X stage
@@ -542,6 +545,12 @@ __shared__ __attribute__((aligned(1024))) float g_hx1[StreamCfg<kHP, kHQ>::kStag
 __shared__ __attribute__((aligned(1024))) float g_hy1[StreamCfg<kHP, kHQ>::kStageY];
 __shared__ __attribute__((aligned(1024))) float g_hx2[StreamCfg<kHP, kHQ>::kStageX];
 __shared__ __attribute__((aligned(1024))) float g_hy2[StreamCfg<kHP, kHQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_mx0[StreamCfg<kMP, kMQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_my0[StreamCfg<kMP, kMQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_mx1[StreamCfg<kMP, kMQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_my1[StreamCfg<kMP, kMQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_mx2[StreamCfg<kMP, kMQ>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_my2[StreamCfg<kMP, kMQ>::kStageY];
 
 __device__ __forceinline__ int rc_swizzle(int p) { return (p & 7) ^ ((p >> 3) & 1); }
 
@@ -667,9 +676,12 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
   if constexpr (TP == kSP) {
     x0 = g_sx0, x1 = g_sx1, x2 = g_sx2;
     y0 = g_sy0, y1 = g_sy1, y2 = g_sy2;
-  } else {
+  } else if constexpr (TP == kHP) {
     x0 = g_hx0, x1 = g_hx1, x2 = g_hx2;
     y0 = g_hy0, y1 = g_hy1, y2 = g_hy2;
+  } else {
+    x0 = g_mx0, x1 = g_mx1, x2 = g_mx2;
+    y0 = g_my0, y1 = g_my1, y2 = g_my2;
   }
 
   // DMA sources: uniform tile bases (advanced by xstep / ystep floats per
@@ -866,6 +878,14 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_stream_small(Gemm d) {
   stream_tile<XRC, YRC, kHP, kHQ, 4, ACT>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
 }
 
+// Mini tiles (64 x 64, 16 KiB stages, three workgroups per CU, each wave one
+// 32 x 32 MFMA block) for batched products whose 128 x 64 tiles would leave
+// CUs idle, such as attention's per-head [256, 64] products at C4.
+template <bool XRC, bool YRC>
+__global__ void __launch_bounds__(kThreads, 3) gemm_stream_mini(Gemm d) {
+  stream_tile<XRC, YRC, kMP, kMQ>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
+}
+
 // Pairs on the streamed path, logical tiles [0, tiles_a) for the first
 // product.  matmul_backward: dA = dC B^T (NT) with dB = A^T dC (TN); the
 // Linear backward: dx = g W (NN) with dW = g^T x (TN).
@@ -901,6 +921,24 @@ __global__ void __launch_bounds__(kThreads, 2) linear_backward_stream_small(Gemm
     stream_tile<true, false, kHP, kHQ>(dx, tile, blockIdx.y);
   else
     stream_tile<false, false, kHP, kHQ>(dw, tile - tiles_a, blockIdx.y);
+}
+
+__global__ void __launch_bounds__(kThreads, 3) matmul_backward_stream_mini(Gemm da, Gemm db,
+                                                                           int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<true, true, kMP, kMQ>(da, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kMP, kMQ>(db, tile - tiles_a, blockIdx.y);
+}
+
+__global__ void __launch_bounds__(kThreads, 3) linear_backward_stream_mini(Gemm dx, Gemm dw,
+                                                                           int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<true, false, kMP, kMQ>(dx, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kMP, kMQ>(dw, tile - tiles_a, blockIdx.y);
 }
 
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
@@ -1240,9 +1278,12 @@ bool stream_fits(const Gemm &g, bool xrc, bool yrc, int tp, int tq) {
          g.ldx < kMaxLd && g.ldy < kMaxLd;
 }
 
-Gemm as_stream(Gemm g, bool small) {
-  g.tiles_p = g.P / (small ? kHP : kSP);
-  g.tiles_q = g.Q / (small ? kHQ : kSQ);
+int shape_tp(int shape) { return shape == kShapeLarge ? kSP : shape == kShapeSmall ? kHP : kMP; }
+int shape_tq(int shape) { return shape == kShapeLarge ? kSQ : shape == kShapeSmall ? kHQ : kMQ; }
+
+Gemm as_stream(Gemm g, int shape) {
+  g.tiles_p = g.P / shape_tp(shape);
+  g.tiles_q = g.Q / shape_tq(shape);
   g.splits = 1;
   g.ktiles_per_split = g.R / kBR;
   g.partial = nullptr;
@@ -1352,21 +1393,33 @@ int64_t stream_grid(const Gemm &g) { return (int64_t)g.tiles_p * g.tiles_q * g.s
 // Tile shape for a batched product (or a pair sharing the grid): no split-K,
 // so the shape whose tiles fill the CUs with the smaller modelled time;
 // false when neither shape fits or gives at least one tile per CU.
+// Mini tiles run up to three per CU: a round of k of them (k = 1..3) costs
+// T steps at the k-way rate plus a fixed cost.
+constexpr double kMiniUs[4] = {0.0, 0.9, 1.25, 1.7}, kMiniFixedUs = 6.0;
+
+double mini_wave_us(int64_t n, int64_t T) {
+  double t = (double)(n / 3) * ((double)T * kMiniUs[3] + kMiniFixedUs);
+  if (n % 3) t += (double)T * kMiniUs[n % 3] + kMiniFixedUs;
+  return t;
+}
+
 bool pick_batched_stream(numrs_hip_ctx *ctx, const Gemm &a, bool xa, bool ya, const Gemm *b,
-                         int64_t batch, bool *small_out) {
+                         int64_t batch, int *shape_out) {
   bool any = false;
   double best = 0.0;
   const int64_t cus = std::max(ctx->num_cus, 1);
-  for (int small = 0; small < 2; ++small) {
-    const int tp = small ? kHP : kSP, tq = small ? kHQ : kSQ;
+  for (int shape = kShapeLarge; shape <= kShapeMini; ++shape) {
+    const int tp = shape_tp(shape), tq = shape_tq(shape);
     if (!stream_fits(a, xa, ya, tp, tq) || (b && !stream_fits(*b, false, false, tp, tq))) continue;
     const int64_t t = (int64_t)(a.P / tp) * (a.Q / tq) + (b ? (int64_t)(b->P / tp) * (b->Q / tq) : 0);
     if (t * batch < cus || t > 0x7fffffff) continue;
     const int64_t T = std::max<int64_t>(a.R, b ? b->R : 0) / kBR;
-    const double est = stream_wave_us(small != 0, (t * batch + cus - 1) / cus, T);
+    const int64_t n = (t * batch + cus - 1) / cus;
+    const double est = shape == kShapeMini ? mini_wave_us(n, T)
+                                           : stream_wave_us(shape == kShapeSmall, n, T);
     if (!any || est < best) {
       best = est;
-      *small_out = small != 0;
+      *shape_out = shape;
     }
     any = true;
   }
@@ -1449,11 +1502,13 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
     if (int rc = numrs_hip::check_launch(ctx, "gemm_stream_kernel")) return rc;
     return reduce_splits(ctx, &sg, nullptr);
   }
-  bool small = false;
-  if (batch > 1 && pick_batched_stream(ctx, g, XRC, YRC, nullptr, batch, &small)) {
-    const Gemm sg = as_stream(g, small);
+  int shape = kShapeLarge;
+  if (batch > 1 && pick_batched_stream(ctx, g, XRC, YRC, nullptr, batch, &shape)) {
+    const Gemm sg = as_stream(g, shape);
     dim3 grid((unsigned)stream_grid(sg), (unsigned)batch);
-    if (small)
+    if (shape == kShapeMini)
+      gemm_stream_mini<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
+    else if (shape == kShapeSmall)
       gemm_stream_small<XRC, YRC><<<grid, kThreads, 0, ctx->stream>>>(sg);
     else
       gemm_stream_kernel<XRC, YRC><<<grid, kBigThreads, 0, ctx->stream>>>(sg);
@@ -1534,12 +1589,14 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
     if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
     return reduce_splits(ctx, &sa, &sb);
   }
-  bool small = false;
-  if (batch > 1 && pick_batched_stream(ctx, ga, true, true, &gb, batch, &small)) {
-    const Gemm sa = as_stream(ga, small), sb = as_stream(gb, small);
+  int shape = kShapeLarge;
+  if (batch > 1 && pick_batched_stream(ctx, ga, true, true, &gb, batch, &shape)) {
+    const Gemm sa = as_stream(ga, shape), sb = as_stream(gb, shape);
     const int64_t ta = stream_grid(sa), tb = stream_grid(sb);
     dim3 grid((unsigned)(ta + tb), (unsigned)batch);
-    if (small)
+    if (shape == kShapeMini)
+      matmul_backward_stream_mini<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    else if (shape == kShapeSmall)
       matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
     else
       matmul_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
@@ -1756,12 +1813,14 @@ int numrs_hip::gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, 
   if (batch == 1) return launch_pair(ctx, ga, gb, false, who);
   if (tiny_fits(ga, batch) && tiny_fits(gb, batch))
     return launch_tiny(ctx, ga, true, false, &gb, batch, nullptr);
-  bool small = false;
-  if (pick_batched_stream(ctx, ga, true, false, &gb, batch, &small)) {
-    const Gemm sa = as_stream(ga, small), sb = as_stream(gb, small);
+  int shape = kShapeLarge;
+  if (pick_batched_stream(ctx, ga, true, false, &gb, batch, &shape)) {
+    const Gemm sa = as_stream(ga, shape), sb = as_stream(gb, shape);
     const int64_t ta = stream_grid(sa), tb = stream_grid(sb);
     dim3 grid((unsigned)(ta + tb), (unsigned)batch);
-    if (small)
+    if (shape == kShapeMini)
+      linear_backward_stream_mini<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    else if (shape == kShapeSmall)
       linear_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
     else
       linear_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta);

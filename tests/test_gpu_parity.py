@@ -170,6 +170,35 @@ def test_matmul_streamed_batched(hip_ctx, rng, ta, tb, K):
     assert_contraction(C.numpy(), ref, K, what="streamed C += A B")
 
 
+# Batched products with [256, 64] outputs per batch (attention's per-head
+# shape at C4): the planner takes the 64 x 64 mini tile, three workgroups per
+# CU; reductions of 1, 3 and 8 tiles cover the ring's prologue cases.
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("K", [32, 96, 256])
+def test_matmul_streamed_batched_mini(hip_ctx, rng, ta, tb, K):
+    batch, M, N = 128, 256, 64
+    say(f"streamed mini matmul batch={batch} M={M} K={K} N={N} ta={ta} tb={tb}")
+    A = rand(rng, (batch, K, M) if ta else (batch, M, K))
+    B = rand(rng, (batch, N, K) if tb else (batch, K, N))
+    C0 = rand(rng, (batch, M, N))
+    c = hip_ctx
+    Ad, Bd = c.to_device(A), c.to_device(B)
+    C = c.to_device(C0)
+    c.matmul_batched(Ad, Bd, C, trans_a=bool(ta), trans_b=bool(tb), accumulate=True)
+    a64 = A.astype(np.float64).transpose(0, 2, 1) if ta else A.astype(np.float64)
+    b64 = B.astype(np.float64).transpose(0, 2, 1) if tb else B.astype(np.float64)
+    ref = C0.astype(np.float64) + a64 @ b64
+    assert_contraction(C.numpy(), ref, K, what="mini C += A B")
+    # the matmul_backward pair at the same per-batch shape (dA NT + dB TN)
+    dC = rand(rng, (batch, M, N))
+    A2, B2 = rand(rng, (batch, M, K)), rand(rng, (batch, K, N))
+    dA, dB = c.empty((batch, M, K)), c.empty((batch, K, N))
+    c.matmul_backward_batched(c.to_device(dC), c.to_device(A2), c.to_device(B2), dA, dB)
+    d64 = dC.astype(np.float64)
+    assert_contraction(dA.numpy(), d64 @ B2.astype(np.float64).transpose(0, 2, 1), N, what="dA")
+    assert_contraction(dB.numpy(), A2.astype(np.float64).transpose(0, 2, 1) @ d64, M, what="dB")
+
+
 @pytest.mark.parametrize("acc", [False, True])
 def test_matmul_backward_streamed(hip_ctx, rng, acc):
     """matmul_backward through the streamed pair kernel (dA NT + dB TN tiles
