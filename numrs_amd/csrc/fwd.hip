@@ -113,33 +113,37 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
-// 64 x 64 tiles with float4 global loads and stores, for 16-byte aligned
-// matrices whose dimensions are multiples of 4 (each float4 is then wholly
-// inside or outside the matrix).  Thread t loads rows t/16 + 16i, columns
-// 4(t%16)..+3, and stores output row t/16 + 16i (a column of x), output
-// columns 4(t%16)..+3, read down the LDS tile.  Row stride 65 keeps the
-// column reads spread over the banks.
-// All four loads are issued before the tile is written: a tile row past the
+// TS x TS tiles (64 or 128) with float4 global loads and stores, for
+// 16-byte aligned matrices whose dimensions are multiples of 4 (each float4
+// is then wholly inside or outside the matrix).  With Q = TS/4 float4 groups
+// per tile row and K = 256/Q rows per pass, thread t loads rows t/Q + K i,
+// columns 4(t%Q)..+3, and stores output row t/Q + K i (a column of x),
+// output columns 4(t%Q)..+3, read down the LDS tile.  Row stride TS + 1
+// keeps the column reads spread over the banks.
+// All loads are issued before the tile is written: a tile row past the
 // matrix edge reloads the last row or column group (rows and cols are
 // nonzero multiples of 4 here) and is not stored, so no load sits in a branch
 // with its use.  VM is the access mode (non-temporal for large matrices).
-template <int VM>
+template <int VM, int TS>
 __global__ void __launch_bounds__(kBlock)
-    transpose64_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
-                       int64_t cols) {
+    transpose_tile_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t rows,
+                          int64_t cols) {
   typedef float f4v __attribute__((ext_vector_type(4)));
-  __shared__ float tile[64][65];
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-  const int t = threadIdx.x, q = t & 15, k0 = t >> 4;
-  f4v v[4];
+  constexpr int kQ = TS / 4;           // float4 groups per tile row
+  constexpr int kK = kBlock / kQ;      // tile rows per pass of the block
+  constexpr int kPass = TS / kK;
+  __shared__ float tile[TS][TS + 1];
+  const int64_t r0 = (int64_t)blockIdx.y * TS, c0 = (int64_t)blockIdx.x * TS;
+  const int t = threadIdx.x, q = t % kQ, k0 = t / kQ;
+  f4v v[kPass];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = r0 + k0 + 16 * i, c = c0 + 4 * q;
+  for (int i = 0; i < kPass; ++i) {
+    const int64_t r = r0 + k0 + kK * i, c = c0 + 4 * q;
     v[i] = numrs_hip::ldv<VM>(x + (r < rows ? r : rows - 1) * cols + (c < cols ? c : cols - 4));
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int k = k0 + 16 * i;
+  for (int i = 0; i < kPass; ++i) {
+    const int k = k0 + kK * i;
     if (r0 + k < rows && c0 + 4 * q < cols) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) tile[k][4 * q + e] = v[i][e];
@@ -147,14 +151,14 @@ __global__ void __launch_bounds__(kBlock)
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int k = k0 + 16 * i;  // output row c0 + k, output columns r0 + 4q..
+  for (int i = 0; i < kPass; ++i) {
+    const int k = k0 + kK * i;  // output row c0 + k, output columns r0 + 4q..
     const int64_t c = c0 + k, r = r0 + 4 * q;
     if (c < cols && r < rows) {
-      f4v v;
+      f4v o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = tile[4 * q + e][k];
-      numrs_hip::stv<VM>(y + c * rows + r, v);
+      for (int e = 0; e < 4; ++e) o[e] = tile[4 * q + e][k];
+      numrs_hip::stv<VM>(y + c * rows + r, o);
     }
   }
 }
@@ -499,11 +503,20 @@ int numrs_hip_transpose(numrs_hip_ctx *ctx, const float *x, float *y, int64_t ro
   if (x == nullptr || y == nullptr) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: null pointer");
   if ((rows + 31) / 32 > 65535) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "transpose: too many rows");
   if ((rows & 3) == 0 && (cols & 3) == 0 && numrs_hip::aligned16(x) && numrs_hip::aligned16(y)) {
-    dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+    // 128 x 128 tiles when both sides hold one: each tile row and column
+    // then moves as 512-byte runs, against 256 with 64 x 64 tiles.
+    const bool big = rows >= 128 && cols >= 128;
+    const int ts = big ? 128 : 64;
+    dim3 grid((unsigned)((cols + ts - 1) / ts), (unsigned)((rows + ts - 1) / ts));
     numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, rows * cols), [&](auto V) {
-      transpose64_kernel<decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
+      if (big)
+        transpose_tile_kernel<decltype(V)::value, 128><<<grid, kBlock, 0, ctx->stream>>>(x, y,
+                                                                                      rows, cols);
+      else
+        transpose_tile_kernel<decltype(V)::value, 64><<<grid, kBlock, 0, ctx->stream>>>(x, y,
+                                                                                     rows, cols);
     });
-    return numrs_hip::check_launch(ctx, "transpose64_kernel");
+    return numrs_hip::check_launch(ctx, "transpose_tile_kernel");
   }
   dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
   transpose_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, y, rows, cols);
