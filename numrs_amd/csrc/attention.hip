@@ -38,13 +38,39 @@ constexpr int kHeadDim = 64;       // dh handled by the fused row-block kernel
 // LDS, and its four consecutive columns per register quad leave as one
 // 16-byte store.  The softmax follows the row kernel's arithmetic: m = max,
 // e = expf(s - m), P = e * (1/sum e).
-template <int MODE, int BJ>
+//
+// With EXTRA the kernel also multiplies the finished rows by E_z, the head's
+// [S, 64] block of a third matrix, into eo (row stride ldo):
+//   MODE 0: eo = P V                       (E = V; the attention output)
+//   MODE 1: eo (+)= ealpha * dS K          (E = K; the query gradient)
+// The rows already sit in the lane layout of an MFMA operand: register
+// 4g + e of block (bi, bj) is element (query 32bi + c, key 32bj + 8g + 4h +
+// e), so eo^T = E^T Y^T runs as 32x32x2 MFMAs with that register as B and
+// E[key][d] as A, each wave reducing over its own S/4 keys.  A wave stages
+// its keys' rows of E in LDS by DMA at the start ([key][64], the 16-byte
+// chunks of rows whose bit 2 is set XOR-ed by 8 so that the two half-waves'
+// rows fall in different banks); the four wave partials then meet in LDS (rows padded to
+// 68 floats) and are added in wave order, each thread finishing 16
+// consecutive outputs of one row with float4 loads and stores.
+constexpr int kPartStride = 68;  // floats per row of a wave's [64, 64] partial in LDS
+
+template <int BJ>
+constexpr int extra_lds_floats() {
+  return 4 * kRowsPerBlock * kPartStride > 4 * 32 * BJ * kHeadDim ? 4 * kRowsPerBlock * kPartStride
+                                                                   : 4 * 32 * BJ * kHeadDim;
+}
+
+template <int MODE, int BJ, bool EXTRA>
 __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict__ X,
                                                         const float *__restrict__ W,
                                                         const float *__restrict__ P,
                                                         float *__restrict__ out, int S, int H,
-                                                        int64_t ldx, int64_t ldw, float alpha) {
+                                                        int64_t ldx, int64_t ldw, float alpha,
+                                                        const float *__restrict__ E, int64_t lde,
+                                                        float *eo, int64_t ldo, float ealpha,
+                                                        int eacc) {
   __shared__ float red[4][kRowsPerBlock];
+  __shared__ __attribute__((aligned(1024))) float ebuf[EXTRA ? extra_lds_floats<BJ>() : 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, hh = lane >> 5;
   const int z = blockIdx.y, b = z / H, head = z - b * H;
@@ -52,6 +78,26 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   const float *Xz = X + (int64_t)b * S * ldx + (int64_t)head * kHeadDim;
   const float *Wz = W + (int64_t)b * S * ldw + (int64_t)head * kHeadDim;
   const int64_t zoff = (int64_t)z * S * S;
+  constexpr int kStage = 8 * BJ;  // DMA instructions per wave (4 rows of E each)
+  float *wbuf = ebuf + wave * (32 * BJ * kHeadDim);
+
+  // The wave's S/4 rows of E go to LDS by DMA before anything else (no
+  // registers held, complete long before the second product needs them):
+  // instruction it writes rows 4 it .. 4 it + 3 of the wave's keys, lane l
+  // the 16-byte slot l % 16 of row 4 it + l / 16, which holds chunk
+  // (l % 16) ^ 8 of rows whose bit 2 is set.
+  if constexpr (EXTRA) {
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const float *Ez = E + ((int64_t)b * S + (int64_t)wave_u * 32 * BJ) * lde +
+                      (int64_t)head * kHeadDim;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)ebuf + (uint32_t)wave_u * (32 * BJ * kHeadDim * 4);
+#pragma unroll
+    for (int it = 0; it < kStage; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int chunk = (lane & 15) ^ (8 * ((kk >> 2) & 1));
+      numrs_hip::lds_dma16(Ez, (uint32_t)(4 * ((int64_t)kk * lde + 4 * chunk)), lds0 + 1024u * it);
+    }
+  }
 
   f16v acc[2][BJ];
 #pragma unroll
@@ -100,7 +146,7 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   };
 
   float t[2];
-  if (MODE == 0) {
+  if constexpr (MODE == 0) {
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
       float m = -INFINITY;
@@ -137,8 +183,12 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
       for (int bj = 0; bj < BJ; ++bj)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
-          const f4 v = {acc[bi][bj][4 * i4] * inv, acc[bi][bj][4 * i4 + 1] * inv,
-                        acc[bi][bj][4 * i4 + 2] * inv, acc[bi][bj][4 * i4 + 3] * inv};
+          f4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = acc[bi][bj][4 * i4 + e] * inv;
+            acc[bi][bj][4 * i4 + e] = v[e];
+          }
           *reinterpret_cast<f4 *>(dst + col_of(bj, i4)) = v;
         }
     }
@@ -171,10 +221,68 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
         for (int i4 = 0; i4 < 4; ++i4) {
           f4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
+          for (int e = 0; e < 4; ++e) {
             v[e] = p[bi][bj][i4][e] * (acc[bi][bj][4 * i4 + e] - t[bi]);
+            acc[bi][bj][4 * i4 + e] = v[e];
+          }
           *reinterpret_cast<f4 *>(dst + col_of(bj, i4)) = v;
         }
+    }
+  }
+
+  if constexpr (EXTRA) {
+    // eo^T partial over the wave's keys: block (bd, bi) holds d rows
+    // 32bd + 8(i/4) + 4hh + (i%4) of query 32bi + c.  The staged row of key
+    // 32bj + 8g + 4hh + e has its chunks XOR-ed by 8 exactly when hh = 1.
+    __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));  // the wave's DMA has landed
+    f16v o[2][2];
+#pragma unroll
+    for (int bd = 0; bd < 2; ++bd)
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi) o[bd][bi] = f16v{};
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float *er = wbuf + (32 * bj + 8 * g + 4 * hh + e) * kHeadDim + c;
+          const float ev[2] = {er[32 * hh], er[32 * (1 - hh)]};
+#pragma unroll
+          for (int bd = 0; bd < 2; ++bd)
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi)
+              o[bd][bi] = __builtin_amdgcn_mfma_f32_32x32x2f32(ev[bd], acc[bi][bj][4 * g + e],
+                                                               o[bd][bi], 0, 0, 0);
+        }
+    __syncthreads();  // every wave is done with its staged rows
+    float *part = ebuf + wave * (kRowsPerBlock * kPartStride);
+#pragma unroll
+    for (int bd = 0; bd < 2; ++bd)
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const f4 v = {o[bd][bi][4 * i4], o[bd][bi][4 * i4 + 1], o[bd][bi][4 * i4 + 2],
+                        o[bd][bi][4 * i4 + 3]};
+          *reinterpret_cast<f4 *>(part + (32 * bi + c) * kPartStride + 32 * bd + 8 * i4 + 4 * hh) = v;
+        }
+    __syncthreads();
+    const int q = threadIdx.x >> 2, d0 = (threadIdx.x & 3) * 16;
+    float *dst = eo + (int64_t)(b * S + row0 + q) * ldo + (int64_t)head * kHeadDim + d0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int off = q * kPartStride + d0 + 4 * j;
+      const f4 s0 = *reinterpret_cast<const f4 *>(ebuf + off);
+      const f4 s1 = *reinterpret_cast<const f4 *>(ebuf + kRowsPerBlock * kPartStride + off);
+      const f4 s2 = *reinterpret_cast<const f4 *>(ebuf + 2 * kRowsPerBlock * kPartStride + off);
+      const f4 s3 = *reinterpret_cast<const f4 *>(ebuf + 3 * kRowsPerBlock * kPartStride + off);
+      f4 v = ((s0 + s1) + s2) + s3;
+      if constexpr (MODE == 1) {
+        v = ealpha * v;
+        if (eacc) v = *reinterpret_cast<const f4 *>(dst + 4 * j) + v;
+      }
+      *reinterpret_cast<f4 *>(dst + 4 * j) = v;
     }
   }
 }
@@ -188,17 +296,32 @@ bool rows_fit(int64_t S, int64_t dh, int64_t ldx, int64_t ldw, const void *x, co
          numrs_hip::aligned16(x) && numrs_hip::aligned16(w) && numrs_hip::aligned16(p);
 }
 
-template <int MODE>
+// The third matrix and its product's output as the fused kernel reads and
+// writes them: 16-byte strides and alignment.
+bool extra_fit(int64_t lde, int64_t ldo, const void *e, const void *eo) {
+  // the DMA's per-lane byte offsets (rows below 128 of a wave's keys) fit 31 bits
+  return lde % 4 == 0 && ldo % 4 == 0 && lde < (int64_t{1} << 22) && numrs_hip::aligned16(e) &&
+         numrs_hip::aligned16(eo);
+}
+
+template <int MODE, bool EXTRA>
 int launch_rows(numrs_hip_ctx *ctx, const float *X, int64_t ldx, const float *W, int64_t ldw,
-                const float *P, float *out, int64_t B, int64_t S, int64_t H, float alpha) {
+                const float *P, float *out, int64_t B, int64_t S, int64_t H, float alpha,
+                const float *E = nullptr, int64_t lde = 0, float *eo = nullptr, int64_t ldo = 0,
+                float ealpha = 1.0f, int eacc = 0) {
   const dim3 grid((unsigned)(S / kRowsPerBlock), (unsigned)(B * H));
   const int s = (int)S, h = (int)H;
+#define NRS_ROWS(BJ)                                                                            \
+  attn_rows_kernel<MODE, BJ, EXTRA><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, \
+                                                                    alpha, E, lde, eo, ldo,     \
+                                                                    ealpha, eacc)
   switch (S / 128) {
-    case 1: attn_rows_kernel<MODE, 1><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
-    case 2: attn_rows_kernel<MODE, 2><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
-    case 3: attn_rows_kernel<MODE, 3><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
-    default: attn_rows_kernel<MODE, 4><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha); break;
+    case 1: NRS_ROWS(1); break;
+    case 2: NRS_ROWS(2); break;
+    case 3: NRS_ROWS(3); break;
+    default: NRS_ROWS(4); break;
   }
+#undef NRS_ROWS
   return numrs_hip::check_launch(ctx, "attn_rows_kernel");
 }
 
@@ -230,8 +353,10 @@ int numrs_hip_attention_forward_strided(numrs_hip_ctx *ctx, const float *q, cons
   const int64_t dh = D / H, Z = B * H, li = ld_qkv, lo = ld_out;
   const float alpha = 1.0f / sqrtf((float)dh);
   if (rows_fit(S, dh, li, li, q, k, P) && B * H < 65536) {
-    // P = softmax_rows(alpha * Q K^T) in one kernel
-    if (int rc = launch_rows<0>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha)) return rc;
+    // P = softmax_rows(alpha * Q K^T) and O = P V in one kernel
+    if (extra_fit(li, lo, v, out))
+      return launch_rows<0, true>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha, v, li, out, lo);
+    if (int rc = launch_rows<0, false>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha)) return rc;
     return numrs_hip_gemm(ctx, P, S, v, li, out, lo, S, S, dh, 0, 0, 1.0f, 0, Z, H, H * S * S,
                           S * S, S * li, dh, S * lo, dh);
   }
@@ -258,32 +383,49 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
   const int64_t dh = D / H, Z = B * H, li = ld_qkv, lo = ld_out;
   const float alpha = 1.0f / sqrtf((float)dh);
   // dV_z = P_z^T dO_z
-  if (dv)
-    if (int rc = numrs_hip_gemm(ctx, P, S, dout, lo, dv, li, S, S, dh, 1, 0, 1.0f, accumulate, Z,
-                                H, H * S * S, S * S, S * lo, dh, S * li, dh))
-      return rc;
-  if (!dq && !dk) return NUMRS_HIP_OK;
-  // dS lives in a block of its own: the dQ/dK products below may split their
+  auto dv_gemm = [&]() {
+    return numrs_hip_gemm(ctx, P, S, dout, lo, dv, li, S, S, dh, 1, 0, 1.0f, accumulate, Z, H,
+                          H * S * S, S * S, S * lo, dh, S * li, dh);
+  };
+  if (!dq && !dk) return dv ? dv_gemm() : NUMRS_HIP_OK;
+  // dS lives in a block of its own: the products below may split their
   // reduction and write partials to the context workspace while reading dS.
   numrs_hip::TempBlock dSb(ctx);
   if (int rc = dSb.alloc((size_t)(Z * S * S) * sizeof(float))) return rc;
-  float *dP = dSb.f();
-  if (rows_fit(S, dh, lo, li, dout, v, P) && numrs_hip::aligned16(dP) && B * H < 65536) {
-    // dS = P * (dP - rowsum(dP * P)) with dP = dO V^T, in one kernel
-    if (int rc = launch_rows<1>(ctx, dout, lo, v, li, P, dP, B, S, H, 1.0f)) return rc;
-  } else {
-    // dP_z = dO_z V_z^T
-    if (int rc = numrs_hip_gemm(ctx, dout, lo, v, li, dP, S, S, dh, S, 0, 1, 1.0f, 0, Z, H,
-                                S * lo, dh, S * li, dh, H * S * S, S * S))
-      return rc;
-    // dS = P * (dP - rowsum(dP * P)), in place over dP
-    if (int rc = numrs_hip_softmax_backward(ctx, P, dP, dP, Z * S, S, 0)) return rc;
-  }
-  // dQ_z = alpha * dS_z K_z ;  dK_z = alpha * dS_z^T Q_z  (one launch for both)
-  const numrs_hip::BatchedMat dS{dP, S, H * S * S, S * S};
+  float *dS = dSb.f();
+  const numrs_hip::BatchedMat dSm{dS, S, H * S * S, S * S};
   const numrs_hip::BatchedMat Km{k, li, S * li, dh}, Qm{q, li, S * li, dh};
   const numrs_hip::BatchedOut dQ{dq, li, S * li, dh}, dK{dk, li, S * li, dh};
-  return numrs_hip::gemm_nn_tn_pair(ctx, dS, Km, dQ, Qm, dK, S, S, dh, alpha, accumulate, Z, H);
+  if (rows_fit(S, dh, lo, li, dout, v, P) && numrs_hip::aligned16(dS) && B * H < 65536) {
+    // dS = P * (dP - rowsum(dP * P)) with dP = dO V^T, and dQ = alpha dS K,
+    // in one kernel; then dV and dK = alpha dS^T Q as one pair launch.
+    if (dq && extra_fit(li, li, k, dq)) {
+      if (int rc = launch_rows<1, true>(ctx, dout, lo, v, li, P, dS, B, S, H, 1.0f, k, li, dq, li,
+                                        alpha, accumulate))
+        return rc;
+    } else {
+      if (int rc = launch_rows<1, false>(ctx, dout, lo, v, li, P, dS, B, S, H, 1.0f)) return rc;
+      if (dq)
+        if (int rc = numrs_hip::gemm_nn_tn_pair(ctx, dSm, Km, dQ, Qm, {nullptr, 0, 0, 0}, S, S,
+                                                dh, alpha, accumulate, Z, H))
+          return rc;
+    }
+    if (!dk) return dv ? dv_gemm() : NUMRS_HIP_OK;
+    const numrs_hip::BatchedMat Pm{P, S, H * S * S, S * S}, dOm{dout, lo, S * lo, dh};
+    const numrs_hip::BatchedOut dV{dv, li, S * li, dh};
+    return numrs_hip::gemm_tn_pair(ctx, Pm, dOm, dV, 1.0f, dSm, Qm, dK, alpha, S, S, dh,
+                                   accumulate, Z, H);
+  }
+  if (dv)
+    if (int rc = dv_gemm()) return rc;
+  // dP_z = dO_z V_z^T
+  if (int rc = numrs_hip_gemm(ctx, dout, lo, v, li, dS, S, S, dh, S, 0, 1, 1.0f, 0, Z, H, S * lo,
+                              dh, S * li, dh, H * S * S, S * S))
+    return rc;
+  // dS = P * (dP - rowsum(dP * P)), in place over dP
+  if (int rc = numrs_hip_softmax_backward(ctx, P, dS, dS, Z * S, S, 0)) return rc;
+  // dQ_z = alpha * dS_z K_z ;  dK_z = alpha * dS_z^T Q_z  (one launch for both)
+  return numrs_hip::gemm_nn_tn_pair(ctx, dSm, Km, dQ, Qm, dK, S, S, dh, alpha, accumulate, Z, H);
 }
 
 int numrs_hip_attention_forward(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,

@@ -180,6 +180,39 @@ struct BatchedOut {
 int gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, BatchedOut C1, BatchedMat Y2,
                     BatchedOut C2, int64_t M, int64_t K, int64_t N, float alpha, int accumulate,
                     int64_t batch, int64_t binner);
+// C1_z = alpha1 X1_z^T Y1_z and C2_z = alpha2 X2_z^T Y2_z (X [M,K], Y [M,N],
+// C [K,N]) for z < batch, in one launch where the streamed path fits
+// (attention's dV = P^T dO with dK = alpha dS^T Q).  Either output may be
+// null; accumulate adds into the outputs.
+int gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, BatchedOut C1, float alpha1,
+                 BatchedMat X2, BatchedMat Y2, BatchedOut C2, float alpha2, int64_t M, int64_t K,
+                 int64_t N, int accumulate, int64_t batch, int64_t binner);
+
+
+// One LDS DMA instruction: each lane copies 16 bytes from base + off (off in
+// bytes, per lane; base uniform) into LDS at lds + 16 * lane.  Written as
+// inline asm so that the compiler neither sinks the issue towards the next
+// barrier nor adds its own vmcnt waits for it (it cannot tell which LDS stage
+// an LDS DMA writes, so it would wait for every outstanding one before any
+// fragment read).  The caller places the vmcnt waits: vector-memory
+// operations complete in issue order.  The s_nop covers the M0 write -> LDS
+// DMA hazard.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const float *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (expcnt and lgkmcnt left at their no-wait maxima).  The
+// 6-bit vmcnt is split: bits 3:0 of the immediate hold vmcnt[3:0] and bits
+// 15:14 hold vmcnt[5:4].
+constexpr int wait_vm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
 
 }  // namespace numrs_hip
 

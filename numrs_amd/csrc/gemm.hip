@@ -503,30 +503,9 @@ struct StreamCfg {
   static constexpr int kBI = kWP / 32, kBJ = TQ / 64;  // 32 x 32 MFMA blocks per wave
 };
 
-// One LDS DMA instruction: each lane copies 16 bytes from base + off (off in
-// bytes, per lane; base uniform) into LDS at lds + 16 * lane.  Written as
-// inline asm so that the compiler neither sinks the issue towards the next
-// barrier nor adds its own vmcnt waits for it (it cannot tell which LDS stage
-// an LDS DMA writes, so it would wait for every outstanding one before any
-// fragment read).  The caller places the vmcnt waits: vector-memory
-// operations complete in issue order.  The s_nop covers the M0 write -> LDS
-// DMA hazard.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const float *base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(off), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
+using numrs_hip::lds_dma16;
+using numrs_hip::wait_vm;
 
-
-// s_waitcnt immediate that waits until at most n vector-memory operations
-// are outstanding (expcnt and lgkmcnt left at their no-wait maxima).  The
-// 6-bit vmcnt is split: bits 3:0 of the immediate hold vmcnt[3:0] and bits
-// 15:14 hold vmcnt[5:4].
-constexpr int wait_vm(int n) { return 0x3f70 | (n & 15) | ((n >> 4) << 14); }
 static_assert(wait_vm(0) == 0x3f70 && wait_vm(12) == 0x3f7c && wait_vm(24) == 0x7f78,
               "vmcnt immediate encoding");
 static_assert(2 * StreamCfg<kSP, kSQ>::kDma < 64, "vmcnt is 6 bits");
@@ -939,6 +918,32 @@ __global__ void __launch_bounds__(kThreads, 3) linear_backward_stream_mini(Gemm 
     stream_tile<true, false, kMP, kMQ>(dx, tile, blockIdx.y);
   else
     stream_tile<false, false, kMP, kMQ>(dw, tile - tiles_a, blockIdx.y);
+}
+
+// Two transposed-left products in one launch (attention's dV = P^T dO with
+// dK = alpha dS^T Q): both TN.
+__global__ void __launch_bounds__(kBigThreads, 1) tn_pair_stream(Gemm a, Gemm b, int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<false, false, kSP, kSQ, kBigWaves>(a, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kSP, kSQ, kBigWaves>(b, tile - tiles_a, blockIdx.y);
+}
+
+__global__ void __launch_bounds__(kThreads, 2) tn_pair_stream_small(Gemm a, Gemm b, int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<false, false, kHP, kHQ>(a, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kHP, kHQ>(b, tile - tiles_a, blockIdx.y);
+}
+
+__global__ void __launch_bounds__(kThreads, 3) tn_pair_stream_mini(Gemm a, Gemm b, int tiles_a) {
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile < tiles_a)
+    stream_tile<false, false, kMP, kMQ>(a, tile, blockIdx.y);
+  else
+    stream_tile<false, false, kMP, kMQ>(b, tile - tiles_a, blockIdx.y);
 }
 
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
@@ -1827,6 +1832,59 @@ int numrs_hip::gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, 
     return numrs_hip::check_launch(ctx, who);
   }
   if (int rc = gemm_dispatch(ctx, ga, batch, true, false)) return rc;
+  return gemm_dispatch(ctx, gb, batch, false, false);
+}
+
+int numrs_hip::gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, BatchedOut C1,
+                            float alpha1, BatchedMat X2, BatchedMat Y2, BatchedOut C2,
+                            float alpha2, int64_t M, int64_t K, int64_t N, int accumulate,
+                            int64_t batch, int64_t binner) {
+  const char *who = "gemm_tn_pair";
+  if (int rc = check_dims(ctx, who, batch, M, K, N)) return rc;
+  if (binner < 1 || binner > std::max<int64_t>(batch, 1))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: batch_inner %lld", who, (long long)binner);
+  if (batch == 0 || N == 0 || K == 0 || (C1.p == nullptr && C2.p == nullptr)) return NUMRS_HIP_OK;
+  if ((C1.p && (X1.p == nullptr || Y1.p == nullptr)) || (C2.p && (X2.p == nullptr || Y2.p == nullptr)))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null input", who);
+  // C[K,N] = alpha X^T Y with X [M,K], Y [M,N]: P=K, Q=N, R=M, both operands
+  // output-contiguous.
+  auto tn = [&](BatchedMat X, BatchedMat Y, BatchedOut C, float alpha) {
+    Gemm g = make(X.p, Y.p, C.p, X.ld, Y.ld, C.ld, X.so, Y.so, C.so, K, N, M, accumulate);
+    g.bsx2 = X.si, g.bsy2 = Y.si, g.bsc2 = C.si;
+    g.binner = (int)binner;
+    g.alpha = alpha;
+    return g;
+  };
+  if (M == 0) {  // an empty reduction leaves zeros (or the accumulated values)
+    for (int64_t z = 0; z < batch && !accumulate; ++z) {
+      const int64_t zo = z / binner, zi = z - zo * binner;
+      for (const BatchedOut *C : {&C1, &C2})
+        if (C->p)
+          for (int64_t r = 0; r < K; ++r)
+            if (int rc = numrs_hip_fill(ctx, C->p + zo * C->so + zi * C->si + r * C->ld, N, 0.0f))
+              return rc;
+    }
+    return NUMRS_HIP_OK;
+  }
+  const Gemm ga = C1.p ? tn(X1, Y1, C1, alpha1) : Gemm{}, gb = C2.p ? tn(X2, Y2, C2, alpha2) : Gemm{};
+  if (C1.p == nullptr) return gemm_dispatch(ctx, gb, batch, false, false);
+  if (C2.p == nullptr) return gemm_dispatch(ctx, ga, batch, false, false);
+  if (batch > 1 && tiny_fits(ga, batch) && tiny_fits(gb, batch))
+    return launch_tiny(ctx, ga, false, false, &gb, batch, nullptr);
+  int shape = kShapeLarge;
+  if (batch > 1 && pick_batched_stream(ctx, ga, false, false, &gb, batch, &shape)) {
+    const Gemm sa = as_stream(ga, shape), sb = as_stream(gb, shape);
+    const int64_t ta = stream_grid(sa), tb = stream_grid(sb);
+    dim3 grid((unsigned)(ta + tb), (unsigned)batch);
+    if (shape == kShapeMini)
+      tn_pair_stream_mini<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    else if (shape == kShapeSmall)
+      tn_pair_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    else
+      tn_pair_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+    return numrs_hip::check_launch(ctx, who);
+  }
+  if (int rc = gemm_dispatch(ctx, ga, batch, false, false)) return rc;
   return gemm_dispatch(ctx, gb, batch, false, false);
 }
 
