@@ -505,12 +505,30 @@ def bench_c1(ctx, steps, warmup):
     for _ in range(warmup):
         step().item()
     _WARM_LAUNCHES["C1"] = [warmup + warm_for(ctx, lambda i: step(), 0, WARM_MS)]
+    # a step is tens of microseconds: time enough of them for a stable mean
+    n = max(steps, 200)
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for _ in range(n):
         loss = step()
     loss.item()
-    per = (time.perf_counter() - t0) / steps
-    return {"us_per_step": per * 1e6, "loss": loss.item()}
+    per = (time.perf_counter() - t0) / n
+    out = {"us_per_step": per * 1e6, "loss": loss.item(), "steps": n}
+    # The same step recorded once into a HIP graph and replayed: every kernel
+    # of every step still runs, queued by one launch per step.
+    g = nr.StepGraph(ctx, step)
+    try:
+        for _ in range(warmup):
+            g.replay()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            g.replay()
+        gloss = g.outputs.item()
+        out["graph_us_per_step"] = (time.perf_counter() - t0) / n * 1e6
+        out["graph_loss"] = gloss
+    finally:
+        g.close()
+    return out
 
 
 def c4_flops(B=16, S=256, D=512, H=8, F=2048):
@@ -1139,7 +1157,14 @@ def main() -> int:
         if not args.no_cpu_baseline:
             ent["cpu_baseline"] = cpu_baseline_c1()
         secondary.append(ent)
-        log(f"  C1 MLP step {c1['us_per_step']:.1f} us")
+        secondary.append({"workload": "C1 MLP train step as above, recorded once into a HIP graph "
+                                      "and replayed per step (numrs_hip_graph_*; every kernel runs "
+                                      "every step)",
+                          "value": round(c1["graph_us_per_step"], 1), "unit": "us/step",
+                          "steps": c1["steps"], "bound": "latency",
+                          "final_loss": round(c1["graph_loss"], 6)})
+        log(f"  C1 MLP step {c1['us_per_step']:.1f} us, graph replay "
+            f"{c1['graph_us_per_step']:.1f} us")
         c4 = bench_c4(ctx, max(3, args.steps // 5), 2)
         secondary.append({"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
                                       "heads, FFN 2048 GELU, MSE, SGD) via the device engine",

@@ -147,6 +147,32 @@ void *numrs_hip_stream(numrs_hip_ctx *ctx);
 int numrs_hip_timer_record(numrs_hip_ctx *ctx, int slot);
 int numrs_hip_timer_elapsed_ms(numrs_hip_ctx *ctx, int slot_start, int slot_end, float *ms);
 
+/* No counterpart in the reference (numrs runs a training step's ops one by
+ * one, train.rs:159-183): graph recording and replay, for training loops
+ * that repeat one fixed step (same shapes, same buffers; new data copied
+ * into the input tensors between replays) and want one launch per step.
+ * numrs_hip_graph_begin starts recording the context's stream: the calls
+ * that follow queue nothing, they are recorded.  numrs_hip_graph_end turns
+ * the recording into a replayable graph; numrs_hip_graph_launch queues one
+ * replay on the context's stream, ordered with other work there.
+ *   - Run the step once before recording it: a workspace that must grow,
+ *     host uploads or downloads and synchronisations fail while recording
+ *     (numrs_hip_graph_abort then discards the recording; the recorded calls
+ *     never ran, so zero the gradients they would have written).
+ *   - Kernel arguments are those of the recording: host-side values that
+ *     change per step (a scheduler's learning rate, Adam's step count) are
+ *     not updated by replays, and the engine refuses to record optimizers
+ *     whose step depends on a host-side step count.
+ *   - Tensors created during the recording must stay alive while the graph
+ *     is replayed; blocks they release during the recording are held by the
+ *     graph until numrs_hip_graph_destroy. */
+typedef struct numrs_hip_graph numrs_hip_graph;
+int numrs_hip_graph_begin(numrs_hip_ctx *ctx);
+int numrs_hip_graph_end(numrs_hip_ctx *ctx, numrs_hip_graph **out);
+int numrs_hip_graph_abort(numrs_hip_ctx *ctx);
+int numrs_hip_graph_launch(numrs_hip_graph *g);
+int numrs_hip_graph_destroy(numrs_hip_graph *g);
+
 /* ---------------------------------------------------------------------- */
 /* Dense contractions (fp32 MFMA)                                          */
 /* ---------------------------------------------------------------------- */

@@ -38,6 +38,11 @@ SIGNATURES = {
     "numrs_hip_stream": (_vp, [_vp]),
     "numrs_hip_timer_record": (_i, [_vp, _i]),
     "numrs_hip_timer_elapsed_ms": (_i, [_vp, _i, _i, ctypes.POINTER(_f)]),
+    "numrs_hip_graph_begin": (_i, [_vp]),
+    "numrs_hip_graph_end": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "numrs_hip_graph_abort": (_i, [_vp]),
+    "numrs_hip_graph_launch": (_i, [_vp]),
+    "numrs_hip_graph_destroy": (_i, [_vp]),
     "numrs_hip_matmul_backward": (_i, [_vp] * 6 + [_i64] * 3 + [_i]),
     "numrs_hip_matmul_backward_batched": (_i, [_vp] * 6 + [_i64] * 7 + [_i]),
     "numrs_hip_matmul": (_i, [_vp] * 4 + [_i64] * 3 + [_i] * 3),

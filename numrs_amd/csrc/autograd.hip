@@ -1792,6 +1792,16 @@ int numrs_hip_optim_adam(numrs_hip_ctx *ctx, numrs_hip_tensor **params, int n, f
 int numrs_hip_optim_step(numrs_hip_optim *opt) {
   if (opt == nullptr) return NUMRS_HIP_E_INVALID;
   Optim &o = opt->o;
+  // A recorded graph replays its kernels with the arguments of the recording:
+  // optimizers whose step passes a host-side step count (bias corrections,
+  // Lookahead's k, L-BFGS's host-side line state) would repeat one step's
+  // values on every replay.
+  if (o.ctx != nullptr && o.ctx->capturing &&
+      (o.adam || o.fam == Family::Lookahead || o.fam == Family::LBFGS ||
+       (o.fam == Family::Kind && kind_uses_t(o.kind))))
+    return fail(o.ctx, NUMRS_HIP_E_INVALID,
+                "this optimizer's step depends on a host-side step count and cannot be recorded "
+                "into a graph; record SGD steps, or run this optimizer eagerly");
   switch (o.fam) {
     case Family::Lookahead: return lookahead_step(o);
     case Family::LBFGS: return lbfgs_step(o);

@@ -36,6 +36,12 @@ struct numrs_hip_ctx {
   int64_t live_blocks = 0;
   bool destroyed = false;
   int unbroadcast_mode = NUMRS_HIP_UNBROADCAST_CORRECT;
+  // Graph recording (numrs_hip_graph_begin .. _end): while `capturing`,
+  // blocks released by tensors are held in `capture_held` instead of going
+  // back to the cache -- the recorded kernels may use them on every replay
+  // -- and the graph takes them over when the recording ends.
+  bool capturing = false;
+  std::vector<std::pair<void *, size_t>> capture_held;
   // Device address of reduce.hip's static partials array on this context's
   // device, resolved at creation (the allocation-free entry point uses it).
   float *noalloc_partials = nullptr;
@@ -55,7 +61,8 @@ int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out);
 int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out);
 
 // Cached device allocation for engine tensors; sizes are rounded up so that
-// released blocks are reusable.  block_free returns the block to the cache.
+// released blocks are reusable.  block_free returns the block to the cache
+// (or, while a graph is being recorded, to the recording's held set).
 int block_alloc(numrs_hip_ctx *ctx, size_t bytes, void **out);
 void block_free(numrs_hip_ctx *ctx, void *p, size_t bytes);
 size_t block_round(size_t bytes);

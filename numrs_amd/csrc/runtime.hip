@@ -16,11 +16,21 @@ int fail(numrs_hip_ctx *ctx, int code, const char *fmt, ...) {
   return code;
 }
 
+// A buffer the recorded kernels address cannot move, and growing one needs a
+// device synchronisation, which a recording stream does not allow.
+static int refuse_growth(numrs_hip_ctx *ctx, const char *what, size_t bytes) {
+  return fail(ctx, NUMRS_HIP_E_INVALID,
+              "%s must grow to %zu bytes while a graph is being recorded: run the step once "
+              "before recording it",
+              what, bytes);
+}
+
 int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out) {
   if (bytes <= ctx->workspace_bytes && ctx->workspace != nullptr) {
     *out = ctx->workspace;
     return NUMRS_HIP_OK;
   }
+  if (ctx->capturing) return refuse_growth(ctx, "the workspace", bytes);
   // Growing: earlier kernels may still read the old buffer, so drain first.
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
   if (ctx->workspace != nullptr) NRS_HIP(ctx, hipFree(ctx->workspace));
@@ -41,6 +51,7 @@ int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out) {
     *out = static_cast<float *>(ctx->scratch);
     return NUMRS_HIP_OK;
   }
+  if (ctx->capturing) return refuse_growth(ctx, "the scratch region", bytes);
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
   if (ctx->scratch != nullptr) NRS_HIP(ctx, hipFree(ctx->scratch));
   ctx->scratch = nullptr;
@@ -80,8 +91,8 @@ int block_alloc(numrs_hip_ctx *ctx, size_t bytes, void **out) {
   }
   if (hipMalloc(out, size) != hipSuccess) {
     (void)hipGetLastError();
-    cache_release(ctx);
-    if (hipMalloc(out, size) != hipSuccess) {
+    if (!ctx->capturing) cache_release(ctx);  // releasing synchronises the stream
+    if (ctx->capturing || hipMalloc(out, size) != hipSuccess) {
       *out = nullptr;
       (void)hipGetLastError();
       return fail(ctx, NUMRS_HIP_E_NOMEM, "device allocation of %zu bytes failed", size);
@@ -93,6 +104,10 @@ int block_alloc(numrs_hip_ctx *ctx, size_t bytes, void **out) {
 
 void block_free(numrs_hip_ctx *ctx, void *p, size_t bytes) {
   if (p == nullptr) return;
+  if (ctx->capturing) {  // still live: the recording owns it now
+    ctx->capture_held.emplace_back(p, bytes);
+    return;
+  }
   --ctx->live_blocks;
   if (ctx->destroyed) {
     (void)hipFree(p);
@@ -124,6 +139,16 @@ int check_launch(numrs_hip_ctx *ctx, const char *what) {
 using numrs_hip::fail;
 
 static thread_local char g_create_error[512] = {0};
+
+// Calls that wait for the stream or move host memory are refused before they
+// reach HIP while a graph is being recorded: HIP would otherwise invalidate
+// the whole recording.
+#define NRS_NOT_RECORDING(ctx, what)                                                         \
+  do {                                                                                    \
+    if ((ctx)->capturing)                                                                 \
+      return fail((ctx), NUMRS_HIP_E_INVALID, "%s is not allowed while a graph is being "  \
+                  "recorded", (what));                                                    \
+  } while (0)
 
 namespace {
 
@@ -196,6 +221,7 @@ const char *numrs_hip_create_error(void) { return g_create_error; }
 int numrs_hip_destroy(numrs_hip_ctx *ctx) {
   NRS_CHECK_CTX(ctx);
   (void)hipSetDevice(ctx->device);
+  if (ctx->capturing) (void)numrs_hip_graph_abort(ctx);
   (void)hipStreamSynchronize(ctx->stream);
   for (int i = 0; i < kMaxTimers; ++i) (void)hipEventDestroy(ctx->events[i]);
   numrs_hip::cache_release(ctx);
@@ -206,6 +232,106 @@ int numrs_hip_destroy(numrs_hip_ctx *ctx) {
   ctx->stream = nullptr;
   ctx->destroyed = true;
   if (ctx->live_blocks == 0) delete ctx;  // else the last engine block frees it
+  return NUMRS_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Graph recording and replay of a fixed sequence of work on the context's
+// stream (a training step with fixed shapes and buffers).
+// ---------------------------------------------------------------------------
+
+struct numrs_hip_graph {
+  numrs_hip_ctx *ctx;
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  // blocks tensors released during the recording: the recorded kernels may
+  // use them on every replay, so they return to the cache only on destroy
+  std::vector<std::pair<void *, size_t>> held;
+};
+
+static void return_held(numrs_hip_ctx *ctx, std::vector<std::pair<void *, size_t>> &held) {
+  for (auto &b : held) numrs_hip::block_free(ctx, b.first, b.second);
+  held.clear();
+}
+
+int numrs_hip_graph_begin(numrs_hip_ctx *ctx) {
+  NRS_CHECK_CTX(ctx);
+  if (ctx->destroyed) return fail(ctx, NUMRS_HIP_E_INVALID, "context already destroyed");
+  if (ctx->capturing)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "a graph is already being recorded on this context");
+  NRS_HIP(ctx, hipSetDevice(ctx->device));
+  NRS_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+  ctx->capturing = true;
+  ctx->capture_held.clear();
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_graph_abort(numrs_hip_ctx *ctx) {
+  NRS_CHECK_CTX(ctx);
+  if (!ctx->capturing) return NUMRS_HIP_OK;
+  ctx->capturing = false;
+  hipGraph_t graph = nullptr;
+  (void)hipStreamEndCapture(ctx->stream, &graph);
+  (void)hipGetLastError();
+  if (graph != nullptr) (void)hipGraphDestroy(graph);
+  // Nothing recorded ever ran, so the held blocks are free again.
+  std::vector<std::pair<void *, size_t>> held;
+  held.swap(ctx->capture_held);
+  return_held(ctx, held);
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_graph_end(numrs_hip_ctx *ctx, numrs_hip_graph **out) {
+  NRS_CHECK_CTX(ctx);
+  if (out == nullptr) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_graph_end: null out pointer");
+  *out = nullptr;
+  if (!ctx->capturing) return fail(ctx, NUMRS_HIP_E_INVALID, "no graph is being recorded");
+  ctx->capturing = false;
+  std::vector<std::pair<void *, size_t>> held;
+  held.swap(ctx->capture_held);
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+  if (e != hipSuccess || graph == nullptr) {
+    (void)hipGetLastError();
+    if (graph != nullptr) (void)hipGraphDestroy(graph);
+    return_held(ctx, held);
+    return fail(ctx, NUMRS_HIP_E_HIP, "graph recording failed: %s", hipGetErrorString(e));
+  }
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipGraphDestroy(graph);
+    return_held(ctx, held);
+    return fail(ctx, NUMRS_HIP_E_HIP, "graph instantiation failed: %s", hipGetErrorString(e));
+  }
+  *out = new numrs_hip_graph{ctx, graph, exec, std::move(held)};
+  ++ctx->live_blocks;  // the graph keeps the context alive, like a tensor's block
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_graph_launch(numrs_hip_graph *g) {
+  if (g == nullptr) return NUMRS_HIP_E_INVALID;
+  numrs_hip_ctx *ctx = g->ctx;
+  if (ctx->destroyed) return fail(ctx, NUMRS_HIP_E_INVALID, "context already destroyed");
+  if (ctx->capturing)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "cannot replay a graph into a recording");
+  NRS_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_graph_destroy(numrs_hip_graph *g) {
+  if (g == nullptr) return NUMRS_HIP_OK;
+  numrs_hip_ctx *ctx = g->ctx;
+  if (ctx->capturing)
+    return fail(ctx, NUMRS_HIP_E_INVALID, "destroy a graph outside a recording");
+  // Queued replays finish first (a destroyed context's stream was drained).
+  if (!ctx->destroyed) NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  return_held(ctx, g->held);
+  delete g;
+  if (--ctx->live_blocks == 0 && ctx->destroyed) delete ctx;
   return NUMRS_HIP_OK;
 }
 
@@ -225,6 +351,7 @@ int numrs_hip_device_info(numrs_hip_ctx *ctx, int *num_cus, char *arch, size_t a
 
 int numrs_hip_malloc(numrs_hip_ctx *ctx, size_t bytes, void **dptr) {
   NRS_CHECK_CTX(ctx);
+  NRS_NOT_RECORDING(ctx, "numrs_hip_malloc");
   if (dptr == nullptr) return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_malloc: null out pointer");
   *dptr = nullptr;
   NRS_HIP(ctx, hipSetDevice(ctx->device));
@@ -239,6 +366,7 @@ int numrs_hip_malloc(numrs_hip_ctx *ctx, size_t bytes, void **dptr) {
 
 int numrs_hip_free(numrs_hip_ctx *ctx, void *dptr) {
   NRS_CHECK_CTX(ctx);
+  NRS_NOT_RECORDING(ctx, "numrs_hip_free");
   if (dptr == nullptr) return NUMRS_HIP_OK;
   NRS_HIP(ctx, hipFree(dptr));
   return NUMRS_HIP_OK;
@@ -246,6 +374,7 @@ int numrs_hip_free(numrs_hip_ctx *ctx, void *dptr) {
 
 int numrs_hip_upload(numrs_hip_ctx *ctx, void *dst, const void *host_src, size_t bytes) {
   NRS_CHECK_CTX(ctx);
+  NRS_NOT_RECORDING(ctx, "a host-to-device upload");
   if (bytes == 0) return NUMRS_HIP_OK;
   if (dst == nullptr || host_src == nullptr)
     return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_upload: null pointer");
@@ -256,6 +385,7 @@ int numrs_hip_upload(numrs_hip_ctx *ctx, void *dst, const void *host_src, size_t
 
 int numrs_hip_download(numrs_hip_ctx *ctx, void *host_dst, const void *src, size_t bytes) {
   NRS_CHECK_CTX(ctx);
+  NRS_NOT_RECORDING(ctx, "a device-to-host download");
   if (bytes == 0) return NUMRS_HIP_OK;
   if (host_dst == nullptr || src == nullptr)
     return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_download: null pointer");
@@ -295,6 +425,7 @@ int numrs_hip_fill(numrs_hip_ctx *ctx, float *dst, int64_t n, float value) {
 
 int numrs_hip_sync(numrs_hip_ctx *ctx) {
   NRS_CHECK_CTX(ctx);
+  NRS_NOT_RECORDING(ctx, "numrs_hip_sync");
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return NUMRS_HIP_OK;
 }
@@ -319,6 +450,7 @@ int numrs_hip_timer_record(numrs_hip_ctx *ctx, int slot) {
 
 int numrs_hip_timer_elapsed_ms(numrs_hip_ctx *ctx, int slot_start, int slot_end, float *ms) {
   NRS_CHECK_CTX(ctx);
+  NRS_NOT_RECORDING(ctx, "numrs_hip_timer_elapsed_ms");
   if (ms == nullptr || slot_start < 0 || slot_start >= kMaxTimers || slot_end < 0 ||
       slot_end >= kMaxTimers)
     return fail(ctx, NUMRS_HIP_E_INVALID, "bad timer slots %d,%d", slot_start, slot_end);
