@@ -370,6 +370,59 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+// The same for rows of at most 64 * 4 * NV columns (cols % 4 == 0, 16-byte
+// aligned operands): a lane holds the float4 column groups lane, lane + 64,
+// ... in registers, so the row is read once, both statistics come from
+// registers and the output leaves as 16-byte stores.  Each element is
+// normalised with the scalar kernel's expression ((x - mu) * rs) * gamma + beta.
+template <int NV>
+__global__ void __launch_bounds__(kBlock)
+    layernorm_fwd_vec(const float *__restrict__ x, const float *__restrict__ gamma,
+                      const float *__restrict__ beta, float *__restrict__ y,
+                      float *__restrict__ mean, float *__restrict__ rstd, int64_t rows, int cols,
+                      float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // uniform over the wave
+  const float *xr = x + row * cols;
+  f4 xv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = 4 * (lane + 64 * i);
+    xv[i] = c < cols ? *reinterpret_cast<const f4 *>(xr + c) : f4{0.f, 0.f, 0.f, 0.f};
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) s += ((xv[i][0] + xv[i][1]) + xv[i][2]) + xv[i][3];
+  const float mu = wave_sum(s) / (float)cols;
+  float v = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (4 * (lane + 64 * i) < cols)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = xv[i][e] - mu;
+        v += d * d;
+      }
+  const float rs = 1.0f / sqrtf(wave_sum(v) / (float)cols + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = 4 * (lane + 64 * i);
+    if (c < cols) {
+      const f4 gv = *reinterpret_cast<const f4 *>(gamma + c);
+      const f4 bv = *reinterpret_cast<const f4 *>(beta + c);
+      f4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (xv[i][e] - mu) * rs * gv[e] + bv[e];
+      *reinterpret_cast<f4 *>(y + row * cols + c) = o;
+    }
+  }
+  if (lane == 0) {
+    if (mean) mean[row] = mu;
+    if (rstd) rstd[row] = rs;
+  }
+}
+
 template <int OP>
 int launch_binary_fwd(numrs_hip_ctx *ctx, const float *a, const int64_t *as, int and_,
                       const float *b, const int64_t *bs, int bnd, float *out) {
@@ -582,8 +635,24 @@ int numrs_hip_layernorm_forward(numrs_hip_ctx *ctx, const float *x, const float 
   if (rows == 0) return NUMRS_HIP_OK;
   if (x == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "layernorm: null pointer");
-  layernorm_fwd_kernel<<<grid_for(rows, 4), kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean,
-                                                                      rstd, rows, cols, eps);
+  const unsigned grid = grid_for(rows, 4);
+  const bool vec = cols % 4 == 0 && cols <= 2048 && numrs_hip::aligned16(x) &&
+                   numrs_hip::aligned16(gamma) && numrs_hip::aligned16(beta) &&
+                   numrs_hip::aligned16(y);
+  if (vec) {
+    const int c = (int)cols;
+    if (cols <= 256)
+      layernorm_fwd_vec<1><<<grid, kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, rows, c, eps);
+    else if (cols <= 512)
+      layernorm_fwd_vec<2><<<grid, kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, rows, c, eps);
+    else if (cols <= 1024)
+      layernorm_fwd_vec<4><<<grid, kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, rows, c, eps);
+    else
+      layernorm_fwd_vec<8><<<grid, kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, rows, c, eps);
+    return numrs_hip::check_launch(ctx, "layernorm_fwd_vec");
+  }
+  layernorm_fwd_kernel<<<grid, kBlock, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, rows, cols,
+                                                         eps);
   return numrs_hip::check_launch(ctx, "layernorm_fwd_kernel");
 }
 

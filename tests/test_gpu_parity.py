@@ -581,6 +581,31 @@ LN_CASES = [(1, 1), (7, 5), (33, 64), (130, 1000), (9, 2048), (5, 2047), (1030, 
             (4096, 512)]
 
 
+@pytest.mark.parametrize("rows,cols", LN_CASES + [(3, 2056), (2, 4096), (64, 256), (8, 1024)])
+def test_layernorm_forward(hip_ctx, rng, rows, cols):
+    """Register-resident rows (cols % 4 == 0, up to 2048) and the looped
+    kernel (other widths) against the float64 statistics."""
+    say(f"layernorm_forward {rows}x{cols}")
+    x = rand(rng, (rows, cols)) + 3.0  # an offset the mean must remove
+    gamma = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    beta = rand(rng, cols)
+    x64 = x.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    rs = 1.0 / np.sqrt(((x64 - mu) ** 2).mean(1, keepdims=True) + 1e-5)
+    want = (x64 - mu) * rs * gamma + beta
+    c = hip_ctx
+    xd, gd, bd = c.to_device(x), c.to_device(gamma), c.to_device(beta)
+    y, m, r = c.empty((rows, cols)), c.empty((rows,)), c.empty((rows,))
+    c._check(L.load().numrs_hip_layernorm_forward(c.handle, xd.ptr, gd.ptr, bd.ptr, y.ptr, m.ptr,
+                                                  r.ptr, rows, cols, 1e-5))
+    assert_close(y.numpy(), want, what="y")
+    assert_close(m.numpy(), mu[:, 0], what="mean")
+    assert_close(r.numpy(), rs[:, 0], what="rstd")
+    # the oracle's LayerNorm (float64 inside, rounded to fp32 on output)
+    want_o, _, _ = O.layernorm_fwd(x, gamma, beta)
+    assert_close(y.numpy(), want_o, what="y vs oracle")
+
+
 @pytest.mark.parametrize("rows,cols", LN_CASES)
 def test_layernorm_backward(hip_ctx, rng, rows, cols):
     say(f"layernorm_backward {rows}x{cols}")
