@@ -382,19 +382,21 @@ __device__ __forceinline__ int64_t colsum_group(int b, int n, int64_t m) {
 }
 
 // Splits are added in order s = 0, 1, ... (deterministic); the loads of a
-// batch of splits are issued before its ordered adds.  blockIdx.y selects one
-// of two products reduced by the same launch, or (y == cs_slot) the column
-// sums `cs`.  VEC: four consecutive elements of one row per thread (Q, ldc
-// and the pointers 16-byte aligned).
+// batch of splits are issued before its ordered adds.  With column sums
+// (has_cs), row y = 0 of the grid computes them and rows 1, 2 reduce the
+// products; otherwise rows 0, 1 reduce the products.  The column sums (one
+// long strided walk per workgroup) go first so that they are dispatched
+// before, and overlap, the short split reductions.  VEC: four consecutive
+// elements of one row per thread (Q, ldc and the pointers 16-byte aligned).
 template <bool VEC>
 __global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, ColSum cs,
-                                                     int cs_slot) {
-  if ((int)blockIdx.y == cs_slot) {
+                                                     int has_cs) {
+  if (has_cs && blockIdx.y == 0) {
     const int64_t grp = colsum_group(blockIdx.x, gridDim.x, cs.cols / kColSumCols);
     if (grp >= 0) colsum_block(cs, grp);
     return;
   }
-  const SplitSet &d = blockIdx.y ? s1 : s0;
+  const SplitSet &d = (int)blockIdx.y - has_cs ? s1 : s0;
   typedef typename std::conditional<VEC, f4, float>::type V;
   constexpr int kW = VEC ? 4 : 1;
   constexpr int kBatch = VEC ? 4 : 8;
@@ -1015,20 +1017,19 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum
   if (m == 1) set[1] = set[0];
   int64_t blocks = (most / (vec ? 4 : 1) + 255) / 256;
   ColSum c{};
-  int slot = -1;
+  const int has_cs = cs != nullptr ? 1 : 0;
   if (cs != nullptr) {
     c = *cs;
-    slot = m;
     blocks = std::max<int64_t>(blocks, c.cols / kColSumCols);
     blocks = (blocks + 7) & ~int64_t{7};  // whole rounds of the eight XCDs
   }
   if (blocks > 0x7fffffff)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "splitk_reduce: too large");
-  dim3 grid((unsigned)std::max<int64_t>(blocks, 1), (unsigned)(m + (cs != nullptr)));
+  dim3 grid((unsigned)std::max<int64_t>(blocks, 1), (unsigned)(m + has_cs));
   if (vec)
-    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, slot);
+    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, has_cs);
   else
-    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, slot);
+    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, has_cs);
   return numrs_hip::check_launch(ctx, "splitk_reduce");
 }
 
