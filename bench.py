@@ -1165,7 +1165,7 @@ def main() -> int:
                           "final_loss": round(c1["graph_loss"], 6)})
         log(f"  C1 MLP step {c1['us_per_step']:.1f} us, graph replay "
             f"{c1['graph_us_per_step']:.1f} us")
-        c4 = bench_c4(ctx, max(3, args.steps // 5), 2)
+        c4 = bench_c4(ctx, max(10, args.steps), 3)
         secondary.append({"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
                                       "heads, FFN 2048 GELU, MSE, SGD) via the device engine",
                           "value": round(c4["ms_per_step"], 3), "unit": "ms/step",
@@ -1174,7 +1174,7 @@ def main() -> int:
                           "bound": "mfma (GEMMs) + hbm (LN/GELU/softmax)",
                           "final_loss": round(c4["loss"], 6)})
         log(f"  C4 block step {c4['ms_per_step']:.3f} ms {c4['tflops']:.1f} TFLOP/s")
-        c5 = bench_c5(ctx, max(3, args.steps // 10), 1)
+        c5 = bench_c5(ctx, max(5, args.steps // 4), 2)
         secondary.append({"workload": "C5 2-layer LSTM forecaster train step (in 64, hidden 256, "
                                       "seq 128, batch 64, head 256->1, MSE, SGD) via the device "
                                       "engine",
