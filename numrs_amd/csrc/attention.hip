@@ -99,6 +99,30 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
     }
   }
 
+  // Register i of block (bi, bj) holds row row0 + 32*bi + c and column
+  // col0 + 32*bj + 8*(i/4) + 4*hh + (i%4).
+  auto col_of = [&](int bj, int i4) { return col0 + 32 * bj + 8 * i4 + 4 * hh; };
+  auto row_ptr = [&](float *base, int bi) { return base + zoff + (int64_t)(row0 + 32 * bi + c) * S; };
+  // The backward's P block (read from HBM): for S <= 256 its loads go out
+  // before the dO V^T MFMAs, which then cover their latency.
+  constexpr bool kEarlyP = MODE == 1 && BJ <= 2;
+  f4 p[MODE == 1 ? 2 : 1][MODE == 1 ? BJ : 1][4];
+  auto load_p = [&]() {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const float *src = row_ptr(const_cast<float *>(P), bi);
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          p[bi][bj][i4] = *reinterpret_cast<const f4 *>(src + col_of(bj, i4));
+    }
+  };
+  if constexpr (kEarlyP) {
+    load_p();
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+  }
+
   f16v acc[2][BJ];
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
@@ -122,10 +146,6 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
           acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[bj][j], a[bi][j], acc[bi][bj], 0, 0, 0);
   }
 
-  // Register i of block (bi, bj) holds row row0 + 32*bi + c and column
-  // col0 + 32*bj + 8*(i/4) + 4*hh + (i%4).
-  auto col_of = [&](int bj, int i4) { return col0 + 32 * bj + 8 * i4 + 4 * hh; };
-  auto row_ptr = [&](float *base, int bi) { return base + zoff + (int64_t)(row0 + 32 * bi + c) * S; };
   // Row totals over the wave's columns (in-lane, then the other half-wave),
   // then over the four waves: op 0 = max, 1 = sum.
   auto row_reduce = [&](float (&v)[2], int op) {
@@ -193,15 +213,7 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
         }
     }
   } else {
-    f4 p[2][BJ][4];
-#pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
-      const float *src = row_ptr(const_cast<float *>(P), bi);
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) p[bi][bj][i4] = *reinterpret_cast<const f4 *>(src + col_of(bj, i4));
-    }
+    if constexpr (!kEarlyP) load_p();
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
       float s = 0.0f;
