@@ -53,6 +53,10 @@ using Buf = std::shared_ptr<Storage>;
 struct GradCell {
   Buf buf;
   bool valid = false;  // false: logically zero
+  // A scalar loss's cell whose buffer holds the backward seed 1, written by the
+  // loss's forward kernel together with the root gradient it pre-formed;
+  // cleared by every other write to the cell.
+  bool seed_preset = false;
 };
 
 struct Node;
@@ -133,6 +137,7 @@ bool recording(std::initializer_list<const T *> ins) {
 // Grad buffer of `t` for a producer; *acc tells whether to add (1) or write (0).
 int grad_target(const T &t, float **ptr, int *acc) {
   GradCell &c = *t->grad;
+  c.seed_preset = false;
   if (!c.buf)
     if (int rc = alloc_buf(t->ctx, t->numel(), sizeof(float), &c.buf)) return rc;
   *acc = c.valid ? 1 : 0;
@@ -144,6 +149,7 @@ int grad_target(const T &t, float **ptr, int *acc) {
 // Grad of `t` as a materialised buffer (zero-filled if never written).
 int grad_materialise(const T &t) {
   GradCell &c = *t->grad;
+  c.seed_preset = false;
   if (!c.buf)
     if (int rc = alloc_buf(t->ctx, t->numel(), sizeof(float), &c.buf)) return rc;
   if (!c.valid) {
@@ -353,8 +359,23 @@ float *take_seed(const T &out) {
   return out->grad->buf->ptr;
 }
 
+// A loss whose forward kernel pre-formed its root gradient (saved[slot]) and
+// wrote the seed 1 into its own cell: when the loss is this sweep's root and
+// the input's cell has never held a buffer, the cell takes the pre-formed
+// buffer and no backward kernel runs.  Returns true when it did.
+bool adopt_preformed(const T &out, Node &n, size_t slot, const T &x) {
+  if (slot >= n.saved.size() || !n.saved[slot] || g_seed_root != out.get() ||
+      !out->grad->seed_preset || x->grad->valid || x->grad->buf)
+    return false;
+  g_seed_root = nullptr;  // the seed is already in the root's cell
+  x->grad->buf = std::move(n.saved[slot]);
+  x->grad->valid = true;
+  return true;
+}
+
 int bw_mse(const T &out, const float *g, Node &n) {  // backward.rs:239-261
   const T &p = n.inputs[0], &t = n.inputs[1];
+  if (p->requires_grad && !t->requires_grad && adopt_preformed(out, n, 0, p)) return NUMRS_HIP_OK;
   float *dp = nullptr, *dt = nullptr;
   int ap = 0, at = 0;
   if (p->requires_grad)
@@ -377,6 +398,7 @@ int bw_mse(const T &out, const float *g, Node &n) {  // backward.rs:239-261
 int bw_ce(const T &out, const float *g, Node &n) {  // backward.rs:265-301
   const T &x = n.inputs[0];
   if (!x->requires_grad) return NUMRS_HIP_OK;  // the target's grad is [0]: nothing to add
+  if (adopt_preformed(out, n, n.op == Op::CrossEntropyLabels ? 1 : 0, x)) return NUMRS_HIP_OK;
   float *dst;
   int acc;
   if (int rc = grad_target(x, &dst, &acc)) return rc;
@@ -815,15 +837,31 @@ int op_sum(const T &a, bool mean, T *out) {  // ops.rs:214-252
   return NUMRS_HIP_OK;
 }
 
+// Buffers for a loss's pre-formed root gradient (n floats) and for its own
+// gradient cell (the seed), when `want`; *pre stays null otherwise.
+int preform_buffers(const T &r, bool want, int64_t n, Buf *pre) {
+  if (!want) return NUMRS_HIP_OK;
+  if (int rc = alloc_buf(r->ctx, n, sizeof(float), pre)) return rc;
+  return alloc_buf(r->ctx, 1, sizeof(float), &r->grad->buf);
+}
+
 int op_mse(const T &p, const T &t, T *out) {  // ops.rs:255-278
   numrs_hip_ctx *ctx = p->ctx;
   if (p->numel() != t->numel()) return fail(ctx, NUMRS_HIP_E_SHAPE, "mse_loss: size mismatch");
   const bool rec = recording({&p, &t});
   T r;
   if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
-  if (int rc = numrs_hip_mse_loss(ctx, p->data->ptr, t->data->ptr, p->numel(), r->data->ptr))
+  // A loss that may be the backward's root forms that gradient (dp) and the
+  // seed with its own kernel; bw_mse adopts them when it is the root.
+  Buf pre;
+  if (int rc = preform_buffers(r, rec && p->requires_grad && !t->requires_grad, p->numel(), &pre))
     return rc;
-  if (rec) attach(r, Op::MSE, {p, t});
+  if (int rc = numrs_hip::mse_loss_impl(ctx, p->data->ptr, t->data->ptr, p->numel(),
+                                        r->data->ptr, pre ? pre->ptr : nullptr,
+                                        pre ? r->grad->buf->ptr : nullptr))
+    return rc;
+  if (pre) r->grad->seed_preset = true;
+  if (rec) attach(r, Op::MSE, {p, t}, 0, 0.f, {pre});
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -836,10 +874,17 @@ int op_ce(const T &x, const T &t, T *out) {  // ops.rs:281-334
   const bool rec = recording({&x, &t});
   T r;
   if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
-  if (int rc = numrs_hip_cross_entropy_loss(ctx, x->data->ptr, t->data->ptr, nullptr, x->shape[0],
-                                            x->shape[1], r->data->ptr))
+  Buf pre;
+  if (int rc = preform_buffers(r, rec && x->requires_grad &&
+                                      numrs_hip::cross_entropy_preforms(x->shape[0]),
+                               x->numel(), &pre))
     return rc;
-  if (rec) attach(r, Op::CrossEntropy, {x, t});
+  if (int rc = numrs_hip::cross_entropy_loss_impl(
+          ctx, x->data->ptr, t->data->ptr, nullptr, x->shape[0], x->shape[1], r->data->ptr,
+          pre ? pre->ptr : nullptr, pre ? r->grad->buf->ptr : nullptr))
+    return rc;
+  if (pre) r->grad->seed_preset = true;
+  if (rec) attach(r, Op::CrossEntropy, {x, t}, 0, 0.f, {pre});
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -858,11 +903,16 @@ int op_ce_labels(const T &x, const int32_t *host_labels, T *out) {
   const bool rec = recording({&x});
   T r;
   if (int rc = make_tensor(ctx, {1}, rec, &r)) return rc;
-  if (int rc = numrs_hip_cross_entropy_loss(ctx, x->data->ptr, nullptr,
-                                            reinterpret_cast<const int32_t *>(lab->ptr), B, C,
-                                            r->data->ptr))
+  Buf pre;
+  if (int rc = preform_buffers(r, rec && x->requires_grad && numrs_hip::cross_entropy_preforms(B),
+                               x->numel(), &pre))
     return rc;
-  if (rec) attach(r, Op::CrossEntropyLabels, {x}, 0, 0.f, {lab});
+  if (int rc = numrs_hip::cross_entropy_loss_impl(
+          ctx, x->data->ptr, nullptr, reinterpret_cast<const int32_t *>(lab->ptr), B, C,
+          r->data->ptr, pre ? pre->ptr : nullptr, pre ? r->grad->buf->ptr : nullptr))
+    return rc;
+  if (pre) r->grad->seed_preset = true;
+  if (rec) attach(r, Op::CrossEntropyLabels, {x}, 0, 0.f, {lab, pre});
   *out = std::move(r);
   return NUMRS_HIP_OK;
 }
@@ -1530,6 +1580,7 @@ int numrs_hip_tensor_set_gradient(numrs_hip_tensor *t, const float *host, int64_
   if (n != x->numel()) return fail(x->ctx, NUMRS_HIP_E_SHAPE, "set_gradient: size mismatch");
   if (!x->grad->buf)
     if (int rc = alloc_buf(x->ctx, n, sizeof(float), &x->grad->buf)) return rc;
+  x->grad->seed_preset = false;
   if (int rc = numrs_hip_upload(x->ctx, x->grad->buf->ptr, host, (size_t)n * sizeof(float))) return rc;
   x->grad->valid = true;
   return NUMRS_HIP_OK;
@@ -1537,7 +1588,10 @@ int numrs_hip_tensor_set_gradient(numrs_hip_tensor *t, const float *host, int64_
 
 int numrs_hip_tensor_zero_grad(numrs_hip_tensor *t) {  // tensor.rs:135-142
   if (t == nullptr) return NUMRS_HIP_E_INVALID;
-  if (t->t->grad) t->t->grad->valid = false;
+  if (t->t->grad) {
+    t->t->grad->valid = false;
+    t->t->grad->seed_preset = false;
+  }
   return NUMRS_HIP_OK;
 }
 

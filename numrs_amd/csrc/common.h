@@ -191,6 +191,18 @@ int gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, BatchedOut 
 // C [K,N]) for z < batch, in one launch where the streamed path fits
 // (attention's dV = P^T dO with dK = alpha dS^T Q).  Either output may be
 // null; accumulate adds into the outputs.
+// The MSE loss (numrs_hip_mse_loss) that, with dp, also writes the gradient
+// its backward forms as the sweep's root (g = 1: dp = (2 (p - t)) / n, the
+// backward kernel's arithmetic) and, with seed, writes 1 there.
+int mse_loss_impl(numrs_hip_ctx *ctx, const float *p, const float *t, int64_t n, float *out,
+                  float *dp, float *seed);
+// The same for the cross-entropy loss (numrs_hip_cross_entropy_loss): dx =
+// (softmax - target) / B, for batches where cross_entropy_preforms(B).
+int cross_entropy_loss_impl(numrs_hip_ctx *ctx, const float *logits, const float *onehot,
+                            const int32_t *labels, int64_t B, int64_t C, float *out, float *dx,
+                            float *seed);
+bool cross_entropy_preforms(int64_t B);
+
 int gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, BatchedOut C1, float alpha1,
                  BatchedMat X2, BatchedMat Y2, BatchedOut C2, float alpha2, int64_t M, int64_t K,
                  int64_t N, int accumulate, int64_t batch, int64_t binner);

@@ -171,10 +171,14 @@ __global__ void __launch_bounds__(kBlock)
 // grid stride (VEC: 16-byte aligned operands), eight loads per operand in
 // flight at once, into four independent partial sums that are added in a
 // fixed order, then across the wave and the block.
+// With dp (KIND 1): dp = ((1 * 2) (x - t)) / n as well, the gradient of the MSE
+// loss's backward when the loss is the root (g = 1), with mse_bwd_kernel's
+// arithmetic.  seed (may be null) receives 1 from a lone block.
 template <int KIND, int VEC>
 __global__ void __launch_bounds__(kBlock)
     reduce_pass1(const float *__restrict__ x, const float *__restrict__ t, int64_t n,
-                 float *__restrict__ partial, float div) {
+                 float *__restrict__ partial, float div, float *__restrict__ dp,
+                 float *__restrict__ seed) {
   __shared__ float red[kBlock / 64];
   auto term = [&](float xv, float tv) {
     if (KIND == 0) return xv;
@@ -188,6 +192,13 @@ __global__ void __launch_bounds__(kBlock)
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const float nf = (float)n;
+    auto grad4 = [&](const f4v &xv, const f4v &tv, int64_t j) {
+      f4v o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = ((1.0f * 2.0f) * (xv[e] - tv[e])) / nf;
+      numrs_hip::stv<VEC>(dp + 4 * j, o);
+    };
     for (; i + 7 * stride < n4; i += 8 * stride) {
       f4v xv[8], tv[8];
 #pragma unroll
@@ -200,6 +211,9 @@ __global__ void __launch_bounds__(kBlock)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           acc[u & 3] += term(xv[u][e], KIND == 1 ? tv[u][e] : 0.0f);
+      if (KIND == 1 && dp != nullptr)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) grad4(xv[u], tv[u], i + u * stride);
     }
     for (; i < n4; i += stride) {
       const f4v xv = numrs_hip::ldv<VEC>(x + 4 * i);
@@ -207,17 +221,22 @@ __global__ void __launch_bounds__(kBlock)
       if (KIND == 1) tv = numrs_hip::ldv<VEC>(t + 4 * i);
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[0] += term(xv[e], tv[e]);
+      if (KIND == 1 && dp != nullptr) grad4(xv, tv, i);
     }
     // The n % 4 tail, taken by the first threads of block 0.
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
       const int64_t k = n4 * 4 + threadIdx.x;
       acc[0] += term(x[k], KIND == 1 ? t[k] : 0.0f);
+      if (KIND == 1 && dp != nullptr) dp[k] = ((1.0f * 2.0f) * (x[k] - t[k])) / nf;
     }
     s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
   } else {
+    const float nf = (float)n;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * kBlock)
+         i += (int64_t)gridDim.x * kBlock) {
       s += term(x[i], KIND == 1 ? t[i] : 0.0f);
+      if (KIND == 1 && dp != nullptr) dp[i] = ((1.0f * 2.0f) * (x[i] - t[i])) / nf;
+    }
   }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -225,13 +244,14 @@ __global__ void __launch_bounds__(kBlock)
   if (threadIdx.x == 0) {
     const float tot = ((red[0] + red[1]) + red[2]) + red[3];
     partial[blockIdx.x] = gridDim.x == 1 ? tot / div : tot;  // a lone block writes the result
+    if (gridDim.x == 1 && seed != nullptr) seed[0] = 1.0f;
   }
 }
 
 // out[0] = (sum of partials) / div   (div = 1 for a plain sum)
 __global__ void __launch_bounds__(kBlock)
     reduce_final(const float *__restrict__ partial, int64_t count, float div,
-                 float *__restrict__ out) {
+                 float *__restrict__ out, float *__restrict__ seed) {
   __shared__ float red[kBlock / 64];
   // Loads go out in batches of 8 before they are added (in index order), so
   // a thread waits for one memory round trip per batch.
@@ -250,7 +270,10 @@ __global__ void __launch_bounds__(kBlock)
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
-  if (threadIdx.x == 0) out[0] = (((red[0] + red[1]) + red[2]) + red[3]) / div;
+  if (threadIdx.x == 0) {
+    out[0] = (((red[0] + red[1]) + red[2]) + red[3]) / div;
+    if (seed != nullptr) seed[0] = 1.0f;
+  }
 }
 
 // Cross-entropy rows (ops.rs:281-318): per row -sum_j t_j * ((x_j - m) - log(sum e)).
@@ -291,7 +314,8 @@ template <bool LABELS>
 __global__ void __launch_bounds__(64 * kCeSmallWaves)
     ce_loss_small_kernel(const float *__restrict__ x, const float *__restrict__ onehot,
                          const int32_t *__restrict__ labels, int64_t B, int64_t C,
-                         float *__restrict__ out) {
+                         float *__restrict__ out, float *__restrict__ dx,
+                         float *__restrict__ seed) {
   __shared__ float red[kCeSmallWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float acc = 0.0f;
@@ -308,6 +332,9 @@ __global__ void __launch_bounds__(64 * kCeSmallWaves)
     for (int64_t j = lane; j < C; j += 64) {
       const float t = LABELS ? (j == (int64_t)labels[row] ? 1.0f : 0.0f) : onehot[row * C + j];
       l += -t * ((xr[j] - m) - ls);
+      // With dx: the gradient this loss's backward forms when it is the root
+      // (g = 1), with softmax_ce_bwd_kernel's arithmetic on the same m and s.
+      if (dx != nullptr) dx[row * C + j] = (expf(xr[j] - m) / s - t) * (1.0f / (float)B);
     }
     acc += wave_sum(l);
   }
@@ -318,6 +345,7 @@ __global__ void __launch_bounds__(64 * kCeSmallWaves)
 #pragma unroll
     for (int w = 1; w < kCeSmallWaves; ++w) t += red[w];
     out[0] = t / (float)B;
+    if (seed != nullptr) seed[0] = 1.0f;
   }
 }
 
@@ -469,7 +497,7 @@ int launch_binary_fwd(numrs_hip_ctx *ctx, const float *a, const int64_t *as, int
 }
 
 int full_reduce(numrs_hip_ctx *ctx, int kind, const float *x, const float *t, int64_t n,
-                float div, float *out) {
+                float div, float *out, float *dp = nullptr, float *seed = nullptr) {
   // One block per CU at most: with more, the partials and the reads spread
   // over more HBM pages (1024 blocks measured 15% slower than 256 at 2^24).
   const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -483,21 +511,69 @@ int full_reduce(numrs_hip_ctx *ctx, int kind, const float *x, const float *t, in
     if (int rc = numrs_hip::workspace(ctx, (size_t)blocks * sizeof(float), &ws)) return rc;
     partial = static_cast<float *>(ws);
   }
-  const bool vec = numrs_hip::aligned16(x) && (kind == 0 || numrs_hip::aligned16(t));
+  const bool vec = numrs_hip::aligned16(x) && (kind == 0 || numrs_hip::aligned16(t)) &&
+                   (dp == nullptr || numrs_hip::aligned16(dp));
   const unsigned grid = (unsigned)blocks;
   numrs_hip::with_vec_mode(numrs_hip::vec_mode(vec, n), [&](auto V) {
     if (kind == 0)
-      reduce_pass1<0, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial, div);
+      reduce_pass1<0, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial, div,
+                                                                            nullptr, seed);
     else
-      reduce_pass1<1, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial, div);
+      reduce_pass1<1, decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(x, t, n, partial, div,
+                                                                            dp, seed);
   });
   if (int rc = numrs_hip::check_launch(ctx, "reduce_pass1")) return rc;
   if (blocks == 1) return NUMRS_HIP_OK;
-  reduce_final<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, div, out);
+  reduce_final<<<1, kBlock, 0, ctx->stream>>>(partial, blocks, div, out, seed);
   return numrs_hip::check_launch(ctx, "reduce_final");
 }
 
 }  // namespace
+
+namespace numrs_hip {
+
+bool cross_entropy_preforms(int64_t B) { return B > 0 && B <= kCeSmallRows; }
+
+int mse_loss_impl(numrs_hip_ctx *ctx, const float *p, const float *t, int64_t n, float *out,
+                  float *dp, float *seed) {
+  NRS_CHECK_CTX(ctx);
+  if (n <= 0 || p == nullptr || t == nullptr || out == nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_loss: bad arguments");
+  return full_reduce(ctx, 1, p, t, n, (float)n, out, dp, seed);
+}
+
+int cross_entropy_loss_impl(numrs_hip_ctx *ctx, const float *logits, const float *onehot,
+                            const int32_t *labels, int64_t B, int64_t C, float *out, float *dx,
+                            float *seed) {
+  NRS_CHECK_CTX(ctx);
+  if (B <= 0 || C <= 0 || logits == nullptr || out == nullptr ||
+      (onehot == nullptr) == (labels == nullptr))
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_cross_entropy_loss: bad arguments");
+  if (B <= kCeSmallRows) {
+    if (labels)
+      ce_loss_small_kernel<true><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(
+          logits, onehot, labels, B, C, out, dx, seed);
+    else
+      ce_loss_small_kernel<false><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(
+          logits, onehot, labels, B, C, out, dx, seed);
+    return numrs_hip::check_launch(ctx, "ce_loss_small_kernel");
+  }
+  if (dx != nullptr || seed != nullptr)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID,
+                           "cross-entropy: the gradient is formed with the loss only for "
+                           "batches of at most %lld rows", (long long)kCeSmallRows);
+  // Row losses live in the scratch region; the reduction below uses the workspace.
+  float *rows = nullptr;
+  if (int rc = numrs_hip::scratch(ctx, (size_t)B * sizeof(float), &rows)) return rc;
+  if (labels)
+    ce_rows_kernel<true><<<grid_for(B, 4), kBlock, 0, ctx->stream>>>(logits, onehot, labels, rows, B, C);
+  else
+    ce_rows_kernel<false><<<grid_for(B, 4), kBlock, 0, ctx->stream>>>(logits, onehot, labels, rows, B, C);
+  if (int rc = numrs_hip::check_launch(ctx, "ce_rows_kernel")) return rc;
+  return full_reduce(ctx, 0, rows, nullptr, B, (float)B, out);
+}
+
+}  // namespace numrs_hip
 
 extern "C" {
 
@@ -585,36 +661,13 @@ int numrs_hip_sum(numrs_hip_ctx *ctx, const float *x, int64_t n, int mean, float
 }
 
 int numrs_hip_mse_loss(numrs_hip_ctx *ctx, const float *p, const float *t, int64_t n, float *out) {
-  NRS_CHECK_CTX(ctx);
-  if (n <= 0 || p == nullptr || t == nullptr || out == nullptr)
-    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_mse_loss: bad arguments");
-  return full_reduce(ctx, 1, p, t, n, (float)n, out);
+  return numrs_hip::mse_loss_impl(ctx, p, t, n, out, nullptr, nullptr);
 }
 
 int numrs_hip_cross_entropy_loss(numrs_hip_ctx *ctx, const float *logits, const float *onehot,
                                  const int32_t *labels, int64_t B, int64_t C, float *out) {
-  NRS_CHECK_CTX(ctx);
-  if (B <= 0 || C <= 0 || logits == nullptr || out == nullptr ||
-      (onehot == nullptr) == (labels == nullptr))
-    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_cross_entropy_loss: bad arguments");
-  if (B <= kCeSmallRows) {
-    if (labels)
-      ce_loss_small_kernel<true><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(logits, onehot,
-                                                                           labels, B, C, out);
-    else
-      ce_loss_small_kernel<false><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(logits, onehot,
-                                                                            labels, B, C, out);
-    return numrs_hip::check_launch(ctx, "ce_loss_small_kernel");
-  }
-  // Row losses live in the scratch region; the reduction below uses the workspace.
-  float *rows = nullptr;
-  if (int rc = numrs_hip::scratch(ctx, (size_t)B * sizeof(float), &rows)) return rc;
-  if (labels)
-    ce_rows_kernel<true><<<grid_for(B, 4), kBlock, 0, ctx->stream>>>(logits, onehot, labels, rows, B, C);
-  else
-    ce_rows_kernel<false><<<grid_for(B, 4), kBlock, 0, ctx->stream>>>(logits, onehot, labels, rows, B, C);
-  if (int rc = numrs_hip::check_launch(ctx, "ce_rows_kernel")) return rc;
-  return full_reduce(ctx, 0, rows, nullptr, B, (float)B, out);
+  return numrs_hip::cross_entropy_loss_impl(ctx, logits, onehot, labels, B, C, out, nullptr,
+                                            nullptr);
 }
 
 int numrs_hip_softmax_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t rows,

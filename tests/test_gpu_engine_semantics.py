@@ -228,3 +228,45 @@ def test_loss_root_seed(hip_ctx, loss_kind, input_grad):
         loss.backward()
         assert loss.gradient().tolist() == [1.0]
         assert_close(xt.gradient(), 2 * first, abs_tol=1e-7, rel_tol=1e-6, what="accumulated")
+
+
+@pytest.mark.parametrize("loss_kind", ["mse", "mse_large", "ce", "ce_labels"])
+def test_preformed_loss_gradient_equals_backward_kernel(hip_ctx, loss_kind):
+    """A scalar loss whose input needs a gradient forms the gradient its
+    backward would form as the root (and the root's seed) in its forward
+    kernel; backward() then adopts it.  It equals the backward kernel's
+    result bit for bit: the same loss reached through a Mul by 1 (so it is no
+    longer the root) runs that kernel with g = 1.  The root's gradient is 1
+    even after set_gradient / zero_grad on it between forward and backward."""
+    print(f"[gpu] pre-formed loss gradient {loss_kind}", flush=True)
+    nr.set_default_context(hip_ctx)
+    rng = np.random.default_rng(11)
+    shape = (4096, 512) if loss_kind == "mse_large" else (64, 10)
+    x = rng.standard_normal(shape).astype(np.float32)
+    t = rng.standard_normal(shape).astype(np.float32)
+    lab = rng.integers(0, shape[1], shape[0])
+    onehot = np.eye(shape[1], dtype=np.float32)[lab]
+
+    def loss_of(xt):
+        if loss_kind.startswith("mse"):
+            return xt.mse_loss(Tensor.new(t, False))
+        if loss_kind == "ce":
+            return xt.cross_entropy_loss(Tensor.new(onehot, False))
+        return xt.cross_entropy_labels(lab)
+
+    xa = Tensor.new(x, True)
+    la = loss_of(xa)
+    la.backward()
+    assert la.gradient().tolist() == [1.0]
+    xb = Tensor.new(x, True)
+    lb = loss_of(xb).mul(Tensor.new(np.ones(1, np.float32), False))
+    lb.backward()
+    assert np.array_equal(xa.gradient(), xb.gradient())
+    # the root's cell written between forward and backward: the seed is still 1
+    xc = Tensor.new(x, True)
+    lc = loss_of(xc)
+    lc.set_gradient(np.array([5.0], np.float32))
+    lc.zero_grad()
+    lc.backward()
+    assert lc.gradient().tolist() == [1.0]
+    assert np.array_equal(xc.gradient(), xa.gradient())
