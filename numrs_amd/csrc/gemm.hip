@@ -1324,8 +1324,11 @@ Gemm as_stream(Gemm g, int shape) {
 // s = 1..32 of either product; each product is cut into ceil(k / T) ranges of
 // equal length (at most 32 ranges, none empty) and the smallest estimate
 // wins, ties going to fewer workgroups.  Product b is absent when tb == 0.
+// A small tile alone on a CU runs a step in 0.9 us since the asm DMA ring
+// (2048 -> 512 forward over 4096 rows, 256 tiles, one per CU: 66.4 us
+// unsplit against 71.8 us split in two and reduced).
 constexpr double kLargeTileUs = 4.22, kLargeFixedUs = 18.0;
-constexpr double kSmallPairUs = 2.3, kSmallAloneUs = 1.4, kSmallFixedUs = 7.0;
+constexpr double kSmallPairUs = 2.3, kSmallAloneUs = 0.9, kSmallFixedUs = 7.0;
 constexpr double kPartialBytesPerUs = 6.0e6;
 
 double stream_wave_us(bool small, int64_t n, int64_t T) {
