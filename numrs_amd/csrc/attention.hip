@@ -47,9 +47,11 @@ constexpr int kHeadDim = 64;       // dh handled by the fused row-block kernel
 // 4g + e of block (bi, bj) is element (query 32bi + c, key 32bj + 8g + 4h +
 // e), so eo^T = E^T Y^T runs as 32x32x2 MFMAs with that register as B and
 // E[key][d] as A, each wave reducing over its own S/4 keys.  A wave stages
-// its keys' rows of E in LDS by DMA at the start ([key][64], the 16-byte
-// chunks of rows whose bit 2 is set XOR-ed by 8 so that the two half-waves'
-// rows fall in different banks); the four wave partials then meet in LDS (rows padded to
+// its keys' rows of E in LDS ([key][64], the 16-byte chunks of rows whose
+// bit 2 is set XOR-ed by 8 so that the two half-waves' rows fall in
+// different banks): the forward for S <= 256 through registers loaded before
+// its first MFMAs, otherwise by DMA at the start.  The four wave partials then
+// meet in LDS (rows padded to
 // 68 floats) and are added in wave order, each thread finishing 16
 // consecutive outputs of one row with float4 loads and stores.
 constexpr int kPartStride = 68;  // floats per row of a wave's [64, 64] partial in LDS
@@ -86,7 +88,17 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   // instruction it writes rows 4 it .. 4 it + 3 of the wave's keys, lane l
   // the 16-byte slot l % 16 of row 4 it + l / 16, which holds chunk
   // (l % 16) ^ 8 of rows whose bit 2 is set.
-  if constexpr (EXTRA) {
+  // The forward for S <= 256 stages through registers instead: its E loads go
+  // out first and are written to LDS after the Q K^T MFMAs (the same layout).
+  constexpr bool kRegStage = EXTRA && MODE == 0 && BJ <= 2;
+  f4 stage[kRegStage ? kStage : 1];
+  if constexpr (kRegStage) {
+    const float *Ez = E + (int64_t)b * S * lde + (int64_t)head * kHeadDim;
+#pragma unroll
+    for (int it = 0; it < kStage; ++it)
+      stage[it] = *reinterpret_cast<const f4 *>(
+          Ez + (int64_t)(col0 + 4 * it + (lane >> 4)) * lde + 4 * (lane & 15));
+  } else if constexpr (EXTRA) {
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const float *Ez = E + ((int64_t)b * S + (int64_t)wave_u * 32 * BJ) * lde +
                       (int64_t)head * kHeadDim;
@@ -164,6 +176,16 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
     }
     __syncthreads();
   };
+
+  if constexpr (kRegStage) {
+    // visible to the wave's reads after the row reductions' barriers below
+#pragma unroll
+    for (int it = 0; it < kStage; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int slot = (lane & 15) ^ (8 * ((kk >> 2) & 1));
+      *reinterpret_cast<f4 *>(wbuf + kk * kHeadDim + 4 * slot) = stage[it];
+    }
+  }
 
   float t[2];
   if constexpr (MODE == 0) {
@@ -246,7 +268,8 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
     // eo^T partial over the wave's keys: block (bd, bi) holds d rows
     // 32bd + 8(i/4) + 4hh + (i%4) of query 32bi + c.  The staged row of key
     // 32bj + 8g + 4hh + e has its chunks XOR-ed by 8 exactly when hh = 1.
-    __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));  // the wave's DMA has landed
+    if constexpr (!kRegStage)
+      __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));  // the wave's DMA has landed
     f16v o[2][2];
 #pragma unroll
     for (int bd = 0; bd < 2; ++bd)
