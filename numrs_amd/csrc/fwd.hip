@@ -92,6 +92,35 @@ __global__ void __launch_bounds__(kBlock)
   if (i < n) y[i] = un<KIND>(x[i], p);
 }
 
+// The same for 16-byte aligned x and y: a thread owns two float4 groups a
+// block-width apart and loads both before computing either (kUnaryPerBlock
+// elements per block); a group past the end is done element by element.
+// Each element's value is the scalar kernel's (x and y may alias).
+constexpr int kUnaryPerBlock = kBlock * 8;
+
+template <int KIND, int VM>
+__global__ void __launch_bounds__(kBlock)
+    unary_fwd_vec(const float *x, float *y, int64_t n, float p) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const int64_t i0 = (int64_t)blockIdx.x * kUnaryPerBlock + 4 * threadIdx.x;
+  const int64_t i1 = i0 + 4 * kBlock;
+  if (i1 + 3 < n) {
+    f4v a = numrs_hip::ldv<VM>(x + i0), b = numrs_hip::ldv<VM>(x + i1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] = un<KIND>(a[e], p);
+      b[e] = un<KIND>(b[e], p);
+    }
+    numrs_hip::stv<VM>(y + i0, a);
+    numrs_hip::stv<VM>(y + i1, b);
+    return;
+  }
+  for (int e = 0; e < 4; ++e) {
+    if (i0 + e < n) y[i0 + e] = un<KIND>(x[i0 + e], p);
+    if (i1 + e < n) y[i1 + e] = un<KIND>(x[i1 + e], p);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Transpose (ops/shape/transpose.rs:9-88): 32x32 LDS tiles, padded rows.
 // ---------------------------------------------------------------------------
@@ -605,8 +634,17 @@ int numrs_hip_unary_forward(numrs_hip_ctx *ctx, int kind, const float *x, float 
   if (n == 0) return NUMRS_HIP_OK;
   if (x == nullptr || y == nullptr)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_unary_forward: null pointer");
-  const unsigned grid = grid_for(n, kBlock);
-#define NRS_UN(K) unary_fwd_kernel<K><<<grid, kBlock, 0, ctx->stream>>>(x, y, n, param); break
+  const bool vec = numrs_hip::aligned16(x) && numrs_hip::aligned16(y);
+  const unsigned grid = grid_for(n, vec ? kUnaryPerBlock : kBlock);
+  const int vm = numrs_hip::vec_mode(true, n);
+#define NRS_UN(K)                                                                              \
+  if (!vec)                                                                                   \
+    unary_fwd_kernel<K><<<grid, kBlock, 0, ctx->stream>>>(x, y, n, param);                     \
+  else if (vm == 2)                                                                           \
+    unary_fwd_vec<K, 2><<<grid, kBlock, 0, ctx->stream>>>(x, y, n, param);                     \
+  else                                                                                        \
+    unary_fwd_vec<K, 1><<<grid, kBlock, 0, ctx->stream>>>(x, y, n, param);                     \
+  break
   switch (kind) {
     case NUMRS_HIP_RELU: NRS_UN(NUMRS_HIP_RELU);
     case NUMRS_HIP_SIGMOID: NRS_UN(NUMRS_HIP_SIGMOID);

@@ -13,6 +13,8 @@ runs on sampled rows for the aggregate bar, and size-independent identities
 """
 import sys
 
+import math
+
 import numpy as np
 import pytest
 
@@ -575,6 +577,44 @@ def test_softmax_ce_backward(hip_ctx, rng, B, C):
     ref = O.cross_entropy_backward(1.0, x, onehot)
     assert_close(d1.numpy(), ref, what="onehot")
     assert_bits(d2.numpy(), d1.numpy(), "labels == onehot")
+
+
+UNARY_FWD_KINDS = [L.RELU, L.SIGMOID, L.TANH, L.EXP, L.LOG, L.GELU, L.SQRT, L.SIN, L.COS, L.TAN,
+                   L.POW]
+
+
+@pytest.mark.parametrize("kind", UNARY_FWD_KINDS)
+@pytest.mark.parametrize("n", [4099, 100003, (1 << 23) + 5])
+def test_unary_forward_vector_equals_scalar(hip_ctx, rng, kind, n):
+    """numrs_hip_unary_forward on 16-byte aligned buffers (float4 groups, the
+    streaming access mode from 2^23 elements, an element-wise tail) gives the
+    same bits as on misaligned ones (the element-per-thread kernel), and both
+    match numpy's float64 value to float32 rounding."""
+    say(f"unary_forward kind {kind} n={n}")
+    x = rng.uniform(-3, 3, n).astype(np.float32)
+    if kind in (L.LOG, L.SQRT, L.POW):
+        x = np.abs(x) + np.float32(0.01)
+    x[:4] = [0.0, -0.0, 1.0, -1.0] if kind not in (L.LOG, L.SQRT, L.POW) else [0.5, 1.0, 2.0, 3.0]
+    c = hip_ctx
+    lib = L.load()
+    xa, ya = c.to_device(x), c.empty((n,))
+    xm_base = c.to_device(np.concatenate([np.zeros(1, np.float32), x]))
+    ym_base = c.empty((n + 1,))
+    xm, ym = xm_base.view(1, (n,)), ym_base.view(1, (n,))
+    p = 1.7
+    assert lib.numrs_hip_unary_forward(c.handle, kind, xa.ptr, ya.ptr, n, p) == 0
+    assert lib.numrs_hip_unary_forward(c.handle, kind, xm.ptr, ym.ptr, n, p) == 0
+    got = ya.numpy()
+    assert_bits(got, ym.numpy(), f"kind {kind}: float4 path vs element path")
+    x64 = x.astype(np.float64)
+    ref = {L.RELU: np.maximum(x64, 0), L.SIGMOID: 1 / (1 + np.exp(-x64)), L.TANH: np.tanh(x64),
+           L.EXP: np.exp(x64), L.LOG: np.log(x64),
+           L.GELU: 0.5 * x64 * (1 + np.vectorize(math.erf)(x64 / math.sqrt(2)))
+           if n < 200000 else None,
+           L.SQRT: np.sqrt(x64), L.SIN: np.sin(x64), L.COS: np.cos(x64), L.TAN: np.tan(x64),
+           L.POW: x64 ** np.float64(np.float32(p))}[kind]
+    if ref is not None:
+        assert_close(got, ref, abs_tol=2e-6, rel_tol=4e-6, what=f"kind {kind} vs float64")
 
 
 LN_CASES = [(1, 1), (7, 5), (33, 64), (130, 1000), (9, 2048), (5, 2047), (1030, 300),
