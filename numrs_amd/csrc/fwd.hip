@@ -39,6 +39,39 @@ __global__ void __launch_bounds__(kBlock)
   out[i] = bin<OP>(a[a_scalar ? 0 : i], b[b_scalar ? 0 : i]);
 }
 
+// The same for 16-byte aligned operands: two float4 groups per thread, a
+// block-width apart, both loaded before either is computed; a scalar operand
+// is read once.  Element values equal binary_flat_kernel's (operands may
+// alias the output).
+template <int OP, int VM>
+__global__ void __launch_bounds__(kBlock)
+    binary_flat_vec(const float *a, const float *b, float *out, int64_t n, int a_scalar,
+                    int b_scalar) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const int64_t i0 = (int64_t)blockIdx.x * kBlock * 8 + 4 * threadIdx.x;
+  const int64_t i1 = i0 + 4 * kBlock;
+  if (i1 + 3 < n) {
+    const float as = a_scalar ? a[0] : 0.0f, bs = b_scalar ? b[0] : 0.0f;
+    const f4v sa = {as, as, as, as}, sb = {bs, bs, bs, bs};
+    const f4v a0 = a_scalar ? sa : numrs_hip::ldv<VM>(a + i0);
+    const f4v a1 = a_scalar ? sa : numrs_hip::ldv<VM>(a + i1);
+    const f4v b0 = b_scalar ? sb : numrs_hip::ldv<VM>(b + i0);
+    const f4v b1 = b_scalar ? sb : numrs_hip::ldv<VM>(b + i1);
+    f4v o0, o1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0[e] = bin<OP>(a0[e], b0[e]);
+      o1[e] = bin<OP>(a1[e], b1[e]);
+    }
+    numrs_hip::stv<VM>(out + i0, o0);
+    numrs_hip::stv<VM>(out + i1, o1);
+    return;
+  }
+  for (int e = 0; e < 4; ++e)
+    for (int64_t i : {i0 + e, i1 + e})
+      if (i < n) out[i] = bin<OP>(a[a_scalar ? 0 : i], b[b_scalar ? 0 : i]);
+}
+
 // [rows, cols] op [cols] (the Linear bias add and its relatives).
 template <int OP>
 __global__ void __launch_bounds__(kBlock)
@@ -500,12 +533,18 @@ int launch_binary_fwd(numrs_hip_ctx *ctx, const float *a, const int64_t *as, int
   }
   if (n == 0) return NUMRS_HIP_OK;
   const unsigned grid = grid_for(n, kBlock);
-  if (an == n && bn == n) {
-    binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, 0, 0);
-  } else if (bn == 1 && an == n) {
-    binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, 0, 1);
-  } else if (an == 1 && bn == n) {
-    binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, 1, 0);
+  const bool flat = (an == n && bn == n) || (bn == 1 && an == n) || (an == 1 && bn == n);
+  if (flat) {
+    const int a_scalar = an == 1 && n != 1, b_scalar = bn == 1 && n != 1;
+    if (numrs_hip::aligned16(a) && numrs_hip::aligned16(b) && numrs_hip::aligned16(out)) {
+      const unsigned vgrid = grid_for(n, kBlock * 8);
+      if (numrs_hip::vec_mode(true, n) == 2)
+        binary_flat_vec<OP, 2><<<vgrid, kBlock, 0, ctx->stream>>>(a, b, out, n, a_scalar, b_scalar);
+      else
+        binary_flat_vec<OP, 1><<<vgrid, kBlock, 0, ctx->stream>>>(a, b, out, n, a_scalar, b_scalar);
+    } else {
+      binary_flat_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n, a_scalar, b_scalar);
+    }
   } else if (an == n && bnd >= 1 && bn == bs[bnd - 1] && bn == bc.shape[nd - 1]) {
     binary_rowbcast_kernel<OP><<<grid, kBlock, 0, ctx->stream>>>(a, b, out, n / bn, bn, 1);
   } else if (bn == n && and_ >= 1 && an == as[and_ - 1] && an == bc.shape[nd - 1]) {

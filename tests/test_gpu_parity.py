@@ -13,6 +13,7 @@ runs on sampled rows for the aggregate bar, and size-independent identities
 """
 import sys
 
+import ctypes
 import math
 
 import numpy as np
@@ -607,14 +608,51 @@ def test_unary_forward_vector_equals_scalar(hip_ctx, rng, kind, n):
     got = ya.numpy()
     assert_bits(got, ym.numpy(), f"kind {kind}: float4 path vs element path")
     x64 = x.astype(np.float64)
-    ref = {L.RELU: np.maximum(x64, 0), L.SIGMOID: 1 / (1 + np.exp(-x64)), L.TANH: np.tanh(x64),
-           L.EXP: np.exp(x64), L.LOG: np.log(x64),
-           L.GELU: 0.5 * x64 * (1 + np.vectorize(math.erf)(x64 / math.sqrt(2)))
-           if n < 200000 else None,
-           L.SQRT: np.sqrt(x64), L.SIN: np.sin(x64), L.COS: np.cos(x64), L.TAN: np.tan(x64),
-           L.POW: x64 ** np.float64(np.float32(p))}[kind]
+    ref = {L.RELU: lambda: np.maximum(x64, 0), L.SIGMOID: lambda: 1 / (1 + np.exp(-x64)),
+           L.TANH: lambda: np.tanh(x64), L.EXP: lambda: np.exp(x64), L.LOG: lambda: np.log(x64),
+           L.GELU: lambda: (0.5 * x64 * (1 + np.vectorize(math.erf)(x64 / math.sqrt(2)))
+                            if n < 200000 else None),
+           L.SQRT: lambda: np.sqrt(x64), L.SIN: lambda: np.sin(x64), L.COS: lambda: np.cos(x64),
+           L.TAN: lambda: np.tan(x64), L.POW: lambda: x64 ** np.float64(np.float32(p))}[kind]()
     if ref is not None:
         assert_close(got, ref, abs_tol=2e-6, rel_tol=4e-6, what=f"kind {kind} vs float64")
+
+
+@pytest.mark.parametrize("kind", [L.ADD, L.SUB, L.MUL, L.DIV])
+@pytest.mark.parametrize("n", [4099, 100003, (1 << 23) + 7])
+@pytest.mark.parametrize("form", ["same", "b_scalar", "a_scalar"])
+def test_binary_forward_vector_equals_scalar(hip_ctx, rng, kind, n, form):
+    """numrs_hip_binary_forward over equal shapes or a one-element operand:
+    16-byte aligned buffers (float4 groups) give the same bits as misaligned
+    views (one element per thread), and both equal numpy's float32 result."""
+    say(f"binary_forward kind {kind} n={n} {form}")
+    a = rng.uniform(-3, 3, n).astype(np.float32)
+    b = (rng.uniform(0.5, 2.0, n) * rng.choice([-1.0, 1.0], n)).astype(np.float32)
+    if form == "b_scalar":
+        b = b[:1].copy()
+    if form == "a_scalar":
+        a = a[:1].copy()
+    c = hip_ctx
+    lib = L.load()
+
+    def run(aligned):
+        def dev(v):
+            if aligned:
+                return c.to_device(v), None
+            base = c.to_device(np.concatenate([np.zeros(1, np.float32), v]))
+            return base.view(1, v.shape), base
+        (ad, _ka), (bd, _kb) = dev(a), dev(b)
+        out_base = c.empty((n + 1,))
+        out = out_base if aligned else out_base.view(1, (n,))
+        ash, bsh = (ctypes.c_int64 * 1)(a.size), (ctypes.c_int64 * 1)(b.size)
+        assert lib.numrs_hip_binary_forward(c.handle, kind, ad.ptr, ash, 1, bd.ptr, bsh, 1,
+                                            out.ptr) == 0
+        return out.numpy()[:n]
+
+    got, ref_scalar = run(True), run(False)
+    assert_bits(got, ref_scalar, f"kind {kind} {form}: float4 path vs element path")
+    want = {L.ADD: np.add, L.SUB: np.subtract, L.MUL: np.multiply, L.DIV: np.divide}[kind](a, b)
+    assert_bits(got, np.broadcast_to(want, (n,)), f"kind {kind} {form}: vs numpy float32")
 
 
 LN_CASES = [(1, 1), (7, 5), (33, 64), (130, 1000), (9, 2048), (5, 2047), (1030, 300),
