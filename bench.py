@@ -854,7 +854,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     # a11 transpose_backward: dX = dY^T (8 B/elem)
     tr_ = Rot(ctx, k, shape=(C, R))
     rs = ns // C
-    record("a11", "transpose_backward", "transpose_kernel", shape, bytes_=8.0 * n,
+    record("a11", "transpose_backward", "transpose_reg_kernel", shape, bytes_=8.0 * n,
            launch=lambda i: ctx._check(L.load().numrs_hip_transpose(ctx.handle, g_[i].ptr,
                                                                       tr_[i].ptr, R, C)),
            cpu_fn=lambda: O.transpose(g[:rs]), cpu_scale=R / rs,

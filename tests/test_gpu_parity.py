@@ -515,10 +515,13 @@ def test_fill_grad_and_mse(hip_ctx, rng):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (64, 64), (68, 132), (4, 4096),
-                                       (4096, 2048), (130, 4), (33, 31)])
+                                       (4096, 2048), (130, 4), (33, 31), (64, 256),
+                                       (68, 260), (196, 1020), (2052, 4)])
 def test_transpose(hip_ctx, rng, rows, cols):
-    """numrs_hip_transpose (ops/shape/transpose.rs:9-88): 64x64 float4 tiles when both
-    dimensions are multiples of 4, 32x32 tiles otherwise; a copy, so bit-exact."""
+    """numrs_hip_transpose (ops/shape/transpose.rs:9-88): the register form (64x256
+    workgroups of 4x4 lane blocks, ragged at both edges in 68x260 and 196x1020) from
+    64x256 up, 128x128 or 64x64 float4 LDS tiles below it when both dimensions are
+    multiples of 4, 32x32 tiles otherwise; a copy, so bit-exact."""
     x = rand(rng, (rows, cols))
     c = hip_ctx
     y, xd = c.empty((cols, rows)), c.to_device(x)  # held for the call: a temporary is freed at once
