@@ -75,8 +75,21 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   __shared__ __attribute__((aligned(1024))) float ebuf[EXTRA ? extra_lds_floats<BJ>() : 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, hh = lane >> 5;
-  const int z = blockIdx.y, b = z / H, head = z - b * H;
-  const int row0 = blockIdx.x * kRowsPerBlock, col0 = wave * 32 * BJ;
+  // gfx950 dispatches workgroup L (x fastest) to XCD L % 8.  The logical
+  // block (row block, head) is permuted so that XCD k owns a contiguous run
+  // of heads with all their row blocks: the blocks of a head, which read the
+  // same S rows of W and E, then share one XCD's L2.
+  int rb = blockIdx.x, z = blockIdx.y;
+  {
+    const int nb = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((nb & 7) == 0) {
+      const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
+      rb = logical % gridDim.x;
+      z = logical / gridDim.x;
+    }
+  }
+  const int b = z / H, head = z - b * H;
+  const int row0 = rb * kRowsPerBlock, col0 = wave * 32 * BJ;
   const float *Xz = X + (int64_t)b * S * ldx + (int64_t)head * kHeadDim;
   const float *Wz = W + (int64_t)b * S * ldw + (int64_t)head * kHeadDim;
   const int64_t zoff = (int64_t)z * S * S;

@@ -939,30 +939,49 @@ __global__ void __launch_bounds__(kThreads, 3) linear_backward_stream_mini(Gemm 
     stream_tile<false, false, kMP, kMQ>(dw, tile - tiles_a, blockIdx.y);
 }
 
+// Maps the hardware workgroup (x fastest, XCD = linear id % 8) to a logical
+// (tile, batch) so that XCD k owns the batch-major logical range
+// [k*nb/8, (k+1)*nb/8): the tiles of one batch entry, which share operand
+// panels, then run on one XCD and share its L2.
+__device__ __forceinline__ void xcd_tile_batch(int &tile, int &batch) {
+  const int nx = gridDim.x, nb = nx * gridDim.y, lin = blockIdx.x + nx * blockIdx.y;
+  if ((nb & 7) != 0) {
+    tile = xcd_tile(blockIdx.x, nx);
+    batch = blockIdx.y;
+    return;
+  }
+  const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
+  tile = logical % nx;
+  batch = logical / nx;
+}
+
 // Two transposed-left products in one launch (attention's dV = P^T dO with
 // dK = alpha dS^T Q): both TN.
 __global__ void __launch_bounds__(kBigThreads, 1) tn_pair_stream(Gemm a, Gemm b, int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  int tile, batch;
+  xcd_tile_batch(tile, batch);
   if (tile < tiles_a)
-    stream_tile<false, false, kSP, kSQ, kBigWaves>(a, tile, blockIdx.y);
+    stream_tile<false, false, kSP, kSQ, kBigWaves>(a, tile, batch);
   else
-    stream_tile<false, false, kSP, kSQ, kBigWaves>(b, tile - tiles_a, blockIdx.y);
+    stream_tile<false, false, kSP, kSQ, kBigWaves>(b, tile - tiles_a, batch);
 }
 
 __global__ void __launch_bounds__(kThreads, 2) tn_pair_stream_small(Gemm a, Gemm b, int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  int tile, batch;
+  xcd_tile_batch(tile, batch);
   if (tile < tiles_a)
-    stream_tile<false, false, kHP, kHQ>(a, tile, blockIdx.y);
+    stream_tile<false, false, kHP, kHQ>(a, tile, batch);
   else
-    stream_tile<false, false, kHP, kHQ>(b, tile - tiles_a, blockIdx.y);
+    stream_tile<false, false, kHP, kHQ>(b, tile - tiles_a, batch);
 }
 
 __global__ void __launch_bounds__(kThreads, 3) tn_pair_stream_mini(Gemm a, Gemm b, int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  int tile, batch;
+  xcd_tile_batch(tile, batch);
   if (tile < tiles_a)
-    stream_tile<false, false, kMP, kMQ>(a, tile, blockIdx.y);
+    stream_tile<false, false, kMP, kMQ>(a, tile, batch);
   else
-    stream_tile<false, false, kMP, kMQ>(b, tile - tiles_a, blockIdx.y);
+    stream_tile<false, false, kMP, kMQ>(b, tile - tiles_a, batch);
 }
 
 int tiles(int64_t n) { return (int)((n + kBP - 1) / kBP); }
