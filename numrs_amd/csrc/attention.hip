@@ -335,6 +335,292 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   }
 }
 
+// Row-block kernel for S <= 256 (BJ = S/128 key blocks of 32 per wave) with
+// EXTRA, the arithmetic of attn_rows_kernel<MODE, BJ, true> in an order that
+// lets the loads overlap the MFMAs:
+//   1. The wave's S/4 rows of W and its 16 of the block's 64 rows of X go to
+//      LDS by DMA; then (MODE 1) the P block and the wave's rows of E are
+//      loaded into registers.  Only the DMA is waited for (vmcnt counts in
+//      issue order), so P and E arrive during the first product.
+//   2. Y = X W^T from LDS: rows at 256 bytes, the 16-byte chunk j of row r
+//      stored at slot j ^ (r % 16), so the lanes reading one chunk of 16
+//      consecutive rows touch 16 different slots.
+//   3. The softmax (MODE 0) or its backward (MODE 1) as in attn_rows_kernel,
+//      the row totals through `red`, which reuses the X rows' space once every
+//      wave is past the product; the rows (P or dS) are stored.
+//   4. E goes from registers into the wave's own W rows (the layout of
+//      attn_rows_kernel's staged E) and eo = E^T-product follows as there,
+//      with the wave partials summed in wave order.
+// Shared memory: four wave slots of S/4 rows of 64 floats and the 64 X rows:
+// 80 KiB at S = 256, two workgroups per CU.
+template <int BJ>
+constexpr int lds_kernel_floats() {
+  return 4 * 32 * BJ * kHeadDim + kRowsPerBlock * kHeadDim > 4 * kRowsPerBlock * kPartStride
+             ? 4 * 32 * BJ * kHeadDim + kRowsPerBlock * kHeadDim
+             : 4 * kRowsPerBlock * kPartStride;
+}
+
+template <int MODE, int BJ>
+__global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
+    const float *__restrict__ X, const float *__restrict__ W, const float *__restrict__ P,
+    float *__restrict__ out, int S, int H, int64_t ldx, int64_t ldw, float alpha,
+    const float *__restrict__ E, int64_t lde, float *eo, int64_t ldo, float ealpha, int eacc) {
+  static_assert(BJ == 1 || BJ == 2, "S <= 256");
+  constexpr int kSlot = 32 * BJ * kHeadDim;  // floats of one wave's key rows
+  constexpr int kXRows = 4 * kSlot;          // offset of the X rows
+  __shared__ __attribute__((aligned(1024))) float lds[lds_kernel_floats<BJ>()];
+  float(*red)[kRowsPerBlock] = reinterpret_cast<float(*)[kRowsPerBlock]>(lds + kXRows);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, hh = lane >> 5;
+  int rb = blockIdx.x, z = blockIdx.y;
+  {
+    // XCD k (hardware ids k, k+8, ...) owns a contiguous run of heads
+    const int nb = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((nb & 7) == 0) {
+      const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
+      rb = logical % gridDim.x;
+      z = logical / gridDim.x;
+    }
+  }
+  const int b = z / H, head = z - b * H;
+  const int row0 = rb * kRowsPerBlock, col0 = wave * 32 * BJ;
+  const int64_t zoff = (int64_t)z * S * S;
+  float *wbuf = lds + wave * kSlot;
+
+  // 1. DMA: instruction it fills rows 4 it .. 4 it + 3 (1 KiB), lane l the
+  // 16-byte slot l % 16 of row 4 it + l / 16 with chunk slot ^ (row % 16).
+  {
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t base = (uint32_t)(uintptr_t)lds;
+    const float *Ww = W + ((int64_t)b * S + (int64_t)wave_u * 32 * BJ) * ldw + (int64_t)head * kHeadDim;
+#pragma unroll
+    for (int it = 0; it < 8 * BJ; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int chunk = (lane & 15) ^ (kk & 15);
+      numrs_hip::lds_dma16(Ww, (uint32_t)(4 * ((int64_t)kk * ldw + 4 * chunk)),
+                           base + 4u * (uint32_t)(wave_u * kSlot) + 1024u * it);
+    }
+    const float *Xw = X + ((int64_t)b * S + row0 + 16 * wave_u) * ldx + (int64_t)head * kHeadDim;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int kk = 4 * it + (lane >> 4);  // row 16 wave + kk of the block; (16 wave + kk) % 16 = kk
+      const int chunk = (lane & 15) ^ kk;
+      numrs_hip::lds_dma16(Xw, (uint32_t)(4 * ((int64_t)kk * ldx + 4 * chunk)),
+                           base + 4u * (uint32_t)(kXRows + wave_u * 16 * kHeadDim) + 1024u * it);
+    }
+  }
+
+  // (MODE 1) the P block, and the wave's E rows, into registers behind the DMA
+  auto col_of = [&](int bj, int i4) { return col0 + 32 * bj + 8 * i4 + 4 * hh; };
+  auto row_ptr = [&](float *base, int bi) { return base + zoff + (int64_t)(row0 + 32 * bi + c) * S; };
+  constexpr int kP = MODE == 1 ? 2 * BJ * 4 : 0;  // register loads of P
+  f4 p[2][MODE == 1 ? BJ : 1][4];
+  if constexpr (MODE == 1) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const float *src = row_ptr(const_cast<float *>(P), bi);
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          p[bi][bj][i4] = *reinterpret_cast<const f4 *>(src + col_of(bj, i4));
+    }
+  }
+  constexpr int kStage = 8 * BJ;
+  f4 stage[kStage];
+  {
+    const float *Ez = E + (int64_t)b * S * lde + (int64_t)head * kHeadDim;
+#pragma unroll
+    for (int it = 0; it < kStage; ++it)
+      stage[it] = *reinterpret_cast<const f4 *>(Ez + (int64_t)(col0 + 4 * it + (lane >> 4)) * lde +
+                                                4 * (lane & 15));
+  }
+  // the kP + kStage register loads above are the newest vector-memory
+  // operations: at most that many outstanding means the DMA has landed
+  __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(kP + kStage));
+  __syncthreads();  // every wave's X rows are in
+
+  // 2. Y^T blocks (bi, bj): rows of X as B, the wave's rows of W as A
+  f16v acc[2][BJ];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = f16v{};
+  const float *xs = lds + kXRows;
+#pragma unroll
+  for (int g = 0; g < kHeadDim / 8; ++g) {
+    const int ch = 2 * g + hh;
+    f4 a[2], w[BJ];
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const int r = 32 * bi + c;
+      a[bi] = *reinterpret_cast<const f4 *>(xs + r * kHeadDim + 4 * (ch ^ (r & 15)));
+    }
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) {
+      const int r = 32 * bj + c;
+      w[bj] = *reinterpret_cast<const f4 *>(wbuf + r * kHeadDim + 4 * (ch ^ (r & 15)));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < BJ; ++bj)
+          acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[bj][j], a[bi][j], acc[bi][bj], 0, 0, 0);
+  }
+
+  // 3. Row totals over the wave's columns (in-lane, then the other half-wave),
+  // then over the four waves: op 0 = max, 1 = sum.
+  __syncthreads();  // every wave is done reading the X rows that `red` reuses
+  auto row_reduce = [&](float (&v)[2], int op) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const float o = __shfl_xor(v[bi], 32, 64);
+      v[bi] = op == 0 ? fmaxf(v[bi], o) : v[bi] + o;
+      if (hh == 0) red[wave][32 * bi + c] = v[bi];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const int r = 32 * bi + c;
+      v[bi] = op == 0 ? fmaxf(fmaxf(red[0][r], red[1][r]), fmaxf(red[2][r], red[3][r]))
+                      : ((red[0][r] + red[1][r]) + red[2][r]) + red[3][r];
+    }
+    __syncthreads();
+  };
+  float t[2];
+  if constexpr (MODE == 0) {
+    // P = softmax_rows(alpha * Y): m = max, e = expf(s - m), P = e * (1/sum e)
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          acc[bi][bj][i] = alpha * acc[bi][bj][i];
+          m = fmaxf(m, acc[bi][bj][i]);
+        }
+      t[bi] = m;
+    }
+    row_reduce(t, 0);
+    float sum[2];
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      float s = 0.0f;
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = expf(acc[bi][bj][i] - t[bi]);
+          acc[bi][bj][i] = e;
+          s += e;
+        }
+      sum[bi] = s;
+    }
+    row_reduce(sum, 1);
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const float inv = 1.0f / sum[bi];
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[bi][bj][i] = acc[bi][bj][i] * inv;
+    }
+  } else {
+    // dS = P * (Y - rowsum(Y * P))
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      float s = 0.0f;
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s += acc[bi][bj][i] * p[bi][bj][i >> 2][i & 3];
+      t[bi] = s;
+    }
+    row_reduce(t, 1);
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          acc[bi][bj][i] = p[bi][bj][i >> 2][i & 3] * (acc[bi][bj][i] - t[bi]);
+  }
+
+  // 4. E into the wave's slot (its W rows are consumed), chunks of rows
+  // whose bit 2 is set XOR-ed by 8; then the rows leave
+#pragma unroll
+  for (int it = 0; it < kStage; ++it) {
+    const int kk = 4 * it + (lane >> 4);
+    const int slot = (lane & 15) ^ (8 * ((kk >> 2) & 1));
+    *reinterpret_cast<f4 *>(wbuf + kk * kHeadDim + 4 * slot) = stage[it];
+  }
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi) {
+    float *dst = row_ptr(out, bi);
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f4 v = {acc[bi][bj][4 * i4], acc[bi][bj][4 * i4 + 1], acc[bi][bj][4 * i4 + 2],
+                      acc[bi][bj][4 * i4 + 3]};
+        *reinterpret_cast<f4 *>(dst + col_of(bj, i4)) = v;
+      }
+  }
+
+  // eo^T partial over the wave's keys, as in attn_rows_kernel
+  f16v o[2][2];
+#pragma unroll
+  for (int bd = 0; bd < 2; ++bd)
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) o[bd][bi] = f16v{};
+#pragma unroll
+  for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float *er = wbuf + (32 * bj + 8 * g + 4 * hh + e) * kHeadDim + c;
+        const float ev[2] = {er[32 * hh], er[32 * (1 - hh)]};
+#pragma unroll
+        for (int bd = 0; bd < 2; ++bd)
+#pragma unroll
+          for (int bi = 0; bi < 2; ++bi)
+            o[bd][bi] = __builtin_amdgcn_mfma_f32_32x32x2f32(ev[bd], acc[bi][bj][4 * g + e], o[bd][bi],
+                                                             0, 0, 0);
+      }
+  __syncthreads();  // every wave is done with its slot
+  float *part = lds + wave * (kRowsPerBlock * kPartStride);
+#pragma unroll
+  for (int bd = 0; bd < 2; ++bd)
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f4 v = {o[bd][bi][4 * i4], o[bd][bi][4 * i4 + 1], o[bd][bi][4 * i4 + 2], o[bd][bi][4 * i4 + 3]};
+        *reinterpret_cast<f4 *>(part + (32 * bi + c) * kPartStride + 32 * bd + 8 * i4 + 4 * hh) = v;
+      }
+  __syncthreads();
+  const int q = threadIdx.x >> 2, d0 = (threadIdx.x & 3) * 16;
+  float *dst = eo + (int64_t)(b * S + row0 + q) * ldo + (int64_t)head * kHeadDim + d0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int off = q * kPartStride + d0 + 4 * j;
+    const f4 s0 = *reinterpret_cast<const f4 *>(lds + off);
+    const f4 s1 = *reinterpret_cast<const f4 *>(lds + kRowsPerBlock * kPartStride + off);
+    const f4 s2 = *reinterpret_cast<const f4 *>(lds + 2 * kRowsPerBlock * kPartStride + off);
+    const f4 s3 = *reinterpret_cast<const f4 *>(lds + 3 * kRowsPerBlock * kPartStride + off);
+    f4 v = ((s0 + s1) + s2) + s3;
+    if constexpr (MODE == 1) {
+      v = ealpha * v;
+      if (eacc) v = *reinterpret_cast<const f4 *>(dst + 4 * j) + v;
+    }
+    *reinterpret_cast<f4 *>(dst + 4 * j) = v;
+  }
+}
+
 // Whether the fused row-block kernel takes this shape: dh = 64, S a multiple
 // of 128 up to 512, rows of both operands at 16-byte strides and 16-byte
 // aligned, 16-byte aligned probability matrices.
@@ -373,6 +659,28 @@ int launch_rows(numrs_hip_ctx *ctx, const float *X, int64_t ldx, const float *W,
   return numrs_hip::check_launch(ctx, "attn_rows_kernel");
 }
 
+// attn_rows_lds_kernel takes S <= 256; its DMA's per-lane byte offsets
+// (rows below 64 of W, below 16 of X) fit 31 bits.
+bool lds_rows_fit(int64_t S, int64_t ldx, int64_t ldw) {
+  return S <= 256 && ldx < (int64_t{1} << 22) && ldw < (int64_t{1} << 22);
+}
+
+template <int MODE>
+int launch_lds_rows(numrs_hip_ctx *ctx, const float *X, int64_t ldx, const float *W, int64_t ldw,
+                    const float *P, float *out, int64_t B, int64_t S, int64_t H, float alpha,
+                    const float *E, int64_t lde, float *eo, int64_t ldo, float ealpha = 1.0f,
+                    int eacc = 0) {
+  const dim3 grid((unsigned)(S / kRowsPerBlock), (unsigned)(B * H));
+  const int s = (int)S, h = (int)H;
+  if (S == 128)
+    attn_rows_lds_kernel<MODE, 1><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha,
+                                                                 E, lde, eo, ldo, ealpha, eacc);
+  else
+    attn_rows_lds_kernel<MODE, 2><<<grid, 256, 0, ctx->stream>>>(X, W, P, out, s, h, ldx, ldw, alpha,
+                                                                 E, lde, eo, ldo, ealpha, eacc);
+  return numrs_hip::check_launch(ctx, "attn_rows_lds_kernel");
+}
+
 int check(numrs_hip_ctx *ctx, int64_t B, int64_t S, int64_t H, int64_t D, int64_t ld_qkv,
           int64_t ld_out) {
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0 || D % H != 0)
@@ -402,6 +710,8 @@ int numrs_hip_attention_forward_strided(numrs_hip_ctx *ctx, const float *q, cons
   const float alpha = 1.0f / sqrtf((float)dh);
   if (rows_fit(S, dh, li, li, q, k, P) && B * H < 65536) {
     // P = softmax_rows(alpha * Q K^T) and O = P V in one kernel
+    if (extra_fit(li, lo, v, out) && lds_rows_fit(S, li, li))
+      return launch_lds_rows<0>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha, v, li, out, lo);
     if (extra_fit(li, lo, v, out))
       return launch_rows<0, true>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha, v, li, out, lo);
     if (int rc = launch_rows<0, false>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha)) return rc;
@@ -447,7 +757,11 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
   if (rows_fit(S, dh, lo, li, dout, v, P) && numrs_hip::aligned16(dS) && B * H < 65536) {
     // dS = P * (dP - rowsum(dP * P)) with dP = dO V^T, and dQ = alpha dS K,
     // in one kernel; then dV and dK = alpha dS^T Q as one pair launch.
-    if (dq && extra_fit(li, li, k, dq)) {
+    if (dq && extra_fit(li, li, k, dq) && lds_rows_fit(S, lo, li)) {
+      if (int rc = launch_lds_rows<1>(ctx, dout, lo, v, li, P, dS, B, S, H, 1.0f, k, li, dq, li,
+                                      alpha, accumulate))
+        return rc;
+    } else if (dq && extra_fit(li, li, k, dq)) {
       if (int rc = launch_rows<1, true>(ctx, dout, lo, v, li, P, dS, B, S, H, 1.0f, k, li, dq, li,
                                         alpha, accumulate))
         return rc;
