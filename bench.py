@@ -1013,12 +1013,13 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
                                                         Hq, Dq))
     dq_, dk_, dv_ = (Rot(ctx, ks, shape=(Bq * Sq, Dq)) for _ in range(3))
     dh = Dq // Hq
-    record("N3", "attention backward (new op)", "attn_rows (dO V^T + softmax bwd) + batched dV, dQ+dK GEMMs",
+    # the engine's call: the backward given the forward's output (row totals dO . O)
+    record("N3", "attention backward (new op)", "attn_bwd_prep + attn_bwd_keys (dV, dK, dQ per key group)",
            "16x256, 8 heads of 64", flops=4 * 2.0 * Bq * Hq * Sq * Sq * dh,
-           launch=lambda i: ctx._check(L.load().numrs_hip_attention_backward(
-               ctx.handle, q_[i].ptr, k_[i].ptr, v_[i].ptr, P_[i].ptr, do_[i].ptr, dq_[i].ptr,
-               dk_[i].ptr, dv_[i].ptr, Bq, Sq, Hq, Dq, 0)),
-           note="four batched products + row softmax backward; no numrs CPU path")
+           launch=lambda i: ctx._check(L.load().numrs_hip_attention_backward_out_strided(
+               ctx.handle, q_[i].ptr, k_[i].ptr, v_[i].ptr, Dq, P_[i].ptr, o_[i].ptr, do_[i].ptr,
+               Dq, dq_[i].ptr, dk_[i].ptr, dv_[i].ptr, Bq, Sq, Hq, Dq, 0)),
+           note="four products per key group, no dS buffer; no numrs CPU path")
     del q_, k_, v_, do_, P_, o_, dq_, dk_, dv_
     return out
 

@@ -300,6 +300,16 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
                                          const float *dout, int64_t ld_out, float *dq, float *dk,
                                          float *dv, int64_t B, int64_t S, int64_t H, int64_t D,
                                          int accumulate);
+/* The backward given also the forward's output out (rows at ld_out, like
+ * dout), from which the softmax backward's row totals come as dO . O.  For
+ * D/H = 64, S = 128 or 256, all three grads non-NULL and accumulate = 0 it
+ * runs one key-block kernel (dV, dK and dQ without a dS buffer; B*H*S floats
+ * of workspace); other calls behave as numrs_hip_attention_backward_strided. */
+int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                             const float *v, int64_t ld_qkv, const float *P,
+                                             const float *out, const float *dout, int64_t ld_out,
+                                             float *dq, float *dk, float *dv, int64_t B, int64_t S,
+                                             int64_t H, int64_t D, int accumulate);
 
 /* LSTM layer (no reference op), gate order i, f, g, o:
  * x [B, T, I], W_ih [4H, I], W_hh [4H, H], b [4H] (NULL = 0), h0/c0 [B, H]

@@ -96,6 +96,8 @@ SIGNATURES = {
     "numrs_hip_attention_forward_strided": (_i, [_vp] * 4 + [_i64, _vp, _vp] + [_i64] * 5),
     "numrs_hip_attention_backward_strided": (_i, [_vp] * 4 + [_i64, _vp, _vp, _i64] + [_vp] * 3 +
                                              [_i64] * 4 + [_i]),
+    "numrs_hip_attention_backward_out_strided": (_i, [_vp] * 4 + [_i64, _vp, _vp, _vp, _i64] +
+                                                 [_vp] * 3 + [_i64] * 4 + [_i]),
     # tensor engine
     "numrs_hip_set_grad_enabled": (None, [_i]),
     "numrs_hip_is_grad_enabled": (_i, []),

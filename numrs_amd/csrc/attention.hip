@@ -621,6 +621,337 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Key-block backward (dh = 64, S = 128 or 256): one workgroup per (head, 128
+// keys) forms dV and dK for its keys over all S queries, and its share of dQ,
+// without storing dS.  The softmax backward's row total needs every key of a
+// row, so it comes from the forward output instead:
+//   rowsum(dP * P) = sum_k P[q,k] (dO[q] . V[k]) = dO[q] . O[q]   (O = P V),
+// 64 products per query, formed in the kernel from the staged dO rows.
+//
+// Wave w owns keys 32w..32w+31 of the group and keeps their V fragments in
+// registers.  For each block of 64 queries (Q and dO rows staged in LDS by
+// DMA, double-buffered; the next block's O rows and P values loaded into
+// registers during this block, the P loads spread over the dV, dK products):
+//   D = dO . O        per query, into LDS, before the block starts,
+//   dP - D            MFMAs from accumulators set to -D, laid out as [query,
+//                     key]: lane (c, h) holds key c and queries 8(i/4) + 4h +
+//                     (i%4) of each 32-query block,
+//   dS = P * (dP - D) in registers,
+//   dV += P^T dO, dK += dS^T Q   with those registers as the B operand (the
+//                     reduction runs over the queries they hold),
+//   dS -> LDS ([query][key], 16-byte chunk j of row q at slot j ^ (q % 32)),
+//   dQ[block] = dS K  wave w forms the 32 x 32 block (query half w/2, d half
+//                     w%2) over the group's 128 keys, K staged in LDS at the
+//                     start ([key][64], chunks of rows with bit 2 set XOR 8).
+// The operands of each product's next step are read from LDS before the
+// current step's MFMAs.  dQ adds alpha * dS K over the S/128 key groups.  At
+// S = 256 the two groups' contributions go to rows zeroed by
+// attn_bwd_zero_kernel through hardware float atomics: 0 + a + b is the same
+// sum in either order, so the result does not depend on which group lands
+// first.  At S = 128 the one group stores.
+// Shared memory: K 32 KiB, two Q/dO tile pairs 64 KiB, dS 32 KiB: one
+// workgroup per CU, four waves.
+constexpr int kKeyGroup = 128;
+constexpr int kKsOff = 0;                              // [128][64] K rows
+constexpr int kTileOff = kKeyGroup * kHeadDim;         // two buffers of Q [64][64], dO [64][64]
+constexpr int kTileFloats = 2 * kRowsPerBlock * kHeadDim;
+constexpr int kDsOff = kTileOff + 2 * kTileFloats;     // [64][128] dS
+constexpr int kDOff = kDsOff + kRowsPerBlock * kKeyGroup;  // the block's 64 row totals
+constexpr int kKeysLds = kDOff + kRowsPerBlock;
+
+// dq's head slices set to 0 (rows of B*S, 64 floats per head, a float4 per
+// thread) before two key groups add into them.
+__global__ void __launch_bounds__(256) attn_bwd_zero_kernel(float *__restrict__ dq, int64_t ldq,
+                                                            int64_t chunks, int chunks_per_row) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t row = i / chunks_per_row;
+  const int ch = (int)(i - row * chunks_per_row);
+  *reinterpret_cast<f4 *>(dq + row * ldq + 4 * ch) = f4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+template <bool ATOMIC>
+__global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
+    const float *Q, const float *K, const float *V, int64_t ldq, const float *P, const float *dO,
+    int64_t ldo, const float *O, float *dq, float *dk, float *dv, int S, int H, float alpha) {
+  // (no __restrict__: the loads must not move across the memory fences below)
+  __shared__ __attribute__((aligned(1024))) float lds[kKeysLds];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, hh = lane >> 5;
+  int kg = blockIdx.x, z = blockIdx.y;
+  {
+    // XCD k (hardware ids k, k+8, ...) owns a contiguous run of heads
+    const int nb = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((nb & 7) == 0) {
+      const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
+      kg = logical % gridDim.x;
+      z = logical / gridDim.x;
+    }
+  }
+  const int b = z / H, head = z - b * H;
+  const int k0 = kg * kKeyGroup, kw = k0 + 32 * wave;  // the group's and the wave's first key
+  const int64_t tok0 = (int64_t)b * S;
+  const float *Qz = Q + tok0 * ldq + head * kHeadDim;
+  const float *Kz = K + tok0 * ldq + head * kHeadDim;
+  const float *Vz = V + tok0 * ldq + head * kHeadDim;
+  const float *dOz = dO + tok0 * ldo + head * kHeadDim;
+  const float *Oz = O + tok0 * ldo + head * kHeadDim;
+  const float *Pz = P + (int64_t)z * S * S;
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+  // K rows 32 wave .. +31 of the group by DMA: instruction it fills rows
+  // 4 it .. 4 it + 3, lane l the 16-byte slot l % 16 of row 4 it + l / 16,
+  // holding chunk slot ^ 8 when the row's bit 2 is set.
+  {
+    const float *src = Kz + (int64_t)(k0 + 32 * wave_u) * ldq;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int chunk = (lane & 15) ^ (8 * ((kk >> 2) & 1));
+      numrs_hip::lds_dma16(src, (uint32_t)(4 * ((int64_t)kk * ldq + 4 * chunk)),
+                           base + 4u * (uint32_t)(kKsOff + 32 * wave_u * kHeadDim) + 1024u * it);
+    }
+  }
+  // Q and dO rows 16 wave .. +15 of query block qb into tile buffer t, chunk
+  // j of tile row r at slot j ^ (r % 16).
+  auto stage_tiles = [&](int qb, int t) {
+    const int r0 = qb * kRowsPerBlock + 16 * wave_u;
+    const float *qs = Qz + (int64_t)r0 * ldq;
+    const float *os = dOz + (int64_t)r0 * ldo;
+    const uint32_t qd = base + 4u * (uint32_t)(kTileOff + t * kTileFloats + 16 * wave_u * kHeadDim);
+    const uint32_t od = qd + 4u * (uint32_t)(kRowsPerBlock * kHeadDim);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int kk = 4 * it + (lane >> 4);  // (16 wave + kk) % 16 = kk
+      const int chunk = (lane & 15) ^ kk;
+      numrs_hip::lds_dma16(qs, (uint32_t)(4 * ((int64_t)kk * ldq + 4 * chunk)), qd + 1024u * it);
+      numrs_hip::lds_dma16(os, (uint32_t)(4 * ((int64_t)kk * ldo + 4 * chunk)), od + 1024u * it);
+    }
+  };
+  // P[q][key kw + c] for the lane's 32 queries of block qb, values
+  // 4n .. 4n + 3 of them (n < 8)
+  auto load_p_part = [&](int qb, float (&pr)[2][16], int n) {
+#pragma unroll
+    for (int m = 4 * n; m < 4 * n + 4; ++m) {
+      const int bi = m >> 4, i = m & 15;
+      const int q = qb * kRowsPerBlock + 32 * bi + 8 * (i >> 2) + 4 * hh + (i & 3);
+      pr[bi][i] = Pz[(int64_t)q * S + kw + c];
+    }
+  };
+  // The softmax backward's row totals D = dO . O for the wave's tile rows
+  // 16 wave + l / 4 of block qb: lane l multiplies 16 of the 64 products
+  // (d = 16 (l % 4) ..), the four lanes of a row add in xor order, and the
+  // first writes D to LDS.  The wave's dO rows are the ones it staged.
+  auto load_o = [&](int qb, f4 (&of)[4]) {
+    const float *src = Oz + (int64_t)(qb * kRowsPerBlock + 16 * wave + (lane >> 2)) * ldo + 16 * (lane & 3);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) of[e] = *reinterpret_cast<const f4 *>(src + 4 * e);
+  };
+  auto row_totals = [&](int t, const f4 (&of)[4]) {
+    const int r = 16 * wave + (lane >> 2);
+    const float *os = lds + kTileOff + t * kTileFloats + kRowsPerBlock * kHeadDim;
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f4 d = *reinterpret_cast<const f4 *>(os + r * kHeadDim + 4 * ((4 * (lane & 3) + e) ^ (r & 15)));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sum += d[u] * of[e][u];
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if ((lane & 3) == 0) lds[kDOff + r] = sum;
+  };
+
+  stage_tiles(0, 0);
+  f4 vr[8];  // V[key kw + c][8g + 4h .. +3]
+#pragma unroll
+  for (int g = 0; g < 8; ++g)
+    vr[g] = *reinterpret_cast<const f4 *>(Vz + (int64_t)(kw + c) * ldq + 8 * g + 4 * hh);
+  float pr[2][16];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) load_p_part(0, pr, n);
+  f4 of[4];
+  load_o(0, of);
+  // Loads stay where they are written: no memory access or instruction moves
+  // across this point (the explicit waits below count on what precedes them).
+  auto pin = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  pin();
+  __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));
+  row_totals(0, of);
+
+  f16v dvacc[2], dkacc[2];
+#pragma unroll
+  for (int dj = 0; dj < 2; ++dj) {
+    dvacc[dj] = f16v{};
+    dkacc[dj] = f16v{};
+  }
+  const int nq = S / kRowsPerBlock;
+  for (int qb = 0; qb < nq; ++qb) {
+    const int t = qb & 1;
+    __syncthreads();  // block qb's tiles (waited for by every wave) are in
+    float prn[2][16];
+    const bool more = qb + 1 < nq;
+    if (more) {
+      stage_tiles(qb + 1, t ^ 1);
+      load_o(qb + 1, of);
+    }
+    pin();  // the prefetch goes out before this block's products (P's in the dV, dK loop)
+    const float *qs = lds + kTileOff + t * kTileFloats;
+    const float *os = qs + kRowsPerBlock * kHeadDim;
+
+    // dP - D = dO V^T - D: the accumulators start at -D of their queries;
+    // A = dO rows (query 32 bi + c), B = the wave's V fragments.  Operands
+    // of step g + 1 are read before step g's MFMAs.
+    f16v acc[2];
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f4 d = *reinterpret_cast<const f4 *>(lds + kDOff + 32 * bi + 8 * g + 4 * hh);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[bi][4 * g + e] = -d[e];
+      }
+    auto read_a = [&](int g, f4 (&a)[2]) {
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi) {
+        const int r = 32 * bi + c;
+        a[bi] = *reinterpret_cast<const f4 *>(os + r * kHeadDim + 4 * ((2 * g + hh) ^ (r & 15)));
+      }
+    };
+    f4 a[2][2];
+    read_a(0, a[0]);
+#pragma unroll
+    for (int g = 0; g < kHeadDim / 8; ++g) {
+      if (g + 1 < kHeadDim / 8) read_a(g + 1, a[(g + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+          acc[bi] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[g & 1][bi][j], vr[g][j], acc[bi], 0, 0, 0);
+    }
+    // dS = P * (dP - D)
+    float ds[2][16];
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ds[bi][i] = pr[bi][i] * acc[bi][i];
+    // dV += P^T dO, dK += dS^T Q: A = dO or Q at [query][32 dj + c], group n
+    // = (bi, g) of four queries; group n + 1's operands are read before group
+    // n's MFMAs.
+    auto read_grp = [&](int n, float (&ao)[4][2], float (&aq)[4][2]) {
+      const int bi = n >> 2, g = n & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 32 * bi + 8 * g + 4 * hh + j;
+#pragma unroll
+        for (int dj = 0; dj < 2; ++dj) {
+          const int col = 4 * (((32 * dj + c) >> 2) ^ (r & 15)) + (c & 3);
+          ao[j][dj] = os[r * kHeadDim + col];
+          aq[j][dj] = qs[r * kHeadDim + col];
+        }
+      }
+    };
+    float ao[2][4][2], aq[2][4][2];
+    read_grp(0, ao[0], aq[0]);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      if (n + 1 < 8) read_grp(n + 1, ao[(n + 1) & 1], aq[(n + 1) & 1]);
+      if (more) load_p_part(qb + 1, prn, n);  // the next block's P, four loads per group
+      pin();
+      const int bi = n >> 2, g = n & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int dj = 0; dj < 2; ++dj) {
+          dvacc[dj] = __builtin_amdgcn_mfma_f32_32x32x2f32(ao[n & 1][j][dj], pr[bi][4 * g + j],
+                                                           dvacc[dj], 0, 0, 0);
+          dkacc[dj] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[n & 1][j][dj], ds[bi][4 * g + j],
+                                                           dkacc[dj], 0, 0, 0);
+        }
+    }
+    // dS -> LDS [query][group key]
+    {
+      const int kc = 32 * wave + c;
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int q = 32 * bi + 8 * (i >> 2) + 4 * hh + (i & 3);
+          lds[kDsOff + q * kKeyGroup + 4 * ((kc >> 2) ^ (q & 31)) + (c & 3)] = ds[bi][i];
+        }
+    }
+    __syncthreads();
+    // dQ block (query half qi, d half di) = dS K over the group's keys; step
+    // g + 1's operands are read before step g's MFMAs
+    const int qi = wave >> 1, di = wave & 1;
+    f16v qacc = f16v{};
+    {
+      const int r = 32 * qi + c;
+      auto read_q = [&](int g, f4 &ad, float (&kv)[4]) {
+        ad = *reinterpret_cast<const f4 *>(lds + kDsOff + r * kKeyGroup + 4 * ((2 * g + hh) ^ (r & 31)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kk = 8 * g + 4 * hh + j;  // (kk >> 2) & 1 == hh
+          kv[j] = lds[kKsOff + kk * kHeadDim + ((32 * di + c) ^ (32 * hh))];
+        }
+      };
+      f4 ad[2];
+      float kv[2][4];
+      read_q(0, ad[0], kv[0]);
+#pragma unroll
+      for (int g = 0; g < kKeyGroup / 8; ++g) {
+        if (g + 1 < kKeyGroup / 8) read_q(g + 1, ad[(g + 1) & 1], kv[(g + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          qacc = __builtin_amdgcn_mfma_f32_32x32x2f32(ad[g & 1][j], kv[g & 1][j], qacc, 0, 0, 0);
+      }
+    }
+    // the next block's tiles and P have landed (and the last block's dQ
+    // writes are done) before this block's dQ leaves
+    pin();
+    __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));
+    if (more) {
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pr[bi][i] = prn[bi][i];
+      // every wave read this block's D at its start, before the dS barrier
+      row_totals(t ^ 1, of);
+    }
+    {
+      float *dst = dq + tok0 * ldq + head * kHeadDim + 32 * di + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int q = qb * kRowsPerBlock + 32 * qi + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if constexpr (ATOMIC)
+          unsafeAtomicAdd(dst + (int64_t)q * ldq, alpha * qacc[i]);
+        else
+          dst[(int64_t)q * ldq] = alpha * qacc[i];
+      }
+    }
+  }
+  // dV and dK rows of the wave's keys: lane (c, h) holds key kw + c at d
+  // = 32 dj + 8 g + 4 h + (0..3)
+#pragma unroll
+  for (int dj = 0; dj < 2; ++dj)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t off = (tok0 + kw + c) * ldq + head * kHeadDim + 32 * dj + 8 * g + 4 * hh;
+      const f4 v = {dvacc[dj][4 * g], dvacc[dj][4 * g + 1], dvacc[dj][4 * g + 2], dvacc[dj][4 * g + 3]};
+      const f4 w = {alpha * dkacc[dj][4 * g], alpha * dkacc[dj][4 * g + 1], alpha * dkacc[dj][4 * g + 2],
+                    alpha * dkacc[dj][4 * g + 3]};
+      *reinterpret_cast<f4 *>(dv + off) = v;
+      *reinterpret_cast<f4 *>(dk + off) = w;
+    }
+}
+
 // Whether the fused row-block kernel takes this shape: dh = 64, S a multiple
 // of 128 up to 512, rows of both operands at 16-byte strides and 16-byte
 // aligned, 16-byte aligned probability matrices.
@@ -788,6 +1119,46 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
   if (int rc = numrs_hip_softmax_backward(ctx, P, dS, dS, Z * S, S, 0)) return rc;
   // dQ_z = alpha * dS_z K_z ;  dK_z = alpha * dS_z^T Q_z  (one launch for both)
   return numrs_hip::gemm_nn_tn_pair(ctx, dSm, Km, dQ, Qm, dK, S, S, dh, alpha, accumulate, Z, H);
+}
+
+// The backward given also the forward's output `out` (rows at ld_out, like
+// dout): for dh = 64, S = 128 or 256 and all three grads written (not
+// accumulated), the key-block kernel; otherwise the row-block path above.
+int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
+                                             const float *v, int64_t ld_qkv, const float *P,
+                                             const float *out, const float *dout, int64_t ld_out,
+                                             float *dq, float *dk, float *dv, int64_t B, int64_t S,
+                                             int64_t H, int64_t D, int accumulate) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check(ctx, B, S, H, D, ld_qkv, ld_out)) return rc;
+  if (!q || !k || !v || !P || !dout || !out)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "attention_backward: null input");
+  const int64_t dh = D / H, li = ld_qkv, lo = ld_out;
+  using numrs_hip::aligned16;
+  const bool keys = dq && dk && dv && !accumulate && dh == kHeadDim && (S == 128 || S == 256) &&
+                    B * H < 65536 && li % 4 == 0 && lo % 4 == 0 && li < (int64_t{1} << 22) &&
+                    lo < (int64_t{1} << 22) && aligned16(q) && aligned16(k) && aligned16(v) &&
+                    aligned16(P) && aligned16(out) && aligned16(dout) && aligned16(dq) &&
+                    aligned16(dk) && aligned16(dv);
+  if (!keys)
+    return numrs_hip_attention_backward_strided(ctx, q, k, v, li, P, dout, lo, dq, dk, dv, B, S, H,
+                                                D, accumulate);
+  const float alpha = 1.0f / sqrtf((float)dh);
+  const bool atomic = S > kKeyGroup;  // two key groups add into dq
+  if (atomic) {
+    const int64_t chunks = B * S * (D / 4);
+    attn_bwd_zero_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ctx->stream>>>(
+        dq, li, chunks, (int)(D / 4));
+    if (int rc = numrs_hip::check_launch(ctx, "attn_bwd_zero_kernel")) return rc;
+  }
+  const dim3 grid((unsigned)(S / kKeyGroup), (unsigned)(B * H));
+  if (atomic)
+    attn_bwd_keys_kernel<true><<<grid, 256, 0, ctx->stream>>>(q, k, v, li, P, dout, lo, out, dq, dk,
+                                                             dv, (int)S, (int)H, alpha);
+  else
+    attn_bwd_keys_kernel<false><<<grid, 256, 0, ctx->stream>>>(q, k, v, li, P, dout, lo, out, dq,
+                                                              dk, dv, (int)S, (int)H, alpha);
+  return numrs_hip::check_launch(ctx, "attn_bwd_keys_kernel");
 }
 
 int numrs_hip_attention_forward(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,

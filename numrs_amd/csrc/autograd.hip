@@ -489,9 +489,10 @@ int bw_attention_packed(const T &out, const float *g, Node &n) {
   float *d;
   int acc;
   if (int rc = grad_target(qkv, &d, &acc)) return rc;
-  return numrs_hip_attention_backward_strided(out->ctx, p, p + D, p + 2 * D, 3 * D,
-                                              n.saved[0]->ptr, g, D, d, d + D, d + 2 * D,
-                                              n.dims[0], n.dims[1], n.dims[2], D, acc);
+  return numrs_hip_attention_backward_out_strided(out->ctx, p, p + D, p + 2 * D, 3 * D,
+                                                  n.saved[0]->ptr, out->data->ptr, g, D, d, d + D,
+                                                  d + 2 * D, n.dims[0], n.dims[1], n.dims[2], D,
+                                                  acc);
 }
 
 int bw_attention(const T &out, const float *g, Node &n) {
@@ -514,9 +515,9 @@ int bw_attention(const T &out, const float *g, Node &n) {
     if (dv && !av) if (int rc = numrs_hip_fill(ctx, dv, v->numel(), 0.0f)) return rc;
   }
   const int64_t D = q->shape[1];
-  if (int rc = numrs_hip_attention_backward(ctx, q->data->ptr, k->data->ptr, v->data->ptr,
-                                            n.saved[0]->ptr, g, dq, dk, dv, n.dims[0], n.dims[1],
-                                            n.dims[2], D, acc))
+  if (int rc = numrs_hip_attention_backward_out_strided(
+          ctx, q->data->ptr, k->data->ptr, v->data->ptr, D, n.saved[0]->ptr, out->data->ptr, g, D,
+          dq, dk, dv, n.dims[0], n.dims[1], n.dims[2], D, acc))
     return rc;
   // Shared grad cells (self-attention on one tensor): the remaining grads add.
   if (k->requires_grad && !dk) {

@@ -91,6 +91,51 @@ def test_attention_strided_packed_qkv(hip_ctx, B, S, H, D, acc):
     assert_contraction(dqkv.numpy(), ref, S + dh, what="dqkv (packed)")
 
 
+@pytest.mark.parametrize("B,S,H,D", [(16, 256, 8, 512), (3, 256, 8, 512), (2, 128, 2, 128),
+                                     (1, 384, 1, 64), (2, 40, 4, 64)])
+@pytest.mark.parametrize("acc", [0, 1])
+def test_attention_backward_with_output(hip_ctx, B, S, H, D, acc):
+    """numrs_hip_attention_backward_out_strided on the packed [B*S, 3D] layout:
+    given the forward's output, dh = 64 with S = 256 (two key groups adding into
+    dq) or S = 128 (one) runs the key-block kernel when nothing accumulates;
+    S = 384, S = 40 and acc = 1 take the row-block or GEMM path.  Each grad
+    against float64, and a second call returns the same bits (dq's two key
+    groups meet in either order)."""
+    from numrs_amd import _lib as L
+    print(f"[gpu] attention backward with output B={B} S={S} H={H} D={D} acc={acc}",
+          flush=True)
+    rng = np.random.default_rng(7 * B + S + acc)
+    qkv, dO, prev = rand(rng, (B * S, 3 * D)), rand(rng, (B * S, D)), rand(rng, (B * S, 3 * D))
+    c = hip_ctx
+    qd, gd = c.to_device(qkv), c.to_device(dO)
+    P, out = c.empty((B * H, S, S)), c.empty((B * S, D))
+    f4 = 4
+    lib = L.load()
+    assert lib.numrs_hip_attention_forward_strided(
+        c.handle, qd.ptr, qd.ptr + D * f4, qd.ptr + 2 * D * f4, 3 * D, P.ptr, out.ptr, D,
+        B, S, H, D) == 0
+    q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    Pr, Q, K, V = _mha_ref(q, k, v, B, S, H)
+    dh = D // H
+    dA = TO._heads(dO.astype(np.float64), B, S, H)
+    dP = dA @ V.transpose(0, 1, 3, 2)
+    dS = Pr * (dP - (dP * Pr).sum(-1, keepdims=True)) / math.sqrt(dh)
+    ref = np.concatenate([TO._merge(dS @ K, B, S), TO._merge(dS.transpose(0, 1, 3, 2) @ Q, B, S),
+                          TO._merge(Pr.transpose(0, 1, 3, 2) @ dA, B, S)], axis=1)
+    if acc:
+        ref = ref + prev.astype(np.float64)
+    got = []
+    for _ in range(2):
+        dqkv = c.to_device(prev) if acc else c.to_device(np.full((B * S, 3 * D), np.nan, np.float32))
+        assert lib.numrs_hip_attention_backward_out_strided(
+            c.handle, qd.ptr, qd.ptr + D * f4, qd.ptr + 2 * D * f4, 3 * D, P.ptr, out.ptr, gd.ptr,
+            D, dqkv.ptr, dqkv.ptr + D * f4, dqkv.ptr + 2 * D * f4, B, S, H, D, acc) == 0
+        got.append(dqkv.numpy())
+    for what, sl in (("dq", slice(0, D)), ("dk", slice(D, 2 * D)), ("dv", slice(2 * D, 3 * D))):
+        assert_contraction(got[0][:, sl], ref[:, sl], S + dh, what=f"{what} (with output)")
+    assert np.array_equal(got[0], got[1]), "two calls differ"
+
+
 def L_attention_fwd(c, q, k, v, P, out, B, S, H, D):
     from numrs_amd import _lib as L
     return L.load().numrs_hip_attention_forward(c.handle, q.ptr, k.ptr, v.ptr, P.ptr, out.ptr,
