@@ -660,15 +660,10 @@ constexpr int kDsOff = kTileOff + 2 * kTileFloats;     // [64][128] dS
 constexpr int kDOff = kDsOff + kRowsPerBlock * kKeyGroup;  // the block's 64 row totals
 constexpr int kKeysLds = kDOff + kRowsPerBlock;
 
-// dq's head slices set to 0 (rows of B*S, 64 floats per head, a float4 per
-// thread) before two key groups add into them.
-__global__ void __launch_bounds__(256) attn_bwd_zero_kernel(float *__restrict__ dq, int64_t ldq,
-                                                            int64_t chunks, int chunks_per_row) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= chunks) return;
-  const int64_t row = i / chunks_per_row;
-  const int ch = (int)(i - row * chunks_per_row);
-  *reinterpret_cast<f4 *>(dq + row * ldq + 4 * ch) = f4{0.0f, 0.0f, 0.0f, 0.0f};
+// dq's rows set to 0 before two key groups add into them: workgroup r
+// clears row r, a float4 per thread (blockDim = D / 4).
+__global__ void __launch_bounds__(1024) attn_bwd_zero_kernel(float *__restrict__ dq, int64_t ldq) {
+  *reinterpret_cast<f4 *>(dq + (int64_t)blockIdx.x * ldq + 4 * threadIdx.x) = f4{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
 template <bool ATOMIC>
@@ -1136,7 +1131,7 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
   const int64_t dh = D / H, li = ld_qkv, lo = ld_out;
   using numrs_hip::aligned16;
   const bool keys = dq && dk && dv && !accumulate && dh == kHeadDim && (S == 128 || S == 256) &&
-                    B * H < 65536 && li % 4 == 0 && lo % 4 == 0 && li < (int64_t{1} << 22) &&
+                    B * H < 65536 && D <= 4096 && li % 4 == 0 && lo % 4 == 0 && li < (int64_t{1} << 22) &&
                     lo < (int64_t{1} << 22) && aligned16(q) && aligned16(k) && aligned16(v) &&
                     aligned16(P) && aligned16(out) && aligned16(dout) && aligned16(dq) &&
                     aligned16(dk) && aligned16(dv);
@@ -1146,9 +1141,8 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
   const float alpha = 1.0f / sqrtf((float)dh);
   const bool atomic = S > kKeyGroup;  // two key groups add into dq
   if (atomic) {
-    const int64_t chunks = B * S * (D / 4);
-    attn_bwd_zero_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ctx->stream>>>(
-        dq, li, chunks, (int)(D / 4));
+    // B S < 2^24 rows (B H < 65536, S <= 256), D / 4 <= 1024 threads
+    attn_bwd_zero_kernel<<<(unsigned)(B * S), (unsigned)(D / 4), 0, ctx->stream>>>(dq, li);
     if (int rc = numrs_hip::check_launch(ctx, "attn_bwd_zero_kernel")) return rc;
   }
   const dim3 grid((unsigned)(S / kKeyGroup), (unsigned)(B * H));
