@@ -660,10 +660,13 @@ constexpr int kDsOff = kTileOff + 2 * kTileFloats;     // [64][128] dS
 constexpr int kDOff = kDsOff + kRowsPerBlock * kKeyGroup;  // the block's 64 row totals
 constexpr int kKeysLds = kDOff + kRowsPerBlock;
 
-// dq's rows set to 0 before two key groups add into them: workgroup r
-// clears row r, a float4 per thread (blockDim = D / 4).
+// dq's rows set to 0 before two key groups add into them: workgroup w
+// clears rows 16 w .. 16 w + 15 (B S is a multiple of 16), a float4 per
+// thread and row (blockDim = D / 4).
 __global__ void __launch_bounds__(1024) attn_bwd_zero_kernel(float *__restrict__ dq, int64_t ldq) {
-  *reinterpret_cast<f4 *>(dq + (int64_t)blockIdx.x * ldq + 4 * threadIdx.x) = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float *row = dq + (int64_t)blockIdx.x * 16 * ldq + 4 * threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) *reinterpret_cast<f4 *>(row + r * ldq) = f4{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
 template <bool ATOMIC>
@@ -1142,7 +1145,7 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
   const bool atomic = S > kKeyGroup;  // two key groups add into dq
   if (atomic) {
     // B S < 2^24 rows (B H < 65536, S <= 256), D / 4 <= 1024 threads
-    attn_bwd_zero_kernel<<<(unsigned)(B * S), (unsigned)(D / 4), 0, ctx->stream>>>(dq, li);
+    attn_bwd_zero_kernel<<<(unsigned)(B * S / 16), (unsigned)(D / 4), 0, ctx->stream>>>(dq, li);
     if (int rc = numrs_hip::check_launch(ctx, "attn_bwd_zero_kernel")) return rc;
   }
   const dim3 grid((unsigned)(S / kKeyGroup), (unsigned)(B * H));
