@@ -1014,7 +1014,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     dq_, dk_, dv_ = (Rot(ctx, ks, shape=(Bq * Sq, Dq)) for _ in range(3))
     dh = Dq // Hq
     # the engine's call: the backward given the forward's output (row totals dO . O)
-    record("N3", "attention backward (new op)", "attn_bwd_prep + attn_bwd_keys (dV, dK, dQ per key group)",
+    record("N3", "attention backward (new op)", "attn_bwd_zero + attn_bwd_keys (dV, dK, dQ per key group)",
            "16x256, 8 heads of 64", flops=4 * 2.0 * Bq * Hq * Sq * Sq * dh,
            launch=lambda i: ctx._check(L.load().numrs_hip_attention_backward_out_strided(
                ctx.handle, q_[i].ptr, k_[i].ptr, v_[i].ptr, Dq, P_[i].ptr, o_[i].ptr, do_[i].ptr,
