@@ -541,8 +541,8 @@ __global__ void __launch_bounds__(kBlock)
     }
   };
   // The wave walks rows band*4 + wave for bands b, b + Q, b + 2Q, ...
-  // (Q = gridDim.x).  The next row's loads, its statistics included, are
-  // issued before the current row is processed (register double buffering):
+  // (Q = gridDim.x).  The next rows' loads, their statistics included, are
+  // issued before the current row is processed (a ring of register sets):
   // the memory counter retires loads in issue order, so a statistic loaded
   // after the prefetch would make the wave wait for the prefetch as well.
   const int64_t q = gridDim.x;
@@ -561,28 +561,39 @@ __global__ void __launch_bounds__(kBlock)
     mu = mean[r];
     rs = rstd[r];
   };
-  // Two register sets alternate (no copies: a copy out of a set with loads
-  // in flight would wait for them).  The prefetch is unconditional -- past
-  // the end it re-reads the current row -- so the wait before a row only
-  // covers that row's own loads.
+  // kDepth register sets form a ring (no copies: a copy out of a set with
+  // loads in flight would wait for them): while a row is processed, the
+  // next kDepth - 1 rows' loads are in flight.  A prefetch past the end
+  // re-reads the row being processed, so the wait before a row only covers
+  // that row's own loads.
+  constexpr int kDepth = 3;
   int64_t r = (int64_t)blockIdx.x * 4 + wave;
   const int64_t step = 4 * q;
   if (r < rows) {
-    f4 xa[NV], ga[NV], xb[NV], gb[NV];
-    float mua, rsa, mub, rsb;
-    load(r, xa, ga, mua, rsa);
+    f4 xs[kDepth][NV], gs[kDepth][NV];
+    float mus[kDepth], rss[kDepth];
+#pragma unroll
+    for (int k = 0; k + 1 < kDepth; ++k) {
+      const int64_t rk = r + k * step;
+      load(rk < rows ? rk : r, xs[k], gs[k], mus[k], rss[k]);
+    }
     while (true) {
-      const int64_t r1 = r + step;
-      load(r1 < rows ? r1 : r, xb, gb, mub, rsb);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the row's work
-      row(r, xa, ga, mua, rsa);
-      if (r1 >= rows) break;
-      const int64_t r2 = r1 + step;
-      load(r2 < rows ? r2 : r1, xa, ga, mua, rsa);
-      __builtin_amdgcn_sched_barrier(0);
-      row(r1, xb, gb, mub, rsb);
-      if (r2 >= rows) break;
-      r = r2;
+      bool done = false;
+#pragma unroll
+      for (int k = 0; k < kDepth; ++k) {
+        const int64_t rk = r + k * step;           // processed now, from set k
+        const int64_t rl = rk + (kDepth - 1) * step;  // loaded now into set k - 1
+        const int kl = (k + kDepth - 1) % kDepth;
+        load(rl < rows ? rl : rk, xs[kl], gs[kl], mus[kl], rss[kl]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the row's work
+        row(rk, xs[k], gs[k], mus[k], rss[k]);
+        if (rk + step >= rows) {
+          done = true;
+          break;
+        }
+      }
+      if (done) break;
+      r += kDepth * step;
     }
   }
   if (!want_params) return;
