@@ -336,7 +336,7 @@ __global__ void __launch_bounds__(kBlock)
 
 // SGD::step, optim/sgd.rs:87-124 (+ apply_weight_decay, optim/base.rs:26-36).
 // One block's kElemsPerBlock elements starting at blk * kElemsPerBlock (shared
-// by sgd_kernel and, for tensors in streaming mode, sgd_multi_kernel).
+// by sgd_kernel and, for 16-byte aligned tensors, sgd_multi_kernel).
 template <bool MOMENTUM, bool DECAY, int VEC>
 __device__ __forceinline__ void sgd_block(float *__restrict__ p, const float *__restrict__ g,
                                           float *__restrict__ v, int64_t n, float lr, float mu,
@@ -434,7 +434,7 @@ __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
 
 // Adam::step, optim/adam.rs:124-167, fused into one pass over p, g, m, v.
 // One block's kElemsPerBlock elements starting at blk * kElemsPerBlock (shared
-// by adam_kernel and, for tensors in streaming mode, adam_multi_kernel).
+// by adam_kernel and, for 16-byte aligned tensors, adam_multi_kernel).
 template <bool DECAY, int VEC>
 __device__ __forceinline__ void adam_block(float *__restrict__ p, const float *__restrict__ g,
                                            float *__restrict__ m, float *__restrict__ v,
@@ -551,6 +551,10 @@ __global__ void __launch_bounds__(kBlock)
     sgd_block<MOMENTUM, DECAY, 2>(p, g, v, n, lr, mu, wd, blockIdx.x - a.start[t]);
     return;
   }
+  if (a.mode[t] == 1) {  // aligned: the same body with cached float4 accesses
+    sgd_block<MOMENTUM, DECAY, 1>(p, g, v, n, lr, mu, wd, blockIdx.x - a.start[t]);
+    return;
+  }
   const int64_t base = (int64_t)(blockIdx.x - a.start[t]) * kElemsPerBlock + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < 4 * kVecPerThread; ++u) {
@@ -574,6 +578,10 @@ __global__ void __launch_bounds__(kBlock) adam_multi_kernel(MultiArgs a, AdamArg
   const int64_t n = a.n[t];
   if (a.mode[t] == 2) {  // a large tensor: the single-tensor kernel's float4 streaming body
     adam_block<DECAY, 2>(a.p[t], a.g[t], a.s1[t], a.s2[t], n, args, blockIdx.x - a.start[t]);
+    return;
+  }
+  if (a.mode[t] == 1) {  // aligned: the same body with cached float4 accesses
+    adam_block<DECAY, 1>(a.p[t], a.g[t], a.s1[t], a.s2[t], n, args, blockIdx.x - a.start[t]);
     return;
   }
   const int64_t base = (int64_t)(blockIdx.x - a.start[t]) * kElemsPerBlock + threadIdx.x;
