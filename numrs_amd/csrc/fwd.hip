@@ -415,7 +415,12 @@ __global__ void __launch_bounds__(kBlock)
 constexpr int kCeSmallWaves = 16;
 constexpr int64_t kCeSmallRows = 512;
 
-template <bool LABELS>
+// RPW > 0 (rows of at most 64 classes, at most RPW rows per wave): every row
+// of the wave, with its targets, is loaded into registers before the first is
+// reduced (one memory round trip instead of one per row); lane j holds
+// column j, and the per-lane values are formed exactly as the loop below
+// forms them, so the sums and outputs are the same bits.
+template <bool LABELS, int RPW>
 __global__ void __launch_bounds__(64 * kCeSmallWaves)
     ce_loss_small_kernel(const float *__restrict__ x, const float *__restrict__ onehot,
                          const int32_t *__restrict__ labels, int64_t B, int64_t C,
@@ -424,6 +429,35 @@ __global__ void __launch_bounds__(64 * kCeSmallWaves)
   __shared__ float red[kCeSmallWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float acc = 0.0f;
+  if constexpr (RPW > 0) {
+    const bool in = lane < C;
+    const int64_t j = in ? lane : 0;  // lanes past the row read column 0 and discard it
+    float xv[RPW], tv[RPW];
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+      int64_t row = wave + (int64_t)k * kCeSmallWaves;
+      if (row > B - 1) row = B - 1;  // loaded, not used
+      xv[k] = x[row * C + j];
+      tv[k] = LABELS ? (j == (int64_t)labels[row] ? 1.0f : 0.0f) : onehot[row * C + j];
+    }
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+      const int64_t row = wave + (int64_t)k * kCeSmallWaves;
+      if (row >= B) break;
+      float m = in ? fmaxf(-INFINITY, xv[k]) : -INFINITY;
+      m = wave_max(m);
+      float s = in ? 0.0f + expf(xv[k] - m) : 0.0f;
+      s = wave_sum(s);
+      const float ls = logf(s);
+      float l = 0.0f;
+      if (in) {
+        const float t = tv[k];
+        l += -t * ((xv[k] - m) - ls);
+        if (dx != nullptr) dx[row * C + j] = (expf(xv[k] - m) / s - t) * (1.0f / (float)B);
+      }
+      acc += wave_sum(l);
+    }
+  } else
   for (int64_t row = wave; row < B; row += kCeSmallWaves) {
     const float *xr = x + row * C;
     float m = -INFINITY;
@@ -661,12 +695,27 @@ int cross_entropy_loss_impl(numrs_hip_ctx *ctx, const float *logits, const float
       (onehot == nullptr) == (labels == nullptr))
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_cross_entropy_loss: bad arguments");
   if (B <= kCeSmallRows) {
-    if (labels)
-      ce_loss_small_kernel<true><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(
-          logits, onehot, labels, B, C, out, dx, seed);
-    else
-      ce_loss_small_kernel<false><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(
-          logits, onehot, labels, B, C, out, dx, seed);
+    // rows per wave for the register path (rows of at most 64 classes)
+    const int64_t rpw = (B + kCeSmallWaves - 1) / kCeSmallWaves;
+    const int tier = C > 64 ? 0 : rpw <= 4 ? 4 : rpw <= 8 ? 8 : rpw <= 16 ? 16 : 32;
+#define NRS_CE(L, R)                                                                \
+  ce_loss_small_kernel<L, R><<<1, 64 * kCeSmallWaves, 0, ctx->stream>>>(logits, onehot, \
+                                                                        labels, B, C, out, dx, seed)
+#define NRS_CE_TIER(L)                  \
+  switch (tier) {                       \
+    case 4: NRS_CE(L, 4); break;        \
+    case 8: NRS_CE(L, 8); break;        \
+    case 16: NRS_CE(L, 16); break;      \
+    case 32: NRS_CE(L, 32); break;      \
+    default: NRS_CE(L, 0); break;       \
+  }
+    if (labels) {
+      NRS_CE_TIER(true)
+    } else {
+      NRS_CE_TIER(false)
+    }
+#undef NRS_CE_TIER
+#undef NRS_CE
     return numrs_hip::check_launch(ctx, "ce_loss_small_kernel");
   }
   if (dx != nullptr || seed != nullptr)
