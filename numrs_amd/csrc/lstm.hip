@@ -378,10 +378,33 @@ __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, 
     }
   };
   const int64_t wr = (int64_t)((r >> 2) * H + j0 + (r & 3));  // W row n(c) of column r
-  if (t > 0 || s.h0 != nullptr)
-    reduce(t > 0 ? s.h_seq + ((int64_t)b * T + t - 1) * H : s.h0 + (int64_t)b * H,
-           s.whh + wr * H, H);
-  if (s.xin != nullptr) reduce(s.xin + ((int64_t)b * T + t) * s.I, s.wih + wr * s.I, s.I);
+  const bool has_h = t > 0 || s.h0 != nullptr;
+  const float *hrow = t > 0 ? s.h_seq + ((int64_t)b * T + t - 1) * H
+                            : (s.h0 != nullptr ? s.h0 + (int64_t)b * H : nullptr);
+  if (has_h && s.xin != nullptr && H == 256 && s.I == 256) {
+    // a stacked layer at H = I = 256 (one 64-long block per wave and operand
+    // pair): both pairs' operands are loaded before either's MFMAs, one
+    // memory round trip instead of two; the MFMAs run in the order above
+    const float *xrow = s.xin + ((int64_t)b * T + t) * s.I;
+    const int kb = wave * 64;
+    f4 a[2][4], w[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[0][i] = *reinterpret_cast<const f4 *>(hrow + kb + 16 * i + 4 * q);
+      w[0][i] = *reinterpret_cast<const f4 *>(s.whh + wr * H + kb + 16 * i + 4 * q);
+      a[1][i] = *reinterpret_cast<const f4 *>(xrow + kb + 16 * i + 4 * q);
+      w[1][i] = *reinterpret_cast<const f4 *>(s.wih + wr * s.I + kb + 16 * i + 4 * q);
+    }
+#pragma unroll
+    for (int pq = 0; pq < 2; ++pq)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[pq][e >> 2][e & 3], w[pq][e >> 2][e & 3], acc,
+                                                   0, 0, 0);
+  } else {
+    if (has_h) reduce(hrow, s.whh + wr * H, H);
+    if (s.xin != nullptr) reduce(s.xin + ((int64_t)b * T + t) * s.I, s.wih + wr * s.I, s.I);
+  }
 #pragma unroll
   for (int v = 0; v < 4; ++v) part[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
   __syncthreads();
