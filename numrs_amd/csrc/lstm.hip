@@ -742,6 +742,50 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Row forms of shift_hidden and time_slice_kernel for 16-byte aligned
+// arrays whose rows are a whole number of float4s: workgroup r copies row r
+// (r = b T + t) with float4 accesses, and the only index arithmetic per
+// thread is one 32-bit division (the element kernels above take two or three
+// 64-bit divisions per element).
+__global__ void __launch_bounds__(64)
+    shift_hidden_rows(const float *__restrict__ h_seq, const float *__restrict__ h0,
+                      float *__restrict__ out, int T, int H) {
+  const int64_t r = blockIdx.x;
+  const int b = (int)(r / T), t = (int)(r - (int64_t)b * T);
+  const float *src = t > 0 ? h_seq + (r - 1) * H : (h0 != nullptr ? h0 + (int64_t)b * H : nullptr);
+  for (int c = 4 * threadIdx.x; c < H; c += 4 * 64) {
+    const f4 v = src != nullptr ? *reinterpret_cast<const f4 *>(src + c) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    *reinterpret_cast<f4 *>(out + r * H + c) = v;
+  }
+}
+
+// forward: y[b, :] = x[b, t, :] (blockIdx.x = b); backward: row r = b T + tt of
+// dx [B, T, D] is g[b, :] at tt = t and 0 elsewhere (added to, or only step t
+// touched, with acc).
+__global__ void __launch_bounds__(64)
+    time_slice_rows(const float *__restrict__ x, float *__restrict__ y, int T, int D, int t,
+                    int backward, int acc) {
+  const int64_t r = blockIdx.x;
+  if (!backward) {
+    for (int c = 4 * threadIdx.x; c < D; c += 4 * 64)
+      *reinterpret_cast<f4 *>(y + r * D + c) =
+          *reinterpret_cast<const f4 *>(x + (r * T + t) * D + c);
+    return;
+  }
+  const int b = (int)(r / T), tt = (int)(r - (int64_t)b * T);
+  if (acc && tt != t) return;
+  for (int c = 4 * threadIdx.x; c < D; c += 4 * 64) {
+    const f4 v = tt == t ? *reinterpret_cast<const f4 *>(x + (int64_t)b * D + c)
+                         : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 *dst = reinterpret_cast<f4 *>(y + r * D + c);
+    if (acc) {
+      *dst = *dst + v;
+    } else {
+      *dst = v;
+    }
+  }
+}
+
 // One layer's parameter and input gradients from its gate gradients dG
 // [B*T, 4H] of every step, batched over time as single products:
 // dW_ih = dG^T x, dW_hh = dG^T H_prev, db = column sum of dG, dx = dG W_ih
@@ -758,8 +802,13 @@ int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const 
   if (dw_hh) {  // dW_hh[4H, H] = dG^T H_prev
     TempBlock hp(ctx);
     if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
-    shift_hidden<<<grid_for(rows * H, 256), 256, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)B,
-                                                                   (int)T, (int)H);
+    if (H % 4 == 0 && numrs_hip::aligned16(h_seq) && numrs_hip::aligned16(hp.f()) &&
+        (h0 == nullptr || numrs_hip::aligned16(h0)) && rows <= 0x7fffffff) {
+      shift_hidden_rows<<<(unsigned)rows, 64, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)T, (int)H);
+    } else {
+      shift_hidden<<<grid_for(rows * H, 256), 256, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)B,
+                                                                     (int)T, (int)H);
+    }
     if (int rc = numrs_hip::check_launch(ctx, "shift_hidden")) return rc;
     if (int rc = numrs_hip_gemm(ctx, dG, H4, hp.f(), H, dw_hh, H, H4, rows, H, 1, 0, 1.0f,
                                 acc_dw_hh, 1, 1, 0, 0, 0, 0, 0, 0))
@@ -996,6 +1045,13 @@ int numrs_hip_time_slice(numrs_hip_ctx *ctx, const float *x, float *y, int64_t B
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "time_slice: bad arguments");
   const int64_t n = backward ? B * T * D : B * D;
   if (n == 0) return NUMRS_HIP_OK;
+  const int64_t nrows = backward ? B * T : B;
+  if (D % 4 == 0 && numrs_hip::aligned16(x) && numrs_hip::aligned16(y) && nrows <= 0x7fffffff &&
+      T <= 0x7fffffff && D <= 0x7fffffff) {
+    time_slice_rows<<<(unsigned)nrows, 64, 0, ctx->stream>>>(x, y, (int)T, (int)D, (int)t,
+                                                             backward, accumulate);
+    return numrs_hip::check_launch(ctx, "time_slice_rows");
+  }
   time_slice_kernel<<<grid_for(n, 256), 256, 0, ctx->stream>>>(x, y, B, T, D, t, backward,
                                                                 accumulate);
   return numrs_hip::check_launch(ctx, "time_slice_kernel");
