@@ -480,8 +480,11 @@ def bench_adam(ctx, rng, n, steps, warmup):
 def bench_c1(ctx, steps, warmup):
     """2-layer MLP (64x784 -> 128 -> ReLU -> 10, softmax CE,
     SGD lr 0.01) -- forward, backward and SGD step through the device
-    autograd engine, timed per step with a device sync at the end of each
-    step (a loss read-back is what a training loop does)."""
+    autograd engine.  n steps are launched back to back and the loss is read
+    back once at the end, so the figure is the step rate a training loop that
+    reads its loss occasionally sees: GPU-bound on a fast host, host-bound
+    (seven kernel launches and the Python calls per step) on a slow one.  The
+    graph replay below queues each step with one launch."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
     from tests.workloads import make_c1
