@@ -487,7 +487,7 @@ def bench_c1(ctx, steps, warmup):
     graph replay below queues each step with one launch."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
-    from tests.workloads import make_c1
+    from workloads import make_c1
 
     nr.set_default_context(ctx)
     p = make_c1(seed=1)
@@ -548,7 +548,7 @@ def bench_c4(ctx, steps, warmup):
     SGD step through the device autograd engine."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
-    from tests.workloads import make_c4
+    from workloads import make_c4
 
     nr.set_default_context(ctx)
     w, x, t, (B, S, H) = make_c4(seed=4)
@@ -589,7 +589,7 @@ def bench_c5(ctx, steps, warmup):
     SGD step through the device autograd engine."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
-    from tests.workloads import make_c5
+    from workloads import make_c5
 
     nr.set_default_context(ctx)
     layers, hw, hb, x, target = make_c5(seed=5)
@@ -657,7 +657,7 @@ def cpu_baseline_c1(reps: int = 5) -> dict:
     tensor.rs:206), transposes, ReLU backward and SGD (sgd.rs:87-124).
     Median of `reps` whole steps."""
     from oracle import oracle as O
-    from tests.workloads import make_c1
+    from workloads import make_c1
 
     p = make_c1(seed=1)
     x, onehot = p["x"], np.eye(10, dtype=np.float32)[p["labels"]]

@@ -165,7 +165,12 @@ int numrs_hip_timer_elapsed_ms(numrs_hip_ctx *ctx, int slot_start, int slot_end,
  *     whose step depends on a host-side step count.
  *   - Tensors created during the recording must stay alive while the graph
  *     is replayed; blocks they release during the recording are held by the
- *     graph until numrs_hip_graph_destroy. */
+ *     graph until numrs_hip_graph_destroy.
+ *   - Eager calls between replays may grow the context's workspace: while
+ *     any graph exists the old region is kept (the graph's kernels address
+ *     it) and freed when the last graph is destroyed.
+ *   - numrs_hip_graph_destroy during another recording returns 0 and
+ *     destroys the graph when that recording ends or is aborted. */
 typedef struct numrs_hip_graph numrs_hip_graph;
 int numrs_hip_graph_begin(numrs_hip_ctx *ctx);
 int numrs_hip_graph_end(numrs_hip_ctx *ctx, numrs_hip_graph **out);
@@ -303,8 +308,11 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
 /* The backward given also the forward's output out (rows at ld_out, like
  * dout), from which the softmax backward's row totals come as dO . O.  For
  * D/H = 64, S = 128 or 256, all three grads non-NULL and accumulate = 0 it
- * runs one key-block kernel (dV, dK and dQ without a dS buffer; B*H*S floats
- * of workspace); other calls behave as numrs_hip_attention_backward_strided. */
+ * runs one key-block kernel (dV, dK and dQ without a dS buffer or any
+ * workspace); other calls behave as numrs_hip_attention_backward_strided.
+ * At S = 256 the two key groups of a head add into dq with device float
+ * atomics onto a zeroed dq, so dq must be ordinary device memory (hipMalloc,
+ * coarse-grained), not managed or fine-grained host-coherent memory. */
 int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
                                              const float *v, int64_t ld_qkv, const float *P,
                                              const float *out, const float *dout, int64_t ld_out,
@@ -649,14 +657,6 @@ int numrs_hip_tensor_sum_axis(numrs_hip_tensor *a, int64_t axis, int mean, numrs
 /* Tensor softmax along one axis (0 <= axis < ndim); the reference rejects an
  * axis (ops/stats/softmax.rs:13-16). */
 int numrs_hip_tensor_softmax_axis(numrs_hip_tensor *a, int64_t axis, numrs_hip_tensor **out);
-/* Softmax along one axis of x viewed as [outer, n, inner] (the reference's
- * ops::softmax rejects an axis, ops/stats/softmax.rs:13-16); the last axis
- * (inner = 1) uses the row kernels.  Backward: softmax_backward
- * (backward.rs:521-541) along the same axis, dx (+)= y * (g - sum(g*y)). */
-int numrs_hip_softmax_axis_forward(numrs_hip_ctx *ctx, const float *x, float *y, int64_t outer,
-                                   int64_t n, int64_t inner);
-int numrs_hip_softmax_axis_backward(numrs_hip_ctx *ctx, const float *y, const float *g, float *dx,
-                                    int64_t outer, int64_t n, int64_t inner, int accumulate);
 /* LayerNorm over the last axis (no reference op). */
 int numrs_hip_tensor_layer_norm(numrs_hip_tensor *x, numrs_hip_tensor *gamma,
                                 numrs_hip_tensor *beta, float eps, numrs_hip_tensor **out);

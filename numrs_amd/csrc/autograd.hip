@@ -364,9 +364,14 @@ float *take_seed(const T &out) {
 // the input's cell has never held a buffer, the cell takes the pre-formed
 // buffer and no backward kernel runs.  Returns true when it did.
 bool adopt_preformed(const T &out, Node &n, size_t slot, const T &x) {
-  if (slot >= n.saved.size() || !n.saved[slot] || g_seed_root != out.get() ||
-      !out->grad->seed_preset || x->grad->valid || x->grad->buf)
+  if (slot >= n.saved.size() || !n.saved[slot]) return false;
+  if (g_seed_root != out.get() || !out->grad->seed_preset || x->grad->valid || x->grad->buf) {
+    // Not adoptable now, and never later (the first sweep through the loss
+    // makes the input's cell valid or leaves the loss a non-root): release
+    // the buffer.  Stream order keeps it intact for work already queued.
+    n.saved[slot].reset();
     return false;
+  }
   g_seed_root = nullptr;  // the seed is already in the root's cell
   x->grad->buf = std::move(n.saved[slot]);
   x->grad->valid = true;
@@ -838,10 +843,17 @@ int op_sum(const T &a, bool mean, T *out) {  // ops.rs:214-252
   return NUMRS_HIP_OK;
 }
 
+// Largest loss input whose root gradient the forward kernel pre-forms.  The
+// buffer is held by the loss node from the forward until a backward sweep
+// adopts or drops it (or the loss dies), so a loss computed with grad
+// recording but never differentiated (a validation loss) costs at most this
+// much extra memory; above it the saved launch is worth little anyway.
+constexpr int64_t kPreformMaxElems = int64_t(1) << 22;
+
 // Buffers for a loss's pre-formed root gradient (n floats) and for its own
 // gradient cell (the seed), when `want`; *pre stays null otherwise.
 int preform_buffers(const T &r, bool want, int64_t n, Buf *pre) {
-  if (!want) return NUMRS_HIP_OK;
+  if (!want || n > kPreformMaxElems) return NUMRS_HIP_OK;
   if (int rc = alloc_buf(r->ctx, n, sizeof(float), pre)) return rc;
   return alloc_buf(r->ctx, 1, sizeof(float), &r->grad->buf);
 }

@@ -42,6 +42,14 @@ struct numrs_hip_ctx {
   // -- and the graph takes them over when the recording ends.
   bool capturing = false;
   std::vector<std::pair<void *, size_t>> capture_held;
+  // Instantiated graphs not yet destroyed.  Their kernels address the
+  // workspace and scratch regions as they were when recorded, so while any
+  // exist a region that grows keeps its old buffer in `retired`; the last
+  // graph_destroy (or the context's destroy) frees them.
+  int64_t live_graphs = 0;
+  std::vector<void *> retired;
+  // graph_destroy calls made while a recording is open; run when it ends.
+  std::vector<struct numrs_hip_graph *> pending_destroy;
   // Device address of reduce.hip's static partials array on this context's
   // device, resolved at creation (the allocation-free entry point uses it).
   float *noalloc_partials = nullptr;

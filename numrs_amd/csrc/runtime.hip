@@ -25,6 +25,23 @@ static int refuse_growth(numrs_hip_ctx *ctx, const char *what, size_t bytes) {
               what, bytes);
 }
 
+// Releases the old buffer of a region that grows.  An instantiated graph's
+// kernels keep the address they were recorded with, so while a graph lives
+// the buffer is retired instead and freed when the last graph is destroyed.
+static hipError_t release_region(numrs_hip_ctx *ctx, void *p) {
+  if (p == nullptr) return hipSuccess;
+  if (ctx->live_graphs > 0) {
+    ctx->retired.push_back(p);
+    return hipSuccess;
+  }
+  return hipFree(p);
+}
+
+static void free_retired(numrs_hip_ctx *ctx) {
+  for (void *p : ctx->retired) (void)hipFree(p);
+  ctx->retired.clear();
+}
+
 int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out) {
   if (bytes <= ctx->workspace_bytes && ctx->workspace != nullptr) {
     *out = ctx->workspace;
@@ -33,7 +50,7 @@ int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out) {
   if (ctx->capturing) return refuse_growth(ctx, "the workspace", bytes);
   // Growing: earlier kernels may still read the old buffer, so drain first.
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  if (ctx->workspace != nullptr) NRS_HIP(ctx, hipFree(ctx->workspace));
+  NRS_HIP(ctx, release_region(ctx, ctx->workspace));
   ctx->workspace = nullptr;
   ctx->workspace_bytes = 0;
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
@@ -53,7 +70,7 @@ int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out) {
   }
   if (ctx->capturing) return refuse_growth(ctx, "the scratch region", bytes);
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  if (ctx->scratch != nullptr) NRS_HIP(ctx, hipFree(ctx->scratch));
+  NRS_HIP(ctx, release_region(ctx, ctx->scratch));
   ctx->scratch = nullptr;
   ctx->scratch_bytes = 0;
   size_t want = bytes < (1u << 16) ? (1u << 16) : bytes;
@@ -228,6 +245,7 @@ int numrs_hip_destroy(numrs_hip_ctx *ctx) {
   if (ctx->workspace != nullptr) (void)hipFree(ctx->workspace);
   if (ctx->scratch != nullptr) (void)hipFree(ctx->scratch);
   ctx->workspace = ctx->scratch = nullptr;
+  numrs_hip::free_retired(ctx);
   (void)hipStreamDestroy(ctx->stream);
   ctx->stream = nullptr;
   ctx->destroyed = true;
@@ -254,6 +272,31 @@ static void return_held(numrs_hip_ctx *ctx, std::vector<std::pair<void *, size_t
   held.clear();
 }
 
+// Destroys an instantiated graph; the context is not recording.  Returns
+// whether the graph's reference was the context's last (the caller then
+// deletes the destroyed context).
+static bool destroy_graph(numrs_hip_graph *g) {
+  numrs_hip_ctx *ctx = g->ctx;
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  return_held(ctx, g->held);
+  delete g;
+  if (--ctx->live_graphs == 0) numrs_hip::free_retired(ctx);
+  return --ctx->live_blocks == 0 && ctx->destroyed;
+}
+
+// Runs the graph_destroy calls made while the recording that just ended was
+// open.  The stream holds no replay of them: launches are refused while
+// recording, and the recording's own work was never queued.
+static bool run_pending_destroys(numrs_hip_ctx *ctx) {
+  std::vector<numrs_hip_graph *> pending;
+  pending.swap(ctx->pending_destroy);
+  if (!pending.empty() && !ctx->destroyed) (void)hipStreamSynchronize(ctx->stream);
+  bool last = false;
+  for (numrs_hip_graph *g : pending) last = destroy_graph(g);
+  return last;
+}
+
 int numrs_hip_graph_begin(numrs_hip_ctx *ctx) {
   NRS_CHECK_CTX(ctx);
   if (ctx->destroyed) return fail(ctx, NUMRS_HIP_E_INVALID, "context already destroyed");
@@ -278,6 +321,7 @@ int numrs_hip_graph_abort(numrs_hip_ctx *ctx) {
   std::vector<std::pair<void *, size_t>> held;
   held.swap(ctx->capture_held);
   return_held(ctx, held);
+  if (run_pending_destroys(ctx)) delete ctx;
   return NUMRS_HIP_OK;
 }
 
@@ -295,6 +339,7 @@ int numrs_hip_graph_end(numrs_hip_ctx *ctx, numrs_hip_graph **out) {
     (void)hipGetLastError();
     if (graph != nullptr) (void)hipGraphDestroy(graph);
     return_held(ctx, held);
+    (void)run_pending_destroys(ctx);  // the context is not destroyed while recording
     return fail(ctx, NUMRS_HIP_E_HIP, "graph recording failed: %s", hipGetErrorString(e));
   }
   hipGraphExec_t exec = nullptr;
@@ -303,10 +348,13 @@ int numrs_hip_graph_end(numrs_hip_ctx *ctx, numrs_hip_graph **out) {
     (void)hipGetLastError();
     (void)hipGraphDestroy(graph);
     return_held(ctx, held);
+    (void)run_pending_destroys(ctx);
     return fail(ctx, NUMRS_HIP_E_HIP, "graph instantiation failed: %s", hipGetErrorString(e));
   }
   *out = new numrs_hip_graph{ctx, graph, exec, std::move(held)};
   ++ctx->live_blocks;  // the graph keeps the context alive, like a tensor's block
+  ++ctx->live_graphs;
+  (void)run_pending_destroys(ctx);  // the new graph keeps the context alive
   return NUMRS_HIP_OK;
 }
 
@@ -323,15 +371,15 @@ int numrs_hip_graph_launch(numrs_hip_graph *g) {
 int numrs_hip_graph_destroy(numrs_hip_graph *g) {
   if (g == nullptr) return NUMRS_HIP_OK;
   numrs_hip_ctx *ctx = g->ctx;
-  if (ctx->capturing)
-    return fail(ctx, NUMRS_HIP_E_INVALID, "destroy a graph outside a recording");
+  if (ctx->capturing) {
+    // A stream synchronisation would invalidate the open recording: the
+    // graph is destroyed when the recording ends (or is aborted).
+    ctx->pending_destroy.push_back(g);
+    return NUMRS_HIP_OK;
+  }
   // Queued replays finish first (a destroyed context's stream was drained).
   if (!ctx->destroyed) NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  (void)hipGraphExecDestroy(g->exec);
-  (void)hipGraphDestroy(g->graph);
-  return_held(ctx, g->held);
-  delete g;
-  if (--ctx->live_blocks == 0 && ctx->destroyed) delete ctx;
+  if (destroy_graph(g)) delete ctx;
   return NUMRS_HIP_OK;
 }
 

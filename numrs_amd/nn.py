@@ -161,15 +161,20 @@ class MultiHeadAttention(Module):
     features, W_qkv = [W_q; W_k; W_v] and b_qkv = [b_q; b_k; b_v], whose packed
     [batch*seq, 3d] output the attention node reads in place: one product
     forward and one product pair backward instead of three.  `fused_qkv =
-    False` keeps three Linear layers; both give the same values and grads."""
+    False` keeps three Linear layers; both give the same values and grads.
+    The choice is made per instance at construction (the class attribute is
+    only the default) and fixes the parameter layout: parameters() is
+    [W_qkv, b_qkv, W_o, b_o] packed, or [W_q, b_q, W_k, b_k, W_v, b_v, W_o,
+    b_o] unpacked, which an optimizer's state and a checkpoint follow."""
 
     fused_qkv = True
 
-    def __init__(self, wq, wk, wv, wo, heads: int, ctx=None):
+    def __init__(self, wq, wk, wv, wo, heads: int, ctx=None, fused_qkv: bool | None = None):
         d = np.asarray(wq).shape[0]
         z = np.zeros(d, np.float32)
         self.heads, self.dim = heads, d
-        if self.fused_qkv:
+        self._fused_qkv = type(self).fused_qkv if fused_qkv is None else bool(fused_qkv)
+        if self._fused_qkv:
             w = np.concatenate([np.asarray(a, np.float32).reshape(d, d) for a in (wq, wk, wv)])
             self.qkv = Linear.with_weights(d, 3 * d, w, np.zeros(3 * d, np.float32), ctx)
             self.projections = [self.qkv]
@@ -185,7 +190,7 @@ class MultiHeadAttention(Module):
         """Attention output projection of x [batch*seq, d]; with `residual`,
         residual + that projection (one node when the projection is a fused
         Linear)."""
-        if self.fused_qkv:
+        if self._fused_qkv:
             a = self.qkv(x).attention_qkv(batch, seq, self.heads)
         else:
             a = self.q(x).attention(self.k(x), self.v(x), batch, seq, self.heads)
@@ -199,7 +204,7 @@ class MultiHeadAttention(Module):
         """Gradients of the q, k, v projections as wq, wk, wv [d, d] and bq,
         bk, bv [d], from either form."""
         d = self.dim
-        if not self.fused_qkv:
+        if not self._fused_qkv:
             out = {f"w{n}": getattr(self, n).weight.gradient() for n in ("q", "k", "v")}
             out.update({f"b{n}": getattr(self, n).bias.gradient() for n in ("q", "k", "v")})
             return out

@@ -8,7 +8,7 @@ import math
 
 import numpy as np
 
-from tests.workloads import make_c5  # noqa: F401  (re-exported for the tests)
+from workloads import make_c5  # noqa: F401  (re-exported for the tests)
 
 
 def _sig(z):

@@ -17,7 +17,7 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import oracle as O
-from tests.workloads import make_c1, xavier  # noqa: F401  (re-exported for the tests)
+from workloads import make_c1, xavier  # noqa: F401  (re-exported for the tests)
 
 
 def _bias_grad(g, n, mode):

@@ -130,3 +130,86 @@ def test_recording_refuses_host_transfers(hip_ctx):
     t = Tensor.new(np.arange(5, dtype=np.float32), True)
     t.sum().backward()
     assert t.gradient().tolist() == [1.0] * 5
+
+
+def test_workspace_growth_between_replays_keeps_graph_valid(hip_ctx):
+    """Eager work between replays that grows the context's workspace (a
+    split-K matmul backward with a long inner dimension, then an explicit
+    reserve) must not free the region the recorded kernels address: every
+    replay still equals an eager step bit for bit."""
+    print("[gpu] graph: workspace growth between C1 replays", flush=True)
+    nr.set_default_context(hip_ctx)
+    p = make_c1(seed=9)
+    eager, pe = _mlp(p)
+    recorded, pr = _mlp(p)
+    x = Tensor.new(p["x"], False)
+    onehot = Tensor.new(np.eye(10, dtype=np.float32)[p["labels"]], False)
+    se = _step(eager, optim.SGD.simple(eager.parameters(), 0.01), x, onehot)
+    sr = _step(recorded, optim.SGD.simple(recorded.parameters(), 0.01), x, onehot)
+    assert se().item() == sr().item()
+    g = StepGraph(hip_ctx, sr)
+    rng = np.random.default_rng(9)
+    M, K, N = 128, 1 << 16, 128
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    dC = rng.standard_normal((M, N)).astype(np.float32)
+    dA_d, dB_d = hip_ctx.zeros((M, K)), hip_ctx.zeros((K, N))
+    A_d, B_d, dC_d = hip_ctx.to_device(A), hip_ctx.to_device(B), hip_ctx.to_device(dC)
+    try:
+        for k in range(3):
+            want = se().item()
+            g.replay()
+            # eager growth between replays: a long-K product (split-K
+            # partials), then a reserve well beyond anything used so far
+            hip_ctx.matmul_backward(dC_d, A_d, B_d, dA_d, dB_d)
+            hip_ctx.reserve((64 << 20) * (k + 1))
+            hip_ctx.sync()
+            assert g.outputs.item() == want, k
+            for i, (a, b) in enumerate(zip(pe, pr)):
+                assert np.array_equal(a.values(), b.values()), (k, i)
+        ref = (A.astype(np.float64).T @ dC.astype(np.float64))
+        got = dB_d.numpy().astype(np.float64)
+        assert np.max(np.abs(got - ref)) <= 1e-3 * np.max(np.abs(ref))
+    finally:
+        g.close()
+    # with no graph left the retired regions are gone and work continues
+    hip_ctx.reserve(1 << 20)
+    assert np.isfinite(sr().item())
+
+
+def test_graph_destroy_during_recording_is_deferred(hip_ctx):
+    """numrs_hip_graph_destroy called while another recording is open is
+    queued and runs when that recording ends; the first graph's replays
+    before that still work and the new graph replays correctly."""
+    print("[gpu] graph: destroy during a recording", flush=True)
+    nr.set_default_context(hip_ctx)
+    w = Tensor.new(np.linspace(-1, 1, 64, dtype=np.float32).reshape(8, 8), True)
+    sgd = optim.SGD.simple([w], 0.1)
+
+    def step():
+        loss = w.mul(w).sum()
+        loss.backward()
+        sgd.step()
+        sgd.zero_grad()
+        return loss
+
+    step()
+    g1 = StepGraph(hip_ctx, step)
+    closed = []
+
+    def step_closing_g1():
+        g1.close()  # queued: the recording is open
+        closed.append(True)
+        return step()
+
+    g2 = StepGraph(hip_ctx, step_closing_g1)
+    assert closed == [True]
+    try:
+        with pytest.raises(RuntimeError, match="closed"):
+            g1.replay()
+        v0 = w.values().astype(np.float64)
+        g2.replay()
+        hip_ctx.sync()
+        np.testing.assert_allclose(w.values(), v0 * 0.8, rtol=1e-6, atol=1e-7)
+    finally:
+        g2.close()

@@ -11,7 +11,7 @@ import math
 
 import numpy as np
 
-from tests.workloads import make_c4  # noqa: F401  (re-exported for the tests)
+from workloads import make_c4  # noqa: F401  (re-exported for the tests)
 
 
 def _ln(x, eps=1e-5):

@@ -1,4 +1,4 @@
-"""Synthetic inputs of the BASELINE configs C1, C4 and C5 (seeded numpy
+"""Synthetic inputs of the configs C1, C4 and C5 (seeded numpy
 generators; numpy only).  bench.py builds its workloads from these, and the
 tests build the same inputs for the oracles.
 """
