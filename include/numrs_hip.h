@@ -319,6 +319,21 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
                                              float *dq, float *dk, float *dv, int64_t B, int64_t S,
                                              int64_t H, int64_t D, int accumulate);
 
+/* How the two-layer LSTM calls run their recurrences (no reference op).
+ * AUTO (the default): one persistent cooperative launch for all steps of
+ * the forward and one for the backward where they apply (H1 = H2 = 256,
+ * 16-byte aligned operands, not while recording a graph, and the device
+ * holds the whole grid at once); per-step launches otherwise.  PER_STEP:
+ * always one launch per diagonal step.  Both give the same bits.  A
+ * persistent launch whose bounded wait for another workgroup runs out
+ * returns its error from the next call that synchronises the stream. */
+#define NUMRS_HIP_RECURRENCE_AUTO 0
+#define NUMRS_HIP_RECURRENCE_PER_STEP 1
+int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode);
+/* Number of persistent recurrence launches queued on the context so far
+ * (-1 for a null context). */
+int64_t numrs_hip_persistent_launches(numrs_hip_ctx *ctx);
+
 /* LSTM layer (no reference op), gate order i, f, g, o:
  * x [B, T, I], W_ih [4H, I], W_hh [4H, H], b [4H] (NULL = 0), h0/c0 [B, H]
  * (NULL = 0).  Forward writes h_seq, c_seq [B, T, H] and the gate

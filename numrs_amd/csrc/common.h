@@ -50,6 +50,18 @@ struct numrs_hip_ctx {
   std::vector<void *> retired;
   // graph_destroy calls made while a recording is open; run when it ends.
   std::vector<struct numrs_hip_graph *> pending_destroy;
+  // Give-up word of the persistent recurrence kernels (lstm.hip): a device
+  // int, allocated on first use, that a kernel sets when a bounded wait for
+  // another workgroup's step ran out.  wait_check marks that such a kernel
+  // was queued since the word was last read; the next call that synchronises
+  // the stream reads it and reports a give-up as an error.
+  int *wait_status = nullptr;
+  bool wait_check = false;
+  // NUMRS_HIP_RECURRENCE_AUTO or _PER_STEP (numrs_hip_set_recurrence_mode),
+  // and the persistent kernels' resident workgroups per CU (-1: not queried).
+  int recurrence_mode = 0;
+  int persist_fwd_per_cu = -1, persist_bwd_per_cu = -1;
+  int64_t persist_launches = 0;  // persistent launches queued on this context
   // Device address of reduce.hip's static partials array on this context's
   // device, resolved at creation (the allocation-free entry point uses it).
   float *noalloc_partials = nullptr;
@@ -97,6 +109,12 @@ struct TempBlock {
 
 // Checks the launch that was just enqueued.
 int check_launch(numrs_hip_ctx *ctx, const char *what);
+
+// The context's give-up word for persistent kernels (zeroed on allocation),
+// and the check of it after a stream synchronisation (no-op unless such a
+// kernel ran since the last check).
+int wait_status_word(numrs_hip_ctx *ctx, int **out);
+int check_wait_status(numrs_hip_ctx *ctx);
 
 // Loss backward kernels for the engine's root node: with `seed` non-null the
 // incoming gradient is the sweep's seed 1 (not read from g_scalar) and the

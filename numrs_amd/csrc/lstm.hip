@@ -43,6 +43,39 @@ constexpr int kBwdStageH = 1024;  // largest H whose dG rows the backward stages
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// One cell's forward from its gate pre-activations (order i, f, g, o) and
+// previous cell state: act = (sigmoid i, sigmoid f, tanh g, sigmoid o),
+// c = f c_prev + i g, h = o tanh(c).  Shared by every step kernel, so all
+// paths round alike.
+__device__ __forceinline__ void cell_forward(const float pre[4], float cp, float act[4], float &c,
+                                             float &h) {
+  act[0] = sigm(pre[0]);
+  act[1] = sigm(pre[1]);
+  act[2] = tanhf(pre[2]);
+  act[3] = sigm(pre[3]);
+  c = act[1] * cp + act[0] * act[2];
+  h = act[3] * tanhf(c);
+}
+
+// One cell's backward: a = saved activations (i, f, g, o), c / cp = cell
+// state at this and the previous step, dh = gradient at h, dcn = dc_{t+1}
+// f_{t+1} (0 at the last step).  Gate pre-activation gradients into dg, the
+// product dc_t f_t for the step before into dcf.  The gate formulas are the
+// reference's sigmoid_backward ((g s)(1 - s), backward.rs:166-177),
+// tanh_backward (g (1 - y^2), backward.rs:503-517) and mul_backward
+// (backward.rs:74-87) composed through c = f c_prev + i g, h = o tanh(c).
+__device__ __forceinline__ void cell_backward(const float a[4], float c, float cp, float dh,
+                                              float dcn, float dg[4], float &dcf) {
+  const float i = a[0], f = a[1], g = a[2], o = a[3];
+  const float tc = tanhf(c);
+  const float dct = dh * o * (1.0f - tc * tc) + dcn;
+  dg[0] = (dct * g) * i * (1.0f - i);
+  dg[1] = (dct * cp) * f * (1.0f - f);
+  dg[2] = (dct * i) * (1.0f - g * g);
+  dg[3] = (dh * tc) * o * (1.0f - o);
+  dcf = dct * f;
+}
+
 // Packed recurrent weights: P[(k * H + j) * 4 + g] = in[g * sg + k * sk + j],
 // so the four gate weights a lane needs for reduction index k are one 16-byte
 // load.  Forward: in = W_hh^T [H, 4H] (sg = H, sk = 4H), P[k, j, g] =
@@ -163,16 +196,12 @@ __global__ void __launch_bounds__(kThreads)
   __syncthreads();
   if (!epi) return;
   const int u = wave;
-  const float i = sigm(gin[0] + part[0][u * 4 + 0][lane]);
-  const float f = sigm(gin[1] + part[0][u * 4 + 1][lane]);
-  const float g = tanhf(gin[2] + part[0][u * 4 + 2][lane]);
-  const float o = sigm(gin[3] + part[0][u * 4 + 3][lane]);
-  const float c = f * cp + i * g;
-  const float h = o * tanhf(c);
-  G[gb + j] = i;
-  G[gb + H + j] = f;
-  G[gb + 2 * H + j] = g;
-  G[gb + 3 * H + j] = o;
+  float pre[4], act[4], c, h;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) pre[k] = gin[k] + part[0][u * 4 + k][lane];
+  cell_forward(pre, cp, act, c, h);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) G[gb + k * H + j] = act[k];
   c_seq[((int64_t)be * T + t) * H + j] = c;
   h_seq[((int64_t)be * T + t) * H + j] = h;
 }
@@ -280,15 +309,11 @@ __global__ void __launch_bounds__(kThreads)
   float r = part[0][u][lane];
 #pragma unroll
   for (int v = 1; v < kWaves; ++v) r += part[v][u][lane];
-  const float i = a[0], f = a[1], g = a[2], o = a[3];
-  const float dh = dho + r;
-  const float tc = tanhf(c);
-  const float dct = dh * o * (1.0f - tc * tc) + dcn;
-  dG[gb + j] = (dct * g) * i * (1.0f - i);
-  dG[gb + H + j] = (dct * cp) * f * (1.0f - f);
-  dG[gb + 2 * H + j] = (dct * i) * (1.0f - g * g);
-  dG[gb + 3 * H + j] = (dh * tc) * o * (1.0f - o);
-  dc[(int64_t)be * H + j] = dct * f;
+  float dg[4], dcf;
+  cell_backward(a, c, cp, dho + r, dcn, dg, dcf);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) dG[gb + k * H + j] = dg[k];
+  dc[(int64_t)be * H + j] = dcf;
 }
 
 static_assert(kRows * 4 == kWaves, "one LDS column of partials per wave");
@@ -415,16 +440,10 @@ __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, 
     const int c = 4 * g + eu;
     pre[g] = gin[g] + (((part[0][em][c] + part[1][em][c]) + part[2][em][c]) + part[3][em][c]);
   }
-  const float i = sigm(pre[0]);
-  const float f = sigm(pre[1]);
-  const float g = tanhf(pre[2]);
-  const float o = sigm(pre[3]);
-  const float c = f * cp + i * g;
-  const float h = o * tanhf(c);
-  s.G[gb + je] = i;
-  s.G[gb + H + je] = f;
-  s.G[gb + 2 * H + je] = g;
-  s.G[gb + 3 * H + je] = o;
+  float act[4], c, h;
+  cell_forward(pre, cp, act, c, h);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s.G[gb + k * H + je] = act[k];
   s.c_seq[((int64_t)be * T + t) * H + je] = c;
   s.h_seq[((int64_t)be * T + t) * H + je] = h;
 }
@@ -564,15 +583,11 @@ __device__ __forceinline__ void bwd_step_tile(const BwdStep &s, int blk, int B, 
   r += __shfl_xor(r, 1, 64);
   r += __shfl_xor(r, 2, 64);
   if (!epi) return;
-  const float i = a[0], f = a[1], g = a[2], o = a[3];
-  const float dh = dho + r;
-  const float tc = tanhf(c);
-  const float dct = dh * o * (1.0f - tc * tc) + dcn;
-  s.dG[gb + je] = (dct * g) * i * (1.0f - i);
-  s.dG[gb + H + je] = (dct * cp) * f * (1.0f - f);
-  s.dG[gb + 2 * H + je] = (dct * i) * (1.0f - g * g);
-  s.dG[gb + 3 * H + je] = (dh * tc) * o * (1.0f - o);
-  s.dc[(int64_t)be * H + je] = dct * f;
+  float dg[4], dcf;
+  cell_backward(a, c, cp, dho + r, dcn, dg, dcf);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s.dG[gb + k * H + je] = dg[k];
+  s.dc[(int64_t)be * H + je] = dcf;
 }
 
 __global__ void __launch_bounds__(256) lstm_bwd_step_tiled(BwdStep s, int B, int T) {
@@ -660,15 +675,11 @@ __device__ __forceinline__ void bwd_step_mfma(const BwdStep &s, int blk, int B, 
   float sum = part[0][em][eu];
 #pragma unroll
   for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
-  const float i = a[0], f = a[1], g = a[2], o = a[3];
-  const float dh = dho + sum;
-  const float tc = tanhf(c);
-  const float dct = dh * o * (1.0f - tc * tc) + dcn;
-  s.dG[gb + je] = (dct * g) * i * (1.0f - i);
-  s.dG[gb + H + je] = (dct * cp) * f * (1.0f - f);
-  s.dG[gb + 2 * H + je] = (dct * i) * (1.0f - g * g);
-  s.dG[gb + 3 * H + je] = (dh * tc) * o * (1.0f - o);
-  s.dc[(int64_t)be * H + je] = dct * f;
+  float dg[4], dcf;
+  cell_backward(a, c, cp, dho + sum, dcn, dg, dcf);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s.dG[gb + k * H + je] = dg[k];
+  s.dc[(int64_t)be * H + je] = dcf;
 }
 
 __global__ void __launch_bounds__(64 * kMWaves) lstm_bwd_step_mfma(BwdStep s, int B, int T) {
@@ -681,6 +692,436 @@ __global__ void __launch_bounds__(64 * kMWaves)
     bwd_step_mfma(a, blockIdx.x, B, T);
   else
     bwd_step_mfma(b, blockIdx.x - blocks_a, B, T);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent recurrences of two stacked layers (H1 = H2 = 256): one
+// cooperative launch runs every step of both layers' forward, one every step
+// of their backward, instead of T + 1 launches each.
+//
+// Each layer runs in workgroups of its own, so the two recurrences are two
+// chains: the forward's lower chain depends only on itself and the upper one
+// on itself and the lower one (which usually runs ahead); the backward's
+// upper chain only on itself and the lower one on itself and the upper one.
+// A step of row group rg (16 batch rows) reads only the previous step's
+// values of the same rows (all units of h, or of dG), so the workgroups of
+// a chain and row group meet at per-workgroup step counters instead of a
+// grid-wide barrier.  The values that cross workgroups (h, dG) are written
+// and read at device scope, one access at a time: stores write through to
+// the device's coherence point and loads fetch from it (the sc1 scope bit),
+// which the eight XCDs' L2 caches need no write-back or invalidation for (a
+// cache-wide write-back and invalidation per step, agent-scope fences,
+// measured 3.3x slower than one launch per step).  After a step every lane
+// waits for its stores to be acknowledged, the block meets, and one thread
+// stores the number of steps the workgroup has finished into its counter
+// (device scope).  Before a step one wave reads the counters the step
+// depends on at device scope until all have reached it; the block meets
+// again and only then loads the step's rows.  (Polling the operands
+// themselves, pre-set to a signalling-NaN pattern, flooded the coherence
+// point with requests and measured slower; so did both layers in one
+// workgroup, whose waits covered twice as many workgroups: a step's wait
+// ends when the slowest workgroup it depends on has finished.)
+//
+// The wait is bounded: after kSpinLimit rounds, or once another workgroup
+// has given up (the abort word after the counters), a workgroup records the
+// give-up in the context's status word and returns, so every workgroup
+// exits; the host reports it at its next synchronisation.  The cooperative
+// launch refuses a grid that cannot be resident all at once.
+//
+// Each wave keeps its slice of the recurrent (and stacked input) weights in
+// registers for the whole launch; a step reads only the rows it reduces and
+// its cells' saved values, and each lane carries its cell's c (forward) or
+// dc f (backward) from step to step in a register.  The per-wave reduction
+// slices, the MFMA operand layout and the order in which partials are added
+// are those of the per-step kernels (lstm_fwd_diag, lstm_bwd_diag_mfma), so
+// both paths give the same bits.
+// ---------------------------------------------------------------------------
+constexpr int kSpinLimit = 1 << 21;  // wait rounds before giving up (seconds of waiting)
+constexpr int kPersistH = 256;       // the hidden size of the persistent kernels
+constexpr int kScDevice = 16;        // buffer access cache-policy bits: sc1 (device scope)
+constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
+constexpr int kPFUnits = 8;          // forward: hidden units per workgroup (two MFMA tiles)
+
+// Buffer resource over `bytes` bytes at p (bytes < 2^31); loads past the end
+// return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)bytes,
+                                           kBufWord3);
+}
+// 16-byte load at device scope, byte offset `off` into the resource.
+__device__ __forceinline__ f4 ld_dev4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice);
+}
+// Store at device scope.
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After a step: every lane's device-scope stores acknowledged, the block
+// met, then thread 0 publishes `steps` in the workgroup's counter.
+__device__ __forceinline__ void publish_step(unsigned *counter, unsigned steps) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counter, steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// On the calling wave: waits until the na counters at fa have reached ta
+// and the nb counters at fb have reached tb (na, nb <= 64).  Returns false,
+// after recording why, when the wait ran out (status 1) or another
+// workgroup gave up (the abort word is set).
+__device__ bool wait_counters(const unsigned *fa, int na, unsigned ta, const unsigned *fb, int nb,
+                              unsigned tb, unsigned *abort_word, int *status) {
+  const int lane = threadIdx.x & 63;
+  for (int it = 0;; ++it) {
+    bool ok = true;
+    if (lane < na)
+      ok = __hip_atomic_load(fa + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= ta;
+    if (lane < nb)
+      ok = ok && __hip_atomic_load(fb + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= tb;
+    if (__all(ok)) return true;
+    const unsigned ab = __hip_atomic_load(abort_word + (lane & 0), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    if (ab != 0u || it >= kSpinLimit) {
+      if (lane == 0) {
+        if (ab == 0u) __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Before a step: wave 0 waits (wait_counters); the block meets; false when
+// the wait gave up (every thread then returns).
+__device__ __forceinline__ bool await_step(const unsigned *fa, int na, unsigned ta,
+                                           const unsigned *fb, int nb, unsigned tb,
+                                           unsigned *abort_word, int *status, int *s_go) {
+  if (threadIdx.x < 64) {
+    const bool ok = wait_counters(fa, na, ta, fb, nb, tb, abort_word, status);
+    if (threadIdx.x == 0) *s_go = ok ? 1 : 0;
+  }
+  __syncthreads();
+  return *s_go != 0;
+}
+
+struct Lstm2Fwd {
+  float *acts1, *acts2;              // [B, T, 4H]; acts1 holds x W_ih1^T + b1 on entry
+  const float *whh1, *wih2, *whh2;   // [4H, H]
+  const float *b2;                   // [4H] or null
+  float *h1, *c1, *h2, *c2;          // [B, T, H]
+  unsigned *count;  // [2][rgroups][H / kPFUnits] steps done (lower, upper), then the abort word
+  int *status;
+  int B, T;
+};
+
+// Forward: workgroups [0, n) run the lower layer, [n, 2n) the upper one;
+// workgroup (row group rg, unit group ug) owns rows b0..b0+15 and units
+// j0..j0+7 of its layer as two kFRows x kFUnits tiles (those of
+// lstm_fwd_diag): wave w forms quarter w % 4 of tile w / 4's reduction, and
+// waves 0 and 4 finish the tiles' 64 cells each.  Lower step t reads h1 at
+// t - 1; upper step t reads h2 at t - 1 and h1 at t.
+__global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
+  constexpr int H = kPersistH, H4 = 4 * H;
+  constexpr int ugroups = H / kPFUnits;
+  __shared__ float part[8][kFRows][16];
+  __shared__ int s_go;
+  const int B = p.B, T = p.T;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rgroups = (int)gridDim.x / (2 * ugroups);
+  const bool upper = (int)blockIdx.x >= rgroups * ugroups;
+  const int blk = upper ? (int)blockIdx.x - rgroups * ugroups : (int)blockIdx.x;
+  const int ug = blk % ugroups, rg = blk / ugroups;
+  const int tile = wave >> 2;
+  const int j0 = ug * kPFUnits + tile * kFUnits, b0 = rg * kFRows;  // the wave's tile
+  const int r = lane & 15, q = lane >> 4;
+  const int b = min(b0 + r, B - 1);
+  const int kb = (wave & 3) * (H / 4) + 4 * q;  // this lane's offset in the wave's 64-long block
+  const int64_t wr = (int64_t)((r >> 2) * H + j0 + (r & 3));  // weight row n(c) of column r
+
+  // The wave's weights: lower W_hh1 (wa); upper W_hh2 (wa) and W_ih2 (wb).
+  f4 wa[4], wb[4];
+  {
+    const float *srca = (upper ? p.whh2 : p.whh1) + wr * H + kb;
+    const float *srcb = p.wih2 + wr * H + kb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wa[i] = *reinterpret_cast<const f4 *>(srca + 16 * i);
+      wb[i] = upper ? *reinterpret_cast<const f4 *>(srcb + 16 * i) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  const int64_t hbytes = (int64_t)B * T * H * 4;
+  const __amdgpu_buffer_rsrc_t rh1 = dev_rsrc(p.h1, hbytes), rh2 = dev_rsrc(p.h2, hbytes);
+  // cell (em, eu) = (lane / 4, lane % 4) of the tile of wave 0 or wave 4
+  const int em = lane >> 2, eu = lane & 3;
+  const int be = b0 + em, je = j0 + eu;
+  const bool epi = (wave & 3) == 0 && be < B;
+  float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (epi && upper && p.b2 != nullptr) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) bias[g] = p.b2[g * H + je];
+  }
+  float cst = 0.0f;  // the cell's state at its previous step (zero initial state)
+  unsigned *lo_cnt = p.count + rg * ugroups;                       // the row group's lower
+  unsigned *up_cnt = p.count + (rgroups + rg) * ugroups;           // and upper counters
+  unsigned *mine = (upper ? up_cnt : lo_cnt) + ug;
+  unsigned *abort_word = p.count + 2 * rgroups * ugroups;
+  float *acts = upper ? p.acts2 : p.acts1;
+  float *cs = upper ? p.c2 : p.c1;
+  float *hs = upper ? p.h2 : p.h1;
+
+  for (int t = 0; t < T; ++t) {
+    float gin[4] = {bias[0], bias[1], bias[2], bias[3]};
+    const int64_t row = (int64_t)be * T + t;
+    if (epi && !upper) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) gin[g] = p.acts1[row * H4 + g * H + je];
+    }
+    // Lower: h1 at t - 1 done.  Upper: first h1 at t (the lower chain, which
+    // runs ahead: its loads are then in flight during the second wait), then
+    // h2 at t - 1.
+    f4 ar[4], ai[4];
+    if (upper) {
+      if (!await_step(lo_cnt, ugroups, (unsigned)(t + 1), lo_cnt, 0, 0u, abort_word, p.status,
+                      &s_go))
+        return;
+      const int off = (int)((((int64_t)b * T + t) * H + kb) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ai[i] = ld_dev4(rh1, off + 64 * i);
+    }
+    if (t > 0) {
+      if (!await_step(upper ? up_cnt : lo_cnt, ugroups, (unsigned)t, lo_cnt, 0, 0u, abort_word,
+                      p.status, &s_go))
+        return;
+      const int off = (int)((((int64_t)b * T + t - 1) * H + kb) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ar[i] = ld_dev4(upper ? rh2 : rh1, off + 64 * i);
+    }
+    // every load issued before the first MFMA waits on one (the scheduler
+    // would otherwise issue later loads after earlier MFMAs, exposing their
+    // latencies one after another)
+    __builtin_amdgcn_sched_barrier(0);
+    // lower: h1_{t-1} W_hh1^T; upper: h2_{t-1} W_hh2^T, then h1_t W_ih2^T
+    // (the per-step kernels' order)
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (t > 0) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[e >> 2][e & 3], wa[e >> 2][e & 3], acc, 0, 0,
+                                                   0);
+    }
+    if (upper) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ai[e >> 2][e & 3], wb[e >> 2][e & 3], acc, 0, 0,
+                                                   0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wave][4 * q + v][r] = acc[v];
+    __syncthreads();
+    if (epi) {
+      const int pw = 4 * tile;
+      float pre[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c = 4 * g + eu;
+        pre[g] = gin[g] + (((part[pw][em][c] + part[pw + 1][em][c]) + part[pw + 2][em][c]) +
+                           part[pw + 3][em][c]);
+      }
+      float act[4], c, h;
+      cell_forward(pre, cst, act, c, h);
+      cst = c;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) acts[row * H4 + g * H + je] = act[g];
+      cs[row * H + je] = c;
+      st_dev(hs + row * H + je, h);
+    }
+    publish_step(mine, (unsigned)(t + 1));
+  }
+}
+
+struct Lstm2Bwd {
+  float *dG1, *dG2;                       // [B, T, 4H] gate gradients
+  const float *whh1, *wih2, *whh2;        // [4H, H]
+  const float *acts1, *c1, *acts2, *c2;   // forward's saved values
+  const float *dh2;                       // [B, T, H] gradient at the upper h, or null
+  unsigned *count;  // [rgroups][2][H / kMUnits] steps done (upper, lower), then the abort word
+  int *status;
+  int B, T;
+};
+
+// Backward: workgroups [0, n) run the upper layer, [n, 2n) the lower one;
+// workgroup (row group rg, unit group ug) owns rows b0..b0+15 and units
+// j0..j0+15 (kMRows x kMUnits, as lstm_bwd_diag_mfma), its 16 waves each a
+// sixteenth of the 4H-long reductions, threads 0..255 one cell each.  Step
+// s runs t = T-1-s: upper dh = dh2 + dG2_{t+1} W_hh2 (its own previous step),
+// lower dh = dG1_{t+1} W_hh1 + dG2_t W_ih2 (its own previous step and the
+// upper layer's step s).
+__global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
+  constexpr int H = kPersistH, H4 = 4 * H;
+  constexpr int ugroups = H / kMUnits;
+  __shared__ float part[kMWaves][16][16];
+  __shared__ int s_go;
+  const int B = p.B, T = p.T;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int per_layer = (int)gridDim.x / 2;
+  const bool lower = (int)blockIdx.x >= per_layer;
+  const int blk = lower ? (int)blockIdx.x - per_layer : (int)blockIdx.x;
+  const int ug = blk % ugroups, rg = blk / ugroups;
+  const int j0 = ug * kMUnits, b0 = rg * kMRows;
+  const int r = lane & 15, q = lane >> 4;
+  const int b = min(b0 + r, B - 1);
+  const int nb = wave * (H4 / kMWaves) + 4 * q;  // this lane's offset in the wave's 64-long block
+
+  // B operands: W[n][j0 + r] for n = nb + 16 i + e (strided loads, once):
+  // wa from the layer's own W_hh, wb (lower layer) from W_ih2.
+  f4 wa[4], wb[4];
+  {
+    const float *srca = (lower ? p.whh1 : p.whh2) + j0 + r;
+    const float *srcb = p.wih2 + j0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = nb + 16 * i + e;
+        wa[i][e] = srca[n * H];
+        wb[i][e] = lower ? srcb[n * H] : 0.0f;
+      }
+  }
+  const int64_t gbytes = (int64_t)B * T * H4 * 4;
+  const __amdgpu_buffer_rsrc_t rg1 = dev_rsrc(p.dG1, gbytes), rg2 = dev_rsrc(p.dG2, gbytes);
+  const int tid = threadIdx.x;
+  const int em = tid >> 4, eu = tid & 15;
+  const int be = b0 + em, je = j0 + eu;
+  const bool epi = tid < 256 && be < B;
+  float dcf = 0.0f;  // dc_{t+1} f_{t+1} of the cell (0 before its last step)
+  const float *acts = lower ? p.acts1 : p.acts2;
+  const float *cs = lower ? p.c1 : p.c2;
+  float *dGo = lower ? p.dG1 : p.dG2;
+  unsigned *up_cnt = p.count + rg * 2 * ugroups;  // the row group's upper, then lower counters
+  unsigned *lo_cnt = up_cnt + ugroups;
+  unsigned *mine = (lower ? lo_cnt : up_cnt) + ug;
+  unsigned *abort_word = p.count + gridDim.x;
+
+  for (int s = 0; s < T; ++s) {
+    const int t = T - 1 - s;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, c = 0.0f, cp = 0.0f, dho = 0.0f;
+    const int64_t row = (int64_t)be * T + t;
+    if (epi) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) a[g] = acts[row * H4 + g * H + je];
+      c = cs[row * H + je];
+      cp = t > 0 ? cs[(row - 1) * H + je] : 0.0f;
+      if (!lower && p.dh2 != nullptr) dho = p.dh2[row * H + je];
+    }
+    // Upper: its step s - 1 done.  Lower: first the upper step s (the upper
+    // chain runs ahead: its loads are then in flight during the second
+    // wait), then its own step s - 1.
+    f4 dr[4], du[4];
+    if (lower) {
+      if (!await_step(up_cnt, ugroups, (unsigned)(s + 1), up_cnt, 0, 0u, abort_word, p.status,
+                      &s_go))
+        return;
+      const int off = (int)((((int64_t)b * T + t) * H4 + nb) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) du[i] = ld_dev4(rg2, off + 64 * i);
+    }
+    if (s > 0) {
+      if (!await_step(lower ? lo_cnt : up_cnt, ugroups, (unsigned)s, up_cnt, 0, 0u, abort_word,
+                      p.status, &s_go))
+        return;
+      const int off = (int)((((int64_t)b * T + t + 1) * H4 + nb) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dr[i] = ld_dev4(lower ? rg1 : rg2, off + 64 * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits on one
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (s > 0) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(dr[e >> 2][e & 3], wa[e >> 2][e & 3], acc, 0, 0,
+                                                   0);
+    }
+    if (lower) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(du[e >> 2][e & 3], wb[e >> 2][e & 3], acc, 0, 0,
+                                                   0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wave][4 * q + v][r] = acc[v];
+    __syncthreads();
+    if (epi) {
+      float sum = part[0][em][eu];
+#pragma unroll
+      for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
+      float dg[4];
+      cell_backward(a, c, cp, dho + sum, dcf, dg, dcf);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) st_dev(dGo + row * H4 + g * H + je, dg[g]);
+    }
+    publish_step(mine, (unsigned)(s + 1));
+  }
+}
+
+// Sets n 32-bit words at p to `bits` (the persistent kernels' counters).
+__global__ void __launch_bounds__(256) fill_bits(unsigned *__restrict__ p, int64_t n, unsigned bits) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (; i < n; i += stride) p[i] = bits;
+}
+
+int fill_words(numrs_hip_ctx *ctx, void *p, int64_t n, unsigned bits) {
+  unsigned grid = grid_for(n, 256);
+  if (grid > 8192) grid = 8192;
+  fill_bits<<<grid, 256, 0, ctx->stream>>>(static_cast<unsigned *>(p), n, bits);
+  return numrs_hip::check_launch(ctx, "fill_bits");
+}
+
+// Whether a persistent kernel's grid can run this call: the context allows
+// it, no graph is being recorded (the cooperative launch is not recorded),
+// the device supports cooperative launches and holds `grid` workgroups of
+// `threads` at once (resident workgroups per CU cached in *per_cu).
+bool persist_fits(numrs_hip_ctx *ctx, const void *kernel, int threads, unsigned grid,
+                  int *per_cu) {
+  if (ctx->capturing || ctx->recurrence_mode != NUMRS_HIP_RECURRENCE_AUTO) return false;
+  if (*per_cu < 0) {
+    int coop = 0, n = 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device) !=
+            hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      coop = 0;
+    }
+    *per_cu = coop ? n : 0;
+  }
+  return (int64_t)*per_cu * ctx->num_cus >= (int64_t)grid;
+}
+
+// Step counters (one per workgroup) and the abort word after them, zeroed,
+// from the context's block cache, and the status word of one persistent
+// launch.
+int persist_words(numrs_hip_ctx *ctx, numrs_hip::TempBlock &cnt, unsigned grid, int **status) {
+  if (int rc = numrs_hip::wait_status_word(ctx, status)) return rc;
+  if (int rc = cnt.alloc((size_t)(grid + 1) * sizeof(unsigned))) return rc;
+  return fill_words(ctx, cnt.p, (int64_t)grid + 1, 0u);
+}
+
+template <typename Args>
+int launch_persist(numrs_hip_ctx *ctx, const void *kernel, unsigned grid, int threads, Args a,
+                   const char *what) {
+  void *args[] = {&a};
+  const hipError_t e =
+      hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_HIP, "cooperative launch of %s failed: %s", what,
+                           hipGetErrorString(e));
+  }
+  ctx->wait_check = true;
+  ++ctx->persist_launches;
+  return NUMRS_HIP_OK;
 }
 
 // Whether the tiled step kernels take this shape.  The forward walks each
@@ -952,11 +1393,24 @@ int numrs_hip_lstm2_forward(numrs_hip_ctx *ctx, const float *x, const float *w_i
   // acts1 <- x W_ih1^T + b1 for every (b, t) row; the upper layer reduces
   // h1 against W_ih2 inside its steps.
   if (int rc = numrs_hip_linear_forward(ctx, x, w_ih1, b1, acts1, B * T, I, 4 * H1)) return rc;
+  const int rgroups = (int)((B + kFRows - 1) / kFRows);
+  if (H1 == kPersistH && H2 == kPersistH && B * T * H1 * 4 < (int64_t{1} << 31)) {
+    const unsigned grid = (unsigned)(2 * rgroups * (kPersistH / kPFUnits));
+    if (persist_fits(ctx, reinterpret_cast<const void *>(lstm2_fwd_persist), 512, grid,
+                     &ctx->persist_fwd_per_cu)) {
+      TempBlock cnt(ctx);
+      int *status = nullptr;
+      if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
+      Lstm2Fwd a{acts1, acts2, w_hh1, w_ih2, w_hh2, b2, h1_seq, c1_seq, h2_seq, c2_seq,
+                 static_cast<unsigned *>(cnt.p), status, (int)B, (int)T};
+      return launch_persist(ctx, reinterpret_cast<const void *>(lstm2_fwd_persist), grid, 512, a,
+                            "lstm2_fwd_persist");
+    }
+  }
   FwdStep lo{acts1, w_hh1, nullptr, nullptr, nullptr, nullptr, nullptr, h1_seq, c1_seq,
              (int)H1, 0, 0};
   FwdStep up{acts2, w_hh2, h1_seq, w_ih2, b2, nullptr, nullptr, h2_seq, c2_seq, (int)H2, (int)H1,
              0};
-  const int rgroups = (int)((B + kFRows - 1) / kFRows);
   const int g_lo = (int)(H1 / kFUnits) * rgroups, g_up = (int)(H2 / kFUnits) * rgroups;
   // Launch d: lower step d and upper step d - 1.
   for (int64_t d = 0; d <= T; ++d) {
@@ -1000,6 +1454,27 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
                                    dh1.f(), dx, dw_ih1, dw_hh1, db1, B, T, I, H1, acc_dx,
                                    acc_dw_ih1, acc_dw_hh1, acc_db1);
   }
+  if (H1 == kPersistH && H2 == kPersistH && B * T * 4 * H1 * 4 < (int64_t{1} << 31)) {
+    const unsigned grid = (unsigned)(2 * ((B + kMRows - 1) / kMRows) * (kPersistH / kMUnits));
+    if (persist_fits(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), 1024, grid,
+                     &ctx->persist_bwd_per_cu)) {
+      {
+        TempBlock cnt(ctx);
+        int *status = nullptr;
+        if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
+        Lstm2Bwd a{dG1.f(), dG2.f(), w_hh1, w_ih2, w_hh2, acts1, c1_seq, acts2, c2_seq, dh2_seq,
+                   static_cast<unsigned *>(cnt.p), status, (int)B, (int)T};
+        if (int rc = launch_persist(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), grid,
+                                    1024, a, "lstm2_bwd_persist"))
+          return rc;
+      }
+      if (int rc = lstm_param_grads(ctx, dG2.f(), h1_seq, w_ih2, h2_seq, nullptr, nullptr, dw_ih2,
+                                    dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2))
+        return rc;
+      return lstm_param_grads(ctx, dG1.f(), x, w_ih1, h1_seq, nullptr, dx, dw_ih1, dw_hh1, db1, B,
+                              T, I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1);
+    }
+  }
   TempBlock dc1(ctx), dc2(ctx), wt1(ctx), wt2(ctx), wtu(ctx);
   if (int rc = dc1.alloc((size_t)(B * H1) * sizeof(float))) return rc;
   if (int rc = dc2.alloc((size_t)(B * H2) * sizeof(float))) return rc;
@@ -1036,6 +1511,18 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
     return rc;
   return lstm_param_grads(ctx, dG1.f(), x, w_ih1, h1_seq, nullptr, dx, dw_ih1, dw_hh1, db1, B, T,
                           I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1);
+}
+
+int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode) {
+  NRS_CHECK_CTX(ctx);
+  if (mode != NUMRS_HIP_RECURRENCE_AUTO && mode != NUMRS_HIP_RECURRENCE_PER_STEP)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "recurrence mode %d", mode);
+  ctx->recurrence_mode = mode;
+  return NUMRS_HIP_OK;
+}
+
+int64_t numrs_hip_persistent_launches(numrs_hip_ctx *ctx) {
+  return ctx == nullptr ? -1 : ctx->persist_launches;
 }
 
 int numrs_hip_time_slice(numrs_hip_ctx *ctx, const float *x, float *y, int64_t B, int64_t T,

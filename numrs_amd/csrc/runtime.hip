@@ -144,6 +144,36 @@ void cache_release(numrs_hip_ctx *ctx) {
   ctx->cached_bytes = 0;
 }
 
+int wait_status_word(numrs_hip_ctx *ctx, int **out) {
+  if (ctx->wait_status == nullptr) {
+    if (ctx->capturing) return refuse_growth(ctx, "the wait status word", sizeof(int));
+    if (hipMalloc(&ctx->wait_status, 256) != hipSuccess) {
+      ctx->wait_status = nullptr;
+      (void)hipGetLastError();
+      return fail(ctx, NUMRS_HIP_E_NOMEM, "wait status allocation failed");
+    }
+    NRS_HIP(ctx, hipMemsetAsync(ctx->wait_status, 0, 256, ctx->stream));
+  }
+  *out = ctx->wait_status;
+  return NUMRS_HIP_OK;
+}
+
+int check_wait_status(numrs_hip_ctx *ctx) {
+  if (!ctx->wait_check || ctx->wait_status == nullptr) return NUMRS_HIP_OK;
+  ctx->wait_check = false;
+  int v = 0;
+  NRS_HIP(ctx, hipMemcpyAsync(&v, ctx->wait_status, sizeof(int), hipMemcpyDeviceToHost,
+                              ctx->stream));
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (v == 0) return NUMRS_HIP_OK;
+  NRS_HIP(ctx, hipMemsetAsync(ctx->wait_status, 0, sizeof(int), ctx->stream));
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return fail(ctx, NUMRS_HIP_E_HIP,
+              "a persistent LSTM recurrence kernel gave up waiting for another workgroup's "
+              "step (code %d): its outputs are invalid",
+              v);
+}
+
 int check_launch(numrs_hip_ctx *ctx, const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -246,6 +276,8 @@ int numrs_hip_destroy(numrs_hip_ctx *ctx) {
   if (ctx->scratch != nullptr) (void)hipFree(ctx->scratch);
   ctx->workspace = ctx->scratch = nullptr;
   numrs_hip::free_retired(ctx);
+  if (ctx->wait_status != nullptr) (void)hipFree(ctx->wait_status);
+  ctx->wait_status = nullptr;
   (void)hipStreamDestroy(ctx->stream);
   ctx->stream = nullptr;
   ctx->destroyed = true;
@@ -439,7 +471,7 @@ int numrs_hip_download(numrs_hip_ctx *ctx, void *host_dst, const void *src, size
     return fail(ctx, NUMRS_HIP_E_INVALID, "numrs_hip_download: null pointer");
   NRS_HIP(ctx, hipMemcpyAsync(host_dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return NUMRS_HIP_OK;
+  return numrs_hip::check_wait_status(ctx);
 }
 
 int numrs_hip_copy(numrs_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
@@ -475,7 +507,7 @@ int numrs_hip_sync(numrs_hip_ctx *ctx) {
   NRS_CHECK_CTX(ctx);
   NRS_NOT_RECORDING(ctx, "numrs_hip_sync");
   NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return NUMRS_HIP_OK;
+  return numrs_hip::check_wait_status(ctx);
 }
 
 int numrs_hip_reserve(numrs_hip_ctx *ctx, size_t bytes) {
@@ -504,7 +536,7 @@ int numrs_hip_timer_elapsed_ms(numrs_hip_ctx *ctx, int slot_start, int slot_end,
     return fail(ctx, NUMRS_HIP_E_INVALID, "bad timer slots %d,%d", slot_start, slot_end);
   NRS_HIP(ctx, hipEventSynchronize(ctx->events[slot_end]));
   NRS_HIP(ctx, hipEventElapsedTime(ms, ctx->events[slot_start], ctx->events[slot_end]));
-  return NUMRS_HIP_OK;
+  return numrs_hip::check_wait_status(ctx);
 }
 
 }  // extern "C"

@@ -159,6 +159,16 @@ class Context:
     def reserve(self, nbytes: int) -> None:
         self._check(L.load().numrs_hip_reserve(self.handle, nbytes))
 
+    def set_recurrence_mode(self, mode: str) -> None:
+        """'auto' (persistent LSTM recurrences where they apply) or 'per_step'
+        (one launch per diagonal step); both give the same bits."""
+        code = {"auto": 0, "per_step": 1}[mode]
+        self._check(L.load().numrs_hip_set_recurrence_mode(self.handle, code))
+
+    def persistent_launches(self) -> int:
+        """Persistent recurrence launches queued on this context so far."""
+        return int(L.load().numrs_hip_persistent_launches(self.handle))
+
     def stream(self) -> int:
         return L.load().numrs_hip_stream(self.handle)
 

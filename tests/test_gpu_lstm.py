@@ -98,3 +98,44 @@ def test_lstm_stack_shared_weight_matches_two_layers(hip_ctx, H, monkeypatch):
     for name, a, b in zip(names, *out):
         scale = max(np.abs(b).max(), 1e-6)
         assert np.abs(a - b).max() <= 1e-5 * scale + 1e-6, name
+
+
+def _forecaster_run(hip_ctx, dims, mode):
+    hip_ctx.set_recurrence_mode(mode)
+    try:
+        layers, hw, hb, x, target = LO.make_c5(seed=11, n_layers=2, **dims)
+        model = nn.LSTMForecaster(layers, hw, hb)
+        xt = Tensor.new(x, True)
+        y = model.forward(xt)
+        loss = y.mse_loss(Tensor.new(target, False))
+        loss.backward()
+        out = {"loss": np.array([loss.item()]), "y": y.values(), "x": xt.gradient(),
+               "head_w": model.head.weight.gradient(), "head_b": model.head.bias.gradient()}
+        for li, layer in enumerate(model.layers):
+            out[f"w_ih{li}"] = layer.w_ih.gradient()
+            out[f"w_hh{li}"] = layer.w_hh.gradient()
+            out[f"b{li}"] = layer.bias.gradient()
+        hip_ctx.sync()
+        return out
+    finally:
+        hip_ctx.set_recurrence_mode("auto")
+
+
+# H = 256 stacked: the persistent forward and backward recurrences (one
+# cooperative launch each) against one launch per diagonal step: the same
+# reduction slices, operand layout and partial order, so the same bits.
+@pytest.mark.parametrize("dims", [dict(B=64, T=128, I=64, H=256), dict(B=20, T=7, I=24, H=256),
+                                  dict(B=16, T=1, I=8, H=256), dict(B=3, T=2, I=256, H=256)],
+                         ids=["baseline", "ragged_rows", "one_step", "two_steps_wide_in"])
+def test_lstm_persistent_equals_per_step(hip_ctx, dims, monkeypatch):
+    print(f"[gpu] lstm persistent vs per-step {dims}", flush=True)
+    nr.set_default_context(hip_ctx)
+    monkeypatch.setattr(nn.LSTMForecaster, "fuse_stack", True)
+    before = hip_ctx.persistent_launches()
+    auto = _forecaster_run(hip_ctx, dims, "auto")
+    ran = hip_ctx.persistent_launches() - before
+    assert ran == 2, f"expected the persistent forward and backward, saw {ran} launches"
+    step = _forecaster_run(hip_ctx, dims, "per_step")
+    assert hip_ctx.persistent_launches() - before == 2
+    for name, v in auto.items():
+        assert np.array_equal(v, step[name]), name
