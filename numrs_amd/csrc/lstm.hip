@@ -618,7 +618,7 @@ __global__ void __launch_bounds__(256)
 constexpr int kMRows = 16, kMUnits = 16, kMWaves = 16;
 
 __device__ __forceinline__ void bwd_step_mfma(const BwdStep &s, int blk, int B, int T) {
-  __shared__ float part[kMWaves][16][16];
+  __shared__ float part[kMWaves][16][16], partu[kMWaves][16][16];
   const int H = s.H, t = s.t;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ugroups = H / kMUnits;
@@ -647,8 +647,8 @@ __device__ __forceinline__ void bwd_step_mfma(const BwdStep &s, int blk, int B, 
 
   const int r = lane & 15, q = lane >> 4;
   const int b = min(b0 + r, B - 1);
-  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto reduce = [&](const float *dbase, int64_t tt, const float *wbase, int Hx) {
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto reduce = [&](f4 &ac, const float *dbase, int64_t tt, const float *wbase, int Hx) {
     const int Hx4 = 4 * Hx;
     const float *drow = dbase + ((int64_t)b * T + tt) * Hx4;
     const float *wrow = wbase + (int64_t)(j0 + r) * Hx4;
@@ -662,19 +662,30 @@ __device__ __forceinline__ void bwd_step_mfma(const BwdStep &s, int blk, int B, 
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(d[e >> 2][e & 3], w[e >> 2][e & 3], acc, 0, 0,
-                                                   0);
+        ac = __builtin_amdgcn_mfma_f32_16x16x4f32(d[e >> 2][e & 3], w[e >> 2][e & 3], ac, 0, 0, 0);
     }
   };
-  if (has_next) reduce(s.dG, t + 1, s.wt, H);
-  if (s.dG_up != nullptr) reduce(s.dG_up, t, s.wt_up, s.Hu);
+  // The two reductions (own recurrence, upper layer's input gradient) in
+  // separate accumulators, each summed over the waves in order, then added:
+  // the persistent kernels form the second one in other workgroups.
+  if (has_next) reduce(acc, s.dG, t + 1, s.wt, H);
+  if (s.dG_up != nullptr) reduce(accu, s.dG_up, t, s.wt_up, s.Hu);
 #pragma unroll
-  for (int v = 0; v < 4; ++v) part[wave][4 * q + v][r] = acc[v];
+  for (int v = 0; v < 4; ++v) {
+    part[wave][4 * q + v][r] = acc[v];
+    partu[wave][4 * q + v][r] = accu[v];
+  }
   __syncthreads();
   if (!epi) return;
   float sum = part[0][em][eu];
 #pragma unroll
   for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
+  if (s.dG_up != nullptr) {
+    float sumu = partu[0][em][eu];
+#pragma unroll
+    for (int w = 1; w < kMWaves; ++w) sumu += partu[w][em][eu];
+    sum = sum + sumu;
+  }
   float dg[4], dcf;
   cell_backward(a, c, cp, dho + sum, dcn, dg, dcf);
 #pragma unroll
@@ -946,18 +957,22 @@ struct Lstm2Bwd {
   const float *whh1, *wih2, *whh2;        // [4H, H]
   const float *acts1, *c1, *acts2, *c2;   // forward's saved values
   const float *dh2;                       // [B, T, H] gradient at the upper h, or null
-  unsigned *count;  // [rgroups][2][H / kMUnits] steps done (upper, lower), then the abort word
+  float *up_in;   // [B, T, H] the lower layer's input-gradient term dG2_t W_ih2 per cell
+  unsigned *count;  // [rgroups][3][H / kMUnits] steps done (upper, lower, helper), then abort
   int *status;
   int B, T;
 };
 
-// Backward: workgroups [0, n) run the upper layer, [n, 2n) the lower one;
-// workgroup (row group rg, unit group ug) owns rows b0..b0+15 and units
-// j0..j0+15 (kMRows x kMUnits, as lstm_bwd_diag_mfma), its 16 waves each a
-// sixteenth of the 4H-long reductions, threads 0..255 one cell each.  Step
-// s runs t = T-1-s: upper dh = dh2 + dG2_{t+1} W_hh2 (its own previous step),
-// lower dh = dG1_{t+1} W_hh1 + dG2_t W_ih2 (its own previous step and the
-// upper layer's step s).
+// Backward: workgroups [0, n) run the upper layer, [n, 2n) the lower one and
+// [2n, 3n) help the lower one; workgroup (row group rg, unit group ug) owns
+// rows b0..b0+15 and units j0..j0+15 (kMRows x kMUnits, as
+// lstm_bwd_diag_mfma), its 16 waves each a sixteenth of a 4H-long reduction,
+// threads 0..255 one cell each.  Step s runs t = T-1-s.  Upper: dh = dh2 +
+// dG2_{t+1} W_hh2 (its own previous step).  Helper: dG2_t W_ih2 for its
+// tile into up_in, as soon as the upper step s is done (the upper chain runs
+// ahead).  Lower: dh = dG1_{t+1} W_hh1 (its own previous step) + up_in
+// (the helper's step s), so the lower chain's own step carries one
+// reduction, like the upper one.
 __global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
   constexpr int H = kPersistH, H4 = 4 * H;
   constexpr int ugroups = H / kMUnits;
@@ -965,88 +980,83 @@ __global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
   __shared__ int s_go;
   const int B = p.B, T = p.T;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int per_layer = (int)gridDim.x / 2;
-  const bool lower = (int)blockIdx.x >= per_layer;
-  const int blk = lower ? (int)blockIdx.x - per_layer : (int)blockIdx.x;
+  const int per_layer = (int)gridDim.x / 3;
+  const int role = (int)blockIdx.x / per_layer;  // 0 upper, 1 lower, 2 helper
+  const int blk = (int)blockIdx.x - role * per_layer;
   const int ug = blk % ugroups, rg = blk / ugroups;
   const int j0 = ug * kMUnits, b0 = rg * kMRows;
   const int r = lane & 15, q = lane >> 4;
   const int b = min(b0 + r, B - 1);
   const int nb = wave * (H4 / kMWaves) + 4 * q;  // this lane's offset in the wave's 64-long block
 
-  // B operands: W[n][j0 + r] for n = nb + 16 i + e (strided loads, once):
-  // wa from the layer's own W_hh, wb (lower layer) from W_ih2.
-  f4 wa[4], wb[4];
+  // B operands W[n][j0 + r] for n = nb + 16 i + e (strided loads, once):
+  // upper W_hh2, lower W_hh1, helper W_ih2.
+  f4 w[4];
   {
-    const float *srca = (lower ? p.whh1 : p.whh2) + j0 + r;
-    const float *srcb = p.wih2 + j0 + r;
+    const float *src = (role == 0 ? p.whh2 : role == 1 ? p.whh1 : p.wih2) + j0 + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t n = nb + 16 * i + e;
-        wa[i][e] = srca[n * H];
-        wb[i][e] = lower ? srcb[n * H] : 0.0f;
-      }
+      for (int e = 0; e < 4; ++e) w[i][e] = src[(int64_t)(nb + 16 * i + e) * H];
   }
   const int64_t gbytes = (int64_t)B * T * H4 * 4;
-  const __amdgpu_buffer_rsrc_t rg1 = dev_rsrc(p.dG1, gbytes), rg2 = dev_rsrc(p.dG2, gbytes);
+  // the reduction's operand rows: the layer's own dG (step t + 1), or the
+  // helper's dG2 (step t)
+  const __amdgpu_buffer_rsrc_t rsrc = dev_rsrc(role == 1 ? p.dG1 : p.dG2, gbytes);
   const int tid = threadIdx.x;
   const int em = tid >> 4, eu = tid & 15;
   const int be = b0 + em, je = j0 + eu;
   const bool epi = tid < 256 && be < B;
   float dcf = 0.0f;  // dc_{t+1} f_{t+1} of the cell (0 before its last step)
-  const float *acts = lower ? p.acts1 : p.acts2;
-  const float *cs = lower ? p.c1 : p.c2;
-  float *dGo = lower ? p.dG1 : p.dG2;
-  unsigned *up_cnt = p.count + rg * 2 * ugroups;  // the row group's upper, then lower counters
-  unsigned *lo_cnt = up_cnt + ugroups;
-  unsigned *mine = (lower ? lo_cnt : up_cnt) + ug;
+  const float *acts = role == 1 ? p.acts1 : p.acts2;
+  const float *cs = role == 1 ? p.c1 : p.c2;
+  float *dGo = role == 1 ? p.dG1 : p.dG2;
+  unsigned *up_cnt = p.count + rg * 3 * ugroups;  // the row group's upper, lower, helper counters
+  unsigned *lo_cnt = up_cnt + ugroups, *hp_cnt = lo_cnt + ugroups;
+  unsigned *mine = up_cnt + role * ugroups + ug;
   unsigned *abort_word = p.count + gridDim.x;
 
   for (int s = 0; s < T; ++s) {
     const int t = T - 1 - s;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, c = 0.0f, cp = 0.0f, dho = 0.0f;
     const int64_t row = (int64_t)be * T + t;
-    if (epi) {
+    if (epi && role != 2) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) a[g] = acts[row * H4 + g * H + je];
       c = cs[row * H + je];
       cp = t > 0 ? cs[(row - 1) * H + je] : 0.0f;
-      if (!lower && p.dh2 != nullptr) dho = p.dh2[row * H + je];
+      if (role == 0 && p.dh2 != nullptr) dho = p.dh2[row * H + je];
     }
-    // Upper: its step s - 1 done.  Lower: first the upper step s (the upper
-    // chain runs ahead: its loads are then in flight during the second
-    // wait), then its own step s - 1.
-    f4 dr[4], du[4];
-    if (lower) {
-      if (!await_step(up_cnt, ugroups, (unsigned)(s + 1), up_cnt, 0, 0u, abort_word, p.status,
-                      &s_go))
-        return;
-      const int off = (int)((((int64_t)b * T + t) * H4 + nb) * 4);
+    // upper: its step s - 1; lower: its step s - 1 and the helper's step s;
+    // helper: the upper step s
+    bool go = true;
+    if (role == 0) {
+      if (s > 0)
+        go = await_step(up_cnt, ugroups, (unsigned)s, up_cnt, 0, 0u, abort_word, p.status, &s_go);
+    } else if (role == 1) {
+      go = await_step(lo_cnt, s > 0 ? ugroups : 0, (unsigned)s, hp_cnt + ug, 1, (unsigned)(s + 1),
+                      abort_word, p.status, &s_go);
+    } else {
+      go = await_step(up_cnt, ugroups, (unsigned)(s + 1), up_cnt, 0, 0u, abort_word, p.status,
+                      &s_go);
+    }
+    if (!go) return;
+    const bool red = role == 2 || s > 0;  // this step has a reduction
+    f4 d[4];
+    if (red) {
+      const int off = (int)((((int64_t)b * T + (role == 2 ? t : t + 1)) * H4 + nb) * 4);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) du[i] = ld_dev4(rg2, off + 64 * i);
+      for (int i = 0; i < 4; ++i) d[i] = ld_dev4(rsrc, off + 64 * i);
     }
-    if (s > 0) {
-      if (!await_step(lower ? lo_cnt : up_cnt, ugroups, (unsigned)s, up_cnt, 0, 0u, abort_word,
-                      p.status, &s_go))
-        return;
-      const int off = (int)((((int64_t)b * T + t + 1) * H4 + nb) * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dr[i] = ld_dev4(lower ? rg1 : rg2, off + 64 * i);
-    }
+    float upin = 0.0f;
+    if (epi && role == 1)
+      upin = __hip_atomic_load(p.up_in + row * H + je, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA waits on one
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (s > 0) {
+    if (red) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(dr[e >> 2][e & 3], wa[e >> 2][e & 3], acc, 0, 0,
-                                                   0);
-    }
-    if (lower) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(du[e >> 2][e & 3], wb[e >> 2][e & 3], acc, 0, 0,
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(d[e >> 2][e & 3], w[e >> 2][e & 3], acc, 0, 0,
                                                    0);
     }
 #pragma unroll
@@ -1055,11 +1065,16 @@ __global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
     if (epi) {
       float sum = part[0][em][eu];
 #pragma unroll
-      for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
-      float dg[4];
-      cell_backward(a, c, cp, dho + sum, dcf, dg, dcf);
+      for (int k = 1; k < kMWaves; ++k) sum += part[k][em][eu];
+      if (role == 2) {
+        st_dev(p.up_in + row * H + je, sum);
+      } else {
+        if (role == 1) sum = sum + upin;  // (dh2 is null for the lower layer)
+        float dg[4];
+        cell_backward(a, c, cp, dho + sum, dcf, dg, dcf);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) st_dev(dGo + row * H4 + g * H + je, dg[g]);
+        for (int g = 0; g < 4; ++g) st_dev(dGo + row * H4 + g * H + je, dg[g]);
+      }
     }
     publish_step(mine, (unsigned)(s + 1));
   }
@@ -1455,15 +1470,16 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
                                    acc_dw_ih1, acc_dw_hh1, acc_db1);
   }
   if (H1 == kPersistH && H2 == kPersistH && B * T * 4 * H1 * 4 < (int64_t{1} << 31)) {
-    const unsigned grid = (unsigned)(2 * ((B + kMRows - 1) / kMRows) * (kPersistH / kMUnits));
+    const unsigned grid = (unsigned)(3 * ((B + kMRows - 1) / kMRows) * (kPersistH / kMUnits));
     if (persist_fits(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), 1024, grid,
                      &ctx->persist_bwd_per_cu)) {
       {
-        TempBlock cnt(ctx);
+        TempBlock cnt(ctx), up_in(ctx);
         int *status = nullptr;
         if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
+        if (int rc = up_in.alloc((size_t)(B * T * H1) * sizeof(float))) return rc;
         Lstm2Bwd a{dG1.f(), dG2.f(), w_hh1, w_ih2, w_hh2, acts1, c1_seq, acts2, c2_seq, dh2_seq,
-                   static_cast<unsigned *>(cnt.p), status, (int)B, (int)T};
+                   up_in.f(), static_cast<unsigned *>(cnt.p), status, (int)B, (int)T};
         if (int rc = launch_persist(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), grid,
                                     1024, a, "lstm2_bwd_persist"))
           return rc;
