@@ -409,16 +409,16 @@ __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, 
   if (has_h && s.xin != nullptr && H == 256 && s.I == 256) {
     // a stacked layer at H = I = 256 (one 64-long block per wave and operand
     // pair): both pairs' operands are loaded before either's MFMAs, one
-    // memory round trip instead of two; the MFMAs run in the order above
+    // memory round trip instead of two; the MFMAs run in the order below
     const float *xrow = s.xin + ((int64_t)b * T + t) * s.I;
     const int kb = wave * 64;
     f4 a[2][4], w[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      a[0][i] = *reinterpret_cast<const f4 *>(hrow + kb + 16 * i + 4 * q);
-      w[0][i] = *reinterpret_cast<const f4 *>(s.whh + wr * H + kb + 16 * i + 4 * q);
-      a[1][i] = *reinterpret_cast<const f4 *>(xrow + kb + 16 * i + 4 * q);
-      w[1][i] = *reinterpret_cast<const f4 *>(s.wih + wr * s.I + kb + 16 * i + 4 * q);
+      a[0][i] = *reinterpret_cast<const f4 *>(xrow + kb + 16 * i + 4 * q);
+      w[0][i] = *reinterpret_cast<const f4 *>(s.wih + wr * s.I + kb + 16 * i + 4 * q);
+      a[1][i] = *reinterpret_cast<const f4 *>(hrow + kb + 16 * i + 4 * q);
+      w[1][i] = *reinterpret_cast<const f4 *>(s.whh + wr * H + kb + 16 * i + 4 * q);
     }
 #pragma unroll
     for (int pq = 0; pq < 2; ++pq)
@@ -427,8 +427,10 @@ __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, 
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[pq][e >> 2][e & 3], w[pq][e >> 2][e & 3], acc,
                                                    0, 0, 0);
   } else {
-    if (has_h) reduce(hrow, s.whh + wr * H, H);
+    // a stacked layer's input reduction first (the persistent kernel forms it
+    // while it waits for the recurrent operand), then the recurrent one
     if (s.xin != nullptr) reduce(s.xin + ((int64_t)b * T + t) * s.I, s.wih + wr * s.I, s.I);
+    if (has_h) reduce(hrow, s.whh + wr * H, H);
   }
 #pragma unroll
   for (int v = 0; v < 4; ++v) part[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
@@ -889,43 +891,41 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) gin[g] = p.acts1[row * H4 + g * H + je];
     }
-    // Lower: h1 at t - 1 done.  Upper: first h1 at t (the lower chain, which
-    // runs ahead: its loads are then in flight during the second wait), then
-    // h2 at t - 1.
-    f4 ar[4], ai[4];
+    // Lower: h1 at t - 1 done, then h1_{t-1} W_hh1^T.  Upper: first h1 at t
+    // (the lower chain, which runs ahead) and h1_t W_ih2^T, whose MFMAs then
+    // run during the second wait, for h2 at t - 1; then h2_{t-1} W_hh2^T onto
+    // the same accumulator (the per-step kernels' order).  Every load is
+    // issued before the MFMAs that wait on it (the scheduler would otherwise
+    // issue later loads after earlier MFMAs, exposing their latencies one
+    // after another).
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (upper) {
       if (!await_step(lo_cnt, ugroups, (unsigned)(t + 1), lo_cnt, 0, 0u, abort_word, p.status,
                       &s_go))
         return;
       const int off = (int)((((int64_t)b * T + t) * H + kb) * 4);
+      f4 ai[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ai[i] = ld_dev4(rh1, off + 64 * i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ai[e >> 2][e & 3], wb[e >> 2][e & 3], acc, 0, 0,
+                                                   0);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (t > 0) {
       if (!await_step(upper ? up_cnt : lo_cnt, ugroups, (unsigned)t, lo_cnt, 0, 0u, abort_word,
                       p.status, &s_go))
         return;
       const int off = (int)((((int64_t)b * T + t - 1) * H + kb) * 4);
+      f4 ar[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ar[i] = ld_dev4(upper ? rh2 : rh1, off + 64 * i);
-    }
-    // every load issued before the first MFMA waits on one (the scheduler
-    // would otherwise issue later loads after earlier MFMAs, exposing their
-    // latencies one after another)
-    __builtin_amdgcn_sched_barrier(0);
-    // lower: h1_{t-1} W_hh1^T; upper: h2_{t-1} W_hh2^T, then h1_t W_ih2^T
-    // (the per-step kernels' order)
-    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (t > 0) {
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[e >> 2][e & 3], wa[e >> 2][e & 3], acc, 0, 0,
-                                                   0);
-    }
-    if (upper) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ai[e >> 2][e & 3], wb[e >> 2][e & 3], acc, 0, 0,
                                                    0);
     }
 #pragma unroll
