@@ -245,13 +245,58 @@ def traffic_probe(ctx, rng, reps: int = 3) -> None:
         ctx.adam_step(p, g, m, v, t + 1, lr=1e-3)
         ctx.sync()
         del p, g, m, v
+    # The HBM rows of bench.py --rows below 0.70 of the HBM peak, each at its
+    # row's shape on fresh operands: a25 full sum and a5 bias unbroadcast of
+    # a 4096^2 gradient, a11 transpose 4096^2, N2 LayerNorm backward
+    # [32768, 512], N5 row argmax [16384, 1024], a18 MSE backward [4096, 512].
+    lib = L.load()
+    for _ in range(reps):
+        g = ctx.to_device(randn(rng, (R, C)))
+        ctx._check(lib.numrs_hip_sum(ctx.handle, g.ptr, R * C, 0, s.ptr))
+        ctx.sync()
+        del g
+    for _ in range(reps):
+        g, b = ctx.to_device(randn(rng, (R, C))), ctx.empty((C,))
+        ctx.sum_to_shape(g, b)
+        ctx.sync()
+        del g, b
+    for _ in range(reps):
+        g, tr = ctx.to_device(randn(rng, (R, C))), ctx.empty((C, R))
+        ctx._check(lib.numrs_hip_transpose(ctx.handle, g.ptr, tr.ptr, R, C))
+        ctx.sync()
+        del g, tr
+    RL, CL = 32768, 512
+    gam = ctx.to_device(np.ones(CL, np.float32))
+    dgm, dbt = ctx.empty((CL,)), ctx.empty((CL,))
+    for _ in range(reps):
+        gl, xl = ctx.to_device(randn(rng, (RL, CL))), ctx.to_device(randn(rng, (RL, CL)))
+        mean, rstd = ctx.to_device(randn(rng, RL)), ctx.to_device(np.ones(RL, np.float32))
+        dxl = ctx.empty((RL, CL))
+        ctx._check(lib.numrs_hip_layernorm_backward(ctx.handle, gl.ptr, xl.ptr, gam.ptr, mean.ptr,
+                                                    rstd.ptr, dxl.ptr, dgm.ptr, dbt.ptr, RL, CL, 0,
+                                                    0, 0))
+        ctx.sync()
+        del gl, xl, mean, rstd, dxl
+    for _ in range(reps):
+        am, idx = ctx.to_device(randn(rng, (16384, 1024))), ctx.empty((16384,), np.int32)
+        ctx.argmax_rows(am, idx)
+        ctx.sync()
+        del am, idx
+    g1 = ctx.to_device(np.array([0.75], np.float32))
+    for _ in range(reps):
+        pm, tm, dp = (ctx.to_device(randn(rng, (4096, 512))), ctx.to_device(randn(rng, (4096, 512))),
+                      ctx.empty((4096, 512)))
+        ctx.mse_backward(g1, pm, tm, dp)
+        ctx.sync()
+        del pm, tm, dp
     log(f"traffic probe: {reps} copies of {COPY_PROBE_BYTES} B, {reps} matmul_backward 2048^3, "
-        f"{reps} relu+bias 4096^2, {reps} Adam 2^24")
+        f"{reps} relu+bias 4096^2, {reps} Adam 2^24, {reps} each of the a25, a5, a11, N2, N5 "
+        f"and a18 rows")
 
 
 def _pmc_per_dispatch(directory: str, counter: str) -> dict:
-    """Mean value of `counter` per dispatch, by kernel name, from a rocprofv3
-    --pmc -f csv output directory."""
+    """The values of `counter`, one per dispatch in dispatch order, by
+    kernel name, from a rocprofv3 --pmc -f csv output directory."""
     import csv
     import glob
     files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
@@ -268,23 +313,43 @@ def _pmc_per_dispatch(directory: str, counter: str) -> dict:
                     raise ValueError(f"{counter}: two records for dispatch {key}")
                 per[key] = float(row["Counter_Value"])
     out = {}
-    for (name, _), v in per.items():
+    for (name, did), v in sorted(per.items(), key=lambda kv: int(kv[0][1])):
         out.setdefault(name, []).append(v)
-    return {k: (float(np.mean(v)), len(v)) for k, v in out.items()}
+    return out  # kernel name -> values in dispatch order
 
 
 # Kernels of the traffic probe: (profile name, workload, [(kernel-name part,
-# access mode)] whose dispatches make up one launch of the workload,
+# access mode, group)] whose dispatches make up one launch of the workload,
 # algorithmic bytes).  Mode "nt": the kernel streams with non-temporal
 # accesses, and its counters are scaled by the non-temporal calibration pair.
+# Group g: the probe's (g+1)-th run of `reps` dispatches of that kernel (the
+# probe launches its workloads in a fixed order, and some kernels serve
+# several of them: reduce_pass1<0, 2> the calibration sum and the a25 row,
+# reduce_final the three sums, colreduce_finalize the C3 relu+bias, a5 and
+# N2 rows).
 TRAFFIC_KERNELS = [
-    ("matmul_backward_2048", "C2 2048^3", [(HEAD_KERNEL, "cached")],
+    ("matmul_backward_2048", "C2 2048^3", [(HEAD_KERNEL, "cached", 0)],
      5 * 2048 * 2048 * 4),                          # read A, B, dC; write dA, dB
     ("relu_bias_4096", "C3 relu(X+b) backward 4096^2",
-     [("colreduce_pass1<true", "nt"), ("colreduce_finalize", "cached")],
+     [("colreduce_pass1<true", "nt", 0), ("colreduce_finalize", "cached", 0)],
      12 * 4096 * 4096 + 4 * 4096),                  # read g, z; write dx; write db
-    ("adam_16m", "C3 Adam step 2^24 params", [("adam_kernel", "nt")],
+    ("adam_16m", "C3 Adam step 2^24 params", [("adam_kernel", "nt", 0)],
      28 * (1 << 24)),                               # read p, g, m, v; write p, m, v
+    ("sum_full_4096", "a25 ops::sum of 4096^2", [("::reduce_pass1<0, 2>", "nt", 1),
+                                                 ("::reduce_final", "cached", 2)],
+     4 * 4096 * 4096),                              # read g
+    ("unbroadcast_bias_4096", "a5 unbroadcast [4096,4096] -> [4096]",
+     [("colreduce_pass1<false, 2>", "nt", 0), ("colreduce_finalize", "cached", 1)],
+     4 * 4096 * 4096 + 4 * 4096),                   # read g; write db
+    ("transpose_4096", "a11 transpose 4096^2", [("transpose_reg_kernel<2>", "nt", 0)],
+     8 * 4096 * 4096),                              # read x; write x^T
+    ("layernorm_backward_32768x512", "N2 LayerNorm backward [32768,512]",
+     [("layernorm_bwd_vec<2, 2>", "nt", 0), ("colreduce_finalize", "cached", 2)],
+     12 * 32768 * 512 + 8 * 32768),                 # read g, x; write dx; read mean, rstd
+    ("argmax_16384x1024", "N5 argmax rows [16384,1024]", [("argmax_vec<4, false, 2>", "nt", 0)],
+     4 * 16384 * 1024 + 4 * 16384),                 # read x; write idx
+    ("mse_backward_4096x512", "a18 mse_backward [4096,512]", [("mse_bwd_kernel<1>", "cached", 0)],
+     12 * 4096 * 512),                              # read p, t; write dp
 ]
 
 
@@ -299,17 +364,18 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> list:
     fetch = _pmc_per_dispatch(fetch_dir, "FETCH_SIZE")
     write = _pmc_per_dispatch(write_dir, "WRITE_SIZE")
 
-    def pick(d, part, reps=3):
-        # The probe makes `reps` dispatches of each kernel; a short or padded
-        # record set is refused.
+    def pick(d, part, group=0, reps=3):
+        # The probe makes `reps` dispatches of a kernel per workload that
+        # uses it; a record set that is not a whole number of such runs, or
+        # lacks the asked-for run, is refused.
         keys = [k for k in d if part in k]
         if len(keys) != 1:
             raise KeyError(f"{part}: {keys}")
-        mean, count = d[keys[0]]
-        if count != reps:
-            raise ValueError(f"{part}: {count} dispatch records, expected {reps}: the counter "
-                             f"output is incomplete")
-        return mean
+        vals = d[keys[0]]
+        if len(vals) % reps or len(vals) < (group + 1) * reps:
+            raise ValueError(f"{part}: {len(vals)} dispatch records, expected a multiple of "
+                             f"{reps} covering run {group}: the counter output is incomplete")
+        return float(np.mean(vals[group * reps:(group + 1) * reps]))
 
     known_kib = COPY_PROBE_BYTES / 1024.0
     small_kib = 4.0 * (1 << 22) / 1024.0
@@ -323,12 +389,13 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> list:
     out = []
     for name, workload, parts, algorithmic in TRAFFIC_KERNELS:
         f_raw = w_raw = traffic = 0.0
-        for part, mode in parts:
-            f, w = pick(fetch, part), pick(write, part)
+        for part, mode, group in parts:
+            f, w = pick(fetch, part, group), pick(write, part, group)
             f_raw, w_raw = f_raw + f, w_raw + w
             traffic += (f * fac[mode][0] + w * fac[mode][1]) * 1024.0
-        out.append({"name": name, "kernel": "+".join(p for p, _ in parts), "workload": workload,
-                    "modes": [m for _, m in parts], "fetch_kib_raw": f_raw, "write_kib_raw": w_raw,
+        out.append({"name": name, "kernel": "+".join(p for p, _, _ in parts),
+                    "workload": workload, "modes": [m for _, m, _ in parts],
+                    "fetch_kib_raw": f_raw, "write_kib_raw": w_raw,
                     "calibration_kib_raw": {m: list(v) for m, v in cal.items()},
                     "calibration_bytes": COPY_PROBE_BYTES,
                     "factors": {m: list(v) for m, v in fac.items()},
@@ -458,7 +525,7 @@ def bench_relu_bias(ctx, rng, rows, cols, steps, warmup):
     total, per = time_launches(ctx, launch, steps, warmup, "C3 relu")
     _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup, "C3 relu")
     return {"ms_per_step": total / steps, "kernel_ms": per, "resident_ms": resident,
-            "sets": k, "bytes": nbytes}
+            "sets": k, "bytes": nbytes, "inputs": (g, z)}
 
 
 def bench_adam(ctx, rng, n, steps, warmup):
@@ -642,7 +709,7 @@ def cpu_baseline(A, B, dC, rows_a: int, rows_b: int):
         "sample": (f"C restatement of numrs matmul_backward (oracle/numrs_oracle.c, fp32 triple "
                    f"loops of backward.rs:123-146, single-threaded as there), {rows_a} of {M} dA "
                    f"rows ({ta:.2f} s) + {rows_b} of {K} dB rows ({tb:.2f} s), scaled to the "
-                   f"full 2048^3 step ({full_s:.1f} s); {cpu['logical_cpus']} logical CPUs, "
+                   f"full {M}x{K}x{N} step ({full_s:.1f} s); {cpu['logical_cpus']} logical CPUs, "
                    f"{cpu['usable_cpus']} usable, 1 thread used"),
     }
 
@@ -707,6 +774,89 @@ def cpu_baseline_adam(n: int, sample: int = 1 << 22) -> dict:
             "cores": 1, "kind": "port", "cpu_model": host_cpu()["model"],
             "sample": f"first {sample:,} of {n:,} params ({dt * sample / n * 1e3:.1f} ms), "
                       f"scaled x{n / sample:g}"}
+
+
+def cpu_baseline_relu_bias(g, z, sample: int = 1 << 22) -> dict:
+    """numrs's backward of y = relu(X + b) on the host: relu_backward
+    (backward.rs:152-163, one thread, scalar) over the first `sample`
+    elements scaled to the whole [R, C], then add_backward's unbroadcast of
+    the bias, which numrs forms as ops::sum of everything (backward.rs:12-39)
+    added into db[0] (tensor.rs:120-132), timed on the whole array on all
+    usable cores (at most 16) in the AVX2 8-lane chunk order of
+    simd.rs:247-283.  GB/s over the GPU row's algorithmic bytes."""
+    from oracle import oracle as O
+
+    R, C = g.shape
+    n = R * C
+    gs, zs = g.ravel()[:sample], z.ravel()[:sample]
+    O.relu_backward(gs, zs)  # page in
+    t0 = time.perf_counter()
+    O.relu_backward(gs, zs)
+    t_relu = (time.perf_counter() - t0) * n / sample
+    dz = O.relu_backward(g, z).ravel()
+    nt = cpu_threads()
+    O.sum_avx2_order_mt(dz, nt)
+    t0 = time.perf_counter()
+    O.sum_avx2_order_mt(dz, nt)
+    t_sum = time.perf_counter() - t0
+    tot = t_relu + t_sum
+    return {"value": round((12.0 * n + 4.0 * C) / tot / 1e9, 3), "unit": "GB/s",
+            "ms": round(tot * 1e3, 2), "cores": nt, "kind": "port", "cpu_model": host_cpu()["model"],
+            "sample": f"relu_backward on the first {sample:,} of {n:,} elements on 1 thread "
+                      f"({t_relu * sample / n * 1e3:.1f} ms, scaled x{n / sample:g}); the bias "
+                      f"unbroadcast as numrs forms it, ops::sum of all {n:,} elements on {nt} "
+                      f"threads x 8-lane AVX2 order ({t_sum * 1e3:.1f} ms)"}
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        return max([int(d.get("num_threads", 1)) for d in threadpool_info()
+                    if d.get("user_api") == "blas"] or [1])
+    except Exception:  # noqa: BLE001  (the count is a label only)
+        return 0
+
+
+def cpu_baseline_c4() -> dict:
+    """No numrs CPU path exists for C4 (the reference has no attention,
+    LayerNorm or GELU).  A clearly non-numrs CPU point instead: the same
+    block's forward and backward in fp32 numpy (oracle/transformer_oracle.py,
+    host BLAS for the products), one step."""
+    from oracle import transformer_oracle as TO
+    from workloads import make_c4
+
+    w, x, t, dims = make_c4(seed=4)
+    TO.block(w, x[:256], t[:256], (1,) + dims[1:], dtype=np.float32)  # warm the BLAS
+    t0 = time.perf_counter()
+    TO.block(w, x, t, dims, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    fwd, bwd = c4_flops()
+    return {"value": round(dt * 1e3, 1), "unit": "ms/step", "tflops": round((fwd + bwd) / dt / 1e12, 3),
+            "cores": _blas_threads(), "kind": "port", "cpu_model": host_cpu()["model"],
+            "sample": "not numrs (the reference has no attention, LayerNorm or GELU): the block's "
+                      "forward + backward in fp32 numpy with host BLAS (oracle/transformer_oracle.py), "
+                      "one whole step; cores = BLAS threads"}
+
+
+def cpu_baseline_c5() -> dict:
+    """No numrs CPU path exists for C5 (the reference has no recurrent
+    layer).  A clearly non-numrs CPU point instead: the forecaster's forward
+    and BPTT in fp32 numpy (oracle/lstm_oracle.py, host BLAS for the per-step
+    products), one step."""
+    from oracle import lstm_oracle as LO
+    from workloads import make_c5
+
+    layers, hw, hb, x, target = make_c5(seed=5)
+    LO.forecaster(layers, hw, hb, x[:, :4], target, dtype=np.float32)  # warm the BLAS
+    t0 = time.perf_counter()
+    LO.forecaster(layers, hw, hb, x, target, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    fwd, bwd = c5_flops()
+    return {"value": round(dt * 1e3, 1), "unit": "ms/step", "tflops": round((fwd + bwd) / dt / 1e12, 3),
+            "cores": _blas_threads(), "kind": "port", "cpu_model": host_cpu()["model"],
+            "sample": "not numrs (the reference has no recurrent layer): the forecaster's forward + "
+                      "BPTT in fp32 numpy with host BLAS (oracle/lstm_oracle.py), one whole step; "
+                      "cores = BLAS threads"}
 
 
 ROW_ELEMS = (4096, 4096)  # BASELINE configs[2] (C3), the elementwise/broadcast config
@@ -1024,6 +1174,49 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
                Dq, dq_[i].ptr, dk_[i].ptr, dv_[i].ptr, Bq, Sq, Hq, Dq, 0)),
            note="four products per key group, no dS buffer; no numrs CPU path")
     del q_, k_, v_, do_, P_, o_, dq_, dk_, dv_
+    # N4 two stacked LSTM layers at C5 (batch 64, seq 128, in 64, hidden 256):
+    # the forward entry point (input projection of layer 1 + the persistent
+    # recurrence of both layers) and the backward one (persistent recurrence
+    # + the weight gradients and dx batched over time).  Latency-bound: 128
+    # dependent steps per direction; the fraction is of the fp32 MFMA peak.
+    from workloads import make_c5
+    layers5, _, _, x5, _ = make_c5(seed=5)
+    B5, T5, I5 = x5.shape
+    H5 = layers5[0]["w_hh"].shape[1]
+    lw = [{kk: ctx.to_device(vv) for kk, vv in l.items()} for l in layers5]
+    x5_ = ctx.to_device(x5)
+    seq = [ctx.empty((B5, T5, H5)) for _ in range(4)]       # h1, c1, h2, c2
+    acts = [ctx.empty((B5, T5, 4 * H5)) for _ in range(2)]  # acts1, acts2
+    dh2_ = ctx.to_device(f32((B5, T5, H5)))
+    dx5_ = ctx.empty((B5, T5, I5))
+    dws = [ctx.empty(l[kk].shape) for l in layers5 for kk in ("w_ih", "w_hh", "b")]
+    lib = L.load()
+
+    def lstm_fwd(i):
+        ctx._check(lib.numrs_hip_lstm2_forward(
+            ctx.handle, x5_.ptr, lw[0]["w_ih"].ptr, lw[0]["w_hh"].ptr, lw[0]["b"].ptr,
+            lw[1]["w_ih"].ptr, lw[1]["w_hh"].ptr, lw[1]["b"].ptr, seq[0].ptr, seq[1].ptr,
+            acts[0].ptr, seq[2].ptr, seq[3].ptr, acts[1].ptr, B5, T5, I5, H5, H5))
+
+    def lstm_bwd(i):
+        ctx._check(lib.numrs_hip_lstm2_backward(
+            ctx.handle, x5_.ptr, lw[0]["w_ih"].ptr, lw[0]["w_hh"].ptr, lw[1]["w_ih"].ptr,
+            lw[1]["w_hh"].ptr, seq[0].ptr, seq[1].ptr, acts[0].ptr, seq[2].ptr, seq[3].ptr,
+            acts[1].ptr, dh2_.ptr, dx5_.ptr, dws[0].ptr, dws[1].ptr, dws[2].ptr, dws[3].ptr,
+            dws[4].ptr, dws[5].ptr, B5, T5, I5, H5, H5, 0, 0, 0, 0, 0, 0, 0))
+
+    prod = 2.0 * B5 * T5 * 4 * H5  # flops per unit of reduction length, all steps
+    fwd_flops = prod * I5 + 3 * prod * H5          # x W_ih1^T, then h1 W_hh1^T, h1 W_ih2^T, h2 W_hh2^T
+    bwd_flops = 3 * prod * H5 + 3 * prod * H5 + 2 * prod * I5  # recurrences; dW_ih2, dW_hh2, dW_hh1; dW_ih1, dx
+    lstm_fwd(0)
+    record("N4", "LSTM x2 forward (new op)", "linear_forward + lstm2_fwd_persist",
+           f"B {B5}, T {T5}, in {I5}, hidden {H5} (C5)", flops=fwd_flops, launch=lstm_fwd,
+           note="one persistent launch for all 128 steps of both layers; no numrs CPU path")
+    record("N4", "LSTM x2 backward (new op)", "lstm2_bwd_persist + weight-gradient GEMMs",
+           f"B {B5}, T {T5}, in {I5}, hidden {H5} (C5)", flops=bwd_flops, launch=lstm_bwd,
+           note="one persistent launch for all 128 steps of both layers, then the weight "
+                "gradients over all steps as single products; no numrs CPU path")
+    del lw, x5_, seq, acts, dh2_, dx5_, dws
     return out
 
 
@@ -1122,24 +1315,31 @@ def main() -> int:
         sq = bench_matmul_backward(ctx, rng, 4096, 1024, 4096, max(5, args.steps // 2),
                                    args.warmup, "C2'")
         tf = sq["flops"] / (sq["kernel_ms"] * 1e-3) / 1e12
-        secondary.append({"workload": "C2' matmul_backward A[4096,1024] B[1024,4096]",
-                          "kernel": HEAD_KERNEL, "kernel_ms": round(sq["kernel_ms"], 5),
-                          "value": round(tf * 1e3, 1), "unit": "GFLOP/s",
-                          "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "bound": "mfma",
-                          "resident_kernel_ms": round(sq["resident_ms"], 5),
-                          "sample_ok": sq["sample_ok"]})
+        ent = {"workload": "C2' matmul_backward A[4096,1024] B[1024,4096]",
+               "kernel": HEAD_KERNEL, "kernel_ms": round(sq["kernel_ms"], 5),
+               "value": round(tf * 1e3, 1), "unit": "GFLOP/s",
+               "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "bound": "mfma",
+               "resident_kernel_ms": round(sq["resident_ms"], 5), "sample_ok": sq["sample_ok"]}
+        if not args.no_cpu_baseline:
+            ent["cpu_baseline"] = cpu_baseline(*sq["inputs"], 256, 48)
+        secondary.append(ent)
         log(f"  C2' {sq['kernel_ms']:.4f} ms {tf:.2f} TFLOP/s (resident {sq['resident_ms']:.4f} ms)")
+        del sq
         rb = bench_relu_bias(ctx, rng, 4096, 4096, args.steps, args.warmup)
         gbs = rb["bytes"] / (rb["kernel_ms"] * 1e-3) / 1e9
-        secondary.append({"workload": "C3 relu(X+b) backward: dX masked + db column sum, 4096x4096",
-                          "kernel": "colreduce_pass1+colreduce_finalize",
-                          "kernel_ms": round(rb["kernel_ms"], 5), "value": round(gbs, 1),
-                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
-                          "algorithmic_bytes": rb["bytes"], "operand_sets": rb["sets"],
-                          "traffic": traffic_from_profile("relu_bias_4096"),
-                          "resident_kernel_ms": round(rb["resident_ms"], 5)})
+        ent = {"workload": "C3 relu(X+b) backward: dX masked + db column sum, 4096x4096",
+               "kernel": "colreduce_pass1+colreduce_finalize",
+               "kernel_ms": round(rb["kernel_ms"], 5), "value": round(gbs, 1),
+               "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
+               "algorithmic_bytes": rb["bytes"], "operand_sets": rb["sets"],
+               "traffic": traffic_from_profile("relu_bias_4096"),
+               "resident_kernel_ms": round(rb["resident_ms"], 5)}
+        if not args.no_cpu_baseline:
+            ent["cpu_baseline"] = cpu_baseline_relu_bias(*rb["inputs"])
+        secondary.append(ent)
         log(f"  C3 relu+bias {rb['kernel_ms']:.4f} ms {gbs:.1f} GB/s "
             f"(resident {rb['resident_ms']:.4f} ms)")
+        del rb
         ad = bench_adam(ctx, rng, 1 << 24, args.steps, args.warmup)
         gbs = ad["bytes"] / (ad["kernel_ms"] * 1e-3) / 1e9
         ent = {"workload": "C3 Adam step, 16,777,216 params", "kernel": "adam_kernel",
@@ -1170,22 +1370,28 @@ def main() -> int:
         log(f"  C1 MLP step {c1['us_per_step']:.1f} us, graph replay "
             f"{c1['graph_us_per_step']:.1f} us")
         c4 = bench_c4(ctx, max(10, args.steps), 3)
-        secondary.append({"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
-                                      "heads, FFN 2048 GELU, MSE, SGD) via the device engine",
-                          "value": round(c4["ms_per_step"], 3), "unit": "ms/step",
-                          "tflops_over_step": round(c4["tflops"], 2),
-                          "frac_of_fp32_mfma": round(c4["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4),
-                          "bound": "mfma (GEMMs) + hbm (LN/GELU/softmax)",
-                          "final_loss": round(c4["loss"], 6)})
+        ent = {"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
+                           "heads, FFN 2048 GELU, MSE, SGD) via the device engine",
+               "value": round(c4["ms_per_step"], 3), "unit": "ms/step",
+               "tflops_over_step": round(c4["tflops"], 2),
+               "frac_of_fp32_mfma": round(c4["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4),
+               "bound": "mfma (GEMMs) + hbm (LN/GELU/softmax)",
+               "final_loss": round(c4["loss"], 6)}
+        if not args.no_cpu_baseline:
+            ent["cpu_baseline"] = cpu_baseline_c4()
+        secondary.append(ent)
         log(f"  C4 block step {c4['ms_per_step']:.3f} ms {c4['tflops']:.1f} TFLOP/s")
         c5 = bench_c5(ctx, max(5, args.steps // 4), 2)
-        secondary.append({"workload": "C5 2-layer LSTM forecaster train step (in 64, hidden 256, "
-                                      "seq 128, batch 64, head 256->1, MSE, SGD) via the device "
-                                      "engine",
-                          "value": round(c5["ms_per_step"], 3), "unit": "ms/step",
-                          "tflops_over_step": round(c5["tflops"], 2),
-                          "bound": "latency (256 sequential step kernels per direction)",
-                          "final_loss": round(c5["loss"], 6)})
+        ent = {"workload": "C5 2-layer LSTM forecaster train step (in 64, hidden 256, "
+                           "seq 128, batch 64, head 256->1, MSE, SGD) via the device engine",
+               "value": round(c5["ms_per_step"], 3), "unit": "ms/step",
+               "tflops_over_step": round(c5["tflops"], 2),
+               "frac_of_fp32_mfma": round(c5["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4),
+               "bound": "latency (128 dependent steps per direction, one persistent launch each)",
+               "final_loss": round(c5["loss"], 6)}
+        if not args.no_cpu_baseline:
+            ent["cpu_baseline"] = cpu_baseline_c5()
+        secondary.append(ent)
         log(f"  C5 LSTM step {c5['ms_per_step']:.3f} ms {c5['tflops']:.2f} TFLOP/s")
 
     cpu = None

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests import lstm_oracle, mlp_oracle, transformer_oracle
+from oracle import lstm_oracle, mlp_oracle, transformer_oracle
 from tests.conftest import assert_close
 from tests.golden import fixtures
 

@@ -2,7 +2,7 @@
 
 Known-answer tests are the reference's (file:line cited), run through
 numrs_amd.Tensor exactly as the Rust tests call Tensor; the C1 MLP step is
-compared with the oracle composition in tests/mlp_oracle.py.
+compared with the oracle composition in oracle/mlp_oracle.py.
 """
 import numpy as np
 import pytest
@@ -11,7 +11,7 @@ import numrs_amd as nr
 from numrs_amd import Tensor, nn, optim
 from oracle import oracle as O
 from tests.conftest import assert_close, assert_contraction, rand
-from tests.mlp_oracle import make_c1, mlp_step
+from oracle.mlp_oracle import make_c1, mlp_step
 
 pytestmark = pytest.mark.gpu
 

@@ -18,8 +18,8 @@ import pytest
 import numrs_amd as nr
 from numrs_amd import Tensor, optim
 from oracle import oracle as O
-from tests import lstm_oracle as LO
-from tests import transformer_oracle as TO
+from oracle import lstm_oracle as LO
+from oracle import transformer_oracle as TO
 from tests.conftest import assert_bits, assert_close, assert_contraction, rand
 
 pytestmark = pytest.mark.gpu

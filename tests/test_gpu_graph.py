@@ -8,7 +8,7 @@ import pytest
 
 import numrs_amd as nr
 from numrs_amd import HipError, StepGraph, Tensor, nn, optim
-from tests.mlp_oracle import make_c1
+from oracle.mlp_oracle import make_c1
 
 pytestmark = pytest.mark.gpu
 

@@ -1,11 +1,11 @@
 """LSTM (N4) forward / BPTT and the C5 forecaster on the GPU against the
-float64 oracle (tests/lstm_oracle.py, pinned to torch autograd)."""
+float64 oracle (oracle/lstm_oracle.py, pinned to torch autograd)."""
 import numpy as np
 import pytest
 
 import numrs_amd as nr
 from numrs_amd import Tensor, nn
-from tests import lstm_oracle as LO
+from oracle import lstm_oracle as LO
 from tests.conftest import assert_chain
 
 pytestmark = pytest.mark.gpu

@@ -1,5 +1,5 @@
 """Attention (N3) kernels and the C4 transformer block on the GPU against the
-float64 oracle (tests/transformer_oracle.py, pinned to torch autograd)."""
+float64 oracle (oracle/transformer_oracle.py, pinned to torch autograd)."""
 import math
 
 import numpy as np
@@ -7,7 +7,7 @@ import pytest
 
 import numrs_amd as nr
 from numrs_amd import Tensor, nn
-from tests import transformer_oracle as TO
+from oracle import transformer_oracle as TO
 from tests.conftest import assert_chain, assert_contraction, rand
 
 pytestmark = pytest.mark.gpu

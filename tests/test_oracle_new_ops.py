@@ -4,7 +4,7 @@ only, no GPU involved."""
 import numpy as np
 import pytest
 
-from tests import transformer_oracle as TO
+from oracle import transformer_oracle as TO
 
 torch = pytest.importorskip("torch")
 
@@ -53,7 +53,7 @@ def test_transformer_block_oracle_matches_torch_autograd():
 
 
 def test_lstm_forecaster_oracle_matches_torch_autograd():
-    from tests import lstm_oracle as LO
+    from oracle import lstm_oracle as LO
 
     layers, hw, hb, x, target = LO.make_c5(seed=3, B=3, T=6, I=4, H=5, n_layers=2)
     loss, g, _ = LO.forecaster(layers, hw, hb, x, target)
