@@ -1235,6 +1235,10 @@ def main() -> int:
     ap.add_argument("--cpu-rows-b", type=int, default=192)
     ap.add_argument("--rows", action="store_true",
                     help="measure every hot-path row's kernel instead (one JSON line per row)")
+    ap.add_argument("--recurrence", choices=["auto", "per_step", "plain_launch"], default="auto",
+                    help="how the LSTM recurrences run (numrs_hip_set_recurrence_mode); "
+                         "plain_launch is for rocprofv3 --pmc runs, whose teardown faults after "
+                         "cooperative launches")
     ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -1271,6 +1275,7 @@ def main() -> int:
     from numrs_amd import Context
 
     ctx = Context(0)
+    ctx.set_recurrence_mode(args.recurrence)
     n_cus, arch = ctx.info()
     log(f"device {arch}, {n_cus} CUs")
     rng = np.random.default_rng(SEED)

@@ -329,6 +329,12 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
  * returns its error from the next call that synchronises the stream. */
 #define NUMRS_HIP_RECURRENCE_AUTO 0
 #define NUMRS_HIP_RECURRENCE_PER_STEP 1
+/* As AUTO, but the persistent kernels start with an ordinary launch after
+ * the same residency check, for profilers whose own teardown faults after
+ * cooperative launches (rocprofv3 --pmc loses its counters then).  Nothing
+ * then guarantees that the whole grid is resident: a wait that runs out is
+ * reported as a give-up, as above. */
+#define NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH 2
 int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode);
 /* Number of persistent recurrence launches queued on the context so far
  * (-1 for a null context). */

@@ -1100,7 +1100,7 @@ int fill_words(numrs_hip_ctx *ctx, void *p, int64_t n, unsigned bits) {
 // `threads` at once (resident workgroups per CU cached in *per_cu).
 bool persist_fits(numrs_hip_ctx *ctx, const void *kernel, int threads, unsigned grid,
                   int *per_cu) {
-  if (ctx->capturing || ctx->recurrence_mode != NUMRS_HIP_RECURRENCE_AUTO) return false;
+  if (ctx->capturing || ctx->recurrence_mode == NUMRS_HIP_RECURRENCE_PER_STEP) return false;
   if (*per_cu < 0) {
     int coop = 0, n = 0;
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device) !=
@@ -1128,7 +1128,9 @@ int launch_persist(numrs_hip_ctx *ctx, const void *kernel, unsigned grid, int th
                    const char *what) {
   void *args[] = {&a};
   const hipError_t e =
-      hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream);
+      ctx->recurrence_mode == NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH
+          ? hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream)
+          : hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream);
   if (e != hipSuccess) {
     (void)hipGetLastError();
     return numrs_hip::fail(ctx, NUMRS_HIP_E_HIP, "cooperative launch of %s failed: %s", what,
@@ -1531,7 +1533,8 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
 
 int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode) {
   NRS_CHECK_CTX(ctx);
-  if (mode != NUMRS_HIP_RECURRENCE_AUTO && mode != NUMRS_HIP_RECURRENCE_PER_STEP)
+  if (mode != NUMRS_HIP_RECURRENCE_AUTO && mode != NUMRS_HIP_RECURRENCE_PER_STEP &&
+      mode != NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "recurrence mode %d", mode);
   ctx->recurrence_mode = mode;
   return NUMRS_HIP_OK;

@@ -137,5 +137,8 @@ def test_lstm_persistent_equals_per_step(hip_ctx, dims, monkeypatch):
     assert ran == 2, f"expected the persistent forward and backward, saw {ran} launches"
     step = _forecaster_run(hip_ctx, dims, "per_step")
     assert hip_ctx.persistent_launches() - before == 2
+    plain = _forecaster_run(hip_ctx, dims, "plain_launch")  # ordinary launches, same kernels
+    assert hip_ctx.persistent_launches() - before == 4
     for name, v in auto.items():
         assert np.array_equal(v, step[name]), name
+        assert np.array_equal(v, plain[name]), name
