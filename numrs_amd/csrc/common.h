@@ -114,6 +114,7 @@ int check_launch(numrs_hip_ctx *ctx, const char *what);
 // and the check of it after a stream synchronisation (no-op unless such a
 // kernel ran since the last check).
 int wait_status_word(numrs_hip_ctx *ctx, int **out);
+
 int check_wait_status(numrs_hip_ctx *ctx);
 
 // Loss backward kernels for the engine's root node: with `seed` non-null the
@@ -172,6 +173,30 @@ void with_vec_mode(int mode, F &&f) {
 }
 
 typedef float nrs_f4 __attribute__((ext_vector_type(4)));
+
+// Device-scope accesses for values that one workgroup hands to another,
+// possibly on another XCD, inside one launch: stores write through to the
+// device's coherence point and loads fetch from it (the sc1 scope bit), so
+// the XCDs' L2 caches need no cache-wide write-back or invalidation.  A
+// writer waits for its stores to be acknowledged (s_waitcnt) before it
+// publishes them with a device-scope atomic; a reader loads them only after
+// it has seen that atomic.
+constexpr int kScDevice = 16;          // buffer access cache-policy bits: sc1
+constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
+// Buffer resource over `bytes` bytes at p (bytes < 2^31); loads past the end
+// return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)bytes,
+                                           kBufWord3);
+}
+// (The buffer-load builtin returns raw 32-bit words; the loaded bits are
+// reinterpreted as floats, never converted.)
+__device__ __forceinline__ nrs_f4 ld_dev4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(nrs_f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice));
+}
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 template <int V>
 __device__ __forceinline__ nrs_f4 ldv(const float *p) {

@@ -751,24 +751,10 @@ __global__ void __launch_bounds__(64 * kMWaves)
 // ---------------------------------------------------------------------------
 constexpr int kSpinLimit = 1 << 21;  // wait rounds before giving up (seconds of waiting)
 constexpr int kPersistH = 256;       // the hidden size of the persistent kernels
-constexpr int kScDevice = 16;        // buffer access cache-policy bits: sc1 (device scope)
-constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
 constexpr int kPFUnits = 8;          // forward: hidden units per workgroup (two MFMA tiles)
-
-// Buffer resource over `bytes` bytes at p (bytes < 2^31); loads past the end
-// return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)bytes,
-                                           kBufWord3);
-}
-// 16-byte load at device scope, byte offset `off` into the resource.
-__device__ __forceinline__ f4 ld_dev4(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice);
-}
-// Store at device scope.
-__device__ __forceinline__ void st_dev(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+using numrs_hip::dev_rsrc;
+using numrs_hip::ld_dev4;
+using numrs_hip::st_dev;
 
 // After a step: every lane's device-scope stores acknowledged, the block
 // met, then thread 0 publishes `steps` in the workgroup's counter.
