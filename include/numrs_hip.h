@@ -339,6 +339,12 @@ int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode);
 /* Number of persistent recurrence launches queued on the context so far
  * (-1 for a null context). */
 int64_t numrs_hip_persistent_launches(numrs_hip_ctx *ctx);
+/* Poll rounds a persistent kernel's wait for another workgroup's step makes
+ * before it gives up (rounds < 0: the default, 2^21, seconds of waiting).
+ * A tiny limit forces the give-up path from the host, for testing: the
+ * kernels still exit, and the next call that synchronises the stream
+ * returns the give-up error. */
+int numrs_hip_set_persistent_wait_limit(numrs_hip_ctx *ctx, int rounds);
 
 /* LSTM layer (no reference op), gate order i, f, g, o:
  * x [B, T, I], W_ih [4H, I], W_hh [4H, H], b [4H] (NULL = 0), h0/c0 [B, H]

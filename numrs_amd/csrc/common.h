@@ -62,6 +62,7 @@ struct numrs_hip_ctx {
   int recurrence_mode = 0;
   int persist_fwd_per_cu = -1, persist_bwd_per_cu = -1;
   int64_t persist_launches = 0;  // persistent launches queued on this context
+  int persist_wait_limit = -1;   // wait rounds before a give-up (-1: the kernels' default)
   // Device address of reduce.hip's static partials array on this context's
   // device, resolved at creation (the allocation-free entry point uses it).
   float *noalloc_partials = nullptr;

@@ -735,7 +735,8 @@ __global__ void __launch_bounds__(64 * kMWaves)
 // workgroup, whose waits covered twice as many workgroups: a step's wait
 // ends when the slowest workgroup it depends on has finished.)
 //
-// The wait is bounded: after kSpinLimit rounds, or once another workgroup
+// The wait is bounded: after `spin` rounds (kSpinLimit unless the context
+// sets another limit), or once another workgroup
 // has given up (the abort word after the counters), a workgroup records the
 // give-up in the context's status word and returns, so every workgroup
 // exits; the host reports it at its next synchronisation.  The cooperative
@@ -770,7 +771,7 @@ __device__ __forceinline__ void publish_step(unsigned *counter, unsigned steps) 
 // after recording why, when the wait ran out (status 1) or another
 // workgroup gave up (the abort word is set).
 __device__ bool wait_counters(const unsigned *fa, int na, unsigned ta, const unsigned *fb, int nb,
-                              unsigned tb, unsigned *abort_word, int *status) {
+                              unsigned tb, unsigned *abort_word, int *status, int spin) {
   const int lane = threadIdx.x & 63;
   for (int it = 0;; ++it) {
     bool ok = true;
@@ -781,7 +782,7 @@ __device__ bool wait_counters(const unsigned *fa, int na, unsigned ta, const uns
     if (__all(ok)) return true;
     const unsigned ab = __hip_atomic_load(abort_word + (lane & 0), __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
-    if (ab != 0u || it >= kSpinLimit) {
+    if (ab != 0u || it >= spin) {
       if (lane == 0) {
         if (ab == 0u) __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -796,9 +797,10 @@ __device__ bool wait_counters(const unsigned *fa, int na, unsigned ta, const uns
 // the wait gave up (every thread then returns).
 __device__ __forceinline__ bool await_step(const unsigned *fa, int na, unsigned ta,
                                            const unsigned *fb, int nb, unsigned tb,
-                                           unsigned *abort_word, int *status, int *s_go) {
+                                           unsigned *abort_word, int *status, int spin,
+                                           int *s_go) {
   if (threadIdx.x < 64) {
-    const bool ok = wait_counters(fa, na, ta, fb, nb, tb, abort_word, status);
+    const bool ok = wait_counters(fa, na, ta, fb, nb, tb, abort_word, status, spin);
     if (threadIdx.x == 0) *s_go = ok ? 1 : 0;
   }
   __syncthreads();
@@ -813,6 +815,7 @@ struct Lstm2Fwd {
   unsigned *count;  // [2][rgroups][H / kPFUnits] steps done (lower, upper), then the abort word
   int *status;
   int B, T;
+  int spin;  // wait rounds before giving up
 };
 
 // Forward: workgroups [0, n) run the lower layer, [n, 2n) the upper one;
@@ -887,7 +890,7 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (upper) {
       if (!await_step(lo_cnt, ugroups, (unsigned)(t + 1), lo_cnt, 0, 0u, abort_word, p.status,
-                      &s_go))
+                      p.spin, &s_go))
         return;
       const int off = (int)((((int64_t)b * T + t) * H + kb) * 4);
       f4 ai[4];
@@ -902,7 +905,7 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
     }
     if (t > 0) {
       if (!await_step(upper ? up_cnt : lo_cnt, ugroups, (unsigned)t, lo_cnt, 0, 0u, abort_word,
-                      p.status, &s_go))
+                      p.status, p.spin, &s_go))
         return;
       const int off = (int)((((int64_t)b * T + t - 1) * H + kb) * 4);
       f4 ar[4];
@@ -947,6 +950,7 @@ struct Lstm2Bwd {
   unsigned *count;  // [rgroups][3][H / kMUnits] steps done (upper, lower, helper), then abort
   int *status;
   int B, T;
+  int spin;  // wait rounds before giving up
 };
 
 // Backward: workgroups [0, n) run the upper layer, [n, 2n) the lower one and
@@ -1018,13 +1022,14 @@ __global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
     bool go = true;
     if (role == 0) {
       if (s > 0)
-        go = await_step(up_cnt, ugroups, (unsigned)s, up_cnt, 0, 0u, abort_word, p.status, &s_go);
+        go = await_step(up_cnt, ugroups, (unsigned)s, up_cnt, 0, 0u, abort_word, p.status,
+                        p.spin, &s_go);
     } else if (role == 1) {
       go = await_step(lo_cnt, s > 0 ? ugroups : 0, (unsigned)s, hp_cnt + ug, 1, (unsigned)(s + 1),
-                      abort_word, p.status, &s_go);
+                      abort_word, p.status, p.spin, &s_go);
     } else {
       go = await_step(up_cnt, ugroups, (unsigned)(s + 1), up_cnt, 0, 0u, abort_word, p.status,
-                      &s_go);
+                      p.spin, &s_go);
     }
     if (!go) return;
     const bool red = role == 2 || s > 0;  // this step has a reduction
@@ -1098,6 +1103,11 @@ bool persist_fits(numrs_hip_ctx *ctx, const void *kernel, int threads, unsigned 
     *per_cu = coop ? n : 0;
   }
   return (int64_t)*per_cu * ctx->num_cus >= (int64_t)grid;
+}
+
+// Wait rounds before a persistent kernel's wait gives up.
+int wait_limit(const numrs_hip_ctx *ctx) {
+  return ctx->persist_wait_limit >= 0 ? ctx->persist_wait_limit : kSpinLimit;
 }
 
 // Step counters (one per workgroup) and the abort word after them, zeroed,
@@ -1405,7 +1415,7 @@ int numrs_hip_lstm2_forward(numrs_hip_ctx *ctx, const float *x, const float *w_i
       int *status = nullptr;
       if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
       Lstm2Fwd a{acts1, acts2, w_hh1, w_ih2, w_hh2, b2, h1_seq, c1_seq, h2_seq, c2_seq,
-                 static_cast<unsigned *>(cnt.p), status, (int)B, (int)T};
+                 static_cast<unsigned *>(cnt.p), status, (int)B, (int)T, wait_limit(ctx)};
       return launch_persist(ctx, reinterpret_cast<const void *>(lstm2_fwd_persist), grid, 512, a,
                             "lstm2_fwd_persist");
     }
@@ -1467,7 +1477,8 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
         if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
         if (int rc = up_in.alloc((size_t)(B * T * H1) * sizeof(float))) return rc;
         Lstm2Bwd a{dG1.f(), dG2.f(), w_hh1, w_ih2, w_hh2, acts1, c1_seq, acts2, c2_seq, dh2_seq,
-                   up_in.f(), static_cast<unsigned *>(cnt.p), status, (int)B, (int)T};
+                   up_in.f(), static_cast<unsigned *>(cnt.p), status, (int)B, (int)T,
+                   wait_limit(ctx)};
         if (int rc = launch_persist(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), grid,
                                     1024, a, "lstm2_bwd_persist"))
           return rc;
@@ -1523,6 +1534,12 @@ int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode) {
       mode != NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "recurrence mode %d", mode);
   ctx->recurrence_mode = mode;
+  return NUMRS_HIP_OK;
+}
+
+int numrs_hip_set_persistent_wait_limit(numrs_hip_ctx *ctx, int rounds) {
+  NRS_CHECK_CTX(ctx);
+  ctx->persist_wait_limit = rounds < 0 ? -1 : rounds;
   return NUMRS_HIP_OK;
 }
 

@@ -167,6 +167,11 @@ class Context:
         code = {"auto": 0, "per_step": 1, "plain_launch": 2}[mode]
         self._check(L.load().numrs_hip_set_recurrence_mode(self.handle, code))
 
+    def set_persistent_wait_limit(self, rounds: int) -> None:
+        """Poll rounds before a persistent kernel's wait gives up (negative:
+        the default); a tiny limit forces the give-up path, for testing."""
+        self._check(L.load().numrs_hip_set_persistent_wait_limit(self.handle, int(rounds)))
+
     def persistent_launches(self) -> int:
         """Persistent recurrence launches queued on this context so far."""
         return int(L.load().numrs_hip_persistent_launches(self.handle))

@@ -142,3 +142,32 @@ def test_lstm_persistent_equals_per_step(hip_ctx, dims, monkeypatch):
     for name, v in auto.items():
         assert np.array_equal(v, step[name]), name
         assert np.array_equal(v, plain[name]), name
+
+
+def test_lstm_persistent_give_up_is_reported(hip_ctx, monkeypatch):
+    """The persistent kernels' bounded wait, forced to give up from the host
+    (a wait limit of 0 poll rounds): every workgroup still exits, the next
+    call that synchronises raises the give-up, the status is cleared, and a
+    run at the default limit afterwards is whole."""
+    print("[gpu] lstm persistent give-up path", flush=True)
+    from numrs_amd import HipError
+    nr.set_default_context(hip_ctx)
+    monkeypatch.setattr(nn.LSTMForecaster, "fuse_stack", True)
+    layers, hw, hb, x, _ = LO.make_c5(seed=3, n_layers=2, B=64, T=128, I=64, H=256)
+    model = nn.LSTMForecaster(layers, hw, hb)
+    hip_ctx.set_persistent_wait_limit(0)
+    try:
+        y = model.forward(Tensor.new(x, False))
+        with pytest.raises(HipError, match="gave up"):
+            y.values()
+    finally:
+        hip_ctx.set_persistent_wait_limit(-1)
+    before = hip_ctx.persistent_launches()
+    y2 = model.forward(Tensor.new(x, False)).values()
+    assert hip_ctx.persistent_launches() == before + 1
+    hip_ctx.set_recurrence_mode("per_step")
+    try:
+        y3 = model.forward(Tensor.new(x, False)).values()
+    finally:
+        hip_ctx.set_recurrence_mode("auto")
+    assert np.array_equal(y2, y3)
