@@ -1235,10 +1235,12 @@ def main() -> int:
     ap.add_argument("--cpu-rows-b", type=int, default=192)
     ap.add_argument("--rows", action="store_true",
                     help="measure every hot-path row's kernel instead (one JSON line per row)")
-    ap.add_argument("--recurrence", choices=["auto", "per_step", "plain_launch"], default="auto",
-                    help="how the LSTM recurrences run (numrs_hip_set_recurrence_mode); "
-                         "plain_launch is for rocprofv3 --pmc runs, whose teardown faults after "
-                         "cooperative launches")
+    ap.add_argument("--recurrence", choices=["auto", "per_step", "plain_launch", "cooperative"],
+                    default="auto",
+                    help="how the LSTM recurrences run (numrs_hip_set_recurrence_mode): auto "
+                         "and plain_launch start the persistent kernels with an ordinary "
+                         "launch, cooperative with a cooperative one (rocprofv3's teardown "
+                         "faults after those)")
     ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
     ap.add_argument("--traffic-probe", action="store_true",

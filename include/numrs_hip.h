@@ -320,21 +320,24 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
                                              int64_t H, int64_t D, int accumulate);
 
 /* How the two-layer LSTM calls run their recurrences (no reference op).
- * AUTO (the default): one persistent cooperative launch for all steps of
- * the forward and one for the backward where they apply (H1 = H2 = 256,
- * 16-byte aligned operands, not while recording a graph, and the device
- * holds the whole grid at once); per-step launches otherwise.  PER_STEP:
- * always one launch per diagonal step.  Both give the same bits.  A
- * persistent launch whose bounded wait for another workgroup runs out
- * returns its error from the next call that synchronises the stream. */
+ * AUTO (the default): one persistent launch for all steps of the forward
+ * and one for the backward where they apply (H1 = H2 = 256, 16-byte aligned
+ * operands, not while recording a graph, and the occupancy query says the
+ * device holds the whole grid at once); per-step launches otherwise.  The
+ * persistent kernels start with an ordinary launch: the stream has finished
+ * its earlier work by then, so the grid becomes resident as soon as work of
+ * other streams leaves the CUs, and every wait for another workgroup is
+ * bounded.  A persistent launch whose wait runs out returns its error from
+ * the next call that synchronises the stream.  PER_STEP: always one launch
+ * per diagonal step.  PLAIN_LAUNCH: the persistent kernels, ordinary launch
+ * (AUTO's form; kept for scripts that name it).  COOPERATIVE: the persistent
+ * kernels through hipLaunchCooperativeKernel, whose runtime guarantees
+ * co-residency but adds about 25 us per launch on MI355X (and rocprofv3's
+ * teardown faults after such launches).  All modes give the same bits. */
 #define NUMRS_HIP_RECURRENCE_AUTO 0
 #define NUMRS_HIP_RECURRENCE_PER_STEP 1
-/* As AUTO, but the persistent kernels start with an ordinary launch after
- * the same residency check, for profilers whose own teardown faults after
- * cooperative launches (rocprofv3 --pmc loses its counters then).  Nothing
- * then guarantees that the whole grid is resident: a wait that runs out is
- * reported as a give-up, as above. */
 #define NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH 2
+#define NUMRS_HIP_RECURRENCE_COOPERATIVE 3
 int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode);
 /* Number of persistent recurrence launches queued on the context so far
  * (-1 for a null context). */

@@ -239,10 +239,6 @@ struct BatchedOut {
 int gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, BatchedOut C1, BatchedMat Y2,
                     BatchedOut C2, int64_t M, int64_t K, int64_t N, float alpha, int accumulate,
                     int64_t batch, int64_t binner);
-// C1_z = alpha1 X1_z^T Y1_z and C2_z = alpha2 X2_z^T Y2_z (X [M,K], Y [M,N],
-// C [K,N]) for z < batch, in one launch where the streamed path fits
-// (attention's dV = P^T dO with dK = alpha dS^T Q).  Either output may be
-// null; accumulate adds into the outputs.
 // The MSE loss (numrs_hip_mse_loss) that, with dp, also writes the gradient
 // its backward forms as the sweep's root (g = 1: dp = (2 (p - t)) / n, the
 // backward kernel's arithmetic) and, with seed, writes 1 there.
@@ -255,9 +251,23 @@ int cross_entropy_loss_impl(numrs_hip_ctx *ctx, const float *logits, const float
                             float *seed);
 bool cross_entropy_preforms(int64_t B);
 
+// C1_z = alpha1 X1_z^T Y1_z and C2_z = alpha2 X2_z^T Y2_z (X [M,K], Y [M,N],
+// C [K,N]) for z < batch, in one launch where the streamed path fits
+// (attention's dV = P^T dO with dK = alpha dS^T Q).  Either output may be
+// null; accumulate adds into the outputs.
 int gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, BatchedOut C1, float alpha1,
                  BatchedMat X2, BatchedMat Y2, BatchedOut C2, float alpha2, int64_t M, int64_t K,
                  int64_t N, int accumulate, int64_t batch, int64_t binner);
+// Two weight gradients of one left operand, C1[K,N1] = X^T Y1 and
+// C2[K,N2] = X^T Y2 (X [M,K] at row stride ldx, Y1 [M,N1], Y2 [M,N2]), in
+// one launch with a joint split plan where the streamed path fits, and the
+// column sums db[K] of X (CORRECT-mode unbroadcast; null for none) formed
+// by the launch that reduces the splits (the LSTM's dW_ih, dW_hh and db).
+// acc* add into the outputs.
+int gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, int64_t M, int64_t K,
+                    const float *Y1, int64_t ldy1, int64_t N1, float *C1, int acc1,
+                    const float *Y2, int64_t ldy2, int64_t N2, float *C2, int acc2, float *db,
+                    int acc_db);
 
 
 // One LDS DMA instruction: each lane copies 16 bytes from base + off (off in

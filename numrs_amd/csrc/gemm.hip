@@ -1928,6 +1928,43 @@ int numrs_hip::gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, Ba
   return gemm_dispatch(ctx, gb, batch, false, false);
 }
 
+int numrs_hip::gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, int64_t M,
+                               int64_t K, const float *Y1, int64_t ldy1, int64_t N1, float *C1,
+                               int acc1, const float *Y2, int64_t ldy2, int64_t N2, float *C2,
+                               int acc2, float *db, int acc_db) {
+  const char *who = "gemm_tn2_colsum";
+  if (int rc = check_dims(ctx, who, 1, M, K, std::max(N1, N2))) return rc;
+  if (X == nullptr || C1 == nullptr || C2 == nullptr || Y1 == nullptr || Y2 == nullptr ||
+      M <= 0 || K <= 0 || N1 <= 0 || N2 <= 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: null or empty operand", who);
+  // C[K,N] = X^T Y with X [M,K], Y [M,N]: P=K, Q=N, R=M (both operands
+  // output-contiguous), as gemm_tn_pair.
+  Gemm ga = make(X, Y1, C1, ldx, ldy1, N1, 0, 0, 0, K, N1, M, acc1);
+  Gemm gb = make(X, Y2, C2, ldx, ldy2, N2, 0, 0, 0, K, N2, M, acc2);
+  ColSum cs{X, db, M, K, ldx, acc_db, nullptr};
+  const bool cs_ok = db != nullptr && colsum_fits(X, M, K, ldx);
+  StreamPlan pl;
+  if (plan_streamed(ctx, ga, false, false, &gb, &pl)) {
+    if (int rc = stream_prepare(ctx, pl, ga, &gb)) return rc;
+    const int64_t na = stream_grid(ga), nt = na + stream_grid(gb);
+    if (nt > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);
+    if (pl.small)
+      tn_pair_stream_small<<<dim3((unsigned)nt, 1), kThreads, 0, ctx->stream>>>(ga, gb, (int)na);
+    else
+      tn_pair_stream<<<dim3((unsigned)nt, 1), kBigThreads, 0, ctx->stream>>>(ga, gb, (int)na);
+    if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
+    if (int rc = reduce_splits(ctx, &ga, &gb, cs_ok ? &cs : nullptr)) return rc;
+  } else {
+    if (int rc = gemm_dispatch(ctx, ga, 1, false, false)) return rc;
+    if (int rc = gemm_dispatch(ctx, gb, 1, false, false)) return rc;
+    if (cs_ok)
+      if (int rc = reduce_splits(ctx, nullptr, nullptr, &cs)) return rc;
+  }
+  if (db == nullptr || cs_ok) return NUMRS_HIP_OK;
+  const int64_t gs[2] = {M, K};
+  return numrs_hip_sum_to_shape(ctx, X, gs, 2, db, &K, 1, NUMRS_HIP_UNBROADCAST_CORRECT, acc_db);
+}
+
 extern "C" {
 
 int numrs_hip_linear_forward(numrs_hip_ctx *ctx, const float *x, const float *W, const float *b,

@@ -708,9 +708,9 @@ __global__ void __launch_bounds__(64 * kMWaves)
 }
 
 // ---------------------------------------------------------------------------
-// Persistent recurrences of two stacked layers (H1 = H2 = 256): one
-// cooperative launch runs every step of both layers' forward, one every step
-// of their backward, instead of T + 1 launches each.
+// Persistent recurrences of two stacked layers (H1 = H2 = 256): one launch
+// runs every step of both layers' forward, one every step of their
+// backward, instead of T + 1 launches each.
 //
 // Each layer runs in workgroups of its own, so the two recurrences are two
 // chains: the forward's lower chain depends only on itself and the upper one
@@ -739,8 +739,13 @@ __global__ void __launch_bounds__(64 * kMWaves)
 // sets another limit), or once another workgroup
 // has given up (the abort word after the counters), a workgroup records the
 // give-up in the context's status word and returns, so every workgroup
-// exits; the host reports it at its next synchronisation.  The cooperative
-// launch refuses a grid that cannot be resident all at once.
+// exits; the host reports it at its next synchronisation.  The host
+// launches only a grid that the occupancy query says the device holds at
+// once.  The launch is an ordinary one: the stream has drained its earlier
+// work when the grid starts, so every workgroup becomes resident once other
+// streams' work leaves the CUs, and the bounded wait covers the time until
+// then.  (A cooperative launch, whose runtime guarantees co-residency, costs
+// about 25 us more per launch on MI355X; COOPERATIVE mode selects it.)
 //
 // Each wave keeps its slice of the recurrent (and stacked input) weights in
 // registers for the whole launch; a step reads only the rows it reduces and
@@ -1086,21 +1091,28 @@ int fill_words(numrs_hip_ctx *ctx, void *p, int64_t n, unsigned bits) {
 }
 
 // Whether a persistent kernel's grid can run this call: the context allows
-// it, no graph is being recorded (the cooperative launch is not recorded),
-// the device supports cooperative launches and holds `grid` workgroups of
-// `threads` at once (resident workgroups per CU cached in *per_cu).
+// it, no graph is being recorded, the device holds `grid` workgroups of
+// `threads` at once (resident workgroups per CU cached in *per_cu), and, in
+// COOPERATIVE mode, the device supports cooperative launches.
 bool persist_fits(numrs_hip_ctx *ctx, const void *kernel, int threads, unsigned grid,
                   int *per_cu) {
   if (ctx->capturing || ctx->recurrence_mode == NUMRS_HIP_RECURRENCE_PER_STEP) return false;
   if (*per_cu < 0) {
-    int coop = 0, n = 0;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    *per_cu = n;
+  }
+  if (ctx->recurrence_mode == NUMRS_HIP_RECURRENCE_COOPERATIVE) {
+    int coop = 0;
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device) !=
-            hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess) {
+        hipSuccess) {
       (void)hipGetLastError();
       coop = 0;
     }
-    *per_cu = coop ? n : 0;
+    if (!coop) return false;
   }
   return (int64_t)*per_cu * ctx->num_cus >= (int64_t)grid;
 }
@@ -1123,14 +1135,14 @@ template <typename Args>
 int launch_persist(numrs_hip_ctx *ctx, const void *kernel, unsigned grid, int threads, Args a,
                    const char *what) {
   void *args[] = {&a};
+  const bool coop = ctx->recurrence_mode == NUMRS_HIP_RECURRENCE_COOPERATIVE;
   const hipError_t e =
-      ctx->recurrence_mode == NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH
-          ? hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream)
-          : hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream);
+      coop ? hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream)
+           : hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, 0, ctx->stream);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    return numrs_hip::fail(ctx, NUMRS_HIP_E_HIP, "cooperative launch of %s failed: %s", what,
-                           hipGetErrorString(e));
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_HIP, "%s launch of %s failed: %s",
+                           coop ? "cooperative" : "persistent", what, hipGetErrorString(e));
   }
   ctx->wait_check = true;
   ++ctx->persist_launches;
@@ -1244,11 +1256,37 @@ __global__ void __launch_bounds__(64)
 // [B*T, 4H] of every step, batched over time as single products:
 // dW_ih = dG^T x, dW_hh = dG^T H_prev, db = column sum of dG, dx = dG W_ih
 // (each output may be null).
+// H_prev[b, t] = h[b, t - 1] (h0, or zero, at t = 0) into hp [B*T, H].
+int shift_rows(numrs_hip_ctx *ctx, const float *h_seq, const float *h0, float *hp, int64_t B,
+               int64_t T, int64_t H) {
+  const int64_t rows = B * T;
+  if (H % 4 == 0 && numrs_hip::aligned16(h_seq) && numrs_hip::aligned16(hp) &&
+      (h0 == nullptr || numrs_hip::aligned16(h0)) && rows <= 0x7fffffff) {
+    shift_hidden_rows<<<(unsigned)rows, 64, 0, ctx->stream>>>(h_seq, h0, hp, (int)T, (int)H);
+  } else {
+    shift_hidden<<<grid_for(rows * H, 256), 256, 0, ctx->stream>>>(h_seq, h0, hp, (int)B, (int)T,
+                                                                   (int)H);
+  }
+  return numrs_hip::check_launch(ctx, "shift_hidden");
+}
+
 int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const float *w_ih,
                      const float *h_seq, const float *h0, float *dx, float *dw_ih, float *dw_hh,
                      float *db, int64_t B, int64_t T, int64_t I, int64_t H, int acc_dx,
                      int acc_dw_ih, int acc_dw_hh, int acc_db) {
   const int64_t rows = B * T, H4 = 4 * H;
+  if (dw_ih && dw_hh && rows > 0 && I > 0) {
+    // dW_ih[4H, I] = dG^T x and dW_hh[4H, H] = dG^T H_prev in one launch
+    // (both read dG), db = column sums of dG in the launch reducing their
+    // splits
+    TempBlock hp(ctx);
+    if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
+    if (int rc = shift_rows(ctx, h_seq, h0, hp.f(), B, T, H)) return rc;
+    if (int rc = numrs_hip::gemm_tn2_colsum(ctx, dG, H4, rows, H4, x, I, I, dw_ih, acc_dw_ih,
+                                            hp.f(), H, H, dw_hh, acc_dw_hh, db, acc_db))
+      return rc;
+    dw_ih = dw_hh = db = nullptr;
+  }
   if (dw_ih)  // dW_ih[4H, I] = dG^T x
     if (int rc = numrs_hip_gemm(ctx, dG, H4, x, I, dw_ih, I, H4, rows, I, 1, 0, 1.0f, acc_dw_ih,
                                 1, 1, 0, 0, 0, 0, 0, 0))
@@ -1256,14 +1294,7 @@ int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const 
   if (dw_hh) {  // dW_hh[4H, H] = dG^T H_prev
     TempBlock hp(ctx);
     if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
-    if (H % 4 == 0 && numrs_hip::aligned16(h_seq) && numrs_hip::aligned16(hp.f()) &&
-        (h0 == nullptr || numrs_hip::aligned16(h0)) && rows <= 0x7fffffff) {
-      shift_hidden_rows<<<(unsigned)rows, 64, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)T, (int)H);
-    } else {
-      shift_hidden<<<grid_for(rows * H, 256), 256, 0, ctx->stream>>>(h_seq, h0, hp.f(), (int)B,
-                                                                     (int)T, (int)H);
-    }
-    if (int rc = numrs_hip::check_launch(ctx, "shift_hidden")) return rc;
+    if (int rc = shift_rows(ctx, h_seq, h0, hp.f(), B, T, H)) return rc;
     if (int rc = numrs_hip_gemm(ctx, dG, H4, hp.f(), H, dw_hh, H, H4, rows, H, 1, 0, 1.0f,
                                 acc_dw_hh, 1, 1, 0, 0, 0, 0, 0, 0))
       return rc;
@@ -1531,7 +1562,7 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
 int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode) {
   NRS_CHECK_CTX(ctx);
   if (mode != NUMRS_HIP_RECURRENCE_AUTO && mode != NUMRS_HIP_RECURRENCE_PER_STEP &&
-      mode != NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH)
+      mode != NUMRS_HIP_RECURRENCE_PLAIN_LAUNCH && mode != NUMRS_HIP_RECURRENCE_COOPERATIVE)
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "recurrence mode %d", mode);
   ctx->recurrence_mode = mode;
   return NUMRS_HIP_OK;

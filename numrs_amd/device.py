@@ -160,11 +160,11 @@ class Context:
         self._check(L.load().numrs_hip_reserve(self.handle, nbytes))
 
     def set_recurrence_mode(self, mode: str) -> None:
-        """'auto' (persistent LSTM recurrences where they apply), 'per_step'
-        (one launch per diagonal step; the same bits) or 'plain_launch' (as
-        'auto' with an ordinary launch of the persistent kernels, for
-        profilers that fault after cooperative launches)."""
-        code = {"auto": 0, "per_step": 1, "plain_launch": 2}[mode]
+        """'auto' (persistent LSTM recurrences, ordinary launch, where they
+        apply), 'per_step' (one launch per diagonal step), 'plain_launch'
+        (the same as 'auto') or 'cooperative' (the persistent kernels through
+        a cooperative launch).  Every mode gives the same bits."""
+        code = {"auto": 0, "per_step": 1, "plain_launch": 2, "cooperative": 3}[mode]
         self._check(L.load().numrs_hip_set_recurrence_mode(self.handle, code))
 
     def set_persistent_wait_limit(self, rounds: int) -> None:

@@ -122,8 +122,9 @@ def _forecaster_run(hip_ctx, dims, mode):
 
 
 # H = 256 stacked: the persistent forward and backward recurrences (one
-# cooperative launch each) against one launch per diagonal step: the same
-# reduction slices, operand layout and partial order, so the same bits.
+# launch each; ordinary in 'auto', cooperative in 'cooperative') against one
+# launch per diagonal step: the same reduction slices, operand layout and
+# partial order, so the same bits.
 @pytest.mark.parametrize("dims", [dict(B=64, T=128, I=64, H=256), dict(B=20, T=7, I=24, H=256),
                                   dict(B=16, T=1, I=8, H=256), dict(B=3, T=2, I=256, H=256)],
                          ids=["baseline", "ragged_rows", "one_step", "two_steps_wide_in"])
@@ -137,11 +138,11 @@ def test_lstm_persistent_equals_per_step(hip_ctx, dims, monkeypatch):
     assert ran == 2, f"expected the persistent forward and backward, saw {ran} launches"
     step = _forecaster_run(hip_ctx, dims, "per_step")
     assert hip_ctx.persistent_launches() - before == 2
-    plain = _forecaster_run(hip_ctx, dims, "plain_launch")  # ordinary launches, same kernels
+    coop = _forecaster_run(hip_ctx, dims, "cooperative")  # cooperative launches, same kernels
     assert hip_ctx.persistent_launches() - before == 4
     for name, v in auto.items():
         assert np.array_equal(v, step[name]), name
-        assert np.array_equal(v, plain[name]), name
+        assert np.array_equal(v, coop[name]), name
 
 
 def test_lstm_persistent_give_up_is_reported(hip_ctx, monkeypatch):
