@@ -57,10 +57,12 @@ struct numrs_hip_ctx {
   // the stream reads it and reports a give-up as an error.
   int *wait_status = nullptr;
   bool wait_check = false;
-  // NUMRS_HIP_RECURRENCE_AUTO or _PER_STEP (numrs_hip_set_recurrence_mode),
-  // and the persistent kernels' resident workgroups per CU (-1: not queried).
+  // A NUMRS_HIP_RECURRENCE_* mode (numrs_hip_set_recurrence_mode), and the
+  // persistent kernels' resident workgroups per CU (-1: not queried; the
+  // forward per input-block count 0..4).
   int recurrence_mode = 0;
-  int persist_fwd_per_cu = -1, persist_bwd_per_cu = -1;
+  int persist_fwd_per_cu[5] = {-1, -1, -1, -1, -1};
+  int persist_bwd_per_cu = -1;
   int64_t persist_launches = 0;  // persistent launches queued on this context
   int persist_wait_limit = -1;   // wait rounds before a give-up (-1: the kernels' default)
   // Device address of reduce.hip's static partials array on this context's

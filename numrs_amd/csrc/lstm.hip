@@ -346,9 +346,11 @@ constexpr int kBUnits = 8;   // backward: hidden units per workgroup
 // inputs are loaded before the product, so their latencies overlap.
 // One layer's forward step for the tiled kernels.  G [B, T, 4H] holds the
 // input projection x W_ih^T + b on entry (xin == nullptr) and the
-// activations on exit.  With xin (a stacked layer fed by the layer below in
-// the same launch), the step reduces its input rows xin[b, t, :] [B, T, I]
-// against W_ih [4H, I] as well, and the bias (may be null) stands in for G.
+// activations on exit.  With xin (the first layer's input, I % 64 == 0 and
+// I <= 256, or a stacked layer fed by the layer below in the same launch),
+// the step reduces its input rows xin[b, t, :] [B, T, I] against
+// W_ih [4H, I] as well, before the recurrent rows, and the bias (may be
+// null) stands in for G.
 struct FwdStep {
   float *G;
   const float *whh;
@@ -356,10 +358,11 @@ struct FwdStep {
   const float *h0, *c0;
   float *h_seq, *c_seq;
   int H, I, t;
+  int sep;  // the input reduction in an accumulator of its own, + bias, then + the recurrent one
 };
 
 __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, int T) {
-  __shared__ float part[4][kFRows][16];
+  __shared__ float part[4][kFRows][16], partx[4][kFRows][16];
   const int H = s.H, t = s.t;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ugroups = H / kFUnits;
@@ -386,27 +389,34 @@ __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, 
   // reduction split over the four waves in 64-long blocks.
   const int r = lane & 15, q = lane >> 4;
   const int b = min(b0 + r, B - 1);
-  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto reduce = [&](const float *arow, const float *wrow, int K) {
-    const int kw = K >> 2;
-    for (int kb = wave * kw; kb < (wave + 1) * kw; kb += 64) {
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, accx = {0.0f, 0.0f, 0.0f, 0.0f};
+  // K % 64 == 0: a wave's range is K/4 long, walked in groups of up to four
+  // 16-long blocks (block i of a group at kb + 16 i), each block four MFMAs
+  // -- the same k order for every K.
+  auto reduce = [&](f4 &acc, const float *arow, const float *wrow, int K) {
+    const int kw = K >> 2, kend = (wave + 1) * kw;
+    for (int kb = wave * kw; kb < kend; kb += 64) {
+      const int nb = min(4, (kend - kb) >> 4);
       f4 a[4], w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        a[i] = *reinterpret_cast<const f4 *>(arow + kb + 16 * i + 4 * q);
-        w[i] = *reinterpret_cast<const f4 *>(wrow + kb + 16 * i + 4 * q);
+        if (i < nb) {
+          a[i] = *reinterpret_cast<const f4 *>(arow + kb + 16 * i + 4 * q);
+          w[i] = *reinterpret_cast<const f4 *>(wrow + kb + 16 * i + 4 * q);
+        }
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e >> 2][e & 3], w[e >> 2][e & 3], acc, 0, 0,
-                                                   0);
+        if ((e >> 2) < nb)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e >> 2][e & 3], w[e >> 2][e & 3], acc, 0, 0,
+                                                     0);
     }
   };
   const int64_t wr = (int64_t)((r >> 2) * H + j0 + (r & 3));  // W row n(c) of column r
   const bool has_h = t > 0 || s.h0 != nullptr;
   const float *hrow = t > 0 ? s.h_seq + ((int64_t)b * T + t - 1) * H
                             : (s.h0 != nullptr ? s.h0 + (int64_t)b * H : nullptr);
-  if (has_h && s.xin != nullptr && H == 256 && s.I == 256) {
+  if (has_h && s.xin != nullptr && !s.sep && H == 256 && s.I == 256) {
     // a stacked layer at H = I = 256 (one 64-long block per wave and operand
     // pair): both pairs' operands are loaded before either's MFMAs, one
     // memory round trip instead of two; the MFMAs run in the order below
@@ -429,17 +439,23 @@ __device__ __forceinline__ void fwd_step_tile(const FwdStep &s, int blk, int B, 
   } else {
     // a stacked layer's input reduction first (the persistent kernel forms it
     // while it waits for the recurrent operand), then the recurrent one
-    if (s.xin != nullptr) reduce(s.xin + ((int64_t)b * T + t) * s.I, s.wih + wr * s.I, s.I);
-    if (has_h) reduce(hrow, s.whh + wr * H, H);
+    if (s.xin != nullptr)
+      reduce(s.sep ? accx : acc, s.xin + ((int64_t)b * T + t) * s.I, s.wih + wr * s.I, s.I);
+    if (has_h) reduce(acc, hrow, s.whh + wr * H, H);
   }
 #pragma unroll
-  for (int v = 0; v < 4; ++v) part[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
+  for (int v = 0; v < 4; ++v) {
+    part[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
+    if (s.sep) partx[wave][4 * (lane >> 4) + v][lane & 15] = accx[v];
+  }
   __syncthreads();
   if (!epi) return;
   float pre[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int c = 4 * g + eu;
+    if (s.sep)  // x W_ih^T + b, as the product with a bias epilogue
+      gin[g] = (((partx[0][em][c] + partx[1][em][c]) + partx[2][em][c]) + partx[3][em][c]) + gin[g];
     pre[g] = gin[g] + (((part[0][em][c] + part[1][em][c]) + part[2][em][c]) + part[3][em][c]);
   }
   float act[4], c, h;
@@ -813,9 +829,10 @@ __device__ __forceinline__ bool await_step(const unsigned *fa, int na, unsigned 
 }
 
 struct Lstm2Fwd {
-  float *acts1, *acts2;              // [B, T, 4H]; acts1 holds x W_ih1^T + b1 on entry
+  float *acts1, *acts2;              // [B, T, 4H]; acts1 holds x W_ih1^T + b1 on entry (NI = 0)
   const float *whh1, *wih2, *whh2;   // [4H, H]
   const float *b2;                   // [4H] or null
+  const float *x, *wih1, *b1;        // NI > 0: x [B, T, I], W_ih1 [4H, I], b1 [4H] or null
   float *h1, *c1, *h2, *c2;          // [B, T, H]
   unsigned *count;  // [2][rgroups][H / kPFUnits] steps done (lower, upper), then the abort word
   int *status;
@@ -828,11 +845,15 @@ struct Lstm2Fwd {
 // j0..j0+7 of its layer as two kFRows x kFUnits tiles (those of
 // lstm_fwd_diag): wave w forms quarter w % 4 of tile w / 4's reduction, and
 // waves 0 and 4 finish the tiles' 64 cells each.  Lower step t reads h1 at
-// t - 1; upper step t reads h2 at t - 1 and h1 at t.
+// t - 1; upper step t reads h2 at t - 1 and h1 at t.  With NI > 0 (I =
+// 64 NI) the lower layer forms x_t W_ih1^T itself, in the per-step kernels'
+// order (the input blocks, then the recurrent ones), before it waits for its
+// previous step: those MFMAs and their loads overlap the wait.
+template <int NI>
 __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
   constexpr int H = kPersistH, H4 = 4 * H;
   constexpr int ugroups = H / kPFUnits;
-  __shared__ float part[8][kFRows][16];
+  __shared__ float part[8][kFRows][16], partx[NI > 0 ? 8 : 1][kFRows][16];
   __shared__ int s_go;
   const int B = p.B, T = p.T;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -847,8 +868,10 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
   const int kb = (wave & 3) * (H / 4) + 4 * q;  // this lane's offset in the wave's 64-long block
   const int64_t wr = (int64_t)((r >> 2) * H + j0 + (r & 3));  // weight row n(c) of column r
 
-  // The wave's weights: lower W_hh1 (wa); upper W_hh2 (wa) and W_ih2 (wb).
-  f4 wa[4], wb[4];
+  // The wave's weights: lower W_hh1 (wa) and W_ih1 (wi, NI > 0); upper W_hh2
+  // (wa) and W_ih2 (wb).
+  f4 wa[4], wb[4], wi[NI > 0 ? NI : 1];
+  const int kx = (wave & 3) * (16 * NI) + 4 * q;  // this lane's offset in the wave's x range
   {
     const float *srca = (upper ? p.whh2 : p.whh1) + wr * H + kb;
     const float *srcb = p.wih2 + wr * H + kb;
@@ -857,6 +880,10 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
       wa[i] = *reinterpret_cast<const f4 *>(srca + 16 * i);
       wb[i] = upper ? *reinterpret_cast<const f4 *>(srcb + 16 * i) : f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      wi[i] = upper ? f4{0.0f, 0.0f, 0.0f, 0.0f}
+                    : *reinterpret_cast<const f4 *>(p.wih1 + wr * (16 * NI * 4) + kx + 16 * i);
   }
   const int64_t hbytes = (int64_t)B * T * H * 4;
   const __amdgpu_buffer_rsrc_t rh1 = dev_rsrc(p.h1, hbytes), rh2 = dev_rsrc(p.h2, hbytes);
@@ -865,9 +892,10 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
   const int be = b0 + em, je = j0 + eu;
   const bool epi = (wave & 3) == 0 && be < B;
   float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (epi && upper && p.b2 != nullptr) {
+  const float *bsrc = upper ? p.b2 : (NI > 0 ? p.b1 : nullptr);
+  if (epi && bsrc != nullptr) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) bias[g] = p.b2[g * H + je];
+    for (int g = 0; g < 4; ++g) bias[g] = bsrc[g * H + je];
   }
   float cst = 0.0f;  // the cell's state at its previous step (zero initial state)
   unsigned *lo_cnt = p.count + rg * ugroups;                       // the row group's lower
@@ -881,7 +909,7 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
   for (int t = 0; t < T; ++t) {
     float gin[4] = {bias[0], bias[1], bias[2], bias[3]};
     const int64_t row = (int64_t)be * T + t;
-    if (epi && !upper) {
+    if (NI == 0 && epi && !upper) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) gin[g] = p.acts1[row * H4 + g * H + je];
     }
@@ -892,7 +920,20 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
     // issued before the MFMAs that wait on it (the scheduler would otherwise
     // issue later loads after earlier MFMAs, exposing their latencies one
     // after another).
-    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, accx = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (NI > 0 && !upper) {
+      const float *xrow = p.x + ((int64_t)b * T + t) * (16 * NI * 4) + kx;
+      f4 xa[NI > 0 ? NI : 1];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) xa[i] = *reinterpret_cast<const f4 *>(xrow + 16 * i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          accx = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i][e], wi[i][e], accx, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (upper) {
       if (!await_step(lo_cnt, ugroups, (unsigned)(t + 1), lo_cnt, 0, 0u, abort_word, p.status,
                       p.spin, &s_go))
@@ -923,7 +964,10 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
                                                    0);
     }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) part[wave][4 * q + v][r] = acc[v];
+    for (int v = 0; v < 4; ++v) {
+      part[wave][4 * q + v][r] = acc[v];
+      if (NI > 0 && !upper) partx[wave][4 * q + v][r] = accx[v];
+    }
     __syncthreads();
     if (epi) {
       const int pw = 4 * tile;
@@ -931,6 +975,10 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c = 4 * g + eu;
+        if (NI > 0 && !upper)  // x W_ih1^T + b1, as the per-step kernels
+          gin[g] = (((partx[pw][em][c] + partx[pw + 1][em][c]) + partx[pw + 2][em][c]) +
+                    partx[pw + 3][em][c]) +
+                   gin[g];
         pre[g] = gin[g] + (((part[pw][em][c] + part[pw + 1][em][c]) + part[pw + 2][em][c]) +
                            part[pw + 3][em][c]);
       }
@@ -1115,6 +1163,18 @@ bool persist_fits(numrs_hip_ctx *ctx, const void *kernel, int threads, unsigned 
     if (!coop) return false;
   }
   return (int64_t)*per_cu * ctx->num_cus >= (int64_t)grid;
+}
+
+// The persistent forward kernel for NI = I / 64 input blocks per wave (0:
+// the input projection is formed before the launch).
+const void *persist_fwd_kernel(int ni) {
+  switch (ni) {
+    case 1: return reinterpret_cast<const void *>(lstm2_fwd_persist<1>);
+    case 2: return reinterpret_cast<const void *>(lstm2_fwd_persist<2>);
+    case 3: return reinterpret_cast<const void *>(lstm2_fwd_persist<3>);
+    case 4: return reinterpret_cast<const void *>(lstm2_fwd_persist<4>);
+    default: return reinterpret_cast<const void *>(lstm2_fwd_persist<0>);
+  }
 }
 
 // Wait rounds before a persistent kernel's wait gives up.
@@ -1434,25 +1494,31 @@ int numrs_hip_lstm2_forward(numrs_hip_ctx *ctx, const float *x, const float *w_i
     return numrs_hip_lstm_forward(ctx, h1_seq, w_ih2, w_hh2, b2, nullptr, nullptr, h2_seq, c2_seq,
                                   acts2, B, T, H1, H2);
   }
-  // acts1 <- x W_ih1^T + b1 for every (b, t) row; the upper layer reduces
-  // h1 against W_ih2 inside its steps.
-  if (int rc = numrs_hip_linear_forward(ctx, x, w_ih1, b1, acts1, B * T, I, 4 * H1)) return rc;
+  // The lower layer reduces x_t against W_ih1 inside its steps where I is a
+  // multiple of 64 up to 256; otherwise acts1 <- x W_ih1^T + b1 for every
+  // (b, t) row first.  The upper layer reduces h1 against W_ih2 inside its
+  // steps.
+  const bool in_x = I % 64 == 0 && I <= 256 && numrs_hip::aligned16(x) &&
+                    numrs_hip::aligned16(w_ih1);
+  if (!in_x)
+    if (int rc = numrs_hip_linear_forward(ctx, x, w_ih1, b1, acts1, B * T, I, 4 * H1)) return rc;
   const int rgroups = (int)((B + kFRows - 1) / kFRows);
   if (H1 == kPersistH && H2 == kPersistH && B * T * H1 * 4 < (int64_t{1} << 31)) {
     const unsigned grid = (unsigned)(2 * rgroups * (kPersistH / kPFUnits));
-    if (persist_fits(ctx, reinterpret_cast<const void *>(lstm2_fwd_persist), 512, grid,
-                     &ctx->persist_fwd_per_cu)) {
+    const void *kern = in_x ? persist_fwd_kernel((int)(I / 64)) : persist_fwd_kernel(0);
+    int *per_cu = &ctx->persist_fwd_per_cu[in_x ? I / 64 : 0];
+    if (persist_fits(ctx, kern, 512, grid, per_cu)) {
       TempBlock cnt(ctx);
       int *status = nullptr;
       if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
-      Lstm2Fwd a{acts1, acts2, w_hh1, w_ih2, w_hh2, b2, h1_seq, c1_seq, h2_seq, c2_seq,
-                 static_cast<unsigned *>(cnt.p), status, (int)B, (int)T, wait_limit(ctx)};
-      return launch_persist(ctx, reinterpret_cast<const void *>(lstm2_fwd_persist), grid, 512, a,
-                            "lstm2_fwd_persist");
+      Lstm2Fwd a{acts1, acts2, w_hh1, w_ih2, w_hh2, b2, in_x ? x : nullptr, w_ih1, b1,
+                 h1_seq, c1_seq, h2_seq, c2_seq, static_cast<unsigned *>(cnt.p), status,
+                 (int)B, (int)T, wait_limit(ctx)};
+      return launch_persist(ctx, kern, grid, 512, a, "lstm2_fwd_persist");
     }
   }
-  FwdStep lo{acts1, w_hh1, nullptr, nullptr, nullptr, nullptr, nullptr, h1_seq, c1_seq,
-             (int)H1, 0, 0};
+  FwdStep lo{acts1, w_hh1, in_x ? x : nullptr, in_x ? w_ih1 : nullptr, in_x ? b1 : nullptr,
+             nullptr, nullptr, h1_seq, c1_seq, (int)H1, in_x ? (int)I : 0, 0, in_x ? 1 : 0};
   FwdStep up{acts2, w_hh2, h1_seq, w_ih2, b2, nullptr, nullptr, h2_seq, c2_seq, (int)H2, (int)H1,
              0};
   const int g_lo = (int)(H1 / kFUnits) * rgroups, g_up = (int)(H2 / kFUnits) * rgroups;

@@ -126,8 +126,10 @@ def _forecaster_run(hip_ctx, dims, mode):
 # launch per diagonal step: the same reduction slices, operand layout and
 # partial order, so the same bits.
 @pytest.mark.parametrize("dims", [dict(B=64, T=128, I=64, H=256), dict(B=20, T=7, I=24, H=256),
-                                  dict(B=16, T=1, I=8, H=256), dict(B=3, T=2, I=256, H=256)],
-                         ids=["baseline", "ragged_rows", "one_step", "two_steps_wide_in"])
+                                  dict(B=16, T=1, I=8, H=256), dict(B=3, T=2, I=256, H=256),
+                                  dict(B=40, T=5, I=128, H=256), dict(B=17, T=3, I=192, H=256)],
+                         ids=["baseline", "ragged_rows", "one_step", "two_steps_wide_in",
+                              "in_128", "in_192"])
 def test_lstm_persistent_equals_per_step(hip_ctx, dims, monkeypatch):
     print(f"[gpu] lstm persistent vs per-step {dims}", flush=True)
     nr.set_default_context(hip_ctx)
