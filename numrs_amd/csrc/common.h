@@ -263,13 +263,15 @@ int gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, BatchedOut C1
 // Two weight gradients of one left operand, C1[K,N1] = X^T Y1 and
 // C2[K,N2] = X^T Y2 (X [M,K] at row stride ldx, Y1 [M,N1], Y2 [M,N2]), in
 // one launch with a joint split plan where the streamed path fits, and the
-// column sums db[K] of X (CORRECT-mode unbroadcast; null for none) formed
-// by the launch that reduces the splits (the LSTM's dW_ih, dW_hh and db).
-// acc* add into the outputs.
+// column sums db[K] of X (null for none) formed by the launch that reduces
+// the splits (the LSTM's dW_ih, dW_hh and db): from db_part [db_rows, K],
+// partial sums of X over row groups added in row order as a compensated sum,
+// when given, else as the CORRECT-mode unbroadcast of X.  acc* add into the
+// outputs.
 int gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, int64_t M, int64_t K,
                     const float *Y1, int64_t ldy1, int64_t N1, float *C1, int acc1,
                     const float *Y2, int64_t ldy2, int64_t N2, float *C2, int acc2, float *db,
-                    int acc_db);
+                    int acc_db, const float *db_part, int64_t db_rows);
 
 
 // One LDS DMA instruction: each lane copies 16 bytes from base + off (off in

@@ -322,6 +322,7 @@ struct SplitSet {
   float *pre;  // optional pre-activation output (row stride ldc)
   const float *res;  // residual added after the bias (row stride ldr)
   int64_t ldr;
+  int kahan;  // the splits added as a compensated (Kahan) sum, in the same order
 };
 
 // Column sums out[c] (+)= sum_r g[r ldg + c] of a [rows, cols] block in one
@@ -400,34 +401,46 @@ __device__ __forceinline__ int64_t colsum_group(int b, int n, int64_t m) {
 
 // Splits are added in order s = 0, 1, ... (deterministic); the loads of a
 // batch of splits are issued before its ordered adds.  With column sums
-// (has_cs), row y = 0 of the grid computes them and rows 1, 2 reduce the
-// products; otherwise rows 0, 1 reduce the products.  The column sums (one
+// (has_cs), row y = 0 of the grid computes them and rows 1, 2, 3 reduce the
+// sets; otherwise rows 0, 1, 2 reduce the sets.  The column sums (one
 // long strided walk per workgroup) go first so that they are dispatched
 // before, and overlap, the short split reductions.  VEC: four consecutive
 // elements of one row per thread (Q, ldc and the pointers 16-byte aligned).
 template <bool VEC>
-__global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, ColSum cs,
-                                                     int has_cs) {
+__global__ void __launch_bounds__(256) splitk_reduce(SplitSet s0, SplitSet s1, SplitSet s2,
+                                                     ColSum cs, int has_cs) {
   if (has_cs && blockIdx.y == 0) {
     const int64_t grp = colsum_group(blockIdx.x, gridDim.x, colsum_groups(cs.cols));
     if (grp >= 0) colsum_block(cs, grp);
     return;
   }
-  const SplitSet &d = (int)blockIdx.y - has_cs ? s1 : s0;
+  const int y = (int)blockIdx.y - has_cs;
+  const SplitSet &d = y == 0 ? s0 : y == 1 ? s1 : s2;
   typedef typename std::conditional<VEC, f4, float>::type V;
   constexpr int kW = VEC ? 4 : 1;
   constexpr int kBatch = VEC ? 4 : 8;
   const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kW;
   if (e >= d.n) return;
-  V s = V{};
+  V s = V{}, comp = V{};
   for (int k0 = 0; k0 < d.splits; k0 += kBatch) {
     V v[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
       if (k0 + u < d.splits) v[u] = *reinterpret_cast<const V *>(d.partial + (k0 + u) * d.n + e);
+    if (d.kahan) {
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (k0 + u < d.splits) s += v[u];
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < d.splits) {
+          const V y = v[u] - comp;
+          const V t = s + y;
+          comp = (t - s) - y;
+          s = t;
+        }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < d.splits) s += v[u];
+    }
   }
   const int64_t p = e / d.Q, q = e - p * d.Q;
   V *dst = reinterpret_cast<V *>(d.C + p * d.ldc + q);
@@ -1029,28 +1042,34 @@ bool colsum_fits(const float *g, int64_t rows, int64_t cols, int64_t ldg) {
 }
 
 // Reduces the split products among a and b (either may be null or unsplit)
-// with one launch, which also forms the column sums `cs` when given (then the
-// launch is made even when nothing was split).
-int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum *cs = nullptr) {
+// with one launch, which also forms the column sums `cs` when given and
+// reduces the set `extra` (then the launch is made even when nothing was
+// split).
+int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum *cs = nullptr,
+                  const SplitSet *extra = nullptr) {
   const Gemm *g[2];
   int m = 0;
   if (a != nullptr && a->splits > 1) g[m++] = a;
   if (b != nullptr && b->splits > 1) g[m++] = b;
-  if (m == 0 && cs == nullptr) return NUMRS_HIP_OK;
-  SplitSet set[2] = {};
+  if (m == 0 && cs == nullptr && extra == nullptr) return NUMRS_HIP_OK;
+  SplitSet set[3] = {};
   bool vec = true;
   int64_t most = 0;
   for (int i = 0; i < m; ++i) {
     const Gemm &d = *g[i];
     set[i] = SplitSet{d.partial, d.C, d.bias, d.ldc, (int64_t)d.P * d.Q, d.Q, d.splits,
                       d.accumulate, d.alpha, d.act, d.pre, d.res, d.ldr};
+  }
+  if (extra != nullptr) set[m++] = *extra;
+  for (int i = 0; i < m; ++i) {
+    const SplitSet &d = set[i];
     vec = vec && d.Q % 4 == 0 && d.ldc % 4 == 0 && numrs_hip::aligned16(d.C) &&
           numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias)) &&
           (d.res == nullptr || (numrs_hip::aligned16(d.res) && d.ldr % 4 == 0)) &&
           (d.pre == nullptr || numrs_hip::aligned16(d.pre));
-    most = std::max(most, set[i].n);
+    most = std::max(most, d.n);
   }
-  if (m == 1) set[1] = set[0];
+  for (int i = m; i < 3; ++i) set[i] = set[0];
   int64_t blocks = (most / (vec ? 4 : 1) + 255) / 256;
   ColSum c{};
   const int has_cs = cs != nullptr ? 1 : 0;
@@ -1063,9 +1082,9 @@ int reduce_splits(numrs_hip_ctx *ctx, const Gemm *a, const Gemm *b, const ColSum
     return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "splitk_reduce: too large");
   dim3 grid((unsigned)std::max<int64_t>(blocks, 1), (unsigned)(m + has_cs));
   if (vec)
-    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, has_cs);
+    splitk_reduce<true><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], set[2], c, has_cs);
   else
-    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], c, has_cs);
+    splitk_reduce<false><<<grid, 256, 0, ctx->stream>>>(set[0], set[1], set[2], c, has_cs);
   return numrs_hip::check_launch(ctx, "splitk_reduce");
 }
 
@@ -1931,7 +1950,8 @@ int numrs_hip::gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, Ba
 int numrs_hip::gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, int64_t M,
                                int64_t K, const float *Y1, int64_t ldy1, int64_t N1, float *C1,
                                int acc1, const float *Y2, int64_t ldy2, int64_t N2, float *C2,
-                               int acc2, float *db, int acc_db) {
+                               int acc2, float *db, int acc_db, const float *db_part,
+                               int64_t db_rows) {
   const char *who = "gemm_tn2_colsum";
   if (int rc = check_dims(ctx, who, 1, M, K, std::max(N1, N2))) return rc;
   if (X == nullptr || C1 == nullptr || C2 == nullptr || Y1 == nullptr || Y2 == nullptr ||
@@ -1942,7 +1962,13 @@ int numrs_hip::gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, 
   Gemm ga = make(X, Y1, C1, ldx, ldy1, N1, 0, 0, 0, K, N1, M, acc1);
   Gemm gb = make(X, Y2, C2, ldx, ldy2, N2, 0, 0, 0, K, N2, M, acc2);
   ColSum cs{X, db, M, K, ldx, acc_db, nullptr};
-  const bool cs_ok = db != nullptr && colsum_fits(X, M, K, ldx);
+  // db from row partials: the compensated sum over db_rows rows of db_part
+  // [db_rows, K] in row order, as one more set of the split reduce
+  const bool by_part = db != nullptr && db_part != nullptr && db_rows >= 1 && db_rows <= (1 << 20);
+  SplitSet part{db_part, db, nullptr, K, K, (int)K, (int)db_rows, acc_db, 1.0f, 0, nullptr,
+                nullptr, 0, 1};
+  const SplitSet *extra = by_part ? &part : nullptr;
+  const bool cs_ok = db != nullptr && !by_part && colsum_fits(X, M, K, ldx);
   StreamPlan pl;
   if (plan_streamed(ctx, ga, false, false, &gb, &pl)) {
     if (int rc = stream_prepare(ctx, pl, ga, &gb)) return rc;
@@ -1953,14 +1979,14 @@ int numrs_hip::gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, 
     else
       tn_pair_stream<<<dim3((unsigned)nt, 1), kBigThreads, 0, ctx->stream>>>(ga, gb, (int)na);
     if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
-    if (int rc = reduce_splits(ctx, &ga, &gb, cs_ok ? &cs : nullptr)) return rc;
+    if (int rc = reduce_splits(ctx, &ga, &gb, cs_ok ? &cs : nullptr, extra)) return rc;
   } else {
     if (int rc = gemm_dispatch(ctx, ga, 1, false, false)) return rc;
     if (int rc = gemm_dispatch(ctx, gb, 1, false, false)) return rc;
-    if (cs_ok)
-      if (int rc = reduce_splits(ctx, nullptr, nullptr, &cs)) return rc;
+    if (cs_ok || by_part)
+      if (int rc = reduce_splits(ctx, nullptr, nullptr, cs_ok ? &cs : nullptr, extra)) return rc;
   }
-  if (db == nullptr || cs_ok) return NUMRS_HIP_OK;
+  if (db == nullptr || cs_ok || by_part) return NUMRS_HIP_OK;
   const int64_t gs[2] = {M, K};
   return numrs_hip_sum_to_shape(ctx, X, gs, 2, db, &K, 1, NUMRS_HIP_UNBROADCAST_CORRECT, acc_db);
 }

@@ -512,7 +512,42 @@ struct BwdStep {
   const float *dG_up, *wt_up;
   float *dc;
   int H, Hu, t;
+  // MFMA steps: when set, dbp [2][B, 4H] holds the compensated sums over the
+  // steps so far (t descending) of each row's gate gradients, then their
+  // compensation terms (kahan_add); the step at t = 0 adds each 16-row
+  // group's sums into dbf [row groups, 4H] (tile_bias_partial) -- the bias
+  // gradient's partials.
+  float *dbp, *dbf;
 };
+
+// One step of a compensated (Kahan) sum: sum += v with the rounding error
+// carried in comp.  The LSTM bias gradient sums each row's T gate gradients
+// this way, as every step kernel forms them, so the per-row partials are
+// about as accurate as a pairwise sum.
+__device__ __forceinline__ void kahan_add(float &sum, float &comp, float v) {
+  const float y = v - comp;
+  const float t = sum + y;
+  comp = (t - sum) - y;
+  sum = t;
+}
+
+// The bias partial of one 16-row x 16-unit tile of the MFMA backward steps:
+// lds[g][m][u] holds cell (row m, unit u)'s compensated step sum of gate g
+// (sum - comp; 0 for rows past B).  Threads 0..63 (gate tid / 16, unit
+// tid % 16) add the 16 rows in order as a compensated sum into
+// out[g H + j0 + u].  The block meets before and after the LDS is read.
+__device__ __forceinline__ void tile_bias_partial(float (*lds)[16][16], float *out, int H,
+                                                  int j0) {
+  __syncthreads();
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    const int g = tid >> 4, u = tid & 15;
+    float sum = 0.0f, comp = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) kahan_add(sum, comp, lds[g][m][u]);
+    out[g * H + j0 + u] = sum - comp;
+  }
+}
 
 __device__ __forceinline__ void bwd_step_tile(const BwdStep &s, int blk, int B, int T) {
   const int H = s.H, t = s.t;
@@ -694,21 +729,45 @@ __device__ __forceinline__ void bwd_step_mfma(const BwdStep &s, int blk, int B, 
     partu[wave][4 * q + v][r] = accu[v];
   }
   __syncthreads();
-  if (!epi) return;
-  float sum = part[0][em][eu];
+  const bool last = s.dbp != nullptr && t == 0;  // this launch forms the tile's bias partial
+  if (!epi && !last) return;
+  float dbv[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // the cell's step sums (last step, rows < B)
+  if (epi) {
+    float sum = part[0][em][eu];
 #pragma unroll
-  for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
-  if (s.dG_up != nullptr) {
-    float sumu = partu[0][em][eu];
+    for (int w = 1; w < kMWaves; ++w) sum += part[w][em][eu];
+    if (s.dG_up != nullptr) {
+      float sumu = partu[0][em][eu];
 #pragma unroll
-    for (int w = 1; w < kMWaves; ++w) sumu += partu[w][em][eu];
-    sum = sum + sumu;
+      for (int w = 1; w < kMWaves; ++w) sumu += partu[w][em][eu];
+      sum = sum + sumu;
+    }
+    float dg[4], dcf;
+    cell_backward(a, c, cp, dho + sum, dcn, dg, dcf);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s.dG[gb + k * H + je] = dg[k];
+    s.dc[(int64_t)be * H + je] = dcf;
+    if (s.dbp != nullptr) {  // the step at T - 1 starts the sums from zero, as a register would
+      float *dp = s.dbp + (int64_t)be * H4 + je, *dq = dp + (int64_t)B * H4;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float bs = has_next ? dp[k * H] : 0.0f, bc = has_next ? dq[k * H] : 0.0f;
+        kahan_add(bs, bc, dg[k]);
+        dp[k * H] = bs;
+        dq[k * H] = bc;
+        dbv[k] = bs - bc;
+      }
+    }
   }
-  float dg[4], dcf;
-  cell_backward(a, c, cp, dho + sum, dcn, dg, dcf);
+  if (last) {  // every thread is here: part is free once the block has met
+    float(*lds)[16][16] = part;
+    __syncthreads();
+    if (tid < 256) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) s.dG[gb + k * H + je] = dg[k];
-  s.dc[(int64_t)be * H + je] = dcf;
+      for (int k = 0; k < 4; ++k) lds[k][em][eu] = dbv[k];
+    }
+    tile_bias_partial(lds, s.dbf + (int64_t)(b0 / kMRows) * H4, H, j0);
+  }
 }
 
 __global__ void __launch_bounds__(64 * kMWaves) lstm_bwd_step_mfma(BwdStep s, int B, int T) {
@@ -1000,6 +1059,7 @@ struct Lstm2Bwd {
   const float *acts1, *c1, *acts2, *c2;   // forward's saved values
   const float *dh2;                       // [B, T, H] gradient at the upper h, or null
   float *up_in;   // [B, T, H] the lower layer's input-gradient term dG2_t W_ih2 per cell
+  float *db1f, *db2f;  // [row groups, 4H] bias-gradient partials (tile_bias_partial), or null
   unsigned *count;  // [rgroups][3][H / kMUnits] steps done (upper, lower, helper), then abort
   int *status;
   int B, T;
@@ -1051,6 +1111,9 @@ __global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
   const int be = b0 + em, je = j0 + eu;
   const bool epi = tid < 256 && be < B;
   float dcf = 0.0f;  // dc_{t+1} f_{t+1} of the cell (0 before its last step)
+  // the cell's gate gradients summed over the steps (compensated)
+  float dbs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dbc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float *dbf = role == 0 ? p.db2f : role == 1 ? p.db1f : nullptr;
   const float *acts = role == 1 ? p.acts1 : p.acts2;
   const float *cs = role == 1 ? p.c1 : p.c2;
   float *dGo = role == 1 ? p.dG1 : p.dG2;
@@ -1117,10 +1180,21 @@ __global__ void __launch_bounds__(1024) lstm2_bwd_persist(Lstm2Bwd p) {
         float dg[4];
         cell_backward(a, c, cp, dho + sum, dcf, dg, dcf);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) st_dev(dGo + row * H4 + g * H + je, dg[g]);
+        for (int g = 0; g < 4; ++g) {
+          st_dev(dGo + row * H4 + g * H + je, dg[g]);
+          kahan_add(dbs[g], dbc[g], dg[g]);
+        }
       }
     }
     publish_step(mine, (unsigned)(s + 1));
+  }
+  if (dbf != nullptr) {  // every thread of the block is here (part is free after the last publish)
+    float(*lds)[16][16] = part;
+    if (tid < 256) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) lds[g][em][eu] = epi ? dbs[g] - dbc[g] : 0.0f;
+    }
+    tile_bias_partial(lds, dbf + (int64_t)rg * H4, H, j0);
   }
 }
 
@@ -1330,10 +1404,14 @@ int shift_rows(numrs_hip_ctx *ctx, const float *h_seq, const float *h0, float *h
   return numrs_hip::check_launch(ctx, "shift_hidden");
 }
 
+// db_part (may be null): [db_rows, 4H] sums of dG over the steps and the
+// rows of each row group (the step kernels' compensated sums), from which db
+// is the sum over the groups.
 int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const float *w_ih,
                      const float *h_seq, const float *h0, float *dx, float *dw_ih, float *dw_hh,
                      float *db, int64_t B, int64_t T, int64_t I, int64_t H, int acc_dx,
-                     int acc_dw_ih, int acc_dw_hh, int acc_db) {
+                     int acc_dw_ih, int acc_dw_hh, int acc_db, const float *db_part = nullptr,
+                     int64_t db_rows = 0) {
   const int64_t rows = B * T, H4 = 4 * H;
   if (dw_ih && dw_hh && rows > 0 && I > 0) {
     // dW_ih[4H, I] = dG^T x and dW_hh[4H, H] = dG^T H_prev in one launch
@@ -1343,7 +1421,8 @@ int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const 
     if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
     if (int rc = shift_rows(ctx, h_seq, h0, hp.f(), B, T, H)) return rc;
     if (int rc = numrs_hip::gemm_tn2_colsum(ctx, dG, H4, rows, H4, x, I, I, dw_ih, acc_dw_ih,
-                                            hp.f(), H, H, dw_hh, acc_dw_hh, db, acc_db))
+                                            hp.f(), H, H, dw_hh, acc_dw_hh, db, acc_db, db_part,
+                                            db_rows))
       return rc;
     dw_ih = dw_hh = db = nullptr;
   }
@@ -1564,6 +1643,20 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
                                    dh1.f(), dx, dw_ih1, dw_hh1, db1, B, T, I, H1, acc_dx,
                                    acc_dw_ih1, acc_dw_hh1, acc_db1);
   }
+  // The bias gradients from per-row-group partials [row groups, 4H] that the
+  // MFMA step kernels (persistent or per step) form as they go (the per-step
+  // launches keep their running sums in [2][B, 4H] first).
+  TempBlock db1p(ctx), db2p(ctx), db1f(ctx), db2f(ctx);
+  const bool mfma = H1 % 256 == 0 && H2 % 256 == 0;
+  const int64_t mgroups = (B + kMRows - 1) / kMRows;
+  if (mfma && db1 != nullptr) {
+    if (int rc = db1p.alloc((size_t)(2 * B * 4 * H1) * sizeof(float))) return rc;
+    if (int rc = db1f.alloc((size_t)(mgroups * 4 * H1) * sizeof(float))) return rc;
+  }
+  if (mfma && db2 != nullptr) {
+    if (int rc = db2p.alloc((size_t)(2 * B * 4 * H2) * sizeof(float))) return rc;
+    if (int rc = db2f.alloc((size_t)(mgroups * 4 * H2) * sizeof(float))) return rc;
+  }
   if (H1 == kPersistH && H2 == kPersistH && B * T * 4 * H1 * 4 < (int64_t{1} << 31)) {
     const unsigned grid = (unsigned)(3 * ((B + kMRows - 1) / kMRows) * (kPersistH / kMUnits));
     if (persist_fits(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), 1024, grid,
@@ -1574,17 +1667,19 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
         if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
         if (int rc = up_in.alloc((size_t)(B * T * H1) * sizeof(float))) return rc;
         Lstm2Bwd a{dG1.f(), dG2.f(), w_hh1, w_ih2, w_hh2, acts1, c1_seq, acts2, c2_seq, dh2_seq,
-                   up_in.f(), static_cast<unsigned *>(cnt.p), status, (int)B, (int)T,
-                   wait_limit(ctx)};
+                   up_in.f(), db1f.f(), db2f.f(), static_cast<unsigned *>(cnt.p), status,
+                   (int)B, (int)T, wait_limit(ctx)};
         if (int rc = launch_persist(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), grid,
                                     1024, a, "lstm2_bwd_persist"))
           return rc;
       }
       if (int rc = lstm_param_grads(ctx, dG2.f(), h1_seq, w_ih2, h2_seq, nullptr, nullptr, dw_ih2,
-                                    dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2))
+                                    dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2,
+                                    db2f.f(), mgroups))
         return rc;
       return lstm_param_grads(ctx, dG1.f(), x, w_ih1, h1_seq, nullptr, dx, dw_ih1, dw_hh1, db1, B,
-                              T, I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1);
+                              T, I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1, db1f.f(),
+                              mgroups);
     }
   }
   TempBlock dc1(ctx), dc2(ctx), wt1(ctx), wt2(ctx), wtu(ctx);
@@ -1596,12 +1691,11 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
   if (int rc = numrs_hip_transpose(ctx, w_hh1, wt1.f(), 4 * H1, H1)) return rc;  // [H1, 4H1]
   if (int rc = numrs_hip_transpose(ctx, w_hh2, wt2.f(), 4 * H2, H2)) return rc;  // [H2, 4H2]
   if (int rc = numrs_hip_transpose(ctx, w_ih2, wtu.f(), 4 * H2, H1)) return rc;  // [H1, 4H2]
-  BwdStep up{dG2.f(), wt2.f(), acts2, c2_seq, nullptr, dh2_seq, nullptr, nullptr, dc2.f(),
-             (int)H2, 0, 0};
-  BwdStep lo{dG1.f(), wt1.f(), acts1, c1_seq, nullptr, nullptr, dG2.f(), wtu.f(), dc1.f(),
-             (int)H1, (int)H2, 0};
   // MFMA steps when both layers' reductions split into 64-long wave blocks.
-  const bool mfma = H1 % 256 == 0 && H2 % 256 == 0;
+  BwdStep up{dG2.f(), wt2.f(), acts2, c2_seq, nullptr, dh2_seq, nullptr, nullptr, dc2.f(),
+             (int)H2, 0, 0, mfma ? db2p.f() : nullptr, db2f.f()};
+  BwdStep lo{dG1.f(), wt1.f(), acts1, c1_seq, nullptr, nullptr, dG2.f(), wtu.f(), dc1.f(),
+             (int)H1, (int)H2, 0, mfma ? db1p.f() : nullptr, db1f.f()};
   const int rows_per = mfma ? kMRows : kBRows, units_per = mfma ? kMUnits : kBUnits;
   const int rgroups = (int)((B + rows_per - 1) / rows_per);
   const int g_up = (int)(H2 / units_per) * rgroups, g_lo = (int)(H1 / units_per) * rgroups;
@@ -1619,10 +1713,11 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
     if (int rc = numrs_hip::check_launch(ctx, "lstm_bwd_diag")) return rc;
   }
   if (int rc = lstm_param_grads(ctx, dG2.f(), h1_seq, w_ih2, h2_seq, nullptr, nullptr, dw_ih2,
-                                dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2))
+                                dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2,
+                                db2f.f(), mgroups))
     return rc;
   return lstm_param_grads(ctx, dG1.f(), x, w_ih1, h1_seq, nullptr, dx, dw_ih1, dw_hh1, db1, B, T,
-                          I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1);
+                          I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1, db1f.f(), mgroups);
 }
 
 int numrs_hip_set_recurrence_mode(numrs_hip_ctx *ctx, int mode) {
