@@ -1259,10 +1259,11 @@ int wait_limit(const numrs_hip_ctx *ctx) {
 // Step counters (one per workgroup) and the abort word after them, zeroed,
 // from the context's block cache, and the status word of one persistent
 // launch.
-int persist_words(numrs_hip_ctx *ctx, numrs_hip::TempBlock &cnt, unsigned grid, int **status) {
+int persist_words(numrs_hip_ctx *ctx, numrs_hip::TempBlock &cnt, unsigned grid, int **status,
+                  bool zero = true) {
   if (int rc = numrs_hip::wait_status_word(ctx, status)) return rc;
   if (int rc = cnt.alloc((size_t)(grid + 1) * sizeof(unsigned))) return rc;
-  return fill_words(ctx, cnt.p, (int64_t)grid + 1, 0u);
+  return zero ? fill_words(ctx, cnt.p, (int64_t)grid + 1, 0u) : NUMRS_HIP_OK;
 }
 
 template <typename Args>
@@ -1359,6 +1360,31 @@ __global__ void __launch_bounds__(64)
   }
 }
 
+// Before the persistent backward, in one launch: H_prev of both layers
+// (blocks [0, rows) shift h1 into hp1, [rows, 2 rows) h2 into hp2, as
+// shift_hidden_rows with zero initial states) and, in the last block, the
+// launch's ncnt step counters and abort word zeroed.
+__global__ void __launch_bounds__(64)
+    lstm2_bwd_prep(const float *__restrict__ h1, float *__restrict__ hp1,
+                   const float *__restrict__ h2, float *__restrict__ hp2, int T, int H,
+                   int64_t rows, unsigned *__restrict__ cnt, int ncnt) {
+  int64_t r = blockIdx.x;
+  if (r == 2 * rows) {
+    for (int i = threadIdx.x; i < ncnt; i += 64) cnt[i] = 0u;
+    return;
+  }
+  const bool upper = r >= rows;
+  if (upper) r -= rows;
+  const float *h = upper ? h2 : h1;
+  float *out = upper ? hp2 : hp1;
+  const int t = (int)(r % T);
+  for (int c = 4 * threadIdx.x; c < H; c += 4 * 64) {
+    const f4 v = t > 0 ? *reinterpret_cast<const f4 *>(h + (r - 1) * H + c)
+                       : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    *reinterpret_cast<f4 *>(out + r * H + c) = v;
+  }
+}
+
 // forward: y[b, :] = x[b, t, :] (blockIdx.x = b); backward: row r = b T + tt of
 // dx [B, T, D] is g[b, :] at tt = t and 0 elsewhere (added to, or only step t
 // touched, with acc).
@@ -1406,23 +1432,25 @@ int shift_rows(numrs_hip_ctx *ctx, const float *h_seq, const float *h0, float *h
 
 // db_part (may be null): [db_rows, 4H] sums of dG over the steps and the
 // rows of each row group (the step kernels' compensated sums), from which db
-// is the sum over the groups.
+// is the sum over the groups.  hp_given (may be null): H_prev already formed.
 int lstm_param_grads(numrs_hip_ctx *ctx, const float *dG, const float *x, const float *w_ih,
                      const float *h_seq, const float *h0, float *dx, float *dw_ih, float *dw_hh,
                      float *db, int64_t B, int64_t T, int64_t I, int64_t H, int acc_dx,
                      int acc_dw_ih, int acc_dw_hh, int acc_db, const float *db_part = nullptr,
-                     int64_t db_rows = 0) {
+                     int64_t db_rows = 0, const float *hp_given = nullptr) {
   const int64_t rows = B * T, H4 = 4 * H;
   if (dw_ih && dw_hh && rows > 0 && I > 0) {
     // dW_ih[4H, I] = dG^T x and dW_hh[4H, H] = dG^T H_prev in one launch
     // (both read dG), db = column sums of dG in the launch reducing their
     // splits
     TempBlock hp(ctx);
-    if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
-    if (int rc = shift_rows(ctx, h_seq, h0, hp.f(), B, T, H)) return rc;
+    if (hp_given == nullptr) {
+      if (int rc = hp.alloc((size_t)(rows * H) * sizeof(float))) return rc;
+      if (int rc = shift_rows(ctx, h_seq, h0, hp.f(), B, T, H)) return rc;
+    }
     if (int rc = numrs_hip::gemm_tn2_colsum(ctx, dG, H4, rows, H4, x, I, I, dw_ih, acc_dw_ih,
-                                            hp.f(), H, H, dw_hh, acc_dw_hh, db, acc_db, db_part,
-                                            db_rows))
+                                            hp_given ? hp_given : hp.f(), H, H, dw_hh, acc_dw_hh,
+                                            db, acc_db, db_part, db_rows))
       return rc;
     dw_ih = dw_hh = db = nullptr;
   }
@@ -1661,10 +1689,26 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
     const unsigned grid = (unsigned)(3 * ((B + kMRows - 1) / kMRows) * (kPersistH / kMUnits));
     if (persist_fits(ctx, reinterpret_cast<const void *>(lstm2_bwd_persist), 1024, grid,
                      &ctx->persist_bwd_per_cu)) {
+      // H_prev of both layers for the weight gradients and the counters'
+      // zeroing in one launch ahead of the recurrence
+      const int64_t rows = B * T;
+      TempBlock hp1(ctx), hp2(ctx);
+      const bool prep = numrs_hip::aligned16(h1_seq) && numrs_hip::aligned16(h2_seq) &&
+                        2 * rows + 1 <= 0x7fffffff;
+      if (prep) {
+        if (int rc = hp1.alloc((size_t)(rows * H1) * sizeof(float))) return rc;
+        if (int rc = hp2.alloc((size_t)(rows * H2) * sizeof(float))) return rc;
+      }
       {
         TempBlock cnt(ctx), up_in(ctx);
         int *status = nullptr;
-        if (int rc = persist_words(ctx, cnt, grid, &status)) return rc;
+        if (int rc = persist_words(ctx, cnt, grid, &status, !prep)) return rc;
+        if (prep) {
+          lstm2_bwd_prep<<<(unsigned)(2 * rows + 1), 64, 0, ctx->stream>>>(
+              h1_seq, hp1.f(), h2_seq, hp2.f(), (int)T, (int)H1, rows,
+              static_cast<unsigned *>(cnt.p), (int)grid + 1);
+          if (int rc = numrs_hip::check_launch(ctx, "lstm2_bwd_prep")) return rc;
+        }
         if (int rc = up_in.alloc((size_t)(B * T * H1) * sizeof(float))) return rc;
         Lstm2Bwd a{dG1.f(), dG2.f(), w_hh1, w_ih2, w_hh2, acts1, c1_seq, acts2, c2_seq, dh2_seq,
                    up_in.f(), db1f.f(), db2f.f(), static_cast<unsigned *>(cnt.p), status,
@@ -1675,11 +1719,11 @@ int numrs_hip_lstm2_backward(numrs_hip_ctx *ctx, const float *x, const float *w_
       }
       if (int rc = lstm_param_grads(ctx, dG2.f(), h1_seq, w_ih2, h2_seq, nullptr, nullptr, dw_ih2,
                                     dw_hh2, db2, B, T, H1, H2, 0, acc_dw_ih2, acc_dw_hh2, acc_db2,
-                                    db2f.f(), mgroups))
+                                    db2f.f(), mgroups, hp2.f()))
         return rc;
       return lstm_param_grads(ctx, dG1.f(), x, w_ih1, h1_seq, nullptr, dx, dw_ih1, dw_hh1, db1, B,
                               T, I, H1, acc_dx, acc_dw_ih1, acc_dw_hh1, acc_db1, db1f.f(),
-                              mgroups);
+                              mgroups, hp1.f());
     }
   }
   TempBlock dc1(ctx), dc2(ctx), wt1(ctx), wt2(ctx), wtu(ctx);
