@@ -887,10 +887,28 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
 
     cpu_model = host_cpu()["model"]
 
+    probe_y_ = ctx.empty((1 << 16,))  # the probe's store target when it writes nothing
+
+    def stream_ceiling(reads, writes, ne, rd, wr):
+        """Mean time of numrs_hip_stream_probe moving the row's traffic (reads and
+        writes of ne floats, one launch) on the row's own buffer copies, cycled
+        like the row, so from HBM."""
+        lib = L.load()
+
+        def probe(i):
+            a = [r[i].ptr for r in rd] + [None] * (3 - len(rd))
+            y = wr[0][i].ptr if writes > 0 else probe_y_.ptr
+            z = wr[1][i].ptr if writes > 1 else None
+            ctx._check(lib.numrs_hip_stream_probe(ctx.handle, a[0], a[1], a[2], y, z, ne,
+                                                  reads, writes))
+        return time_launches(ctx, probe, steps, warmup)[1]
+
     def record(row, fn_name, kernel, shape, bytes_=None, flops=None, launch=None,
-               cpu_fn=None, cpu_scale=1.0, cpu_sample="", check=None, note="", cpu_cores=1):
+               cpu_fn=None, cpu_scale=1.0, cpu_sample="", check=None, note="", cpu_cores=1,
+               ceil=None):
         total, per = time_launches(ctx, launch, steps, warmup)
         _, resident = time_launches(ctx, lambda i: launch(0), steps, warmup)
+        cper = stream_ceiling(*ceil) if ceil is not None else None
         launch(0)  # the checks read copy 0
         ent = {"row": row, "function": fn_name, "kernel": kernel, "shape": shape,
                "kernel_us": round(per * 1e3, 2), "resident_us": round(resident * 1e3, 2)}
@@ -901,6 +919,16 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
                         "frac": round(gbs / PEAK_HBM_GBS, 4),
                         "resident_frac": round(bytes_ / (resident * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                                4)})
+            if cper is not None:
+                reads, writes, ne = ceil[0], ceil[1], ceil[2]
+                pb = 4.0 * (reads + writes) * ne
+                pgbs = pb / (cper * 1e-3) / 1e9
+                ent["ceiling"] = {
+                    "kernel": f"stream_probe ({reads} reads, {writes} writes of {ne:,} floats, "
+                              f"one launch)",
+                    "us": round(cper * 1e3, 2), "achieved": round(pgbs, 1), "unit": "GB/s",
+                    "frac": round(pgbs / PEAK_HBM_GBS, 4),
+                    "row_frac_of_ceiling": round(gbs / pgbs, 4)}
         else:
             tf = flops / (per * 1e-3) / 1e12
             ent.update({"bound": "mfma", "algorithmic_flops": int(flops),
@@ -920,7 +948,9 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
             ent["note"] = note
         out.append(ent)
         log(f"  {row:4s} {fn_name:28s} {ent['kernel_us']:9.2f} us  {ent['achieved']:9.1f} "
-            f"{ent['unit']}  frac {ent['frac']:.3f}  (resident {ent['resident_us']:.2f} us)")
+            f"{ent['unit']}  frac {ent['frac']:.3f}  (resident {ent['resident_us']:.2f} us)"
+            + (f"  ceiling {ent['ceiling']['us']:.2f} us = {ent['ceiling']['frac']:.3f}, row at "
+               f"{ent['ceiling']['row_frac_of_ceiling']:.3f} of it" if "ceiling" in ent else ""))
 
     def same_bits(a, b):
         return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
@@ -945,16 +975,19 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a3", "accumulate_gradient", "binary_backward(ADD, acc)", shape, bytes_=12.0 * n,
            launch=lambda i: ctx.binary_backward(L.ADD, g_[i], None, None, acc_[i], None,
                                                 accumulate=True),
+           ceil=(2, 1, n, [g_, acc_], [dx_]),
            cpu_fn=lambda: O.accumulate(y.ravel()[:ns].copy(), g.ravel()[:ns]), cpu_scale=scale,
            cpu_sample=samp)
     # a7 sub_backward: dx = g, dy = -g
     record("a7", "sub_backward", "binary_backward(SUB)", shape, bytes_=12.0 * n,
            launch=lambda i: ctx.binary_backward(L.SUB, g_[i], None, None, dx_[i], dy_[i]),
+           ceil=(1, 2, n, [g_], [dx_, dy_]),
            cpu_fn=lambda: O.sub_backward(g.ravel()[:ns]), cpu_scale=scale, cpu_sample=samp,
            check=lambda: same_bits(dy_[0].numpy().ravel()[:ns], O.sub_backward(g.ravel()[:ns])[1]))
     # a8 mul_backward: dx = g*y, dy = g*x
     record("a8", "mul_backward", "binary_backward(MUL)", shape, bytes_=20.0 * n,
            launch=lambda i: ctx.binary_backward(L.MUL, g_[i], x_[i], y_[i], dx_[i], dy_[i]),
+           ceil=(3, 2, n, [g_, x_, y_], [dx_, dy_]),
            cpu_fn=lambda: O.mul_backward(g.ravel()[:ns], x.ravel()[:ns], y.ravel()[:ns]),
            cpu_scale=scale, cpu_sample=samp,
            check=lambda: same_bits(dx_[0].numpy().ravel()[:ns],
@@ -963,6 +996,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     # a9 div_backward: dx = g/y, dy = -g*x/y^2
     record("a9", "div_backward", "binary_backward(DIV)", shape, bytes_=20.0 * n,
            launch=lambda i: ctx.binary_backward(L.DIV, g_[i], x_[i], y_[i], dx_[i], dy_[i]),
+           ceil=(3, 2, n, [g_, x_, y_], [dx_, dy_]),
            cpu_fn=lambda: O.div_backward(g.ravel()[:ns], x.ravel()[:ns], y.ravel()[:ns]),
            cpu_scale=scale, cpu_sample=samp,
            check=lambda: same_bits(dy_[0].numpy().ravel()[:ns],
@@ -996,10 +1030,12 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
                bytes_=12.0 * n,
                launch=(lambda i, kind=kind, v_=v_: ctx.unary_backward(kind, g_[i], v_[i],
                                                                       dx_[i])),
+               ceil=(2, 1, n, [g_, v_], [dx_]),
                cpu_fn=cfn, cpu_scale=scale, cpu_sample=samp, check=chk,
                note="" if ofn is not None else "no numrs CPU path: the reference has no GELU")
     record("a21", "pow_backward (n=3)", "unary_backward(POW)", shape, bytes_=12.0 * n,
            launch=lambda i: ctx.unary_backward(L.POW, g_[i], x_[i], dx_[i], 3.0),
+           ceil=(2, 1, n, [g_, x_], [dx_]),
            cpu_fn=lambda: O.pow_backward(g.ravel()[:ns], x.ravel()[:ns], 3.0), cpu_scale=scale,
            cpu_sample=samp,
            check=lambda: close(dx_[0].numpy().ravel()[:ns],
@@ -1010,6 +1046,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a11", "transpose_backward", "transpose_reg_kernel", shape, bytes_=8.0 * n,
            launch=lambda i: ctx._check(L.load().numrs_hip_transpose(ctx.handle, g_[i].ptr,
                                                                       tr_[i].ptr, R, C)),
+           ceil=(1, 1, n, [g_], [tr_]),
            cpu_fn=lambda: O.transpose(g[:rs]), cpu_scale=R / rs,
            cpu_sample=f"first {rs} of {R} rows, scaled x{R / rs:g}",
            check=lambda: same_bits(tr_[0].numpy()[:, :rs], O.transpose(g[:rs])))
@@ -1018,6 +1055,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     g1_ = ctx.to_device(np.array([0.75], np.float32))
     record("a17", "mean_backward", "fill_grad", shape, bytes_=4.0 * n,
            launch=lambda i: ctx.fill_grad(g1_, dx_[i], divide_by_n=True),
+           ceil=(0, 1, n, [], [dx_]),
            cpu_fn=lambda: O.mean_backward(0.75, (ns,)), cpu_scale=scale, cpu_sample=samp,
            check=lambda: same_bits(dx_[0].numpy().ravel()[:16],
                                    O.mean_backward(0.75, (n,))[:16]))
@@ -1032,6 +1070,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a25", "ops::sum (full)", "reduce_pass1+final", shape, bytes_=4.0 * n,
            launch=lambda i: ctx._check(L.load().numrs_hip_sum(ctx.handle, g_[i].ptr, n, 0,
                                                                 s_.ptr)),
+           ceil=(1, 0, n, [g_], []),
            cpu_fn=lambda: O.sum_avx2_order_mt(gflat, nt), cpu_cores=nt, cpu_sample=mt_samp,
            check=lambda: abs(float(s_.numpy()[0]) - float(g.astype(np.float64).sum()))
            <= 1e-3 * np.sqrt(n))
@@ -1042,6 +1081,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a5", "unbroadcast (bias, CORRECT)", "colreduce_pass1+finalize", shape,
            bytes_=4.0 * n + 4.0 * C,
            launch=lambda i: ctx.sum_to_shape(g_[i], b_),
+           ceil=(1, 0, n, [g_], []),
            cpu_fn=lambda: O.sum_avx2_order_mt(gflat, nt), cpu_cores=nt,
            cpu_sample=mt_samp + " (numrs reduces with ops::sum, backward.rs:12-39)",
            check=lambda: close(b_.numpy(), g.astype(np.float64).sum(0), 1e-4, 1e-3))
@@ -1053,6 +1093,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a18", "mse_backward", "mse_backward_kernel", "[4096,512] (C4 output)",
            bytes_=12.0 * p.size,
            launch=lambda i: ctx.mse_backward(g1_, p_[i], t_[i], dp_[i]),
+           ceil=(2, 1, p.size, [p_, t_], [dp_]),
            cpu_fn=lambda: O.mse_backward(0.75, p, t), cpu_sample="whole input",
            check=lambda: same_bits(dp_[0].numpy(), O.mse_backward(0.75, p, t)[0]))
     del p_, t_, dp_
@@ -1067,6 +1108,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a19", "cross_entropy_backward", "softmax_ce_backward", f"[{B_},{C_}] one-hot",
            bytes_=12.0 * B_ * C_,
            launch=lambda i: ctx.softmax_ce_backward(g1_, lg_[i], dl_[i], onehot=oh_[i]),
+           ceil=(2, 1, B_ * C_, [lg_, oh_], [dl_]),
            cpu_fn=lambda: O.cross_entropy_backward(0.75, logits[:512], onehot[:512]),
            cpu_scale=B_ / 512, cpu_sample=f"first 512 of {B_} rows, scaled x{B_ / 512:g}",
            check=lambda: close(dl_[0].numpy()[:512],
@@ -1083,6 +1125,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("a20", "softmax_backward", "softmax_backward_kernel", "[32768,256] (C4 attention)",
            bytes_=12.0 * sm.size,
            launch=lambda i: ctx.softmax_backward(sm_[i], gs_[i], ds_[i]),
+           ceil=(2, 1, sm.size, [sm_, gs_], [ds_]),
            cpu_fn=lambda: O.softmax_backward(sm[:4096], gs[:4096]), cpu_scale=rows_s / 4096,
            cpu_sample=f"first 4096 of {rows_s} rows, scaled x{rows_s / 4096:g}",
            check=lambda: close(ds_[0].numpy()[:4096], O.softmax_backward(sm[:4096], gs[:4096]),
@@ -1102,6 +1145,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
            launch=lambda i: ctx._check(L.load().numrs_hip_layernorm_backward(
                ctx.handle, gl_[i].ptr, xl_[i].ptr, gam_.ptr, mean_[i].ptr, rstd_[i].ptr,
                dxl_[i].ptr, dgm_.ptr, dbt_.ptr, RL, 512, 0, 0, 0)),
+           ceil=(2, 1, xl.size, [xl_, gl_], [dxl_]),
            check=lambda: close(dxl_[0].numpy()[:4096],
                                O.layernorm_backward(gl[:4096], xl[:4096], gam)[0], 1e-4, 1e-5),
            note="no numrs CPU path: the reference has no LayerNorm; C4's own [4096,512] "
@@ -1114,6 +1158,7 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     record("N5", "argmax (rows, first max)", "argmax_vec", "[16384,1024]",
            bytes_=4.0 * am.size + 4.0 * 16384,
            launch=lambda i: ctx.argmax_rows(am_[i], idx_[i]),
+           ceil=(1, 0, am.size, [am_], []),
            cpu_fn=lambda: O.argmax_rows(am[:512]), cpu_scale=32.0,
            cpu_sample="first 512 of 16384 rows, scaled x32",
            check=lambda: np.array_equal(idx_[0].numpy(), O.argmax_rows(am)),

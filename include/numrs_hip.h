@@ -133,6 +133,16 @@ int numrs_hip_free(numrs_hip_ctx *ctx, void *dptr);
 int numrs_hip_upload(numrs_hip_ctx *ctx, void *dst, const void *host_src, size_t bytes);
 int numrs_hip_download(numrs_hip_ctx *ctx, void *host_dst, const void *src, size_t bytes);
 int numrs_hip_copy(numrs_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* No counterpart in the reference: a measurement aid for callers that time
+ * the library against the device.  One launch streams n floats (n % 4 == 0,
+ * operands 16-byte aligned) in the access pattern of the library's streaming
+ * kernels (float4, non-temporal from 2^23 floats on): it reads the first
+ * `reads` (0..3) of a, b, c and writes their sum to y and, for writes = 2,
+ * to z; writes = 0 stores nothing (y must still hold one float per 2048
+ * elements).  Its time is the ceiling a kernel moving the same bytes in the
+ * same read/write mix and number of launches can reach. */
+int numrs_hip_stream_probe(numrs_hip_ctx *ctx, const float *a, const float *b, const float *c,
+                           float *y, float *z, int64_t n, int reads, int writes);
 /* Fills `n` floats with `value` by a kernel (safe inside HIP graph capture).
  * value = 0 is Tensor::zero_grad (autograd/tensor.rs:135-142). */
 int numrs_hip_fill(numrs_hip_ctx *ctx, float *dst, int64_t n, float value);

@@ -33,6 +33,7 @@ SIGNATURES = {
     "numrs_hip_download": (_i, [_vp, _vp, _vp, _sz]),
     "numrs_hip_copy": (_i, [_vp, _vp, _vp, _sz]),
     "numrs_hip_fill": (_i, [_vp, _vp, _i64, _f]),
+    "numrs_hip_stream_probe": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i, _i]),
     "numrs_hip_sync": (_i, [_vp]),
     "numrs_hip_reserve": (_i, [_vp, _sz]),
     "numrs_hip_stream": (_vp, [_vp]),

@@ -418,6 +418,46 @@ __global__ void __launch_bounds__(kBlock)
   sgd_block<MOMENTUM, DECAY, VEC>(p, g, v, n, lr, mu, wd, blockIdx.x);
 }
 
+// The streaming probe (numrs_hip_stream_probe): y = a + b + c over the first
+// `reads` of a, b, c (zeros when reads = 0), stored to y and, when writes =
+// 2, to z; with writes = 0 nothing is stored (a block stores its first sum
+// into y[blk] only if it equals -1.25, so the loads stay live).  Blocks of
+// kElemsPerBlock, every load of a thread before its stores, as the other
+// streaming kernels here.
+template <int VEC>
+__global__ void __launch_bounds__(kBlock)
+    stream_probe_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                        const float *__restrict__ c, float *__restrict__ y,
+                        float *__restrict__ z, int64_t n, int reads, int writes) {
+  const int64_t blk = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t wbase = blk * kElemsPerBlock + (int64_t)wave * 256 * kVecPerThread + lane * 4;
+  f4 v[kVecPerThread], w[3][kVecPerThread];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    const float *src = r == 0 ? a : r == 1 ? b : c;
+#pragma unroll
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int64_t i = wbase + 256 * u;
+      w[r][u] = r < reads && i + 3 < n ? ldv<VEC>(src + i) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) v[u] = (w[0][u] + w[1][u]) + w[2][u];
+  if (writes == 0) {
+    if (v[0][0] == -1.25f) y[blk] = v[0][0];
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < kVecPerThread; ++u) {
+    const int64_t i = wbase + 256 * u;
+    if (i + 3 < n) {
+      stv<VEC>(y + i, v[u]);
+      if (writes == 2) stv<VEC>(z + i, v[u]);
+    }
+  }
+}
+
 struct AdamArgs {
   float lr, b1, b2, eps, wd, omb1, omb2, bc1, bc2;
 };
@@ -730,6 +770,29 @@ int numrs_hip_mse_backward(numrs_hip_ctx *ctx, const float *g_scalar, const floa
                            const float *t, float *dp, float *dt, int64_t n, int accumulate) {
   NRS_CHECK_CTX(ctx);
   return numrs_hip::mse_backward_impl(ctx, g_scalar, nullptr, p, t, dp, dt, n, accumulate);
+}
+
+int numrs_hip_stream_probe(numrs_hip_ctx *ctx, const float *a, const float *b, const float *c,
+                           float *y, float *z, int64_t n, int reads, int writes) {
+  NRS_CHECK_CTX(ctx);
+  if (int rc = check_n(ctx, "numrs_hip_stream_probe", n)) return rc;
+  if (reads < 0 || reads > 3 || writes < 0 || writes > 2 || n % 4 != 0)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID,
+                           "numrs_hip_stream_probe: reads %d writes %d n %lld", reads, writes,
+                           (long long)n);
+  if (n == 0) return NUMRS_HIP_OK;
+  const float *src[3] = {a, b, c};
+  bool ok = y != nullptr && numrs_hip::aligned16(y) && (writes < 2 || numrs_hip::aligned16(z));
+  for (int r = 0; r < reads; ++r) ok = ok && numrs_hip::aligned16(src[r]);
+  if (!ok)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID,
+                           "numrs_hip_stream_probe: null or unaligned operand");
+  const unsigned grid = grid_for(n, kElemsPerBlock);
+  numrs_hip::with_vec_mode(numrs_hip::vec_mode(true, n), [&](auto V) {
+    stream_probe_kernel<decltype(V)::value><<<grid, kBlock, 0, ctx->stream>>>(a, b, c, y, z, n,
+                                                                              reads, writes);
+  });
+  return numrs_hip::check_launch(ctx, "stream_probe_kernel");
 }
 
 int numrs_hip_sgd_step(numrs_hip_ctx *ctx, float *p, const float *g, float *v, int64_t n,

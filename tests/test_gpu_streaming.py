@@ -130,3 +130,31 @@ def test_sums_transpose_layernorm_streaming(hip_ctx, rng):
     wdx, wdg, wdb = O.layernorm_backward(gl[:2048], xl[:2048], gam)
     assert_close(dxl.numpy()[:2048], wdx, abs_tol=1e-5, rel_tol=1e-4, what="ln dx")
     assert_sum(db.numpy(), gl.astype(np.float64).sum(0), RL, what="ln dbeta")
+
+
+@pytest.mark.parametrize("n", [4096 + 4, 1 << 23], ids=["cached", "streaming"])
+@pytest.mark.parametrize("reads,writes", [(0, 1), (1, 0), (1, 1), (1, 2), (2, 1), (3, 2)])
+def test_stream_probe(hip_ctx, rng, n, reads, writes):
+    """numrs_hip_stream_probe (the bench's ceiling for the streaming rows):
+    y (and z) = (a + b) + c over the first `reads` operands, zeros for none;
+    nothing stored for writes = 0; bad arguments refused."""
+    say(f"stream_probe reads={reads} writes={writes} n={n}")
+    c = hip_ctx
+    ops = [rand(rng, n) for _ in range(3)]
+    dev = [c.to_device(a) for a in ops]
+    y = c.to_device(np.full(n, 7.0, np.float32))
+    z = c.to_device(np.full(n, 7.0, np.float32))
+    ptr = [d.ptr if i < reads else None for i, d in enumerate(dev)]
+    c._check(L.load().numrs_hip_stream_probe(c.handle, ptr[0], ptr[1], ptr[2], y.ptr,
+                                             z.ptr if writes == 2 else None, n, reads, writes))
+    used = [a if i < reads else np.zeros(n, np.float32) for i, a in enumerate(ops)]
+    want = (used[0] + used[1]) + used[2]
+    if writes == 0:
+        assert np.array_equal(y.numpy(), np.full(n, 7.0, np.float32))
+    else:
+        assert_bits(y.numpy(), want)
+    assert_bits(z.numpy(), want if writes == 2 else np.full(n, 7.0, np.float32))
+    from numrs_amd import HipError
+    with pytest.raises(HipError):
+        c._check(L.load().numrs_hip_stream_probe(c.handle, ptr[0], ptr[1], ptr[2], y.ptr,
+                                                 None, n + 2, reads, writes))
