@@ -1254,13 +1254,16 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     fwd_flops = prod * I5 + 3 * prod * H5          # x W_ih1^T, then h1 W_hh1^T, h1 W_ih2^T, h2 W_hh2^T
     bwd_flops = 3 * prod * H5 + 3 * prod * H5 + 2 * prod * I5  # recurrences; dW_ih2, dW_hh2, dW_hh1; dW_ih1, dx
     lstm_fwd(0)
-    record("N4", "LSTM x2 forward (new op)", "linear_forward + lstm2_fwd_persist",
+    record("N4", "LSTM x2 forward (new op)", "fill_bits + lstm2_fwd_persist",
            f"B {B5}, T {T5}, in {I5}, hidden {H5} (C5)", flops=fwd_flops, launch=lstm_fwd,
-           note="one persistent launch for all 128 steps of both layers; no numrs CPU path")
-    record("N4", "LSTM x2 backward (new op)", "lstm2_bwd_persist + weight-gradient GEMMs",
+           note="one persistent launch for all 128 steps of both layers, the first layer's "
+                "input projection inside the steps; no numrs CPU path")
+    record("N4", "LSTM x2 backward (new op)",
+           "lstm2_bwd_prep + lstm2_bwd_persist + 2 x (tn_pair_stream_small + splitk_reduce)",
            f"B {B5}, T {T5}, in {I5}, hidden {H5} (C5)", flops=bwd_flops, launch=lstm_bwd,
-           note="one persistent launch for all 128 steps of both layers, then the weight "
-                "gradients over all steps as single products; no numrs CPU path")
+           note="one persistent launch for all 128 steps of both layers (bias partials formed "
+                "in the steps), then each layer's dW_ih and dW_hh over all steps as one paired "
+                "launch; no numrs CPU path")
     del lw, x5_, seq, acts, dh2_, dx5_, dws
     return out
 
