@@ -598,6 +598,32 @@ def bench_c1(ctx, steps, warmup):
         out["graph_loss"] = gloss
     finally:
         g.close()
+    # The floor a chain of dependent launches sits on: seven of the smallest
+    # kernel the library has (numrs_hip_stream_probe writing four floats) on
+    # the same stream, recorded into a graph like the step above and replayed,
+    # so that the host's launch rate does not enter.
+    from numrs_amd import _lib as L
+    lib = L.load()
+    tiny = ctx.empty((4,))
+
+    def seven():
+        for _ in range(7):
+            ctx._check(lib.numrs_hip_stream_probe(ctx.handle, None, None, None, tiny.ptr, None,
+                                                  4, 0, 1))
+        return tiny
+    seven()
+    g7 = nr.StepGraph(ctx, seven)
+    try:
+        for _ in range(warmup):
+            g7.replay()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            g7.replay()
+        ctx.sync()
+        out["launch_floor_us"] = (time.perf_counter() - t0) / n / 7 * 1e6
+    finally:
+        g7.close()
     return out
 
 
@@ -1412,7 +1438,9 @@ def main() -> int:
         ent = {"workload": "C1 MLP train step 64x784->128->10, CE, SGD 0.01 "
                            "(forward+backward+step via the device autograd engine)",
                "value": round(c1["us_per_step"], 1), "unit": "us/step",
-               "bound": "latency", "final_loss": round(c1["loss"], 6)}
+               "bound": "latency", "kernels_per_step": 7,
+               "launch_floor_us": round(c1["launch_floor_us"], 2),
+               "final_loss": round(c1["loss"], 6)}
         if not args.no_cpu_baseline:
             ent["cpu_baseline"] = cpu_baseline_c1()
         secondary.append(ent)
@@ -1423,7 +1451,8 @@ def main() -> int:
                           "steps": c1["steps"], "bound": "latency",
                           "final_loss": round(c1["graph_loss"], 6)})
         log(f"  C1 MLP step {c1['us_per_step']:.1f} us, graph replay "
-            f"{c1['graph_us_per_step']:.1f} us")
+            f"{c1['graph_us_per_step']:.1f} us, dependent-launch floor "
+            f"{c1['launch_floor_us']:.2f} us (7 tiny kernels, graph-replayed)")
         c4 = bench_c4(ctx, max(10, args.steps), 3)
         ent = {"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
                            "heads, FFN 2048 GELU, MSE, SGD) via the device engine",
