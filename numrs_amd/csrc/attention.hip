@@ -176,8 +176,8 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   auto row_reduce = [&](float (&v)[2], int op) {
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
-      const float o = __shfl_xor(v[bi], 32, 64);
-      v[bi] = op == 0 ? fmaxf(v[bi], o) : v[bi] + o;
+      v[bi] = op == 0 ? half_pair(v[bi], [](float x, float y) { return fmaxf(x, y); })
+                      : half_pair(v[bi], [](float x, float y) { return x + y; });
       if (hh == 0) red[wave][32 * bi + c] = v[bi];
     }
     __syncthreads();
@@ -476,8 +476,8 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
   auto row_reduce = [&](float (&v)[2], int op) {
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
-      const float o = __shfl_xor(v[bi], 32, 64);
-      v[bi] = op == 0 ? fmaxf(v[bi], o) : v[bi] + o;
+      v[bi] = op == 0 ? half_pair(v[bi], [](float x, float y) { return fmaxf(x, y); })
+                      : half_pair(v[bi], [](float x, float y) { return x + y; });
       if (hh == 0) red[wave][32 * bi + c] = v[bi];
     }
     __syncthreads();
@@ -757,8 +757,7 @@ __global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
 #pragma unroll
       for (int u = 0; u < 4; ++u) sum += d[u] * of[e][u];
     }
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    sum = quad_sum(sum);
     if ((lane & 3) == 0) lds[kDOff + r] = sum;
   };
 

@@ -322,15 +322,61 @@ inline unsigned grid_for(int64_t work_items, int per_block) {
   return static_cast<unsigned>(g);
 }
 
-// Wavefront (64 lanes) reductions via DPP-free cross-lane shuffles.
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// Wavefront (64 lanes) reductions: a butterfly over lane distances 32, 16,
+// 8, 4, 2, 1, after which every lane holds the same value, formed from the
+// same pairs in the same order as an xor-shuffle butterfly.  The exchanges
+// stay in registers (one VALU operation each, against an LDS-crossbar round
+// trip per ds_bpermute step of __shfl_xor):
+//   distance 32: v_permlane32_swap of v with itself returns (low halves,
+//                high halves) in every lane;
+//   distance 16: v_permlane16_swap likewise returns (even rows, odd rows) of
+//                each 32-lane half;
+//   distance 8:  DPP row_ror:8 within each 16-lane row;
+//   distance 4:  DPP row_half_mirror (lane i of 8 reads 7 - i = i ^ 7), then
+//                a reversed quad (i ^ 3);
+//   distance 2, 1: DPP quad permutations [2,3,0,1] and [1,0,3,2].
+// x + y and fmaxf(x, y) give the same bits as y + x and fmaxf(y, x) on gfx950
+// (signed zeros and NaN payloads included), so which operand of a pair a
+// lane holds does not change the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+
+template <class Op>
+__device__ __forceinline__ float wave_butterfly(float v, Op op) {
+  const unsigned u32 = __builtin_bit_cast(unsigned, v);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u32, u32, false, false);
+  v = op(__builtin_bit_cast(float, (unsigned)r32[0]), __builtin_bit_cast(float, (unsigned)r32[1]));
+  const unsigned u16 = __builtin_bit_cast(unsigned, v);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u16, u16, false, false);
+  v = op(__builtin_bit_cast(float, (unsigned)r16[0]), __builtin_bit_cast(float, (unsigned)r16[1]));
+  v = op(v, dpp_mov<0x128>(v));                    // row_ror:8
+  v = op(v, dpp_mov<0x1B>(dpp_mov<0x141>(v)));     // row_half_mirror, quad [3,2,1,0]
+  v = op(v, dpp_mov<0x4E>(v));                     // quad [2,3,0,1]
+  v = op(v, dpp_mov<0xB1>(v));                     // quad [1,0,3,2]
   return v;
 }
 
+// v op (v of the lane 32 away), in every lane: the first butterfly level.
+template <class Op>
+__device__ __forceinline__ float half_pair(float v, Op op) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return op(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
+// Sum over each quad of lanes: distance 1, then distance 2.
+__device__ __forceinline__ float quad_sum(float v) {
+  v = v + dpp_mov<0xB1>(v);
+  return v + dpp_mov<0x4E>(v);
+}
+
+__device__ inline float wave_sum(float v) {
+  return wave_butterfly(v, [](float a, float b) { return a + b; });
+}
+
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  return wave_butterfly(v, [](float a, float b) { return fmaxf(a, b); });
 }

@@ -633,8 +633,7 @@ __device__ __forceinline__ void bwd_step_tile(const BwdStep &s, int blk, int B, 
     r = (((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]))) +
         (((p2[0] + p2[1]) + (p2[2] + p2[3])) + ((p3[0] + p3[1]) + (p3[2] + p3[3])));
   }
-  r += __shfl_xor(r, 1, 64);
-  r += __shfl_xor(r, 2, 64);
+  r = quad_sum(r);
   if (!epi) return;
   float dg[4], dcf;
   cell_backward(a, c, cp, dho + r, dcn, dg, dcf);
