@@ -1309,6 +1309,10 @@ def main() -> int:
     ap.add_argument("--cpu-rows-b", type=int, default=192)
     ap.add_argument("--rows", action="store_true",
                     help="measure every hot-path row's kernel instead (one JSON line per row)")
+    ap.add_argument("--split-reduction", choices=["fused", "separate"], default="fused",
+                    help="where split-K partials are added (numrs_hip_set_split_reduction): "
+                         "inside the products' own launch (fused, the default) or by one more "
+                         "launch (separate); the same bits either way")
     ap.add_argument("--recurrence", choices=["auto", "per_step", "plain_launch", "cooperative"],
                     default="auto",
                     help="how the LSTM recurrences run (numrs_hip_set_recurrence_mode): auto "
@@ -1352,6 +1356,7 @@ def main() -> int:
 
     ctx = Context(0)
     ctx.set_recurrence_mode(args.recurrence)
+    ctx.set_split_reduction(args.split_reduction)
     n_cus, arch = ctx.info()
     log(f"device {arch}, {n_cus} CUs")
     rng = np.random.default_rng(SEED)

@@ -218,6 +218,18 @@ int numrs_hip_matmul_backward_batched(numrs_hip_ctx *ctx, const float *dC, const
 int numrs_hip_matmul(numrs_hip_ctx *ctx, const float *A, const float *B, float *C, int64_t M,
                      int64_t K, int64_t N, int trans_a, int trans_b, int accumulate);
 
+/* No counterpart in the reference: where the products of one call cut their
+ * reduction into split-K ranges (weight gradients over many tokens), how the
+ * partial products are added.  FUSED (the default): inside the products' own
+ * launch -- the grid's last workgroups (or the last split to arrive) add each
+ * output block's partials once all of its splits have stored them, with no
+ * workgroup waiting for another.  SEPARATE: one more launch after the
+ * products.  Both add the splits in the same order with the same
+ * arithmetic: the same bits. */
+#define NUMRS_HIP_SPLIT_REDUCE_FUSED 0
+#define NUMRS_HIP_SPLIT_REDUCE_SEPARATE 1
+int numrs_hip_set_split_reduction(numrs_hip_ctx *ctx, int mode);
+
 /* Batched form of numrs_hip_matmul with element strides between matrices. */
 int numrs_hip_matmul_batched(numrs_hip_ctx *ctx, const float *A, const float *B, float *C,
                              int64_t batch, int64_t M, int64_t K, int64_t N, int64_t stride_a,

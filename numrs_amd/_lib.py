@@ -104,6 +104,7 @@ SIGNATURES = {
     "numrs_hip_is_grad_enabled": (_i, []),
     "numrs_hip_set_unbroadcast_mode": (_i, [_vp, _i]),
     "numrs_hip_set_recurrence_mode": (_i, [_vp, _i]),
+    "numrs_hip_set_split_reduction": (_i, [_vp, _i]),
     "numrs_hip_persistent_launches": (_i64, [_vp]),
     "numrs_hip_set_persistent_wait_limit": (_i, [_vp, _i]),
     "numrs_hip_tensor_new": (_i, [_vp, _vp, _i64p, _i, _i, ctypes.POINTER(_vp)]),

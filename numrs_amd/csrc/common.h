@@ -65,6 +65,13 @@ struct numrs_hip_ctx {
   int persist_bwd_per_cu = -1;
   int64_t persist_launches = 0;  // persistent launches queued on this context
   int persist_wait_limit = -1;   // wait rounds before a give-up (-1: the kernels' default)
+  // Arrival counters of the products that reduce their split-K partials
+  // inside their own launch (gemm.hip): zero between launches -- each
+  // launch's last arrival at a counter sets it back -- so they are cleared
+  // only when the region is allocated.
+  unsigned *arrivals = nullptr;
+  size_t arrival_words = 0;
+  int split_reduce_mode = NUMRS_HIP_SPLIT_REDUCE_FUSED;  // numrs_hip_set_split_reduction
   // Device address of reduce.hip's static partials array on this context's
   // device, resolved at creation (the allocation-free entry point uses it).
   float *noalloc_partials = nullptr;
@@ -82,6 +89,10 @@ int workspace(numrs_hip_ctx *ctx, size_t bytes, void **out);
 
 // Second scratch region (see numrs_hip_ctx::scratch).
 int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out);
+
+// The context's arrival counters, at least `words` of them, all zero when
+// the stream reaches the next launch (grows and clears the region).
+int arrival_counters(numrs_hip_ctx *ctx, size_t words, unsigned **out);
 
 // Cached device allocation for engine tensors; sizes are rounded up so that
 // released blocks are reusable.  block_free returns the block to the cache

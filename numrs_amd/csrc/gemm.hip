@@ -91,6 +91,9 @@ struct Gemm {
   // into the product's epilogue (batch-1 products).
   const float *res;
   int64_t ldr;
+  // Split products reduced inside their own launch: per output tile, eight
+  // arrival counters (one per sub-block of TP/8 rows); null otherwise.
+  unsigned *arrive;
 };
 
 // Epilogue activations: the ReLU forward kernel's x.max(0) and the unary
@@ -351,12 +354,13 @@ constexpr int kColSumClasses = 256 / kColSumLanes;  // row classes of a workgrou
 // Column groups of a [., cols] block.
 __host__ __device__ inline int64_t colsum_groups(int64_t cols) { return (cols + kColSumCols - 1) / kColSumCols; }
 
+// Threads past the first 256 of a larger workgroup only meet the barriers.
 __device__ __forceinline__ void colsum_block(const ColSum &c, int64_t blk) {
   __shared__ f4 red[256];
   const int k = threadIdx.x;
   const int j = k % kColSumLanes, rc = k / kColSumLanes;  // column chunk, row class
   const float *p = c.g + blk * kColSumCols + 4 * j;
-  const bool live = blk * kColSumCols + 4 * j < c.cols;
+  const bool live = k < 256 && blk * kColSumCols + 4 * j < c.cols;
   f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int64_t r0 = rc; live && r0 < c.rows; r0 += kColSumClasses * 16) {
     f4 v[16];
@@ -368,7 +372,7 @@ __device__ __forceinline__ void colsum_block(const ColSum &c, int64_t blk) {
 #pragma unroll
     for (int u = 0; u < 16; ++u) s += v[u];
   }
-  red[k] = s;  // k = kColSumLanes * class + chunk
+  if (k < 256) red[k] = s;  // k = kColSumLanes * class + chunk
   __syncthreads();
   // 64 partials: chunk t % lanes, classes 4 (t / lanes) .. + 3, added in order
   f4 t = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -398,6 +402,56 @@ __device__ __forceinline__ int64_t colsum_group(int b, int n, int64_t m) {
   const int64_t idx = b >> 3;
   return idx < (m >> 3) ? (b & 7) * (m >> 3) + idx : -1;
 }
+
+// Adds the splits' values v[0..n) to the running sum s in split order, plain
+// or compensated (kahan): the operations of splitk_reduce's loop, for the
+// reductions made inside a product's launch (Fused).
+template <class V, int N>
+__device__ __forceinline__ void add_splits(int kahan, V &s, V &comp, const V (&v)[N], int n) {
+  if (kahan) {
+#pragma unroll
+    for (int u = 0; u < N; ++u)
+      if (u < n) {
+        const V y = v[u] - comp;
+        const V t = s + y;
+        comp = (t - s) - y;
+        s = t;
+      }
+  } else {
+#pragma unroll
+    for (int u = 0; u < N; ++u)
+      if (u < n) s += v[u];
+  }
+}
+
+// The end of a split reduction at C[p, q..]: alpha, bias, residual,
+// accumulate, activation (pre-activation stored first) -- splitk_reduce's
+// epilogue, operation for operation.  Takes the set's fields one by one (a
+// reference to a kernel argument, once inlined, had fields copied to private
+// memory).  splitk_reduce keeps its own copy of this arithmetic: with these
+// helpers inlined its set selection was promoted to LDS.
+template <class V>
+__device__ __forceinline__ void finish_split(float *C, int64_t ldc, const float *bias,
+                                             const float *res, int64_t ldr, int acc, float alpha,
+                                             int act, float *pre, int64_t p, int64_t q, V s) {
+  V *dst = reinterpret_cast<V *>(C + p * ldc + q);
+  V v = alpha * s;
+  if (bias != nullptr) v = v + *reinterpret_cast<const V *>(bias + q);
+  if (res != nullptr) v = v + *reinterpret_cast<const V *>(res + p * ldr + q);
+  v = acc ? *dst + v : v;
+  if (act) {
+    if (pre != nullptr) *reinterpret_cast<V *>(pre + p * ldc + q) = v;
+    if constexpr (std::is_same<V, f4>::value) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = act_value(act, v[e]);
+    } else {
+      v = act_value(act, v);
+    }
+  }
+  *dst = v;
+}
+#define NRS_FINISH_SPLIT(d, p, q, s) \
+  finish_split((d).C, (d).ldc, (d).bias, (d).res, (d).ldr, (d).acc, (d).alpha, (d).act, (d).pre, p, q, s)
 
 // Splits are added in order s = 0, 1, ... (deterministic); the loads of a
 // batch of splits are issued before its ordered adds.  With column sums
@@ -644,23 +698,34 @@ __device__ __forceinline__ void stream_read(
     f.b[j] = stream_frag<YRC, TQ>(yl, wq * (TQ / 2) + 32 * j, c, h, g);
 }
 
+// Output tile (tp, tq) of logical tile `tile`: tiles run in groups of
+// kGroupRows tile rows, column by column within a group.
+__device__ __forceinline__ void tile_rc(int tiles_p, int tiles_q, int tile, int &tp, int &tq) {
+  const int per_group = kGroupRows * tiles_q;
+  const int gidx = tile / per_group;
+  const int first_p = gidx * kGroupRows;
+  const int rows_in_group = min(tiles_p - first_p, kGroupRows);
+  const int in_group = tile - gidx * per_group;
+  tp = first_p + in_group % rows_in_group;
+  tq = in_group / rows_in_group;
+}
+
 // ACT: the epilogue applies d.act (and stores d.pre); a separate
 // instantiation, so products without an activation keep the plain epilogue.
-template <bool XRC, bool YRC, int TP, int TQ, int NW = 4, bool ACT = false>
-__device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) {
+// FUSE (the fused launches of Fused, whose split products carry d.arrive):
+// returns -1, or, for a split whose partial completed the arrivals at some of
+// its tile's sub-blocks, (output tile << 8) | mask of those sub-blocks, which
+// the caller then reduces.  Without FUSE, -1.
+template <bool XRC, bool YRC, int TP, int TQ, int NW = 4, bool ACT = false, bool FUSE = false>
+__device__ __forceinline__ int stream_tile(const Gemm &d, int tile, int batch) {
   using Cfg = StreamCfg<TP, TQ, NW>;
   constexpr int kBI = Cfg::kBI, kBJ = Cfg::kBJ, kDma = Cfg::kDma;
   // Split-K: consecutive logical tiles are the k-ranges of one output tile
   // (the planner leaves no range empty).
   const int split = tile % d.splits;
   tile /= d.splits;
-  const int per_group = kGroupRows * d.tiles_q;
-  const int gidx = tile / per_group;
-  const int first_p = gidx * kGroupRows;
-  const int rows_in_group = min(d.tiles_p - first_p, kGroupRows);
-  const int in_group = tile - gidx * per_group;
-  const int tp = first_p + in_group % rows_in_group;
-  const int tq = in_group / rows_in_group;
+  int tp, tq;
+  tile_rc(d.tiles_p, d.tiles_q, tile, tp, tq);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -856,7 +921,10 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
         const int p = p0 + wp * Cfg::kWP + bi * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         float *dst = C + (int64_t)p * ldc + q;
         if (part) {
-          *dst = tot[bi][bj][i];
+          if constexpr (FUSE)
+            numrs_hip::st_dev(dst, tot[bi][bj][i]);  // read by another workgroup
+          else
+            *dst = tot[bi][bj][i];
         } else {
           float v = d.alpha * tot[bi][bj][i];
           if (d.bias != nullptr) v = v + bq[bj];
@@ -870,6 +938,32 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
         }
       }
     }
+  if constexpr (!FUSE) {
+    return -1;
+  } else {
+  if (!part) return -1;
+  // Arrival: every lane's partial stores acknowledged at device scope, the
+  // block met; then one counter per sub-block of this tile.  splits + 1
+  // arrivals in all (the splits and the sub-block's reducer workgroup); the
+  // last one reduces and sets the counter back to zero.
+  __shared__ int s_arrived;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    bool last = false;
+    if (threadIdx.x < 8) {
+      unsigned *ctr = d.arrive + (int64_t)tile * 8 + threadIdx.x;
+      last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)d.splits;
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const unsigned long long m = __ballot(last);
+    if (threadIdx.x == 0) s_arrived = (int)(m & 0xffu);
+  }
+  __syncthreads();
+  const int mask = s_arrived;
+  return mask != 0 ? (tile << 8) | mask : -1;
+  }
 }
 
 // Large tiles run eight waves (two per SIMD, 64 x 64 outputs each): while
@@ -877,6 +971,169 @@ __device__ __forceinline__ void stream_tile(const Gemm &d, int tile, int batch) 
 // MFMAs issue (measured 3-4% faster than four waves of 128 x 64 at 2048^3).
 constexpr int kBigWaves = 8;
 constexpr int kBigThreads = 64 * kBigWaves;
+
+// ---------------------------------------------------------------------------
+// Split products reduced inside their own launch.  A batch-1 streamed launch
+// of products a and b may end its grid with tail workgroups after the n_units
+// product workgroups:
+//   * one reducer per (split product, output tile, sub-block of TP/8 rows);
+//   * (padding to the next multiple of eight hardware ids, so that the
+//     column sums start on XCD 0 as in splitk_reduce);
+//   * the column sums `cs`, as splitk_reduce's grid row 0 forms them;
+//   * an independent split set `extra` (row partials of an earlier kernel),
+//     NT float4 groups per workgroup.
+// Each split of a tile stores its partial with device-scope (write-through)
+// stores, waits until they are acknowledged, and then adds one to the
+// arrival counter of each of the tile's eight sub-blocks; each reducer adds
+// one to its own.  Of the splits + 1 arrivals, the last reduces the
+// sub-block -- normally the reducer, which is dispatched after every product
+// workgroup; a split that arrives after it does the work itself -- and sets
+// the counter back to zero, so the counters are zero again for the next
+// launch (and for each replay of a recorded graph).  No workgroup waits for
+// another.  The partials are read at device scope, added in split order by
+// add_splits and finished by finish_split: the bits of splitk_reduce.
+// Order of the grid: with exactly one product split (and both unit counts
+// multiples of 8), the split units come first (each XCD its share), then the
+// tail, then the unsplit units -- workgroups are dispatched in hardware-id
+// order, so the reductions run on the CUs the splits free while the unsplit
+// tiles still run elsewhere; otherwise the product units in xcd_tile's order
+// and the tail after them.
+struct Fused {
+  int n_units;               // product workgroups; 0: not a fused launch
+  int n_tail;                // tail workgroups (a multiple of 8 when first_n > 0)
+  int first_n, first_base, rest_base;  // unit order (first_n = 0: xcd_tile)
+  SplitSet set[2];           // the reductions of products a and b (splits 0: none)
+  int tiles_p[2], tiles_q[2];
+  unsigned *count[2];        // arrival counters, 8 per output tile
+  int sub[2];                // reducer workgroups per set (8 per output tile)
+  int pad;                   // idle tail workgroups before the column sums
+  ColSum cs;
+  int cs_wgs;                // column-sum workgroups (a multiple of 8 when the groups are)
+  SplitSet extra;
+  int extra_wgs;
+};
+
+// Hardware id b -> product unit, or -1 - (tail index).
+__device__ __forceinline__ int fused_unit(int b, const Fused &f) {
+  if (f.first_n <= 0) return b < f.n_units ? xcd_tile(b, f.n_units) : -1 - (b - f.n_units);
+  if (b < f.first_n) return f.first_base + (b & 7) * (f.first_n >> 3) + (b >> 3);
+  if (b < f.first_n + f.n_tail) return -1 - (b - f.first_n);
+  const int r = b - f.first_n - f.n_tail;  // r % 8 == b % 8: n_first and n_tail are multiples of 8
+  return f.rest_base + (r & 7) * ((f.n_units - f.first_n) >> 3) + (r >> 3);
+}
+
+// Sub-block j of output tile `tile` of a split set: NT threads, each a float4
+// group of the sub-block's TP/8 rows x TQ columns per pass.
+template <int TP, int TQ, int NT>
+__device__ __forceinline__ void fused_reduce_sub(const SplitSet &d, int tiles_p, int tiles_q, int tile, int j) {
+  int tp, tq;
+  tile_rc(tiles_p, tiles_q, tile, tp, tq);
+  constexpr int kRows = TP / 8, kC4 = TQ / 4, kF4 = kRows * kC4;
+  constexpr int kPass = (kF4 + NT - 1) / NT;  // float4 groups per thread
+  constexpr int kBatch = 8;                  // splits loaded together
+  const __amdgpu_buffer_rsrc_t rs = numrs_hip::dev_rsrc(d.partial, (int64_t)d.splits * d.n * 4);
+  int64_t p[kPass], q[kPass], e[kPass];
+  f4 s[kPass], comp[kPass];
+#pragma unroll
+  for (int i = 0; i < kPass; ++i) {
+    const int f = threadIdx.x + i * NT;
+    const int r = f / kC4, c4 = f - r * kC4;
+    p[i] = (int64_t)tp * TP + j * kRows + r;
+    q[i] = (int64_t)tq * TQ + 4 * c4;
+    e[i] = p[i] * d.Q + q[i];
+    s[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    comp[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  for (int k0 = 0; k0 < d.splits; k0 += kBatch) {
+    f4 v[kPass][kBatch];
+#pragma unroll
+    for (int i = 0; i < kPass; ++i)
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < d.splits && threadIdx.x + i * NT < kF4)
+          v[i][u] = numrs_hip::ld_dev4(rs, (int)(4 * ((k0 + u) * d.n + e[i])));
+#pragma unroll
+    for (int i = 0; i < kPass; ++i) add_splits(d.kahan, s[i], comp[i], v[i], d.splits - k0);
+  }
+#pragma unroll
+  for (int i = 0; i < kPass; ++i)
+    if (threadIdx.x + i * NT < kF4) NRS_FINISH_SPLIT(d, p[i], q[i], s[i]);
+}
+
+// The sub-blocks in `mask` of the output tile in `r` (stream_tile's return).
+template <int TP, int TQ, int NT>
+__device__ __forceinline__ void fused_reduce_mask(const Fused &f, int set, int r) {
+  const int tile = r >> 8;
+  for (int j = 0; j < 8; ++j)
+    if ((r >> j) & 1) fused_reduce_sub<TP, TQ, NT>(f.set[set], f.tiles_p[set], f.tiles_q[set], tile, j);
+}
+
+// A reducer's arrival: true for the last of the splits + 1 arrivals.
+__device__ __forceinline__ bool fused_arrive(unsigned *ctr, int splits) {
+  __shared__ int s_last;
+  if (threadIdx.x == 0) {
+    const bool last =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)splits;
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
+// Tail workgroup u (hardware id n_units + u).
+template <int TP, int TQ, int NT>
+__device__ __forceinline__ void fused_tail(const Fused &f, int u) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (u < f.sub[k]) {
+      if (fused_arrive(f.count[k] + u, f.set[k].splits))
+        fused_reduce_sub<TP, TQ, NT>(f.set[k], f.tiles_p[k], f.tiles_q[k], u >> 3, u & 7);
+      return;
+    }
+    u -= f.sub[k];
+  }
+  if (u < f.pad) return;
+  u -= f.pad;
+  if (u < f.cs_wgs) {
+    const int64_t grp = colsum_group(u, f.cs_wgs, colsum_groups(f.cs.cols));
+    if (grp >= 0) colsum_block(f.cs, grp);
+    return;
+  }
+  u -= f.cs_wgs;
+  if (u < f.extra_wgs) {
+    const SplitSet &d = f.extra;
+    const int64_t e = ((int64_t)u * NT + threadIdx.x) * 4;
+    if (e < d.n) {
+      f4 s = {0.0f, 0.0f, 0.0f, 0.0f}, comp = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k0 = 0; k0 < d.splits; k0 += 4) {
+        f4 v[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          if (k0 + w < d.splits) v[w] = *reinterpret_cast<const f4 *>(d.partial + (k0 + w) * d.n + e);
+        add_splits(d.kahan, s, comp, v, d.splits - k0);
+      }
+      const int64_t p = e / d.Q, q = e - p * d.Q;
+      NRS_FINISH_SPLIT(d, p, q, s);
+    }
+  }
+}
+
+// A pair kernel's body: the fused tail, or product a's tiles [0, tiles_a)
+// then product b's (with a fused launch's reductions for sets 0 and 1).
+template <bool XA, bool YA, int TP, int TQ, int NW, int NT, bool FUSE>
+__device__ __forceinline__ void pair_body(const Gemm &a, const Gemm &b, int tiles_a, const Fused &f,
+                                          int tile, int batch) {
+  if (tile < tiles_a) {
+    const int r = stream_tile<XA, YA, TP, TQ, NW, false, FUSE>(a, tile, batch);
+    if constexpr (FUSE)
+      if (r >= 0) fused_reduce_mask<TP, TQ, NT>(f, 0, r);
+  } else {
+    const int r = stream_tile<false, false, TP, TQ, NW, false, FUSE>(b, tile - tiles_a, batch);
+    if constexpr (FUSE)
+      if (r >= 0) fused_reduce_mask<TP, TQ, NT>(f, 1, r);
+  }
+}
 
 template <bool XRC, bool YRC, bool ACT = false>
 __global__ void __launch_bounds__(kBigThreads, 1) gemm_stream_kernel(Gemm d) {
@@ -900,38 +1157,49 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_stream_mini(Gemm d) {
 // Pairs on the streamed path, logical tiles [0, tiles_a) for the first
 // product.  matmul_backward: dA = dC B^T (NT) with dB = A^T dC (TN); the
 // Linear backward: dx = g W (NN) with dW = g^T x (TN).
-__global__ void __launch_bounds__(kBigThreads, 1) matmul_backward_stream(Gemm da, Gemm db, int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  if (tile < tiles_a)
-    stream_tile<true, true, kSP, kSQ, kBigWaves>(da, tile, blockIdx.y);
-  else
-    stream_tile<false, false, kSP, kSQ, kBigWaves>(db, tile - tiles_a, blockIdx.y);
+// A pair kernel's workgroup: with f.n_units != 0 (batch 1) a fused launch,
+// whose hardware ids past n_units are tail workgroups and whose product units
+// follow fused_unit's order; otherwise xcd_tile's (plain) or
+// xcd_tile_batch's (BATCHED) order.  False for a tail workgroup, which has
+// then done its work.
+template <int TP, int TQ, int NT, bool BATCHED, bool FUSE>
+__device__ __forceinline__ bool pair_unit(const Fused &f, int &tile, int &batch);
+
+// FUSE: the fused launches' instantiation (Fused); the others keep the plain
+// epilogue and order.
+template <bool XA, bool YA, int TP, int TQ, int NW, int NT, bool BATCHED, bool FUSE>
+__device__ __forceinline__ void pair_kernel_body(const Gemm &a, const Gemm &b, int tiles_a,
+                                                 const Fused &f) {
+  int tile, batch;
+  if (!pair_unit<TP, TQ, NT, BATCHED, FUSE>(f, tile, batch)) return;
+  // uniform by construction; said so, so that the DMA bases stay scalar
+  tile = __builtin_amdgcn_readfirstlane(tile);
+  batch = __builtin_amdgcn_readfirstlane(batch);
+  pair_body<XA, YA, TP, TQ, NW, NT, FUSE>(a, b, tiles_a, f, tile, batch);
 }
 
-__global__ void __launch_bounds__(kThreads, 2) matmul_backward_stream_small(Gemm da, Gemm db,
-                                                                            int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  if (tile < tiles_a)
-    stream_tile<true, true, kHP, kHQ>(da, tile, blockIdx.y);
-  else
-    stream_tile<false, false, kHP, kHQ>(db, tile - tiles_a, blockIdx.y);
+template <bool FUSE>
+__global__ void __launch_bounds__(kBigThreads, 1)
+    matmul_backward_stream(Gemm a, Gemm b, int tiles_a, Fused f) {
+  pair_kernel_body<true, true, kSP, kSQ, kBigWaves, kBigThreads, false, FUSE>(a, b, tiles_a, f);
 }
 
-__global__ void __launch_bounds__(kBigThreads, 1) linear_backward_stream(Gemm dx, Gemm dw, int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  if (tile < tiles_a)
-    stream_tile<true, false, kSP, kSQ, kBigWaves>(dx, tile, blockIdx.y);
-  else
-    stream_tile<false, false, kSP, kSQ, kBigWaves>(dw, tile - tiles_a, blockIdx.y);
+template <bool FUSE>
+__global__ void __launch_bounds__(kThreads, 2)
+    matmul_backward_stream_small(Gemm a, Gemm b, int tiles_a, Fused f) {
+  pair_kernel_body<true, true, kHP, kHQ, 4, kThreads, false, FUSE>(a, b, tiles_a, f);
 }
 
-__global__ void __launch_bounds__(kThreads, 2) linear_backward_stream_small(Gemm dx, Gemm dw,
-                                                                            int tiles_a) {
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  if (tile < tiles_a)
-    stream_tile<true, false, kHP, kHQ>(dx, tile, blockIdx.y);
-  else
-    stream_tile<false, false, kHP, kHQ>(dw, tile - tiles_a, blockIdx.y);
+template <bool FUSE>
+__global__ void __launch_bounds__(kBigThreads, 1)
+    linear_backward_stream(Gemm a, Gemm b, int tiles_a, Fused f) {
+  pair_kernel_body<true, false, kSP, kSQ, kBigWaves, kBigThreads, false, FUSE>(a, b, tiles_a, f);
+}
+
+template <bool FUSE>
+__global__ void __launch_bounds__(kThreads, 2)
+    linear_backward_stream_small(Gemm a, Gemm b, int tiles_a, Fused f) {
+  pair_kernel_body<true, false, kHP, kHQ, 4, kThreads, false, FUSE>(a, b, tiles_a, f);
 }
 
 __global__ void __launch_bounds__(kThreads, 3) matmul_backward_stream_mini(Gemm da, Gemm db,
@@ -970,22 +1238,34 @@ __device__ __forceinline__ void xcd_tile_batch(int &tile, int &batch) {
 
 // Two transposed-left products in one launch (attention's dV = P^T dO with
 // dK = alpha dS^T Q): both TN.
-__global__ void __launch_bounds__(kBigThreads, 1) tn_pair_stream(Gemm a, Gemm b, int tiles_a) {
-  int tile, batch;
-  xcd_tile_batch(tile, batch);
-  if (tile < tiles_a)
-    stream_tile<false, false, kSP, kSQ, kBigWaves>(a, tile, batch);
-  else
-    stream_tile<false, false, kSP, kSQ, kBigWaves>(b, tile - tiles_a, batch);
+template <int TP, int TQ, int NT, bool BATCHED, bool FUSE>
+__device__ __forceinline__ bool pair_unit(const Fused &f, int &tile, int &batch) {
+  if constexpr (FUSE) {
+    const int u = fused_unit(blockIdx.x, f);
+    if (u < 0) {
+      fused_tail<TP, TQ, NT>(f, -1 - u);
+      return false;
+    }
+    tile = u;
+    batch = 0;
+  } else if (BATCHED) {
+    xcd_tile_batch(tile, batch);
+  } else {
+    tile = xcd_tile(blockIdx.x, gridDim.x);
+    batch = blockIdx.y;
+  }
+  return true;
 }
 
-__global__ void __launch_bounds__(kThreads, 2) tn_pair_stream_small(Gemm a, Gemm b, int tiles_a) {
-  int tile, batch;
-  xcd_tile_batch(tile, batch);
-  if (tile < tiles_a)
-    stream_tile<false, false, kHP, kHQ>(a, tile, batch);
-  else
-    stream_tile<false, false, kHP, kHQ>(b, tile - tiles_a, batch);
+template <bool FUSE>
+__global__ void __launch_bounds__(kBigThreads, 1) tn_pair_stream(Gemm a, Gemm b, int tiles_a, Fused f) {
+  pair_kernel_body<false, false, kSP, kSQ, kBigWaves, kBigThreads, true, FUSE>(a, b, tiles_a, f);
+}
+
+template <bool FUSE>
+__global__ void __launch_bounds__(kThreads, 2) tn_pair_stream_small(Gemm a, Gemm b, int tiles_a,
+                                                                    Fused f) {
+  pair_kernel_body<false, false, kHP, kHQ, 4, kThreads, true, FUSE>(a, b, tiles_a, f);
 }
 
 __global__ void __launch_bounds__(kThreads, 3) tn_pair_stream_mini(Gemm a, Gemm b, int tiles_a) {
@@ -1454,6 +1734,129 @@ int stream_prepare(numrs_hip_ctx *ctx, const StreamPlan &pl, Gemm &ga, Gemm *gb)
 
 int64_t stream_grid(const Gemm &g) { return (int64_t)g.tiles_p * g.tiles_q * g.splits; }
 
+SplitSet split_set(const Gemm &d) {
+  return SplitSet{d.partial, d.C, d.bias, d.ldc, (int64_t)d.P * d.Q, d.Q, d.splits,
+                  d.accumulate, d.alpha, d.act, d.pre, d.res, d.ldr, 0};
+}
+
+// splitk_reduce's float4 conditions for a set.
+bool split_set_vec(const SplitSet &d) {
+  return d.Q % 4 == 0 && d.ldc % 4 == 0 && numrs_hip::aligned16(d.C) &&
+         numrs_hip::aligned16(d.partial) && (d.bias == nullptr || numrs_hip::aligned16(d.bias)) &&
+         (d.res == nullptr || (numrs_hip::aligned16(d.res) && d.ldr % 4 == 0)) &&
+         (d.pre == nullptr || numrs_hip::aligned16(d.pre));
+}
+
+// The fused form (see Fused) of a batch-1 streamed launch of a and b with
+// the column sums cs and the set extra: fills f (marking the split products'
+// tiles with their arrival counters) and the tail's workgroup count.  Leaves
+// f.n_units = 0 -- the launch is then followed by splitk_reduce -- when there
+// is nothing to reduce, or when a split set is not float4-addressable or its
+// partials exceed the 32-bit device-scope offsets.
+int fuse_plan(numrs_hip_ctx *ctx, int nt, Gemm &a, Gemm &b, const ColSum *cs,
+              const SplitSet *extra, Fused &f, int64_t &tail) {
+  f = Fused{};
+  tail = 0;
+  const bool sa = a.splits > 1, sb = b.splits > 1;
+  if (!sa && !sb && cs == nullptr && extra == nullptr) return NUMRS_HIP_OK;
+  if (ctx->split_reduce_mode != NUMRS_HIP_SPLIT_REDUCE_FUSED) return NUMRS_HIP_OK;
+  const SplitSet s0 = sa ? split_set(a) : SplitSet{}, s1 = sb ? split_set(b) : SplitSet{};
+  auto fits = [](const SplitSet &d) {
+    return split_set_vec(d) && (int64_t)d.splits * d.n * 4 < (int64_t{1} << 31);
+  };
+  if ((sa && !fits(s0)) || (sb && !fits(s1)) || (extra != nullptr && !split_set_vec(*extra)))
+    return NUMRS_HIP_OK;
+  const int64_t na = stream_grid(a), nb = stream_grid(b);
+  const int64_t ta = sa ? (int64_t)a.tiles_p * a.tiles_q : 0;
+  const int64_t tb = sb ? (int64_t)b.tiles_p * b.tiles_q : 0;
+  unsigned *cnt = nullptr;
+  if (ta + tb > 0)
+    if (int rc = numrs_hip::arrival_counters(ctx, (size_t)(8 * (ta + tb)), &cnt)) return rc;
+  f.n_units = (int)(na + nb);
+  if (sa != sb && na % 8 == 0 && nb % 8 == 0) {
+    f.first_n = (int)(sa ? na : nb);
+    f.first_base = sa ? 0 : (int)na;
+    f.rest_base = sa ? (int)na : 0;
+  }
+  f.set[0] = s0;
+  f.set[1] = s1;
+  f.tiles_p[0] = a.tiles_p, f.tiles_q[0] = a.tiles_q;
+  f.tiles_p[1] = b.tiles_p, f.tiles_q[1] = b.tiles_q;
+  f.count[0] = sa ? cnt : nullptr;
+  f.count[1] = sb ? cnt + 8 * ta : nullptr;
+  f.sub[0] = (int)(8 * ta);
+  f.sub[1] = (int)(8 * tb);
+  a.arrive = f.count[0];
+  b.arrive = f.count[1];
+  const int64_t h = f.n_units + f.sub[0] + f.sub[1];
+  if (cs != nullptr) {
+    f.pad = (int)((8 - h % 8) % 8);
+    f.cs = *cs;
+    f.cs_wgs = (int)colsum_groups(cs->cols);
+  }
+  if (extra != nullptr) {
+    f.extra = *extra;
+    f.extra_wgs = (int)((extra->n / 4 + nt - 1) / nt);
+  }
+  tail = f.sub[0] + f.sub[1] + f.pad + f.cs_wgs + f.extra_wgs;
+  if (f.first_n > 0) tail = (tail + 7) & ~int64_t{7};  // the unsplit units keep their XCDs
+  f.n_tail = (int)tail;
+  return NUMRS_HIP_OK;
+}
+
+// Streamed pair kernels by operand layout: dA = dC B^T with dB = A^T dC,
+// dx = g W with dW = g^T x, and two transposed-left products.
+enum PairKind { kPairMatmulBwd = 0, kPairLinearBwd = 1, kPairTN = 2 };
+
+// One batch-1 launch of a streamed pair (tile shape `small`) with its split
+// reductions, the column sums cs and the set extra in the same grid where
+// fuse_plan allows; otherwise followed by splitk_reduce.  Only the 128 x 64
+// tiles fuse: inside the C4 step the fused 256 x 128 launches measured
+// slower than the product plus splitk_reduce (the reducers, which can only
+// take a CU that a 148 KiB product workgroup has left, run behind the last
+// product tiles), the 128 x 64 ones faster.
+int launch_stream_pair(numrs_hip_ctx *ctx, PairKind kind, bool small, Gemm sa, Gemm sb,
+                       const ColSum *cs, const SplitSet *extra, const char *who) {
+  Fused f{};
+  int64_t tail = 0;
+  if (small)
+    if (int rc = fuse_plan(ctx, kThreads, sa, sb, cs, extra, f, tail)) return rc;
+  const int64_t na = stream_grid(sa), total = na + stream_grid(sb) + tail;
+  if (total > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);
+  const dim3 grid((unsigned)total, 1);
+  const int ta = (int)na;
+  auto go = [&](auto fuse_t) {
+    constexpr bool kF = decltype(fuse_t)::value;
+    switch (kind) {
+      case kPairMatmulBwd:
+        if (small)
+          matmul_backward_stream_small<kF><<<grid, kThreads, 0, ctx->stream>>>(sa, sb, ta, f);
+        else
+          matmul_backward_stream<kF><<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, ta, f);
+        break;
+      case kPairLinearBwd:
+        if (small)
+          linear_backward_stream_small<kF><<<grid, kThreads, 0, ctx->stream>>>(sa, sb, ta, f);
+        else
+          linear_backward_stream<kF><<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, ta, f);
+        break;
+      default:
+        if (small)
+          tn_pair_stream_small<kF><<<grid, kThreads, 0, ctx->stream>>>(sa, sb, ta, f);
+        else
+          tn_pair_stream<kF><<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, ta, f);
+        break;
+    }
+  };
+  if (f.n_units != 0)
+    go(std::true_type{});
+  else
+    go(std::false_type{});
+  if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
+  if (f.n_units != 0) return NUMRS_HIP_OK;
+  return reduce_splits(ctx, &sa, &sb, cs, extra);
+}
+
 // Tile shape for a batched product (or a pair sharing the grid): no split-K,
 // so the shape whose tiles fill the CUs with the smaller modelled time;
 // false when neither shape fits or gives at least one tile per CU.
@@ -1524,6 +1927,7 @@ Gemm make(const float *X, const float *Y, float *C, int64_t ldx, int64_t ldy, in
   g.pre = nullptr;
   g.res = nullptr;
   g.ldr = 0;
+  g.arrive = nullptr;
   g.P = (int)P;
   g.Q = (int)Q;
   g.R = (int)R;
@@ -1644,14 +2048,8 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
   if (batch == 1 && plan_streamed(ctx, ga, true, true, &gb, &pl)) {
     Gemm sa = ga, sb = gb;
     if (int rc2 = stream_prepare(ctx, pl, sa, &sb)) return rc2;
-    const int64_t na = stream_grid(sa);
-    const dim3 grid((unsigned)(na + stream_grid(sb)), 1);
-    if (pl.small)
-      matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
-    else
-      matmul_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)na);
-    if (int rc2 = numrs_hip::check_launch(ctx, "matmul_backward_stream")) return rc2;
-    return reduce_splits(ctx, &sa, &sb);
+    return launch_stream_pair(ctx, kPairMatmulBwd, pl.small, sa, sb, nullptr, nullptr,
+                              "matmul_backward_stream");
   }
   int shape = kShapeLarge;
   if (batch > 1 && pick_batched_stream(ctx, ga, true, true, &gb, batch, &shape)) {
@@ -1661,9 +2059,9 @@ int matmul_backward_impl(numrs_hip_ctx *ctx, const float *dC, const float *A, co
     if (shape == kShapeMini)
       matmul_backward_stream_mini<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
     else if (shape == kShapeSmall)
-      matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      matmul_backward_stream_small<false><<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta, Fused{});
     else
-      matmul_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      matmul_backward_stream<false><<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta, Fused{});
     return numrs_hip::check_launch(ctx, "matmul_backward_stream");
   }
   const int sa_ = plan_splits(ga, batch), sb_ = plan_splits(gb, batch);
@@ -1777,18 +2175,8 @@ int launch_pair(numrs_hip_ctx *ctx, Gemm ga, Gemm gb, bool first_nt, const char 
   if (plan_streamed(ctx, ga, true, first_nt, &gb, &pl)) {
     Gemm sa = ga, sb = gb;
     if (int rc = stream_prepare(ctx, pl, sa, &sb)) return rc;
-    const int64_t na = stream_grid(sa);
-    const dim3 grid((unsigned)(na + stream_grid(sb)), 1);
-    if (first_nt && pl.small)
-      matmul_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
-    else if (first_nt)
-      matmul_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)na);
-    else if (pl.small)
-      linear_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)na);
-    else
-      linear_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)na);
-    if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
-    return reduce_splits(ctx, &sa, &sb, cs);
+    return launch_stream_pair(ctx, first_nt ? kPairMatmulBwd : kPairLinearBwd, pl.small, sa, sb,
+                              cs, nullptr, who);
   }
   // Joint split plan, balanced by work: the pair shares one grid, and a
   // workgroup's time is its number of reduction tiles.  The weight gradient
@@ -1885,9 +2273,9 @@ int numrs_hip::gemm_nn_tn_pair(numrs_hip_ctx *ctx, BatchedMat X, BatchedMat Y1, 
     if (shape == kShapeMini)
       linear_backward_stream_mini<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
     else if (shape == kShapeSmall)
-      linear_backward_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      linear_backward_stream_small<false><<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta, Fused{});
     else
-      linear_backward_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      linear_backward_stream<false><<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta, Fused{});
     return numrs_hip::check_launch(ctx, who);
   }
   if (int rc = gemm_dispatch(ctx, ga, batch, true, false)) return rc;
@@ -1938,9 +2326,9 @@ int numrs_hip::gemm_tn_pair(numrs_hip_ctx *ctx, BatchedMat X1, BatchedMat Y1, Ba
     if (shape == kShapeMini)
       tn_pair_stream_mini<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
     else if (shape == kShapeSmall)
-      tn_pair_stream_small<<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      tn_pair_stream_small<false><<<grid, kThreads, 0, ctx->stream>>>(sa, sb, (int)ta, Fused{});
     else
-      tn_pair_stream<<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta);
+      tn_pair_stream<false><<<grid, kBigThreads, 0, ctx->stream>>>(sa, sb, (int)ta, Fused{});
     return numrs_hip::check_launch(ctx, who);
   }
   if (int rc = gemm_dispatch(ctx, ga, batch, false, false)) return rc;
@@ -1972,14 +2360,9 @@ int numrs_hip::gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, 
   StreamPlan pl;
   if (plan_streamed(ctx, ga, false, false, &gb, &pl)) {
     if (int rc = stream_prepare(ctx, pl, ga, &gb)) return rc;
-    const int64_t na = stream_grid(ga), nt = na + stream_grid(gb);
-    if (nt > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);
-    if (pl.small)
-      tn_pair_stream_small<<<dim3((unsigned)nt, 1), kThreads, 0, ctx->stream>>>(ga, gb, (int)na);
-    else
-      tn_pair_stream<<<dim3((unsigned)nt, 1), kBigThreads, 0, ctx->stream>>>(ga, gb, (int)na);
-    if (int rc = numrs_hip::check_launch(ctx, who)) return rc;
-    if (int rc = reduce_splits(ctx, &ga, &gb, cs_ok ? &cs : nullptr, extra)) return rc;
+    if (int rc = launch_stream_pair(ctx, kPairTN, pl.small, ga, gb, cs_ok ? &cs : nullptr, extra,
+                                    who))
+      return rc;
   } else {
     if (int rc = gemm_dispatch(ctx, ga, 1, false, false)) return rc;
     if (int rc = gemm_dispatch(ctx, gb, 1, false, false)) return rc;
@@ -1992,6 +2375,14 @@ int numrs_hip::gemm_tn2_colsum(numrs_hip_ctx *ctx, const float *X, int64_t ldx, 
 }
 
 extern "C" {
+
+int numrs_hip_set_split_reduction(numrs_hip_ctx *ctx, int mode) {
+  NRS_CHECK_CTX(ctx);
+  if (mode != NUMRS_HIP_SPLIT_REDUCE_FUSED && mode != NUMRS_HIP_SPLIT_REDUCE_SEPARATE)
+    return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "split reduction mode %d", mode);
+  ctx->split_reduce_mode = mode;
+  return NUMRS_HIP_OK;
+}
 
 int numrs_hip_linear_forward(numrs_hip_ctx *ctx, const float *x, const float *W, const float *b,
                              float *y, int64_t T, int64_t in, int64_t out) {

@@ -84,6 +84,28 @@ int scratch(numrs_hip_ctx *ctx, size_t bytes, float **out) {
   return NUMRS_HIP_OK;
 }
 
+int arrival_counters(numrs_hip_ctx *ctx, size_t words, unsigned **out) {
+  if (words <= ctx->arrival_words && ctx->arrivals != nullptr) {
+    *out = ctx->arrivals;
+    return NUMRS_HIP_OK;
+  }
+  if (ctx->capturing) return refuse_growth(ctx, "the arrival counters", words * sizeof(unsigned));
+  NRS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  NRS_HIP(ctx, release_region(ctx, ctx->arrivals));
+  ctx->arrivals = nullptr;
+  ctx->arrival_words = 0;
+  const size_t want = words < 4096 ? 4096 : words;
+  if (hipMalloc(&ctx->arrivals, want * sizeof(unsigned)) != hipSuccess) {
+    ctx->arrivals = nullptr;
+    (void)hipGetLastError();
+    return fail(ctx, NUMRS_HIP_E_NOMEM, "arrival counter allocation of %zu words failed", want);
+  }
+  NRS_HIP(ctx, hipMemsetAsync(ctx->arrivals, 0, want * sizeof(unsigned), ctx->stream));
+  ctx->arrival_words = want;
+  *out = ctx->arrivals;
+  return NUMRS_HIP_OK;
+}
+
 size_t block_round(size_t bytes) {
   if (bytes <= 4096) return (bytes + 255) & ~size_t(255);
   // Round up to 1/8 steps of the enclosing power of two.
@@ -275,6 +297,8 @@ int numrs_hip_destroy(numrs_hip_ctx *ctx) {
   if (ctx->workspace != nullptr) (void)hipFree(ctx->workspace);
   if (ctx->scratch != nullptr) (void)hipFree(ctx->scratch);
   ctx->workspace = ctx->scratch = nullptr;
+  if (ctx->arrivals != nullptr) (void)hipFree(ctx->arrivals);
+  ctx->arrivals = nullptr;
   numrs_hip::free_retired(ctx);
   if (ctx->wait_status != nullptr) (void)hipFree(ctx->wait_status);
   ctx->wait_status = nullptr;

@@ -167,6 +167,13 @@ class Context:
         code = {"auto": 0, "per_step": 1, "plain_launch": 2, "cooperative": 3}[mode]
         self._check(L.load().numrs_hip_set_recurrence_mode(self.handle, code))
 
+    def set_split_reduction(self, mode: str) -> None:
+        """'fused' (the default: split-K partials added inside the products'
+        own launch) or 'separate' (one more launch after the products).  Both
+        give the same bits."""
+        code = {"fused": 0, "separate": 1}[mode]
+        self._check(L.load().numrs_hip_set_split_reduction(self.handle, code))
+
     def set_persistent_wait_limit(self, rounds: int) -> None:
         """Poll rounds before a persistent kernel's wait gives up (negative:
         the default); a tiny limit forces the give-up path, for testing."""
