@@ -208,6 +208,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p, int64
 __device__ __forceinline__ nrs_f4 ld_dev4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(nrs_f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice));
 }
+__device__ __forceinline__ float ld_dev1(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScDevice));
+}
 __device__ __forceinline__ void st_dev(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -1403,7 +1403,12 @@ constexpr int kTinyColsumRows = 8192;
 constexpr int64_t kTinyMacs = int64_t{1} << 24;
 constexpr int kTinyMaxR = 4096;  // at most four load batches per wave
 
-template <bool XRC, bool YRC, int U>
+// FUSE (batch 1, d.arrive set for a split product): a split stores its
+// partial at device scope and arrives at its output block's counter; the
+// last of the block's splits adds the block's partials in split order with
+// splitk_reduce's arithmetic (add_splits, finish_split) and sets the counter
+// back to zero -- no reduce launch, and no workgroup waits for another.
+template <bool XRC, bool YRC, int U, bool FUSE = false>
 __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
   // Split-K: consecutive logical blocks are the k-ranges of one output block.
   const int split = tile % d.splits;
@@ -1469,7 +1474,11 @@ __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
     for (int ww = 1; ww < kTinyWaves; ++ww) s += part[ww][t];
     const int pp = tp * 16 + (t >> 4), qq = tq * 16 + (t & 15);
     if (pp < d.P && qq < d.Q && d.splits > 1) {
-      d.partial[((int64_t)split * d.P + pp) * d.Q + qq] = s;  // splitk_reduce finishes
+      float *dst = d.partial + ((int64_t)split * d.P + pp) * d.Q + qq;
+      if constexpr (FUSE)
+        numrs_hip::st_dev(dst, s);  // read by the block's last split
+      else
+        *dst = s;  // splitk_reduce finishes
     } else if (pp < d.P && qq < d.Q) {
       float *dst = C + (int64_t)pp * d.ldc + qq;
       float v = d.alpha * s;
@@ -1481,6 +1490,39 @@ __device__ __forceinline__ void tiny_tile(const Gemm &d, int tile, int batch) {
         v = act_value(d.act, v);
       }
       *dst = v;
+    }
+  }
+  if constexpr (FUSE) {
+    if (d.splits > 1) {
+      __shared__ int s_last;
+      __builtin_amdgcn_s_waitcnt(0);  // this lane's partial stores acknowledged
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        unsigned *ctr = d.arrive + tile;
+        const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                          (unsigned)(d.splits - 1);
+        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last ? 1 : 0;
+      }
+      __syncthreads();
+      if (s_last != 0 && threadIdx.x < 256) {
+        const int t = threadIdx.x;
+        const int pp = tp * 16 + (t >> 4), qq = tq * 16 + (t & 15);
+        if (pp < d.P && qq < d.Q) {
+          const int64_t n = (int64_t)d.P * d.Q, e = (int64_t)pp * d.Q + qq;
+          const __amdgpu_buffer_rsrc_t rs = numrs_hip::dev_rsrc(d.partial, (int64_t)d.splits * n * 4);
+          float sum = 0.0f, comp = 0.0f;
+          for (int k0 = 0; k0 < d.splits; k0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              if (k0 + u < d.splits) v[u] = numrs_hip::ld_dev1(rs, (int)(4 * ((k0 + u) * n + e)));
+            add_splits(0, sum, comp, v, d.splits - k0);
+          }
+          finish_split(C, d.ldc, d.bias, d.res, d.ldr, d.accumulate, d.alpha, d.act, d.pre,
+                       (int64_t)pp, (int64_t)qq, sum);
+        }
+      }
     }
   }
 }
@@ -1518,14 +1560,14 @@ __device__ __forceinline__ void tiny_colsum(const ColSum &c, int blk) {
 
 // Workgroups [0, tiles_a) form product a (layout XA, YA), the next tiles_b
 // product b (TN), the rest (batch 0 only) the column sums cs.
-template <bool XA, bool YA, int U>
+template <bool XA, bool YA, int U, bool FUSE = false>
 __global__ void __launch_bounds__(kTinyThreads) tiny_gemm_kernel(Gemm a, Gemm b, int tiles_a,
                                                                  int tiles_b, ColSum cs) {
   const int t = blockIdx.x;
   if (t < tiles_a)
-    tiny_tile<XA, YA, U>(a, t, blockIdx.y);
+    tiny_tile<XA, YA, U, FUSE>(a, t, blockIdx.y);
   else if (t < tiles_a + tiles_b)
-    tiny_tile<false, false, U>(b, t - tiles_a, blockIdx.y);
+    tiny_tile<false, false, U, FUSE>(b, t - tiles_a, blockIdx.y);
   else if (blockIdx.y == 0)
     tiny_colsum(cs, t - tiles_a - tiles_b);
 }
@@ -1572,6 +1614,10 @@ int launch_tiny(numrs_hip_ctx *ctx, const Gemm &a_in, bool xa, bool ya, const Ge
     sa = tiny_split(cus, ta + tb, a.R);
     if (b != nullptr) sb = tiny_split(cus, ta + tb, b->R);
   }
+  // Split products reduce inside this launch (tiny_tile's FUSE) unless the
+  // context asks for the separate launch; offsets of the partials at device
+  // scope are 32-bit.
+  bool fuse = false;
   if (sa > 1 || sb > 1) {
     const size_t na = sa > 1 ? (size_t)sa * a.P * a.Q : 0;
     const size_t nb = sb > 1 ? (size_t)sb * bb.P * bb.Q : 0;
@@ -1580,32 +1626,43 @@ int launch_tiny(numrs_hip_ctx *ctx, const Gemm &a_in, bool xa, bool ya, const Ge
     float *base = static_cast<float *>(ws);
     if (sa > 1) apply_splits(a, sa, base);
     if (sb > 1) apply_splits(bb, sb, base + na);
+    fuse = ctx->split_reduce_mode == NUMRS_HIP_SPLIT_REDUCE_FUSED && 4 * (na + nb) < (size_t{1} << 31);
+    if (fuse) {
+      unsigned *cnt = nullptr;
+      if (int rc = numrs_hip::arrival_counters(ctx, (size_t)(ta + tb), &cnt)) return rc;
+      if (sa > 1) a.arrive = cnt;
+      if (sb > 1) bb.arrive = cnt + ta;
+    }
     ta *= sa;
     tb *= sb;
   }
   const dim3 grid((unsigned)(ta + tb + tc), (unsigned)batch);
   const ColSum c = cs != nullptr ? *cs : ColSum{};
   const int most_r = std::max(a.R, b != nullptr ? b->R : 0);
-  auto go = [&](auto U) {
+  auto go = [&](auto U, auto fuse_t) {
     constexpr int kU = decltype(U)::value;
+    constexpr bool kF = decltype(fuse_t)::value;
     if (xa && ya)
-      tiny_gemm_kernel<true, true, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
-                                                                                (int)tb, c);
+      tiny_gemm_kernel<true, true, kU, kF><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                    (int)tb, c);
     else if (xa)
-      tiny_gemm_kernel<true, false, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
-                                                                                 (int)tb, c);
+      tiny_gemm_kernel<true, false, kU, kF><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                     (int)tb, c);
     else if (ya)
-      tiny_gemm_kernel<false, true, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
-                                                                                 (int)tb, c);
+      tiny_gemm_kernel<false, true, kU, kF><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                     (int)tb, c);
     else
-      tiny_gemm_kernel<false, false, kU><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
-                                                                                  (int)tb, c);
+      tiny_gemm_kernel<false, false, kU, kF><<<grid, kTinyThreads, 0, ctx->stream>>>(a, bb, (int)ta,
+                                                                                      (int)tb, c);
   };
-  if (most_r > 16 * kTinyWaves * kTinyUSmall && sa == 1 && sb == 1)
-    go(std::integral_constant<int, kTinyUBig>{});
+  if (fuse)
+    go(std::integral_constant<int, kTinyUSmall>{}, std::true_type{});
+  else if (most_r > 16 * kTinyWaves * kTinyUSmall && sa == 1 && sb == 1)
+    go(std::integral_constant<int, kTinyUBig>{}, std::false_type{});
   else
-    go(std::integral_constant<int, kTinyUSmall>{});
+    go(std::integral_constant<int, kTinyUSmall>{}, std::false_type{});
   if (int rc = numrs_hip::check_launch(ctx, "tiny_gemm_kernel")) return rc;
+  if (fuse) return NUMRS_HIP_OK;
   return reduce_splits(ctx, sa > 1 ? &a : nullptr, sb > 1 ? &bb : nullptr);
 }
 

@@ -1,8 +1,9 @@
 """Split-K partials added inside the products' own launch (the default,
-numrs_hip_set_split_reduction FUSED, for the 128 x 64 streamed tiles) against
-one more launch after them (SEPARATE): the same bits, for the Linear backward
-pairs of the C4 block, for matmul_backward shapes whose weight-side product
-splits, and for the C5 forecaster's paired LSTM weight gradients.  (Products
+numrs_hip_set_split_reduction FUSED, for the 128 x 64 streamed tiles and the
+16 x 16 tiny blocks) against one more launch after them (SEPARATE): the same
+bits, for the Linear backward pairs of the C4 block, for matmul_backward
+shapes whose weight-side product splits, for C1's first layer, and for the
+C5 forecaster's paired LSTM weight gradients.  (Products
 on the 256 x 128 tiles keep the separate launch in both modes.)  The fused
 form's arrival counters are reset by the launches themselves, so
 back-to-back calls and replays of a recorded graph must each be whole."""
@@ -81,6 +82,46 @@ def test_matmul_backward_fused_equals_separate(hip_ctx, rng, M, K, N):
         c.set_split_reduction("fused")
     assert np.array_equal(got["separate"][0], got["fused"][0]), "dA"
     assert np.array_equal(got["separate"][1], got["fused"][1]), "dB"
+
+
+# Tiny products (16 x 16 blocks) split over a long reduction: C1's first
+# layer (Linear 784 -> 128 over 64 rows, with and without the ReLU epilogue)
+# and a plain product with ragged blocks; the block's last split reduces it.
+@pytest.mark.parametrize("what", ["linear", "linear_relu", "matmul_ragged"])
+def test_tiny_split_fused_equals_separate(hip_ctx, rng, what):
+    print(f"[gpu] fused split reduction: tiny {what}", flush=True)
+    c = hip_ctx
+    lib = L.load()
+    if what == "matmul_ragged":
+        M, K, N = 37, 3000, 45
+        A = c.to_device(rng.standard_normal((M, K), dtype=np.float32))
+        B = c.to_device(rng.standard_normal((K, N), dtype=np.float32))
+        prev = rng.standard_normal((M, N), dtype=np.float32)
+
+        def run():
+            C = c.to_device(prev)
+            c.matmul(A, B, C, accumulate=True)
+            return C.numpy()
+    else:
+        T, fin, fout = 64, 784, 128
+        x = c.to_device(rng.standard_normal((T, fin), dtype=np.float32))
+        W = c.to_device(rng.standard_normal((fout, fin), dtype=np.float32))
+        b = c.to_device(rng.standard_normal((fout,), dtype=np.float32))
+        fn = lib.numrs_hip_linear_forward if what == "linear" else lib.numrs_hip_linear_relu_forward
+
+        def run():
+            y = c.empty((T, fout))
+            assert fn(c.handle, x.ptr, W.ptr, b.ptr, y.ptr, T, fin, fout) == 0
+            return y.numpy()
+    try:
+        c.set_split_reduction("separate")
+        sep = run()
+        c.set_split_reduction("fused")
+        first, second = run(), run()  # twice: the counters are back at zero
+    finally:
+        c.set_split_reduction("fused")
+    assert np.array_equal(sep, first)
+    assert np.array_equal(sep, second)
 
 
 def test_lstm_forecaster_fused_equals_separate(hip_ctx, monkeypatch):
