@@ -544,13 +544,19 @@ def bench_adam(ctx, rng, n, steps, warmup):
             "sets": k, "bytes": 28.0 * n}
 
 
+# Kernels of one C1 step: layer 1 forward (split-K reduced in the same
+# launch), layer 2 forward, the cross-entropy loss, layer 2's backward pair,
+# layer 1's weight gradient, SGD.
+C1_KERNELS = 6
+
+
 def bench_c1(ctx, steps, warmup):
     """2-layer MLP (64x784 -> 128 -> ReLU -> 10, softmax CE,
     SGD lr 0.01) -- forward, backward and SGD step through the device
     autograd engine.  n steps are launched back to back and the loss is read
     back once at the end, so the figure is the step rate a training loop that
     reads its loss occasionally sees: GPU-bound on a fast host, host-bound
-    (seven kernel launches and the Python calls per step) on a slow one.  The
+    (six kernel launches and the Python calls per step) on a slow one.  The
     graph replay below queues each step with one launch."""
     import numrs_amd as nr
     from numrs_amd import Tensor, nn, optim
@@ -598,21 +604,21 @@ def bench_c1(ctx, steps, warmup):
         out["graph_loss"] = gloss
     finally:
         g.close()
-    # The floor a chain of dependent launches sits on: seven of the smallest
-    # kernel the library has (numrs_hip_stream_probe writing four floats) on
-    # the same stream, recorded into a graph like the step above and replayed,
-    # so that the host's launch rate does not enter.
+    # The floor a chain of dependent launches sits on: as many of the smallest
+    # kernel the library has (numrs_hip_stream_probe writing four floats) as
+    # the step launches, on the same stream, recorded into a graph like the
+    # step above and replayed, so that the host's launch rate does not enter.
     from numrs_amd import _lib as L
     lib = L.load()
     tiny = ctx.empty((4,))
 
-    def seven():
-        for _ in range(7):
+    def chain():
+        for _ in range(C1_KERNELS):
             ctx._check(lib.numrs_hip_stream_probe(ctx.handle, None, None, None, tiny.ptr, None,
                                                   4, 0, 1))
         return tiny
-    seven()
-    g7 = nr.StepGraph(ctx, seven)
+    chain()
+    g7 = nr.StepGraph(ctx, chain)
     try:
         for _ in range(warmup):
             g7.replay()
@@ -621,7 +627,7 @@ def bench_c1(ctx, steps, warmup):
         for _ in range(n):
             g7.replay()
         ctx.sync()
-        out["launch_floor_us"] = (time.perf_counter() - t0) / n / 7 * 1e6
+        out["launch_floor_us"] = (time.perf_counter() - t0) / n / C1_KERNELS * 1e6
     finally:
         g7.close()
     return out
@@ -1443,7 +1449,7 @@ def main() -> int:
         ent = {"workload": "C1 MLP train step 64x784->128->10, CE, SGD 0.01 "
                            "(forward+backward+step via the device autograd engine)",
                "value": round(c1["us_per_step"], 1), "unit": "us/step",
-               "bound": "latency", "kernels_per_step": 7,
+               "bound": "latency", "kernels_per_step": C1_KERNELS,
                "launch_floor_us": round(c1["launch_floor_us"], 2),
                "final_loss": round(c1["loss"], 6)}
         if not args.no_cpu_baseline:
@@ -1457,7 +1463,7 @@ def main() -> int:
                           "final_loss": round(c1["graph_loss"], 6)})
         log(f"  C1 MLP step {c1['us_per_step']:.1f} us, graph replay "
             f"{c1['graph_us_per_step']:.1f} us, dependent-launch floor "
-            f"{c1['launch_floor_us']:.2f} us (7 tiny kernels, graph-replayed)")
+            f"{c1['launch_floor_us']:.2f} us ({C1_KERNELS} tiny kernels, graph-replayed)")
         c4 = bench_c4(ctx, max(10, args.steps), 3)
         ent = {"workload": "C4 pre-LN transformer block train step (16x256, d512, 8 "
                            "heads, FFN 2048 GELU, MSE, SGD) via the device engine",

@@ -576,6 +576,12 @@ __global__ void __launch_bounds__(kThreads, 2) matmul_backward_kernel(Gemm da, G
 constexpr int kSP = 256, kSQ = 128;  // large workgroup tile
 constexpr int kHP = 128, kHQ = 64;   // small workgroup tile
 constexpr int kMP = 64, kMQ = 64;    // mini workgroup tile (batched products, up to 3 per CU)
+// Wide workgroup tile: eight waves of 32 x 96 (three MFMA blocks each), for
+// single products with both operands reduction-contiguous whose outputs are
+// a multiple of 192 wide -- the packed q/k/v projection's [4096, 1536] is
+// exactly 256 of them, one round on 256 CUs, where its 768 small tiles need
+// a round and a half.
+constexpr int kWP = 128, kWQ = 192;
 // Streamed tile shapes, as the planners name them.
 constexpr int kShapeLarge = 0, kShapeSmall = 1, kShapeMini = 2;
 template <int TP, int TQ, int NW = 4>
@@ -610,6 +616,12 @@ __shared__ __attribute__((aligned(1024))) float g_hx1[StreamCfg<kHP, kHQ>::kStag
 __shared__ __attribute__((aligned(1024))) float g_hy1[StreamCfg<kHP, kHQ>::kStageY];
 __shared__ __attribute__((aligned(1024))) float g_hx2[StreamCfg<kHP, kHQ>::kStageX];
 __shared__ __attribute__((aligned(1024))) float g_hy2[StreamCfg<kHP, kHQ>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_wx0[StreamCfg<kWP, kWQ, 8>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_wy0[StreamCfg<kWP, kWQ, 8>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_wx1[StreamCfg<kWP, kWQ, 8>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_wy1[StreamCfg<kWP, kWQ, 8>::kStageY];
+__shared__ __attribute__((aligned(1024))) float g_wx2[StreamCfg<kWP, kWQ, 8>::kStageX];
+__shared__ __attribute__((aligned(1024))) float g_wy2[StreamCfg<kWP, kWQ, 8>::kStageY];
 __shared__ __attribute__((aligned(1024))) float g_mx0[StreamCfg<kMP, kMQ>::kStageX];
 __shared__ __attribute__((aligned(1024))) float g_my0[StreamCfg<kMP, kMQ>::kStageY];
 __shared__ __attribute__((aligned(1024))) float g_mx1[StreamCfg<kMP, kMQ>::kStageX];
@@ -752,6 +764,10 @@ __device__ __forceinline__ int stream_tile(const Gemm &d, int tile, int batch) {
   if constexpr (TP == kSP) {
     x0 = g_sx0, x1 = g_sx1, x2 = g_sx2;
     y0 = g_sy0, y1 = g_sy1, y2 = g_sy2;
+  } else if constexpr (TQ == kWQ) {
+    static_assert(XRC && YRC, "wide tiles: reduction-contiguous operands only");
+    x0 = g_wx0, x1 = g_wx1, x2 = g_wx2;
+    y0 = g_wy0, y1 = g_wy1, y2 = g_wy2;
   } else if constexpr (TP == kHP) {
     x0 = g_hx0, x1 = g_hx1, x2 = g_hx2;
     y0 = g_hy0, y1 = g_hy1, y2 = g_hy2;
@@ -1139,6 +1155,11 @@ template <bool XRC, bool YRC, bool ACT = false>
 __global__ void __launch_bounds__(kBigThreads, 1) gemm_stream_kernel(Gemm d) {
   stream_tile<XRC, YRC, kSP, kSQ, kBigWaves, ACT>(d, xcd_tile(blockIdx.x, gridDim.x),
                                                   blockIdx.y);
+}
+
+template <bool ACT = false>
+__global__ void __launch_bounds__(kBigThreads, 1) gemm_stream_wide(Gemm d) {
+  stream_tile<true, true, kWP, kWQ, 8, ACT>(d, xcd_tile(blockIdx.x, gridDim.x), blockIdx.y);
 }
 
 template <bool XRC, bool YRC, bool ACT = false>
@@ -1703,6 +1724,10 @@ Gemm as_stream(Gemm g, int shape) {
 // (2048 -> 512 forward over 4096 rows, 256 tiles, one per CU: 66.4 us
 // unsplit against 71.8 us split in two and reduced).
 constexpr double kLargeTileUs = 4.22, kLargeFixedUs = 18.0;
+// Wide tiles (kWP x kWQ, one per CU): a reduction step and the fixed cost
+// as measured for [4096, K] x [K, 1536] over K = 128..2048 on MI355X (a
+// step in 2.5-2.7 us, 9-15 us besides).
+constexpr double kWideTileUs = 2.6, kWideFixedUs = 12.0;
 constexpr double kSmallPairUs = 2.3, kSmallAloneUs = 0.9, kSmallFixedUs = 7.0;
 constexpr double kPartialBytesPerUs = 6.0e6;
 
@@ -2007,6 +2032,29 @@ int launch_one(numrs_hip_ctx *ctx, Gemm g, int64_t batch) {
   if (tiny_fits(g, batch)) return launch_tiny(ctx, g, XRC, YRC, nullptr, batch, nullptr);
   StreamPlan pl;
   if (batch == 1 && plan_streamed(ctx, g, XRC, YRC, nullptr, &pl)) {
+    if constexpr (XRC && YRC) {
+      // the wide tile where it fits and its modelled time beats the plan's
+      const int64_t cus = std::max<int64_t>(ctx->num_cus, 1);
+      if (g.P % kWP == 0 && g.Q % kWQ == 0 && vec_ok(g, true, true) && g.ldx < (int64_t{1} << 22) &&
+          g.ldy < (int64_t{1} << 22)) {
+        const int64_t tw = (int64_t)(g.P / kWP) * (g.Q / kWQ);
+        const double t = (double)((tw + cus - 1) / cus) * ((g.R / kBR) * kWideTileUs + kWideFixedUs);
+        if (t < pl.t && tw <= 0x7fffffff) {
+          Gemm sg = g;
+          sg.tiles_p = g.P / kWP;
+          sg.tiles_q = g.Q / kWQ;
+          sg.splits = 1;
+          sg.ktiles_per_split = g.R / kBR;
+          sg.partial = nullptr;
+          const dim3 grid((unsigned)tw, 1);
+          if (sg.act)
+            gemm_stream_wide<true><<<grid, kBigThreads, 0, ctx->stream>>>(sg);
+          else
+            gemm_stream_wide<false><<<grid, kBigThreads, 0, ctx->stream>>>(sg);
+          return numrs_hip::check_launch(ctx, "gemm_stream_wide");
+        }
+      }
+    }
     Gemm sg = g;
     if (int rc = stream_prepare(ctx, pl, sg, nullptr)) return rc;
     const dim3 grid((unsigned)stream_grid(sg), 1);

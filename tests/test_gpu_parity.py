@@ -975,10 +975,11 @@ def test_linear_relu_forward_backward(hip_ctx, rng, T, fin, fout):
 # y = res + (x W^T + b) with the residual in the epilogue of each GEMM path:
 # tiny (64, 784, 128) and (130, 96, 18), streamed (4096, 512, 512), streamed
 # with split-K (4096, 2048, 512: the epilogue runs in the split reduction),
-# the 128 x 128 path (1000, 300, 136).  Bit for bit the Linear forward
-# followed by an add; also with res aliasing y.
+# the wide 128 x 192 tile (4096, 512, 1536), the 128 x 128 path (1000, 300,
+# 136).  Bit for bit the Linear forward followed by an add; also with res
+# aliasing y.
 @pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (130, 96, 18), (4096, 512, 512),
-                                        (4096, 2048, 512), (1000, 300, 136)])
+                                        (4096, 2048, 512), (4096, 512, 1536), (1000, 300, 136)])
 def test_linear_residual_forward(hip_ctx, rng, T, fin, fout):
     say(f"linear+residual T={T} in={fin} out={fout}")
     lib = L.load()
@@ -1002,9 +1003,10 @@ def test_linear_residual_forward(hip_ctx, rng, T, fin, fout):
 # Linear followed by GELU as one op, the pre-activation stored by the
 # epilogue: tiny (64, 784, 128) and (33, 17, 5), streamed (4096, 512, 2048:
 # the C4 FFN's first projection), streamed with split-K (4096, 2048, 512),
-# the 128 x 128 path (1000, 300, 136).  Bit for bit the two-op composition.
+# the wide 128 x 192 tile (4096, 512, 1536), the 128 x 128 path (1000, 300,
+# 136).  Bit for bit the two-op composition.
 @pytest.mark.parametrize("T,fin,fout", [(64, 784, 128), (33, 17, 5), (4096, 512, 2048),
-                                        (4096, 2048, 512), (1000, 300, 136)])
+                                        (4096, 2048, 512), (4096, 512, 1536), (1000, 300, 136)])
 def test_linear_gelu_forward_backward(hip_ctx, rng, T, fin, fout):
     say(f"linear+gelu T={T} in={fin} out={fout}")
     lib = L.load()
