@@ -550,7 +550,7 @@ def bench_adam(ctx, rng, n, steps, warmup):
 C1_KERNELS = 6
 
 
-def bench_c1(ctx, steps, warmup):
+def bench_c1(ctx, steps, warmup, graphs=True):
     """2-layer MLP (64x784 -> 128 -> ReLU -> 10, softmax CE,
     SGD lr 0.01) -- forward, backward and SGD step through the device
     autograd engine.  n steps are launched back to back and the loss is read
@@ -589,6 +589,8 @@ def bench_c1(ctx, steps, warmup):
     loss.item()
     per = (time.perf_counter() - t0) / n
     out = {"us_per_step": per * 1e6, "loss": loss.item(), "steps": n}
+    if not graphs:
+        return out
     # The same step recorded once into a HIP graph and replayed: every kernel
     # of every step still runs, queued by one launch per step.
     g = nr.StepGraph(ctx, step)
@@ -1325,6 +1327,10 @@ def main() -> int:
                          "and plain_launch start the persistent kernels with an ordinary "
                          "launch, cooperative with a cooperative one (rocprofv3's teardown "
                          "faults after those)")
+    ap.add_argument("--eager-only", action="store_true",
+                    help="with --only c1: the eager steps only, no graph recording or replay "
+                         "(for kernel traces: rocprofv3's kernel trace ended in a host "
+                         "segmentation fault inside hipGraphLaunch on one run)")
     ap.add_argument("--only", choices=["c1", "c4", "c5"], default=None,
                     help="run only this secondary workload (for profiling); prints its entry")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -1383,7 +1389,7 @@ def main() -> int:
         return 0
 
     if args.only is not None:
-        fn = {"c1": lambda: bench_c1(ctx, args.steps, args.warmup),
+        fn = {"c1": lambda: bench_c1(ctx, args.steps, args.warmup, graphs=not args.eager_only),
               "c4": lambda: bench_c4(ctx, args.steps, args.warmup),
               "c5": lambda: bench_c5(ctx, args.steps, args.warmup)}[args.only]
         res = fn()

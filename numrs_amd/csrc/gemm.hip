@@ -1892,16 +1892,21 @@ enum PairKind { kPairMatmulBwd = 0, kPairLinearBwd = 1, kPairTN = 2 };
 
 // One batch-1 launch of a streamed pair (tile shape `small`) with its split
 // reductions, the column sums cs and the set extra in the same grid where
-// fuse_plan allows; otherwise followed by splitk_reduce.  Only the 128 x 64
-// tiles fuse: inside the C4 step the fused 256 x 128 launches measured
-// slower than the product plus splitk_reduce (the reducers, which can only
-// take a CU that a 148 KiB product workgroup has left, run behind the last
-// product tiles), the 128 x 64 ones faster.
+// fuse_plan allows; otherwise followed by splitk_reduce.  Only 128 x 64
+// grids that fill every workgroup slot fuse: inside the C4 step the fused
+// 256 x 128 launches measured slower than the product plus splitk_reduce (the
+// reducers, which can only take a CU that a 148 KiB product workgroup has
+// left, run behind the last product tiles), the 128 x 64 ones faster; and
+// where the product leaves slots free (the LSTM weight gradients: 256 units)
+// the reducers start at once, arrive before the splits, and the last split of
+// each tile then reduces all of its sub-blocks alone (C5's pairs 82 + 59 us
+// against 80 + 57 with the separate launch).
 int launch_stream_pair(numrs_hip_ctx *ctx, PairKind kind, bool small, Gemm sa, Gemm sb,
                        const ColSum *cs, const SplitSet *extra, const char *who) {
   Fused f{};
   int64_t tail = 0;
-  if (small)
+  const int64_t slots = 2 * std::max<int64_t>(ctx->num_cus, 1);  // two 128 x 64 workgroups per CU
+  if (small && stream_grid(sa) + stream_grid(sb) >= slots)
     if (int rc = fuse_plan(ctx, kThreads, sa, sb, cs, extra, f, tail)) return rc;
   const int64_t na = stream_grid(sa), total = na + stream_grid(sb) + tail;
   if (total > 0x7fffffff) return numrs_hip::fail(ctx, NUMRS_HIP_E_INVALID, "%s: too large", who);

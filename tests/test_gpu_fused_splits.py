@@ -125,8 +125,9 @@ def test_tiny_split_fused_equals_separate(hip_ctx, rng, what):
 
 
 def test_lstm_forecaster_fused_equals_separate(hip_ctx, monkeypatch):
-    """C5: each layer's dW_ih and dW_hh as one TN pair launch whose bias
-    gradient (row partials, compensated) rides in the same launch."""
+    """C5 end to end: the head Linear's split product (tiny blocks) reduces
+    in its own launch; the layers' paired weight gradients (a 128 x 64 grid
+    that leaves slots free) keep the separate reduce in both modes."""
     print("[gpu] fused split reduction: C5 forecaster", flush=True)
     nr.set_default_context(hip_ctx)
     monkeypatch.setattr(nn.LSTMForecaster, "fuse_stack", True)
