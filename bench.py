@@ -1214,7 +1214,8 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     k = n_sets(4.0 * (T_ * In + Out * In + 2 * T_ * Out))
     xw_, W_, bb_ = Rot(ctx, k, xw), Rot(ctx, k, W), Rot(ctx, k, bb)
     yw_ = Rot(ctx, k, shape=(T_, Out))
-    record("a26", "Linear::forward (fused)", "gemm (bias epilogue)", "[4096,512]x[512,2048]",
+    record("a26", "Linear::forward (fused)", "gemm_stream_kernel (bias epilogue)",
+           "[4096,512]x[512,2048]",
            flops=2.0 * T_ * In * Out,
            launch=lambda i: ctx._check(L.load().numrs_hip_linear_forward(
                ctx.handle, xw_[i].ptr, W_[i].ptr, bb_[i].ptr, yw_[i].ptr, T_, In, Out)),
@@ -1225,7 +1226,8 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
     gw = f32((T_, Out))
     gw_, dxw_ = Rot(ctx, k, gw), Rot(ctx, k, shape=(T_, In))
     dW_, db_ = Rot(ctx, k, shape=(Out, In)), Rot(ctx, k, shape=(Out,))
-    record("a10+a11+a5", "Linear backward (fused)", "gemm_pair + colreduce",
+    record("a10+a11+a5", "Linear backward (fused)",
+           "linear_backward_stream_small (split reduction and bias sums in the launch)",
            "[4096,512]x[512,2048]", flops=4.0 * T_ * In * Out,
            launch=lambda i: ctx._check(L.load().numrs_hip_linear_backward(
                ctx.handle, gw_[i].ptr, xw_[i].ptr, W_[i].ptr, dxw_[i].ptr, dW_[i].ptr, db_[i].ptr,
