@@ -36,8 +36,8 @@ constexpr int kHeadDim = 64;       // dh handled by the fused row-block kernel
 // 32-row block at 16 columns: a row's max or sum is a sum over the lane's
 // registers, one xor-32 shuffle and the four waves in a fixed order through
 // LDS, and its four consecutive columns per register quad leave as one
-// 16-byte store.  The softmax follows the row kernel's arithmetic: m = max,
-// e = expf(s - m), P = e * (1/sum e).
+// 16-byte store.  The softmax is the row kernel's in base 2: s = alpha
+// log2(e) y, m = max, e = 2^(s - m) (one v_exp_f32), P = e * (1/sum e).
 //
 // With EXTRA the kernel also multiplies the finished rows by E_z, the head's
 // [S, 64] block of a third matrix, into eo (row stride ldo):
@@ -202,6 +202,10 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
 
   float t[2];
   if constexpr (MODE == 0) {
+    // Softmax in base 2: the scores scaled by alpha log2(e), then 2^(s - m)
+    // is one v_exp_f32 (within a few ulp of expf(alpha (y - max y)), which
+    // took a dozen instructions per score and half of this phase).
+    const float alpha_l2e = alpha * 1.44269504088896341f;
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
       float m = -INFINITY;
@@ -209,7 +213,7 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
       for (int bj = 0; bj < BJ; ++bj)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          acc[bi][bj][i] = alpha * acc[bi][bj][i];
+          acc[bi][bj][i] = alpha_l2e * acc[bi][bj][i];
           m = fmaxf(m, acc[bi][bj][i]);
         }
       t[bi] = m;
@@ -223,7 +227,7 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
       for (int bj = 0; bj < BJ; ++bj)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float e = expf(acc[bi][bj][i] - t[bi]);
+          const float e = __builtin_amdgcn_exp2f(acc[bi][bj][i] - t[bi]);
           acc[bi][bj][i] = e;
           s += e;
         }
@@ -491,7 +495,10 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
   };
   float t[2];
   if constexpr (MODE == 0) {
-    // P = softmax_rows(alpha * Y): m = max, e = expf(s - m), P = e * (1/sum e)
+    // Softmax in base 2: the scores scaled by alpha log2(e), then 2^(s - m)
+    // is one v_exp_f32 (within a few ulp of expf(alpha (y - max y)), which
+    // took a dozen instructions per score and half of this phase).
+    const float alpha_l2e = alpha * 1.44269504088896341f;
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
       float m = -INFINITY;
@@ -499,7 +506,7 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
       for (int bj = 0; bj < BJ; ++bj)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          acc[bi][bj][i] = alpha * acc[bi][bj][i];
+          acc[bi][bj][i] = alpha_l2e * acc[bi][bj][i];
           m = fmaxf(m, acc[bi][bj][i]);
         }
       t[bi] = m;
@@ -513,7 +520,7 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
       for (int bj = 0; bj < BJ; ++bj)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float e = expf(acc[bi][bj][i] - t[bi]);
+          const float e = __builtin_amdgcn_exp2f(acc[bi][bj][i] - t[bi]);
           acc[bi][bj][i] = e;
           s += e;
         }
