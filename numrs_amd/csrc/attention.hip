@@ -342,10 +342,11 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
 // Row-block kernel for S <= 256 (BJ = S/128 key blocks of 32 per wave) with
 // EXTRA, the arithmetic of attn_rows_kernel<MODE, BJ, true> in an order that
 // lets the loads overlap the MFMAs:
-//   1. The wave's S/4 rows of W and its 16 of the block's 64 rows of X go to
-//      LDS by DMA; then (MODE 1) the P block and the wave's rows of E are
-//      loaded into registers.  Only the DMA is waited for (vmcnt counts in
-//      issue order), so P and E arrive during the first product.
+//   1. The wave's 16 of the block's 64 rows of X and its S/4 rows of W go to
+//      LDS by DMA, then (MODE 1) the P block is loaded into registers.  Only
+//      the X rows and the first 32 W rows are waited for (vmcnt counts in
+//      issue order); the wave's rows of E are loaded into registers after
+//      that, so the next W rows, P and E arrive during the product.
 //   2. Y = X W^T from LDS: rows at 256 bytes, the 16-byte chunk j of row r
 //      stored at slot j ^ (r % 16), so the lanes reading one chunk of 16
 //      consecutive rows touch 16 different slots.
@@ -393,17 +394,11 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
 
   // 1. DMA: instruction it fills rows 4 it .. 4 it + 3 (1 KiB), lane l the
   // 16-byte slot l % 16 of row 4 it + l / 16 with chunk slot ^ (row % 16).
+  // The X rows go first, then the wave's W rows in key order: the first 32
+  // keys' products start while the next 32 keys' rows are still arriving.
   {
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t base = (uint32_t)(uintptr_t)lds;
-    const float *Ww = W + ((int64_t)b * S + (int64_t)wave_u * 32 * BJ) * ldw + (int64_t)head * kHeadDim;
-#pragma unroll
-    for (int it = 0; it < 8 * BJ; ++it) {
-      const int kk = 4 * it + (lane >> 4);
-      const int chunk = (lane & 15) ^ (kk & 15);
-      numrs_hip::lds_dma16(Ww, (uint32_t)(4 * ((int64_t)kk * ldw + 4 * chunk)),
-                           base + 4u * (uint32_t)(wave_u * kSlot) + 1024u * it);
-    }
     const float *Xw = X + ((int64_t)b * S + row0 + 16 * wave_u) * ldx + (int64_t)head * kHeadDim;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -412,9 +407,17 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
       numrs_hip::lds_dma16(Xw, (uint32_t)(4 * ((int64_t)kk * ldx + 4 * chunk)),
                            base + 4u * (uint32_t)(kXRows + wave_u * 16 * kHeadDim) + 1024u * it);
     }
+    const float *Ww = W + ((int64_t)b * S + (int64_t)wave_u * 32 * BJ) * ldw + (int64_t)head * kHeadDim;
+#pragma unroll
+    for (int it = 0; it < 8 * BJ; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int chunk = (lane & 15) ^ (kk & 15);
+      numrs_hip::lds_dma16(Ww, (uint32_t)(4 * ((int64_t)kk * ldw + 4 * chunk)),
+                           base + 4u * (uint32_t)(wave_u * kSlot) + 1024u * it);
+    }
   }
 
-  // (MODE 1) the P block, and the wave's E rows, into registers behind the DMA
+  // (MODE 1) the P block into registers behind the DMA
   auto col_of = [&](int bj, int i4) { return col0 + 32 * bj + 8 * i4 + 4 * hh; };
   auto row_ptr = [&](float *base, int bi) { return base + zoff + (int64_t)(row0 + 32 * bi + c) * S; };
   constexpr int kP = MODE == 1 ? 2 * BJ * 4 : 0;  // register loads of P
@@ -430,6 +433,16 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
           p[bi][bj][i4] = *reinterpret_cast<const f4 *>(src + col_of(bj, i4));
     }
   }
+  // The kP register loads above are the newest vector-memory operations and
+  // the W rows of key block bj > 0 the DMA issued last: at most 8 (BJ - 1) +
+  // kP outstanding means the X rows and key block 0 have landed
+  // (vector-memory operations complete in issue order).
+  __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(8 * (BJ - 1) + kP));
+  __syncthreads();  // every wave's X rows are in
+
+  // The wave's E rows into registers, issued only now so that they do not
+  // compete with the X and W rows every workgroup waits for; they arrive
+  // during the product.
   constexpr int kStage = 8 * BJ;
   f4 stage[kStage];
   {
@@ -439,12 +452,9 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
       stage[it] = *reinterpret_cast<const f4 *>(Ez + (int64_t)(col0 + 4 * it + (lane >> 4)) * lde +
                                                 4 * (lane & 15));
   }
-  // the kP + kStage register loads above are the newest vector-memory
-  // operations: at most that many outstanding means the DMA has landed
-  __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(kP + kStage));
-  __syncthreads();  // every wave's X rows are in
 
-  // 2. Y^T blocks (bi, bj): rows of X as B, the wave's rows of W as A
+  // 2. Y^T blocks (bi, bj): rows of X as B, the wave's rows of W as A, key
+  // block by key block (each accumulator's products in the same order)
   f16v acc[2][BJ];
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi)
@@ -452,26 +462,26 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
     for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = f16v{};
   const float *xs = lds + kXRows;
 #pragma unroll
-  for (int g = 0; g < kHeadDim / 8; ++g) {
-    const int ch = 2 * g + hh;
-    f4 a[2], w[BJ];
+  for (int bj = 0; bj < BJ; ++bj) {
+    if (bj == 1)  // key block 1's rows (this wave's own DMA; P and E are newer) have landed
+      __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(kP + kStage));
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
-      const int r = 32 * bi + c;
-      a[bi] = *reinterpret_cast<const f4 *>(xs + r * kHeadDim + 4 * (ch ^ (r & 15)));
+    for (int g = 0; g < kHeadDim / 8; ++g) {
+      const int ch = 2 * g + hh;
+      f4 a[2];
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi) {
+        const int r = 32 * bi + c;
+        a[bi] = *reinterpret_cast<const f4 *>(xs + r * kHeadDim + 4 * (ch ^ (r & 15)));
+      }
+      const int rw = 32 * bj + c;
+      const f4 w = *reinterpret_cast<const f4 *>(wbuf + rw * kHeadDim + 4 * (ch ^ (rw & 15)));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi)
+          acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[j], a[bi][j], acc[bi][bj], 0, 0, 0);
     }
-#pragma unroll
-    for (int bj = 0; bj < BJ; ++bj) {
-      const int r = 32 * bj + c;
-      w[bj] = *reinterpret_cast<const f4 *>(wbuf + r * kHeadDim + 4 * (ch ^ (r & 15)));
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-        for (int bj = 0; bj < BJ; ++bj)
-          acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[bj][j], a[bi][j], acc[bi][bj], 0, 0, 0);
   }
 
   // 3. Row totals over the wave's columns (in-lane, then the other half-wave),
