@@ -339,20 +339,21 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(const float *__restrict_
   }
 }
 
-// Row-block kernel for S <= 256 (BJ = S/128 key blocks of 32 per wave) with
-// EXTRA, the arithmetic of attn_rows_kernel<MODE, BJ, true> in an order that
-// lets the loads overlap the MFMAs:
+// Row-block kernel for the backward's dS and dQ at S <= 256 (BJ = S/128 key
+// blocks of 32 per wave): the arithmetic of attn_rows_kernel<1, BJ, true> in
+// an order that lets the loads overlap the MFMAs (the forward at these
+// lengths is attn_fwd_wave_rows_kernel):
 //   1. The wave's 16 of the block's 64 rows of X and its S/4 rows of W go to
-//      LDS by DMA, then (MODE 1) the P block is loaded into registers.  Only
+//      LDS by DMA, then the P block is loaded into registers.  Only
 //      the X rows and the first 32 W rows are waited for (vmcnt counts in
 //      issue order); the wave's rows of E are loaded into registers after
 //      that, so the next W rows, P and E arrive during the product.
 //   2. Y = X W^T from LDS: rows at 256 bytes, the 16-byte chunk j of row r
 //      stored at slot j ^ (r % 16), so the lanes reading one chunk of 16
 //      consecutive rows touch 16 different slots.
-//   3. The softmax (MODE 0) or its backward (MODE 1) as in attn_rows_kernel,
-//      the row totals through `red`, which reuses the X rows' space once every
-//      wave is past the product; the rows (P or dS) are stored.
+//   3. The softmax backward as in attn_rows_kernel, the row totals through
+//      `red`, which reuses the X rows' space once every wave is past the
+//      product; the dS rows are stored.
 //   4. E goes from registers into the wave's own W rows (the layout of
 //      attn_rows_kernel's staged E) and eo = E^T-product follows as there,
 //      with the wave partials summed in wave order.
@@ -371,6 +372,7 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
     float *__restrict__ out, int S, int H, int64_t ldx, int64_t ldw, float alpha,
     const float *__restrict__ E, int64_t lde, float *eo, int64_t ldo, float ealpha, int eacc) {
   static_assert(BJ == 1 || BJ == 2, "S <= 256");
+  static_assert(MODE == 1, "the softmax backward");
   constexpr int kSlot = 32 * BJ * kHeadDim;  // floats of one wave's key rows
   constexpr int kXRows = 4 * kSlot;          // offset of the X rows
   __shared__ __attribute__((aligned(1024))) float lds[lds_kernel_floats<BJ>()];
@@ -504,48 +506,7 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
     __syncthreads();
   };
   float t[2];
-  if constexpr (MODE == 0) {
-    // Softmax in base 2: the scores scaled by alpha log2(e), then 2^(s - m)
-    // is one v_exp_f32 (within a few ulp of expf(alpha (y - max y)), which
-    // took a dozen instructions per score and half of this phase).
-    const float alpha_l2e = alpha * 1.44269504088896341f;
-#pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
-      float m = -INFINITY;
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          acc[bi][bj][i] = alpha_l2e * acc[bi][bj][i];
-          m = fmaxf(m, acc[bi][bj][i]);
-        }
-      t[bi] = m;
-    }
-    row_reduce(t, 0);
-    float sum[2];
-#pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
-      float s = 0.0f;
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = __builtin_amdgcn_exp2f(acc[bi][bj][i] - t[bi]);
-          acc[bi][bj][i] = e;
-          s += e;
-        }
-      sum[bi] = s;
-    }
-    row_reduce(sum, 1);
-#pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
-      const float inv = 1.0f / sum[bi];
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[bi][bj][i] = acc[bi][bj][i] * inv;
-    }
-  } else {
+  {
     // dS = P * (Y - rowsum(Y * P))
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
@@ -636,6 +597,198 @@ __global__ void __launch_bounds__(256, 2) attn_rows_lds_kernel(
     }
     *reinterpret_cast<f4 *>(dst + 4 * j) = v;
   }
+}
+
+// Forward for dh = 64 and S = 128 or 256 (NKB = S/16 key blocks of 16): a
+// workgroup of eight waves owns 128 query rows of one head and wave w the 16
+// rows row0 + 16 w .. + 15 against every key, so a row's max and sum stay in
+// the wave (no LDS round, no barrier between the product and the softmax) and
+// O = P V needs no sum of wave partials.  The products are 16x16x4 fp32 MFMAs
+// (lane l = 16 g + j: A row j at reduction slot g, B slot g at column j, D
+// column j at rows 4 g + r):
+//   S^T block kb = K_kb Q_w^T: for step t = 4 q + e (q, e = 0..3) A holds
+//     K[16 kb + j][d] and B Q[16 w + j][d] with d = 16 q + 4 g + e, so step
+//     t reduces over dh {16 q + e, 16 q + 4 + e, 16 q + 8 + e, 16 q + 12 + e}
+//     and the four lanes of a Q row read 64 contiguous bytes per load; lane
+//     (j, g) ends with S[query j][key 16 kb + 4 g + r], r = 0..3.
+//   O^T block db = V^T P^T: for each key block kb and r, B is the lane's own
+//     register r of block kb (keys 16 kb + 4 g + r over the slots g) and A
+//     holds V[16 kb + 4 g + r][4 j + db], so row i of block db is output
+//     column 4 i + db and lane (j, g) ends with O[query j][16 g + 4 r + db].
+// The lane's Q values load straight into registers; K and V go to LDS by
+// DMA, K's 16-byte chunk c of row r at slot c ^ (r % 16) so that the 16
+// lanes reading one chunk of 16 rows hit 16 slots (V unpermuted: 16 lanes
+// read one row).  Loads, in issue order: Q, the first half of the keys' K
+// rows (waited for, with Q), the second half, V.  QK^T over the first half
+// of the keys runs while the rest arrives; one barrier in the middle of the
+// product makes the second half and V visible, after which the waves run
+// apart (a wave's softmax beside the other wave's MFMAs on its SIMD).  The
+// softmax is in base 2: m = max y, e = 2^(alpha log2(e) y - alpha log2(e) m)
+// (one fma and one v_exp_f32), P = e * (1/sum e).  128 KiB of LDS at S = 256:
+// one workgroup per CU, two waves per SIMD.
+template <int NKB>
+__global__ void __launch_bounds__(512) attn_fwd_wave_rows_kernel(
+    const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
+    int64_t ld, float *__restrict__ P, float *__restrict__ O, int64_t ldo, int S, int H,
+    float alpha) {
+  static_assert(NKB == 8 || NKB == 16, "S = 128 or 256");
+  constexpr int kKeys = 16 * NKB;
+  constexpr int kHalf = kKeys / 16;  // K rows per wave in each half of the keys
+  constexpr int kVPer = kKeys / 32;  // V DMA instructions per wave (4 rows each)
+  __shared__ __attribute__((aligned(1024))) float lds[2 * kKeys * kHeadDim];
+  const float *ks = lds;
+  const float *vs = lds + kKeys * kHeadDim;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  int rb = blockIdx.x, z = blockIdx.y;
+  {
+    // XCD k (hardware ids k, k+8, ...) owns a contiguous run of heads
+    const int nb = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((nb & 7) == 0) {
+      const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
+      rb = logical % gridDim.x;
+      z = logical / gridDim.x;
+    }
+  }
+  const int b = z / H, head = z - b * H;
+  const int row0 = rb * 128;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  const float *Kh = K + (int64_t)b * S * ld + (int64_t)head * kHeadDim;
+
+  // 1. Loads.  qf[q][e] = Q[16 w + j][16 q + 4 g + e].  DMA instruction it of
+  // a run fills 4 rows (1 KiB), lane l the 16-byte slot l % 16 of run row
+  // 4 it + l / 16.
+  f4 qf[4];
+  {
+    const float *qr = Q + ((int64_t)b * S + row0 + 16 * wave + j) * ld + (int64_t)head * kHeadDim + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) qf[q] = *reinterpret_cast<const f4 *>(qr + 16 * q);
+  }
+  auto k_half = [&](int h) {
+    const int r0 = h * (kKeys / 2) + kHalf * wave_u;  // the wave's first row of this half
+#pragma unroll
+    for (int it = 0; it < kHalf / 4; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int chunk = (lane & 15) ^ ((r0 + kk) & 15);
+      numrs_hip::lds_dma16(Kh + (int64_t)r0 * ld, (uint32_t)(4 * ((int64_t)kk * ld + 4 * chunk)),
+                           base + 4u * (uint32_t)(r0 * kHeadDim) + 1024u * it);
+    }
+  };
+  k_half(0);
+  // Q is used here, so the compiler waits for the Q loads -- and with them
+  // (vector-memory operations complete in issue order) for the DMA of the
+  // first half of K -- before the second half and V are issued.
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
+  k_half(1);
+  {
+    const int r0 = kVPer * 4 * wave_u;
+    const float *Vw = V + ((int64_t)b * S + r0) * ld + (int64_t)head * kHeadDim;
+#pragma unroll
+    for (int it = 0; it < kVPer; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      numrs_hip::lds_dma16(Vw, (uint32_t)(4 * ((int64_t)kk * ld + 4 * (lane & 15))),
+                           base + 4u * (uint32_t)((kKeys + r0) * kHeadDim) + 1024u * it);
+    }
+  }
+  __syncthreads();  // every wave's rows of the first half of K are in
+
+  // 2. S^T = K Q^T, the first half of the key blocks, then (after every
+  // wave's second half of K and V have landed) the second; two key blocks at
+  // a time (alternating accumulators), each accumulator's steps in t order.
+  f4 acc[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) acc[kb] = f4{};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1) {
+      __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));  // no store has been issued yet
+      __syncthreads();
+    }
+    // step i = (q, key-block pair): the next step's two K reads are issued
+    // ahead of this step's eight MFMAs
+    constexpr int kPairs = NKB / 4, kSteps = 4 * kPairs;
+    auto kread = [&](int i, int d) {
+      const int q = i / kPairs, kb = h * NKB / 2 + 2 * (i % kPairs) + d;
+      return *reinterpret_cast<const f4 *>(ks + (16 * kb + j) * kHeadDim + 4 * ((4 * q + g) ^ j));
+    };
+    f4 k0 = kread(0, 0), k1 = kread(0, 1);
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) {
+      f4 n0 = k0, n1 = k1;
+      if (i + 1 < kSteps) {
+        n0 = kread(i + 1, 0);
+        n1 = kread(i + 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const int q = i / kPairs, kb = h * NKB / 2 + 2 * (i % kPairs);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[e], qf[q][e], acc[kb], 0, 0, 0);
+        acc[kb + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[e], qf[q][e], acc[kb + 1], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      k0 = n0;
+      k1 = n1;
+    }
+  }
+
+  // 3. Softmax of each query row: the row's 4 NKB values in the lane, then
+  // the four lanes j, j + 16, j + 32, j + 48.
+  {
+    const float a = alpha * 1.44269504088896341f;
+    float m = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m = fmaxf(m, acc[kb][r]);
+    m = rows4(m, [](float x, float y) { return fmaxf(x, y); });
+    const float am = a * m;  // alpha > 0: the scaled scores' max
+    float sum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[kb][r], a, -am));
+        acc[kb][r] = e;
+        sum += e;
+      }
+    sum = rows4(sum, [](float x, float y) { return x + y; });
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc[kb] = acc[kb] * inv;
+  }
+
+  // 4. P rows leave (four consecutive keys per lane and block), then O = P V
+  {
+    float *Pw = P + (int64_t)z * S * S + (int64_t)(row0 + 16 * wave + j) * S + 4 * g;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) *reinterpret_cast<f4 *>(Pw + 16 * kb) = acc[kb];
+  }
+  f4 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f4{};
+  // step i = (kb, r): the next step's V read is issued ahead of this step's
+  // four MFMAs
+  auto vread = [&](int i) {
+    return *reinterpret_cast<const f4 *>(vs + (16 * (i >> 2) + 4 * g + (i & 3)) * kHeadDim + 4 * j);
+  };
+  f4 v = vread(0);
+#pragma unroll
+  for (int i = 0; i < 4 * NKB; ++i) {
+    f4 nv = v;
+    if (i + 1 < 4 * NKB) nv = vread(i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[db], acc[i >> 2][i & 3], o[db], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    v = nv;
+  }
+  float *Ow = O + ((int64_t)b * S + row0 + 16 * wave + j) * ldo + (int64_t)head * kHeadDim + 16 * g;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *reinterpret_cast<f4 *>(Ow + 4 * r) = f4{o[0][r], o[1][r], o[2][r], o[3][r]};
 }
 
 // ---------------------------------------------------------------------------
@@ -1026,6 +1179,19 @@ int launch_lds_rows(numrs_hip_ctx *ctx, const float *X, int64_t ldx, const float
   return numrs_hip::check_launch(ctx, "attn_rows_lds_kernel");
 }
 
+// attn_fwd_wave_rows_kernel: S = 128 or 256, q, k, v at one row stride.
+int launch_wave_rows(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,
+                     int64_t ld, float *P, float *out, int64_t ldo, int64_t B, int64_t S,
+                     int64_t H, float alpha) {
+  const dim3 grid((unsigned)(S / 128), (unsigned)(B * H));
+  const int s = (int)S, h = (int)H;
+  if (S == 128)
+    attn_fwd_wave_rows_kernel<8><<<grid, 512, 0, ctx->stream>>>(q, k, v, ld, P, out, ldo, s, h, alpha);
+  else
+    attn_fwd_wave_rows_kernel<16><<<grid, 512, 0, ctx->stream>>>(q, k, v, ld, P, out, ldo, s, h, alpha);
+  return numrs_hip::check_launch(ctx, "attn_fwd_wave_rows_kernel");
+}
+
 int check(numrs_hip_ctx *ctx, int64_t B, int64_t S, int64_t H, int64_t D, int64_t ld_qkv,
           int64_t ld_out) {
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0 || D % H != 0)
@@ -1056,7 +1222,7 @@ int numrs_hip_attention_forward_strided(numrs_hip_ctx *ctx, const float *q, cons
   if (rows_fit(S, dh, li, li, q, k, P) && B * H < 65536) {
     // P = softmax_rows(alpha * Q K^T) and O = P V in one kernel
     if (extra_fit(li, lo, v, out) && lds_rows_fit(S, li, li))
-      return launch_lds_rows<0>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha, v, li, out, lo);
+      return launch_wave_rows(ctx, q, k, v, li, P, out, lo, B, S, H, alpha);
     if (extra_fit(li, lo, v, out))
       return launch_rows<0, true>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha, v, li, out, lo);
     if (int rc = launch_rows<0, false>(ctx, q, li, k, li, nullptr, P, B, S, H, alpha)) return rc;

@@ -381,6 +381,17 @@ __device__ __forceinline__ float half_pair(float v, Op op) {
   return op(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
 }
 
+// op over the lane's column of the wave's four 16-lane rows (lanes l,
+// l ^ 16, l ^ 32, l ^ 48): distance 32, then distance 16, as wave_butterfly
+// begins.
+template <class Op>
+__device__ __forceinline__ float rows4(float v, Op op) {
+  v = half_pair(v, op);
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return op(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
 // Sum over each quad of lanes: distance 1, then distance 2.
 __device__ __forceinline__ float quad_sum(float v) {
   v = v + dpp_mov<0xB1>(v);
