@@ -865,7 +865,10 @@ __global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
   const float *Vz = V + tok0 * ldq + head * kHeadDim;
   const float *dOz = dO + tok0 * ldo + head * kHeadDim;
   const float *Oz = O + tok0 * ldo + head * kHeadDim;
-  const float *Pz = P + (int64_t)z * S * S;
+  // P rows of head z, and dq rows of (b, head): 32-bit byte offsets (the
+  // launch keeps S * ldq below 2^29), row part in the scalar offset
+  const __amdgpu_buffer_rsrc_t prs = numrs_hip::dev_rsrc(P + (int64_t)z * S * S, (int64_t)S * S * 4);
+  const __amdgpu_buffer_rsrc_t qrs = numrs_hip::dev_rsrc(dq + tok0 * ldq + head * kHeadDim, (int64_t)S * ldq * 4);
   const uint32_t base = (uint32_t)(uintptr_t)lds;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
@@ -900,12 +903,13 @@ __global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
   };
   // P[q][key kw + c] for the lane's 32 queries of block qb, values
   // 4n .. 4n + 3 of them (n < 8)
+  const int p_lane = 4 * (4 * hh * S + kw + c);  // query 4h, key kw + c
   auto load_p_part = [&](int qb, float (&pr)[2][16], int n) {
 #pragma unroll
     for (int m = 4 * n; m < 4 * n + 4; ++m) {
       const int bi = m >> 4, i = m & 15;
-      const int q = qb * kRowsPerBlock + 32 * bi + 8 * (i >> 2) + 4 * hh + (i & 3);
-      pr[bi][i] = Pz[(int64_t)q * S + kw + c];
+      const int q = qb * kRowsPerBlock + 32 * bi + 8 * (i >> 2) + (i & 3);  // + 4h in p_lane
+      pr[bi][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, p_lane, 4 * q * S, 0));
     }
   };
   // The softmax backward's row totals D = dO . O for the wave's tile rows
@@ -1056,7 +1060,7 @@ __global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
     __syncthreads();
     // dQ block (query half qi, d half di) = dS K over the group's keys; step
     // g + 1's operands are read before step g's MFMAs
-    const int qi = wave >> 1, di = wave & 1;
+    const int qi = wave_u >> 1, di = wave_u & 1;  // wave-uniform (scalar offsets below)
     f16v qacc = f16v{};
     {
       const int r = 32 * qi + c;
@@ -1093,14 +1097,15 @@ __global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
       row_totals(t ^ 1, of);
     }
     {
-      float *dst = dq + tok0 * ldq + head * kHeadDim + 32 * di + c;
+      const int lane_off = 4 * (int)(4 * hh * ldq + 32 * di + c);  // query + 4h, column 32 di + c
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int q = qb * kRowsPerBlock + 32 * qi + 8 * (i >> 2) + 4 * hh + (i & 3);
+        const int q = qb * kRowsPerBlock + 32 * qi + 8 * (i >> 2) + (i & 3);
         if constexpr (ATOMIC)
-          unsafeAtomicAdd(dst + (int64_t)q * ldq, alpha * qacc[i]);
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(alpha * qacc[i], qrs, lane_off, 4 * q * (int)ldq, 0);
         else
-          dst[(int64_t)q * ldq] = alpha * qacc[i];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, alpha * qacc[i]), qrs, lane_off,
+                                                4 * q * (int)ldq, 0);
       }
     }
   }
@@ -1316,7 +1321,7 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
   const int64_t dh = D / H, li = ld_qkv, lo = ld_out;
   using numrs_hip::aligned16;
   const bool keys = dq && dk && dv && !accumulate && dh == kHeadDim && (S == 128 || S == 256) &&
-                    B * H < 65536 && D <= 4096 && li % 4 == 0 && lo % 4 == 0 && li < (int64_t{1} << 22) &&
+                    B * H < 65536 && D <= 4096 && li % 4 == 0 && lo % 4 == 0 && S * li < (int64_t{1} << 29) &&
                     lo < (int64_t{1} << 22) && aligned16(q) && aligned16(k) && aligned16(v) &&
                     aligned16(P) && aligned16(out) && aligned16(dout) && aligned16(dq) &&
                     aligned16(dk) && aligned16(dv);
