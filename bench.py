@@ -1245,15 +1245,21 @@ def bench_rows(ctx, rng, steps: int, warmup: int, cpu: bool = True) -> list:
         ctx._check(L.load().numrs_hip_attention_forward(ctx.handle, q_[i].ptr, k_[i].ptr,
                                                         v_[i].ptr, P_[i].ptr, o_[i].ptr, Bq, Sq,
                                                         Hq, Dq))
-    dq_, dk_, dv_ = (Rot(ctx, ks, shape=(Bq * Sq, Dq)) for _ in range(3))
     dh = Dq // Hq
+    # the forward at C4: P = softmax(alpha Q K^T) stored, O = P V
+    record("N3f", "attention forward (new op)", "attn_fwd_wave_rows_kernel (eight waves of whole query rows)",
+           "16x256, 8 heads of 64", flops=2 * 2.0 * Bq * Hq * Sq * Sq * dh,
+           launch=lambda i: ctx._check(L.load().numrs_hip_attention_forward(
+               ctx.handle, q_[i].ptr, k_[i].ptr, v_[i].ptr, P_[i].ptr, o_[i].ptr, Bq, Sq, Hq, Dq)),
+           note="two products per head, P stored (33.5 MB); no numrs CPU path")
+    dq_, dk_, dv_ = (Rot(ctx, ks, shape=(Bq * Sq, Dq)) for _ in range(3))
     # the engine's call: the backward given the forward's output (row totals dO . O)
-    record("N3", "attention backward (new op)", "attn_bwd_zero + attn_bwd_keys (dV, dK, dQ per key group)",
+    record("N3", "attention backward (new op)", "attn_bwd_wave_rows (dS, dQ) + attn_bwd_wave_keys (dV, dK)",
            "16x256, 8 heads of 64", flops=4 * 2.0 * Bq * Hq * Sq * Sq * dh,
            launch=lambda i: ctx._check(L.load().numrs_hip_attention_backward_out_strided(
                ctx.handle, q_[i].ptr, k_[i].ptr, v_[i].ptr, Dq, P_[i].ptr, o_[i].ptr, do_[i].ptr,
                Dq, dq_[i].ptr, dk_[i].ptr, dv_[i].ptr, Bq, Sq, Hq, Dq, 0)),
-           note="four products per key group, no dS buffer; no numrs CPU path")
+           note="four products per head, dS through a [B H, S, S] buffer; no numrs CPU path")
     del q_, k_, v_, do_, P_, o_, dq_, dk_, dv_
     # N4 two stacked LSTM layers at C5 (batch 64, seq 128, in 64, hidden 256):
     # the forward entry point (input projection of layer 1 + the persistent

@@ -9,8 +9,11 @@
 //   forward:   S = alpha * Q K^T,  P = softmax_rows(S),  O = P V
 //   backward:  dV = P^T dO,  dP = dO V^T,  dS = P * (dP - rowsum(dP*P)),
 //              dQ = alpha * dS K,  dK = alpha * dS^T Q
-// with alpha = 1/sqrt(dh).  All products are fp32 MFMA GEMMs; the row
-// softmax and its backward are the one-wave-per-row kernels.
+// with alpha = 1/sqrt(dh), all products fp32 MFMAs.  For dh = 64 and S = 128
+// or 256 the forward is one kernel and the backward given the forward's output
+// two (waves owning whole query rows, then whole key rows); dh = 64 with S =
+// 384 or 512 takes the four-wave row-block kernels; other shapes the batched
+// GEMMs and the one-wave-per-row softmax kernels.
 #include <cmath>
 
 #include "common.h"
@@ -791,65 +794,196 @@ __global__ void __launch_bounds__(512) attn_fwd_wave_rows_kernel(
     *reinterpret_cast<f4 *>(Ow + 4 * r) = f4{o[0][r], o[1][r], o[2][r], o[3][r]};
 }
 
-// ---------------------------------------------------------------------------
-// Key-block backward (dh = 64, S = 128 or 256): one workgroup per (head, 128
-// keys) forms dV and dK for its keys over all S queries, and its share of dQ,
-// without storing dS.  The softmax backward's row total needs every key of a
-// row, so it comes from the forward output instead:
-//   rowsum(dP * P) = sum_k P[q,k] (dO[q] . V[k]) = dO[q] . O[q]   (O = P V),
-// 64 products per query, formed in the kernel from the staged dO rows.
-//
-// Wave w owns keys 32w..32w+31 of the group and keeps their V fragments in
-// registers.  For each block of 64 queries (Q and dO rows staged in LDS by
-// DMA, double-buffered; the next block's O rows and P values loaded into
-// registers during this block, the P loads spread over the dV, dK products):
-//   D = dO . O        per query, into LDS, before the block starts,
-//   dP - D            MFMAs from accumulators set to -D, laid out as [query,
-//                     key]: lane (c, h) holds key c and queries 8(i/4) + 4h +
-//                     (i%4) of each 32-query block,
-//   dS = P * (dP - D) in registers,
-//   dV += P^T dO, dK += dS^T Q   with those registers as the B operand (the
-//                     reduction runs over the queries they hold),
-//   dS -> LDS ([query][key], 16-byte chunk j of row q at slot j ^ (q % 32)),
-//   dQ[block] = dS K  wave w forms the 32 x 32 block (query half w/2, d half
-//                     w%2) over the group's 128 keys, K staged in LDS at the
-//                     start ([key][64], chunks of rows with bit 2 set XOR 8).
-// The operands of each product's next step are read from LDS before the
-// current step's MFMAs.  dQ adds alpha * dS K over the S/128 key groups.  At
-// S = 256 the two groups' contributions go to rows zeroed by
-// attn_bwd_zero_kernel through hardware float atomics: 0 + a + b is the same
-// sum in either order, so the result does not depend on which group lands
-// first.  At S = 128 the one group stores.
-// Shared memory: K 32 KiB, two Q/dO tile pairs 64 KiB, dS 32 KiB: one
-// workgroup per CU, four waves.
-constexpr int kKeyGroup = 128;
-constexpr int kKsOff = 0;                              // [128][64] K rows
-constexpr int kTileOff = kKeyGroup * kHeadDim;         // two buffers of Q [64][64], dO [64][64]
-constexpr int kTileFloats = 2 * kRowsPerBlock * kHeadDim;
-constexpr int kDsOff = kTileOff + 2 * kTileFloats;     // [64][128] dS
-constexpr int kDOff = kDsOff + kRowsPerBlock * kKeyGroup;  // the block's 64 row totals
-constexpr int kKeysLds = kDOff + kRowsPerBlock;
-
-// dq's rows set to 0 before two key groups add into them: workgroup w
-// clears rows 16 w .. 16 w + 15 (B S is a multiple of 16), a float4 per
-// thread and row (blockDim = D / 4).
-__global__ void __launch_bounds__(1024) attn_bwd_zero_kernel(float *__restrict__ dq, int64_t ldq) {
-  float *row = dq + (int64_t)blockIdx.x * 16 * ldq + 4 * threadIdx.x;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) *reinterpret_cast<f4 *>(row + r * ldq) = f4{0.0f, 0.0f, 0.0f, 0.0f};
-}
-
-template <bool ATOMIC>
-__global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
-    const float *Q, const float *K, const float *V, int64_t ldq, const float *P, const float *dO,
-    int64_t ldo, const float *O, float *dq, float *dk, float *dv, int S, int H, float alpha) {
-  // (no __restrict__: the loads must not move across the memory fences below)
-  __shared__ __attribute__((aligned(1024))) float lds[kKeysLds];
+// Backward for dh = 64 and S = 128 or 256 given the forward's output O (the
+// softmax backward's row total rowsum(dP * P) = dO . O), in two launches
+// whose waves own whole rows of the products, as the forward's do:
+//   attn_bwd_wave_rows_kernel: eight waves of 16 query rows against every
+//     key: dP^T = V dO^T (the forward's S^T with V for K and dO for Q), D =
+//     dO . O in the wave, dS = P (dP - D) stored to a [B H, S, S] buffer in
+//     P's layout, and dQ = alpha dS K (the forward's O = P V with K for V):
+//     no sum across waves, no atomics.
+//   attn_bwd_wave_keys_kernel: eight waves of 16 keys against every query:
+//     dV = P^T dO and dK = alpha dS^T Q.
+// Both: one workgroup per CU at S = 256 (128 KiB of LDS), two waves per SIMD.
+template <int NKB>
+__global__ void __launch_bounds__(512) attn_bwd_wave_rows_kernel(
+    const float *__restrict__ K, const float *__restrict__ V, int64_t ld,
+    const float *__restrict__ P, const float *__restrict__ dO, const float *__restrict__ O,
+    int64_t ldo, float *__restrict__ dS, float *__restrict__ dq, int S, int H, float alpha) {
+  static_assert(NKB == 8 || NKB == 16, "S = 128 or 256");
+  constexpr int kKeys = 16 * NKB;
+  constexpr int kHalf = kKeys / 16;  // V rows per wave in each half of the keys
+  constexpr int kKPer = kKeys / 32;  // K DMA instructions per wave (4 rows each)
+  __shared__ __attribute__((aligned(1024))) float lds[2 * kKeys * kHeadDim];
+  const float *vs = lds;                     // V: chunk c of row r at slot c ^ (r % 16)
+  const float *ks = lds + kKeys * kHeadDim;  // K: unpermuted (16 lanes read one row)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c = lane & 31, hh = lane >> 5;
-  int kg = blockIdx.x, z = blockIdx.y;
+  const int j = lane & 15, g = lane >> 4;
+  int rb = blockIdx.x, z = blockIdx.y;
   {
     // XCD k (hardware ids k, k+8, ...) owns a contiguous run of heads
+    const int nb = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((nb & 7) == 0) {
+      const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
+      rb = logical % gridDim.x;
+      z = logical / gridDim.x;
+    }
+  }
+  const int b = z / H, head = z - b * H;
+  const int row0 = rb * 128;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  const float *Vh = V + (int64_t)b * S * ld + (int64_t)head * kHeadDim;
+  const float *Kh = K + (int64_t)b * S * ld + (int64_t)head * kHeadDim;
+  const int64_t prow = (int64_t)z * S * S + (int64_t)(row0 + 16 * wave + j) * S + 4 * g;
+
+  // 1. Loads, in issue order: the lane's dO values ([q][e] = row 16 w + j,
+  // column 16 q + 4 g + e), the first half of V (waited for, with them), the
+  // second half of V, K, and after the barrier (so that no wave's later loads
+  // queue ahead of another wave's first ones) the lane's O values (dO's
+  // layout) and P values (pf[kb] = P[query j][16 kb + 4 g ..]).
+  f4 df[4], of[4];
+  const int64_t roff = ((int64_t)b * S + row0 + 16 * wave + j) * ldo + (int64_t)head * kHeadDim + 4 * g;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) df[q] = *reinterpret_cast<const f4 *>(dO + roff + 16 * q);
+  auto v_half = [&](int h) {
+    const int r0 = h * (kKeys / 2) + kHalf * wave_u;
+#pragma unroll
+    for (int it = 0; it < kHalf / 4; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      const int chunk = (lane & 15) ^ ((r0 + kk) & 15);
+      numrs_hip::lds_dma16(Vh + (int64_t)r0 * ld, (uint32_t)(4 * ((int64_t)kk * ld + 4 * chunk)),
+                           base + 4u * (uint32_t)(r0 * kHeadDim) + 1024u * it);
+    }
+  };
+  v_half(0);
+  // dO is used here, so the compiler waits for it -- and with it
+  // (vector-memory operations complete in issue order) for the first half of
+  // V -- before the rest is issued.
+  asm volatile("" ::"v"(df[0]), "v"(df[1]), "v"(df[2]), "v"(df[3]) : "memory");
+  v_half(1);
+  {
+    const int r0 = 4 * kKPer * wave_u;
+#pragma unroll
+    for (int it = 0; it < kKPer; ++it) {
+      const int kk = 4 * it + (lane >> 4);
+      numrs_hip::lds_dma16(Kh + (int64_t)r0 * ld, (uint32_t)(4 * ((int64_t)kk * ld + 4 * (lane & 15))),
+                           base + 4u * (uint32_t)((kKeys + r0) * kHeadDim) + 1024u * it);
+    }
+  }
+  __syncthreads();  // every wave's rows of the first half of V are in
+#pragma unroll
+  for (int q = 0; q < 4; ++q) of[q] = *reinterpret_cast<const f4 *>(O + roff + 16 * q);
+  f4 pf[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) pf[kb] = *reinterpret_cast<const f4 *>(P + prow + 16 * kb);
+
+  // 2. dP^T = V dO^T, the first half of the key blocks, then (after every
+  // wave's second half of V and K have landed) the second; operand reads one
+  // step ahead of the MFMAs.
+  f4 acc[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) acc[kb] = f4{};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1) {
+      // the NKB P loads are the newest vector-memory operations: at most NKB
+      // outstanding means O, the second half of V and K have landed
+      __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(NKB));
+      __syncthreads();
+    }
+    constexpr int kPairs = NKB / 4, kSteps = 4 * kPairs;
+    auto vread = [&](int i, int d) {
+      const int q = i / kPairs, kb = h * NKB / 2 + 2 * (i % kPairs) + d;
+      return *reinterpret_cast<const f4 *>(vs + (16 * kb + j) * kHeadDim + 4 * ((4 * q + g) ^ j));
+    };
+    f4 w0 = vread(0, 0), w1 = vread(0, 1);
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) {
+      f4 n0 = w0, n1 = w1;
+      if (i + 1 < kSteps) {
+        n0 = vread(i + 1, 0);
+        n1 = vread(i + 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const int q = i / kPairs, kb = h * NKB / 2 + 2 * (i % kPairs);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(w0[e], df[q][e], acc[kb], 0, 0, 0);
+        acc[kb + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(w1[e], df[q][e], acc[kb + 1], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      w0 = n0;
+      w1 = n1;
+    }
+  }
+
+  // 3. D = dO . O of query j (the lane's 16 products, then the four lanes of
+  // the row), dS = P (dP - D), stored in P's layout
+  float D = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) D += df[q][e] * of[q][e];
+  D = rows4(D, [](float x, float y) { return x + y; });
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    acc[kb] = pf[kb] * (acc[kb] - D);
+    *reinterpret_cast<f4 *>(dS + prow + 16 * kb) = acc[kb];
+  }
+
+  // 4. dQ = alpha dS K: B is the lane's register r of dS block kb, A holds
+  // K[16 kb + 4 g + r][4 j + db]; lane (j, g) ends with dQ[query j][16 g +
+  // 4 r + db].  The K read of the next step goes ahead of this step's MFMAs.
+  f4 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f4{};
+  auto kread = [&](int i) {
+    return *reinterpret_cast<const f4 *>(ks + (16 * (i >> 2) + 4 * g + (i & 3)) * kHeadDim + 4 * j);
+  };
+  f4 kv = kread(0);
+#pragma unroll
+  for (int i = 0; i < 4 * NKB; ++i) {
+    f4 nk = kv;
+    if (i + 1 < 4 * NKB) nk = kread(i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[db], acc[i >> 2][i & 3], o[db], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    kv = nk;
+  }
+  float *qw = dq + ((int64_t)b * S + row0 + 16 * wave + j) * ld + (int64_t)head * kHeadDim + 16 * g;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *reinterpret_cast<f4 *>(qw + 4 * r) =
+        f4{alpha * o[0][r], alpha * o[1][r], alpha * o[2][r], alpha * o[3][r]};
+}
+
+// dV = P^T dO and dK = alpha dS^T Q for 128 keys of one head (NQB = S/16):
+// wave w owns keys key0 = 128 kg + 16 w .. + 15.  Step t of the S/4 steps
+// covers queries 4 t + g at reduction slot g: A holds P (dS) [4 t + g][key0
+// + j], loaded from global memory kPD steps ahead into a register ring; B
+// holds dO (Q) [4 t + g][4 j + db] from LDS (rows by DMA, unpermuted: 16
+// lanes read one row), so block db's column j is output column 4 j + db and
+// lane (j, g) ends with dV (dK) [key0 + 4 g + r][4 j + db].
+template <int NQB>
+__global__ void __launch_bounds__(512) attn_bwd_wave_keys_kernel(
+    const float *__restrict__ Q, int64_t ld, const float *__restrict__ P,
+    const float *__restrict__ dS, const float *__restrict__ dO, int64_t ldo,
+    float *__restrict__ dk, float *__restrict__ dv, int S, int H, float alpha) {
+  static_assert(NQB == 8 || NQB == 16, "S = 128 or 256");
+  constexpr int kQ = 16 * NQB;     // queries
+  constexpr int kSteps = kQ / 4;   // MFMA steps of four queries
+  constexpr int kPer = kQ / 32;    // DMA instructions per wave for Q, and for dO
+  constexpr int kPD = 16;          // steps of P and dS loaded ahead
+  __shared__ __attribute__((aligned(1024))) float lds[2 * kQ * kHeadDim];
+  const float *qs = lds;
+  const float *os = lds + kQ * kHeadDim;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  int kg = blockIdx.x, z = blockIdx.y;
+  {
     const int nb = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
     if ((nb & 7) == 0) {
       const int logical = (lin & 7) * (nb >> 3) + (lin >> 3);
@@ -858,270 +992,72 @@ __global__ void __launch_bounds__(256, 1) attn_bwd_keys_kernel(
     }
   }
   const int b = z / H, head = z - b * H;
-  const int k0 = kg * kKeyGroup, kw = k0 + 32 * wave;  // the group's and the wave's first key
-  const int64_t tok0 = (int64_t)b * S;
-  const float *Qz = Q + tok0 * ldq + head * kHeadDim;
-  const float *Kz = K + tok0 * ldq + head * kHeadDim;
-  const float *Vz = V + tok0 * ldq + head * kHeadDim;
-  const float *dOz = dO + tok0 * ldo + head * kHeadDim;
-  const float *Oz = O + tok0 * ldo + head * kHeadDim;
-  // P rows of head z, and dq rows of (b, head): 32-bit byte offsets (the
-  // launch keeps S * ldq below 2^29), row part in the scalar offset
-  const __amdgpu_buffer_rsrc_t prs = numrs_hip::dev_rsrc(P + (int64_t)z * S * S, (int64_t)S * S * 4);
-  const __amdgpu_buffer_rsrc_t qrs = numrs_hip::dev_rsrc(dq + tok0 * ldq + head * kHeadDim, (int64_t)S * ldq * 4);
-  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  const int key0 = kg * 128 + 16 * wave;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-
-  // K rows 32 wave .. +31 of the group by DMA: instruction it fills rows
-  // 4 it .. 4 it + 3, lane l the 16-byte slot l % 16 of row 4 it + l / 16,
-  // holding chunk slot ^ 8 when the row's bit 2 is set.
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
   {
-    const float *src = Kz + (int64_t)(k0 + 32 * wave_u) * ldq;
+    const int r0 = 4 * kPer * wave_u;
+    const float *qsrc = Q + ((int64_t)b * S + r0) * ld + (int64_t)head * kHeadDim;
+    const float *osrc = dO + ((int64_t)b * S + r0) * ldo + (int64_t)head * kHeadDim;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
+    for (int it = 0; it < kPer; ++it) {
       const int kk = 4 * it + (lane >> 4);
-      const int chunk = (lane & 15) ^ (8 * ((kk >> 2) & 1));
-      numrs_hip::lds_dma16(src, (uint32_t)(4 * ((int64_t)kk * ldq + 4 * chunk)),
-                           base + 4u * (uint32_t)(kKsOff + 32 * wave_u * kHeadDim) + 1024u * it);
+      numrs_hip::lds_dma16(qsrc, (uint32_t)(4 * ((int64_t)kk * ld + 4 * (lane & 15))),
+                           base + 4u * (uint32_t)(r0 * kHeadDim) + 1024u * it);
+      numrs_hip::lds_dma16(osrc, (uint32_t)(4 * ((int64_t)kk * ldo + 4 * (lane & 15))),
+                           base + 4u * (uint32_t)((kQ + r0) * kHeadDim) + 1024u * it);
     }
   }
-  // Q and dO rows 16 wave .. +15 of query block qb into tile buffer t, chunk
-  // j of tile row r at slot j ^ (r % 16).
-  auto stage_tiles = [&](int qb, int t) {
-    const int r0 = qb * kRowsPerBlock + 16 * wave_u;
-    const float *qs = Qz + (int64_t)r0 * ldq;
-    const float *os = dOz + (int64_t)r0 * ldo;
-    const uint32_t qd = base + 4u * (uint32_t)(kTileOff + t * kTileFloats + 16 * wave_u * kHeadDim);
-    const uint32_t od = qd + 4u * (uint32_t)(kRowsPerBlock * kHeadDim);
+  const int64_t col = (int64_t)z * S * S + (int64_t)g * S + key0 + j;  // query g, key key0 + j
+  float pa[kPD], sa[kPD];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int kk = 4 * it + (lane >> 4);  // (16 wave + kk) % 16 = kk
-      const int chunk = (lane & 15) ^ kk;
-      numrs_hip::lds_dma16(qs, (uint32_t)(4 * ((int64_t)kk * ldq + 4 * chunk)), qd + 1024u * it);
-      numrs_hip::lds_dma16(os, (uint32_t)(4 * ((int64_t)kk * ldo + 4 * chunk)), od + 1024u * it);
-    }
-  };
-  // P[q][key kw + c] for the lane's 32 queries of block qb, values
-  // 4n .. 4n + 3 of them (n < 8)
-  const int p_lane = 4 * (4 * hh * S + kw + c);  // query 4h, key kw + c
-  auto load_p_part = [&](int qb, float (&pr)[2][16], int n) {
-#pragma unroll
-    for (int m = 4 * n; m < 4 * n + 4; ++m) {
-      const int bi = m >> 4, i = m & 15;
-      const int q = qb * kRowsPerBlock + 32 * bi + 8 * (i >> 2) + (i & 3);  // + 4h in p_lane
-      pr[bi][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, p_lane, 4 * q * S, 0));
-    }
-  };
-  // The softmax backward's row totals D = dO . O for the wave's tile rows
-  // 16 wave + l / 4 of block qb: lane l multiplies 16 of the 64 products
-  // (d = 16 (l % 4) ..), the four lanes of a row add in xor order, and the
-  // first writes D to LDS.  The wave's dO rows are the ones it staged.
-  auto load_o = [&](int qb, f4 (&of)[4]) {
-    const float *src = Oz + (int64_t)(qb * kRowsPerBlock + 16 * wave + (lane >> 2)) * ldo + 16 * (lane & 3);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) of[e] = *reinterpret_cast<const f4 *>(src + 4 * e);
-  };
-  auto row_totals = [&](int t, const f4 (&of)[4]) {
-    const int r = 16 * wave + (lane >> 2);
-    const float *os = lds + kTileOff + t * kTileFloats + kRowsPerBlock * kHeadDim;
-    float sum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const f4 d = *reinterpret_cast<const f4 *>(os + r * kHeadDim + 4 * ((4 * (lane & 3) + e) ^ (r & 15)));
-#pragma unroll
-      for (int u = 0; u < 4; ++u) sum += d[u] * of[e][u];
-    }
-    sum = quad_sum(sum);
-    if ((lane & 3) == 0) lds[kDOff + r] = sum;
-  };
+  for (int t = 0; t < kPD; ++t) {
+    pa[t] = P[col + (int64_t)4 * t * S];
+    sa[t] = dS[col + (int64_t)4 * t * S];
+  }
+  // the 2 kPD loads above are the newest vector-memory operations
+  __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(2 * kPD));
+  __syncthreads();  // every wave's Q and dO rows are in
 
-  stage_tiles(0, 0);
-  f4 vr[8];  // V[key kw + c][8g + 4h .. +3]
+  f4 vacc[4], kacc[4];
 #pragma unroll
-  for (int g = 0; g < 8; ++g)
-    vr[g] = *reinterpret_cast<const f4 *>(Vz + (int64_t)(kw + c) * ldq + 8 * g + 4 * hh);
-  float pr[2][16];
+  for (int db = 0; db < 4; ++db) {
+    vacc[db] = f4{};
+    kacc[db] = f4{};
+  }
+  auto bread = [&](const float *m, int t) {
+    return *reinterpret_cast<const f4 *>(m + (4 * t + g) * kHeadDim + 4 * j);
+  };
+  f4 bo = bread(os, 0), bq = bread(qs, 0);
 #pragma unroll
-  for (int n = 0; n < 8; ++n) load_p_part(0, pr, n);
-  f4 of[4];
-  load_o(0, of);
-  // Loads stay where they are written: no memory access or instruction moves
-  // across this point (the explicit waits below count on what precedes them).
-  auto pin = [] {
-    asm volatile("" ::: "memory");
+  for (int t = 0; t < kSteps; ++t) {
+    const float pv = pa[t % kPD], sv = sa[t % kPD];
+    if (t + kPD < kSteps) {
+      pa[t % kPD] = P[col + (int64_t)4 * (t + kPD) * S];
+      sa[t % kPD] = dS[col + (int64_t)4 * (t + kPD) * S];
+    }
+    f4 no = bo, nq = bq;
+    if (t + 1 < kSteps) {
+      no = bread(os, t + 1);
+      nq = bread(qs, t + 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
-  };
-  pin();
-  __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));
-  row_totals(0, of);
-
-  f16v dvacc[2], dkacc[2];
 #pragma unroll
-  for (int dj = 0; dj < 2; ++dj) {
-    dvacc[dj] = f16v{};
-    dkacc[dj] = f16v{};
+    for (int db = 0; db < 4; ++db) {
+      vacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv, bo[db], vacc[db], 0, 0, 0);
+      kacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv, bq[db], kacc[db], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    bo = no;
+    bq = nq;
   }
-  const int nq = S / kRowsPerBlock;
-  for (int qb = 0; qb < nq; ++qb) {
-    const int t = qb & 1;
-    __syncthreads();  // block qb's tiles (waited for by every wave) are in
-    float prn[2][16];
-    const bool more = qb + 1 < nq;
-    if (more) {
-      stage_tiles(qb + 1, t ^ 1);
-      load_o(qb + 1, of);
-    }
-    pin();  // the prefetch goes out before this block's products (P's in the dV, dK loop)
-    const float *qs = lds + kTileOff + t * kTileFloats;
-    const float *os = qs + kRowsPerBlock * kHeadDim;
-
-    // dP - D = dO V^T - D: the accumulators start at -D of their queries;
-    // A = dO rows (query 32 bi + c), B = the wave's V fragments.  Operands
-    // of step g + 1 are read before step g's MFMAs.
-    f16v acc[2];
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f4 d = *reinterpret_cast<const f4 *>(lds + kDOff + 32 * bi + 8 * g + 4 * hh);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[bi][4 * g + e] = -d[e];
-      }
-    auto read_a = [&](int g, f4 (&a)[2]) {
-#pragma unroll
-      for (int bi = 0; bi < 2; ++bi) {
-        const int r = 32 * bi + c;
-        a[bi] = *reinterpret_cast<const f4 *>(os + r * kHeadDim + 4 * ((2 * g + hh) ^ (r & 15)));
-      }
-    };
-    f4 a[2][2];
-    read_a(0, a[0]);
-#pragma unroll
-    for (int g = 0; g < kHeadDim / 8; ++g) {
-      if (g + 1 < kHeadDim / 8) read_a(g + 1, a[(g + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi)
-          acc[bi] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[g & 1][bi][j], vr[g][j], acc[bi], 0, 0, 0);
-    }
-    // dS = P * (dP - D)
-    float ds[2][16];
-#pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) ds[bi][i] = pr[bi][i] * acc[bi][i];
-    // dV += P^T dO, dK += dS^T Q: A = dO or Q at [query][32 dj + c], group n
-    // = (bi, g) of four queries; group n + 1's operands are read before group
-    // n's MFMAs.
-    auto read_grp = [&](int n, float (&ao)[4][2], float (&aq)[4][2]) {
-      const int bi = n >> 2, g = n & 3;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 32 * bi + 8 * g + 4 * hh + j;
-#pragma unroll
-        for (int dj = 0; dj < 2; ++dj) {
-          const int col = 4 * (((32 * dj + c) >> 2) ^ (r & 15)) + (c & 3);
-          ao[j][dj] = os[r * kHeadDim + col];
-          aq[j][dj] = qs[r * kHeadDim + col];
-        }
-      }
-    };
-    float ao[2][4][2], aq[2][4][2];
-    read_grp(0, ao[0], aq[0]);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      if (n + 1 < 8) read_grp(n + 1, ao[(n + 1) & 1], aq[(n + 1) & 1]);
-      if (more) load_p_part(qb + 1, prn, n);  // the next block's P, four loads per group
-      pin();
-      const int bi = n >> 2, g = n & 3;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int dj = 0; dj < 2; ++dj) {
-          dvacc[dj] = __builtin_amdgcn_mfma_f32_32x32x2f32(ao[n & 1][j][dj], pr[bi][4 * g + j],
-                                                           dvacc[dj], 0, 0, 0);
-          dkacc[dj] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[n & 1][j][dj], ds[bi][4 * g + j],
-                                                           dkacc[dj], 0, 0, 0);
-        }
-    }
-    // dS -> LDS [query][group key]
-    {
-      const int kc = 32 * wave + c;
-#pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int q = 32 * bi + 8 * (i >> 2) + 4 * hh + (i & 3);
-          lds[kDsOff + q * kKeyGroup + 4 * ((kc >> 2) ^ (q & 31)) + (c & 3)] = ds[bi][i];
-        }
-    }
-    __syncthreads();
-    // dQ block (query half qi, d half di) = dS K over the group's keys; step
-    // g + 1's operands are read before step g's MFMAs
-    const int qi = wave_u >> 1, di = wave_u & 1;  // wave-uniform (scalar offsets below)
-    f16v qacc = f16v{};
-    {
-      const int r = 32 * qi + c;
-      auto read_q = [&](int g, f4 &ad, float (&kv)[4]) {
-        ad = *reinterpret_cast<const f4 *>(lds + kDsOff + r * kKeyGroup + 4 * ((2 * g + hh) ^ (r & 31)));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int kk = 8 * g + 4 * hh + j;  // (kk >> 2) & 1 == hh
-          kv[j] = lds[kKsOff + kk * kHeadDim + ((32 * di + c) ^ (32 * hh))];
-        }
-      };
-      f4 ad[2];
-      float kv[2][4];
-      read_q(0, ad[0], kv[0]);
-#pragma unroll
-      for (int g = 0; g < kKeyGroup / 8; ++g) {
-        if (g + 1 < kKeyGroup / 8) read_q(g + 1, ad[(g + 1) & 1], kv[(g + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          qacc = __builtin_amdgcn_mfma_f32_32x32x2f32(ad[g & 1][j], kv[g & 1][j], qacc, 0, 0, 0);
-      }
-    }
-    // the next block's tiles and P have landed (and the last block's dQ
-    // writes are done) before this block's dQ leaves
-    pin();
-    __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));
-    if (more) {
-#pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) pr[bi][i] = prn[bi][i];
-      // every wave read this block's D at its start, before the dS barrier
-      row_totals(t ^ 1, of);
-    }
-    {
-      const int lane_off = 4 * (int)(4 * hh * ldq + 32 * di + c);  // query + 4h, column 32 di + c
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int q = qb * kRowsPerBlock + 32 * qi + 8 * (i >> 2) + (i & 3);
-        if constexpr (ATOMIC)
-          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(alpha * qacc[i], qrs, lane_off, 4 * q * (int)ldq, 0);
-        else
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, alpha * qacc[i]), qrs, lane_off,
-                                                4 * q * (int)ldq, 0);
-      }
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int64_t off = ((int64_t)b * S + key0 + 4 * g + r) * ld + (int64_t)head * kHeadDim + 4 * j;
+    *reinterpret_cast<f4 *>(dv + off) = f4{vacc[0][r], vacc[1][r], vacc[2][r], vacc[3][r]};
+    *reinterpret_cast<f4 *>(dk + off) =
+        f4{alpha * kacc[0][r], alpha * kacc[1][r], alpha * kacc[2][r], alpha * kacc[3][r]};
   }
-  // dV and dK rows of the wave's keys: lane (c, h) holds key kw + c at d
-  // = 32 dj + 8 g + 4 h + (0..3)
-#pragma unroll
-  for (int dj = 0; dj < 2; ++dj)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int64_t off = (tok0 + kw + c) * ldq + head * kHeadDim + 32 * dj + 8 * g + 4 * hh;
-      const f4 v = {dvacc[dj][4 * g], dvacc[dj][4 * g + 1], dvacc[dj][4 * g + 2], dvacc[dj][4 * g + 3]};
-      const f4 w = {alpha * dkacc[dj][4 * g], alpha * dkacc[dj][4 * g + 1], alpha * dkacc[dj][4 * g + 2],
-                    alpha * dkacc[dj][4 * g + 3]};
-      *reinterpret_cast<f4 *>(dv + off) = v;
-      *reinterpret_cast<f4 *>(dk + off) = w;
-    }
 }
 
 // Whether the fused row-block kernel takes this shape: dh = 64, S a multiple
@@ -1329,20 +1265,24 @@ int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q,
     return numrs_hip_attention_backward_strided(ctx, q, k, v, li, P, dout, lo, dq, dk, dv, B, S, H,
                                                 D, accumulate);
   const float alpha = 1.0f / sqrtf((float)dh);
-  const bool atomic = S > kKeyGroup;  // two key groups add into dq
-  if (atomic) {
-    // B S < 2^24 rows (B H < 65536, S <= 256), D / 4 <= 1024 threads
-    attn_bwd_zero_kernel<<<(unsigned)(B * S / 16), (unsigned)(D / 4), 0, ctx->stream>>>(dq, li);
-    if (int rc = numrs_hip::check_launch(ctx, "attn_bwd_zero_kernel")) return rc;
-  }
-  const dim3 grid((unsigned)(S / kKeyGroup), (unsigned)(B * H));
-  if (atomic)
-    attn_bwd_keys_kernel<true><<<grid, 256, 0, ctx->stream>>>(q, k, v, li, P, dout, lo, out, dq, dk,
-                                                             dv, (int)S, (int)H, alpha);
+  // dS between the two launches, in P's layout
+  numrs_hip::TempBlock dSb(ctx);
+  if (int rc = dSb.alloc((size_t)(B * H * S * S) * sizeof(float))) return rc;
+  float *dS = dSb.f();
+  const dim3 grid((unsigned)(S / 128), (unsigned)(B * H));
+  const int s = (int)S, h = (int)H;
+  if (S == 128)
+    attn_bwd_wave_rows_kernel<8><<<grid, 512, 0, ctx->stream>>>(k, v, li, P, dout, out, lo, dS, dq, s, h,
+                                                                alpha);
   else
-    attn_bwd_keys_kernel<false><<<grid, 256, 0, ctx->stream>>>(q, k, v, li, P, dout, lo, out, dq,
-                                                              dk, dv, (int)S, (int)H, alpha);
-  return numrs_hip::check_launch(ctx, "attn_bwd_keys_kernel");
+    attn_bwd_wave_rows_kernel<16><<<grid, 512, 0, ctx->stream>>>(k, v, li, P, dout, out, lo, dS, dq, s, h,
+                                                                 alpha);
+  if (int rc = numrs_hip::check_launch(ctx, "attn_bwd_wave_rows_kernel")) return rc;
+  if (S == 128)
+    attn_bwd_wave_keys_kernel<8><<<grid, 512, 0, ctx->stream>>>(q, li, P, dS, dout, lo, dk, dv, s, h, alpha);
+  else
+    attn_bwd_wave_keys_kernel<16><<<grid, 512, 0, ctx->stream>>>(q, li, P, dS, dout, lo, dk, dv, s, h, alpha);
+  return numrs_hip::check_launch(ctx, "attn_bwd_wave_keys_kernel");
 }
 
 int numrs_hip_attention_forward(numrs_hip_ctx *ctx, const float *q, const float *k, const float *v,
