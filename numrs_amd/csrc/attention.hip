@@ -841,7 +841,8 @@ __global__ void __launch_bounds__(512) attn_bwd_wave_rows_kernel(
   // column 16 q + 4 g + e), the first half of V (waited for, with them), the
   // second half of V, K, and after the barrier (so that no wave's later loads
   // queue ahead of another wave's first ones) the lane's O values (dO's
-  // layout) and P values (pf[kb] = P[query j][16 kb + 4 g ..]).
+  // layout); the lane's P values (pf[kb] = P[query j][16 kb + 4 g ..]) after
+  // the barrier in the middle of dP.
   f4 df[4], of[4];
   const int64_t roff = ((int64_t)b * S + row0 + 16 * wave + j) * ldo + (int64_t)head * kHeadDim + 4 * g;
 #pragma unroll
@@ -875,8 +876,6 @@ __global__ void __launch_bounds__(512) attn_bwd_wave_rows_kernel(
 #pragma unroll
   for (int q = 0; q < 4; ++q) of[q] = *reinterpret_cast<const f4 *>(O + roff + 16 * q);
   f4 pf[NKB];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) pf[kb] = *reinterpret_cast<const f4 *>(P + prow + 16 * kb);
 
   // 2. dP^T = V dO^T, the first half of the key blocks, then (after every
   // wave's second half of V and K have landed) the second; operand reads one
@@ -887,10 +886,10 @@ __global__ void __launch_bounds__(512) attn_bwd_wave_rows_kernel(
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     if (h == 1) {
-      // the NKB P loads are the newest vector-memory operations: at most NKB
-      // outstanding means O, the second half of V and K have landed
-      __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(NKB));
+      __builtin_amdgcn_s_waitcnt(numrs_hip::wait_vm(0));  // O, the second half of V, K
       __syncthreads();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) pf[kb] = *reinterpret_cast<const f4 *>(P + prow + 16 * kb);
     }
     constexpr int kPairs = NKB / 4, kSteps = 4 * kPairs;
     auto vread = [&](int i, int d) {
