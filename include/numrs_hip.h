@@ -330,11 +330,10 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
 /* The backward given also the forward's output out (rows at ld_out, like
  * dout), from which the softmax backward's row totals come as dO . O.  For
  * D/H = 64, S = 128 or 256, all three grads non-NULL and accumulate = 0 it
- * runs one key-block kernel (dV, dK and dQ without a dS buffer or any
- * workspace); other calls behave as numrs_hip_attention_backward_strided.
- * At S = 256 the two key groups of a head add into dq with device float
- * atomics onto a zeroed dq, so dq must be ordinary device memory (hipMalloc,
- * coarse-grained), not managed or fine-grained host-coherent memory. */
+ * runs two kernels: one over query rows (dS = P (dP - dO . O) into a
+ * B*H*S*S-float block of the context's memory, and dQ), then one over key
+ * rows (dV and dK); every output element is written once, with no atomics.
+ * Other calls behave as numrs_hip_attention_backward_strided. */
 int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
                                              const float *v, int64_t ld_qkv, const float *P,
                                              const float *out, const float *dout, int64_t ld_out,

@@ -1243,7 +1243,8 @@ int numrs_hip_attention_backward_strided(numrs_hip_ctx *ctx, const float *q, con
 
 // The backward given also the forward's output `out` (rows at ld_out, like
 // dout): for dh = 64, S = 128 or 256 and all three grads written (not
-// accumulated), the key-block kernel; otherwise the row-block path above.
+// accumulated), the query-row kernel (dS, dQ) then the key-row kernel (dV,
+// dK); otherwise the row-block path above.
 int numrs_hip_attention_backward_out_strided(numrs_hip_ctx *ctx, const float *q, const float *k,
                                              const float *v, int64_t ld_qkv, const float *P,
                                              const float *out, const float *dout, int64_t ld_out,

@@ -260,6 +260,50 @@ __global__ void __launch_bounds__(kBlock)
   if (lane == 0) idx[row] = (int32_t)(bi < 0 ? start : bi);
 }
 
+// (bv, bi) <- the better of (bv, bi) and (ov, oi); bi < 0 is an empty slot.
+template <bool TIE_LAST>
+__device__ __forceinline__ void pick_pair(float &bv, int &bi, float ov, int oi) {
+  const bool take = (oi >= 0) && (bi < 0 || (TIE_LAST ? better_last(ov, oi, bv, bi)
+                                                      : better_first(ov, oi, bv, bi)));
+  if (take) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+// Every lane ends with the wave's best (value, index) pair: the exchange
+// pattern of wave_butterfly (permlane32/16 swaps, then DPP row
+// and quad moves), applied to both halves of the pair.
+template <bool TIE_LAST>
+__device__ __forceinline__ void pair_butterfly(float &bv, int &bi) {
+  {
+    const unsigned uv = __builtin_bit_cast(unsigned, bv), ui = (unsigned)bi;
+    const auto rv = __builtin_amdgcn_permlane32_swap(uv, uv, false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap(ui, ui, false, false);
+    bv = __builtin_bit_cast(float, (unsigned)rv[0]);
+    bi = (int)(unsigned)ri[0];
+    pick_pair<TIE_LAST>(bv, bi, __builtin_bit_cast(float, (unsigned)rv[1]), (int)(unsigned)ri[1]);
+  }
+  {
+    const unsigned uv = __builtin_bit_cast(unsigned, bv), ui = (unsigned)bi;
+    const auto rv = __builtin_amdgcn_permlane16_swap(uv, uv, false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap(ui, ui, false, false);
+    bv = __builtin_bit_cast(float, (unsigned)rv[0]);
+    bi = (int)(unsigned)ri[0];
+    pick_pair<TIE_LAST>(bv, bi, __builtin_bit_cast(float, (unsigned)rv[1]), (int)(unsigned)ri[1]);
+  }
+  pick_pair<TIE_LAST>(bv, bi, dpp_mov<0x128>(bv), dpp_mov_i<0x128>(bi));  // row_ror:8
+  pick_pair<TIE_LAST>(bv, bi, dpp_mov<0x1B>(dpp_mov<0x141>(bv)),
+                      dpp_mov_i<0x1B>(dpp_mov_i<0x141>(bi)));  // row_half_mirror, quad [3,2,1,0]
+  pick_pair<TIE_LAST>(bv, bi, dpp_mov<0x4E>(bv), dpp_mov_i<0x4E>(bi));  // quad [2,3,0,1]
+  pick_pair<TIE_LAST>(bv, bi, dpp_mov<0xB1>(bv), dpp_mov_i<0xB1>(bi));  // quad [1,0,3,2]
+}
+
 // Argmax of a register-resident row (lane l holds the float4 groups
 // vcol<NV>(l, i)).  A lane visits its elements in increasing column order,
 // so within a lane the tie rule reduces to one comparison: first max keeps
@@ -280,13 +324,18 @@ __device__ __forceinline__ int argmax_regs(const f4 (&xv)[NV], int ncols, int la
           if (xv[i][e] != xv[i][e]) last_nan = c + e;
       }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) last_nan = max(last_nan, __shfl_xor(last_nan, off, 64));
+    last_nan = __builtin_bit_cast(int, wave_butterfly(
+                   __builtin_bit_cast(float, last_nan),
+                   [](float a, float b) {
+                     return __builtin_bit_cast(float, max(__builtin_bit_cast(int, a),
+                                                          __builtin_bit_cast(int, b)));
+                   }));
     if (last_nan == ncols - 1) return last_nan;
     start = last_nan + 1;
   } else {
     // x[0] is lane 0's first element; a NaN there stays the maximum.
-    const float x0 = __shfl(xv[0][0], 0, 64);
+    const float x0 = __builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, xv[0][0])));
     if (x0 != x0) return 0;
   }
   // Lane scan.  No NaN lies at or after `start` with TIE_LAST; without it a
@@ -310,18 +359,11 @@ __device__ __forceinline__ int argmax_regs(const f4 (&xv)[NV], int ncols, int la
       }
     }
   }
-  // Wave combine of (value, index) pairs with the full rule.
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, 64);
-    const int oi = __shfl_xor(bi, off, 64);
-    const bool take = (oi >= 0) && (bi < 0 || (TIE_LAST ? better_last(ov, oi, bv, bi)
-                                                        : better_first(ov, oi, bv, bi)));
-    if (take) {
-      bv = ov;
-      bi = oi;
-    }
-  }
+  // Wave combine of (value, index) pairs with the full rule, over the lane
+  // pairs of an xor butterfly (distances 32, 16, ..., 1), exchanged in
+  // registers.  Indices are distinct and the rule is a strict order, so the
+  // pair's winner does not depend on which lane holds which operand.
+  pair_butterfly<TIE_LAST>(bv, bi);
   return bi < 0 ? start : bi;
 }
 
@@ -333,7 +375,8 @@ __device__ __forceinline__ void load_row_regs(f4 (&xv)[NV], const float *xr, int
 
 // One wave per row.  (Measured on MI355X at [16384, 1024]: persistent
 // waves that load the next row before reducing the current one ran 10-20%
-// slower than this one-shot form.)
+// slower than this one-shot form, and waves of two rows with all eight
+// loads issued first 3% slower.)
 template <int NV, bool TIE_LAST, int VM>
 __global__ void __launch_bounds__(kBlock)
     argmax_vec(const float *__restrict__ x, int32_t *__restrict__ idx, int64_t rows,

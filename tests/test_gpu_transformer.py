@@ -96,11 +96,10 @@ def test_attention_strided_packed_qkv(hip_ctx, B, S, H, D, acc):
 @pytest.mark.parametrize("acc", [0, 1])
 def test_attention_backward_with_output(hip_ctx, B, S, H, D, acc):
     """numrs_hip_attention_backward_out_strided on the packed [B*S, 3D] layout:
-    given the forward's output, dh = 64 with S = 256 (two key groups adding into
-    dq) or S = 128 (one) runs the key-block kernel when nothing accumulates;
-    S = 384, S = 40 and acc = 1 take the row-block or GEMM path.  Each grad
-    against float64, and a second call returns the same bits (dq's two key
-    groups meet in either order)."""
+    given the forward's output, dh = 64 with S = 256 (two row blocks per head)
+    or S = 128 (one) runs the query-row and key-row kernels when nothing
+    accumulates; S = 384, S = 40 and acc = 1 take the row-block or GEMM path.
+    Each grad against float64, and a second call returns the same bits."""
     from numrs_amd import _lib as L
     print(f"[gpu] attention backward with output B={B} S={S} H={H} D={D} acc={acc}",
           flush=True)
