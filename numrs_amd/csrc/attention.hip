@@ -975,7 +975,11 @@ __global__ void __launch_bounds__(512) attn_bwd_wave_keys_kernel(
   constexpr int kQ = 16 * NQB;     // queries
   constexpr int kSteps = kQ / 4;   // MFMA steps of four queries
   constexpr int kPer = kQ / 32;    // DMA instructions per wave for Q, and for dO
-  constexpr int kPD = 16;          // steps of P and dS loaded ahead
+  // Steps of P and dS loaded ahead.  Measured at C4 (N3, from HBM): 4 ahead
+  // 54.3 us, 8 54.6, 16 55.6, 32 57.6 -- the loads hit in the caches (dS was
+  // just written, P is shared by the head's two key groups), and a longer
+  // ring only holds more loads in the memory pipeline.
+  constexpr int kPD = 4;
   __shared__ __attribute__((aligned(1024))) float lds[2 * kQ * kHeadDim];
   const float *qs = lds;
   const float *os = lds + kQ * kHeadDim;
