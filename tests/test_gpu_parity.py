@@ -752,6 +752,13 @@ def test_argmax_rows(hip_ctx, rng):
                        [0, 2, 1, 2, 1, 2, 1, np.nan], [0.0, -0.0, 0.0, -0.0, 0, 0, -0.0, 0],
                        [3, 3, 3, 3, 3, 3, 3, 3], [np.nan] * 8], np.float32),
              rand(rng, (33, 2048)), rng.integers(0, 2, (7, 1000)).astype(np.float32)]
+    # Wide register-resident rows (four and eight float4 groups per lane) with
+    # ties spread over every lane and NaNs in some rows: the wave's combine of
+    # (value, index) pairs across lanes decides these.
+    for w in (1024, 2048):
+        t = rng.integers(0, 4, (96, w)).astype(np.float32)
+        t[rng.random(t.shape) < 0.002] = np.nan
+        cases.append(t)
     for x in cases:
         for tie_last in (False, True):
             idx = c.empty((x.shape[0],), np.int32)
