@@ -966,6 +966,7 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
 
   for (int t = 0; t < T; ++t) {
     float gin[4] = {bias[0], bias[1], bias[2], bias[3]};
+    float act[4];
     const int64_t row = (int64_t)be * T + t;
     if (NI == 0 && epi && !upper) {
 #pragma unroll
@@ -1040,15 +1041,20 @@ __global__ void __launch_bounds__(512) lstm2_fwd_persist(Lstm2Fwd p) {
         pre[g] = gin[g] + (((part[pw][em][c] + part[pw + 1][em][c]) + part[pw + 2][em][c]) +
                            part[pw + 3][em][c]);
       }
-      float act[4], c, h;
+      float c, h;
       cell_forward(pre, cst, act, c, h);
       cst = c;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) acts[row * H4 + g * H + je] = act[g];
-      cs[row * H + je] = c;
       st_dev(hs + row * H + je, h);
     }
     publish_step(mine, (unsigned)(t + 1));
+    // The saved gates and cell state are read only by the backward (a later
+    // launch): stored after the step is published, so that its wait covers
+    // only h; the next step's publish waits for them.
+    if (epi) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) acts[row * H4 + g * H + je] = act[g];
+      cs[row * H + je] = cst;
+    }
   }
 }
 
